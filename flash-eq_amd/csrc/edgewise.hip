@@ -1,0 +1,451 @@
+// Fused EquivariantEdgewiseLinear: y = Q-rotate( Lambda(r) (x P) ).
+//
+// Reference pipeline (flash_eq/layers/linear.py:100-160): f = bmm(x, P);
+// out = block_diagonal_cuda(f, rw(), r, ...); y = bmm(out, Q^T), where the
+// table rw() = einsum('koi,bkw->boiw', C, F) is the SeparableRadialNet output
+// (radial.py:259-275).  Because the table has rank K in the channel pair,
+//   lerp_t(T)[co,ci,w] = sum_k C[k,co,ci] F_e[k,w],   F_e = (1-t) F[lo] + t F[lo+1],
+// so the per-edge mix factorises as
+//   Z_k[ci, o] = sum_i F_e[k, w(o,i)] fs[ci, i]      (cheap, per edge)
+//   yd[co, o]  = sum_k sum_ci C[k,co,ci] Z_k[ci, o]  (the GEMM-shaped part)
+// with fs = s^l (x P) and the 2x2 [[a,b],[-b,a]] structure on (+m,-m) pairs.
+// The table (num_bins+1, Cout, Cin, Wdim) is never formed.
+//
+// Backward (H_k = C_k^T gd, gd = s^l (gy Q)):
+//   dfs[ci,i] = sum_k sum_o F_e[k,w(o,i)] H_k[ci,o]     -> dx = s^l dfs P^T
+//   dF_e[k,w(o,i)] = sum_ci fs[ci,i] H_k[ci,o]         -> dF[lo] += (1-t) dF_e, dF[hi] += t dF_e
+//   dC[k,co,ci] = sum_e sum_o gd[co,o] Z_k[ci,o]
+//   dr = dt/dr sum_{k,w} (F[hi]-F[lo]) dF_e + sigma/(r(r+sigma)) sum_{k,w} (l_i+l_o) F_e dF_e
+// which equals the reference's grad_distances (block_diagonal.cu:990-1036,
+// 1113-1160) for a table of this form, including NaN at r = 0.
+#include "feq_internal.h"
+
+namespace feq {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kBwdGroups = 1024;  // workgroups of the backward pass
+
+struct Blk {
+    int m, ni, no, in_off, out_off, w_off;
+};
+
+__device__ __forceinline__ Blk get_blk(const feq_layout& L, int k) {
+    return {L.blk[k][0], L.blk[k][1], L.blk[k][2], L.blk[k][3], L.blk[k][4], L.blk[k][5]};
+}
+
+// Block / index / component of an m-first output slot (blk = -1: not mixed).
+__device__ __forceinline__ int out_block(const feq_layout& L, int slot, int& o, int& c) {
+    for (int k = 0; k < L.nblocks; ++k) {
+        const int w = L.blk[k][0] == 0 ? 1 : 2;
+        const int off = L.blk[k][4];
+        if (slot >= off && slot < off + w * L.blk[k][2]) {
+            o = (slot - off) / w;
+            c = (slot - off) % w;
+            return k;
+        }
+    }
+    return -1;
+}
+
+__device__ __forceinline__ int in_block(const feq_layout& L, int slot, int& i, int& c) {
+    for (int k = 0; k < L.nblocks; ++k) {
+        const int w = L.blk[k][0] == 0 ? 1 : 2;
+        const int off = L.blk[k][3];
+        if (slot >= off && slot < off + w * L.blk[k][1]) {
+            i = (slot - off) / w;
+            c = (slot - off) % w;
+            return k;
+        }
+    }
+    return -1;
+}
+
+// Z[ci, slot] = sum_i F_e[w(o,i)] fs[ci, i] for one rank component (sFk = F_e[k, :]).
+__device__ __forceinline__ float z_entry(const feq_layout& L, const float* sFk, const float* sf,
+                                         int ci, int slot) {
+    int o, c;
+    const int kb = out_block(L, slot, o, c);
+    if (kb < 0) return 0.0f;
+    const Blk b = get_blk(L, kb);
+    const float* f = sf + ci * L.din + b.in_off;
+    float acc = 0.0f;
+    if (b.m == 0) {
+        const float* w = sFk + b.w_off + o * b.ni;
+        for (int i = 0; i < b.ni; ++i) acc += w[i] * f[i];
+    } else {
+        const float* w = sFk + b.w_off + 2 * o * b.ni;
+        for (int i = 0; i < b.ni; ++i) {
+            const float a = w[2 * i], bb = w[2 * i + 1];
+            const float fr = f[2 * i], fi = f[2 * i + 1];
+            acc += c == 0 ? (a * fr + bb * fi) : (a * fi - bb * fr);
+        }
+    }
+    return acc;
+}
+
+// dfs[ci, slot] contribution of one rank component: sum_o F_e[w(o,i)] H[ci, o] (transposed 2x2).
+__device__ __forceinline__ float dz_entry(const feq_layout& L, const float* sFk, const float* sH,
+                                          int ci, int slot) {
+    int i, c;
+    const int kb = in_block(L, slot, i, c);
+    if (kb < 0) return 0.0f;
+    const Blk b = get_blk(L, kb);
+    const float* h = sH + ci * L.dout + b.out_off;
+    float acc = 0.0f;
+    if (b.m == 0) {
+        for (int o = 0; o < b.no; ++o) acc += sFk[b.w_off + o * b.ni + i] * h[o];
+    } else {
+        for (int o = 0; o < b.no; ++o) {
+            const float a = sFk[b.w_off + 2 * (o * b.ni + i)];
+            const float bb = sFk[b.w_off + 2 * (o * b.ni + i) + 1];
+            const float hr = h[2 * o], hi = h[2 * o + 1];
+            acc += c == 0 ? (a * hr - bb * hi) : (bb * hr + a * hi);
+        }
+    }
+    return acc;
+}
+
+// Weight w -> (block, o, i, component) and its degree sum l_i + l_o.
+__device__ __forceinline__ int weight_info(const feq_layout& L, int w, Blk& b, int& o, int& i,
+                                           int& comp) {
+    int k = L.nblocks - 1;
+    while (k > 0 && w < L.blk[k][5]) --k;
+    b = get_blk(L, k);
+    const int rel = w - b.w_off;
+    if (b.m == 0) {
+        o = rel / b.ni;
+        i = rel % b.ni;
+        comp = 0;
+        return L.lslot_in[b.in_off + i] + L.lslot_out[b.out_off + o];
+    }
+    comp = rel & 1;
+    o = (rel >> 1) / b.ni;
+    i = (rel >> 1) % b.ni;
+    return L.lslot_in[b.in_off + 2 * i] + L.lslot_out[b.out_off + 2 * o];
+}
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int w = 0; w < kThreads / 64; ++w) s += red[w];
+    __syncthreads();
+    return s;
+}
+
+struct EwDims {
+    int K;
+    int nbins;
+};
+
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(kThreads)
+k_ew_fwd(feq_layout L, feq_binning B, EwDims D, const float* __restrict__ x,
+         const float* __restrict__ P, const float* __restrict__ Q, const float* __restrict__ dist,
+         const float* __restrict__ C, const float* __restrict__ F, float* __restrict__ y) {
+    extern __shared__ float sm[];
+    const int cin = L.cin, cout = L.cout, din = L.din, dout = L.dout, wd = L.wdim, K = D.K;
+    float* sx = sm;                 // cin*din
+    float* sP = sx + cin * din;     // din*din
+    float* sQ = sP + din * din;     // dout*dout
+    float* sf = sQ + dout * dout;   // cin*din
+    float* sF = sf + cin * din;     // K*wd
+    float* sZ = sF + K * wd;        // cin*dout
+    float* sy = sZ + cin * dout;    // cout*dout
+    const int64_t e = blockIdx.x;
+    const int tid = threadIdx.x;
+    for (int q = tid; q < cin * din; q += kThreads) sx[q] = x[e * cin * din + q];
+    for (int q = tid; q < din * din; q += kThreads) sP[q] = P[e * din * din + q];
+    for (int q = tid; q < dout * dout; q += kThreads) sQ[q] = Q[e * dout * dout + q];
+    const float r = dist[e];
+    const EdgeBin eb = edge_bin(r, B);
+    const float sw = r / (r + B.sh_scale);
+    {
+        const float* flo = F + static_cast<int64_t>(eb.lo) * K * wd;
+        const float* fhi = flo + K * wd;
+        for (int q = tid; q < K * wd; q += kThreads) sF[q] = lerp_bins(flo[q], fhi[q], eb.t);
+    }
+    for (int q = tid; q < cout * dout; q += kThreads) sy[q] = 0.0f;
+    __syncthreads();
+    for (int q = tid; q < cin * din; q += kThreads) {
+        const int ci = q / din, j = q % din;
+        float acc = 0.0f;
+        for (int d = 0; d < din; ++d) acc += sx[ci * din + d] * sP[d * din + j];
+        sf[q] = acc * ipowf(sw, L.lslot_in[j]);
+    }
+    __syncthreads();
+    for (int k = 0; k < K; ++k) {
+        for (int q = tid; q < cin * dout; q += kThreads)
+            sZ[q] = z_entry(L, sF + k * wd, sf, q / dout, q % dout);
+        __syncthreads();
+        const float* Ck = C + static_cast<int64_t>(k) * cout * cin;
+        for (int q = tid; q < cout * dout; q += kThreads) {
+            const int co = q / dout, slot = q % dout;
+            float acc = 0.0f;
+            for (int ci = 0; ci < cin; ++ci) acc += Ck[co * cin + ci] * sZ[ci * dout + slot];
+            sy[q] += acc;
+        }
+        __syncthreads();
+    }
+    for (int q = tid; q < cout * dout; q += kThreads) sy[q] *= ipowf(sw, L.lslot_out[q % dout]);
+    __syncthreads();
+    for (int q = tid; q < cout * dout; q += kThreads) {
+        const int co = q / dout, d = q % dout;
+        float acc = 0.0f;
+        for (int j = 0; j < dout; ++j) acc += sy[co * dout + j] * sQ[d * dout + j];
+        y[e * cout * dout + q] = acc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Each workgroup walks a contiguous edge range; dC is accumulated per
+// workgroup in LDS and written as a partial, then reduced in a fixed order.
+__global__ void __launch_bounds__(kThreads)
+k_ew_bwd(feq_layout L, feq_binning B, EwDims D, int64_t E, const float* __restrict__ gy,
+         const float* __restrict__ x, const float* __restrict__ P, const float* __restrict__ Q,
+         const float* __restrict__ dist, const float* __restrict__ C,
+         const float* __restrict__ F, float* __restrict__ gx, float* __restrict__ gF,
+         float* __restrict__ gdist, float* __restrict__ gP, float* __restrict__ gQ,
+         float* __restrict__ dC_part) {
+    extern __shared__ float sm[];
+    __shared__ float red[kThreads / 64];
+    const int cin = L.cin, cout = L.cout, din = L.din, dout = L.dout, wd = L.wdim, K = D.K;
+    float* sx = sm;                 // cin*din
+    float* sP = sx + cin * din;     // din*din
+    float* sQ = sP + din * din;     // dout*dout
+    float* sg = sQ + dout * dout;   // cout*dout : gy, then gd
+    float* sgd = sg + cout * dout;  // cout*dout
+    float* sf = sgd + cout * dout;  // cin*din
+    float* sdf = sf + cin * din;    // cin*din
+    float* sF = sdf + cin * din;    // K*wd
+    float* sZ = sF + K * wd;        // cin*dout
+    float* sH = sZ + cin * dout;    // cin*dout
+    float* sy = sH + cin * dout;    // cout*dout (only with gQ)
+    float* sdC = sy + cout * dout;  // K*cout*cin
+    const int tid = threadIdx.x;
+    const int64_t per = (E + gridDim.x - 1) / gridDim.x;
+    const int64_t e0 = blockIdx.x * per;
+    const int64_t e1 = e0 + per < E ? e0 + per : E;
+    const int ncc = K * cout * cin;
+    for (int q = tid; q < ncc; q += kThreads) sdC[q] = 0.0f;
+    for (int64_t e = e0; e < e1; ++e) {
+        __syncthreads();
+        for (int q = tid; q < cin * din; q += kThreads) sx[q] = x[e * cin * din + q];
+        for (int q = tid; q < din * din; q += kThreads) sP[q] = P[e * din * din + q];
+        for (int q = tid; q < dout * dout; q += kThreads) sQ[q] = Q[e * dout * dout + q];
+        for (int q = tid; q < cout * dout; q += kThreads) sg[q] = gy[e * cout * dout + q];
+        const float r = dist[e];
+        const EdgeBin eb = edge_bin(r, B);
+        const float sigma = B.sh_scale;
+        const float sw = r / (r + sigma);
+        const float* flo = F + static_cast<int64_t>(eb.lo) * K * wd;
+        const float* fhi = flo + K * wd;
+        for (int q = tid; q < K * wd; q += kThreads) sF[q] = lerp_bins(flo[q], fhi[q], eb.t);
+        for (int q = tid; q < cin * din; q += kThreads) sdf[q] = 0.0f;
+        if (gQ)
+            for (int q = tid; q < cout * dout; q += kThreads) sy[q] = 0.0f;
+        __syncthreads();
+        for (int q = tid; q < cin * din; q += kThreads) {
+            const int ci = q / din, j = q % din;
+            float acc = 0.0f;
+            for (int d = 0; d < din; ++d) acc += sx[ci * din + d] * sP[d * din + j];
+            sf[q] = acc * ipowf(sw, L.lslot_in[j]);
+        }
+        for (int q = tid; q < cout * dout; q += kThreads) {
+            const int co = q / dout, j = q % dout;
+            float acc = 0.0f;
+            for (int d = 0; d < dout; ++d) acc += sg[co * dout + d] * sQ[d * dout + j];
+            sgd[q] = acc * ipowf(sw, L.lslot_out[j]);
+        }
+        __syncthreads();
+        float acc_t = 0.0f, acc_s = 0.0f;
+        for (int k = 0; k < K; ++k) {
+            const float* Ck = C + static_cast<int64_t>(k) * cout * cin;
+            for (int q = tid; q < cin * dout; q += kThreads) {
+                const int ci = q / dout, slot = q % dout;
+                float acc = 0.0f;
+                for (int co = 0; co < cout; ++co) acc += Ck[co * cin + ci] * sgd[co * dout + slot];
+                sH[q] = acc;
+                sZ[q] = z_entry(L, sF + k * wd, sf, ci, slot);
+            }
+            __syncthreads();
+            // dC[k] += gd Z^T
+            for (int q = tid; q < cout * cin; q += kThreads) {
+                const int co = q / cin, ci = q % cin;
+                float acc = 0.0f;
+                for (int s = 0; s < dout; ++s) acc += sgd[co * dout + s] * sZ[ci * dout + s];
+                sdC[k * cout * cin + q] += acc;
+            }
+            // dfs += F_e^T H
+            for (int q = tid; q < cin * din; q += kThreads)
+                sdf[q] += dz_entry(L, sF + k * wd, sH, q / din, q % din);
+            // recomputed forward output (only for grad_Q)
+            if (gQ)
+                for (int q = tid; q < cout * dout; q += kThreads) {
+                    const int co = q / dout, slot = q % dout;
+                    float acc = 0.0f;
+                    for (int ci = 0; ci < cin; ++ci) acc += Ck[co * cin + ci] * sZ[ci * dout + slot];
+                    sy[q] += acc;
+                }
+            // dF_e[k, w] and the distance-gradient partial sums
+            for (int w = tid; w < wd; w += kThreads) {
+                Blk b;
+                int o, i, comp;
+                const int Lsum = weight_info(L, w, b, o, i, comp);
+                float g = 0.0f;
+                for (int ci = 0; ci < cin; ++ci) {
+                    const float* f = sf + ci * din + b.in_off;
+                    const float* h = sH + ci * dout + b.out_off;
+                    if (b.m == 0) {
+                        g += f[i] * h[o];
+                    } else {
+                        const float fr = f[2 * i], fi = f[2 * i + 1];
+                        const float hr = h[2 * o], hi = h[2 * o + 1];
+                        g += comp == 0 ? (fr * hr + fi * hi) : (fi * hr - fr * hi);
+                    }
+                }
+                const int64_t fo = static_cast<int64_t>(k) * wd + w;
+                atomicAdd(&gF[static_cast<int64_t>(eb.lo) * K * wd + fo], (1.0f - eb.t) * g);
+                atomicAdd(&gF[static_cast<int64_t>(eb.lo + 1) * K * wd + fo], eb.t * g);
+                acc_t += (fhi[fo] - flo[fo]) * g;
+                acc_s += static_cast<float>(Lsum) * sF[fo] * g;
+            }
+            __syncthreads();
+        }
+        if (gdist) {
+            const float st = block_sum(acc_t, red);
+            const float ss = block_sum(acc_s, red);
+            if (tid == 0) {
+                float v = st * eb.dtdr;
+                if (L.has_lpos) v += ss * (sigma / (r * (r + sigma)));
+                gdist[e] = v;
+            }
+        }
+        // dx = s^l dfs P^T ; dP = x^T (s^l dfs)
+        for (int q = tid; q < cin * din; q += kThreads) sdf[q] *= ipowf(sw, L.lslot_in[q % din]);
+        if (gQ)
+            for (int q = tid; q < cout * dout; q += kThreads) sy[q] *= ipowf(sw, L.lslot_out[q % dout]);
+        __syncthreads();
+        if (gx)
+            for (int q = tid; q < cin * din; q += kThreads) {
+                const int ci = q / din, d = q % din;
+                float acc = 0.0f;
+                for (int j = 0; j < din; ++j) acc += sdf[ci * din + j] * sP[d * din + j];
+                gx[e * cin * din + q] = acc;
+            }
+        if (gP)
+            for (int q = tid; q < din * din; q += kThreads) {
+                const int d = q / din, j = q % din;
+                float acc = 0.0f;
+                for (int ci = 0; ci < cin; ++ci) acc += sx[ci * din + d] * sdf[ci * din + j];
+                gP[e * din * din + q] = acc;
+            }
+        if (gQ)
+            for (int q = tid; q < dout * dout; q += kThreads) {
+                const int d = q / dout, j = q % dout;
+                float acc = 0.0f;
+                for (int co = 0; co < cout; ++co) acc += sg[co * dout + d] * sy[co * dout + j];
+                gQ[e * dout * dout + q] = acc;
+            }
+    }
+    __syncthreads();
+    for (int q = tid; q < ncc; q += kThreads) dC_part[static_cast<int64_t>(blockIdx.x) * ncc + q] = sdC[q];
+}
+
+__global__ void k_reduce_partials(const float* __restrict__ part, int groups, int64_t n,
+                                  float* __restrict__ out) {
+    const int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (q >= n) return;
+    float acc = 0.0f;
+    for (int g = 0; g < groups; ++g) acc += part[g * n + q];
+    out[q] = acc;
+}
+
+size_t fwd_lds(const feq_layout& L, int K) {
+    return sizeof(float) * (2 * L.cin * L.din + L.din * L.din + L.dout * L.dout + K * L.wdim +
+                            L.cin * L.dout + L.cout * L.dout);
+}
+
+size_t bwd_lds(const feq_layout& L, int K) {
+    return sizeof(float) * (2 * L.cin * L.din + L.din * L.din + L.dout * L.dout +
+                            3 * L.cout * L.dout + L.cin * L.din + K * L.wdim +
+                            2 * L.cin * L.dout + static_cast<size_t>(K) * L.cout * L.cin);
+}
+
+int ensure_lds(const void* fn, size_t bytes) {
+    if (bytes > 160 * 1024) return fail(FEQ_ERR_UNSUPPORTED, "needs %zu bytes of LDS", bytes);
+    if (bytes > 64 * 1024)
+        FEQ_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(bytes)));
+    return FEQ_OK;
+}
+
+int groups_for(int64_t E) { return static_cast<int>(E < kBwdGroups ? (E > 0 ? E : 1) : kBwdGroups); }
+
+}  // namespace
+}  // namespace feq
+
+using namespace feq;
+
+extern "C" size_t feq_edgewise_workspace(const feq_layout* L, const feq_binning*, int32_t rank,
+                                         int64_t E) {
+    if (!L || rank < 1) return 0;
+    return sizeof(float) * static_cast<size_t>(groups_for(E)) * rank * L->cout * L->cin + 256;
+}
+
+extern "C" int feq_edgewise_fwd(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                int64_t E, const float* x, const float* P, const float* Q,
+                                const float* dist, const float* C, const float* F, float* y,
+                                void*, size_t, feq_stream_t stream) {
+    if (int rc = check_layout(L)) return rc;
+    if (int rc = check_binning(b)) return rc;
+    if (rank < 1) return fail(FEQ_ERR_INVALID, "rank must be positive");
+    if (E < 0) return fail(FEQ_ERR_INVALID, "negative edge count");
+    if (E == 0) return FEQ_OK;
+    if (E > 0x7fffffffLL) return fail(FEQ_ERR_UNSUPPORTED, "more than 2^31-1 edges");
+    if (!x || !P || !Q || !dist || !C || !F || !y) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    const size_t lds = fwd_lds(*L, rank);
+    if (int rc = ensure_lds(reinterpret_cast<const void*>(&k_ew_fwd), lds)) return rc;
+    EwDims D{rank, b->num_bins};
+    hipLaunchKernelGGL(k_ew_fwd, dim3(E), dim3(kThreads), lds, stream_of(stream), *L, *b, D, x, P,
+                       Q, dist, C, F, y);
+    FEQ_LAUNCH_CHECK("k_ew_fwd");
+    return FEQ_OK;
+}
+
+extern "C" int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                int64_t E, const float* gy, const float* x, const float* P,
+                                const float* Q, const float* dist, const float* C, const float* F,
+                                float* gx, float* gC, float* gF, float* gdist, float* gP,
+                                float* gQ, void* ws, size_t ws_bytes, feq_stream_t stream) {
+    if (int rc = check_layout(L)) return rc;
+    if (int rc = check_binning(b)) return rc;
+    if (rank < 1) return fail(FEQ_ERR_INVALID, "rank must be positive");
+    if (E < 0) return fail(FEQ_ERR_INVALID, "negative edge count");
+    if (E > 0x7fffffffLL) return fail(FEQ_ERR_UNSUPPORTED, "more than 2^31-1 edges");
+    if (!gC || !gF) return fail(FEQ_ERR_INVALID, "grad_C and grad_F are required");
+    hipStream_t s = stream_of(stream);
+    const int64_t ncc = static_cast<int64_t>(rank) * L->cout * L->cin;
+    const int64_t nF = static_cast<int64_t>(b->num_bins + 1) * rank * L->wdim;
+    if (int rc = fill_zero(gF, nF, s)) return rc;
+    if (E == 0) return fill_zero(gC, ncc, s);
+    if (!gy || !x || !P || !Q || !dist || !C || !F) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (!ws || ws_bytes < feq_edgewise_workspace(L, b, rank, E))
+        return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
+    const size_t lds = bwd_lds(*L, rank);
+    if (int rc = ensure_lds(reinterpret_cast<const void*>(&k_ew_bwd), lds)) return rc;
+    const int G = groups_for(E);
+    float* part = static_cast<float*>(ws);
+    EwDims D{rank, b->num_bins};
+    hipLaunchKernelGGL(k_ew_bwd, dim3(G), dim3(kThreads), lds, s, *L, *b, D, E, gy, x, P, Q, dist,
+                       C, F, gx, gF, gdist, gP, gQ, part);
+    FEQ_LAUNCH_CHECK("k_ew_bwd");
+    hipLaunchKernelGGL(k_reduce_partials, dim3(ceil_div(ncc, 256)), dim3(256), 0, s, part, G, ncc,
+                       gC);
+    FEQ_LAUNCH_CHECK("k_reduce_partials");
+    return FEQ_OK;
+}

@@ -1,0 +1,124 @@
+// Internal helpers shared by the HIP translation units of libflasheq.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "flasheq.h"
+
+namespace feq {
+
+// ---- error reporting ---------------------------------------------------------
+void set_error(const char* fmt, ...);
+int fail(int code, const char* fmt, ...);
+
+#define FEQ_HIP(call)                                                              \
+    do {                                                                           \
+        hipError_t e_ = (call);                                                    \
+        if (e_ != hipSuccess)                                                      \
+            return ::feq::fail(FEQ_ERR_HIP, "%s failed: %s", #call,                \
+                               hipGetErrorString(e_));                             \
+    } while (0)
+
+#define FEQ_LAUNCH_CHECK(name)                                                     \
+    do {                                                                           \
+        hipError_t e_ = hipGetLastError();                                         \
+        if (e_ != hipSuccess)                                                      \
+            return ::feq::fail(FEQ_ERR_HIP, "launch of %s failed: %s", name,       \
+                               hipGetErrorString(e_));                             \
+    } while (0)
+
+inline hipStream_t stream_of(feq_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Zero-fill by kernel (never hipMemsetAsync: callers may capture the stream).
+int fill_zero(float* p, int64_t n, hipStream_t s);
+
+// Checks shared by every layout-consuming entry point.
+int check_layout(const feq_layout* L);
+int check_binning(const feq_binning* b);
+
+// Carves consecutive 256-byte aligned regions out of a caller workspace.
+struct Carver {
+    char* base;
+    size_t used = 0;
+    explicit Carver(void* p) : base(static_cast<char*>(p)) {}
+    template <class T>
+    T* take(size_t n) {
+        used = align_up(used, 256);
+        T* p = reinterpret_cast<T*>(base ? base + used : nullptr);
+        used += n * sizeof(T);
+        return p;
+    }
+};
+
+// ---- per-edge distance state ---------------------------------------------------
+// Lower bin index lo (hi = lo + 1), interpolation weight t, dt/dr.
+// The index is found in float32 exactly as the reference kernel does
+// (block_diagonal.cu:82-115): normalized = (r - p1) * p2 (linear) or
+// (log(max(r, exp(p1))) - p1) * p2 * nb (log), clamped to [0, nb],
+// lo = min(floor(normalized), nb - 1).  Linear t is not clamped (it
+// extrapolates outside [min, max]); log t is clamped to <= 1 and r below the
+// bin's lower edge maps to t = 0.  dt/dr follows binning_derivative (:121-138).
+struct EdgeBin {
+    int lo;
+    float t;
+    float dtdr;
+};
+
+__device__ __forceinline__ EdgeBin edge_bin(float r, const feq_binning& b) {
+    EdgeBin s;
+    const int nb = b.num_bins;
+    float nrm;
+    if (b.log_bins) {
+        nrm = (logf(fmaxf(r, expf(b.p1))) - b.p1) * b.p2 * static_cast<float>(nb);
+    } else {
+        nrm = (r - b.p1) * b.p2;
+    }
+    nrm = fminf(fmaxf(nrm, 0.0f), static_cast<float>(nb));
+    int lo = static_cast<int>(floorf(nrm));
+    lo = lo < nb - 1 ? lo : nb - 1;
+    s.lo = lo;
+    if (b.log_bins) {
+        const float ilbw = b.p2 * static_cast<float>(nb);
+        const float log_lo = b.p1 + static_cast<float>(lo) / ilbw;
+        const float e_lo = static_cast<float>(exp(static_cast<double>(log_lo)));
+        const float e_hi = static_cast<float>(exp(static_cast<double>(log_lo + 1.0f / ilbw)));
+        const float c = r > e_lo ? r : e_lo;
+        float t = (c - e_lo) / (e_hi - e_lo);
+        s.t = t < 1.0f ? t : 1.0f;
+        s.dtdr = 1.0f / (e_hi - e_lo);
+    } else {
+        const float width = 1.0f / b.p2;
+        const float e_lo = b.p1 + static_cast<float>(lo) * width;
+        s.t = (r - e_lo) / width;
+        s.dtdr = b.p2;
+    }
+    return s;
+}
+
+// Interpolated table value (1-t) lo + t hi, evaluated as lo + t (hi - lo):
+// identical in exact arithmetic and well conditioned when linear bins
+// extrapolate (|t| >> 1 beyond max_dist).
+__device__ __forceinline__ float lerp_bins(float lo, float hi, float t) {
+    return fmaf(t, hi - lo, lo);
+}
+
+// s^l for small non-negative integer l by repeated squaring (as ipow, :202-213).
+__device__ __forceinline__ float ipowf(float base, int e) {
+    float r = 1.0f;
+    while (e > 0) {
+        if (e & 1) r *= base;
+        base *= base;
+        e >>= 1;
+    }
+    return r;
+}
+
+}  // namespace feq

@@ -1,0 +1,147 @@
+"""ctypes binding of ``libflasheq.so`` (the C ABI declared in ``include/flasheq.h``).
+
+The library is the only compute path for the hot-path ops.  Loading fails
+loudly: without a GPU the ops raise ``CUDANotAvailableError`` (the reference's
+error type, ``flash_eq/cuda/block_diagonal.py:34-55``); with a GPU but no built
+library they raise ``ImportError`` naming the build command.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence
+
+import torch
+
+from ._build import LIB_PATH
+
+FEQ_MAX_BLOCKS = 17
+FEQ_MAX_SLOTS = 128
+
+
+class CUDANotAvailableError(RuntimeError):
+    """Raised when a GPU is required but none is visible (reference name kept)."""
+
+
+class FeqLayout(ctypes.Structure):
+    _fields_ = [
+        ("cin", ctypes.c_int32), ("cout", ctypes.c_int32),
+        ("din", ctypes.c_int32), ("dout", ctypes.c_int32),
+        ("wdim", ctypes.c_int32), ("nblocks", ctypes.c_int32),
+        ("blk", (ctypes.c_int32 * 6) * FEQ_MAX_BLOCKS),
+        ("lslot_in", ctypes.c_int8 * FEQ_MAX_SLOTS),
+        ("lslot_out", ctypes.c_int8 * FEQ_MAX_SLOTS),
+        ("has_lpos", ctypes.c_int32),
+    ]
+
+
+class FeqBinning(ctypes.Structure):
+    _fields_ = [
+        ("p1", ctypes.c_float), ("p2", ctypes.c_float),
+        ("num_bins", ctypes.c_int32), ("log_bins", ctypes.c_int32),
+        ("sh_scale", ctypes.c_float),
+    ]
+
+
+_lib: Optional[ctypes.CDLL] = None
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+_SIGS = {
+    "feq_last_error": ([], ctypes.c_char_p),
+    "feq_abi_version": ([], ctypes.c_int),
+    "feq_layout_init": ([_P, _P, _I32, _P, _I32, _I32, _I32], ctypes.c_int),
+    "feq_bin_edges": ([_P, _I64, _P, _P, _P, _P], ctypes.c_int),
+    "feq_blockdiag_workspace": ([_P, _P, _I64], _SZ),
+    "feq_blockdiag_fwd": ([_P, _P, _I64, _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
+    "feq_blockdiag_bwd": ([_P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
+    "feq_edgewise_workspace": ([_P, _P, _I32, _I64], _SZ),
+    "feq_edgewise_fwd": ([_P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
+    "feq_edgewise_bwd": ([_P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _P,
+                          _P, _P, _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
+    "feq_wigner_plan_doubles": ([_P, _I32], _SZ),
+    "feq_wigner_basis": ([_P, _I32, _P, _P, _I64, _P, _P, _P], ctypes.c_int),
+    "feq_csr_workspace": ([_I64, _I64], _SZ),
+    "feq_csr_by_dst": ([_P, _I64, _I64, _P, _P, _P, _SZ, _P], ctypes.c_int),
+    "feq_segment_sum": ([_P, _I64, _P, _P, _I64, _P, _P], ctypes.c_int),
+    "feq_gather_rows": ([_P, _I64, _I64, _P, _I64, _P, _P], ctypes.c_int),
+    "feq_edge_softmax_fwd": ([_P, _P, _P, _I64, _I32, _I32, _F, _F, _P, _P, _I64, _P, _P, _P],
+                             ctypes.c_int),
+    "feq_edge_softmax_bwd": ([_P, _P, _P, _P, _I64, _I32, _I32, _F, _F, _P, _P, _I64,
+                              _P, _P, _P, _P, _P], ctypes.c_int),
+    "feq_attn_pool_fwd": ([_P, _P, _I64, _I32, _I32, _I32, _P, _P, _I64, _P, _P], ctypes.c_int),
+    "feq_attn_pool_bwd": ([_P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P], ctypes.c_int),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGS)
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load the shared library and declare every signature (no GPU needed)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ImportError(
+            f"flash-eq HIP library not found at {path}.\n"
+            "Build it with: python -c 'import __graft_entry__ as g; g.build()' "
+            "(or python flash-eq_amd/flash_eq/_build.py)")
+    lib = ctypes.CDLL(path)
+    for name, (args, res) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = lib
+    return lib
+
+
+def lib() -> ctypes.CDLL:
+    """The library, for compute calls: requires a visible GPU."""
+    if not torch.cuda.is_available():
+        raise CUDANotAvailableError(
+            "flash-eq (MI355X build) requires a ROCm GPU. No GPU was detected: "
+            "torch.cuda.is_available() is False.")
+    return load_library()
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load_library().feq_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what}: {msg} (code {rc})")
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def make_layout(lvals_in: Sequence[int], lvals_out: Sequence[int], cin: int, cout: int) -> FeqLayout:
+    li = (ctypes.c_int32 * len(lvals_in))(*[int(v) for v in lvals_in])
+    lo = (ctypes.c_int32 * len(lvals_out))(*[int(v) for v in lvals_out])
+    out = FeqLayout()
+    rc = load_library().feq_layout_init(ctypes.byref(out), li, len(lvals_in), lo, len(lvals_out),
+                                        int(cin), int(cout))
+    check(rc, "feq_layout_init")
+    return out
+
+
+def make_binning(p1: float, p2: float, num_bins: int, log_bins: bool, sh_scale: float) -> FeqBinning:
+    return FeqBinning(float(p1), float(p2), int(num_bins), int(bool(log_bins)), float(sh_scale))
+
+
+def require_cuda_tensor(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise CUDANotAvailableError(
+            f"{name} must be a GPU tensor: the flash-eq hot path runs only on the GPU "
+            f"(got device {t.device}).")
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Caller-owned scratch for the library, from the caching allocator."""
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)

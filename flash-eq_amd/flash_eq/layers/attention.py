@@ -1,0 +1,120 @@
+"""Equivariant graph attention (drop-in for ``flash_eq/layers/attention.py``).
+
+* logits and the per-destination softmax (``attention.py:92-141``) run in one
+  HIP kernel per node segment (``feq_edge_softmax_fwd``): max shift,
+  exponentials, the ``+1e-8`` denominator, in CSR order without atomics;
+* ``EquivariantAttention`` fuses the head weighting of V with the sum pooling
+  (``attention.py:143-167`` + ``pooling.py:21-30``) in ``feq_attn_pool_fwd``, so
+  the weighted (E, mult, dim) tensor is never written;
+* V comes from the fused ``EquivariantEdgewiseLinear``.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from .. import _native as N
+from ..graph import Graph
+from ..ops import AttnPoolFn, EdgeSoftmaxFn
+from ..representations import Repr
+from .linear import EquivariantEdgewiseLinear, EquivariantLinear
+from .norm import EquivariantLayerNorm
+from .pooling import GraphPooling
+
+
+class EquivariantEdgeAttention(nn.Module):
+    """Scaled dot-product attention over the edges that share a destination."""
+
+    def __init__(self, num_heads: int, qk_dim: int, dropout: float = 0.0,
+                 distance_decay_scale: float | None = None) -> None:
+        super().__init__()
+        self.num_heads = num_heads
+        self.qk_dim = qk_dim
+        self.distance_decay_scale = distance_decay_scale
+        self.log_scale = nn.Parameter(torch.tensor(qk_dim ** -0.5).log())
+        self.dropout = nn.Dropout(dropout) if dropout > 0 else nn.Identity()
+
+    @property
+    def scale(self) -> torch.Tensor:
+        return self.log_scale.exp()
+
+    def attention_weights(self, Q: torch.Tensor, K: torch.Tensor, graph: Graph,
+                          distances: torch.Tensor | None = None) -> torch.Tensor:
+        """Softmax-normalised weights (E, H) after dropout."""
+        N.require_cuda_tensor(Q, "Q")
+        perm, offsets = graph.csr()
+        decay = float(self.distance_decay_scale) if (
+            self.distance_decay_scale is not None and distances is not None) else 0.0
+        attn = EdgeSoftmaxFn.apply(Q, K, distances if decay > 0 else None, self.log_scale, decay,
+                                   perm, offsets, graph.num_nodes)
+        return self.dropout(attn)
+
+    def forward(self, Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, graph: Graph,
+                distances: torch.Tensor | None = None) -> torch.Tensor:
+        """Q, K (E, H, qk_dim); V (E, mult, dim) -> attention-weighted V (E, mult, dim)."""
+        attn = self.attention_weights(Q, K, graph, distances)
+        return self._apply_attention(V, attn)
+
+    def _apply_attention(self, V: torch.Tensor, attn: torch.Tensor) -> torch.Tensor:
+        E, mult, dim = V.shape
+        if self.num_heads == 1:
+            return V * attn.view(E, 1, 1)
+        hd = mult // self.num_heads
+        return (V.view(E, self.num_heads, hd, dim) * attn.view(E, self.num_heads, 1, 1)).view(E, mult, dim)
+
+    def extra_repr(self) -> str:
+        return f"num_heads={self.num_heads}, qk_dim={self.qk_dim}"
+
+
+class EquivariantAttention(nn.Module):
+    """Equivariant Q/K projections + edgewise V + neighbour softmax + pooling."""
+
+    def __init__(self, in_repr: Repr, out_repr: Repr, num_heads: int = 1, num_bins: int = 100,
+                 rank: int = 4, hidden_dim: int = 64, min_dist: float = 0.0,
+                 max_dist: float = 10.0, log_bins: bool = False, dropout: float = 0.0,
+                 reduce: str = "sum", distance_decay_scale: float | None = None) -> None:
+        super().__init__()
+        if in_repr.mult % num_heads != 0:
+            raise ValueError(f"num_heads ({num_heads}) must divide in_repr.mult ({in_repr.mult})")
+        if out_repr.mult % num_heads != 0:
+            raise ValueError(f"num_heads ({num_heads}) must divide out_repr.mult ({out_repr.mult})")
+        self.in_repr = in_repr
+        self.out_repr = out_repr
+        self.num_heads = num_heads
+        # module creation order follows attention.py:241-269 (seeded init parity)
+        self.norm_qk = EquivariantLayerNorm(in_repr)
+        self.linear_qk = EquivariantLinear(in_repr, Repr(lvals=in_repr.lvals, mult=in_repr.mult * 2),
+                                           bias=False)
+        qk_dim = (in_repr.mult // num_heads) * in_repr.dim()
+        self.attention = EquivariantEdgeAttention(num_heads=num_heads, qk_dim=qk_dim,
+                                                  dropout=dropout,
+                                                  distance_decay_scale=distance_decay_scale)
+        self.linear_v = EquivariantEdgewiseLinear(in_repr=in_repr, out_repr=out_repr,
+                                                  num_bins=num_bins, rank=rank,
+                                                  hidden_dim=hidden_dim, min_dist=min_dist,
+                                                  max_dist=max_dist, log_bins=log_bins)
+        self.pool = GraphPooling(reduce=reduce)
+
+    def forward(self, P: torch.Tensor, Q_basis: torch.Tensor, node_features: torch.Tensor,
+                distances: torch.Tensor, graph: Graph,
+                edge_features: torch.Tensor | None = None) -> torch.Tensor:
+        """node_features (N, mult_in, dim_in) -> (N, mult_out, dim_out)."""
+        E = graph.num_edges
+        mult = self.in_repr.mult
+        qk = self.linear_qk(self.norm_qk(node_features))            # (N, 2 mult, dim)
+        Qe = qk[:, :mult][graph.dst].view(E, self.num_heads, -1)
+        Ke = qk[:, mult:][graph.src].view(E, self.num_heads, -1)
+        gathered = node_features[graph.src]
+        if edge_features is not None:
+            gathered = gathered + edge_features
+        V = self.linear_v(P, Q_basis, gathered, distances)           # (E, mult_out, dim_out)
+        attn = self.attention.attention_weights(Qe, Ke, graph, distances)
+        if self.pool.reduce == "sum":
+            perm, offsets = graph.csr()
+            return AttnPoolFn.apply(V, attn, graph.dst, perm, offsets, graph.num_nodes,
+                                    self.num_heads)
+        return self.pool(self.attention._apply_attention(V, attn), graph)
+
+    def extra_repr(self) -> str:
+        return (f"in_repr={self.in_repr}, out_repr={self.out_repr}, "
+                f"num_heads={self.num_heads}, reduce='{self.pool.reduce}'")

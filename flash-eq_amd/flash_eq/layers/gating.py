@@ -1,0 +1,30 @@
+"""Norm-based gating (drop-in for ``flash_eq/layers/gating.py:17-76``); node-side PyTorch."""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from ..representations import Repr
+from ..utils import init_linear_weights
+from .norm import RepNorm
+
+
+class EquivariantGating(nn.Module):
+    """x * sigmoid(Linear(per-irrep norms)) broadcast over each irrep's components."""
+
+    def __init__(self, repr: Repr) -> None:
+        super().__init__()
+        self.repr = repr
+        self.norm = RepNorm(repr)
+        width = repr.nreps() * repr.mult
+        self.linear = nn.Linear(width, width)
+        self.register_buffer("ix", torch.tensor(repr.indices(), dtype=torch.long))
+        self.outdims = (repr.mult, repr.nreps())
+        self.activation = nn.Sigmoid()
+        self.apply(init_linear_weights)
+
+    def forward(self, st: torch.Tensor) -> torch.Tensor:
+        norms = self.norm(st)
+        *batch, _, _ = norms.shape
+        gates = self.activation(self.linear(norms.flatten(-2, -1)).view(*batch, *self.outdims))
+        return st * gates[..., self.ix]

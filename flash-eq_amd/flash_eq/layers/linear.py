@@ -1,0 +1,115 @@
+"""SO(3)-equivariant linear layers (drop-in for ``flash_eq/layers/linear.py``).
+
+``EquivariantEdgewiseLinear`` computes ``out = Q Lambda(r) P^T f`` per edge
+(``linear.py:100-160``) in ONE fused HIP pass per direction
+(``csrc/edgewise.hip``): rotate into the m-first frame with P, apply the
+binned, interpolated, solid-harmonic-scaled radial weights in their separable
+form ``sum_k C_k (x) F_k`` (the ``SeparableRadialNet`` factors), rotate back
+with Q.  Neither the rotated features nor the (num_bins+1, Cout, Cin, Wdim)
+table are written to memory.
+
+``EquivariantLinear`` is the node-side per-degree channel mix
+(``linear.py:172-268``); it is O(N) work and stays a PyTorch matmul.
+"""
+from __future__ import annotations
+
+from functools import lru_cache
+from typing import Tuple
+
+import torch
+import torch.nn as nn
+
+from .. import _native as N
+from ..ops import edgewise_linear
+from ..representations import ProductRepr, Repr
+from .radial import SeparableRadialNet
+
+
+@lru_cache(maxsize=256)
+def _layout(lvals_in: Tuple[int, ...], lvals_out: Tuple[int, ...], cin: int, cout: int):
+    return N.make_layout(lvals_in, lvals_out, cin, cout)
+
+
+class EquivariantEdgewiseLinear(nn.Module):
+    """Edge-to-edge equivariant linear map with distance-dependent binned weights."""
+
+    radial_weights: SeparableRadialNet
+
+    def __init__(self, in_repr: Repr, out_repr: Repr, num_bins: int = 100, rank: int = 4,
+                 hidden_dim: int = 64, min_dist: float = 0.0, max_dist: float = 10.0,
+                 log_bins: bool = False, solid_harmonic_scale: float = 0.1) -> None:
+        super().__init__()
+        self.in_repr = in_repr
+        self.out_repr = out_repr
+        self.rank = rank
+        self.solid_harmonic_scale = solid_harmonic_scale
+        self.product_repr = ProductRepr(in_repr, out_repr)
+        self.weight_dim = self.product_repr.nreps()
+        self.channels_in = in_repr.mult
+        self.channels_out = out_repr.mult
+        self.radial_weights = SeparableRadialNet(
+            num_bins=num_bins, out_mult=self.channels_out, in_mult=self.channels_in,
+            weight_dim=self.weight_dim, rank=rank, hidden_dim=hidden_dim,
+            min_val=min_dist, max_val=max_dist, log=log_bins)
+        self._lin = tuple(int(l) for l in in_repr.lvals.tolist())
+        self._lout = tuple(int(l) for l in out_repr.lvals.tolist())
+
+    def layout(self) -> N.FeqLayout:
+        return _layout(self._lin, self._lout, self.channels_in, self.channels_out)
+
+    def binning(self) -> N.FeqBinning:
+        rw = self.radial_weights
+        p1, p2 = rw.binning_params()
+        return N.make_binning(p1, p2, rw.num_bins, rw.log, self.solid_harmonic_scale)
+
+    def forward(self, P: torch.Tensor, Q: torch.Tensor, edge_features: torch.Tensor,
+                distances: torch.Tensor) -> torch.Tensor:
+        """P (E, Din, Din), Q (E, Dout, Dout), edge_features (E, Cin, Din), distances (E,)
+        -> (E, Cout, Dout), all in the standard SH basis."""
+        N.require_cuda_tensor(edge_features, "edge_features")
+        rw = self.radial_weights
+        return edgewise_linear(edge_features, P, Q, distances, rw.channel_patterns,
+                               rw.radial_functions(), self.layout(), self.binning(), rw.rank)
+
+    def extra_repr(self) -> str:
+        rw = self.radial_weights
+        spacing = "log" if rw.log else "linear"
+        return (f"in_repr={self.in_repr}, out_repr={self.out_repr}, num_bins={rw.num_bins}, "
+                f"dist=[{rw.min_val}, {rw.max_val}], spacing={spacing}, rank={self.rank}")
+
+
+class EquivariantLinear(nn.Module):
+    """Per-degree channel mixing of node features; bias/activation on scalars only."""
+
+    def __init__(self, in_repr: Repr, out_repr: Repr, bias: bool = True,
+                 activation: nn.Module | None = None) -> None:
+        super().__init__()
+        if not torch.equal(in_repr.lvals, out_repr.lvals):
+            raise ValueError(
+                "EquivariantLinear cannot modify the degrees of a representation. "
+                f"Got input lvals={in_repr.lvals.tolist()}, output lvals={out_repr.lvals.tolist()}")
+        self.in_repr = in_repr
+        self.out_repr = out_repr
+        self.weight = nn.Parameter(torch.empty(in_repr.nreps() * out_repr.mult, in_repr.mult))
+        nn.init.xavier_uniform_(self.weight)
+        self.register_buffer("indices", torch.tensor(in_repr.indices(), dtype=torch.long))
+        offs = in_repr.cumdims().tolist()
+        self._slices = [(offs[k], offs[k + 1]) for k in range(in_repr.nreps())]
+        nscalar, locs = in_repr.find_scalar()
+        self.scalar_locs = locs
+        self.bias: nn.Parameter | None
+        if nscalar > 0 and bias:
+            self.bias = nn.Parameter(torch.zeros(out_repr.mult, nscalar), requires_grad=True)
+        else:
+            self.bias = None
+        self.activation = activation if activation is not None else nn.Identity()
+
+    def forward(self, f: torch.Tensor) -> torch.Tensor:
+        """(..., in_mult, dim) -> (..., out_mult, dim)."""
+        w = self.weight.view(self.in_repr.nreps(), self.out_repr.mult, self.in_repr.mult)
+        out = torch.cat([torch.matmul(w[k], f[..., a:b]) for k, (a, b) in enumerate(self._slices)],
+                        dim=-1)
+        if self.bias is not None:
+            out = out.clone()
+            out[..., self.scalar_locs] = self.activation(out[..., self.scalar_locs] + self.bias).to(out.dtype)
+        return out

@@ -1,0 +1,304 @@
+"""Autograd wrappers around the HIP library (``libflasheq.so``).
+
+Every function here runs the GPU kernels through the C ABI on the current
+stream of the tensors' device; PyTorch only allocates outputs and workspaces.
+Inputs must be GPU tensors; float16/bfloat16/float32 inputs are computed in
+float32 (fp32 accumulation) and returned in the input dtype.  float64 is
+rejected: the kernels are float32.
+"""
+from __future__ import annotations
+
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _native as N
+
+_SUPPORTED = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def _f32(t: torch.Tensor, name: str) -> torch.Tensor:
+    N.require_cuda_tensor(t, name)
+    if t.dtype == torch.float64:
+        raise TypeError(f"{name}: float64 is not supported by the MI355X kernels (use float32)")
+    if t.dtype not in _SUPPORTED:
+        raise TypeError(f"{name}: unsupported dtype {t.dtype}")
+    return t.detach().to(torch.float32).contiguous()
+
+
+def _same_device(*ts: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+# ---------------------------------------------------------------------------
+# fused EquivariantEdgewiseLinear
+# ---------------------------------------------------------------------------
+class EdgewiseLinearFn(torch.autograd.Function):
+    """y = (Lambda(r) (x P)) Q^T with Lambda from (C, F); see ``csrc/edgewise.hip``."""
+
+    @staticmethod
+    def forward(ctx, x, P, Q, dist, C, F, layout: N.FeqLayout, binning: N.FeqBinning, rank: int):
+        dev = _same_device(x, P, Q, dist, C, F)
+        E = x.shape[0]
+        xs, Ps, Qs = _f32(x, "edge_features"), _f32(P, "P"), _f32(Q, "Q")
+        rs, Cs, Fs = _f32(dist, "distances"), _f32(C, "channel_patterns"), _f32(F, "radial")
+        _check_edgewise_shapes(layout, binning, rank, xs, Ps, Qs, rs, Cs, Fs)
+        y = torch.empty(E, layout.cout, layout.dout, dtype=torch.float32, device=dev)
+        if E:
+            lib = N.lib()
+            with torch.cuda.device(dev):
+                rc = lib.feq_edgewise_fwd(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
+                                          N.ptr(xs), N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs),
+                                          N.ptr(Fs), N.ptr(y), None, 0, N.stream_ptr(dev))
+            N.check(rc, "feq_edgewise_fwd")
+        ctx.save_for_backward(xs, Ps, Qs, rs, Cs, Fs)
+        ctx.meta = (layout, binning, rank, x.dtype, P.dtype, Q.dtype, dist.dtype, C.dtype, F.dtype)
+        return y.to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, gy):
+        xs, Ps, Qs, rs, Cs, Fs = ctx.saved_tensors
+        layout, binning, rank, xdt, pdt, qdt, rdt, cdt, fdt = ctx.meta
+        dev = xs.device
+        E = xs.shape[0]
+        need = ctx.needs_input_grad
+        g = gy.detach().to(torch.float32).contiguous()
+        gx = torch.empty_like(xs) if need[0] else None
+        gP = torch.empty_like(Ps) if need[1] else None
+        gQ = torch.empty_like(Qs) if need[2] else None
+        gr = torch.empty_like(rs) if need[3] else None
+        gC = torch.empty_like(Cs)
+        gF = torch.empty_like(Fs)
+        lib = N.lib()
+        ws = N.workspace(lib.feq_edgewise_workspace(N.ctypes.byref(layout), N.ctypes.byref(binning),
+                                                    rank, E), dev)
+        with torch.cuda.device(dev):
+            rc = lib.feq_edgewise_bwd(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
+                                      N.ptr(g), N.ptr(xs), N.ptr(Ps), N.ptr(Qs), N.ptr(rs),
+                                      N.ptr(Cs), N.ptr(Fs), N.ptr(gx), N.ptr(gC), N.ptr(gF),
+                                      N.ptr(gr), N.ptr(gP), N.ptr(gQ), N.ptr(ws), ws.numel(),
+                                      N.stream_ptr(dev))
+        N.check(rc, "feq_edgewise_bwd")
+        cast = lambda t, dt: None if t is None else t.to(dt)
+        return (cast(gx, xdt), cast(gP, pdt), cast(gQ, qdt), cast(gr, rdt),
+                gC.to(cdt) if need[4] else None, gF.to(fdt) if need[5] else None,
+                None, None, None)
+
+
+def _check_edgewise_shapes(L, b, rank, x, P, Q, r, C, F) -> None:
+    E = x.shape[0]
+    if x.shape != (E, L.cin, L.din):
+        raise ValueError(f"edge_features must be (E, {L.cin}, {L.din}), got {tuple(x.shape)}")
+    if P.shape != (E, L.din, L.din):
+        raise ValueError(f"P must be (E, {L.din}, {L.din}), got {tuple(P.shape)}")
+    if Q.shape != (E, L.dout, L.dout):
+        raise ValueError(f"Q must be (E, {L.dout}, {L.dout}), got {tuple(Q.shape)}")
+    if r.shape != (E,):
+        raise ValueError(f"distances must be (E,), got {tuple(r.shape)}")
+    if C.shape != (rank, L.cout, L.cin):
+        raise ValueError(f"channel_patterns must be ({rank}, {L.cout}, {L.cin}), got {tuple(C.shape)}")
+    if F.shape != (b.num_bins + 1, rank, L.wdim):
+        raise ValueError(f"radial functions must be ({b.num_bins + 1}, {rank}, {L.wdim}), "
+                         f"got {tuple(F.shape)}")
+
+
+def edgewise_linear(x, P, Q, dist, C, F, layout, binning, rank) -> torch.Tensor:
+    return EdgewiseLinearFn.apply(x, P, Q, dist, C, F, layout, binning, rank)
+
+
+# ---------------------------------------------------------------------------
+# generic block-diagonal op (reference table layout)
+# ---------------------------------------------------------------------------
+class BlockDiagonalFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, features, table, dist, layout: N.FeqLayout, binning: N.FeqBinning):
+        dev = _same_device(features, table, dist)
+        xs, ts, rs = _f32(features, "features"), _f32(table, "radial_table"), _f32(dist, "distances")
+        E = xs.shape[0]
+        if xs.shape[1:] != (layout.cin, layout.din):
+            raise ValueError(f"features must be (E, {layout.cin}, {layout.din}), got {tuple(xs.shape)}")
+        if ts.shape != (binning.num_bins + 1, layout.cout, layout.cin, layout.wdim):
+            raise ValueError(f"radial_table must be ({binning.num_bins + 1}, {layout.cout}, "
+                             f"{layout.cin}, {layout.wdim}), got {tuple(ts.shape)}")
+        y = torch.empty(E, layout.cout, layout.dout, dtype=torch.float32, device=dev)
+        if E:
+            with torch.cuda.device(dev):
+                rc = N.lib().feq_blockdiag_fwd(N.ctypes.byref(layout), N.ctypes.byref(binning), E,
+                                               N.ptr(xs), N.ptr(ts), N.ptr(rs), N.ptr(y), None, 0,
+                                               N.stream_ptr(dev))
+            N.check(rc, "feq_blockdiag_fwd")
+        ctx.save_for_backward(xs, ts, rs)
+        ctx.meta = (layout, binning, features.dtype, table.dtype, dist.dtype)
+        return y.to(features.dtype)
+
+    @staticmethod
+    def backward(ctx, gy):
+        xs, ts, rs = ctx.saved_tensors
+        layout, binning, xdt, tdt, rdt = ctx.meta
+        dev = xs.device
+        E = xs.shape[0]
+        g = gy.detach().to(torch.float32).contiguous()
+        gx = torch.empty_like(xs)
+        gt = torch.empty_like(ts)
+        gr = torch.empty_like(rs) if ctx.needs_input_grad[2] else None
+        with torch.cuda.device(dev):
+            rc = N.lib().feq_blockdiag_bwd(N.ctypes.byref(layout), N.ctypes.byref(binning), E,
+                                           N.ptr(g), N.ptr(xs), N.ptr(ts), N.ptr(rs), N.ptr(gx),
+                                           N.ptr(gt), N.ptr(gr), None, 0, N.stream_ptr(dev))
+        N.check(rc, "feq_blockdiag_bwd")
+        return gx.to(xdt), gt.to(tdt), (None if gr is None else gr.to(rdt)), None, None
+
+
+# ---------------------------------------------------------------------------
+# graph reductions
+# ---------------------------------------------------------------------------
+class SegmentSumFn(torch.autograd.Function):
+    """out[n] = sum_{e: dst[e]=n} x[e] over the cached CSR (GraphPooling 'sum')."""
+
+    @staticmethod
+    def forward(ctx, x, dst, perm, offsets, num_nodes: int):
+        dev = _same_device(x, dst, perm, offsets)
+        xs = _f32(x, "edge_features")
+        E = xs.shape[0]
+        row = int(xs[0].numel()) if E else int(torch.tensor(xs.shape[1:]).prod())
+        out = torch.empty((num_nodes,) + tuple(xs.shape[1:]), dtype=torch.float32, device=dev)
+        with torch.cuda.device(dev):
+            rc = N.lib().feq_segment_sum(N.ptr(xs) if E else None, row, N.ptr(perm) if E else None,
+                                         N.ptr(offsets), num_nodes, N.ptr(out), N.stream_ptr(dev))
+        N.check(rc, "feq_segment_sum")
+        ctx.save_for_backward(dst)
+        ctx.meta = (x.dtype, E, row, num_nodes, tuple(xs.shape))
+        return out.to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, gout):
+        (dst,) = ctx.saved_tensors
+        xdt, E, row, num_nodes, shape = ctx.meta
+        dev = dst.device
+        g = gout.detach().to(torch.float32).contiguous()
+        gx = torch.empty(shape, dtype=torch.float32, device=dev)
+        if E:
+            d64 = dst.to(torch.int64).contiguous()
+            with torch.cuda.device(dev):
+                rc = N.lib().feq_gather_rows(N.ptr(g), num_nodes, row, N.ptr(d64), E, N.ptr(gx),
+                                             N.stream_ptr(dev))
+            N.check(rc, "feq_gather_rows")
+        return gx.to(xdt), None, None, None, None
+
+
+class EdgeSoftmaxFn(torch.autograd.Function):
+    """Per-destination softmax of scale*<Q,K> (- r/decay) with +1e-8 (``attention.py:92-141``)."""
+
+    @staticmethod
+    def forward(ctx, Q, K, dist, log_scale, decay: float, perm, offsets, num_nodes: int):
+        dev = _same_device(Q, K, log_scale, perm, offsets)
+        Qs, Ks = _f32(Q, "Q"), _f32(K, "K")
+        E, H, Dh = Qs.shape
+        scale_t = log_scale.detach().float().exp()
+        rs = _f32(dist, "distances") if (dist is not None and decay > 0) else None
+        attn = torch.empty(E, H, dtype=torch.float32, device=dev)
+        qk = torch.empty(E, H, dtype=torch.float32, device=dev)
+        if E:
+            scale = _host_scalar(scale_t)
+            with torch.cuda.device(dev):
+                rc = N.lib().feq_edge_softmax_fwd(N.ptr(Qs), N.ptr(Ks), N.ptr(rs), E, H, Dh, scale,
+                                                  float(decay), N.ptr(perm), N.ptr(offsets),
+                                                  num_nodes, N.ptr(attn), N.ptr(qk),
+                                                  N.stream_ptr(dev))
+            N.check(rc, "feq_edge_softmax_fwd")
+        ctx.save_for_backward(Qs, Ks, attn, perm, offsets, scale_t)
+        ctx.meta = (decay, num_nodes, Q.dtype, K.dtype, None if dist is None else dist.dtype,
+                    log_scale.dtype)
+        return attn.to(Q.dtype)
+
+    @staticmethod
+    def backward(ctx, gattn):
+        Qs, Ks, attn, perm, offsets, scale_t = ctx.saved_tensors
+        decay, num_nodes, qdt, kdt, rdt, ldt = ctx.meta
+        dev = Qs.device
+        E, H, Dh = Qs.shape
+        need = ctx.needs_input_grad
+        ga = gattn.detach().to(torch.float32).contiguous()
+        gQ = torch.empty_like(Qs)
+        gK = torch.empty_like(Ks)
+        gls = torch.empty(E, dtype=torch.float32, device=dev)
+        gr = torch.empty(E, dtype=torch.float32, device=dev) if (need[2] and decay > 0) else None
+        if E:
+            with torch.cuda.device(dev):
+                rc = N.lib().feq_edge_softmax_bwd(N.ptr(Qs), N.ptr(Ks), N.ptr(attn), N.ptr(ga), E, H,
+                                                  Dh, _host_scalar(scale_t), float(decay),
+                                                  N.ptr(perm), N.ptr(offsets), num_nodes,
+                                                  N.ptr(gQ), N.ptr(gK), N.ptr(gls), N.ptr(gr),
+                                                  N.stream_ptr(dev))
+            N.check(rc, "feq_edge_softmax_bwd")
+        g_log = gls.sum().to(ldt) if need[3] else None
+        g_dist = None
+        if need[2]:
+            g_dist = gr.to(rdt) if gr is not None else None
+        return gQ.to(qdt), gK.to(kdt), g_dist, g_log, None, None, None, None
+
+
+def _host_scalar(t: torch.Tensor) -> float:
+    # The kernels take the softmax temperature by value; reading the
+    # one-element parameter is the only host synchronisation of the attention.
+    return float(t)
+
+
+class AttnPoolFn(torch.autograd.Function):
+    """out[n,c,:] = sum_{e->n} attn[e, head(c)] V[e,c,:] (``attention.py:143-167`` + sum pooling)."""
+
+    @staticmethod
+    def forward(ctx, V, attn, dst, perm, offsets, num_nodes: int, heads: int):
+        dev = _same_device(V, attn, dst, perm, offsets)
+        Vs, As = _f32(V, "V"), _f32(attn, "attention")
+        E, mult, dim = Vs.shape
+        out = torch.empty(num_nodes, mult, dim, dtype=torch.float32, device=dev)
+        with torch.cuda.device(dev):
+            rc = N.lib().feq_attn_pool_fwd(N.ptr(Vs) if E else None, N.ptr(As) if E else None, E,
+                                           mult, dim, heads, N.ptr(perm) if E else None,
+                                           N.ptr(offsets), num_nodes, N.ptr(out), N.stream_ptr(dev))
+        N.check(rc, "feq_attn_pool_fwd")
+        ctx.save_for_backward(Vs, As, dst)
+        ctx.meta = (num_nodes, heads, V.dtype, attn.dtype)
+        return out.to(V.dtype)
+
+    @staticmethod
+    def backward(ctx, gout):
+        Vs, As, dst = ctx.saved_tensors
+        num_nodes, heads, vdt, adt = ctx.meta
+        dev = Vs.device
+        E, mult, dim = Vs.shape
+        g = gout.detach().to(torch.float32).contiguous()
+        gV = torch.empty_like(Vs)
+        gA = torch.empty_like(As)
+        if E:
+            d64 = dst.to(torch.int64).contiguous()
+            with torch.cuda.device(dev):
+                rc = N.lib().feq_attn_pool_bwd(N.ptr(Vs), N.ptr(As), N.ptr(g), N.ptr(d64), E,
+                                               num_nodes, mult, dim, heads, N.ptr(gV), N.ptr(gA),
+                                               N.stream_ptr(dev))
+            N.check(rc, "feq_attn_pool_bwd")
+        return gV.to(vdt), gA.to(adt), None, None, None, None, None
+
+
+def bin_edges(dist: torch.Tensor, binning: N.FeqBinning) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(lo int32, t float32) per edge from the kernels' binning (for checks and tools)."""
+    dev = dist.device
+    rs = _f32(dist, "distances")
+    E = rs.shape[0]
+    lo = torch.empty(E, dtype=torch.int32, device=dev)
+    t = torch.empty(E, dtype=torch.float32, device=dev)
+    if E:
+        with torch.cuda.device(dev):
+            rc = N.lib().feq_bin_edges(N.ctypes.byref(binning), E, N.ptr(rs), N.ptr(lo), N.ptr(t),
+                                       N.stream_ptr(dev))
+        N.check(rc, "feq_bin_edges")
+    return lo, t

@@ -1,0 +1,30 @@
+"""Small numeric helpers shared by the layers.
+
+Mirrors the behaviour of the reference helpers in ``flash_eq/utils.py:8-27``
+(Xavier init for ``nn.Linear`` with zero bias; dtype-aware epsilon).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+_LOW_PRECISION = (torch.float16, torch.bfloat16)
+
+
+def init_linear_weights(module: nn.Module) -> None:
+    """Xavier-uniform weight and zero bias for every ``nn.Linear``.
+
+    Meant for ``module.apply(init_linear_weights)``; the RNG is consumed in
+    the same order as the reference (``utils.py:8-16``) so seeded
+    construction yields identical parameters.
+    """
+    if not isinstance(module, nn.Linear):
+        return
+    nn.init.xavier_uniform_(module.weight)
+    if module.bias is not None:
+        nn.init.zeros_(module.bias)
+
+
+def get_epsilon(dtype: torch.dtype) -> float:
+    """Stabilising epsilon: 1e-5 for 16-bit floats, 1e-8 otherwise (``utils.py:19-27``)."""
+    return 1e-5 if dtype in _LOW_PRECISION else 1e-8

@@ -1,0 +1,171 @@
+/*
+ * flasheq.h -- C ABI of the MI355X (gfx950) equivariant edge hot path.
+ *
+ * Plain pointers and sizes only.  Every device pointer is caller-owned memory
+ * (the Python host side allocates it through PyTorch's caching allocator);
+ * the library never allocates device memory.  Every entry point launches on
+ * the caller's stream, returns FEQ_OK (0) or an FEQ_ERR_* code, and leaves a
+ * human-readable message for feq_last_error() (thread-local).
+ *
+ * Reference interfaces replaced (paths are in the reference repository):
+ *   feq_layout_init          block-layout bookkeeping of precompute_block_info
+ *                            (flash_eq/cuda/csrc/block_diagonal.cu:1191-1266) and
+ *                            _compute_block_sizes (flash_eq/cuda/block_diagonal.py:181-203)
+ *   feq_bin_edges            compute_binning (block_diagonal.cu:82-115), exposed so
+ *                            bin ids can be checked bit-exactly
+ *   feq_blockdiag_fwd        pybind "forward"  -> block_diagonal_forward_cuda
+ *                            (block_diagonal.cu:1268-1282, 1758-1761)
+ *   feq_blockdiag_bwd        pybind "backward" -> block_diagonal_backward_cuda
+ *                            (block_diagonal.cu:1543-1558, 1758-1761)
+ *   feq_edgewise_fwd/_bwd    EquivariantEdgewiseLinear.forward = bmm(X,P) ->
+ *                            block_diagonal_cuda(rw()) -> bmm(.,Q^T)
+ *                            (flash_eq/layers/linear.py:100-160, radial.py:259-275),
+ *                            fused, with the radial table kept in its separable
+ *                            form T[b,o,i,w] = sum_k C[k,o,i] F[b,k,w]
+ *   feq_wigner_basis         WignerDBasis.forward / WignerD.rot_to_ez
+ *                            (flash_eq/representations/wigner.py:198-240, 341-370)
+ *   feq_csr_by_dst           grouping of edges by destination that the scatter
+ *                            ops of pooling.py:21-30 / attention.py:124-141 imply
+ *   feq_segment_sum          GraphPooling 'sum' forward (flash_eq/layers/pooling.py:21-30)
+ *   feq_gather_rows          its backward (index_select of the node gradient)
+ *   feq_edge_softmax_fwd/bwd EquivariantEdgeAttention logits + _neighbor_softmax
+ *                            (flash_eq/layers/attention.py:92-141)
+ *   feq_attn_pool_fwd/bwd    _apply_attention + GraphPooling 'sum'
+ *                            (flash_eq/layers/attention.py:143-167, pooling.py:21-30)
+ */
+#ifndef FLASHEQ_H
+#define FLASHEQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Opaque stream handle; pass a hipStream_t (torch.cuda.current_stream().cuda_stream). */
+typedef void* feq_stream_t;
+
+enum {
+    FEQ_OK = 0,
+    FEQ_ERR_INVALID = 1,      /* bad argument, shape or size */
+    FEQ_ERR_UNSUPPORTED = 2,  /* valid but outside this build's limits */
+    FEQ_ERR_HIP = 3,          /* a HIP runtime call failed */
+    FEQ_ERR_WORKSPACE = 4     /* workspace missing or too small */
+};
+
+#define FEQ_MAX_BLOCKS 17     /* m = 0..16: l <= 16 like the reference (block_diagonal.cu:172) */
+#define FEQ_MAX_SLOTS 128     /* components per representation (dim) */
+#define FEQ_MAX_IRREPS 32     /* irreps per representation */
+
+/* m-first block layout of one (in_repr, out_repr) pair. */
+typedef struct feq_layout {
+    int32_t cin, cout;                    /* multiplicities */
+    int32_t din, dout;                    /* representation dimensions */
+    int32_t wdim;                         /* radial weights per channel pair */
+    int32_t nblocks;                      /* non-empty m-blocks */
+    int32_t blk[FEQ_MAX_BLOCKS][6];       /* m, n_in, n_out, in_off, out_off, w_off */
+    int8_t lslot_in[FEQ_MAX_SLOTS];       /* l of every m-first input component */
+    int8_t lslot_out[FEQ_MAX_SLOTS];      /* l of every m-first output component */
+    int32_t has_lpos;                     /* any pair with l_in + l_out > 0 */
+} feq_layout;
+
+/* Distance binning: p1/p2 are SeparableRadialNet.binning_params() as float32. */
+typedef struct feq_binning {
+    float p1;          /* min_val (linear) or log(min_val) (log) */
+    float p2;          /* num_bins/(max-min) (linear) or 1/log(max/min) (log) */
+    int32_t num_bins;  /* table has num_bins + 1 rows */
+    int32_t log_bins;  /* 0 linear, 1 logarithmic */
+    float sh_scale;    /* solid-harmonic length scale sigma */
+} feq_binning;
+
+const char* feq_last_error(void);
+int feq_abi_version(void);
+
+/* Fill *out from the irrep degrees (host arrays, lvals order, duplicates allowed). */
+int feq_layout_init(feq_layout* out, const int32_t* lvals_in, int32_t n_in,
+                    const int32_t* lvals_out, int32_t n_out, int32_t cin, int32_t cout);
+
+/* Per-edge lower bin index and interpolation weight t (float32 path). */
+int feq_bin_edges(const feq_binning* b, int64_t num_edges, const float* dist,
+                  int32_t* lo, float* t, feq_stream_t stream);
+
+/* ---- generic block-diagonal op: table (num_bins+1, Cout, Cin, Wdim) ---------- */
+size_t feq_blockdiag_workspace(const feq_layout* L, const feq_binning* b, int64_t num_edges);
+int feq_blockdiag_fwd(const feq_layout* L, const feq_binning* b, int64_t num_edges,
+                      const float* x, const float* table, const float* dist, float* y,
+                      void* workspace, size_t ws_bytes, feq_stream_t stream);
+/* grad_dist may be NULL (not needed). grad_x / grad_table are overwritten. */
+int feq_blockdiag_bwd(const feq_layout* L, const feq_binning* b, int64_t num_edges,
+                      const float* grad_y, const float* x, const float* table, const float* dist,
+                      float* grad_x, float* grad_table, float* grad_dist,
+                      void* workspace, size_t ws_bytes, feq_stream_t stream);
+
+/* ---- fused EquivariantEdgewiseLinear (separable radial weights) ---------------
+ * x (E, Cin, Din) standard basis; P (E, Din, Din); Q (E, Dout, Dout);
+ * C (K, Cout, Cin) channel patterns; F (num_bins+1, K, Wdim) radial functions;
+ * y (E, Cout, Dout) standard basis.  y = (Lambda(r) (x P)) Q^T. */
+size_t feq_edgewise_workspace(const feq_layout* L, const feq_binning* b, int32_t rank,
+                              int64_t num_edges);
+int feq_edgewise_fwd(const feq_layout* L, const feq_binning* b, int32_t rank, int64_t num_edges,
+                     const float* x, const float* P, const float* Q, const float* dist,
+                     const float* C, const float* F, float* y,
+                     void* workspace, size_t ws_bytes, feq_stream_t stream);
+/* Outputs may be NULL when not needed: grad_x, grad_dist, grad_P, grad_Q.
+ * grad_C (K,Cout,Cin) and grad_F (num_bins+1,K,Wdim) are overwritten. */
+int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32_t rank, int64_t num_edges,
+                     const float* grad_y, const float* x, const float* P, const float* Q,
+                     const float* dist, const float* C, const float* F,
+                     float* grad_x, float* grad_C, float* grad_F, float* grad_dist,
+                     float* grad_P, float* grad_Q,
+                     void* workspace, size_t ws_bytes, feq_stream_t stream);
+
+/* ---- Wigner-D basis ------------------------------------------------------------
+ * plan: host-built per-representation constants (see feq_wigner_plan_size);
+ * out (E, dim, dim): column j = column perm[j] of D(g), g e_z = dir/|dir|. */
+size_t feq_wigner_plan_doubles(const int32_t* lvals, int32_t n);
+int feq_wigner_basis(const int32_t* lvals, int32_t n, const double* plan_dev,
+                     const int32_t* perm_dev, int64_t num_edges, const float* dirs,
+                     float* out, feq_stream_t stream);
+
+/* ---- graph ops -----------------------------------------------------------------
+ * CSR by destination: perm (E) lists edge ids grouped by dst in increasing
+ * order, stable within a node; offsets (N+1). */
+size_t feq_csr_workspace(int64_t num_edges, int64_t num_nodes);
+int feq_csr_by_dst(const int64_t* dst, int64_t num_edges, int64_t num_nodes,
+                   int32_t* perm, int32_t* offsets, void* workspace, size_t ws_bytes,
+                   feq_stream_t stream);
+/* out[n, :] = sum over the node's edges (perm order) of x[e, :]; row = C*D floats. */
+int feq_segment_sum(const float* x, int64_t row, const int32_t* perm, const int32_t* offsets,
+                    int64_t num_nodes, float* out, feq_stream_t stream);
+/* out[e, :] = src[idx[e], :] for 0 <= idx[e] < num_src, else 0. */
+int feq_gather_rows(const float* src, int64_t num_src, int64_t row, const int64_t* idx,
+                    int64_t num_rows, float* out, feq_stream_t stream);
+
+/* logits[e,h] = scale * <Q[e,h,:], K[e,h,:]> - dist[e]/decay (decay <= 0: none);
+ * attn = per-destination softmax with max shift and +1e-8 in the denominator.
+ * Q, K (E, H, Dh).  logits_out may be NULL. */
+int feq_edge_softmax_fwd(const float* Q, const float* K, const float* dist, int64_t num_edges,
+                         int32_t heads, int32_t head_dim, float scale, float decay,
+                         const int32_t* perm, const int32_t* offsets, int64_t num_nodes,
+                         float* attn, float* qk_out, feq_stream_t stream);
+/* Given grad_attn (E,H): grad_Q, grad_K (E,H,Dh); grad_logscale_partial (E) holds
+ * sum_h glogit*scale*<Q,K> per edge (nullable); grad_dist (nullable). */
+int feq_edge_softmax_bwd(const float* Q, const float* K, const float* attn, const float* grad_attn,
+                         int64_t num_edges, int32_t heads, int32_t head_dim, float scale, float decay,
+                         const int32_t* perm, const int32_t* offsets, int64_t num_nodes,
+                         float* grad_Q, float* grad_K, float* grad_logscale_partial,
+                         float* grad_dist, feq_stream_t stream);
+/* out[n,c,:] = sum_{e in seg(n)} attn[e, c / (mult/H)] * V[e,c,:]; V (E, mult, dim). */
+int feq_attn_pool_fwd(const float* V, const float* attn, int64_t num_edges, int32_t mult,
+                      int32_t dim, int32_t heads, const int32_t* perm, const int32_t* offsets,
+                      int64_t num_nodes, float* out, feq_stream_t stream);
+/* grad_V[e] = attn[e,h(c)] * gout[dst[e]]; grad_attn[e,h] = sum_{c in h, d} V*gout[dst]. */
+int feq_attn_pool_bwd(const float* V, const float* attn, const float* grad_out, const int64_t* dst,
+                      int64_t num_edges, int64_t num_nodes, int32_t mult, int32_t dim, int32_t heads,
+                      float* grad_V, float* grad_attn, feq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FLASHEQ_H */

@@ -1,0 +1,187 @@
+"""GPU parity of the fused EquivariantEdgewiseLinear against the float64 oracle.
+
+The oracle composes bmm(x, P) -> block-diagonal mix with the materialised
+SeparableRadialNet table (explicit reference backward) -> bmm(., Q^T); the
+product runs one fused HIP kernel per direction with the separable factors.
+Gradients compared: edge features, distances, P, Q and every radial-network
+parameter.  Equivariance is reported with the reference's metric.
+"""
+import pytest
+import torch
+
+import flash_eq as fe
+from helpers import equivariance_err, rel_err
+from oracle import layer as OL
+from oracle import wigner as OW
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def _inputs(lin, lout, E, cin, seed, rmax=12.0, rmin=0.0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(E, cin, sum(2 * l + 1 for l in lin), generator=g)
+    d = torch.randn(E, 3, generator=g)
+    r = torch.rand(E, generator=g) * (rmax - rmin) + rmin
+    gy_seed = torch.Generator().manual_seed(seed + 1)
+    return x, d, r, gy_seed
+
+
+def _run_parity(dev, lin, lout, cin, cout, E, seed=0, log=False, grad_pq=False, rmin=0.0):
+    torch.manual_seed(seed)
+    kw = dict(log_bins=True, min_dist=0.5) if log else {}
+    layer = fe.EquivariantEdgewiseLinear(fe.Repr(lin, cin), fe.Repr(lout, cout), num_bins=50, **kw)
+    x, d, r, g = _inputs(lin, lout, E, cin, seed, rmin=rmin)
+    P = OW.basis(lin, d).float()
+    Q = OW.basis(lout, d).float()
+    layer = layer.to(dev)
+    xg = x.to(dev).requires_grad_(True)
+    rg = r.to(dev).requires_grad_(True)
+    Pg = P.to(dev).requires_grad_(grad_pq)
+    Qg = Q.to(dev).requires_grad_(grad_pq)
+    y = layer(Pg, Qg, xg, rg)
+    params, cfg = OL.module_cfg(layer)
+    xd, rd = x.double().requires_grad_(True), r.double().requires_grad_(True)
+    Pd, Qd = P.double().requires_grad_(grad_pq), Q.double().requires_grad_(grad_pq)
+    yref = OL.edgewise_linear(xd, Pd, Qd, rd, params, cfg)
+    assert y.shape == yref.shape
+    assert rel_err(y, yref) < TOL, rel_err(y, yref)
+    gy = torch.randn(y.shape, generator=g)
+    y.backward(gy.to(dev))
+    yref.backward(gy.double())
+    assert rel_err(xg.grad, xd.grad) < TOL
+    assert rel_err(rg.grad, rd.grad) < 1e-4
+    for name, p in layer.radial_weights.named_parameters():
+        assert rel_err(p.grad, params[name].grad) < TOL, name
+    if grad_pq:
+        assert rel_err(Pg.grad, Pd.grad) < TOL
+        assert rel_err(Qg.grad, Qd.grad) < TOL
+
+
+@pytest.mark.parametrize("lin,lout", [([0, 1, 2], [0, 1, 2]), ([0, 1], [0, 1, 2]), ([1, 2], [0, 1]),
+                                      ([0, 1, 1], [0, 1, 2]), ([1, 2, 2], [0, 1]), ([2], [0, 1, 2]),
+                                      ([0], [0]), ([1, 2, 3], [1, 2, 3])])
+def test_edgewise_parity(dev, lin, lout):
+    _run_parity(dev, lin, lout, cin=6, cout=5, E=400)
+
+
+def test_edgewise_parity_c1_shape(dev):
+    """BASELINE config 1 layer shape: [0,1]x32 -> [0,1,2]x64, E=500."""
+    _run_parity(dev, [0, 1], [0, 1, 2], cin=32, cout=64, E=500, seed=1)
+
+
+def test_edgewise_parity_c2_shape(dev):
+    """BASELINE config 2 layer shape ([0,1,2]x64, num_bins=100 range) at a reduced E."""
+    _run_parity(dev, [0, 1, 2], [0, 1, 2], cin=64, cout=64, E=1500, seed=2)
+
+
+def test_edgewise_parity_log_bins(dev):
+    _run_parity(dev, [0, 1, 2], [0, 1], cin=8, cout=8, E=600, seed=3, log=True, rmin=0.1)
+
+
+def test_edgewise_grad_wrt_basis(dev):
+    _run_parity(dev, [0, 1], [0, 1, 2], cin=4, cout=3, E=200, seed=4, grad_pq=True)
+
+
+def test_edgewise_empty_and_single_edge(dev):
+    r4 = fe.Repr([0, 1, 2], 4)
+    layer = fe.EquivariantEdgewiseLinear(r4, r4).to(dev)
+    P = torch.zeros(0, 9, 9, device=dev)
+    out = layer(P, P, torch.zeros(0, 4, 9, device=dev), torch.zeros(0, device=dev))
+    assert out.shape == (0, 4, 9)
+    _run_parity(dev, [0, 1, 2], [0, 1, 2], cin=4, cout=4, E=1, seed=5)
+
+
+def test_zero_distance_self_loop(dev):
+    """r = 0: l>0 outputs vanish (test_self_loops.py:42-66), dr is NaN like the reference."""
+    torch.manual_seed(6)
+    r4 = fe.Repr([0, 1, 2], 4)
+    layer = fe.EquivariantEdgewiseLinear(r4, r4).to(dev)
+    E = 8
+    d = torch.randn(E, 3)
+    P = OW.basis([0, 1, 2], d).float().to(dev)
+    x = torch.randn(E, 4, 9, device=dev)
+    r = torch.rand(E, device=dev) * 5 + 0.5
+    r[0] = 0.0
+    rg = r.clone().requires_grad_(True)
+    y = layer(P, P, x, rg)
+    assert y[0, :, 1:].abs().max() < 1e-6 and y[0, :, 0].abs().max() > 1e-3
+    (y ** 2).sum().backward()
+    assert torch.isnan(rg.grad[0]) and torch.isfinite(rg.grad[1:]).all()
+
+
+def test_out_of_range_distances_extrapolate(dev):
+    _run_parity(dev, [0, 1], [0, 1], cin=4, cout=4, E=300, seed=7)   # r up to 12 > max_dist 10
+
+
+@pytest.mark.parametrize("lin,lout", [([0, 1, 2], [0, 1, 2]), ([0, 1], [0, 1, 2]), ([1, 2, 2], [0, 1])])
+def test_equivariance(dev, lin, lout):
+    """Reference protocol (test_equivariance.py:47-99): rotate inputs and directions."""
+    torch.manual_seed(42)
+    mult, N, E = 4, 20, 50
+    rin, rout = fe.Repr(lin, mult), fe.Repr(lout, mult)
+    layer = fe.EquivariantEdgewiseLinear(rin, rout, num_bins=50).to(dev)
+    basis = fe.WignerDBasis([rin, rout]).to(dev)
+    nf = torch.randn(N, mult, rin.dim(), device=dev)
+    src = torch.randint(0, N, (E,), device=dev)
+    r = torch.rand(E, device=dev) * 5
+    dirs = torch.randn(E, 3, device=dev)
+    dirs = dirs / dirs.norm(dim=-1, keepdim=True)
+    axis, angle = fe.random_rotation(device=dev)
+    D_in = fe.WignerD(rin).to(dev).rot(axis, angle)
+    D_out = fe.WignerD(rout).to(dev).rot(axis, angle)
+    R = fe.WignerD(fe.Repr([1])).to(dev).rot(axis, angle, cartesian=True)
+    P, Q = basis(dirs)
+    out1 = torch.einsum("ij,ecj->eci", D_out, layer(P, Q, nf[src], r))
+    P2, Q2 = basis(dirs @ R.T)
+    out2 = layer(P2, Q2, torch.einsum("ij,ncj->nci", D_in, nf)[src], r)
+    err = equivariance_err(out1, out2)
+    print(f"equivariance error {lin}->{lout}: {err:.2e}")
+    assert err < 1e-4
+
+
+def test_gradient_equivariance(dev):
+    torch.manual_seed(101)
+    lv, mult, N, E = [0, 1, 2], 4, 10, 30
+    rp = fe.Repr(lv, mult)
+    layer = fe.EquivariantEdgewiseLinear(rp, rp, num_bins=50).to(dev)
+    basis = fe.WignerDBasis([rp]).to(dev)
+    axis, angle = fe.random_rotation(device=dev)
+    D = fe.WignerD(rp).to(dev).rot(axis, angle)
+    R = fe.WignerD(fe.Repr([1])).to(dev).rot(axis, angle, cartesian=True)
+    src = torch.randint(0, N, (E,), device=dev)
+    r = torch.rand(E, device=dev) * 5
+    dirs = torch.randn(E, 3, device=dev)
+    (P,) = basis(dirs)
+    nf = torch.randn(N, mult, 9, device=dev, requires_grad=True)
+    (layer(P, P, nf[src], r) ** 2).sum().backward()
+    g1 = torch.einsum("ij,ncj->nci", D, nf.grad)
+    nf2 = torch.einsum("ij,ncj->nci", D, nf.detach()).requires_grad_(True)
+    (P2,) = basis(dirs @ R.T)
+    (layer(P2, P2, nf2[src], r) ** 2).sum().backward()
+    assert equivariance_err(g1, nf2.grad) < 1e-4
+
+
+def test_distance_gradient_finite_difference(dev):
+    """dL/dr vs central differences (test_equivariance.py:324-395 protocol), linear and log bins."""
+    for log in (False, True):
+        torch.manual_seed(123)
+        rp = fe.Repr([0, 1], 2)
+        kw = dict(log_bins=True, min_dist=0.5) if log else {}
+        layer = fe.EquivariantEdgewiseLinear(rp, rp, num_bins=50, max_dist=10.0, **kw).to(dev)
+        E = 10
+        (P,) = fe.WignerDBasis([rp]).to(dev)(torch.randn(E, 3, device=dev))
+        x = torch.randn(E, 2, 4, device=dev)
+        r = torch.rand(E, device=dev) * 5.0 + (0.5 if log else 0.0) + 0.5
+        rg = r.clone().requires_grad_(True)
+        (layer(P, P, x, rg) ** 2).sum().backward()
+        eps = 1e-3
+        fd = torch.zeros(E, device=dev)
+        with torch.no_grad():
+            for i in range(E):
+                rp_, rm_ = r.clone(), r.clone()
+                rp_[i] += eps
+                rm_[i] -= eps
+                fd[i] = ((layer(P, P, x, rp_) ** 2).sum() - (layer(P, P, x, rm_) ** 2).sum()) / (2 * eps)
+        rel = ((rg.grad - fd).abs() / (fd.abs() + 1e-8)).max().item()
+        assert rel < 0.10, (log, rel)

@@ -1,0 +1,67 @@
+"""The C-ABI library loads on a GPU-less host and exports every symbol of include/flasheq.h.
+
+No compute calls here: only host-side entry points (layout construction,
+size queries, error reporting).
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+from flash_eq import _native as N
+from oracle import layout as OL
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "flasheq.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(feq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = N.load_library()
+    names = declared_functions()
+    assert len(names) >= 20
+    for name in names:
+        assert hasattr(lib, name), f"{name} not exported"
+    assert set(names) == set(N.EXPORTED_SYMBOLS), "ctypes signatures out of sync with the header"
+
+
+def test_abi_version():
+    assert N.load_library().feq_abi_version() == 1
+
+
+CONFIGS = [([0, 1, 2], [0, 1, 2]), ([0, 1], [0, 1, 2]), ([1, 2, 2], [0, 1]), ([0, 1], [2]),
+           ([2], [0, 1, 2]), (list(range(7)), list(range(7))), ([0, 0], [0, 0]), ([3, 1], [0])]
+
+
+@pytest.mark.parametrize("lin,lout", CONFIGS)
+def test_layout_matches_oracle(lin, lout):
+    L = N.make_layout(lin, lout, 5, 7)
+    assert (L.cin, L.cout, L.din, L.dout) == (5, 7, OL.dim_of(lin), OL.dim_of(lout))
+    assert L.wdim == OL.weight_dim(lin, lout)
+    blocks = [tuple(L.blk[k]) for k in range(L.nblocks)]
+    assert blocks == OL.block_params(lin, lout)
+    assert list(L.lslot_in[:L.din]) == OL.slot_l(lin)
+    assert list(L.lslot_out[:L.dout]) == OL.slot_l(lout)
+    assert L.has_lpos == int(max(lin) + max(lout) > 0)
+
+
+def test_layout_errors():
+    with pytest.raises(RuntimeError, match="exceeds supported limit"):
+        N.make_layout([17], [0], 1, 1)
+    with pytest.raises(RuntimeError, match="dimension exceeds"):
+        N.make_layout([16, 16, 16, 16, 16], [0], 1, 1)
+
+
+def test_size_queries_need_no_gpu():
+    lib = N.load_library()
+    L = N.make_layout([0, 1, 2], [0, 1, 2], 64, 64)
+    b = N.make_binning(0.0, 10.0, 100, False, 0.1)
+    assert lib.feq_edgewise_workspace(ctypes.byref(L), ctypes.byref(b), 4, 160000) > 0
+    assert lib.feq_csr_workspace(1000, 100) > 0
+    lv = (ctypes.c_int32 * 3)(0, 1, 2)
+    assert lib.feq_wigner_plan_doubles(lv, 3) == (1 + 2) + (9 + 6) + (25 + 10)
