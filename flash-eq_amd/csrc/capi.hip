@@ -1,6 +1,7 @@
 // Library-level C ABI: errors, version, layout construction, edge binning.
 #include "feq_internal.h"
 
+#include <cstdlib>
 #include <cstring>
 
 namespace feq {
@@ -35,6 +36,11 @@ int check_layout(const feq_layout* L) {
     if (L->nblocks <= 0 || L->nblocks > FEQ_MAX_BLOCKS)
         return fail(FEQ_ERR_INVALID, "layout has %d m-blocks", L->nblocks);
     return FEQ_OK;
+}
+
+bool force_generic() {
+    const char* v = getenv("FEQ_FORCE_GENERIC");
+    return v && v[0] == '1';
 }
 
 int check_binning(const feq_binning* b) {

@@ -391,10 +391,12 @@ int groups_for(int64_t E) { return static_cast<int>(E < kBwdGroups ? (E > 0 ? E 
 
 using namespace feq;
 
-extern "C" size_t feq_edgewise_workspace(const feq_layout* L, const feq_binning*, int32_t rank,
+extern "C" size_t feq_edgewise_workspace(const feq_layout* L, const feq_binning* b, int32_t rank,
                                          int64_t E) {
     if (!L || rank < 1) return 0;
-    return sizeof(float) * static_cast<size_t>(groups_for(E)) * rank * L->cout * L->cin + 256;
+    const size_t generic = sizeof(float) * static_cast<size_t>(groups_for(E)) * rank * L->cout * L->cin + 256;
+    const size_t fast = b ? ew_mfma_bwd_workspace(*L, *b, rank, E) : 0;
+    return generic > fast ? generic : fast;
 }
 
 extern "C" int feq_edgewise_fwd(const feq_layout* L, const feq_binning* b, int32_t rank,
@@ -408,6 +410,10 @@ extern "C" int feq_edgewise_fwd(const feq_layout* L, const feq_binning* b, int32
     if (E == 0) return FEQ_OK;
     if (E > 0x7fffffffLL) return fail(FEQ_ERR_UNSUPPORTED, "more than 2^31-1 edges");
     if (!x || !P || !Q || !dist || !C || !F || !y) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (!force_generic()) {
+        const int rc = ew_mfma_fwd(*L, *b, rank, E, x, P, Q, dist, C, F, y, stream_of(stream));
+        if (rc != -1) return rc;
+    }
     const size_t lds = fwd_lds(*L, rank);
     if (int rc = ensure_lds(reinterpret_cast<const void*>(&k_ew_fwd), lds)) return rc;
     EwDims D{rank, b->num_bins};
@@ -436,6 +442,11 @@ extern "C" int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32
     if (!gy || !x || !P || !Q || !dist || !C || !F) return fail(FEQ_ERR_INVALID, "NULL pointer");
     if (!ws || ws_bytes < feq_edgewise_workspace(L, b, rank, E))
         return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
+    if (!force_generic() && !gP && !gQ) {
+        const int rc = ew_mfma_bwd(*L, *b, rank, E, gy, x, P, Q, dist, C, F, gx, gC, gF, gdist, ws,
+                                   ws_bytes, s);
+        if (rc != -1) return rc;
+    }
     const size_t lds = bwd_lds(*L, rank);
     if (int rc = ensure_lds(reinterpret_cast<const void*>(&k_ew_bwd), lds)) return rc;
     const int G = groups_for(E);

@@ -40,6 +40,22 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 // Zero-fill by kernel (never hipMemsetAsync: callers may capture the stream).
 int fill_zero(float* p, int64_t n, hipStream_t s);
 
+// Fast paths of the fused edgewise layer for compile-time shapes
+// (edgewise_mfma.hip).  They return -1 when the shape has no instantiation.
+int ew_mfma_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
+                const float* P, const float* Q, const float* dist, const float* C, const float* F,
+                float* y, hipStream_t s);
+
+size_t ew_mfma_bwd_workspace(const feq_layout& L, const feq_binning& B, int rank, int64_t E);
+int ew_mfma_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* gy,
+                const float* x, const float* P, const float* Q, const float* dist, const float* C,
+                const float* F, float* gx, float* gC, float* gF, float* gdist, void* ws,
+                size_t ws_bytes, hipStream_t s);
+
+// FEQ_FORCE_GENERIC=1 in the environment selects the shape-generic kernels
+// (used by the tests to check both implementations).
+bool force_generic();
+
 // Checks shared by every layout-consuming entry point.
 int check_layout(const feq_layout* L);
 int check_binning(const feq_binning* b);

@@ -65,14 +65,60 @@ def test_edgewise_parity(dev, lin, lout):
     _run_parity(dev, lin, lout, cin=6, cout=5, E=400)
 
 
-def test_edgewise_parity_c1_shape(dev):
+@pytest.fixture(params=["fast", "generic"])
+def impl(request, monkeypatch):
+    """Run with the shape-specialised MFMA kernels (default) or force the generic ones."""
+    if request.param == "generic":
+        monkeypatch.setenv("FEQ_FORCE_GENERIC", "1")
+    else:
+        monkeypatch.delenv("FEQ_FORCE_GENERIC", raising=False)
+    return request.param
+
+
+def test_edgewise_parity_c1_shape(dev, impl):
     """BASELINE config 1 layer shape: [0,1]x32 -> [0,1,2]x64, E=500."""
     _run_parity(dev, [0, 1], [0, 1, 2], cin=32, cout=64, E=500, seed=1)
 
 
-def test_edgewise_parity_c2_shape(dev):
+def test_edgewise_parity_c2_shape(dev, impl):
     """BASELINE config 2 layer shape ([0,1,2]x64, num_bins=100 range) at a reduced E."""
     _run_parity(dev, [0, 1, 2], [0, 1, 2], cin=64, cout=64, E=1500, seed=2)
+
+
+def test_edgewise_parity_c2_ragged_tiles(dev, impl):
+    """E not a multiple of the 16-edge tile; permuted lvals with the c2 dimensions."""
+    _run_parity(dev, [0, 1, 2], [0, 1, 2], cin=64, cout=64, E=4003, seed=8)
+    _run_parity(dev, [2, 0, 1], [1, 2, 0], cin=64, cout=64, E=37, seed=9)
+
+
+def test_fast_and_generic_agree_at_scale(dev, monkeypatch):
+    """c2 shape at E = 40,000: the MFMA path against the generic kernels (float32 both)."""
+    torch.manual_seed(3)
+    rp = fe.Repr([0, 1, 2], 64)
+    layer = fe.EquivariantEdgewiseLinear(rp, rp).to(dev)
+    E = 40000
+    g = torch.Generator().manual_seed(10)
+    (P,) = fe.WignerDBasis([rp]).to(dev)(torch.randn(E, 3, generator=g).to(dev))
+    x = torch.randn(E, 64, 9, generator=g).to(dev)
+    r = (torch.rand(E, generator=g) * 11).to(dev)
+    gy = torch.randn(E, 64, 9, generator=g).to(dev)
+    outs = {}
+    for mode in ("fast", "generic"):
+        if mode == "generic":
+            monkeypatch.setenv("FEQ_FORCE_GENERIC", "1")
+        else:
+            monkeypatch.delenv("FEQ_FORCE_GENERIC", raising=False)
+        layer.zero_grad()
+        xg, rg = x.clone().requires_grad_(True), r.clone().requires_grad_(True)
+        y = layer(P, P, xg, rg)
+        y.backward(gy)
+        outs[mode] = (y.detach(), xg.grad, rg.grad,
+                      [p.grad.clone() for p in layer.radial_weights.parameters()])
+    a, b = outs["fast"], outs["generic"]
+    assert rel_err(a[0], b[0]) < 2e-6 and rel_err(a[1], b[1]) < 2e-6
+    assert rel_err(a[2], b[2]) < 2e-5
+    for pa, pb in zip(a[3], b[3]):
+        assert rel_err(pa, pb) < 2e-5
 
 
 def test_edgewise_parity_log_bins(dev):
