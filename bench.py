@@ -7,17 +7,21 @@ N = 10,000 nodes uniform in a 40^3 cube, k = 16 nearest neighbours
 max_dist = 10, num_bins = 100.  Node features (N, 64, 9) ~ N(0,1) are gathered
 to edges by src.  One step = gather + layer forward + (out**2).sum() +
 backward into the node features and every layer parameter.  P = Q come from
-WignerDBasis outside the timed region.
+WignerDBasis outside the timed region (as in the reference's benchmark,
+benchmarks/compare_all.py:168).
 
-Prints one JSON line (driver contract) with edges/s, the roofline of the
-dominant kernel (timed live with HIP events on the launch stream) and the
-CPU-oracle baseline timed on a bounded sample on this host.
+Prints one JSON line (driver contract).  ``roofline`` describes the dominant
+library kernel: its launches are bracketed with HIP events on their own
+stream during the timed steps (feq_profile_enable), and its achieved rate is
+the algorithmic work per launch (per-edge figures below x E) over the mean
+launch duration.  ``cpu_baseline`` times the float32 CPU oracle on this host.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -29,8 +33,10 @@ for _p in (ROOT, os.path.join(ROOT, "flash-eq_amd")):
 import numpy as np
 import torch
 
-PEAK_FP32_TFLOPS = 157.3      # MI355X dense fp32 (matrix) peak
-PEAK_HBM_GBS = 8000.0
+PEAK_FP32_TFLOPS = 157.3      # MI355X dense fp32 matrix peak
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+METRIC = "edges/s fwd+bwd, edgewise linear L=2 mult=64; % of HBM/MFMA roofline"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "edgewise_c2_hbm_traffic.md")
 
 
 def knn_graph(n: int, k: int, box: float, seed: int):
@@ -46,37 +52,56 @@ def knn_graph(n: int, k: int, box: float, seed: int):
     return coords, src, dst
 
 
-def edgewise_flops(cin, cout, din, dout, rank, mcount, backward=True):
-    """Algorithmic MAC count per edge of the fused separable formulation (x2 = flop)."""
-    gemm = rank * cout * cin * dout
-    small = rank * cin * mcount
-    fwd = cin * din * din + small + gemm + cout * dout * dout
-    bwd = cout * dout * dout + gemm + small + gemm + small + small + cin * din * din + cin * din * din
-    return 2 * fwd, 2 * bwd
+def algorithmic_per_edge(lin, lout, cin, cout, same_pq=True):
+    """Algorithmic flop and HBM bytes per edge of each fused kernel (fp32).
+
+    The mix of one (co, ci) pair costs M real MACs, M = n0_in n0_out +
+    2 sum_{m>=1} 2 n_in(m) n_out(m); a rotation of one channel costs
+    S = sum (2l+1)^2 MACs (P and Q are block diagonal over irreps).  Bytes are
+    the tensors each kernel must move once: x, P (= Q), r, y for the forward;
+    gy, x, P, r, gx for the input-gradient kernel; gy, x, P, r for the
+    channel-pattern-gradient kernel.  The distance-gradient mix is excluded
+    (the benchmark does not differentiate the distances).
+    """
+    mmax = max(max(lin), max(lout))
+    M = 0
+    for m in range(mmax + 1):
+        ni = sum(1 for l in lin if l >= m)
+        no = sum(1 for l in lout if l >= m)
+        M += ni * no if m == 0 else 4 * ni * no
+    s_in = sum((2 * l + 1) ** 2 for l in lin)
+    s_out = sum((2 * l + 1) ** 2 for l in lout)
+    din = sum(2 * l + 1 for l in lin)
+    dout = sum(2 * l + 1 for l in lout)
+    mix = 2 * cout * cin * M
+    rot = 2 * cin * s_in + 2 * cout * s_out
+    X, Y = 4 * cin * din, 4 * cout * dout
+    PQ = 4 * din * din + (0 if same_pq else 4 * dout * dout)
+    return {
+        "k_ewc_fwd": (mix + rot, X + PQ + 4 + Y),
+        "k_ewc_bwd_x": (mix + rot, Y + X + PQ + 4 + X),
+        "k_ewc_bwd_c": (mix, Y + X + PQ + 4),
+        "_mix_macs_per_pair": M,
+    }
 
 
-def edgewise_bytes(cin, cout, din, dout):
-    """Algorithmic HBM bytes per edge: x, P, Q, r in and y out (fwd); + gy in, gx out (bwd)."""
-    fwd = 4 * (cin * din + din * din + dout * dout + 1 + cout * dout)
-    bwd = 4 * (cout * dout + cin * din + din * din + dout * dout + 1 + cin * din)
-    return fwd, bwd
+def read_traffic(path: str = TRAFFIC_FILE) -> dict:
+    """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE.
+
+    Parsed from the committed summary: rows ``| kernel | fetch_bytes | write_bytes | ...``.
+    """
+    out = {}
+    if not os.path.exists(path):
+        return out
+    for line in open(path):
+        m = re.match(r"\|\s*(k_\w+)\s*\|\s*([0-9.e+]+)\s*\|\s*([0-9.e+]+)\s*\|", line)
+        if m:
+            out[m.group(1)] = float(m.group(2)) + float(m.group(3))
+    return out
 
 
-def time_events(fn, reps: int) -> float:
-    """Mean milliseconds of fn() measured with HIP events on the current stream."""
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(reps):
-        fn()
-    stop.record()
-    stop.synchronize()
-    return start.elapsed_time(stop) / reps
-
-
-def cpu_baseline(layer, feats, src, dst, coords, sample_edges: int, reps: int = 3):
-    """Oracle (bin-grouped BLAS restatement, float32 on CPU) fwd+bwd on the first edges."""
+def cpu_baseline(layer, feats, src, dst, coords, sample_edges: int, reps: int):
+    """Float32 CPU oracle (bin-grouped BLAS restatement) fwd+bwd on the first edges."""
     from oracle import layer as OL
     from oracle import wigner as OW
     torch.set_num_threads(min(os.cpu_count() or 1, 16))
@@ -96,7 +121,17 @@ def cpu_baseline(layer, feats, src, dst, coords, sample_edges: int, reps: int = 
         dt = time.perf_counter() - t0
         if it:
             times.append(dt)
-    return sample_edges / float(np.median(times)), torch.get_num_threads()
+    return sample_edges / float(np.median(times)), torch.get_num_threads(), times
+
+
+def copy_calibration(dev, nbytes: int = 1 << 30, reps: int = 3) -> None:
+    """Plain device-to-device copies of a known size (reference for the --pmc byte counters)."""
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(f"copy calibration: {reps} copies of {nbytes} bytes", file=sys.stderr)
 
 
 def main() -> int:
@@ -104,17 +139,23 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--cpu-sample", type=int, default=40000, help="edges in the CPU baseline sample")
+    ap.add_argument("--cpu-sample", type=int, default=160000, help="edges in the CPU baseline sample")
+    ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--grad-dist", action="store_true", help="also differentiate w.r.t. distances")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run 1 GiB device copies first (for rocprofv3 --pmc byte calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
-              "multi-GPU path.", file=sys.stderr)
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
+              "multi-GPU path; run it with --gpus 1.", file=sys.stderr)
         return 2
     import flash_eq as fe
+    from flash_eq import _native as NAT
 
     dev = torch.device("cuda", 0)
+    if args.copy_calibration:
+        copy_calibration(dev)
     N, K_NN, BOX, MULT = 10000, 16, 40.0, 64
     coords, src, dst = knn_graph(N, K_NN, BOX, seed=1002)
     E = src.numel()
@@ -138,54 +179,63 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    NAT.profile_summary()                      # drop anything recorded so far
+    NAT.profile_enable(True)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ms_ev = time_events(step, args.steps)
+    start.record()
+    for _ in range(args.steps):
+        step()
+    stop.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    NAT.profile_enable(False)
+    kern = NAT.profile_summary()
     ms_per_step = wall * 1e3 / args.steps
+    ms_events = start.elapsed_time(stop) / args.steps
 
-    # ---- dominant-kernel timing (forward and backward kernels in isolation) ----
-    from flash_eq.ops import EdgewiseLinearFn
-    rw = layer.radial_weights
-    C, F = rw.channel_patterns.detach(), rw.radial_functions().detach()
-    L, B = layer.layout(), layer.binning()
-    xe = feats.detach()[src_d].contiguous()
-    with torch.no_grad():
-        y0 = EdgewiseLinearFn.apply(xe, P, P, dist.detach(), C, F, L, B, rw.rank)
-    fwd_ms = time_events(lambda: EdgewiseLinearFn.apply(xe, P, P, dist.detach(), C, F, L, B, rw.rank), 10)
-    xr = xe.clone().requires_grad_(True)
-    out = EdgewiseLinearFn.apply(xr, P, P, dist.detach(), C, F, L, B, rw.rank)
-    gy = torch.randn_like(out)
-    bwd_ms = time_events(lambda: torch.autograd.grad(out, xr, gy, retain_graph=True), 5)
-    mcount = 9 + 4 * (2 * 2 + 1 * 1)
-    f_fwd, f_bwd = edgewise_flops(MULT, MULT, 9, 9, rw.rank, mcount)
-    b_fwd, b_bwd = edgewise_bytes(MULT, MULT, 9, 9)
-    dom = "bwd" if bwd_ms >= fwd_ms else "fwd"
-    dom_ms = max(bwd_ms, fwd_ms)
-    dom_flops = (f_bwd if dom == "bwd" else f_fwd) * E
-    dom_bytes = (b_bwd if dom == "bwd" else b_fwd) * E
-    achieved = dom_flops / (dom_ms * 1e-3) / 1e12
+    work = algorithmic_per_edge([0, 1, 2], [0, 1, 2], MULT, MULT)
+    traffic = read_traffic()
+    per_kernel = {}
+    for name, (calls, tot) in kern.items():
+        avg = tot / calls
+        entry = {"launches": calls, "avg_ms": round(avg, 4), "ms_per_step": round(tot / args.steps, 4)}
+        if name in work:
+            fl, by = work[name]
+            entry["tflops"] = round(fl * E / (avg * 1e-3) / 1e12, 2)
+            entry["frac_fp32_peak"] = round(fl * E / (avg * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4)
+            entry["hbm_gbs_algorithmic"] = round(by * E / (avg * 1e-3) / 1e9, 1)
+        per_kernel[name] = entry
+    dom = max((n for n in kern if n in work), key=lambda n: kern[n][1])
+    calls, tot = kern[dom]
+    avg_ms = tot / calls
+    fl, by = work[dom]
+    achieved = fl * E / (avg_ms * 1e-3) / 1e12
     roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": None,
-                "kernel": f"edgewise_{dom}", "kernel_ms": round(dom_ms, 4),
-                "algorithmic_flop_per_edge": (f_bwd if dom == "bwd" else f_fwd),
-                "algorithmic_bytes_per_edge": (b_bwd if dom == "bwd" else b_fwd),
-                "hbm_frac_at_algorithmic_bytes": round(dom_bytes / (dom_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4)}
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
+                "traffic": (round(traffic[dom]) if dom in traffic else None),
+                "kernel": dom, "kernel_avg_ms": round(avg_ms, 4),
+                "algorithmic_flop_per_edge": fl, "algorithmic_bytes_per_edge": by, "edges_per_launch": E,
+                "hbm_frac_at_algorithmic_bytes": round(by * E / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                "per_kernel": per_kernel}
 
     cpu = None
     if not args.no_cpu:
-        v, cores = cpu_baseline(layer.cpu(), feats_cpu, src, dst, coords, args.cpu_sample)
+        v, cores, times = cpu_baseline(layer.cpu(), feats_cpu, src, dst, coords, args.cpu_sample,
+                                       args.cpu_reps)
         layer.to(dev)
         cpu = {"value": round(v, 1), "unit": "edges/s", "cores": cores, "kind": "port",
-               "sample": f"first {args.cpu_sample} of the {E} edges, fwd+bwd of the float32 "
-                         "oracle (bin-grouped BLAS), median of 3 after 1 warmup"}
+               "sample": f"first {args.cpu_sample} of the {E} edges: fwd + (y**2).sum() + bwd of the "
+                         f"float32 CPU oracle (bin-grouped BLAS), median of {args.cpu_reps} after 1 "
+                         f"warmup ({sum(times):.1f} s timed)"}
 
     value = E * args.steps / wall
-    line = {"metric": "edges/s fwd+bwd, edgewise linear L=2 mult=64; % of HBM/MFMA roofline",
+    line = {"metric": METRIC,
             "value": round(value, 1), "unit": "edges/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
-            "ms_per_step_events": round(ms_ev, 4), "higher_is_better": True, "scaling": "weak",
+            "ms_per_step_events": round(ms_events, 4), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "f32", "data": "synthetic",
             "config": {"workload": "c2: EquivariantEdgewiseLinear [0,1,2]x64 -> [0,1,2]x64, "
                                    "kNN k=16 on 10k uniform nodes in 40^3, E=160000, 100 bins",

@@ -239,8 +239,7 @@ __global__ void k_fill_zero(float* __restrict__ p, int64_t n) {
 int fill_zero(float* p, int64_t n, hipStream_t s) {
     if (n <= 0) return FEQ_OK;
     const int64_t blocks = ceil_div(n, 256) < 4096 ? ceil_div(n, 256) : 4096;
-    hipLaunchKernelGGL(k_fill_zero, dim3(blocks), dim3(256), 0, s, p, n);
-    FEQ_LAUNCH_CHECK("k_fill_zero");
+    FEQ_LAUNCH("k_fill_zero", k_fill_zero, dim3(blocks), dim3(256), 0, s, p, n);
     return FEQ_OK;
 }
 
@@ -263,9 +262,8 @@ extern "C" int feq_blockdiag_fwd(const feq_layout* L, const feq_binning* b, int6
     if (E > 0x7fffffffLL) return fail(FEQ_ERR_UNSUPPORTED, "more than 2^31-1 edges");
     const size_t lds = sizeof(float) * L->cin * L->din;
     if (lds > 64 * 1024) return fail(FEQ_ERR_UNSUPPORTED, "Cin*Din too large for this kernel");
-    hipLaunchKernelGGL(k_bd_fwd, dim3(E), dim3(kThreads), lds, stream_of(stream), *L, *b, x,
+    FEQ_LAUNCH("k_bd_fwd", k_bd_fwd, dim3(E), dim3(kThreads), lds, stream_of(stream), *L, *b, x,
                        table, dist, y);
-    FEQ_LAUNCH_CHECK("k_bd_fwd");
     return FEQ_OK;
 }
 
@@ -286,10 +284,8 @@ extern "C" int feq_blockdiag_bwd(const feq_layout* L, const feq_binning* b, int6
     const size_t lds_x = sizeof(float) * L->cout * L->dout;
     const size_t lds_t = sizeof(float) * (L->cin * L->din + L->cout * L->dout);
     if (lds_t > 64 * 1024) return fail(FEQ_ERR_UNSUPPORTED, "channel*dim too large for this kernel");
-    hipLaunchKernelGGL(k_bd_bwd_x, dim3(E), dim3(kThreads), lds_x, s, *L, *b, gy, table, dist, gx);
-    FEQ_LAUNCH_CHECK("k_bd_bwd_x");
-    hipLaunchKernelGGL(k_bd_bwd_t, dim3(E), dim3(kThreads), lds_t, s, *L, *b, gy, x, table, dist,
+    FEQ_LAUNCH("k_bd_bwd_x", k_bd_bwd_x, dim3(E), dim3(kThreads), lds_x, s, *L, *b, gy, table, dist, gx);
+    FEQ_LAUNCH("k_bd_bwd_t", k_bd_bwd_t, dim3(E), dim3(kThreads), lds_t, s, *L, *b, gy, x, table, dist,
                        gtable, gdist);
-    FEQ_LAUNCH_CHECK("k_bd_bwd_t");
     return FEQ_OK;
 }

@@ -144,8 +144,7 @@ extern "C" int feq_bin_edges(const feq_binning* b, int64_t n, const float* dist,
     if (n == 0) return FEQ_OK;
     if (!dist || !lo || !t) return fail(FEQ_ERR_INVALID, "NULL pointer");
     const int threads = 256;
-    hipLaunchKernelGGL(k_bin_edges, dim3(ceil_div(n, threads)), dim3(threads), 0,
+    FEQ_LAUNCH("k_bin_edges", k_bin_edges, dim3(ceil_div(n, threads)), dim3(threads), 0,
                        stream_of(stream), *b, n, dist, lo, t);
-    FEQ_LAUNCH_CHECK("k_bin_edges");
     return FEQ_OK;
 }

@@ -417,9 +417,8 @@ extern "C" int feq_edgewise_fwd(const feq_layout* L, const feq_binning* b, int32
     const size_t lds = fwd_lds(*L, rank);
     if (int rc = ensure_lds(reinterpret_cast<const void*>(&k_ew_fwd), lds)) return rc;
     EwDims D{rank, b->num_bins};
-    hipLaunchKernelGGL(k_ew_fwd, dim3(E), dim3(kThreads), lds, stream_of(stream), *L, *b, D, x, P,
+    FEQ_LAUNCH("k_ew_fwd", k_ew_fwd, dim3(E), dim3(kThreads), lds, stream_of(stream), *L, *b, D, x, P,
                        Q, dist, C, F, y);
-    FEQ_LAUNCH_CHECK("k_ew_fwd");
     return FEQ_OK;
 }
 
@@ -452,11 +451,9 @@ extern "C" int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32
     const int G = groups_for(E);
     float* part = static_cast<float*>(ws);
     EwDims D{rank, b->num_bins};
-    hipLaunchKernelGGL(k_ew_bwd, dim3(G), dim3(kThreads), lds, s, *L, *b, D, E, gy, x, P, Q, dist,
+    FEQ_LAUNCH("k_ew_bwd", k_ew_bwd, dim3(G), dim3(kThreads), lds, s, *L, *b, D, E, gy, x, P, Q, dist,
                        C, F, gx, gF, gdist, gP, gQ, part);
-    FEQ_LAUNCH_CHECK("k_ew_bwd");
-    hipLaunchKernelGGL(k_reduce_partials, dim3(ceil_div(ncc, 256)), dim3(256), 0, s, part, G, ncc,
+    FEQ_LAUNCH("k_reduce_partials", k_reduce_partials, dim3(ceil_div(ncc, 256)), dim3(256), 0, s, part, G, ncc,
                        gC);
-    FEQ_LAUNCH_CHECK("k_reduce_partials");
     return FEQ_OK;
 }

@@ -652,8 +652,7 @@ __global__ void k_sum_partials(const float* __restrict__ part, int groups, int64
 }
 
 int reduce_partials(const float* part, int groups, int64_t n, float* out, hipStream_t s) {
-    hipLaunchKernelGGL(k_sum_partials, dim3(ceil_div(n, 256)), dim3(256), 0, s, part, groups, n, out);
-    FEQ_LAUNCH_CHECK("k_sum_partials");
+    FEQ_LAUNCH("k_sum_partials", k_sum_partials, dim3(ceil_div(n, 256)), dim3(256), 0, s, part, groups, n, out);
     return FEQ_OK;
 }
 
@@ -722,9 +721,8 @@ int launch_fwd(const feq_binning& B, int64_t E, const float* x, const float* P, 
     auto kern = k_ewc_fwd<CIN, COUT, LIN, LOUT, K>;
     if (int rc = set_lds(reinterpret_cast<const void*>(kern), lds)) return rc;
     const int64_t ntiles = ceil_div(E, kNE);
-    hipLaunchKernelGGL(kern, dim3(grid_for(ntiles, lds <= 80 * 1024 ? 2 : 1)), dim3(kThreads), lds,
+    FEQ_LAUNCH("k_ewc_fwd", kern, dim3(grid_for(ntiles, lds <= 80 * 1024 ? 2 : 1)), dim3(kThreads), lds,
                        s, B, E, ntiles, x, P, Q, dist, C, F, y);
-    FEQ_LAUNCH_CHECK("k_ewc_fwd");
     return FEQ_OK;
 }
 
@@ -761,17 +759,14 @@ int launch_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const float
     float* hp = cv.take<float>(nchunks * hsz);
     if (cv.used > ws_bytes) return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
     if (int rc = set_lds(reinterpret_cast<const void*>(kx), xlds)) return rc;
-    hipLaunchKernelGGL(kx, dim3(Gx), dim3(kThreads), xlds, s, B, E, ntiles, gy, x, P, Q, dist, C, F,
+    FEQ_LAUNCH("k_ewc_bwd_x", kx, dim3(Gx), dim3(kThreads), xlds, s, B, E, ntiles, gy, x, P, Q, dist, C, F,
                        gx, dFe);
-    FEQ_LAUNCH_CHECK("k_ewc_bwd_x");
     if (int rc = set_lds(reinterpret_cast<const void*>(kc), clds)) return rc;
-    hipLaunchKernelGGL(kc, dim3(G), dim3(kThreads), clds, s, B, E, ntiles, gy, x, P, Q, dist, F,
+    FEQ_LAUNCH("k_ewc_bwd_c", kc, dim3(G), dim3(kThreads), clds, s, B, E, ntiles, gy, x, P, Q, dist, F,
                        dCp);
-    FEQ_LAUNCH_CHECK("k_ewc_bwd_c");
     if (int rc = set_lds(reinterpret_cast<const void*>(&k_ewm_bins), blds)) return rc;
-    hipLaunchKernelGGL(k_ewm_bins, dim3(nchunks), dim3(kThreads), blds, s, L, B, K, E, kBinChunk,
+    FEQ_LAUNCH("k_ewm_bins", k_ewm_bins, dim3(nchunks), dim3(kThreads), blds, s, L, B, K, E, kBinChunk,
                        dist, F, dFe, gdist, hp);
-    FEQ_LAUNCH_CHECK("k_ewm_bins");
     if (int rc = reduce_partials(dCp, G, static_cast<int64_t>(K) * COUT * CIN, gC, s)) return rc;
     return reduce_partials(hp, static_cast<int>(nchunks), hsz, gF, s);
 }

@@ -34,6 +34,33 @@ int fail(int code, const char* fmt, ...);
 
 inline hipStream_t stream_of(feq_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Brackets one launch with timing events while feq_profile_enable(1) is in
+// effect (profile.hip); otherwise does nothing.
+class ProfScope {
+   public:
+    ProfScope(const char* name, hipStream_t s);
+    ~ProfScope();
+    ProfScope(const ProfScope&) = delete;
+    ProfScope& operator=(const ProfScope&) = delete;
+
+   private:
+    const char* name_;
+    hipStream_t s_;
+    hipEvent_t a_;
+};
+
+// hipLaunchKernelGGL plus the profiling bracket and the launch-error check;
+// returns from the enclosing function on a launch error.  `kern` must be a
+// single token (bind template instantiations to a variable first).
+#define FEQ_LAUNCH(name, kern, grid, block, lds, stream, ...)                      \
+    do {                                                                           \
+        {                                                                          \
+            ::feq::ProfScope ps_(name, stream);                                    \
+            hipLaunchKernelGGL(kern, grid, block, lds, stream, __VA_ARGS__);       \
+        }                                                                          \
+        FEQ_LAUNCH_CHECK(name);                                                    \
+    } while (0)
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 

@@ -260,9 +260,8 @@ extern "C" int feq_csr_by_dst(const int64_t* dst, int64_t E, int64_t N, int32_t*
     if (!offsets) return fail(FEQ_ERR_INVALID, "NULL offsets");
     hipStream_t s = stream_of(stream);
     if (E == 0) {
-        hipLaunchKernelGGL(k_csr_offsets, dim3(ceil_div(N + 1, 256)), dim3(256), 0, s,
+        FEQ_LAUNCH("k_csr_offsets", k_csr_offsets, dim3(ceil_div(N + 1, 256)), dim3(256), 0, s,
                            static_cast<const int32_t*>(nullptr), int64_t(0), N, offsets);
-        FEQ_LAUNCH_CHECK("k_csr_offsets");
         return FEQ_OK;
     }
     if (!dst || !perm) return fail(FEQ_ERR_INVALID, "NULL pointer");
@@ -274,16 +273,14 @@ extern "C" int feq_csr_by_dst(const int64_t* dst, int64_t E, int64_t N, int32_t*
     int32_t* vals_in = cv.take<int32_t>(E);
     size_t tb = radix_temp_bytes(E);
     void* temp = cv.take<char>(tb);
-    hipLaunchKernelGGL(k_csr_keys, dim3(ceil_div(E, 256)), dim3(256), 0, s, dst, E, N, keys_in,
+    FEQ_LAUNCH("k_csr_keys", k_csr_keys, dim3(ceil_div(E, 256)), dim3(256), 0, s, dst, E, N, keys_in,
                        vals_in);
-    FEQ_LAUNCH_CHECK("k_csr_keys");
     int end_bit = 1;
     while ((int64_t(1) << end_bit) <= N) ++end_bit;  // keys lie in [0, N]
     FEQ_HIP(hipcub::DeviceRadixSort::SortPairs(temp, tb, keys_in, keys_out, vals_in, perm,
                                                static_cast<int>(E), 0, end_bit, s));
-    hipLaunchKernelGGL(k_csr_offsets, dim3(ceil_div(N + 1, 256)), dim3(256), 0, s, keys_out, E, N,
+    FEQ_LAUNCH("k_csr_offsets", k_csr_offsets, dim3(ceil_div(N + 1, 256)), dim3(256), 0, s, keys_out, E, N,
                        offsets);
-    FEQ_LAUNCH_CHECK("k_csr_offsets");
     return FEQ_OK;
 }
 
@@ -293,9 +290,8 @@ extern "C" int feq_segment_sum(const float* x, int64_t row, const int32_t* perm,
     if (row < 0 || N < 0) return fail(FEQ_ERR_INVALID, "invalid sizes");
     if (N == 0 || row == 0) return FEQ_OK;
     if (!offsets || !out) return fail(FEQ_ERR_INVALID, "NULL pointer");
-    hipLaunchKernelGGL(k_segment_sum, dim3(N), dim3(kThreads), 0, stream_of(stream), x, row, perm,
+    FEQ_LAUNCH("k_segment_sum", k_segment_sum, dim3(N), dim3(kThreads), 0, stream_of(stream), x, row, perm,
                        offsets, out);
-    FEQ_LAUNCH_CHECK("k_segment_sum");
     return FEQ_OK;
 }
 
@@ -304,9 +300,8 @@ extern "C" int feq_gather_rows(const float* src, int64_t nsrc, int64_t row, cons
     if (row < 0 || nrows < 0 || nsrc < 0) return fail(FEQ_ERR_INVALID, "invalid sizes");
     if (nrows == 0 || row == 0) return FEQ_OK;
     if (!src || !idx || !out) return fail(FEQ_ERR_INVALID, "NULL pointer");
-    hipLaunchKernelGGL(k_gather_rows, dim3(nrows), dim3(row < 256 ? 64 : 256), 0,
+    FEQ_LAUNCH("k_gather_rows", k_gather_rows, dim3(nrows), dim3(row < 256 ? 64 : 256), 0,
                        stream_of(stream), src, row, idx, nrows, nsrc, out);
-    FEQ_LAUNCH_CHECK("k_gather_rows");
     return FEQ_OK;
 }
 
@@ -326,9 +321,8 @@ extern "C" int feq_edge_softmax_fwd(const float* Q, const float* K, const float*
     if (E == 0) return FEQ_OK;
     if (!Q || !K || !perm || !offsets || !attn) return fail(FEQ_ERR_INVALID, "NULL pointer");
     if (decay > 0.0f && !dist) return fail(FEQ_ERR_INVALID, "distance decay needs distances");
-    hipLaunchKernelGGL(k_softmax_fwd, dim3(N), dim3(kThreads), 0, stream_of(stream), Q, K, dist, H,
+    FEQ_LAUNCH("k_softmax_fwd", k_softmax_fwd, dim3(N), dim3(kThreads), 0, stream_of(stream), Q, K, dist, H,
                        Dh, scale, decay, perm, offsets, attn, qk_out);
-    FEQ_LAUNCH_CHECK("k_softmax_fwd");
     return FEQ_OK;
 }
 
@@ -342,9 +336,8 @@ extern "C" int feq_edge_softmax_bwd(const float* Q, const float* K, const float*
     if (E == 0) return FEQ_OK;
     if (!Q || !K || !attn || !gattn || !perm || !offsets || !gQ || !gK)
         return fail(FEQ_ERR_INVALID, "NULL pointer");
-    hipLaunchKernelGGL(k_softmax_bwd, dim3(N), dim3(kThreads), 0, stream_of(stream), Q, K, attn,
+    FEQ_LAUNCH("k_softmax_bwd", k_softmax_bwd, dim3(N), dim3(kThreads), 0, stream_of(stream), Q, K, attn,
                        gattn, H, Dh, scale, decay, perm, offsets, gQ, gK, gls, gdist);
-    FEQ_LAUNCH_CHECK("k_softmax_bwd");
     return FEQ_OK;
 }
 
@@ -355,9 +348,8 @@ extern "C" int feq_attn_pool_fwd(const float* V, const float* attn, int64_t E, i
     if (H < 1 || mult % H) return fail(FEQ_ERR_INVALID, "num_heads must divide mult");
     if (E < 0 || N < 1 || dim < 1) return fail(FEQ_ERR_INVALID, "invalid sizes");
     if (!offsets || !out) return fail(FEQ_ERR_INVALID, "NULL pointer");
-    hipLaunchKernelGGL(k_attn_pool_fwd, dim3(N), dim3(kThreads), 0, stream_of(stream), V, attn,
+    FEQ_LAUNCH("k_attn_pool_fwd", k_attn_pool_fwd, dim3(N), dim3(kThreads), 0, stream_of(stream), V, attn,
                        mult, dim, H, perm, offsets, out);
-    FEQ_LAUNCH_CHECK("k_attn_pool_fwd");
     return FEQ_OK;
 }
 
@@ -369,8 +361,7 @@ extern "C" int feq_attn_pool_bwd(const float* V, const float* attn, const float*
     if (E < 0 || dim < 1) return fail(FEQ_ERR_INVALID, "invalid sizes");
     if (E == 0) return FEQ_OK;
     if (!V || !attn || !gout || !dst || !gV || !gattn) return fail(FEQ_ERR_INVALID, "NULL pointer");
-    hipLaunchKernelGGL(k_attn_pool_bwd, dim3(E), dim3(kThreads), 0, stream_of(stream), V, attn,
+    FEQ_LAUNCH("k_attn_pool_bwd", k_attn_pool_bwd, dim3(E), dim3(kThreads), 0, stream_of(stream), V, attn,
                        gout, dst, N, mult, dim, H, gV, gattn);
-    FEQ_LAUNCH_CHECK("k_attn_pool_bwd");
     return FEQ_OK;
 }

@@ -161,8 +161,7 @@ extern "C" int feq_wigner_basis(const int32_t* lvals, int32_t n, const double* p
     if (E == 0) return FEQ_OK;
     if (!plan || !perm || !dirs || !out) return fail(FEQ_ERR_INVALID, "NULL pointer");
     const int64_t total = E * dim;
-    hipLaunchKernelGGL(k_wigner, dim3(ceil_div(total, 256)), dim3(256), 0, stream_of(stream), A,
+    FEQ_LAUNCH("k_wigner", k_wigner, dim3(ceil_div(total, 256)), dim3(256), 0, stream_of(stream), A,
                        plan, perm, E, dirs, out);
-    FEQ_LAUNCH_CHECK("k_wigner");
     return FEQ_OK;
 }

@@ -53,6 +53,8 @@ _SZ = ctypes.c_size_t
 _SIGS = {
     "feq_last_error": ([], ctypes.c_char_p),
     "feq_abi_version": ([], ctypes.c_int),
+    "feq_profile_enable": ([ctypes.c_int], ctypes.c_int),
+    "feq_profile_summary": ([ctypes.c_char_p, _SZ], ctypes.c_int),
     "feq_layout_init": ([_P, _P, _I32, _P, _I32, _I32, _I32], ctypes.c_int),
     "feq_bin_edges": ([_P, _I64, _P, _P, _P, _P], ctypes.c_int),
     "feq_blockdiag_workspace": ([_P, _P, _I64], _SZ),
@@ -145,3 +147,21 @@ def require_cuda_tensor(t: torch.Tensor, name: str) -> None:
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     """Caller-owned scratch for the library, from the caching allocator."""
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def profile_enable(on: bool) -> None:
+    """Start (clearing nothing) or stop bracketing every library launch with HIP events."""
+    check(load_library().feq_profile_enable(int(bool(on))), "feq_profile_enable")
+
+
+def profile_summary() -> dict:
+    """{kernel name: (launches, total milliseconds)} of the launches recorded so far.
+
+    Waits for the recorded events, then forgets them."""
+    buf = ctypes.create_string_buffer(1 << 16)
+    check(load_library().feq_profile_summary(buf, len(buf)), "feq_profile_summary")
+    out = {}
+    for line in buf.value.decode().splitlines():
+        name, calls, ms = line.split("\t")
+        out[name] = (int(calls), float(ms))
+    return out

@@ -82,6 +82,15 @@ typedef struct feq_binning {
 const char* feq_last_error(void);
 int feq_abi_version(void);
 
+/* ---- per-kernel timing (no reference counterpart: the reference times its
+ * kernels from Python with CUDA events, scripts/profile_kernels.py:7-76) ------
+ * While enabled, every kernel launch is bracketed by two events recorded on its
+ * own stream.  feq_profile_summary waits for them and writes one line per
+ * kernel, "name<TAB>launches<TAB>total_ms\n", then forgets the records.
+ * Process-global, for one host thread. */
+int feq_profile_enable(int on);
+int feq_profile_summary(char* buf, size_t len);
+
 /* Fill *out from the irrep degrees (host arrays, lvals order, duplicates allowed). */
 int feq_layout_init(feq_layout* out, const int32_t* lvals_in, int32_t n_in,
                     const int32_t* lvals_out, int32_t n_out, int32_t cin, int32_t cout);
