@@ -120,24 +120,67 @@ struct TileEdge {
     int valid;
 };
 
-// Per-edge bins, solid-harmonic powers and F_e of one tile; P, Q tiles.
-template <int LIN, int LOUT, int K>
-__device__ void stage_tile(const feq_binning& B, int64_t E, int64_t e0,
-                           const float* __restrict__ P, const float* __restrict__ Q,
-                           const float* __restrict__ dist, const float* __restrict__ F,
-                           float* sP, float* sQ, TileEdge* sE, float* sSin, float* sSout,
-                           float* sFe) {
-    using T = Canon<LIN, LOUT>;
-    constexpr int DIN = T::DIN, DOUT = T::DOUT, KW = K * T::WD;
+// ---- register prefetch of a tile's raw inputs ------------------------------
+// While the matrix cores work on tile t, every thread already holds its share
+// of tile t + gridDim.x in registers: its (edge, channel) rows of x (or gy),
+// its slice of the tile's P and Q blocks and (threads < kNE) one distance.
+// Rows past the last edge read as zero, so a prefetch beyond the last tile
+// touches no memory.
+
+// Rows (e, c) of a (E, CH, D) tensor; thread t holds rows q = t + kThreads j.
+template <int CH, int D>
+struct RowRegs {
+    static constexpr int NR = kNE * CH / kThreads;
+    static_assert(kNE * CH % kThreads == 0, "rows must split evenly over the workgroup");
+    float v[NR][D];
+    __device__ __forceinline__ void load(const float* __restrict__ src, int64_t e0, int64_t E) {
+#pragma unroll
+        for (int j = 0; j < NR; ++j) {
+            const int q = threadIdx.x + kThreads * j;
+            const int e = q / CH, c = q % CH;
+            if (e0 + e < E) {
+                const float* p = src + ((e0 + e) * CH + c) * D;
+#pragma unroll
+                for (int d = 0; d < D; ++d) v[j][d] = p[d];
+            } else {
+#pragma unroll
+                for (int d = 0; d < D; ++d) v[j][d] = 0.0f;
+            }
+        }
+    }
+};
+
+// N consecutive floats starting at element `base` (a tile's P or Q block).
+template <int N>
+struct BlockRegs {
+    static constexpr int NR = (N + kThreads - 1) / kThreads;
+    float v[NR];
+    __device__ __forceinline__ void load(const float* __restrict__ src, int64_t base, int64_t end) {
+#pragma unroll
+        for (int j = 0; j < NR; ++j) {
+            const int q = threadIdx.x + kThreads * j;
+            v[j] = (q < N && base + q < end) ? src[base + q] : 0.0f;
+        }
+    }
+    __device__ __forceinline__ void store(float* dst) const {
+#pragma unroll
+        for (int j = 0; j < NR; ++j) {
+            const int q = threadIdx.x + kThreads * j;
+            if (q < N) dst[q] = v[j];
+        }
+    }
+};
+
+// Edge state of a tile from the prefetched distances (threads < kNE).
+template <int LIN, int LOUT>
+__device__ __forceinline__ void commit_edges(const feq_binning& B, int64_t E, int64_t e0, float r,
+                                             TileEdge* sE, float* sSin, float* sSout) {
+    constexpr int DIN = (LIN + 1) * (LIN + 1), DOUT = (LOUT + 1) * (LOUT + 1);
     const int tid = threadIdx.x;
-    for (int q = tid; q < kNE * DIN * DIN; q += kThreads)
-        sP[q] = (e0 + q / (DIN * DIN) < E) ? P[e0 * DIN * DIN + q] : 0.0f;
-    for (int q = tid; q < kNE * DOUT * DOUT; q += kThreads)
-        sQ[q] = (e0 + q / (DOUT * DOUT) < E) ? Q[e0 * DOUT * DOUT + q] : 0.0f;
     if (tid < kNE) {
         TileEdge te;
         te.valid = (e0 + tid) < E;
-        const float r = te.valid ? dist[e0 + tid] : 1.0f;
+        if (!te.valid) r = 1.0f;
         const EdgeBin eb = edge_bin(r, B);
         te.lo = eb.lo;
         te.t = eb.t;
@@ -148,37 +191,62 @@ __device__ void stage_tile(const feq_binning& B, int64_t E, int64_t e0,
 #pragma unroll
         for (int j = 0; j < DOUT; ++j) sSout[tid * DOUT + j] = ipowf(te.s, SlotL<LOUT>::l[j]);
     }
-    __syncthreads();
-    for (int q = tid; q < kNE * KW; q += kThreads) {
+}
+
+// F_e = (1-t) F[lo] + t F[lo+1] for the tile's edges; Ft is the radial-function
+// table (num_bins+1, KW), in LDS or in global memory.
+template <int KW>
+__device__ __forceinline__ void interp_tile(const TileEdge* sE, const float* Ft, float* sFe) {
+    for (int q = threadIdx.x; q < kNE * KW; q += kThreads) {
         const int e = q / KW, rest = q % KW;
         const TileEdge te = sE[e];
-        const float* flo = F + static_cast<int64_t>(te.lo) * KW;
+        const float* flo = Ft + te.lo * KW;
         sFe[q] = lerp_bins(flo[rest], flo[KW + rest], te.t);
     }
 }
 
-// fs[ci][16 i + e] = s^l_i sum_d x[e, ci, d] P[e, d, i]
-template <int CIN, int DIN>
-__device__ void rotate_in(int64_t E, int64_t e0, const float* __restrict__ x, const float* sP,
-                          const float* sSin, float* sf, int fs) {
-    for (int q = threadIdx.x; q < kNE * CIN; q += kThreads) {
-        const int e = q / CIN, ci = q % CIN;
-        float xv[DIN];
-        if (e0 + e < E) {
-            const float* xr = x + ((e0 + e) * CIN + ci) * DIN;
+// Rows F[lo] and F[lo + 1] of the radial-function table for a tile's edges;
+// thread t holds elements q = t + kThreads j of the (kNE, KW) tile.  `sLo`
+// holds the tile's lower bins (in range even for padding edges).
+template <int KW>
+struct FRowRegs {
+    static constexpr int NR = (kNE * KW + kThreads - 1) / kThreads;
+    float lo[NR], hi[NR];
+    __device__ __forceinline__ void load(const float* __restrict__ F, const int* sLo) {
 #pragma unroll
-            for (int d = 0; d < DIN; ++d) xv[d] = xr[d];
-        } else {
-#pragma unroll
-            for (int d = 0; d < DIN; ++d) xv[d] = 0.0f;
+        for (int j = 0; j < NR; ++j) {
+            const int q = threadIdx.x + kThreads * j;
+            if (q < kNE * KW) {
+                const float* f = F + sLo[q / KW] * KW + q % KW;
+                lo[j] = f[0];
+                hi[j] = f[KW];
+            }
         }
-        const float* pe = sP + e * DIN * DIN;
+    }
+    __device__ __forceinline__ void commit(const TileEdge* sE, float* sFe) const {
 #pragma unroll
-        for (int i = 0; i < DIN; ++i) {
+        for (int j = 0; j < NR; ++j) {
+            const int q = threadIdx.x + kThreads * j;
+            if (q < kNE * KW) sFe[q] = lerp_bins(lo[j], hi[j], sE[q / KW].t);
+        }
+    }
+};
+
+// dst[c * stride + 16 i + e] = s^l_i sum_d rows(e, c)[d] R_e[d, i]  (x P or gy Q)
+template <int CH, int D>
+__device__ __forceinline__ void rotate_regs(const RowRegs<CH, D>& rr, const float* sR,
+                                            const float* sS, float* dst, int stride) {
+#pragma unroll
+    for (int j = 0; j < RowRegs<CH, D>::NR; ++j) {
+        const int q = threadIdx.x + kThreads * j;
+        const int e = q / CH, c = q % CH;
+        const float* re = sR + e * D * D;
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
             float acc = 0.0f;
 #pragma unroll
-            for (int d = 0; d < DIN; ++d) acc += xv[d] * pe[d * DIN + i];
-            sf[ci * fs + 16 * i + e] = acc * sSin[e * DIN + i];
+            for (int d = 0; d < D; ++d) acc += rr.v[j][d] * re[d * D + i];
+            dst[c * stride + 16 * i + e] = acc * sS[e * D + i];
         }
     }
 }
@@ -198,8 +266,49 @@ __device__ void stage_frags(const float* __restrict__ C, int cout, int cin, floa
     }
 }
 
+// x rows of a tile rotated into the m-first frame: fs[ci][16 i + e] =
+// s^l_i sum_d x[e, ci, d] P_e[d, i] (thread t handles rows q = t + kThreads j).
+template <int CIN, int DIN>
+__device__ __forceinline__ void rotate_rows(const float* __restrict__ x, int64_t e0, int64_t E,
+                                            const float* sP, const float* sSin, float* sf,
+                                            int fs) {
+    RowRegs<CIN, DIN> rr;
+    rr.load(x, e0, E);
+    rotate_regs<CIN, DIN>(rr, sP, sSin, sf, fs);
+}
+
+// A fragments held in registers for the whole launch.  Lane (le, lg) of wave w
+// keeps A[16 (w + 4 j) + le][lg * NS + s] of every rank component k, with
+// A = C_k (rows co, cols ci) or A = C_k^T (rows ci, cols co).  The reduction
+// index of every product is ordered c = lg * NS + s: any order is valid as long
+// as the B fragments use the same one.
+template <int RPW, int K, int NS>
+struct AFrags {
+    float v[RPW][K][NS];
+    __device__ __forceinline__ void load(const float* __restrict__ C, int cout, int cin,
+                                         bool trans) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        const int le = lane & 15, lg = lane >> 4;
+#pragma unroll
+        for (int j = 0; j < RPW; ++j)
+#pragma unroll
+            for (int k = 0; k < K; ++k)
+#pragma unroll
+                for (int s = 0; s < NS; ++s) {
+                    const int row = 16 * (wave + 4 * j) + le, col = lg * NS + s;
+                    v[j][k][s] = trans ? C[(static_cast<int64_t>(k) * cout + col) * cin + row]
+                                       : C[(static_cast<int64_t>(k) * cout + row) * cin + col];
+                }
+    }
+};
+
+// Forward: G_k = C_k fs on the matrix cores, y = Q-rotate(s^l sum_k M_ek G_k).
+// Two workgroups share a CU (C_k lives in registers, not LDS), so one
+// workgroup's rotations, contractions and memory traffic overlap the other's
+// matrix-core loop.  The rank components run in two passes to halve the live
+// accumulators.
 template <int CIN, int COUT, int LIN, int LOUT, int K>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kThreads, 2)
 k_ewc_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
           const float* __restrict__ P, const float* __restrict__ Q,
           const float* __restrict__ dist, const float* __restrict__ C,
@@ -208,12 +317,11 @@ k_ewc_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
     constexpr int FS = 16 * DIN + 1;
     constexpr int YS = COUT * DOUT + 1;
-    constexpr int RB = COUT / 16, RPW = RB / 4, NS = CIN / 4;
+    constexpr int RPW = COUT / 64, NS = CIN / 4, KH = 1;
     constexpr int BIG = CIN * FS > kNE * YS ? CIN * FS : kNE * YS;
     static_assert(COUT % 64 == 0 && CIN % 16 == 0, "unsupported channel counts");
     extern __shared__ float4 smem4[];
-    float* sCf = reinterpret_cast<float*>(smem4);  // K x RB x NS x 64 A fragments
-    float* sf = sCf + K * RB * NS * 64;            // fs tile, later the y staging tile
+    float* sf = reinterpret_cast<float*>(smem4);   // fs tile, later the y staging tile
     float* sP = sf + BIG;
     float* sQ = sP + kNE * DIN * DIN;
     float* sSin = sQ + kNE * DOUT * DOUT;
@@ -223,39 +331,28 @@ k_ewc_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int le = lane & 15, lg = lane >> 4;
-    stage_frags<K, RB, NS, false>(C, COUT, CIN, sCf);
+    AFrags<RPW, K, NS> A;
+    A.load(C, COUT, CIN, false);
 
     for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
         const int64_t e0 = tile * kNE;
+        __syncthreads();   // the previous tile's readers of the LDS tiles are done
+        {
+            BlockRegs<kNE * DIN * DIN> pr;
+            BlockRegs<kNE * DOUT * DOUT> qr;
+            pr.load(P, e0 * DIN * DIN, E * DIN * DIN);
+            qr.load(Q, e0 * DOUT * DOUT, E * DOUT * DOUT);
+            const float r = (tid < kNE && e0 + tid < E) ? dist[e0 + tid] : 1.0f;
+            pr.store(sP);
+            qr.store(sQ);
+            commit_edges<LIN, LOUT>(B, E, e0, r, sE, sSin, sSout);
+        }
         __syncthreads();
-        stage_tile<LIN, LOUT, K>(B, E, e0, P, Q, dist, F, sP, sQ, sE, sSin, sSout, sFe);
-        __syncthreads();
-        rotate_in<CIN, DIN>(E, e0, x, sP, sSin, sf, FS);
+        interp_tile<KW>(sE, F, sFe);
+        rotate_rows<CIN, DIN>(x, e0, E, sP, sSin, sf, FS);
         __syncthreads();
 
-        v4f acc[RPW][K][DIN];
-#pragma unroll
-        for (int j = 0; j < RPW; ++j)
-#pragma unroll
-            for (int k = 0; k < K; ++k)
-#pragma unroll
-                for (int i = 0; i < DIN; ++i) acc[j][k][i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 2
-        for (int s = 0; s < NS; ++s) {
-            float b[DIN];
-            const float* row = sf + (4 * s + lg) * FS + le;
-#pragma unroll
-            for (int i = 0; i < DIN; ++i) b[i] = row[16 * i];
-#pragma unroll
-            for (int j = 0; j < RPW; ++j)
-#pragma unroll
-                for (int k = 0; k < K; ++k) {
-                    const float a = sCf[((k * RB + wave + 4 * j) * NS + s) * 64 + lane];
-#pragma unroll
-                    for (int i = 0; i < DIN; ++i) acc[j][k][i] = mfma(a, b[i], acc[j][k][i]);
-                }
-        }
-        // epilogue: lane (edge le, rows 16(wave+4j) + 4 lg + r)
+        // lane (edge le, rows co = 16 (wave + 4 j) + 4 lg + r)
         float yv[RPW][DOUT][4];
 #pragma unroll
         for (int j = 0; j < RPW; ++j)
@@ -264,18 +361,49 @@ k_ewc_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
 #pragma unroll
                 for (int r = 0; r < 4; ++r) yv[j][o][r] = 0.0f;
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
-            float fk[WD];
+        for (int k0 = 0; k0 < K; k0 += KH) {
+            v4f acc[RPW][KH][DIN];
 #pragma unroll
-            for (int w = 0; w < WD; ++w) fk[w] = sFe[le * KW + k * WD + w];
+            for (int j = 0; j < RPW; ++j)
 #pragma unroll
-            for (int t = 0; t < T::NT; ++t) {
-                const Term tm = T::terms[t];
-                const float c = tm.neg ? -fk[tm.w] : fk[tm.w];
+                for (int kk = 0; kk < KH; ++kk)
+#pragma unroll
+                    for (int i = 0; i < DIN; ++i) acc[j][kk][i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            // B fragments are loaded one step ahead; the scheduling fence after
+            // each step keeps the compiler from hoisting every step's loads.
+            float b[2][DIN];
+#pragma unroll
+            for (int i = 0; i < DIN; ++i) b[0][i] = sf[lg * NS * FS + le + 16 * i];
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                if (s + 1 < NS) {
+                    const float* row = sf + (lg * NS + s + 1) * FS + le;
+#pragma unroll
+                    for (int i = 0; i < DIN; ++i) b[(s + 1) & 1][i] = row[16 * i];
+                }
 #pragma unroll
                 for (int j = 0; j < RPW; ++j)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) yv[j][tm.o][r] += c * acc[j][k][tm.i][r];
+                    for (int kk = 0; kk < KH; ++kk)
+#pragma unroll
+                        for (int i = 0; i < DIN; ++i)
+                            acc[j][kk][i] = mfma(A.v[j][k0 + kk][s], b[s & 1][i], acc[j][kk][i]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int kk = 0; kk < KH; ++kk) {
+                float fk[WD];
+#pragma unroll
+                for (int w = 0; w < WD; ++w) fk[w] = sFe[le * KW + (k0 + kk) * WD + w];
+#pragma unroll
+                for (int t = 0; t < T::NT; ++t) {
+                    const Term tm = T::terms[t];
+                    const float c = tm.neg ? -fk[tm.w] : fk[tm.w];
+#pragma unroll
+                    for (int j = 0; j < RPW; ++j)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) yv[j][tm.o][r] += c * acc[j][kk][tm.i][r];
+                }
             }
         }
 #pragma unroll
@@ -297,53 +425,103 @@ k_ewc_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
             for (int j = 0; j < RPW; ++j)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    float a = 0.0f;
+                    float acc_d = 0.0f;
 #pragma unroll
-                    for (int o = 0; o < DOUT; ++o) a += yv[j][o][r] * qrow[o];
-                    sf[le * YS + (16 * (wave + 4 * j) + 4 * lg + r) * DOUT + d] = a;
+                    for (int o = 0; o < DOUT; ++o) acc_d += yv[j][o][r] * qrow[o];
+                    sf[le * YS + (16 * (wave + 4 * j) + 4 * lg + r) * DOUT + d] = acc_d;
                 }
         }
         __syncthreads();
-        const int64_t nval = E - e0 < kNE ? E - e0 : kNE;
         float* yt = y + e0 * COUT * DOUT;
-        for (int q = tid; q < nval * COUT * DOUT; q += kThreads) {
-            const int e = q / (COUT * DOUT), rest = q % (COUT * DOUT);
-            yt[q] = sf[e * YS + rest];
+        if (E - e0 >= kNE) {
+#pragma unroll
+            for (int m = 0; m < kNE * COUT * DOUT / kThreads; ++m) {
+                const int q = tid + kThreads * m;
+                yt[q] = sf[(q / (COUT * DOUT)) * YS + q % (COUT * DOUT)];
+            }
+        } else {
+            for (int q = tid; q < (E - e0) * COUT * DOUT; q += kThreads)
+                yt[q] = sf[(q / (COUT * DOUT)) * YS + q % (COUT * DOUT)];
         }
     }
 }
 
-// ---------------------------------------------------------------------------
-// gd[co][16 o + e] = s^l_o sum_d gy[e, co, d] Q[e, d, o]
-template <int COUT, int DOUT>
-__device__ void rotate_grad(int64_t E, int64_t e0, const float* __restrict__ gy, const float* sQ,
-                            const float* sSout, float* sG, int gs) {
-    for (int q = threadIdx.x; q < kNE * COUT; q += kThreads) {
-        const int e = q / COUT, co = q % COUT;
-        float gv[DOUT];
-        if (e0 + e < E) {
-            const float* gr = gy + ((e0 + e) * COUT + co) * DOUT;
-#pragma unroll
-            for (int d = 0; d < DOUT; ++d) gv[d] = gr[d];
-        } else {
-#pragma unroll
-            for (int d = 0; d < DOUT; ++d) gv[d] = 0.0f;
-        }
-        const float* qe = sQ + e * DOUT * DOUT;
-#pragma unroll
-        for (int o = 0; o < DOUT; ++o) {
-            float a = 0.0f;
-#pragma unroll
-            for (int d = 0; d < DOUT; ++d) a += gv[d] * qe[d * DOUT + o];
-            sG[co * gs + 16 * o + e] = a * sSout[e * DOUT + o];
-        }
+// Register pipeline of the backward kernels.  At the top of the iteration for
+// tile t the registers hold tile t's x and gy rows, P and Q blocks and F rows,
+// and the distances of tiles t and t + G (G = gridDim.x); `next()` issues the
+// loads for tile t + G (whose bins are known one tile ahead) and the distance
+// of tile t + 2G, so every global load has a whole tile of work to arrive.
+template <int CIN, int COUT, int LIN, int LOUT, int K>
+struct BwdPipe {
+    using T = Canon<LIN, LOUT>;
+    static constexpr int DIN = T::DIN, DOUT = T::DOUT, KW = K * T::WD;
+    RowRegs<CIN, DIN> xr;
+    RowRegs<COUT, DOUT> gr;
+    BlockRegs<kNE * DIN * DIN> pr;
+    BlockRegs<kNE * DOUT * DOUT> qr;
+    FRowRegs<KW> fr;
+    float r_cur = 1.0f, r_next = 1.0f;
+
+    __device__ __forceinline__ float load_dist(const float* __restrict__ dist, int64_t t,
+                                               int64_t E) const {
+        const int64_t e = t * kNE + threadIdx.x;
+        return (threadIdx.x < kNE && e < E) ? dist[e] : 1.0f;
     }
-}
+    __device__ __forceinline__ void load_rows(int64_t t, int64_t E, const float* __restrict__ x,
+                                              const float* __restrict__ gy,
+                                              const float* __restrict__ P,
+                                              const float* __restrict__ Q) {
+        const int64_t p0 = t * kNE;
+        xr.load(x, p0, E);
+        gr.load(gy, p0, E);
+        pr.load(P, p0 * DIN * DIN, E * DIN * DIN);
+        qr.load(Q, p0 * DOUT * DOUT, E * DOUT * DOUT);
+    }
+    // Before the loop: tile t0's rows, bins and F rows; tile t0 + G's distance.
+    __device__ void prologue(const feq_binning& B, int64_t t0, int64_t G, int64_t E,
+                             const float* x, const float* gy, const float* P, const float* Q,
+                             const float* dist, const float* F, int* sLo) {
+        r_cur = load_dist(dist, t0, E);
+        if (threadIdx.x < kNE) sLo[threadIdx.x] = edge_bin(r_cur, B).lo;
+        r_next = load_dist(dist, t0 + G, E);
+        load_rows(t0, E, x, gy, P, Q);
+        __syncthreads();
+        fr.load(F, sLo);
+    }
+    // Tile top (after a barrier): P/Q blocks and edge state to LDS, and the
+    // next tile's bins for the F-row prefetch.
+    __device__ __forceinline__ void commit(const feq_binning& B, int64_t E, int64_t e0, float* sP,
+                                           float* sQ, TileEdge* sE, float* sSin, float* sSout,
+                                           int* sLo) {
+        pr.store(sP);
+        qr.store(sQ);
+        commit_edges<LIN, LOUT>(B, E, e0, r_cur, sE, sSin, sSout);
+        if (threadIdx.x < kNE) sLo[threadIdx.x] = edge_bin(r_next, B).lo;
+    }
+    // After the next barrier: F_e, fs = s^l (x P) and gd = s^l (gy Q) to LDS.
+    __device__ __forceinline__ void rotate(const TileEdge* sE, float* sFe, const float* sP,
+                                           const float* sQ, const float* sSin,
+                                           const float* sSout, float* sf, int fs, float* sG,
+                                           int gs) const {
+        fr.commit(sE, sFe);
+        rotate_regs<CIN, DIN>(xr, sP, sSin, sf, fs);
+        rotate_regs<COUT, DOUT>(gr, sQ, sSout, sG, gs);
+    }
+    // Once the tile's register data is in LDS (after a barrier): loads for tile t + G.
+    __device__ __forceinline__ void next(int64_t t, int64_t G, int64_t E, const float* x,
+                                         const float* gy, const float* P, const float* Q,
+                                         const float* dist, const float* F, const int* sLo) {
+        load_rows(t + G, E, x, gy, P, Q);
+        fr.load(F, sLo);
+        r_cur = r_next;
+        r_next = load_dist(dist, t + 2 * G, E);
+    }
+};
 
 // Backward, part 1: H_k = C_k^T gd (MFMA), dfs = sum_k M_ek^T H_k and
 // dF_e[k, w] = sum_ci fs H_k in registers, dx = s^l dfs P^T.
 template <int CIN, int COUT, int LIN, int LOUT, int K>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kThreads, 1)
 k_ewc_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
             const float* __restrict__ x, const float* __restrict__ P, const float* __restrict__ Q,
             const float* __restrict__ dist, const float* __restrict__ C,
@@ -356,6 +534,8 @@ k_ewc_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     constexpr int HRB = CIN / 16, RPW = HRB / 4, NS = COUT / 4;
     constexpr int GBIG = COUT * GS > kNE * XS ? COUT * GS : kNE * XS;
     constexpr int DFN = 4 * K * kNE * WD;
+    constexpr int KH = K % 2 == 0 ? K / 2 : K;   // rank components per MFMA pass
+    constexpr int WQ = (WD + 3) / 4;             // dF partials per lane group
     static_assert(CIN % 64 == 0 && COUT % 4 == 0, "unsupported channel counts");
     static_assert(DFN <= GBIG, "dF partials must fit the gd tile");
     extern __shared__ float4 smem4[];
@@ -368,43 +548,27 @@ k_ewc_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     float* sSout = sSin + kNE * DIN;
     float* sFe = sSout + kNE * DOUT;
     TileEdge* sE = reinterpret_cast<TileEdge*>(sFe + kNE * KW);
+    int* sLo = reinterpret_cast<int*>(sE + kNE);   // next tile's lower bins
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int le = lane & 15, lg = lane >> 4;
     stage_frags<K, HRB, NS, true>(C, COUT, CIN, sCf);
+    const int64_t G = gridDim.x;
+    BwdPipe<CIN, COUT, LIN, LOUT, K> pipe;
+    pipe.prologue(B, blockIdx.x, G, E, x, gy, P, Q, dist, F, sLo);
 
-    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    for (int64_t tile = blockIdx.x; tile < ntiles; tile += G) {
         const int64_t e0 = tile * kNE;
+        __syncthreads();   // the previous tile's readers of the LDS tiles are done
+        pipe.commit(B, E, e0, sP, sQ, sE, sSin, sSout, sLo);
         __syncthreads();
-        stage_tile<LIN, LOUT, K>(B, E, e0, P, Q, dist, F, sP, sQ, sE, sSin, sSout, sFe);
+        pipe.rotate(sE, sFe, sP, sQ, sSin, sSout, sf, FS, sG, GS);
         __syncthreads();
-        rotate_in<CIN, DIN>(E, e0, x, sP, sSin, sf, FS);
-        rotate_grad<COUT, DOUT>(E, e0, gy, sQ, sSout, sG, GS);
-        __syncthreads();
-        v4f accH[RPW][K][DOUT];
-#pragma unroll
-        for (int j = 0; j < RPW; ++j)
-#pragma unroll
-            for (int k = 0; k < K; ++k)
-#pragma unroll
-                for (int o = 0; o < DOUT; ++o) accH[j][k][o] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 2
-        for (int s = 0; s < NS; ++s) {
-            float b[DOUT];
-            const float* row = sG + (4 * s + lg) * GS + le;
-#pragma unroll
-            for (int o = 0; o < DOUT; ++o) b[o] = row[16 * o];
-#pragma unroll
-            for (int j = 0; j < RPW; ++j)
-#pragma unroll
-                for (int k = 0; k < K; ++k) {
-                    const float a = sCf[((k * HRB + wave + 4 * j) * NS + s) * 64 + lane];
-#pragma unroll
-                    for (int o = 0; o < DOUT; ++o) accH[j][k][o] = mfma(a, b[o], accH[j][k][o]);
-                }
-        }
-        __syncthreads();   // gd no longer needed: its tile holds the dF partials, then dx
+        pipe.next(tile, G, E, x, gy, P, Q, dist, F, sLo);   // in flight during the MFMA loops
+        // Two passes over the rank components keep half the accumulators live.
+        // Lane group lg keeps the per-edge dF partials of the weights w = 4q + lg.
         float dfs[RPW][DIN][4];
+        float pfs[K][WQ];
 #pragma unroll
         for (int j = 0; j < RPW; ++j)
 #pragma unroll
@@ -412,43 +576,82 @@ k_ewc_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 #pragma unroll
                 for (int r = 0; r < 4; ++r) dfs[j][i][r] = 0.0f;
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
-            float fk[WD], pf[WD];
-#pragma unroll
-            for (int w = 0; w < WD; ++w) {
-                fk[w] = sFe[le * KW + k * WD + w];
-                pf[w] = 0.0f;
-            }
+        for (int k0 = 0; k0 < K; k0 += KH) {
+            v4f accH[RPW][KH][DOUT];
 #pragma unroll
             for (int j = 0; j < RPW; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float* frow = sf + (16 * (wave + 4 * j) + 4 * lg + r) * FS + le;
-                    float fv[DIN];
+                for (int kk = 0; kk < KH; ++kk)
 #pragma unroll
-                    for (int i = 0; i < DIN; ++i) fv[i] = frow[16 * i];
+                    for (int o = 0; o < DOUT; ++o) accH[j][kk][o] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 2
+            for (int s = 0; s < NS; ++s) {
+                float b[DOUT];
+                const float* row = sG + (4 * s + lg) * GS + le;
 #pragma unroll
-                    for (int t = 0; t < T::NT; ++t) {
-                        const Term tm = T::terms[t];
-                        const float h = accH[j][k][tm.o][r];
-                        const float c = tm.neg ? -fk[tm.w] : fk[tm.w];
-                        dfs[j][tm.i][r] += c * h;
-                        pf[tm.w] += (tm.neg ? -fv[tm.i] : fv[tm.i]) * h;
+                for (int o = 0; o < DOUT; ++o) b[o] = row[16 * o];
+#pragma unroll
+                for (int j = 0; j < RPW; ++j)
+#pragma unroll
+                    for (int kk = 0; kk < KH; ++kk) {
+                        const float a = sCf[(((k0 + kk) * HRB + wave + 4 * j) * NS + s) * 64 + lane];
+#pragma unroll
+                        for (int o = 0; o < DOUT; ++o)
+                            accH[j][kk][o] = mfma(a, b[o], accH[j][kk][o]);
                     }
-                }
-            // sum over the 4 lane groups: the wave's 16 ci rows of this edge
-#pragma unroll
-            for (int w = 0; w < WD; ++w) {
-                float v = pf[w];
-                v += __shfl_xor(v, 16, 64);
-                v += __shfl_xor(v, 32, 64);
-                pf[w] = v;
             }
-            if (lg == 0) {
 #pragma unroll
-                for (int w = 0; w < WD; ++w) sG[((wave * K + k) * kNE + le) * WD + w] = pf[w];
+            for (int kk = 0; kk < KH; ++kk) {
+                const int k = k0 + kk;
+                float fk[WD], pf[WD];
+#pragma unroll
+                for (int w = 0; w < WD; ++w) {
+                    fk[w] = sFe[le * KW + k * WD + w];
+                    pf[w] = 0.0f;
+                }
+#pragma unroll
+                for (int j = 0; j < RPW; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float* frow = sf + (16 * (wave + 4 * j) + 4 * lg + r) * FS + le;
+                        float fv[DIN];
+#pragma unroll
+                        for (int i = 0; i < DIN; ++i) fv[i] = frow[16 * i];
+#pragma unroll
+                        for (int t = 0; t < T::NT; ++t) {
+                            const Term tm = T::terms[t];
+                            const float h = accH[j][kk][tm.o][r];
+                            const float c = tm.neg ? -fk[tm.w] : fk[tm.w];
+                            dfs[j][tm.i][r] += c * h;
+                            pf[tm.w] += (tm.neg ? -fv[tm.i] : fv[tm.i]) * h;
+                        }
+                    }
+                // sum over the 4 lane groups: the wave's 16 ci rows of this edge
+#pragma unroll
+                for (int w = 0; w < WD; ++w) {
+                    float v = pf[w];
+                    v += __shfl_xor(v, 16, 64);
+                    v += __shfl_xor(v, 32, 64);
+                    pf[w] = v;
+                }
+#pragma unroll
+                for (int q = 0; q < WQ; ++q) {
+                    const float v0 = pf[4 * q];
+                    const float v1 = 4 * q + 1 < WD ? pf[4 * q + 1 < WD ? 4 * q + 1 : 0] : 0.0f;
+                    const float v2 = 4 * q + 2 < WD ? pf[4 * q + 2 < WD ? 4 * q + 2 : 0] : 0.0f;
+                    const float v3 = 4 * q + 3 < WD ? pf[4 * q + 3 < WD ? 4 * q + 3 : 0] : 0.0f;
+                    pfs[k][q] = lg == 0 ? v0 : lg == 1 ? v1 : lg == 2 ? v2 : v3;
+                }
             }
         }
+        __syncthreads();   // gd no longer needed: its tile holds the dF partials, then dx
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+#pragma unroll
+            for (int q = 0; q < WQ; ++q) {
+                const int w = 4 * q + lg;
+                if (w < WD) sG[((wave * K + k) * kNE + le) * WD + w] = pfs[k][q];
+            }
         __syncthreads();
         const int64_t nval = E - e0 < kNE ? E - e0 : kNE;
         for (int q = tid; q < nval * KW; q += kThreads) {
@@ -491,7 +694,7 @@ k_ewc_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 // Backward, part 2: dC_k += U_k fs^T, U_k[co][16 i + e] = sum_t sign F_e[k, w] gd[co][16 o + e],
 // accumulated over the workgroup's tiles; one partial per workgroup.
 template <int CIN, int COUT, int LIN, int LOUT, int K>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kThreads, 1)
 k_ewc_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
             const float* __restrict__ x, const float* __restrict__ P, const float* __restrict__ Q,
             const float* __restrict__ dist, const float* __restrict__ F,
@@ -512,6 +715,7 @@ k_ewc_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     float* sSout = sSin + kNE * DIN;
     float* sFe = sSout + kNE * DOUT;
     TileEdge* sE = reinterpret_cast<TileEdge*>(sFe + kNE * KW);
+    int* sLo = reinterpret_cast<int*>(sE + kNE);   // next tile's lower bins
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int le = lane & 15, lg = lane >> 4;
@@ -520,14 +724,17 @@ k_ewc_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     for (int k = 0; k < K; ++k)
 #pragma unroll
         for (int j = 0; j < CTPW; ++j) accC[k][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    const int64_t G = gridDim.x;
+    BwdPipe<CIN, COUT, LIN, LOUT, K> pipe;
+    pipe.prologue(B, blockIdx.x, G, E, x, gy, P, Q, dist, F, sLo);
 
-    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    for (int64_t tile = blockIdx.x; tile < ntiles; tile += G) {
         const int64_t e0 = tile * kNE;
+        __syncthreads();   // the previous tile's readers of the LDS tiles are done
+        pipe.commit(B, E, e0, sP, sQ, sE, sSin, sSout, sLo);
         __syncthreads();
-        stage_tile<LIN, LOUT, K>(B, E, e0, P, Q, dist, F, sP, sQ, sE, sSin, sSout, sFe);
-        __syncthreads();
-        rotate_in<CIN, DIN>(E, e0, x, sP, sSin, sf, FS);
-        rotate_grad<COUT, DOUT>(E, e0, gy, sQ, sSout, sG, GS);
+        pipe.rotate(sE, sFe, sP, sQ, sSin, sSout, sf, FS, sG, GS);
+        pipe.next(tile, G, E, x, gy, P, Q, dist, F, sLo);   // in flight during the MFMA loops
 #pragma unroll
         for (int k = 0; k < K; ++k) {
             __syncthreads();   // gd ready; previous readers of sU are done
@@ -684,8 +891,8 @@ constexpr size_t fwd_lds() {
     using T = Canon<LIN, LOUT>;
     constexpr size_t FS = 16 * T::DIN + 1, YS = COUT * T::DOUT + 1;
     constexpr size_t BIG = CIN * FS > kNE * YS ? CIN * FS : kNE * YS;
-    return 4 * (static_cast<size_t>(K) * COUT * CIN + BIG + kNE * T::DIN * T::DIN +
-                kNE * T::DOUT * T::DOUT + kNE * T::DIN + kNE * T::DOUT + kNE * K * T::WD) +
+    return 4 * (BIG + kNE * T::DIN * T::DIN + kNE * T::DOUT * T::DOUT + kNE * T::DIN +
+                kNE * T::DOUT + kNE * K * T::WD) +
            kNE * sizeof(TileEdge);
 }
 
@@ -696,7 +903,7 @@ constexpr size_t bwd_x_lds() {
     constexpr size_t GBIG = COUT * GS > kNE * XS ? COUT * GS : kNE * XS;
     return 4 * (static_cast<size_t>(K) * COUT * CIN + CIN * FS + GBIG + kNE * T::DIN * T::DIN +
                 kNE * T::DOUT * T::DOUT + kNE * T::DIN + kNE * T::DOUT + kNE * K * T::WD) +
-           kNE * sizeof(TileEdge);
+           kNE * (sizeof(TileEdge) + sizeof(int));
 }
 
 template <int CIN, int COUT, int LIN, int LOUT, int K>
@@ -705,7 +912,7 @@ constexpr size_t bwd_c_lds() {
     constexpr size_t FS = 16 * T::DIN + 1, GS = 16 * T::DOUT + 1;
     return 4 * (CIN * FS + COUT * GS + COUT * FS + kNE * T::DIN * T::DIN + kNE * T::DOUT * T::DOUT +
                 kNE * T::DIN + kNE * T::DOUT + kNE * K * T::WD) +
-           kNE * sizeof(TileEdge);
+           kNE * (sizeof(TileEdge) + sizeof(int));
 }
 
 constexpr int64_t kBinChunk = 1024;
@@ -718,11 +925,12 @@ template <int CIN, int COUT, int LIN, int LOUT, int K>
 int launch_fwd(const feq_binning& B, int64_t E, const float* x, const float* P, const float* Q,
                const float* dist, const float* C, const float* F, float* y, hipStream_t s) {
     constexpr size_t lds = fwd_lds<CIN, COUT, LIN, LOUT, K>();
+    static_assert(lds <= 80 * 1024, "two forward workgroups must fit one CU's LDS");
     auto kern = k_ewc_fwd<CIN, COUT, LIN, LOUT, K>;
     if (int rc = set_lds(reinterpret_cast<const void*>(kern), lds)) return rc;
     const int64_t ntiles = ceil_div(E, kNE);
-    FEQ_LAUNCH("k_ewc_fwd", kern, dim3(grid_for(ntiles, lds <= 80 * 1024 ? 2 : 1)), dim3(kThreads), lds,
-                       s, B, E, ntiles, x, P, Q, dist, C, F, y);
+    FEQ_LAUNCH("k_ewc_fwd", kern, dim3(grid_for(ntiles, 2)), dim3(kThreads), lds, s, B, E, ntiles,
+               x, P, Q, dist, C, F, y);
     return FEQ_OK;
 }
 

@@ -305,9 +305,12 @@ extern "C" int feq_gather_rows(const float* src, int64_t nsrc, int64_t row, cons
     return FEQ_OK;
 }
 
+// Thread t of a node's workgroup serves head t % H of edge slot t / H; with H
+// not dividing kThreads the last partial slot idles and feeds neutral values
+// to the head reductions, so any 1 <= H <= kThreads works.
 static int check_heads(int32_t H, int32_t Dh) {
-    if (H < 1 || H > kThreads || (kThreads % H) != 0)
-        return fail(FEQ_ERR_UNSUPPORTED, "num_heads must divide %d", kThreads);
+    if (H < 1 || H > kThreads)
+        return fail(FEQ_ERR_UNSUPPORTED, "num_heads must be in [1, %d]", kThreads);
     if (Dh < 1) return fail(FEQ_ERR_INVALID, "head dim must be positive");
     return FEQ_OK;
 }
