@@ -25,6 +25,7 @@
 #include "feq_internal.h"
 
 #include <array>
+#include <type_traits>
 
 namespace feq {
 namespace {
@@ -147,6 +148,33 @@ struct RowRegs {
                 for (int d = 0; d < D; ++d) v[j][d] = 0.0f;
             }
         }
+    }
+};
+
+// x rows in the MFMA accumulator layout: lane (le, lg) of wave w holds rows
+// (e0 + le, c = 16 (w + 4 j) + 4 lg + r), r < 4.
+template <int CH, int D>
+struct LaneRows {
+    static constexpr int RPW = CH / 64;
+    static_assert(CH % 64 == 0, "lane rows need whole 64-channel groups");
+    float v[RPW][4][D];
+    __device__ __forceinline__ void load(const float* __restrict__ src, int64_t e0, int64_t E) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        const int le = lane & 15, lg = lane >> 4;
+        const bool ok = e0 + le < E;
+#pragma unroll
+        for (int j = 0; j < RPW; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (ok) {
+                    const float* p = src + ((e0 + le) * CH + 16 * (wave + 4 * j) + 4 * lg + r) * D;
+#pragma unroll
+                    for (int d = 0; d < D; ++d) v[j][r][d] = p[d];
+                } else {
+#pragma unroll
+                    for (int d = 0; d < D; ++d) v[j][r][d] = 0.0f;
+                }
+            }
     }
 };
 
@@ -451,11 +479,13 @@ k_ewc_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
 // and the distances of tiles t and t + G (G = gridDim.x); `next()` issues the
 // loads for tile t + G (whose bins are known one tile ahead) and the distance
 // of tile t + 2G, so every global load has a whole tile of work to arrive.
-template <int CIN, int COUT, int LIN, int LOUT, int K>
+template <int CIN, int COUT, int LIN, int LOUT, int K, bool XLANE>
 struct BwdPipe {
     using T = Canon<LIN, LOUT>;
     static constexpr int DIN = T::DIN, DOUT = T::DOUT, KW = K * T::WD;
-    RowRegs<CIN, DIN> xr;
+    // x rows: one (edge, channel) row per thread and pass (XLANE false, for an
+    // fs tile in LDS) or in the accumulator layout (XLANE true, fs in registers)
+    typename std::conditional<XLANE, LaneRows<CIN, DIN>, RowRegs<CIN, DIN>>::type xr;
     RowRegs<COUT, DOUT> gr;
     BlockRegs<kNE * DIN * DIN> pr;
     BlockRegs<kNE * DOUT * DOUT> qr;
@@ -498,14 +528,34 @@ struct BwdPipe {
         commit_edges<LIN, LOUT>(B, E, e0, r_cur, sE, sSin, sSout);
         if (threadIdx.x < kNE) sLo[threadIdx.x] = edge_bin(r_next, B).lo;
     }
-    // After the next barrier: F_e, fs = s^l (x P) and gd = s^l (gy Q) to LDS.
+    // After the next barrier: F_e, gd = s^l (gy Q) and (row layout) fs =
+    // s^l (x P) to LDS.
     __device__ __forceinline__ void rotate(const TileEdge* sE, float* sFe, const float* sP,
                                            const float* sQ, const float* sSin,
                                            const float* sSout, float* sf, int fs, float* sG,
                                            int gs) const {
         fr.commit(sE, sFe);
-        rotate_regs<CIN, DIN>(xr, sP, sSin, sf, fs);
+        if constexpr (!XLANE) rotate_regs<CIN, DIN>(xr, sP, sSin, sf, fs);
         rotate_regs<COUT, DOUT>(gr, sQ, sSout, sG, gs);
+    }
+    // Accumulator layout only: fsr[j][r][i] = s^l_i sum_d x[d] P_e[d, i] for
+    // the lane's rows of edge le.
+    template <int RPW>
+    __device__ __forceinline__ void lane_fs(const float* sP, const float* sSin,
+                                            float (&fsr)[RPW][4][DIN]) const {
+        const int le = threadIdx.x & 15;
+        const float* pe = sP + le * DIN * DIN;
+#pragma unroll
+        for (int j = 0; j < RPW; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int i = 0; i < DIN; ++i) {
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int d = 0; d < DIN; ++d) acc += xr.v[j][r][d] * pe[d * DIN + i];
+                    fsr[j][r][i] = acc * sSin[le * DIN + i];
+                }
     }
     // Once the tile's register data is in LDS (after a barrier): loads for tile t + G.
     __device__ __forceinline__ void next(int64_t t, int64_t G, int64_t E, const float* x,
@@ -518,8 +568,27 @@ struct BwdPipe {
     }
 };
 
-// Backward, part 1: H_k = C_k^T gd (MFMA), dfs = sum_k M_ek^T H_k and
-// dF_e[k, w] = sum_ci fs H_k in registers, dx = s^l dfs P^T.
+// A fragments of C_k^T for every rank component, staged once per workgroup in
+// fragment order: frag[((k * RB + rb) * NS + s) * 64 + lane] =
+// C_k[lg * NS + s][16 rb + le] (rows ci, reduction index co = lg * NS + s).
+template <int K, int RB, int NS>
+__device__ void stage_ct_frags(const float* __restrict__ C, int cout, int cin, float* frag) {
+    for (int q = threadIdx.x; q < K * RB * NS * 64; q += kThreads) {
+        const int lane = q & 63, s = (q >> 6) % NS, rb = ((q >> 6) / NS) % RB;
+        const int k = (q >> 6) / (NS * RB);
+        frag[q] = C[(static_cast<int64_t>(k) * cout + (lane >> 4) * NS + s) * cin + 16 * rb +
+                    (lane & 15)];
+    }
+}
+
+// Backward, part 1: H_k = C_k^T gd on the matrix cores, one rank component per
+// pass; in registers dfs = sum_k M_ek^T H_k and the per-edge radial gradient
+// dF_e[k, w] = sum_ci fs H_k; then dx = s^l dfs P^T.  One workgroup per CU
+// (512 registers per lane): the register contractions of pass k-1 are split
+// into NS chunks interleaved with the NS matrix-core steps of pass k, so the
+// vector ALU works in the matrix cores' shadow.  The next tile's inputs
+// (x rows in the accumulator layout, gy rows, P, Q, F rows) are loaded while
+// this tile's outputs are reduced and stored.
 template <int CIN, int COUT, int LIN, int LOUT, int K>
 __global__ void __launch_bounds__(kThreads, 1)
 k_ewc_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
@@ -528,21 +597,17 @@ k_ewc_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             const float* __restrict__ F, float* __restrict__ gx, float* __restrict__ dFe) {
     using T = Canon<LIN, LOUT>;
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
-    constexpr int FS = 16 * DIN + 1;      // fs rows
     constexpr int GS = 16 * DOUT + 1;     // gd rows
     constexpr int XS = CIN * DIN + 1;     // dx staging per edge
-    constexpr int HRB = CIN / 16, RPW = HRB / 4, NS = COUT / 4;
+    constexpr int RB = CIN / 16, RPW = CIN / 64, NS = COUT / 4;
     constexpr int GBIG = COUT * GS > kNE * XS ? COUT * GS : kNE * XS;
-    constexpr int DFN = 4 * K * kNE * WD;
-    constexpr int KH = K % 2 == 0 ? K / 2 : K;   // rank components per MFMA pass
-    constexpr int WQ = (WD + 3) / 4;             // dF partials per lane group
-    static_assert(CIN % 64 == 0 && COUT % 4 == 0, "unsupported channel counts");
-    static_assert(DFN <= GBIG, "dF partials must fit the gd tile");
+    constexpr int NTS = RPW * 4 * T::NT;  // register contraction steps per pass
+    static_assert(CIN % 64 == 0 && COUT % 16 == 0, "unsupported channel counts");
     extern __shared__ float4 smem4[];
-    float* sCf = reinterpret_cast<float*>(smem4);  // K x HRB x NS x 64 fragments of C_k^T
-    float* sf = sCf + K * HRB * NS * 64;           // CIN x FS
-    float* sG = sf + CIN * FS;                     // gd tile; later dF partials and dx staging
-    float* sP = sG + GBIG;
+    float* sA = reinterpret_cast<float*>(smem4);   // C_k^T fragments
+    float* sG = sA + K * CIN * COUT;               // gd tile, later dx staging
+    float* sDF = sG + GBIG;                        // dF_e partials per wave
+    float* sP = sDF + 4 * K * kNE * WD;
     float* sQ = sP + kNE * DIN * DIN;
     float* sSin = sQ + kNE * DOUT * DOUT;
     float* sSout = sSin + kNE * DIN;
@@ -552,9 +617,9 @@ k_ewc_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int le = lane & 15, lg = lane >> 4;
-    stage_frags<K, HRB, NS, true>(C, COUT, CIN, sCf);
+    stage_ct_frags<K, RB, NS>(C, COUT, CIN, sA);
     const int64_t G = gridDim.x;
-    BwdPipe<CIN, COUT, LIN, LOUT, K> pipe;
+    BwdPipe<CIN, COUT, LIN, LOUT, K, true> pipe;
     pipe.prologue(B, blockIdx.x, G, E, x, gy, P, Q, dist, F, sLo);
 
     for (int64_t tile = blockIdx.x; tile < ntiles; tile += G) {
@@ -562,106 +627,92 @@ k_ewc_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
         __syncthreads();   // the previous tile's readers of the LDS tiles are done
         pipe.commit(B, E, e0, sP, sQ, sE, sSin, sSout, sLo);
         __syncthreads();
-        pipe.rotate(sE, sFe, sP, sQ, sSin, sSout, sf, FS, sG, GS);
+        pipe.rotate(sE, sFe, sP, sQ, sSin, sSout, nullptr, 0, sG, GS);
+        float fsr[RPW][4][DIN];
+        pipe.template lane_fs<RPW>(sP, sSin, fsr);
         __syncthreads();
-        pipe.next(tile, G, E, x, gy, P, Q, dist, F, sLo);   // in flight during the MFMA loops
-        // Two passes over the rank components keep half the accumulators live.
-        // Lane group lg keeps the per-edge dF partials of the weights w = 4q + lg.
-        float dfs[RPW][DIN][4];
-        float pfs[K][WQ];
+
+        float dfs[RPW][4][DIN];
 #pragma unroll
         for (int j = 0; j < RPW; ++j)
 #pragma unroll
-            for (int i = 0; i < DIN; ++i)
+            for (int r = 0; r < 4; ++r)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) dfs[j][i][r] = 0.0f;
+                for (int i = 0; i < DIN; ++i) dfs[j][r][i] = 0.0f;
+        v4f accH[2][RPW][DOUT];
+        float fk[WD], pf[WD];
+        // pass k: matrix-core steps of rank component k (k < K) interleaved
+        // with the register contractions of component k - 1 (k > 0)
 #pragma unroll
-        for (int k0 = 0; k0 < K; k0 += KH) {
-            v4f accH[RPW][KH][DOUT];
-#pragma unroll
-            for (int j = 0; j < RPW; ++j)
-#pragma unroll
-                for (int kk = 0; kk < KH; ++kk)
-#pragma unroll
-                    for (int o = 0; o < DOUT; ++o) accH[j][kk][o] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 2
-            for (int s = 0; s < NS; ++s) {
-                float b[DOUT];
-                const float* row = sG + (4 * s + lg) * GS + le;
-#pragma unroll
-                for (int o = 0; o < DOUT; ++o) b[o] = row[16 * o];
+        for (int k = 0; k <= K; ++k) {
+            float b[2][DOUT];
+            if (k < K) {
 #pragma unroll
                 for (int j = 0; j < RPW; ++j)
 #pragma unroll
-                    for (int kk = 0; kk < KH; ++kk) {
-                        const float a = sCf[(((k0 + kk) * HRB + wave + 4 * j) * NS + s) * 64 + lane];
+                    for (int o = 0; o < DOUT; ++o) accH[k & 1][j][o] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int o = 0; o < DOUT; ++o) b[0][o] = sG[lg * NS * GS + le + 16 * o];
+            }
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                if (k < K) {
+                    if (s + 1 < NS) {
+                        const float* row = sG + (lg * NS + s + 1) * GS + le;
+#pragma unroll
+                        for (int o = 0; o < DOUT; ++o) b[(s + 1) & 1][o] = row[16 * o];
+                    }
+#pragma unroll
+                    for (int j = 0; j < RPW; ++j) {
+                        const float a = sA[((k * RB + wave + 4 * j) * NS + s) * 64 + lane];
 #pragma unroll
                         for (int o = 0; o < DOUT; ++o)
-                            accH[j][kk][o] = mfma(a, b[o], accH[j][kk][o]);
+                            accH[k & 1][j][o] = mfma(a, b[s & 1][o], accH[k & 1][j][o]);
                     }
-            }
-#pragma unroll
-            for (int kk = 0; kk < KH; ++kk) {
-                const int k = k0 + kk;
-                float fk[WD], pf[WD];
-#pragma unroll
-                for (int w = 0; w < WD; ++w) {
-                    fk[w] = sFe[le * KW + k * WD + w];
-                    pf[w] = 0.0f;
                 }
+                if (k > 0) {
+                    const int kp = k - 1;
+                    if (s == 0) {
 #pragma unroll
-                for (int j = 0; j < RPW; ++j)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float* frow = sf + (16 * (wave + 4 * j) + 4 * lg + r) * FS + le;
-                        float fv[DIN];
-#pragma unroll
-                        for (int i = 0; i < DIN; ++i) fv[i] = frow[16 * i];
-#pragma unroll
-                        for (int t = 0; t < T::NT; ++t) {
-                            const Term tm = T::terms[t];
-                            const float h = accH[j][kk][tm.o][r];
-                            const float c = tm.neg ? -fk[tm.w] : fk[tm.w];
-                            dfs[j][tm.i][r] += c * h;
-                            pf[tm.w] += (tm.neg ? -fv[tm.i] : fv[tm.i]) * h;
+                        for (int w = 0; w < WD; ++w) {
+                            fk[w] = sFe[le * KW + kp * WD + w];
+                            pf[w] = 0.0f;
                         }
                     }
-                // sum over the 4 lane groups: the wave's 16 ci rows of this edge
 #pragma unroll
-                for (int w = 0; w < WD; ++w) {
-                    float v = pf[w];
-                    v += __shfl_xor(v, 16, 64);
-                    v += __shfl_xor(v, 32, 64);
-                    pf[w] = v;
-                }
+                    for (int ts = s * NTS / NS; ts < (s + 1) * NTS / NS; ++ts) {
+                        const int j = ts / (4 * T::NT), r = (ts / T::NT) % 4;
+                        const Term tm = T::terms[ts % T::NT];
+                        const float h = accH[kp & 1][j][tm.o][r];
+                        const float c = tm.neg ? -fk[tm.w] : fk[tm.w];
+                        dfs[j][r][tm.i] += c * h;
+                        pf[tm.w] += (tm.neg ? -fsr[j][r][tm.i] : fsr[j][r][tm.i]) * h;
+                    }
+                    if (s == NS - 1) {
+                        // sum over the 4 lane groups: the wave's rows of this edge
 #pragma unroll
-                for (int q = 0; q < WQ; ++q) {
-                    const float v0 = pf[4 * q];
-                    const float v1 = 4 * q + 1 < WD ? pf[4 * q + 1 < WD ? 4 * q + 1 : 0] : 0.0f;
-                    const float v2 = 4 * q + 2 < WD ? pf[4 * q + 2 < WD ? 4 * q + 2 : 0] : 0.0f;
-                    const float v3 = 4 * q + 3 < WD ? pf[4 * q + 3 < WD ? 4 * q + 3 : 0] : 0.0f;
-                    pfs[k][q] = lg == 0 ? v0 : lg == 1 ? v1 : lg == 2 ? v2 : v3;
+                        for (int w = 0; w < WD; ++w) {
+                            float v = pf[w];
+                            v += __shfl_xor(v, 16, 64);
+                            v += __shfl_xor(v, 32, 64);
+                            if (lg == 0) sDF[((wave * K + kp) * kNE + le) * WD + w] = v;
+                        }
+                    }
                 }
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-        __syncthreads();   // gd no longer needed: its tile holds the dF partials, then dx
-#pragma unroll
-        for (int k = 0; k < K; ++k)
-#pragma unroll
-            for (int q = 0; q < WQ; ++q) {
-                const int w = 4 * q + lg;
-                if (w < WD) sG[((wave * K + k) * kNE + le) * WD + w] = pfs[k][q];
-            }
-        __syncthreads();
+        __syncthreads();   // dF partials complete; gd no longer needed
+        // next tile's loads: in flight during the dF reduction, dx and the stores
+        pipe.next(tile, G, E, x, gy, P, Q, dist, F, sLo);
         const int64_t nval = E - e0 < kNE ? E - e0 : kNE;
         for (int q = tid; q < nval * KW; q += kThreads) {
             const int e = q / KW, kw = q % KW, k = kw / WD, w = kw % WD;
-            float a = 0.0f;
+            float acc = 0.0f;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) a += sG[((v * K + k) * kNE + e) * WD + w];
-            dFe[(e0 + e) * KW + kw] = a;
+            for (int v = 0; v < 4; ++v) acc += sDF[((v * K + k) * kNE + e) * WD + w];
+            dFe[(e0 + e) * KW + kw] = acc;
         }
-        __syncthreads();
         // dx = s^l dfs P^T, staged through LDS for coalesced stores
         {
             const float* pe = sP + le * DIN * DIN;
@@ -673,97 +724,180 @@ k_ewc_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int ci = 16 * (wave + 4 * j) + 4 * lg + r;
+                    float ds[DIN];
+#pragma unroll
+                    for (int i = 0; i < DIN; ++i) ds[i] = dfs[j][r][i] * si[i];
 #pragma unroll
                     for (int d = 0; d < DIN; ++d) {
-                        float a = 0.0f;
+                        float acc = 0.0f;
 #pragma unroll
-                        for (int i = 0; i < DIN; ++i) a += dfs[j][i][r] * si[i] * pe[d * DIN + i];
-                        sG[le * XS + ci * DIN + d] = a;
+                        for (int i = 0; i < DIN; ++i) acc += ds[i] * pe[d * DIN + i];
+                        sG[le * XS + ci * DIN + d] = acc;
                     }
                 }
         }
         __syncthreads();
         float* xt = gx + e0 * CIN * DIN;
-        for (int q = tid; q < nval * CIN * DIN; q += kThreads) {
-            const int e = q / (CIN * DIN), rest = q % (CIN * DIN);
-            xt[q] = sG[e * XS + rest];
+        if (nval == kNE) {
+#pragma unroll
+            for (int m = 0; m < kNE * CIN * DIN / kThreads; ++m) {
+                const int q = tid + kThreads * m;
+                xt[q] = sG[(q / (CIN * DIN)) * XS + q % (CIN * DIN)];
+            }
+        } else {
+            for (int q = tid; q < nval * CIN * DIN; q += kThreads)
+                xt[q] = sG[(q / (CIN * DIN)) * XS + q % (CIN * DIN)];
         }
     }
 }
 
-// Backward, part 2: dC_k += U_k fs^T, U_k[co][16 i + e] = sum_t sign F_e[k, w] gd[co][16 o + e],
-// accumulated over the workgroup's tiles; one partial per workgroup.
+// s^l of every m-first slot of a canonical representation with lmax L, from s.
+template <int L>
+__device__ __forceinline__ void slot_powers(float s, float (&pw)[(L + 1) * (L + 1)]) {
+    float p[L + 1];
+    p[0] = 1.0f;
+#pragma unroll
+    for (int l = 1; l <= L; ++l) p[l] = p[l - 1] * s;
+#pragma unroll
+    for (int j = 0; j < (L + 1) * (L + 1); ++j) pw[j] = p[SlotL<L>::l[j]];
+}
+
+// Rows (e, c) of a tile rotated into the m-first frame with per-edge matrices
+// read by wave-uniform (scalar) loads; thread t owns rows q = t + kThreads j,
+// whose edge e = q / CH is the same for the whole wave (CH % 64 == 0).
+// out[j][i] = s_e^l_i sum_d rows(e, c)[d] R_e[d, i]; padding edges give zeros.
+template <int CH, int L>
+__device__ __forceinline__ void rotate_rows_uniform(const float* __restrict__ src,
+                                                    const float* __restrict__ R, int64_t e0,
+                                                    int64_t E, const TileEdge* sE,
+                                                    float (&out)[kNE * CH / kThreads][(L + 1) * (L + 1)]) {
+    constexpr int D = (L + 1) * (L + 1), NR = kNE * CH / kThreads;
+    static_assert(CH % 64 == 0, "one edge per wave and row");
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+        const int q = wv * 64 + lane + kThreads * j;
+        const int e = (wv * 64 + kThreads * j) / CH, c = q % CH;
+        if (e0 + e < E) {
+            const float* row = src + ((e0 + e) * CH + c) * D;
+            const float* re = R + (e0 + e) * D * D;
+            float v[D], pw[D];
+#pragma unroll
+            for (int d = 0; d < D; ++d) v[d] = row[d];
+            slot_powers<L>(sE[e].s, pw);
+#pragma unroll
+            for (int i = 0; i < D; ++i) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int d = 0; d < D; ++d) acc += v[d] * re[d * D + i];
+                out[j][i] = acc * pw[i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < D; ++i) out[j][i] = 0.0f;
+        }
+    }
+}
+
+// Backward, part 2: dC_k += U_k fs^T with U_k[co][16 i + e] = (M_ek^T gd)[co][i]
+// for rank component k; one partial per workgroup.  Two workgroups share a
+// CU: P and Q are read with wave-uniform loads, gd stays in the registers of
+// the threads that build U_k, and LDS holds only the fs tile and one U_k tile
+// (row stride 16 Din + 4 floats, so each 16-lane quarter of a 128-bit operand
+// read covers all 64 banks once).  The reduction index is ordered c = KL lg +
+// s: lane group lg covers KL = 4 Din consecutive columns, read four at a time.
 template <int CIN, int COUT, int LIN, int LOUT, int K>
-__global__ void __launch_bounds__(kThreads, 1)
+__global__ void __launch_bounds__(kThreads, 2)
 k_ewc_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
             const float* __restrict__ x, const float* __restrict__ P, const float* __restrict__ Q,
             const float* __restrict__ dist, const float* __restrict__ F,
             float* __restrict__ dC_part) {
     using T = Canon<LIN, LOUT>;
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
-    constexpr int FS = 16 * DIN + 1, GS = 16 * DOUT + 1;
+    constexpr int RS = 16 * DIN + 4;
+    constexpr int KL = 4 * DIN, NG = DIN;       // columns per lane group, float4 groups
     constexpr int CT = (COUT / 16) * (CIN / 16);
     constexpr int CTPW = CT / 4;
-    static_assert(CT % 4 == 0, "dC tiles must split over 4 waves");
+    constexpr int NRX = kNE * CIN / kThreads, NRG = kNE * COUT / kThreads;
+    static_assert(CT % 4 == 0 && CIN % 64 == 0 && COUT % 64 == 0, "unsupported channel counts");
     extern __shared__ float4 smem4[];
-    float* sf = reinterpret_cast<float*>(smem4);   // CIN x FS
-    float* sG = sf + CIN * FS;                     // COUT x GS
-    float* sU = sG + COUT * GS;                    // COUT x FS
-    float* sP = sU + COUT * FS;
-    float* sQ = sP + kNE * DIN * DIN;
-    float* sSin = sQ + kNE * DOUT * DOUT;
-    float* sSout = sSin + kNE * DIN;
-    float* sFe = sSout + kNE * DOUT;
+    float* sf = reinterpret_cast<float*>(smem4);   // CIN x RS, fs[ci][16 i + e]
+    float* sU = sf + CIN * RS;                     // COUT x RS, U_k[co][16 i + e]
+    float* sFe = sU + COUT * RS;
     TileEdge* sE = reinterpret_cast<TileEdge*>(sFe + kNE * KW);
-    int* sLo = reinterpret_cast<int*>(sE + kNE);   // next tile's lower bins
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int le = lane & 15, lg = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
     v4f accC[K][CTPW];
 #pragma unroll
     for (int k = 0; k < K; ++k)
 #pragma unroll
         for (int j = 0; j < CTPW; ++j) accC[k][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    const int64_t G = gridDim.x;
-    BwdPipe<CIN, COUT, LIN, LOUT, K> pipe;
-    pipe.prologue(B, blockIdx.x, G, E, x, gy, P, Q, dist, F, sLo);
 
-    for (int64_t tile = blockIdx.x; tile < ntiles; tile += G) {
+    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
         const int64_t e0 = tile * kNE;
         __syncthreads();   // the previous tile's readers of the LDS tiles are done
-        pipe.commit(B, E, e0, sP, sQ, sE, sSin, sSout, sLo);
+        if (tid < kNE) {
+            TileEdge te;
+            te.valid = (e0 + tid) < E;
+            const float r = te.valid ? dist[e0 + tid] : 1.0f;
+            const EdgeBin eb = edge_bin(r, B);
+            te.lo = eb.lo;
+            te.t = eb.t;
+            te.s = r / (r + B.sh_scale);
+            sE[tid] = te;
+        }
         __syncthreads();
-        pipe.rotate(sE, sFe, sP, sQ, sSin, sSout, sf, FS, sG, GS);
-        pipe.next(tile, G, E, x, gy, P, Q, dist, F, sLo);   // in flight during the MFMA loops
+        interp_tile<KW>(sE, F, sFe);
+        {
+            float fsr[NRX][DIN];
+            rotate_rows_uniform<CIN, LIN>(x, P, e0, E, sE, fsr);
+#pragma unroll
+            for (int j = 0; j < NRX; ++j) {
+                const int e = (wv * 64 + kThreads * j) / CIN, c = (wv * 64 + lane + kThreads * j) % CIN;
+#pragma unroll
+                for (int i = 0; i < DIN; ++i) sf[c * RS + 16 * i + e] = fsr[j][i];
+            }
+        }
+        float gdr[NRG][DOUT];
+        rotate_rows_uniform<COUT, LOUT>(gy, Q, e0, E, sE, gdr);
 #pragma unroll
         for (int k = 0; k < K; ++k) {
-            __syncthreads();   // gd ready; previous readers of sU are done
-            for (int q = tid; q < kNE * COUT; q += kThreads) {
-                const int e = q / COUT, co = q % COUT;
-                float g[DOUT], u[DIN];
+            if (k > 0) __syncthreads();   // the previous U_k is no longer read
 #pragma unroll
-                for (int o = 0; o < DOUT; ++o) g[o] = sG[co * GS + 16 * o + e];
+            for (int j = 0; j < NRG; ++j) {
+                const int e = (wv * 64 + kThreads * j) / COUT, co = (wv * 64 + lane + kThreads * j) % COUT;
+                const float* fe = sFe + e * KW + k * WD;
+                float u[DIN];
 #pragma unroll
                 for (int i = 0; i < DIN; ++i) u[i] = 0.0f;
-                const float* fe = sFe + e * KW + k * WD;
 #pragma unroll
                 for (int t = 0; t < T::NT; ++t) {
                     const Term tm = T::terms[t];
                     const float c = tm.neg ? -fe[tm.w] : fe[tm.w];
-                    u[tm.i] += c * g[tm.o];
+                    u[tm.i] += c * gdr[j][tm.o];
                 }
 #pragma unroll
-                for (int i = 0; i < DIN; ++i) sU[co * FS + 16 * i + e] = u[i];
+                for (int i = 0; i < DIN; ++i) sU[co * RS + 16 * i + e] = u[i];
             }
-            __syncthreads();
+            __syncthreads();   // U_k (and at k = 0 the fs tile) complete
 #pragma unroll
-            for (int j = 0; j < CTPW; ++j) {
-                const int tt = wave + 4 * j;
-                const int rbA = tt / (CIN / 16), cbB = tt % (CIN / 16);
-                const float* arow = sU + (16 * rbA + le) * FS + lg;
-                const float* brow = sf + (16 * cbB + le) * FS + lg;
-#pragma unroll 4
-                for (int s = 0; s < 4 * DIN; ++s) accC[k][j] = mfma(arow[4 * s], brow[4 * s], accC[k][j]);
+            for (int g = 0; g < NG; ++g) {
+#pragma unroll
+                for (int j = 0; j < CTPW; ++j) {
+                    const int tt = wave + 4 * j;
+                    const int rbA = tt / (CIN / 16), cbB = tt % (CIN / 16);
+                    const float4 aq = *reinterpret_cast<const float4*>(
+                        sU + (16 * rbA + le) * RS + KL * lg + 4 * g);
+                    const float4 bq = *reinterpret_cast<const float4*>(
+                        sf + (16 * cbB + le) * RS + KL * lg + 4 * g);
+                    accC[k][j] = mfma(aq.x, bq.x, accC[k][j]);
+                    accC[k][j] = mfma(aq.y, bq.y, accC[k][j]);
+                    accC[k][j] = mfma(aq.z, bq.z, accC[k][j]);
+                    accC[k][j] = mfma(aq.w, bq.w, accC[k][j]);
+                }
             }
         }
     }
@@ -899,20 +1033,19 @@ constexpr size_t fwd_lds() {
 template <int CIN, int COUT, int LIN, int LOUT, int K>
 constexpr size_t bwd_x_lds() {
     using T = Canon<LIN, LOUT>;
-    constexpr size_t FS = 16 * T::DIN + 1, GS = 16 * T::DOUT + 1, XS = CIN * T::DIN + 1;
+    constexpr size_t GS = 16 * T::DOUT + 1, XS = CIN * T::DIN + 1;
     constexpr size_t GBIG = COUT * GS > kNE * XS ? COUT * GS : kNE * XS;
-    return 4 * (static_cast<size_t>(K) * COUT * CIN + CIN * FS + GBIG + kNE * T::DIN * T::DIN +
-                kNE * T::DOUT * T::DOUT + kNE * T::DIN + kNE * T::DOUT + kNE * K * T::WD) +
+    return 4 * (static_cast<size_t>(K) * CIN * COUT + GBIG + 4 * K * kNE * T::WD +
+                kNE * T::DIN * T::DIN + kNE * T::DOUT * T::DOUT + kNE * T::DIN + kNE * T::DOUT +
+                kNE * K * T::WD) +
            kNE * (sizeof(TileEdge) + sizeof(int));
 }
 
 template <int CIN, int COUT, int LIN, int LOUT, int K>
 constexpr size_t bwd_c_lds() {
     using T = Canon<LIN, LOUT>;
-    constexpr size_t FS = 16 * T::DIN + 1, GS = 16 * T::DOUT + 1;
-    return 4 * (CIN * FS + COUT * GS + COUT * FS + kNE * T::DIN * T::DIN + kNE * T::DOUT * T::DOUT +
-                kNE * T::DIN + kNE * T::DOUT + kNE * K * T::WD) +
-           kNE * (sizeof(TileEdge) + sizeof(int));
+    constexpr size_t RS = 16 * T::DIN + 4;
+    return 4 * (CIN * RS + COUT * RS + kNE * K * T::WD) + kNE * sizeof(TileEdge);
 }
 
 constexpr int64_t kBinChunk = 1024;
