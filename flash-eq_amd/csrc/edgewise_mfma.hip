@@ -568,187 +568,18 @@ struct BwdPipe {
     }
 };
 
-// A fragments of C_k^T for every rank component, staged once per workgroup in
-// fragment order: frag[((k * RB + rb) * NS + s) * 64 + lane] =
-// C_k[lg * NS + s][16 rb + le] (rows ci, reduction index co = lg * NS + s).
-template <int K, int RB, int NS>
-__device__ void stage_ct_frags(const float* __restrict__ C, int cout, int cin, float* frag) {
-    for (int q = threadIdx.x; q < K * RB * NS * 64; q += kThreads) {
-        const int lane = q & 63, s = (q >> 6) % NS, rb = ((q >> 6) / NS) % RB;
-        const int k = (q >> 6) / (NS * RB);
-        frag[q] = C[(static_cast<int64_t>(k) * cout + (lane >> 4) * NS + s) * cin + 16 * rb +
-                    (lane & 15)];
-    }
-}
-
-// Backward, part 1: H_k = C_k^T gd on the matrix cores, one rank component per
-// pass; in registers dfs = sum_k M_ek^T H_k and the per-edge radial gradient
-// dF_e[k, w] = sum_ci fs H_k; then dx = s^l dfs P^T.  One workgroup per CU
-// (512 registers per lane): the register contractions of pass k-1 are split
-// into NS chunks interleaved with the NS matrix-core steps of pass k, so the
-// vector ALU works in the matrix cores' shadow.  The next tile's inputs
-// (x rows in the accumulator layout, gy rows, P, Q, F rows) are loaded while
-// this tile's outputs are reduced and stored.
-template <int CIN, int COUT, int LIN, int LOUT, int K>
-__global__ void __launch_bounds__(kThreads, 1)
-k_ewc_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
-            const float* __restrict__ x, const float* __restrict__ P, const float* __restrict__ Q,
-            const float* __restrict__ dist, const float* __restrict__ C,
-            const float* __restrict__ F, float* __restrict__ gx, float* __restrict__ dFe) {
-    using T = Canon<LIN, LOUT>;
-    constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
-    constexpr int GS = 16 * DOUT + 1;     // gd rows
-    constexpr int XS = CIN * DIN + 1;     // dx staging per edge
-    constexpr int RB = CIN / 16, RPW = CIN / 64, NS = COUT / 4;
-    constexpr int GBIG = COUT * GS > kNE * XS ? COUT * GS : kNE * XS;
-    constexpr int NTS = RPW * 4 * T::NT;  // register contraction steps per pass
-    static_assert(CIN % 64 == 0 && COUT % 16 == 0, "unsupported channel counts");
-    extern __shared__ float4 smem4[];
-    float* sA = reinterpret_cast<float*>(smem4);   // C_k^T fragments
-    float* sG = sA + K * CIN * COUT;               // gd tile, later dx staging
-    float* sDF = sG + GBIG;                        // dF_e partials per wave
-    float* sP = sDF + 4 * K * kNE * WD;
-    float* sQ = sP + kNE * DIN * DIN;
-    float* sSin = sQ + kNE * DOUT * DOUT;
-    float* sSout = sSin + kNE * DIN;
-    float* sFe = sSout + kNE * DOUT;
-    TileEdge* sE = reinterpret_cast<TileEdge*>(sFe + kNE * KW);
-    int* sLo = reinterpret_cast<int*>(sE + kNE);   // next tile's lower bins
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// A fragments of C_k^T for one rank component: lane (le, lg) of wave w holds
+// C_k[lg * NS + s][16 (w + 4 j) + le] for every s (read from L2 per pass).
+template <int RPW, int NS>
+__device__ __forceinline__ void load_ct_frags(const float* __restrict__ C, int k, int cout,
+                                              int cin, float (&a)[RPW][NS]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int le = lane & 15, lg = lane >> 4;
-    stage_ct_frags<K, RB, NS>(C, COUT, CIN, sA);
-    const int64_t G = gridDim.x;
-    BwdPipe<CIN, COUT, LIN, LOUT, K, true> pipe;
-    pipe.prologue(B, blockIdx.x, G, E, x, gy, P, Q, dist, F, sLo);
-
-    for (int64_t tile = blockIdx.x; tile < ntiles; tile += G) {
-        const int64_t e0 = tile * kNE;
-        __syncthreads();   // the previous tile's readers of the LDS tiles are done
-        pipe.commit(B, E, e0, sP, sQ, sE, sSin, sSout, sLo);
-        __syncthreads();
-        pipe.rotate(sE, sFe, sP, sQ, sSin, sSout, nullptr, 0, sG, GS);
-        float fsr[RPW][4][DIN];
-        pipe.template lane_fs<RPW>(sP, sSin, fsr);
-        __syncthreads();
-
-        float dfs[RPW][4][DIN];
 #pragma unroll
-        for (int j = 0; j < RPW; ++j)
+    for (int j = 0; j < RPW; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-                for (int i = 0; i < DIN; ++i) dfs[j][r][i] = 0.0f;
-        v4f accH[2][RPW][DOUT];
-        float fk[WD], pf[WD];
-        // pass k: matrix-core steps of rank component k (k < K) interleaved
-        // with the register contractions of component k - 1 (k > 0)
-#pragma unroll
-        for (int k = 0; k <= K; ++k) {
-            float b[2][DOUT];
-            if (k < K) {
-#pragma unroll
-                for (int j = 0; j < RPW; ++j)
-#pragma unroll
-                    for (int o = 0; o < DOUT; ++o) accH[k & 1][j][o] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int o = 0; o < DOUT; ++o) b[0][o] = sG[lg * NS * GS + le + 16 * o];
-            }
-#pragma unroll
-            for (int s = 0; s < NS; ++s) {
-                if (k < K) {
-                    if (s + 1 < NS) {
-                        const float* row = sG + (lg * NS + s + 1) * GS + le;
-#pragma unroll
-                        for (int o = 0; o < DOUT; ++o) b[(s + 1) & 1][o] = row[16 * o];
-                    }
-#pragma unroll
-                    for (int j = 0; j < RPW; ++j) {
-                        const float a = sA[((k * RB + wave + 4 * j) * NS + s) * 64 + lane];
-#pragma unroll
-                        for (int o = 0; o < DOUT; ++o)
-                            accH[k & 1][j][o] = mfma(a, b[s & 1][o], accH[k & 1][j][o]);
-                    }
-                }
-                if (k > 0) {
-                    const int kp = k - 1;
-                    if (s == 0) {
-#pragma unroll
-                        for (int w = 0; w < WD; ++w) {
-                            fk[w] = sFe[le * KW + kp * WD + w];
-                            pf[w] = 0.0f;
-                        }
-                    }
-#pragma unroll
-                    for (int ts = s * NTS / NS; ts < (s + 1) * NTS / NS; ++ts) {
-                        const int j = ts / (4 * T::NT), r = (ts / T::NT) % 4;
-                        const Term tm = T::terms[ts % T::NT];
-                        const float h = accH[kp & 1][j][tm.o][r];
-                        const float c = tm.neg ? -fk[tm.w] : fk[tm.w];
-                        dfs[j][r][tm.i] += c * h;
-                        pf[tm.w] += (tm.neg ? -fsr[j][r][tm.i] : fsr[j][r][tm.i]) * h;
-                    }
-                    if (s == NS - 1) {
-                        // sum over the 4 lane groups: the wave's rows of this edge
-#pragma unroll
-                        for (int w = 0; w < WD; ++w) {
-                            float v = pf[w];
-                            v += __shfl_xor(v, 16, 64);
-                            v += __shfl_xor(v, 32, 64);
-                            if (lg == 0) sDF[((wave * K + kp) * kNE + le) * WD + w] = v;
-                        }
-                    }
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-        __syncthreads();   // dF partials complete; gd no longer needed
-        // next tile's loads: in flight during the dF reduction, dx and the stores
-        pipe.next(tile, G, E, x, gy, P, Q, dist, F, sLo);
-        const int64_t nval = E - e0 < kNE ? E - e0 : kNE;
-        for (int q = tid; q < nval * KW; q += kThreads) {
-            const int e = q / KW, kw = q % KW, k = kw / WD, w = kw % WD;
-            float acc = 0.0f;
-#pragma unroll
-            for (int v = 0; v < 4; ++v) acc += sDF[((v * K + k) * kNE + e) * WD + w];
-            dFe[(e0 + e) * KW + kw] = acc;
-        }
-        // dx = s^l dfs P^T, staged through LDS for coalesced stores
-        {
-            const float* pe = sP + le * DIN * DIN;
-            float si[DIN];
-#pragma unroll
-            for (int i = 0; i < DIN; ++i) si[i] = sSin[le * DIN + i];
-#pragma unroll
-            for (int j = 0; j < RPW; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int ci = 16 * (wave + 4 * j) + 4 * lg + r;
-                    float ds[DIN];
-#pragma unroll
-                    for (int i = 0; i < DIN; ++i) ds[i] = dfs[j][r][i] * si[i];
-#pragma unroll
-                    for (int d = 0; d < DIN; ++d) {
-                        float acc = 0.0f;
-#pragma unroll
-                        for (int i = 0; i < DIN; ++i) acc += ds[i] * pe[d * DIN + i];
-                        sG[le * XS + ci * DIN + d] = acc;
-                    }
-                }
-        }
-        __syncthreads();
-        float* xt = gx + e0 * CIN * DIN;
-        if (nval == kNE) {
-#pragma unroll
-            for (int m = 0; m < kNE * CIN * DIN / kThreads; ++m) {
-                const int q = tid + kThreads * m;
-                xt[q] = sG[(q / (CIN * DIN)) * XS + q % (CIN * DIN)];
-            }
-        } else {
-            for (int q = tid; q < nval * CIN * DIN; q += kThreads)
-                xt[q] = sG[(q / (CIN * DIN)) * XS + q % (CIN * DIN)];
-        }
-    }
+        for (int s = 0; s < NS; ++s)
+            a[j][s] = C[(static_cast<int64_t>(k) * cout + lg * NS + s) * cin + 16 * (wave + 4 * j) + le];
 }
 
 // s^l of every m-first slot of a canonical representation with lmax L, from s.
@@ -796,6 +627,192 @@ __device__ __forceinline__ void rotate_rows_uniform(const float* __restrict__ sr
         } else {
 #pragma unroll
             for (int i = 0; i < D; ++i) out[j][i] = 0.0f;
+        }
+    }
+}
+
+// Backward, part 1: H_k = C_k^T gd on the matrix cores, one rank component per
+// pass; in registers dfs = sum_k M_ek^T H_k and the per-edge radial gradient
+// dF_e[k, w] = sum_ci fs H_k; then dx = s^l dfs P^T.  Two workgroups share a
+// CU: C_k^T streams from L2 (the next component is prefetched during the
+// current pass), Q is read with wave-uniform loads, fs is built directly in
+// the accumulator layout, and LDS holds the gd tile, P and the dF partials.
+template <int CIN, int COUT, int LIN, int LOUT, int K>
+__global__ void __launch_bounds__(kThreads, 2)
+k_ewc_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
+            const float* __restrict__ x, const float* __restrict__ P, const float* __restrict__ Q,
+            const float* __restrict__ dist, const float* __restrict__ C,
+            const float* __restrict__ F, float* __restrict__ gx, float* __restrict__ dFe) {
+    using T = Canon<LIN, LOUT>;
+    constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
+    constexpr int GS = 16 * DOUT + 1;     // gd rows
+    constexpr int XS = CIN * DIN + 1;     // dx staging per edge
+    constexpr int RPW = CIN / 64, NS = COUT / 4, NRG = kNE * COUT / kThreads;
+    constexpr int GBIG = COUT * GS > kNE * XS ? COUT * GS : kNE * XS;
+    static_assert(CIN % 64 == 0 && COUT % 64 == 0, "unsupported channel counts");
+    extern __shared__ float4 smem4[];
+    float* sG = reinterpret_cast<float*>(smem4);   // gd tile, later dx staging
+    float* sDF = sG + GBIG;                        // dF_e partials per wave
+    float* sP = sDF + 4 * K * kNE * WD;
+    float* sFe = sP + kNE * DIN * DIN;
+    TileEdge* sE = reinterpret_cast<TileEdge*>(sFe + kNE * KW);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int le = lane & 15, lg = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+
+    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const int64_t e0 = tile * kNE;
+        __syncthreads();   // the previous tile's readers of the LDS tiles are done
+        {
+            BlockRegs<kNE * DIN * DIN> pr;
+            pr.load(P, e0 * DIN * DIN, E * DIN * DIN);
+            pr.store(sP);
+        }
+        if (tid < kNE) {
+            TileEdge te;
+            te.valid = (e0 + tid) < E;
+            const float r = te.valid ? dist[e0 + tid] : 1.0f;
+            const EdgeBin eb = edge_bin(r, B);
+            te.lo = eb.lo;
+            te.t = eb.t;
+            te.s = r / (r + B.sh_scale);
+            sE[tid] = te;
+        }
+        __syncthreads();
+        interp_tile<KW>(sE, F, sFe);
+        {
+            float gdr[NRG][DOUT];
+            rotate_rows_uniform<COUT, LOUT>(gy, Q, e0, E, sE, gdr);
+#pragma unroll
+            for (int j = 0; j < NRG; ++j) {
+                const int e = (wv * 64 + kThreads * j) / COUT;
+                const int co = (wv * 64 + lane + kThreads * j) % COUT;
+#pragma unroll
+                for (int o = 0; o < DOUT; ++o) sG[co * GS + 16 * o + e] = gdr[j][o];
+            }
+        }
+        float pin[DIN];
+        slot_powers<LIN>(sE[le].s, pin);
+        float fsr[RPW][4][DIN];
+        {
+            LaneRows<CIN, DIN> xr;
+            xr.load(x, e0, E);
+            const float* pe = sP + le * DIN * DIN;
+#pragma unroll
+            for (int j = 0; j < RPW; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int i = 0; i < DIN; ++i) {
+                        float acc = 0.0f;
+#pragma unroll
+                        for (int d = 0; d < DIN; ++d) acc += xr.v[j][r][d] * pe[d * DIN + i];
+                        fsr[j][r][i] = acc * pin[i];
+                    }
+        }
+        float a_cur[RPW][NS];
+        __syncthreads();   // gd tile complete
+
+        float dfs[RPW][4][DIN];
+#pragma unroll
+        for (int j = 0; j < RPW; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int i = 0; i < DIN; ++i) dfs[j][r][i] = 0.0f;
+#pragma unroll 1
+        for (int k = 0; k < K; ++k) {
+            load_ct_frags<RPW, NS>(C, k, COUT, CIN, a_cur);
+            v4f accH[RPW][DOUT];
+#pragma unroll
+            for (int j = 0; j < RPW; ++j)
+#pragma unroll
+                for (int o = 0; o < DOUT; ++o) accH[j][o] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            float b[2][DOUT];
+#pragma unroll
+            for (int o = 0; o < DOUT; ++o) b[0][o] = sG[lg * NS * GS + le + 16 * o];
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                if (s + 1 < NS) {
+                    const float* row = sG + (lg * NS + s + 1) * GS + le;
+#pragma unroll
+                    for (int o = 0; o < DOUT; ++o) b[(s + 1) & 1][o] = row[16 * o];
+                }
+#pragma unroll
+                for (int j = 0; j < RPW; ++j)
+#pragma unroll
+                    for (int o = 0; o < DOUT; ++o)
+                        accH[j][o] = mfma(a_cur[j][s], b[s & 1][o], accH[j][o]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            float fk[WD], pf[WD];
+#pragma unroll
+            for (int w = 0; w < WD; ++w) {
+                fk[w] = sFe[le * KW + k * WD + w];
+                pf[w] = 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < RPW; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int t = 0; t < T::NT; ++t) {
+                        const Term tm = T::terms[t];
+                        const float h = accH[j][tm.o][r];
+                        const float c = tm.neg ? -fk[tm.w] : fk[tm.w];
+                        dfs[j][r][tm.i] += c * h;
+                        pf[tm.w] += (tm.neg ? -fsr[j][r][tm.i] : fsr[j][r][tm.i]) * h;
+                    }
+            // sum over the 4 lane groups: the wave's rows of this edge
+#pragma unroll
+            for (int w = 0; w < WD; ++w) {
+                float v = pf[w];
+                v += __shfl_xor(v, 16, 64);
+                v += __shfl_xor(v, 32, 64);
+                if (lg == 0) sDF[((wave * K + k) * kNE + le) * WD + w] = v;
+            }
+        }
+        __syncthreads();   // dF partials complete; gd no longer needed
+        const int64_t nval = E - e0 < kNE ? E - e0 : kNE;
+        for (int q = tid; q < nval * KW; q += kThreads) {
+            const int e = q / KW, kw = q % KW, k = kw / WD, w = kw % WD;
+            float acc = 0.0f;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc += sDF[((v * K + k) * kNE + e) * WD + w];
+            dFe[(e0 + e) * KW + kw] = acc;
+        }
+        // dx = s^l dfs P^T, staged through LDS for coalesced stores
+        {
+            const float* pe = sP + le * DIN * DIN;
+#pragma unroll
+            for (int j = 0; j < RPW; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int ci = 16 * (wave + 4 * j) + 4 * lg + r;
+                    float ds[DIN];
+#pragma unroll
+                    for (int i = 0; i < DIN; ++i) ds[i] = dfs[j][r][i] * pin[i];
+#pragma unroll
+                    for (int d = 0; d < DIN; ++d) {
+                        float acc = 0.0f;
+#pragma unroll
+                        for (int i = 0; i < DIN; ++i) acc += ds[i] * pe[d * DIN + i];
+                        sG[le * XS + ci * DIN + d] = acc;
+                    }
+                }
+        }
+        __syncthreads();
+        float* xt = gx + e0 * CIN * DIN;
+        if (nval == kNE) {
+#pragma unroll
+            for (int m = 0; m < kNE * CIN * DIN / kThreads; ++m) {
+                const int q = tid + kThreads * m;
+                xt[q] = sG[(q / (CIN * DIN)) * XS + q % (CIN * DIN)];
+            }
+        } else {
+            for (int q = tid; q < nval * CIN * DIN; q += kThreads)
+                xt[q] = sG[(q / (CIN * DIN)) * XS + q % (CIN * DIN)];
         }
     }
 }
@@ -1035,10 +1052,8 @@ constexpr size_t bwd_x_lds() {
     using T = Canon<LIN, LOUT>;
     constexpr size_t GS = 16 * T::DOUT + 1, XS = CIN * T::DIN + 1;
     constexpr size_t GBIG = COUT * GS > kNE * XS ? COUT * GS : kNE * XS;
-    return 4 * (static_cast<size_t>(K) * CIN * COUT + GBIG + 4 * K * kNE * T::WD +
-                kNE * T::DIN * T::DIN + kNE * T::DOUT * T::DOUT + kNE * T::DIN + kNE * T::DOUT +
-                kNE * K * T::WD) +
-           kNE * (sizeof(TileEdge) + sizeof(int));
+    return 4 * (GBIG + 4 * K * kNE * T::WD + kNE * T::DIN * T::DIN + kNE * K * T::WD) +
+           kNE * sizeof(TileEdge);
 }
 
 template <int CIN, int COUT, int LIN, int LOUT, int K>
