@@ -22,8 +22,6 @@
 namespace feq {
 namespace {
 
-constexpr int kMaxN = 2 * (FEQ_MAX_BLOCKS - 1) + 1;  // 33
-
 struct WignerArgs {
     int32_t nirr;
     int32_t dim;
@@ -40,87 +38,147 @@ __device__ __forceinline__ float sanitize(double v) {
     return static_cast<float>(v);
 }
 
-__global__ void __launch_bounds__(256)
-k_wigner(WignerArgs A, const double* __restrict__ plan, const int32_t* __restrict__ perm,
-         int64_t E, const float* __restrict__ dirs, float* __restrict__ out) {
-    const int64_t g = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-    const int dim = A.dim;
-    if (g >= E * dim) return;
-    const int64_t e = g / dim;
-    const int j = static_cast<int>(g % dim);
-    const int c0 = perm[j];
-    int k = 0;
-    while (k + 1 < A.nirr && c0 >= A.off[k + 1]) ++k;
-    const int l = A.lvals[k], n = 2 * l + 1, base = A.off[k];
-    const int c = c0 - base;
-    float* col = out + e * dim * dim + j;  // element (row r) at col[r * dim]
+// Column c of D for an irrep of degree L (n = 2L + 1) and edge angles (phi,
+// ang = theta rho): D = Z(phi) V Z(ang) V^T Z(-phi), where Z(x) rotates the
+// (r, 2L - r) pair by (L - r) x -- the structure of the m-diagonal generator,
+// which the host checks when it builds V.  All indices are compile-time, so
+// the vectors live in registers.
+template <int L>
+__device__ __forceinline__ void wigner_column(const double* __restrict__ V, int c, double phi,
+                                              double ang, double (&y)[2 * L + 1]) {
+    constexpr int n = 2 * L + 1;
+    double cp[L + 1], sp[L + 1], ca[L + 1], sa[L + 1];
+    cp[0] = 1.0;
+    sp[0] = 0.0;
+    ca[0] = 1.0;
+    sa[0] = 0.0;
+    double c1p, s1p, c1a, s1a;
+    sincos(phi, &s1p, &c1p);
+    sincos(ang, &s1a, &c1a);
+#pragma unroll
+    for (int q = 1; q <= L; ++q) {
+        cp[q] = cp[q - 1] * c1p - sp[q - 1] * s1p;
+        sp[q] = sp[q - 1] * c1p + cp[q - 1] * s1p;
+        ca[q] = ca[q - 1] * c1a - sa[q - 1] * s1a;
+        sa[q] = sa[q - 1] * c1a + ca[q - 1] * s1a;
+    }
+    // v1 = Z(-phi) e_c: entries at c (cos) and its partner n-1-c (sin of the
+    // partner's coupling), then w = V^T v1
+    const int pc = n - 1 - c;
+    const int mc = L - c;                         // coupling of row c
+    const int amc = mc < 0 ? -mc : mc;
+    double cphi = 1.0, sphi = 0.0;
+#pragma unroll
+    for (int q = 0; q <= L; ++q)
+        if (q == amc) {
+            cphi = cp[q];
+            sphi = sp[q];
+        }
+    const double v_c = cphi;
+    const double v_p = pc != c ? (mc < 0 ? -sphi : sphi) : 0.0;
+    double w[n], u[n];
+#pragma unroll
+    for (int q = 0; q < n; ++q) w[q] = V[c * n + q] * v_c + V[pc * n + q] * v_p;
+    // u = Z(ang) w
+#pragma unroll
+    for (int r = 0; r < n; ++r) {
+        const int m = L - r, am = m < 0 ? -m : m;
+        u[r] = ca[am] * w[r] + (r != L ? (m < 0 ? -sa[am] : sa[am]) * w[n - 1 - r] : 0.0);
+    }
+    // x = V u, y = Z(phi) x
+    double xv[n];
+#pragma unroll
+    for (int r = 0; r < n; ++r) {
+        double acc = 0.0;
+#pragma unroll
+        for (int q = 0; q < n; ++q) acc += V[r * n + q] * u[q];
+        xv[r] = acc;
+    }
+#pragma unroll
+    for (int r = 0; r < n; ++r) {
+        const int m = L - r, am = m < 0 ? -m : m;
+        y[r] = cp[am] * xv[r] + (r != L ? (m < 0 ? -sp[am] : sp[am]) * xv[n - 1 - r] : 0.0);
+    }
+}
 
-    // ---- edge frame, float32 like rot_to_ez -----------------------------------
-    const float eps = 1e-8f;
-    const float vx = dirs[3 * e], vy = dirs[3 * e + 1], vz = dirs[3 * e + 2];
-    const float nv = sqrtf(vx * vx + vy * vy + vz * vz) + eps;
-    const float dx = vx / nv, dy = vy / nv, dz = vz / nv;
-    const float a0r = -dy, a1r = dx;
-    const float na = sqrtf(a0r * a0r + a1r * a1r) + eps;
-    const float a0 = a0r / na, a1 = a1r / na;
-    const float theta = acosf(fminf(fmaxf(dz, -1.0f), 1.0f));
-
-    double y[kMaxN];
-    const double* V = plan + A.plan_off[k];
-    const double* z = V + n * n;
-    const double* pr = z + n;
-    const double rho = sqrt(static_cast<double>(a0) * a0 + static_cast<double>(a1) * a1);
-    if (l == 0) {
+template <int L>
+__device__ __forceinline__ void column_into(const double* V, int c, double phi, double ang,
+                                            bool ident, float* dst, int stride) {
+    constexpr int n = 2 * L + 1;
+    double y[n];
+    if (L == 0) {
         y[0] = 1.0;
-    } else if (rho == 0.0) {
+    } else if (ident) {
+#pragma unroll
         for (int r = 0; r < n; ++r) y[r] = r == c ? 1.0 : 0.0;
     } else {
-        const double phi = atan2(static_cast<double>(a1), static_cast<double>(a0));
-        const double ang = static_cast<double>(theta) * rho;
-        // cos/sin of k*phi and k*ang, k = 0..l, by the angle-addition recurrence
-        double cp[FEQ_MAX_BLOCKS], sp[FEQ_MAX_BLOCKS], ca[FEQ_MAX_BLOCKS], sa[FEQ_MAX_BLOCKS];
-        cp[0] = 1.0; sp[0] = 0.0; ca[0] = 1.0; sa[0] = 0.0;
-        double c1p, s1p, c1a, s1a;
-        sincos(phi, &s1p, &c1p);
-        sincos(ang, &s1a, &c1a);
-        for (int q = 1; q <= l; ++q) {
-            cp[q] = cp[q - 1] * c1p - sp[q - 1] * s1p;
-            sp[q] = sp[q - 1] * c1p + cp[q - 1] * s1p;
-            ca[q] = ca[q - 1] * c1a - sa[q - 1] * s1a;
-            sa[q] = sa[q - 1] * c1a + ca[q - 1] * s1a;
-        }
-        // sin/cos of (zr * x) with zr a signed integer
-        auto zc = [&](int r, const double* cc) { int m = static_cast<int>(z[r]); return cc[m < 0 ? -m : m]; };
-        auto zs = [&](int r, const double* ss) { int m = static_cast<int>(z[r]); double v = ss[m < 0 ? -m : m]; return m < 0 ? -v : v; };
-        // v1 = Z(-phi) e_c: entries at c and its partner p
-        const int p = static_cast<int>(pr[c]);
-        const double v_c = zc(c, cp);
-        const double v_p = p != c ? -zs(p, sp) : 0.0;
-        // w = V^T v1
-        double w[kMaxN], u[kMaxN];
-        for (int q = 0; q < n; ++q) w[q] = V[c * n + q] * v_c + (p != c ? V[p * n + q] * v_p : 0.0);
-        // u = Z(ang) w
-        for (int r = 0; r < n; ++r) {
-            const int pr_r = static_cast<int>(pr[r]);
-            u[r] = zc(r, ca) * w[r] + (pr_r != r ? zs(r, sa) * w[pr_r] : 0.0);
-        }
-        // x = V u  (reuse w)
-        for (int r = 0; r < n; ++r) {
-            double acc = 0.0;
-            for (int q = 0; q < n; ++q) acc += V[r * n + q] * u[q];
-            w[r] = acc;
-        }
-        // y = Z(phi) x
-        for (int r = 0; r < n; ++r) {
-            const int pr_r = static_cast<int>(pr[r]);
-            y[r] = zc(r, cp) * w[r] + (pr_r != r ? zs(r, sp) * w[pr_r] : 0.0);
+        wigner_column<L>(V, c, phi, ang, y);
+    }
+#pragma unroll
+    for (int r = 0; r < n; ++r) dst[r * stride] = sanitize(y[r]);
+}
+
+struct EdgeFrame {
+    double phi, ang;
+    int ident;   // axis of zero length: D = I
+};
+
+// Workgroup: a tile of EPB edges; thread t computes standard column c0 = t % dim
+// of edge t / dim into an LDS tile of the edges' M = D[:, perm] matrices, which
+// is then written with coalesced stores.
+__global__ void __launch_bounds__(256)
+k_wigner(WignerArgs A, int epb, const double* __restrict__ plan, const int32_t* __restrict__ perm,
+         int64_t E, const float* __restrict__ dirs, float* __restrict__ out) {
+    extern __shared__ float sM[];                      // epb x dim x dim
+    __shared__ EdgeFrame sFr[256];
+    __shared__ int sInv[FEQ_MAX_SLOTS];
+    const int dim = A.dim, dd = dim * dim;
+    const int64_t e0 = static_cast<int64_t>(blockIdx.x) * epb;
+    const int ne = static_cast<int>(E - e0 < epb ? E - e0 : epb);
+    for (int q = threadIdx.x; q < epb * dd; q += blockDim.x) sM[q] = 0.0f;
+    for (int j = threadIdx.x; j < dim; j += blockDim.x) sInv[perm[j]] = j;
+    if (threadIdx.x < ne) {
+        // edge frame in float32 like rot_to_ez: d = v/(|v|+eps), axis = (-d_y, d_x, 0)/(|.|+eps),
+        // theta = acos(clamp(d_z, -1, 1)); a = rho (cos phi, sin phi)
+        const int64_t e = e0 + threadIdx.x;
+        const float eps = 1e-8f;
+        const float vx = dirs[3 * e], vy = dirs[3 * e + 1], vz = dirs[3 * e + 2];
+        const float nv = sqrtf(vx * vx + vy * vy + vz * vz) + eps;
+        const float dx = vx / nv, dy = vy / nv, dz = vz / nv;
+        const float a0r = -dy, a1r = dx;
+        const float na = sqrtf(a0r * a0r + a1r * a1r) + eps;
+        const float a0 = a0r / na, a1 = a1r / na;
+        const float theta = acosf(fminf(fmaxf(dz, -1.0f), 1.0f));
+        const double rho = sqrt(static_cast<double>(a0) * a0 + static_cast<double>(a1) * a1);
+        EdgeFrame f;
+        f.ident = rho == 0.0;
+        f.phi = f.ident ? 0.0 : atan2(static_cast<double>(a1), static_cast<double>(a0));
+        f.ang = static_cast<double>(theta) * rho;
+        sFr[threadIdx.x] = f;
+    }
+    __syncthreads();
+    const int el = threadIdx.x / dim;
+    if (el < ne) {
+        const int c0 = threadIdx.x % dim;
+        int k = 0;
+        while (k + 1 < A.nirr && c0 >= A.off[k + 1]) ++k;
+        const int l = A.lvals[k], base = A.off[k], c = c0 - base;
+        const double* V = plan + A.plan_off[k];
+        const EdgeFrame f = sFr[el];
+        float* dst = sM + el * dd + base * dim + sInv[c0];   // rows base.., column j
+        switch (l) {
+#define FEQ_WCASE(LL) \
+    case LL: column_into<LL>(V, c, f.phi, f.ang, f.ident, dst, dim); break;
+            FEQ_WCASE(0) FEQ_WCASE(1) FEQ_WCASE(2) FEQ_WCASE(3) FEQ_WCASE(4) FEQ_WCASE(5)
+            FEQ_WCASE(6) FEQ_WCASE(7) FEQ_WCASE(8) FEQ_WCASE(9) FEQ_WCASE(10) FEQ_WCASE(11)
+            FEQ_WCASE(12) FEQ_WCASE(13) FEQ_WCASE(14) FEQ_WCASE(15) FEQ_WCASE(16)
+#undef FEQ_WCASE
+            default: break;
         }
     }
-    for (int r = 0; r < dim; ++r) {
-        float v = 0.0f;
-        if (r >= base && r < base + n) v = sanitize(y[r - base]);
-        col[static_cast<int64_t>(r) * dim] = v;
-    }
+    __syncthreads();
+    float* o = out + e0 * dd;
+    for (int q = threadIdx.x; q < ne * dd; q += blockDim.x) o[q] = sM[q];
 }
 
 }  // namespace
@@ -160,8 +218,11 @@ extern "C" int feq_wigner_basis(const int32_t* lvals, int32_t n, const double* p
     A.dim = dim;
     if (E == 0) return FEQ_OK;
     if (!plan || !perm || !dirs || !out) return fail(FEQ_ERR_INVALID, "NULL pointer");
-    const int64_t total = E * dim;
-    FEQ_LAUNCH("k_wigner", k_wigner, dim3(ceil_div(total, 256)), dim3(256), 0, stream_of(stream), A,
-                       plan, perm, E, dirs, out);
+    // one thread per (edge, column); the edges' matrices are staged in LDS
+    const int epb = 256 / dim;
+    const size_t lds = sizeof(float) * static_cast<size_t>(epb) * dim * dim;
+    if (lds > 64 * 1024) return fail(FEQ_ERR_UNSUPPORTED, "representation dimension %d too large", dim);
+    FEQ_LAUNCH("k_wigner", k_wigner, dim3(ceil_div(E, epb)), dim3(256), lds, stream_of(stream), A,
+               epb, plan, perm, E, dirs, out);
     return FEQ_OK;
 }

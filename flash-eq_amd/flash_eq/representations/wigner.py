@@ -153,6 +153,10 @@ def _wigner_plan(repr: Repr) -> torch.Tensor:
                 if abs(m - round(m)) > 1e-5:
                     raise RuntimeError("non-integer coupling in the m-diagonal generator")
                 z[r], partner[r] = round(m), nz[0]
+        # the kernel relies on this structure: row r pairs with row 2l - r at m = l - r
+        l = (n - 1) // 2
+        if any(int(z[r]) != l - r or int(partner[r]) != n - 1 - r for r in range(n)):
+            raise RuntimeError("m-diagonal generator does not pair row r with row 2l - r")
         _check_factorisation(g, v, z, partner)
         chunks += [v.reshape(-1), z, partner]
     return torch.cat(chunks) if chunks else torch.zeros(0, dtype=torch.float64)
