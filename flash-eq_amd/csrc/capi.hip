@@ -38,10 +38,17 @@ int check_layout(const feq_layout* L) {
     return FEQ_OK;
 }
 
-bool force_generic() {
-    const char* v = getenv("FEQ_FORCE_GENERIC");
-    return v && v[0] == '1';
+int ew_path() {
+    const char* g = getenv("FEQ_FORCE_GENERIC");
+    if (g && g[0] == '1') return kPathGeneric;
+    const char* v = getenv("FEQ_EW_PATH");
+    if (!v) return kPathSplit;
+    if (strcmp(v, "generic") == 0) return kPathGeneric;
+    if (strcmp(v, "fp32mfma") == 0) return kPathFp32Mfma;
+    return kPathSplit;
 }
+
+bool force_generic() { return ew_path() == kPathGeneric; }
 
 int check_binning(const feq_binning* b) {
     if (!b) return fail(FEQ_ERR_INVALID, "binning is NULL");

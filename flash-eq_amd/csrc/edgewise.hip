@@ -396,13 +396,21 @@ extern "C" size_t feq_edgewise_workspace(const feq_layout* L, const feq_binning*
     if (!L || rank < 1) return 0;
     const size_t generic = sizeof(float) * static_cast<size_t>(groups_for(E)) * rank * L->cout * L->cin + 256;
     const size_t fast = b ? ew_mfma_bwd_workspace(*L, *b, rank, E) : 0;
-    return generic > fast ? generic : fast;
+    const size_t split = ew_split_workspace(*L, rank);
+    const size_t m = generic > fast ? generic : fast;
+    return m > split ? m : split;
+}
+
+extern "C" size_t feq_edgewise_fwd_workspace(const feq_layout* L, const feq_binning*, int32_t rank,
+                                             int64_t) {
+    if (!L || rank < 1) return 0;
+    return ew_split_workspace(*L, rank) + 256;
 }
 
 extern "C" int feq_edgewise_fwd(const feq_layout* L, const feq_binning* b, int32_t rank,
                                 int64_t E, const float* x, const float* P, const float* Q,
                                 const float* dist, const float* C, const float* F, float* y,
-                                void*, size_t, feq_stream_t stream) {
+                                void* ws, size_t ws_bytes, feq_stream_t stream) {
     if (int rc = check_layout(L)) return rc;
     if (int rc = check_binning(b)) return rc;
     if (rank < 1) return fail(FEQ_ERR_INVALID, "rank must be positive");
@@ -410,7 +418,13 @@ extern "C" int feq_edgewise_fwd(const feq_layout* L, const feq_binning* b, int32
     if (E == 0) return FEQ_OK;
     if (E > 0x7fffffffLL) return fail(FEQ_ERR_UNSUPPORTED, "more than 2^31-1 edges");
     if (!x || !P || !Q || !dist || !C || !F || !y) return fail(FEQ_ERR_INVALID, "NULL pointer");
-    if (!force_generic()) {
+    const int path = ew_path();
+    if (path == kPathSplit) {
+        const int rc = ew_split_fwd(*L, *b, rank, E, x, P, Q, dist, C, F, y, ws, ws_bytes,
+                                    stream_of(stream));
+        if (rc != -1) return rc;
+    }
+    if (path != kPathGeneric) {
         const int rc = ew_mfma_fwd(*L, *b, rank, E, x, P, Q, dist, C, F, y, stream_of(stream));
         if (rc != -1) return rc;
     }

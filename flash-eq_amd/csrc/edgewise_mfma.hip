@@ -23,6 +23,7 @@
 // rows use odd strides, so the column-wise stores of the builders and the MFMA
 // fragment loads are bank-conflict free.
 #include "feq_internal.h"
+#include "ew_canon.h"
 
 #include <algorithm>
 #include <array>
@@ -39,81 +40,6 @@ constexpr int kThreads = 256;
 __device__ __forceinline__ v4f mfma(float a, float b, v4f c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
-
-// ---- compile-time m-first layout of a canonical (lvals = 0..L) pair --------
-struct Term {
-    int o, i, w, neg;
-};
-
-template <int LIN, int LOUT>
-struct Canon {
-    static constexpr int DIN = (LIN + 1) * (LIN + 1);
-    static constexpr int DOUT = (LOUT + 1) * (LOUT + 1);
-    static constexpr int MMIN = LIN < LOUT ? LIN : LOUT;
-    static constexpr int nin(int m) { return LIN - m + 1; }
-    static constexpr int nout(int m) { return LOUT - m + 1; }
-    static constexpr int in_off(int m) {
-        int o = 0;
-        for (int q = 0; q < m; ++q) o += (q ? 2 : 1) * nin(q);
-        return o;
-    }
-    static constexpr int out_off(int m) {
-        int o = 0;
-        for (int q = 0; q < m; ++q) o += (q ? 2 : 1) * nout(q);
-        return o;
-    }
-    static constexpr int w_off(int m) {
-        int o = 0;
-        for (int q = 0; q < m; ++q) o += (q ? 2 : 1) * nin(q) * nout(q);
-        return o;
-    }
-    static constexpr int WD = w_off(MMIN + 1);
-    static constexpr int count() {
-        int n = 0;
-        for (int m = 0; m <= MMIN; ++m) n += (m ? 4 : 1) * nin(m) * nout(m);
-        return n;
-    }
-    static constexpr int NT = count();
-    static constexpr std::array<Term, NT> make_terms() {
-        std::array<Term, NT> t{};
-        int n = 0;
-        for (int m = 0; m <= MMIN; ++m) {
-            const int ni = nin(m), no = nout(m), io = in_off(m), oo = out_off(m), wo = w_off(m);
-            for (int o = 0; o < no; ++o)
-                for (int i = 0; i < ni; ++i) {
-                    if (m == 0) {
-                        t[n++] = Term{oo + o, io + i, wo + o * ni + i, 0};
-                    } else {
-                        const int wa = wo + 2 * (o * ni + i);
-                        const int ro = oo + 2 * o, im_o = ro + 1, ri = io + 2 * i, im_i = ri + 1;
-                        t[n++] = Term{ro, ri, wa, 0};          // re += a f_re
-                        t[n++] = Term{ro, im_i, wa + 1, 0};    // re += b f_im
-                        t[n++] = Term{im_o, im_i, wa, 0};      // im += a f_im
-                        t[n++] = Term{im_o, ri, wa + 1, 1};    // im -= b f_re
-                    }
-                }
-        }
-        return t;
-    }
-    static constexpr std::array<Term, NT> terms = make_terms();
-};
-
-// l of every m-first component of a canonical representation with lmax L
-template <int L>
-struct SlotL {
-    static constexpr std::array<int, (L + 1) * (L + 1)> make() {
-        std::array<int, (L + 1) * (L + 1)> v{};
-        int s = 0;
-        for (int l = 0; l <= L; ++l) v[s++] = l;
-        for (int m = 1; m <= L; ++m)
-            for (int l = m; l <= L; ++l) {
-                v[s++] = l;
-                v[s++] = l;
-            }
-        return v;
-    }
-    static constexpr std::array<int, (L + 1) * (L + 1)> l = make();
-};
 
 struct TileEdge {
     int lo;

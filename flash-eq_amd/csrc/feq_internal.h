@@ -79,8 +79,19 @@ int ew_mfma_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, 
                 const float* F, float* gx, float* gC, float* gF, float* gdist, void* ws,
                 size_t ws_bytes, hipStream_t s);
 
-// FEQ_FORCE_GENERIC=1 in the environment selects the shape-generic kernels
-// (used by the tests to check both implementations).
+// Split-fp16 fast paths (edgewise_split.hip); -1 when the shape has none.
+size_t ew_split_workspace(const feq_layout& L, int rank);
+int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
+                 const float* P, const float* Q, const float* dist, const float* C, const float* F,
+                 float* y, void* ws, size_t ws_bytes, hipStream_t s);
+
+// Kernel family of the fused edgewise layer.  The default tries the split-fp16
+// kernels, then the fp32-MFMA kernels, then the shape-generic ones;
+// FEQ_EW_PATH=fp32mfma starts at the fp32-MFMA kernels and FEQ_EW_PATH=generic
+// (or FEQ_FORCE_GENERIC=1) uses only the generic ones, so tests can check the
+// implementations against each other.
+enum { kPathSplit = 0, kPathFp32Mfma = 1, kPathGeneric = 2 };
+int ew_path();
 bool force_generic();
 
 // Checks shared by every layout-consuming entry point.

@@ -54,10 +54,13 @@ class EdgewiseLinearFn(torch.autograd.Function):
         y = torch.empty(E, layout.cout, layout.dout, dtype=torch.float32, device=dev)
         if E:
             lib = N.lib()
+            ws = N.workspace(lib.feq_edgewise_fwd_workspace(N.ctypes.byref(layout),
+                                                            N.ctypes.byref(binning), rank, E), dev)
             with torch.cuda.device(dev):
                 rc = lib.feq_edgewise_fwd(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
                                           N.ptr(xs), N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs),
-                                          N.ptr(Fs), N.ptr(y), None, 0, N.stream_ptr(dev))
+                                          N.ptr(Fs), N.ptr(y), N.ptr(ws), ws.numel(),
+                                          N.stream_ptr(dev))
             N.check(rc, "feq_edgewise_fwd")
         ctx.save_for_backward(xs, Ps, Qs, rs, Cs, Fs)
         ctx.meta = (layout, binning, rank, x.dtype, P.dtype, Q.dtype, dist.dtype, C.dtype, F.dtype)

@@ -113,7 +113,12 @@ int feq_blockdiag_bwd(const feq_layout* L, const feq_binning* b, int64_t num_edg
 /* ---- fused EquivariantEdgewiseLinear (separable radial weights) ---------------
  * x (E, Cin, Din) standard basis; P (E, Din, Din); Q (E, Dout, Dout);
  * C (K, Cout, Cin) channel patterns; F (num_bins+1, K, Wdim) radial functions;
- * y (E, Cout, Dout) standard basis.  y = (Lambda(r) (x P)) Q^T. */
+ * y (E, Cout, Dout) standard basis.  y = (Lambda(r) (x P)) Q^T.
+ * Workspaces: feq_edgewise_fwd_workspace bytes for the forward (it keeps the
+ * fp16-split channel patterns there; independent of num_edges) and
+ * feq_edgewise_workspace bytes for the backward. */
+size_t feq_edgewise_fwd_workspace(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                  int64_t num_edges);
 size_t feq_edgewise_workspace(const feq_layout* L, const feq_binning* b, int32_t rank,
                               int64_t num_edges);
 int feq_edgewise_fwd(const feq_layout* L, const feq_binning* b, int32_t rank, int64_t num_edges,

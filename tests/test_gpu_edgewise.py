@@ -65,13 +65,21 @@ def test_edgewise_parity(dev, lin, lout):
     _run_parity(dev, lin, lout, cin=6, cout=5, E=400)
 
 
-@pytest.fixture(params=["fast", "generic"])
-def impl(request, monkeypatch):
-    """Run with the shape-specialised MFMA kernels (default) or force the generic ones."""
-    if request.param == "generic":
-        monkeypatch.setenv("FEQ_FORCE_GENERIC", "1")
+PATHS = ("split", "fp32mfma", "generic")
+
+
+def _select(monkeypatch, path):
+    """Kernel family of the fused layer: split-fp16 MFMA (default), fp32 MFMA or generic."""
+    monkeypatch.delenv("FEQ_FORCE_GENERIC", raising=False)
+    if path == "split":
+        monkeypatch.delenv("FEQ_EW_PATH", raising=False)
     else:
-        monkeypatch.delenv("FEQ_FORCE_GENERIC", raising=False)
+        monkeypatch.setenv("FEQ_EW_PATH", path)
+
+
+@pytest.fixture(params=PATHS)
+def impl(request, monkeypatch):
+    _select(monkeypatch, request.param)
     return request.param
 
 
@@ -91,8 +99,8 @@ def test_edgewise_parity_c2_ragged_tiles(dev, impl):
     _run_parity(dev, [2, 0, 1], [1, 2, 0], cin=64, cout=64, E=37, seed=9)
 
 
-def test_fast_and_generic_agree_at_scale(dev, monkeypatch):
-    """c2 shape at E = 40,000: the MFMA path against the generic kernels (float32 both)."""
+def test_kernel_families_agree_at_scale(dev, monkeypatch):
+    """c2 shape at E = 40,000: the split-fp16 and fp32 MFMA paths against the generic kernels."""
     torch.manual_seed(3)
     rp = fe.Repr([0, 1, 2], 64)
     layer = fe.EquivariantEdgewiseLinear(rp, rp).to(dev)
@@ -103,22 +111,43 @@ def test_fast_and_generic_agree_at_scale(dev, monkeypatch):
     r = (torch.rand(E, generator=g) * 11).to(dev)
     gy = torch.randn(E, 64, 9, generator=g).to(dev)
     outs = {}
-    for mode in ("fast", "generic"):
-        if mode == "generic":
-            monkeypatch.setenv("FEQ_FORCE_GENERIC", "1")
-        else:
-            monkeypatch.delenv("FEQ_FORCE_GENERIC", raising=False)
+    for mode in PATHS:
+        _select(monkeypatch, mode)
         layer.zero_grad()
         xg, rg = x.clone().requires_grad_(True), r.clone().requires_grad_(True)
         y = layer(P, P, xg, rg)
         y.backward(gy)
         outs[mode] = (y.detach(), xg.grad, rg.grad,
                       [p.grad.clone() for p in layer.radial_weights.parameters()])
-    a, b = outs["fast"], outs["generic"]
-    assert rel_err(a[0], b[0]) < 2e-6 and rel_err(a[1], b[1]) < 2e-6
-    assert rel_err(a[2], b[2]) < 2e-5
-    for pa, pb in zip(a[3], b[3]):
-        assert rel_err(pa, pb) < 2e-5
+    b = outs["generic"]
+    for mode in ("split", "fp32mfma"):
+        a = outs[mode]
+        assert rel_err(a[0], b[0]) < 2e-6 and rel_err(a[1], b[1]) < 2e-6, mode
+        assert rel_err(a[2], b[2]) < 2e-5, mode
+        for pa, pb in zip(a[3], b[3]):
+            assert rel_err(pa, pb) < 2e-5, mode
+
+
+@pytest.mark.parametrize("lin,lout,cin,cout,E", [([0, 1, 2], [0, 1, 2], 64, 64, 1000),
+                                                 ([0, 1], [0, 1, 2], 32, 64, 1000)])
+def test_split_path_is_dispatched(dev, monkeypatch, lin, lout, cin, cout, E):
+    """The default forward of the compiled shapes runs the split-fp16 kernel."""
+    from flash_eq import _native as NAT
+    _select(monkeypatch, "split")
+    layer = fe.EquivariantEdgewiseLinear(fe.Repr(lin, cin), fe.Repr(lout, cout)).to(dev)
+    g = torch.Generator().manual_seed(11)
+    d = torch.randn(E, 3, generator=g).to(dev)
+    P, Q = fe.WignerDBasis([fe.Repr(lin, 1), fe.Repr(lout, 1)]).to(dev)(d)
+    x = torch.randn(E, cin, P.shape[-1], generator=g).to(dev)
+    r = (torch.rand(E, generator=g) * 9).to(dev)
+    torch.cuda.synchronize()
+    NAT.profile_summary()
+    NAT.profile_enable(True)
+    layer(P, Q, x, r)
+    torch.cuda.synchronize()
+    NAT.profile_enable(False)
+    names = NAT.profile_summary()
+    assert "k_ews_fwd" in names and "k_ews_prep" in names, names
 
 
 def test_edgewise_parity_log_bins(dev):
