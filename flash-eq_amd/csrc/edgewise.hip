@@ -396,7 +396,7 @@ extern "C" size_t feq_edgewise_workspace(const feq_layout* L, const feq_binning*
     if (!L || rank < 1) return 0;
     const size_t generic = sizeof(float) * static_cast<size_t>(groups_for(E)) * rank * L->cout * L->cin + 256;
     const size_t fast = b ? ew_mfma_bwd_workspace(*L, *b, rank, E) : 0;
-    const size_t split = ew_split_workspace(*L, rank);
+    const size_t split = b ? ew_split_bwd_workspace(*L, *b, rank, E) : 0;
     const size_t m = generic > fast ? generic : fast;
     return m > split ? m : split;
 }
@@ -455,7 +455,13 @@ extern "C" int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32
     if (!gy || !x || !P || !Q || !dist || !C || !F) return fail(FEQ_ERR_INVALID, "NULL pointer");
     if (!ws || ws_bytes < feq_edgewise_workspace(L, b, rank, E))
         return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
-    if (!force_generic() && !gP && !gQ) {
+    const int path = ew_path();
+    if (path == kPathSplit && !gP && !gQ) {
+        const int rc = ew_split_bwd(*L, *b, rank, E, gy, x, P, Q, dist, C, F, gx, gC, gF, gdist, ws,
+                                    ws_bytes, s);
+        if (rc != -1) return rc;
+    }
+    if (path != kPathGeneric && !gP && !gQ) {
         const int rc = ew_mfma_bwd(*L, *b, rank, E, gy, x, P, Q, dist, C, F, gx, gC, gF, gdist, ws,
                                    ws_bytes, s);
         if (rc != -1) return rc;

@@ -858,135 +858,6 @@ k_ewc_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
         }
 }
 
-// l_in + l_out of every weight slot w < wdim of a layout, into fl (LDS).
-__device__ void weight_lsum(const feq_layout& L, int* fl) {
-    if (threadIdx.x == 0) {
-        for (int k = 0; k < L.nblocks; ++k) {
-            const int m = L.blk[k][0], ni = L.blk[k][1], no = L.blk[k][2];
-            const int ioff = L.blk[k][3], ooff = L.blk[k][4], woff = L.blk[k][5];
-            for (int o = 0; o < no; ++o)
-                for (int i = 0; i < ni; ++i) {
-                    if (m == 0) {
-                        fl[woff + o * ni + i] = L.lslot_in[ioff + i] + L.lslot_out[ooff + o];
-                    } else {
-                        const int lsum = L.lslot_in[ioff + 2 * i] + L.lslot_out[ooff + 2 * o];
-                        fl[woff + 2 * (o * ni + i)] = lsum;
-                        fl[woff + 2 * (o * ni + i) + 1] = lsum;
-                    }
-                }
-        }
-    }
-    __syncthreads();
-}
-
-// Binned radial-function gradient of one edge chunk: dF[lo] += (1 - t) dF_e and
-// dF[lo + 1] += t dF_e.  Thread t serves the columns c = t % kw (+ kThreads
-// multiples when kw > kThreads) of edge stream t / kw; every stream keeps its
-// own LDS histogram, so each cell has one writer and a fixed summation order.
-// One partial histogram per workgroup.
-__global__ void __launch_bounds__(kThreads)
-k_ewm_hist(feq_binning B, int kw, int streams, int64_t E, int64_t chunk,
-           const float* __restrict__ dist, const float* __restrict__ dFe,
-           float* __restrict__ hist_part) {
-    extern __shared__ float sh[];
-    const int hsz = (B.num_bins + 1) * kw;
-    float* sT = sh + static_cast<int64_t>(streams) * hsz;
-    int* sLo = reinterpret_cast<int*>(sT + chunk);
-    for (int q = threadIdx.x; q < streams * hsz; q += kThreads) sh[q] = 0.0f;
-    const int64_t e_begin = blockIdx.x * chunk;
-    const int n = static_cast<int>(E - e_begin < chunk ? E - e_begin : chunk);
-    for (int q = threadIdx.x; q < n; q += kThreads) {
-        const EdgeBin eb = edge_bin(dist[e_begin + q], B);
-        sLo[q] = eb.lo;
-        sT[q] = eb.t;
-    }
-    __syncthreads();
-    const int per = kw <= kThreads ? kw : kThreads;   // threads per stream
-    const int st = threadIdx.x / per;
-    if (st < streams) {
-        float* h = sh + static_cast<int64_t>(st) * hsz;
-        for (int c = threadIdx.x % per; c < kw; c += per)
-            for (int q = st; q < n; q += streams) {
-                const float v = dFe[(e_begin + q) * kw + c];
-                const int lo = sLo[q];
-                const float t = sT[q];
-                h[lo * kw + c] += (1.0f - t) * v;
-                h[(lo + 1) * kw + c] += t * v;
-            }
-    }
-    __syncthreads();
-    float* out = hist_part + static_cast<int64_t>(blockIdx.x) * hsz;
-    for (int q = threadIdx.x; q < hsz; q += kThreads) {
-        float acc = sh[q];
-        for (int v = 1; v < streams; ++v) acc += sh[static_cast<int64_t>(v) * hsz + q];
-        out[q] = acc;
-    }
-}
-
-// Distance gradient from dF_e, one thread per edge (sums in slot order):
-// dr = dt/dr sum (F[hi] - F[lo]) dF_e + [l > 0 pairs] sigma/(r(r+sigma)) sum (l_i+l_o) F_e dF_e.
-__global__ void __launch_bounds__(kThreads)
-k_ewm_dr(feq_layout L, feq_binning B, int K, int64_t E, const float* __restrict__ dist,
-         const float* __restrict__ F, const float* __restrict__ dFe, float* __restrict__ gdist) {
-    extern __shared__ int fl[];   // l_in + l_out per weight slot (wdim entries)
-    weight_lsum(L, fl);
-    const int64_t e = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x;
-    if (e >= E) return;
-    const int kw = K * L.wdim;
-    const float r = dist[e];
-    const EdgeBin eb = edge_bin(r, B);
-    const float* flo = F + static_cast<int64_t>(eb.lo) * kw;
-    const float* g = dFe + e * kw;
-    float st = 0.0f, ss = 0.0f;
-    for (int q = 0; q < kw; ++q) {
-        const float gv = g[q], lo = flo[q], hi = flo[kw + q];
-        st += (hi - lo) * gv;
-        ss += static_cast<float>(fl[q % L.wdim]) * lerp_bins(lo, hi, eb.t) * gv;
-    }
-    const float sigma = B.sh_scale;
-    float v = st * eb.dtdr;
-    if (L.has_lpos) v += ss * (sigma / (r * (r + sigma)));
-    gdist[e] = v;
-}
-
-// out[s * n + q] = sum of part[g * n + q] over the groups g of slice s
-// (blockIdx.y), in increasing g.
-__global__ void k_sum_partials(const float* __restrict__ part, int groups, int per_slice,
-                               int64_t n, float* __restrict__ out) {
-    const int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-    if (q >= n) return;
-    const int g0 = blockIdx.y * per_slice;
-    const int g1 = g0 + per_slice < groups ? g0 + per_slice : groups;
-    float acc = 0.0f;
-    for (int g = g0; g < g1; ++g) acc += part[static_cast<int64_t>(g) * n + q];
-    out[blockIdx.y * n + q] = acc;
-}
-
-constexpr int kSliceGroups = 32;   // partials summed per thread in one pass
-
-size_t reduce_tmp_floats(int groups, int64_t n) {
-    return groups > kSliceGroups ? static_cast<size_t>((groups + kSliceGroups - 1) / kSliceGroups) * n
-                                 : 0;
-}
-
-// Deterministic sum of `groups` partial arrays of n floats: slices of at most
-// kSliceGroups partials into tmp, then the slices into out.
-int reduce_partials(const float* part, int groups, int64_t n, float* out, float* tmp,
-                    hipStream_t s) {
-    const unsigned nb = static_cast<unsigned>(ceil_div(n, 256));
-    if (groups <= kSliceGroups) {
-        FEQ_LAUNCH("k_sum_partials", k_sum_partials, dim3(nb, 1), dim3(256), 0, s, part, groups,
-                   groups, n, out);
-        return FEQ_OK;
-    }
-    const int slices = (groups + kSliceGroups - 1) / kSliceGroups;
-    FEQ_LAUNCH("k_sum_partials", k_sum_partials, dim3(nb, slices), dim3(256), 0, s, part, groups,
-               kSliceGroups, n, tmp);
-    FEQ_LAUNCH("k_sum_partials", k_sum_partials, dim3(nb, 1), dim3(256), 0, s, tmp, slices, slices,
-               n, out);
-    return FEQ_OK;
-}
-
 int device_cus() {
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) == hipSuccess) {
@@ -1036,22 +907,6 @@ constexpr size_t bwd_c_lds() {
     return 4 * (CIN * RS + COUT * RS + kNE * K * T::WD) + kNE * sizeof(TileEdge);
 }
 
-constexpr int64_t kBinChunk = 256;   // edges per histogram workgroup
-constexpr size_t kHistLds = 64 * 1024;
-
-// Histogram streams per workgroup (0: the histogram does not fit LDS).
-int hist_streams(const feq_binning& B, int kw) {
-    const size_t hbytes = 4 * static_cast<size_t>(B.num_bins + 1) * kw;
-    const size_t avail = kHistLds - 8 * kBinChunk;
-    int st = kw <= kThreads ? kThreads / kw : 1;
-    while (st > 0 && st * hbytes > avail) --st;
-    return st;
-}
-
-size_t hist_lds(const feq_binning& B, int kw, int streams) {
-    return 4 * static_cast<size_t>(streams) * (B.num_bins + 1) * kw + 8 * kBinChunk;
-}
-
 template <int CIN, int COUT, int LIN, int LOUT, int K>
 int launch_fwd(const feq_binning& B, int64_t E, const float* x, const float* P, const float* Q,
                const float* dist, const float* C, const float* F, float* y, hipStream_t s) {
@@ -1069,15 +924,13 @@ template <int CIN, int COUT, int LIN, int LOUT, int K>
 size_t bwd_ws(const feq_binning& B, int64_t E) {
     using T = Canon<LIN, LOUT>;
     const int G = grid_for(ceil_div(E, kNE), 2);
-    const int64_t kw = static_cast<int64_t>(K) * T::WD;
-    const int nchunks = static_cast<int>(ceil_div(E, kBinChunk));
-    const int64_t hsz = (B.num_bins + 1) * kw, ncc = static_cast<int64_t>(K) * COUT * CIN;
-    const size_t tmp = reduce_tmp_floats(G, ncc) > reduce_tmp_floats(nchunks, hsz)
-                           ? reduce_tmp_floats(G, ncc) : reduce_tmp_floats(nchunks, hsz);
+    const int64_t kw = static_cast<int64_t>(K) * T::WD, ncc = static_cast<int64_t>(K) * COUT * CIN;
     return align_up(4 * E * kw, 256) + align_up(4 * static_cast<size_t>(G) * ncc, 256) +
-           align_up(4 * static_cast<size_t>(nchunks) * hsz, 256) + align_up(4 * tmp, 256) + 1024;
+           4 * ew_tail_floats(B, static_cast<int>(kw), E, G, ncc) + 1024;
 }
 
+// Backward launches: input gradient and dF_e, channel-pattern partials, then
+// the shared tail (binned radial-function gradient, distance gradient, sums).
 template <int CIN, int COUT, int LIN, int LOUT, int K>
 int launch_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const float* gy,
                const float* x, const float* P, const float* Q, const float* dist, const float* C,
@@ -1087,22 +940,17 @@ int launch_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const float
     constexpr size_t xlds = bwd_x_lds<CIN, COUT, LIN, LOUT, K>();
     constexpr size_t clds = bwd_c_lds<CIN, COUT, LIN, LOUT, K>();
     const int kw = K * T::WD;
-    const int streams = hist_streams(B, kw);
-    if (streams < 1) return -1;
-    const size_t hlds = hist_lds(B, kw, streams);
+    if (!ew_tail_supported(B, kw)) return -1;
     auto kx = k_ewc_bwd_x<CIN, COUT, LIN, LOUT, K>;
     auto kc = k_ewc_bwd_c<CIN, COUT, LIN, LOUT, K>;
     const int64_t ntiles = ceil_div(E, kNE);
     const int Gx = grid_for(ntiles, xlds <= 80 * 1024 ? 2 : 1);
     const int G = grid_for(ntiles, clds <= 80 * 1024 ? 2 : 1);
-    const int nchunks = static_cast<int>(ceil_div(E, kBinChunk));
-    const int64_t hsz = (B.num_bins + 1) * static_cast<int64_t>(kw);
     const int64_t ncc = static_cast<int64_t>(K) * COUT * CIN;
     Carver cv(ws);
     float* dFe = cv.take<float>(E * kw);
     float* dCp = cv.take<float>(static_cast<size_t>(G) * ncc);
-    float* hp = cv.take<float>(static_cast<size_t>(nchunks) * hsz);
-    float* tmp = cv.take<float>(std::max(reduce_tmp_floats(G, ncc), reduce_tmp_floats(nchunks, hsz)));
+    float* tail = cv.take<float>(ew_tail_floats(B, kw, E, G, ncc));
     if (cv.used > ws_bytes) return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
     if (int rc = set_lds(reinterpret_cast<const void*>(kx), xlds)) return rc;
     FEQ_LAUNCH("k_ewc_bwd_x", kx, dim3(Gx), dim3(kThreads), xlds, s, B, E, ntiles, gy, x, P, Q,
@@ -1110,14 +958,7 @@ int launch_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const float
     if (int rc = set_lds(reinterpret_cast<const void*>(kc), clds)) return rc;
     FEQ_LAUNCH("k_ewc_bwd_c", kc, dim3(G), dim3(kThreads), clds, s, B, E, ntiles, gy, x, P, Q,
                dist, F, dCp);
-    if (int rc = set_lds(reinterpret_cast<const void*>(&k_ewm_hist), hlds)) return rc;
-    FEQ_LAUNCH("k_ewm_hist", k_ewm_hist, dim3(nchunks), dim3(kThreads), hlds, s, B, kw, streams,
-               E, kBinChunk, dist, dFe, hp);
-    if (gdist)
-        FEQ_LAUNCH("k_ewm_dr", k_ewm_dr, dim3(ceil_div(E, kThreads)), dim3(kThreads),
-                   sizeof(int) * L.wdim, s, L, B, K, E, dist, F, dFe, gdist);
-    if (int rc = reduce_partials(dCp, G, ncc, gC, tmp, s)) return rc;
-    return reduce_partials(hp, nchunks, hsz, gF, tmp, s);
+    return ew_tail(L, B, K, E, dist, F, dFe, dCp, G, ncc, gC, gF, gdist, tail, s);
 }
 
 // The layout is the canonical (0..lin) x (0..lout) pair the kernels are built for.

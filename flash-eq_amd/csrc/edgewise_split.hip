@@ -176,32 +176,193 @@ __device__ __forceinline__ void store_tile4(const float4 (&v)[NV], float* dst) {
     for (int n = 0; n < NV; ++n) {
         const int q = tid + kThreads * n;
         if (q < NQ) {
-            const float f[4] = {v[n].x, v[n].y, v[n].z, v[n].w};
+            if constexpr (S == N) {
+                // rows are packed: one 16-byte store (scalar stores at a 16-byte
+                // lane stride would hit a quarter of the banks)
+                *reinterpret_cast<float4*>(dst + 4 * q) = v[n];
+            } else {
+                const float f[4] = {v[n].x, v[n].y, v[n].z, v[n].w};
 #pragma unroll
-            for (int c = 0; c < 4; ++c) dst[((4 * q + c) / N) * S + (4 * q + c) % N] = f[c];
+                for (int c = 0; c < 4; ++c) dst[((4 * q + c) / N) * S + (4 * q + c) % N] = f[c];
+            }
         }
     }
+}
+
+// Row stride (floats) of a tile of kNE rows of n floats staged in LDS: a
+// multiple of 4 (16-byte rows) with an odd number of 16-byte units, so 16-byte
+// accesses of consecutive rows hit distinct banks.
+constexpr int stage_stride(int n) { return ((n + 3) / 4 | 1) * 4; }
+
+// Writes this lane's 4 rows x D floats (rows c0 .. c0 + 3 of edge le, contiguous
+// in global memory) into the staging tile, whose edge rows hold CH * D floats.
+template <int CH, int D>
+__device__ __forceinline__ void stage_rows(float* stage, int le, int c0, const float (&out)[4 * D]) {
+    float4* dst = reinterpret_cast<float4*>(stage + le * stage_stride(CH * D) + c0 * D);
+#pragma unroll
+    for (int v = 0; v < D; ++v) dst[v] = make_float4(out[4 * v], out[4 * v + 1], out[4 * v + 2], out[4 * v + 3]);
+}
+
+// Copies the staged tile (nval edges) to its contiguous global rows with
+// fully coalesced 16-byte stores.
+template <int CH, int D>
+__device__ __forceinline__ void flush_stage(const float* stage, float* __restrict__ g, int nval) {
+    constexpr int ROW4 = CH * D / 4, SS4 = stage_stride(CH * D) / 4;
+    static_assert((CH * D) % 4 == 0, "rows of whole float4s");
+    const float4* s4 = reinterpret_cast<const float4*>(stage);
+    float4* g4 = reinterpret_cast<float4*>(g);
+    if (nval == kNE) {
+#pragma unroll
+        for (int n = 0; n < kNE * ROW4 / kThreads; ++n) {
+            const int q = threadIdx.x + kThreads * n;
+            g4[q] = s4[(q / ROW4) * SS4 + q % ROW4];
+        }
+        if constexpr ((kNE * ROW4) % kThreads != 0) {
+            const int q = threadIdx.x + kThreads * (kNE * ROW4 / kThreads);
+            if (q < kNE * ROW4) g4[q] = s4[(q / ROW4) * SS4 + q % ROW4];
+        }
+    } else {
+        for (int q = threadIdx.x; q < nval * ROW4; q += kThreads) g4[q] = s4[(q / ROW4) * SS4 + q % ROW4];
+    }
+}
+
+// Degree of m-first slot j of a canonical representation (4-bit packed table).
+template <int L>
+struct SlotDegPacked {
+    static constexpr int D = (L + 1) * (L + 1), NW = (D + 15) / 16;
+    static constexpr std::array<unsigned long long, NW> make() {
+        std::array<unsigned long long, NW> w{};
+        for (int j = 0; j < D; ++j)
+            w[j / 16] |= static_cast<unsigned long long>(SlotL<L>::l[j]) << (4 * (j % 16));
+        return w;
+    }
+    static constexpr std::array<unsigned long long, NW> words = make();
+};
+
+template <int L>
+__device__ __forceinline__ int slot_degree(int j) {
+    using S = SlotDegPacked<L>;
+    unsigned long long w = S::words[0];
+#pragma unroll
+    for (int n = 1; n < S::NW; ++n) w = (j >> 4) == n ? S::words[n] : w;
+    return static_cast<int>((w >> (4 * (j & 15))) & 15u);
+}
+
+__device__ __forceinline__ int std_degree(int d, int L) {
+    int l = 0;
+    for (int k = 1; k <= L; ++k) l += d >= k * k;
+    return l;
+}
+
+// 1 when an element of this thread's share of a (kNE, D, D) basis tile (read by
+// load_tile4) lies outside the degree blocks and is non-zero.
+template <int L, int NV>
+__device__ __forceinline__ int off_block_nonzero(const float4 (&v)[NV]) {
+    constexpr int D = (L + 1) * (L + 1), N = D * D, NQ = kNE * N / 4;
+    int any = 0;
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+        const int q = threadIdx.x + kThreads * n;
+        if (q < NQ) {
+            const float f[4] = {v[n].x, v[n].y, v[n].z, v[n].w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int pos = (4 * q + c) % N;
+                any |= (f[c] != 0.0f) & (std_degree(pos / D, L) != slot_degree<L>(pos % D));
+            }
+        }
+    }
+    return any;
+}
+
+// out[r][j] = sum_d x[r][d] R[d][j] for NR rows (x P, gy Q).  SPARSE sums only
+// the degree block of column j.
+template <int L, bool SPARSE, int NR>
+__device__ __forceinline__ void rotate_cols(const float* __restrict__ x, const float* re,
+                                            float (&out)[NR][(L + 1) * (L + 1)]) {
+    constexpr int D = (L + 1) * (L + 1);
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+        for (int j = 0; j < D; ++j) out[r][j] = 0.0f;
+    if constexpr (SPARSE) {
+        static_for<D>([&](auto JJ) {
+            constexpr int j = decltype(JJ)::value, l = SlotL<L>::l[j];
+#pragma unroll
+            for (int d = l * l; d < (l + 1) * (l + 1); ++d) {
+                const float rv = re[d * D + j];
+#pragma unroll
+                for (int r = 0; r < NR; ++r) out[r][j] += x[r * D + d] * rv;
+            }
+        });
+    } else {
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                const float rv = re[d * D + j];
+#pragma unroll
+                for (int r = 0; r < NR; ++r) out[r][j] += x[r * D + d] * rv;
+            }
+    }
+}
+
+// out[r][d] = sum_j R[d][j] v(r, j) for 4 rows (y = v Q^T, dx = v P^T);
+// v(r, j) = vin[j][r].  SPARSE sums only the degree block of row d.
+template <int L, bool SPARSE>
+__device__ __forceinline__ void rotate_rows(const float (&vin)[(L + 1) * (L + 1)][4], const float* re,
+                                            float (&out)[4 * (L + 1) * (L + 1)]) {
+    constexpr int D = (L + 1) * (L + 1);
+    using DB = DegreeBlocks<L>;
+    static_for<D>([&](auto DD) {
+        constexpr int d = decltype(DD)::value, l = DB::deg(d);
+        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (SPARSE) {
+#pragma unroll
+            for (int n = l * l; n < (l + 1) * (l + 1); ++n) {
+                const int j = DB::slots[n];
+                const float rv = re[d * D + j];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) a[r] += vin[j][r] * rv;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                const float rv = re[d * D + j];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) a[r] += vin[j][r] * rv;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) out[r * D + d] = a[r];
+    });
 }
 
 // ---------------------------------------------------------------------------
 // Forward: y = Q-rotate(s^l_out sum_k M_ek G_k), G_k = C_k fs, fs = s^l_in (x P).
 // A workgroup owns one 16-edge tile at a time; wave w owns output rows
-// co = 16 (w + 4 j) + ..., j < Cout / 64.  Per tile: (1) global loads of x,
-// P, Q and distances; (2) P/Q to LDS; (3) fs rows are rotated by threads that
-// own 4 channels of one edge, scaled per edge, split and written as fp16
-// fragments; (4) per slot i the waves run the 3-term MFMA products for all
-// rank components and contract them into y (registers); (5) Q rotation and
-// direct 16-byte stores (each lane owns 4 consecutive channels of one edge).
-template <int CIN, int COUT, int LIN, int LOUT, int K>
-__global__ void __launch_bounds__(kThreads, 2)
+// co = 16 (w + 4 j) + ..., j < Cout / 64.  Per tile: (1) P, Q and edge state
+// to LDS, and a test whether every off-block entry of the tile's P and Q is
+// zero (then the rotations sum over the degree blocks only); (2) fs rows are
+// rotated by threads that own 4 channels of one edge, scaled per edge, split
+// and written as fp16 fragments; (3) the rank components run in passes of KP:
+// per slot i the 3-term MFMA products of the pass's components are contracted
+// into y (registers); (4) the next tile's global loads are issued, then the Q
+// rotation and direct 16-byte stores (each lane owns 4 consecutive channels
+// of one edge).  Row strides of the per-edge LDS blocks are odd, so the 16
+// edges of a wave's lanes hit distinct banks.
+template <int CIN, int COUT, int LIN, int LOUT, int K, int OCC>
+__global__ void __launch_bounds__(kThreads, OCC)
 k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
           const float* __restrict__ P, const float* __restrict__ Q,
           const float* __restrict__ dist, const h8* __restrict__ Cfrag,
           const float* __restrict__ Cinv, const float* __restrict__ F, float* __restrict__ y) {
     using T = Canon<LIN, LOUT>;
+    using TG = TermGroups<LIN, LOUT, false>;
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
-    constexpr int PS = (DIN * DIN + 3) / 4 * 4, QS = (DOUT * DOUT + 3) / 4 * 4;
+    constexpr int PS = DIN * DIN | 1, QS = DOUT * DOUT | 1, KWS = KW | 1;
     constexpr int RPW = COUT / 64, NKS = CIN / 32, NC4 = CIN / 4;
+    constexpr int KP = K % 2 == 0 ? 2 : 1;                       // rank components per pass
     constexpr int CHUNK = 1024;                                  // bytes per fragment chunk
     constexpr int NPR = (kNE * NC4 + kThreads - 1) / kThreads;   // producer passes
     constexpr int NPL = (kNE * DIN * DIN / 4 + kThreads - 1) / kThreads;
@@ -209,30 +370,35 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
     static_assert(COUT % 64 == 0 && CIN % 32 == 0 && NC4 <= 64, "unsupported channel counts");
     static_assert((kNE * NC4) % kThreads == 0 || kNE * NC4 < kThreads, "producer split");
 
+    constexpr int BREG = 2 * DIN * NKS * CHUNK > 4 * kNE * stage_stride(COUT * DOUT)
+                             ? 2 * DIN * NKS * CHUNK : 4 * kNE * stage_stride(COUT * DOUT);
     extern __shared__ float4 smem4[];
-    char* sB = reinterpret_cast<char*>(smem4);                   // [2][DIN][NKS] chunks
-    float* sP = reinterpret_cast<float*>(sB + 2 * DIN * NKS * CHUNK);
+    char* sB = reinterpret_cast<char*>(smem4);                   // [2][DIN][NKS] chunks, then the y stage
+    float* sP = reinterpret_cast<float*>(sB + BREG);
     float* sQ = sP + kNE * PS;
     float* sFe = sQ + kNE * QS;
-    float* sSout = sFe + kNE * KW;
+    float* sSout = sFe + kNE * KWS;
     float* sInvK = sSout + kNE * DOUT;
     EdgeState* sE = reinterpret_cast<EdgeState*>(sInvK + K);
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
     const int le = lane & 15, lg = lane >> 4;
 
     if (tid < K) sInvK[tid] = Cinv[tid];   // read after the first tile barrier
 
-    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        const int64_t e0 = tile * kNE;
-        // (1) global loads for this tile
-        float xr[NPR][4 * DIN];
+    // global loads of one tile (zeros past the last edge)
+    float xr[NPR][4 * DIN];
+    float4 pr[NPL], qr[NQL];
+    float rd;
+    auto load_tile = [&](int64_t t) {
+        const int64_t f0 = t * kNE;
 #pragma unroll
         for (int p = 0; p < NPR; ++p) {
             const int q = tid + kThreads * p;
             const int e = q / NC4, c4 = q % NC4;
-            if (q < kNE * NC4 && e0 + e < E) {
-                const float4* src = reinterpret_cast<const float4*>(x + ((e0 + e) * CIN + 4 * c4) * DIN);
+            if (q < kNE * NC4 && f0 + e < E) {
+                const float4* src = reinterpret_cast<const float4*>(x + ((f0 + e) * CIN + 4 * c4) * DIN);
 #pragma unroll
                 for (int v = 0; v < DIN; ++v) {
                     const float4 f = src[v];
@@ -246,34 +412,14 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
                 for (int v = 0; v < 4 * DIN; ++v) xr[p][v] = 0.0f;
             }
         }
-        float4 pr[NPL], qr[NQL];
-        load_tile4<DIN * DIN, NPL>(P, e0, E, pr);
-        load_tile4<DOUT * DOUT, NQL>(Q, e0, E, qr);
-        const float rd = (tid < kNE && e0 + tid < E) ? dist[e0 + tid] : 1.0f;
+        load_tile4<DIN * DIN, NPL>(P, f0, E, pr);
+        load_tile4<DOUT * DOUT, NQL>(Q, f0, E, qr);
+        rd = (tid < kNE && f0 + tid < E) ? dist[f0 + tid] : 1.0f;
+    };
 
-        __syncthreads();   // the previous tile's readers of every LDS buffer are done
-        // (2) P, Q and edge state to LDS
-        store_tile4<DIN * DIN, NPL, PS>(pr, sP);
-        store_tile4<DOUT * DOUT, NQL, QS>(qr, sQ);
-        if (tid < kNE) {
-            EdgeState es;
-            es.valid = e0 + tid < E;
-            const EdgeBin eb = edge_bin(rd, B);
-            es.lo = eb.lo;
-            es.t = eb.t;
-            es.s = rd / (rd + B.sh_scale);
-            sE[tid] = es;
-        }
-        __syncthreads();
-
-        // (3) radial functions of the tile (with 1/scale_k folded in)
-        for (int q = tid; q < kNE * KW; q += kThreads) {
-            const int e = q / KW, rest = q % KW;
-            const EdgeState es = sE[e];
-            const float* flo = F + static_cast<int64_t>(es.lo) * KW + rest;
-            sFe[q] = lerp_bins(flo[0], flo[KW], es.t) * sInvK[rest / WD];
-        }
-        // fs rows: thread (e, c4) owns channels 4 c4 .. 4 c4 + 3 of edge e
+    // fs rows of this thread: rotation, per-edge scale, split, fragment writes
+    auto produce = [&](auto sparse) {
+        constexpr bool SP = decltype(sparse)::value;
 #pragma unroll
         for (int p = 0; p < NPR; ++p) {
             const int q = tid + kThreads * p;
@@ -283,19 +429,7 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
             float pw[DIN];
             slot_pow<LIN>(sE[ee].s, pw);
             float fs[4][DIN];
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-                for (int i = 0; i < DIN; ++i) fs[r][i] = 0.0f;
-            const float* pe = sP + ee * PS;
-#pragma unroll
-            for (int d = 0; d < DIN; ++d)
-#pragma unroll
-                for (int i = 0; i < DIN; ++i) {
-                    const float pv = pe[d * DIN + i];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) fs[r][i] += xr[p][r * DIN + d] * pv;
-                }
+            rotate_cols<LIN, SP, 4>(xr[p], sP + ee * PS, fs);
             float m = 0.0f;
 #pragma unroll
             for (int r = 0; r < 4; ++r)
@@ -333,27 +467,41 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
                 }
             }
         }
-        // A fragments of this wave's rows (L2-resident), in flight across the
-        // barrier.  The empty asm makes the pointer opaque per tile, so the
-        // loads are not hoisted out of the tile loop (their registers would
-        // then stay live through the producer phase).
-        const h8* cfr = Cfrag;
-        asm volatile("" : "+s"(cfr));
-        h8 ahi[RPW][K][NKS], alo[RPW][K][NKS];
-#pragma unroll
-        for (int j = 0; j < RPW; ++j)
-#pragma unroll
-            for (int k = 0; k < K; ++k)
-#pragma unroll
-                for (int ks = 0; ks < NKS; ++ks) {
-                    const h8* src = cfr + 2 * (((k * (COUT / 16) + wave + 4 * j) * NKS + ks) * 64 + lane);
-                    ahi[j][k][ks] = src[0];
-                    alo[j][k][ks] = src[1];
-                }
+    };
+
+    load_tile(blockIdx.x);
+    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const int64_t e0 = tile * kNE;
+        __syncthreads();   // the previous tile's readers of every LDS buffer are done
+        // (1) P, Q and edge state to LDS; block-structure test of the tile
+        store_tile4<DIN * DIN, NPL, PS>(pr, sP);
+        store_tile4<DOUT * DOUT, NQL, QS>(qr, sQ);
+        if (tid < kNE) {
+            EdgeState es;
+            es.valid = e0 + tid < E;
+            const EdgeBin eb = edge_bin(rd, B);
+            es.lo = eb.lo;
+            es.t = eb.t;
+            es.s = rd / (rd + B.sh_scale);
+            sE[tid] = es;
+        }
+        const bool dense =
+            __syncthreads_or(off_block_nonzero<LIN>(pr) | off_block_nonzero<LOUT>(qr)) != 0;
+
+        // (2) radial functions of the tile (1/scale_k folded in) and fs fragments
+        for (int q = tid; q < kNE * KW; q += kThreads) {
+            const int e = q / KW, rest = q % KW;
+            const EdgeState es = sE[e];
+            const float* flo = F + static_cast<int64_t>(es.lo) * KW + rest;
+            sFe[e * KWS + rest] = lerp_bins(flo[0], flo[KW], es.t) * sInvK[rest / WD];
+        }
+        if (dense)
+            produce(std::false_type{});
+        else
+            produce(std::true_type{});
         __syncthreads();
 
-        // (4) GEMM per input slot and contraction into y (m-first output slots)
-        using TG = TermGroups<LIN, LOUT, false>;
+        // (3) GEMM per input slot, rank components in passes of KP
         float yv[RPW][DOUT][4];
 #pragma unroll
         for (int j = 0; j < RPW; ++j)
@@ -361,113 +509,755 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
             for (int o = 0; o < DOUT; ++o)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) yv[j][o][r] = 0.0f;
-        const float* fe = sFe + le * KW;
+        const float* fe = sFe + le * KWS;
         const int myslot = bslot(lg, le);
-        // B fragments are double-buffered one slot ahead; the scheduling fence
-        // at the end of each slot keeps the compiler from hoisting every
-        // slot's loads (which would not fit the register budget).
-        h8 bh[2][NKS], bl[2][NKS];
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-            bh[0][ks] = *reinterpret_cast<const h8*>(sB + ks * CHUNK + myslot);
-            bl[0][ks] = *reinterpret_cast<const h8*>(sB + (DIN * NKS + ks) * CHUNK + myslot);
-        }
-        static_for<DIN>([&](auto I) {
-            constexpr int i = decltype(I)::value;
-            constexpr int cur = i & 1;
-            if constexpr (i + 1 < DIN) {
-#pragma unroll
-                for (int ks = 0; ks < NKS; ++ks) {
-                    bh[cur ^ 1][ks] = *reinterpret_cast<const h8*>(sB + ((i + 1) * NKS + ks) * CHUNK + myslot);
-                    bl[cur ^ 1][ks] =
-                        *reinterpret_cast<const h8*>(sB + ((DIN + i + 1) * NKS + ks) * CHUNK + myslot);
-                }
-            }
-            v4f acc[RPW][K];
+        static_for<K / KP>([&](auto PP) {
+            constexpr int k0 = decltype(PP)::value * KP;
+            // A fragments of this pass (L2-resident); the opaque pointer keeps
+            // the loads inside the tile loop
+            const h8* cfr = Cfrag;
+            asm volatile("" : "+s"(cfr));
+            h8 ahi[RPW][KP][NKS], alo[RPW][KP][NKS];
 #pragma unroll
             for (int j = 0; j < RPW; ++j)
 #pragma unroll
-                for (int k = 0; k < K; ++k) acc[j][k] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                for (int kk = 0; kk < KP; ++kk)
 #pragma unroll
-            for (int ks = 0; ks < NKS; ++ks)
+                    for (int ks = 0; ks < NKS; ++ks) {
+                        const h8* src =
+                            cfr + 2 * ((((k0 + kk) * (COUT / 16) + wave + 4 * j) * NKS + ks) * 64 + lane);
+                        ahi[j][kk][ks] = src[0];
+                        alo[j][kk][ks] = src[1];
+                    }
+            // B fragments double-buffered one slot ahead; the fence at the end
+            // of each slot keeps the compiler from hoisting every slot's loads
+            h8 bh[2][NKS], bl[2][NKS];
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                bh[0][ks] = *reinterpret_cast<const h8*>(sB + ks * CHUNK + myslot);
+                bl[0][ks] = *reinterpret_cast<const h8*>(sB + (DIN * NKS + ks) * CHUNK + myslot);
+            }
+            static_for<DIN>([&](auto I) {
+                constexpr int i = decltype(I)::value;
+                constexpr int cur = i & 1;
+                if constexpr (i + 1 < DIN) {
+#pragma unroll
+                    for (int ks = 0; ks < NKS; ++ks) {
+                        bh[cur ^ 1][ks] =
+                            *reinterpret_cast<const h8*>(sB + ((i + 1) * NKS + ks) * CHUNK + myslot);
+                        bl[cur ^ 1][ks] =
+                            *reinterpret_cast<const h8*>(sB + ((DIN + i + 1) * NKS + ks) * CHUNK + myslot);
+                    }
+                }
+                v4f acc[RPW][KP];
 #pragma unroll
                 for (int j = 0; j < RPW; ++j)
 #pragma unroll
-                    for (int k = 0; k < K; ++k) {
-                        acc[j][k] = mfma_h(alo[j][k][ks], bh[cur][ks], acc[j][k]);
-                        acc[j][k] = mfma_h(ahi[j][k][ks], bl[cur][ks], acc[j][k]);
-                        acc[j][k] = mfma_h(ahi[j][k][ks], bh[cur][ks], acc[j][k]);
-                    }
-            static_for<TG::count(i)>([&](auto TT) {
-                constexpr Term tm = TG::sorted[TG::start[i] + decltype(TT)::value];
+                    for (int kk = 0; kk < KP; ++kk) acc[j][kk] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int k = 0; k < K; ++k) {
-                    const float c = tm.neg ? -fe[k * WD + tm.w] : fe[k * WD + tm.w];
+                for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
                     for (int j = 0; j < RPW; ++j)
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) yv[j][tm.o][r] += c * acc[j][k][r];
-                }
-            });
-            __builtin_amdgcn_sched_barrier(0);
-        });
-        // Uses of every y register here keep the compiler from sinking the
-        // contractions into the store branch below (which would keep all
-        // MFMA results live until then).
+                        for (int kk = 0; kk < KP; ++kk) {
+                            acc[j][kk] = mfma_h(alo[j][kk][ks], bh[cur][ks], acc[j][kk]);
+                            acc[j][kk] = mfma_h(ahi[j][kk][ks], bl[cur][ks], acc[j][kk]);
+                            acc[j][kk] = mfma_h(ahi[j][kk][ks], bh[cur][ks], acc[j][kk]);
+                        }
+                static_for<TG::count(i)>([&](auto TT) {
+                    constexpr Term tm = TG::sorted[TG::start[i] + decltype(TT)::value];
 #pragma unroll
-        for (int j = 0; j < RPW; ++j)
+                    for (int kk = 0; kk < KP; ++kk) {
+                        const float f = fe[(k0 + kk) * WD + tm.w];
+                        const float c = tm.neg ? -f : f;
 #pragma unroll
-            for (int o = 0; o < DOUT; ++o)
+                        for (int j = 0; j < RPW; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) asm volatile("" ::"v"(yv[j][o][r]));
-
-        // (5) output scaling, Q rotation and stores
-        {
-            const float* so = sSout + le * DOUT;
-            const float* qe = sQ + le * QS;
-#pragma unroll
-            for (int o = 0; o < DOUT; ++o) {
-                const float sc = so[o];
+                            for (int r = 0; r < 4; ++r) yv[j][tm.o][r] += c * acc[j][kk][r];
+                    }
+                });
+                // Pin the contraction to this slot: without these (empty)
+                // read-modify-write uses the compiler defers it past later
+                // slots' MFMAs and keeps their results live.
 #pragma unroll
                 for (int j = 0; j < RPW; ++j)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) yv[j][o][r] *= sc;
+                    for (int o = 0; o < DOUT; ++o)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(yv[j][o][r]));
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        });
+
+        // (4) next tile's global loads, then output scaling, Q rotation and stores
+        load_tile(tile + gridDim.x);
+        const float* so = sSout + le * DOUT;
+        const float* qe = sQ + le * QS;
+#pragma unroll
+        for (int o = 0; o < DOUT; ++o) {
+            const float sc = so[o];
+#pragma unroll
+            for (int j = 0; j < RPW; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) yv[j][o][r] *= sc;
+        }
+        __syncthreads();   // every wave is done with the fragments: the buffer becomes the y stage
+#pragma unroll
+        for (int j = 0; j < RPW; ++j) {
+            float out[4 * DOUT];
+            if (dense)
+                rotate_rows<LOUT, false>(yv[j], qe, out);
+            else
+                rotate_rows<LOUT, true>(yv[j], qe, out);
+            stage_rows<COUT, DOUT>(reinterpret_cast<float*>(sB), le, 16 * (wave + 4 * j) + 4 * lg, out);
+        }
+        __syncthreads();
+        flush_stage<COUT, DOUT>(reinterpret_cast<const float*>(sB), y + e0 * COUT * DOUT,
+                                static_cast<int>(E - e0 < kNE ? E - e0 : kNE));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Input gradient: H_k = C_k^T gd (M = Cin, N = 16 Dout, K = Cout) with
+// gd = s^l_out (gy Q), then in registers
+//   dfs[ci, i] = sum_k sum_o M_ek[o][i] H_k[ci, o]      dx = s^l_in dfs P^T
+//   dF_e[k, w] = sum_ci sum_{terms (o, i, w)} sign fs[ci, i] H_k[ci, o]
+// (the per-edge radial-function gradient, binned afterwards), where
+// fs = s^l_in (x P) is built directly in the accumulator layout: lane
+// (le, lg) of wave w holds rows ci = 16 (w + 4 j) + 4 lg + r of edge le.
+// gd is scaled per edge and split into fp16 fragments like fs in the forward;
+// C_k^T comes pre-split from k_ews_prep (same per-rank scale as C_k), one pass
+// of KP rank components at a time.  The dF_e partials of a weight w are
+// complete after the last output slot that uses it: they are summed over the
+// wave's four lane groups with two lane shuffles, unscaled, and summed over
+// the four waves in LDS.  Rotations use the degree blocks when the tile's P
+// and Q have no entry off them; dx is staged in LDS and stored coalesced.
+template <int CIN, int COUT, int LIN, int LOUT, int K>
+__global__ void __launch_bounds__(kThreads, 2)
+k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
+            const float* __restrict__ x, const float* __restrict__ P,
+            const float* __restrict__ Q, const float* __restrict__ dist,
+            const h8* __restrict__ Cfrag, const float* __restrict__ Cinv,
+            const float* __restrict__ F, float* __restrict__ gx, float* __restrict__ dFe) {
+    using T = Canon<LIN, LOUT>;
+    using TG = TermGroups<LIN, LOUT, true>;
+    constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
+    constexpr int PS = DIN * DIN | 1, QS = DOUT * DOUT | 1, KWS = KW | 1;
+    constexpr int KP = K % 2 == 0 ? 2 : 1;   // rank components per GEMM pass
+    constexpr int RPW = CIN / 64, NKS = COUT / 32, NC4 = COUT / 4;
+    constexpr int CHUNK = 1024;
+    constexpr int NPR = (kNE * NC4 + kThreads - 1) / kThreads;
+    constexpr int NPL = (kNE * DIN * DIN / 4 + kThreads - 1) / kThreads;
+    constexpr int NQL = (kNE * DOUT * DOUT / 4 + kThreads - 1) / kThreads;
+    constexpr int BREG = 2 * DOUT * NKS * CHUNK > 4 * kNE * stage_stride(CIN * DIN)
+                             ? 2 * DOUT * NKS * CHUNK : 4 * kNE * stage_stride(CIN * DIN);
+    static_assert(CIN % 64 == 0 && COUT % 32 == 0 && NC4 <= 64, "unsupported channel counts");
+    static_assert((kNE * NC4) % kThreads == 0 || kNE * NC4 < kThreads, "producer split");
+
+    extern __shared__ float4 smem4[];
+    char* sB = reinterpret_cast<char*>(smem4);                   // gd fragments, then the dx stage
+    float* sP = reinterpret_cast<float*>(sB + BREG);
+    float* sQ = sP + kNE * PS;
+    float* sFe = sQ + kNE * QS;
+    float* sDF = sFe + kNE * KWS;                                 // [4 waves][kNE][KW]
+    float* sSin = sDF + 4 * kNE * KW;                             // s^l_in / scale_e
+    float* sEinv = sSin + kNE * DIN;                              // 1 / scale_e
+    float* sInvK = sEinv + kNE;
+    EdgeState* sE = reinterpret_cast<EdgeState*>(sInvK + K);
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
+    const int le = lane & 15, lg = lane >> 4;
+    if (tid < K) sInvK[tid] = Cinv[tid];
+
+    // global loads of one tile: gy rows of the producer threads, x rows of the
+    // lane layout, P, Q, distances (zeros past the last edge)
+    float gr[NPR][4 * DOUT];
+    float xl[RPW][4 * DIN];
+    float4 pr[NPL], qr[NQL];
+    float rd;
+    auto load_tile = [&](int64_t t) {
+        const int64_t f0 = t * kNE;
+#pragma unroll
+        for (int p = 0; p < NPR; ++p) {
+            const int q = tid + kThreads * p;
+            const int e = q / NC4, c4 = q % NC4;
+            if (q < kNE * NC4 && f0 + e < E) {
+                const float4* src = reinterpret_cast<const float4*>(gy + ((f0 + e) * COUT + 4 * c4) * DOUT);
+#pragma unroll
+                for (int v = 0; v < DOUT; ++v) {
+                    const float4 f = src[v];
+                    gr[p][4 * v] = f.x;
+                    gr[p][4 * v + 1] = f.y;
+                    gr[p][4 * v + 2] = f.z;
+                    gr[p][4 * v + 3] = f.w;
+                }
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4 * DOUT; ++v) gr[p][v] = 0.0f;
             }
+        }
 #pragma unroll
-            for (int j = 0; j < RPW; ++j) {
-                float out[4 * DOUT];
+        for (int j = 0; j < RPW; ++j) {
+            if (f0 + le < E) {
+                const float4* src = reinterpret_cast<const float4*>(
+                    x + ((f0 + le) * CIN + 16 * (wave + 4 * j) + 4 * lg) * DIN);
 #pragma unroll
-                for (int d = 0; d < DOUT; ++d) {
-                    float qrow[DOUT];
+                for (int v = 0; v < DIN; ++v) {
+                    const float4 f = src[v];
+                    xl[j][4 * v] = f.x;
+                    xl[j][4 * v + 1] = f.y;
+                    xl[j][4 * v + 2] = f.z;
+                    xl[j][4 * v + 3] = f.w;
+                }
+            } else {
 #pragma unroll
-                    for (int o = 0; o < DOUT; ++o) qrow[o] = qe[d * DOUT + o];
+                for (int v = 0; v < 4 * DIN; ++v) xl[j][v] = 0.0f;
+            }
+        }
+        load_tile4<DIN * DIN, NPL>(P, f0, E, pr);
+        load_tile4<DOUT * DOUT, NQL>(Q, f0, E, qr);
+        rd = (tid < kNE && f0 + tid < E) ? dist[f0 + tid] : 1.0f;
+    };
+
+    // gd fragments (producer threads) and fs in the lane layout
+    float fsr[RPW][4][DIN];
+    auto produce = [&](auto sparse) {
+        constexpr bool SP = decltype(sparse)::value;
+#pragma unroll
+        for (int p = 0; p < NPR; ++p) {
+            const int q = tid + kThreads * p;
+            const int e = q / NC4, c4 = q % NC4;
+            const bool act = q < kNE * NC4;
+            const int ee = act ? e : 0;
+            float pw[DOUT];
+            slot_pow<LOUT>(sE[ee].s, pw);
+            float gd[4][DOUT];
+            rotate_cols<LOUT, SP, 4>(gr[p], sQ + ee * QS, gd);
+            float m = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int o = 0; o < DOUT; ++o) {
+                    gd[r][o] *= pw[o];
+                    m = fmaxf(m, fabsf(gd[r][o]));
+                }
+#pragma unroll
+            for (int off = NC4 / 2; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+            const int ex = scale_exp(m);
+            const float sc = exp2i(ex);
+            if (act && c4 == 0) {
+                float pi[DIN];
+                slot_pow<LIN>(sE[e].s, pi);
+                const float inv = exp2i(-ex);
+                sEinv[e] = inv;
+#pragma unroll
+                for (int i = 0; i < DIN; ++i) sSin[e * DIN + i] = pi[i] * inv;
+            }
+            if (act) {
+                const int ks = c4 / 8, g = (c4 / 2) % 4, half = c4 % 2;
+                char* base = sB + ks * CHUNK + bslot(g, e) + 8 * half;
+#pragma unroll
+                for (int o = 0; o < DOUT; ++o) {
+                    h4 hv, lv;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        float a = 0.0f;
-#pragma unroll
-                        for (int o = 0; o < DOUT; ++o) a += yv[j][o][r] * qrow[o];
-                        out[r * DOUT + d] = a;
+                        _Float16 h, l;
+                        split_f16(gd[r][o] * sc, h, l);
+                        hv[r] = h;
+                        lv[r] = l;
                     }
-                }
-                if (e0 + le < E) {
-                    float4* dst = reinterpret_cast<float4*>(
-                        y + ((e0 + le) * COUT + 16 * (wave + 4 * j) + 4 * lg) * DOUT);
-#pragma unroll
-                    for (int v = 0; v < DOUT; ++v)
-                        dst[v] = make_float4(out[4 * v], out[4 * v + 1], out[4 * v + 2], out[4 * v + 3]);
+                    *reinterpret_cast<h4*>(base + (o * NKS) * CHUNK) = hv;
+                    *reinterpret_cast<h4*>(base + ((DOUT + o) * NKS) * CHUNK) = lv;
                 }
             }
         }
+        float pi[DIN];
+        slot_pow<LIN>(sE[le].s, pi);
+#pragma unroll
+        for (int j = 0; j < RPW; ++j) {
+            rotate_cols<LIN, SP, 4>(xl[j], sP + le * PS, fsr[j]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int i = 0; i < DIN; ++i) fsr[j][r][i] *= pi[i];
+        }
+    };
+
+    load_tile(blockIdx.x);
+    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const int64_t e0 = tile * kNE;
+        __syncthreads();   // the previous tile's readers of every LDS buffer are done
+        store_tile4<DIN * DIN, NPL, PS>(pr, sP);
+        store_tile4<DOUT * DOUT, NQL, QS>(qr, sQ);
+        if (tid < kNE) {
+            EdgeState es;
+            es.valid = e0 + tid < E;
+            const EdgeBin eb = edge_bin(rd, B);
+            es.lo = eb.lo;
+            es.t = eb.t;
+            es.s = rd / (rd + B.sh_scale);
+            sE[tid] = es;
+        }
+        const bool dense =
+            __syncthreads_or(off_block_nonzero<LIN>(pr) | off_block_nonzero<LOUT>(qr)) != 0;
+
+        // radial functions (1/scale_k folded in), gd fragments, fs in lane layout
+        for (int q = tid; q < kNE * KW; q += kThreads) {
+            const int e = q / KW, rest = q % KW;
+            const EdgeState es = sE[e];
+            const float* flo = F + static_cast<int64_t>(es.lo) * KW + rest;
+            sFe[e * KWS + rest] = lerp_bins(flo[0], flo[KW], es.t) * sInvK[rest / WD];
+        }
+        if (dense)
+            produce(std::false_type{});
+        else
+            produce(std::true_type{});
+        __syncthreads();
+
+        // GEMM per output slot o, rank components in passes of KP; contractions
+        // into dfs and the dF_e partials
+        float dfs[RPW][4][DIN];
+#pragma unroll
+        for (int j = 0; j < RPW; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int i = 0; i < DIN; ++i) dfs[j][r][i] = 0.0f;
+        const float* fe = sFe + le * KWS;
+        const float einv = sEinv[le];
+        const int myslot = bslot(lg, le);
+        static_for<K / KP>([&](auto PP) {
+            constexpr int k0 = decltype(PP)::value * KP;
+            const h8* cfr = Cfrag;
+            asm volatile("" : "+s"(cfr));
+            h8 ahi[RPW][KP][NKS], alo[RPW][KP][NKS];
+#pragma unroll
+            for (int j = 0; j < RPW; ++j)
+#pragma unroll
+                for (int kk = 0; kk < KP; ++kk)
+#pragma unroll
+                    for (int ks = 0; ks < NKS; ++ks) {
+                        const h8* src =
+                            cfr + 2 * ((((k0 + kk) * (CIN / 16) + wave + 4 * j) * NKS + ks) * 64 + lane);
+                        ahi[j][kk][ks] = src[0];
+                        alo[j][kk][ks] = src[1];
+                    }
+            float pf[KP][WD];
+#pragma unroll
+            for (int kk = 0; kk < KP; ++kk)
+#pragma unroll
+                for (int w = 0; w < WD; ++w) pf[kk][w] = 0.0f;
+            h8 bh[2][NKS], bl[2][NKS];
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                bh[0][ks] = *reinterpret_cast<const h8*>(sB + ks * CHUNK + myslot);
+                bl[0][ks] = *reinterpret_cast<const h8*>(sB + (DOUT * NKS + ks) * CHUNK + myslot);
+            }
+            static_for<DOUT>([&](auto OO) {
+                constexpr int o = decltype(OO)::value;
+                constexpr int cur = o & 1;
+                if constexpr (o + 1 < DOUT) {
+#pragma unroll
+                    for (int ks = 0; ks < NKS; ++ks) {
+                        bh[cur ^ 1][ks] =
+                            *reinterpret_cast<const h8*>(sB + ((o + 1) * NKS + ks) * CHUNK + myslot);
+                        bl[cur ^ 1][ks] =
+                            *reinterpret_cast<const h8*>(sB + ((DOUT + o + 1) * NKS + ks) * CHUNK + myslot);
+                    }
+                }
+                v4f acc[RPW][KP];
+#pragma unroll
+                for (int j = 0; j < RPW; ++j)
+#pragma unroll
+                    for (int kk = 0; kk < KP; ++kk) acc[j][kk] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+                    for (int j = 0; j < RPW; ++j)
+#pragma unroll
+                        for (int kk = 0; kk < KP; ++kk) {
+                            acc[j][kk] = mfma_h(alo[j][kk][ks], bh[cur][ks], acc[j][kk]);
+                            acc[j][kk] = mfma_h(ahi[j][kk][ks], bl[cur][ks], acc[j][kk]);
+                            acc[j][kk] = mfma_h(ahi[j][kk][ks], bh[cur][ks], acc[j][kk]);
+                        }
+                static_for<TG::count(o)>([&](auto TT) {
+                    constexpr Term tm = TG::sorted[TG::start[o] + decltype(TT)::value];
+#pragma unroll
+                    for (int kk = 0; kk < KP; ++kk) {
+                        const float f = fe[(k0 + kk) * WD + tm.w];
+                        const float c = tm.neg ? -f : f;
+                        float part = 0.0f;
+#pragma unroll
+                        for (int j = 0; j < RPW; ++j)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                dfs[j][r][tm.i] += c * acc[j][kk][r];
+                                part += fsr[j][r][tm.i] * acc[j][kk][r];
+                            }
+                        pf[kk][tm.w] += tm.neg ? -part : part;
+                    }
+                });
+                // Pin the contraction to this slot: without these (empty)
+                // read-modify-write uses the compiler defers it past later
+                // slots' MFMAs and keeps their results live.
+#pragma unroll
+                for (int j = 0; j < RPW; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+#pragma unroll
+                        for (int i = 0; i < DIN; ++i) asm volatile("" : "+v"(dfs[j][r][i]));
+                // radial weights whose last output slot is o: finish their partials
+                static_for<WD>([&](auto WW) {
+                    constexpr int w = decltype(WW)::value;
+                    if constexpr (TG::last[w] == o) {
+#pragma unroll
+                        for (int kk = 0; kk < KP; ++kk) {
+                            float v = pf[kk][w];
+                            v += __shfl_xor(v, 16, 64);
+                            v += __shfl_xor(v, 32, 64);
+                            if (lg == 0)
+                                sDF[(wave * kNE + le) * KW + (k0 + kk) * WD + w] = v * sInvK[k0 + kk] * einv;
+                        }
+                    }
+                });
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        });
+
+        // next tile's global loads, then dx = s^l_in dfs P^T (1/scale_e folded
+        // into sSin) staged in LDS, and the dF_e sums over the waves
+        load_tile(tile + gridDim.x);
+        __syncthreads();   // fragments consumed, dF_e partials complete
+        {
+            const float* si = sSin + le * DIN;
+            const float* pe = sP + le * PS;
+            asm volatile("" : "+v"(pe));   // no reuse of the P values loaded for fs
+#pragma unroll
+            for (int i = 0; i < DIN; ++i) {
+                const float sc = si[i];
+#pragma unroll
+                for (int j = 0; j < RPW; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) dfs[j][r][i] *= sc;
+            }
+#pragma unroll
+            for (int j = 0; j < RPW; ++j) {
+                float vin[DIN][4], out[4 * DIN];
+#pragma unroll
+                for (int i = 0; i < DIN; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) vin[i][r] = dfs[j][r][i];
+                if (dense)
+                    rotate_rows<LIN, false>(vin, pe, out);
+                else
+                    rotate_rows<LIN, true>(vin, pe, out);
+                stage_rows<CIN, DIN>(reinterpret_cast<float*>(sB), le, 16 * (wave + 4 * j) + 4 * lg, out);
+            }
+        }
+        const int nval = static_cast<int>(E - e0 < kNE ? E - e0 : kNE);
+        for (int q = tid; q < nval * KW; q += kThreads) {
+            float a = sDF[q];
+#pragma unroll
+            for (int v = 1; v < 4; ++v) a += sDF[v * kNE * KW + q];
+            dFe[e0 * KW + q] = a;
+        }
+        __syncthreads();
+        flush_stage<CIN, DIN>(reinterpret_cast<const float*>(sB), gx + e0 * CIN * DIN, nval);
     }
+}
+
+// ---------------------------------------------------------------------------
+// Channel-pattern gradient: per 16-edge tile, for every rank component k,
+//   dC_k[co][ci] += sum over (slot i, edge e) of U_k[co][(i, e)] fs[ci][(i, e)],
+//   U_k[co][e][i] = sum_{terms (o, i, w)} sign F_e[k, w] gd[co][e][o]   (M_ek^T gd)
+// with gd = s^l_out (gy Q), fs = s^l_in (x P): a GEMM with M = Cout, N = Cin
+// and a reduction over the 16 Din (slot, edge) pairs of the tile (slot-major,
+// padded to whole 32-steps with zero fragments).  Producers own one channel
+// of four edges (threads 4 c .. 4 c + 3 share channel c), so each U_k row and
+// fs column gets its own power-of-two scale from a lane-quad maximum (no
+// extra barrier); each rank's tile product is unscaled row by column into a
+// float32 accumulator that lives for the whole launch.  fs fragments stay in
+// LDS for the tile; the U_k fragments of one rank at a time share their
+// buffer with the tile's P and Q.  Wave (wr, wc) owns a 2 x 2 block grid of
+// the output.  One partial dC per workgroup.
+template <int CIN, int COUT, int LIN, int LOUT, int K>
+__global__ void __launch_bounds__(kThreads, 2)
+k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
+            const float* __restrict__ x, const float* __restrict__ P,
+            const float* __restrict__ Q, const float* __restrict__ dist,
+            const float* __restrict__ F, float* __restrict__ dC_part) {
+    using T = Canon<LIN, LOUT>;
+    constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
+    constexpr int PS = DIN * DIN | 1, QS = DOUT * DOUT | 1, KWS = KW | 1;
+    constexpr int RB = COUT / 16, CB = CIN / 16;                 // 16-row / 16-column blocks
+    constexpr int WR = RB / 2, WC = CB / 2;                      // blocks per wave (2 x 2 waves)
+    constexpr int NKG = 2 * DIN;                                 // 8-edge groups of the reduction
+    constexpr int NKS = (NKG + 3) / 4;                           // 32-steps
+    constexpr int ARR = NKG * 256;                               // bytes per (split, block) array
+    constexpr int NPL = (kNE * DIN * DIN / 4 + kThreads - 1) / kThreads;
+    constexpr int NQL = (kNE * DOUT * DOUT / 4 + kThreads - 1) / kThreads;
+    static_assert(RB % 2 == 0 && CB % 2 == 0 && 4 * CIN <= kThreads && 4 * COUT <= kThreads,
+                  "unsupported channel counts");
+    static_assert(4 * (kNE * PS + kNE * QS) <= 2 * RB * ARR, "P and Q must fit the U buffer");
+
+    extern __shared__ float4 smem4[];
+    char* sF = reinterpret_cast<char*>(smem4);                   // fs fragments [2][CB][NKG][16][16 B]
+    char* sU = sF + 2 * CB * ARR;                                // U_k fragments [2][RB][NKG][16][16 B]
+    float* sP = reinterpret_cast<float*>(sU);                    // P, Q of the tile (producer phase only)
+    float* sQ = sP + kNE * PS;
+    float* sFe = reinterpret_cast<float*>(sU + 2 * RB * ARR);
+    float* sInvF = sFe + kNE * KWS;                              // 1 / scale of fs column ci
+    float* sInvU = sInvF + CIN;                                  // 1 / scale of U_k row co
+    EdgeState* sE = reinterpret_cast<EdgeState*>(sInvU + COUT);
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int le = lane & 15, lg = lane >> 4;
+    const int wr = wave >> 1, wc = wave & 1;
+    const int pc = tid >> 2, pq = tid & 3;                        // producer: channel, edge quad
+
+    v4f acc_tot[K][WR][WC];
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int a = 0; a < WR; ++a)
+#pragma unroll
+            for (int b = 0; b < WC; ++b) acc_tot[k][a][b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const int64_t e0 = tile * kNE;
+        // global loads: four edges' rows of one input channel / one output channel
+        float xr[4][DIN], gr[4][DOUT];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int64_t e = e0 + 4 * pq + q;
+            const bool ok = e < E;
+#pragma unroll
+            for (int d = 0; d < DIN; ++d) xr[q][d] = (ok && pc < CIN) ? x[(e * CIN + pc) * DIN + d] : 0.0f;
+#pragma unroll
+            for (int d = 0; d < DOUT; ++d) gr[q][d] = (ok && pc < COUT) ? gy[(e * COUT + pc) * DOUT + d] : 0.0f;
+        }
+        float4 pr[NPL], qr[NQL];
+        load_tile4<DIN * DIN, NPL>(P, e0, E, pr);
+        load_tile4<DOUT * DOUT, NQL>(Q, e0, E, qr);
+        const float rd = (tid < kNE && e0 + tid < E) ? dist[e0 + tid] : 1.0f;
+
+        __syncthreads();   // the previous tile's readers of every LDS buffer are done
+        store_tile4<DIN * DIN, NPL, PS>(pr, sP);
+        store_tile4<DOUT * DOUT, NQL, QS>(qr, sQ);
+        if (tid < kNE) {
+            EdgeState es;
+            es.valid = e0 + tid < E;
+            const EdgeBin eb = edge_bin(rd, B);
+            es.lo = eb.lo;
+            es.t = eb.t;
+            es.s = rd / (rd + B.sh_scale);
+            sE[tid] = es;
+        }
+        const bool dense =
+            __syncthreads_or(off_block_nonzero<LIN>(pr) | off_block_nonzero<LOUT>(qr)) != 0;
+
+        for (int q = tid; q < kNE * KW; q += kThreads) {
+            const int e = q / KW, rest = q % KW;
+            const EdgeState es = sE[e];
+            const float* flo = F + static_cast<int64_t>(es.lo) * KW + rest;
+            sFe[e * KWS + rest] = lerp_bins(flo[0], flo[KW], es.t);
+        }
+        // fs (input channel pc of edges 4 pq .. 4 pq + 3) and gd (output channel pc)
+        float gd[4][DOUT];
+        {
+            float fs[4][DIN];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int e = 4 * pq + q;
+                float pi[DIN], po[DOUT], t1[1][DIN], t2[1][DOUT];
+                slot_pow<LIN>(sE[e].s, pi);
+                slot_pow<LOUT>(sE[e].s, po);
+                if (dense) {
+                    rotate_cols<LIN, false, 1>(xr[q], sP + e * PS, t1);
+                    rotate_cols<LOUT, false, 1>(gr[q], sQ + e * QS, t2);
+                } else {
+                    rotate_cols<LIN, true, 1>(xr[q], sP + e * PS, t1);
+                    rotate_cols<LOUT, true, 1>(gr[q], sQ + e * QS, t2);
+                }
+#pragma unroll
+                for (int i = 0; i < DIN; ++i) fs[q][i] = t1[0][i] * pi[i];
+#pragma unroll
+                for (int o = 0; o < DOUT; ++o) gd[q][o] = t2[0][o] * po[o];
+            }
+            float m = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int i = 0; i < DIN; ++i) m = fmaxf(m, fabsf(fs[q][i]));
+            m = fmaxf(m, __shfl_xor(m, 1, 64));
+            m = fmaxf(m, __shfl_xor(m, 2, 64));
+            const int ex = scale_exp(m);
+            const float sc = exp2i(ex);
+            if (pc < CIN) {
+                if (pq == 0) sInvF[pc] = exp2i(-ex);
+                char* arr = sF + (pc / 16) * ARR;
+#pragma unroll
+                for (int i = 0; i < DIN; ++i) {
+                    h4 hv, lv;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        _Float16 h, l;
+                        split_f16(fs[q][i] * sc, h, l);
+                        hv[q] = h;
+                        lv[q] = l;
+                    }
+                    const int off = ((2 * i + (pq >> 1)) * 16 + pc % 16) * 16 + 8 * (pq & 1);
+                    *reinterpret_cast<h4*>(arr + off) = hv;
+                    *reinterpret_cast<h4*>(arr + CB * ARR + off) = lv;
+                }
+            }
+        }
+        __syncthreads();   // fs fragments complete; P and Q no longer read
+
+        const int nbase = lane;   // fragment reads: lane (g, n) at 16-byte slot 16 g + n of an 8-edge group row
+        static_for<K>([&](auto KK) {
+            constexpr int k = decltype(KK)::value;
+            // U_k row pc of edges 4 pq .. 4 pq + 3, scaled per row, to fragments
+            if (pc < COUT) {
+                float u[4][DIN];
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int i = 0; i < DIN; ++i) u[q][i] = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float* fe = sFe + (4 * pq + q) * KWS + k * WD;
+#pragma unroll
+                    for (int t = 0; t < T::NT; ++t) {
+                        const Term tm = T::terms[t];
+                        const float c = tm.neg ? -fe[tm.w] : fe[tm.w];
+                        u[q][tm.i] += c * gd[q][tm.o];
+                    }
+                }
+                float m = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int i = 0; i < DIN; ++i) m = fmaxf(m, fabsf(u[q][i]));
+                m = fmaxf(m, __shfl_xor(m, 1, 64));
+                m = fmaxf(m, __shfl_xor(m, 2, 64));
+                const int ex = scale_exp(m);
+                const float sc = exp2i(ex);
+                if (pq == 0) sInvU[pc] = exp2i(-ex);
+                char* arr = sU + (pc / 16) * ARR;
+#pragma unroll
+                for (int i = 0; i < DIN; ++i) {
+                    h4 hv, lv;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        _Float16 h, l;
+                        split_f16(u[q][i] * sc, h, l);
+                        hv[q] = h;
+                        lv[q] = l;
+                    }
+                    const int off = ((2 * i + (pq >> 1)) * 16 + pc % 16) * 16 + 8 * (pq & 1);
+                    *reinterpret_cast<h4*>(arr + off) = hv;
+                    *reinterpret_cast<h4*>(arr + RB * ARR + off) = lv;
+                }
+            }
+            __syncthreads();   // U_k fragments and row scales complete
+
+            v4f acc[WR][WC];
+#pragma unroll
+            for (int a = 0; a < WR; ++a)
+#pragma unroll
+                for (int b = 0; b < WC; ++b) acc[a][b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                const int kg = 4 * ks + lg;
+                const bool live = kg < NKG;   // the last step's upper lane groups pad with zeros
+                h8 ah[WR], al[WR], bh[WC], bl[WC];
+                const h8 z = h8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+                for (int a = 0; a < WR; ++a) {
+                    const char* arr = sU + (WR * wr + a) * ARR + (16 * ks * 4 + nbase) * 16;
+                    ah[a] = live ? *reinterpret_cast<const h8*>(arr) : z;
+                    al[a] = live ? *reinterpret_cast<const h8*>(arr + RB * ARR) : z;
+                }
+#pragma unroll
+                for (int b = 0; b < WC; ++b) {
+                    const char* arr = sF + (WC * wc + b) * ARR + (16 * ks * 4 + nbase) * 16;
+                    bh[b] = live ? *reinterpret_cast<const h8*>(arr) : z;
+                    bl[b] = live ? *reinterpret_cast<const h8*>(arr + CB * ARR) : z;
+                }
+#pragma unroll
+                for (int a = 0; a < WR; ++a)
+#pragma unroll
+                    for (int b = 0; b < WC; ++b) {
+                        acc[a][b] = mfma_h(al[a], bh[b], acc[a][b]);
+                        acc[a][b] = mfma_h(ah[a], bl[b], acc[a][b]);
+                        acc[a][b] = mfma_h(ah[a], bh[b], acc[a][b]);
+                    }
+            }
+            // unscale row (co) by column (ci) into the launch accumulator
+#pragma unroll
+            for (int a = 0; a < WR; ++a) {
+                float ru[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ru[r] = sInvU[16 * (WR * wr + a) + 4 * lg + r];
+#pragma unroll
+                for (int b = 0; b < WC; ++b) {
+                    const float cf = sInvF[16 * (WC * wc + b) + le];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc_tot[k][a][b][r] += acc[a][b][r] * (ru[r] * cf);
+                }
+            }
+            if constexpr (k + 1 < K) __syncthreads();   // before the next U_k overwrites the buffer
+        });
+    }
+    float* part = dC_part + static_cast<int64_t>(blockIdx.x) * K * COUT * CIN;
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int a = 0; a < WR; ++a)
+#pragma unroll
+            for (int b = 0; b < WC; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    part[(k * COUT + 16 * (WR * wr + a) + 4 * lg + r) * CIN + 16 * (WC * wc + b) + le] =
+                        acc_tot[k][a][b][r];
+}
+
+template <int CIN, int COUT, int LIN, int LOUT, int K>
+constexpr size_t ews_bwd_c_lds() {
+    using T = Canon<LIN, LOUT>;
+    constexpr size_t ARR = 2 * T::DIN * 256, KWS = K * T::WD | 1;
+    return 2 * (CIN / 16) * ARR + 2 * (COUT / 16) * ARR + 4 * (kNE * KWS + CIN + COUT) +
+           kNE * sizeof(EdgeState);
+}
+
+template <int CIN, int COUT, int LIN, int LOUT, int K>
+constexpr size_t ews_bwd_x_lds() {
+    using T = Canon<LIN, LOUT>;
+    constexpr size_t PS = T::DIN * T::DIN | 1, QS = T::DOUT * T::DOUT | 1;
+    constexpr size_t KW = K * T::WD, KWS = KW | 1;
+    constexpr size_t FR = 2 * T::DOUT * (COUT / 32) * 1024, ST = 4 * kNE * stage_stride(CIN * T::DIN);
+    return (FR > ST ? FR : ST) +
+           4 * (kNE * PS + kNE * QS + kNE * KWS + 4 * kNE * KW + kNE * T::DIN + kNE + K) +
+           kNE * sizeof(EdgeState);
 }
 
 template <int CIN, int COUT, int LIN, int LOUT, int K>
 constexpr size_t ews_fwd_lds() {
     using T = Canon<LIN, LOUT>;
-    constexpr size_t PS = (T::DIN * T::DIN + 3) / 4 * 4, QS = (T::DOUT * T::DOUT + 3) / 4 * 4;
-    return 2 * T::DIN * (CIN / 32) * 1024 +
-           4 * (kNE * PS + kNE * QS + kNE * K * T::WD + kNE * T::DOUT + K) +
+    constexpr size_t PS = T::DIN * T::DIN | 1, QS = T::DOUT * T::DOUT | 1, KWS = K * T::WD | 1;
+    constexpr size_t FR = 2 * T::DIN * (CIN / 32) * 1024, ST = 4 * kNE * stage_stride(COUT * T::DOUT);
+    return (FR > ST ? FR : ST) + 4 * (kNE * PS + kNE * QS + kNE * KWS + kNE * T::DOUT + K) +
            kNE * sizeof(EdgeState);
+}
+
+// Workgroups per CU of the forward: as many as the 160 KB of LDS allow, at most 3.
+template <int CIN, int COUT, int LIN, int LOUT, int K>
+constexpr int ews_fwd_occ() {
+    constexpr size_t lds = ews_fwd_lds<CIN, COUT, LIN, LOUT, K>();
+    return lds * 3 <= 160 * 1024 ? 3 : 2;
 }
 
 int ews_cus() {
@@ -499,6 +1289,7 @@ int launch_ews_fwd(const feq_binning& B, int64_t E, const float* x, const float*
                    const float* dist, const float* C, const float* F, float* y, void* ws,
                    size_t ws_bytes, hipStream_t s) {
     constexpr size_t lds = ews_fwd_lds<CIN, COUT, LIN, LOUT, K>();
+    constexpr int occ = ews_fwd_occ<CIN, COUT, LIN, LOUT, K>();
     static_assert(lds <= 80 * 1024, "two forward workgroups must fit one CU's LDS");
     if (!ws || ws_bytes < ews_cfrag_bytes<CIN, COUT, K>())
         return fail(FEQ_ERR_WORKSPACE, "edgewise forward workspace too small");
@@ -507,14 +1298,62 @@ int launch_ews_fwd(const feq_binning& B, int64_t E, const float* x, const float*
     float* inv = cv.take<float>(K);
     auto prep = k_ews_prep<K, COUT, CIN, false>;
     FEQ_LAUNCH("k_ews_prep", prep, dim3(K * COUT / 16), dim3(kThreads), 0, s, C, frag, inv);
-    auto kern = k_ews_fwd<CIN, COUT, LIN, LOUT, K>;
+    auto kern = k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ>;
     if (int rc = ews_set_lds(reinterpret_cast<const void*>(kern), lds)) return rc;
     const int64_t ntiles = ceil_div(E, kNE);
-    const int64_t g = static_cast<int64_t>(ews_cus()) * 2;
+    const int64_t g = static_cast<int64_t>(ews_cus()) * occ;
     const int grid = static_cast<int>(ntiles < g ? ntiles : g);
     FEQ_LAUNCH("k_ews_fwd", kern, dim3(grid), dim3(kThreads), lds, s, B, E, ntiles, x, P, Q, dist,
                frag, inv, F, y);
     return FEQ_OK;
+}
+
+// Workspace of the split backward: dF_e (E, K Wdim), the per-workgroup dC
+// partials, the tail's histogram partials and sums, the C^T fragments.
+template <int CIN, int COUT, int LIN, int LOUT, int K>
+size_t ews_bwd_ws(const feq_binning& B, int64_t E) {
+    using T = Canon<LIN, LOUT>;
+    const int64_t ntiles = ceil_div(E, kNE), g = static_cast<int64_t>(ews_cus()) * 2;
+    const int G = static_cast<int>(ntiles < g ? ntiles : g);
+    const int64_t kw = static_cast<int64_t>(K) * T::WD, ncc = static_cast<int64_t>(K) * COUT * CIN;
+    return align_up(4 * E * kw, 256) + align_up(4 * static_cast<size_t>(G) * ncc, 256) +
+           align_up(4 * ew_tail_floats(B, static_cast<int>(kw), E, G, ncc), 256) +
+           ews_cfrag_bytes<CIN, COUT, K>() + 1024;
+}
+
+template <int CIN, int COUT, int LIN, int LOUT, int K>
+int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const float* gy,
+                   const float* x, const float* P, const float* Q, const float* dist,
+                   const float* C, const float* F, float* gx, float* gC, float* gF, float* gdist,
+                   void* ws, size_t ws_bytes, hipStream_t s) {
+    using T = Canon<LIN, LOUT>;
+    constexpr size_t xlds = ews_bwd_x_lds<CIN, COUT, LIN, LOUT, K>();
+    constexpr size_t clds = ews_bwd_c_lds<CIN, COUT, LIN, LOUT, K>();
+    static_assert(xlds <= 80 * 1024, "two input-gradient workgroups must fit one CU's LDS");
+    static_assert(clds <= 80 * 1024, "two channel-gradient workgroups must fit one CU's LDS");
+    const int kw = K * T::WD;
+    if (!ew_tail_supported(B, kw)) return -1;
+    const int64_t ntiles = ceil_div(E, kNE), g = static_cast<int64_t>(ews_cus()) * 2;
+    const int G = static_cast<int>(ntiles < g ? ntiles : g);
+    const int64_t ncc = static_cast<int64_t>(K) * COUT * CIN;
+    Carver cv(ws);
+    float* dFe = cv.take<float>(E * kw);
+    float* dCp = cv.take<float>(static_cast<size_t>(G) * ncc);
+    float* tail = cv.take<float>(ew_tail_floats(B, kw, E, G, ncc));
+    h8* frag = cv.take<h8>(static_cast<size_t>(K) * COUT * CIN / 4);
+    float* inv = cv.take<float>(K);
+    if (!ws || cv.used > ws_bytes) return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
+    auto prep = k_ews_prep<K, CIN, COUT, true>;
+    FEQ_LAUNCH("k_ews_prep", prep, dim3(K * CIN / 16), dim3(kThreads), 0, s, C, frag, inv);
+    auto kx = k_ews_bwd_x<CIN, COUT, LIN, LOUT, K>;
+    if (int rc = ews_set_lds(reinterpret_cast<const void*>(kx), xlds)) return rc;
+    FEQ_LAUNCH("k_ews_bwd_x", kx, dim3(G), dim3(kThreads), xlds, s, B, E, ntiles, gy, x, P, Q,
+               dist, frag, inv, F, gx, dFe);
+    auto kc = k_ews_bwd_c<CIN, COUT, LIN, LOUT, K>;
+    if (int rc = ews_set_lds(reinterpret_cast<const void*>(kc), clds)) return rc;
+    FEQ_LAUNCH("k_ews_bwd_c", kc, dim3(G), dim3(kThreads), clds, s, B, E, ntiles, gy, x, P, Q,
+               dist, F, dCp);
+    return ew_tail(L, B, K, E, dist, F, dFe, dCp, G, ncc, gC, gF, gdist, tail, s);
 }
 
 // The layout is the canonical (0..lin) x (0..lout) pair of the instantiation.
@@ -554,6 +1393,36 @@ size_t ew_split_workspace(const feq_layout& L, int rank) {
 
 // The split kernels read and write x, P, Q and y with 16-byte accesses.
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+size_t ew_split_bwd_workspace(const feq_layout& L, const feq_binning& B, int rank, int64_t E) {
+    if (rank != 4) return 0;
+#define FEQ_WS(ci, co, li, lo)                                                                 \
+    if constexpr ((ci) % 64 == 0) {                                                            \
+        if (L.cin == ci && L.cout == co && canonical(L, li, lo))                               \
+            return ews_bwd_ws<ci, co, li, lo, 4>(B, E);                                        \
+    }
+    FEQ_EWS_SHAPES(FEQ_WS)
+#undef FEQ_WS
+    return 0;
+}
+
+int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* gy,
+                 const float* x, const float* P, const float* Q, const float* dist, const float* C,
+                 const float* F, float* gx, float* gC, float* gF, float* gdist, void* ws,
+                 size_t ws_bytes, hipStream_t s) {
+    if (rank != 4 || !gx || !aligned16(gy) || !aligned16(x) || !aligned16(P) || !aligned16(Q) ||
+        !aligned16(gx))
+        return -1;
+#define FEQ_BWD(ci, co, li, lo)                                                                \
+    if constexpr ((ci) % 64 == 0) {                                                            \
+        if (L.cin == ci && L.cout == co && canonical(L, li, lo))                               \
+            return launch_ews_bwd<ci, co, li, lo, 4>(L, B, E, gy, x, P, Q, dist, C, F, gx, gC, \
+                                                     gF, gdist, ws, ws_bytes, s);              \
+    }
+    FEQ_EWS_SHAPES(FEQ_BWD)
+#undef FEQ_BWD
+    return -1;
+}
 
 int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
                  const float* P, const float* Q, const float* dist, const float* C, const float* F,

@@ -89,6 +89,41 @@ struct SlotL {
     static constexpr std::array<int, (L + 1) * (L + 1)> l = make();
 };
 
+// Degree-block structure of a Wigner-D basis matrix of a canonical
+// representation (lvals = 0..L): row d is in the standard (l, m) order,
+// column j in the m-first order, and the entry can be non-zero only when
+// deg(d) == SlotL<L>::l[j] (the matrix is block diagonal over irreps).
+template <int L>
+struct DegreeBlocks {
+    static constexpr int D = (L + 1) * (L + 1);
+    static constexpr int NW = (D * D + 31) / 32;
+    static constexpr int deg(int d) {
+        int l = 0;
+        while ((l + 1) * (l + 1) <= d) ++l;
+        return l;
+    }
+    // m-first slots of degree l: slots[l * l .. (l + 1) * (l + 1))
+    static constexpr std::array<int, D> make_slots() {
+        std::array<int, D> v{};
+        std::array<int, L + 1> fill{};
+        for (int j = 0; j < D; ++j) {
+            const int l = SlotL<L>::l[j];
+            v[l * l + fill[l]++] = j;
+        }
+        return v;
+    }
+    static constexpr std::array<int, D> slots = make_slots();
+    // bit (d D + j) set where the entry lies outside the blocks
+    static constexpr std::array<unsigned, NW> make_offmask() {
+        std::array<unsigned, NW> m{};
+        for (int d = 0; d < D; ++d)
+            for (int j = 0; j < D; ++j)
+                if (deg(d) != SlotL<L>::l[j]) m[(d * D + j) / 32] |= 1u << ((d * D + j) % 32);
+        return m;
+    }
+    static constexpr std::array<unsigned, NW> offmask = make_offmask();
+};
+
 // Compile-time loop: f(std::integral_constant<int, 0>{}), ..., up to N - 1.
 template <class Fn, int... Is>
 __device__ __forceinline__ void static_for_impl(Fn&& f, std::integer_sequence<int, Is...>) {
@@ -123,6 +158,17 @@ struct TermGroups {
     }
     static constexpr std::array<Term, T::NT> sorted = make_sorted();
     static constexpr int count(int s) { return start[s + 1] - start[s]; }
+    // last group (in increasing group order) that uses radial weight w
+    static constexpr std::array<int, T::WD> make_last() {
+        std::array<int, T::WD> l{};
+        for (int w = 0; w < T::WD; ++w) l[w] = -1;
+        for (int t = 0; t < T::NT; ++t) {
+            const int s = BY_OUT ? T::terms[t].o : T::terms[t].i;
+            if (s > l[T::terms[t].w]) l[T::terms[t].w] = s;
+        }
+        return l;
+    }
+    static constexpr std::array<int, T::WD> last = make_last();
 };
 
 }  // namespace

@@ -79,8 +79,23 @@ int ew_mfma_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, 
                 const float* F, float* gx, float* gC, float* gF, float* gdist, void* ws,
                 size_t ws_bytes, hipStream_t s);
 
+// Tail shared by the fused backward families (edgewise_tail.hip): binned
+// radial-function gradient from dF_e (E, K wdim), distance gradient (gdist may
+// be NULL), and the sums of `groups` channel-pattern partials of ncc floats.
+// `tail` holds ew_tail_floats(...) floats of workspace.
+bool ew_tail_supported(const feq_binning& B, int kw);
+size_t ew_tail_floats(const feq_binning& B, int kw, int64_t E, int groups, int64_t ncc);
+int ew_tail(const feq_layout& L, const feq_binning& B, int K, int64_t E, const float* dist,
+            const float* F, const float* dFe, const float* dCp, int groups, int64_t ncc, float* gC,
+            float* gF, float* gdist, float* tail, hipStream_t s);
+
 // Split-fp16 fast paths (edgewise_split.hip); -1 when the shape has none.
 size_t ew_split_workspace(const feq_layout& L, int rank);
+size_t ew_split_bwd_workspace(const feq_layout& L, const feq_binning& B, int rank, int64_t E);
+int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* gy,
+                 const float* x, const float* P, const float* Q, const float* dist, const float* C,
+                 const float* F, float* gx, float* gC, float* gF, float* gdist, void* ws,
+                 size_t ws_bytes, hipStream_t s);
 int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
                  const float* P, const float* Q, const float* dist, const float* C, const float* F,
                  float* y, void* ws, size_t ws_bytes, hipStream_t s);

@@ -138,16 +138,48 @@ def test_split_path_is_dispatched(dev, monkeypatch, lin, lout, cin, cout, E):
     g = torch.Generator().manual_seed(11)
     d = torch.randn(E, 3, generator=g).to(dev)
     P, Q = fe.WignerDBasis([fe.Repr(lin, 1), fe.Repr(lout, 1)]).to(dev)(d)
-    x = torch.randn(E, cin, P.shape[-1], generator=g).to(dev)
+    x = torch.randn(E, cin, P.shape[-1], generator=g).to(dev).requires_grad_(True)
     r = (torch.rand(E, generator=g) * 9).to(dev)
     torch.cuda.synchronize()
     NAT.profile_summary()
     NAT.profile_enable(True)
-    layer(P, Q, x, r)
+    y = layer(P, Q, x, r)
+    y.backward(torch.ones_like(y))
     torch.cuda.synchronize()
     NAT.profile_enable(False)
     names = NAT.profile_summary()
     assert "k_ews_fwd" in names and "k_ews_prep" in names, names
+    if cin % 64 == 0:
+        assert "k_ews_bwd_x" in names and "k_ews_bwd_c" in names, names
+
+
+@pytest.mark.parametrize("lin,lout,cin,cout", [([0, 1, 2], [0, 1, 2], 64, 64), ([0, 1], [0, 1, 2], 32, 64)])
+def test_edgewise_parity_general_basis(dev, lin, lout, cin, cout):
+    """P and Q need not be Wigner-D matrices: tiles whose matrices have entries off
+    the degree blocks take the dense rotations, the others the block-sparse ones."""
+    torch.manual_seed(12)
+    layer = fe.EquivariantEdgewiseLinear(fe.Repr(lin, cin), fe.Repr(lout, cout), num_bins=50)
+    E = 100
+    x, d, r, g = _inputs(lin, lout, E, cin, 12)
+    P = OW.basis(lin, d).float()
+    Q = OW.basis(lout, d).float()
+    gen = torch.Generator().manual_seed(13)
+    for lo, hi in ((16, 32), (70, 71)):          # one full dense tile, one tile with a single edge
+        P[lo:hi] = torch.randn(hi - lo, *P.shape[1:], generator=gen) * 0.4
+        Q[lo:hi] = torch.randn(hi - lo, *Q.shape[1:], generator=gen) * 0.4
+    layer = layer.to(dev)
+    xg = x.to(dev).requires_grad_(True)
+    y = layer(P.to(dev), Q.to(dev), xg, r.to(dev))
+    params, cfg = OL.module_cfg(layer)
+    xd = x.double().requires_grad_(True)
+    yref = OL.edgewise_linear(xd, P.double(), Q.double(), r.double(), params, cfg)
+    assert rel_err(y, yref) < TOL, rel_err(y, yref)
+    gy = torch.randn(y.shape, generator=g)
+    y.backward(gy.to(dev))
+    yref.backward(gy.double())
+    assert rel_err(xg.grad, xd.grad) < TOL
+    for name, p in layer.radial_weights.named_parameters():
+        assert rel_err(p.grad, params[name].grad) < TOL, name
 
 
 def test_edgewise_parity_log_bins(dev):
