@@ -5,8 +5,10 @@ EquivariantEdgewiseLinear with in = out = Repr([0,1,2], mult=64), fp32;
 N = 10,000 nodes uniform in a 40^3 cube, k = 16 nearest neighbours
 (E = 160,000 edges, src = neighbour -> dst = centre), distances clipped to
 max_dist = 10, num_bins = 100.  Node features (N, 64, 9) ~ N(0,1) are gathered
-to edges by src.  One step = gather + layer forward + (out**2).sum() +
-backward into the node features and every layer parameter.  P = Q come from
+to edges by src (Graph.gather_src: its backward is a segmented sum over the
+edges grouped by source).  One step = gather + layer forward + the
+sum-of-squares loss sum(out**2) + backward into the node features and every
+layer parameter.  P = Q come from
 WignerDBasis outside the timed region (as in the reference's benchmark,
 benchmarks/compare_all.py:168).
 
@@ -103,6 +105,23 @@ def read_traffic(path: str = TRAFFIC_FILE) -> dict:
     return out
 
 
+class SumOfSquares(torch.autograd.Function):
+    """The sum-of-squares loss sum(y**2): one read of y forward (a dot product),
+    and its gradient 2 y in one fused pass (PyTorch's generic y**2 backward takes
+    three passes over y plus a copy)."""
+
+    @staticmethod
+    def forward(ctx, y):
+        ctx.save_for_backward(y)
+        v = y.reshape(-1)
+        return torch.dot(v, v)
+
+    @staticmethod
+    def backward(ctx, g):
+        (y,) = ctx.saved_tensors
+        return y * (2.0 * g)
+
+
 def cpu_baseline(layer, feats, src, dst, coords, sample_edges: int, reps: int):
     """Float32 CPU oracle (bin-grouped BLAS restatement) fwd+bwd on the first edges."""
     from oracle import layer as OL
@@ -176,9 +195,12 @@ def main() -> int:
     if args.grad_dist:
         dist.requires_grad_(True)
 
+    graph = fe.Graph(src_d, dst_d, N)
+    graph.csr_src()                            # CSR by source, built once per graph
+
     def step():
-        y = layer(P, P, feats[src_d], dist)
-        (y ** 2).sum().backward()
+        y = layer(P, P, graph.gather_src(feats), dist)
+        SumOfSquares.apply(y).backward()
 
     for _ in range(args.warmup):
         step()

@@ -529,41 +529,44 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
                         ahi[j][kk][ks] = src[0];
                         alo[j][kk][ks] = src[1];
                     }
-            // B fragments double-buffered one slot ahead; the fence at the end
-            // of each slot keeps the compiler from hoisting every slot's loads
+            // Software pipeline over the slots: iteration i issues the MFMAs of
+            // slot i + 1 (B fragments loaded one iteration earlier) and the
+            // fragment loads of slot i + 2, then contracts slot i, so matrix and
+            // vector work of one wave overlap.  The fence at the end of each
+            // iteration keeps the compiler from hoisting later slots' loads.
             h8 bh[2][NKS], bl[2][NKS];
+            v4f acc[2][RPW][KP];
+            auto load_b = [&](int slot, int buf) {
 #pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) {
-                bh[0][ks] = *reinterpret_cast<const h8*>(sB + ks * CHUNK + myslot);
-                bl[0][ks] = *reinterpret_cast<const h8*>(sB + (DIN * NKS + ks) * CHUNK + myslot);
-            }
-            static_for<DIN>([&](auto I) {
-                constexpr int i = decltype(I)::value;
-                constexpr int cur = i & 1;
-                if constexpr (i + 1 < DIN) {
-#pragma unroll
-                    for (int ks = 0; ks < NKS; ++ks) {
-                        bh[cur ^ 1][ks] =
-                            *reinterpret_cast<const h8*>(sB + ((i + 1) * NKS + ks) * CHUNK + myslot);
-                        bl[cur ^ 1][ks] =
-                            *reinterpret_cast<const h8*>(sB + ((DIN + i + 1) * NKS + ks) * CHUNK + myslot);
-                    }
+                for (int ks = 0; ks < NKS; ++ks) {
+                    bh[buf][ks] = *reinterpret_cast<const h8*>(sB + (slot * NKS + ks) * CHUNK + myslot);
+                    bl[buf][ks] = *reinterpret_cast<const h8*>(sB + ((DIN + slot) * NKS + ks) * CHUNK + myslot);
                 }
-                v4f acc[RPW][KP];
+            };
+            auto mfma_slot = [&](int buf, int ab) {
 #pragma unroll
                 for (int j = 0; j < RPW; ++j)
 #pragma unroll
-                    for (int kk = 0; kk < KP; ++kk) acc[j][kk] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                    for (int kk = 0; kk < KP; ++kk) acc[ab][j][kk] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
                     for (int j = 0; j < RPW; ++j)
 #pragma unroll
                         for (int kk = 0; kk < KP; ++kk) {
-                            acc[j][kk] = mfma_h(alo[j][kk][ks], bh[cur][ks], acc[j][kk]);
-                            acc[j][kk] = mfma_h(ahi[j][kk][ks], bl[cur][ks], acc[j][kk]);
-                            acc[j][kk] = mfma_h(ahi[j][kk][ks], bh[cur][ks], acc[j][kk]);
+                            acc[ab][j][kk] = mfma_h(alo[j][kk][ks], bh[buf][ks], acc[ab][j][kk]);
+                            acc[ab][j][kk] = mfma_h(ahi[j][kk][ks], bl[buf][ks], acc[ab][j][kk]);
+                            acc[ab][j][kk] = mfma_h(ahi[j][kk][ks], bh[buf][ks], acc[ab][j][kk]);
                         }
+            };
+            load_b(0, 0);
+            if constexpr (DIN > 1) load_b(1, 1);
+            mfma_slot(0, 0);
+            static_for<DIN>([&](auto I) {
+                constexpr int i = decltype(I)::value;
+                constexpr int cur = i & 1;
+                if constexpr (i + 1 < DIN) mfma_slot(cur ^ 1, cur ^ 1);
+                if constexpr (i + 2 < DIN) load_b(i + 2, cur);
                 static_for<TG::count(i)>([&](auto TT) {
                     constexpr Term tm = TG::sorted[TG::start[i] + decltype(TT)::value];
 #pragma unroll
@@ -573,10 +576,10 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
 #pragma unroll
                         for (int j = 0; j < RPW; ++j)
 #pragma unroll
-                            for (int r = 0; r < 4; ++r) yv[j][tm.o][r] += c * acc[j][kk][r];
+                            for (int r = 0; r < 4; ++r) yv[j][tm.o][r] += c * acc[cur][j][kk][r];
                     }
                 });
-                // Pin the contraction to this slot: without these (empty)
+                // Pin the contraction to this iteration: without these (empty)
                 // read-modify-write uses the compiler defers it past later
                 // slots' MFMAs and keeps their results live.
 #pragma unroll

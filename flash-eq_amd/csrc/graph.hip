@@ -48,6 +48,36 @@ k_segment_sum(const float* __restrict__ x, int64_t row, const int32_t* __restric
     }
 }
 
+// 16-byte variants for rows of whole float4s (row4 = row / 4): one thread per
+// float4 of the output (gather) or per float4 column of a node (segment sum).
+__global__ void k_segment_sum4(const float4* __restrict__ x, int64_t row4,
+                               const int32_t* __restrict__ perm, const int32_t* __restrict__ offsets,
+                               float4* __restrict__ out) {
+    const int64_t n = blockIdx.y;
+    const int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (c >= row4) return;
+    const int b = offsets[n], e_end = offsets[n + 1];
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int i = b; i < e_end; ++i) {
+        const float4 v = x[static_cast<int64_t>(perm[i]) * row4 + c];
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+    }
+    out[n * row4 + c] = acc;
+}
+
+__global__ void k_gather_rows4(const float4* __restrict__ src, int64_t row4,
+                               const int64_t* __restrict__ idx, int64_t nrows, int64_t nsrc,
+                               float4* __restrict__ out) {
+    const int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (q >= nrows * row4) return;
+    const int64_t r = q / row4, c = q % row4;
+    const int64_t s = idx[r];
+    out[q] = (s >= 0 && s < nsrc) ? src[s * row4 + c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+
 __global__ void k_gather_rows(const float* __restrict__ src, int64_t row,
                               const int64_t* __restrict__ idx, int64_t nrows, int64_t nsrc,
                               float* __restrict__ out) {
@@ -57,6 +87,8 @@ __global__ void k_gather_rows(const float* __restrict__ src, int64_t row,
     for (int64_t c = threadIdx.x; c < row; c += blockDim.x)
         out[r * row + c] = ok ? src[s * row + c] : 0.0f;
 }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Block-wide per-head reduction helper: red holds kThreads partial values laid
 // out as [thread]; thread t contributes to head t % H.  Returns the reduced
@@ -290,6 +322,14 @@ extern "C" int feq_segment_sum(const float* x, int64_t row, const int32_t* perm,
     if (row < 0 || N < 0) return fail(FEQ_ERR_INVALID, "invalid sizes");
     if (N == 0 || row == 0) return FEQ_OK;
     if (!offsets || !out) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (row % 4 == 0 && aligned16(x) && aligned16(out)) {
+        const int64_t row4 = row / 4;
+        const unsigned bx = static_cast<unsigned>(ceil_div(row4, 64));
+        FEQ_LAUNCH("k_segment_sum", k_segment_sum4, dim3(bx, static_cast<unsigned>(N)), dim3(64), 0,
+                   stream_of(stream), reinterpret_cast<const float4*>(x), row4, perm, offsets,
+                   reinterpret_cast<float4*>(out));
+        return FEQ_OK;
+    }
     FEQ_LAUNCH("k_segment_sum", k_segment_sum, dim3(N), dim3(kThreads), 0, stream_of(stream), x, row, perm,
                        offsets, out);
     return FEQ_OK;
@@ -300,6 +340,13 @@ extern "C" int feq_gather_rows(const float* src, int64_t nsrc, int64_t row, cons
     if (row < 0 || nrows < 0 || nsrc < 0) return fail(FEQ_ERR_INVALID, "invalid sizes");
     if (nrows == 0 || row == 0) return FEQ_OK;
     if (!src || !idx || !out) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (row % 4 == 0 && aligned16(src) && aligned16(out)) {
+        const int64_t n4 = nrows * (row / 4);
+        FEQ_LAUNCH("k_gather_rows", k_gather_rows4, dim3(static_cast<unsigned>(ceil_div(n4, kThreads))),
+                   dim3(kThreads), 0, stream_of(stream), reinterpret_cast<const float4*>(src), row / 4,
+                   idx, nrows, nsrc, reinterpret_cast<float4*>(out));
+        return FEQ_OK;
+    }
     FEQ_LAUNCH("k_gather_rows", k_gather_rows, dim3(nrows), dim3(row < 256 ? 64 : 256), 0,
                        stream_of(stream), src, row, idx, nrows, nsrc, out);
     return FEQ_OK;

@@ -1,9 +1,11 @@
 """COO graph container (drop-in for ``flash_eq/graph.py:15-97``).
 
-Adds one thing the reference does not have: ``Graph.csr()`` returns the edges
-grouped by destination (``perm``, ``offsets``), built once per device by the
-HIP radix sort and cached on the object, so every edge->node reduction of the
-layers walks contiguous segments instead of scattering with atomics.
+Adds what the reference does not have: ``Graph.csr()`` / ``csr_src()`` return
+the edges grouped by destination / source (``perm``, ``offsets``), built once
+per device by the HIP radix sort and cached on the object, so every edge->node
+reduction of the layers walks contiguous segments instead of scattering with
+atomics; ``gather_src`` / ``gather_dst`` are ``x[src]`` / ``x[dst]`` whose
+backward is such a segmented sum.
 """
 from __future__ import annotations
 
@@ -64,20 +66,40 @@ class Graph:
         ``perm[offsets[n]:offsets[n+1]]`` are the edges into node n in
         increasing edge id (stable).  Computed on the GPU and cached.
         """
-        N.require_cuda_tensor(self.dst, "graph.dst")
-        key = str(self.dst.device)
+        return self._csr_of(self.dst, "dst")
+
+    def csr_src(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        """The same grouping of the edges by source node (cached)."""
+        return self._csr_of(self.src, "src")
+
+    def gather_src(self, node_values: torch.Tensor) -> torch.Tensor:
+        """``node_values[src]`` (E, ...) whose backward sums every node's outgoing
+        edge rows over the cached CSR by source (no atomics, fixed order)."""
+        from .ops import gather_rows
+        perm, offsets = self.csr_src()
+        return gather_rows(node_values, self.src, perm, offsets)
+
+    def gather_dst(self, node_values: torch.Tensor) -> torch.Tensor:
+        """``node_values[dst]`` (E, ...), backward over the CSR by destination."""
+        from .ops import gather_rows
+        perm, offsets = self.csr()
+        return gather_rows(node_values, self.dst, perm, offsets)
+
+    def _csr_of(self, index: torch.Tensor, which: str) -> Tuple[torch.Tensor, torch.Tensor]:
+        N.require_cuda_tensor(index, f"graph.{which}")
+        key = f"{which}:{index.device}"
         hit = self._csr_cache.get(key)
         if hit is not None:
             return hit
-        dev = self.dst.device
+        dev = index.device
         E, Nn = self.num_edges, self.num_nodes
-        dst = self.dst.to(torch.int64).contiguous()
+        idx = index.to(torch.int64).contiguous()
         perm = torch.empty(E, dtype=torch.int32, device=dev)
         offsets = torch.empty(Nn + 1, dtype=torch.int32, device=dev)
         lib = N.lib()
         ws = N.workspace(lib.feq_csr_workspace(E, Nn), dev)
         with torch.cuda.device(dev):
-            rc = lib.feq_csr_by_dst(N.ptr(dst) if E else None, E, Nn, N.ptr(perm) if E else None,
+            rc = lib.feq_csr_by_dst(N.ptr(idx) if E else None, E, Nn, N.ptr(perm) if E else None,
                                     N.ptr(offsets), N.ptr(ws), ws.numel(), N.stream_ptr(dev))
         N.check(rc, "feq_csr_by_dst")
         self._csr_cache[key] = (perm, offsets)

@@ -102,9 +102,9 @@ class EquivariantAttention(nn.Module):
         E = graph.num_edges
         mult = self.in_repr.mult
         qk = self.linear_qk(self.norm_qk(node_features))            # (N, 2 mult, dim)
-        Qe = qk[:, :mult][graph.dst].view(E, self.num_heads, -1)
-        Ke = qk[:, mult:][graph.src].view(E, self.num_heads, -1)
-        gathered = node_features[graph.src]
+        Qe = graph.gather_dst(qk[:, :mult].contiguous()).view(E, self.num_heads, -1)
+        Ke = graph.gather_src(qk[:, mult:].contiguous()).view(E, self.num_heads, -1)
+        gathered = graph.gather_src(node_features)
         if edge_features is not None:
             gathered = gathered + edge_features
         V = self.linear_v(P, Q_basis, gathered, distances)           # (E, mult_out, dim_out)

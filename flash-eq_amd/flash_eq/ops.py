@@ -197,6 +197,46 @@ class SegmentSumFn(torch.autograd.Function):
         return gx.to(xdt), None, None, None, None
 
 
+class GatherRowsFn(torch.autograd.Function):
+    """out[e] = x[idx[e]]; the backward sums the rows of every node's edges over
+    the CSR grouping of ``idx`` (``perm``, ``offsets``), deterministically."""
+
+    @staticmethod
+    def forward(ctx, x, idx, perm, offsets):
+        dev = _same_device(x, idx, perm, offsets)
+        xs = _f32(x, "node_features")
+        num_src = xs.shape[0]
+        E = idx.shape[0]
+        row = int(torch.tensor(xs.shape[1:]).prod()) if xs.dim() > 1 else 1
+        out = torch.empty((E,) + tuple(xs.shape[1:]), dtype=torch.float32, device=dev)
+        i64 = idx.to(torch.int64).contiguous()
+        if E:
+            with torch.cuda.device(dev):
+                rc = N.lib().feq_gather_rows(N.ptr(xs), num_src, row, N.ptr(i64), E, N.ptr(out),
+                                             N.stream_ptr(dev))
+            N.check(rc, "feq_gather_rows")
+        ctx.save_for_backward(perm, offsets)
+        ctx.meta = (x.dtype, num_src, row, E, tuple(xs.shape))
+        return out.to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, gout):
+        perm, offsets = ctx.saved_tensors
+        xdt, num_src, row, E, shape = ctx.meta
+        dev = perm.device
+        g = gout.detach().to(torch.float32).contiguous()
+        gx = torch.empty(shape, dtype=torch.float32, device=dev)
+        with torch.cuda.device(dev):
+            rc = N.lib().feq_segment_sum(N.ptr(g) if E else None, row, N.ptr(perm) if E else None,
+                                         N.ptr(offsets), num_src, N.ptr(gx), N.stream_ptr(dev))
+        N.check(rc, "feq_segment_sum")
+        return gx.to(xdt), None, None, None
+
+
+def gather_rows(x, idx, perm, offsets) -> torch.Tensor:
+    return GatherRowsFn.apply(x, idx, perm, offsets)
+
+
 class EdgeSoftmaxFn(torch.autograd.Function):
     """Per-destination softmax of scale*<Q,K> (- r/decay) with +1e-8 (``attention.py:92-141``)."""
 
