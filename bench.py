@@ -122,15 +122,15 @@ def read_traffic(path: str = TRAFFIC_FILE) -> dict:
 
 
 class SumOfSquares(torch.autograd.Function):
-    """The sum-of-squares loss sum(y**2): one read of y forward (a dot product),
-    and its gradient 2 y in one fused pass (PyTorch's generic y**2 backward takes
-    three passes over y plus a copy)."""
+    """The sum-of-squares loss sum(y**2): one read of y forward (the squared
+    2-norm, a single reduction pass; measured faster than torch.dot(y, y) on
+    MI355X), and its gradient 2 y in one fused pass (PyTorch's generic y**2
+    backward takes three passes over y plus a copy)."""
 
     @staticmethod
     def forward(ctx, y):
         ctx.save_for_backward(y)
-        v = y.reshape(-1)
-        return torch.dot(v, v)
+        return torch.linalg.vector_norm(y.reshape(-1)) ** 2
 
     @staticmethod
     def backward(ctx, g):

@@ -33,46 +33,95 @@ __device__ void weight_lsum(const feq_layout& L, int* fl) {
     __syncthreads();
 }
 
-// Binned radial-function gradient of one edge chunk: dF[lo] += (1 - t) dF_e and
-// dF[lo + 1] += t dF_e.  Thread t serves the columns c = t % kw (+ kThreads
-// multiples when kw > kThreads) of edge stream t / kw; every stream keeps its
-// own LDS histogram, so each cell has one writer and a fixed summation order.
-// One partial histogram per workgroup.
+// Binned radial-function gradient: dF[lo] += (1 - t) dF_e and dF[lo + 1] += t dF_e.
+// Every wave owns a private LDS histogram and a contiguous run of edges, and
+// adds into it in edge order (plain read-add-write; LDS float atomics are
+// several times slower), so every cell's summation order is fixed and the
+// result is deterministic.  Lane c serves the columns c, c + 64, ... of an edge.  Edges
+// are taken in batches of kHistBatch whose loads are issued together, one batch
+// ahead.  One
+// partial histogram per workgroup (its waves' histograms summed in wave order).
+constexpr int kHistBatch = 16;
+
 __global__ void __launch_bounds__(kThreads)
-k_ewm_hist(feq_binning B, int kw, int streams, int64_t E, int64_t chunk,
-           const float* __restrict__ dist, const float* __restrict__ dFe,
-           float* __restrict__ hist_part) {
+k_ewm_hist(feq_binning B, int kw, int64_t E, int64_t per_wave, const float* __restrict__ dist,
+           const float* __restrict__ dFe, float* __restrict__ hist_part) {
     extern __shared__ float sh[];
+    const int waves = blockDim.x / 64;
     const int hsz = (B.num_bins + 1) * kw;
-    float* sT = sh + static_cast<int64_t>(streams) * hsz;
-    int* sLo = reinterpret_cast<int*>(sT + chunk);
-    for (int q = threadIdx.x; q < streams * hsz; q += kThreads) sh[q] = 0.0f;
-    const int64_t e_begin = blockIdx.x * chunk;
-    const int n = static_cast<int>(E - e_begin < chunk ? E - e_begin : chunk);
-    for (int q = threadIdx.x; q < n; q += kThreads) {
-        const EdgeBin eb = edge_bin(dist[e_begin + q], B);
-        sLo[q] = eb.lo;
-        sT[q] = eb.t;
-    }
+    for (int q = threadIdx.x; q < waves * hsz; q += blockDim.x) sh[q] = 0.0f;
     __syncthreads();
-    const int per = kw <= kThreads ? kw : kThreads;   // threads per stream
-    const int st = threadIdx.x / per;
-    if (st < streams) {
-        float* h = sh + static_cast<int64_t>(st) * hsz;
-        for (int c = threadIdx.x % per; c < kw; c += per)
-            for (int q = st; q < n; q += streams) {
-                const float v = dFe[(e_begin + q) * kw + c];
-                const int lo = sLo[q];
-                const float t = sT[q];
-                h[lo * kw + c] += (1.0f - t) * v;
-                h[(lo + 1) * kw + c] += t * v;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float* h = sh + static_cast<int64_t>(wave) * hsz;
+    const int64_t e_begin = (static_cast<int64_t>(blockIdx.x) * waves + wave) * per_wave;
+    const int64_t e_end = e_begin + per_wave < E ? e_begin + per_wave : E;
+    for (int c0 = 0; c0 < kw; c0 += 128) {
+        const int ca = c0 + lane, cb = c0 + 64 + lane;
+        const int la = ca < kw ? ca : kw - 1, lb = cb < kw ? cb : kw - 1;   // in-bounds loads
+        const bool ina = ca < kw, inb = cb < kw;
+        // Batch of kHistBatch edges from e: lane j < kHistBatch bins edge e + j;
+        // the loads are unconditional (rows past the run repeat its last edge and
+        // are not added).  The next batch's loads are issued before this one is
+        // added in.
+        struct Batch {
+            float va[kHistBatch], vb[kHistBatch];
+            EdgeBin eb;
+        };
+        auto load = [&](int64_t e, Batch& b) {
+            const int nb = static_cast<int>(e_end - e < kHistBatch ? e_end - e : kHistBatch);
+            const int jl = (lane % kHistBatch) < nb ? lane % kHistBatch : nb - 1;
+            b.eb = edge_bin(dist[e + jl], B);
+#pragma unroll
+            for (int j = 0; j < kHistBatch; ++j) {
+                const float* row = dFe + (e + (j < nb ? j : nb - 1)) * kw;
+                b.va[j] = row[la];
+                b.vb[j] = row[lb];
             }
+        };
+        auto add = [&](int64_t e, const Batch& b) {
+            const int nb = static_cast<int>(e_end - e < kHistBatch ? e_end - e : kHistBatch);
+#pragma unroll
+            for (int j = 0; j < kHistBatch; ++j) {
+                if (j < nb) {
+                    const int lo = __builtin_amdgcn_readlane(b.eb.lo, j);
+                    const float t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b.eb.t), j));
+                    float* hl = h + lo * kw;
+                    // read-add-write: the wave's LDS operations execute in issue
+                    // order, so the next edge's reads see these writes (a lane's
+                    // four cells are distinct: read all, then write)
+                    const float a0 = ina ? hl[ca] : 0.0f, a1 = ina ? hl[kw + ca] : 0.0f;
+                    const float b0 = inb ? hl[cb] : 0.0f, b1 = inb ? hl[kw + cb] : 0.0f;
+                    if (ina) {
+                        hl[ca] = a0 + (1.0f - t) * b.va[j];
+                        hl[kw + ca] = a1 + t * b.va[j];
+                    }
+                    if (inb) {
+                        hl[cb] = b0 + (1.0f - t) * b.vb[j];
+                        hl[kw + cb] = b1 + t * b.vb[j];
+                    }
+                }
+            }
+        };
+        Batch b0, b1;
+        int64_t e = e_begin;
+        if (e < e_end) load(e, b0);
+        while (e < e_end) {
+            const int64_t e1 = e + kHistBatch;
+            if (e1 < e_end) load(e1, b1);
+            add(e, b0);
+            if (e1 >= e_end) break;
+            const int64_t e2 = e1 + kHistBatch;
+            if (e2 < e_end) load(e2, b0);
+            add(e1, b1);
+            e = e2;
+        }
     }
     __syncthreads();
     float* out = hist_part + static_cast<int64_t>(blockIdx.x) * hsz;
-    for (int q = threadIdx.x; q < hsz; q += kThreads) {
+    for (int q = threadIdx.x; q < hsz; q += blockDim.x) {
         float acc = sh[q];
-        for (int v = 1; v < streams; ++v) acc += sh[static_cast<int64_t>(v) * hsz + q];
+        for (int v = 1; v < waves; ++v) acc += sh[static_cast<int64_t>(v) * hsz + q];
         out[q] = acc;
     }
 }
@@ -141,54 +190,48 @@ int reduce_partials(const float* part, int groups, int64_t n, float* out, float*
     return FEQ_OK;
 }
 
-constexpr int64_t kBinChunk = 256;   // edges per histogram workgroup
-constexpr size_t kHistLds = 64 * 1024;
+constexpr int kHistGroups = 256;           // histogram workgroups (fixed: the order is set by E alone)
+constexpr size_t kHistLds = 160 * 1024;
 
-// Histogram streams per workgroup (0: the histogram does not fit LDS).
-int hist_streams(const feq_binning& B, int kw) {
+// Waves (private histograms) per histogram workgroup; 0: one does not fit LDS.
+int hist_waves(const feq_binning& B, int kw) {
     const size_t hbytes = 4 * static_cast<size_t>(B.num_bins + 1) * kw;
-    const size_t avail = kHistLds - 8 * kBinChunk;
-    int st = kw <= kThreads ? kThreads / kw : 1;
-    while (st > 0 && st * hbytes > avail) --st;
-    return st;
-}
-
-size_t hist_lds(const feq_binning& B, int kw, int streams) {
-    return 4 * static_cast<size_t>(streams) * (B.num_bins + 1) * kw + 8 * kBinChunk;
+    const size_t w = kHistLds / hbytes;
+    return static_cast<int>(w < 4 ? w : 4);
 }
 
 }  // namespace
 
-bool ew_tail_supported(const feq_binning& B, int kw) { return hist_streams(B, kw) >= 1; }
+bool ew_tail_supported(const feq_binning& B, int kw) { return hist_waves(B, kw) >= 1; }
 
 size_t ew_tail_floats(const feq_binning& B, int kw, int64_t E, int groups, int64_t ncc) {
-    const int nchunks = static_cast<int>(ceil_div(E, kBinChunk));
+    (void)E;
     const int64_t hsz = (B.num_bins + 1) * static_cast<int64_t>(kw);
-    const size_t tmp = std::max(reduce_tmp_floats(groups, ncc), reduce_tmp_floats(nchunks, hsz));
-    return align_up(static_cast<size_t>(nchunks) * hsz, 64) + align_up(tmp, 64) + 64;
+    const size_t tmp = std::max(reduce_tmp_floats(groups, ncc), reduce_tmp_floats(kHistGroups, hsz));
+    return align_up(static_cast<size_t>(kHistGroups) * hsz, 64) + align_up(tmp, 64) + 64;
 }
 
 int ew_tail(const feq_layout& L, const feq_binning& B, int K, int64_t E, const float* dist,
             const float* F, const float* dFe, const float* dCp, int groups, int64_t ncc, float* gC,
             float* gF, float* gdist, float* tail, hipStream_t s) {
     const int kw = K * L.wdim;
-    const int streams = hist_streams(B, kw);
-    if (streams < 1) return fail(FEQ_ERR_UNSUPPORTED, "radial-function histogram does not fit LDS");
-    const size_t hlds = hist_lds(B, kw, streams);
-    const int nchunks = static_cast<int>(ceil_div(E, kBinChunk));
+    const int waves = hist_waves(B, kw);
+    if (waves < 1) return fail(FEQ_ERR_UNSUPPORTED, "radial-function histogram does not fit LDS");
     const int64_t hsz = (B.num_bins + 1) * static_cast<int64_t>(kw);
+    const size_t hlds = 4 * static_cast<size_t>(waves) * hsz;
+    const int64_t per_wave = ceil_div(E, static_cast<int64_t>(kHistGroups) * waves);
     float* hp = tail;
-    float* tmp = tail + align_up(static_cast<size_t>(nchunks) * hsz, 64);
+    float* tmp = tail + align_up(static_cast<size_t>(kHistGroups) * hsz, 64);
     if (hlds > 64 * 1024)
         FEQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_ewm_hist),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(hlds)));
-    FEQ_LAUNCH("k_ewm_hist", k_ewm_hist, dim3(nchunks), dim3(kThreads), hlds, s, B, kw, streams,
-               E, kBinChunk, dist, dFe, hp);
+    FEQ_LAUNCH("k_ewm_hist", k_ewm_hist, dim3(kHistGroups), dim3(64 * waves), hlds, s, B, kw, E,
+               per_wave, dist, dFe, hp);
     if (gdist)
         FEQ_LAUNCH("k_ewm_dr", k_ewm_dr, dim3(ceil_div(E, kThreads)), dim3(kThreads),
                    sizeof(int) * L.wdim, s, L, B, K, E, dist, F, dFe, gdist);
     if (int rc = reduce_partials(dCp, groups, ncc, gC, tmp, s)) return rc;
-    return reduce_partials(hp, nchunks, hsz, gF, tmp, s);
+    return reduce_partials(hp, kHistGroups, hsz, gF, tmp, s);
 }
 
 }  // namespace feq
