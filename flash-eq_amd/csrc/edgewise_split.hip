@@ -275,6 +275,21 @@ __device__ __forceinline__ int off_block_nonzero(const float4 (&v)[NV]) {
     return any;
 }
 
+// Sums of four per-lane values over the wave's four 16-lane rows: lane
+// (row g, column c) returns sum over rows of v[g] at column c.  Two
+// v_permlane16_swap (odd rows of the first operand <-> even rows of the second)
+// and one v_permlane32_swap (upper half of the first <-> lower half of the
+// second) instead of eight cross-lane shuffles.
+__device__ __forceinline__ float quad_lane_sums(const float (&v)[4]) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[0]), __float_as_uint(v[1]), false, false);
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[2]), __float_as_uint(v[3]), false, false);
+    // rows of s: v0 (0+1), v1 (0+1), v0 (2+3), v1 (2+3); of t likewise for v2, v3
+    const float s = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    const float t = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    const auto z = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(t), false, false);
+    return __uint_as_float(z[0]) + __uint_as_float(z[1]);
+}
+
 // out[r][j] = sum_d x[r][d] R[d][j] for NR rows (x P, gy Q).  SPARSE sums only
 // the degree block of column j.
 template <int L, bool SPARSE, int NR>
@@ -630,10 +645,9 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
 // (le, lg) of wave w holds rows ci = 16 (w + 4 j) + 4 lg + r of edge le.
 // gd is scaled per edge and split into fp16 fragments like fs in the forward;
 // C_k^T comes pre-split from k_ews_prep (same per-rank scale as C_k), one pass
-// of KP rank components at a time.  The dF_e partials of a weight w are
-// complete after the last output slot that uses it: they are summed over the
-// wave's four lane groups with two lane shuffles, unscaled, and summed over
-// the four waves in LDS.  Rotations use the degree blocks when the tile's P
+// of KP rank components at a time.  At the end of a pass its dF_e partials are
+// summed over the wave's four lane groups with lane swaps (four values per
+// register), unscaled, and summed over the four waves in LDS.  Rotations use the degree blocks when the tile's P
 // and Q have no entry off them; dx is staged in LDS and stored coalesced.
 template <int CIN, int COUT, int LIN, int LOUT, int K>
 __global__ void __launch_bounds__(kThreads, 2)
@@ -851,39 +865,42 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             for (int kk = 0; kk < KP; ++kk)
 #pragma unroll
                 for (int w = 0; w < WD; ++w) pf[kk][w] = 0.0f;
+            // software pipeline over the output slots: slot o + 1's MFMAs are
+            // issued before slot o is contracted, slot o + 2's fragments loaded
             h8 bh[2][NKS], bl[2][NKS];
+            v4f acc2[2][RPW][KP];
+            auto load_b = [&](int slot, int buf) {
 #pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) {
-                bh[0][ks] = *reinterpret_cast<const h8*>(sB + ks * CHUNK + myslot);
-                bl[0][ks] = *reinterpret_cast<const h8*>(sB + (DOUT * NKS + ks) * CHUNK + myslot);
-            }
-            static_for<DOUT>([&](auto OO) {
-                constexpr int o = decltype(OO)::value;
-                constexpr int cur = o & 1;
-                if constexpr (o + 1 < DOUT) {
-#pragma unroll
-                    for (int ks = 0; ks < NKS; ++ks) {
-                        bh[cur ^ 1][ks] =
-                            *reinterpret_cast<const h8*>(sB + ((o + 1) * NKS + ks) * CHUNK + myslot);
-                        bl[cur ^ 1][ks] =
-                            *reinterpret_cast<const h8*>(sB + ((DOUT + o + 1) * NKS + ks) * CHUNK + myslot);
-                    }
+                for (int ks = 0; ks < NKS; ++ks) {
+                    bh[buf][ks] = *reinterpret_cast<const h8*>(sB + (slot * NKS + ks) * CHUNK + myslot);
+                    bl[buf][ks] = *reinterpret_cast<const h8*>(sB + ((DOUT + slot) * NKS + ks) * CHUNK + myslot);
                 }
-                v4f acc[RPW][KP];
+            };
+            auto mfma_slot = [&](int buf, int ab) {
 #pragma unroll
                 for (int j = 0; j < RPW; ++j)
 #pragma unroll
-                    for (int kk = 0; kk < KP; ++kk) acc[j][kk] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                    for (int kk = 0; kk < KP; ++kk) acc2[ab][j][kk] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
                     for (int j = 0; j < RPW; ++j)
 #pragma unroll
                         for (int kk = 0; kk < KP; ++kk) {
-                            acc[j][kk] = mfma_h(alo[j][kk][ks], bh[cur][ks], acc[j][kk]);
-                            acc[j][kk] = mfma_h(ahi[j][kk][ks], bl[cur][ks], acc[j][kk]);
-                            acc[j][kk] = mfma_h(ahi[j][kk][ks], bh[cur][ks], acc[j][kk]);
+                            acc2[ab][j][kk] = mfma_h(alo[j][kk][ks], bh[buf][ks], acc2[ab][j][kk]);
+                            acc2[ab][j][kk] = mfma_h(ahi[j][kk][ks], bl[buf][ks], acc2[ab][j][kk]);
+                            acc2[ab][j][kk] = mfma_h(ahi[j][kk][ks], bh[buf][ks], acc2[ab][j][kk]);
                         }
+            };
+            load_b(0, 0);
+            if constexpr (DOUT > 1) load_b(1, 1);
+            mfma_slot(0, 0);
+            static_for<DOUT>([&](auto OO) {
+                constexpr int o = decltype(OO)::value;
+                constexpr int cur = o & 1;
+                if constexpr (o + 1 < DOUT) mfma_slot(cur ^ 1, cur ^ 1);
+                if constexpr (o + 2 < DOUT) load_b(o + 2, cur);
+                auto& acc = acc2[cur];
                 static_for<TG::count(o)>([&](auto TT) {
                     constexpr Term tm = TG::sorted[TG::start[o] + decltype(TT)::value];
 #pragma unroll
@@ -910,21 +927,25 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
                     for (int r = 0; r < 4; ++r)
 #pragma unroll
                         for (int i = 0; i < DIN; ++i) asm volatile("" : "+v"(dfs[j][r][i]));
-                // radial weights whose last output slot is o: finish their partials
-                static_for<WD>([&](auto WW) {
-                    constexpr int w = decltype(WW)::value;
-                    if constexpr (TG::last[w] == o) {
-#pragma unroll
-                        for (int kk = 0; kk < KP; ++kk) {
-                            float v = pf[kk][w];
-                            v += __shfl_xor(v, 16, 64);
-                            v += __shfl_xor(v, 32, 64);
-                            if (lg == 0)
-                                sDF[(wave * kNE + le) * KW + (k0 + kk) * WD + w] = v * sInvK[k0 + kk] * einv;
-                        }
-                    }
-                });
                 __builtin_amdgcn_sched_barrier(0);
+            });
+            // the pass's dF_e partials, value n = KP w + kk: sums over the four
+            // lane groups, four values per register (lane group g keeps value
+            // 4 q + g of quad q), unscaled and stored by every lane
+            constexpr int NV = KP * WD, NQ = (NV + 3) / 4;
+            const float sck = sInvK[k0 + lg % KP] * einv;   // 4 q + lg = lg (mod KP)
+            float* dst = sDF + (wave * kNE + le) * KW + k0 * WD;
+            static_for<NQ>([&](auto QQ) {
+                constexpr int q = decltype(QQ)::value;
+                float v[4];
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int n = 4 * q + g;
+                    v[g] = n < NV ? pf[n % KP][n / KP] : 0.0f;
+                }
+                const float u = quad_lane_sums(v);
+                const int n = 4 * q + lg;
+                if (4 * q + 3 < NV || n < NV) dst[(n % KP) * WD + n / KP] = u * sck;
             });
         });
 
