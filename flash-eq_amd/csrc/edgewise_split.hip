@@ -360,11 +360,11 @@ __device__ __forceinline__ void rotate_rows(const float (&vin)[(L + 1) * (L + 1)
 // to LDS, and a test whether every off-block entry of the tile's P and Q is
 // zero (then the rotations sum over the degree blocks only); (2) fs rows are
 // rotated by threads that own 4 channels of one edge, scaled per edge, split
-// and written as fp16 fragments; (3) the rank components run in passes of KP:
-// per slot i the 3-term MFMA products of the pass's components are contracted
-// into y (registers); (4) the next tile's global loads are issued, then the Q
-// rotation and direct 16-byte stores (each lane owns 4 consecutive channels
-// of one edge).  Row strides of the per-edge LDS blocks are odd, so the 16
+// and written as fp16 fragments; (3) one pass over the slots with the A
+// fragments of every rank component in registers: per slot i the 3-term MFMA
+// products are contracted into y (registers); (4) the next tile's global loads
+// are issued, then the Q rotation, staged in LDS and stored with coalesced
+// 16-byte stores.  Row strides of the per-edge LDS blocks are odd, so the 16
 // edges of a wave's lanes hit distinct banks.
 template <int CIN, int COUT, int LIN, int LOUT, int K, int OCC>
 __global__ void __launch_bounds__(kThreads, OCC)
@@ -377,7 +377,7 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
     constexpr int PS = DIN * DIN | 1, QS = DOUT * DOUT | 1, KWS = KW | 1;
     constexpr int RPW = COUT / 64, NKS = CIN / 32, NC4 = CIN / 4;
-    constexpr int KP = K % 2 == 0 ? 2 : 1;                       // rank components per pass
+    constexpr int KP = K;                                        // rank components per pass
     constexpr int CHUNK = 1024;                                  // bytes per fragment chunk
     constexpr int NPR = (kNE * NC4 + kThreads - 1) / kThreads;   // producer passes
     constexpr int NPL = (kNE * DIN * DIN / 4 + kThreads - 1) / kThreads;
@@ -516,7 +516,7 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
             produce(std::true_type{});
         __syncthreads();
 
-        // (3) GEMM per input slot, rank components in passes of KP
+        // (3) GEMM per input slot, all rank components (KP = K) in one pass
         float yv[RPW][DOUT][4];
 #pragma unroll
         for (int j = 0; j < RPW; ++j)
@@ -1003,8 +1003,9 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 // extra barrier); each rank's tile product is unscaled row by column into a
 // float32 accumulator that lives for the whole launch.  fs fragments stay in
 // LDS for the tile; the U_k fragments of one rank at a time share their
-// buffer with the tile's P and Q.  Wave (wr, wc) owns a 2 x 2 block grid of
-// the output.  One partial dC per workgroup.
+// buffer with the tile's P and Q.  Wave w owns output rows 16 w .. 16 w + 15,
+// whose U_k rows its own lanes produce, so only the fs fragments are shared
+// between waves.  One partial dC per workgroup.
 template <int CIN, int COUT, int LIN, int LOUT, int K>
 __global__ void __launch_bounds__(kThreads, 2)
 k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
@@ -1013,15 +1014,15 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             const float* __restrict__ F, float* __restrict__ dC_part) {
     using T = Canon<LIN, LOUT>;
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
-    constexpr int PS = DIN * DIN | 1, QS = DOUT * DOUT | 1, KWS = KW | 1;
+    constexpr int PS = DIN * DIN | 1, QS = DOUT * DOUT | 1;
+    constexpr int WDP = (WD + 3) / 4 * 4;                        // radial row of one (k, edge), float4s
     constexpr int RB = COUT / 16, CB = CIN / 16;                 // 16-row / 16-column blocks
-    constexpr int WR = RB / 2, WC = CB / 2;                      // blocks per wave (2 x 2 waves)
     constexpr int NKG = 2 * DIN;                                 // 8-edge groups of the reduction
     constexpr int NKS = (NKG + 3) / 4;                           // 32-steps
     constexpr int ARR = NKG * 256;                               // bytes per (split, block) array
     constexpr int NPL = (kNE * DIN * DIN / 4 + kThreads - 1) / kThreads;
     constexpr int NQL = (kNE * DOUT * DOUT / 4 + kThreads - 1) / kThreads;
-    static_assert(RB % 2 == 0 && CB % 2 == 0 && 4 * CIN <= kThreads && 4 * COUT <= kThreads,
+    static_assert(RB == kThreads / 64 && 4 * CIN <= kThreads && 4 * COUT == kThreads,
                   "unsupported channel counts");
     static_assert(4 * (kNE * PS + kNE * QS) <= 2 * RB * ARR, "P and Q must fit the U buffer");
 
@@ -1030,37 +1031,39 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     char* sU = sF + 2 * CB * ARR;                                // U_k fragments [2][RB][NKG][16][16 B]
     float* sP = reinterpret_cast<float*>(sU);                    // P, Q of the tile (producer phase only)
     float* sQ = sP + kNE * PS;
-    float* sFe = reinterpret_cast<float*>(sU + 2 * RB * ARR);
-    float* sInvF = sFe + kNE * KWS;                              // 1 / scale of fs column ci
+    float* sFe = reinterpret_cast<float*>(sU + 2 * RB * ARR);   // [K][kNE][WDP], 0 past the last edge
+    float* sInvF = sFe + K * kNE * WDP;                          // 1 / scale of fs column ci
     float* sInvU = sInvF + CIN;                                  // 1 / scale of U_k row co
     EdgeState* sE = reinterpret_cast<EdgeState*>(sInvU + COUT);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int le = lane & 15, lg = lane >> 4;
-    const int wr = wave >> 1, wc = wave & 1;
     const int pc = tid >> 2, pq = tid & 3;                        // producer: channel, edge quad
 
-    v4f acc_tot[K][WR][WC];
+    v4f acc_tot[K][CB];
 #pragma unroll
     for (int k = 0; k < K; ++k)
 #pragma unroll
-        for (int a = 0; a < WR; ++a)
-#pragma unroll
-            for (int b = 0; b < WC; ++b) acc_tot[k][a][b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int b = 0; b < CB; ++b) acc_tot[k][b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
     for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
         const int64_t e0 = tile * kNE;
-        // global loads: four edges' rows of one input channel / one output channel
+        // global loads: four edges' rows of one input channel / one output channel.
+        // Unconditional: edges past the last (and channels past Cin / Cout) read
+        // the last one's rows; their radial functions are zero, so their U_k rows
+        // are zero and they add nothing to dC.
         float xr[4][DIN], gr[4][DOUT];
+        const int pci = pc < CIN ? pc : CIN - 1, pco = pc < COUT ? pc : COUT - 1;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const int64_t e = e0 + 4 * pq + q;
-            const bool ok = e < E;
+            const int64_t e = e0 + 4 * pq + q < E ? e0 + 4 * pq + q : E - 1;
+            const float* xs = x + (e * CIN + pci) * DIN;
+            const float* gs = gy + (e * COUT + pco) * DOUT;
 #pragma unroll
-            for (int d = 0; d < DIN; ++d) xr[q][d] = (ok && pc < CIN) ? x[(e * CIN + pc) * DIN + d] : 0.0f;
+            for (int d = 0; d < DIN; ++d) xr[q][d] = xs[d];
 #pragma unroll
-            for (int d = 0; d < DOUT; ++d) gr[q][d] = (ok && pc < COUT) ? gy[(e * COUT + pc) * DOUT + d] : 0.0f;
+            for (int d = 0; d < DOUT; ++d) gr[q][d] = gs[d];
         }
         float4 pr[NPL], qr[NQL];
         load_tile4<DIN * DIN, NPL>(P, e0, E, pr);
@@ -1086,7 +1089,7 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             const int e = q / KW, rest = q % KW;
             const EdgeState es = sE[e];
             const float* flo = F + static_cast<int64_t>(es.lo) * KW + rest;
-            sFe[e * KWS + rest] = lerp_bins(flo[0], flo[KW], es.t);
+            sFe[((rest / WD) * kNE + e) * WDP + rest % WD] = es.valid ? lerp_bins(flo[0], flo[KW], es.t) : 0.0f;
         }
         // fs (input channel pc of edges 4 pq .. 4 pq + 3) and gd (output channel pc)
         float gd[4][DOUT];
@@ -1140,11 +1143,16 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
         }
         __syncthreads();   // fs fragments complete; P and Q no longer read
 
+        // Wave w owns output rows co = 16 w + ..., the channels its own producer
+        // lanes hold gd for: its U_k fragments are written and read by the wave
+        // alone (a wave's LDS operations execute in issue order), so the rank
+        // components need no workgroup barrier.
         const int nbase = lane;   // fragment reads: lane (g, n) at 16-byte slot 16 g + n of an 8-edge group row
+        char* uarr = sU + wave * ARR;
         static_for<K>([&](auto KK) {
             constexpr int k = decltype(KK)::value;
             // U_k row pc of edges 4 pq .. 4 pq + 3, scaled per row, to fragments
-            if (pc < COUT) {
+            {
                 float u[4][DIN];
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
@@ -1152,7 +1160,16 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
                     for (int i = 0; i < DIN; ++i) u[q][i] = 0.0f;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const float* fe = sFe + (4 * pq + q) * KWS + k * WD;
+                    const float4* fe4 = reinterpret_cast<const float4*>(sFe + (k * kNE + 4 * pq + q) * WDP);
+                    float fe[WDP];
+#pragma unroll
+                    for (int v = 0; v < WDP / 4; ++v) {
+                        const float4 f = fe4[v];
+                        fe[4 * v] = f.x;
+                        fe[4 * v + 1] = f.y;
+                        fe[4 * v + 2] = f.z;
+                        fe[4 * v + 3] = f.w;
+                    }
 #pragma unroll
                     for (int t = 0; t < T::NT; ++t) {
                         const Term tm = T::terms[t];
@@ -1170,7 +1187,6 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
                 const int ex = scale_exp(m);
                 const float sc = exp2i(ex);
                 if (pq == 0) sInvU[pc] = exp2i(-ex);
-                char* arr = sU + (pc / 16) * ARR;
 #pragma unroll
                 for (int i = 0; i < DIN; ++i) {
                     h4 hv, lv;
@@ -1182,78 +1198,65 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
                         lv[q] = l;
                     }
                     const int off = ((2 * i + (pq >> 1)) * 16 + pc % 16) * 16 + 8 * (pq & 1);
-                    *reinterpret_cast<h4*>(arr + off) = hv;
-                    *reinterpret_cast<h4*>(arr + RB * ARR + off) = lv;
+                    *reinterpret_cast<h4*>(uarr + off) = hv;
+                    *reinterpret_cast<h4*>(uarr + RB * ARR + off) = lv;
                 }
             }
-            __syncthreads();   // U_k fragments and row scales complete
 
-            v4f acc[WR][WC];
+            v4f acc[CB];
 #pragma unroll
-            for (int a = 0; a < WR; ++a)
-#pragma unroll
-                for (int b = 0; b < WC; ++b) acc[a][b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int b = 0; b < CB; ++b) acc[b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int ks = 0; ks < NKS; ++ks) {
                 const int kg = 4 * ks + lg;
                 const bool live = kg < NKG;   // the last step's upper lane groups pad with zeros
-                h8 ah[WR], al[WR], bh[WC], bl[WC];
                 const h8 z = h8{0, 0, 0, 0, 0, 0, 0, 0};
+                // all fragments of the step first, then the three products of
+                // the CB blocks interleaved (CB independent accumulation chains)
+                const char* ua = uarr + (16 * ks * 4 + nbase) * 16;
+                const h8 ah = live ? *reinterpret_cast<const h8*>(ua) : z;
+                const h8 al = live ? *reinterpret_cast<const h8*>(ua + RB * ARR) : z;
+                h8 bh[CB], bl[CB];
 #pragma unroll
-                for (int a = 0; a < WR; ++a) {
-                    const char* arr = sU + (WR * wr + a) * ARR + (16 * ks * 4 + nbase) * 16;
-                    ah[a] = live ? *reinterpret_cast<const h8*>(arr) : z;
-                    al[a] = live ? *reinterpret_cast<const h8*>(arr + RB * ARR) : z;
-                }
-#pragma unroll
-                for (int b = 0; b < WC; ++b) {
-                    const char* arr = sF + (WC * wc + b) * ARR + (16 * ks * 4 + nbase) * 16;
+                for (int b = 0; b < CB; ++b) {
+                    const char* arr = sF + b * ARR + (16 * ks * 4 + nbase) * 16;
                     bh[b] = live ? *reinterpret_cast<const h8*>(arr) : z;
                     bl[b] = live ? *reinterpret_cast<const h8*>(arr + CB * ARR) : z;
                 }
 #pragma unroll
-                for (int a = 0; a < WR; ++a)
+                for (int b = 0; b < CB; ++b) acc[b] = mfma_h(al, bh[b], acc[b]);
 #pragma unroll
-                    for (int b = 0; b < WC; ++b) {
-                        acc[a][b] = mfma_h(al[a], bh[b], acc[a][b]);
-                        acc[a][b] = mfma_h(ah[a], bl[b], acc[a][b]);
-                        acc[a][b] = mfma_h(ah[a], bh[b], acc[a][b]);
-                    }
+                for (int b = 0; b < CB; ++b) acc[b] = mfma_h(ah, bl[b], acc[b]);
+#pragma unroll
+                for (int b = 0; b < CB; ++b) acc[b] = mfma_h(ah, bh[b], acc[b]);
             }
             // unscale row (co) by column (ci) into the launch accumulator
+            float ru[4];
 #pragma unroll
-            for (int a = 0; a < WR; ++a) {
-                float ru[4];
+            for (int r = 0; r < 4; ++r) ru[r] = sInvU[16 * wave + 4 * lg + r];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) ru[r] = sInvU[16 * (WR * wr + a) + 4 * lg + r];
+            for (int b = 0; b < CB; ++b) {
+                const float cf = sInvF[16 * b + le];
 #pragma unroll
-                for (int b = 0; b < WC; ++b) {
-                    const float cf = sInvF[16 * (WC * wc + b) + le];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) acc_tot[k][a][b][r] += acc[a][b][r] * (ru[r] * cf);
-                }
+                for (int r = 0; r < 4; ++r) acc_tot[k][b][r] += acc[b][r] * (ru[r] * cf);
             }
-            if constexpr (k + 1 < K) __syncthreads();   // before the next U_k overwrites the buffer
         });
     }
     float* part = dC_part + static_cast<int64_t>(blockIdx.x) * K * COUT * CIN;
 #pragma unroll
     for (int k = 0; k < K; ++k)
 #pragma unroll
-        for (int a = 0; a < WR; ++a)
+        for (int b = 0; b < CB; ++b)
 #pragma unroll
-            for (int b = 0; b < WC; ++b)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    part[(k * COUT + 16 * (WR * wr + a) + 4 * lg + r) * CIN + 16 * (WC * wc + b) + le] =
-                        acc_tot[k][a][b][r];
+            for (int r = 0; r < 4; ++r)
+                part[(k * COUT + 16 * wave + 4 * lg + r) * CIN + 16 * b + le] = acc_tot[k][b][r];
 }
 
 template <int CIN, int COUT, int LIN, int LOUT, int K>
 constexpr size_t ews_bwd_c_lds() {
     using T = Canon<LIN, LOUT>;
-    constexpr size_t ARR = 2 * T::DIN * 256, KWS = K * T::WD | 1;
-    return 2 * (CIN / 16) * ARR + 2 * (COUT / 16) * ARR + 4 * (kNE * KWS + CIN + COUT) +
+    constexpr size_t ARR = 2 * T::DIN * 256, WDP = (T::WD + 3) / 4 * 4;
+    return 2 * (CIN / 16) * ARR + 2 * (COUT / 16) * ARR + 4 * (K * kNE * WDP + CIN + COUT) +
            kNE * sizeof(EdgeState);
 }
 
@@ -1277,11 +1280,14 @@ constexpr size_t ews_fwd_lds() {
            kNE * sizeof(EdgeState);
 }
 
-// Workgroups per CU of the forward: as many as the 160 KB of LDS allow, at most 3.
+// Workgroups per CU of the forward.  Two, measured on MI355X at 160k edges
+// with all rank components in one GEMM pass: 253 us, against 261 us with two
+// passes and 306 us at three workgroups per CU, where the 168-register budget
+// forces spills.
 template <int CIN, int COUT, int LIN, int LOUT, int K>
 constexpr int ews_fwd_occ() {
-    constexpr size_t lds = ews_fwd_lds<CIN, COUT, LIN, LOUT, K>();
-    return lds * 3 <= 160 * 1024 ? 3 : 2;
+    static_assert(2 * ews_fwd_lds<CIN, COUT, LIN, LOUT, K>() <= 160 * 1024, "forward LDS");
+    return 2;
 }
 
 int ews_cus() {
