@@ -58,7 +58,22 @@ __global__ void k_segment_sum4(const float4* __restrict__ x, int64_t row4,
     if (c >= row4) return;
     const int b = offsets[n], e_end = offsets[n + 1];
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int i = b; i < e_end; ++i) {
+    // loads of eight edges at a time in flight, summed in segment order
+    constexpr int U = 8;
+    int i = b;
+    for (; i + U <= e_end; i += U) {
+        float4 v[U];
+#pragma unroll
+        for (int j = 0; j < U; ++j) v[j] = x[static_cast<int64_t>(perm[i + j]) * row4 + c];
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            acc.x += v[j].x;
+            acc.y += v[j].y;
+            acc.z += v[j].z;
+            acc.w += v[j].w;
+        }
+    }
+    for (; i < e_end; ++i) {
         const float4 v = x[static_cast<int64_t>(perm[i]) * row4 + c];
         acc.x += v.x;
         acc.y += v.y;
@@ -68,14 +83,18 @@ __global__ void k_segment_sum4(const float4* __restrict__ x, int64_t row4,
     out[n * row4 + c] = acc;
 }
 
-__global__ void k_gather_rows4(const float4* __restrict__ src, int64_t row4,
-                               const int64_t* __restrict__ idx, int64_t nrows, int64_t nsrc,
-                               float4* __restrict__ out) {
-    const int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-    if (q >= nrows * row4) return;
-    const int64_t r = q / row4, c = q % row4;
+// One row per wave (the row index is wave-uniform), lanes across its float4s.
+__global__ void __launch_bounds__(256)
+k_gather_rows4(const float4* __restrict__ src, int64_t row4, const int64_t* __restrict__ idx,
+               int64_t nrows, int64_t nsrc, float4* __restrict__ out) {
+    const int64_t r = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (r >= nrows) return;
+    const int lane = threadIdx.x & 63;
     const int64_t s = idx[r];
-    out[q] = (s >= 0 && s < nsrc) ? src[s * row4 + c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const bool ok = s >= 0 && s < nsrc;
+    const float4* in = src + (ok ? s : 0) * row4;
+    float4* o = out + r * row4;
+    for (int64_t c = lane; c < row4; c += 64) o[c] = ok ? in[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
 __global__ void k_gather_rows(const float* __restrict__ src, int64_t row,
@@ -341,9 +360,8 @@ extern "C" int feq_gather_rows(const float* src, int64_t nsrc, int64_t row, cons
     if (nrows == 0 || row == 0) return FEQ_OK;
     if (!src || !idx || !out) return fail(FEQ_ERR_INVALID, "NULL pointer");
     if (row % 4 == 0 && aligned16(src) && aligned16(out)) {
-        const int64_t n4 = nrows * (row / 4);
-        FEQ_LAUNCH("k_gather_rows", k_gather_rows4, dim3(static_cast<unsigned>(ceil_div(n4, kThreads))),
-                   dim3(kThreads), 0, stream_of(stream), reinterpret_cast<const float4*>(src), row / 4,
+        FEQ_LAUNCH("k_gather_rows", k_gather_rows4, dim3(static_cast<unsigned>(ceil_div(nrows, 4))),
+                   dim3(256), 0, stream_of(stream), reinterpret_cast<const float4*>(src), row / 4,
                    idx, nrows, nsrc, reinterpret_cast<float4*>(out));
         return FEQ_OK;
     }
