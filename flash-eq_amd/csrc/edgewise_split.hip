@@ -66,6 +66,15 @@ __device__ __forceinline__ void split_f16(float a, _Float16& hi, _Float16& lo) {
     lo = static_cast<_Float16>(a - static_cast<float>(hi));
 }
 
+// split_f16(a * sc) with both halves formed by fused multiply-adds with a
+// half-precision result (v_fma_mix): hi = fp16(a sc), lo = fp16(a sc - hi),
+// where a sc - hi is exact inside the fma.  sc is a power of two, so a sc is
+// exact and the halves equal split_f16's.
+__device__ __forceinline__ void split_f16s(float a, float sc, _Float16& hi, _Float16& lo) {
+    hi = static_cast<_Float16>(__builtin_fmaf(a, sc, 0.0f));
+    lo = static_cast<_Float16>(__builtin_fmaf(a, sc, -static_cast<float>(hi)));
+}
+
 // Byte offset of lane slot (g, e) = lane 16 g + e inside a 1 KB fragment chunk
 // (64 lanes x 8 halves).  The XOR swizzle keeps the fragment reads (a
 // permutation of the chunk per 16 lanes) and the producers' 8-byte writes
@@ -128,7 +137,7 @@ k_ews_prep(const float* __restrict__ C, h8* __restrict__ frag, float* __restrict
             // A = C_k (row co, reduction ci) or C_k^T (row ci, reduction co); C is (K, Cout, Cin)
             const float a = TRANS ? Ck[(c0 + jj) * NROW + row] : Ck[row * NRED + c0 + jj];
             _Float16 h, lw;
-            split_f16(a * sc, h, lw);
+            split_f16s(a, sc, h, lw);
             hi[jj] = h;
             lo[jj] = lw;
         }
@@ -473,7 +482,7 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         _Float16 h, l;
-                        split_f16(fs[r][i] * sc, h, l);
+                        split_f16s(fs[r][i], sc, h, l);
                         hv[r] = h;
                         lv[r] = l;
                     }
@@ -784,7 +793,7 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         _Float16 h, l;
-                        split_f16(gd[r][o] * sc, h, l);
+                        split_f16s(gd[r][o], sc, h, l);
                         hv[r] = h;
                         lv[r] = l;
                     }
@@ -1135,7 +1144,7 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         _Float16 h, l;
-                        split_f16(fs[q][i] * sc, h, l);
+                        split_f16s(fs[q][i], sc, h, l);
                         hv[q] = h;
                         lv[q] = l;
                     }
@@ -1197,7 +1206,7 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         _Float16 h, l;
-                        split_f16(u[q][i] * sc, h, l);
+                        split_f16s(u[q][i], sc, h, l);
                         hv[q] = h;
                         lv[q] = l;
                     }
