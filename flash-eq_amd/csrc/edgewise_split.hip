@@ -263,25 +263,39 @@ __device__ __forceinline__ int std_degree(int d, int L) {
     return l;
 }
 
-// 1 when an element of this thread's share of a (kNE, D, D) basis tile (read by
-// load_tile4) lies outside the degree blocks and is non-zero.
+// Bit 4 n + c set when component c of float4 n of this thread's share of a
+// (kNE, D, D) basis tile (as read by load_tile4) lies outside the degree blocks.
+// The positions are the same for every tile, so this runs once per launch.
 template <int L, int NV>
-__device__ __forceinline__ int off_block_nonzero(const float4 (&v)[NV]) {
+__device__ __forceinline__ unsigned off_block_bits() {
+    static_assert(4 * NV <= 32, "one bit per component");
     constexpr int D = (L + 1) * (L + 1), N = D * D, NQ = kNE * N / 4;
-    int any = 0;
+    unsigned bits = 0;
 #pragma unroll
     for (int n = 0; n < NV; ++n) {
         const int q = threadIdx.x + kThreads * n;
-        if (q < NQ) {
-            const float f[4] = {v[n].x, v[n].y, v[n].z, v[n].w};
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int pos = (4 * q + c) % N;
-                any |= (f[c] != 0.0f) & (std_degree(pos / D, L) != slot_degree<L>(pos % D));
-            }
+        for (int c = 0; c < 4; ++c) {
+            const int pos = (4 * q + c) % N;
+            const bool off = q < NQ && std_degree(pos / D, L) != slot_degree<L>(pos % D);
+            bits |= static_cast<unsigned>(off) << (4 * n + c);
         }
     }
-    return any;
+    return bits;
+}
+
+// 1 when an element of this thread's share of a basis tile that lies outside
+// the degree blocks (bits from off_block_bits) is non-zero (-0 counts as zero).
+template <int NV>
+__device__ __forceinline__ int off_block_nonzero(const float4 (&v)[NV], unsigned bits) {
+    unsigned acc = 0;
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+        const float f[4] = {v[n].x, v[n].y, v[n].z, v[n].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc |= ((bits >> (4 * n + c)) & 1u) ? __float_as_uint(f[c]) : 0u;
+    }
+    return (acc & 0x7fffffffu) != 0;
 }
 
 // Sums of four per-lane values over the wave's four 16-lane rows: lane
@@ -408,6 +422,7 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
     const int le = lane & 15, lg = lane >> 4;
+    const unsigned pbits = off_block_bits<LIN, NPL>(), qbits = off_block_bits<LOUT, NQL>();
 
     if (tid < K) sInvK[tid] = Cinv[tid];   // read after the first tile barrier
 
@@ -510,7 +525,7 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
             sE[tid] = es;
         }
         const bool dense =
-            __syncthreads_or(off_block_nonzero<LIN>(pr) | off_block_nonzero<LOUT>(qr)) != 0;
+            __syncthreads_or(off_block_nonzero(pr, pbits) | off_block_nonzero(qr, qbits)) != 0;
 
         // (2) radial functions of the tile (1/scale_k folded in) and fs fragments
         for (int q = tid; q < kNE * KW; q += kThreads) {
@@ -698,6 +713,7 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
     const int le = lane & 15, lg = lane >> 4;
+    const unsigned pbits = off_block_bits<LIN, NPL>(), qbits = off_block_bits<LOUT, NQL>();
     if (tid < K) sInvK[tid] = Cinv[tid];
 
     // global loads of one tile: gy rows of the producer threads, x rows of the
@@ -830,7 +846,7 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             sE[tid] = es;
         }
         const bool dense =
-            __syncthreads_or(off_block_nonzero<LIN>(pr) | off_block_nonzero<LOUT>(qr)) != 0;
+            __syncthreads_or(off_block_nonzero(pr, pbits) | off_block_nonzero(qr, qbits)) != 0;
 
         // radial functions (1/scale_k folded in), gd fragments, fs in lane layout
         for (int q = tid; q < kNE * KW; q += kThreads) {
@@ -1052,6 +1068,7 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int le = lane & 15, lg = lane >> 4;
+    const unsigned pbits = off_block_bits<LIN, NPL>(), qbits = off_block_bits<LOUT, NQL>();
     const int pc = tid >> 2, pq = tid & 3;                        // producer: channel, edge quad
 
     v4f acc_tot[K][CB];
@@ -1096,7 +1113,7 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             sE[tid] = es;
         }
         const bool dense =
-            __syncthreads_or(off_block_nonzero<LIN>(pr) | off_block_nonzero<LOUT>(qr)) != 0;
+            __syncthreads_or(off_block_nonzero(pr, pbits) | off_block_nonzero(qr, qbits)) != 0;
 
         for (int q = tid; q < kNE * KW; q += kThreads) {
             const int e = q / KW, rest = q % KW;
