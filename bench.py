@@ -5,10 +5,11 @@ EquivariantEdgewiseLinear with in = out = Repr([0,1,2], mult=64), fp32;
 N = 10,000 nodes uniform in a 40^3 cube, k = 16 nearest neighbours
 (E = 160,000 edges, src = neighbour -> dst = centre), distances clipped to
 max_dist = 10, num_bins = 100.  Node features (N, 64, 9) ~ N(0,1) are gathered
-to edges by src (Graph.gather_src: its backward is a segmented sum over the
-edges grouped by source).  One step = gather + layer forward + the
-sum-of-squares loss sum(out**2) + backward into the node features and every
-layer parameter.  P = Q come from
+to edges by src inside the fused layer (layer(P, P, feats, r, graph=graph):
+the kernels read row src[e] of the node table; the backward sums the per-edge
+input gradient over the edges grouped by source).  One step = gather + layer
+forward + the sum-of-squares loss sum(out**2) + backward into the node
+features and every layer parameter.  P = Q come from
 WignerDBasis outside the timed region (as in the reference's benchmark,
 benchmarks/compare_all.py:168).
 
@@ -215,7 +216,7 @@ def main() -> int:
     graph.csr_src()                            # CSR by source, built once per graph
 
     def step():
-        y = layer(P, P, graph.gather_src(feats), dist)
+        y = layer(P, P, feats, dist, graph=graph)
         SumOfSquares.apply(y).backward()
 
     for _ in range(args.warmup):

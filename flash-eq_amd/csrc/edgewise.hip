@@ -420,8 +420,8 @@ extern "C" int feq_edgewise_fwd(const feq_layout* L, const feq_binning* b, int32
     if (!x || !P || !Q || !dist || !C || !F || !y) return fail(FEQ_ERR_INVALID, "NULL pointer");
     const int path = ew_path();
     if (path == kPathSplit) {
-        const int rc = ew_split_fwd(*L, *b, rank, E, x, P, Q, dist, C, F, y, ws, ws_bytes,
-                                    stream_of(stream));
+        const int rc = ew_split_fwd(*L, *b, rank, E, x, nullptr, 0, P, Q, dist, C, F, y, ws,
+                                    ws_bytes, stream_of(stream));
         if (rc != -1) return rc;
     }
     if (path != kPathGeneric) {
@@ -450,15 +450,17 @@ extern "C" int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32
     hipStream_t s = stream_of(stream);
     const int64_t ncc = static_cast<int64_t>(rank) * L->cout * L->cin;
     const int64_t nF = static_cast<int64_t>(b->num_bins + 1) * rank * L->wdim;
-    if (int rc = fill_zero(gF, nF, s)) return rc;
-    if (E == 0) return fill_zero(gC, ncc, s);
+    if (E == 0) {
+        if (int rc = fill_zero(gF, nF, s)) return rc;
+        return fill_zero(gC, ncc, s);
+    }
     if (!gy || !x || !P || !Q || !dist || !C || !F) return fail(FEQ_ERR_INVALID, "NULL pointer");
     if (!ws || ws_bytes < feq_edgewise_workspace(L, b, rank, E))
         return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
     const int path = ew_path();
     if (path == kPathSplit && !gP && !gQ) {
-        const int rc = ew_split_bwd(*L, *b, rank, E, gy, x, P, Q, dist, C, F, gx, gC, gF, gdist, ws,
-                                    ws_bytes, s);
+        const int rc = ew_split_bwd(*L, *b, rank, E, gy, x, nullptr, 0, P, Q, dist, C, F, gx, gC, gF,
+                                    gdist, ws, ws_bytes, s);
         if (rc != -1) return rc;
     }
     if (path != kPathGeneric && !gP && !gQ) {
@@ -466,6 +468,8 @@ extern "C" int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32
                                    ws_bytes, s);
         if (rc != -1) return rc;
     }
+    // the fused paths above overwrite gF; the generic kernel accumulates into it
+    if (int rc = fill_zero(gF, nF, s)) return rc;
     const size_t lds = bwd_lds(*L, rank);
     if (int rc = ensure_lds(reinterpret_cast<const void*>(&k_ew_bwd), lds)) return rc;
     const int G = groups_for(E);
@@ -476,4 +480,57 @@ extern "C" int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32
     FEQ_LAUNCH("k_reduce_partials", k_reduce_partials, dim3(ceil_div(ncc, 256)), dim3(256), 0, s, part, G, ncc,
                        gC);
     return FEQ_OK;
+}
+
+// ---- message-passing form: x is a node table, edge e reads row src[e] -----------
+extern "C" int feq_edgewise_src_supported(const feq_layout* L, const feq_binning* b, int32_t rank) {
+    if (!L || !b || check_layout(L) || check_binning(b)) return 0;
+    if (ew_path() != kPathSplit) return 0;
+    return ew_split_supported(*L, *b, rank, false) && ew_split_supported(*L, *b, rank, true);
+}
+
+extern "C" int feq_edgewise_fwd_src(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                    int64_t E, const float* x, int64_t num_src, const int64_t* src,
+                                    const float* P, const float* Q, const float* dist,
+                                    const float* C, const float* F, float* y, void* ws,
+                                    size_t ws_bytes, feq_stream_t stream) {
+    if (int rc = check_layout(L)) return rc;
+    if (int rc = check_binning(b)) return rc;
+    if (rank < 1) return fail(FEQ_ERR_INVALID, "rank must be positive");
+    if (E < 0 || num_src < 0) return fail(FEQ_ERR_INVALID, "negative edge or node count");
+    if (E == 0) return FEQ_OK;
+    if (E > 0x7fffffffLL) return fail(FEQ_ERR_UNSUPPORTED, "more than 2^31-1 edges");
+    if (!x || !src || !P || !Q || !dist || !C || !F || !y) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (!feq_edgewise_src_supported(L, b, rank))
+        return fail(FEQ_ERR_UNSUPPORTED, "no message-passing kernels for this layout");
+    const int rc = ew_split_fwd(*L, *b, rank, E, x, src, num_src, P, Q, dist, C, F, y, ws, ws_bytes,
+                                stream_of(stream));
+    return rc == -1 ? fail(FEQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned") : rc;
+}
+
+extern "C" int feq_edgewise_bwd_src(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                    int64_t E, const float* gy, const float* x, int64_t num_src,
+                                    const int64_t* src, const float* P, const float* Q,
+                                    const float* dist, const float* C, const float* F,
+                                    float* gx_edges, float* gC, float* gF, float* gdist, void* ws,
+                                    size_t ws_bytes, feq_stream_t stream) {
+    if (int rc = check_layout(L)) return rc;
+    if (int rc = check_binning(b)) return rc;
+    if (rank < 1) return fail(FEQ_ERR_INVALID, "rank must be positive");
+    if (E < 0 || num_src < 0) return fail(FEQ_ERR_INVALID, "negative edge or node count");
+    if (E > 0x7fffffffLL) return fail(FEQ_ERR_UNSUPPORTED, "more than 2^31-1 edges");
+    if (!gC || !gF || !gx_edges) return fail(FEQ_ERR_INVALID, "grad_x_edges, grad_C and grad_F are required");
+    hipStream_t s = stream_of(stream);
+    if (E == 0) {
+        if (int rc = fill_zero(gF, static_cast<int64_t>(b->num_bins + 1) * rank * L->wdim, s)) return rc;
+        return fill_zero(gC, static_cast<int64_t>(rank) * L->cout * L->cin, s);
+    }
+    if (!gy || !x || !src || !P || !Q || !dist || !C || !F) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (!feq_edgewise_src_supported(L, b, rank))
+        return fail(FEQ_ERR_UNSUPPORTED, "no message-passing kernels for this layout");
+    if (!ws || ws_bytes < feq_edgewise_workspace(L, b, rank, E))
+        return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
+    const int rc = ew_split_bwd(*L, *b, rank, E, gy, x, src, num_src, P, Q, dist, C, F, gx_edges, gC,
+                                gF, gdist, ws, ws_bytes, s);
+    return rc == -1 ? fail(FEQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned") : rc;
 }

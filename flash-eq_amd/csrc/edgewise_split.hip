@@ -147,6 +147,26 @@ k_ews_prep(const float* __restrict__ C, h8* __restrict__ frag, float* __restrict
     }
 }
 
+// Rows of the layer input: row e of x, or, in the message-passing form, row
+// src[e] of a node table of nsrc rows (the gather x[src] done inside the
+// kernels).  x_row returns the row an edge reads, or -1 for an index outside
+// [0, nsrc), which reads as a zero row.
+struct XRows {
+    const float* x;
+    const int64_t* src;
+    int64_t nsrc;
+};
+
+template <bool GATHER>
+__device__ __forceinline__ int64_t x_row(const XRows& X, int64_t e) {
+    if constexpr (!GATHER) {
+        return e;
+    } else {
+        const int64_t r = X.src[e];
+        return r >= 0 && r < X.nsrc ? r : -1;
+    }
+}
+
 // The (kNE, N) block of a (E, N) tensor that starts at edge e0, as float4s:
 // thread t holds float4 q = t + kThreads n of the block.  A full tile is read
 // with 16-byte loads (the block starts at a multiple of 16 edges, so it is
@@ -389,9 +409,9 @@ __device__ __forceinline__ void rotate_rows(const float (&vin)[(L + 1) * (L + 1)
 // are issued, then the Q rotation, staged in LDS and stored with coalesced
 // 16-byte stores.  Row strides of the per-edge LDS blocks are odd, so the 16
 // edges of a wave's lanes hit distinct banks.
-template <int CIN, int COUT, int LIN, int LOUT, int K, int OCC>
+template <int CIN, int COUT, int LIN, int LOUT, int K, int OCC, bool GATHER>
 __global__ void __launch_bounds__(kThreads, OCC)
-k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
+k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
           const float* __restrict__ P, const float* __restrict__ Q,
           const float* __restrict__ dist, const h8* __restrict__ Cfrag,
           const float* __restrict__ Cinv, const float* __restrict__ F, float* __restrict__ y) {
@@ -436,8 +456,9 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
         for (int p = 0; p < NPR; ++p) {
             const int q = tid + kThreads * p;
             const int e = q / NC4, c4 = q % NC4;
-            if (q < kNE * NC4 && f0 + e < E) {
-                const float4* src = reinterpret_cast<const float4*>(x + ((f0 + e) * CIN + 4 * c4) * DIN);
+            const int64_t row = q < kNE * NC4 && f0 + e < E ? x_row<GATHER>(X, f0 + e) : -1;
+            if (row >= 0) {
+                const float4* src = reinterpret_cast<const float4*>(X.x + (row * CIN + 4 * c4) * DIN);
 #pragma unroll
                 for (int v = 0; v < DIN; ++v) {
                     const float4 f = src[v];
@@ -673,10 +694,10 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ x,
 // summed over the wave's four lane groups with lane swaps (four values per
 // register), unscaled, and summed over the four waves in LDS.  Rotations use the degree blocks when the tile's P
 // and Q have no entry off them; dx is staged in LDS and stored coalesced.
-template <int CIN, int COUT, int LIN, int LOUT, int K>
+template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER>
 __global__ void __launch_bounds__(kThreads, 2)
 k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
-            const float* __restrict__ x, const float* __restrict__ P,
+            XRows X, const float* __restrict__ P,
             const float* __restrict__ Q, const float* __restrict__ dist,
             const h8* __restrict__ Cfrag, const float* __restrict__ Cinv,
             const float* __restrict__ F, float* __restrict__ gx, float* __restrict__ dFe) {
@@ -745,9 +766,10 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
         }
 #pragma unroll
         for (int j = 0; j < RPW; ++j) {
-            if (f0 + le < E) {
+            const int64_t row = f0 + le < E ? x_row<GATHER>(X, f0 + le) : -1;
+            if (row >= 0) {
                 const float4* src = reinterpret_cast<const float4*>(
-                    x + ((f0 + le) * CIN + 16 * (wave + 4 * j) + 4 * lg) * DIN);
+                    X.x + (row * CIN + 16 * (wave + 4 * j) + 4 * lg) * DIN);
 #pragma unroll
                 for (int v = 0; v < DIN; ++v) {
                     const float4 f = src[v];
@@ -1035,10 +1057,10 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 // buffer with the tile's P and Q.  Wave w owns output rows 16 w .. 16 w + 15,
 // whose U_k rows its own lanes produce, so only the fs fragments are shared
 // between waves.  One partial dC per workgroup.
-template <int CIN, int COUT, int LIN, int LOUT, int K>
+template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER>
 __global__ void __launch_bounds__(kThreads, 2)
 k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
-            const float* __restrict__ x, const float* __restrict__ P,
+            XRows X, const float* __restrict__ P,
             const float* __restrict__ Q, const float* __restrict__ dist,
             const float* __restrict__ F, float* __restrict__ dC_part) {
     using T = Canon<LIN, LOUT>;
@@ -1088,10 +1110,11 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int64_t e = e0 + 4 * pq + q < E ? e0 + 4 * pq + q : E - 1;
-            const float* xs = x + (e * CIN + pci) * DIN;
+            const int64_t row = x_row<GATHER>(X, e);   // -1 only in the message-passing form
+            const float* xs = X.x + ((row >= 0 ? row : 0) * CIN + pci) * DIN;
             const float* gs = gy + (e * COUT + pco) * DOUT;
 #pragma unroll
-            for (int d = 0; d < DIN; ++d) xr[q][d] = xs[d];
+            for (int d = 0; d < DIN; ++d) xr[q][d] = row >= 0 ? xs[d] : 0.0f;
 #pragma unroll
             for (int d = 0; d < DOUT; ++d) gr[q][d] = gs[d];
         }
@@ -1344,8 +1367,8 @@ constexpr size_t ews_cfrag_bytes() {
     return align_up(static_cast<size_t>(K) * COUT * CIN * 2 * sizeof(_Float16), 256) + 256;
 }
 
-template <int CIN, int COUT, int LIN, int LOUT, int K>
-int launch_ews_fwd(const feq_binning& B, int64_t E, const float* x, const float* P, const float* Q,
+template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER>
+int launch_ews_fwd(const feq_binning& B, int64_t E, XRows x, const float* P, const float* Q,
                    const float* dist, const float* C, const float* F, float* y, void* ws,
                    size_t ws_bytes, hipStream_t s) {
     constexpr size_t lds = ews_fwd_lds<CIN, COUT, LIN, LOUT, K>();
@@ -1358,7 +1381,7 @@ int launch_ews_fwd(const feq_binning& B, int64_t E, const float* x, const float*
     float* inv = cv.take<float>(K);
     auto prep = k_ews_prep<K, COUT, CIN, false>;
     FEQ_LAUNCH("k_ews_prep", prep, dim3(K * COUT / 16), dim3(kThreads), 0, s, C, frag, inv);
-    auto kern = k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ>;
+    auto kern = k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, GATHER>;
     if (int rc = ews_set_lds(reinterpret_cast<const void*>(kern), lds)) return rc;
     const int64_t ntiles = ceil_div(E, kNE);
     const int64_t g = static_cast<int64_t>(ews_cus()) * occ;
@@ -1381,9 +1404,9 @@ size_t ews_bwd_ws(const feq_binning& B, int64_t E) {
            ews_cfrag_bytes<CIN, COUT, K>() + 1024;
 }
 
-template <int CIN, int COUT, int LIN, int LOUT, int K>
+template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER>
 int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const float* gy,
-                   const float* x, const float* P, const float* Q, const float* dist,
+                   XRows x, const float* P, const float* Q, const float* dist,
                    const float* C, const float* F, float* gx, float* gC, float* gF, float* gdist,
                    void* ws, size_t ws_bytes, hipStream_t s) {
     using T = Canon<LIN, LOUT>;
@@ -1405,11 +1428,11 @@ int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const f
     if (!ws || cv.used > ws_bytes) return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
     auto prep = k_ews_prep<K, CIN, COUT, true>;
     FEQ_LAUNCH("k_ews_prep", prep, dim3(K * CIN / 16), dim3(kThreads), 0, s, C, frag, inv);
-    auto kx = k_ews_bwd_x<CIN, COUT, LIN, LOUT, K>;
+    auto kx = k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, GATHER>;
     if (int rc = ews_set_lds(reinterpret_cast<const void*>(kx), xlds)) return rc;
     FEQ_LAUNCH("k_ews_bwd_x", kx, dim3(G), dim3(kThreads), xlds, s, B, E, ntiles, gy, x, P, Q,
                dist, frag, inv, F, gx, dFe);
-    auto kc = k_ews_bwd_c<CIN, COUT, LIN, LOUT, K>;
+    auto kc = k_ews_bwd_c<CIN, COUT, LIN, LOUT, K, GATHER>;
     if (int rc = ews_set_lds(reinterpret_cast<const void*>(kc), clds)) return rc;
     FEQ_LAUNCH("k_ews_bwd_c", kc, dim3(G), dim3(kThreads), clds, s, B, E, ntiles, gy, x, P, Q,
                dist, F, dCp);
@@ -1467,17 +1490,20 @@ size_t ew_split_bwd_workspace(const feq_layout& L, const feq_binning& B, int ran
 }
 
 int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* gy,
-                 const float* x, const float* P, const float* Q, const float* dist, const float* C,
-                 const float* F, float* gx, float* gC, float* gF, float* gdist, void* ws,
-                 size_t ws_bytes, hipStream_t s) {
+                 const float* x, const int64_t* src, int64_t nsrc, const float* P, const float* Q,
+                 const float* dist, const float* C, const float* F, float* gx, float* gC, float* gF,
+                 float* gdist, void* ws, size_t ws_bytes, hipStream_t s) {
     if (rank != 4 || !gx || !aligned16(gy) || !aligned16(x) || !aligned16(P) || !aligned16(Q) ||
         !aligned16(gx))
         return -1;
-#define FEQ_BWD(ci, co, li, lo)                                                                \
-    if constexpr ((ci) % 64 == 0) {                                                            \
-        if (L.cin == ci && L.cout == co && canonical(L, li, lo))                               \
-            return launch_ews_bwd<ci, co, li, lo, 4>(L, B, E, gy, x, P, Q, dist, C, F, gx, gC, \
-                                                     gF, gdist, ws, ws_bytes, s);              \
+    const XRows X{x, src, nsrc};
+#define FEQ_BWD(ci, co, li, lo)                                                                   \
+    if constexpr ((ci) % 64 == 0) {                                                               \
+        if (L.cin == ci && L.cout == co && canonical(L, li, lo))                                  \
+            return src ? launch_ews_bwd<ci, co, li, lo, 4, true>(L, B, E, gy, X, P, Q, dist, C, F, \
+                                                                 gx, gC, gF, gdist, ws, ws_bytes, s) \
+                       : launch_ews_bwd<ci, co, li, lo, 4, false>(L, B, E, gy, X, P, Q, dist, C, F, \
+                                                                  gx, gC, gF, gdist, ws, ws_bytes, s); \
     }
     FEQ_EWS_SHAPES(FEQ_BWD)
 #undef FEQ_BWD
@@ -1485,15 +1511,31 @@ int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
 }
 
 int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
-                 const float* P, const float* Q, const float* dist, const float* C, const float* F,
-                 float* y, void* ws, size_t ws_bytes, hipStream_t s) {
+                 const int64_t* src, int64_t nsrc, const float* P, const float* Q, const float* dist,
+                 const float* C, const float* F, float* y, void* ws, size_t ws_bytes, hipStream_t s) {
     if (rank != 4 || !aligned16(x) || !aligned16(P) || !aligned16(Q) || !aligned16(y)) return -1;
-#define FEQ_FWD(ci, co, li, lo)                                \
-    if (L.cin == ci && L.cout == co && canonical(L, li, lo))   \
-        return launch_ews_fwd<ci, co, li, lo, 4>(B, E, x, P, Q, dist, C, F, y, ws, ws_bytes, s);
+    const XRows X{x, src, nsrc};
+#define FEQ_FWD(ci, co, li, lo)                                                                  \
+    if (L.cin == ci && L.cout == co && canonical(L, li, lo))                                     \
+        return src ? launch_ews_fwd<ci, co, li, lo, 4, true>(B, E, X, P, Q, dist, C, F, y, ws,    \
+                                                             ws_bytes, s)                         \
+                   : launch_ews_fwd<ci, co, li, lo, 4, false>(B, E, X, P, Q, dist, C, F, y, ws,   \
+                                                              ws_bytes, s);
     FEQ_EWS_SHAPES(FEQ_FWD)
 #undef FEQ_FWD
     return -1;
+}
+
+// Shapes the split kernels (and so the message-passing entry points) serve.
+bool ew_split_supported(const feq_layout& L, const feq_binning& B, int rank, bool backward) {
+    if (rank != 4) return false;
+    bool ok = false;
+#define FEQ_SUP(ci, co, li, lo)                                                          \
+    if (L.cin == ci && L.cout == co && canonical(L, li, lo))                             \
+        ok = backward ? ((ci) % 64 == 0 && ew_tail_supported(B, 4 * L.wdim)) : true;
+    FEQ_EWS_SHAPES(FEQ_SUP)
+#undef FEQ_SUP
+    return ok;
 }
 
 }  // namespace feq

@@ -92,13 +92,16 @@ int ew_tail(const feq_layout& L, const feq_binning& B, int K, int64_t E, const f
 // Split-fp16 fast paths (edgewise_split.hip); -1 when the shape has none.
 size_t ew_split_workspace(const feq_layout& L, int rank);
 size_t ew_split_bwd_workspace(const feq_layout& L, const feq_binning& B, int rank, int64_t E);
+// src (may be NULL): message-passing form, edge e reads row src[e] of the node
+// table x (nsrc rows; indices outside [0, nsrc) read zeros).
 int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* gy,
-                 const float* x, const float* P, const float* Q, const float* dist, const float* C,
-                 const float* F, float* gx, float* gC, float* gF, float* gdist, void* ws,
-                 size_t ws_bytes, hipStream_t s);
+                 const float* x, const int64_t* src, int64_t nsrc, const float* P, const float* Q,
+                 const float* dist, const float* C, const float* F, float* gx, float* gC, float* gF,
+                 float* gdist, void* ws, size_t ws_bytes, hipStream_t s);
 int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
-                 const float* P, const float* Q, const float* dist, const float* C, const float* F,
-                 float* y, void* ws, size_t ws_bytes, hipStream_t s);
+                 const int64_t* src, int64_t nsrc, const float* P, const float* Q, const float* dist,
+                 const float* C, const float* F, float* y, void* ws, size_t ws_bytes, hipStream_t s);
+bool ew_split_supported(const feq_layout& L, const feq_binning& B, int rank, bool backward);
 
 // Kernel family of the fused edgewise layer.  The default tries the split-fp16
 // kernels, then the fp32-MFMA kernels, then the shape-generic ones;

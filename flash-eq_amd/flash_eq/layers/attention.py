@@ -104,10 +104,12 @@ class EquivariantAttention(nn.Module):
         qk = self.linear_qk(self.norm_qk(node_features))            # (N, 2 mult, dim)
         Qe = graph.gather_dst(qk[:, :mult].contiguous()).view(E, self.num_heads, -1)
         Ke = graph.gather_src(qk[:, mult:].contiguous()).view(E, self.num_heads, -1)
-        gathered = graph.gather_src(node_features)
         if edge_features is not None:
-            gathered = gathered + edge_features
-        V = self.linear_v(P, Q_basis, gathered, distances)           # (E, mult_out, dim_out)
+            gathered = graph.gather_src(node_features) + edge_features
+            V = self.linear_v(P, Q_basis, gathered, distances)       # (E, mult_out, dim_out)
+        else:
+            # x[src] gathered inside the fused layer (message-passing form)
+            V = self.linear_v(P, Q_basis, node_features.contiguous(), distances, graph=graph)
         attn = self.attention.attention_weights(Qe, Ke, graph, distances)
         if self.pool.reduce == "sum":
             perm, offsets = graph.csr()

@@ -20,7 +20,7 @@ import torch
 import torch.nn as nn
 
 from .. import _native as N
-from ..ops import edgewise_linear
+from ..ops import edgewise_linear, edgewise_linear_src, edgewise_src_supported
 from ..representations import ProductRepr, Repr
 from .radial import SeparableRadialNet
 
@@ -63,13 +63,29 @@ class EquivariantEdgewiseLinear(nn.Module):
         return N.make_binning(p1, p2, rw.num_bins, rw.log, self.solid_harmonic_scale)
 
     def forward(self, P: torch.Tensor, Q: torch.Tensor, edge_features: torch.Tensor,
-                distances: torch.Tensor) -> torch.Tensor:
+                distances: torch.Tensor, *, graph=None) -> torch.Tensor:
         """P (E, Din, Din), Q (E, Dout, Dout), edge_features (E, Cin, Din), distances (E,)
-        -> (E, Cout, Dout), all in the standard SH basis."""
+        -> (E, Cout, Dout), all in the standard SH basis.
+
+        ``graph`` (keyword, not in the reference): ``edge_features`` then holds node
+        features (N, Cin, Din) and edge e reads row ``graph.src[e]``, i.e. the layer
+        of ``graph.gather_src(edge_features)``.  Where the fused kernels have the
+        layout, the gather happens inside them and its backward is a segmented sum
+        over the graph's CSR by source; otherwise the rows are gathered first."""
         N.require_cuda_tensor(edge_features, "edge_features")
         rw = self.radial_weights
+        layout, binning = self.layout(), self.binning()
+        if graph is not None:
+            if graph.num_edges != distances.shape[0]:
+                raise ValueError(f"graph has {graph.num_edges} edges, distances {distances.shape[0]}")
+            if edgewise_src_supported(layout, binning, rw.rank):
+                perm, offsets = graph.csr_src()
+                return edgewise_linear_src(edge_features, graph.src, perm, offsets, P, Q, distances,
+                                           rw.channel_patterns, rw.radial_functions(), layout,
+                                           binning, rw.rank)
+            edge_features = graph.gather_src(edge_features)
         return edgewise_linear(edge_features, P, Q, distances, rw.channel_patterns,
-                               rw.radial_functions(), self.layout(), self.binning(), rw.rank)
+                               rw.radial_functions(), layout, binning, rw.rank)
 
     def extra_repr(self) -> str:
         rw = self.radial_weights

@@ -96,6 +96,83 @@ class EdgewiseLinearFn(torch.autograd.Function):
                 None, None, None)
 
 
+class EdgewiseLinearSrcFn(torch.autograd.Function):
+    """The message-passing form: y = layer(x[src]) with the gather inside the
+    kernels (``feq_edgewise_fwd_src``); the backward sums the per-edge input
+    gradient over every source node's edges (``perm``, ``offsets``: the CSR by
+    source), so x[src] is never materialised in either direction."""
+
+    @staticmethod
+    def forward(ctx, x, src, perm, offsets, P, Q, dist, C, F, layout: N.FeqLayout,
+                binning: N.FeqBinning, rank: int):
+        dev = _same_device(x, src, perm, offsets, P, Q, dist, C, F)
+        E = src.shape[0]
+        xs, Ps, Qs = _f32(x, "node_features"), _f32(P, "P"), _f32(Q, "Q")
+        rs, Cs, Fs = _f32(dist, "distances"), _f32(C, "channel_patterns"), _f32(F, "radial")
+        if xs.dim() != 3 or xs.shape[1:] != (layout.cin, layout.din):
+            raise ValueError(f"node_features must be (N, {layout.cin}, {layout.din}), got {tuple(xs.shape)}")
+        _check_edgewise_shapes(layout, binning, rank, torch.empty(E, layout.cin, layout.din, device="meta"),
+                               Ps, Qs, rs, Cs, Fs)
+        si = src.to(torch.int64).contiguous()
+        y = torch.empty(E, layout.cout, layout.dout, dtype=torch.float32, device=dev)
+        if E:
+            lib = N.lib()
+            ws = N.workspace(lib.feq_edgewise_fwd_workspace(N.ctypes.byref(layout),
+                                                            N.ctypes.byref(binning), rank, E), dev)
+            with torch.cuda.device(dev):
+                rc = lib.feq_edgewise_fwd_src(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
+                                              N.ptr(xs), xs.shape[0], N.ptr(si), N.ptr(Ps), N.ptr(Qs),
+                                              N.ptr(rs), N.ptr(Cs), N.ptr(Fs), N.ptr(y), N.ptr(ws),
+                                              ws.numel(), N.stream_ptr(dev))
+            N.check(rc, "feq_edgewise_fwd_src")
+        ctx.save_for_backward(xs, si, perm, offsets, Ps, Qs, rs, Cs, Fs)
+        ctx.meta = (layout, binning, rank, x.dtype, dist.dtype, C.dtype, F.dtype)
+        return y.to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, gy):
+        xs, si, perm, offsets, Ps, Qs, rs, Cs, Fs = ctx.saved_tensors
+        layout, binning, rank, xdt, rdt, cdt, fdt = ctx.meta
+        dev = xs.device
+        E = si.shape[0]
+        need = ctx.needs_input_grad
+        g = gy.detach().to(torch.float32).contiguous()
+        gxe = torch.empty(E, layout.cin, layout.din, dtype=torch.float32, device=dev)
+        gr = torch.empty_like(rs) if need[6] else None
+        gC = torch.empty_like(Cs)
+        gF = torch.empty_like(Fs)
+        lib = N.lib()
+        ws = N.workspace(lib.feq_edgewise_workspace(N.ctypes.byref(layout), N.ctypes.byref(binning),
+                                                    rank, E), dev)
+        with torch.cuda.device(dev):
+            rc = lib.feq_edgewise_bwd_src(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
+                                          N.ptr(g) if E else None, N.ptr(xs), xs.shape[0], N.ptr(si),
+                                          N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs), N.ptr(Fs),
+                                          N.ptr(gxe), N.ptr(gC), N.ptr(gF), N.ptr(gr), N.ptr(ws),
+                                          ws.numel(), N.stream_ptr(dev))
+        N.check(rc, "feq_edgewise_bwd_src")
+        gx = None
+        if need[0]:
+            gx = torch.empty_like(xs)
+            row = layout.cin * layout.din
+            with torch.cuda.device(dev):
+                rc = lib.feq_segment_sum(N.ptr(gxe) if E else None, row, N.ptr(perm) if E else None,
+                                         N.ptr(offsets), xs.shape[0], N.ptr(gx), N.stream_ptr(dev))
+            N.check(rc, "feq_segment_sum")
+            gx = gx.to(xdt)
+        return (gx, None, None, None, None, None, None if gr is None else gr.to(rdt),
+                gC.to(cdt) if need[7] else None, gF.to(fdt) if need[8] else None, None, None, None)
+
+
+def edgewise_src_supported(layout: N.FeqLayout, binning: N.FeqBinning, rank: int) -> bool:
+    """Whether ``feq_edgewise_fwd_src``/``_bwd_src`` have kernels for this layout."""
+    return bool(N.lib().feq_edgewise_src_supported(N.ctypes.byref(layout), N.ctypes.byref(binning), rank))
+
+
+def edgewise_linear_src(x, src, perm, offsets, P, Q, dist, C, F, layout, binning, rank) -> torch.Tensor:
+    return EdgewiseLinearSrcFn.apply(x, src, perm, offsets, P, Q, dist, C, F, layout, binning, rank)
+
+
 def _check_edgewise_shapes(L, b, rank, x, P, Q, r, C, F) -> None:
     E = x.shape[0]
     if x.shape != (E, L.cin, L.din):

@@ -134,6 +134,28 @@ int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32_t rank, in
                      float* grad_P, float* grad_Q,
                      void* workspace, size_t ws_bytes, feq_stream_t stream);
 
+/* ---- message-passing form of the fused layer ---------------------------------
+ * The same layer with its input gathered inside the kernels: x is a node table
+ * (num_src, Cin, Din) and edge e reads row src[e] (int64; an index outside
+ * [0, num_src) reads a zero row), i.e. feq_edgewise_fwd(x[src], ...) without
+ * materialising x[src] (reference: the x[src] gather before
+ * EquivariantEdgewiseLinear in layers/attention.py:307-310).  The backward
+ * writes the per-edge input gradient grad_x_edges (E, Cin, Din); the caller
+ * sums it over the edges of each source node (feq_segment_sum over a CSR by
+ * source).  Workspaces as for feq_edgewise_fwd/_bwd.  Only the layouts that
+ * feq_edgewise_src_supported accepts (1) have these kernels; the others return
+ * FEQ_ERR_UNSUPPORTED, and the caller gathers and calls feq_edgewise_fwd/_bwd. */
+int feq_edgewise_src_supported(const feq_layout* L, const feq_binning* b, int32_t rank);
+int feq_edgewise_fwd_src(const feq_layout* L, const feq_binning* b, int32_t rank, int64_t num_edges,
+                         const float* x, int64_t num_src, const int64_t* src, const float* P,
+                         const float* Q, const float* dist, const float* C, const float* F, float* y,
+                         void* workspace, size_t ws_bytes, feq_stream_t stream);
+int feq_edgewise_bwd_src(const feq_layout* L, const feq_binning* b, int32_t rank, int64_t num_edges,
+                         const float* grad_y, const float* x, int64_t num_src, const int64_t* src,
+                         const float* P, const float* Q, const float* dist, const float* C,
+                         const float* F, float* grad_x_edges, float* grad_C, float* grad_F,
+                         float* grad_dist, void* workspace, size_t ws_bytes, feq_stream_t stream);
+
 /* ---- Wigner-D basis ------------------------------------------------------------
  * plan: host-built per-representation constants (see feq_wigner_plan_size);
  * out (E, dim, dim): column j = column perm[j] of D(g), g e_z = dir/|dir|. */
