@@ -396,6 +396,22 @@ __device__ __forceinline__ void rotate_rows(const float (&vin)[(L + 1) * (L + 1)
     });
 }
 
+// Solid-harmonic factors.  Every term (i -> o, w) of the mixing matrix joins
+// degrees l_in(w) and l_out(w), so the forward and input-gradient kernels fold
+// the factors s^l_in of the input slots and s^l_out of the output slots into
+// the per-edge radial functions, F'_e[k, w] = F_e[k, w] s_e^(l_in(w) + l_out(w)),
+// and use the rotated rows unscaled (the channel-pattern kernel scales its rows:
+// measured faster there, its register allocation being tighter).  The powers s_e^l, l <= LIN + LOUT, of a tile's edges sit in
+// LDS; the threads filling F' serve one fixed (k, w) each (so the degree sum
+// of a thread is fixed for the launch) and the edges t / KW, t / KW + G, ...
+__device__ __forceinline__ void edge_powers(float s, int n, float* out) {
+    float p = 1.0f;
+    for (int l = 0; l < n; ++l) {
+        out[l] = p;
+        p *= s;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Forward: y = Q-rotate(s^l_out sum_k M_ek G_k), G_k = C_k fs, fs = s^l_in (x P).
 // A workgroup owns one 16-edge tile at a time; wave w owns output rows
@@ -419,6 +435,8 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
     using TG = TermGroups<LIN, LOUT, false>;
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
     constexpr int PS = DIN * DIN | 1, QS = DOUT * DOUT | 1, KWS = KW | 1;
+    constexpr int NSP = LIN + LOUT + 1, FG = kThreads / KW;
+    static_assert(KW <= kThreads, "one radial (k, w) per fill thread");
     constexpr int RPW = COUT / 64, NKS = CIN / 32, NC4 = CIN / 4;
     constexpr int KP = K;                                        // rank components per pass
     constexpr int CHUNK = 1024;                                  // bytes per fragment chunk
@@ -435,14 +453,16 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
     float* sP = reinterpret_cast<float*>(sB + BREG);
     float* sQ = sP + kNE * PS;
     float* sFe = sQ + kNE * QS;
-    float* sSout = sFe + kNE * KWS;
-    float* sInvK = sSout + kNE * DOUT;
+    float* sSout = sFe + kNE * KWS;                              // 1 / scale_e
+    float* sSp = sSout + kNE;                                    // s_e^l, l < NSP
+    float* sInvK = sSp + kNE * NSP;
     EdgeState* sE = reinterpret_cast<EdgeState*>(sInvK + K);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
     const int le = lane & 15, lg = lane >> 4;
     const unsigned pbits = off_block_bits<LIN, NPL>(), qbits = off_block_bits<LOUT, NQL>();
+    const int fkw = tid % KW, fe0 = tid / KW, fl = T::wl_of(fkw % WD);   // radial fill: fixed (k, w)
 
     if (tid < K) sInvK[tid] = Cinv[tid];   // read after the first tile barrier
 
@@ -486,29 +506,18 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
             const int e = q / NC4, c4 = q % NC4;
             const bool act = q < kNE * NC4;
             const int ee = act ? e : 0;
-            float pw[DIN];
-            slot_pow<LIN>(sE[ee].s, pw);
             float fs[4][DIN];
             rotate_cols<LIN, SP, 4>(xr[p], sP + ee * PS, fs);
             float m = 0.0f;
 #pragma unroll
             for (int r = 0; r < 4; ++r)
 #pragma unroll
-                for (int i = 0; i < DIN; ++i) {
-                    fs[r][i] *= pw[i];
-                    m = fmaxf(m, fabsf(fs[r][i]));
-                }
+                for (int i = 0; i < DIN; ++i) m = fmaxf(m, fabsf(fs[r][i]));
 #pragma unroll
             for (int off = NC4 / 2; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
             const int ex = scale_exp(m);
             const float sc = exp2i(ex);
-            if (act && c4 == 0) {
-                float po[DOUT];
-                slot_pow<LOUT>(sE[e].s, po);
-                const float inv = exp2i(-ex);
-#pragma unroll
-                for (int o = 0; o < DOUT; ++o) sSout[e * DOUT + o] = po[o] * inv;
-            }
+            if (act && c4 == 0) sSout[e] = exp2i(-ex);
             if (act) {
                 const int ks = c4 / 8, g = (c4 / 2) % 4, half = c4 % 2;
                 char* base = sB + ks * CHUNK + bslot(g, e) + 8 * half;
@@ -544,16 +553,19 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
             es.t = eb.t;
             es.s = rd / (rd + B.sh_scale);
             sE[tid] = es;
+            edge_powers(es.s, NSP, sSp + tid * NSP);
         }
         const bool dense =
             __syncthreads_or(off_block_nonzero(pr, pbits) | off_block_nonzero(qr, qbits)) != 0;
 
         // (2) radial functions of the tile (1/scale_k folded in) and fs fragments
-        for (int q = tid; q < kNE * KW; q += kThreads) {
-            const int e = q / KW, rest = q % KW;
-            const EdgeState es = sE[e];
-            const float* flo = F + static_cast<int64_t>(es.lo) * KW + rest;
-            sFe[e * KWS + rest] = lerp_bins(flo[0], flo[KW], es.t) * sInvK[rest / WD];
+        if (fe0 < FG) {
+            const float ik = sInvK[fkw / WD];
+            for (int e = fe0; e < kNE; e += FG) {
+                const EdgeState es = sE[e];
+                const float* flo = F + static_cast<int64_t>(es.lo) * KW + fkw;
+                sFe[e * KWS + fkw] = lerp_bins(flo[0], flo[KW], es.t) * ik * sSp[e * NSP + fl];
+            }
         }
         if (dense)
             produce(std::false_type{});
@@ -654,15 +666,15 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
 
         // (4) next tile's global loads, then output scaling, Q rotation and stores
         load_tile(tile + gridDim.x);
-        const float* so = sSout + le * DOUT;
         const float* qe = sQ + le * QS;
+        {
+            const float sc = sSout[le];
 #pragma unroll
-        for (int o = 0; o < DOUT; ++o) {
-            const float sc = so[o];
+            for (int o = 0; o < DOUT; ++o)
 #pragma unroll
-            for (int j = 0; j < RPW; ++j)
+                for (int j = 0; j < RPW; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) yv[j][o][r] *= sc;
+                    for (int r = 0; r < 4; ++r) yv[j][o][r] *= sc;
         }
         __syncthreads();   // every wave is done with the fragments: the buffer becomes the y stage
 #pragma unroll
@@ -705,6 +717,8 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     using TG = TermGroups<LIN, LOUT, true>;
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
     constexpr int PS = DIN * DIN | 1, QS = DOUT * DOUT | 1, KWS = KW | 1;
+    constexpr int NSP = LIN + LOUT + 1, FG = kThreads / KW;
+    static_assert(KW <= kThreads, "one radial (k, w) per fill thread");
     // One rank component per GEMM pass: measured on MI355X at 160k edges, 432 us
     // against 457 us with passes of two (whose extra A fragments and
     // accumulators spill at two workgroups per CU) and 567 us for one pass at
@@ -726,8 +740,8 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     float* sQ = sP + kNE * PS;
     float* sFe = sQ + kNE * QS;
     float* sDF = sFe + kNE * KWS;                                 // [4 waves][kNE][KW]
-    float* sSin = sDF + 4 * kNE * KW;                             // s^l_in / scale_e
-    float* sEinv = sSin + kNE * DIN;                              // 1 / scale_e
+    float* sSp = sDF + 4 * kNE * KW;                              // s_e^l, l < NSP
+    float* sEinv = sSp + kNE * NSP;                               // 1 / scale_e
     float* sInvK = sEinv + kNE;
     EdgeState* sE = reinterpret_cast<EdgeState*>(sInvK + K);
 
@@ -735,6 +749,7 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
     const int le = lane & 15, lg = lane >> 4;
     const unsigned pbits = off_block_bits<LIN, NPL>(), qbits = off_block_bits<LOUT, NQL>();
+    const int fkw = tid % KW, fe0 = tid / KW, fl = T::wl_of(fkw % WD);   // radial fill: fixed (k, w)
     if (tid < K) sInvK[tid] = Cinv[tid];
 
     // global loads of one tile: gy rows of the producer threads, x rows of the
@@ -798,30 +813,18 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             const int e = q / NC4, c4 = q % NC4;
             const bool act = q < kNE * NC4;
             const int ee = act ? e : 0;
-            float pw[DOUT];
-            slot_pow<LOUT>(sE[ee].s, pw);
             float gd[4][DOUT];
             rotate_cols<LOUT, SP, 4>(gr[p], sQ + ee * QS, gd);
             float m = 0.0f;
 #pragma unroll
             for (int r = 0; r < 4; ++r)
 #pragma unroll
-                for (int o = 0; o < DOUT; ++o) {
-                    gd[r][o] *= pw[o];
-                    m = fmaxf(m, fabsf(gd[r][o]));
-                }
+                for (int o = 0; o < DOUT; ++o) m = fmaxf(m, fabsf(gd[r][o]));
 #pragma unroll
             for (int off = NC4 / 2; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
             const int ex = scale_exp(m);
             const float sc = exp2i(ex);
-            if (act && c4 == 0) {
-                float pi[DIN];
-                slot_pow<LIN>(sE[e].s, pi);
-                const float inv = exp2i(-ex);
-                sEinv[e] = inv;
-#pragma unroll
-                for (int i = 0; i < DIN; ++i) sSin[e * DIN + i] = pi[i] * inv;
-            }
+            if (act && c4 == 0) sEinv[e] = exp2i(-ex);
             if (act) {
                 const int ks = c4 / 8, g = (c4 / 2) % 4, half = c4 % 2;
                 char* base = sB + ks * CHUNK + bslot(g, e) + 8 * half;
@@ -840,16 +843,8 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
                 }
             }
         }
-        float pi[DIN];
-        slot_pow<LIN>(sE[le].s, pi);
 #pragma unroll
-        for (int j = 0; j < RPW; ++j) {
-            rotate_cols<LIN, SP, 4>(xl[j], sP + le * PS, fsr[j]);
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-                for (int i = 0; i < DIN; ++i) fsr[j][r][i] *= pi[i];
-        }
+        for (int j = 0; j < RPW; ++j) rotate_cols<LIN, SP, 4>(xl[j], sP + le * PS, fsr[j]);
     };
 
     load_tile(blockIdx.x);
@@ -866,16 +861,19 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             es.t = eb.t;
             es.s = rd / (rd + B.sh_scale);
             sE[tid] = es;
+            edge_powers(es.s, NSP, sSp + tid * NSP);
         }
         const bool dense =
             __syncthreads_or(off_block_nonzero(pr, pbits) | off_block_nonzero(qr, qbits)) != 0;
 
         // radial functions (1/scale_k folded in), gd fragments, fs in lane layout
-        for (int q = tid; q < kNE * KW; q += kThreads) {
-            const int e = q / KW, rest = q % KW;
-            const EdgeState es = sE[e];
-            const float* flo = F + static_cast<int64_t>(es.lo) * KW + rest;
-            sFe[e * KWS + rest] = lerp_bins(flo[0], flo[KW], es.t) * sInvK[rest / WD];
+        if (fe0 < FG) {
+            const float ik = sInvK[fkw / WD];
+            for (int e = fe0; e < kNE; e += FG) {
+                const EdgeState es = sE[e];
+                const float* flo = F + static_cast<int64_t>(es.lo) * KW + fkw;
+                sFe[e * KWS + fkw] = lerp_bins(flo[0], flo[KW], es.t) * ik * sSp[e * NSP + fl];
+            }
         }
         if (dense)
             produce(std::false_type{});
@@ -1000,22 +998,20 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             });
         });
 
-        // next tile's global loads, then dx = s^l_in dfs P^T (1/scale_e folded
-        // into sSin) staged in LDS, and the dF_e sums over the waves
+        // next tile's global loads, then dx = dfs P^T / scale_e (s^l_in is in
+        // the radial functions) staged in LDS, and the dF_e sums over the waves
         load_tile(tile + gridDim.x);
         __syncthreads();   // fragments consumed, dF_e partials complete
         {
-            const float* si = sSin + le * DIN;
             const float* pe = sP + le * PS;
             asm volatile("" : "+v"(pe));   // no reuse of the P values loaded for fs
+            const float sc = sEinv[le];
 #pragma unroll
-            for (int i = 0; i < DIN; ++i) {
-                const float sc = si[i];
+            for (int i = 0; i < DIN; ++i)
 #pragma unroll
                 for (int j = 0; j < RPW; ++j)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) dfs[j][r][i] *= sc;
-            }
 #pragma unroll
             for (int j = 0; j < RPW; ++j) {
                 float vin[DIN][4], out[4 * DIN];
@@ -1031,11 +1027,15 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             }
         }
         const int nval = static_cast<int>(E - e0 < kNE ? E - e0 : kNE);
-        for (int q = tid; q < nval * KW; q += kThreads) {
-            float a = sDF[q];
+        // dF_e of the unscaled rows times s^(l_in(w) + l_out(w))
+        if (fe0 < FG) {
+            for (int e = fe0; e < nval; e += FG) {
+                const int q = e * KW + fkw;
+                float a = sDF[q];
 #pragma unroll
-            for (int v = 1; v < 4; ++v) a += sDF[v * kNE * KW + q];
-            dFe[e0 * KW + q] = a;
+                for (int v = 1; v < 4; ++v) a += sDF[v * kNE * KW + q];
+                dFe[e0 * KW + q] = a * sSp[e * NSP + fl];
+            }
         }
         __syncthreads();
         flush_stage<CIN, DIN>(reinterpret_cast<const float*>(sB), gx + e0 * CIN * DIN, nval);
@@ -1320,7 +1320,7 @@ constexpr size_t ews_bwd_x_lds() {
     constexpr size_t KW = K * T::WD, KWS = KW | 1;
     constexpr size_t FR = 2 * T::DOUT * (COUT / 32) * 1024, ST = 4 * kNE * stage_stride(CIN * T::DIN);
     return (FR > ST ? FR : ST) +
-           4 * (kNE * PS + kNE * QS + kNE * KWS + 4 * kNE * KW + kNE * T::DIN + kNE + K) +
+           4 * (kNE * PS + kNE * QS + kNE * KWS + 4 * kNE * KW + kNE * (LIN + LOUT + 1) + kNE + K) +
            kNE * sizeof(EdgeState);
 }
 
@@ -1329,7 +1329,8 @@ constexpr size_t ews_fwd_lds() {
     using T = Canon<LIN, LOUT>;
     constexpr size_t PS = T::DIN * T::DIN | 1, QS = T::DOUT * T::DOUT | 1, KWS = K * T::WD | 1;
     constexpr size_t FR = 2 * T::DIN * (CIN / 32) * 1024, ST = 4 * kNE * stage_stride(COUT * T::DOUT);
-    return (FR > ST ? FR : ST) + 4 * (kNE * PS + kNE * QS + kNE * KWS + kNE * T::DOUT + K) +
+    return (FR > ST ? FR : ST) +
+           4 * (kNE * PS + kNE * QS + kNE * KWS + kNE + kNE * (LIN + LOUT + 1) + K) +
            kNE * sizeof(EdgeState);
 }
 

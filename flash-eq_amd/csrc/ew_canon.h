@@ -70,6 +70,37 @@ struct Canon {
         return t;
     }
     static constexpr std::array<Term, NT> terms = make_terms();
+    // l_in + l_out of radial weight w: in m-block m, pair (o, i) joins degrees
+    // m + i (in) and m + o (out).
+    static constexpr std::array<int, WD> make_wl() {
+        std::array<int, WD> v{};
+        for (int m = 0; m <= MMIN; ++m)
+            for (int o = 0; o < nout(m); ++o)
+                for (int i = 0; i < nin(m); ++i) {
+                    if (m == 0) {
+                        v[w_off(m) + o * nin(m) + i] = o + i;
+                    } else {
+                        v[w_off(m) + 2 * (o * nin(m) + i)] = 2 * m + o + i;
+                        v[w_off(m) + 2 * (o * nin(m) + i) + 1] = 2 * m + o + i;
+                    }
+                }
+        return v;
+    }
+    static constexpr std::array<int, WD> wl = make_wl();
+    // wl packed 4 bits per weight, for lookups with a run-time index
+    static constexpr int NWW = (WD + 15) / 16;
+    static constexpr std::array<unsigned long long, NWW> make_wl_words() {
+        std::array<unsigned long long, NWW> w{};
+        for (int j = 0; j < WD; ++j) w[j / 16] |= static_cast<unsigned long long>(wl[j]) << (4 * (j % 16));
+        return w;
+    }
+    static constexpr std::array<unsigned long long, NWW> wl_words = make_wl_words();
+    static __device__ __forceinline__ int wl_of(int w) {
+        unsigned long long word = wl_words[0];
+#pragma unroll
+        for (int n = 1; n < NWW; ++n) word = (w >> 4) == n ? wl_words[n] : word;
+        return static_cast<int>((word >> (4 * (w & 15))) & 15u);
+    }
 };
 
 // l of every m-first component of a canonical representation with lmax L
