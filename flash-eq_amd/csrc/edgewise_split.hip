@@ -1110,11 +1110,13 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int64_t e = e0 + 4 * pq + q < E ? e0 + 4 * pq + q : E - 1;
-            const int64_t row = x_row<GATHER>(X, e);   // -1 only in the message-passing form
+            // an index outside the node table (message-passing form) reads row 0;
+            // the edge is then marked invalid, so it adds nothing either
+            const int64_t row = x_row<GATHER>(X, e);
             const float* xs = X.x + ((row >= 0 ? row : 0) * CIN + pci) * DIN;
             const float* gs = gy + (e * COUT + pco) * DOUT;
 #pragma unroll
-            for (int d = 0; d < DIN; ++d) xr[q][d] = row >= 0 ? xs[d] : 0.0f;
+            for (int d = 0; d < DIN; ++d) xr[q][d] = xs[d];
 #pragma unroll
             for (int d = 0; d < DOUT; ++d) gr[q][d] = gs[d];
         }
@@ -1128,7 +1130,7 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
         store_tile4<DOUT * DOUT, NQL, QS>(qr, sQ);
         if (tid < kNE) {
             EdgeState es;
-            es.valid = e0 + tid < E;
+            es.valid = e0 + tid < E && x_row<GATHER>(X, e0 + tid) >= 0;
             const EdgeBin eb = edge_bin(rd, B);
             es.lo = eb.lo;
             es.t = eb.t;

@@ -94,9 +94,11 @@ def test_message_passing_dispatch(dev):
 
 
 def test_message_passing_out_of_range_rows_read_zero(dev):
-    """Source indices outside [0, N) read zero rows (as feq_gather_rows): output,
-    channel-pattern and radial gradients equal those of an explicit table with a
-    zero row for them."""
+    """Source indices outside [0, N) read zero rows (as feq_gather_rows): output
+    and radial gradient equal those of an explicit table with a zero row for them
+    bit for bit; the channel-pattern kernel drops such edges instead of zeroing
+    their rows (their rows still enter its per-column fp16 scales), so its
+    gradient agrees to fp32 accuracy."""
     layer, graph, P, Q, x, r, gy = _setup(dev, [0, 1, 2], [0, 1, 2], 64, 64, N=97, E=1000, seed=4)
     N = x.shape[0]
     src = graph.src.clone()
@@ -118,7 +120,7 @@ def test_message_passing_out_of_range_rows_read_zero(dev):
     y_ref = ops.edgewise_linear(xe, P, Q, r, C, F, L, B, rw.rank)
     gC_ref, gF_ref, _ = torch.autograd.grad(y_ref, [C, F, xe], gy)
     assert torch.equal(y, y_ref)
-    assert torch.equal(gC, gC_ref)
+    assert rel_err(gC, gC_ref) < 1e-6
     assert torch.equal(gF, gF_ref)
 
 
