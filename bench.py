@@ -173,6 +173,113 @@ def copy_calibration(dev, nbytes: int = 1 << 30, reps: int = 3) -> None:
     print(f"copy calibration: {reps} copies of {nbytes} bytes", file=sys.stderr)
 
 
+def radius_graph(n: int, box: float, radius: float, kmax: int, seed: int):
+    """Uniform points in [0, box)^3; each node's neighbours within ``radius``, the
+    ``kmax`` nearest kept (ties by index), src = neighbour -> dst = centre."""
+    from scipy.spatial import cKDTree
+    g = torch.Generator().manual_seed(seed)
+    coords = torch.rand(n, 3, generator=g, dtype=torch.float32) * box
+    tree = cKDTree(coords.double().numpy())
+    d, idx = tree.query(coords.double().numpy(), k=kmax + 1, distance_upper_bound=radius)
+    idx, d = idx[:, 1:], d[:, 1:]
+    keep = np.isfinite(d)
+    dst = np.repeat(np.arange(n), kmax).reshape(n, kmax)[keep]
+    src = idx[keep]
+    return coords, torch.from_numpy(src.astype(np.int64)), torch.from_numpy(dst.astype(np.int64))
+
+
+def timed_steps(step, steps: int, warmup: int):
+    """Runs warmup + timed steps; returns (wall ms/step, event ms/step, library kernel summary)."""
+    from flash_eq import _native as NAT
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    NAT.profile_summary()
+    NAT.profile_enable(True)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    NAT.profile_enable(False)
+    return wall * 1e3 / steps, start.elapsed_time(stop) / steps, NAT.profile_summary()
+
+
+def secondary_workload(name: str, steps: int, warmup: int) -> dict:
+    """The other BASELINE configs at their full sizes (parity-test cases, reported
+    beside the metric's line): c3 = EquivariantTransformerBlock, 8 heads,
+    [0,1,2]x64, radius-10 graph capped at 32 neighbours on 20k nodes in 60^3
+    (E = 640k), fwd + bwd including WignerDBasis, fp32 or bf16; c5 = one
+    EquivariantEdgewiseLinear [0..6]x128, kNN k=32 on 5k nodes in 30^3
+    (E = 160k), bf16 edge features, fwd + bwd."""
+    import flash_eq as fe
+    dev = torch.device("cuda", 0)
+    if name.startswith("c3"):
+        dtype = torch.bfloat16 if name == "c3bf16" else torch.float32
+        coords, src, dst = radius_graph(20000, 60.0, 10.0, 32, seed=1003)
+        E, N = src.numel(), 20000
+        g = torch.Generator().manual_seed(2003)
+        feats = torch.randn(N, 64, 9, generator=g).to(dev, dtype).requires_grad_(True)
+        torch.manual_seed(3)
+        rep = fe.Repr([0, 1, 2], 64)
+        block = fe.EquivariantTransformerBlock(rep, rep, num_heads=8, max_dist=10.0).to(dev, dtype)
+        basis = fe.WignerDBasis([rep]).to(dev)
+        graph = fe.Graph(src.to(dev), dst.to(dev), N)
+        xyz = coords.to(dev)
+
+        def step():
+            vec = xyz[graph.src] - xyz[graph.dst]
+            dist = vec.norm(dim=-1)
+            (P,) = basis(vec)
+            out = block(P.to(dtype), P.to(dtype), feats, dist.to(dtype), graph)
+            SumOfSquares.apply(out.float()).backward()
+        workload = (f"c3: EquivariantTransformerBlock 8 heads [0,1,2]x64, radius-10 graph capped at "
+                    f"k=32 on 20k nodes in 60^3, E={E}, fwd+bwd incl. WignerDBasis, {dtype}")
+        work = algorithmic_per_edge([0, 1, 2], [0, 1, 2], 64, 64)
+    elif name == "c5":
+        lv = list(range(7))
+        coords, src, dst = knn_graph(5000, 32, 30.0, seed=1005)
+        E, N = src.numel(), 5000
+        g = torch.Generator().manual_seed(2005)
+        x = torch.randn(E, 128, 49, generator=g).to(dev, torch.bfloat16).requires_grad_(True)
+        torch.manual_seed(5)
+        rep = fe.Repr(lv, 128)
+        layer = fe.EquivariantEdgewiseLinear(rep, rep, num_bins=100, max_dist=10.0).to(dev)
+        xyz = coords.to(dev)
+        vec = xyz[src.to(dev)] - xyz[dst.to(dev)]
+        dist = vec.norm(dim=-1).clamp(max=10.0)
+        (P,) = fe.WignerDBasis([rep]).to(dev)(vec)
+        P = P.to(torch.bfloat16)
+
+        def step():
+            y = layer(P, P, x, dist.to(torch.bfloat16))
+            SumOfSquares.apply(y.float()).backward()
+        workload = ("c5: EquivariantEdgewiseLinear [0..6]x128 -> [0..6]x128, kNN k=32 on 5k nodes "
+                    f"in 30^3, E={E}, bf16 edge features, fwd+bwd")
+        work = algorithmic_per_edge(lv, lv, 128, 128)
+    else:
+        raise SystemExit(f"unknown workload {name}")
+    ms, ms_ev, kern = timed_steps(step, steps, warmup)
+    per_kernel = {}
+    for kname, (calls, tot) in kern.items():
+        avg = tot / calls
+        entry = {"launches": calls, "avg_ms": round(avg, 4), "ms_per_step": round(tot / steps, 4)}
+        if kname in work:
+            fl, by = work[kname]
+            entry["hbm_frac_algorithmic_fp32"] = round(by * E / (avg * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
+            entry["fp32_tflops_algorithmic"] = round(fl * E / (avg * 1e-3) / 1e12, 2)
+        per_kernel[kname] = entry
+    return {"workload": name, "config": workload, "edges": E, "nodes": N,
+            "value": round(E * steps / (ms * 1e-3) / steps, 1), "unit": "edges/s",
+            "ms_per_step": round(ms, 4), "ms_per_step_events": round(ms_ev, 4),
+            "steps": steps, "warmup": warmup, "per_kernel": per_kernel}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -184,11 +291,17 @@ def main() -> int:
     ap.add_argument("--grad-dist", action="store_true", help="also differentiate w.r.t. distances")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run 1 GiB device copies first (for rocprofv3 --pmc byte calibration)")
+    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c3bf16", "c5"],
+                    help="c2 (default) is the metric's configuration; the others print a "
+                         "secondary line with their full-size throughput and kernel times")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
               "multi-GPU path; run it with --gpus 1.", file=sys.stderr)
         return 2
+    if args.workload != "c2":
+        print(json.dumps(secondary_workload(args.workload, args.steps, args.warmup)))
+        return 0
     import flash_eq as fe
     from flash_eq import _native as NAT
 

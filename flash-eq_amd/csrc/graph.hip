@@ -1,5 +1,5 @@
-// Graph-side kernels: CSR grouping by destination, segmented sums, and the
-// per-destination edge softmax of EquivariantEdgeAttention.
+// Graph-side kernels: CSR grouping of the edges by destination (or source),
+// row gathers and segmented sums.  The attention kernels are in attention.hip.
 //
 // All edge->node reductions walk each node's edge segment in CSR order, one
 // workgroup per node, so results are deterministic and need no atomics
@@ -109,180 +109,6 @@ __global__ void k_gather_rows(const float* __restrict__ src, int64_t row,
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Block-wide per-head reduction helper: red holds kThreads partial values laid
-// out as [thread]; thread t contributes to head t % H.  Returns the reduced
-// value of head h via LDS slot res[h].
-template <bool kMax>
-__device__ void head_reduce(float v, int H, float* red, float* res) {
-    red[threadIdx.x] = v;
-    __syncthreads();
-    if (threadIdx.x < H) {
-        float a = kMax ? -INFINITY : 0.0f;
-        for (int t = threadIdx.x; t < kThreads; t += H) a = kMax ? fmaxf(a, red[t]) : a + red[t];
-        res[threadIdx.x] = a;
-    }
-    __syncthreads();
-}
-
-__global__ void __launch_bounds__(kThreads)
-k_softmax_fwd(const float* __restrict__ Q, const float* __restrict__ K,
-              const float* __restrict__ dist, int H, int Dh, float scale, float decay,
-              const int32_t* __restrict__ perm, const int32_t* __restrict__ offsets,
-              float* __restrict__ attn, float* __restrict__ qk_out) {
-    __shared__ float red[kThreads];
-    __shared__ float hmax[kThreads], hsum[kThreads];
-    const int64_t n = blockIdx.x;
-    const int b = offsets[n], cnt = offsets[n + 1] - b;
-    const int h = threadIdx.x % H;
-    const int step = kThreads / H;  // edges handled in parallel
-    const int lane_e = threadIdx.x / H;
-    const bool active = lane_e < step;
-    // pass 1: logits, running max
-    float mx = -INFINITY;
-    for (int i = lane_e; active && i < cnt; i += step) {
-        const int64_t e = perm[b + i];
-        const float* q = Q + (e * H + h) * Dh;
-        const float* k = K + (e * H + h) * Dh;
-        float acc = 0.0f;
-        for (int d = 0; d < Dh; ++d) acc += q[d] * k[d];
-        const float qk = acc * scale;
-        if (qk_out) qk_out[e * H + h] = qk;
-        float lg = qk;
-        if (decay > 0.0f) lg -= dist[e] / decay;
-        attn[e * H + h] = lg;  // logits staged in the output buffer
-        mx = fmaxf(mx, lg);
-    }
-    head_reduce<true>(active ? mx : -INFINITY, H, red, hmax);
-    const float m = hmax[h];
-    // pass 2: sum of exponentials
-    float s = 0.0f;
-    for (int i = lane_e; active && i < cnt; i += step) {
-        const int64_t e = perm[b + i];
-        s += expf(attn[e * H + h] - m);
-    }
-    head_reduce<false>(active ? s : 0.0f, H, red, hsum);
-    const float denom = hsum[h] + 1e-8f;
-    // pass 3: normalise
-    for (int i = lane_e; active && i < cnt; i += step) {
-        const int64_t e = perm[b + i];
-        attn[e * H + h] = expf(attn[e * H + h] - m) / denom;
-    }
-}
-
-__global__ void __launch_bounds__(kThreads)
-k_softmax_bwd(const float* __restrict__ Q, const float* __restrict__ K,
-              const float* __restrict__ attn, const float* __restrict__ gattn, int H, int Dh,
-              float scale, float decay, const int32_t* __restrict__ perm,
-              const int32_t* __restrict__ offsets, float* __restrict__ gQ, float* __restrict__ gK,
-              float* __restrict__ gls, float* __restrict__ gdist) {
-    __shared__ float red[kThreads];
-    __shared__ float hdot[kThreads];
-    __shared__ float eacc[kThreads];
-    const int64_t n = blockIdx.x;
-    const int b = offsets[n], cnt = offsets[n + 1] - b;
-    const int h = threadIdx.x % H;
-    const int step = kThreads / H;
-    const int lane_e = threadIdx.x / H;
-    const bool active = lane_e < step;
-    float s = 0.0f;
-    for (int i = lane_e; active && i < cnt; i += step) {
-        const int64_t e = perm[b + i];
-        s += attn[e * H + h] * gattn[e * H + h];
-    }
-    head_reduce<false>(active ? s : 0.0f, H, red, hdot);
-    const float S = hdot[h];
-    // per edge: glogit, gQ, gK; per-edge sums over heads go through eacc
-    for (int i0 = 0; i0 < cnt; i0 += step) {
-        const int i = i0 + lane_e;
-        float ls_part = 0.0f, gd_part = 0.0f;
-        if (active && i < cnt) {
-            const int64_t e = perm[b + i];
-            const float a = attn[e * H + h];
-            const float gl = a * (gattn[e * H + h] - S);
-            const float* q = Q + (e * H + h) * Dh;
-            const float* k = K + (e * H + h) * Dh;
-            float* gq = gQ + (e * H + h) * Dh;
-            float* gk = gK + (e * H + h) * Dh;
-            float dot = 0.0f;
-            for (int d = 0; d < Dh; ++d) {
-                const float qd = q[d], kd = k[d];
-                dot += qd * kd;
-                gq[d] = gl * scale * kd;
-                gk[d] = gl * scale * qd;
-            }
-            ls_part = gl * dot * scale;
-            gd_part = decay > 0.0f ? -gl / decay : 0.0f;
-        }
-        if (gls || gdist) {
-            // sum the H heads of each edge (threads lane_e*H .. lane_e*H+H-1)
-            red[threadIdx.x] = ls_part;
-            eacc[threadIdx.x] = gd_part;
-            __syncthreads();
-            if (threadIdx.x < step && i0 + threadIdx.x < cnt) {
-                const int64_t e = perm[b + i0 + threadIdx.x];
-                float a1 = 0.0f, a2 = 0.0f;
-                for (int hh = 0; hh < H; ++hh) {
-                    a1 += red[threadIdx.x * H + hh];
-                    a2 += eacc[threadIdx.x * H + hh];
-                }
-                if (gls) gls[e] = a1;
-                if (gdist) gdist[e] = a2;
-            }
-            __syncthreads();
-        }
-    }
-}
-
-__global__ void __launch_bounds__(kThreads)
-k_attn_pool_fwd(const float* __restrict__ V, const float* __restrict__ attn, int mult, int dim,
-                int H, const int32_t* __restrict__ perm, const int32_t* __restrict__ offsets,
-                float* __restrict__ out) {
-    const int64_t n = blockIdx.x;
-    const int b = offsets[n], e_end = offsets[n + 1];
-    const int row = mult * dim;
-    const int hd = mult / H;
-    for (int c = threadIdx.x; c < row; c += kThreads) {
-        const int h = (c / dim) / hd;
-        float acc = 0.0f;
-        for (int i = b; i < e_end; ++i) {
-            const int64_t e = perm[i];
-            acc += attn[e * H + h] * V[e * row + c];
-        }
-        out[n * row + c] = acc;
-    }
-}
-
-__global__ void __launch_bounds__(kThreads)
-k_attn_pool_bwd(const float* __restrict__ V, const float* __restrict__ attn,
-                const float* __restrict__ gout, const int64_t* __restrict__ dst, int64_t N,
-                int mult, int dim, int H, float* __restrict__ gV, float* __restrict__ gattn) {
-    __shared__ float red[kThreads];
-    const int64_t e = blockIdx.x;
-    const int64_t d = dst[e];
-    const bool ok = d >= 0 && d < N;
-    const int row = mult * dim;
-    const int hd = mult / H;
-    const int per_head = hd * dim;  // contiguous elements of one head
-    for (int h = 0; h < H; ++h) {
-        float part = 0.0f;
-        const float a = attn[e * H + h];
-        for (int c = threadIdx.x; c < per_head; c += kThreads) {
-            const int64_t q = static_cast<int64_t>(h) * per_head + c;
-            const float g = ok ? gout[d * row + q] : 0.0f;
-            gV[e * row + q] = a * g;
-            part += V[e * row + q] * g;
-        }
-        red[threadIdx.x] = part;
-        __syncthreads();
-        for (int s = kThreads / 2; s > 0; s >>= 1) {
-            if (threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
-            __syncthreads();
-        }
-        if (threadIdx.x == 0) gattn[e * H + h] = red[0];
-        __syncthreads();
-    }
-}
-
 }  // namespace
 }  // namespace feq
 
@@ -367,69 +193,5 @@ extern "C" int feq_gather_rows(const float* src, int64_t nsrc, int64_t row, cons
     }
     FEQ_LAUNCH("k_gather_rows", k_gather_rows, dim3(nrows), dim3(row < 256 ? 64 : 256), 0,
                        stream_of(stream), src, row, idx, nrows, nsrc, out);
-    return FEQ_OK;
-}
-
-// Thread t of a node's workgroup serves head t % H of edge slot t / H; with H
-// not dividing kThreads the last partial slot idles and feeds neutral values
-// to the head reductions, so any 1 <= H <= kThreads works.
-static int check_heads(int32_t H, int32_t Dh) {
-    if (H < 1 || H > kThreads)
-        return fail(FEQ_ERR_UNSUPPORTED, "num_heads must be in [1, %d]", kThreads);
-    if (Dh < 1) return fail(FEQ_ERR_INVALID, "head dim must be positive");
-    return FEQ_OK;
-}
-
-extern "C" int feq_edge_softmax_fwd(const float* Q, const float* K, const float* dist, int64_t E,
-                                    int32_t H, int32_t Dh, float scale, float decay,
-                                    const int32_t* perm, const int32_t* offsets, int64_t N,
-                                    float* attn, float* qk_out, feq_stream_t stream) {
-    if (int rc = check_heads(H, Dh)) return rc;
-    if (E < 0 || N < 1) return fail(FEQ_ERR_INVALID, "invalid graph sizes");
-    if (E == 0) return FEQ_OK;
-    if (!Q || !K || !perm || !offsets || !attn) return fail(FEQ_ERR_INVALID, "NULL pointer");
-    if (decay > 0.0f && !dist) return fail(FEQ_ERR_INVALID, "distance decay needs distances");
-    FEQ_LAUNCH("k_softmax_fwd", k_softmax_fwd, dim3(N), dim3(kThreads), 0, stream_of(stream), Q, K, dist, H,
-                       Dh, scale, decay, perm, offsets, attn, qk_out);
-    return FEQ_OK;
-}
-
-extern "C" int feq_edge_softmax_bwd(const float* Q, const float* K, const float* attn,
-                                    const float* gattn, int64_t E, int32_t H, int32_t Dh,
-                                    float scale, float decay, const int32_t* perm,
-                                    const int32_t* offsets, int64_t N, float* gQ, float* gK,
-                                    float* gls, float* gdist, feq_stream_t stream) {
-    if (int rc = check_heads(H, Dh)) return rc;
-    if (E < 0 || N < 1) return fail(FEQ_ERR_INVALID, "invalid graph sizes");
-    if (E == 0) return FEQ_OK;
-    if (!Q || !K || !attn || !gattn || !perm || !offsets || !gQ || !gK)
-        return fail(FEQ_ERR_INVALID, "NULL pointer");
-    FEQ_LAUNCH("k_softmax_bwd", k_softmax_bwd, dim3(N), dim3(kThreads), 0, stream_of(stream), Q, K, attn,
-                       gattn, H, Dh, scale, decay, perm, offsets, gQ, gK, gls, gdist);
-    return FEQ_OK;
-}
-
-extern "C" int feq_attn_pool_fwd(const float* V, const float* attn, int64_t E, int32_t mult,
-                                 int32_t dim, int32_t H, const int32_t* perm,
-                                 const int32_t* offsets, int64_t N, float* out,
-                                 feq_stream_t stream) {
-    if (H < 1 || mult % H) return fail(FEQ_ERR_INVALID, "num_heads must divide mult");
-    if (E < 0 || N < 1 || dim < 1) return fail(FEQ_ERR_INVALID, "invalid sizes");
-    if (!offsets || !out) return fail(FEQ_ERR_INVALID, "NULL pointer");
-    FEQ_LAUNCH("k_attn_pool_fwd", k_attn_pool_fwd, dim3(N), dim3(kThreads), 0, stream_of(stream), V, attn,
-                       mult, dim, H, perm, offsets, out);
-    return FEQ_OK;
-}
-
-extern "C" int feq_attn_pool_bwd(const float* V, const float* attn, const float* gout,
-                                 const int64_t* dst, int64_t E, int64_t N, int32_t mult,
-                                 int32_t dim, int32_t H, float* gV, float* gattn,
-                                 feq_stream_t stream) {
-    if (H < 1 || mult % H) return fail(FEQ_ERR_INVALID, "num_heads must divide mult");
-    if (E < 0 || dim < 1) return fail(FEQ_ERR_INVALID, "invalid sizes");
-    if (E == 0) return FEQ_OK;
-    if (!V || !attn || !gout || !dst || !gV || !gattn) return fail(FEQ_ERR_INVALID, "NULL pointer");
-    FEQ_LAUNCH("k_attn_pool_bwd", k_attn_pool_bwd, dim3(E), dim3(kThreads), 0, stream_of(stream), V, attn,
-                       gout, dst, N, mult, dim, H, gV, gattn);
     return FEQ_OK;
 }

@@ -1,8 +1,11 @@
 """Equivariant graph attention (drop-in for ``flash_eq/layers/attention.py``).
 
 * logits and the per-destination softmax (``attention.py:92-141``) run in one
-  HIP kernel per node segment (``feq_edge_softmax_fwd``): max shift,
+  HIP kernel over the node segments (``feq_attn_softmax_fwd``): max shift,
   exponentials, the ``+1e-8`` denominator, in CSR order without atomics;
+  ``EquivariantAttention`` reads Q and K straight from the node table of its
+  fused QK projection (the gathers of ``attention.py:298-304`` happen inside
+  the kernels, so no (E, H, Dh) tensor is formed);
 * ``EquivariantAttention`` fuses the head weighting of V with the sum pooling
   (``attention.py:143-167`` + ``pooling.py:21-30``) in ``feq_attn_pool_fwd``, so
   the weighted (E, mult, dim) tensor is never written;
@@ -15,7 +18,7 @@ import torch.nn as nn
 
 from .. import _native as N
 from ..graph import Graph
-from ..ops import AttnPoolFn, EdgeSoftmaxFn
+from ..ops import AttnPoolFn, EdgeSoftmaxFn, NodeSoftmaxFn
 from ..representations import Repr
 from .linear import EquivariantEdgewiseLinear, EquivariantLinear
 from .norm import EquivariantLayerNorm
@@ -47,6 +50,20 @@ class EquivariantEdgeAttention(nn.Module):
             self.distance_decay_scale is not None and distances is not None) else 0.0
         attn = EdgeSoftmaxFn.apply(Q, K, distances if decay > 0 else None, self.log_scale, decay,
                                    perm, offsets, graph.num_nodes)
+        return self.dropout(attn)
+
+    def node_attention_weights(self, qk: torch.Tensor, graph: Graph,
+                               distances: torch.Tensor | None = None) -> torch.Tensor:
+        """The same weights (E, H) with Q = qk[dst, :mult] and K = qk[src, mult:]
+        read from the (N, 2 mult, dim) node table inside the kernels."""
+        N.require_cuda_tensor(qk, "qk")
+        perm, offsets = graph.csr()
+        perm_s, offsets_s = graph.csr_src()
+        decay = float(self.distance_decay_scale) if (
+            self.distance_decay_scale is not None and distances is not None) else 0.0
+        attn = NodeSoftmaxFn.apply(qk, distances if decay > 0 else None, self.log_scale, decay,
+                                   self.num_heads, graph.src, graph.dst, perm, offsets, perm_s,
+                                   offsets_s, graph.num_nodes)
         return self.dropout(attn)
 
     def forward(self, Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, graph: Graph,
@@ -99,18 +116,14 @@ class EquivariantAttention(nn.Module):
                 distances: torch.Tensor, graph: Graph,
                 edge_features: torch.Tensor | None = None) -> torch.Tensor:
         """node_features (N, mult_in, dim_in) -> (N, mult_out, dim_out)."""
-        E = graph.num_edges
-        mult = self.in_repr.mult
         qk = self.linear_qk(self.norm_qk(node_features))            # (N, 2 mult, dim)
-        Qe = graph.gather_dst(qk[:, :mult].contiguous()).view(E, self.num_heads, -1)
-        Ke = graph.gather_src(qk[:, mult:].contiguous()).view(E, self.num_heads, -1)
         if edge_features is not None:
             gathered = graph.gather_src(node_features) + edge_features
             V = self.linear_v(P, Q_basis, gathered, distances)       # (E, mult_out, dim_out)
         else:
             # x[src] gathered inside the fused layer (message-passing form)
             V = self.linear_v(P, Q_basis, node_features.contiguous(), distances, graph=graph)
-        attn = self.attention.attention_weights(Qe, Ke, graph, distances)
+        attn = self.attention.node_attention_weights(qk, graph, distances)
         if self.pool.reduce == "sum":
             perm, offsets = graph.csr()
             return AttnPoolFn.apply(V, attn, graph.dst, perm, offsets, graph.num_nodes,

@@ -315,33 +315,36 @@ def gather_rows(x, idx, perm, offsets) -> torch.Tensor:
 
 
 class EdgeSoftmaxFn(torch.autograd.Function):
-    """Per-destination softmax of scale*<Q,K> (- r/decay) with +1e-8 (``attention.py:92-141``)."""
+    """Per-destination softmax of scale*<Q,K> (- r/decay) with +1e-8 (``attention.py:92-141``),
+    for edge-level Q, K (E, H, Dh) (the edge form of ``feq_attn_softmax_fwd``)."""
 
     @staticmethod
     def forward(ctx, Q, K, dist, log_scale, decay: float, perm, offsets, num_nodes: int):
         dev = _same_device(Q, K, log_scale, perm, offsets)
         Qs, Ks = _f32(Q, "Q"), _f32(K, "K")
         E, H, Dh = Qs.shape
+        if Ks.shape != Qs.shape:
+            raise ValueError(f"Q and K shapes differ: {tuple(Qs.shape)} and {tuple(Ks.shape)}")
         scale_t = log_scale.detach().float().exp()
         rs = _f32(dist, "distances") if (dist is not None and decay > 0) else None
         attn = torch.empty(E, H, dtype=torch.float32, device=dev)
         qk = torch.empty(E, H, dtype=torch.float32, device=dev)
         if E:
-            scale = _host_scalar(scale_t)
             with torch.cuda.device(dev):
-                rc = N.lib().feq_edge_softmax_fwd(N.ptr(Qs), N.ptr(Ks), N.ptr(rs), E, H, Dh, scale,
+                rc = N.lib().feq_attn_softmax_fwd(N.ptr(Qs), H * Dh, N.ptr(Ks), H * Dh, None, None,
+                                                  E, N.ptr(rs), E, H, Dh, _host_scalar(scale_t),
                                                   float(decay), N.ptr(perm), N.ptr(offsets),
                                                   num_nodes, N.ptr(attn), N.ptr(qk),
                                                   N.stream_ptr(dev))
-            N.check(rc, "feq_edge_softmax_fwd")
-        ctx.save_for_backward(Qs, Ks, attn, perm, offsets, scale_t)
+            N.check(rc, "feq_attn_softmax_fwd")
+        ctx.save_for_backward(Qs, Ks, attn, qk, perm, offsets, scale_t)
         ctx.meta = (decay, num_nodes, Q.dtype, K.dtype, None if dist is None else dist.dtype,
                     log_scale.dtype)
         return attn.to(Q.dtype)
 
     @staticmethod
     def backward(ctx, gattn):
-        Qs, Ks, attn, perm, offsets, scale_t = ctx.saved_tensors
+        Qs, Ks, attn, qk, perm, offsets, scale_t = ctx.saved_tensors
         decay, num_nodes, qdt, kdt, rdt, ldt = ctx.meta
         dev = Qs.device
         E, H, Dh = Qs.shape
@@ -349,21 +352,92 @@ class EdgeSoftmaxFn(torch.autograd.Function):
         ga = gattn.detach().to(torch.float32).contiguous()
         gQ = torch.empty_like(Qs)
         gK = torch.empty_like(Ks)
-        gls = torch.empty(E, dtype=torch.float32, device=dev)
-        gr = torch.empty(E, dtype=torch.float32, device=dev) if (need[2] and decay > 0) else None
+        glog = torch.empty(E, H, dtype=torch.float32, device=dev)
         if E:
             with torch.cuda.device(dev):
-                rc = N.lib().feq_edge_softmax_bwd(N.ptr(Qs), N.ptr(Ks), N.ptr(attn), N.ptr(ga), E, H,
+                rc = N.lib().feq_attn_softmax_bwd(N.ptr(Qs), H * Dh, N.ptr(Ks), H * Dh, None, None,
+                                                  E, N.ptr(attn), N.ptr(ga), E, H, Dh,
+                                                  _host_scalar(scale_t), N.ptr(perm),
+                                                  N.ptr(offsets), num_nodes, None, None,
+                                                  N.ptr(gQ), H * Dh, N.ptr(gK), H * Dh,
+                                                  N.ptr(glog), N.stream_ptr(dev))
+            N.check(rc, "feq_attn_softmax_bwd")
+        return (gQ.to(qdt), gK.to(kdt), *_softmax_scalar_grads(glog, qk, need[2], need[3], decay,
+                                                                 rdt, ldt),
+                None, None, None, None)
+
+
+def _softmax_scalar_grads(glog, qk, need_dist: bool, need_scale: bool, decay: float, rdt, ldt):
+    """Distance and log-scale gradients from the logit gradient (E, H):
+    d logit / d r = -1/decay, d logit / d log_scale = scale <Q,K> = qk."""
+    g_dist = (glog.sum(1) * (-1.0 / decay)).to(rdt) if (need_dist and decay > 0) else None
+    g_log = (glog * qk).sum().to(ldt) if need_scale else None
+    return g_dist, g_log
+
+
+class NodeSoftmaxFn(torch.autograd.Function):
+    """The same softmax with Q and K read from the node table of the fused QK
+    projection (``attention.py:298-304``): qk (N, 2 mult, dim), Q = channels
+    [0, mult) read at dst[e], K = channels [mult, 2 mult) read at src[e], H
+    heads of (mult / H) * dim values.  The gathers run inside the kernels (node
+    form of ``feq_attn_softmax_fwd``), so the (E, H, Dh) Q and K are never
+    formed; the backward sums the Q gradient per destination and the K
+    gradient per source (CSR by source), writing the (N, 2 mult, dim) gradient."""
+
+    @staticmethod
+    def forward(ctx, qk, dist, log_scale, decay: float, heads: int, src, dst, perm, offsets,
+                perm_s, offsets_s, num_nodes: int):
+        dev = _same_device(qk, log_scale, src, dst, perm, offsets, perm_s, offsets_s)
+        qs = _f32(qk, "qk")
+        src = src.to(torch.int64).contiguous()
+        dst = dst.to(torch.int64).contiguous()
+        Nn, two_mult, dim = qs.shape
+        mult = two_mult // 2
+        if two_mult != 2 * mult or mult % heads:
+            raise ValueError(f"qk must be (N, 2*mult, dim) with heads | mult, got {tuple(qs.shape)}")
+        E = src.shape[0]
+        Dh, ld = mult // heads * dim, two_mult * dim
+        scale_t = log_scale.detach().float().exp()
+        rs = _f32(dist, "distances") if (dist is not None and decay > 0) else None
+        attn = torch.empty(E, heads, dtype=torch.float32, device=dev)
+        qkv = torch.empty(E, heads, dtype=torch.float32, device=dev)
+        if E:
+            with torch.cuda.device(dev):
+                rc = N.lib().feq_attn_softmax_fwd(N.ptr(qs), ld, N.ptr(qs) + 4 * mult * dim, ld,
+                                                  N.ptr(dst), N.ptr(src), Nn, N.ptr(rs), E, heads,
                                                   Dh, _host_scalar(scale_t), float(decay),
                                                   N.ptr(perm), N.ptr(offsets), num_nodes,
-                                                  N.ptr(gQ), N.ptr(gK), N.ptr(gls), N.ptr(gr),
-                                                  N.stream_ptr(dev))
-            N.check(rc, "feq_edge_softmax_bwd")
-        g_log = gls.sum().to(ldt) if need[3] else None
-        g_dist = None
-        if need[2]:
-            g_dist = gr.to(rdt) if gr is not None else None
-        return gQ.to(qdt), gK.to(kdt), g_dist, g_log, None, None, None, None
+                                                  N.ptr(attn), N.ptr(qkv), N.stream_ptr(dev))
+            N.check(rc, "feq_attn_softmax_fwd")
+        ctx.save_for_backward(qs, attn, qkv, src, dst, perm, offsets, perm_s, offsets_s, scale_t)
+        ctx.meta = (decay, num_nodes, heads, qk.dtype, None if dist is None else dist.dtype,
+                    log_scale.dtype)
+        return attn.to(qk.dtype)
+
+    @staticmethod
+    def backward(ctx, gattn):
+        qs, attn, qkv, src, dst, perm, offsets, perm_s, offsets_s, scale_t = ctx.saved_tensors
+        decay, num_nodes, heads, qdt, rdt, ldt = ctx.meta
+        dev = qs.device
+        Nn, two_mult, dim = qs.shape
+        mult = two_mult // 2
+        E = src.shape[0]
+        Dh, ld = mult // heads * dim, two_mult * dim
+        need = ctx.needs_input_grad
+        ga = gattn.detach().to(torch.float32).contiguous()
+        gqk = torch.empty_like(qs)
+        glog = torch.empty(E, heads, dtype=torch.float32, device=dev)
+        with torch.cuda.device(dev):
+            rc = N.lib().feq_attn_softmax_bwd(N.ptr(qs), ld, N.ptr(qs) + 4 * mult * dim, ld,
+                                              N.ptr(dst), N.ptr(src), Nn, N.ptr(attn), N.ptr(ga),
+                                              E, heads, Dh, _host_scalar(scale_t), N.ptr(perm),
+                                              N.ptr(offsets), num_nodes, N.ptr(perm_s),
+                                              N.ptr(offsets_s), N.ptr(gqk), ld,
+                                              N.ptr(gqk) + 4 * mult * dim, ld, N.ptr(glog),
+                                              N.stream_ptr(dev))
+        N.check(rc, "feq_attn_softmax_bwd")
+        g_dist, g_log = _softmax_scalar_grads(glog, qkv, need[1], need[2], decay, rdt, ldt)
+        return (gqk.to(qdt), g_dist, g_log, None, None, None, None, None, None, None, None, None)
 
 
 def _host_scalar(t: torch.Tensor) -> float:
@@ -386,13 +460,13 @@ class AttnPoolFn(torch.autograd.Function):
                                            mult, dim, heads, N.ptr(perm) if E else None,
                                            N.ptr(offsets), num_nodes, N.ptr(out), N.stream_ptr(dev))
         N.check(rc, "feq_attn_pool_fwd")
-        ctx.save_for_backward(Vs, As, dst)
+        ctx.save_for_backward(Vs, As, perm, offsets)
         ctx.meta = (num_nodes, heads, V.dtype, attn.dtype)
         return out.to(V.dtype)
 
     @staticmethod
     def backward(ctx, gout):
-        Vs, As, dst = ctx.saved_tensors
+        Vs, As, perm, offsets = ctx.saved_tensors
         num_nodes, heads, vdt, adt = ctx.meta
         dev = Vs.device
         E, mult, dim = Vs.shape
@@ -400,11 +474,10 @@ class AttnPoolFn(torch.autograd.Function):
         gV = torch.empty_like(Vs)
         gA = torch.empty_like(As)
         if E:
-            d64 = dst.to(torch.int64).contiguous()
             with torch.cuda.device(dev):
-                rc = N.lib().feq_attn_pool_bwd(N.ptr(Vs), N.ptr(As), N.ptr(g), N.ptr(d64), E,
-                                               num_nodes, mult, dim, heads, N.ptr(gV), N.ptr(gA),
-                                               N.stream_ptr(dev))
+                rc = N.lib().feq_attn_pool_bwd(N.ptr(Vs), N.ptr(As), N.ptr(g), N.ptr(perm),
+                                               N.ptr(offsets), E, num_nodes, mult, dim, heads,
+                                               N.ptr(gV), N.ptr(gA), N.stream_ptr(dev))
             N.check(rc, "feq_attn_pool_bwd")
         return gV.to(vdt), gA.to(adt), None, None, None, None, None
 

@@ -28,8 +28,10 @@
  *                            ops of pooling.py:21-30 / attention.py:124-141 imply
  *   feq_segment_sum          GraphPooling 'sum' forward (flash_eq/layers/pooling.py:21-30)
  *   feq_gather_rows          its backward (index_select of the node gradient)
- *   feq_edge_softmax_fwd/bwd EquivariantEdgeAttention logits + _neighbor_softmax
- *                            (flash_eq/layers/attention.py:92-141)
+ *   feq_attn_softmax_fwd/bwd EquivariantEdgeAttention logits + _neighbor_softmax
+ *                            (flash_eq/layers/attention.py:92-141), with the Q/K
+ *                            gathers of EquivariantAttention.forward
+ *                            (attention.py:298-304) inside the kernels
  *   feq_attn_pool_fwd/bwd    _apply_attention + GraphPooling 'sum'
  *                            (flash_eq/layers/attention.py:143-167, pooling.py:21-30)
  */
@@ -178,27 +180,48 @@ int feq_segment_sum(const float* x, int64_t row, const int32_t* perm, const int3
 int feq_gather_rows(const float* src, int64_t num_src, int64_t row, const int64_t* idx,
                     int64_t num_rows, float* out, feq_stream_t stream);
 
-/* logits[e,h] = scale * <Q[e,h,:], K[e,h,:]> - dist[e]/decay (decay <= 0: none);
- * attn = per-destination softmax with max shift and +1e-8 in the denominator.
- * Q, K (E, H, Dh).  logits_out may be NULL. */
-int feq_edge_softmax_fwd(const float* Q, const float* K, const float* dist, int64_t num_edges,
-                         int32_t heads, int32_t head_dim, float scale, float decay,
-                         const int32_t* perm, const int32_t* offsets, int64_t num_nodes,
-                         float* attn, float* qk_out, feq_stream_t stream);
-/* Given grad_attn (E,H): grad_Q, grad_K (E,H,Dh); grad_logscale_partial (E) holds
- * sum_h glogit*scale*<Q,K> per edge (nullable); grad_dist (nullable). */
-int feq_edge_softmax_bwd(const float* Q, const float* K, const float* attn, const float* grad_attn,
-                         int64_t num_edges, int32_t heads, int32_t head_dim, float scale, float decay,
-                         const int32_t* perm, const int32_t* offsets, int64_t num_nodes,
-                         float* grad_Q, float* grad_K, float* grad_logscale_partial,
-                         float* grad_dist, feq_stream_t stream);
+/* Attention over head-major rows: a row of Q, K or V holds heads*head_dim floats,
+ * head h at offset h*head_dim; row r of a table T starts at T + r*ld (floats).
+ * Edges are visited in the CSR by destination (perm, offsets, num_nodes);
+ * edges whose destination lies outside [0, num_nodes) get zero weights and
+ * gradients.  Two forms:
+ *   edge form (q_idx = k_idx = NULL): edge e reads row e of Q and of K;
+ *   node form (q_idx = dst, k_idx = src): edge e reads row dst[e] of the node
+ *     table Q (num_nodes rows) and row k_idx[e] of the node table K (num_k rows;
+ *     an index outside [0, num_k) reads a zero row) -- the gathers of
+ *     attention.py:298-304 done inside the kernels.
+ * logits[e,h] = scale <Q_h, K_h> - dist[e]/decay (decay <= 0: no decay term);
+ * attn = per-destination softmax with max shift and +1e-8 in the denominator
+ * (attention.py:92-141).  qk_out (E, heads; nullable) receives scale <Q_h, K_h>.
+ * Limit: head_dim <= 16 * V * 64 / NG, NG = next power of two >= heads (at most
+ * 64), V = 4 when every row start is 16-byte aligned, else 1. */
+int feq_attn_softmax_fwd(const float* Q, int64_t ldq, const float* K, int64_t ldk,
+                         const int64_t* q_idx, const int64_t* k_idx, int64_t num_k,
+                         const float* dist, int64_t num_edges, int32_t heads, int32_t head_dim,
+                         float scale, float decay, const int32_t* perm, const int32_t* offsets,
+                         int64_t num_nodes, float* attn, float* qk_out, feq_stream_t stream);
+/* Given grad_attn (E, heads): grad_logits (E, heads) = attn (grad_attn - S), S the
+ * per-destination sum of attn*grad_attn (the caller forms the log-scale gradient
+ * sum(grad_logits*qk) and the distance gradient -sum_h grad_logits/decay from it).
+ * Edge form: grad_Q[e], grad_K[e] (E rows).  Node form: grad_Q (num_nodes rows)
+ * and grad_K (num_k rows) summed per node, every row written; grad_K walks the
+ * CSR of the edges by k_idx (perm_k, offsets_k). */
+int feq_attn_softmax_bwd(const float* Q, int64_t ldq, const float* K, int64_t ldk,
+                         const int64_t* q_idx, const int64_t* k_idx, int64_t num_k,
+                         const float* attn, const float* grad_attn, int64_t num_edges,
+                         int32_t heads, int32_t head_dim, float scale, const int32_t* perm,
+                         const int32_t* offsets, int64_t num_nodes, const int32_t* perm_k,
+                         const int32_t* offsets_k, float* grad_Q, int64_t ldgq, float* grad_K,
+                         int64_t ldgk, float* grad_logits, feq_stream_t stream);
 /* out[n,c,:] = sum_{e in seg(n)} attn[e, c / (mult/H)] * V[e,c,:]; V (E, mult, dim). */
 int feq_attn_pool_fwd(const float* V, const float* attn, int64_t num_edges, int32_t mult,
                       int32_t dim, int32_t heads, const int32_t* perm, const int32_t* offsets,
                       int64_t num_nodes, float* out, feq_stream_t stream);
-/* grad_V[e] = attn[e,h(c)] * gout[dst[e]]; grad_attn[e,h] = sum_{c in h, d} V*gout[dst]. */
-int feq_attn_pool_bwd(const float* V, const float* attn, const float* grad_out, const int64_t* dst,
-                      int64_t num_edges, int64_t num_nodes, int32_t mult, int32_t dim, int32_t heads,
+/* grad_V[e] = attn[e,h(c)] * gout[dst[e]]; grad_attn[e,h] = sum_{c in h, d} V*gout[dst],
+ * walking the CSR by destination (gout[n] read once per node). */
+int feq_attn_pool_bwd(const float* V, const float* attn, const float* grad_out,
+                      const int32_t* perm, const int32_t* offsets, int64_t num_edges,
+                      int64_t num_nodes, int32_t mult, int32_t dim, int32_t heads,
                       float* grad_V, float* grad_attn, feq_stream_t stream);
 
 #ifdef __cplusplus
