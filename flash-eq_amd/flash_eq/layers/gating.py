@@ -6,7 +6,7 @@ import torch.nn as nn
 
 from ..representations import Repr
 from ..utils import init_linear_weights
-from .norm import RepNorm
+from .norm import RepNorm, irrep_expand, irrep_slices
 
 
 class EquivariantGating(nn.Module):
@@ -20,6 +20,7 @@ class EquivariantGating(nn.Module):
         self.linear = nn.Linear(width, width)
         self.register_buffer("ix", torch.tensor(repr.indices(), dtype=torch.long))
         self.outdims = (repr.mult, repr.nreps())
+        self._slices = irrep_slices(repr)
         self.activation = nn.Sigmoid()
         self.apply(init_linear_weights)
 
@@ -27,4 +28,4 @@ class EquivariantGating(nn.Module):
         norms = self.norm(st)
         *batch, _, _ = norms.shape
         gates = self.activation(self.linear(norms.flatten(-2, -1)).view(*batch, *self.outdims))
-        return st * gates[..., self.ix]
+        return st * irrep_expand(gates, self._slices)

@@ -123,9 +123,12 @@ class EquivariantLinear(nn.Module):
     def forward(self, f: torch.Tensor) -> torch.Tensor:
         """(..., in_mult, dim) -> (..., out_mult, dim)."""
         w = self.weight.view(self.in_repr.nreps(), self.out_repr.mult, self.in_repr.mult)
-        out = torch.cat([torch.matmul(w[k], f[..., a:b]) for k, (a, b) in enumerate(self._slices)],
-                        dim=-1)
-        if self.bias is not None:
-            out = out.clone()
-            out[..., self.scalar_locs] = self.activation(out[..., self.scalar_locs] + self.bias).to(out.dtype)
-        return out
+        parts, j = [], 0
+        for k, (a, b) in enumerate(self._slices):
+            y = torch.matmul(w[k], f[..., a:b])
+            if self.bias is not None and a in self.scalar_locs:
+                # bias column j belongs to the j-th scalar irrep (out[..., scalar_locs] + bias)
+                y = self.activation(y + self.bias[:, j:j + 1]).to(y.dtype)
+                j += 1
+            parts.append(y)
+        return torch.cat(parts, dim=-1)

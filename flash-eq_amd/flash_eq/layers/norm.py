@@ -1,7 +1,12 @@
 """Equivariant normalisations (drop-in for ``flash_eq/layers/norm.py``).
 
 Node-side O(N C D) elementwise work, kept in PyTorch (not on the edge hot path).
-Formulas follow ``norm.py:19-249``.
+Formulas follow ``norm.py:19-249``.  Per-irrep reductions and broadcasts are
+written with slices of the component axis (one run of 2l+1 components per
+irrep): their backward passes are slices, sums and broadcasts again.  The
+reference's ``x[..., ix]`` expansion has an ``index_put_(accumulate=True)``
+backward, which PyTorch runs as a sort over every element (4.5 ms per call at
+20k nodes x 128 channels on MI355X).
 """
 from __future__ import annotations
 
@@ -12,6 +17,25 @@ from ..representations import Repr
 from ..utils import get_epsilon
 
 
+def irrep_slices(repr: Repr) -> list[tuple[int, int]]:
+    """[start, stop) of every irrep's components along the last axis."""
+    offs = repr.cumdims().tolist()
+    return [(offs[k], offs[k + 1]) for k in range(repr.nreps())]
+
+
+def irrep_sums(x: torch.Tensor, slices: list[tuple[int, int]]) -> torch.Tensor:
+    """(..., dim) -> (..., nreps): the sum of each irrep's components."""
+    return torch.stack([x[..., a:b].sum(-1) for a, b in slices], dim=-1)
+
+
+def irrep_expand(g: torch.Tensor, slices: list[tuple[int, int]]) -> torch.Tensor:
+    """(..., nreps) -> (..., dim): value k repeated over irrep k's components
+    (the reference's ``g[..., repr.indices()]``)."""
+    lead = g.shape[:-1]
+    return torch.cat([g[..., k:k + 1].expand(*lead, b - a) for k, (a, b) in enumerate(slices)],
+                     dim=-1)
+
+
 class RepNorm(nn.Module):
     """Per-irrep Euclidean norms sqrt(sum_{d in irrep} x_d^2 + eps): (..., dim) -> (..., nreps)."""
 
@@ -20,13 +44,11 @@ class RepNorm(nn.Module):
         self.num_reps = repr.nreps()
         self._epsilon = epsilon
         self.register_buffer("indices", torch.tensor(repr.indices(), dtype=torch.long))
+        self._slices = irrep_slices(repr)
 
     def forward(self, st: torch.Tensor) -> torch.Tensor:
         eps = self._epsilon if self._epsilon is not None else get_epsilon(st.dtype)
-        sq = st * st
-        acc = torch.zeros(*sq.shape[:-1], self.num_reps, device=sq.device, dtype=sq.dtype)
-        acc = acc.index_add(-1, self.indices, sq)
-        return (acc + eps).sqrt()
+        return (irrep_sums(st * st, self._slices) + eps).sqrt()
 
 
 class _ChannelLayerNorm(nn.Module):
@@ -54,9 +76,16 @@ class _EquivariantRMSNorm(nn.Module):
         self._epsilon = epsilon
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        eps = self._epsilon if self._epsilon is not None else get_epsilon(x.dtype)
-        rms = torch.sqrt(x.pow(2).mean(dim=(-2, -1), keepdim=True) + eps)
-        return x * (self.weight[..., None] / rms)
+        return x * self.factor([x])
+
+    def factor(self, parts: list[torch.Tensor]) -> torch.Tensor:
+        """weight / RMS over the channels and components of ``parts`` (the l > 0
+        runs of one feature tensor), shaped (..., mult, 1)."""
+        eps = self._epsilon if self._epsilon is not None else get_epsilon(parts[0].dtype)
+        count = sum(p.shape[-2] * p.shape[-1] for p in parts)
+        ssq = sum(p.pow(2).sum(dim=(-2, -1), keepdim=True) for p in parts)
+        rms = torch.sqrt(ssq / count + eps)
+        return self.weight[..., None] / rms
 
 
 class EquivariantLayerNorm(nn.Module):
@@ -69,14 +98,15 @@ class EquivariantLayerNorm(nn.Module):
         self.lnorm = nn.LayerNorm(repr.mult) if repr.mult > 1 else None
         self._epsilon = epsilon
         self.register_buffer("ix", torch.tensor(repr.indices(), dtype=torch.long))
+        self._slices = irrep_slices(repr)
 
     def forward(self, f: torch.Tensor) -> torch.Tensor:
         eps = self._epsilon if self._epsilon is not None else get_epsilon(f.dtype)
         norms = self.norm(f)                                  # (..., mult, nreps)
         if self.lnorm is None:
-            return f * (1.0 / (norms + eps))[..., self.ix]
+            return f * irrep_expand(1.0 / (norms + eps), self._slices)
         ln = self.lnorm(norms.transpose(-2, -1)).transpose(-2, -1)
-        return f * (ln / (norms + eps))[..., self.ix]
+        return f * irrep_expand(ln / (norms + eps), self._slices)
 
 
 class SeparableEquivariantLayerNorm(nn.Module):
@@ -96,14 +126,32 @@ class SeparableEquivariantLayerNorm(nn.Module):
             self.scalar_norm = _ChannelLayerNorm(repr.mult, nscalar, epsilon)
         if self.nhigher > 0:
             self.higher_norm = _EquivariantRMSNorm(repr.mult, epsilon)
+        # component runs in order: ("s", j) = scalar number j, ("h", a, b) = a run
+        # of consecutive l > 0 components
+        self._runs: list[tuple] = []
+        for k, (a, b) in enumerate(irrep_slices(repr)):
+            if a in locs:
+                self._runs.append(("s", locs.index(a)))
+            elif self._runs and self._runs[-1][0] == "h" and self._runs[-1][2] == a:
+                self._runs[-1] = ("h", self._runs[-1][1], b)
+            else:
+                self._runs.append(("h", a, b))
 
     def forward(self, f: torch.Tensor) -> torch.Tensor:
-        out = f.clone()
+        ys = None
         if self.nscalar > 0:
-            out[..., self.scalar_locs] = self.scalar_norm(f[..., self.scalar_locs])
-        if self.nhigher > 0:
-            out[..., self.higher_mask] = self.higher_norm(f[..., self.higher_mask])
-        return out
+            xs = torch.cat([f[..., a:a + 1] for a in self.scalar_locs], dim=-1)
+            ys = self.scalar_norm(xs)
+        hp = [f[..., r[1]:r[2]] for r in self._runs if r[0] == "h"]
+        fac = self.higher_norm.factor(hp) if hp else None
+        out, i = [], 0
+        for r in self._runs:
+            if r[0] == "s":
+                out.append(ys[..., r[1]:r[1] + 1])
+            else:
+                out.append(hp[i] * fac)
+                i += 1
+        return torch.cat(out, dim=-1) if len(out) > 1 else out[0]
 
     def extra_repr(self) -> str:
         return f"nscalar={self.nscalar}, nhigher={self.nhigher}"

@@ -104,6 +104,43 @@ def equivariant_linear(f, weight, lvals):
     return torch.cat(parts, -1)
 
 
+def _component_irreps(lvals):
+    return torch.tensor([k for k, l in enumerate(lvals) for _ in range(2 * int(l) + 1)])
+
+
+def separable_layer_norm(f, lvals, s_weight, s_bias, h_weight, eps: float = 1e-8):
+    """SeparableEquivariantLayerNorm (norm.py:177-246), in the reference's index
+    form: LayerNorm over channels of the l = 0 components (norm.py:89-93), one
+    RMS over every channel and l > 0 component with a per-channel weight
+    (norm.py:109-112), written back at their component positions."""
+    offs = [0]
+    for l in lvals:
+        offs.append(offs[-1] + 2 * int(l) + 1)
+    locs = [offs[k] for k, l in enumerate(lvals) if int(l) == 0]
+    higher = torch.ones(offs[-1], dtype=torch.bool)
+    higher[locs] = False
+    out = f.clone()
+    if locs:
+        x = f[..., locs]
+        mu = x.mean(-2, keepdim=True)
+        sd = x.std(-2, keepdim=True, unbiased=False)
+        out[..., locs] = (x - mu) / (sd + eps) * s_weight + s_bias
+    if bool(higher.any()):
+        x = f[..., higher]
+        rms = torch.sqrt((x ** 2).mean(dim=(-2, -1), keepdim=True) + eps)
+        out[..., higher] = x * (h_weight[..., None] / rms)
+    return out
+
+
+def gating(f, lvals, weight, bias, eps: float = 1e-8):
+    """EquivariantGating (gating.py:54-76): sigmoid(Linear(flattened irrep norms))
+    broadcast over each irrep's components."""
+    norms = rep_norms(f, lvals, eps)                         # (..., mult, nreps)
+    lead = norms.shape[:-2]
+    g = torch.sigmoid(norms.flatten(-2, -1) @ weight.t() + bias).view(*lead, *norms.shape[-2:])
+    return f * g[..., _component_irreps(lvals)]
+
+
 def attention_layer(layer, P, Qb, x, r, src, dst, num_nodes):
     """EquivariantAttention.forward (attention.py:294-314) in float64 from a product layer's weights.
 
