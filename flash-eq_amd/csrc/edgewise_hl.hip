@@ -1,0 +1,789 @@
+// EquivariantEdgewiseLinear at high degree (canonical lvals 0..L in and out,
+// L = 6: dim 49, 13x13 Wigner blocks) for bfloat16 features, on the bf16
+// matrix cores of gfx950 with float32 accumulation.
+//
+// Same mathematics as edgewise.hip: with the separable radial table
+// T[b,o,i,w] = sum_k C[k,o,i] F[b,k,w] (SeparableRadialNet, radial.py:259-275)
+//   y = Q-rotate( s^l_out sum_k M_ek (C_k fs) ),   fs = s^l_in (x P),
+// where M_ek is the per-edge mixing matrix of the interpolated radial
+// functions F_e (2x2 [[a, b], [-b, a]] blocks on (+m, -m) pairs, block
+// diagonal over m).  At dim 49 an edge's slots no longer fit the registers of
+// the lanes that own it, so the layer runs in stages:
+//   k_hl_rot_in   fs^T[e, j, c] = s^l(j) sum_d x[e, c, d] P[e, d, j]  (bf16, slot-major);
+//                 the same kernel forms gd^T = s^l (gy Q) in the backward;
+//   k_hl_mix      per 16-edge tile and m-group, G_k = C_k fs on MFMA (bf16 in,
+//                 fp32 out) and the contraction with F_e in registers, one
+//                 source slot at a time: ym[e, o, co] (fp32, slot-major); with
+//                 C_k^T and the transposed terms it forms dfs^T from gd^T;
+//   k_hl_rot_out  y[e, c, d] = sum_j Q[e, d, j] s^l(j) ym[e, j, c] (and dx from dfs);
+//   k_hl_dfe      dF_e[k, w] = sum over the terms (o, i, w) of sign <gd_o, C_k fs_i>,
+//                 G_k recomputed on MFMA, the sums over the 128 rows taken with
+//                 lane swaps (lane rows) and a per-wave LDS buffer (waves);
+//   k_hl_u        U_k[e, i, co] = sum over the terms (o, i, w) of sign F_e[k, w] gd[e, o, co];
+//   dC_k = sum over (e, i) of U_k fs^T: a plain GEMM with a reduction over
+//                 E * dim rows, run by rocBLAS as split-K batches whose partials
+//                 are summed in a fixed order.
+// The binned radial-function and distance gradients reuse the tail of the
+// other fused families (edgewise_tail.hip).
+#include <rocblas/rocblas.h>
+
+#include "ew_canon.h"
+#include "feq_internal.h"
+
+namespace feq {
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
+
+constexpr int kT = 256;   // threads per workgroup
+constexpr int kNE = 16;   // edges per MFMA tile (the B columns)
+
+__device__ __forceinline__ v4f mfma_bf(bf8 a, bf8 b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+template <int L>
+struct HL {
+    using Cn = Canon<L, L>;
+    static constexpr int D = Cn::DIN;
+    static constexpr int WD = Cn::WD;
+    static constexpr int NG = L + 1;                      // m-groups
+    static constexpr int goff(int m) { return Cn::in_off(m); }
+    static constexpr int gsize(int m) { return (m ? 2 : 1) * (L - m + 1); }
+    static constexpr int group_of(int s) {
+        int m = 0;
+        while (m + 1 < NG && goff(m + 1) <= s) ++m;
+        return m;
+    }
+    static constexpr int GMAX = gsize(1) > gsize(0) ? gsize(1) : gsize(0);
+    static constexpr int wsize(int m) { return Cn::w_off(m + 1) - Cn::w_off(m); }
+    static constexpr int WGMAX = [] {
+        int w = 0;
+        for (int m = 0; m < NG; ++m) w = wsize(m) > w ? wsize(m) : w;
+        return w;
+    }();
+    // degree of component d in the standard (l, m) order
+    static constexpr int deg(int d) {
+        int l = 0;
+        while ((l + 1) * (l + 1) <= d) ++l;
+        return l;
+    }
+};
+
+__device__ __forceinline__ float ipowf_small(float s, int l) {
+    float p = 1.0f;
+    for (int i = 0; i < l; ++i) p *= s;
+    return p;
+}
+
+// ---- rotations ------------------------------------------------------------------
+// A workgroup rotates EPB = 256 / C edges; thread (edge el, channel c) holds
+// its channel's D values in registers and walks the degree blocks at compile
+// time, reading the basis entries as LDS broadcasts (every lane of a wave
+// serves the same edge).  Rows move between HBM and LDS with coalesced
+// 16-byte accesses.  Basis rows d are in the standard (l, m) order, columns j
+// in the m-first order (the WignerDBasis layout); when an edge's basis has a
+// non-zero entry off the degree blocks, the workgroup sums over all entries.
+
+// Stages the EPB bases of the workgroup in LDS with column j scaled by
+// s_e^{l(j)}; returns whether any has a non-zero entry off the degree blocks.
+template <int L, typename T, int EPB>
+__device__ __forceinline__ bool stage_bases(int64_t E, int64_t e0, const T* __restrict__ R,
+                                            const float* __restrict__ dist, float sigma, float* sR) {
+    using H = HL<L>;
+    constexpr int D = H::D;
+    int off = 0;
+    for (int q = threadIdx.x; q < EPB * D * D; q += kT) {
+        const int el = q / (D * D), dj = q % (D * D), d = dj / D, j = dj % D;
+        const int64_t e = e0 + el;
+        float v = 0.0f, sc = 0.0f;
+        if (e < E) {
+            v = static_cast<float>(R[e * D * D + dj]);
+            const float r = dist[e];
+            sc = ipowf_small(r / (r + sigma), SlotL<L>::l[j]);
+        }
+        off |= (v != 0.0f) & (H::deg(d) != SlotL<L>::l[j]);
+        sR[q] = v * sc;
+    }
+    return __syncthreads_or(off) != 0;
+}
+
+// out[e, j, c] = s_e^{l(j)} sum_d in[e, c, d] R[e, d, j]   (fs^T = s^l (x P), gd^T = s^l (gy Q))
+template <int L, typename T, int C>
+__global__ void __launch_bounds__(kT)
+k_hl_rot_in(int64_t E, const T* __restrict__ in, const T* __restrict__ R,
+            const float* __restrict__ dist, float sigma, __bf16* __restrict__ out) {
+    using H = HL<L>;
+    constexpr int D = H::D, EPB = kT / C, ROW = C * D;
+    static_assert(kT % C == 0 && (ROW * sizeof(T)) % 16 == 0, "rows of whole 16-byte units");
+    constexpr int VE = 16 / sizeof(T);                 // elements per 16-byte unit
+    __shared__ float sx[EPB * ROW];                    // the rows, [el][c][d]
+    __shared__ float sR[EPB * D * D];
+    const int tid = threadIdx.x, el = tid / C, c = tid % C;
+    const int64_t e0 = static_cast<int64_t>(blockIdx.x) * EPB;
+    const int ne = static_cast<int>(E - e0 < EPB ? E - e0 : EPB);
+    for (int q = tid; q < ne * ROW / VE; q += kT) {
+        const uint4 u = reinterpret_cast<const uint4*>(in + e0 * ROW)[q];
+        const T* t = reinterpret_cast<const T*>(&u);
+#pragma unroll
+        for (int v = 0; v < VE; ++v) sx[q * VE + v] = static_cast<float>(t[v]);
+    }
+    const bool dense = stage_bases<L, T, EPB>(E, e0, R, dist, sigma, sR);
+    if (el >= ne) return;
+    float xr[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) xr[d] = sx[el * ROW + c * D + d];
+    const float* Rl = sR + el * D * D;
+    __bf16* oe = out + (e0 + el) * ROW + c;
+    if (!dense) {
+        static_for<D>([&](auto JJ) __attribute__((always_inline)) {
+            constexpr int j = decltype(JJ)::value, l = SlotL<L>::l[j];
+            float acc = 0.0f;
+#pragma unroll
+            for (int d = l * l; d < (l + 1) * (l + 1); ++d) acc += xr[d] * Rl[d * D + j];
+            oe[j * C] = static_cast<__bf16>(acc);
+        });
+    } else {
+        for (int j = 0; j < D; ++j) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int d = 0; d < D; ++d) acc += xr[d] * Rl[d * D + j];
+            oe[j * C] = static_cast<__bf16>(acc);
+        }
+    }
+}
+
+// out[e, c, d] = sum_j R[e, d, j] s_e^{l(j)} in[e, j, c]   (y = (s^l ym) Q^T, dx = (s^l dfs) P^T)
+template <int L, typename T, int C>
+__global__ void __launch_bounds__(kT)
+k_hl_rot_out(int64_t E, const float* __restrict__ in, const T* __restrict__ R,
+             const float* __restrict__ dist, float sigma, T* __restrict__ out) {
+    using H = HL<L>;
+    constexpr int D = H::D, EPB = kT / C, ROW = C * D;
+    static_assert(kT % C == 0 && (ROW * sizeof(T)) % 16 == 0, "rows of whole 16-byte units");
+    constexpr int VE = 16 / sizeof(T);
+    __shared__ T so[EPB * ROW];                        // the output rows, [el][c][d]
+    __shared__ float sR[EPB * D * D];
+    const int tid = threadIdx.x, el = tid / C, c = tid % C;
+    const int64_t e0 = static_cast<int64_t>(blockIdx.x) * EPB;
+    const int ne = static_cast<int>(E - e0 < EPB ? E - e0 : EPB);
+    float v[D];
+    const int64_t ec = e0 + (el < ne ? el : 0);
+#pragma unroll
+    for (int j = 0; j < D; ++j) v[j] = in[(ec * D + j) * C + c];     // coalesced over c
+    const bool dense = stage_bases<L, T, EPB>(E, e0, R, dist, sigma, sR);
+    const float* Rl = sR + el * D * D;
+    T* ol = so + el * ROW + c * D;
+    if (!dense) {
+        static_for<D>([&](auto DD) __attribute__((always_inline)) {
+            constexpr int d = decltype(DD)::value, l = H::deg(d);
+            float acc = 0.0f;
+#pragma unroll
+            for (int t = l * l; t < (l + 1) * (l + 1); ++t) {
+                const int j = DegreeBlocks<L>::slots[t];
+                acc += Rl[d * D + j] * v[j];
+            }
+            ol[d] = static_cast<T>(acc);
+        });
+    } else {
+        for (int d = 0; d < D; ++d) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < D; ++j) acc += Rl[d * D + j] * v[j];
+            ol[d] = static_cast<T>(acc);
+        }
+    }
+    __syncthreads();
+    for (int q = tid; q < ne * ROW / VE; q += kT)
+        reinterpret_cast<uint4*>(out + e0 * ROW)[q] = reinterpret_cast<const uint4*>(so)[q];
+}
+
+// ---- constant GEMM operand --------------------------------------------------------
+// bf16 A-operand fragments of C_k (TRANS = false: rows co, reduction ci) or C_k^T
+// (rows ci, reduction co); C is (K, Cout, Cin).  Fragment (k, rb, ks) of lane l
+// (row 16 rb + l % 16, reduction indices 32 ks + 8 (l / 16) + 0..7) at
+// ((k * NRB + rb) * NKS + ks) * 64 + l.
+template <bool TRANS>
+__global__ void k_hl_prep(const float* __restrict__ C, int K, int cout, int cin,
+                          bf8* __restrict__ frag) {
+    const int nrow = TRANS ? cin : cout, nred = TRANS ? cout : cin;
+    const int nrb = nrow / 16, nks = nred / 32;
+    const int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (q >= static_cast<int64_t>(K) * nrb * nks * 64) return;
+    const int l = static_cast<int>(q % 64), ks = static_cast<int>((q / 64) % nks);
+    const int rb = static_cast<int>((q / 64 / nks) % nrb), k = static_cast<int>(q / 64 / nks / nrb);
+    const int row = 16 * rb + (l & 15), c0 = 32 * ks + 8 * (l >> 4);
+    const float* Ck = C + static_cast<int64_t>(k) * cout * cin;
+    bf8 v;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        v[j] = static_cast<__bf16>(TRANS ? Ck[(c0 + j) * cin + row] : Ck[row * cin + c0 + j]);
+    frag[q] = v;
+}
+
+// Interpolated radial functions of a 16-edge tile: sF[(k WD + w) 16 + e]
+// (zero for edges past the last), and the tile's bins.
+template <int KW, int NT>
+__device__ __forceinline__ void fill_tile_F(const feq_binning& B, int64_t E, int64_t e0,
+                                            const float* __restrict__ dist,
+                                            const float* __restrict__ F, float* sF, int* slo,
+                                            float* st) {
+    const int tid = threadIdx.x;
+    if (tid < kNE) {
+        const int64_t e = e0 + tid;
+        const bool valid = e < E;
+        const EdgeBin eb = edge_bin(valid ? dist[e] : 0.0f, B);
+        slo[tid] = valid ? eb.lo : -1;
+        st[tid] = eb.t;
+    }
+    __syncthreads();
+    for (int q = tid; q < KW * kNE; q += NT) {
+        const int ed = q % kNE, kw = q / kNE;
+        const int lo = slo[ed];
+        sF[q] = lo >= 0 ? lerp_bins(F[static_cast<int64_t>(lo) * KW + kw],
+                                    F[static_cast<int64_t>(lo + 1) * KW + kw], st[ed])
+                        : 0.0f;
+    }
+    __syncthreads();
+}
+
+// ---- the mix on the matrix cores -----------------------------------------------------
+// Forward (TRANS = false): src = fs^T (E, D, NRED = Cin) bf16, A = C_k,
+//   dst[e, o, co] = sum_k sum_{terms (o, i, w)} sign F_e[k, w] G_k[co, (e, i)].
+// Input gradient (TRANS = true): src = gd^T (E, D, NRED = Cout), A = C_k^T,
+//   dst[e, i, ci] = sum_k sum_{terms (o, i, w)} sign F_e[k, w] H_k[ci, (e, o)].
+// A workgroup of NROW / 16 waves owns a 16-edge tile at a time (lane l serves
+// edge l % 16, the B column); wave w owns the output rows 16 w .. 16 w + 15 and
+// holds the A fragments of every rank for them (one row block per wave keeps
+// the fragments and the accumulators of a group within 256 registers; the
+// waves read the same B fragments, from L1 after the first).  The source slots
+// run in m-first order; the slots of one m-group write into the same group's
+// destination slots only, so the accumulators of a group live in registers
+// until the group's last slot, then go out as 16-byte stores.  B fragments
+// are loaded two slots ahead.
+template <int L, int NROW, int NRED, int K, bool TRANS>
+__global__ void __launch_bounds__(NROW * 4, 1)
+k_hl_mix(feq_binning B, int64_t E, int64_t ntiles, const __bf16* __restrict__ src,
+         const float* __restrict__ dist, const float* __restrict__ F,
+         const bf8* __restrict__ frag, float* __restrict__ dst) {
+    using H = HL<L>;
+    using TG = TermGroups<L, L, TRANS>;
+    constexpr int D = H::D, WD = H::WD, KW = K * WD;
+    constexpr int RBW = 1, NKS = NRED / 32, NRB = NROW / 16, NT = NROW * 4;
+    static_assert(NROW % 16 == 0 && NRED % 32 == 0 && NT <= 1024, "channel counts");
+    __shared__ float sF[KW * kNE];
+    __shared__ int slo[kNE];
+    __shared__ float st[kNE];
+    const int tid = threadIdx.x, lane = tid & 63, le = lane & 15, lg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    bf8 A[K][RBW][NKS];
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks)
+                A[k][rb][ks] = frag[((k * NRB + wave * RBW + rb) * NKS + ks) * 64 + lane];
+
+    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const int64_t e0 = tile * kNE;
+        __syncthreads();   // the previous tile's readers of sF are done
+        fill_tile_F<KW, NT>(B, E, e0, dist, F, sF, slo, st);
+        const bool ok = e0 + le < E;
+        const int64_t ec = ok ? e0 + le : E - 1;
+        const __bf16* srow = src + ec * D * NRED + 8 * lg;
+        float* drow = dst + ec * D * NROW + 16 * wave * RBW + 4 * lg;
+        bf8 b[3][NKS];
+        auto load = [&](int s, bf8(&bb)[NKS]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks)
+                bb[ks] = *reinterpret_cast<const bf8*>(srow + s * NRED + 32 * ks);
+        };
+        load(0, b[0]);
+        if (D > 1) load(1, b[1]);
+        float acc[RBW][H::GMAX][4];
+        static_for<D>([&](auto SS) __attribute__((always_inline)) {
+            constexpr int s = decltype(SS)::value;
+            constexpr int m = H::group_of(s), s0 = H::goff(m), ns = H::gsize(m);
+            if constexpr (s == s0) {
+#pragma unroll
+                for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+                    for (int d = 0; d < ns; ++d)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[rb][d][r] = 0.0f;
+            }
+            if constexpr (s + 2 < D) load(s + 2, b[(s + 2) % 3]);
+            v4f G[K][RBW];
+#pragma unroll
+            for (int k = 0; k < K; ++k)
+#pragma unroll
+                for (int rb = 0; rb < RBW; ++rb) {
+                    v4f g = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int ks = 0; ks < NKS; ++ks) g = mfma_bf(A[k][rb][ks], b[s % 3][ks], g);
+                    G[k][rb] = g;
+                }
+            static_for<TG::count(s)>([&](auto TT) __attribute__((always_inline)) {
+                constexpr Term tm = TG::sorted[TG::start[s] + decltype(TT)::value];
+                constexpr int dsl = (TRANS ? tm.i : tm.o) - s0;
+#pragma unroll
+                for (int k = 0; k < K; ++k) {
+                    const float f0 = sF[(k * WD + tm.w) * kNE + le];
+                    const float f = tm.neg ? -f0 : f0;
+#pragma unroll
+                    for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[rb][dsl][r] += f * G[k][rb][r];
+                }
+            });
+            if constexpr (s == s0 + ns - 1) {
+                if (ok) {
+#pragma unroll
+                    for (int d = 0; d < ns; ++d)
+#pragma unroll
+                        for (int rb = 0; rb < RBW; ++rb)
+                            *reinterpret_cast<float4*>(drow + (s0 + d) * NROW + 16 * rb) =
+                                make_float4(acc[rb][d][0], acc[rb][d][1], acc[rb][d][2], acc[rb][d][3]);
+                }
+            }
+        });
+    }
+}
+
+// Sums of four per-lane values over the wave's four 16-lane rows: lane (row g,
+// column c) returns the sum over rows of v[g] at column c (gfx950 lane swaps).
+__device__ __forceinline__ float quad_row_sums(float v0, float v1, float v2, float v3) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v0), __float_as_uint(v1), false, false);
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v2), __float_as_uint(v3), false, false);
+    const float s = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    const float t = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    const auto z = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(t), false, false);
+    return __uint_as_float(z[0]) + __uint_as_float(z[1]);
+}
+
+// ---- per-edge radial-function gradient ---------------------------------------------------
+// dF_e[e, k, w] = sum over the terms (o, i, w) of sign <gd[e, o, :], G_k[:, (e, i)]>,
+// G_k = C_k fs recomputed on the matrix cores as in the forward (source slots i
+// in m-first order).  Per term a lane forms the dot products over its 4 RBW
+// rows for the four ranks; they are summed over the wave's lane rows with lane
+// swaps (lane row g receives rank g) and added into the wave's LDS buffer of
+// the m-group's weights (read-add-write in the wave's program order); at the
+// group's end the four waves' buffers are summed in wave order and stored.
+template <int L, int COUT, int CIN, int K>
+__global__ void __launch_bounds__(kT, 1)
+k_hl_dfe(int64_t E, int64_t ntiles, const __bf16* __restrict__ fsT,
+         const __bf16* __restrict__ gdT, const bf8* __restrict__ frag, float* __restrict__ dFe) {
+    using H = HL<L>;
+    using TG = TermGroups<L, L, false>;
+    constexpr int D = H::D, WD = H::WD, KW = K * WD;
+    constexpr int RBW = COUT / 64, NKS = CIN / 32, NRB = COUT / 16;
+    constexpr int WGM = H::WGMAX;
+    __shared__ float sD[4][K * WGM * kNE];     // per wave: [k WGM + w - w_off(m)][edge]
+    const int tid = threadIdx.x, lane = tid & 63, le = lane & 15, lg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    bf8 A[K][RBW][NKS];
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks)
+                A[k][rb][ks] = frag[((k * NRB + wave * RBW + rb) * NKS + ks) * 64 + lane];
+    float* sw = sD[wave];
+    for (int q = lane; q < K * WGM * kNE; q += 64) sw[q] = 0.0f;
+
+    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const int64_t e0 = tile * kNE;
+        const bool ok = e0 + le < E;
+        const int64_t ec = ok ? e0 + le : E - 1;
+        const __bf16* srow = fsT + ec * D * CIN + 8 * lg;
+        const __bf16* grow = gdT + ec * D * COUT + 16 * wave * RBW + 4 * lg;
+        bf8 b[3][NKS];
+        auto load = [&](int s, bf8(&bb)[NKS]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks)
+                bb[ks] = *reinterpret_cast<const bf8*>(srow + s * CIN + 32 * ks);
+        };
+        load(0, b[0]);
+        if (D > 1) load(1, b[1]);
+        float gd[H::GMAX][RBW][4];
+        static_for<D>([&](auto SS) __attribute__((always_inline)) {
+            constexpr int s = decltype(SS)::value;
+            constexpr int m = H::group_of(s), s0 = H::goff(m), ns = H::gsize(m);
+            constexpr int wo = Canon<L, L>::w_off(m);
+            if constexpr (s == s0) {
+                // gd rows of this lane for the group's output slots (zero for
+                // edges past the last: their terms then add nothing)
+#pragma unroll
+                for (int d = 0; d < ns; ++d)
+#pragma unroll
+                    for (int rb = 0; rb < RBW; ++rb) {
+                        const bf4 v = *reinterpret_cast<const bf4*>(grow + (s0 + d) * COUT + 16 * rb);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) gd[d][rb][r] = ok ? static_cast<float>(v[r]) : 0.0f;
+                    }
+            }
+            if constexpr (s + 2 < D) load(s + 2, b[(s + 2) % 3]);
+            v4f G[K][RBW];
+#pragma unroll
+            for (int k = 0; k < K; ++k)
+#pragma unroll
+                for (int rb = 0; rb < RBW; ++rb) {
+                    v4f g = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int ks = 0; ks < NKS; ++ks) g = mfma_bf(A[k][rb][ks], b[s % 3][ks], g);
+                    G[k][rb] = g;
+                }
+            static_for<TG::count(s)>([&](auto TT) __attribute__((always_inline)) {
+                constexpr Term tm = TG::sorted[TG::start[s] + decltype(TT)::value];
+                constexpr int o = tm.o - s0;
+                static_assert(K == 4, "one lane-row sum per term: the four ranks");
+                float p[K];
+#pragma unroll
+                for (int k = 0; k < K; ++k) {
+                    float a = 0.0f;
+#pragma unroll
+                    for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) a += gd[o][rb][r] * G[k][rb][r];
+                    p[k] = tm.neg ? -a : a;
+                }
+                // lane row lg receives the wave's sum for rank lg
+                const float v = quad_row_sums(p[0], p[1], p[2], p[3]);
+                sw[(lg * WGM + tm.w - wo) * kNE + le] += v;
+            });
+            if constexpr (s == s0 + ns - 1) {
+                __syncthreads();   // every wave's buffer of the group is complete
+                constexpr int nw = H::wsize(m);
+                for (int q = tid; q < K * nw * kNE; q += kT) {
+                    const int ed = q % kNE, kwl = q / kNE, k = kwl / nw, w = kwl % nw;
+                    const int cell = (k * WGM + w) * kNE + ed;
+                    const float v = sD[0][cell] + sD[1][cell] + sD[2][cell] + sD[3][cell];
+                    if (e0 + ed < E) dFe[(e0 + ed) * KW + k * WD + wo + w] = v;
+                }
+                __syncthreads();
+                for (int q = lane; q < K * nw * kNE; q += 64) {
+                    const int ed = q % kNE, kwl = q / kNE, k = kwl / nw, w = kwl % nw;
+                    sw[(k * WGM + w) * kNE + ed] = 0.0f;
+                }
+            }
+        });
+    }
+}
+
+// ---- U for the channel-pattern gradient ---------------------------------------------------
+// U[e, i, k, co] = sum over the terms (o, i, w) of sign F_e[k, w] gd[e, o, co]
+// (bf16), one workgroup per edge; a thread serves (k, co) pairs with the
+// edge's gd column of co in registers.
+template <int L, int K>
+__global__ void __launch_bounds__(kT)
+k_hl_u(feq_binning B, int C, const __bf16* __restrict__ gdT, const float* __restrict__ dist,
+       const float* __restrict__ F, __bf16* __restrict__ U) {
+    using H = HL<L>;
+    using TG = TermGroups<L, L, false>;
+    constexpr int D = H::D, WD = H::WD, KW = K * WD;
+    __shared__ float sFe[KW];
+    const int64_t e = blockIdx.x;
+    const int tid = threadIdx.x;
+    const EdgeBin eb = edge_bin(dist[e], B);
+    for (int q = tid; q < KW; q += kT)
+        sFe[q] = lerp_bins(F[static_cast<int64_t>(eb.lo) * KW + q],
+                           F[static_cast<int64_t>(eb.lo + 1) * KW + q], eb.t);
+    __syncthreads();
+    const __bf16* ge = gdT + e * D * C;
+    __bf16* ue = U + e * D * K * C;
+    for (int q = tid; q < K * C; q += kT) {
+        const int k = q / C, co = q % C;
+        float g[D];
+#pragma unroll
+        for (int o = 0; o < D; ++o) g[o] = static_cast<float>(ge[o * C + co]);
+        const float* fk = sFe + k * WD;
+        static_for<D>([&](auto II) __attribute__((always_inline)) {
+            constexpr int i = decltype(II)::value;
+            float u = 0.0f;
+            static_for<TG::count(i)>([&](auto TT) __attribute__((always_inline)) {
+                constexpr Term tm = TG::sorted[TG::start[i] + decltype(TT)::value];
+                const float f = fk[tm.w];
+                u += (tm.neg ? -f : f) * g[tm.o];
+            });
+            ue[(i * K + k) * C + co] = static_cast<__bf16>(u);
+        });
+    }
+}
+
+// ---- host side ----------------------------------------------------------------------------
+constexpr int kRank = 4;
+constexpr int kSplitK = 64;              // dC GEMM batches
+constexpr size_t kBlasWs = 32u << 20;    // rocBLAS workspace carved from the caller's
+
+rocblas_handle blas_handle() {
+    static rocblas_handle h[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    if (!h[dev] && rocblas_create_handle(&h[dev]) != rocblas_status_success) h[dev] = nullptr;
+    return h[dev];
+}
+
+int grid_tiles(int64_t ntiles) {
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus = 256;
+    return static_cast<int>(ntiles < cus ? ntiles : cus);
+}
+
+struct HLWs {
+    bf8* cfrag;      // A fragments (C_k or C_k^T)
+    __bf16* fsT;     // (E, D, Cin)
+    float* stage;    // ym (E, D, Cout) or dfs^T (E, D, Cin)
+    __bf16* gdT;     // (E, D, Cout)               backward
+    float* dFe;      // (E, K WD)                  backward
+    __bf16* U;       // (E, D, K, Cout)            backward
+    float* dCp;      // (kSplitK + 1, K Cout, Cin) backward
+    float* tail;     // ew_tail workspace          backward
+    void* blas;      // rocBLAS workspace          backward
+};
+
+template <int L>
+size_t hl_layout(const feq_binning& B, int C, int64_t E, bool backward, HLWs* w, void* base) {
+    constexpr int D = HL<L>::D, KW = kRank * HL<L>::WD;
+    const size_t nfrag = static_cast<size_t>(kRank) * C * C / 8;   // bf8 fragments
+    size_t off = 0;
+    char* p = static_cast<char*>(base);
+    auto take = [&](size_t bytes) -> void* {
+        void* r = p ? p + off : nullptr;
+        off += align_up(bytes, 256);
+        return r;
+    };
+    HLWs t{};
+    t.cfrag = static_cast<bf8*>(take(nfrag * sizeof(bf8)));
+    t.fsT = static_cast<__bf16*>(take(2 * static_cast<size_t>(E) * D * C));
+    t.stage = static_cast<float*>(take(4 * static_cast<size_t>(E) * D * C));
+    if (backward) {
+        t.gdT = static_cast<__bf16*>(take(2 * static_cast<size_t>(E) * D * C));
+        t.dFe = static_cast<float*>(take(4 * static_cast<size_t>(E) * KW));
+        t.U = static_cast<__bf16*>(take(2 * static_cast<size_t>(E) * D * kRank * C));
+        t.dCp = static_cast<float*>(take(4 * static_cast<size_t>(kSplitK + 1) * kRank * C * C));
+        t.tail = static_cast<float*>(take(4 * ew_tail_floats(B, KW, E, kSplitK + 1,
+                                                             static_cast<int64_t>(kRank) * C * C)));
+        t.blas = take(kBlasWs);
+    }
+    if (w) *w = t;
+    return off + 256;
+}
+
+template <int L, int C>
+int hl_rot_in(int64_t E, const __bf16* in, const __bf16* R, const float* dist, float sigma,
+              __bf16* out, hipStream_t s) {
+    auto kern = k_hl_rot_in<L, __bf16, C>;
+    FEQ_LAUNCH("k_hl_rot_in", kern, dim3(ceil_div(E, kT / C)), dim3(kT), 0, s, E, in, R, dist, sigma, out);
+    return FEQ_OK;
+}
+
+template <int L, int C>
+int hl_rot_out(int64_t E, const float* in, const __bf16* R, const float* dist, float sigma,
+               __bf16* out, hipStream_t s) {
+    auto kern = k_hl_rot_out<L, __bf16, C>;
+    FEQ_LAUNCH("k_hl_rot_out", kern, dim3(ceil_div(E, kT / C)), dim3(kT), 0, s, E, in, R, dist, sigma, out);
+    return FEQ_OK;
+}
+
+template <bool TRANS>
+int hl_prep(const float* C, int K, int cout, int cin, bf8* frag, hipStream_t s) {
+    const int64_t n = static_cast<int64_t>(K) * cout * cin / 8;
+    auto kern = k_hl_prep<TRANS>;
+    FEQ_LAUNCH("k_hl_prep", kern, dim3(ceil_div(n, 256)), dim3(256), 0, s, C, K, cout, cin, frag);
+    return FEQ_OK;
+}
+
+template <int L, int CH>
+int hl_fwd(const feq_binning& B, int64_t E, const __bf16* x, const __bf16* P, const __bf16* Q,
+           const float* dist, const float* C, const float* F, __bf16* y, void* ws, size_t ws_bytes,
+           hipStream_t s) {
+    HLWs w;
+    if (ws_bytes < hl_layout<L>(B, CH, E, false, &w, ws)) return fail(FEQ_ERR_WORKSPACE, "high-degree workspace too small");
+    if (int rc = hl_prep<false>(C, kRank, CH, CH, w.cfrag, s)) return rc;
+    if (int rc = hl_rot_in<L, CH>(E, x, P, dist, B.sh_scale, w.fsT, s)) return rc;
+    const int64_t ntiles = ceil_div(E, kNE);
+    auto mix = k_hl_mix<L, CH, CH, kRank, false>;
+    FEQ_LAUNCH("k_hl_mix", mix, dim3(grid_tiles(ntiles)), dim3(4 * CH), 0, s, B, E, ntiles, w.fsT,
+               dist, F, w.cfrag, w.stage);
+    return hl_rot_out<L, CH>(E, w.stage, Q, dist, B.sh_scale, y, s);
+}
+
+// dC = sum over the E D rows of U^T fs (column-major view: dC^T (C x K C) =
+// fs^T-matrix (C x R) * U-matrix^T), as kSplitK equal batches plus a remainder,
+// then the partials summed in batch order.
+template <int CH>
+int hl_dc(int64_t rows, const __bf16* U, const __bf16* fsT, float* dCp, float* gC, float* tmp,
+          void* blas_ws, hipStream_t s) {
+    rocblas_handle h = blas_handle();
+    if (!h) return fail(FEQ_ERR_HIP, "rocBLAS handle creation failed");
+    if (rocblas_set_stream(h, s) != rocblas_status_success) return fail(FEQ_ERR_HIP, "rocblas_set_stream failed");
+    if (rocblas_set_workspace(h, blas_ws, kBlasWs) != rocblas_status_success)
+        return fail(FEQ_ERR_HIP, "rocblas_set_workspace failed");
+    const int m = CH, n = kRank * CH;
+    const float one = 1.0f, zero = 0.0f;
+    const int64_t ks = rows / kSplitK, rem = rows - ks * kSplitK;
+    const int64_t nout = static_cast<int64_t>(m) * n;
+    int parts = 0;
+    if (ks > 0) {
+        const rocblas_status st = rocblas_gemm_strided_batched_ex(
+            h, rocblas_operation_none, rocblas_operation_transpose, m, n, static_cast<rocblas_int>(ks), &one,
+            fsT, rocblas_datatype_bf16_r, m, ks * m, U, rocblas_datatype_bf16_r, n, ks * n, &zero,
+            dCp, rocblas_datatype_f32_r, m, nout, dCp, rocblas_datatype_f32_r, m, nout, kSplitK,
+            rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+        if (st != rocblas_status_success) return fail(FEQ_ERR_HIP, "rocblas_gemm_strided_batched_ex failed (%d)", static_cast<int>(st));
+        parts = kSplitK;
+    }
+    if (rem > 0) {
+        const int64_t r0 = ks * kSplitK;
+        const rocblas_status st = rocblas_gemm_ex(
+            h, rocblas_operation_none, rocblas_operation_transpose, m, n, static_cast<rocblas_int>(rem), &one,
+            fsT + r0 * m, rocblas_datatype_bf16_r, m, U + r0 * n, rocblas_datatype_bf16_r, n, &zero,
+            dCp + parts * nout, rocblas_datatype_f32_r, m, dCp + parts * nout, rocblas_datatype_f32_r, m,
+            rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+        if (st != rocblas_status_success) return fail(FEQ_ERR_HIP, "rocblas_gemm_ex failed (%d)", static_cast<int>(st));
+        ++parts;
+    }
+    return reduce_partials(dCp, parts, nout, gC, tmp, s);
+}
+
+template <int L, int CH>
+int hl_bwd(const feq_layout& Lay, const feq_binning& B, int64_t E, const __bf16* gy, const __bf16* x,
+           const __bf16* P, const __bf16* Q, const float* dist, const float* C, const float* F,
+           __bf16* gx, float* gC, float* gF, float* gdist, void* ws, size_t ws_bytes, hipStream_t s) {
+    using H = HL<L>;
+    HLWs w;
+    if (ws_bytes < hl_layout<L>(B, CH, E, true, &w, ws)) return fail(FEQ_ERR_WORKSPACE, "high-degree workspace too small");
+    const int64_t ntiles = ceil_div(E, kNE);
+    const int G = grid_tiles(ntiles);
+    // gd = s^l_out (gy Q), fs = s^l_in (x P)
+    if (int rc = hl_rot_in<L, CH>(E, gy, Q, dist, B.sh_scale, w.gdT, s)) return rc;
+    if (int rc = hl_rot_in<L, CH>(E, x, P, dist, B.sh_scale, w.fsT, s)) return rc;
+    // dF_e from <gd, C_k fs>
+    if (int rc = hl_prep<false>(C, kRank, CH, CH, w.cfrag, s)) return rc;
+    auto kd = k_hl_dfe<L, CH, CH, kRank>;
+    FEQ_LAUNCH("k_hl_dfe", kd, dim3(G), dim3(kT), 0, s, E, ntiles, w.fsT, w.gdT, w.cfrag, w.dFe);
+    // dfs = sum_k M_ek^T C_k^T gd, dx = (s^l_in dfs) P^T
+    if (gx) {
+        if (int rc = hl_prep<true>(C, kRank, CH, CH, w.cfrag, s)) return rc;
+        auto km = k_hl_mix<L, CH, CH, kRank, true>;
+        FEQ_LAUNCH("k_hl_mix_t", km, dim3(G), dim3(4 * CH), 0, s, B, E, ntiles, w.gdT, dist, F,
+                   w.cfrag, w.stage);
+        if (int rc = hl_rot_out<L, CH>(E, w.stage, P, dist, B.sh_scale, gx, s)) return rc;
+    }
+    // dC = sum U^T fs
+    auto ku = k_hl_u<L, kRank>;
+    FEQ_LAUNCH("k_hl_u", ku, dim3(E), dim3(kT), 0, s, B, CH, w.gdT, dist, F, w.U);
+    float* tmp = w.tail + align_up(static_cast<size_t>(256) * (B.num_bins + 1) * kRank * H::WD, 64);
+    if (int rc = hl_dc<CH>(E * H::D, w.U, w.fsT, w.dCp, gC, tmp, w.blas, s)) return rc;
+    // binned radial-function gradient and distance gradient (no dC partials left)
+    return ew_tail(Lay, B, kRank, E, dist, F, w.dFe, nullptr, 0, 0, nullptr, gF, gdist, w.tail, s);
+}
+
+bool canonical_pair(const feq_layout& L, int lmax) {
+    int32_t lv[FEQ_MAX_BLOCKS];
+    for (int i = 0; i <= lmax; ++i) lv[i] = i;
+    feq_layout ref;
+    if (feq_layout_init(&ref, lv, lmax + 1, lv, lmax + 1, L.cin, L.cout) != FEQ_OK) return false;
+    if (ref.din != L.din || ref.dout != L.dout || ref.wdim != L.wdim || ref.nblocks != L.nblocks)
+        return false;
+    for (int k = 0; k < L.nblocks; ++k)
+        for (int c = 0; c < 6; ++c)
+            if (ref.blk[k][c] != L.blk[k][c]) return false;
+    for (int q = 0; q < L.din; ++q)
+        if (ref.lslot_in[q] != L.lslot_in[q] || ref.lslot_out[q] != L.lslot_out[q]) return false;
+    return true;
+}
+
+// Shapes with a high-degree path: lvals 0..L in and out, Cin = Cout = CH, rank 4.
+#define FEQ_HL_SHAPES(X) \
+    X(6, 128)            \
+    X(6, 64)
+
+bool hl_supported(const feq_layout& L, const feq_binning& B, int rank) {
+    if (rank != kRank || L.cin != L.cout) return false;
+#define FEQ_SUP(l, ch) \
+    if (L.cin == ch && canonical_pair(L, l)) return ew_tail_supported(B, kRank * HL<l>::WD);
+    FEQ_HL_SHAPES(FEQ_SUP)
+#undef FEQ_SUP
+    return false;
+}
+
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace feq
+
+using namespace feq;
+
+extern "C" int feq_edgewise_hl_supported(const feq_layout* L, const feq_binning* b, int32_t rank) {
+    if (!L || !b) return 0;
+    return hl_supported(*L, *b, rank) ? 1 : 0;
+}
+
+extern "C" size_t feq_edgewise_hl_workspace(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                            int64_t E, int32_t backward) {
+    if (!L || !b || !hl_supported(*L, *b, rank) || E < 0) return 0;
+#define FEQ_WS(l, ch) \
+    if (L->cin == ch && canonical_pair(*L, l)) return hl_layout<l>(*b, ch, E, backward != 0, nullptr, nullptr);
+    FEQ_HL_SHAPES(FEQ_WS)
+#undef FEQ_WS
+    return 0;
+}
+
+extern "C" int feq_edgewise_hl_fwd(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                   int64_t E, const void* x, const void* P, const void* Q,
+                                   const float* dist, const float* C, const float* F, void* y,
+                                   void* ws, size_t ws_bytes, feq_stream_t stream) {
+    if (!L || !b) return fail(FEQ_ERR_INVALID, "NULL layout or binning");
+    if (!hl_supported(*L, *b, rank)) return fail(FEQ_ERR_UNSUPPORTED, "no high-degree kernels for this layout");
+    if (E < 0) return fail(FEQ_ERR_INVALID, "negative edge count");
+    if (E == 0) return FEQ_OK;
+    if (E > 0x7fffffffLL) return fail(FEQ_ERR_UNSUPPORTED, "more than 2^31-1 edges");
+    if (!x || !P || !Q || !dist || !C || !F || !y || !ws) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (!al16(x) || !al16(ws)) return fail(FEQ_ERR_INVALID, "x and the workspace must be 16-byte aligned");
+    hipStream_t s = stream_of(stream);
+    const auto* xb = static_cast<const __bf16*>(x);
+    const auto* Pb = static_cast<const __bf16*>(P);
+    const auto* Qb = static_cast<const __bf16*>(Q);
+#define FEQ_FWD(l, ch) \
+    if (L->cin == ch && canonical_pair(*L, l)) \
+        return hl_fwd<l, ch>(*b, E, xb, Pb, Qb, dist, C, F, static_cast<__bf16*>(y), ws, ws_bytes, s);
+    FEQ_HL_SHAPES(FEQ_FWD)
+#undef FEQ_FWD
+    return fail(FEQ_ERR_UNSUPPORTED, "no high-degree kernels for this layout");
+}
+
+extern "C" int feq_edgewise_hl_bwd(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                   int64_t E, const void* gy, const void* x, const void* P,
+                                   const void* Q, const float* dist, const float* C, const float* F,
+                                   void* gx, float* gC, float* gF, float* gdist, void* ws,
+                                   size_t ws_bytes, feq_stream_t stream) {
+    if (!L || !b) return fail(FEQ_ERR_INVALID, "NULL layout or binning");
+    if (!hl_supported(*L, *b, rank)) return fail(FEQ_ERR_UNSUPPORTED, "no high-degree kernels for this layout");
+    if (E < 0) return fail(FEQ_ERR_INVALID, "negative edge count");
+    if (E > 0x7fffffffLL) return fail(FEQ_ERR_UNSUPPORTED, "more than 2^31-1 edges");
+    if (!gC || !gF) return fail(FEQ_ERR_INVALID, "grad_C and grad_F are required");
+    hipStream_t s = stream_of(stream);
+    if (E == 0) {
+        if (int rc = fill_zero(gF, static_cast<int64_t>(b->num_bins + 1) * rank * L->wdim, s)) return rc;
+        return fill_zero(gC, static_cast<int64_t>(rank) * L->cout * L->cin, s);
+    }
+    if (!gy || !x || !P || !Q || !dist || !C || !F || !ws) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (!al16(gy) || !al16(x) || !al16(ws)) return fail(FEQ_ERR_INVALID, "gy, x and the workspace must be 16-byte aligned");
+    const auto* gyb = static_cast<const __bf16*>(gy);
+    const auto* xb = static_cast<const __bf16*>(x);
+    const auto* Pb = static_cast<const __bf16*>(P);
+    const auto* Qb = static_cast<const __bf16*>(Q);
+#define FEQ_BWD(l, ch) \
+    if (L->cin == ch && canonical_pair(*L, l)) \
+        return hl_bwd<l, ch>(*L, *b, E, gyb, xb, Pb, Qb, dist, C, F, static_cast<__bf16*>(gx), gC, gF, gdist, ws, ws_bytes, s);
+    FEQ_HL_SHAPES(FEQ_BWD)
+#undef FEQ_BWD
+    return fail(FEQ_ERR_UNSUPPORTED, "no high-degree kernels for this layout");
+}

@@ -43,9 +43,12 @@ __device__ void weight_lsum(const feq_layout& L, int* fl) {
 // partial histogram per workgroup (its waves' histograms summed in wave order).
 constexpr int kHistBatch = 16;
 
+// A launch bins the column window [cw0, cw0 + cwn) of the kw-wide rows (the
+// whole row when it fits LDS) into the same columns of its partial.
 __global__ void __launch_bounds__(kThreads)
-k_ewm_hist(feq_binning B, int kw, int64_t E, int64_t per_wave, const float* __restrict__ dist,
-           const float* __restrict__ dFe, float* __restrict__ hist_part) {
+k_ewm_hist(feq_binning B, int kw_row, int cw0, int kw, int64_t E, int64_t per_wave,
+           const float* __restrict__ dist, const float* __restrict__ dFe,
+           float* __restrict__ hist_part) {
     extern __shared__ float sh[];
     const int waves = blockDim.x / 64;
     const int hsz = (B.num_bins + 1) * kw;
@@ -74,7 +77,7 @@ k_ewm_hist(feq_binning B, int kw, int64_t E, int64_t per_wave, const float* __re
             b.eb = edge_bin(dist[e + jl], B);
 #pragma unroll
             for (int j = 0; j < kHistBatch; ++j) {
-                const float* row = dFe + (e + (j < nb ? j : nb - 1)) * kw;
+                const float* row = dFe + (e + (j < nb ? j : nb - 1)) * kw_row + cw0;
                 b.va[j] = row[la];
                 b.vb[j] = row[lb];
             }
@@ -118,11 +121,11 @@ k_ewm_hist(feq_binning B, int kw, int64_t E, int64_t per_wave, const float* __re
         }
     }
     __syncthreads();
-    float* out = hist_part + static_cast<int64_t>(blockIdx.x) * hsz;
+    float* out = hist_part + static_cast<int64_t>(blockIdx.x) * (B.num_bins + 1) * kw_row + cw0;
     for (int q = threadIdx.x; q < hsz; q += blockDim.x) {
         float acc = sh[q];
         for (int v = 1; v < waves; ++v) acc += sh[static_cast<int64_t>(v) * hsz + q];
-        out[q] = acc;
+        out[(q / kw) * kw_row + q % kw] = acc;
     }
 }
 
@@ -172,6 +175,8 @@ size_t reduce_tmp_floats(int groups, int64_t n) {
                                  : 0;
 }
 
+}  // namespace
+
 // Deterministic sum of `groups` partial arrays of n floats: slices of at most
 // kSliceGroups partials into tmp, then the slices into out.
 int reduce_partials(const float* part, int groups, int64_t n, float* out, float* tmp,
@@ -190,6 +195,8 @@ int reduce_partials(const float* part, int groups, int64_t n, float* out, float*
     return FEQ_OK;
 }
 
+namespace {
+
 constexpr int kHistGroups = 256;           // histogram workgroups (fixed: the order is set by E alone)
 constexpr size_t kHistLds = 160 * 1024;
 
@@ -200,9 +207,17 @@ int hist_waves(const feq_binning& B, int kw) {
     return static_cast<int>(w < 4 ? w : 4);
 }
 
+// Column window of the histogram: the whole row when one histogram fits LDS,
+// else the widest multiple of 128 columns that does (0: not even 128 fit).
+int hist_window(const feq_binning& B, int kw) {
+    if (hist_waves(B, kw) >= 1) return kw;
+    const int w = static_cast<int>(kHistLds / (4 * static_cast<size_t>(B.num_bins + 1))) / 128 * 128;
+    return w;
+}
+
 }  // namespace
 
-bool ew_tail_supported(const feq_binning& B, int kw) { return hist_waves(B, kw) >= 1; }
+bool ew_tail_supported(const feq_binning& B, int kw) { return hist_window(B, kw) >= 1; }
 
 size_t ew_tail_floats(const feq_binning& B, int kw, int64_t E, int groups, int64_t ncc) {
     (void)E;
@@ -215,22 +230,26 @@ int ew_tail(const feq_layout& L, const feq_binning& B, int K, int64_t E, const f
             const float* F, const float* dFe, const float* dCp, int groups, int64_t ncc, float* gC,
             float* gF, float* gdist, float* tail, hipStream_t s) {
     const int kw = K * L.wdim;
-    const int waves = hist_waves(B, kw);
-    if (waves < 1) return fail(FEQ_ERR_UNSUPPORTED, "radial-function histogram does not fit LDS");
+    const int win = hist_window(B, kw);
+    if (win < 1) return fail(FEQ_ERR_UNSUPPORTED, "radial-function histogram does not fit LDS");
     const int64_t hsz = (B.num_bins + 1) * static_cast<int64_t>(kw);
-    const size_t hlds = 4 * static_cast<size_t>(waves) * hsz;
-    const int64_t per_wave = ceil_div(E, static_cast<int64_t>(kHistGroups) * waves);
     float* hp = tail;
     float* tmp = tail + align_up(static_cast<size_t>(kHistGroups) * hsz, 64);
-    if (hlds > 64 * 1024)
-        FEQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_ewm_hist),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(hlds)));
-    FEQ_LAUNCH("k_ewm_hist", k_ewm_hist, dim3(kHistGroups), dim3(64 * waves), hlds, s, B, kw, E,
-               per_wave, dist, dFe, hp);
+    FEQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_ewm_hist),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kHistLds)));
+    for (int c0 = 0; c0 < kw; c0 += win) {
+        const int cn = kw - c0 < win ? kw - c0 : win;
+        const int waves = hist_waves(B, cn);
+        const size_t hlds = 4 * static_cast<size_t>(waves) * (B.num_bins + 1) * cn;
+        const int64_t per_wave = ceil_div(E, static_cast<int64_t>(kHistGroups) * waves);
+        FEQ_LAUNCH("k_ewm_hist", k_ewm_hist, dim3(kHistGroups), dim3(64 * waves), hlds, s, B, kw,
+                   c0, cn, E, per_wave, dist, dFe, hp);
+    }
     if (gdist)
         FEQ_LAUNCH("k_ewm_dr", k_ewm_dr, dim3(ceil_div(E, kThreads)), dim3(kThreads),
                    sizeof(int) * L.wdim, s, L, B, K, E, dist, F, dFe, gdist);
-    if (int rc = reduce_partials(dCp, groups, ncc, gC, tmp, s)) return rc;
+    if (groups > 0)
+        if (int rc = reduce_partials(dCp, groups, ncc, gC, tmp, s)) return rc;
     return reduce_partials(hp, kHistGroups, hsz, gF, tmp, s);
 }
 

@@ -82,7 +82,12 @@ int ew_mfma_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, 
 // Tail shared by the fused backward families (edgewise_tail.hip): binned
 // radial-function gradient from dF_e (E, K wdim), distance gradient (gdist may
 // be NULL), and the sums of `groups` channel-pattern partials of ncc floats.
-// `tail` holds ew_tail_floats(...) floats of workspace.
+// Deterministic sum of `groups` partial arrays of n floats into out (tmp holds
+// ceil(groups / 32) * n floats when groups > 32).
+int reduce_partials(const float* part, int groups, int64_t n, float* out, float* tmp,
+                    hipStream_t s);
+
+// `tail` holds ew_tail_floats(...) floats of workspace.  groups = 0: no dC partials.
 bool ew_tail_supported(const feq_binning& B, int kw);
 size_t ew_tail_floats(const feq_binning& B, int kw, int64_t E, int groups, int64_t ncc);
 int ew_tail(const feq_layout& L, const feq_binning& B, int K, int64_t E, const float* dist,

@@ -190,7 +190,74 @@ def _check_edgewise_shapes(L, b, rank, x, P, Q, r, C, F) -> None:
                          f"got {tuple(F.shape)}")
 
 
+class EdgewiseLinearHLFn(torch.autograd.Function):
+    """The high-degree form for bfloat16 features (``csrc/edgewise_hl.hip``):
+    x, P, Q and y stay bf16 (no float32 copies), the GEMMs run on the bf16
+    matrix cores with float32 accumulation; the radial parameters and
+    distances are float32."""
+
+    @staticmethod
+    def forward(ctx, x, P, Q, dist, C, F, layout: N.FeqLayout, binning: N.FeqBinning, rank: int):
+        dev = _same_device(x, P, Q, dist, C, F)
+        E = x.shape[0]
+        xs, Ps, Qs = (t.detach().contiguous() for t in (x, P, Q))
+        rs, Cs, Fs = _f32(dist, "distances"), _f32(C, "channel_patterns"), _f32(F, "radial")
+        _check_edgewise_shapes(layout, binning, rank, xs, Ps, Qs, rs, Cs, Fs)
+        y = torch.empty(E, layout.cout, layout.dout, dtype=torch.bfloat16, device=dev)
+        if E:
+            lib = N.lib()
+            ws = N.workspace(lib.feq_edgewise_hl_workspace(N.ctypes.byref(layout),
+                                                           N.ctypes.byref(binning), rank, E, 0), dev)
+            with torch.cuda.device(dev):
+                rc = lib.feq_edgewise_hl_fwd(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
+                                             N.ptr(xs), N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs),
+                                             N.ptr(Fs), N.ptr(y), N.ptr(ws), ws.numel(),
+                                             N.stream_ptr(dev))
+            N.check(rc, "feq_edgewise_hl_fwd")
+        ctx.save_for_backward(xs, Ps, Qs, rs, Cs, Fs)
+        ctx.meta = (layout, binning, rank, dist.dtype, C.dtype, F.dtype)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        xs, Ps, Qs, rs, Cs, Fs = ctx.saved_tensors
+        layout, binning, rank, rdt, cdt, fdt = ctx.meta
+        dev = xs.device
+        E = xs.shape[0]
+        need = ctx.needs_input_grad
+        g = gy.detach().to(torch.bfloat16).contiguous()
+        gx = torch.empty_like(xs) if need[0] else None
+        gr = torch.empty_like(rs) if need[3] else None
+        gC = torch.empty_like(Cs)
+        gF = torch.empty_like(Fs)
+        lib = N.lib()
+        ws = N.workspace(lib.feq_edgewise_hl_workspace(N.ctypes.byref(layout), N.ctypes.byref(binning),
+                                                       rank, E, 1), dev)
+        with torch.cuda.device(dev):
+            rc = lib.feq_edgewise_hl_bwd(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
+                                         N.ptr(g), N.ptr(xs), N.ptr(Ps), N.ptr(Qs), N.ptr(rs),
+                                         N.ptr(Cs), N.ptr(Fs), N.ptr(gx), N.ptr(gC), N.ptr(gF),
+                                         N.ptr(gr), N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+        N.check(rc, "feq_edgewise_hl_bwd")
+        return (gx, None, None, None if gr is None else gr.to(rdt),
+                gC.to(cdt) if need[4] else None, gF.to(fdt) if need[5] else None,
+                None, None, None)
+
+
+def _use_hl(x, P, Q, layout, binning, rank) -> bool:
+    """bf16 features, bases and a layout with high-degree kernels; P and Q
+    without gradients (the high-degree backward does not form them)."""
+    if not (x.dtype == P.dtype == Q.dtype == torch.bfloat16):
+        return False
+    if P.requires_grad or Q.requires_grad:
+        return False
+    return bool(N.lib().feq_edgewise_hl_supported(N.ctypes.byref(layout), N.ctypes.byref(binning),
+                                                  rank))
+
+
 def edgewise_linear(x, P, Q, dist, C, F, layout, binning, rank) -> torch.Tensor:
+    if _use_hl(x, P, Q, layout, binning, rank):
+        return EdgewiseLinearHLFn.apply(x, P, Q, dist, C, F, layout, binning, rank)
     return EdgewiseLinearFn.apply(x, P, Q, dist, C, F, layout, binning, rank)
 
 

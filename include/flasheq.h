@@ -180,6 +180,27 @@ int feq_segment_sum(const float* x, int64_t row, const int32_t* perm, const int3
 int feq_gather_rows(const float* src, int64_t num_src, int64_t row, const int64_t* idx,
                     int64_t num_rows, float* out, feq_stream_t stream);
 
+/* High-degree form for bfloat16 features (canonical lvals 0..6 in and out,
+ * Cin = Cout in {64, 128}, rank 4): x (E, Cin, Din), P, Q, y and the gradients
+ * of x and y are bf16 (uint16 storage), dist, C, F and their gradients float32.
+ * Same interface and results as feq_edgewise_fwd/_bwd (EquivariantEdgewiseLinear,
+ * flash_eq/layers/linear.py:100-160) to bf16 accuracy: the GEMMs against the
+ * channel patterns run on bf16 matrix cores with float32 accumulation.  The
+ * backward forms no P/Q gradients.  The workspace holds rotated features and
+ * staging (about 24 * E * Din * Cin bytes for the backward). */
+int feq_edgewise_hl_supported(const feq_layout* layout, const feq_binning* binning, int32_t rank);
+size_t feq_edgewise_hl_workspace(const feq_layout* layout, const feq_binning* binning, int32_t rank,
+                                 int64_t num_edges, int32_t backward);
+int feq_edgewise_hl_fwd(const feq_layout* layout, const feq_binning* binning, int32_t rank,
+                        int64_t num_edges, const void* x, const void* P, const void* Q,
+                        const float* dist, const float* C, const float* F, void* y, void* workspace,
+                        size_t workspace_bytes, feq_stream_t stream);
+int feq_edgewise_hl_bwd(const feq_layout* layout, const feq_binning* binning, int32_t rank,
+                        int64_t num_edges, const void* grad_y, const void* x, const void* P,
+                        const void* Q, const float* dist, const float* C, const float* F,
+                        void* grad_x, float* grad_C, float* grad_F, float* grad_dist,
+                        void* workspace, size_t workspace_bytes, feq_stream_t stream);
+
 /* Attention over head-major rows: a row of Q, K or V holds heads*head_dim floats,
  * head h at offset h*head_dim; row r of a table T starts at T + r*ld (floats).
  * Edges are visited in the CSR by destination (perm, offsets, num_nodes);
