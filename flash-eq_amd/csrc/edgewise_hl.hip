@@ -89,23 +89,40 @@ __device__ __forceinline__ float ipowf_small(float s, int l) {
 
 // Stages the EPB bases of the workgroup in LDS with column j scaled by
 // s_e^{l(j)}; returns whether any has a non-zero entry off the degree blocks.
+// The degrees of rows and columns and the powers of s come from small LDS
+// tables.
 template <int L, typename T, int EPB>
 __device__ __forceinline__ bool stage_bases(int64_t E, int64_t e0, const T* __restrict__ R,
                                             const float* __restrict__ dist, float sigma, float* sR) {
     using H = HL<L>;
     constexpr int D = H::D;
-    int off = 0;
-    for (int q = threadIdx.x; q < EPB * D * D; q += kT) {
-        const int el = q / (D * D), dj = q % (D * D), d = dj / D, j = dj % D;
-        const int64_t e = e0 + el;
-        float v = 0.0f, sc = 0.0f;
-        if (e < E) {
-            v = static_cast<float>(R[e * D * D + dj]);
-            const float r = dist[e];
-            sc = ipowf_small(r / (r + sigma), SlotL<L>::l[j]);
+    __shared__ int s_lj[D], s_ld[D];
+    __shared__ float s_pw[EPB][L + 1];
+    const int tid = threadIdx.x;
+    if (tid < D) {
+        s_lj[tid] = SlotL<L>::l[tid];
+        s_ld[tid] = H::deg(tid);
+    }
+    if (tid < EPB) {
+        const int64_t e = e0 + tid;
+        const float r = e < E ? dist[e] : 0.0f;
+        const float sv = r / (r + sigma);
+        float p = 1.0f;
+        for (int l = 0; l <= L; ++l) {
+            s_pw[tid][l] = e < E ? p : 0.0f;
+            p *= sv;
         }
-        off |= (v != 0.0f) & (H::deg(d) != SlotL<L>::l[j]);
-        sR[q] = v * sc;
+    }
+    __syncthreads();
+    int off = 0;
+    const int64_t nvalid = E - e0 < EPB ? E - e0 : EPB;
+    const T* Rb = R + e0 * D * D;
+    for (int q = tid; q < EPB * D * D; q += kT) {
+        const int el = q / (D * D), dj = q - el * (D * D), d = dj / D, j = dj - d * D;
+        const float v = el < nvalid ? static_cast<float>(Rb[q]) : 0.0f;
+        const int lj = s_lj[j];
+        off |= (v != 0.0f) & (s_ld[d] != lj);
+        sR[q] = v * s_pw[el][lj];
     }
     return __syncthreads_or(off) != 0;
 }
@@ -119,22 +136,18 @@ k_hl_rot_in(int64_t E, const T* __restrict__ in, const T* __restrict__ R,
     constexpr int D = H::D, EPB = kT / C, ROW = C * D;
     static_assert(kT % C == 0 && (ROW * sizeof(T)) % 16 == 0, "rows of whole 16-byte units");
     constexpr int VE = 16 / sizeof(T);                 // elements per 16-byte unit
-    __shared__ float sx[EPB * ROW];                    // the rows, [el][c][d]
+    __shared__ uint4 sx4[EPB * ROW / VE];              // the rows, [el][c][d]
     __shared__ float sR[EPB * D * D];
+    const T* sx = reinterpret_cast<const T*>(sx4);
     const int tid = threadIdx.x, el = tid / C, c = tid % C;
     const int64_t e0 = static_cast<int64_t>(blockIdx.x) * EPB;
     const int ne = static_cast<int>(E - e0 < EPB ? E - e0 : EPB);
-    for (int q = tid; q < ne * ROW / VE; q += kT) {
-        const uint4 u = reinterpret_cast<const uint4*>(in + e0 * ROW)[q];
-        const T* t = reinterpret_cast<const T*>(&u);
-#pragma unroll
-        for (int v = 0; v < VE; ++v) sx[q * VE + v] = static_cast<float>(t[v]);
-    }
+    for (int q = tid; q < ne * ROW / VE; q += kT) sx4[q] = reinterpret_cast<const uint4*>(in + e0 * ROW)[q];
     const bool dense = stage_bases<L, T, EPB>(E, e0, R, dist, sigma, sR);
     if (el >= ne) return;
     float xr[D];
 #pragma unroll
-    for (int d = 0; d < D; ++d) xr[d] = sx[el * ROW + c * D + d];
+    for (int d = 0; d < D; ++d) xr[d] = static_cast<float>(sx[el * ROW + c * D + d]);
     const float* Rl = sR + el * D * D;
     __bf16* oe = out + (e0 + el) * ROW + c;
     if (!dense) {
@@ -476,8 +489,8 @@ k_hl_dfe(int64_t E, int64_t ntiles, const __bf16* __restrict__ fsT,
 
 // ---- U for the channel-pattern gradient ---------------------------------------------------
 // U[e, i, k, co] = sum over the terms (o, i, w) of sign F_e[k, w] gd[e, o, co]
-// (bf16), one workgroup per edge; a thread serves (k, co) pairs with the
-// edge's gd column of co in registers.
+// (bf16), one workgroup per edge; a thread holds the edge's gd column of one
+// channel co in registers and serves 256 / C of the ranks.
 template <int L, int K>
 __global__ void __launch_bounds__(kT)
 k_hl_u(feq_binning B, int C, const __bf16* __restrict__ gdT, const float* __restrict__ dist,
@@ -495,11 +508,13 @@ k_hl_u(feq_binning B, int C, const __bf16* __restrict__ gdT, const float* __rest
     __syncthreads();
     const __bf16* ge = gdT + e * D * C;
     __bf16* ue = U + e * D * K * C;
-    for (int q = tid; q < K * C; q += kT) {
-        const int k = q / C, co = q % C;
-        float g[D];
+    // thread (co, h) serves ranks h, h + KS, ... with the gd column of co in registers
+    const int KS = kT / C;
+    const int co = tid % C, h = tid / C;
+    float g[D];
 #pragma unroll
-        for (int o = 0; o < D; ++o) g[o] = static_cast<float>(ge[o * C + co]);
+    for (int o = 0; o < D; ++o) g[o] = static_cast<float>(ge[o * C + co]);
+    for (int k = h; k < K; k += KS) {
         const float* fk = sFe + k * WD;
         static_for<D>([&](auto II) __attribute__((always_inline)) {
             constexpr int i = decltype(II)::value;
