@@ -6,6 +6,7 @@ import torch.nn as nn
 
 from ..representations import Repr
 from ..utils import init_linear_weights
+from .linear import rows_linear
 from .norm import RepNorm, irrep_expand, irrep_slices
 
 
@@ -27,5 +28,7 @@ class EquivariantGating(nn.Module):
     def forward(self, st: torch.Tensor) -> torch.Tensor:
         norms = self.norm(st)
         *batch, _, _ = norms.shape
-        gates = self.activation(self.linear(norms.flatten(-2, -1)).view(*batch, *self.outdims))
+        flat = norms.flatten(-2, -1)
+        lin = rows_linear(flat.reshape(-1, flat.shape[-1]), self.linear.weight) + self.linear.bias
+        gates = self.activation(lin.view(*batch, *self.outdims))
         return st * irrep_expand(gates, self._slices)
