@@ -366,6 +366,36 @@ k_hl_mix(feq_binning B, int64_t E, int64_t ntiles, const __bf16* __restrict__ sr
     }
 }
 
+// Units of the m-block structure in m-first order: the L + 1 single slots of
+// m = 0, then for m = 1..L the L - m + 1 (+m, -m) slot pairs.  Unit u covers
+// source slots first(u) .. first(u) + width(u) - 1; its index within its
+// m-group is idx(u).
+template <int L>
+struct Units {
+    using H = HL<L>;
+    static constexpr int NU = (L + 1) + L * (L + 1) / 2;
+    static constexpr int m(int u) {
+        if (u <= L) return 0;
+        int mm = 1, rest = u - (L + 1);
+        while (rest >= L - mm + 1) {
+            rest -= L - mm + 1;
+            ++mm;
+        }
+        return mm;
+    }
+    static constexpr int idx(int u) {
+        if (u <= L) return u;
+        int mm = 1, rest = u - (L + 1);
+        while (rest >= L - mm + 1) {
+            rest -= L - mm + 1;
+            ++mm;
+        }
+        return rest;
+    }
+    static constexpr int width(int u) { return m(u) ? 2 : 1; }
+    static constexpr int first(int u) { return H::goff(m(u)) + width(u) * idx(u); }
+};
+
 // Sums of four per-lane values over the wave's four 16-lane rows: lane (row g,
 // column c) returns the sum over rows of v[g] at column c (gfx950 lane swaps).
 __device__ __forceinline__ float quad_row_sums(float v0, float v1, float v2, float v3) {
@@ -379,21 +409,25 @@ __device__ __forceinline__ float quad_row_sums(float v0, float v1, float v2, flo
 
 // ---- per-edge radial-function gradient ---------------------------------------------------
 // dF_e[e, k, w] = sum over the terms (o, i, w) of sign <gd[e, o, :], G_k[:, (e, i)]>,
-// G_k = C_k fs recomputed on the matrix cores as in the forward (source slots i
-// in m-first order).  Per term a lane forms the dot products over its 4 RBW
-// rows for the four ranks; they are summed over the wave's lane rows with lane
-// swaps (lane row g receives rank g) and added into the wave's LDS buffer of
-// the m-group's weights (read-add-write in the wave's program order); at the
+// G_k = C_k fs recomputed on the matrix cores (source units in m-first order).
+// In m-block m a source unit i and a destination o give, per rank,
+//   da = <gd_re(o), G_re(i)> + <gd_im(o), G_im(i)>,   db = <gd_re(o), G_im(i)> - <gd_im(o), G_re(i)>
+// for w = w_off(m) + 2 (o n + i) and w + 1 (block_diagonal.cu:514-517), and
+// <gd(o), G(i)> for w_off(0) + o n + i in m-block 0.  A lane forms the dot
+// products over its 4 RBW rows; the four ranks' values of one weight are
+// summed over the wave's lane rows with lane swaps (lane row g receives rank
+// g) and stored into the wave's LDS buffer of the m-group's weights; at the
 // group's end the four waves' buffers are summed in wave order and stored.
 template <int L, int COUT, int CIN, int K>
 __global__ void __launch_bounds__(kT, 1)
 k_hl_dfe(int64_t E, int64_t ntiles, const __bf16* __restrict__ fsT,
          const __bf16* __restrict__ gdT, const bf8* __restrict__ frag, float* __restrict__ dFe) {
     using H = HL<L>;
-    using TG = TermGroups<L, L, false>;
+    using U = Units<L>;
     constexpr int D = H::D, WD = H::WD, KW = K * WD;
     constexpr int RBW = COUT / 64, NKS = CIN / 32, NRB = COUT / 16;
     constexpr int WGM = H::WGMAX;
+    static_assert(K == 4, "one lane-row sum per weight: the four ranks");
     __shared__ float sD[4][K * WGM * kNE];     // per wave: [k WGM + w - w_off(m)][edge]
     const int tid = threadIdx.x, lane = tid & 63, le = lane & 15, lg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -406,7 +440,6 @@ k_hl_dfe(int64_t E, int64_t ntiles, const __bf16* __restrict__ fsT,
             for (int ks = 0; ks < NKS; ++ks)
                 A[k][rb][ks] = frag[((k * NRB + wave * RBW + rb) * NKS + ks) * 64 + lane];
     float* sw = sD[wave];
-    for (int q = lane; q < K * WGM * kNE; q += 64) sw[q] = 0.0f;
 
     for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
         const int64_t e0 = tile * kNE;
@@ -414,22 +447,24 @@ k_hl_dfe(int64_t E, int64_t ntiles, const __bf16* __restrict__ fsT,
         const int64_t ec = ok ? e0 + le : E - 1;
         const __bf16* srow = fsT + ec * D * CIN + 8 * lg;
         const __bf16* grow = gdT + ec * D * COUT + 16 * wave * RBW + 4 * lg;
-        bf8 b[3][NKS];
-        auto load = [&](int s, bf8(&bb)[NKS]) __attribute__((always_inline)) {
+        bf8 b[2][2][NKS];
+        auto load = [&](int s0, int w, bf8(&bb)[2][NKS]) __attribute__((always_inline)) {
 #pragma unroll
-            for (int ks = 0; ks < NKS; ++ks)
-                bb[ks] = *reinterpret_cast<const bf8*>(srow + s * CIN + 32 * ks);
+            for (int j = 0; j < 2; ++j)
+                if (j < w)
+#pragma unroll
+                    for (int ks = 0; ks < NKS; ++ks)
+                        bb[j][ks] = *reinterpret_cast<const bf8*>(srow + (s0 + j) * CIN + 32 * ks);
         };
-        load(0, b[0]);
-        if (D > 1) load(1, b[1]);
+        load(U::first(0), U::width(0), b[0]);
         float gd[H::GMAX][RBW][4];
-        static_for<D>([&](auto SS) __attribute__((always_inline)) {
-            constexpr int s = decltype(SS)::value;
-            constexpr int m = H::group_of(s), s0 = H::goff(m), ns = H::gsize(m);
-            constexpr int wo = Canon<L, L>::w_off(m);
-            if constexpr (s == s0) {
-                // gd rows of this lane for the group's output slots (zero for
-                // edges past the last: their terms then add nothing)
+        static_for<U::NU>([&](auto UU) __attribute__((always_inline)) {
+            constexpr int u = decltype(UU)::value;
+            constexpr int m = U::m(u), p = U::idx(u), n = L - m + 1, wdt = U::width(u);
+            constexpr int s0 = H::goff(m), ns = H::gsize(m), wo = Canon<L, L>::w_off(m);
+            if constexpr (p == 0) {
+                // gd rows of this lane for the group's slots (zero for edges past
+                // the last: their dot products then vanish)
 #pragma unroll
                 for (int d = 0; d < ns; ++d)
 #pragma unroll
@@ -439,36 +474,56 @@ k_hl_dfe(int64_t E, int64_t ntiles, const __bf16* __restrict__ fsT,
                         for (int r = 0; r < 4; ++r) gd[d][rb][r] = ok ? static_cast<float>(v[r]) : 0.0f;
                     }
             }
-            if constexpr (s + 2 < D) load(s + 2, b[(s + 2) % 3]);
-            v4f G[K][RBW];
+            if constexpr (u + 1 < U::NU) load(U::first(u + 1), U::width(u + 1), b[(u + 1) & 1]);
+            v4f G[2][K][RBW];
 #pragma unroll
-            for (int k = 0; k < K; ++k)
+            for (int j = 0; j < wdt; ++j)
 #pragma unroll
-                for (int rb = 0; rb < RBW; ++rb) {
-                    v4f g = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                for (int k = 0; k < K; ++k)
 #pragma unroll
-                    for (int ks = 0; ks < NKS; ++ks) g = mfma_bf(A[k][rb][ks], b[s % 3][ks], g);
-                    G[k][rb] = g;
+                    for (int rb = 0; rb < RBW; ++rb) {
+                        v4f g = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                        for (int ks = 0; ks < NKS; ++ks) g = mfma_bf(A[k][rb][ks], b[u & 1][j][ks], g);
+                        G[j][k][rb] = g;
+                    }
+#pragma unroll
+            for (int q = 0; q < n; ++q) {         // destination degree index o
+                if constexpr (m == 0) {
+                    float v[K];
+#pragma unroll
+                    for (int k = 0; k < K; ++k) {
+                        float a = 0.0f;
+#pragma unroll
+                        for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) a += gd[q][rb][r] * G[0][k][rb][r];
+                        v[k] = a;
+                    }
+                    const int wl = q * n + p;
+                    sw[(lg * WGM + wl) * kNE + le] = quad_row_sums(v[0], v[1], v[2], v[3]);
+                } else {
+                    float va[K], vb[K];
+#pragma unroll
+                    for (int k = 0; k < K; ++k) {
+                        float da = 0.0f, db = 0.0f;
+#pragma unroll
+                        for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const float gre = gd[2 * q][rb][r], gim = gd[2 * q + 1][rb][r];
+                                da += gre * G[0][k][rb][r] + gim * G[1][k][rb][r];
+                                db += gre * G[1][k][rb][r] - gim * G[0][k][rb][r];
+                            }
+                        va[k] = da;
+                        vb[k] = db;
+                    }
+                    const int wl = 2 * (q * n + p);
+                    sw[(lg * WGM + wl) * kNE + le] = quad_row_sums(va[0], va[1], va[2], va[3]);
+                    sw[(lg * WGM + wl + 1) * kNE + le] = quad_row_sums(vb[0], vb[1], vb[2], vb[3]);
                 }
-            static_for<TG::count(s)>([&](auto TT) __attribute__((always_inline)) {
-                constexpr Term tm = TG::sorted[TG::start[s] + decltype(TT)::value];
-                constexpr int o = tm.o - s0;
-                static_assert(K == 4, "one lane-row sum per term: the four ranks");
-                float p[K];
-#pragma unroll
-                for (int k = 0; k < K; ++k) {
-                    float a = 0.0f;
-#pragma unroll
-                    for (int rb = 0; rb < RBW; ++rb)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) a += gd[o][rb][r] * G[k][rb][r];
-                    p[k] = tm.neg ? -a : a;
-                }
-                // lane row lg receives the wave's sum for rank lg
-                const float v = quad_row_sums(p[0], p[1], p[2], p[3]);
-                sw[(lg * WGM + tm.w - wo) * kNE + le] += v;
-            });
-            if constexpr (s == s0 + ns - 1) {
+            }
+            if constexpr (p == n - 1) {
                 __syncthreads();   // every wave's buffer of the group is complete
                 constexpr int nw = H::wsize(m);
                 for (int q = tid; q < K * nw * kNE; q += kT) {
@@ -477,11 +532,7 @@ k_hl_dfe(int64_t E, int64_t ntiles, const __bf16* __restrict__ fsT,
                     const float v = sD[0][cell] + sD[1][cell] + sD[2][cell] + sD[3][cell];
                     if (e0 + ed < E) dFe[(e0 + ed) * KW + k * WD + wo + w] = v;
                 }
-                __syncthreads();
-                for (int q = lane; q < K * nw * kNE; q += 64) {
-                    const int ed = q % kNE, kwl = q / kNE, k = kwl / nw, w = kwl % nw;
-                    sw[(k * WGM + w) * kNE + ed] = 0.0f;
-                }
+                __syncthreads();   // the buffers are read before the next group writes them
             }
         });
     }
