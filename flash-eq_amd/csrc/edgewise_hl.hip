@@ -264,41 +264,42 @@ __device__ __forceinline__ void fill_tile_F(const feq_binning& B, int64_t E, int
 
 // ---- the mix on the matrix cores -----------------------------------------------------
 // Forward (TRANS = false): src = fs^T (E, D, NRED = Cin) bf16, A = C_k,
-//   dst[e, o, co] = sum_k sum_{terms (o, i, w)} sign F_e[k, w] G_k[co, (e, i)].
-// Input gradient (TRANS = true): src = gd^T (E, D, NRED = Cout), A = C_k^T,
-//   dst[e, i, ci] = sum_k sum_{terms (o, i, w)} sign F_e[k, w] H_k[ci, (e, o)].
+//   dst[e, o, co] = sum_k (M_ek G_k[co, (e, .)])[o],  G_k = C_k fs;
+// input gradient (TRANS = true): src = gd^T (E, D, NRED = Cout), A = C_k^T,
+//   dst[e, i, ci] = sum_k (M_ek^T H_k[ci, (e, .)])[i], H_k = C_k^T gd.
+// M_ek is applied block by block: in m-block m (n = L - m + 1 degrees) with
+// weights a = F_e[k, w], b = F_e[k, w + 1], w = w_off(m) + 2 (o n + i),
+//   forward:  y_re(o) += a G_re(i) + b G_im(i),   y_im(o) += a G_im(i) - b G_re(i)
+//   gradient: g_re(i) += a H_re(o) - b H_im(o),   g_im(i) += b H_re(o) + a H_im(o)
+// (block_diagonal.cu:483-503), and y(o) += F_e[k, o n + i] G(i) in m-block 0.
 // A workgroup of NROW / 16 waves owns a 16-edge tile at a time (lane l serves
 // edge l % 16, the B column); wave w owns the output rows 16 w .. 16 w + 15 and
-// holds the A fragments of every rank for them (one row block per wave keeps
-// the fragments and the accumulators of a group within 256 registers; the
-// waves read the same B fragments, from L1 after the first).  The source slots
-// run in m-first order; the slots of one m-group write into the same group's
-// destination slots only, so the accumulators of a group live in registers
-// until the group's last slot, then go out as 16-byte stores.  B fragments
-// are loaded two slots ahead.
+// holds the A fragments of every rank for them.  The m-groups are unrolled;
+// the source units of a group (single slots for m = 0, (+m, -m) pairs above)
+// run as a loop, whose bounds keep each unit's products, weights and
+// accumulator updates together (fully unrolled, the compiler interleaves the
+// units and spills).  The group's accumulators live in registers until its
+// end, then go out as 16-byte stores; each unit's B fragments are loaded
+// while the previous unit is contracted.
 template <int L, int NROW, int NRED, int K, bool TRANS>
 __global__ void __launch_bounds__(NROW * 4, 1)
 k_hl_mix(feq_binning B, int64_t E, int64_t ntiles, const __bf16* __restrict__ src,
          const float* __restrict__ dist, const float* __restrict__ F,
          const bf8* __restrict__ frag, float* __restrict__ dst) {
     using H = HL<L>;
-    using TG = TermGroups<L, L, TRANS>;
     constexpr int D = H::D, WD = H::WD, KW = K * WD;
-    constexpr int RBW = 1, NKS = NRED / 32, NRB = NROW / 16, NT = NROW * 4;
+    constexpr int NKS = NRED / 32, NRB = NROW / 16, NT = NROW * 4;
     static_assert(NROW % 16 == 0 && NRED % 32 == 0 && NT <= 1024, "channel counts");
     __shared__ float sF[KW * kNE];
     __shared__ int slo[kNE];
     __shared__ float st[kNE];
     const int tid = threadIdx.x, lane = tid & 63, le = lane & 15, lg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    bf8 A[K][RBW][NKS];
+    bf8 A[K][NKS];
 #pragma unroll
     for (int k = 0; k < K; ++k)
 #pragma unroll
-        for (int rb = 0; rb < RBW; ++rb)
-#pragma unroll
-            for (int ks = 0; ks < NKS; ++ks)
-                A[k][rb][ks] = frag[((k * NRB + wave * RBW + rb) * NKS + ks) * 64 + lane];
+        for (int ks = 0; ks < NKS; ++ks) A[k][ks] = frag[((k * NRB + wave) * NKS + ks) * 64 + lane];
 
     for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
         const int64_t e0 = tile * kNE;
@@ -307,94 +308,81 @@ k_hl_mix(feq_binning B, int64_t E, int64_t ntiles, const __bf16* __restrict__ sr
         const bool ok = e0 + le < E;
         const int64_t ec = ok ? e0 + le : E - 1;
         const __bf16* srow = src + ec * D * NRED + 8 * lg;
-        float* drow = dst + ec * D * NROW + 16 * wave * RBW + 4 * lg;
-        bf8 b[3][NKS];
-        auto load = [&](int s, bf8(&bb)[NKS]) __attribute__((always_inline)) {
+        float* drow = dst + ec * D * NROW + 16 * wave + 4 * lg;
+        const float* fl = sF + le;
+        bf8 b[2][NKS];                           // the unit's slots x k-steps
+        auto load = [&](int s0, int w) __attribute__((always_inline)) {
 #pragma unroll
-            for (int ks = 0; ks < NKS; ++ks)
-                bb[ks] = *reinterpret_cast<const bf8*>(srow + s * NRED + 32 * ks);
+            for (int j = 0; j < 2; ++j)
+                if (j < w)
+#pragma unroll
+                    for (int ks = 0; ks < NKS; ++ks)
+                        b[j][ks] = *reinterpret_cast<const bf8*>(srow + (s0 + j) * NRED + 32 * ks);
         };
-        load(0, b[0]);
-        if (D > 1) load(1, b[1]);
-        float acc[RBW][H::GMAX][4];
-        static_for<D>([&](auto SS) __attribute__((always_inline)) {
-            constexpr int s = decltype(SS)::value;
-            constexpr int m = H::group_of(s), s0 = H::goff(m), ns = H::gsize(m);
-            if constexpr (s == s0) {
+        load(0, 1);
+        float acc[H::GMAX][4];
+        static_for<H::NG>([&](auto MM) __attribute__((always_inline)) {
+            constexpr int m = decltype(MM)::value, n = L - m + 1, wdt = m ? 2 : 1;
+            constexpr int s0 = H::goff(m), ns = H::gsize(m), wo = Canon<L, L>::w_off(m);
 #pragma unroll
-                for (int rb = 0; rb < RBW; ++rb)
+            for (int d = 0; d < ns; ++d)
 #pragma unroll
-                    for (int d = 0; d < ns; ++d)
+                for (int r = 0; r < 4; ++r) acc[d][r] = 0.0f;
+#pragma unroll 1
+            for (int p = 0; p < n; ++p) {
+                v4f G[2][K];
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) acc[rb][d][r] = 0.0f;
+                for (int j = 0; j < wdt; ++j)
+#pragma unroll
+                    for (int k = 0; k < K; ++k) {
+                        v4f g = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                        for (int ks = 0; ks < NKS; ++ks) g = mfma_bf(A[k][ks], b[j][ks], g);
+                        G[j][k] = g;
+                    }
+                // the unit's B fragments are consumed: the next unit's (or the
+                // next group's first) loads fly during this unit's contraction
+                if (p + 1 < n) {
+                    load(s0 + wdt * (p + 1), wdt);
+                } else if constexpr (m + 1 < H::NG) {
+                    load(H::goff(m + 1), 2);
+                }
+#pragma unroll
+                for (int q = 0; q < n; ++q) {
+#pragma unroll
+                    for (int k = 0; k < K; ++k) {
+                        if constexpr (m == 0) {
+                            const int w = TRANS ? wo + p * n + q : wo + q * n + p;
+                            const float f = fl[(k * WD + w) * kNE];
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) acc[q][r] += f * G[0][k][r];
+                        } else {
+                            const int w = TRANS ? wo + 2 * (p * n + q) : wo + 2 * (q * n + p);
+                            const float fa = fl[(k * WD + w) * kNE], fb = fl[(k * WD + w + 1) * kNE];
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const float gre = G[0][k][r], gim = G[1][k][r];
+                                if constexpr (!TRANS) {
+                                    acc[2 * q][r] += fa * gre + fb * gim;
+                                    acc[2 * q + 1][r] += fa * gim - fb * gre;
+                                } else {
+                                    acc[2 * q][r] += fa * gre - fb * gim;
+                                    acc[2 * q + 1][r] += fb * gre + fa * gim;
+                                }
+                            }
+                        }
+                    }
+                }
             }
-            if constexpr (s + 2 < D) load(s + 2, b[(s + 2) % 3]);
-            v4f G[K][RBW];
+            if (ok) {
 #pragma unroll
-            for (int k = 0; k < K; ++k)
-#pragma unroll
-                for (int rb = 0; rb < RBW; ++rb) {
-                    v4f g = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                    for (int ks = 0; ks < NKS; ++ks) g = mfma_bf(A[k][rb][ks], b[s % 3][ks], g);
-                    G[k][rb] = g;
-                }
-            static_for<TG::count(s)>([&](auto TT) __attribute__((always_inline)) {
-                constexpr Term tm = TG::sorted[TG::start[s] + decltype(TT)::value];
-                constexpr int dsl = (TRANS ? tm.i : tm.o) - s0;
-#pragma unroll
-                for (int k = 0; k < K; ++k) {
-                    const float f0 = sF[(k * WD + tm.w) * kNE + le];
-                    const float f = tm.neg ? -f0 : f0;
-#pragma unroll
-                    for (int rb = 0; rb < RBW; ++rb)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) acc[rb][dsl][r] += f * G[k][rb][r];
-                }
-            });
-            if constexpr (s == s0 + ns - 1) {
-                if (ok) {
-#pragma unroll
-                    for (int d = 0; d < ns; ++d)
-#pragma unroll
-                        for (int rb = 0; rb < RBW; ++rb)
-                            *reinterpret_cast<float4*>(drow + (s0 + d) * NROW + 16 * rb) =
-                                make_float4(acc[rb][d][0], acc[rb][d][1], acc[rb][d][2], acc[rb][d][3]);
-                }
+                for (int d = 0; d < ns; ++d)
+                    *reinterpret_cast<float4*>(drow + (s0 + d) * NROW) =
+                        make_float4(acc[d][0], acc[d][1], acc[d][2], acc[d][3]);
             }
         });
     }
 }
-
-// Units of the m-block structure in m-first order: the L + 1 single slots of
-// m = 0, then for m = 1..L the L - m + 1 (+m, -m) slot pairs.  Unit u covers
-// source slots first(u) .. first(u) + width(u) - 1; its index within its
-// m-group is idx(u).
-template <int L>
-struct Units {
-    using H = HL<L>;
-    static constexpr int NU = (L + 1) + L * (L + 1) / 2;
-    static constexpr int m(int u) {
-        if (u <= L) return 0;
-        int mm = 1, rest = u - (L + 1);
-        while (rest >= L - mm + 1) {
-            rest -= L - mm + 1;
-            ++mm;
-        }
-        return mm;
-    }
-    static constexpr int idx(int u) {
-        if (u <= L) return u;
-        int mm = 1, rest = u - (L + 1);
-        while (rest >= L - mm + 1) {
-            rest -= L - mm + 1;
-            ++mm;
-        }
-        return rest;
-    }
-    static constexpr int width(int u) { return m(u) ? 2 : 1; }
-    static constexpr int first(int u) { return H::goff(m(u)) + width(u) * idx(u); }
-};
 
 // Sums of four per-lane values over the wave's four 16-lane rows: lane (row g,
 // column c) returns the sum over rows of v[g] at column c (gfx950 lane swaps).
@@ -409,7 +397,8 @@ __device__ __forceinline__ float quad_row_sums(float v0, float v1, float v2, flo
 
 // ---- per-edge radial-function gradient ---------------------------------------------------
 // dF_e[e, k, w] = sum over the terms (o, i, w) of sign <gd[e, o, :], G_k[:, (e, i)]>,
-// G_k = C_k fs recomputed on the matrix cores (source units in m-first order).
+// G_k = C_k fs recomputed on the matrix cores (m-groups unrolled, the units of
+// a group in a loop, as in k_hl_mix).
 // In m-block m a source unit i and a destination o give, per rank,
 //   da = <gd_re(o), G_re(i)> + <gd_im(o), G_im(i)>,   db = <gd_re(o), G_im(i)> - <gd_im(o), G_re(i)>
 // for w = w_off(m) + 2 (o n + i) and w + 1 (block_diagonal.cu:514-517), and
@@ -423,7 +412,6 @@ __global__ void __launch_bounds__(kT, 1)
 k_hl_dfe(int64_t E, int64_t ntiles, const __bf16* __restrict__ fsT,
          const __bf16* __restrict__ gdT, const bf8* __restrict__ frag, float* __restrict__ dFe) {
     using H = HL<L>;
-    using U = Units<L>;
     constexpr int D = H::D, WD = H::WD, KW = K * WD;
     constexpr int RBW = COUT / 64, NKS = CIN / 32, NRB = COUT / 16;
     constexpr int WGM = H::WGMAX;
@@ -447,93 +435,96 @@ k_hl_dfe(int64_t E, int64_t ntiles, const __bf16* __restrict__ fsT,
         const int64_t ec = ok ? e0 + le : E - 1;
         const __bf16* srow = fsT + ec * D * CIN + 8 * lg;
         const __bf16* grow = gdT + ec * D * COUT + 16 * wave * RBW + 4 * lg;
-        bf8 b[2][2][NKS];
-        auto load = [&](int s0, int w, bf8(&bb)[2][NKS]) __attribute__((always_inline)) {
+        bf8 b[2][NKS];
+        auto load = [&](int s0, int w) __attribute__((always_inline)) {
 #pragma unroll
             for (int j = 0; j < 2; ++j)
                 if (j < w)
 #pragma unroll
                     for (int ks = 0; ks < NKS; ++ks)
-                        bb[j][ks] = *reinterpret_cast<const bf8*>(srow + (s0 + j) * CIN + 32 * ks);
+                        b[j][ks] = *reinterpret_cast<const bf8*>(srow + (s0 + j) * CIN + 32 * ks);
         };
-        load(U::first(0), U::width(0), b[0]);
+        load(0, 1);
         float gd[H::GMAX][RBW][4];
-        static_for<U::NU>([&](auto UU) __attribute__((always_inline)) {
-            constexpr int u = decltype(UU)::value;
-            constexpr int m = U::m(u), p = U::idx(u), n = L - m + 1, wdt = U::width(u);
-            constexpr int s0 = H::goff(m), ns = H::gsize(m), wo = Canon<L, L>::w_off(m);
-            if constexpr (p == 0) {
-                // gd rows of this lane for the group's slots (zero for edges past
-                // the last: their dot products then vanish)
+        static_for<H::NG>([&](auto MM) __attribute__((always_inline)) {
+            constexpr int m = decltype(MM)::value, n = L - m + 1, wdt = m ? 2 : 1;
+            constexpr int s0 = H::goff(m), ns = H::gsize(m);
+            constexpr int wo = Canon<L, L>::w_off(m);
+            // gd rows of this lane for the group's slots (zero for edges past the
+            // last: their dot products then vanish)
 #pragma unroll
-                for (int d = 0; d < ns; ++d)
+            for (int d = 0; d < ns; ++d)
 #pragma unroll
-                    for (int rb = 0; rb < RBW; ++rb) {
-                        const bf4 v = *reinterpret_cast<const bf4*>(grow + (s0 + d) * COUT + 16 * rb);
+                for (int rb = 0; rb < RBW; ++rb) {
+                    const bf4 v = *reinterpret_cast<const bf4*>(grow + (s0 + d) * COUT + 16 * rb);
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) gd[d][rb][r] = ok ? static_cast<float>(v[r]) : 0.0f;
+                    for (int r = 0; r < 4; ++r) gd[d][rb][r] = ok ? static_cast<float>(v[r]) : 0.0f;
+                }
+#pragma unroll 1
+            for (int p = 0; p < n; ++p) {
+                v4f G[2][K][RBW];
+#pragma unroll
+                for (int j = 0; j < wdt; ++j)
+#pragma unroll
+                    for (int k = 0; k < K; ++k)
+#pragma unroll
+                        for (int rb = 0; rb < RBW; ++rb) {
+                            v4f g = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                            for (int ks = 0; ks < NKS; ++ks) g = mfma_bf(A[k][rb][ks], b[j][ks], g);
+                            G[j][k][rb] = g;
+                        }
+                if (p + 1 < n) {
+                    load(s0 + wdt * (p + 1), wdt);
+                } else if constexpr (m + 1 < H::NG) {
+                    load(H::goff(m + 1), 2);
+                }
+#pragma unroll
+                for (int q = 0; q < n; ++q) {     // destination degree index o
+                    if constexpr (m == 0) {
+                        float v[K];
+#pragma unroll
+                        for (int k = 0; k < K; ++k) {
+                            float a = 0.0f;
+#pragma unroll
+                            for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+                                for (int r = 0; r < 4; ++r) a += gd[q][rb][r] * G[0][k][rb][r];
+                            v[k] = a;
+                        }
+                        const int wl = q * n + p;
+                        sw[(lg * WGM + wl) * kNE + le] = quad_row_sums(v[0], v[1], v[2], v[3]);
+                    } else {
+                        float va[K], vb[K];
+#pragma unroll
+                        for (int k = 0; k < K; ++k) {
+                            float da = 0.0f, db = 0.0f;
+#pragma unroll
+                            for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+                                for (int r = 0; r < 4; ++r) {
+                                    const float gre = gd[2 * q][rb][r], gim = gd[2 * q + 1][rb][r];
+                                    da += gre * G[0][k][rb][r] + gim * G[1][k][rb][r];
+                                    db += gre * G[1][k][rb][r] - gim * G[0][k][rb][r];
+                                }
+                            va[k] = da;
+                            vb[k] = db;
+                        }
+                        const int wl = 2 * (q * n + p);
+                        sw[(lg * WGM + wl) * kNE + le] = quad_row_sums(va[0], va[1], va[2], va[3]);
+                        sw[(lg * WGM + wl + 1) * kNE + le] = quad_row_sums(vb[0], vb[1], vb[2], vb[3]);
                     }
-            }
-            if constexpr (u + 1 < U::NU) load(U::first(u + 1), U::width(u + 1), b[(u + 1) & 1]);
-            v4f G[2][K][RBW];
-#pragma unroll
-            for (int j = 0; j < wdt; ++j)
-#pragma unroll
-                for (int k = 0; k < K; ++k)
-#pragma unroll
-                    for (int rb = 0; rb < RBW; ++rb) {
-                        v4f g = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                        for (int ks = 0; ks < NKS; ++ks) g = mfma_bf(A[k][rb][ks], b[u & 1][j][ks], g);
-                        G[j][k][rb] = g;
-                    }
-#pragma unroll
-            for (int q = 0; q < n; ++q) {         // destination degree index o
-                if constexpr (m == 0) {
-                    float v[K];
-#pragma unroll
-                    for (int k = 0; k < K; ++k) {
-                        float a = 0.0f;
-#pragma unroll
-                        for (int rb = 0; rb < RBW; ++rb)
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) a += gd[q][rb][r] * G[0][k][rb][r];
-                        v[k] = a;
-                    }
-                    const int wl = q * n + p;
-                    sw[(lg * WGM + wl) * kNE + le] = quad_row_sums(v[0], v[1], v[2], v[3]);
-                } else {
-                    float va[K], vb[K];
-#pragma unroll
-                    for (int k = 0; k < K; ++k) {
-                        float da = 0.0f, db = 0.0f;
-#pragma unroll
-                        for (int rb = 0; rb < RBW; ++rb)
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) {
-                                const float gre = gd[2 * q][rb][r], gim = gd[2 * q + 1][rb][r];
-                                da += gre * G[0][k][rb][r] + gim * G[1][k][rb][r];
-                                db += gre * G[1][k][rb][r] - gim * G[0][k][rb][r];
-                            }
-                        va[k] = da;
-                        vb[k] = db;
-                    }
-                    const int wl = 2 * (q * n + p);
-                    sw[(lg * WGM + wl) * kNE + le] = quad_row_sums(va[0], va[1], va[2], va[3]);
-                    sw[(lg * WGM + wl + 1) * kNE + le] = quad_row_sums(vb[0], vb[1], vb[2], vb[3]);
                 }
             }
-            if constexpr (p == n - 1) {
-                __syncthreads();   // every wave's buffer of the group is complete
-                constexpr int nw = H::wsize(m);
-                for (int q = tid; q < K * nw * kNE; q += kT) {
-                    const int ed = q % kNE, kwl = q / kNE, k = kwl / nw, w = kwl % nw;
-                    const int cell = (k * WGM + w) * kNE + ed;
-                    const float v = sD[0][cell] + sD[1][cell] + sD[2][cell] + sD[3][cell];
-                    if (e0 + ed < E) dFe[(e0 + ed) * KW + k * WD + wo + w] = v;
-                }
-                __syncthreads();   // the buffers are read before the next group writes them
+            __syncthreads();   // every wave's buffer of the group is complete
+            constexpr int nw = H::wsize(m);
+            for (int q = tid; q < K * nw * kNE; q += kT) {
+                const int ed = q % kNE, kwl = q / kNE, k = kwl / nw, w = kwl % nw;
+                const int cell = (k * WGM + w) * kNE + ed;
+                const float v = sD[0][cell] + sD[1][cell] + sD[2][cell] + sD[3][cell];
+                if (e0 + ed < E) dFe[(e0 + ed) * KW + k * WD + wo + w] = v;
             }
+            __syncthreads();   // the buffers are read before the next group writes them
         });
     }
 }
