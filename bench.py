@@ -212,7 +212,9 @@ def timed_steps(step, steps: int, warmup: int):
 
 def secondary_workload(name: str, steps: int, warmup: int) -> dict:
     """The other BASELINE configs at their full sizes (parity-test cases, reported
-    beside the metric's line): c3 = EquivariantTransformerBlock, 8 heads,
+    beside the metric's line): c1 = the reference's CPU-sized layer (gather,
+    layer, scatter-sum); c4 = the 6-layer EquivariantTransformer on a 50k-node
+    random-walk chain (E = 1.2M); c3 = EquivariantTransformerBlock, 8 heads,
     [0,1,2]x64, radius-10 graph capped at 32 neighbours on 20k nodes in 60^3
     (E = 640k), fwd + bwd including WignerDBasis, fp32 or bf16; c5 = one
     EquivariantEdgewiseLinear [0..6]x128, kNN k=32 on 5k nodes in 30^3
@@ -241,6 +243,61 @@ def secondary_workload(name: str, steps: int, warmup: int) -> dict:
         workload = (f"c3: EquivariantTransformerBlock 8 heads [0,1,2]x64, radius-10 graph capped at "
                     f"k=32 on 20k nodes in 60^3, E={E}, fwd+bwd incl. WignerDBasis, {dtype}")
         work = algorithmic_per_edge([0, 1, 2], [0, 1, 2], 64, 64)
+    elif name == "c4":
+        # random-walk chain, 3.8-unit steps in uniform random directions
+        g = torch.Generator().manual_seed(1004)
+        N = 50000
+        u = torch.randn(N, 3, generator=g, dtype=torch.float64)
+        u = u / u.norm(dim=1, keepdim=True)
+        coords = torch.cumsum(3.8 * u, 0).float()
+        coords = coords - coords[0]
+        from scipy.spatial import cKDTree
+        _, idx = cKDTree(coords.double().numpy()).query(coords.double().numpy(), k=25)
+        src = torch.from_numpy(idx[:, 1:].astype(np.int64)).reshape(-1)
+        dst = torch.arange(N).repeat_interleave(24)
+        E = src.numel()
+        feats = torch.randn(N, 32, 4, generator=g).to(dev).requires_grad_(True)
+        torch.manual_seed(4)
+        # out Repr([0], mult=1) cannot be split into 8 heads (attention.py:233-234);
+        # mult=8 is the nearest constructible output
+        model = fe.EquivariantTransformer(fe.Repr([0, 1], 32), fe.Repr([0, 1, 2], 64),
+                                          fe.Repr([0], 8), num_layers=6, num_heads=8,
+                                          max_dist=10.0).to(dev)
+        graph = fe.Graph(src.to(dev), dst.to(dev), N)
+        xyz = coords.to(dev)
+
+        def step():
+            out = model(xyz, feats, graph)
+            SumOfSquares.apply(out).backward()
+        workload = (f"c4: EquivariantTransformer 6 layers, in [0,1]x32, hidden [0,1,2]x64, out [0]x8 "
+                    f"(x1 is not divisible into 8 heads), 8 heads, random-walk chain of 50k nodes, "
+                    f"kNN k=24, E={E}, fwd+bwd incl. WignerDBasis, fp32")
+        work = algorithmic_per_edge([0, 1, 2], [0, 1, 2], 64, 64)
+    elif name == "c1":
+        g = torch.Generator().manual_seed(1001)
+        N, E = 100, 500
+        coords = torch.randn(N, 3, generator=g) * 3
+        src = torch.randint(0, N, (E,), generator=g)
+        dst = torch.randint(0, N, (E,), generator=g)
+        while (src == dst).any():
+            bad = src == dst
+            dst[bad] = torch.randint(0, N, (int(bad.sum()),), generator=g)
+        feats = torch.randn(N, 32, 4, generator=g).to(dev).requires_grad_(True)
+        torch.manual_seed(1)
+        rin, rout = fe.Repr([0, 1], 32), fe.Repr([0, 1, 2], 64)
+        layer = fe.EquivariantEdgewiseLinear(rin, rout, num_bins=100, max_dist=10.0).to(dev)
+        graph = fe.Graph(src.to(dev), dst.to(dev), N)
+        vec = coords.to(dev)[graph.src] - coords.to(dev)[graph.dst]
+        dist = vec.norm(dim=-1)
+        P, Q = fe.WignerDBasis([rin, rout]).to(dev)(vec)
+        pool = fe.GraphPooling("sum")
+
+        def step():
+            y = layer(P, Q, feats, dist, graph=graph)
+            SumOfSquares.apply(pool(y, graph)).backward()
+        workload = ("c1: EquivariantEdgewiseLinear [0,1]x32 -> [0,1,2]x64, N=100, E=500 random "
+                    "edges (self-loops resampled), gather + layer + scatter-sum, fp32")
+        work = algorithmic_per_edge([0, 1], [0, 1, 2], 32, 64)
     elif name == "c5":
         lv = list(range(7))
         coords, src, dst = knn_graph(5000, 32, 30.0, seed=1005)
@@ -291,7 +348,7 @@ def main() -> int:
     ap.add_argument("--grad-dist", action="store_true", help="also differentiate w.r.t. distances")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run 1 GiB device copies first (for rocprofv3 --pmc byte calibration)")
-    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c3bf16", "c5"],
+    ap.add_argument("--workload", default="c2", choices=["c2", "c1", "c3", "c3bf16", "c4", "c5"],
                     help="c2 (default) is the metric's configuration; the others print a "
                          "secondary line with their full-size throughput and kernel times")
     args = ap.parse_args()

@@ -13,6 +13,7 @@ table are written to memory.
 """
 from __future__ import annotations
 
+import os
 from functools import lru_cache
 from typing import Tuple
 
@@ -20,7 +21,7 @@ import torch
 import torch.nn as nn
 
 from .. import _native as N
-from ..ops import edgewise_linear, edgewise_linear_src, edgewise_src_supported
+from ..ops import edgewise_linear, edgewise_linear_src, edgewise_src_supported, embedding_for
 from ..representations import ProductRepr, Repr
 from .radial import SeparableRadialNet
 
@@ -95,6 +96,23 @@ class EquivariantEdgewiseLinear(nn.Module):
     def layout(self) -> N.FeqLayout:
         return _layout(self._lin, self._lout, self.channels_in, self.channels_out)
 
+    # below this many edges the shape-generic kernels beat the padded fast ones
+    EMBED_MIN_EDGES = 4096
+
+    def _embedding(self, x, num_edges, layout, binning):
+        """The zero-embedding into the [0,1,2]x64 kernels when this layout has no
+        split-fp16 backward of its own, else None (only canonical prefixes of
+        [0, 1, 2] with at most 64 channels embed).  ``FEQ_EW_PATH`` other than the default keeps the
+        layout's own kernels."""
+        if os.environ.get("FEQ_EW_PATH") or os.environ.get("FEQ_FORCE_GENERIC") == "1":
+            return None
+        if num_edges < self.EMBED_MIN_EDGES:
+            return None
+        if edgewise_src_supported(layout, binning, self.radial_weights.rank):
+            return None
+        return embedding_for(self._lin, self._lout, self.channels_in, self.channels_out,
+                             self.radial_weights.rank, x.device)
+
     def binning(self) -> N.FeqBinning:
         rw = self.radial_weights
         p1, p2 = rw.binning_params()
@@ -113,6 +131,22 @@ class EquivariantEdgewiseLinear(nn.Module):
         N.require_cuda_tensor(edge_features, "edge_features")
         rw = self.radial_weights
         layout, binning = self.layout(), self.binning()
+        emb = self._embedding(edge_features, distances.shape[0], layout, binning)
+        if emb is not None:
+            # a small layout without split-fp16 backward kernels: run it
+            # zero-embedded in the [0,1,2]x64 kernels (ops._Embedding)
+            x = emb.features(edge_features)
+            Pp, Qp = emb.basis(P, emb.pcols), emb.basis(Q, emb.qcols)
+            C, F = emb.channels(rw.channel_patterns), emb.radial(rw.radial_functions())
+            if graph is not None:
+                if graph.num_edges != distances.shape[0]:
+                    raise ValueError(f"graph has {graph.num_edges} edges, distances {distances.shape[0]}")
+                perm, offsets = graph.csr_src()
+                y = edgewise_linear_src(x, graph.src, perm, offsets, Pp, Qp, distances, C, F,
+                                        emb.layout, binning, rw.rank)
+            else:
+                y = edgewise_linear(x, Pp, Qp, distances, C, F, emb.layout, binning, rw.rank)
+            return emb.output(y)
         if graph is not None:
             if graph.num_edges != distances.shape[0]:
                 raise ValueError(f"graph has {graph.num_edges} edges, distances {distances.shape[0]}")

@@ -173,6 +173,113 @@ def edgewise_linear_src(x, src, perm, offsets, P, Q, dist, C, F, layout, binning
     return EdgewiseLinearSrcFn.apply(x, src, perm, offsets, P, Q, dist, C, F, layout, binning, rank)
 
 
+# ---------------------------------------------------------------------------
+# embedding of small canonical layouts into the config-2 shape
+# ---------------------------------------------------------------------------
+_EMB_L, _EMB_C = 2, 64
+
+
+def _mfirst_positions(L: int) -> dict:
+    """(l, m, c) -> slot of the m-first order of lvals 0..L (m = 0 one slot per
+    l; then for m = 1..L and l >= m the (+m, -m) pair, c = 0 / 1)."""
+    pos, k = {}, 0
+    for l in range(L + 1):
+        pos[(l, 0, 0)] = k
+        k += 1
+    for m in range(1, L + 1):
+        for l in range(m, L + 1):
+            pos[(l, m, 0)], pos[(l, m, 1)] = k, k + 1
+            k += 2
+    return pos
+
+
+def _weight_positions(lin: int, lout: int) -> dict:
+    """(m, o, i, c) -> radial weight index of the m-block layout of the canonical
+    pair 0..lin -> 0..lout (block_diagonal.cu:1220-1258): in block m the i-th
+    input degree is m + i and the o-th output degree m + o."""
+    pos, off = {}, 0
+    for m in range(min(lin, lout) + 1):
+        ni, no = lin - m + 1, lout - m + 1
+        for o in range(no):
+            for i in range(ni):
+                if m == 0:
+                    pos[(m, o, i, 0)] = off + o * ni + i
+                else:
+                    pos[(m, o, i, 0)] = off + 2 * (o * ni + i)
+                    pos[(m, o, i, 1)] = off + 2 * (o * ni + i) + 1
+        off += (1 if m == 0 else 2) * ni * no
+    return pos
+
+
+class _Embedding:
+    """Runs a layer of canonical lvals 0..lin -> 0..lout (lin, lout <= 2) and at
+    most 64 channels with the kernels of [0,1,2]x64 -> [0,1,2]x64: features,
+    channel patterns and bases are zero-padded, the radial functions placed at
+    their weights' positions in the larger layout (zeros elsewhere), and the
+    output cut back.  Padded inputs are zero, so they add exact zeros; the
+    power-of-two block scales of the split kernels come from block maxima and
+    do not change.  All steps are torch ops, so autograd carries the gradients."""
+
+    def __init__(self, lin: int, lout: int, cin: int, cout: int, device):
+        L = _EMB_L
+        self.lin, self.lout, self.cin, self.cout = lin, lout, cin, cout
+        self.din, self.dout, self.D = (lin + 1) ** 2, (lout + 1) ** 2, (L + 1) ** 2
+
+        def cols(lmax):
+            big, small = _mfirst_positions(L), _mfirst_positions(lmax)
+            src = [None] * self.D
+            for key, js in small.items():
+                src[big[key]] = js
+            d = (lmax + 1) ** 2
+            pad = iter(range(d, self.D))
+            return torch.tensor([j if j is not None else next(pad) for j in src], device=device)
+
+        self.pcols, self.qcols = cols(lin), cols(lout)
+        ws, wb = _weight_positions(lin, lout), _weight_positions(L, L)
+        self.wdim = len(ws)
+        wsrc = [self.wdim] * len(wb)          # index wdim: an appended zero column
+        for key, w in ws.items():
+            wsrc[wb[key]] = w
+        self.wsrc = torch.tensor(wsrc, device=device)
+        self.layout = N.make_layout(list(range(L + 1)), list(range(L + 1)), _EMB_C, _EMB_C)
+
+    def features(self, x):
+        return torch.nn.functional.pad(x, (0, self.D - x.shape[-1], 0, _EMB_C - x.shape[-2]))
+
+    def basis(self, R, cols):
+        d = R.shape[-1]
+        Rp = torch.nn.functional.pad(R, (0, self.D - d, 0, self.D - d))
+        return torch.index_select(Rp, 2, cols)
+
+    def channels(self, C):
+        return torch.nn.functional.pad(C, (0, _EMB_C - self.cin, 0, _EMB_C - self.cout))
+
+    def radial(self, F):
+        return torch.index_select(torch.nn.functional.pad(F, (0, 1)), 2, self.wsrc)
+
+    def output(self, y):
+        return y[:, :self.cout, :self.dout]
+
+
+_EMB_CACHE: dict = {}
+
+
+def embedding_for(lvals_in, lvals_out, cin: int, cout: int, rank: int, device) -> Optional[_Embedding]:
+    """The embedding of a layout into the config-2 kernels, or None when the
+    layout is not a canonical prefix of [0, 1, 2] with at most 64 channels."""
+    lin, lout = tuple(lvals_in), tuple(lvals_out)
+    if rank != 4 or cin > _EMB_C or cout > _EMB_C:
+        return None
+    if lin != tuple(range(len(lin))) or lout != tuple(range(len(lout))):
+        return None
+    if len(lin) - 1 > _EMB_L or len(lout) - 1 > _EMB_L:
+        return None
+    key = (lin, lout, cin, cout, str(device))
+    if key not in _EMB_CACHE:
+        _EMB_CACHE[key] = _Embedding(len(lin) - 1, len(lout) - 1, cin, cout, device)
+    return _EMB_CACHE[key]
+
+
 def _check_edgewise_shapes(L, b, rank, x, P, Q, r, C, F) -> None:
     E = x.shape[0]
     if x.shape != (E, L.cin, L.din):
