@@ -226,13 +226,15 @@ class _Embedding:
         self.din, self.dout, self.D = (lin + 1) ** 2, (lout + 1) ** 2, (L + 1) ** 2
 
         def cols(lmax):
+            """Slots of the larger m-first order that the small order's slots take
+            (None when the small order is the larger one)."""
+            if lmax == L:
+                return None
             big, small = _mfirst_positions(L), _mfirst_positions(lmax)
-            src = [None] * self.D
+            at = [0] * len(small)
             for key, js in small.items():
-                src[big[key]] = js
-            d = (lmax + 1) ** 2
-            pad = iter(range(d, self.D))
-            return torch.tensor([j if j is not None else next(pad) for j in src], device=device)
+                at[js] = big[key]
+            return torch.tensor(at, device=device)
 
         self.pcols, self.qcols = cols(lin), cols(lout)
         ws, wb = _weight_positions(lin, lout), _weight_positions(L, L)
@@ -247,9 +249,14 @@ class _Embedding:
         return torch.nn.functional.pad(x, (0, self.D - x.shape[-1], 0, _EMB_C - x.shape[-2]))
 
     def basis(self, R, cols):
+        """R (E, d, d) placed in a zero (E, D, D): rows d in the standard order
+        keep their index, column j goes to cols[j]."""
+        if cols is None:
+            return R
         d = R.shape[-1]
-        Rp = torch.nn.functional.pad(R, (0, self.D - d, 0, self.D - d))
-        return torch.index_select(Rp, 2, cols)
+        Rp = R.new_zeros(R.shape[0], self.D, self.D)
+        Rp[:, :d, cols] = R
+        return Rp
 
     def channels(self, C):
         return torch.nn.functional.pad(C, (0, _EMB_C - self.cin, 0, _EMB_C - self.cout))
