@@ -315,7 +315,7 @@ def secondary_workload(name: str, steps: int, warmup: int) -> dict:
 
         def step():
             y = layer(P, P, x, dist.to(torch.bfloat16))
-            SumOfSquares.apply(y.float()).backward()
+            SumOfSquares.apply(y).backward()      # the norm accumulates in fp32
         workload = ("c5: EquivariantEdgewiseLinear [0..6]x128 -> [0..6]x128, kNN k=32 on 5k nodes "
                     f"in 30^3, E={E}, bf16 edge features, fwd+bwd")
         work = algorithmic_per_edge(lv, lv, 128, 128)

@@ -84,32 +84,57 @@ __device__ __forceinline__ float ipowf_small(float s, int l) {
 // time, reading the basis entries as LDS broadcasts (every lane of a wave
 // serves the same edge).  Rows move between HBM and LDS with coalesced
 // 16-byte accesses.  Basis rows d are in the standard (l, m) order, columns j
-// in the m-first order (the WignerDBasis layout); when an edge's basis has a
-// non-zero entry off the degree blocks, the workgroup sums over all entries.
+// in the m-first order (the WignerDBasis layout).  Only the degree blocks of
+// each basis are staged (455 of 2401 entries at L = 6), so several
+// workgroups share a CU; when an edge's basis has a non-zero entry off the
+// blocks, the workgroup sums over all entries, read from global memory.
 
-// Stages the EPB bases of the workgroup in LDS with column j scaled by
-// s_e^{l(j)}; returns whether any has a non-zero entry off the degree blocks.
-// The degrees of rows and columns and the powers of s come from small LDS
-// tables.
+template <int L>
+struct Blocks {
+    static constexpr int boff(int l) {        // offset of degree l's block in the compact store
+        int o = 0;
+        for (int q = 0; q < l; ++q) o += (2 * q + 1) * (2 * q + 1);
+        return o;
+    }
+    static constexpr int NB = boff(L + 1);
+    // position t of m-first slot j among the slots of its degree
+    static constexpr std::array<int, (L + 1) * (L + 1)> make_tpos() {
+        std::array<int, (L + 1) * (L + 1)> v{};
+        for (int k = 0; k < (L + 1) * (L + 1); ++k) {
+            const int j = DegreeBlocks<L>::slots[k];
+            const int l = SlotL<L>::l[j];
+            v[j] = k - l * l;
+        }
+        return v;
+    }
+    static constexpr std::array<int, (L + 1) * (L + 1)> tpos = make_tpos();
+};
+
+// Stages the degree blocks of the workgroup's EPB bases in LDS, sB[el][boff(l)
+// + r (2l + 1) + t] = R[e, l^2 + r, slots(l)[t]] s_e^l, and the powers s_e^l in
+// pw; returns whether any basis has a non-zero entry off the blocks.
 template <int L, typename T, int EPB>
 __device__ __forceinline__ bool stage_bases(int64_t E, int64_t e0, const T* __restrict__ R,
-                                            const float* __restrict__ dist, float sigma, float* sR) {
+                                            const float* __restrict__ dist, float sigma, float* sB,
+                                            float (*pw)[L + 1]) {
     using H = HL<L>;
+    using BL = Blocks<L>;
     constexpr int D = H::D;
-    __shared__ int s_lj[D], s_ld[D];
-    __shared__ float s_pw[EPB][L + 1];
+    __shared__ int s_lj[D], s_ld[D], s_tp[D], s_bo[L + 1];
     const int tid = threadIdx.x;
     if (tid < D) {
         s_lj[tid] = SlotL<L>::l[tid];
         s_ld[tid] = H::deg(tid);
+        s_tp[tid] = BL::tpos[tid];
     }
+    if (tid <= L) s_bo[tid] = BL::boff(tid);
     if (tid < EPB) {
         const int64_t e = e0 + tid;
         const float r = e < E ? dist[e] : 0.0f;
         const float sv = r / (r + sigma);
         float p = 1.0f;
         for (int l = 0; l <= L; ++l) {
-            s_pw[tid][l] = e < E ? p : 0.0f;
+            pw[tid][l] = e < E ? p : 0.0f;
             p *= sv;
         }
     }
@@ -120,9 +145,12 @@ __device__ __forceinline__ bool stage_bases(int64_t E, int64_t e0, const T* __re
     for (int q = tid; q < EPB * D * D; q += kT) {
         const int el = q / (D * D), dj = q - el * (D * D), d = dj / D, j = dj - d * D;
         const float v = el < nvalid ? static_cast<float>(Rb[q]) : 0.0f;
-        const int lj = s_lj[j];
-        off |= (v != 0.0f) & (s_ld[d] != lj);
-        sR[q] = v * s_pw[el][lj];
+        const int lj = s_lj[j], ld = s_ld[d];
+        if (ld != lj) {
+            off |= v != 0.0f;
+        } else {
+            sB[el * BL::NB + s_bo[lj] + (d - lj * lj) * (2 * lj + 1) + s_tp[j]] = v * pw[el][lj];
+        }
     }
     return __syncthreads_or(off) != 0;
 }
@@ -133,37 +161,42 @@ __global__ void __launch_bounds__(kT)
 k_hl_rot_in(int64_t E, const T* __restrict__ in, const T* __restrict__ R,
             const float* __restrict__ dist, float sigma, __bf16* __restrict__ out) {
     using H = HL<L>;
+    using BL = Blocks<L>;
     constexpr int D = H::D, EPB = kT / C, ROW = C * D;
     static_assert(kT % C == 0 && (ROW * sizeof(T)) % 16 == 0, "rows of whole 16-byte units");
     constexpr int VE = 16 / sizeof(T);                 // elements per 16-byte unit
     __shared__ uint4 sx4[EPB * ROW / VE];              // the rows, [el][c][d]
-    __shared__ float sR[EPB * D * D];
+    __shared__ float sB[EPB * BL::NB];
+    __shared__ float pw[EPB][L + 1];
     const T* sx = reinterpret_cast<const T*>(sx4);
     const int tid = threadIdx.x, el = tid / C, c = tid % C;
     const int64_t e0 = static_cast<int64_t>(blockIdx.x) * EPB;
     const int ne = static_cast<int>(E - e0 < EPB ? E - e0 : EPB);
     for (int q = tid; q < ne * ROW / VE; q += kT) sx4[q] = reinterpret_cast<const uint4*>(in + e0 * ROW)[q];
-    const bool dense = stage_bases<L, T, EPB>(E, e0, R, dist, sigma, sR);
+    const bool dense = stage_bases<L, T, EPB>(E, e0, R, dist, sigma, sB, pw);
     if (el >= ne) return;
     float xr[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) xr[d] = static_cast<float>(sx[el * ROW + c * D + d]);
-    const float* Rl = sR + el * D * D;
     __bf16* oe = out + (e0 + el) * ROW + c;
     if (!dense) {
+        const float* Bl = sB + el * BL::NB;
         static_for<D>([&](auto JJ) __attribute__((always_inline)) {
-            constexpr int j = decltype(JJ)::value, l = SlotL<L>::l[j];
+            constexpr int j = decltype(JJ)::value, l = SlotL<L>::l[j], n = 2 * l + 1;
+            constexpr int t = BL::tpos[j], bo = BL::boff(l);
             float acc = 0.0f;
 #pragma unroll
-            for (int d = l * l; d < (l + 1) * (l + 1); ++d) acc += xr[d] * Rl[d * D + j];
+            for (int r = 0; r < n; ++r) acc += xr[l * l + r] * Bl[bo + r * n + t];
             oe[j * C] = static_cast<__bf16>(acc);
         });
     } else {
+        const T* Re = R + (e0 + el) * D * D;
         for (int j = 0; j < D; ++j) {
+            const float sc = pw[el][SlotL<L>::l[j]];
             float acc = 0.0f;
 #pragma unroll
-            for (int d = 0; d < D; ++d) acc += xr[d] * Rl[d * D + j];
-            oe[j * C] = static_cast<__bf16>(acc);
+            for (int d = 0; d < D; ++d) acc += xr[d] * static_cast<float>(Re[d * D + j]);
+            oe[j * C] = static_cast<__bf16>(acc * sc);
         }
     }
 }
@@ -174,11 +207,13 @@ __global__ void __launch_bounds__(kT)
 k_hl_rot_out(int64_t E, const float* __restrict__ in, const T* __restrict__ R,
              const float* __restrict__ dist, float sigma, T* __restrict__ out) {
     using H = HL<L>;
+    using BL = Blocks<L>;
     constexpr int D = H::D, EPB = kT / C, ROW = C * D;
     static_assert(kT % C == 0 && (ROW * sizeof(T)) % 16 == 0, "rows of whole 16-byte units");
     constexpr int VE = 16 / sizeof(T);
     __shared__ T so[EPB * ROW];                        // the output rows, [el][c][d]
-    __shared__ float sR[EPB * D * D];
+    __shared__ float sB[EPB * BL::NB];
+    __shared__ float pw[EPB][L + 1];
     const int tid = threadIdx.x, el = tid / C, c = tid % C;
     const int64_t e0 = static_cast<int64_t>(blockIdx.x) * EPB;
     const int ne = static_cast<int>(E - e0 < EPB ? E - e0 : EPB);
@@ -186,25 +221,28 @@ k_hl_rot_out(int64_t E, const float* __restrict__ in, const T* __restrict__ R,
     const int64_t ec = e0 + (el < ne ? el : 0);
 #pragma unroll
     for (int j = 0; j < D; ++j) v[j] = in[(ec * D + j) * C + c];     // coalesced over c
-    const bool dense = stage_bases<L, T, EPB>(E, e0, R, dist, sigma, sR);
-    const float* Rl = sR + el * D * D;
+    const bool dense = stage_bases<L, T, EPB>(E, e0, R, dist, sigma, sB, pw);
     T* ol = so + el * ROW + c * D;
     if (!dense) {
+        const float* Bl = sB + el * BL::NB;
         static_for<D>([&](auto DD) __attribute__((always_inline)) {
-            constexpr int d = decltype(DD)::value, l = H::deg(d);
+            constexpr int d = decltype(DD)::value, l = H::deg(d), n = 2 * l + 1, r = d - l * l;
+            constexpr int bo = BL::boff(l);
             float acc = 0.0f;
-#pragma unroll
-            for (int t = l * l; t < (l + 1) * (l + 1); ++t) {
-                const int j = DegreeBlocks<L>::slots[t];
-                acc += Rl[d * D + j] * v[j];
-            }
+            static_for<n>([&](auto TT) __attribute__((always_inline)) {
+                constexpr int t = decltype(TT)::value;
+                constexpr int j = DegreeBlocks<L>::slots[l * l + t];
+                acc += Bl[bo + r * n + t] * v[j];
+            });
             ol[d] = static_cast<T>(acc);
         });
     } else {
+        const T* Re = R + ec * D * D;
         for (int d = 0; d < D; ++d) {
             float acc = 0.0f;
 #pragma unroll
-            for (int j = 0; j < D; ++j) acc += Rl[d * D + j] * v[j];
+            for (int j = 0; j < D; ++j)
+                acc += static_cast<float>(Re[d * D + j]) * pw[el][SlotL<L>::l[j]] * v[j];
             ol[d] = static_cast<T>(acc);
         }
     }
@@ -658,15 +696,16 @@ int hl_prep(const float* C, int K, int cout, int cin, bf8* frag, hipStream_t s) 
 
 template <int L, int CH>
 int hl_fwd(const feq_binning& B, int64_t E, const __bf16* x, const __bf16* P, const __bf16* Q,
-           const float* dist, const float* C, const float* F, __bf16* y, void* ws, size_t ws_bytes,
-           hipStream_t s) {
+           const float* dist, const float* C, const float* F, __bf16* y, __bf16* fs_out, void* ws,
+           size_t ws_bytes, hipStream_t s) {
     HLWs w;
     if (ws_bytes < hl_layout<L>(B, CH, E, false, &w, ws)) return fail(FEQ_ERR_WORKSPACE, "high-degree workspace too small");
+    __bf16* fs = fs_out ? fs_out : w.fsT;
     if (int rc = hl_prep<false>(C, kRank, CH, CH, w.cfrag, s)) return rc;
-    if (int rc = hl_rot_in<L, CH>(E, x, P, dist, B.sh_scale, w.fsT, s)) return rc;
+    if (int rc = hl_rot_in<L, CH>(E, x, P, dist, B.sh_scale, fs, s)) return rc;
     const int64_t ntiles = ceil_div(E, kNE);
     auto mix = k_hl_mix<L, CH, CH, kRank, false>;
-    FEQ_LAUNCH("k_hl_mix", mix, dim3(grid_tiles(ntiles)), dim3(4 * CH), 0, s, B, E, ntiles, w.fsT,
+    FEQ_LAUNCH("k_hl_mix", mix, dim3(grid_tiles(ntiles)), dim3(4 * CH), 0, s, B, E, ntiles, fs,
                dist, F, w.cfrag, w.stage);
     return hl_rot_out<L, CH>(E, w.stage, Q, dist, B.sh_scale, y, s);
 }
@@ -712,7 +751,8 @@ int hl_dc(int64_t rows, const __bf16* U, const __bf16* fsT, float* dCp, float* g
 template <int L, int CH>
 int hl_bwd(const feq_layout& Lay, const feq_binning& B, int64_t E, const __bf16* gy, const __bf16* x,
            const __bf16* P, const __bf16* Q, const float* dist, const float* C, const float* F,
-           __bf16* gx, float* gC, float* gF, float* gdist, void* ws, size_t ws_bytes, hipStream_t s) {
+           __bf16* gx, float* gC, float* gF, float* gdist, const __bf16* fs_in, void* ws,
+           size_t ws_bytes, hipStream_t s) {
     using H = HL<L>;
     HLWs w;
     if (ws_bytes < hl_layout<L>(B, CH, E, true, &w, ws)) return fail(FEQ_ERR_WORKSPACE, "high-degree workspace too small");
@@ -720,11 +760,15 @@ int hl_bwd(const feq_layout& Lay, const feq_binning& B, int64_t E, const __bf16*
     const int G = grid_tiles(ntiles);
     // gd = s^l_out (gy Q), fs = s^l_in (x P)
     if (int rc = hl_rot_in<L, CH>(E, gy, Q, dist, B.sh_scale, w.gdT, s)) return rc;
-    if (int rc = hl_rot_in<L, CH>(E, x, P, dist, B.sh_scale, w.fsT, s)) return rc;
+    const __bf16* fs = fs_in;
+    if (!fs) {
+        if (int rc = hl_rot_in<L, CH>(E, x, P, dist, B.sh_scale, w.fsT, s)) return rc;
+        fs = w.fsT;
+    }
     // dF_e from <gd, C_k fs>
     if (int rc = hl_prep<false>(C, kRank, CH, CH, w.cfrag, s)) return rc;
     auto kd = k_hl_dfe<L, CH, CH, kRank>;
-    FEQ_LAUNCH("k_hl_dfe", kd, dim3(G), dim3(kT), 0, s, E, ntiles, w.fsT, w.gdT, w.cfrag, w.dFe);
+    FEQ_LAUNCH("k_hl_dfe", kd, dim3(G), dim3(kT), 0, s, E, ntiles, fs, w.gdT, w.cfrag, w.dFe);
     // dfs = sum_k M_ek^T C_k^T gd, dx = (s^l_in dfs) P^T
     if (gx) {
         if (int rc = hl_prep<true>(C, kRank, CH, CH, w.cfrag, s)) return rc;
@@ -737,7 +781,7 @@ int hl_bwd(const feq_layout& Lay, const feq_binning& B, int64_t E, const __bf16*
     auto ku = k_hl_u<L, kRank>;
     FEQ_LAUNCH("k_hl_u", ku, dim3(E), dim3(kT), 0, s, B, CH, w.gdT, dist, F, w.U);
     float* tmp = w.tail + align_up(static_cast<size_t>(256) * (B.num_bins + 1) * kRank * H::WD, 64);
-    if (int rc = hl_dc<CH>(E * H::D, w.U, w.fsT, w.dCp, gC, tmp, w.blas, s)) return rc;
+    if (int rc = hl_dc<CH>(E * H::D, w.U, fs, w.dCp, gC, tmp, w.blas, s)) return rc;
     // binned radial-function gradient and distance gradient (no dC partials left)
     return ew_tail(Lay, B, kRank, E, dist, F, w.dFe, nullptr, 0, 0, nullptr, gF, gdist, w.tail, s);
 }
@@ -771,7 +815,7 @@ bool hl_supported(const feq_layout& L, const feq_binning& B, int rank) {
     return false;
 }
 
-bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }  // NULL passes
 
 }  // namespace
 }  // namespace feq
@@ -796,21 +840,23 @@ extern "C" size_t feq_edgewise_hl_workspace(const feq_layout* L, const feq_binni
 extern "C" int feq_edgewise_hl_fwd(const feq_layout* L, const feq_binning* b, int32_t rank,
                                    int64_t E, const void* x, const void* P, const void* Q,
                                    const float* dist, const float* C, const float* F, void* y,
-                                   void* ws, size_t ws_bytes, feq_stream_t stream) {
+                                   void* fs_out, void* ws, size_t ws_bytes, feq_stream_t stream) {
     if (!L || !b) return fail(FEQ_ERR_INVALID, "NULL layout or binning");
     if (!hl_supported(*L, *b, rank)) return fail(FEQ_ERR_UNSUPPORTED, "no high-degree kernels for this layout");
     if (E < 0) return fail(FEQ_ERR_INVALID, "negative edge count");
     if (E == 0) return FEQ_OK;
     if (E > 0x7fffffffLL) return fail(FEQ_ERR_UNSUPPORTED, "more than 2^31-1 edges");
     if (!x || !P || !Q || !dist || !C || !F || !y || !ws) return fail(FEQ_ERR_INVALID, "NULL pointer");
-    if (!al16(x) || !al16(ws)) return fail(FEQ_ERR_INVALID, "x and the workspace must be 16-byte aligned");
+    if (!al16(x) || !al16(ws) || !al16(fs_out))
+        return fail(FEQ_ERR_INVALID, "x, fs_out and the workspace must be 16-byte aligned");
     hipStream_t s = stream_of(stream);
     const auto* xb = static_cast<const __bf16*>(x);
     const auto* Pb = static_cast<const __bf16*>(P);
     const auto* Qb = static_cast<const __bf16*>(Q);
 #define FEQ_FWD(l, ch) \
     if (L->cin == ch && canonical_pair(*L, l)) \
-        return hl_fwd<l, ch>(*b, E, xb, Pb, Qb, dist, C, F, static_cast<__bf16*>(y), ws, ws_bytes, s);
+        return hl_fwd<l, ch>(*b, E, xb, Pb, Qb, dist, C, F, static_cast<__bf16*>(y), \
+                             static_cast<__bf16*>(fs_out), ws, ws_bytes, s);
     FEQ_HL_SHAPES(FEQ_FWD)
 #undef FEQ_FWD
     return fail(FEQ_ERR_UNSUPPORTED, "no high-degree kernels for this layout");
@@ -819,8 +865,9 @@ extern "C" int feq_edgewise_hl_fwd(const feq_layout* L, const feq_binning* b, in
 extern "C" int feq_edgewise_hl_bwd(const feq_layout* L, const feq_binning* b, int32_t rank,
                                    int64_t E, const void* gy, const void* x, const void* P,
                                    const void* Q, const float* dist, const float* C, const float* F,
-                                   void* gx, float* gC, float* gF, float* gdist, void* ws,
-                                   size_t ws_bytes, feq_stream_t stream) {
+                                   void* gx, float* gC, float* gF, float* gdist,
+                                   const void* fs_in, void* ws, size_t ws_bytes,
+                                   feq_stream_t stream) {
     if (!L || !b) return fail(FEQ_ERR_INVALID, "NULL layout or binning");
     if (!hl_supported(*L, *b, rank)) return fail(FEQ_ERR_UNSUPPORTED, "no high-degree kernels for this layout");
     if (E < 0) return fail(FEQ_ERR_INVALID, "negative edge count");
@@ -832,14 +879,16 @@ extern "C" int feq_edgewise_hl_bwd(const feq_layout* L, const feq_binning* b, in
         return fill_zero(gC, static_cast<int64_t>(rank) * L->cout * L->cin, s);
     }
     if (!gy || !x || !P || !Q || !dist || !C || !F || !ws) return fail(FEQ_ERR_INVALID, "NULL pointer");
-    if (!al16(gy) || !al16(x) || !al16(ws)) return fail(FEQ_ERR_INVALID, "gy, x and the workspace must be 16-byte aligned");
+    if (!al16(gy) || !al16(x) || !al16(ws) || !al16(fs_in))
+        return fail(FEQ_ERR_INVALID, "gy, x, fs_in and the workspace must be 16-byte aligned");
     const auto* gyb = static_cast<const __bf16*>(gy);
     const auto* xb = static_cast<const __bf16*>(x);
     const auto* Pb = static_cast<const __bf16*>(P);
     const auto* Qb = static_cast<const __bf16*>(Q);
 #define FEQ_BWD(l, ch) \
     if (L->cin == ch && canonical_pair(*L, l)) \
-        return hl_bwd<l, ch>(*L, *b, E, gyb, xb, Pb, Qb, dist, C, F, static_cast<__bf16*>(gx), gC, gF, gdist, ws, ws_bytes, s);
+        return hl_bwd<l, ch>(*L, *b, E, gyb, xb, Pb, Qb, dist, C, F, static_cast<__bf16*>(gx), gC, gF, \
+                             gdist, static_cast<const __bf16*>(fs_in), ws, ws_bytes, s);
     FEQ_HL_SHAPES(FEQ_BWD)
 #undef FEQ_BWD
     return fail(FEQ_ERR_UNSUPPORTED, "no high-degree kernels for this layout");

@@ -72,10 +72,10 @@ _SIGS = {
                               _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
     "feq_edgewise_hl_supported": ([_P, _P, _I32], ctypes.c_int),
     "feq_edgewise_hl_workspace": ([_P, _P, _I32, _I64, _I32], _SZ),
-    "feq_edgewise_hl_fwd": ([_P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+    "feq_edgewise_hl_fwd": ([_P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
                             ctypes.c_int),
     "feq_edgewise_hl_bwd": ([_P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                             _SZ, _P], ctypes.c_int),
+                             _P, _SZ, _P], ctypes.c_int),
     "feq_wigner_plan_doubles": ([_P, _I32], _SZ),
     "feq_wigner_basis": ([_P, _I32, _P, _P, _I64, _P, _P, _P], ctypes.c_int),
     "feq_csr_workspace": ([_I64, _I64], _SZ),

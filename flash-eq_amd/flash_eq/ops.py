@@ -318,6 +318,8 @@ class EdgewiseLinearHLFn(torch.autograd.Function):
         rs, Cs, Fs = _f32(dist, "distances"), _f32(C, "channel_patterns"), _f32(F, "radial")
         _check_edgewise_shapes(layout, binning, rank, xs, Ps, Qs, rs, Cs, Fs)
         y = torch.empty(E, layout.cout, layout.dout, dtype=torch.bfloat16, device=dev)
+        # the rotated input s^l (x P), kept for the backward (one bf16 copy of x)
+        fs = torch.empty(E, layout.din, layout.cin, dtype=torch.bfloat16, device=dev)
         if E:
             lib = N.lib()
             ws = N.workspace(lib.feq_edgewise_hl_workspace(N.ctypes.byref(layout),
@@ -325,16 +327,16 @@ class EdgewiseLinearHLFn(torch.autograd.Function):
             with torch.cuda.device(dev):
                 rc = lib.feq_edgewise_hl_fwd(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
                                              N.ptr(xs), N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs),
-                                             N.ptr(Fs), N.ptr(y), N.ptr(ws), ws.numel(),
+                                             N.ptr(Fs), N.ptr(y), N.ptr(fs), N.ptr(ws), ws.numel(),
                                              N.stream_ptr(dev))
             N.check(rc, "feq_edgewise_hl_fwd")
-        ctx.save_for_backward(xs, Ps, Qs, rs, Cs, Fs)
+        ctx.save_for_backward(xs, Ps, Qs, rs, Cs, Fs, fs)
         ctx.meta = (layout, binning, rank, dist.dtype, C.dtype, F.dtype)
         return y
 
     @staticmethod
     def backward(ctx, gy):
-        xs, Ps, Qs, rs, Cs, Fs = ctx.saved_tensors
+        xs, Ps, Qs, rs, Cs, Fs, fs = ctx.saved_tensors
         layout, binning, rank, rdt, cdt, fdt = ctx.meta
         dev = xs.device
         E = xs.shape[0]
@@ -351,7 +353,8 @@ class EdgewiseLinearHLFn(torch.autograd.Function):
             rc = lib.feq_edgewise_hl_bwd(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
                                          N.ptr(g), N.ptr(xs), N.ptr(Ps), N.ptr(Qs), N.ptr(rs),
                                          N.ptr(Cs), N.ptr(Fs), N.ptr(gx), N.ptr(gC), N.ptr(gF),
-                                         N.ptr(gr), N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+                                         N.ptr(gr), N.ptr(fs) if E else None, N.ptr(ws), ws.numel(),
+                                         N.stream_ptr(dev))
         N.check(rc, "feq_edgewise_hl_bwd")
         return (gx, None, None, None if gr is None else gr.to(rdt),
                 gC.to(cdt) if need[4] else None, gF.to(fdt) if need[5] else None,

@@ -193,13 +193,17 @@ size_t feq_edgewise_hl_workspace(const feq_layout* layout, const feq_binning* bi
                                  int64_t num_edges, int32_t backward);
 int feq_edgewise_hl_fwd(const feq_layout* layout, const feq_binning* binning, int32_t rank,
                         int64_t num_edges, const void* x, const void* P, const void* Q,
-                        const float* dist, const float* C, const float* F, void* y, void* workspace,
-                        size_t workspace_bytes, feq_stream_t stream);
+                        const float* dist, const float* C, const float* F, void* y, void* fs_out,
+                        void* workspace, size_t workspace_bytes, feq_stream_t stream);
+/* fs_out (nullable, bf16 (E, Din, Cin)): receives the rotated, s^l-scaled input
+ * s^l (x P) in slot-major order; passing it to feq_edgewise_hl_bwd as fs_in
+ * (nullable) spares the backward that rotation. */
 int feq_edgewise_hl_bwd(const feq_layout* layout, const feq_binning* binning, int32_t rank,
                         int64_t num_edges, const void* grad_y, const void* x, const void* P,
                         const void* Q, const float* dist, const float* C, const float* F,
                         void* grad_x, float* grad_C, float* grad_F, float* grad_dist,
-                        void* workspace, size_t workspace_bytes, feq_stream_t stream);
+                        const void* fs_in, void* workspace, size_t workspace_bytes,
+                        feq_stream_t stream);
 
 /* Attention over head-major rows: a row of Q, K or V holds heads*head_dim floats,
  * head h at offset h*head_dim; row r of a table T starts at T + r*ld (floats).

@@ -86,3 +86,27 @@ def test_high_degree_edges_past_a_tile_and_empty(dev):
     y0.float().sum().backward()
     for p in layer.radial_weights.parameters():
         assert p.grad is None or torch.all(p.grad == 0)
+
+
+def test_high_degree_dense_bases(dev):
+    """Bases with entries off the degree blocks (any P, Q is accepted): the
+    rotations then sum over every entry, read from global memory."""
+    torch.manual_seed(9)
+    rp = fe.Repr(L6, 64)
+    layer = fe.EquivariantEdgewiseLinear(rp, rp, num_bins=100).to(dev)
+    g = torch.Generator().manual_seed(90)
+    E = 37
+    x = torch.randn(E, 64, 49, generator=g).bfloat16()
+    P = (torch.randn(E, 49, 49, generator=g) / 7).bfloat16()
+    Q = (torch.randn(E, 49, 49, generator=g) / 7).bfloat16()
+    r = torch.rand(E, generator=g) * 9 + 0.1
+    xg = x.to(dev).requires_grad_(True)
+    y = layer(P.to(dev), Q.to(dev), xg, r.to(dev))
+    gy = torch.randn(y.shape, generator=g)
+    y.backward(gy.to(dev).bfloat16())
+    params, cfg = OL.module_cfg(layer)
+    xd = x.double().requires_grad_(True)
+    yref = OL.edgewise_linear(xd, P.double(), Q.double(), r.double(), params, cfg)
+    yref.backward(gy.bfloat16().double())
+    assert rel_err(y, yref) < BF16_TOL
+    assert rel_err(xg.grad, xd.grad) < BF16_TOL
