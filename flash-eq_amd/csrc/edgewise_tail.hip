@@ -164,6 +164,7 @@ __global__ void k_sum_partials(const float* __restrict__ part, int groups, int p
     const int g0 = blockIdx.y * per_slice;
     const int g1 = g0 + per_slice < groups ? g0 + per_slice : groups;
     float acc = 0.0f;
+#pragma unroll 8
     for (int g = g0; g < g1; ++g) acc += part[static_cast<int64_t>(g) * n + q];
     out[blockIdx.y * n + q] = acc;
 }

@@ -1,0 +1,780 @@
+// Node-side neighbours of the edge path: the separable equivariant layer norm,
+// the equivariant layer norm and the norm gating of the transformer block,
+// forward and backward, on node tables x (N, mult, dim) of float32.
+//
+// Norm kernels run one wave per node: lane l owns channels l, l + 64, ...;
+// statistics over channels are wave reductions (__shfl_xor, the same order on
+// every lane), so results do not depend on the grid.  Parameter gradients are
+// per-wave partials over a fixed grid, summed by reduce_partials in a fixed
+// order (deterministic, no atomics).  The gating's Linear stays a library GEMM;
+// its kernels run one thread per (node, channel) row.
+//
+// Formulas: SeparableEquivariantLayerNorm norm.py:177-246 (_ChannelLayerNorm
+// :89-93, _EquivariantRMSNorm :109-112), EquivariantLayerNorm norm.py:148-174,
+// RepNorm norm.py:19-55, EquivariantGating gating.py:54-76.
+#include "feq_internal.h"
+
+#include <algorithm>
+
+namespace feq {
+namespace {
+
+constexpr int kWaves = 4;                          // nodes per workgroup, one per wave
+constexpr int kMaxS = FEQ_NODE_MAX_SCALARS;
+constexpr int kBwdGroups = 512;                    // workgroups of the backward norm kernels
+constexpr int kStageRow = 1152;                    // node rows (mult * dim floats) staged in LDS
+constexpr int kRowThreads = 256;
+
+struct NodeL {
+    int mult, dim, nreps;
+    int ns;   // scalar (l = 0) irreps
+    int nhc;  // l > 0 components per channel
+    int off[FEQ_MAX_IRREPS + 1];
+    int deg[FEQ_MAX_IRREPS];
+    int spos[kMaxS];  // component offset of each scalar irrep, in order
+};
+
+int make_nodel(const int32_t* lvals, int32_t nreps, int32_t mult, NodeL* L) {
+    if (!lvals || nreps < 1 || nreps > FEQ_MAX_IRREPS)
+        return fail(FEQ_ERR_INVALID, "node layout: 1..%d irreps required", FEQ_MAX_IRREPS);
+    if (mult < 1 || mult > FEQ_NODE_MAX_MULT)
+        return fail(FEQ_ERR_UNSUPPORTED, "node kernels take 1..%d channels (got %d)",
+                    FEQ_NODE_MAX_MULT, mult);
+    *L = NodeL{};
+    L->mult = mult;
+    L->nreps = nreps;
+    int o = 0;
+    for (int k = 0; k < nreps; ++k) {
+        const int l = lvals[k];
+        if (l < 0 || l > 16) return fail(FEQ_ERR_INVALID, "node layout: degree %d out of range", l);
+        L->off[k] = o;
+        L->deg[k] = l;
+        if (l == 0) {
+            if (L->ns < kMaxS) L->spos[L->ns] = o;
+            ++L->ns;
+        } else {
+            L->nhc += 2 * l + 1;
+        }
+        o += 2 * l + 1;
+    }
+    L->off[nreps] = o;
+    L->dim = o;
+    return FEQ_OK;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// Orders a wave's LDS writes before its other lanes' reads.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Coalesced copy of one node row by a wave.
+__device__ __forceinline__ void row_copy(float* __restrict__ d, const float* __restrict__ s, int64_t n,
+                                         int lane) {
+    for (int64_t i = lane; i < n; i += 64) d[i] = s[i];
+}
+
+__device__ __forceinline__ float sigmoidf(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+// ---- separable layer norm ---------------------------------------------------
+// scalars: (v - mu) / (sd + eps) * w_s[c, j] + b_s[c, j], mu and sd (biased)
+// over the channels; l > 0 components: v * w_h[c] / sqrt(mean(v^2) + eps), the
+// mean over every channel and l > 0 component of the node.
+
+// STAGE: the node row moves through LDS (coalesced), computed in place.
+template <int CPL, bool STAGE>
+__global__ void __launch_bounds__(64 * kWaves)
+k_sepnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __restrict__ ws,
+              const float* __restrict__ bs, const float* __restrict__ wh, float eps,
+              float* __restrict__ y) {
+    __shared__ float lds[STAGE ? kWaves * kStageRow : 1];
+    const int lane = threadIdx.x & 63;
+    const int64_t n = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    if (n >= N) return;
+    const int64_t row = static_cast<int64_t>(L.mult) * L.dim;
+    float* sx = lds + (threadIdx.x >> 6) * kStageRow;
+    if (STAGE) {
+        row_copy(sx, x + n * row, row, lane);
+        wave_sync();
+    }
+    const float* xn = STAGE ? sx : x + n * row;
+    float* yn = STAGE ? sx : y + n * row;
+    const float fm = static_cast<float>(L.mult);
+#pragma unroll
+    for (int j = 0; j < kMaxS; ++j) {
+        if (j >= L.ns) break;
+        const int d = L.spos[j];
+        float v[CPL];
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = lane + 64 * i;
+            v[i] = c < L.mult ? xn[c * L.dim + d] : 0.0f;
+            s += v[i];
+        }
+        const float mu = wave_sum(s) / fm;
+        float q = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i)
+            if (lane + 64 * i < L.mult) q += (v[i] - mu) * (v[i] - mu);
+        const float den = sqrtf(wave_sum(q) / fm) + eps;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = lane + 64 * i;
+            if (c < L.mult) yn[c * L.dim + d] = (v[i] - mu) / den * ws[c * L.ns + j] + bs[c * L.ns + j];
+        }
+    }
+    if (L.nhc > 0) {  // w_h is NULL without l > 0 irreps
+        float h = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = lane + 64 * i;
+            if (c >= L.mult) continue;
+            for (int k = 0; k < L.nreps; ++k) {
+                if (L.deg[k] == 0) continue;
+                for (int d = L.off[k]; d < L.off[k + 1]; ++d) {
+                    const float v = xn[c * L.dim + d];
+                    h += v * v;
+                }
+            }
+        }
+        const float rms = sqrtf(wave_sum(h) / (fm * L.nhc) + eps);
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = lane + 64 * i;
+            if (c >= L.mult) continue;
+            const float f = wh[c] / rms;
+            for (int k = 0; k < L.nreps; ++k) {
+                if (L.deg[k] == 0) continue;
+                for (int d = L.off[k]; d < L.off[k + 1]; ++d) yn[c * L.dim + d] = xn[c * L.dim + d] * f;
+            }
+        }
+    }
+    if (STAGE) {
+        wave_sync();
+        row_copy(y + n * row, sx, row, lane);
+    }
+}
+
+// Backward.  Scalars, with gp = gy w_s and den = sd + eps:
+//   gx = (gp - mean(gp)) / den - sum(gp (v - mu)) (v - mu) / (mult sd den^2);
+// l > 0, with S = sum over the node of gy v w_h[c]:
+//   gx = gy w_h[c] / rms - S v / (count rms^3).
+// Per-wave partials: pS, pB (mult, ns) of gy (v - mu) / den and gy; pH (mult) of
+// sum_d gy v / rms.
+template <int CPL, bool STAGE>
+__global__ void __launch_bounds__(64 * kWaves)
+k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __restrict__ x,
+              const float* __restrict__ ws, const float* __restrict__ wh, float eps,
+              float* __restrict__ gx, float* __restrict__ pS, float* __restrict__ pB,
+              float* __restrict__ pH) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * kWaves;
+    const int64_t row = static_cast<int64_t>(L.mult) * L.dim;
+    const float fm = static_cast<float>(L.mult);
+    const float cnt = fm * L.nhc;
+    float aS[CPL][kMaxS], aB[CPL][kMaxS], aH[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        aH[i] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kMaxS; ++j) aS[i][j] = aB[i][j] = 0.0f;
+    }
+    __shared__ float lds[STAGE ? 2 * kWaves * kStageRow : 1];
+    float* sx = lds + (threadIdx.x >> 6) * 2 * kStageRow;
+    float* sg = sx + kStageRow;
+    for (int64_t n = wave; n < N; n += nw) {
+        if (STAGE) {
+            wave_sync();  // the previous node's stores have read sg
+            row_copy(sx, x + n * row, row, lane);
+            row_copy(sg, gy + n * row, row, lane);
+            wave_sync();
+        }
+        const float* xn = STAGE ? sx : x + n * row;
+        const float* gn = STAGE ? sg : gy + n * row;
+        float* on = STAGE ? sg : gx + n * row;
+#pragma unroll
+        for (int j = 0; j < kMaxS; ++j) {
+            if (j >= L.ns) break;
+            const int d = L.spos[j];
+            float v[CPL], gp[CPL], g[CPL];
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                const int c = lane + 64 * i;
+                const bool ok = c < L.mult;
+                v[i] = ok ? xn[c * L.dim + d] : 0.0f;
+                g[i] = ok ? gn[c * L.dim + d] : 0.0f;
+                gp[i] = ok ? g[i] * ws[c * L.ns + j] : 0.0f;
+                s += v[i];
+            }
+            const float mu = wave_sum(s) / fm;
+            float q = 0.0f, sg = 0.0f, sgv = 0.0f;
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                if (lane + 64 * i >= L.mult) continue;
+                const float t = v[i] - mu;
+                q += t * t;
+                sg += gp[i];
+                sgv += gp[i] * t;
+            }
+            const float sd = sqrtf(wave_sum(q) / fm);
+            const float mg = wave_sum(sg) / fm;
+            sgv = wave_sum(sgv);
+            const float den = sd + eps;
+            const float coef = sd > 0.0f ? sgv / (fm * sd * den * den) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                const int c = lane + 64 * i;
+                if (c >= L.mult) continue;
+                const float t = v[i] - mu;
+                on[c * L.dim + d] = (gp[i] - mg) / den - coef * t;
+                aS[i][j] += g[i] * (t / den);
+                aB[i][j] += g[i];
+            }
+        }
+        if (L.nhc > 0) {  // w_h is NULL without l > 0 irreps
+            float h = 0.0f, S = 0.0f;
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                const int c = lane + 64 * i;
+                if (c >= L.mult) continue;
+                float t = 0.0f;
+                for (int k = 0; k < L.nreps; ++k) {
+                    if (L.deg[k] == 0) continue;
+                    for (int d = L.off[k]; d < L.off[k + 1]; ++d) {
+                        const float v = xn[c * L.dim + d];
+                        h += v * v;
+                        t += gn[c * L.dim + d] * v;
+                    }
+                }
+                S += t * wh[c];
+            }
+            const float rms = sqrtf(wave_sum(h) / cnt + eps);
+            const float k2 = wave_sum(S) / (cnt * rms * rms * rms);
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                const int c = lane + 64 * i;
+                if (c >= L.mult) continue;
+                const float a = wh[c] / rms;
+                float t = 0.0f;
+                for (int k = 0; k < L.nreps; ++k) {
+                    if (L.deg[k] == 0) continue;
+                    for (int d = L.off[k]; d < L.off[k + 1]; ++d) {
+                        const float v = xn[c * L.dim + d];
+                        const float g = gn[c * L.dim + d];
+                        on[c * L.dim + d] = g * a - k2 * v;
+                        t += g * v;
+                    }
+                }
+                aH[i] += t / rms;
+            }
+        }
+        if (STAGE) {
+            wave_sync();
+            row_copy(gx + n * row, sg, row, lane);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const int c = lane + 64 * i;
+        if (c >= L.mult) continue;
+        if (pH) pH[wave * L.mult + c] = aH[i];
+#pragma unroll
+        for (int j = 0; j < kMaxS; ++j) {
+            if (j >= L.ns) break;
+            pS[(wave * L.mult + c) * L.ns + j] = aS[i][j];
+            pB[(wave * L.mult + c) * L.ns + j] = aB[i][j];
+        }
+    }
+}
+
+// ---- equivariant layer norm ---------------------------------------------------
+// Per irrep k: norm n_c = sqrt(sum_d x^2 + eps); with weights, a LayerNorm over
+// the channels ln_c = (n_c - mu) rstd w_c + b_c (rstd = 1 / sqrt(var + ln_eps));
+// y = x ln_c / (n_c + eps), or x / (n_c + eps) without weights (one channel).
+
+template <int CPL, bool STAGE>
+__global__ void __launch_bounds__(64 * kWaves)
+k_eqnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __restrict__ w,
+             const float* __restrict__ b, float eps, float ln_eps, float* __restrict__ y) {
+    __shared__ float lds[STAGE ? kWaves * kStageRow : 1];
+    const int lane = threadIdx.x & 63;
+    const int64_t n = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    if (n >= N) return;
+    const int64_t row = static_cast<int64_t>(L.mult) * L.dim;
+    float* sx = lds + (threadIdx.x >> 6) * kStageRow;
+    if (STAGE) {
+        row_copy(sx, x + n * row, row, lane);
+        wave_sync();
+    }
+    const float* xn = STAGE ? sx : x + n * row;
+    float* yn = STAGE ? sx : y + n * row;
+    const float fm = static_cast<float>(L.mult);
+    for (int k = 0; k < L.nreps; ++k) {
+        const int d0 = L.off[k], d1 = L.off[k + 1];
+        float nr[CPL];
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = lane + 64 * i;
+            float q = 0.0f;
+            if (c < L.mult)
+                for (int d = d0; d < d1; ++d) q += xn[c * L.dim + d] * xn[c * L.dim + d];
+            nr[i] = sqrtf(q + eps);
+            if (c < L.mult) s += nr[i];
+        }
+        float mu = 0.0f, rstd = 0.0f;
+        if (w) {
+            mu = wave_sum(s) / fm;
+            float q = 0.0f;
+#pragma unroll
+            for (int i = 0; i < CPL; ++i)
+                if (lane + 64 * i < L.mult) q += (nr[i] - mu) * (nr[i] - mu);
+            rstd = 1.0f / sqrtf(wave_sum(q) / fm + ln_eps);
+        }
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = lane + 64 * i;
+            if (c >= L.mult) continue;
+            const float f = w ? ((nr[i] - mu) * rstd * w[c] + b[c]) / (nr[i] + eps)
+                              : 1.0f / (nr[i] + eps);
+            for (int d = d0; d < d1; ++d) yn[c * L.dim + d] = xn[c * L.dim + d] * f;
+        }
+    }
+    if (STAGE) {
+        wave_sync();
+        row_copy(y + n * row, sx, row, lane);
+    }
+}
+
+// Backward per irrep: dfac = sum_d gy x; with weights dln = dfac / (n + eps),
+// dn = -dfac ln / (n + eps)^2 + rstd (dnh - mean(dnh) - nh mean(dnh nh)) with
+// dnh = dln w, nh = (n - mu) rstd; gx = gy fac + x dn / n.
+// Per-wave partials of sum dln nh (pW) and sum dln (pB), per channel.
+template <int CPL, bool STAGE>
+__global__ void __launch_bounds__(64 * kWaves)
+k_eqnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __restrict__ x,
+             const float* __restrict__ w, const float* __restrict__ b, float eps, float ln_eps,
+             float* __restrict__ gx, float* __restrict__ pW, float* __restrict__ pB) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * kWaves;
+    const int64_t row = static_cast<int64_t>(L.mult) * L.dim;
+    const float fm = static_cast<float>(L.mult);
+    float aW[CPL], aB[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) aW[i] = aB[i] = 0.0f;
+    __shared__ float lds[STAGE ? 2 * kWaves * kStageRow : 1];
+    float* sx = lds + (threadIdx.x >> 6) * 2 * kStageRow;
+    float* sg = sx + kStageRow;
+    for (int64_t n = wave; n < N; n += nw) {
+        if (STAGE) {
+            wave_sync();
+            row_copy(sx, x + n * row, row, lane);
+            row_copy(sg, gy + n * row, row, lane);
+            wave_sync();
+        }
+        const float* xn = STAGE ? sx : x + n * row;
+        const float* gn = STAGE ? sg : gy + n * row;
+        float* on = STAGE ? sg : gx + n * row;
+        for (int k = 0; k < L.nreps; ++k) {
+            const int d0 = L.off[k], d1 = L.off[k + 1];
+            float nr[CPL], df[CPL];
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                const int c = lane + 64 * i;
+                float q = 0.0f, t = 0.0f;
+                if (c < L.mult)
+                    for (int d = d0; d < d1; ++d) {
+                        const float v = xn[c * L.dim + d];
+                        q += v * v;
+                        t += gn[c * L.dim + d] * v;
+                    }
+                nr[i] = sqrtf(q + eps);
+                df[i] = t;
+                if (c < L.mult) s += nr[i];
+            }
+            float fac[CPL], dn[CPL];
+            if (w) {
+                const float mu = wave_sum(s) / fm;
+                float q = 0.0f;
+#pragma unroll
+                for (int i = 0; i < CPL; ++i)
+                    if (lane + 64 * i < L.mult) q += (nr[i] - mu) * (nr[i] - mu);
+                const float rstd = 1.0f / sqrtf(wave_sum(q) / fm + ln_eps);
+                float nh[CPL], dnh[CPL], dln[CPL];
+                float m1 = 0.0f, m2 = 0.0f;
+#pragma unroll
+                for (int i = 0; i < CPL; ++i) {
+                    const int c = lane + 64 * i;
+                    const bool ok = c < L.mult;
+                    const float den = nr[i] + eps;
+                    nh[i] = (nr[i] - mu) * rstd;
+                    const float ln = ok ? nh[i] * w[c] + b[c] : 0.0f;
+                    fac[i] = ln / den;
+                    dln[i] = df[i] / den;
+                    dnh[i] = ok ? dln[i] * w[c] : 0.0f;
+                    dn[i] = -df[i] * ln / (den * den);
+                    if (ok) {
+                        m1 += dnh[i];
+                        m2 += dnh[i] * nh[i];
+                    }
+                }
+                m1 = wave_sum(m1) / fm;
+                m2 = wave_sum(m2) / fm;
+#pragma unroll
+                for (int i = 0; i < CPL; ++i) {
+                    dn[i] += rstd * (dnh[i] - m1 - nh[i] * m2);
+                    if (lane + 64 * i < L.mult) {
+                        aW[i] += dln[i] * nh[i];
+                        aB[i] += dln[i];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < CPL; ++i) {
+                    const float den = nr[i] + eps;
+                    fac[i] = 1.0f / den;
+                    dn[i] = -df[i] / (den * den);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                const int c = lane + 64 * i;
+                if (c >= L.mult) continue;
+                const float r = dn[i] / nr[i];
+                for (int d = d0; d < d1; ++d)
+                    on[c * L.dim + d] = gn[c * L.dim + d] * fac[i] + xn[c * L.dim + d] * r;
+            }
+        }
+        if (STAGE) {
+            wave_sync();
+            row_copy(gx + n * row, sg, row, lane);
+        }
+    }
+    if (!pW) return;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const int c = lane + 64 * i;
+        if (c >= L.mult) continue;
+        pW[wave * L.mult + c] = aW[i];
+        pB[wave * L.mult + c] = aB[i];
+    }
+}
+
+// ---- gating ---------------------------------------------------------------------
+// A workgroup takes a tile of consecutive (node, channel) rows: the tile's
+// components move between HBM and LDS with coalesced loads and stores, and
+// thread t works on row t of the tile in LDS (odd row strides such as 9 floats
+// are free of bank conflicts).
+
+constexpr int kTileFloats = 2560;  // LDS floats per staged tensor (10 KB: 256 rows of up to 10 components)
+
+__device__ __forceinline__ int tile_rows(const NodeL& L) {
+    return min(kRowThreads, kTileFloats / L.dim);
+}
+
+__device__ __forceinline__ void tile_load(float* __restrict__ s, const float* __restrict__ g, int64_t n) {
+    for (int64_t i = threadIdx.x; i < n; i += kRowThreads) s[i] = g[i];
+}
+
+__device__ __forceinline__ void tile_store(float* __restrict__ g, const float* __restrict__ s, int64_t n) {
+    for (int64_t i = threadIdx.x; i < n; i += kRowThreads) g[i] = s[i];
+}
+
+__global__ void __launch_bounds__(kRowThreads)
+k_gate_norms(NodeL L, int64_t rows, const float* __restrict__ x, float eps, float* __restrict__ nrm) {
+    __shared__ float sx[kTileFloats];
+    const int R = tile_rows(L);
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * R;
+    const int nr = static_cast<int>(min<int64_t>(R, rows - r0));
+    tile_load(sx, x + r0 * L.dim, int64_t(nr) * L.dim);
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t >= nr) return;
+    for (int k = 0; k < L.nreps; ++k) {
+        float q = 0.0f;
+        for (int d = L.off[k]; d < L.off[k + 1]; ++d) q += sx[t * L.dim + d] * sx[t * L.dim + d];
+        nrm[(r0 + t) * L.nreps + k] = sqrtf(q + eps);
+    }
+}
+
+__global__ void __launch_bounds__(kRowThreads)
+k_gate_apply(NodeL L, int64_t rows, const float* __restrict__ x, const float* __restrict__ lin,
+             float* __restrict__ y) {
+    __shared__ float sx[kTileFloats];
+    const int R = tile_rows(L);
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * R;
+    const int nr = static_cast<int>(min<int64_t>(R, rows - r0));
+    const int64_t n = int64_t(nr) * L.dim;
+    tile_load(sx, x + r0 * L.dim, n);
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < nr)
+        for (int k = 0; k < L.nreps; ++k) {
+            const float g = sigmoidf(lin[(r0 + t) * L.nreps + k]);
+            for (int d = L.off[k]; d < L.off[k + 1]; ++d) sx[t * L.dim + d] *= g;
+        }
+    __syncthreads();
+    tile_store(y + r0 * L.dim, sx, n);
+}
+
+__global__ void __launch_bounds__(kRowThreads)
+k_gate_bwd_lin(NodeL L, int64_t rows, const float* __restrict__ gy, const float* __restrict__ x,
+               const float* __restrict__ lin, float* __restrict__ dlin) {
+    __shared__ float sx[kTileFloats];
+    __shared__ float sg[kTileFloats];
+    const int R = tile_rows(L);
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * R;
+    const int nr = static_cast<int>(min<int64_t>(R, rows - r0));
+    const int64_t n = int64_t(nr) * L.dim;
+    tile_load(sx, x + r0 * L.dim, n);
+    tile_load(sg, gy + r0 * L.dim, n);
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t >= nr) return;
+    for (int k = 0; k < L.nreps; ++k) {
+        float q = 0.0f;
+        for (int d = L.off[k]; d < L.off[k + 1]; ++d) q += sg[t * L.dim + d] * sx[t * L.dim + d];
+        const float g = sigmoidf(lin[(r0 + t) * L.nreps + k]);
+        dlin[(r0 + t) * L.nreps + k] = q * (g * (1.0f - g));
+    }
+}
+
+__global__ void __launch_bounds__(kRowThreads)
+k_gate_bwd_x(NodeL L, int64_t rows, const float* __restrict__ gy, const float* __restrict__ x,
+             const float* __restrict__ lin, const float* __restrict__ nrm,
+             const float* __restrict__ dnrm, float* __restrict__ gx) {
+    __shared__ float sx[kTileFloats];
+    __shared__ float sg[kTileFloats];
+    const int R = tile_rows(L);
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * R;
+    const int nr = static_cast<int>(min<int64_t>(R, rows - r0));
+    const int64_t n = int64_t(nr) * L.dim;
+    tile_load(sx, x + r0 * L.dim, n);
+    tile_load(sg, gy + r0 * L.dim, n);
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < nr)
+        for (int k = 0; k < L.nreps; ++k) {
+            const int64_t i = (r0 + t) * L.nreps + k;
+            const float g = sigmoidf(lin[i]);
+            const float q = dnrm[i] / nrm[i];
+            for (int d = L.off[k]; d < L.off[k + 1]; ++d)
+                sg[t * L.dim + d] = sg[t * L.dim + d] * g + sx[t * L.dim + d] * q;
+        }
+    __syncthreads();
+    tile_store(gx + r0 * L.dim, sg, n);
+}
+
+// ---- host ---------------------------------------------------------------------
+
+int cpl_of(int mult) { return mult <= 64 ? 1 : mult <= 128 ? 2 : 4; }
+
+int64_t bwd_waves(int64_t N) {
+    return std::min<int64_t>(ceil_div(N, kWaves), kBwdGroups) * kWaves;
+}
+
+// partials of n floats per wave, and reduce_partials' temporary
+size_t partial_floats(int64_t waves, int64_t n) {
+    return align_up(static_cast<size_t>(waves * n), 64) + align_up(static_cast<size_t>(ceil_div(waves, 32) * n), 64);
+}
+
+int check_rows(int64_t N, const void* a, const void* b, const void* c) {
+    if (N < 0) return fail(FEQ_ERR_INVALID, "negative node count");
+    if (N > 0 && (!a || !b || !c)) return fail(FEQ_ERR_INVALID, "NULL tensor pointer");
+    return FEQ_OK;
+}
+
+}  // namespace
+}  // namespace feq
+
+using namespace feq;
+
+#define FEQ_NODE_DISPATCH_S(CPL_, ...)                         \
+    switch (CPL_) {                                            \
+        case 1: { constexpr int cpl = 1; __VA_ARGS__; } break; \
+        case 2: { constexpr int cpl = 2; __VA_ARGS__; } break; \
+        default: { constexpr int cpl = 4; __VA_ARGS__; } break; \
+    }
+// channels per lane and whether a node row is staged in LDS
+#define FEQ_NODE_DISPATCH(L_, ...)                                                        \
+    if (int64_t(L_.mult) * L_.dim <= kStageRow) {                                         \
+        constexpr bool stage = true;                                                      \
+        FEQ_NODE_DISPATCH_S(cpl_of(L_.mult), __VA_ARGS__)                                 \
+    } else {                                                                              \
+        constexpr bool stage = false;                                                     \
+        FEQ_NODE_DISPATCH_S(cpl_of(L_.mult), __VA_ARGS__)                                 \
+    }
+
+extern "C" int feq_sepnorm_fwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                               const float* x, const float* w_s, const float* b_s,
+                               const float* w_h, float eps, float* y, feq_stream_t stream) {
+    NodeL L;
+    if (int rc = make_nodel(lvals, nreps, mult, &L)) return rc;
+    if (L.ns > kMaxS) return fail(FEQ_ERR_UNSUPPORTED, "at most %d scalar irreps", kMaxS);
+    if (int rc = check_rows(N, x, y, x)) return rc;
+    if ((L.ns && (!w_s || !b_s)) || (L.nhc && !w_h)) return fail(FEQ_ERR_INVALID, "NULL norm weight");
+    if (N == 0) return FEQ_OK;
+    hipStream_t s = stream_of(stream);
+    const dim3 grid(static_cast<unsigned>(ceil_div(N, kWaves)));
+    FEQ_NODE_DISPATCH(L, {
+        auto k = k_sepnorm_fwd<cpl, stage>;
+        FEQ_LAUNCH("k_sepnorm_fwd", k, grid, dim3(64 * kWaves), 0, s, L, N, x, w_s, b_s, w_h, eps, y);
+    })
+    return FEQ_OK;
+}
+
+extern "C" size_t feq_sepnorm_workspace(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N) {
+    NodeL L;
+    if (make_nodel(lvals, nreps, mult, &L) || N <= 0) return 0;
+    const int64_t w = bwd_waves(N);
+    return sizeof(float) * (2 * partial_floats(w, int64_t(mult) * L.ns) + partial_floats(w, mult)) + 256;
+}
+
+extern "C" int feq_sepnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                               const float* gy, const float* x, const float* w_s, const float* w_h,
+                               float eps, float* gx, float* gw_s, float* gb_s, float* gw_h,
+                               void* ws, size_t ws_bytes, feq_stream_t stream) {
+    NodeL L;
+    if (int rc = make_nodel(lvals, nreps, mult, &L)) return rc;
+    if (L.ns > kMaxS) return fail(FEQ_ERR_UNSUPPORTED, "at most %d scalar irreps", kMaxS);
+    if (int rc = check_rows(N, gy, x, gx)) return rc;
+    if ((L.ns && (!w_s || !gw_s || !gb_s)) || (L.nhc && (!w_h || !gw_h)))
+        return fail(FEQ_ERR_INVALID, "NULL norm weight or gradient");
+    hipStream_t s = stream_of(stream);
+    const int64_t nsc = int64_t(mult) * L.ns;
+    if (N == 0) {
+        if (L.ns) {
+            if (int rc = fill_zero(gw_s, nsc, s)) return rc;
+            if (int rc = fill_zero(gb_s, nsc, s)) return rc;
+        }
+        if (L.nhc) return fill_zero(gw_h, mult, s);
+        return FEQ_OK;
+    }
+    if (!ws || ws_bytes < feq_sepnorm_workspace(lvals, nreps, mult, N))
+        return fail(FEQ_ERR_WORKSPACE, "separable norm workspace too small");
+    const int64_t w = bwd_waves(N);
+    float* base = static_cast<float*>(ws);
+    float* pS = base;
+    float* pB = pS + partial_floats(w, nsc);
+    float* pH = pB + partial_floats(w, nsc);
+    FEQ_NODE_DISPATCH(L, {
+        auto k = k_sepnorm_bwd<cpl, stage>;
+        FEQ_LAUNCH("k_sepnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
+                   s, L, N, gy, x, w_s, w_h, eps, gx, pS, pB, L.nhc ? pH : nullptr);
+    })
+    if (L.ns) {
+        if (int rc = reduce_partials(pS, int(w), nsc, gw_s, pS + w * nsc, s)) return rc;
+        if (int rc = reduce_partials(pB, int(w), nsc, gb_s, pB + w * nsc, s)) return rc;
+    }
+    if (L.nhc)
+        if (int rc = reduce_partials(pH, int(w), mult, gw_h, pH + w * mult, s)) return rc;
+    return FEQ_OK;
+}
+
+extern "C" int feq_eqnorm_fwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                              const float* x, const float* w_ln, const float* b_ln, float eps,
+                              float ln_eps, float* y, feq_stream_t stream) {
+    NodeL L;
+    if (int rc = make_nodel(lvals, nreps, mult, &L)) return rc;
+    if (int rc = check_rows(N, x, y, x)) return rc;
+    if (!w_ln != !b_ln) return fail(FEQ_ERR_INVALID, "LayerNorm weight and bias go together");
+    if (N == 0) return FEQ_OK;
+    hipStream_t s = stream_of(stream);
+    FEQ_NODE_DISPATCH(L, {
+        auto k = k_eqnorm_fwd<cpl, stage>;
+        FEQ_LAUNCH("k_eqnorm_fwd", k, dim3(static_cast<unsigned>(ceil_div(N, kWaves))),
+                   dim3(64 * kWaves), 0, s, L, N, x, w_ln, b_ln, eps, ln_eps, y);
+    })
+    return FEQ_OK;
+}
+
+extern "C" size_t feq_eqnorm_workspace(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N) {
+    NodeL L;
+    if (make_nodel(lvals, nreps, mult, &L) || N <= 0) return 0;
+    return sizeof(float) * 2 * partial_floats(bwd_waves(N), mult) + 256;
+}
+
+extern "C" int feq_eqnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                              const float* gy, const float* x, const float* w_ln, const float* b_ln,
+                              float eps, float ln_eps, float* gx, float* gw_ln, float* gb_ln,
+                              void* ws, size_t ws_bytes, feq_stream_t stream) {
+    NodeL L;
+    if (int rc = make_nodel(lvals, nreps, mult, &L)) return rc;
+    if (int rc = check_rows(N, gy, x, gx)) return rc;
+    if (!w_ln != !b_ln) return fail(FEQ_ERR_INVALID, "LayerNorm weight and bias go together");
+    if (w_ln && (!gw_ln || !gb_ln)) return fail(FEQ_ERR_INVALID, "NULL LayerNorm gradient");
+    hipStream_t s = stream_of(stream);
+    if (N == 0) {
+        if (!w_ln) return FEQ_OK;
+        if (int rc = fill_zero(gw_ln, mult, s)) return rc;
+        return fill_zero(gb_ln, mult, s);
+    }
+    if (w_ln && (!ws || ws_bytes < feq_eqnorm_workspace(lvals, nreps, mult, N)))
+        return fail(FEQ_ERR_WORKSPACE, "equivariant norm workspace too small");
+    const int64_t w = bwd_waves(N);
+    float* pW = w_ln ? static_cast<float*>(ws) : nullptr;
+    float* pB = w_ln ? pW + partial_floats(w, mult) : nullptr;
+    FEQ_NODE_DISPATCH(L, {
+        auto k = k_eqnorm_bwd<cpl, stage>;
+        FEQ_LAUNCH("k_eqnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
+                   s, L, N, gy, x, w_ln, b_ln, eps, ln_eps, gx, pW, pB);
+    })
+    if (!w_ln) return FEQ_OK;
+    if (int rc = reduce_partials(pW, int(w), mult, gw_ln, pW + w * mult, s)) return rc;
+    return reduce_partials(pB, int(w), mult, gb_ln, pB + w * mult, s);
+}
+
+#define FEQ_GATE_PRELUDE(a, b, c)                                                         \
+    NodeL L;                                                                              \
+    if (int rc = make_nodel(lvals, nreps, mult, &L)) return rc;                           \
+    if (int rc = check_rows(N, a, b, c)) return rc;                                       \
+    if (N == 0) return FEQ_OK;                                                            \
+    const int64_t rows = N * mult;                                                        \
+    const dim3 grid(static_cast<unsigned>(ceil_div(rows, std::min(kRowThreads, kTileFloats / L.dim)))); \
+    hipStream_t s = stream_of(stream);
+
+extern "C" int feq_gate_norms(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                              const float* x, float eps, float* norms, feq_stream_t stream) {
+    FEQ_GATE_PRELUDE(x, norms, x)
+    FEQ_LAUNCH("k_gate_norms", k_gate_norms, grid, dim3(kRowThreads), 0, s, L, rows, x, eps, norms);
+    return FEQ_OK;
+}
+
+extern "C" int feq_gate_apply(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                              const float* x, const float* lin, float* y, feq_stream_t stream) {
+    FEQ_GATE_PRELUDE(x, lin, y)
+    FEQ_LAUNCH("k_gate_apply", k_gate_apply, grid, dim3(kRowThreads), 0, s, L, rows, x, lin, y);
+    return FEQ_OK;
+}
+
+extern "C" int feq_gate_bwd_lin(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                                const float* gy, const float* x, const float* lin, float* grad_lin,
+                                feq_stream_t stream) {
+    FEQ_GATE_PRELUDE(gy, x, lin)
+    if (!grad_lin) return fail(FEQ_ERR_INVALID, "NULL tensor pointer");
+    FEQ_LAUNCH("k_gate_bwd_lin", k_gate_bwd_lin, grid, dim3(kRowThreads), 0, s, L, rows, gy, x, lin,
+               grad_lin);
+    return FEQ_OK;
+}
+
+extern "C" int feq_gate_bwd_x(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                              const float* gy, const float* x, const float* lin, const float* norms,
+                              const float* grad_norms, float* gx, feq_stream_t stream) {
+    FEQ_GATE_PRELUDE(gy, x, lin)
+    if (!norms || !grad_norms || !gx) return fail(FEQ_ERR_INVALID, "NULL tensor pointer");
+    FEQ_LAUNCH("k_gate_bwd_x", k_gate_bwd_x, grid, dim3(kRowThreads), 0, s, L, rows, gy, x, lin,
+               norms, grad_norms, gx);
+    return FEQ_OK;
+}

@@ -72,6 +72,19 @@ _SIGS = {
                               _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
     "feq_edgewise_hl_supported": ([_P, _P, _I32], ctypes.c_int),
     "feq_edgewise_hl_workspace": ([_P, _P, _I32, _I64, _I32], _SZ),
+    # node-side norms and gating: (lvals, nreps, mult, N, ...)
+    "feq_sepnorm_fwd": ([_P, _I32, _I32, _I64, _P, _P, _P, _P, _F, _P, _P], ctypes.c_int),
+    "feq_sepnorm_workspace": ([_P, _I32, _I32, _I64], _SZ),
+    "feq_sepnorm_bwd": ([_P, _I32, _I32, _I64, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _SZ, _P],
+                        ctypes.c_int),
+    "feq_eqnorm_fwd": ([_P, _I32, _I32, _I64, _P, _P, _P, _F, _F, _P, _P], ctypes.c_int),
+    "feq_eqnorm_workspace": ([_P, _I32, _I32, _I64], _SZ),
+    "feq_eqnorm_bwd": ([_P, _I32, _I32, _I64, _P, _P, _P, _P, _F, _F, _P, _P, _P, _P, _SZ, _P],
+                       ctypes.c_int),
+    "feq_gate_norms": ([_P, _I32, _I32, _I64, _P, _F, _P, _P], ctypes.c_int),
+    "feq_gate_apply": ([_P, _I32, _I32, _I64, _P, _P, _P, _P], ctypes.c_int),
+    "feq_gate_bwd_lin": ([_P, _I32, _I32, _I64, _P, _P, _P, _P, _P], ctypes.c_int),
+    "feq_gate_bwd_x": ([_P, _I32, _I32, _I64, _P, _P, _P, _P, _P, _P, _P], ctypes.c_int),
     "feq_edgewise_hl_fwd": ([_P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
                             ctypes.c_int),
     "feq_edgewise_hl_bwd": ([_P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,

@@ -1,11 +1,15 @@
-"""Norm-based gating (drop-in for ``flash_eq/layers/gating.py:17-76``); node-side PyTorch."""
+"""Norm-based gating (drop-in for ``flash_eq/layers/gating.py:17-76``).
+
+On float32 GPU tables the irrep norms and the sigmoid gate run as kernels
+(``csrc/nodeside.hip``) around the Linear's GEMM; otherwise PyTorch."""
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
 
+from .. import ops
 from ..representations import Repr
-from ..utils import init_linear_weights
+from ..utils import get_epsilon, init_linear_weights
 from .linear import rows_linear
 from .norm import RepNorm, irrep_expand, irrep_slices
 
@@ -24,8 +28,13 @@ class EquivariantGating(nn.Module):
         self._slices = irrep_slices(repr)
         self.activation = nn.Sigmoid()
         self.apply(init_linear_weights)
+        self._lv = tuple(int(l) for l in repr.lvals.tolist())
 
     def forward(self, st: torch.Tensor) -> torch.Tensor:
+        if (self.norm._epsilon is None and ops.node_kernels_ok(
+                st, self._lv, self.repr.mult, self.linear.weight, self.linear.bias)):
+            return ops.GatingFn.apply(st, self.linear.weight, self.linear.bias, self._lv,
+                                      self.repr.mult, get_epsilon(st.dtype))
         norms = self.norm(st)
         *batch, _, _ = norms.shape
         flat = norms.flatten(-2, -1)

@@ -21,7 +21,8 @@ import torch
 import torch.nn as nn
 
 from .. import _native as N
-from ..ops import edgewise_linear, edgewise_linear_src, edgewise_src_supported, embedding_for
+from ..ops import (edgewise_linear, edgewise_linear_src, edgewise_src_supported, embedding_for,
+                   rows_weight_grad)
 from ..representations import ProductRepr, Repr
 from .radial import SeparableRadialNet
 
@@ -44,19 +45,7 @@ class RowsLinearFn(torch.autograd.Function):
     def backward(ctx, gy):
         x, w = ctx.saved_tensors
         gx = torch.mm(gy, w) if ctx.needs_input_grad[0] else None
-        gw = None
-        if ctx.needs_input_grad[1]:
-            rows = x.shape[0]
-            s = RowsLinearFn.CHUNKS if rows >= 64 * RowsLinearFn.CHUNKS else 1
-            per = rows // s
-            head = s * per
-            gyc = gy[:head].reshape(s, per, gy.shape[1]).transpose(1, 2).contiguous()
-            xc = x[:head].reshape(s, per, x.shape[1])
-            acc = torch.promote_types(w.dtype, torch.float32)
-            gw = torch.bmm(gyc, xc).to(acc).sum(0)
-            if head < rows:
-                gw = gw + torch.mm(gy[head:].t().to(acc), x[head:].to(acc))
-            gw = gw.to(w.dtype)
+        gw = rows_weight_grad(gy, x, w.dtype, RowsLinearFn.CHUNKS) if ctx.needs_input_grad[1] else None
         return gx, gw
 
 

@@ -1,18 +1,22 @@
 """Equivariant normalisations (drop-in for ``flash_eq/layers/norm.py``).
 
-Node-side O(N C D) elementwise work, kept in PyTorch (not on the edge hot path).
-Formulas follow ``norm.py:19-249``.  Per-irrep reductions and broadcasts are
-written with slices of the component axis (one run of 2l+1 components per
-irrep): their backward passes are slices, sums and broadcasts again.  The
-reference's ``x[..., ix]`` expansion has an ``index_put_(accumulate=True)``
-backward, which PyTorch runs as a sort over every element (4.5 ms per call at
-20k nodes x 128 channels on MI355X).
+Node-side O(N C D) work next to the edge path.  Formulas follow
+``norm.py:19-249``.  On float32 GPU tables, ``SeparableEquivariantLayerNorm``
+and ``EquivariantLayerNorm`` run fused HIP kernels (one wave per node, forward
+and backward: ``csrc/nodeside.hip``).  Other dtypes and devices run the
+PyTorch formulation below, in which per-irrep reductions and broadcasts are
+slices of the component axis (one run of 2l+1 components per irrep): their
+backward passes are slices, sums and broadcasts again.  The reference's
+``x[..., ix]`` expansion has an ``index_put_(accumulate=True)`` backward, which
+PyTorch runs as a sort over every element (4.5 ms per call at 20k nodes x 128
+channels on MI355X).
 """
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
 
+from .. import ops
 from ..representations import Repr
 from ..utils import get_epsilon
 
@@ -99,9 +103,16 @@ class EquivariantLayerNorm(nn.Module):
         self._epsilon = epsilon
         self.register_buffer("ix", torch.tensor(repr.indices(), dtype=torch.long))
         self._slices = irrep_slices(repr)
+        self._lv = tuple(int(l) for l in repr.lvals.tolist())
 
     def forward(self, f: torch.Tensor) -> torch.Tensor:
         eps = self._epsilon if self._epsilon is not None else get_epsilon(f.dtype)
+        w = self.lnorm.weight if self.lnorm is not None else None
+        b = self.lnorm.bias if self.lnorm is not None else None
+        if self._epsilon is None and ops.node_kernels_ok(f, self._lv, self.mult, w, b) and (
+                self.lnorm is None or (w is not None and b is not None)):
+            ln_eps = self.lnorm.eps if self.lnorm is not None else 0.0
+            return ops.EqNormFn.apply(f, w, b, self._lv, self.mult, eps, ln_eps)
         norms = self.norm(f)                                  # (..., mult, nreps)
         if self.lnorm is None:
             return f * irrep_expand(1.0 / (norms + eps), self._slices)
@@ -126,6 +137,7 @@ class SeparableEquivariantLayerNorm(nn.Module):
             self.scalar_norm = _ChannelLayerNorm(repr.mult, nscalar, epsilon)
         if self.nhigher > 0:
             self.higher_norm = _EquivariantRMSNorm(repr.mult, epsilon)
+        self._lv = tuple(int(l) for l in repr.lvals.tolist())
         # component runs in order: ("s", j) = scalar number j, ("h", a, b) = a run
         # of consecutive l > 0 components
         self._runs: list[tuple] = []
@@ -138,6 +150,14 @@ class SeparableEquivariantLayerNorm(nn.Module):
                 self._runs.append(("h", a, b))
 
     def forward(self, f: torch.Tensor) -> torch.Tensor:
+        ws = self.scalar_norm.weight if self.nscalar > 0 else None
+        bs = self.scalar_norm.bias if self.nscalar > 0 else None
+        wh = self.higher_norm.weight if self.nhigher > 0 else None
+        if (self.nscalar <= ops.NODE_MAX_SCALARS
+                and ops.node_kernels_ok(f, self._lv, self.repr.mult, ws, bs, wh)):
+            mod = self.scalar_norm if self.nscalar > 0 else self.higher_norm
+            eps = mod._epsilon if mod._epsilon is not None else get_epsilon(f.dtype)
+            return ops.SepNormFn.apply(f, ws, bs, wh, self._lv, self.repr.mult, eps)
         ys = None
         if self.nscalar > 0:
             xs = torch.cat([f[..., a:a + 1] for a in self.scalar_locs], dim=-1)

@@ -8,6 +8,7 @@ rejected: the kernels are float32.
 """
 from __future__ import annotations
 
+from functools import lru_cache
 from typing import Optional, Sequence, Tuple
 
 import torch
@@ -679,3 +680,189 @@ def bin_edges(dist: torch.Tensor, binning: N.FeqBinning) -> Tuple[torch.Tensor, 
                                        N.stream_ptr(dev))
         N.check(rc, "feq_bin_edges")
     return lo, t
+
+
+# ---- node-side norms and gating (csrc/nodeside.hip) ---------------------------------
+
+NODE_MAX_MULT = 256
+NODE_MAX_SCALARS = 8
+
+
+@lru_cache(maxsize=256)
+def _lvals_i32(lvals: Tuple[int, ...]):
+    return (N.ctypes.c_int32 * len(lvals))(*lvals)
+
+
+def node_kernels_ok(x: torch.Tensor, lvals: Tuple[int, ...], mult: int,
+                    *params: Optional[torch.Tensor]) -> bool:
+    """The node-side kernels take float32 GPU tables of at most NODE_MAX_MULT
+    channels whose float32 parameters live on the same device; other inputs run
+    the modules' PyTorch formulation."""
+    if not (x.is_cuda and x.dtype == torch.float32 and 1 <= mult <= NODE_MAX_MULT):
+        return False
+    if not 1 <= len(lvals) <= 32:
+        return False
+    return all(p is None or (p.dtype == torch.float32 and p.device == x.device) for p in params)
+
+
+def _node_rows(x: torch.Tensor, mult: int, dim: int) -> int:
+    if x.dim() < 2 or x.shape[-2] != mult or x.shape[-1] != dim:
+        raise RuntimeError(f"node features must be (..., {mult}, {dim}); got {tuple(x.shape)}")
+    return x.numel() // (mult * dim) if x.numel() else 0
+
+
+def _c(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    return None if t is None else t.detach().contiguous()
+
+
+class SepNormFn(torch.autograd.Function):
+    """SeparableEquivariantLayerNorm (norm.py:177-246) on feq_sepnorm_fwd/bwd."""
+
+    @staticmethod
+    def forward(ctx, x, w_s, b_s, w_h, lvals, mult, eps):
+        dim = sum(2 * l + 1 for l in lvals)
+        xs = x.contiguous()
+        n = _node_rows(xs, mult, dim)
+        w_s, b_s, w_h = _c(w_s), _c(b_s), _c(w_h)
+        y = torch.empty_like(xs)
+        if n:
+            with torch.cuda.device(xs.device):
+                rc = N.lib().feq_sepnorm_fwd(_lvals_i32(lvals), len(lvals), mult, n, N.ptr(xs),
+                                             N.ptr(w_s), N.ptr(b_s), N.ptr(w_h), eps, N.ptr(y),
+                                             N.stream_ptr(xs.device))
+            N.check(rc, "feq_sepnorm_fwd")
+        ctx.save_for_backward(xs, w_s, b_s, w_h)
+        ctx.meta = (lvals, mult, eps, n)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        xs, w_s, b_s, w_h = ctx.saved_tensors
+        lvals, mult, eps, n = ctx.meta
+        gy = gy.contiguous()
+        dev = xs.device
+        gx = torch.empty_like(xs)
+        gws = torch.empty_like(w_s) if w_s is not None else None
+        gbs = torch.empty_like(b_s) if b_s is not None else None
+        gwh = torch.empty_like(w_h) if w_h is not None else None
+        lib = N.lib()
+        arr = _lvals_i32(lvals)
+        ws = N.workspace(lib.feq_sepnorm_workspace(arr, len(lvals), mult, n), dev)
+        with torch.cuda.device(dev):
+            rc = lib.feq_sepnorm_bwd(arr, len(lvals), mult, n, N.ptr(gy), N.ptr(xs), N.ptr(w_s),
+                                     N.ptr(w_h), eps, N.ptr(gx), N.ptr(gws), N.ptr(gbs), N.ptr(gwh),
+                                     N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+        N.check(rc, "feq_sepnorm_bwd")
+        return gx, gws, gbs, gwh, None, None, None
+
+
+class EqNormFn(torch.autograd.Function):
+    """EquivariantLayerNorm (norm.py:148-174) on feq_eqnorm_fwd/bwd."""
+
+    @staticmethod
+    def forward(ctx, x, w_ln, b_ln, lvals, mult, eps, ln_eps):
+        dim = sum(2 * l + 1 for l in lvals)
+        xs = x.contiguous()
+        n = _node_rows(xs, mult, dim)
+        w_ln, b_ln = _c(w_ln), _c(b_ln)
+        y = torch.empty_like(xs)
+        if n:
+            with torch.cuda.device(xs.device):
+                rc = N.lib().feq_eqnorm_fwd(_lvals_i32(lvals), len(lvals), mult, n, N.ptr(xs),
+                                            N.ptr(w_ln), N.ptr(b_ln), eps, ln_eps, N.ptr(y),
+                                            N.stream_ptr(xs.device))
+            N.check(rc, "feq_eqnorm_fwd")
+        ctx.save_for_backward(xs, w_ln, b_ln)
+        ctx.meta = (lvals, mult, eps, ln_eps, n)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        xs, w_ln, b_ln = ctx.saved_tensors
+        lvals, mult, eps, ln_eps, n = ctx.meta
+        gy = gy.contiguous()
+        dev = xs.device
+        gx = torch.empty_like(xs)
+        gw = torch.empty_like(w_ln) if w_ln is not None else None
+        gb = torch.empty_like(b_ln) if b_ln is not None else None
+        lib = N.lib()
+        arr = _lvals_i32(lvals)
+        ws = N.workspace(lib.feq_eqnorm_workspace(arr, len(lvals), mult, n), dev)
+        with torch.cuda.device(dev):
+            rc = lib.feq_eqnorm_bwd(arr, len(lvals), mult, n, N.ptr(gy), N.ptr(xs), N.ptr(w_ln),
+                                    N.ptr(b_ln), eps, ln_eps, N.ptr(gx), N.ptr(gw), N.ptr(gb),
+                                    N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+        N.check(rc, "feq_eqnorm_bwd")
+        return gx, gw, gb, None, None, None, None
+
+
+def rows_weight_grad(gy: torch.Tensor, x: torch.Tensor, dtype: torch.dtype,
+                     chunks: int = 64) -> torch.Tensor:
+    """gy^T x over many rows, as a batched GEMM over row chunks whose partial
+    products are summed in float32 (or the inputs' wider type).  As one GEMM
+    (M = out, N = in, K = rows) the library runs it on a few output tiles (about
+    5 TFLOP/s at 100k rows on MI355X)."""
+    rows = x.shape[0]
+    s = chunks if rows >= 64 * chunks else 1
+    per = rows // s
+    head = s * per
+    gyc = gy[:head].reshape(s, per, gy.shape[1]).transpose(1, 2).contiguous()
+    xc = x[:head].reshape(s, per, x.shape[1])
+    acc = torch.promote_types(dtype, torch.float32)
+    gw = torch.bmm(gyc, xc).to(acc).sum(0)
+    if head < rows:
+        gw = gw + torch.mm(gy[head:].t().to(acc), x[head:].to(acc))
+    return gw.to(dtype)
+
+
+class GatingFn(torch.autograd.Function):
+    """EquivariantGating (gating.py:54-76): irrep norms and the sigmoid gate
+    in kernels (feq_gate_*), the Linear over the flattened norms as a GEMM."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, lvals, mult, eps):
+        dim = sum(2 * l + 1 for l in lvals)
+        nreps = len(lvals)
+        xs = x.contiguous()
+        n = _node_rows(xs, mult, dim)
+        dev = xs.device
+        lib = N.lib()
+        arr = _lvals_i32(lvals)
+        norms = torch.empty(n, mult * nreps, dtype=torch.float32, device=dev)
+        with torch.cuda.device(dev):
+            rc = lib.feq_gate_norms(arr, nreps, mult, n, N.ptr(xs), eps, N.ptr(norms),
+                                    N.stream_ptr(dev))
+        N.check(rc, "feq_gate_norms")
+        lin = torch.addmm(bias.detach(), norms, weight.detach().t())
+        y = torch.empty_like(xs)
+        with torch.cuda.device(dev):
+            rc = lib.feq_gate_apply(arr, nreps, mult, n, N.ptr(xs), N.ptr(lin), N.ptr(y),
+                                    N.stream_ptr(dev))
+        N.check(rc, "feq_gate_apply")
+        ctx.save_for_backward(xs, weight, norms, lin)
+        ctx.meta = (lvals, mult, n)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        xs, weight, norms, lin = ctx.saved_tensors
+        lvals, mult, n = ctx.meta
+        gy = gy.contiguous()
+        dev = xs.device
+        lib = N.lib()
+        arr = _lvals_i32(lvals)
+        nreps = len(lvals)
+        dlin = torch.empty_like(lin)
+        with torch.cuda.device(dev):
+            rc = lib.feq_gate_bwd_lin(arr, nreps, mult, n, N.ptr(gy), N.ptr(xs), N.ptr(lin),
+                                      N.ptr(dlin), N.stream_ptr(dev))
+        N.check(rc, "feq_gate_bwd_lin")
+        dnorms = torch.mm(dlin, weight.detach())
+        gw = rows_weight_grad(dlin, norms, weight.dtype) if ctx.needs_input_grad[1] else None
+        gb = dlin.sum(0) if ctx.needs_input_grad[2] else None
+        gx = torch.empty_like(xs)
+        with torch.cuda.device(dev):
+            rc = lib.feq_gate_bwd_x(arr, nreps, mult, n, N.ptr(gy), N.ptr(xs), N.ptr(lin),
+                                    N.ptr(norms), N.ptr(dnorms), N.ptr(gx), N.stream_ptr(dev))
+        N.check(rc, "feq_gate_bwd_x")
+        return gx, gw, gb, None, None, None

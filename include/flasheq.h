@@ -34,6 +34,11 @@
  *                            (attention.py:298-304) inside the kernels
  *   feq_attn_pool_fwd/bwd    _apply_attention + GraphPooling 'sum'
  *                            (flash_eq/layers/attention.py:143-167, pooling.py:21-30)
+ *   feq_sepnorm_fwd/bwd      SeparableEquivariantLayerNorm.forward and its autograd
+ *                            (flash_eq/layers/norm.py:177-246, 76-112)
+ *   feq_eqnorm_fwd/bwd       EquivariantLayerNorm.forward (norm.py:148-174, RepNorm :51-73)
+ *   feq_gate_*               EquivariantGating.forward (flash_eq/layers/gating.py:54-76)
+ *                            around its nn.Linear, which stays a library GEMM
  */
 #ifndef FLASHEQ_H
 #define FLASHEQ_H
@@ -248,6 +253,60 @@ int feq_attn_pool_bwd(const float* V, const float* attn, const float* grad_out,
                       const int32_t* perm, const int32_t* offsets, int64_t num_edges,
                       int64_t num_nodes, int32_t mult, int32_t dim, int32_t heads,
                       float* grad_V, float* grad_attn, feq_stream_t stream);
+
+/* ---- node-side neighbours of the path (transformer block norms, gating) ----
+ * Node tables x, y, gy, gx are (N, mult, dim) float32, contiguous; the layout is
+ * the irreps' degrees lvals[nreps] (component offsets follow from 2l+1) and the
+ * channel count mult <= FEQ_NODE_MAX_MULT.  Parameter gradients are written
+ * (not accumulated) and are deterministic. */
+#define FEQ_NODE_MAX_MULT 256
+#define FEQ_NODE_MAX_SCALARS 8   /* l = 0 irreps per layout (separable norm) */
+
+/* SeparableEquivariantLayerNorm (norm.py:177-246): l = 0 components get a
+ * LayerNorm over channels, (v - mu) / (sd + eps) * w_s + b_s with w_s, b_s
+ * (mult, nscalar) (_ChannelLayerNorm, norm.py:76-93); the l > 0 components
+ * v * w_h[c] / sqrt(mean(v^2) + eps) over all channels and l > 0 components of a
+ * node (_EquivariantRMSNorm, norm.py:96-112).  w_s/b_s may be NULL without
+ * scalars, w_h without l > 0 irreps. */
+int feq_sepnorm_fwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
+                    const float* x, const float* w_s, const float* b_s, const float* w_h,
+                    float eps, float* y, feq_stream_t stream);
+size_t feq_sepnorm_workspace(const int32_t* lvals, int32_t nreps, int32_t mult,
+                             int64_t num_nodes);
+int feq_sepnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
+                    const float* grad_y, const float* x, const float* w_s, const float* w_h,
+                    float eps, float* grad_x, float* grad_w_s, float* grad_b_s,
+                    float* grad_w_h, void* workspace, size_t workspace_bytes,
+                    feq_stream_t stream);
+
+/* EquivariantLayerNorm (norm.py:148-174): per irrep k, n = sqrt(sum x^2 + eps)
+ * (RepNorm, norm.py:51-73); y = x * LayerNorm_c(n)[w_ln, b_ln, ln_eps] / (n + eps),
+ * or x / (n + eps) when w_ln = b_ln = NULL (one channel: no LayerNorm). */
+int feq_eqnorm_fwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
+                   const float* x, const float* w_ln, const float* b_ln, float eps,
+                   float ln_eps, float* y, feq_stream_t stream);
+size_t feq_eqnorm_workspace(const int32_t* lvals, int32_t nreps, int32_t mult,
+                            int64_t num_nodes);
+int feq_eqnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
+                   const float* grad_y, const float* x, const float* w_ln, const float* b_ln,
+                   float eps, float ln_eps, float* grad_x, float* grad_w_ln, float* grad_b_ln,
+                   void* workspace, size_t workspace_bytes, feq_stream_t stream);
+
+/* EquivariantGating (gating.py:54-76) as norms -> [caller's Linear] -> apply:
+ * norms (N, mult, nreps) = sqrt(sum_irrep x^2 + eps); y = x * sigmoid(lin)
+ * broadcast over each irrep's components, lin (N, mult, nreps) the Linear's output.
+ * Backward: grad_lin = sigmoid'(lin) * sum_irrep gy x (feed it to the Linear's
+ * backward for grad_norms), then grad_x = gy sigmoid(lin) + x grad_norms / norms. */
+int feq_gate_norms(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
+                   const float* x, float eps, float* norms, feq_stream_t stream);
+int feq_gate_apply(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
+                   const float* x, const float* lin, float* y, feq_stream_t stream);
+int feq_gate_bwd_lin(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
+                     const float* grad_y, const float* x, const float* lin, float* grad_lin,
+                     feq_stream_t stream);
+int feq_gate_bwd_x(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
+                   const float* grad_y, const float* x, const float* lin, const float* norms,
+                   const float* grad_norms, float* grad_x, feq_stream_t stream);
 
 #ifdef __cplusplus
 }

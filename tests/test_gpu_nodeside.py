@@ -1,0 +1,138 @@
+"""GPU parity of the node-side kernels (csrc/nodeside.hip): the separable
+equivariant layer norm, the equivariant layer norm and the norm gating, forward
+and every gradient, against the float64 oracle (whose index-form restatements
+are pinned to the reference's own vectors in test_node_side_cpu.py).
+
+Layouts cover scalars in the middle, repeated and missing scalars, a single
+irrep, one channel (no LayerNorm), and 1, 2 and 4 channels per lane (up to 256
+channels, with a partial last lane group).  The library's launch log confirms
+that the kernels, not the PyTorch formulation, produced the results.
+"""
+import pytest
+import torch
+
+import flash_eq as fe
+from flash_eq import _native as NAT
+from helpers import rel_err
+from oracle import layer as OL
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+CASES = [([0, 1, 2], 64), ([1, 0, 2], 5), ([0, 0, 1, 2], 7), ([2, 1], 33), ([0], 8),
+         ([1, 2, 0, 1], 100), ([0, 1, 2], 128), ([0, 1], 200), ([0, 1, 2], 256), ([0, 1, 2], 1)]
+
+
+def _randomise(m, g):
+    with torch.no_grad():
+        for p in m.parameters():
+            p.copy_(torch.randn(p.shape, generator=g) * 0.5 + 1.0)
+    return m
+
+
+def _run(module, x, gy, dev):
+    """Forward and backward on the GPU with the launch log on; returns
+    (y, grad_x, {param name: grad}, launched kernel names)."""
+    m = module.to(dev)
+    xg = x.to(dev).requires_grad_(True)
+    NAT.profile_summary()
+    NAT.profile_enable(True)
+    y = m(xg)
+    y.backward(gy.to(dev))
+    torch.cuda.synchronize()
+    NAT.profile_enable(False)
+    launched = NAT.profile_summary()
+    return y, xg.grad, {n: p.grad for n, p in m.named_parameters()}, launched
+
+
+def _leaf(t):
+    return t.detach().double().cpu().requires_grad_(True)
+
+
+@pytest.mark.parametrize("lvals,mult", CASES)
+def test_separable_norm_matches_oracle(dev, lvals, mult):
+    g = torch.Generator().manual_seed(mult + len(lvals))
+    rp = fe.Repr(lvals, mult)
+    m = _randomise(fe.SeparableEquivariantLayerNorm(rp), g)
+    # scalars with a large common offset: the channel statistics are two-pass
+    x = torch.randn(37, mult, rp.dim(), generator=g) + 3.0
+    gy = torch.randn(x.shape, generator=g)
+    ws = _leaf(m.scalar_norm.weight) if m.nscalar else None
+    bs = _leaf(m.scalar_norm.bias) if m.nscalar else None
+    wh = _leaf(m.higher_norm.weight) if m.nhigher else None
+    y, gx, grads, launched = _run(m, x, gy, dev)
+    assert "k_sepnorm_fwd" in launched and "k_sepnorm_bwd" in launched, launched
+    xd = _leaf(x)
+    yref = OL.separable_layer_norm(xd, lvals, ws, bs, wh)
+    yref.backward(gy.double())
+    assert rel_err(y, yref) < TOL
+    assert rel_err(gx, xd.grad) < TOL
+    if ws is not None:
+        assert rel_err(grads["scalar_norm.weight"], ws.grad) < TOL
+        assert rel_err(grads["scalar_norm.bias"], bs.grad) < TOL
+    if wh is not None:
+        assert rel_err(grads["higher_norm.weight"], wh.grad) < TOL
+
+
+@pytest.mark.parametrize("lvals,mult", CASES)
+def test_equivariant_norm_matches_oracle(dev, lvals, mult):
+    g = torch.Generator().manual_seed(100 + mult + len(lvals))
+    rp = fe.Repr(lvals, mult)
+    m = _randomise(fe.EquivariantLayerNorm(rp), g)
+    x = torch.randn(29, mult, rp.dim(), generator=g)
+    gy = torch.randn(x.shape, generator=g)
+    y, gx, grads, launched = _run(m, x, gy, dev)
+    assert "k_eqnorm_fwd" in launched and "k_eqnorm_bwd" in launched, launched
+    xd = _leaf(x)
+    if m.lnorm is not None:
+        w, b = _leaf(m.lnorm.weight), _leaf(m.lnorm.bias)
+        yref = OL.equivariant_layer_norm(xd, lvals, w, b)
+    else:   # one channel: x / (norm + eps) (norm.py:160-165)
+        idx = torch.tensor([k for k, l in enumerate(lvals) for _ in range(2 * l + 1)])
+        yref = xd / (OL.rep_norms(xd, lvals, 1e-8) + 1e-8)[..., idx]
+    yref.backward(gy.double())
+    assert rel_err(y, yref) < TOL
+    assert rel_err(gx, xd.grad) < TOL
+    if m.lnorm is not None:
+        assert rel_err(grads["lnorm.weight"], w.grad) < TOL
+        assert rel_err(grads["lnorm.bias"], b.grad) < TOL
+
+
+@pytest.mark.parametrize("lvals,mult", CASES[:8])
+def test_gating_matches_oracle(dev, lvals, mult):
+    g = torch.Generator().manual_seed(200 + mult + len(lvals))
+    rp = fe.Repr(lvals, mult)
+    m = fe.EquivariantGating(rp)
+    with torch.no_grad():
+        m.linear.weight.copy_(torch.randn(m.linear.weight.shape, generator=g) * 0.2)
+        m.linear.bias.copy_(torch.randn(m.linear.bias.shape, generator=g))
+    x = torch.randn(300, mult, rp.dim(), generator=g)
+    gy = torch.randn(x.shape, generator=g)
+    W, b = _leaf(m.linear.weight), _leaf(m.linear.bias)
+    y, gx, grads, launched = _run(m, x, gy, dev)
+    assert "k_gate_apply" in launched and "k_gate_bwd_x" in launched, launched
+    xd = _leaf(x)
+    yref = OL.gating(xd, lvals, W, b)
+    yref.backward(gy.double())
+    assert rel_err(y, yref) < TOL
+    assert rel_err(gx, xd.grad) < TOL
+    assert rel_err(grads["linear.weight"], W.grad) < TOL
+    assert rel_err(grads["linear.bias"], b.grad) < TOL
+
+
+def test_node_kernels_batched_and_empty(dev):
+    """Leading batch dimensions flatten to nodes; zero nodes give zero parameter
+    gradients."""
+    rp = fe.Repr([0, 1, 2], 16)
+    torch.manual_seed(3)
+    sln = fe.SeparableEquivariantLayerNorm(rp).to(dev)
+    x = torch.randn(3, 5, 16, 9, device=dev)
+    y = sln(x)
+    y2 = sln(x.reshape(15, 16, 9)).reshape(3, 5, 16, 9)
+    assert torch.equal(y, y2)
+    for m in (sln, fe.EquivariantLayerNorm(rp).to(dev), fe.EquivariantGating(rp).to(dev)):
+        x0 = torch.zeros(0, 16, 9, device=dev, requires_grad=True)
+        y0 = m(x0)
+        assert y0.shape == (0, 16, 9)
+        y0.sum().backward()
+        for n, p in m.named_parameters():
+            assert p.grad is not None and torch.all(p.grad == 0), n
