@@ -577,6 +577,58 @@ k_gate_bwd_x(NodeL L, int64_t rows, const float* __restrict__ gy, const float* _
     tile_store(gx + r0 * L.dim, sg, n);
 }
 
+// Component-major tables (dim, N, mult): element (p, d) of pair p = (node,
+// channel) sits at d * P + p, so consecutive threads read consecutive floats.
+
+__global__ void __launch_bounds__(kRowThreads)
+k_gate_norms_cm(NodeL L, int64_t P, const float* __restrict__ x, float eps, float* __restrict__ nrm) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * kRowThreads + threadIdx.x;
+    if (p >= P) return;
+    for (int k = 0; k < L.nreps; ++k) {
+        float q = 0.0f;
+        for (int d = L.off[k]; d < L.off[k + 1]; ++d) q += x[d * P + p] * x[d * P + p];
+        nrm[p * L.nreps + k] = sqrtf(q + eps);
+    }
+}
+
+__global__ void __launch_bounds__(kRowThreads)
+k_gate_apply_cm(NodeL L, int64_t P, const float* __restrict__ x, const float* __restrict__ lin,
+                float* __restrict__ y) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * kRowThreads + threadIdx.x;
+    if (p >= P) return;
+    for (int k = 0; k < L.nreps; ++k) {
+        const float g = sigmoidf(lin[p * L.nreps + k]);
+        for (int d = L.off[k]; d < L.off[k + 1]; ++d) y[d * P + p] = x[d * P + p] * g;
+    }
+}
+
+__global__ void __launch_bounds__(kRowThreads)
+k_gate_bwd_lin_cm(NodeL L, int64_t P, const float* __restrict__ gy, const float* __restrict__ x,
+                  const float* __restrict__ lin, float* __restrict__ dlin) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * kRowThreads + threadIdx.x;
+    if (p >= P) return;
+    for (int k = 0; k < L.nreps; ++k) {
+        float q = 0.0f;
+        for (int d = L.off[k]; d < L.off[k + 1]; ++d) q += gy[d * P + p] * x[d * P + p];
+        const float g = sigmoidf(lin[p * L.nreps + k]);
+        dlin[p * L.nreps + k] = q * (g * (1.0f - g));
+    }
+}
+
+__global__ void __launch_bounds__(kRowThreads)
+k_gate_bwd_x_cm(NodeL L, int64_t P, const float* __restrict__ gy, const float* __restrict__ x,
+                const float* __restrict__ lin, const float* __restrict__ nrm,
+                const float* __restrict__ dnrm, float* __restrict__ gx) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * kRowThreads + threadIdx.x;
+    if (p >= P) return;
+    for (int k = 0; k < L.nreps; ++k) {
+        const int64_t i = p * L.nreps + k;
+        const float g = sigmoidf(lin[i]);
+        const float q = dnrm[i] / nrm[i];
+        for (int d = L.off[k]; d < L.off[k + 1]; ++d) gx[d * P + p] = gy[d * P + p] * g + x[d * P + p] * q;
+    }
+}
+
 // ---- host ---------------------------------------------------------------------
 
 int cpl_of(int mult) { return mult <= 64 ? 1 : mult <= 128 ? 2 : 4; }
@@ -742,39 +794,57 @@ extern "C" int feq_eqnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult,
     if (int rc = check_rows(N, a, b, c)) return rc;                                       \
     if (N == 0) return FEQ_OK;                                                            \
     const int64_t rows = N * mult;                                                        \
-    const dim3 grid(static_cast<unsigned>(ceil_div(rows, std::min(kRowThreads, kTileFloats / L.dim)))); \
+    const dim3 grid(static_cast<unsigned>(                                                \
+        ceil_div(rows, cm ? kRowThreads : std::min(kRowThreads, kTileFloats / L.dim))));  \
     hipStream_t s = stream_of(stream);
 
 extern "C" int feq_gate_norms(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
-                              const float* x, float eps, float* norms, feq_stream_t stream) {
+                              int32_t cm, const float* x, float eps, float* norms,
+                              feq_stream_t stream) {
     FEQ_GATE_PRELUDE(x, norms, x)
-    FEQ_LAUNCH("k_gate_norms", k_gate_norms, grid, dim3(kRowThreads), 0, s, L, rows, x, eps, norms);
+    if (cm)
+        FEQ_LAUNCH("k_gate_norms", k_gate_norms_cm, grid, dim3(kRowThreads), 0, s, L, rows, x, eps, norms);
+    else
+        FEQ_LAUNCH("k_gate_norms", k_gate_norms, grid, dim3(kRowThreads), 0, s, L, rows, x, eps, norms);
     return FEQ_OK;
 }
 
 extern "C" int feq_gate_apply(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
-                              const float* x, const float* lin, float* y, feq_stream_t stream) {
+                              int32_t cm, const float* x, const float* lin, float* y,
+                              feq_stream_t stream) {
     FEQ_GATE_PRELUDE(x, lin, y)
-    FEQ_LAUNCH("k_gate_apply", k_gate_apply, grid, dim3(kRowThreads), 0, s, L, rows, x, lin, y);
+    if (cm)
+        FEQ_LAUNCH("k_gate_apply", k_gate_apply_cm, grid, dim3(kRowThreads), 0, s, L, rows, x, lin, y);
+    else
+        FEQ_LAUNCH("k_gate_apply", k_gate_apply, grid, dim3(kRowThreads), 0, s, L, rows, x, lin, y);
     return FEQ_OK;
 }
 
 extern "C" int feq_gate_bwd_lin(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
-                                const float* gy, const float* x, const float* lin, float* grad_lin,
-                                feq_stream_t stream) {
+                                int32_t cm, const float* gy, const float* x, const float* lin,
+                                float* grad_lin, feq_stream_t stream) {
     FEQ_GATE_PRELUDE(gy, x, lin)
     if (!grad_lin) return fail(FEQ_ERR_INVALID, "NULL tensor pointer");
-    FEQ_LAUNCH("k_gate_bwd_lin", k_gate_bwd_lin, grid, dim3(kRowThreads), 0, s, L, rows, gy, x, lin,
-               grad_lin);
+    if (cm)
+        FEQ_LAUNCH("k_gate_bwd_lin", k_gate_bwd_lin_cm, grid, dim3(kRowThreads), 0, s, L, rows, gy, x,
+                   lin, grad_lin);
+    else
+        FEQ_LAUNCH("k_gate_bwd_lin", k_gate_bwd_lin, grid, dim3(kRowThreads), 0, s, L, rows, gy, x,
+                   lin, grad_lin);
     return FEQ_OK;
 }
 
 extern "C" int feq_gate_bwd_x(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
-                              const float* gy, const float* x, const float* lin, const float* norms,
-                              const float* grad_norms, float* gx, feq_stream_t stream) {
+                              int32_t cm, const float* gy, const float* x, const float* lin,
+                              const float* norms, const float* grad_norms, float* gx,
+                              feq_stream_t stream) {
     FEQ_GATE_PRELUDE(gy, x, lin)
     if (!norms || !grad_norms || !gx) return fail(FEQ_ERR_INVALID, "NULL tensor pointer");
-    FEQ_LAUNCH("k_gate_bwd_x", k_gate_bwd_x, grid, dim3(kRowThreads), 0, s, L, rows, gy, x, lin,
-               norms, grad_norms, gx);
+    if (cm)
+        FEQ_LAUNCH("k_gate_bwd_x", k_gate_bwd_x_cm, grid, dim3(kRowThreads), 0, s, L, rows, gy, x, lin,
+                   norms, grad_norms, gx);
+    else
+        FEQ_LAUNCH("k_gate_bwd_x", k_gate_bwd_x, grid, dim3(kRowThreads), 0, s, L, rows, gy, x, lin,
+                   norms, grad_norms, gx);
     return FEQ_OK;
 }

@@ -81,10 +81,10 @@ _SIGS = {
     "feq_eqnorm_workspace": ([_P, _I32, _I32, _I64], _SZ),
     "feq_eqnorm_bwd": ([_P, _I32, _I32, _I64, _P, _P, _P, _P, _F, _F, _P, _P, _P, _P, _SZ, _P],
                        ctypes.c_int),
-    "feq_gate_norms": ([_P, _I32, _I32, _I64, _P, _F, _P, _P], ctypes.c_int),
-    "feq_gate_apply": ([_P, _I32, _I32, _I64, _P, _P, _P, _P], ctypes.c_int),
-    "feq_gate_bwd_lin": ([_P, _I32, _I32, _I64, _P, _P, _P, _P, _P], ctypes.c_int),
-    "feq_gate_bwd_x": ([_P, _I32, _I32, _I64, _P, _P, _P, _P, _P, _P, _P], ctypes.c_int),
+    "feq_gate_norms": ([_P, _I32, _I32, _I64, _I32, _P, _F, _P, _P], ctypes.c_int),
+    "feq_gate_apply": ([_P, _I32, _I32, _I64, _I32, _P, _P, _P, _P], ctypes.c_int),
+    "feq_gate_bwd_lin": ([_P, _I32, _I32, _I64, _I32, _P, _P, _P, _P, _P], ctypes.c_int),
+    "feq_gate_bwd_x": ([_P, _I32, _I32, _I64, _I32, _P, _P, _P, _P, _P, _P, _P], ctypes.c_int),
     "feq_edgewise_hl_fwd": ([_P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
                             ctypes.c_int),
     "feq_edgewise_hl_bwd": ([_P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,

@@ -30,9 +30,17 @@ class EquivariantGating(nn.Module):
         self.apply(init_linear_weights)
         self._lv = tuple(int(l) for l in repr.lvals.tolist())
 
+    def kernels_ok(self, st: torch.Tensor) -> bool:
+        return self.norm._epsilon is None and ops.node_kernels_ok(
+            st, self._lv, self.repr.mult, self.linear.weight, self.linear.bias)
+
+    def forward_cm(self, st_cm: torch.Tensor) -> torch.Tensor:
+        """The gating of component-major features (dim, N, mult); kernels_ok."""
+        return ops.GatingFn.apply(st_cm, self.linear.weight, self.linear.bias, self._lv,
+                                  self.repr.mult, get_epsilon(st_cm.dtype), True)
+
     def forward(self, st: torch.Tensor) -> torch.Tensor:
-        if (self.norm._epsilon is None and ops.node_kernels_ok(
-                st, self._lv, self.repr.mult, self.linear.weight, self.linear.bias)):
+        if self.kernels_ok(st):
             return ops.GatingFn.apply(st, self.linear.weight, self.linear.bias, self._lv,
                                       self.repr.mult, get_epsilon(st.dtype))
         norms = self.norm(st)

@@ -22,7 +22,7 @@ import torch.nn as nn
 
 from .. import _native as N
 from ..ops import (edgewise_linear, edgewise_linear_src, edgewise_src_supported, embedding_for,
-                   rows_weight_grad)
+                   rows_weight_grad, BiasRowsFn, EqLinearFn)
 from ..representations import ProductRepr, Repr
 from .radial import SeparableRadialNet
 
@@ -180,6 +180,20 @@ class EquivariantLinear(nn.Module):
         else:
             self.bias = None
         self.activation = activation if activation is not None else nn.Identity()
+        # per irrep: the bias column of a scalar irrep, -1 otherwise
+        self._bias_cols = tuple(locs.index(a) if (self.bias is not None and a in locs) else -1
+                                for a, _ in self._slices)
+
+    def fused_ok(self, f: torch.Tensor) -> bool:
+        """Float32 GPU features without an activation take EqLinearFn."""
+        return (f.is_cuda and f.dtype == torch.float32 and self.weight.dtype == torch.float32
+                and isinstance(self.activation, nn.Identity))
+
+    def forward_layout(self, f: torch.Tensor, in_cm: bool, out_cm: bool) -> torch.Tensor:
+        """The map on node-major (rows, cin, dim) or component-major (dim, rows,
+        cin) features (in_cm), returning either layout (out_cm); fused_ok(f)."""
+        return EqLinearFn.apply(f, self.weight, self.bias, self._slices, self._bias_cols,
+                                self.in_repr.mult, self.out_repr.mult, in_cm, out_cm)
 
     def forward(self, f: torch.Tensor) -> torch.Tensor:
         """(..., in_mult, dim) -> (..., out_mult, dim).
@@ -192,6 +206,8 @@ class EquivariantLinear(nn.Module):
         before summing them.)"""
         cin, cout = self.in_repr.mult, self.out_repr.mult
         lead = f.shape[:-2]
+        if self.fused_ok(f):
+            return self.forward_layout(f, False, False).view(*lead, cout, f.shape[-1])
         w = self.weight.view(self.in_repr.nreps(), cout, cin)
         fd = f.reshape(-1, cin, f.shape[-1]).permute(2, 0, 1).contiguous()   # (dim, rows, cin)
         rows = fd.shape[1]
@@ -200,7 +216,7 @@ class EquivariantLinear(nn.Module):
             y = rows_linear(fd[a:b].reshape(-1, cin), w[k]).view(b - a, rows, cout)
             if self.bias is not None and a in self.scalar_locs:
                 # bias column j belongs to the j-th scalar irrep (out[..., scalar_locs] + bias)
-                y = self.activation(y + self.bias[:, j]).to(y.dtype)
+                y = self.activation(BiasRowsFn.apply(y, self.bias[:, j])).to(y.dtype)
                 j += 1
             parts.append(y)
         out = torch.cat(parts, dim=0) if len(parts) > 1 else parts[0]     # (dim, rows, cout)

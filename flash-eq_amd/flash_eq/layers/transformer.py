@@ -11,6 +11,7 @@ import torch.nn as nn
 
 from ..graph import Graph
 from ..representations import Repr, WignerDBasis
+from ..ops import ScaleFn
 from .attention import EquivariantAttention
 from .gating import EquivariantGating
 from .linear import EquivariantLinear
@@ -25,6 +26,8 @@ class LayerScale(nn.Module):
         self.gamma = nn.Parameter(torch.tensor(init_value))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.is_cuda and x.dtype == self.gamma.dtype:
+            return ScaleFn.apply(x, self.gamma)   # gradient of gamma as one dot product
         return x * self.gamma
 
 
@@ -89,7 +92,16 @@ class EquivariantTransformerBlock(nn.Module):
             x = node_features + self.drop_path(self.layer_scale_attn(attn_out))
         else:
             x = attn_out
-        mlp_out = self.mlp_down(self.mlp_act(self.mlp_up(self.norm2(x))))
+        h = self.norm2(x)
+        if (isinstance(self.mlp_act, EquivariantGating) and self.mlp_act.kernels_ok(h)
+                and self.mlp_up.fused_ok(h) and self.mlp_down.fused_ok(h)):
+            # the hidden features stay component-major (dim, N, 2 mult) between
+            # the two linear maps and the gating: no transposes in between
+            t = self.mlp_act.forward_cm(self.mlp_up.forward_layout(h, False, True))
+            mlp_out = self.mlp_down.forward_layout(t, True, False).view(
+                *h.shape[:-2], self.out_repr.mult, h.shape[-1])
+        else:
+            mlp_out = self.mlp_down(self.mlp_act(self.mlp_up(h)))
         return x + self.drop_path(self.layer_scale_mlp(mlp_out))
 
     def extra_repr(self) -> str:

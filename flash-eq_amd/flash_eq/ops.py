@@ -796,6 +796,55 @@ class EqNormFn(torch.autograd.Function):
         return gx, gw, gb, None, None, None, None
 
 
+_ONES: dict = {}
+
+
+def column_sums(t: torch.Tensor) -> torch.Tensor:
+    """Sum over the rows of a 2-D tensor as a GEMV against a ones vector: one
+    pass over t at memory speed (PyTorch's outer-dimension sum of a tall matrix
+    runs at a fraction of HBM bandwidth on MI355X)."""
+    rows = t.shape[0]
+    if rows == 0:
+        return torch.zeros(t.shape[1], dtype=t.dtype, device=t.device)
+    key = (t.device, t.dtype)
+    ones = _ONES.get(key)
+    if ones is None or ones.numel() < rows:
+        ones = torch.ones(max(rows, 4096), dtype=t.dtype, device=t.device)
+        _ONES[key] = ones
+    return torch.mv(t.t(), ones[:rows])
+
+
+class BiasRowsFn(torch.autograd.Function):
+    """y + b for y (rows, n) and b (n,); the bias gradient by column_sums."""
+
+    @staticmethod
+    def forward(ctx, y, b):
+        return y + b
+
+    @staticmethod
+    def backward(ctx, gy):
+        gb = column_sums(gy.reshape(-1, gy.shape[-1])) if ctx.needs_input_grad[1] else None
+        return gy, gb
+
+
+class ScaleFn(torch.autograd.Function):
+    """x * g for a scalar parameter g; its gradient is one dot product."""
+
+    @staticmethod
+    def forward(ctx, x, g):
+        ctx.save_for_backward(x, g)
+        return x * g
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, g = ctx.saved_tensors
+        gx = gy * g if ctx.needs_input_grad[0] else None
+        gg = None
+        if ctx.needs_input_grad[1]:
+            gg = torch.dot(gy.reshape(-1), x.reshape(-1)).reshape(g.shape).to(g.dtype)
+        return gx, gg
+
+
 def rows_weight_grad(gy: torch.Tensor, x: torch.Tensor, dtype: torch.dtype,
                      chunks: int = 64) -> torch.Tensor:
     """gy^T x over many rows, as a batched GEMM over row chunks whose partial
@@ -809,7 +858,7 @@ def rows_weight_grad(gy: torch.Tensor, x: torch.Tensor, dtype: torch.dtype,
     gyc = gy[:head].reshape(s, per, gy.shape[1]).transpose(1, 2).contiguous()
     xc = x[:head].reshape(s, per, x.shape[1])
     acc = torch.promote_types(dtype, torch.float32)
-    gw = torch.bmm(gyc, xc).to(acc).sum(0)
+    gw = column_sums(torch.bmm(gyc, xc).to(acc).reshape(s, -1)).view(gy.shape[1], x.shape[1])
     if head < rows:
         gw = gw + torch.mm(gy[head:].t().to(acc), x[head:].to(acc))
     return gw.to(dtype)
@@ -820,33 +869,40 @@ class GatingFn(torch.autograd.Function):
     in kernels (feq_gate_*), the Linear over the flattened norms as a GEMM."""
 
     @staticmethod
-    def forward(ctx, x, weight, bias, lvals, mult, eps):
+    def forward(ctx, x, weight, bias, lvals, mult, eps, cm=False):
+        """x: (..., mult, dim), or (dim, N, mult) with cm (component-major)."""
         dim = sum(2 * l + 1 for l in lvals)
         nreps = len(lvals)
         xs = x.contiguous()
-        n = _node_rows(xs, mult, dim)
+        if cm:
+            if xs.dim() != 3 or xs.shape[0] != dim or xs.shape[2] != mult:
+                raise RuntimeError(f"component-major features must be ({dim}, N, {mult}); "
+                                   f"got {tuple(xs.shape)}")
+            n = xs.shape[1]
+        else:
+            n = _node_rows(xs, mult, dim)
         dev = xs.device
         lib = N.lib()
         arr = _lvals_i32(lvals)
         norms = torch.empty(n, mult * nreps, dtype=torch.float32, device=dev)
         with torch.cuda.device(dev):
-            rc = lib.feq_gate_norms(arr, nreps, mult, n, N.ptr(xs), eps, N.ptr(norms),
+            rc = lib.feq_gate_norms(arr, nreps, mult, n, int(cm), N.ptr(xs), eps, N.ptr(norms),
                                     N.stream_ptr(dev))
         N.check(rc, "feq_gate_norms")
         lin = torch.addmm(bias.detach(), norms, weight.detach().t())
         y = torch.empty_like(xs)
         with torch.cuda.device(dev):
-            rc = lib.feq_gate_apply(arr, nreps, mult, n, N.ptr(xs), N.ptr(lin), N.ptr(y),
+            rc = lib.feq_gate_apply(arr, nreps, mult, n, int(cm), N.ptr(xs), N.ptr(lin), N.ptr(y),
                                     N.stream_ptr(dev))
         N.check(rc, "feq_gate_apply")
         ctx.save_for_backward(xs, weight, norms, lin)
-        ctx.meta = (lvals, mult, n)
+        ctx.meta = (lvals, mult, n, cm)
         return y
 
     @staticmethod
     def backward(ctx, gy):
         xs, weight, norms, lin = ctx.saved_tensors
-        lvals, mult, n = ctx.meta
+        lvals, mult, n, cm = ctx.meta
         gy = gy.contiguous()
         dev = xs.device
         lib = N.lib()
@@ -854,15 +910,69 @@ class GatingFn(torch.autograd.Function):
         nreps = len(lvals)
         dlin = torch.empty_like(lin)
         with torch.cuda.device(dev):
-            rc = lib.feq_gate_bwd_lin(arr, nreps, mult, n, N.ptr(gy), N.ptr(xs), N.ptr(lin),
-                                      N.ptr(dlin), N.stream_ptr(dev))
+            rc = lib.feq_gate_bwd_lin(arr, nreps, mult, n, int(cm), N.ptr(gy), N.ptr(xs),
+                                      N.ptr(lin), N.ptr(dlin), N.stream_ptr(dev))
         N.check(rc, "feq_gate_bwd_lin")
         dnorms = torch.mm(dlin, weight.detach())
         gw = rows_weight_grad(dlin, norms, weight.dtype) if ctx.needs_input_grad[1] else None
-        gb = dlin.sum(0) if ctx.needs_input_grad[2] else None
+        gb = column_sums(dlin) if ctx.needs_input_grad[2] else None
         gx = torch.empty_like(xs)
         with torch.cuda.device(dev):
-            rc = lib.feq_gate_bwd_x(arr, nreps, mult, n, N.ptr(gy), N.ptr(xs), N.ptr(lin),
-                                    N.ptr(norms), N.ptr(dnorms), N.ptr(gx), N.stream_ptr(dev))
+            rc = lib.feq_gate_bwd_x(arr, nreps, mult, n, int(cm), N.ptr(gy), N.ptr(xs),
+                                    N.ptr(lin), N.ptr(norms), N.ptr(dnorms), N.ptr(gx),
+                                    N.stream_ptr(dev))
         N.check(rc, "feq_gate_bwd_x")
-        return gx, gw, gb, None, None, None
+        return gx, gw, gb, None, None, None, None
+
+
+class EqLinearFn(torch.autograd.Function):
+    """EquivariantLinear (linear.py:242-268) in component-major form: one GEMM
+    per irrep, (rows * (2l+1), cin) x (cin, cout), written straight into its
+    slice of a (dim, rows, cout) table (no concatenation); the bias of the j-th
+    scalar irrep is the GEMM's bias column.  Input and output are node-major
+    (rows, c, dim) or, with in_cm / out_cm, component-major (dim, rows, c), so
+    consecutive linear maps and the gating can skip the transposes."""
+
+    @staticmethod
+    def forward(ctx, f, weight, bias, slices, bias_cols, cin, cout, in_cm, out_cm):
+        if in_cm:
+            fd = f.contiguous()
+        else:
+            fd = f.reshape(-1, cin, f.shape[-1]).permute(2, 0, 1).contiguous()
+        D, rows = fd.shape[0], fd.shape[1]
+        w = weight.detach().view(-1, cout, cin)
+        out = torch.empty(D, rows, cout, dtype=fd.dtype, device=fd.device)
+        for k, (a, b) in enumerate(slices):
+            xk = fd[a:b].view(-1, cin)
+            ok = out[a:b].view(-1, cout)
+            j = bias_cols[k]
+            if bias is not None and j >= 0:
+                torch.addmm(bias.detach()[:, j], xk, w[k].t(), out=ok)
+            else:
+                torch.mm(xk, w[k].t(), out=ok)
+        ctx.save_for_backward(fd, weight, bias)
+        ctx.meta = (slices, bias_cols, cin, cout, in_cm, out_cm, tuple(f.shape))
+        return out if out_cm else out.permute(1, 2, 0).contiguous()
+
+    @staticmethod
+    def backward(ctx, gy):
+        fd, weight, bias = ctx.saved_tensors
+        slices, bias_cols, cin, cout, in_cm, out_cm, fshape = ctx.meta
+        gyd = gy.contiguous() if out_cm else gy.permute(2, 0, 1).contiguous()
+        w = weight.detach().view(-1, cout, cin)
+        gfd = torch.empty_like(fd) if ctx.needs_input_grad[0] else None
+        gw = torch.empty_like(w) if ctx.needs_input_grad[1] else None
+        gb = torch.zeros_like(bias) if bias is not None and ctx.needs_input_grad[2] else None
+        for k, (a, b) in enumerate(slices):
+            gk = gyd[a:b].view(-1, cout)
+            if gfd is not None:
+                torch.mm(gk, w[k], out=gfd[a:b].view(-1, cin))
+            if gw is not None:
+                gw[k] = rows_weight_grad(gk, fd[a:b].view(-1, cin), weight.dtype)
+            if gb is not None and bias_cols[k] >= 0:
+                gb[:, bias_cols[k]] = column_sums(gk)
+        gx = None
+        if gfd is not None:
+            gx = gfd if in_cm else gfd.permute(1, 2, 0).contiguous().view(fshape)
+        return (gx, gw.view_as(weight) if gw is not None else None, gb,
+                None, None, None, None, None, None)

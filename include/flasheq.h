@@ -296,17 +296,23 @@ int feq_eqnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t nu
  * norms (N, mult, nreps) = sqrt(sum_irrep x^2 + eps); y = x * sigmoid(lin)
  * broadcast over each irrep's components, lin (N, mult, nreps) the Linear's output.
  * Backward: grad_lin = sigmoid'(lin) * sum_irrep gy x (feed it to the Linear's
- * backward for grad_norms), then grad_x = gy sigmoid(lin) + x grad_norms / norms. */
+ * backward for grad_norms), then grad_x = gy sigmoid(lin) + x grad_norms / norms.
+ * component_major != 0: x, y, grad_y, grad_x are (dim, N, mult) instead (the
+ * layout EquivariantLinear's per-irrep GEMMs produce and consume); norms, lin
+ * and their gradients are (N, mult, nreps) either way. */
 int feq_gate_norms(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
-                   const float* x, float eps, float* norms, feq_stream_t stream);
+                   int32_t component_major, const float* x, float eps, float* norms,
+                   feq_stream_t stream);
 int feq_gate_apply(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
-                   const float* x, const float* lin, float* y, feq_stream_t stream);
+                   int32_t component_major, const float* x, const float* lin, float* y,
+                   feq_stream_t stream);
 int feq_gate_bwd_lin(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
-                     const float* grad_y, const float* x, const float* lin, float* grad_lin,
-                     feq_stream_t stream);
+                     int32_t component_major, const float* grad_y, const float* x,
+                     const float* lin, float* grad_lin, feq_stream_t stream);
 int feq_gate_bwd_x(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
-                   const float* grad_y, const float* x, const float* lin, const float* norms,
-                   const float* grad_norms, float* grad_x, feq_stream_t stream);
+                   int32_t component_major, const float* grad_y, const float* x,
+                   const float* lin, const float* norms, const float* grad_norms, float* grad_x,
+                   feq_stream_t stream);
 
 #ifdef __cplusplus
 }

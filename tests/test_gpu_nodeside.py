@@ -136,3 +136,99 @@ def test_node_kernels_batched_and_empty(dev):
         y0.sum().backward()
         for n, p in m.named_parameters():
             assert p.grad is not None and torch.all(p.grad == 0), n
+
+
+@pytest.mark.parametrize("lvals,cin,cout", [([0, 1, 2], 64, 128), ([1, 0, 2], 5, 3),
+                                            ([0, 0, 1, 2], 7, 9), ([2, 1], 33, 16)])
+def test_equivariant_linear_matches_oracle(dev, lvals, cin, cout):
+    """EqLinearFn (one GEMM per irrep into a component-major table, bias as the
+    GEMM's bias column) against the oracle's per-irrep einsum plus bias."""
+    g = torch.Generator().manual_seed(300 + cin + cout)
+    lin = fe.EquivariantLinear(fe.Repr(lvals, cin), fe.Repr(lvals, cout), bias=True)
+    if lin.bias is not None:
+        with torch.no_grad():
+            lin.bias.copy_(torch.randn(lin.bias.shape, generator=g))
+    x = torch.randn(41, cin, fe.Repr(lvals, cin).dim(), generator=g)
+    gy = torch.randn(41, cout, x.shape[-1], generator=g)
+    W = _leaf(lin.weight)
+    bias = _leaf(lin.bias) if lin.bias is not None else None
+    y, gx, grads, _ = _run(lin, x, gy, dev)
+    xd = _leaf(x)
+    yref = OL.equivariant_linear(xd, W, lvals)
+    if bias is not None:
+        offs = fe.Repr(lvals, cin).cumdims().tolist()
+        locs = [offs[k] for k, l in enumerate(lvals) if l == 0]
+        yref = yref.clone()
+        yref[..., locs] = yref[..., locs] + bias
+    yref.backward(gy.double())
+    assert rel_err(y, yref) < TOL
+    assert rel_err(gx, xd.grad) < TOL
+    assert rel_err(grads["weight"], W.grad) < TOL
+    if bias is not None:
+        assert rel_err(grads["bias"], bias.grad) < TOL
+
+
+def test_component_major_gating_equals_node_major(dev):
+    """The (dim, N, mult) gating kernels give the node-major kernels' results."""
+    g = torch.Generator().manual_seed(17)
+    rp = fe.Repr([0, 1, 2], 128)
+    m = fe.EquivariantGating(rp).to(dev)
+    x = torch.randn(500, 128, 9, generator=g).to(dev)
+    gy = torch.randn(500, 128, 9, generator=g).to(dev)
+    x1 = x.clone().requires_grad_(True)
+    y1 = m(x1)
+    y1.backward(gy)
+    gw1 = m.linear.weight.grad.clone()
+    m.zero_grad()
+    x2 = x.permute(2, 0, 1).contiguous().requires_grad_(True)
+    y2 = m.forward_cm(x2)
+    y2.backward(gy.permute(2, 0, 1).contiguous())
+    assert rel_err(y2.permute(1, 2, 0), y1) < 1e-6
+    assert rel_err(x2.grad.permute(1, 2, 0), x1.grad) < 1e-6
+    assert rel_err(m.linear.weight.grad, gw1) < 1e-6
+
+
+def test_block_kernels_equal_pytorch_formulation(dev, monkeypatch):
+    """A whole transformer block with the node-side kernels (fused norms,
+    component-major MLP) against the same block with its node side in the
+    PyTorch formulation (pinned to the oracle in test_node_side_cpu.py), both
+    float32 on the GPU: output and every gradient."""
+    import flash_eq.ops as fops
+    from flash_eq.layers import linear as flin
+
+    torch.manual_seed(21)
+    rp = fe.Repr([0, 1, 2], 16)
+    blk = fe.EquivariantTransformerBlock(rp, rp, num_heads=2, layer_scale_init=0.5).to(dev)
+    g = torch.Generator().manual_seed(22)
+    Nn, E = 60, 600
+    src = torch.randint(0, Nn, (E,), generator=g).to(dev)
+    dst = torch.randint(0, Nn, (E,), generator=g).to(dev)
+    vec = (torch.randn(E, 3, generator=g) * 2).to(dev)
+    x = torch.randn(Nn, 16, 9, generator=g).to(dev)
+    gy = torch.randn(Nn, 16, 9, generator=g).to(dev)
+    P = fe.WignerDBasis([rp]).to(dev)(vec)[0]
+    graph = fe.Graph(src, dst, Nn)
+
+    def run():
+        blk.zero_grad()
+        xg = x.clone().requires_grad_(True)
+        y = blk(P, P, xg, vec.norm(dim=-1), graph)
+        y.backward(gy)
+        return y.detach(), xg.grad, {n: p.grad.clone() for n, p in blk.named_parameters()
+                                     if p.grad is not None}
+
+    NAT.profile_summary()
+    NAT.profile_enable(True)
+    y1, gx1, g1 = run()
+    torch.cuda.synchronize()
+    NAT.profile_enable(False)
+    launched = NAT.profile_summary()
+    assert "k_sepnorm_bwd" in launched and "k_gate_bwd_x" in launched, launched
+    monkeypatch.setattr(fops, "node_kernels_ok", lambda *a, **k: False)
+    monkeypatch.setattr(flin.EquivariantLinear, "fused_ok", lambda self, f: False)
+    y2, gx2, g2 = run()
+    assert rel_err(y1, y2) < TOL
+    assert rel_err(gx1, gx2) < TOL
+    assert set(g1) == set(g2)
+    for n in g1:
+        assert rel_err(g1[n], g2[n]) < TOL, n
