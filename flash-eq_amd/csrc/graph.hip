@@ -195,3 +195,53 @@ extern "C" int feq_gather_rows(const float* src, int64_t nsrc, int64_t row, cons
                        stream_of(stream), src, row, idx, nrows, nsrc, out);
     return FEQ_OK;
 }
+
+// ---- sum of squares (the benchmarks' training loss sum(y^2)) -----------------
+// A fixed grid of kSsqGroups workgroups each sums a strided share of y^2 into
+// one partial; the partials are summed in a fixed order.  Deterministic, and
+// no memset: safe to record into a HIP graph.
+namespace feq {
+namespace {
+constexpr int kSsqGroups = 1024;
+
+__global__ void __launch_bounds__(256)
+k_sum_squares(const float* __restrict__ y, int64_t n, float* __restrict__ part) {
+    __shared__ float s[4];
+    float acc = 0.0f;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if ((reinterpret_cast<uintptr_t>(y) & 15u) == 0) {
+        const float4* y4 = reinterpret_cast<const float4*>(y);
+        const int64_t n4 = n / 4;
+        for (int64_t i = t0; i < n4; i += stride) {
+            const float4 v = y4[i];
+            acc += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        for (int64_t i = 4 * n4 + t0; i < n; i += stride) acc += y[i] * y[i];
+    } else {
+        for (int64_t i = t0; i < n; i += stride) acc += y[i] * y[i];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+    if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) part[blockIdx.x] = (s[0] + s[1]) + (s[2] + s[3]);
+}
+}  // namespace
+}  // namespace feq
+
+extern "C" size_t feq_sum_squares_workspace(void) {
+    return sizeof(float) * (kSsqGroups + kSsqGroups / 32) + 256;
+}
+
+extern "C" int feq_sum_squares(const float* y, int64_t n, float* out, void* ws, size_t ws_bytes,
+                               feq_stream_t stream) {
+    if (n < 0) return fail(FEQ_ERR_INVALID, "negative length");
+    if (!out || (n > 0 && !y)) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (!ws || ws_bytes < feq_sum_squares_workspace())
+        return fail(FEQ_ERR_WORKSPACE, "sum-of-squares workspace too small");
+    hipStream_t s = stream_of(stream);
+    float* part = static_cast<float*>(ws);
+    FEQ_LAUNCH("k_sum_squares", k_sum_squares, dim3(kSsqGroups), dim3(256), 0, s, y, n, part);
+    return reduce_partials(part, kSsqGroups, 1, out, part + kSsqGroups, s);
+}

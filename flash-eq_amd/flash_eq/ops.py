@@ -976,3 +976,26 @@ class EqLinearFn(torch.autograd.Function):
             gx = gfd if in_cm else gfd.permute(1, 2, 0).contiguous().view(fshape)
         return (gx, gw.view_as(weight) if gw is not None else None, gb,
                 None, None, None, None, None, None)
+
+
+class SumSquaresFn(torch.autograd.Function):
+    """sum(y ** 2) of a float32 GPU tensor (feq_sum_squares: deterministic, graph
+    capturable); the gradient 2 y g in one elementwise pass."""
+
+    @staticmethod
+    def forward(ctx, y):
+        ys = y.contiguous()
+        out = torch.empty((), dtype=torch.float32, device=ys.device)
+        lib = N.lib()
+        ws = N.workspace(lib.feq_sum_squares_workspace(), ys.device)
+        with torch.cuda.device(ys.device):
+            rc = lib.feq_sum_squares(N.ptr(ys), ys.numel(), N.ptr(out), N.ptr(ws), ws.numel(),
+                                     N.stream_ptr(ys.device))
+        N.check(rc, "feq_sum_squares")
+        ctx.save_for_backward(ys)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        (ys,) = ctx.saved_tensors
+        return ys * (2.0 * g)

@@ -184,6 +184,13 @@ int feq_segment_sum(const float* x, int64_t row, const int32_t* perm, const int3
 /* out[e, :] = src[idx[e], :] for 0 <= idx[e] < num_src, else 0. */
 int feq_gather_rows(const float* src, int64_t num_src, int64_t row, const int64_t* idx,
                     int64_t num_rows, float* out, feq_stream_t stream);
+/* out[0] = sum of y[i]^2 (the sum-of-squares loss of the reference's benchmark,
+ * benchmarks/compare_all.py: (out**2).sum()), deterministic (a fixed grid of
+ * partials summed in a fixed order) and free of memsets, so it can be recorded
+ * in a HIP graph.  Workspace: feq_sum_squares_workspace() bytes. */
+size_t feq_sum_squares_workspace(void);
+int feq_sum_squares(const float* y, int64_t n, float* out, void* workspace, size_t ws_bytes,
+                    feq_stream_t stream);
 
 /* High-degree form for bfloat16 features (canonical lvals 0..6 in and out,
  * Cin = Cout in {64, 128}, rank 4): x (E, Cin, Din), P, Q, y and the gradients
