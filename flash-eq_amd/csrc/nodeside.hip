@@ -21,7 +21,7 @@ namespace {
 
 constexpr int kWaves = 4;                          // nodes per workgroup, one per wave
 constexpr int kMaxS = FEQ_NODE_MAX_SCALARS;
-constexpr int kBwdGroups = 512;                    // workgroups of the backward norm kernels
+constexpr int kBwdGroups = 1024;                   // workgroups of the backward norm kernels (4 per CU)
 constexpr int kStageRow = 1152;                    // node rows (mult * dim floats) staged in LDS
 constexpr int kRowThreads = 256;
 
