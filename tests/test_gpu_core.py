@@ -108,7 +108,9 @@ def test_block_diagonal_op_parity(dev, lin, lout, log):
     gx, gt, gr = BD.backward(gy.double(), x.double(), T.double(), r.double(), lin, lout, b)
     assert rel_err(xg.grad, gx) < TOL
     assert rel_err(Tg.grad, gt) < TOL
-    assert rel_err(rg.grad, gr) < 1e-4   # sum of many signed terms; see DESIGN.md tolerance note
+    # the distance gradient of an edge is a sum of Cout*Cin*Wdim signed terms that
+    # largely cancel, so its float32 rounding relative to its own size is ~1e-5
+    assert rel_err(rg.grad, gr) < 1e-4
 
 
 # ------------------------------------------------------------------ graph --
