@@ -26,7 +26,7 @@ class LayerScale(nn.Module):
         self.gamma = nn.Parameter(torch.tensor(init_value))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if x.is_cuda and x.dtype == self.gamma.dtype:
+        if x.is_cuda and x.dtype == self.gamma.dtype == torch.float32:
             return ScaleFn.apply(x, self.gamma)   # gradient of gamma as one dot product
         return x * self.gamma
 

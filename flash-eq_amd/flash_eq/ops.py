@@ -804,6 +804,8 @@ def column_sums(t: torch.Tensor) -> torch.Tensor:
     pass over t at memory speed (PyTorch's outer-dimension sum of a tall matrix
     runs at a fraction of HBM bandwidth on MI355X)."""
     rows = t.shape[0]
+    if t.dtype not in (torch.float32, torch.float64):
+        return t.sum(0)             # half-precision GEMV is far slower than the reduction
     if rows == 0:
         return torch.zeros(t.shape[1], dtype=t.dtype, device=t.device)
     key = (t.device, t.dtype)
