@@ -131,9 +131,10 @@ template <int V, int NT, bool NODE>
 __global__ void __launch_bounds__(64 * kWaves)
 k_att_fwd(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ K, int64_t ldk,
           const int64_t* __restrict__ kidx, int64_t nk, const float* __restrict__ dist, int64_t E,
-          int H, int Dh, int lgG, float scale, float decay, const int32_t* __restrict__ perm,
-          const int32_t* __restrict__ offsets, int64_t N, float* __restrict__ attn,
-          float* __restrict__ qk) {
+          int H, int Dh, int lgG, const float* __restrict__ scale_p, float decay,
+          const int32_t* __restrict__ perm, const int32_t* __restrict__ offsets, int64_t N,
+          float* __restrict__ attn, float* __restrict__ qk) {
+    const float scale = *scale_p;
     int64_t n;
     int b, cnt;
     if (!wave_segment(offsets, N, E, n, b, cnt)) return;
@@ -214,10 +215,11 @@ template <int V, int NT, bool NODE>
 __global__ void __launch_bounds__(64 * kWaves)
 k_att_bwd_dst(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ K, int64_t ldk,
               const int64_t* __restrict__ kidx, int64_t nk, const float* __restrict__ attn,
-              const float* __restrict__ gattn, int64_t E, int H, int Dh, int lgG, float scale,
-              const int32_t* __restrict__ perm, const int32_t* __restrict__ offsets, int64_t N,
-              float* __restrict__ gQ, int64_t ldgq, float* __restrict__ gK, int64_t ldgk,
-              float* __restrict__ glogit) {
+              const float* __restrict__ gattn, int64_t E, int H, int Dh, int lgG,
+              const float* __restrict__ scale_p, const int32_t* __restrict__ perm,
+              const int32_t* __restrict__ offsets, int64_t N, float* __restrict__ gQ, int64_t ldgq,
+              float* __restrict__ gK, int64_t ldgk, float* __restrict__ glogit) {
+    const float scale = *scale_p;
     int64_t n;
     int b, cnt;
     if (!wave_segment(offsets, N, E, n, b, cnt)) return;
@@ -295,8 +297,9 @@ template <int V, int NT>
 __global__ void __launch_bounds__(64 * kWaves)
 k_att_bwd_src(const float* __restrict__ Q, int64_t ldq, const int64_t* __restrict__ qidx,
               int64_t nq, const float* __restrict__ glogit, int64_t E, int H, int Dh, int lgG,
-              float scale, const int32_t* __restrict__ perm, const int32_t* __restrict__ offsets,
-              int64_t NK, float* __restrict__ gK, int64_t ldgk) {
+              const float* __restrict__ scale_p, const int32_t* __restrict__ perm,
+              const int32_t* __restrict__ offsets, int64_t NK, float* __restrict__ gK, int64_t ldgk) {
+    const float scale = *scale_p;
     int64_t n;
     int b, cnt;
     if (!wave_segment(offsets, NK, E, n, b, cnt) || n == NK) return;
@@ -498,9 +501,10 @@ using namespace feq;
 extern "C" int feq_attn_softmax_fwd(const float* Q, int64_t ldq, const float* K, int64_t ldk,
                                     const int64_t* q_idx, const int64_t* k_idx, int64_t num_k,
                                     const float* dist, int64_t num_edges, int32_t heads,
-                                    int32_t head_dim, float scale, float decay,
+                                    int32_t head_dim, const float* scale, float decay,
                                     const int32_t* perm, const int32_t* offsets, int64_t num_nodes,
                                     float* attn, float* qk_out, feq_stream_t stream) {
+    if (!scale) return fail(FEQ_ERR_INVALID, "NULL scale (a device float)");
     if (int rc = check_graph(num_edges, num_nodes)) return rc;
     const bool node = q_idx != nullptr;
     if (node != (k_idx != nullptr)) return fail(FEQ_ERR_INVALID, "q_idx and k_idx must both be given or both be NULL");
@@ -533,11 +537,12 @@ extern "C" int feq_attn_softmax_fwd(const float* Q, int64_t ldq, const float* K,
 extern "C" int feq_attn_softmax_bwd(const float* Q, int64_t ldq, const float* K, int64_t ldk,
                                     const int64_t* q_idx, const int64_t* k_idx, int64_t num_k,
                                     const float* attn, const float* grad_attn, int64_t num_edges,
-                                    int32_t heads, int32_t head_dim, float scale,
+                                    int32_t heads, int32_t head_dim, const float* scale,
                                     const int32_t* perm, const int32_t* offsets, int64_t num_nodes,
                                     const int32_t* perm_k, const int32_t* offsets_k,
                                     float* grad_Q, int64_t ldgq, float* grad_K, int64_t ldgk,
                                     float* grad_logits, feq_stream_t stream) {
+    if (!scale) return fail(FEQ_ERR_INVALID, "NULL scale (a device float)");
     if (int rc = check_graph(num_edges, num_nodes)) return rc;
     const bool node = q_idx != nullptr;
     if (node != (k_idx != nullptr)) return fail(FEQ_ERR_INVALID, "q_idx and k_idx must both be given or both be NULL");

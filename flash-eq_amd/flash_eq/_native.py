@@ -97,9 +97,9 @@ _SIGS = {
     "feq_gather_rows": ([_P, _I64, _I64, _P, _I64, _P, _P], ctypes.c_int),
     "feq_sum_squares_workspace": ([], _SZ),
     "feq_sum_squares": ([_P, _I64, _P, _P, _SZ, _P], ctypes.c_int),
-    "feq_attn_softmax_fwd": ([_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I32, _I32, _F, _F,
+    "feq_attn_softmax_fwd": ([_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I32, _I32, _P, _F,
                               _P, _P, _I64, _P, _P, _P], ctypes.c_int),
-    "feq_attn_softmax_bwd": ([_P, _I64, _P, _I64, _P, _P, _I64, _P, _P, _I64, _I32, _I32, _F,
+    "feq_attn_softmax_bwd": ([_P, _I64, _P, _I64, _P, _P, _I64, _P, _P, _I64, _I32, _I32, _P,
                               _P, _P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _P], ctypes.c_int),
     "feq_attn_pool_fwd": ([_P, _P, _I64, _I32, _I32, _I32, _P, _P, _I64, _P, _P], ctypes.c_int),
     "feq_attn_pool_bwd": ([_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P],

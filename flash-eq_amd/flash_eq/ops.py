@@ -510,14 +510,14 @@ class EdgeSoftmaxFn(torch.autograd.Function):
         E, H, Dh = Qs.shape
         if Ks.shape != Qs.shape:
             raise ValueError(f"Q and K shapes differ: {tuple(Qs.shape)} and {tuple(Ks.shape)}")
-        scale_t = log_scale.detach().float().exp()
+        scale_t = log_scale.detach().float().exp().reshape(1).contiguous()   # read by the kernels
         rs = _f32(dist, "distances") if (dist is not None and decay > 0) else None
         attn = torch.empty(E, H, dtype=torch.float32, device=dev)
         qk = torch.empty(E, H, dtype=torch.float32, device=dev)
         if E:
             with torch.cuda.device(dev):
                 rc = N.lib().feq_attn_softmax_fwd(N.ptr(Qs), H * Dh, N.ptr(Ks), H * Dh, None, None,
-                                                  E, N.ptr(rs), E, H, Dh, _host_scalar(scale_t),
+                                                  E, N.ptr(rs), E, H, Dh, N.ptr(scale_t),
                                                   float(decay), N.ptr(perm), N.ptr(offsets),
                                                   num_nodes, N.ptr(attn), N.ptr(qk),
                                                   N.stream_ptr(dev))
@@ -542,7 +542,7 @@ class EdgeSoftmaxFn(torch.autograd.Function):
             with torch.cuda.device(dev):
                 rc = N.lib().feq_attn_softmax_bwd(N.ptr(Qs), H * Dh, N.ptr(Ks), H * Dh, None, None,
                                                   E, N.ptr(attn), N.ptr(ga), E, H, Dh,
-                                                  _host_scalar(scale_t), N.ptr(perm),
+                                                  N.ptr(scale_t), N.ptr(perm),
                                                   N.ptr(offsets), num_nodes, None, None,
                                                   N.ptr(gQ), H * Dh, N.ptr(gK), H * Dh,
                                                   N.ptr(glog), N.stream_ptr(dev))
@@ -582,7 +582,7 @@ class NodeSoftmaxFn(torch.autograd.Function):
             raise ValueError(f"qk must be (N, 2*mult, dim) with heads | mult, got {tuple(qs.shape)}")
         E = src.shape[0]
         Dh, ld = mult // heads * dim, two_mult * dim
-        scale_t = log_scale.detach().float().exp()
+        scale_t = log_scale.detach().float().exp().reshape(1).contiguous()   # read by the kernels
         rs = _f32(dist, "distances") if (dist is not None and decay > 0) else None
         attn = torch.empty(E, heads, dtype=torch.float32, device=dev)
         qkv = torch.empty(E, heads, dtype=torch.float32, device=dev)
@@ -590,7 +590,7 @@ class NodeSoftmaxFn(torch.autograd.Function):
             with torch.cuda.device(dev):
                 rc = N.lib().feq_attn_softmax_fwd(N.ptr(qs), ld, N.ptr(qs) + 4 * mult * dim, ld,
                                                   N.ptr(dst), N.ptr(src), Nn, N.ptr(rs), E, heads,
-                                                  Dh, _host_scalar(scale_t), float(decay),
+                                                  Dh, N.ptr(scale_t), float(decay),
                                                   N.ptr(perm), N.ptr(offsets), num_nodes,
                                                   N.ptr(attn), N.ptr(qkv), N.stream_ptr(dev))
             N.check(rc, "feq_attn_softmax_fwd")
@@ -615,7 +615,7 @@ class NodeSoftmaxFn(torch.autograd.Function):
         with torch.cuda.device(dev):
             rc = N.lib().feq_attn_softmax_bwd(N.ptr(qs), ld, N.ptr(qs) + 4 * mult * dim, ld,
                                               N.ptr(dst), N.ptr(src), Nn, N.ptr(attn), N.ptr(ga),
-                                              E, heads, Dh, _host_scalar(scale_t), N.ptr(perm),
+                                              E, heads, Dh, N.ptr(scale_t), N.ptr(perm),
                                               N.ptr(offsets), num_nodes, N.ptr(perm_s),
                                               N.ptr(offsets_s), N.ptr(gqk), ld,
                                               N.ptr(gqk) + 4 * mult * dim, ld, N.ptr(glog),
@@ -623,12 +623,6 @@ class NodeSoftmaxFn(torch.autograd.Function):
         N.check(rc, "feq_attn_softmax_bwd")
         g_dist, g_log = _softmax_scalar_grads(glog, qkv, need[1], need[2], decay, rdt, ldt)
         return (gqk.to(qdt), g_dist, g_log, None, None, None, None, None, None, None, None, None)
-
-
-def _host_scalar(t: torch.Tensor) -> float:
-    # The kernels take the softmax temperature by value; reading the
-    # one-element parameter is the only host synchronisation of the attention.
-    return float(t)
 
 
 class AttnPoolFn(torch.autograd.Function):

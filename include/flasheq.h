@@ -228,6 +228,8 @@ int feq_edgewise_hl_bwd(const feq_layout* layout, const feq_binning* binning, in
  *     an index outside [0, num_k) reads a zero row) -- the gathers of
  *     attention.py:298-304 done inside the kernels.
  * logits[e,h] = scale <Q_h, K_h> - dist[e]/decay (decay <= 0: no decay term);
+ * scale is a device pointer to one float (exp(log_scale), attention.py:95-96),
+ * read by the kernels, so no host synchronisation is needed to pass it;
  * attn = per-destination softmax with max shift and +1e-8 in the denominator
  * (attention.py:92-141).  qk_out (E, heads; nullable) receives scale <Q_h, K_h>.
  * Limit: head_dim <= 16 * V * 64 / NG, NG = next power of two >= heads (at most
@@ -235,8 +237,9 @@ int feq_edgewise_hl_bwd(const feq_layout* layout, const feq_binning* binning, in
 int feq_attn_softmax_fwd(const float* Q, int64_t ldq, const float* K, int64_t ldk,
                          const int64_t* q_idx, const int64_t* k_idx, int64_t num_k,
                          const float* dist, int64_t num_edges, int32_t heads, int32_t head_dim,
-                         float scale, float decay, const int32_t* perm, const int32_t* offsets,
-                         int64_t num_nodes, float* attn, float* qk_out, feq_stream_t stream);
+                         const float* scale, float decay, const int32_t* perm,
+                         const int32_t* offsets, int64_t num_nodes, float* attn, float* qk_out,
+                         feq_stream_t stream);
 /* Given grad_attn (E, heads): grad_logits (E, heads) = attn (grad_attn - S), S the
  * per-destination sum of attn*grad_attn (the caller forms the log-scale gradient
  * sum(grad_logits*qk) and the distance gradient -sum_h grad_logits/decay from it).
@@ -246,7 +249,7 @@ int feq_attn_softmax_fwd(const float* Q, int64_t ldq, const float* K, int64_t ld
 int feq_attn_softmax_bwd(const float* Q, int64_t ldq, const float* K, int64_t ldk,
                          const int64_t* q_idx, const int64_t* k_idx, int64_t num_k,
                          const float* attn, const float* grad_attn, int64_t num_edges,
-                         int32_t heads, int32_t head_dim, float scale, const int32_t* perm,
+                         int32_t heads, int32_t head_dim, const float* scale, const int32_t* perm,
                          const int32_t* offsets, int64_t num_nodes, const int32_t* perm_k,
                          const int32_t* offsets_k, float* grad_Q, int64_t ldgq, float* grad_K,
                          int64_t ldgk, float* grad_logits, feq_stream_t stream);
