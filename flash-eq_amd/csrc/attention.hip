@@ -546,7 +546,10 @@ extern "C" int feq_attn_softmax_bwd(const float* Q, int64_t ldq, const float* K,
     if (int rc = check_graph(num_edges, num_nodes)) return rc;
     const bool node = q_idx != nullptr;
     if (node != (k_idx != nullptr)) return fail(FEQ_ERR_INVALID, "q_idx and k_idx must both be given or both be NULL");
-    if (node && (num_k < 1 || !perm_k || !offsets_k))
+    // node form: grad_Q gets one row per destination segment (num_nodes rows),
+    // grad_K one row per segment of the CSR by k_idx (num_k rows, offsets_k has
+    // num_k + 1 entries); rows without edges are written as zeros
+    if (node && (num_k < 1 || !offsets_k || (num_edges > 0 && !perm_k)))
         return fail(FEQ_ERR_INVALID, "the node form needs the CSR of the edges by k_idx");
     const int64_t row = static_cast<int64_t>(heads) * head_dim;
     if (ldq < row || ldk < row || ldgq < row || ldgk < row)

@@ -68,6 +68,17 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// The per-node statistics of the norms (means, variances, their gradient
+// sums) are formed in float64: a LayerNorm output near zero is v - mu, and a
+// float32 mu leaves it with an absolute error of ~1e-7, which the next norm's
+// 1/|v| (an EquivariantLayerNorm of a scalar irrep) turns into relative errors
+// of 1e-4 and more downstream.  The elements stay float32 in memory.
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
 // Orders a wave's LDS writes before its other lanes' reads.
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -111,28 +122,30 @@ k_sepnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __re
     for (int j = 0; j < kMaxS; ++j) {
         if (j >= L.ns) break;
         const int d = L.spos[j];
-        float v[CPL];
-        float s = 0.0f;
+        double v[CPL];
+        double s = 0.0;
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
             const int c = lane + 64 * i;
             v[i] = c < L.mult ? xn[c * L.dim + d] : 0.0f;
             s += v[i];
         }
-        const float mu = wave_sum(s) / fm;
-        float q = 0.0f;
+        const double mu = wave_sum(s) / fm;
+        double q = 0.0;
 #pragma unroll
         for (int i = 0; i < CPL; ++i)
             if (lane + 64 * i < L.mult) q += (v[i] - mu) * (v[i] - mu);
-        const float den = sqrtf(wave_sum(q) / fm) + eps;
+        const double den = sqrt(wave_sum(q) / fm) + eps;
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
             const int c = lane + 64 * i;
-            if (c < L.mult) yn[c * L.dim + d] = (v[i] - mu) / den * ws[c * L.ns + j] + bs[c * L.ns + j];
+            if (c < L.mult)
+                yn[c * L.dim + d] = static_cast<float>((v[i] - mu) / den * ws[c * L.ns + j] +
+                                                       bs[c * L.ns + j]);
         }
     }
     if (L.nhc > 0) {  // w_h is NULL without l > 0 irreps
-        float h = 0.0f;
+        double h = 0.0;
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
             const int c = lane + 64 * i;
@@ -140,17 +153,17 @@ k_sepnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __re
             for (int k = 0; k < L.nreps; ++k) {
                 if (L.deg[k] == 0) continue;
                 for (int d = L.off[k]; d < L.off[k + 1]; ++d) {
-                    const float v = xn[c * L.dim + d];
+                    const double v = xn[c * L.dim + d];
                     h += v * v;
                 }
             }
         }
-        const float rms = sqrtf(wave_sum(h) / (fm * L.nhc) + eps);
+        const double rms = sqrt(wave_sum(h) / (fm * L.nhc) + eps);
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
             const int c = lane + 64 * i;
             if (c >= L.mult) continue;
-            const float f = wh[c] / rms;
+            const float f = static_cast<float>(wh[c] / rms);
             for (int k = 0; k < L.nreps; ++k) {
                 if (L.deg[k] == 0) continue;
                 for (int d = L.off[k]; d < L.off[k + 1]; ++d) yn[c * L.dim + d] = xn[c * L.dim + d] * f;
@@ -205,66 +218,68 @@ k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __r
         for (int j = 0; j < kMaxS; ++j) {
             if (j >= L.ns) break;
             const int d = L.spos[j];
-            float v[CPL], gp[CPL], g[CPL];
-            float s = 0.0f;
+            double v[CPL], gp[CPL];
+            float g[CPL];
+            double s = 0.0;
 #pragma unroll
             for (int i = 0; i < CPL; ++i) {
                 const int c = lane + 64 * i;
                 const bool ok = c < L.mult;
                 v[i] = ok ? xn[c * L.dim + d] : 0.0f;
                 g[i] = ok ? gn[c * L.dim + d] : 0.0f;
-                gp[i] = ok ? g[i] * ws[c * L.ns + j] : 0.0f;
+                gp[i] = ok ? static_cast<double>(g[i]) * ws[c * L.ns + j] : 0.0;
                 s += v[i];
             }
-            const float mu = wave_sum(s) / fm;
-            float q = 0.0f, sg = 0.0f, sgv = 0.0f;
+            const double mu = wave_sum(s) / fm;
+            double q = 0.0, sg = 0.0, sgv = 0.0;
 #pragma unroll
             for (int i = 0; i < CPL; ++i) {
                 if (lane + 64 * i >= L.mult) continue;
-                const float t = v[i] - mu;
+                const double t = v[i] - mu;
                 q += t * t;
                 sg += gp[i];
                 sgv += gp[i] * t;
             }
-            const float sd = sqrtf(wave_sum(q) / fm);
-            const float mg = wave_sum(sg) / fm;
+            const double sd = sqrt(wave_sum(q) / fm);
+            const double mg = wave_sum(sg) / fm;
             sgv = wave_sum(sgv);
-            const float den = sd + eps;
-            const float coef = sd > 0.0f ? sgv / (fm * sd * den * den) : 0.0f;
+            const double den = sd + eps;
+            const double coef = sd > 0.0 ? sgv / (fm * sd * den * den) : 0.0;
 #pragma unroll
             for (int i = 0; i < CPL; ++i) {
                 const int c = lane + 64 * i;
                 if (c >= L.mult) continue;
-                const float t = v[i] - mu;
-                on[c * L.dim + d] = (gp[i] - mg) / den - coef * t;
-                aS[i][j] += g[i] * (t / den);
+                const double t = v[i] - mu;
+                on[c * L.dim + d] = static_cast<float>((gp[i] - mg) / den - coef * t);
+                aS[i][j] += g[i] * static_cast<float>(t / den);
                 aB[i][j] += g[i];
             }
         }
         if (L.nhc > 0) {  // w_h is NULL without l > 0 irreps
-            float h = 0.0f, S = 0.0f;
+            double h = 0.0, S = 0.0;
 #pragma unroll
             for (int i = 0; i < CPL; ++i) {
                 const int c = lane + 64 * i;
                 if (c >= L.mult) continue;
-                float t = 0.0f;
+                double t = 0.0;
                 for (int k = 0; k < L.nreps; ++k) {
                     if (L.deg[k] == 0) continue;
                     for (int d = L.off[k]; d < L.off[k + 1]; ++d) {
-                        const float v = xn[c * L.dim + d];
+                        const double v = xn[c * L.dim + d];
                         h += v * v;
                         t += gn[c * L.dim + d] * v;
                     }
                 }
                 S += t * wh[c];
             }
-            const float rms = sqrtf(wave_sum(h) / cnt + eps);
-            const float k2 = wave_sum(S) / (cnt * rms * rms * rms);
+            const double rms_d = sqrt(wave_sum(h) / cnt + eps);
+            const float rms = static_cast<float>(rms_d);
+            const float k2 = static_cast<float>(wave_sum(S) / (cnt * rms_d * rms_d * rms_d));
 #pragma unroll
             for (int i = 0; i < CPL; ++i) {
                 const int c = lane + 64 * i;
                 if (c >= L.mult) continue;
-                const float a = wh[c] / rms;
+                const float a = static_cast<float>(wh[c] / rms_d);
                 float t = 0.0f;
                 for (int k = 0; k < L.nreps; ++k) {
                     if (L.deg[k] == 0) continue;
@@ -321,32 +336,35 @@ k_eqnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __res
     const float fm = static_cast<float>(L.mult);
     for (int k = 0; k < L.nreps; ++k) {
         const int d0 = L.off[k], d1 = L.off[k + 1];
-        float nr[CPL];
-        float s = 0.0f;
+        double nr[CPL];
+        double s = 0.0;
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
             const int c = lane + 64 * i;
-            float q = 0.0f;
+            double q = 0.0;
             if (c < L.mult)
-                for (int d = d0; d < d1; ++d) q += xn[c * L.dim + d] * xn[c * L.dim + d];
-            nr[i] = sqrtf(q + eps);
+                for (int d = d0; d < d1; ++d) {
+                    const double v = xn[c * L.dim + d];
+                    q += v * v;
+                }
+            nr[i] = sqrt(q + eps);
             if (c < L.mult) s += nr[i];
         }
-        float mu = 0.0f, rstd = 0.0f;
+        double mu = 0.0, rstd = 0.0;
         if (w) {
             mu = wave_sum(s) / fm;
-            float q = 0.0f;
+            double q = 0.0;
 #pragma unroll
             for (int i = 0; i < CPL; ++i)
                 if (lane + 64 * i < L.mult) q += (nr[i] - mu) * (nr[i] - mu);
-            rstd = 1.0f / sqrtf(wave_sum(q) / fm + ln_eps);
+            rstd = 1.0 / sqrt(wave_sum(q) / fm + ln_eps);
         }
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
             const int c = lane + 64 * i;
             if (c >= L.mult) continue;
-            const float f = w ? ((nr[i] - mu) * rstd * w[c] + b[c]) / (nr[i] + eps)
-                              : 1.0f / (nr[i] + eps);
+            const float f = static_cast<float>(w ? ((nr[i] - mu) * rstd * w[c] + b[c]) / (nr[i] + eps)
+                                                 : 1.0 / (nr[i] + eps));
             for (int d = d0; d < d1; ++d) yn[c * L.dim + d] = xn[c * L.dim + d] * f;
         }
     }
@@ -388,42 +406,43 @@ k_eqnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __re
         float* on = STAGE ? sg : gx + n * row;
         for (int k = 0; k < L.nreps; ++k) {
             const int d0 = L.off[k], d1 = L.off[k + 1];
-            float nr[CPL], df[CPL];
-            float s = 0.0f;
+            double nr[CPL], df[CPL];
+            double s = 0.0;
 #pragma unroll
             for (int i = 0; i < CPL; ++i) {
                 const int c = lane + 64 * i;
-                float q = 0.0f, t = 0.0f;
+                double q = 0.0, t = 0.0;
                 if (c < L.mult)
                     for (int d = d0; d < d1; ++d) {
-                        const float v = xn[c * L.dim + d];
+                        const double v = xn[c * L.dim + d];
                         q += v * v;
                         t += gn[c * L.dim + d] * v;
                     }
-                nr[i] = sqrtf(q + eps);
+                nr[i] = sqrt(q + eps);
                 df[i] = t;
                 if (c < L.mult) s += nr[i];
             }
-            float fac[CPL], dn[CPL];
+            float fac[CPL];
+            double dn[CPL];
             if (w) {
-                const float mu = wave_sum(s) / fm;
-                float q = 0.0f;
+                const double mu = wave_sum(s) / fm;
+                double q = 0.0;
 #pragma unroll
                 for (int i = 0; i < CPL; ++i)
                     if (lane + 64 * i < L.mult) q += (nr[i] - mu) * (nr[i] - mu);
-                const float rstd = 1.0f / sqrtf(wave_sum(q) / fm + ln_eps);
-                float nh[CPL], dnh[CPL], dln[CPL];
-                float m1 = 0.0f, m2 = 0.0f;
+                const double rstd = 1.0 / sqrt(wave_sum(q) / fm + ln_eps);
+                double nh[CPL], dnh[CPL], dln[CPL];
+                double m1 = 0.0, m2 = 0.0;
 #pragma unroll
                 for (int i = 0; i < CPL; ++i) {
                     const int c = lane + 64 * i;
                     const bool ok = c < L.mult;
-                    const float den = nr[i] + eps;
+                    const double den = nr[i] + eps;
                     nh[i] = (nr[i] - mu) * rstd;
-                    const float ln = ok ? nh[i] * w[c] + b[c] : 0.0f;
-                    fac[i] = ln / den;
+                    const double ln = ok ? nh[i] * w[c] + b[c] : 0.0;
+                    fac[i] = static_cast<float>(ln / den);
                     dln[i] = df[i] / den;
-                    dnh[i] = ok ? dln[i] * w[c] : 0.0f;
+                    dnh[i] = ok ? dln[i] * w[c] : 0.0;
                     dn[i] = -df[i] * ln / (den * den);
                     if (ok) {
                         m1 += dnh[i];
@@ -436,15 +455,15 @@ k_eqnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __re
                 for (int i = 0; i < CPL; ++i) {
                     dn[i] += rstd * (dnh[i] - m1 - nh[i] * m2);
                     if (lane + 64 * i < L.mult) {
-                        aW[i] += dln[i] * nh[i];
-                        aB[i] += dln[i];
+                        aW[i] += static_cast<float>(dln[i] * nh[i]);
+                        aB[i] += static_cast<float>(dln[i]);
                     }
                 }
             } else {
 #pragma unroll
                 for (int i = 0; i < CPL; ++i) {
-                    const float den = nr[i] + eps;
-                    fac[i] = 1.0f / den;
+                    const double den = nr[i] + eps;
+                    fac[i] = static_cast<float>(1.0 / den);
                     dn[i] = -df[i] / (den * den);
                 }
             }
@@ -452,7 +471,7 @@ k_eqnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __re
             for (int i = 0; i < CPL; ++i) {
                 const int c = lane + 64 * i;
                 if (c >= L.mult) continue;
-                const float r = dn[i] / nr[i];
+                const float r = static_cast<float>(dn[i] / nr[i]);
                 for (int d = d0; d < d1; ++d)
                     on[c * L.dim + d] = gn[c * L.dim + d] * fac[i] + xn[c * L.dim + d] * r;
             }

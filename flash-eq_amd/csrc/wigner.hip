@@ -18,6 +18,7 @@
 
 #include <cfloat>
 #include <cmath>
+#include <type_traits>
 
 namespace feq {
 namespace {
@@ -126,6 +127,9 @@ struct EdgeFrame {
 // Workgroup: a tile of EPB edges; thread t computes standard column c0 = t % dim
 // of edge t / dim into an LDS tile of the edges' M = D[:, perm] matrices, which
 // is then written with coalesced stores.
+// LMAX: the largest degree the launch handles (the register footprint of the
+// per-column vectors grows with it, so small representations get a small kernel).
+template <int LMAX>
 __global__ void __launch_bounds__(256)
 k_wigner(WignerArgs A, int epb, const double* __restrict__ plan, const int32_t* __restrict__ perm,
          int64_t E, const float* __restrict__ dirs, float* __restrict__ out) {
@@ -168,7 +172,9 @@ k_wigner(WignerArgs A, int epb, const double* __restrict__ plan, const int32_t* 
         float* dst = sM + el * dd + base * dim + sInv[c0];   // rows base.., column j
         switch (l) {
 #define FEQ_WCASE(LL) \
-    case LL: column_into<LL>(V, c, f.phi, f.ang, f.ident, dst, dim); break;
+    case LL:                                                                             \
+        if constexpr (LL <= LMAX) column_into<LL>(V, c, f.phi, f.ang, f.ident, dst, dim); \
+        break;
             FEQ_WCASE(0) FEQ_WCASE(1) FEQ_WCASE(2) FEQ_WCASE(3) FEQ_WCASE(4) FEQ_WCASE(5)
             FEQ_WCASE(6) FEQ_WCASE(7) FEQ_WCASE(8) FEQ_WCASE(9) FEQ_WCASE(10) FEQ_WCASE(11)
             FEQ_WCASE(12) FEQ_WCASE(13) FEQ_WCASE(14) FEQ_WCASE(15) FEQ_WCASE(16)
@@ -179,6 +185,258 @@ k_wigner(WignerArgs A, int epb, const double* __restrict__ plan, const int32_t* 
     __syncthreads();
     float* o = out + e0 * dd;
     for (int q = threadIdx.x; q < ne * dd; q += blockDim.x) o[q] = sM[q];
+}
+
+// ---- backward: gradient with respect to the edge directions --------------------------
+//
+// With X(phi) = cos(phi) G0 + sin(phi) G1 = Z(phi) V G2 V^T Z(-phi) and the
+// exponent theta (a0 G0 + a1 G1) = ang X(phi) (a = rho (cos phi, sin phi),
+// ang = theta rho), the derivatives of D = exp(ang X(phi)) are exact and cheap:
+//     dD/dang = X D,        dD/dphi = G2 D - D G2
+// (phi enters as a conjugation by the z-rotation Z(phi) = exp(phi G2)).  Each
+// thread takes one column c of an irrep block of D and adds, with G = dL/dD
+// (the columns of dL/dM moved back through perm):
+//     <G[:,c], X D[:,c]>                                 to dL/dang,
+//     <G[:,c], G2 D[:,c]> - z_c <G[:,pc], D[:,c]>        to dL/dphi
+// (z_c = L - c: G2's coupling of row c to its partner row pc = n-1-c).  At
+// rho = 0 (the forward's D = I) the exponent is theta (a0 G0 + a1 G1) at a = 0,
+// whose derivative is dD/da_k = theta G_k: the threads add <G[:,c], G_k e_c>.
+// One thread per edge then chains (phi, ang) -- or (a0, a1) -- back through
+// a = a_raw/(|a_raw|+eps), a_raw = (-d_y, d_x), theta = acos(d_z) and
+// d = v/(|v|+eps), the operations of rot_to_ez (wigner.py:220-238), with
+// torch's conventions (the norm's gradient is 0 at 0).
+
+// out = X(phi) y for one irrep: Z(phi) V G2 V^T Z(-phi) y, with cos(q phi),
+// sin(q phi) for q = 0..L in cpm, spm.
+template <int L>
+__device__ __forceinline__ void apply_axis_generator(const double* __restrict__ V,
+                                                     const double (&cpm)[L + 1],
+                                                     const double (&spm)[L + 1],
+                                                     const double (&y)[2 * L + 1],
+                                                     double (&out)[2 * L + 1]) {
+    constexpr int n = 2 * L + 1;
+    double u[n], w[n], x[n];
+    // u = Z(-phi) y
+#pragma unroll
+    for (int r = 0; r < n; ++r) {
+        const int m = L - r, am = m < 0 ? -m : m;
+        u[r] = cpm[am] * y[r] - (r != L ? (m < 0 ? -spm[am] : spm[am]) * y[n - 1 - r] : 0.0);
+    }
+    // w = V^T u
+#pragma unroll
+    for (int q = 0; q < n; ++q) {
+        double acc = 0.0;
+#pragma unroll
+        for (int r = 0; r < n; ++r) acc += V[r * n + q] * u[r];
+        w[q] = acc;
+    }
+    // w <- G2 w: (G2 w)[r] = (L - r) w[n-1-r]
+#pragma unroll
+    for (int r = 0; r < n; ++r) u[r] = static_cast<double>(L - r) * w[n - 1 - r];
+    // x = V u
+#pragma unroll
+    for (int r = 0; r < n; ++r) {
+        double acc = 0.0;
+#pragma unroll
+        for (int q = 0; q < n; ++q) acc += V[r * n + q] * u[q];
+        x[r] = acc;
+    }
+    // out = Z(phi) x
+#pragma unroll
+    for (int r = 0; r < n; ++r) {
+        const int m = L - r, am = m < 0 ? -m : m;
+        out[r] = cpm[am] * x[r] + (r != L ? (m < 0 ? -spm[am] : spm[am]) * x[n - 1 - r] : 0.0);
+    }
+}
+
+template <int L>
+__device__ __forceinline__ void multiples(double ang, double (&c)[L + 1], double (&s)[L + 1]) {
+    c[0] = 1.0;
+    s[0] = 0.0;
+    if (L == 0) return;
+    double s1, c1;
+    sincos(ang, &s1, &c1);
+#pragma unroll
+    for (int q = 1; q <= L; ++q) {
+        c[q] = c[q - 1] * c1 - s[q - 1] * s1;
+        s[q] = s[q - 1] * c1 + c[q - 1] * s1;
+    }
+}
+
+// Contributions of column c of one irrep block.  gcol / gpar: columns c and
+// n-1-c of dL/dD restricted to the block's rows.  t0/t1: (dL/dang, dL/dphi), or
+// at rho = 0 (ident) (dL/da0, dL/da1) without the factor theta.
+template <int L>
+__device__ __forceinline__ void column_grad(const double* V, int c, double phi, double ang,
+                                            bool ident, const float* gcol, const float* gpar,
+                                            int stride, double& t0, double& t1) {
+    constexpr int n = 2 * L + 1;
+    t0 = 0.0;
+    t1 = 0.0;
+    if (L == 0) return;                       // D = 1 is constant
+    double g[n], gp[n], y[n], xy[n];
+#pragma unroll
+    for (int r = 0; r < n; ++r) {
+        g[r] = gcol[r * stride];
+        gp[r] = gpar[r * stride];
+    }
+    if (ident) {
+        double cz[L + 1], sz[L + 1], c9[L + 1], s9[L + 1];
+        multiples<L>(0.0, cz, sz);
+        multiples<L>(0.5 * M_PI, c9, s9);
+#pragma unroll
+        for (int r = 0; r < n; ++r) y[r] = r == c ? 1.0 : 0.0;
+        apply_axis_generator<L>(V, cz, sz, y, xy);      // G0 e_c
+#pragma unroll
+        for (int r = 0; r < n; ++r) t0 += g[r] * xy[r];
+        apply_axis_generator<L>(V, c9, s9, y, xy);      // G1 e_c
+#pragma unroll
+        for (int r = 0; r < n; ++r) t1 += g[r] * xy[r];
+        return;
+    }
+    wigner_column<L>(V, c, phi, ang, y);
+    double cp[L + 1], sp[L + 1];
+    multiples<L>(phi, cp, sp);
+    apply_axis_generator<L>(V, cp, sp, y, xy);
+#pragma unroll
+    for (int r = 0; r < n; ++r) {
+        t0 += g[r] * xy[r];
+        t1 += g[r] * static_cast<double>(L - r) * y[n - 1 - r] - static_cast<double>(L - c) * gp[r] * y[r];
+    }
+}
+
+template <int LMAX>
+__global__ void __launch_bounds__(256)
+k_wigner_bwd(WignerArgs A, int epb, const double* __restrict__ plan, const int32_t* __restrict__ perm,
+             int64_t E, const float* __restrict__ dirs, const float* __restrict__ gM,
+             float* __restrict__ gdirs) {
+    extern __shared__ float sG[];                      // epb x dim x dim (dL/dM tile)
+    __shared__ EdgeFrame sFr[256];
+    __shared__ int sInv[FEQ_MAX_SLOTS];
+    __shared__ double sT0[256], sT1[256];
+    const int dim = A.dim, dd = dim * dim;
+    const int64_t e0 = static_cast<int64_t>(blockIdx.x) * epb;
+    const int ne = static_cast<int>(E - e0 < epb ? E - e0 : epb);
+    const float* gsrc = gM + e0 * dd;
+    for (int q = threadIdx.x; q < ne * dd; q += blockDim.x) sG[q] = gsrc[q];
+    for (int j = threadIdx.x; j < dim; j += blockDim.x) sInv[perm[j]] = j;
+    // The frame in double from the float32 directions: near the poles (|d_z| -> 1)
+    // d theta / d d_z = -1/sqrt(1 - d_z^2) amplifies the float32 rounding of d_z
+    // (1 - |d_z| = 3e-6 loses 2% to it), while the forward's matrices are
+    // insensitive to it; the gradient is therefore formed from an exact frame.
+    double dxv = 0.0, dyv = 0.0, dzv = 0.0, nvv = 0.0, nav = 0.0, a0v = 0.0, a1v = 0.0, thv = 0.0;
+    const double eps = 1e-8;
+    if (threadIdx.x < ne) {
+        const int64_t e = e0 + threadIdx.x;
+        const double vx = dirs[3 * e], vy = dirs[3 * e + 1], vz = dirs[3 * e + 2];
+        nvv = sqrt(vx * vx + vy * vy + vz * vz);
+        const double nv = nvv + eps;
+        dxv = vx / nv;
+        dyv = vy / nv;
+        dzv = vz / nv;
+        const double a0r = -dyv, a1r = dxv;
+        nav = sqrt(a0r * a0r + a1r * a1r);
+        const double na = nav + eps;
+        a0v = a0r / na;
+        a1v = a1r / na;
+        thv = acos(fmin(fmax(dzv, -1.0), 1.0));
+        const double rho = sqrt(a0v * a0v + a1v * a1v);
+        EdgeFrame f;
+        f.ident = rho == 0.0;
+        f.phi = f.ident ? 0.0 : atan2(a1v, a0v);
+        f.ang = thv * rho;
+        sFr[threadIdx.x] = f;
+    }
+    __syncthreads();
+    const int el = threadIdx.x / dim;
+    double t0 = 0.0, t1 = 0.0;
+    if (el < ne) {
+        const int c0 = threadIdx.x % dim;
+        int k = 0;
+        while (k + 1 < A.nirr && c0 >= A.off[k + 1]) ++k;
+        const int l = A.lvals[k], base = A.off[k], c = c0 - base, n = 2 * l + 1;
+        const double* V = plan + A.plan_off[k];
+        const EdgeFrame f = sFr[el];
+        // column c of dL/dD is column sInv[c] of dL/dM; rows base.. of the block
+        const float* gcol = sG + el * dd + base * dim + sInv[c0];
+        const float* gpar = sG + el * dd + base * dim + sInv[base + n - 1 - c];
+        switch (l) {
+#define FEQ_WCASE(LL)                                                                    \
+    case LL:                                                                             \
+        if constexpr (LL <= LMAX)                                                        \
+            column_grad<LL>(V, c, f.phi, f.ang, f.ident, gcol, gpar, dim, t0, t1);       \
+        break;
+            FEQ_WCASE(0) FEQ_WCASE(1) FEQ_WCASE(2) FEQ_WCASE(3) FEQ_WCASE(4) FEQ_WCASE(5)
+            FEQ_WCASE(6) FEQ_WCASE(7) FEQ_WCASE(8) FEQ_WCASE(9) FEQ_WCASE(10) FEQ_WCASE(11)
+            FEQ_WCASE(12) FEQ_WCASE(13) FEQ_WCASE(14) FEQ_WCASE(15) FEQ_WCASE(16)
+#undef FEQ_WCASE
+            default: break;
+        }
+    }
+    sT0[threadIdx.x] = t0;
+    sT1[threadIdx.x] = t1;
+    __syncthreads();
+    if (threadIdx.x >= ne) return;
+    // per edge: sum the columns in a fixed order, then the chain rule
+    double s0 = 0.0, s1 = 0.0;
+    for (int q = 0; q < dim; ++q) {
+        s0 += sT0[threadIdx.x * dim + q];
+        s1 += sT1[threadIdx.x * dim + q];
+    }
+    const EdgeFrame f = sFr[threadIdx.x];
+    const double th = thv, a0 = a0v, a1 = a1v;
+    double ga0, ga1, gth;
+    if (f.ident) {
+        ga0 = th * s0;
+        ga1 = th * s1;
+        gth = 0.0;                            // the exponent theta * (a . G) vanishes with a
+    } else {
+        const double rho = sqrt(a0 * a0 + a1 * a1);
+        const double cph = a0 / rho, sph = a1 / rho;
+        const double grho = th * s0;          // ang = theta rho
+        gth = rho * s0;
+        ga0 = cph * grho - sph / rho * s1;
+        ga1 = sph * grho + cph / rho * s1;
+    }
+    // a = a_raw / (|a_raw| + eps), a_raw = (-d_y, d_x)
+    const double ar0 = -dyv, ar1 = dxv, na = nav, ta = na + eps;
+    double gr0 = ga0 / ta, gr1 = ga1 / ta;
+    if (na > 0.0) {
+        const double dotp = (ga0 * ar0 + ga1 * ar1) / (na * ta * ta);
+        gr0 -= dotp * ar0;
+        gr1 -= dotp * ar1;
+    }
+    double gd0 = gr1, gd1 = -gr0, gd2 = 0.0;
+    // theta = acos(clamp(d_z, -1, 1)): -1/sqrt(1 - d_z^2), passed through the clamp
+    const double dz = dzv;
+    if (gth != 0.0) gd2 = -gth / sqrt(1.0 - dz * dz);
+    // d = v / (|v| + eps)
+    const int64_t e = e0 + threadIdx.x;
+    const double vx = dirs[3 * e], vy = dirs[3 * e + 1], vz = dirs[3 * e + 2];
+    const double nv = nvv, tv = nv + eps;
+    double gv0 = gd0 / tv, gv1 = gd1 / tv, gv2 = gd2 / tv;
+    if (nv > 0.0) {
+        const double dotv = (gd0 * vx + gd1 * vy + gd2 * vz) / (nv * tv * tv);
+        gv0 -= dotv * vx;
+        gv1 -= dotv * vy;
+        gv2 -= dotv * vz;
+    }
+    gdirs[3 * e] = static_cast<float>(gv0);
+    gdirs[3 * e + 1] = static_cast<float>(gv1);
+    gdirs[3 * e + 2] = static_cast<float>(gv2);
+}
+
+// Calls f with std::integral_constant<int, LMAX> for the smallest compiled LMAX
+// that covers every degree of A.
+template <class Fn>
+int with_lmax(const WignerArgs& A, Fn&& f) {
+    int lmax = 0;
+    for (int i = 0; i < A.nirr; ++i) lmax = A.lvals[i] > lmax ? A.lvals[i] : lmax;
+    if (lmax <= 2) return f(std::integral_constant<int, 2>{});
+    if (lmax <= 4) return f(std::integral_constant<int, 4>{});
+    if (lmax <= 6) return f(std::integral_constant<int, 6>{});
+    if (lmax <= 10) return f(std::integral_constant<int, 10>{});
+    return f(std::integral_constant<int, 16>{});
 }
 
 }  // namespace
@@ -222,7 +480,45 @@ extern "C" int feq_wigner_basis(const int32_t* lvals, int32_t n, const double* p
     const int epb = 256 / dim;
     const size_t lds = sizeof(float) * static_cast<size_t>(epb) * dim * dim;
     if (lds > 64 * 1024) return fail(FEQ_ERR_UNSUPPORTED, "representation dimension %d too large", dim);
-    FEQ_LAUNCH("k_wigner", k_wigner, dim3(ceil_div(E, epb)), dim3(256), lds, stream_of(stream), A,
-               epb, plan, perm, E, dirs, out);
-    return FEQ_OK;
+    return with_lmax(A, [&](auto LL) -> int {
+        auto kern = k_wigner<decltype(LL)::value>;
+        FEQ_LAUNCH("k_wigner", kern, dim3(ceil_div(E, epb)), dim3(256), lds, stream_of(stream), A,
+                   epb, plan, perm, E, dirs, out);
+        return FEQ_OK;
+    });
+}
+
+extern "C" int feq_wigner_basis_bwd(const int32_t* lvals, int32_t n, const double* plan,
+                                    const int32_t* perm, int64_t E, const float* dirs,
+                                    const float* grad_out, float* grad_dirs, feq_stream_t stream) {
+    if (!lvals || n < 1) return fail(FEQ_ERR_INVALID, "lvals must be non-empty");
+    if (n > FEQ_MAX_IRREPS) return fail(FEQ_ERR_UNSUPPORTED, "more than %d irreps", FEQ_MAX_IRREPS);
+    if (E < 0) return fail(FEQ_ERR_INVALID, "negative edge count");
+    WignerArgs A{};
+    A.nirr = n;
+    int dim = 0;
+    size_t po = 0;
+    for (int i = 0; i < n; ++i) {
+        if (lvals[i] < 0 || lvals[i] >= FEQ_MAX_BLOCKS)
+            return fail(FEQ_ERR_UNSUPPORTED, "degree %d outside [0, %d]", lvals[i], FEQ_MAX_BLOCKS - 1);
+        A.lvals[i] = lvals[i];
+        A.off[i] = dim;
+        A.plan_off[i] = static_cast<int32_t>(po);
+        const int d = 2 * lvals[i] + 1;
+        dim += d;
+        po += static_cast<size_t>(d) * d + 2 * d;
+    }
+    A.dim = dim;
+    if (E == 0) return FEQ_OK;
+    if (!plan || !perm || !dirs || !grad_out || !grad_dirs) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    const int epb = 256 / dim;
+    if (epb < 1) return fail(FEQ_ERR_UNSUPPORTED, "representation dimension %d too large", dim);
+    const size_t lds = sizeof(float) * static_cast<size_t>(epb) * dim * dim;
+    if (lds > 64 * 1024) return fail(FEQ_ERR_UNSUPPORTED, "representation dimension %d too large", dim);
+    return with_lmax(A, [&](auto LL) -> int {
+        auto kern = k_wigner_bwd<decltype(LL)::value>;
+        FEQ_LAUNCH("k_wigner_bwd", kern, dim3(ceil_div(E, epb)), dim3(256), lds,
+                   stream_of(stream), A, epb, plan, perm, E, dirs, grad_out, grad_dirs);
+        return FEQ_OK;
+    });
 }

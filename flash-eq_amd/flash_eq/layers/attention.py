@@ -23,6 +23,7 @@ from ..representations import Repr
 from .linear import EquivariantEdgewiseLinear, EquivariantLinear
 from .norm import EquivariantLayerNorm
 from .pooling import GraphPooling
+from ._precision import half_dtype, run_float32
 
 
 class EquivariantEdgeAttention(nn.Module):
@@ -116,6 +117,10 @@ class EquivariantAttention(nn.Module):
                 distances: torch.Tensor, graph: Graph,
                 edge_features: torch.Tensor | None = None) -> torch.Tensor:
         """node_features (N, mult_in, dim_in) -> (N, mult_out, dim_out)."""
+        half = half_dtype(node_features)
+        if half is not None:
+            return run_float32(self, half, (P, Q_basis, node_features, distances, graph),
+                               dict(edge_features=edge_features))
         qk = self.linear_qk(self.norm_qk(node_features))            # (N, 2 mult, dim)
         if edge_features is not None:
             gathered = graph.gather_src(node_features) + edge_features

@@ -120,6 +120,15 @@ class EquivariantEdgewiseLinear(nn.Module):
         N.require_cuda_tensor(edge_features, "edge_features")
         rw = self.radial_weights
         layout, binning = self.layout(), self.binning()
+        if torch.is_grad_enabled() and (P.requires_grad or Q.requires_grad):
+            # gradients for the bases: the kernels that form gP and gQ take
+            # edge rows, so the gather (if any) happens first
+            if graph is not None:
+                if graph.num_edges != distances.shape[0]:
+                    raise ValueError(f"graph has {graph.num_edges} edges, distances {distances.shape[0]}")
+                edge_features = graph.gather_src(edge_features)
+            return edgewise_linear(edge_features, P, Q, distances, rw.channel_patterns,
+                                   rw.radial_functions(), layout, binning, rw.rank)
         emb = self._embedding(edge_features, distances.shape[0], layout, binning)
         if emb is not None:
             # a small layout without split-fp16 backward kernels: run it

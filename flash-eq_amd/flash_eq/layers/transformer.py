@@ -2,6 +2,7 @@
 
 Host orchestration in PyTorch; the per-edge work inside runs the HIP kernels
 (WignerDBasis, fused edgewise linear, edge softmax, attention pooling).
+bfloat16/float16 blocks and models compute in float32 inside (``_precision``).
 Module creation order follows ``transformer.py:143-211, 329-387``.
 """
 from __future__ import annotations
@@ -16,6 +17,7 @@ from .attention import EquivariantAttention
 from .gating import EquivariantGating
 from .linear import EquivariantLinear
 from .norm import SeparableEquivariantLayerNorm
+from ._precision import half_dtype, run_float32
 
 
 class LayerScale(nn.Module):
@@ -86,6 +88,10 @@ class EquivariantTransformerBlock(nn.Module):
     def forward(self, P: torch.Tensor, Q: torch.Tensor, node_features: torch.Tensor,
                 distances: torch.Tensor, graph: Graph,
                 edge_features: torch.Tensor | None = None) -> torch.Tensor:
+        half = half_dtype(node_features)
+        if half is not None:
+            return run_float32(self, half, (P, Q, node_features, distances, graph),
+                               dict(edge_features=edge_features))
         attn_out = self.attn(P, Q, self.norm1(node_features), distances, graph,
                              edge_features=edge_features)
         if self._use_attn_residual:
@@ -141,6 +147,9 @@ class EquivariantTransformer(nn.Module):
 
     def forward(self, coordinates: torch.Tensor, node_features: torch.Tensor,
                 graph: Graph) -> torch.Tensor:
+        half = half_dtype(node_features)
+        if half is not None:
+            return run_float32(self, half, (coordinates, node_features, graph), {})
         vec = coordinates[graph.src] - coordinates[graph.dst]      # src - dst, as transformer.py:406
         distances = vec.norm(dim=-1)
         m_in, m_hidden, m_out = self.basis(vec)

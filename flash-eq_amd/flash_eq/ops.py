@@ -171,6 +171,9 @@ def edgewise_src_supported(layout: N.FeqLayout, binning: N.FeqBinning, rank: int
 
 
 def edgewise_linear_src(x, src, perm, offsets, P, Q, dist, C, F, layout, binning, rank) -> torch.Tensor:
+    if torch.is_grad_enabled() and (P.requires_grad or Q.requires_grad):
+        raise ValueError("the message-passing form does not form gradients for P and Q; "
+                         "gather the rows and call edgewise_linear")
     return EdgewiseLinearSrcFn.apply(x, src, perm, offsets, P, Q, dist, C, F, layout, binning, rank)
 
 
@@ -556,7 +559,8 @@ def _softmax_scalar_grads(glog, qk, need_dist: bool, need_scale: bool, decay: fl
     """Distance and log-scale gradients from the logit gradient (E, H):
     d logit / d r = -1/decay, d logit / d log_scale = scale <Q,K> = qk."""
     g_dist = (glog.sum(1) * (-1.0 / decay)).to(rdt) if (need_dist and decay > 0) else None
-    g_log = (glog * qk).sum().to(ldt) if need_scale else None
+    # one scalar from E*H products that largely cancel: accumulated in float64
+    g_log = torch.dot(glog.reshape(-1).double(), qk.reshape(-1).double()).to(ldt) if need_scale else None
     return g_dist, g_log
 
 
@@ -580,6 +584,10 @@ class NodeSoftmaxFn(torch.autograd.Function):
         mult = two_mult // 2
         if two_mult != 2 * mult or mult % heads:
             raise ValueError(f"qk must be (N, 2*mult, dim) with heads | mult, got {tuple(qs.shape)}")
+        if Nn != num_nodes:
+            # the backward writes one Q-gradient row per destination segment and
+            # one K-gradient row per source segment of the graph's CSRs
+            raise ValueError(f"qk has {Nn} rows but the graph has {num_nodes} nodes")
         E = src.shape[0]
         Dh, ld = mult // heads * dim, two_mult * dim
         scale_t = log_scale.detach().float().exp().reshape(1).contiguous()   # read by the kernels
@@ -610,8 +618,12 @@ class NodeSoftmaxFn(torch.autograd.Function):
         Dh, ld = mult // heads * dim, two_mult * dim
         need = ctx.needs_input_grad
         ga = gattn.detach().to(torch.float32).contiguous()
-        gqk = torch.empty_like(qs)
         glog = torch.empty(E, heads, dtype=torch.float32, device=dev)
+        if E == 0:
+            g_dist, g_log = _softmax_scalar_grads(glog, qkv, need[1], need[2], decay, rdt, ldt)
+            return (torch.zeros_like(qs).to(qdt), g_dist, g_log, None, None, None, None, None, None,
+                    None, None, None)
+        gqk = torch.empty_like(qs)
         with torch.cuda.device(dev):
             rc = N.lib().feq_attn_softmax_bwd(N.ptr(qs), ld, N.ptr(qs) + 4 * mult * dim, ld,
                                               N.ptr(dst), N.ptr(src), Nn, N.ptr(attn), N.ptr(ga),
@@ -824,7 +836,9 @@ class BiasRowsFn(torch.autograd.Function):
 
 
 class ScaleFn(torch.autograd.Function):
-    """x * g for a scalar parameter g; its gradient is one dot product."""
+    """x * g for a scalar parameter g; its gradient is one dot product (float64
+    accumulation: the products cancel, and a float32 sum of a million of them
+    loses several digits)."""
 
     @staticmethod
     def forward(ctx, x, g):
@@ -837,7 +851,8 @@ class ScaleFn(torch.autograd.Function):
         gx = gy * g if ctx.needs_input_grad[0] else None
         gg = None
         if ctx.needs_input_grad[1]:
-            gg = torch.dot(gy.reshape(-1), x.reshape(-1)).reshape(g.shape).to(g.dtype)
+            # one scalar from many products that largely cancel: accumulated in float64
+            gg = torch.dot(gy.reshape(-1).double(), x.reshape(-1).double()).reshape(g.shape).to(g.dtype)
         return gx, gg
 
 

@@ -163,6 +163,11 @@ def _wigner_plan(repr: Repr) -> torch.Tensor:
 
 
 class _WignerBasisFn(torch.autograd.Function):
+    """One WignerDBasis output M (E, dim, dim) from the directions (E, 3); the
+    backward (``feq_wigner_basis_bwd``) is the exact derivative of the
+    reference's ``matrix_exp`` path (rot_to_ez, wigner.py:198-240) with respect
+    to the directions."""
+
     @staticmethod
     def forward(ctx, directions, lvals_i32, plan, perm_i32):
         dev = directions.device
@@ -176,13 +181,25 @@ class _WignerBasisFn(torch.autograd.Function):
                                           N.ptr(dirs) if E else None, N.ptr(out) if E else None,
                                           N.stream_ptr(dev))
         N.check(rc, "feq_wigner_basis")
+        ctx.save_for_backward(dirs, plan, perm_i32)
+        ctx.meta = (tuple(lvals_i32), directions.dtype)
         return out
 
     @staticmethod
     def backward(ctx, grad):
-        raise NotImplementedError(
-            "gradients through WignerDBasis (w.r.t. edge directions) are not implemented "
-            "in the MI355X build")
+        dirs, plan, perm_i32 = ctx.saved_tensors
+        lvals, ddt = ctx.meta
+        dev = dirs.device
+        E = dirs.shape[0]
+        g = grad.detach().to(torch.float32).contiguous()
+        gd = torch.empty_like(dirs)
+        lv = (N.ctypes.c_int32 * len(lvals))(*lvals)
+        with torch.cuda.device(dev):
+            rc = N.lib().feq_wigner_basis_bwd(lv, len(lvals), N.ptr(plan), N.ptr(perm_i32), E,
+                                              N.ptr(dirs) if E else None, N.ptr(g) if E else None,
+                                              N.ptr(gd) if E else None, N.stream_ptr(dev))
+        N.check(rc, "feq_wigner_basis_bwd")
+        return gd.to(ddt), None, None, None
 
 
 class WignerDBasis(nn.Module):
@@ -228,10 +245,6 @@ class WignerDBasis(nn.Module):
 
     def forward(self, directions: torch.Tensor) -> tuple:
         N.require_cuda_tensor(directions, "directions")
-        if directions.requires_grad and torch.is_grad_enabled():
-            raise NotImplementedError(
-                "WignerDBasis: gradients w.r.t. directions are not implemented in the MI355X "
-                "build; pass directions.detach()")
         if directions.dim() != 2 or directions.shape[-1] != 3:
             raise ValueError(f"directions must have shape (E, 3), got {tuple(directions.shape)}")
         outs = []

@@ -5,6 +5,9 @@ Mirrors the behaviour of the reference helpers in ``flash_eq/utils.py:8-27``
 """
 from __future__ import annotations
 
+import contextlib
+import threading
+
 import torch
 import torch.nn as nn
 
@@ -25,6 +28,25 @@ def init_linear_weights(module: nn.Module) -> None:
         nn.init.zeros_(module.bias)
 
 
+_EPS = threading.local()
+
+
 def get_epsilon(dtype: torch.dtype) -> float:
-    """Stabilising epsilon: 1e-5 for 16-bit floats, 1e-8 otherwise (``utils.py:19-27``)."""
+    """Stabilising epsilon: 1e-5 for 16-bit floats, 1e-8 otherwise (``utils.py:19-27``).
+
+    Inside ``epsilon_dtype(d)`` float32 tensors get d's epsilon: a half-precision
+    module computed in float32 keeps the epsilon of its own dtype."""
+    over = getattr(_EPS, "dtype", None)
+    if over is not None and dtype == torch.float32:
+        dtype = over
     return 1e-5 if dtype in _LOW_PRECISION else 1e-8
+
+
+@contextlib.contextmanager
+def epsilon_dtype(dtype: torch.dtype):
+    prev = getattr(_EPS, "dtype", None)
+    _EPS.dtype = dtype
+    try:
+        yield
+    finally:
+        _EPS.dtype = prev

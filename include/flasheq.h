@@ -24,6 +24,7 @@
  *                            form T[b,o,i,w] = sum_k C[k,o,i] F[b,k,w]
  *   feq_wigner_basis         WignerDBasis.forward / WignerD.rot_to_ez
  *                            (flash_eq/representations/wigner.py:198-240, 341-370)
+ *   feq_wigner_basis_bwd     its autograd backward (matrix_exp's, wigner.py:183)
  *   feq_csr_by_dst           grouping of edges by destination that the scatter
  *                            ops of pooling.py:21-30 / attention.py:124-141 imply
  *   feq_segment_sum          GraphPooling 'sum' forward (flash_eq/layers/pooling.py:21-30)
@@ -170,6 +171,15 @@ size_t feq_wigner_plan_doubles(const int32_t* lvals, int32_t n);
 int feq_wigner_basis(const int32_t* lvals, int32_t n, const double* plan_dev,
                      const int32_t* perm_dev, int64_t num_edges, const float* dirs,
                      float* out, feq_stream_t stream);
+/* Backward of feq_wigner_basis: grad_dirs (E, 3) = d<grad_out, M>/d dirs, the
+ * exact derivative of the reference's matrix_exp path (autograd through
+ * rot_to_ez and matrix_exp, flash_eq/representations/wigner.py:144-240, 358-367)
+ * in closed form: dD/dangle = X D and dD/dphi = [G2, D] for the axis generator
+ * X, chained through the axis normalisation, arccos and d = v/(|v|+eps).
+ * grad_out (E, dim, dim) float32; grad_dirs is written (not accumulated). */
+int feq_wigner_basis_bwd(const int32_t* lvals, int32_t n, const double* plan_dev,
+                         const int32_t* perm_dev, int64_t num_edges, const float* dirs,
+                         const float* grad_out, float* grad_dirs, feq_stream_t stream);
 
 /* ---- graph ops -----------------------------------------------------------------
  * CSR by destination: perm (E) lists edge ids grouped by dst in increasing
@@ -245,7 +255,9 @@ int feq_attn_softmax_fwd(const float* Q, int64_t ldq, const float* K, int64_t ld
  * sum(grad_logits*qk) and the distance gradient -sum_h grad_logits/decay from it).
  * Edge form: grad_Q[e], grad_K[e] (E rows).  Node form: grad_Q (num_nodes rows)
  * and grad_K (num_k rows) summed per node, every row written; grad_K walks the
- * CSR of the edges by k_idx (perm_k, offsets_k). */
+ * CSR of the edges by k_idx (perm_k, offsets_k), so num_k is that CSR's node
+ * count (offsets_k has num_k + 1 entries).  With num_edges == 0, perm and
+ * perm_k may be NULL and every gradient row is written as zero. */
 int feq_attn_softmax_bwd(const float* Q, int64_t ldq, const float* K, int64_t ldk,
                          const int64_t* q_idx, const int64_t* k_idx, int64_t num_k,
                          const float* attn, const float* grad_attn, int64_t num_edges,

@@ -83,12 +83,14 @@ def rep_norms(f: torch.Tensor, lvals, eps: float) -> torch.Tensor:
 def equivariant_layer_norm(f, lvals, ln_weight, ln_bias, eps: float = 1e-8):
     """EquivariantLayerNorm (norm.py:148-174): LayerNorm over channels of the irrep norms."""
     norms = rep_norms(f, lvals, eps)                         # (..., mult, nreps)
+    idx = torch.tensor([k for k, l in enumerate(lvals) for _ in range(2 * int(l) + 1)])
+    if ln_weight is None:                                    # mult = 1: no LayerNorm (norm.py:160-163)
+        return f * (1.0 / (norms + eps))[..., idx]
     t = norms.transpose(-2, -1)
     mu = t.mean(-1, keepdim=True)
     var = t.var(-1, unbiased=False, keepdim=True)
     ln = ((t - mu) / torch.sqrt(var + 1e-5) * ln_weight + ln_bias).transpose(-2, -1)
     scale = ln / (norms + eps)
-    idx = torch.tensor([k for k, l in enumerate(lvals) for _ in range(2 * int(l) + 1)])
     return f * scale[..., idx]
 
 

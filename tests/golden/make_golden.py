@@ -2,7 +2,13 @@
 
 Run once, in the build container, where the reference checkout is mounted:
 
-    python tests/golden/make_golden.py /root/reference
+    python tests/golden/make_golden.py /root/reference [--composed-only]
+
+It writes two files: ``reference_vectors.npz`` (below) and
+``composed_vectors.npz`` (``composed()``: outputs and gradients of the
+reference's edgewise linear, attention layer, transformer block and
+transformer, run in float64 with the reference's block-diagonal CUDA op
+replaced by the oracle's CPU op, which is pinned without the reference).
 
 It covers what no closed form or reference test pins exactly:
 
@@ -44,6 +50,17 @@ def load_reference(root: str):
         mod = types.ModuleType(name)
         mod.__path__ = [os.path.join(pkg, sub) if sub else pkg]
         sys.modules[name] = mod
+    # transformer.py imports the S2 activation (-> spherical -> sphericart, not
+    # installed); the blocks built here use gating (use_s2_activation=False), so
+    # the import only has to resolve: a placeholder module that refuses use
+    s2 = types.ModuleType("feq_ref.layers.s2_activation")
+
+    class _Unavailable:
+        def __init__(self, *a, **k):
+            raise RuntimeError("S2 activation is not available in the golden generator")
+
+    s2.S2Activation = s2.SeparableS2Activation = _Unavailable
+    sys.modules["feq_ref.layers.s2_activation"] = s2
     ns = types.SimpleNamespace()
     ns.rep = importlib.import_module("feq_ref.representations")
     ns.graph = importlib.import_module("feq_ref.graph")
@@ -53,6 +70,7 @@ def load_reference(root: str):
     ns.gating = importlib.import_module("feq_ref.layers.gating")
     ns.pooling = importlib.import_module("feq_ref.layers.pooling")
     ns.attention = importlib.import_module("feq_ref.layers.attention")
+    ns.transformer = importlib.import_module("feq_ref.layers.transformer")
     return ns
 
 
@@ -70,7 +88,7 @@ def directions() -> torch.Tensor:
 
 def state(prefix: str, module: torch.nn.Module, out: dict) -> None:
     for k, v in module.state_dict().items():
-        out[f"{prefix}__sd__{k}"] = v.detach().cpu().numpy()
+        out[f"{prefix}__sd__{k}"] = v.detach().cpu().numpy().copy()
 
 
 def main(root: str) -> None:
@@ -154,5 +172,167 @@ def main(root: str) -> None:
     print(f"wrote {OUT}: {len(out)} arrays, {os.path.getsize(OUT)} bytes")
 
 
+# ---- composed layers: outputs and gradients of the reference's own modules -------------------
+COMPOSED_OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "composed_vectors.npz")
+
+
+def oracle_block_op(repo_root: str):
+    """The reference signature of ``block_diagonal_cuda`` (cuda/block_diagonal.py:206-216)
+    over the oracle's CPU block op (``oracle.layer.BlockDiag``), which is pinned
+    independently of the reference (closed forms, brute force, the C restatement)."""
+    if repo_root not in sys.path:
+        sys.path.insert(0, repo_root)
+    from oracle import blockdiag as BD
+    from oracle.layer import BlockDiag
+
+    def op(features, radial_table, distances, product_repr, bin_param1, bin_param2, num_bins,
+           log_bins=False, sh_scale=0.1):
+        lin = [int(l) for l in product_repr.rep1.lvals]
+        lout = [int(l) for l in product_repr.rep2.lvals]
+        b = BD.Binning(float(bin_param1), float(bin_param2), int(num_bins), bool(log_bins),
+                       float(sh_scale))
+        return BlockDiag.apply(features, radial_table, distances.to(features.dtype), lin, lout, b)
+
+    return op
+
+
+def _graph(E: int, N: int, seed: int, isolated: bool = True, no_self_loops: bool = True):
+    g = torch.Generator().manual_seed(seed)
+    hi = N - 1 if isolated else N                    # node N-1 receives no edge
+    dst = torch.randint(0, hi, (E,), generator=g)
+    src = torch.randint(0, N, (E,), generator=g)
+    if no_self_loops:
+        for e in range(E):
+            while int(src[e]) == int(dst[e]):
+                src[e] = torch.randint(0, N, (1,), generator=g)
+    return src, dst
+
+
+def _grads(prefix: str, module, y, inputs: dict, out: dict, seed: int) -> None:
+    """Weights W (fixed, seeded) of the loss sum(y * W); the loss's gradient with
+    respect to every named input and every parameter of the module."""
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(y.shape, generator=g, dtype=torch.float64)
+    out[f"{prefix}__y"] = y.detach().numpy()
+    out[f"{prefix}__lossw"] = w.numpy()
+    (y * w).sum().backward()
+    for k, t in inputs.items():
+        out[f"{prefix}__in__{k}"] = t.detach().numpy()
+        if t.requires_grad:
+            out[f"{prefix}__grad__{k}"] = t.grad.detach().numpy()
+    for k, p in module.named_parameters():
+        out[f"{prefix}__pgrad__{k}"] = p.grad.detach().numpy()
+
+
+def composed(root: str) -> None:
+    """Reference outputs and gradients (float64 modules built from float32 seeded
+    init) of EquivariantEdgewiseLinear, EquivariantAttention, EquivariantTransformerBlock
+    and EquivariantTransformer on small graphs (E <= 64, mult <= 8)."""
+    R = load_reference(root)
+    R.linear.block_diagonal_cuda = oracle_block_op(os.path.dirname(os.path.dirname(
+        os.path.dirname(os.path.abspath(__file__)))))
+    Repr = R.rep.Repr
+    out: dict[str, np.ndarray] = {}
+    dd = torch.float64
+    HID = 16                               # radial-MLP width of the modules below (small fixtures)
+
+    def dirs(E, seed):
+        g = torch.Generator().manual_seed(seed)
+        return torch.randn(E, 3, generator=g, dtype=dd)
+
+    # ---- EquivariantEdgewiseLinear: P != Q, linear bins with extrapolation; log bins
+    for name, seed, rin, rout, kw in (
+            ("ewl", 21, Repr([0, 1], 4), Repr([0, 1, 2], 3), dict(num_bins=10, hidden_dim=HID)),
+            ("ewlL", 22, Repr([0, 1, 2], 3), Repr([0, 1, 2], 3),
+             dict(num_bins=8, log_bins=True, min_dist=0.5, max_dist=8.0, hidden_dim=HID))):
+        torch.manual_seed(seed)
+        m = R.linear.EquivariantEdgewiseLinear(rin, rout, **kw)
+        state(name, m, out)
+        m = m.double()
+        E = 24
+        g = torch.Generator().manual_seed(seed + 100)
+        v = dirs(E, seed + 200)
+        P, Q = R.rep.WignerDBasis([rin, rout]).double()(v)
+        P = P.detach().clone().requires_grad_(True)
+        Q = Q.detach().clone().requires_grad_(True)
+        x = torch.randn(E, rin.mult, rin.dim(), generator=g, dtype=dd).requires_grad_(True)
+        r = (torch.rand(E, generator=g, dtype=dd) * 12.0 + 0.3).requires_grad_(True)
+        y = m(P, Q, x, r)
+        _grads(name, m, y, dict(x=x, P=P, Q=Q, r=r, dirs=v), out, seed + 300)
+
+    # ---- EquivariantAttention with distance decay; with and without edge features
+    for name, seed, with_ef in (("att", 31, False), ("attE", 32, True)):
+        rp = Repr([0, 1, 2], 4)
+        torch.manual_seed(seed)
+        m = R.attention.EquivariantAttention(rp, rp, num_heads=2, num_bins=10, hidden_dim=HID,
+                                             distance_decay_scale=3.0)
+        state(name, m, out)
+        m = m.double()
+        E, Nn = 40, 9
+        src, dst = _graph(E, Nn, seed + 100)
+        graph = R.graph.Graph(src, dst, Nn)
+        g = torch.Generator().manual_seed(seed + 200)
+        v = torch.randn(E, 3, generator=g, dtype=dd)
+        (P,) = R.rep.WignerDBasis([rp]).double()(v)
+        x = torch.randn(Nn, 4, 9, generator=g, dtype=dd).requires_grad_(True)
+        r = (torch.rand(E, generator=g, dtype=dd) * 9.0 + 0.2).requires_grad_(True)
+        inputs = dict(x=x, r=r, src=src, dst=dst, dirs=v)
+        ef = None
+        if with_ef:
+            ef = torch.randn(E, 4, 9, generator=g, dtype=dd).requires_grad_(True)
+            inputs["ef"] = ef
+        y = m(P, P, x, r, graph, edge_features=ef)
+        _grads(name, m, y, inputs, out, seed + 300)
+
+    # ---- EquivariantTransformerBlock: residual (equal reprs) and not
+    for name, seed, rin, rout, decay in (("blk", 41, Repr([0, 1, 2], 4), Repr([0, 1, 2], 4), None),
+                                         ("blkN", 42, Repr([0, 1], 4), Repr([0, 1, 2], 6), 2.5)):
+        torch.manual_seed(seed)
+        m = R.transformer.EquivariantTransformerBlock(rin, rout, num_heads=2, num_bins=10,
+                                                      hidden_dim=HID, distance_decay_scale=decay)
+        state(name, m, out)
+        with torch.no_grad():              # sizeable residual branches for the comparison
+            for mod in (m.layer_scale_attn, m.layer_scale_mlp):
+                if hasattr(mod, "gamma"):
+                    mod.gamma.fill_(0.6)
+        m = m.double()
+        E, Nn = 48, 11
+        src, dst = _graph(E, Nn, seed + 100)
+        graph = R.graph.Graph(src, dst, Nn)
+        g = torch.Generator().manual_seed(seed + 200)
+        v = torch.randn(E, 3, generator=g, dtype=dd)
+        P, Q = R.rep.WignerDBasis([rin, rout]).double()(v)
+        x = torch.randn(Nn, rin.mult, rin.dim(), generator=g, dtype=dd).requires_grad_(True)
+        r = (torch.rand(E, generator=g, dtype=dd) * 9.0 + 0.2).requires_grad_(True)
+        y = m(P, Q, x, r, graph)
+        _grads(name, m, y, dict(x=x, r=r, src=src, dst=dst, dirs=v), out, seed + 300)
+
+    # ---- EquivariantTransformer: coordinates -> bases -> 3 blocks -> final norm
+    rin, rh, ro = Repr([0, 1], 4), Repr([0, 1, 2], 4), Repr([0], 4)
+    torch.manual_seed(51)
+    m = R.transformer.EquivariantTransformer(rin, rh, ro, num_layers=3, num_heads=2, num_bins=10)
+    state("tf", m, out)                    # default init (hidden_dim 64): the seeded-init pin
+    torch.manual_seed(51)
+    m = R.transformer.EquivariantTransformer(rin, rh, ro, num_layers=3, num_heads=2, num_bins=10,
+                                             hidden_dim=HID, layer_scale_init=0.6)
+    state("tfS", m, out)
+    m = m.double()
+    E, Nn = 56, 12
+    src, dst = _graph(E, Nn, 151, isolated=False)
+    graph = R.graph.Graph(src, dst, Nn)
+    g = torch.Generator().manual_seed(251)
+    coords = (torch.randn(Nn, 3, generator=g, dtype=dd) * 3.0).requires_grad_(True)
+    x = torch.randn(Nn, 4, 4, generator=g, dtype=dd).requires_grad_(True)
+    y = m(coords, x, graph)
+    _grads("tfS", m, y, dict(x=x, coords=coords, src=src, dst=dst), out, 351)
+
+    np.savez_compressed(COMPOSED_OUT, **out)
+    print(f"wrote {COMPOSED_OUT}: {len(out)} arrays, {os.path.getsize(COMPOSED_OUT)} bytes")
+
+
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    args = [a for a in sys.argv[1:] if not a.startswith("--")]
+    ref_root = args[0] if args else "/root/reference"
+    if "--composed-only" not in sys.argv:
+        main(ref_root)
+    composed(ref_root)
