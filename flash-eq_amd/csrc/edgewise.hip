@@ -20,6 +20,8 @@
 // 1113-1160) for a table of this form, including NaN at r = 0.
 #include "feq_internal.h"
 
+#include <mutex>
+
 namespace feq {
 namespace {
 
@@ -487,6 +489,54 @@ extern "C" int feq_edgewise_src_supported(const feq_layout* L, const feq_binning
     if (!L || !b || check_layout(L) || check_binning(b)) return 0;
     if (ew_path() != kPathSplit) return 0;
     return ew_split_supported(*L, *b, rank, false) && ew_split_supported(*L, *b, rank, true);
+}
+
+// ---- allocation-free message-passing forward ---------------------------------------
+// The forward's only scratch is the fp16-split copy of the channel patterns
+// (written by k_ews_prep on every call).  This variant keeps it in a
+// file-scope device array, so it needs no caller workspace and allocates
+// nothing; every device holds its own copy of the array, at its own address.
+static __device__ __align__(256) unsigned char scratch[FEQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[FEQ_MAX_DEVICES] = {};
+
+// Device address of `scratch` on the current device, looked up once per device
+// (the array's host-side name is not a device address).
+int scratch_ptr(void** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= FEQ_MAX_DEVICES)
+        return fail(FEQ_ERR_HIP, "no current HIP device (or device id beyond %d)", FEQ_MAX_DEVICES);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !p)
+            return fail(FEQ_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(err));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return FEQ_OK;
+}
+}  // namespace
+
+extern "C" int feq_edgewise_fwd_src_noalloc(const feq_layout* L, const feq_binning* b,
+                                            int32_t rank, int64_t E, const float* x,
+                                            int64_t num_src, const int64_t* src, const float* P,
+                                            const float* Q, const float* dist, const float* C,
+                                            const float* F, float* y, feq_stream_t stream) {
+    if (int rc = check_layout(L)) return rc;
+    if (int rc = check_binning(b)) return rc;
+    if (rank < 1) return fail(FEQ_ERR_INVALID, "rank must be positive");
+    const size_t need = feq_edgewise_fwd_workspace(L, b, rank, E);
+    if (need > FEQ_NOALLOC_SCRATCH_BYTES)
+        return fail(FEQ_ERR_UNSUPPORTED, "layout needs %zu bytes of scratch, the static array holds %d",
+                    need, FEQ_NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    if (int rc = scratch_ptr(&ws)) return rc;
+    return feq_edgewise_fwd_src(L, b, rank, E, x, num_src, src, P, Q, dist, C, F, y, ws,
+                                FEQ_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 extern "C" int feq_edgewise_fwd_src(const feq_layout* L, const feq_binning* b, int32_t rank,

@@ -68,6 +68,8 @@ _SIGS = {
     "feq_edgewise_src_supported": ([_P, _P, _I32], ctypes.c_int),
     "feq_edgewise_fwd_src": ([_P, _P, _I32, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
                              ctypes.c_int),
+    "feq_edgewise_fwd_src_noalloc": ([_P, _P, _I32, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P],
+                                     ctypes.c_int),
     "feq_edgewise_bwd_src": ([_P, _P, _I32, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P,
                               _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
     "feq_edgewise_hl_supported": ([_P, _P, _I32], ctypes.c_int),

@@ -158,6 +158,20 @@ int feq_edgewise_fwd_src(const feq_layout* L, const feq_binning* b, int32_t rank
                          const float* x, int64_t num_src, const int64_t* src, const float* P,
                          const float* Q, const float* dist, const float* C, const float* F, float* y,
                          void* workspace, size_t ws_bytes, feq_stream_t stream);
+/* Allocation-free form of feq_edgewise_fwd_src.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Its scratch
+ * (the split channel patterns) lives in a static device array of
+ * FEQ_NOALLOC_SCRATCH_BYTES per device instead of a caller workspace; layouts
+ * needing more are rejected with FEQ_ERR_UNSUPPORTED.  Calls that overlap on
+ * one device race on that array.  Calls nothing that allocates. */
+#define FEQ_NOALLOC_SCRATCH_BYTES (256 * 1024)
+#define FEQ_MAX_DEVICES 64
+int feq_edgewise_fwd_src_noalloc(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                 int64_t num_edges, const float* x, int64_t num_src,
+                                 const int64_t* src, const float* P, const float* Q,
+                                 const float* dist, const float* C, const float* F, float* y,
+                                 feq_stream_t stream);
 int feq_edgewise_bwd_src(const feq_layout* L, const feq_binning* b, int32_t rank, int64_t num_edges,
                          const float* grad_y, const float* x, int64_t num_src, const int64_t* src,
                          const float* P, const float* Q, const float* dist, const float* C,
