@@ -24,6 +24,7 @@ this host.
 from __future__ import annotations
 
 import argparse
+import copy
 import json
 import os
 import re
@@ -210,26 +211,69 @@ def timed_steps(step, steps: int, warmup: int):
     return wall * 1e3 / steps, start.elapsed_time(stop) / steps, NAT.profile_summary()
 
 
-def secondary_workload(name: str, steps: int, warmup: int) -> dict:
-    """The other BASELINE configs at their full sizes (parity-test cases, reported
-    beside the metric's line): c1 = the reference's CPU-sized layer (gather,
-    layer, scatter-sum); c4 = the 6-layer EquivariantTransformer on a 50k-node
-    random-walk chain (E = 1.2M); c3 = EquivariantTransformerBlock, 8 heads,
-    [0,1,2]x64, radius-10 graph capped at 32 neighbours on 20k nodes in 60^3
-    (E = 640k), fwd + bwd including WignerDBasis, fp32 or bf16; c5 = one
-    EquivariantEdgewiseLinear [0..6]x128, kNN k=32 on 5k nodes in 30^3
-    (E = 160k), bf16 edge features, fwd + bwd."""
+def cpu_info() -> dict:
+    """The host's logical CPU count and model (the CPU baselines' hardware)."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(), "model": model}
+
+
+def _median_time(fn, reps: int):
+    times = []
+    for it in range(reps + 1):
+        t0 = time.perf_counter()
+        fn()
+        dt = time.perf_counter() - t0
+        if it:
+            times.append(dt)
+    return float(np.median(times)), times
+
+
+def _rotation(dev, seed: int):
     import flash_eq as fe
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(4, generator=g, dtype=torch.float64)
+    q = q / q.norm()
+    angle = 2 * torch.acos(q[0].abs().clamp(max=1.0))
+    axis = (q[1:] * torch.sign(q[0] if q[0] != 0 else torch.tensor(1.0)))
+    axis = axis / axis.norm()
+    return axis.float().to(dev), angle.float().to(dev)
+
+
+def equivariance_error(out1: torch.Tensor, out2: torch.Tensor) -> float:
+    """max|a-b| / (max|a| + 1e-8): the reference's metric (tests/helpers.py:54-69)."""
+    return float(((out1 - out2).abs().max() / (out1.abs().max() + 1e-8)).item())
+
+
+def build_workload(name: str):
+    """Full-size secondary configurations (3, 4, 5).
+
+    Returns a dict: step (one fwd + loss + bwd), E, N, config text, the
+    algorithmic table of the fused kernels, a bounded CPU-oracle timing
+    (edges/s on a stated sample; None to skip) and an equivariance check."""
+    import flash_eq as fe
+    from flash_eq.ops import SumSquaresFn
     dev = torch.device("cuda", 0)
+    wl = {"name": name}
     if name.startswith("c3"):
         dtype = torch.bfloat16 if name == "c3bf16" else torch.float32
         coords, src, dst = radius_graph(20000, 60.0, 10.0, 32, seed=1003)
         E, N = src.numel(), 20000
         g = torch.Generator().manual_seed(2003)
-        feats = torch.randn(N, 64, 9, generator=g).to(dev, dtype).requires_grad_(True)
+        feats_cpu = torch.randn(N, 64, 9, generator=g)
+        feats = feats_cpu.to(dev, dtype).requires_grad_(True)
         torch.manual_seed(3)
         rep = fe.Repr([0, 1, 2], 64)
-        block = fe.EquivariantTransformerBlock(rep, rep, num_heads=8, max_dist=10.0).to(dev, dtype)
+        block = fe.EquivariantTransformerBlock(rep, rep, num_heads=8, max_dist=10.0)
+        block_cpu = {k: v.clone() for k, v in block.state_dict().items()}
+        block = block.to(dev, dtype)
         basis = fe.WignerDBasis([rep]).to(dev)
         graph = fe.Graph(src.to(dev), dst.to(dev), N)
         xyz = coords.to(dev)
@@ -239,12 +283,54 @@ def secondary_workload(name: str, steps: int, warmup: int) -> dict:
             dist = vec.norm(dim=-1)
             (P,) = basis(vec)
             out = block(P.to(dtype), P.to(dtype), feats, dist.to(dtype), graph)
-            SumOfSquares.apply(out.float()).backward()
-        workload = (f"c3: EquivariantTransformerBlock 8 heads [0,1,2]x64, radius-10 graph capped at "
-                    f"k=32 on 20k nodes in 60^3, E={E}, fwd+bwd incl. WignerDBasis, {dtype}")
-        work = algorithmic_per_edge([0, 1, 2], [0, 1, 2], 64, 64)
+            SumSquaresFn.apply(out.float()).backward()
+
+        def equiv():
+            axis, angle = _rotation(dev, 77)
+            D = fe.WignerD(rep).to(dev).rot(axis, angle)
+            R = fe.WignerD(fe.Repr([1])).to(dev).rot(axis, angle, cartesian=True)
+            with torch.no_grad():
+                vec = xyz[graph.src] - xyz[graph.dst]
+                dist = vec.norm(dim=-1).to(dtype)
+                (P1,) = basis(vec)
+                (P2,) = basis(vec @ R.T)
+                x = feats.detach()
+                o1 = torch.einsum("ij,ncj->nci", D, block(P1.to(dtype), P1.to(dtype), x, dist, graph).float())
+                x2 = torch.einsum("ij,ncj->nci", D, x.float()).to(dtype)
+                o2 = block(P2.to(dtype), P2.to(dtype), x2, dist, graph).float()
+            return equivariance_error(o1, o2)
+
+        def cpu():
+            # the oracle's block (float32) on the edges into the first 500 nodes
+            from oracle import model as OM
+            from oracle import wigner as OW
+            sel = dst < 500
+            s, d = src[sel], dst[sel]
+            vec = coords[s] - coords[d]
+            P = OW.basis([0, 1, 2], vec).float()
+            r = vec.norm(dim=-1)
+            params = {k: (v.float().requires_grad_(True) if v.is_floating_point()
+                          and not k.endswith(("bin_edges", "frequencies")) else v.float()
+                          if v.is_floating_point() else v) for k, v in block_cpu.items()}
+            cfg = OM.block_cfg([0, 1, 2], [0, 1, 2], 64, 64, heads=8, num_bins=100, max_dist=10.0)
+            x = feats_cpu.clone().requires_grad_(True)
+
+            def run():
+                out = OM.block(params, cfg, P, P, x, r, s, d, N)
+                (out ** 2).sum().backward()
+            med, times = _median_time(run, 2)
+            return {"value": round(int(sel.sum()) / med, 1),
+                    "sample": f"edges into nodes 0..499 ({int(sel.sum())} of {E}), all {N} node "
+                              f"rows: fwd + (out**2).sum() + bwd of the float32 oracle block "
+                              f"(oracle/model.py), median of 2 after 1 warmup ({sum(times):.1f} s)"}
+
+        wl.update(step=step, E=E, N=N, equiv=equiv, cpu=None if dtype != torch.float32 else cpu,
+                  work=algorithmic_per_edge([0, 1, 2], [0, 1, 2], 64, 64),
+                  config=(f"c3: EquivariantTransformerBlock 8 heads [0,1,2]x64, radius-10 graph "
+                          f"capped at k=32 on 20k nodes in 60^3, E={E}, fwd+bwd incl. "
+                          f"WignerDBasis, {str(dtype).replace('torch.', '')}"),
+                  dtype="bf16" if dtype == torch.bfloat16 else "f32")
     elif name == "c4":
-        # random-walk chain, 3.8-unit steps in uniform random directions
         g = torch.Generator().manual_seed(1004)
         N = 50000
         u = torch.randn(N, 3, generator=g, dtype=torch.float64)
@@ -256,23 +342,53 @@ def secondary_workload(name: str, steps: int, warmup: int) -> dict:
         src = torch.from_numpy(idx[:, 1:].astype(np.int64)).reshape(-1)
         dst = torch.arange(N).repeat_interleave(24)
         E = src.numel()
-        feats = torch.randn(N, 32, 4, generator=g).to(dev).requires_grad_(True)
+        feats_cpu = torch.randn(N, 32, 4, generator=g)
+        feats = feats_cpu.to(dev).requires_grad_(True)
         torch.manual_seed(4)
         # out Repr([0], mult=1) cannot be split into 8 heads (attention.py:233-234);
         # mult=8 is the nearest constructible output
         model = fe.EquivariantTransformer(fe.Repr([0, 1], 32), fe.Repr([0, 1, 2], 64),
-                                          fe.Repr([0], 8), num_layers=6, num_heads=8,
-                                          max_dist=10.0).to(dev)
+                                          fe.Repr([0], 8), num_layers=6, num_heads=8, max_dist=10.0)
+        model_cpu = {k: v.clone() for k, v in model.state_dict().items()}
+        model = model.to(dev)
         graph = fe.Graph(src.to(dev), dst.to(dev), N)
         xyz = coords.to(dev)
 
         def step():
             out = model(xyz, feats, graph)
-            SumOfSquares.apply(out).backward()
-        workload = (f"c4: EquivariantTransformer 6 layers, in [0,1]x32, hidden [0,1,2]x64, out [0]x8 "
-                    f"(x1 is not divisible into 8 heads), 8 heads, random-walk chain of 50k nodes, "
-                    f"kNN k=24, E={E}, fwd+bwd incl. WignerDBasis, fp32")
-        work = algorithmic_per_edge([0, 1, 2], [0, 1, 2], 64, 64)
+            SumSquaresFn.apply(out).backward()
+
+        def cpu():
+            # the oracle's 6-layer model (float32) on the first 600 nodes of the chain
+            from oracle import model as OM
+            n = 600
+            c = coords[:n]
+            _, ii = cKDTree(c.double().numpy()).query(c.double().numpy(), k=25)
+            s = torch.from_numpy(ii[:, 1:].astype(np.int64)).reshape(-1)
+            d = torch.arange(n).repeat_interleave(24)
+            params = {k: (v.float().requires_grad_(True) if v.is_floating_point()
+                          and not k.endswith(("bin_edges", "frequencies")) else v.float()
+                          if v.is_floating_point() else v) for k, v in model_cpu.items()}
+            cfg = OM.transformer_cfg([0, 1], [0, 1, 2], [0], 32, 64, 8, num_layers=6, heads=8,
+                                     num_bins=100, max_dist=10.0)
+            x = feats_cpu[:n].clone().requires_grad_(True)
+
+            def run():
+                out = OM.transformer(params, cfg, c, x, s, d, n)
+                (out ** 2).sum().backward()
+            med, times = _median_time(run, 1)
+            return {"value": round(s.numel() / med, 1),
+                    "sample": f"the first {n} nodes of the chain with their own k=24 graph "
+                              f"({s.numel()} edges): fwd + (out**2).sum() + bwd of the float32 "
+                              f"oracle transformer (oracle/model.py), median of 1 after 1 warmup "
+                              f"({sum(times):.1f} s)"}
+
+        wl.update(step=step, E=E, N=N, equiv=None, cpu=cpu,
+                  work=algorithmic_per_edge([0, 1, 2], [0, 1, 2], 64, 64),
+                  config=(f"c4: EquivariantTransformer 6 layers, in [0,1]x32, hidden [0,1,2]x64, "
+                          f"out [0]x8 (x1 is not divisible into 8 heads), 8 heads, random-walk "
+                          f"chain of 50k nodes, kNN k=24, E={E}, fwd+bwd incl. WignerDBasis, fp32"),
+                  dtype="f32")
     elif name == "c1":
         g = torch.Generator().manual_seed(1001)
         N, E = 100, 500
@@ -282,10 +398,12 @@ def secondary_workload(name: str, steps: int, warmup: int) -> dict:
         while (src == dst).any():
             bad = src == dst
             dst[bad] = torch.randint(0, N, (int(bad.sum()),), generator=g)
-        feats = torch.randn(N, 32, 4, generator=g).to(dev).requires_grad_(True)
+        feats_cpu = torch.randn(N, 32, 4, generator=g)
+        feats = feats_cpu.to(dev).requires_grad_(True)
         torch.manual_seed(1)
         rin, rout = fe.Repr([0, 1], 32), fe.Repr([0, 1, 2], 64)
-        layer = fe.EquivariantEdgewiseLinear(rin, rout, num_bins=100, max_dist=10.0).to(dev)
+        layer_cpu = fe.EquivariantEdgewiseLinear(rin, rout, num_bins=100, max_dist=10.0)
+        layer = copy.deepcopy(layer_cpu).to(dev)
         graph = fe.Graph(src.to(dev), dst.to(dev), N)
         vec = coords.to(dev)[graph.src] - coords.to(dev)[graph.dst]
         dist = vec.norm(dim=-1)
@@ -294,19 +412,44 @@ def secondary_workload(name: str, steps: int, warmup: int) -> dict:
 
         def step():
             y = layer(P, Q, feats, dist, graph=graph)
-            SumOfSquares.apply(pool(y, graph)).backward()
-        workload = ("c1: EquivariantEdgewiseLinear [0,1]x32 -> [0,1,2]x64, N=100, E=500 random "
-                    "edges (self-loops resampled), gather + layer + scatter-sum, fp32")
-        work = algorithmic_per_edge([0, 1], [0, 1, 2], 32, 64)
+            SumSquaresFn.apply(pool(y, graph)).backward()
+
+        def cpu():
+            from oracle import graphops as OG
+            from oracle import layer as OL
+            from oracle import wigner as OW
+            v = coords[src] - coords[dst]
+            Pc, Qc = OW.basis([0, 1], v).float(), OW.basis([0, 1, 2], v).float()
+            r = v.norm(dim=-1)
+            params, cfg = OL.module_cfg(layer_cpu)
+            params = {k: t.detach().float().requires_grad_(True) for k, t in params.items()}
+            cfg["bin_edges"] = cfg["bin_edges"].float()
+            x = feats_cpu.clone().requires_grad_(True)
+
+            def run():
+                y = OG.pool_sum(OL.edgewise_linear(x[src], Pc, Qc, r, params, cfg), dst, N)
+                (y ** 2).sum().backward()
+            med, times = _median_time(run, 5)
+            return {"value": round(E / med, 1),
+                    "sample": f"all {E} edges: gather + float32 oracle layer + sum pooling, fwd + "
+                              f"bwd, median of 5 after 1 warmup ({sum(times):.2f} s)"}
+
+        wl.update(step=step, E=E, N=N, equiv=None, cpu=cpu,
+                  work=algorithmic_per_edge([0, 1], [0, 1, 2], 32, 64),
+                  config=("c1: EquivariantEdgewiseLinear [0,1]x32 -> [0,1,2]x64, N=100, E=500 "
+                          "random edges (self-loops resampled), gather + layer + scatter-sum, fp32"),
+                  dtype="f32")
     elif name == "c5":
         lv = list(range(7))
         coords, src, dst = knn_graph(5000, 32, 30.0, seed=1005)
         E, N = src.numel(), 5000
         g = torch.Generator().manual_seed(2005)
-        x = torch.randn(E, 128, 49, generator=g).to(dev, torch.bfloat16).requires_grad_(True)
+        x_cpu = torch.randn(E, 128, 49, generator=g).to(torch.bfloat16)
+        x = x_cpu.to(dev).requires_grad_(True)
         torch.manual_seed(5)
         rep = fe.Repr(lv, 128)
-        layer = fe.EquivariantEdgewiseLinear(rep, rep, num_bins=100, max_dist=10.0).to(dev)
+        layer_cpu = fe.EquivariantEdgewiseLinear(rep, rep, num_bins=100, max_dist=10.0)
+        layer = copy.deepcopy(layer_cpu).to(dev)
         xyz = coords.to(dev)
         vec = xyz[src.to(dev)] - xyz[dst.to(dev)]
         dist = vec.norm(dim=-1).clamp(max=10.0)
@@ -316,25 +459,84 @@ def secondary_workload(name: str, steps: int, warmup: int) -> dict:
         def step():
             y = layer(P, P, x, dist.to(torch.bfloat16))
             SumOfSquares.apply(y).backward()      # the norm accumulates in fp32
-        workload = ("c5: EquivariantEdgewiseLinear [0..6]x128 -> [0..6]x128, kNN k=32 on 5k nodes "
-                    f"in 30^3, E={E}, bf16 edge features, fwd+bwd")
-        work = algorithmic_per_edge(lv, lv, 128, 128)
+
+        def cpu():
+            from oracle import layer as OL
+            n = 400
+            Pc = P[:n].float().cpu()
+            r = dist[:n].to(torch.bfloat16).float().cpu()
+            params, cfg = OL.module_cfg(layer_cpu)
+            params = {k: t.detach().float().requires_grad_(True) for k, t in params.items()}
+            cfg["bin_edges"] = cfg["bin_edges"].float()
+            xs = x_cpu[:n].float().requires_grad_(True)
+
+            def run():
+                y = OL.edgewise_linear(xs, Pc, Pc, r, params, cfg)
+                (y ** 2).sum().backward()
+            med, times = _median_time(run, 1)
+            return {"value": round(n / med, 1),
+                    "sample": f"the first {n} of the {E} edges: fwd + (y**2).sum() + bwd of the "
+                              f"float32 oracle layer on the bf16 values (its (101, 128, 128, 231) "
+                              f"radial table dominates), 1 run after 1 warmup ({sum(times):.1f} s)"}
+
+        wl.update(step=step, E=E, N=N, equiv=None, cpu=cpu,
+                  work=algorithmic_per_edge(lv, lv, 128, 128),
+                  config=("c5: EquivariantEdgewiseLinear [0..6]x128 -> [0..6]x128, kNN k=32 on 5k "
+                          f"nodes in 30^3, E={E}, bf16 edge features, fwd+bwd"),
+                  dtype="bf16")
     else:
         raise SystemExit(f"unknown workload {name}")
-    ms, ms_ev, kern = timed_steps(step, steps, warmup)
-    per_kernel = {}
-    for kname, (calls, tot) in kern.items():
+    return wl
+
+
+def run_workload(name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
+    """One secondary configuration at full size: eager steps timed (synchronised
+    on both sides), a second pass with every library launch bracketed by events
+    (per-kernel times, the dominant kernel's algorithmic HBM fraction), the
+    CPU oracle on a bounded sample and, where defined, the equivariance error
+    under one random rotation."""
+    wl = build_workload(name)
+    E = wl["E"]
+    t0 = time.perf_counter()
+    for _ in range(warmup):
+        wl["step"]()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(steps):
+        wl["step"]()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t1) * 1e3 / steps
+    from flash_eq import _native as NAT
+    NAT.profile_summary()
+    NAT.profile_enable(True)
+    for _ in range(steps):
+        wl["step"]()
+    torch.cuda.synchronize()
+    NAT.profile_enable(False)
+    kern = NAT.profile_summary()
+    per_kernel, dom = {}, None
+    for kname, (calls, tot) in sorted(kern.items(), key=lambda kv: -kv[1][1]):
         avg = tot / calls
         entry = {"launches": calls, "avg_ms": round(avg, 4), "ms_per_step": round(tot / steps, 4)}
-        if kname in work:
-            fl, by = work[kname]
-            entry["hbm_frac_algorithmic_fp32"] = round(by * E / (avg * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
-            entry["fp32_tflops_algorithmic"] = round(fl * E / (avg * 1e-3) / 1e12, 2)
+        if kname in wl["work"]:
+            fl, by = wl["work"][kname]
+            entry["hbm_frac_algorithmic"] = round(by * E / (avg * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
         per_kernel[kname] = entry
-    return {"workload": name, "config": workload, "edges": E, "nodes": N,
-            "value": round(E * steps / (ms * 1e-3) / steps, 1), "unit": "edges/s",
-            "ms_per_step": round(ms, 4), "ms_per_step_events": round(ms_ev, 4),
-            "steps": steps, "warmup": warmup, "per_kernel": per_kernel}
+        dom = dom or kname
+    out = {"workload": name, "config": wl["config"], "edges": E, "nodes": wl["N"],
+           "dtype": wl["dtype"], "ms_per_step": round(ms, 4),
+           "value": round(E / (ms * 1e-3), 1), "unit": "edges/s", "steps": steps,
+           "warmup": warmup, "dominant_kernel": dom,
+           "dominant_kernel_hbm_frac": per_kernel.get(dom, {}).get("hbm_frac_algorithmic"),
+           "per_kernel": per_kernel}
+    if wl.get("equiv") is not None:
+        out["equivariance_err"] = wl["equiv"]()
+    if with_cpu and wl.get("cpu") is not None:
+        c = wl["cpu"]()
+        c.update({"unit": "edges/s", "kind": "port", "cores": torch.get_num_threads()})
+        out["cpu_baseline"] = c
+    out["wall_s"] = round(time.perf_counter() - t0, 1)
+    return out
 
 
 def main() -> int:
@@ -354,13 +556,17 @@ def main() -> int:
     ap.add_argument("--workload", default="c2", choices=["c2", "c1", "c3", "c3bf16", "c4", "c5"],
                     help="c2 (default) is the metric's configuration; the others print a "
                          "secondary line with their full-size throughput and kernel times")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the other BASELINE configurations (by default each runs at full "
+                         "size after the metric's step and is reported under 'secondary')")
+    ap.add_argument("--secondary-steps", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
               "multi-GPU path; run it with --gpus 1.", file=sys.stderr)
         return 2
     if args.workload != "c2":
-        print(json.dumps(secondary_workload(args.workload, args.steps, args.warmup)))
+        print(json.dumps(run_workload(args.workload, args.steps, args.warmup, not args.no_cpu)))
         return 0
     import flash_eq as fe
     from flash_eq import _native as NAT
@@ -486,11 +692,36 @@ def main() -> int:
                                        args.cpu_reps)
         layer.to(dev)
         cpu = {"value": round(v, 1), "unit": "edges/s", "cores": cores, "kind": "port",
+               "host": cpu_info(),
                "sample": f"first {args.cpu_sample} of the {E} edges: fwd + (y**2).sum() + bwd of the "
                          f"float32 CPU oracle (bin-grouped BLAS), median of {args.cpu_reps} after 1 "
                          f"warmup ({sum(times):.1f} s timed)"}
 
+    # equivariance under one random rotation (inputs and directions rotated)
+    axis, angle = _rotation(dev, 1234)
+    D = fe.WignerD(rep).to(dev).rot(axis, angle)
+    R = fe.WignerD(fe.Repr([1])).to(dev).rot(axis, angle, cartesian=True)
+    with torch.no_grad():
+        o1 = torch.einsum("ij,ecj->eci", D, layer(P, P, feats.detach(), dist.detach(), graph=graph))
+        (P2,) = basis(vec @ R.T)
+        o2 = layer(P2, P2, torch.einsum("ij,ncj->nci", D, feats.detach()), dist.detach(), graph=graph)
+    equiv = equivariance_error(o1, o2)
+
     value = E / (ms_per_step * 1e-3)
+    # each tensor once per pass: forward (x, P, r, y), backward (gy, x, P, r, gx) and the
+    # radial table read and its gradient written once per step (SURVEY's 12 573 B per edge)
+    table_bytes = 4 * (layer.radial_weights.num_bins + 1) * MULT * MULT * layer.weight_dim
+    step_bytes = work["k_ews_fwd"][1] + work["k_ews_bwd_x"][1] + 2 * table_bytes / E
+    step_flop = work["k_ews_fwd"][0] + work["k_ews_bwd_x"][0] + work["k_ews_bwd_c"][0]
+    secondary = []
+    if not args.no_secondary:
+        for wname in ("c1", "c3", "c3bf16", "c4", "c5"):
+            print(f"secondary {wname} ...", file=sys.stderr, flush=True)
+            try:
+                secondary.append(run_workload(wname, args.secondary_steps, 2, not args.no_cpu))
+            except Exception as exc:     # one failing configuration must not lose the headline
+                secondary.append({"workload": wname, "error": f"{type(exc).__name__}: {exc}"})
+            torch.cuda.empty_cache()
     line = {"metric": METRIC,
             "value": round(value, 1), "unit": "edges/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
@@ -505,7 +736,13 @@ def main() -> int:
                        "edges": E, "nodes": N, "grad_distances": bool(args.grad_dist),
                        "parallelism": "single-gpu"},
             "roofline": roofline, "cpu_baseline": cpu,
-            "wigner_basis_ms": round(wigner_ms, 4)}
+            # the whole step against its algorithmic bytes and fp32 flops per edge
+            "step_hbm_frac": round(step_bytes * E / (ms_per_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "step_algorithmic_bytes_per_edge": round(step_bytes, 1),
+            "step_fp32_tflops_algorithmic": round(step_flop * E / (ms_per_step * 1e-3) / 1e12, 2),
+            "equivariance_err": equiv,
+            "wigner_basis_ms": round(wigner_ms, 4),
+            "secondary": secondary}
     print(json.dumps(line))
     return 0
 
