@@ -149,21 +149,33 @@ struct EdgeBin {
     float dtdr;
 };
 
-__device__ __forceinline__ EdgeBin edge_bin(float r, const feq_binning& b) {
-    EdgeBin s;
+// float32 log and exp rounded from float64 (correctly rounded but for values
+// within 2^-29 of a rounding boundary): the bin index of a log-binned distance
+// then depends on nothing but the float32 inputs, and the CPU oracle's
+// float64-then-round restatement reproduces it bit for bit.
+__device__ __forceinline__ float cr_logf(float x) { return static_cast<float>(log(static_cast<double>(x))); }
+__device__ __forceinline__ float cr_expf(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
+
+// Lower bin index of distance r: the float32 index path of compute_binning.
+__device__ __forceinline__ int bin_index(float r, const feq_binning& b) {
     const int nb = b.num_bins;
     float nrm;
     if (b.log_bins) {
-        nrm = (logf(fmaxf(r, expf(b.p1))) - b.p1) * b.p2 * static_cast<float>(nb);
+        nrm = (cr_logf(fmaxf(r, cr_expf(b.p1))) - b.p1) * b.p2 * static_cast<float>(nb);
     } else {
         nrm = (r - b.p1) * b.p2;
     }
     nrm = fminf(fmaxf(nrm, 0.0f), static_cast<float>(nb));
-    int lo = static_cast<int>(floorf(nrm));
-    lo = lo < nb - 1 ? lo : nb - 1;
+    const int lo = static_cast<int>(floorf(nrm));
+    return lo < nb - 1 ? lo : nb - 1;
+}
+
+__device__ __forceinline__ EdgeBin edge_bin(float r, const feq_binning& b) {
+    EdgeBin s;
+    const int lo = bin_index(r, b);
     s.lo = lo;
     if (b.log_bins) {
-        const float ilbw = b.p2 * static_cast<float>(nb);
+        const float ilbw = b.p2 * static_cast<float>(b.num_bins);
         const float log_lo = b.p1 + static_cast<float>(lo) / ilbw;
         const float e_lo = static_cast<float>(exp(static_cast<double>(log_lo)));
         const float e_hi = static_cast<float>(exp(static_cast<double>(log_lo + 1.0f / ilbw)));
@@ -188,14 +200,49 @@ __device__ __forceinline__ float lerp_bins(float lo, float hi, float t) {
 }
 
 // s^l for small non-negative integer l by repeated squaring (as ipow, :202-213).
-__device__ __forceinline__ float ipowf(float base, int e) {
-    float r = 1.0f;
+template <class T>
+__device__ __forceinline__ T ipow_t(T base, int e) {
+    T r = T(1);
     while (e > 0) {
         if (e & 1) r *= base;
         base *= base;
         e >>= 1;
     }
     return r;
+}
+__device__ __forceinline__ float ipowf(float base, int e) { return ipow_t<float>(base, e); }
+
+// Bin state with t and dt/dr in the feature precision T (the reference's
+// InterpState<scalar_t>): the index in float32, t as compute_binning forms it
+// in T (block_diagonal.cu:82-115), dt/dr as binning_derivative (:121-138).
+template <class T>
+struct EdgeBinT {
+    int lo;
+    T t;
+    T dtdr;
+};
+
+template <class T>
+__device__ __forceinline__ EdgeBinT<T> edge_bin_t(T r, const feq_binning& b) {
+    EdgeBinT<T> s;
+    const int lo = bin_index(static_cast<float>(r), b);
+    s.lo = lo;
+    if (b.log_bins) {
+        const T ilbw = static_cast<T>(b.p2 * static_cast<float>(b.num_bins));
+        const T log_lo = static_cast<T>(b.p1) + static_cast<T>(lo) / ilbw;
+        const T e_lo = static_cast<T>(exp(static_cast<double>(log_lo)));
+        const T e_hi = static_cast<T>(exp(static_cast<double>(log_lo + T(1) / ilbw)));
+        const T c = r > e_lo ? r : e_lo;
+        const T t = (c - e_lo) / (e_hi - e_lo);
+        s.t = t < T(1) ? t : T(1);
+        s.dtdr = T(1) / (e_hi - e_lo);
+    } else {
+        const T width = T(1) / static_cast<T>(b.p2);
+        const T e_lo = static_cast<T>(b.p1) + static_cast<T>(lo) * width;
+        s.t = (r - e_lo) / width;
+        s.dtdr = static_cast<T>(b.p2);
+    }
+    return s;
 }
 
 }  // namespace feq

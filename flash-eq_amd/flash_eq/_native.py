@@ -60,6 +60,8 @@ _SIGS = {
     "feq_blockdiag_workspace": ([_P, _P, _I64], _SZ),
     "feq_blockdiag_fwd": ([_P, _P, _I64, _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
     "feq_blockdiag_bwd": ([_P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
+    "feq_blockdiag_fwd_f64": ([_P, _P, _I64, _P, _P, _P, _P, _P], ctypes.c_int),
+    "feq_blockdiag_bwd_f64": ([_P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
     "feq_edgewise_fwd_workspace": ([_P, _P, _I32, _I64], _SZ),
     "feq_edgewise_workspace": ([_P, _P, _I32, _I64], _SZ),
     "feq_edgewise_fwd": ([_P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),

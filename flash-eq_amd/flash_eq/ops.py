@@ -3,8 +3,9 @@
 Every function here runs the GPU kernels through the C ABI on the current
 stream of the tensors' device; PyTorch only allocates outputs and workspaces.
 Inputs must be GPU tensors; float16/bfloat16/float32 inputs are computed in
-float32 (fp32 accumulation) and returned in the input dtype.  float64 is
-rejected: the kernels are float32.
+float32 (fp32 accumulation) and returned in the input dtype.  float64 runs the
+generic block-diagonal op's own float64 kernels and is rejected elsewhere
+(the fused kernels are float32).
 """
 from __future__ import annotations
 
@@ -25,6 +26,13 @@ def _f32(t: torch.Tensor, name: str) -> torch.Tensor:
     if t.dtype not in _SUPPORTED:
         raise TypeError(f"{name}: unsupported dtype {t.dtype}")
     return t.detach().to(torch.float32).contiguous()
+
+
+def _f64(t: torch.Tensor, name: str) -> torch.Tensor:
+    N.require_cuda_tensor(t, name)
+    if t.dtype not in _SUPPORTED + (torch.float64,):
+        raise TypeError(f"{name}: unsupported dtype {t.dtype}")
+    return t.detach().to(torch.float64).contiguous()
 
 
 def _same_device(*ts: Optional[torch.Tensor]) -> torch.device:
@@ -386,20 +394,34 @@ def edgewise_linear(x, P, Q, dist, C, F, layout, binning, rank) -> torch.Tensor:
 # generic block-diagonal op (reference table layout)
 # ---------------------------------------------------------------------------
 class BlockDiagonalFn(torch.autograd.Function):
+    """The reference's block-diagonal op on a (num_bins+1, Cout, Cin, Wdim) table
+    (``_BlockDiagonalFunction``, block_diagonal.py:77-174): float32 and float64
+    run their own kernels, float16/bfloat16 compute in float32 and return the
+    input dtype.  Gradients for features, table and distances; the table
+    gradient is summed per bin in a fixed order (deterministic)."""
+
     @staticmethod
     def forward(ctx, features, table, dist, layout: N.FeqLayout, binning: N.FeqBinning):
         dev = _same_device(features, table, dist)
-        xs, ts, rs = _f32(features, "features"), _f32(table, "radial_table"), _f32(dist, "distances")
+        f64 = features.dtype == torch.float64
+        cast = (lambda t, n: _f64(t, n)) if f64 else _f32
+        xs, ts, rs = cast(features, "features"), cast(table, "radial_table"), cast(dist, "distances")
         E = xs.shape[0]
         if xs.shape[1:] != (layout.cin, layout.din):
             raise ValueError(f"features must be (E, {layout.cin}, {layout.din}), got {tuple(xs.shape)}")
         if ts.shape != (binning.num_bins + 1, layout.cout, layout.cin, layout.wdim):
             raise ValueError(f"radial_table must be ({binning.num_bins + 1}, {layout.cout}, "
                              f"{layout.cin}, {layout.wdim}), got {tuple(ts.shape)}")
-        y = torch.empty(E, layout.cout, layout.dout, dtype=torch.float32, device=dev)
+        y = torch.empty(E, layout.cout, layout.dout, dtype=xs.dtype, device=dev)
         if E:
+            lib = N.lib()
             with torch.cuda.device(dev):
-                rc = N.lib().feq_blockdiag_fwd(N.ctypes.byref(layout), N.ctypes.byref(binning), E,
+                if f64:
+                    rc = lib.feq_blockdiag_fwd_f64(N.ctypes.byref(layout), N.ctypes.byref(binning), E,
+                                                   N.ptr(xs), N.ptr(ts), N.ptr(rs), N.ptr(y),
+                                                   N.stream_ptr(dev))
+                else:
+                    rc = lib.feq_blockdiag_fwd(N.ctypes.byref(layout), N.ctypes.byref(binning), E,
                                                N.ptr(xs), N.ptr(ts), N.ptr(rs), N.ptr(y), None, 0,
                                                N.stream_ptr(dev))
             N.check(rc, "feq_blockdiag_fwd")
@@ -413,14 +435,18 @@ class BlockDiagonalFn(torch.autograd.Function):
         layout, binning, xdt, tdt, rdt = ctx.meta
         dev = xs.device
         E = xs.shape[0]
-        g = gy.detach().to(torch.float32).contiguous()
+        g = gy.detach().to(xs.dtype).contiguous()
         gx = torch.empty_like(xs)
         gt = torch.empty_like(ts)
         gr = torch.empty_like(rs) if ctx.needs_input_grad[2] else None
+        lib = N.lib()
+        ws = N.workspace(lib.feq_blockdiag_workspace(N.ctypes.byref(layout), N.ctypes.byref(binning),
+                                                     E), dev)
+        fn = lib.feq_blockdiag_bwd_f64 if xs.dtype == torch.float64 else lib.feq_blockdiag_bwd
         with torch.cuda.device(dev):
-            rc = N.lib().feq_blockdiag_bwd(N.ctypes.byref(layout), N.ctypes.byref(binning), E,
-                                           N.ptr(g), N.ptr(xs), N.ptr(ts), N.ptr(rs), N.ptr(gx),
-                                           N.ptr(gt), N.ptr(gr), None, 0, N.stream_ptr(dev))
+            rc = fn(N.ctypes.byref(layout), N.ctypes.byref(binning), E, N.ptr(g) if E else None,
+                    N.ptr(xs), N.ptr(ts), N.ptr(rs), N.ptr(gx), N.ptr(gt), N.ptr(gr), N.ptr(ws),
+                    ws.numel(), N.stream_ptr(dev))
         N.check(rc, "feq_blockdiag_bwd")
         return gx.to(xdt), gt.to(tdt), (None if gr is None else gr.to(rdt)), None, None
 

@@ -17,6 +17,7 @@
  *                            (block_diagonal.cu:1268-1282, 1758-1761)
  *   feq_blockdiag_bwd        pybind "backward" -> block_diagonal_backward_cuda
  *                            (block_diagonal.cu:1543-1558, 1758-1761)
+ *   feq_blockdiag_*_f64      their float64 dispatch (block_diagonal.cu:1332, 1605)
  *   feq_edgewise_fwd/_bwd    EquivariantEdgewiseLinear.forward = bmm(X,P) ->
  *                            block_diagonal_cuda(rw()) -> bmm(.,Q^T)
  *                            (flash_eq/layers/linear.py:100-160, radial.py:259-275),
@@ -107,16 +108,31 @@ int feq_layout_init(feq_layout* out, const int32_t* lvals_in, int32_t n_in,
 int feq_bin_edges(const feq_binning* b, int64_t num_edges, const float* dist,
                   int32_t* lo, float* t, feq_stream_t stream);
 
-/* ---- generic block-diagonal op: table (num_bins+1, Cout, Cin, Wdim) ---------- */
+/* ---- generic block-diagonal op: table (num_bins+1, Cout, Cin, Wdim) ----------
+ * The forward needs no workspace (pass NULL, 0).  The backward needs
+ * feq_blockdiag_workspace bytes: it groups the edges by lower bin and sums the
+ * table gradient per bin in a fixed order (no atomics: the same bits on every
+ * run).  grad_dist may be NULL (not needed).  grad_x, grad_table and
+ * grad_dist are overwritten. */
 size_t feq_blockdiag_workspace(const feq_layout* L, const feq_binning* b, int64_t num_edges);
 int feq_blockdiag_fwd(const feq_layout* L, const feq_binning* b, int64_t num_edges,
                       const float* x, const float* table, const float* dist, float* y,
                       void* workspace, size_t ws_bytes, feq_stream_t stream);
-/* grad_dist may be NULL (not needed). grad_x / grad_table are overwritten. */
 int feq_blockdiag_bwd(const feq_layout* L, const feq_binning* b, int64_t num_edges,
                       const float* grad_y, const float* x, const float* table, const float* dist,
                       float* grad_x, float* grad_table, float* grad_dist,
                       void* workspace, size_t ws_bytes, feq_stream_t stream);
+/* The same op in float64: the reference dispatches the kernels on float64 as well
+ * (block_diagonal.cu:1332, 1605, AT_DISPATCH_FLOATING_TYPES_AND_HALF); bin
+ * indices in float32, t and dt/dr in float64, as its InterpState<double>. */
+int feq_blockdiag_fwd_f64(const feq_layout* L, const feq_binning* b, int64_t num_edges,
+                          const double* x, const double* table, const double* dist, double* y,
+                          feq_stream_t stream);
+int feq_blockdiag_bwd_f64(const feq_layout* L, const feq_binning* b, int64_t num_edges,
+                          const double* grad_y, const double* x, const double* table,
+                          const double* dist, double* grad_x, double* grad_table,
+                          double* grad_dist, void* workspace, size_t ws_bytes,
+                          feq_stream_t stream);
 
 /* ---- fused EquivariantEdgewiseLinear (separable radial weights) ---------------
  * x (E, Cin, Din) standard basis; P (E, Din, Din); Q (E, Dout, Dout);

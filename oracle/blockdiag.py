@@ -73,7 +73,12 @@ def bin_state(r: torch.Tensor, b: Binning):
     p1, p2, nb = _f32(b.p1), _f32(b.p2), b.num_bins
     with np.errstate(all="ignore"):
         if b.log_bins:
-            lg = np.log(np.maximum(rf, np.exp(p1, dtype=np.float32)), dtype=np.float32)
+            # float32 log/exp rounded from float64 (correctly rounded), as the
+            # kernels form them; CUDA's logf/expf (<= 1 ulp) can differ from
+            # these in the last bit, moving r within one float32 ulp of a bin
+            # edge to the neighbouring bin
+            lo_edge = np.float32(np.exp(np.float64(p1)))
+            lg = np.log(np.maximum(rf, lo_edge).astype(np.float64)).astype(np.float32)
             norm = ((lg - p1) * p2) * np.float32(nb)
         else:
             norm = (rf - p1) * p2

@@ -49,6 +49,10 @@ static int build_blocks(const int* lin, int nlin, const int* lout, int nlout, bl
     return 0;
 }
 
+/* float32 log/exp rounded from double (correctly rounded), as the kernels form them */
+static float cr_logf(float x) { return (float)log((double)x); }
+static float cr_expf(float x) { return (float)exp((double)x); }
+
 #define DEFINE_ORACLE(T, SUF)                                                               \
 static T ipow_##SUF(T base, int e) {                                                       \
     T r = (T)1;                                                                             \
@@ -58,7 +62,7 @@ static T ipow_##SUF(T base, int e) {                                            
 static void binning_##SUF(T dist, float p1, float p2, int nbins, int logb,                 \
                           int* lo, int* hi, T* t, T* dtdr) {                               \
     float nrm;                                                                              \
-    if (logb) nrm = (logf(fmaxf((float)dist, expf(p1))) - p1) * p2 * (float)nbins;        \
+    if (logb) nrm = (cr_logf(fmaxf((float)dist, cr_expf(p1))) - p1) * p2 * (float)nbins;  \
     else      nrm = ((float)dist - p1) * p2;                                               \
     nrm = fminf(fmaxf(nrm, 0.0f), (float)nbins);                                           \
     int l = (int)floorf(nrm); if (l > nbins - 1) l = nbins - 1;                            \
