@@ -86,11 +86,8 @@ def algorithmic_per_edge(lin, lout, cin, cout, same_pq=True):
     PQ = 4 * din * din + (0 if same_pq else 4 * dout * dout)
     return {
         "k_ews_fwd": (mix + rot, X + PQ + 4 + Y),
-        "k_ewc_fwd": (mix + rot, X + PQ + 4 + Y),
         "k_ews_bwd_x": (mix + rot, Y + X + PQ + 4 + X),
         "k_ews_bwd_c": (mix, Y + X + PQ + 4),
-        "k_ewc_bwd_x": (mix + rot, Y + X + PQ + 4 + X),
-        "k_ewc_bwd_c": (mix, Y + X + PQ + 4),
         "_mix_macs_per_pair": M,
     }
 

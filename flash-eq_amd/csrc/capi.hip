@@ -44,7 +44,6 @@ int ew_path() {
     const char* v = getenv("FEQ_EW_PATH");
     if (!v) return kPathSplit;
     if (strcmp(v, "generic") == 0) return kPathGeneric;
-    if (strcmp(v, "fp32mfma") == 0) return kPathFp32Mfma;
     return kPathSplit;
 }
 

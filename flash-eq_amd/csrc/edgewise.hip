@@ -205,12 +205,14 @@ k_ew_fwd(feq_layout L, feq_binning B, EwDims D, const float* __restrict__ x,
 
 // ---------------------------------------------------------------------------
 // Each workgroup walks a contiguous edge range; dC is accumulated per
-// workgroup in LDS and written as a partial, then reduced in a fixed order.
+// workgroup in LDS and written as a partial, and the per-edge radial-function
+// gradient dF_e is written per edge; the shared tail bins dF_e and sums the
+// partials in a fixed order (deterministic, no atomics).
 __global__ void __launch_bounds__(kThreads)
 k_ew_bwd(feq_layout L, feq_binning B, EwDims D, int64_t E, const float* __restrict__ gy,
          const float* __restrict__ x, const float* __restrict__ P, const float* __restrict__ Q,
          const float* __restrict__ dist, const float* __restrict__ C,
-         const float* __restrict__ F, float* __restrict__ gx, float* __restrict__ gF,
+         const float* __restrict__ F, float* __restrict__ gx, float* __restrict__ dFe,
          float* __restrict__ gdist, float* __restrict__ gP, float* __restrict__ gQ,
          float* __restrict__ dC_part) {
     extern __shared__ float sm[];
@@ -311,8 +313,7 @@ k_ew_bwd(feq_layout L, feq_binning B, EwDims D, int64_t E, const float* __restri
                     }
                 }
                 const int64_t fo = static_cast<int64_t>(k) * wd + w;
-                atomicAdd(&gF[static_cast<int64_t>(eb.lo) * K * wd + fo], (1.0f - eb.t) * g);
-                atomicAdd(&gF[static_cast<int64_t>(eb.lo + 1) * K * wd + fo], eb.t * g);
+                dFe[e * K * wd + fo] = g;    // binned afterwards in a fixed order (ew_tail)
                 acc_t += (fhi[fo] - flo[fo]) * g;
                 acc_s += static_cast<float>(Lsum) * sF[fo] * g;
             }
@@ -358,15 +359,6 @@ k_ew_bwd(feq_layout L, feq_binning B, EwDims D, int64_t E, const float* __restri
     for (int q = tid; q < ncc; q += kThreads) dC_part[static_cast<int64_t>(blockIdx.x) * ncc + q] = sdC[q];
 }
 
-__global__ void k_reduce_partials(const float* __restrict__ part, int groups, int64_t n,
-                                  float* __restrict__ out) {
-    const int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-    if (q >= n) return;
-    float acc = 0.0f;
-    for (int g = 0; g < groups; ++g) acc += part[g * n + q];
-    out[q] = acc;
-}
-
 size_t fwd_lds(const feq_layout& L, int K) {
     return sizeof(float) * (2 * L.cin * L.din + L.din * L.din + L.dout * L.dout + K * L.wdim +
                             L.cin * L.dout + L.cout * L.dout);
@@ -396,11 +388,14 @@ using namespace feq;
 extern "C" size_t feq_edgewise_workspace(const feq_layout* L, const feq_binning* b, int32_t rank,
                                          int64_t E) {
     if (!L || rank < 1) return 0;
-    const size_t generic = sizeof(float) * static_cast<size_t>(groups_for(E)) * rank * L->cout * L->cin + 256;
-    const size_t fast = b ? ew_mfma_bwd_workspace(*L, *b, rank, E) : 0;
+    const int64_t ncc = static_cast<int64_t>(rank) * L->cout * L->cin, kw = static_cast<int64_t>(rank) * L->wdim;
+    // dC partials, the per-edge radial-function gradient dF_e and the tail's buffers
+    const size_t generic = b ? sizeof(float) * (static_cast<size_t>(groups_for(E)) * ncc + 64 +
+                                                static_cast<size_t>(E) * kw + 64 +
+                                                ew_tail_floats(*b, static_cast<int>(kw), E, groups_for(E), ncc)) + 256
+                             : 0;
     const size_t split = b ? ew_split_bwd_workspace(*L, *b, rank, E) : 0;
-    const size_t m = generic > fast ? generic : fast;
-    return m > split ? m : split;
+    return generic > split ? generic : split;
 }
 
 extern "C" size_t feq_edgewise_fwd_workspace(const feq_layout* L, const feq_binning*, int32_t rank,
@@ -424,10 +419,6 @@ extern "C" int feq_edgewise_fwd(const feq_layout* L, const feq_binning* b, int32
     if (path == kPathSplit) {
         const int rc = ew_split_fwd(*L, *b, rank, E, x, nullptr, 0, P, Q, dist, C, F, y, ws,
                                     ws_bytes, stream_of(stream));
-        if (rc != -1) return rc;
-    }
-    if (path != kPathGeneric) {
-        const int rc = ew_mfma_fwd(*L, *b, rank, E, x, P, Q, dist, C, F, y, stream_of(stream));
         if (rc != -1) return rc;
     }
     const size_t lds = fwd_lds(*L, rank);
@@ -465,23 +456,21 @@ extern "C" int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32
                                     gdist, ws, ws_bytes, s);
         if (rc != -1) return rc;
     }
-    if (path != kPathGeneric && !gP && !gQ) {
-        const int rc = ew_mfma_bwd(*L, *b, rank, E, gy, x, P, Q, dist, C, F, gx, gC, gF, gdist, ws,
-                                   ws_bytes, s);
-        if (rc != -1) return rc;
-    }
-    // the fused paths above overwrite gF; the generic kernel accumulates into it
-    if (int rc = fill_zero(gF, nF, s)) return rc;
+    // generic kernel: per-workgroup dC partials and the per-edge dF_e, then the
+    // fixed-order binning and partial sums of the shared tail (no atomics)
+    const int kw = rank * L->wdim;
+    if (!ew_tail_supported(*b, kw))
+        return fail(FEQ_ERR_UNSUPPORTED, "radial-function histogram does not fit LDS");
     const size_t lds = bwd_lds(*L, rank);
     if (int rc = ensure_lds(reinterpret_cast<const void*>(&k_ew_bwd), lds)) return rc;
     const int G = groups_for(E);
     float* part = static_cast<float*>(ws);
+    float* dFe = part + align_up(static_cast<size_t>(G) * ncc, 64);
+    float* tail = dFe + align_up(static_cast<size_t>(E) * kw, 64);
     EwDims D{rank, b->num_bins};
     FEQ_LAUNCH("k_ew_bwd", k_ew_bwd, dim3(G), dim3(kThreads), lds, s, *L, *b, D, E, gy, x, P, Q, dist,
-                       C, F, gx, gF, gdist, gP, gQ, part);
-    FEQ_LAUNCH("k_reduce_partials", k_reduce_partials, dim3(ceil_div(ncc, 256)), dim3(256), 0, s, part, G, ncc,
-                       gC);
-    return FEQ_OK;
+                       C, F, gx, dFe, gdist, gP, gQ, part);
+    return ew_tail(*L, *b, rank, E, dist, F, dFe, part, G, ncc, gC, gF, nullptr, tail, s);
 }
 
 // ---- message-passing form: x is a node table, edge e reads row src[e] -----------

@@ -1,7 +1,7 @@
 // Fused EquivariantEdgewiseLinear with its GEMMs on the fp16 matrix cores of
 // gfx950, at fp32 accuracy.
 //
-// Same mathematics as edgewise.hip and edgewise_mfma.hip: with the separable
+// Same mathematics as edgewise.hip: with the separable
 // radial table T[b,o,i,w] = sum_k C[k,o,i] F[b,k,w] the per-edge mix of a
 // 16-edge tile is one GEMM shared by all edges, G_k = C_k fs (M = Cout,
 // N = 16 Din, K = Cin), followed by a per-edge contraction with the

@@ -67,19 +67,7 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 // Zero-fill by kernel (never hipMemsetAsync: callers may capture the stream).
 int fill_zero(float* p, int64_t n, hipStream_t s);
 
-// Fast paths of the fused edgewise layer for compile-time shapes
-// (edgewise_mfma.hip).  They return -1 when the shape has no instantiation.
-int ew_mfma_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
-                const float* P, const float* Q, const float* dist, const float* C, const float* F,
-                float* y, hipStream_t s);
-
-size_t ew_mfma_bwd_workspace(const feq_layout& L, const feq_binning& B, int rank, int64_t E);
-int ew_mfma_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* gy,
-                const float* x, const float* P, const float* Q, const float* dist, const float* C,
-                const float* F, float* gx, float* gC, float* gF, float* gdist, void* ws,
-                size_t ws_bytes, hipStream_t s);
-
-// Tail shared by the fused backward families (edgewise_tail.hip): binned
+// Tail shared by the fused backward kernels (edgewise_tail.hip): binned
 // radial-function gradient from dF_e (E, K wdim), distance gradient (gdist may
 // be NULL), and the sums of `groups` channel-pattern partials of ncc floats.
 // Deterministic sum of `groups` partial arrays of n floats into out (tmp holds
@@ -109,11 +97,10 @@ int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
 bool ew_split_supported(const feq_layout& L, const feq_binning& B, int rank, bool backward);
 
 // Kernel family of the fused edgewise layer.  The default tries the split-fp16
-// kernels, then the fp32-MFMA kernels, then the shape-generic ones;
-// FEQ_EW_PATH=fp32mfma starts at the fp32-MFMA kernels and FEQ_EW_PATH=generic
-// (or FEQ_FORCE_GENERIC=1) uses only the generic ones, so tests can check the
+// kernels, then the shape-generic ones; FEQ_EW_PATH=generic (or
+// FEQ_FORCE_GENERIC=1) uses only the generic ones, so tests can check the
 // implementations against each other.
-enum { kPathSplit = 0, kPathFp32Mfma = 1, kPathGeneric = 2 };
+enum { kPathSplit = 0, kPathGeneric = 2 };
 int ew_path();
 bool force_generic();
 
