@@ -280,7 +280,9 @@ def build_workload(name: str):
             dist = vec.norm(dim=-1)
             (P,) = basis(vec)
             out = block(P.to(dtype), P.to(dtype), feats, dist.to(dtype), graph)
-            SumSquaresFn.apply(out.float()).backward()
+            loss = SumSquaresFn.apply(out.float())
+            loss.backward()
+            return loss
 
         def equiv():
             axis, angle = _rotation(dev, 77)
@@ -322,6 +324,7 @@ def build_workload(name: str):
                               f"(oracle/model.py), median of 2 after 1 warmup ({sum(times):.1f} s)"}
 
         wl.update(step=step, E=E, N=N, equiv=equiv, cpu=None if dtype != torch.float32 else cpu,
+                  leaves=[feats] + list(block.parameters()),
                   work=algorithmic_per_edge([0, 1, 2], [0, 1, 2], 64, 64),
                   config=(f"c3: EquivariantTransformerBlock 8 heads [0,1,2]x64, radius-10 graph "
                           f"capped at k=32 on 20k nodes in 60^3, E={E}, fwd+bwd incl. "
@@ -353,7 +356,9 @@ def build_workload(name: str):
 
         def step():
             out = model(xyz, feats, graph)
-            SumSquaresFn.apply(out).backward()
+            loss = SumSquaresFn.apply(out)
+            loss.backward()
+            return loss
 
         def cpu():
             # the oracle's 6-layer model (float32) on the first 600 nodes of the chain
@@ -380,7 +385,7 @@ def build_workload(name: str):
                               f"oracle transformer (oracle/model.py), median of 1 after 1 warmup "
                               f"({sum(times):.1f} s)"}
 
-        wl.update(step=step, E=E, N=N, equiv=None, cpu=cpu,
+        wl.update(step=step, E=E, N=N, equiv=None, cpu=cpu, leaves=[feats] + list(model.parameters()),
                   work=algorithmic_per_edge([0, 1, 2], [0, 1, 2], 64, 64),
                   config=(f"c4: EquivariantTransformer 6 layers, in [0,1]x32, hidden [0,1,2]x64, "
                           f"out [0]x8 (x1 is not divisible into 8 heads), 8 heads, random-walk "
@@ -409,7 +414,9 @@ def build_workload(name: str):
 
         def step():
             y = layer(P, Q, feats, dist, graph=graph)
-            SumSquaresFn.apply(pool(y, graph)).backward()
+            loss = SumSquaresFn.apply(pool(y, graph))
+            loss.backward()
+            return loss
 
         def cpu():
             from oracle import graphops as OG
@@ -431,7 +438,7 @@ def build_workload(name: str):
                     "sample": f"all {E} edges: gather + float32 oracle layer + sum pooling, fwd + "
                               f"bwd, median of 5 after 1 warmup ({sum(times):.2f} s)"}
 
-        wl.update(step=step, E=E, N=N, equiv=None, cpu=cpu,
+        wl.update(step=step, E=E, N=N, equiv=None, cpu=cpu, leaves=[feats] + list(layer.parameters()),
                   work=algorithmic_per_edge([0, 1], [0, 1, 2], 32, 64),
                   config=("c1: EquivariantEdgewiseLinear [0,1]x32 -> [0,1,2]x64, N=100, E=500 "
                           "random edges (self-loops resampled), gather + layer + scatter-sum, fp32"),
@@ -455,7 +462,9 @@ def build_workload(name: str):
 
         def step():
             y = layer(P, P, x, dist.to(torch.bfloat16))
-            SumOfSquares.apply(y).backward()      # the norm accumulates in fp32
+            loss = SumOfSquares.apply(y)          # the norm accumulates in fp32
+            loss.backward()
+            return loss
 
         def cpu():
             from oracle import layer as OL
@@ -476,7 +485,7 @@ def build_workload(name: str):
                               f"float32 oracle layer on the bf16 values (its (101, 128, 128, 231) "
                               f"radial table dominates), 1 run after 1 warmup ({sum(times):.1f} s)"}
 
-        wl.update(step=step, E=E, N=N, equiv=None, cpu=cpu,
+        wl.update(step=step, E=E, N=N, equiv=None, cpu=cpu, leaves=[x] + list(layer.parameters()),
                   work=algorithmic_per_edge(lv, lv, 128, 128),
                   config=("c5: EquivariantEdgewiseLinear [0..6]x128 -> [0..6]x128, kNN k=32 on 5k "
                           f"nodes in 30^3, E={E}, bf16 edge features, fwd+bwd"),
@@ -502,7 +511,30 @@ def run_workload(name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
     for _ in range(steps):
         wl["step"]()
     torch.cuda.synchronize()
-    ms = (time.perf_counter() - t1) * 1e3 / steps
+    ms_eager = (time.perf_counter() - t1) * 1e3 / steps
+    # the same step recorded once in a HIP graph and replayed (no host work per
+    # step); kept only when its loss equals an eager step's
+    ms_graph, graph_note = None, None
+    try:
+        from flash_eq.capture import capture_step
+        for t in wl["leaves"]:
+            t.grad = None
+        ref = float(wl["step"]())
+        cg, loss = capture_step(wl["step"], wl["leaves"], warmup=1)
+        cg.replay()
+        torch.cuda.synchronize()
+        if abs(float(loss) - ref) <= 1e-5 * max(abs(ref), 1.0):
+            t2 = time.perf_counter()
+            for _ in range(steps):
+                cg.replay()
+            torch.cuda.synchronize()
+            ms_graph = (time.perf_counter() - t2) * 1e3 / steps
+        else:
+            graph_note = f"replayed loss {float(loss)} differs from the eager {ref}"
+        del cg
+    except Exception as exc:      # a step that cannot be captured reports the eager time
+        graph_note = f"{type(exc).__name__}: {exc}"[:200]
+    ms = ms_graph if ms_graph is not None else ms_eager
     from flash_eq import _native as NAT
     NAT.profile_summary()
     NAT.profile_enable(True)
@@ -522,6 +554,10 @@ def run_workload(name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
         dom = dom or kname
     out = {"workload": name, "config": wl["config"], "edges": E, "nodes": wl["N"],
            "dtype": wl["dtype"], "ms_per_step": round(ms, 4),
+           "step_form": "hip_graph" if ms_graph is not None else "eager",
+           "ms_per_step_eager": round(ms_eager, 4),
+           "ms_per_step_graph": None if ms_graph is None else round(ms_graph, 4),
+           "graph_note": graph_note,
            "value": round(E / (ms * 1e-3), 1), "unit": "edges/s", "steps": steps,
            "warmup": warmup, "dominant_kernel": dom,
            "dominant_kernel_hbm_frac": per_kernel.get(dom, {}).get("hbm_frac_algorithmic"),
