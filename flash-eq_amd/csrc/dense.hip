@@ -1,0 +1,350 @@
+// Dense helpers of the node-side layers: tiled transposes between node-major
+// (rows, c, dim) and component-major (dim, rows, c) tables, deterministic
+// column sums (bias gradients), and float32 dot products accumulated in
+// float64 (gradients of scalar parameters).  All are single passes at HBM
+// speed, deterministic, and free of memsets (safe to record into HIP graphs).
+#include "feq_internal.h"
+
+namespace feq {
+namespace {
+
+constexpr int kTileElems = 4096;   // elements of one transpose tile
+
+// q = n / d for n, d < 2^16 with m = ceil(2^32 / d) (2^32 itself for d = 1):
+// n * m / 2^32 exceeds n / d by less than n * d / (d * 2^32) < 1 / d, so the
+// floor is exact.
+__device__ inline uint32_t div16(uint32_t n, uint64_t m) {
+    return static_cast<uint32_t>((static_cast<uint64_t>(n) * m) >> 32);
+}
+
+inline uint64_t div16_magic(uint32_t d) { return ((uint64_t{1} << 32) + d - 1) / d; }
+
+// out[b][j][i] = in[b][i][j] for in (batch, M, N).  A workgroup moves one
+// TM x TN tile through LDS: the reads walk the tile's input rows, the writes its
+// output rows, both in consecutive addresses.  With TN = N (narrow input) the
+// tile's reads are one contiguous run, with TM = M (narrow output) its writes.
+// The LDS row stride is odd so neither phase has bank conflicts.
+template <typename T>
+__global__ void __launch_bounds__(256)
+k_transpose(const T* __restrict__ in, int64_t M, int64_t N, int TM, int TN, int S, uint64_t mag_tn,
+            uint64_t mag_tm, int64_t tiles_n, T* __restrict__ out) {
+    extern __shared__ __align__(16) unsigned char lds_raw[];
+    T* s = reinterpret_cast<T*>(lds_raw);
+    const int64_t tile = blockIdx.x;
+    const int64_t tm = tile / tiles_n, tn = tile - tm * tiles_n;
+    const int64_t m0 = tm * TM, n0 = tn * TN;
+    const int h = static_cast<int>(M - m0 < TM ? M - m0 : TM);
+    const int w = static_cast<int>(N - n0 < TN ? N - n0 : TN);
+    const int64_t boff = static_cast<int64_t>(blockIdx.y) * M * N;
+    const T* src = in + boff;
+    T* dst = out + boff;
+    const uint32_t total = static_cast<uint32_t>(TM) * TN;
+    for (uint32_t i = threadIdx.x; i < total; i += 256) {
+        const int r = static_cast<int>(div16(i, mag_tn));
+        const int c = static_cast<int>(i) - r * TN;
+        if (r < h && c < w) s[c * S + r] = src[(m0 + r) * N + n0 + c];
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < total; i += 256) {
+        const int c = static_cast<int>(div16(i, mag_tm));
+        const int r = static_cast<int>(i) - c * TM;
+        if (r < h && c < w) dst[(n0 + c) * M + m0 + r] = s[c * S + r];
+    }
+}
+
+struct TransposePlan {
+    int TM, TN, S;
+    int64_t tiles_m, tiles_n;
+};
+
+TransposePlan transpose_plan(int64_t M, int64_t N) {
+    TransposePlan p{};
+    if (N <= 32) {
+        p.TN = static_cast<int>(N);
+        p.TM = kTileElems / p.TN / 64 * 64;
+    } else if (M <= 32) {
+        p.TM = static_cast<int>(M);
+        p.TN = kTileElems / p.TM / 64 * 64;
+    } else {
+        p.TM = 64;
+        p.TN = 64;
+    }
+    p.S = p.TM | 1;
+    p.tiles_m = ceil_div(M, p.TM);
+    p.tiles_n = ceil_div(N, p.TN);
+    return p;
+}
+
+template <typename T>
+int transpose(const T* in, int64_t batch, int64_t M, int64_t N, T* out, hipStream_t s) {
+    const TransposePlan p = transpose_plan(M, N);
+    const int64_t tiles = p.tiles_m * p.tiles_n;
+    if (tiles > 0x7fffffff || batch > 65535)
+        return fail(FEQ_ERR_UNSUPPORTED, "transpose: %lld tiles x %lld matrices exceeds the grid",
+                    static_cast<long long>(tiles), static_cast<long long>(batch));
+    const size_t lds = sizeof(T) * static_cast<size_t>(p.S) * p.TN;
+    auto kern = k_transpose<T>;
+    FEQ_LAUNCH("k_transpose", kern, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(batch)),
+               dim3(256), lds, s, in, M, N, p.TM, p.TN, p.S, div16_magic(p.TN),
+               div16_magic(p.TM), p.tiles_n, out);
+    return FEQ_OK;
+}
+
+// ---- column sums ---------------------------------------------------------------
+// out[k][j] = sum of in[i][j] over the rows i of chunk k.  A workgroup covers a
+// tile of TPR * VEC columns (TPR threads across, VEC columns per thread) and one
+// chunk of rows; its 256 / TPR thread rows take interleaved input rows, and
+// their partials are combined by a fixed tree in LDS.
+template <typename T, int VEC>
+__global__ void __launch_bounds__(256)
+k_colsum(const T* __restrict__ in, int64_t rows, int64_t cols, int tpr_log2, int64_t rows_per_chunk,
+         T* __restrict__ out) {
+    __shared__ T s[256 * VEC];
+    const int tpr = 1 << tpr_log2;
+    const int rpp = 256 >> tpr_log2;
+    const int lc = threadIdx.x & (tpr - 1);
+    const int rg = threadIdx.x >> tpr_log2;
+    const int64_t col = static_cast<int64_t>(blockIdx.x) * tpr * VEC + lc * VEC;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * rows_per_chunk;
+    const int64_t r1 = r0 + rows_per_chunk < rows ? r0 + rows_per_chunk : rows;
+    T acc[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[v] = T(0);
+    if (col + VEC <= cols) {
+        for (int64_t r = r0 + rg; r < r1; r += rpp) {
+            const T* p = in + r * cols + col;
+            if constexpr (VEC == 4) {
+                const float4 q = *reinterpret_cast<const float4*>(p);
+                acc[0] += q.x; acc[1] += q.y; acc[2] += q.z; acc[3] += q.w;
+            } else if constexpr (VEC == 2) {
+                const double2 q = *reinterpret_cast<const double2*>(p);
+                acc[0] += q.x; acc[1] += q.y;
+            } else {
+                acc[0] += p[0];
+            }
+        }
+    } else {
+        for (int64_t r = r0 + rg; r < r1; r += rpp)
+#pragma unroll
+            for (int v = 0; v < VEC; ++v)
+                if (col + v < cols) acc[v] += in[r * cols + col + v];
+    }
+    const int width = tpr * VEC;
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) s[rg * width + lc * VEC + v] = acc[v];
+    __syncthreads();
+    for (int half = rpp >> 1; half > 0; half >>= 1) {
+        if (rg < half)
+#pragma unroll
+            for (int v = 0; v < VEC; ++v)
+                s[rg * width + lc * VEC + v] += s[(rg + half) * width + lc * VEC + v];
+        __syncthreads();
+    }
+    if (rg == 0)
+#pragma unroll
+        for (int v = 0; v < VEC; ++v)
+            if (col + v < cols) out[static_cast<int64_t>(blockIdx.y) * cols + col + v] = s[lc * VEC + v];
+}
+
+constexpr int64_t kColsumGroups = 2048;   // target workgroups per pass
+
+struct ColsumPass {
+    int64_t rows, chunks, rows_per_chunk;
+    int vec, tpr_log2;
+    int64_t ctiles;
+};
+
+ColsumPass colsum_pass(int64_t rows, int64_t cols, int vec) {
+    ColsumPass p{};
+    p.rows = rows;
+    p.vec = vec;
+    const int64_t lanes = ceil_div(cols, vec);
+    int t = 0;
+    while ((int64_t{1} << t) < lanes && t < 6) ++t;
+    p.tpr_log2 = t;
+    p.ctiles = ceil_div(cols, (int64_t{1} << t) * vec);
+    const int64_t rpp = 256 >> t;
+    int64_t chunks = ceil_div(kColsumGroups, p.ctiles);
+    const int64_t most = ceil_div(rows, rpp * 8);     // at least eight rows per thread
+    if (chunks > most) chunks = most;
+    if (chunks < 1) chunks = 1;
+    p.rows_per_chunk = ceil_div(rows, chunks);
+    p.chunks = p.rows_per_chunk > 0 ? ceil_div(rows, p.rows_per_chunk) : 1;
+    return p;
+}
+
+// The passes of one column sum: the first reads the input with vector width
+// first_vec, the later ones read the previous pass's partial table (256-byte
+// aligned) with later_vec; the last pass writes the output.
+template <typename Fn>
+void colsum_passes(int64_t rows, int64_t cols, int first_vec, int later_vec, Fn fn) {
+    int v = first_vec;
+    for (int k = 0;; ++k) {
+        const ColsumPass p = colsum_pass(rows, cols, v);
+        fn(k, p);
+        if (p.chunks == 1) return;
+        rows = p.chunks;
+        v = later_vec;
+    }
+}
+
+// Bytes of the two partial tables (even passes, odd passes), the larger of
+// the two first-pass vector widths, so the layout does not depend on alignment.
+template <typename T>
+void colsum_tables(int64_t rows, int64_t cols, size_t* even, size_t* odd) {
+    constexpr int kVec = sizeof(T) == 4 ? 4 : 2;
+    const int later = cols % kVec == 0 ? kVec : 1;
+    *even = *odd = 0;
+    for (int first : {1, later})
+        colsum_passes(rows, cols, first, later, [&](int k, const ColsumPass& p) {
+            if (p.chunks == 1) return;
+            size_t& slot = (k & 1) ? *odd : *even;
+            const size_t need = align_up(static_cast<size_t>(p.chunks * cols) * sizeof(T), 256);
+            if (need > slot) slot = need;
+        });
+}
+
+template <typename T>
+size_t colsum_ws_bytes(int64_t rows, int64_t cols) {
+    size_t even, odd;
+    colsum_tables<T>(rows, cols, &even, &odd);
+    return even + odd;
+}
+
+template <typename T, int V>
+int colsum_launch(const ColsumPass& p, const T* in, int64_t cols, T* out, hipStream_t s) {
+    if (p.ctiles > 0x7fffffff || p.chunks > 65535)
+        return fail(FEQ_ERR_UNSUPPORTED, "column sums: grid too large");
+    auto kern = k_colsum<T, V>;
+    FEQ_LAUNCH("k_colsum", kern, dim3(static_cast<unsigned>(p.ctiles), static_cast<unsigned>(p.chunks)),
+               dim3(256), 0, s, in, p.rows, cols, p.tpr_log2, p.rows_per_chunk, out);
+    return FEQ_OK;
+}
+
+template <typename T>
+int column_sums(const T* in, int64_t rows, int64_t cols, T* out, void* ws, size_t ws_bytes,
+                hipStream_t s) {
+    constexpr int kVec = sizeof(T) == 4 ? 4 : 2;
+    size_t even, odd;
+    colsum_tables<T>(rows, cols, &even, &odd);
+    if (even + odd > 0 && (!ws || ws_bytes < even + odd))
+        return fail(FEQ_ERR_WORKSPACE, "column-sum workspace too small");
+    const int later = cols % kVec == 0 ? kVec : 1;
+    const int first = later == kVec && (reinterpret_cast<uintptr_t>(in) & 15u) == 0 ? kVec : 1;
+    unsigned char* w = static_cast<unsigned char*>(ws);
+    const T* src = in;
+    int rc = FEQ_OK;
+    colsum_passes(rows, cols, first, later, [&](int k, const ColsumPass& p) {
+        if (rc) return;
+        T* dst = p.chunks == 1 ? out : reinterpret_cast<T*>(w + ((k & 1) ? even : 0));
+        rc = p.vec == kVec ? colsum_launch<T, kVec>(p, src, cols, dst, s)
+                           : colsum_launch<T, 1>(p, src, cols, dst, s);
+        src = dst;
+    });
+    return rc;
+}
+
+// ---- dot products accumulated in float64 -----------------------------------------
+constexpr int kDotGroups = 1024;
+
+__device__ inline double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__global__ void __launch_bounds__(256)
+k_dot_f64(const float* __restrict__ a, const float* __restrict__ b, int64_t n,
+          double* __restrict__ part) {
+    __shared__ double s[4];
+    double acc = 0.0;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15u) == 0) {
+        const float4* a4 = reinterpret_cast<const float4*>(a);
+        const float4* b4 = reinterpret_cast<const float4*>(b);
+        const int64_t n4 = n / 4;
+        for (int64_t i = t0; i < n4; i += stride) {
+            const float4 x = a4[i], y = b4[i];
+            acc += (static_cast<double>(x.x) * y.x + static_cast<double>(x.y) * y.y) +
+                   (static_cast<double>(x.z) * y.z + static_cast<double>(x.w) * y.w);
+        }
+        for (int64_t i = 4 * n4 + t0; i < n; i += stride) acc += static_cast<double>(a[i]) * b[i];
+    } else {
+        for (int64_t i = t0; i < n; i += stride) acc += static_cast<double>(a[i]) * b[i];
+    }
+    acc = wave_sum_d(acc);
+    if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) part[blockIdx.x] = (s[0] + s[1]) + (s[2] + s[3]);
+}
+
+// out[0] = (float) sum of part[0..groups) by one workgroup in a fixed order.
+__global__ void __launch_bounds__(256)
+k_dot_finish(const double* __restrict__ part, int groups, float* __restrict__ out) {
+    __shared__ double s[4];
+    double acc = 0.0;
+    for (int i = threadIdx.x; i < groups; i += 256) acc += part[i];
+    acc = wave_sum_d(acc);
+    if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) out[0] = static_cast<float>((s[0] + s[1]) + (s[2] + s[3]));
+}
+
+}  // namespace
+}  // namespace feq
+
+using namespace feq;
+
+extern "C" int feq_transpose(const void* in, int64_t batch, int64_t rows, int64_t cols,
+                             int32_t elem_bytes, void* out, feq_stream_t stream) {
+    if (batch < 0 || rows < 0 || cols < 0) return fail(FEQ_ERR_INVALID, "negative size");
+    if (batch == 0 || rows == 0 || cols == 0) return FEQ_OK;
+    if (!in || !out) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (in == out) return fail(FEQ_ERR_INVALID, "transpose: in-place is not supported");
+    hipStream_t s = stream_of(stream);
+    switch (elem_bytes) {
+        case 2: return transpose(static_cast<const uint16_t*>(in), batch, rows, cols,
+                                 static_cast<uint16_t*>(out), s);
+        case 4: return transpose(static_cast<const float*>(in), batch, rows, cols,
+                                 static_cast<float*>(out), s);
+        case 8: return transpose(static_cast<const double*>(in), batch, rows, cols,
+                                 static_cast<double*>(out), s);
+        default: return fail(FEQ_ERR_UNSUPPORTED, "transpose: element size %d", elem_bytes);
+    }
+}
+
+extern "C" size_t feq_column_sums_workspace(int64_t rows, int64_t cols, int32_t elem_bytes) {
+    if (rows <= 0 || cols <= 0) return 0;
+    return elem_bytes == 8 ? colsum_ws_bytes<double>(rows, cols) : colsum_ws_bytes<float>(rows, cols);
+}
+
+extern "C" int feq_column_sums(const void* in, int64_t rows, int64_t cols, int32_t elem_bytes,
+                               void* out, void* ws, size_t ws_bytes, feq_stream_t stream) {
+    if (rows < 0 || cols < 0) return fail(FEQ_ERR_INVALID, "negative size");
+    if (cols == 0) return FEQ_OK;
+    if (!out || (rows > 0 && !in)) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    hipStream_t s = stream_of(stream);
+    switch (elem_bytes) {
+        case 4: return column_sums(static_cast<const float*>(in), rows, cols,
+                                   static_cast<float*>(out), ws, ws_bytes, s);
+        case 8: return column_sums(static_cast<const double*>(in), rows, cols,
+                                   static_cast<double*>(out), ws, ws_bytes, s);
+        default: return fail(FEQ_ERR_UNSUPPORTED, "column sums: element size %d", elem_bytes);
+    }
+}
+
+extern "C" size_t feq_dot_f64_workspace(void) { return sizeof(double) * kDotGroups; }
+
+extern "C" int feq_dot_f64(const float* a, const float* b, int64_t n, float* out, void* ws,
+                           size_t ws_bytes, feq_stream_t stream) {
+    if (n < 0) return fail(FEQ_ERR_INVALID, "negative length");
+    if (!out || (n > 0 && (!a || !b))) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (!ws || ws_bytes < feq_dot_f64_workspace())
+        return fail(FEQ_ERR_WORKSPACE, "dot workspace too small");
+    hipStream_t s = stream_of(stream);
+    double* part = static_cast<double*>(ws);
+    FEQ_LAUNCH("k_dot_f64", k_dot_f64, dim3(kDotGroups), dim3(256), 0, s, a, b, n, part);
+    FEQ_LAUNCH("k_dot_finish", k_dot_finish, dim3(1), dim3(256), 0, s, part, kDotGroups, out);
+    return FEQ_OK;
+}

@@ -586,7 +586,7 @@ def _softmax_scalar_grads(glog, qk, need_dist: bool, need_scale: bool, decay: fl
     d logit / d r = -1/decay, d logit / d log_scale = scale <Q,K> = qk."""
     g_dist = (glog.sum(1) * (-1.0 / decay)).to(rdt) if (need_dist and decay > 0) else None
     # one scalar from E*H products that largely cancel: accumulated in float64
-    g_log = torch.dot(glog.reshape(-1).double(), qk.reshape(-1).double()).to(ldt) if need_scale else None
+    g_log = dot_f64(glog, qk).to(ldt) if need_scale else None
     return g_dist, g_log
 
 
@@ -828,24 +828,67 @@ class EqNormFn(torch.autograd.Function):
         return gx, gw, gb, None, None, None, None
 
 
-_ONES: dict = {}
+def transpose_last2(t: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+    """A contiguous tensor read as (batch, rows, cols) -> a new (batch, cols, rows)
+    tensor (feq_transpose: LDS-tiled, reads and writes in consecutive addresses).
+    The caller reshapes the result.  CPU tensors (host-side tests of the
+    layers' index logic) are transposed by PyTorch."""
+    if not t.is_contiguous():
+        raise RuntimeError("transpose_last2: the input must be contiguous")
+    n = t.numel()
+    if rows * cols == 0 or n % (rows * cols):
+        if n == 0:
+            return torch.empty_like(t)
+        raise RuntimeError(f"transpose_last2: {n} elements are not a batch of {rows} x {cols}")
+    if not t.is_cuda:
+        return t.view(-1, rows, cols).transpose(1, 2).contiguous().view(t.shape)
+    out = torch.empty_like(t)
+    with torch.cuda.device(t.device):
+        rc = N.lib().feq_transpose(N.ptr(t), n // (rows * cols), rows, cols, t.element_size(),
+                                   N.ptr(out), N.stream_ptr(t.device))
+    N.check(rc, "feq_transpose")
+    return out
 
 
 def column_sums(t: torch.Tensor) -> torch.Tensor:
-    """Sum over the rows of a 2-D tensor as a GEMV against a ones vector: one
-    pass over t at memory speed (PyTorch's outer-dimension sum of a tall matrix
-    runs at a fraction of HBM bandwidth on MI355X)."""
-    rows = t.shape[0]
-    if t.dtype not in (torch.float32, torch.float64):
-        return t.sum(0)             # half-precision GEMV is far slower than the reduction
-    if rows == 0:
-        return torch.zeros(t.shape[1], dtype=t.dtype, device=t.device)
-    key = (t.device, t.dtype)
-    ones = _ONES.get(key)
-    if ones is None or ones.numel() < rows:
-        ones = torch.ones(max(rows, 4096), dtype=t.dtype, device=t.device)
-        _ONES[key] = ones
-    return torch.mv(t.t(), ones[:rows])
+    """Sum over the rows of a 2-D tensor (feq_column_sums: one pass at memory
+    speed, partial sums per row chunk combined in a fixed order, so the result
+    is the same on every run).  Half precision, and CPU tensors (host-side
+    tests), go through PyTorch's sum."""
+    if t.dtype not in (torch.float32, torch.float64) or not t.is_cuda:
+        return t.sum(0)
+    ts = t.contiguous()
+    rows, cols = ts.shape
+    out = torch.empty(cols, dtype=ts.dtype, device=ts.device)
+    lib = N.lib()
+    es = ts.element_size()
+    ws = N.workspace(lib.feq_column_sums_workspace(rows, cols, es), ts.device)
+    with torch.cuda.device(ts.device):
+        rc = lib.feq_column_sums(N.ptr(ts), rows, cols, es, N.ptr(out), N.ptr(ws), ws.numel(),
+                                 N.stream_ptr(ts.device))
+    N.check(rc, "feq_column_sums")
+    return out
+
+
+def dot_f64(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """sum(a * b) over all elements, the products and their sum in float64
+    (one scalar from many products that largely cancel; a float32 sum of a
+    million of them loses several digits).  float32 GPU inputs: feq_dot_f64 (no
+    float64 copies); others (float64, CPU tensors): PyTorch in float64.  Returns a float32 0-d tensor
+    for float32 inputs, else float64."""
+    if a.dtype == torch.float32 and b.dtype == torch.float32 and a.is_cuda:
+        a_, b_ = a.detach().contiguous(), b.detach().contiguous()
+        if a_.numel() != b_.numel():
+            raise RuntimeError(f"dot_f64: {a_.numel()} and {b_.numel()} elements")
+        out = torch.empty((), dtype=torch.float32, device=a_.device)
+        lib = N.lib()
+        ws = N.workspace(lib.feq_dot_f64_workspace(), a_.device)
+        with torch.cuda.device(a_.device):
+            rc = lib.feq_dot_f64(N.ptr(a_), N.ptr(b_), a_.numel(), N.ptr(out), N.ptr(ws),
+                                 ws.numel(), N.stream_ptr(a_.device))
+        N.check(rc, "feq_dot_f64")
+        return out
+    return torch.dot(a.reshape(-1).double(), b.reshape(-1).double())
 
 
 class BiasRowsFn(torch.autograd.Function):
@@ -878,7 +921,7 @@ class ScaleFn(torch.autograd.Function):
         gg = None
         if ctx.needs_input_grad[1]:
             # one scalar from many products that largely cancel: accumulated in float64
-            gg = torch.dot(gy.reshape(-1).double(), x.reshape(-1).double()).reshape(g.shape).to(g.dtype)
+            gg = dot_f64(gy, x).reshape(g.shape).to(g.dtype)
         return gx, gg
 
 
@@ -892,7 +935,7 @@ def rows_weight_grad(gy: torch.Tensor, x: torch.Tensor, dtype: torch.dtype,
     s = chunks if rows >= 64 * chunks else 1
     per = rows // s
     head = s * per
-    gyc = gy[:head].reshape(s, per, gy.shape[1]).transpose(1, 2).contiguous()
+    gyc = transpose_last2(gy[:head].contiguous(), per, gy.shape[1]).view(s, gy.shape[1], per)
     xc = x[:head].reshape(s, per, x.shape[1])
     acc = torch.promote_types(dtype, torch.float32)
     gw = column_sums(torch.bmm(gyc, xc).to(acc).reshape(s, -1)).view(gy.shape[1], x.shape[1])
@@ -975,7 +1018,9 @@ class EqLinearFn(torch.autograd.Function):
         if in_cm:
             fd = f.contiguous()
         else:
-            fd = f.reshape(-1, cin, f.shape[-1]).permute(2, 0, 1).contiguous()
+            D = f.shape[-1]
+            fc = f.contiguous()
+            fd = transpose_last2(fc, fc.numel() // D, D).view(D, -1, cin)
         D, rows = fd.shape[0], fd.shape[1]
         w = weight.detach().view(-1, cout, cin)
         out = torch.empty(D, rows, cout, dtype=fd.dtype, device=fd.device)
@@ -989,13 +1034,16 @@ class EqLinearFn(torch.autograd.Function):
                 torch.mm(xk, w[k].t(), out=ok)
         ctx.save_for_backward(fd, weight, bias)
         ctx.meta = (slices, bias_cols, cin, cout, in_cm, out_cm, tuple(f.shape))
-        return out if out_cm else out.permute(1, 2, 0).contiguous()
+        return out if out_cm else transpose_last2(out, D, rows * cout).view(rows, cout, D)
 
     @staticmethod
     def backward(ctx, gy):
         fd, weight, bias = ctx.saved_tensors
         slices, bias_cols, cin, cout, in_cm, out_cm, fshape = ctx.meta
-        gyd = gy.contiguous() if out_cm else gy.permute(2, 0, 1).contiguous()
+        D = fd.shape[0]
+        gyd = gy.contiguous()
+        if not out_cm:
+            gyd = transpose_last2(gyd, gyd.numel() // D, D).view(D, -1, cout)
         w = weight.detach().view(-1, cout, cin)
         gfd = torch.empty_like(fd) if ctx.needs_input_grad[0] else None
         gw = torch.empty_like(w) if ctx.needs_input_grad[1] else None
@@ -1010,7 +1058,7 @@ class EqLinearFn(torch.autograd.Function):
                 gb[:, bias_cols[k]] = column_sums(gk)
         gx = None
         if gfd is not None:
-            gx = gfd if in_cm else gfd.permute(1, 2, 0).contiguous().view(fshape)
+            gx = gfd if in_cm else transpose_last2(gfd, D, gfd.numel() // D).view(fshape)
         return (gx, gw.view_as(weight) if gw is not None else None, gb,
                 None, None, None, None, None, None)
 

@@ -41,6 +41,10 @@
  *   feq_eqnorm_fwd/bwd       EquivariantLayerNorm.forward (norm.py:148-174, RepNorm :51-73)
  *   feq_gate_*               EquivariantGating.forward (flash_eq/layers/gating.py:54-76)
  *                            around its nn.Linear, which stays a library GEMM
+ *   feq_transpose, feq_column_sums, feq_dot_f64
+ *                            PyTorch work inside the reference's modules: layout
+ *                            changes around EquivariantLinear (linear.py:242-268),
+ *                            bias gradients, scalar-parameter gradients
  */
 #ifndef FLASHEQ_H
 #define FLASHEQ_H
@@ -365,6 +369,34 @@ int feq_gate_bwd_x(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t nu
                    int32_t component_major, const float* grad_y, const float* x,
                    const float* lin, const float* norms, const float* grad_norms, float* grad_x,
                    feq_stream_t stream);
+
+/* ---- dense helpers of the node-side layers ------------------------------------
+ * The reference leaves this work to PyTorch inside its modules: its
+ * EquivariantLinear forms all degrees in one broadcast product and a gather
+ * (linear.py:242-268), which this build runs as one GEMM per degree on
+ * component-major (dim, rows, c) tables, moved to and from node-major
+ * (rows, c, dim) by feq_transpose; the bias gradients of its Linear and
+ * EquivariantLinear biases (linear.py:262-266) are autograd's sums over rows;
+ * and the gradients of scalar parameters, EquivariantAttention's log_scale
+ * (attention.py:64-70) and LayerScale's gamma (transformer.py:35-39), are dot
+ * products.  Here each is one deterministic pass, free of memsets (safe in HIP
+ * graphs). */
+
+/* out[b][j][i] = in[b][i][j] for in (batch, rows, cols) of elem_bytes-wide
+ * elements (2, 4 or 8); out must not overlap in. */
+int feq_transpose(const void* in, int64_t batch, int64_t rows, int64_t cols,
+                  int32_t elem_bytes, void* out, feq_stream_t stream);
+/* out[j] = sum over i of in[i][j] for in (rows, cols) float32 (elem_bytes 4,
+ * float32 sums) or float64 (8).  rows = 0 writes zeros.  Partial sums per row
+ * chunk are combined in a fixed order: the result does not depend on timing. */
+size_t feq_column_sums_workspace(int64_t rows, int64_t cols, int32_t elem_bytes);
+int feq_column_sums(const void* in, int64_t rows, int64_t cols, int32_t elem_bytes, void* out,
+                    void* workspace, size_t ws_bytes, feq_stream_t stream);
+/* out[0] = (float) sum of (double) a[i] * b[i], the products and their sum in
+ * float64 in a fixed order (many products that largely cancel). */
+size_t feq_dot_f64_workspace(void);
+int feq_dot_f64(const float* a, const float* b, int64_t n, float* out, void* workspace,
+                size_t ws_bytes, feq_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,6 +1,6 @@
 """Host-side pieces of the node path that are plain PyTorch, checked on the CPU
 in float64: the component-major EquivariantLinear (EqLinearFn, node- and
-component-major inputs and outputs) against the oracle, and the GEMV column
+component-major inputs and outputs) against the oracle, and the column
 sums, chunked weight gradients, bias and LayerScale functions against direct
 formulas, with gradcheck where they carry gradients."""
 import pytest
