@@ -211,6 +211,26 @@ def test_edgewise_parity_log_bins(dev):
     _run_parity(dev, [0, 1, 2], [0, 1], cin=8, cout=8, E=600, seed=3, log=True, rmin=0.1)
 
 
+@pytest.mark.parametrize("lin,cin", [([0, 1, 2], 64), ([0, 1], 32)])
+def test_edgewise_parity_log_bins_split_kernels(dev, monkeypatch, lin, cin):
+    """Logarithmic bins through the split-fp16 kernels (c1/c2 layouts), with
+    distances below min_dist and beyond max_dist; the launch log shows that the
+    split kernels ran."""
+    from flash_eq import _native as NAT
+    _select(monkeypatch, "split")
+    NAT.profile_summary()
+    NAT.profile_enable(True)
+    try:
+        _run_parity(dev, lin, [0, 1, 2], cin=cin, cout=64, E=2003, seed=21, log=True, rmin=0.05)
+        torch.cuda.synchronize()
+        names = NAT.profile_summary()
+    finally:
+        NAT.profile_enable(False)
+    assert "k_ews_fwd" in names, names
+    if cin % 64 == 0:
+        assert "k_ews_bwd_x" in names and "k_ews_bwd_c" in names, names
+
+
 def test_edgewise_grad_wrt_basis(dev):
     _run_parity(dev, [0, 1], [0, 1, 2], cin=4, cout=3, E=200, seed=4, grad_pq=True)
 

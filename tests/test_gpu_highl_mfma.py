@@ -22,15 +22,17 @@ L6 = list(range(7))
 BF16_TOL = 2e-2
 
 
-@pytest.mark.parametrize("C,E,seed", [(64, 300, 1), (128, 97, 2)])
-def test_high_degree_bf16_matches_oracle(dev, C, E, seed):
+@pytest.mark.parametrize("C,E,seed,log", [(64, 300, 1, False), (128, 97, 2, False), (64, 500, 3, True)])
+def test_high_degree_bf16_matches_oracle(dev, C, E, seed, log):
+    """log: logarithmic bins (min_dist 0.5), distances from 0.05 to 12.05."""
     torch.manual_seed(seed)
     rp = fe.Repr(L6, C)
-    layer = fe.EquivariantEdgewiseLinear(rp, rp, num_bins=100).to(dev)
+    kw = dict(log_bins=True, min_dist=0.5) if log else {}
+    layer = fe.EquivariantEdgewiseLinear(rp, rp, num_bins=100, **kw).to(dev)
     g = torch.Generator().manual_seed(seed + 50)
     x = torch.randn(E, C, 49, generator=g).bfloat16()
     d = torch.randn(E, 3, generator=g)
-    r = torch.rand(E, generator=g) * 9.5 + 0.05
+    r = torch.rand(E, generator=g) * (12.0 if log else 9.5) + 0.05
     P = OW.basis(L6, d).float().bfloat16()
     xg = x.to(dev).requires_grad_(True)
     rg = r.to(dev).requires_grad_(True)
