@@ -130,3 +130,37 @@ def test_zero_edges(dev):
     assert gt.shape == T.shape and gt.abs().max() == 0
     assert block_diagonal_cuda(x.float().to(dev), T.float().to(dev), r.float().to(dev), pr, b.p1, b.p2,
                                5).shape == (0, 2, 4)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_sh_scale_zero_like_patched_conv(dev, dtype):
+    """PatchedConvSE3 (patch/_patched_conv.py:93-104) calls the op with sh_scale = 0.
+    For r > 0 the solid-harmonic factor is r / r = 1 (no suppression); at r = 0 the
+    reference's s = 0 / 0 is NaN, and its ipow(s, l_in + l_out) (block_diagonal.cu:202-219)
+    is 1 for l_in + l_out = 0 and NaN otherwise.  With lvals_in = [0] and lvals_out =
+    [0, 1] an r = 0 edge therefore has a finite l = 0 output, a NaN (l = 1, m = 0)
+    output and zero (l = 1, m = +-1) outputs, which no m-block reaches (m-first slots
+    0, 1, 2, 3)."""
+    lin, lout, nb = [0], [0, 1], 12
+    g = torch.Generator().manual_seed(18)
+    b = BD.Binning.linear(nb, 0.0, 10.0, sigma=0.0)
+    E = 200
+    x = torch.randn(E, 3, 1, generator=g, dtype=torch.float64)
+    T = torch.randn(nb + 1, 4, 3, weight_dim(lin, lout), generator=g, dtype=torch.float64)
+    r = torch.rand(E, generator=g, dtype=torch.float64) * 12
+    r[::17] = 0.0
+    pr = fe.ProductRepr(fe.Repr(lin, 3), fe.Repr(lout, 4))
+    y = block_diagonal_cuda(x.to(dev, dtype), T.to(dev, dtype), r.to(dev, dtype), pr, b.p1, b.p2, nb,
+                            sh_scale=0.0).double().cpu()
+    ref = BD.forward(x, T, r, lin, lout, b)
+    zero = r == 0
+    assert torch.isnan(ref[zero][..., 1]).all() and torch.isfinite(ref[zero][..., 0]).all()
+    assert (ref[zero][..., 2:] == 0).all() and not torch.isnan(ref[~zero]).any()
+    assert torch.equal(torch.isnan(y), torch.isnan(ref))
+    fin = torch.isfinite(ref)
+    tol = 1e-12 if dtype == torch.float64 else 1e-5
+    assert ((y[fin] - ref[fin]).abs().max() / ref[fin].abs().max()).item() < tol
+    # r > 0: identical to the layer without suppression at all (s = 1)
+    pos = ~zero
+    ones = BD.forward(x[pos], T, r[pos], lin, lout, BD.Binning.linear(nb, 0.0, 10.0, sigma=1e-30))
+    assert ((y[pos] - ones).abs().max() / ones.abs().max()).item() < tol
