@@ -204,23 +204,61 @@ namespace feq {
 namespace {
 constexpr int kSsqGroups = 1024;
 
+__device__ inline float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ inline float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Sum of y^2 of float32 (BF16 = false) or bfloat16 (BF16 = true) values, each
+// squared and summed in float32: 16-byte loads (4 floats or 8 bf16) when y is
+// aligned, two of them in flight per thread.
+template <bool BF16>
 __global__ void __launch_bounds__(256)
-k_sum_squares(const float* __restrict__ y, int64_t n, float* __restrict__ part) {
+k_sum_squares(const void* __restrict__ yv, int64_t n, float* __restrict__ part) {
     __shared__ float s[4];
-    float acc = 0.0f;
+    constexpr int PER = BF16 ? 8 : 4;     // values per 16-byte load
+    float acc = 0.0f, acc2 = 0.0f;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if ((reinterpret_cast<uintptr_t>(y) & 15u) == 0) {
-        const float4* y4 = reinterpret_cast<const float4*>(y);
-        const int64_t n4 = n / 4;
-        for (int64_t i = t0; i < n4; i += stride) {
-            const float4 v = y4[i];
-            acc += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    auto sq = [](uint4 v) {
+        if constexpr (BF16) {
+            float a = 0.0f;
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float lo = bf16_lo(w[j]), hi = bf16_hi(w[j]);
+                a += lo * lo + hi * hi;
+            }
+            return a;
+        } else {
+            const float a = __uint_as_float(v.x), b = __uint_as_float(v.y);
+            const float c = __uint_as_float(v.z), d = __uint_as_float(v.w);
+            return a * a + b * b + c * c + d * d;
         }
-        for (int64_t i = 4 * n4 + t0; i < n; i += stride) acc += y[i] * y[i];
-    } else {
-        for (int64_t i = t0; i < n; i += stride) acc += y[i] * y[i];
+    };
+    auto scalar = [&](int64_t i) {
+        if constexpr (BF16) {
+            const uint16_t h = static_cast<const uint16_t*>(yv)[i];
+            const float f = __uint_as_float(static_cast<uint32_t>(h) << 16);
+            return f * f;
+        } else {
+            const float f = static_cast<const float*>(yv)[i];
+            return f * f;
+        }
+    };
+    int64_t tail0 = 0;
+    if ((reinterpret_cast<uintptr_t>(yv) & 15u) == 0) {
+        const uint4* y4 = static_cast<const uint4*>(yv);
+        const int64_t n4 = n / PER;
+        int64_t i = t0;
+        for (; i + stride < n4; i += 2 * stride) {
+            const uint4 a = y4[i], b = y4[i + stride];
+            acc += sq(a);
+            acc2 += sq(b);
+        }
+        if (i < n4) acc += sq(y4[i]);
+        tail0 = PER * n4;
     }
+    for (int64_t i = tail0 + t0; i < n; i += stride) acc += scalar(i);
+    acc += acc2;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
     if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = acc;
@@ -242,6 +280,20 @@ extern "C" int feq_sum_squares(const float* y, int64_t n, float* out, void* ws, 
         return fail(FEQ_ERR_WORKSPACE, "sum-of-squares workspace too small");
     hipStream_t s = stream_of(stream);
     float* part = static_cast<float*>(ws);
-    FEQ_LAUNCH("k_sum_squares", k_sum_squares, dim3(kSsqGroups), dim3(256), 0, s, y, n, part);
+    auto kern = k_sum_squares<false>;
+    FEQ_LAUNCH("k_sum_squares", kern, dim3(kSsqGroups), dim3(256), 0, s, y, n, part);
+    return reduce_partials(part, kSsqGroups, 1, out, part + kSsqGroups, s);
+}
+
+extern "C" int feq_sum_squares_bf16(const void* y, int64_t n, float* out, void* ws, size_t ws_bytes,
+                                    feq_stream_t stream) {
+    if (n < 0) return fail(FEQ_ERR_INVALID, "negative length");
+    if (!out || (n > 0 && !y)) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (!ws || ws_bytes < feq_sum_squares_workspace())
+        return fail(FEQ_ERR_WORKSPACE, "sum-of-squares workspace too small");
+    hipStream_t s = stream_of(stream);
+    float* part = static_cast<float*>(ws);
+    auto kern = k_sum_squares<true>;
+    FEQ_LAUNCH("k_sum_squares", kern, dim3(kSsqGroups), dim3(256), 0, s, y, n, part);
     return reduce_partials(part, kSsqGroups, 1, out, part + kSsqGroups, s);
 }

@@ -102,6 +102,7 @@ _SIGS = {
     "feq_gather_rows": ([_P, _I64, _I64, _P, _I64, _P, _P], ctypes.c_int),
     "feq_sum_squares_workspace": ([], _SZ),
     "feq_sum_squares": ([_P, _I64, _P, _P, _SZ, _P], ctypes.c_int),
+    "feq_sum_squares_bf16": ([_P, _I64, _P, _P, _SZ, _P], ctypes.c_int),
     "feq_transpose": ([_P, _I64, _I64, _I64, _I32, _P, _P], ctypes.c_int),
     "feq_column_sums_workspace": ([_I64, _I64, _I32], _SZ),
     "feq_column_sums": ([_P, _I64, _I64, _I32, _P, _P, _SZ, _P], ctypes.c_int),

@@ -1064,18 +1064,22 @@ class EqLinearFn(torch.autograd.Function):
 
 
 class SumSquaresFn(torch.autograd.Function):
-    """sum(y ** 2) of a float32 GPU tensor (feq_sum_squares: deterministic, graph
-    capturable); the gradient 2 y g in one elementwise pass."""
+    """sum(y ** 2) of a float32 or bfloat16 GPU tensor (feq_sum_squares /
+    feq_sum_squares_bf16: float32 sums, deterministic, graph capturable), a
+    float32 scalar; the gradient 2 y g in one elementwise pass, in y's dtype."""
 
     @staticmethod
     def forward(ctx, y):
+        N.require_cuda_tensor(y, "sum-of-squares input")
+        if y.dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError(f"SumSquaresFn: float32 or bfloat16 expected, got {y.dtype}")
         ys = y.contiguous()
         out = torch.empty((), dtype=torch.float32, device=ys.device)
         lib = N.lib()
+        fn = lib.feq_sum_squares if ys.dtype == torch.float32 else lib.feq_sum_squares_bf16
         ws = N.workspace(lib.feq_sum_squares_workspace(), ys.device)
         with torch.cuda.device(ys.device):
-            rc = lib.feq_sum_squares(N.ptr(ys), ys.numel(), N.ptr(out), N.ptr(ws), ws.numel(),
-                                     N.stream_ptr(ys.device))
+            rc = fn(N.ptr(ys), ys.numel(), N.ptr(out), N.ptr(ws), ws.numel(), N.stream_ptr(ys.device))
         N.check(rc, "feq_sum_squares")
         ctx.save_for_backward(ys)
         return out

@@ -235,6 +235,9 @@ int feq_gather_rows(const float* src, int64_t num_src, int64_t row, const int64_
 size_t feq_sum_squares_workspace(void);
 int feq_sum_squares(const float* y, int64_t n, float* out, void* workspace, size_t ws_bytes,
                     feq_stream_t stream);
+/* The same for bfloat16 y (16-bit storage): squares and sums in float32, out float32. */
+int feq_sum_squares_bf16(const void* y, int64_t n, float* out, void* workspace, size_t ws_bytes,
+                         feq_stream_t stream);
 
 /* High-degree form for bfloat16 features (canonical lvals 0..6 in and out,
  * Cin = Cout in {64, 128}, rank 4): x (E, Cin, Din), P, Q, y and the gradients

@@ -26,6 +26,21 @@ def test_sum_squares_matches_torch(dev):
     assert abs(SumSquaresFn.apply(y).item() - (y.double() ** 2).sum().item()) < 1e-3
 
 
+def test_sum_squares_bf16(dev):
+    """bfloat16 input: float32 squares and sums (8 values per 16-byte load), gradient 2y in bf16."""
+    g = torch.Generator().manual_seed(6)
+    for n in (0, 1, 9, 4001, 2 * 1024 * 256 * 8 + 13):
+        y = torch.randn(n, generator=g).to(dev, torch.bfloat16).requires_grad_(True)
+        s = SumSquaresFn.apply(y)
+        assert s.dtype == torch.float32
+        ref = (y.detach().double() ** 2).sum()
+        assert abs(s.item() - ref.item()) <= 1e-6 * max(ref.item(), 1.0)
+        s.backward()
+        assert y.grad.dtype == torch.bfloat16 and torch.equal(y.grad, 2 * y.detach())
+    y = torch.randn(1003, generator=g).to(dev, torch.bfloat16)[3:]   # 6-byte offset: scalar loads
+    assert abs(SumSquaresFn.apply(y).item() - (y.double() ** 2).sum().item()) < 1e-3
+
+
 def test_captured_step_replays_match_eager(dev):
     torch.manual_seed(2)
     rep = fe.Repr([0, 1, 2], 64)
