@@ -59,7 +59,7 @@ def knn_graph(n: int, k: int, box: float, seed: int):
     return coords, src, dst
 
 
-def algorithmic_per_edge(lin, lout, cin, cout, same_pq=True):
+def algorithmic_per_edge(lin, lout, cin, cout, same_pq=True, nodes_per_edge=None):
     """Algorithmic flop and HBM bytes per edge of each fused kernel (fp32).
 
     The mix of one (co, ci) pair costs M real MACs, M = n0_in n0_out +
@@ -67,8 +67,10 @@ def algorithmic_per_edge(lin, lout, cin, cout, same_pq=True):
     S = sum (2l+1)^2 MACs (P and Q are block diagonal over irreps).  Bytes are
     the tensors each kernel must move once: x, P (= Q), r, y for the forward;
     gy, x, P, r, gx for the input-gradient kernel; gy, x, P, r for the
-    channel-pattern-gradient kernel.  The distance-gradient mix is excluded
-    (the benchmark does not differentiate the distances).
+    channel-pattern-gradient kernel.  In the message-passing form
+    (nodes_per_edge = N / E) the input-gradient kernel writes node rows, N / E
+    of them per edge, instead of a row per edge.  The distance-gradient mix is
+    excluded (the benchmark does not differentiate the distances).
     """
     mmax = max(max(lin), max(lout))
     M = 0
@@ -86,7 +88,7 @@ def algorithmic_per_edge(lin, lout, cin, cout, same_pq=True):
     PQ = 4 * din * din + (0 if same_pq else 4 * dout * dout)
     return {
         "k_ews_fwd": (mix + rot, X + PQ + 4 + Y),
-        "k_ews_bwd_x": (mix + rot, Y + X + PQ + 4 + X),
+        "k_ews_bwd_x": (mix + rot, Y + X + PQ + 4 + X * (1.0 if nodes_per_edge is None else nodes_per_edge)),
         "k_ews_bwd_c": (mix, Y + X + PQ + 4),
         "_mix_macs_per_pair": M,
     }
@@ -308,7 +310,7 @@ def build_workload(name: str):
 
         wl.update(step=step, E=E, N=N, equiv=equiv, cpu=None if dtype != torch.float32 else cpu,
                   leaves=[feats] + list(block.parameters()),
-                  work=algorithmic_per_edge([0, 1, 2], [0, 1, 2], 64, 64),
+                  work=algorithmic_per_edge([0, 1, 2], [0, 1, 2], 64, 64, nodes_per_edge=N / E),
                   config=(f"c3: EquivariantTransformerBlock 8 heads [0,1,2]x64, radius-10 graph "
                           f"capped at k=32 on 20k nodes in 60^3, E={E}, fwd+bwd incl. "
                           f"WignerDBasis, {str(dtype).replace('torch.', '')}"),
@@ -369,7 +371,7 @@ def build_workload(name: str):
                               f"({sum(times):.1f} s)"}
 
         wl.update(step=step, E=E, N=N, equiv=None, cpu=cpu, leaves=[feats] + list(model.parameters()),
-                  work=algorithmic_per_edge([0, 1, 2], [0, 1, 2], 64, 64),
+                  work=algorithmic_per_edge([0, 1, 2], [0, 1, 2], 64, 64, nodes_per_edge=N / E),
                   config=(f"c4: EquivariantTransformer 6 layers, in [0,1]x32, hidden [0,1,2]x64, "
                           f"out [0]x8 (x1 is not divisible into 8 heads), 8 heads, random-walk "
                           f"chain of 50k nodes, kNN k=24, E={E}, fwd+bwd incl. WignerDBasis, fp32"),
@@ -668,7 +670,7 @@ def main() -> int:
     torch.cuda.synchronize()
     wigner_ms = wstart.elapsed_time(wstop) / 10
 
-    work = algorithmic_per_edge([0, 1, 2], [0, 1, 2], MULT, MULT)
+    work = algorithmic_per_edge([0, 1, 2], [0, 1, 2], MULT, MULT, nodes_per_edge=N / E)
     mfma_exec = executed_mfma_flop_per_edge([0, 1, 2], [0, 1, 2], MULT, MULT)
     traffic = read_traffic()
     per_kernel = {}
@@ -725,9 +727,11 @@ def main() -> int:
 
     value = E / (ms_per_step * 1e-3)
     # each tensor once per pass: forward (x, P, r, y), backward (gy, x, P, r, gx) and the
-    # radial table read and its gradient written once per step (SURVEY's 12 573 B per edge)
+    # radial table read and its gradient written once per step (SURVEY's 12 573 B per edge;
+    # gx counted per edge, as the reference's layer writes it, for a fixed yardstick)
     table_bytes = 4 * (layer.radial_weights.num_bins + 1) * MULT * MULT * layer.weight_dim
-    step_bytes = work["k_ews_fwd"][1] + work["k_ews_bwd_x"][1] + 2 * table_bytes / E
+    work_ref = algorithmic_per_edge([0, 1, 2], [0, 1, 2], MULT, MULT)
+    step_bytes = work_ref["k_ews_fwd"][1] + work_ref["k_ews_bwd_x"][1] + 2 * table_bytes / E
     step_flop = work["k_ews_fwd"][0] + work["k_ews_bwd_x"][0] + work["k_ews_bwd_c"][0]
     secondary = []
     if not args.no_secondary:

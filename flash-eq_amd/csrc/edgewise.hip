@@ -394,7 +394,7 @@ extern "C" size_t feq_edgewise_workspace(const feq_layout* L, const feq_binning*
                                                 static_cast<size_t>(E) * kw + 64 +
                                                 ew_tail_floats(*b, static_cast<int>(kw), E, groups_for(E), ncc)) + 256
                              : 0;
-    const size_t split = b ? ew_split_bwd_workspace(*L, *b, rank, E) : 0;
+    const size_t split = b ? ew_split_bwd_workspace(*L, *b, rank, E, false) : 0;
     return generic > split ? generic : split;
 }
 
@@ -453,7 +453,7 @@ extern "C" int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32
     const int path = ew_path();
     if (path == kPathSplit && !gP && !gQ) {
         const int rc = ew_split_bwd(*L, *b, rank, E, gy, x, nullptr, 0, P, Q, dist, C, F, gx, gC, gF,
-                                    gdist, ws, ws_bytes, s);
+                                    gdist, nullptr, ws, ws_bytes, s);
         if (rc != -1) return rc;
     }
     // generic kernel: per-workgroup dC partials and the per-edge dF_e, then the
@@ -570,6 +570,45 @@ extern "C" int feq_edgewise_bwd_src(const feq_layout* L, const feq_binning* b, i
     if (!ws || ws_bytes < feq_edgewise_workspace(L, b, rank, E))
         return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
     const int rc = ew_split_bwd(*L, *b, rank, E, gy, x, src, num_src, P, Q, dist, C, F, gx_edges, gC,
-                                gF, gdist, ws, ws_bytes, s);
+                                gF, gdist, nullptr, ws, ws_bytes, s);
+    return rc == -1 ? fail(FEQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned") : rc;
+}
+
+extern "C" size_t feq_edgewise_bwd_src_nodes_workspace(const feq_layout* L, const feq_binning* b,
+                                                       int32_t rank, int64_t E) {
+    if (!L || !b || rank < 1 || E < 0) return 0;
+    return ew_split_bwd_workspace(*L, *b, rank, E, true) + 256;
+}
+
+extern "C" int feq_edgewise_bwd_src_nodes(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                          int64_t E, const float* gy, const float* x, int64_t num_src,
+                                          const int64_t* src, const int32_t* perm_src,
+                                          const int32_t* offsets_src, const float* P, const float* Q,
+                                          const float* dist, const float* C, const float* F,
+                                          float* gx_nodes, float* gC, float* gF, float* gdist,
+                                          void* ws, size_t ws_bytes, feq_stream_t stream) {
+    if (int rc = check_layout(L)) return rc;
+    if (int rc = check_binning(b)) return rc;
+    if (rank < 1) return fail(FEQ_ERR_INVALID, "rank must be positive");
+    if (E < 0 || num_src < 0) return fail(FEQ_ERR_INVALID, "negative edge or node count");
+    if (E > 0x7fffffffLL || num_src > 0x7fffffffLL)
+        return fail(FEQ_ERR_UNSUPPORTED, "more than 2^31-1 edges or nodes");
+    if (!gC || !gF || (num_src > 0 && !gx_nodes))
+        return fail(FEQ_ERR_INVALID, "grad_x_nodes, grad_C and grad_F are required");
+    hipStream_t s = stream_of(stream);
+    if (E == 0) {
+        if (int rc = fill_zero(gF, static_cast<int64_t>(b->num_bins + 1) * rank * L->wdim, s)) return rc;
+        if (int rc = fill_zero(gx_nodes, num_src * L->cin * L->din, s)) return rc;
+        return fill_zero(gC, static_cast<int64_t>(rank) * L->cout * L->cin, s);
+    }
+    if (!gy || !x || !src || !perm_src || !offsets_src || !P || !Q || !dist || !C || !F)
+        return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (!feq_edgewise_src_supported(L, b, rank))
+        return fail(FEQ_ERR_UNSUPPORTED, "no message-passing kernels for this layout");
+    if (!ws || ws_bytes < feq_edgewise_bwd_src_nodes_workspace(L, b, rank, E))
+        return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
+    const NodeScatter ns{perm_src, offsets_src, gx_nodes, nullptr};
+    const int rc = ew_split_bwd(*L, *b, rank, E, gy, x, src, num_src, P, Q, dist, C, F, nullptr, gC,
+                                gF, gdist, &ns, ws, ws_bytes, s);
     return rc == -1 ? fail(FEQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned") : rc;
 }

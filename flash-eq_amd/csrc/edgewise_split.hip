@@ -167,54 +167,42 @@ __device__ __forceinline__ int64_t x_row(const XRows& X, int64_t e) {
     }
 }
 
-// The (kNE, N) block of a (E, N) tensor that starts at edge e0, as float4s:
-// thread t holds float4 q = t + kThreads n of the block.  A full tile is read
-// with 16-byte loads (the block starts at a multiple of 16 edges, so it is
-// 16-byte aligned); the last, partial tile element by element, zero-padded.
-template <int N, int NV>
-__device__ __forceinline__ void load_tile4(const float* __restrict__ src, int64_t e0, int64_t E,
-                                           float4 (&v)[NV]) {
-    constexpr int NQ = kNE * N / 4;
-    const int tid = threadIdx.x;
-    if (e0 + kNE <= E) {
-        const float4* s4 = reinterpret_cast<const float4*>(src + e0 * N);
+__device__ __forceinline__ bool node_crosses_tiles(int b, int e) { return b / kNE != (e - 1) / kNE; }
+
+// Rows e0 + j (j < kNE) of a (E, N) tensor, or rows perm[e0 + j] (PERM):
+// thread t reads elements t % 16 + 16 k of row t / 16 (one index lookup per
+// thread; a row of N floats need not be 16-byte aligned), zeros past the last
+// edge.  (Fewer registers in flight than 16-byte loads of the tile's block.)
+template <int N>
+constexpr int rows_per_thread() { return (N + 15) / 16; }
+
+template <int N, bool PERM>
+__device__ __forceinline__ void load_rows(const float* __restrict__ src, int64_t e0, int64_t E,
+                                          const int32_t* __restrict__ perm,
+                                          float (&v)[rows_per_thread<N>()]) {
+    static_assert(kThreads == 16 * kNE, "16 threads per edge row");
+    const int j = threadIdx.x >> 4, c = threadIdx.x & 15;
+    const bool ok = e0 + j < E;
+    int64_t r = 0;
+    if (ok) {
+        if constexpr (PERM) r = perm[e0 + j]; else r = e0 + j;
+    }
+    const float* row = src + r * N;
 #pragma unroll
-        for (int n = 0; n < NV; ++n) {
-            const int q = tid + kThreads * n;
-            v[n] = q < NQ ? s4[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
-    } else {
-        const int64_t lim = (E - e0) * N;
-#pragma unroll
-        for (int n = 0; n < NV; ++n) {
-            const int q = tid + kThreads * n;
-            float f[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) f[c] = (q < NQ && 4 * q + c < lim) ? src[e0 * N + 4 * q + c] : 0.0f;
-            v[n] = make_float4(f[0], f[1], f[2], f[3]);
-        }
+    for (int k = 0; k < rows_per_thread<N>(); ++k) {
+        const int idx = c + 16 * k;
+        v[k] = (ok && idx < N) ? row[idx] : 0.0f;
     }
 }
 
-// Stores a block read by load_tile4 into LDS with a row stride of S floats per edge.
-template <int N, int NV, int S>
-__device__ __forceinline__ void store_tile4(const float4 (&v)[NV], float* dst) {
-    constexpr int NQ = kNE * N / 4;
-    const int tid = threadIdx.x;
+// Stores rows read by load_rows into LDS with a row stride of S floats.
+template <int N, int S>
+__device__ __forceinline__ void store_rows(const float (&v)[rows_per_thread<N>()], float* dst) {
+    const int j = threadIdx.x >> 4, c = threadIdx.x & 15;
 #pragma unroll
-    for (int n = 0; n < NV; ++n) {
-        const int q = tid + kThreads * n;
-        if (q < NQ) {
-            if constexpr (S == N) {
-                // rows are packed: one 16-byte store (scalar stores at a 16-byte
-                // lane stride would hit a quarter of the banks)
-                *reinterpret_cast<float4*>(dst + 4 * q) = v[n];
-            } else {
-                const float f[4] = {v[n].x, v[n].y, v[n].z, v[n].w};
-#pragma unroll
-                for (int c = 0; c < 4; ++c) dst[((4 * q + c) / N) * S + (4 * q + c) % N] = f[c];
-            }
-        }
+    for (int k = 0; k < rows_per_thread<N>(); ++k) {
+        const int idx = c + 16 * k;
+        if (idx < N) dst[j * S + idx] = v[k];
     }
 }
 
@@ -255,6 +243,67 @@ __device__ __forceinline__ void flush_stage(const float* stage, float* __restric
     }
 }
 
+// The staged tile's rows (nval edges, source nodes node[j], -1 for none) summed
+// per node in tile order: a node within the tile gets its row, a node that
+// crosses a tile boundary a partial row (NodeScatter).
+template <int CH, int D>
+__device__ __forceinline__ void scatter_stage(const float* stage, const int* node, const NodeScatter& NS,
+                                              int64_t tile, int nval) {
+    constexpr int ROW4 = CH * D / 4, SS4 = stage_stride(CH * D) / 4;
+    static_assert((CH * D) % 4 == 0, "rows of whole float4s");
+    const float4* s4 = reinterpret_cast<const float4*>(stage);
+    float4* out4 = reinterpret_cast<float4*>(NS.out);
+    float4* part4 = reinterpret_cast<float4*>(NS.part);
+    for (int q = threadIdx.x; q < ROW4; q += kThreads) {
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        int js = 0;   // first position of the current node's run
+        for (int j = 0; j < nval; ++j) {
+            const float4 v = s4[j * SS4 + q];
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+            const int n = node[j];
+            if (j + 1 < nval && node[j + 1] == n) continue;
+            if (n >= 0) {
+                if (node_crosses_tiles(NS.offsets[n], NS.offsets[n + 1]))
+                    part4[(2 * tile + (js == 0 ? 0 : 1)) * ROW4 + q] = acc;
+                else
+                    out4[static_cast<int64_t>(n) * ROW4 + q] = acc;
+            }
+            acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            js = j + 1;
+        }
+    }
+}
+
+// Rows of the nodes that scatter_stage did not write: the sums of the partial
+// rows of a node that crosses tile boundaries (in tile order), zeros for a node
+// without edges.  One 64-lane workgroup per node.
+__global__ void __launch_bounds__(64)
+k_ews_node_fix(NodeScatter NS, int64_t row4) {
+    const int64_t n = blockIdx.x;
+    const int b = NS.offsets[n], e = NS.offsets[n + 1];
+    if (b < e && !node_crosses_tiles(b, e)) return;
+    const float4* part4 = reinterpret_cast<const float4*>(NS.part);
+    float4* out4 = reinterpret_cast<float4*>(NS.out);
+    for (int64_t q = threadIdx.x; q < row4; q += 64) {
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (b < e) {
+            const int t0 = b / kNE, t1 = (e - 1) / kNE;
+            for (int t = t0; t <= t1; ++t) {
+                const int slot = (t == t0 && b % kNE != 0) ? 1 : 0;
+                const float4 v = part4[(2 * static_cast<int64_t>(t) + slot) * row4 + q];
+                acc.x += v.x;
+                acc.y += v.y;
+                acc.z += v.z;
+                acc.w += v.w;
+            }
+        }
+        out4[n * row4 + q] = acc;
+    }
+}
+
 // Degree of m-first slot j of a canonical representation (4-bit packed table).
 template <int L>
 struct SlotDegPacked {
@@ -283,38 +332,30 @@ __device__ __forceinline__ int std_degree(int d, int L) {
     return l;
 }
 
-// Bit 4 n + c set when component c of float4 n of this thread's share of a
-// (kNE, D, D) basis tile (as read by load_tile4) lies outside the degree blocks.
-// The positions are the same for every tile, so this runs once per launch.
-template <int L, int NV>
-__device__ __forceinline__ unsigned off_block_bits() {
-    static_assert(4 * NV <= 32, "one bit per component");
-    constexpr int D = (L + 1) * (L + 1), N = D * D, NQ = kNE * N / 4;
+// Bit k set when element t % 16 + 16 k of a (D, D) basis row (this thread's
+// share, as read by load_rows) lies outside the degree blocks.  The positions
+// are the same for every tile, so this runs once per launch.
+template <int L>
+__device__ __forceinline__ unsigned off_block_bits_rows() {
+    constexpr int D = (L + 1) * (L + 1), N = D * D;
+    static_assert(rows_per_thread<N>() <= 32, "one bit per element");
     unsigned bits = 0;
 #pragma unroll
-    for (int n = 0; n < NV; ++n) {
-        const int q = threadIdx.x + kThreads * n;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int pos = (4 * q + c) % N;
-            const bool off = q < NQ && std_degree(pos / D, L) != slot_degree<L>(pos % D);
-            bits |= static_cast<unsigned>(off) << (4 * n + c);
-        }
+    for (int k = 0; k < rows_per_thread<N>(); ++k) {
+        const int pos = (threadIdx.x & 15) + 16 * k;
+        const bool off = pos < N && std_degree(pos / D, L) != slot_degree<L>(pos % D);
+        bits |= static_cast<unsigned>(off) << k;
     }
     return bits;
 }
 
-// 1 when an element of this thread's share of a basis tile that lies outside
-// the degree blocks (bits from off_block_bits) is non-zero (-0 counts as zero).
-template <int NV>
-__device__ __forceinline__ int off_block_nonzero(const float4 (&v)[NV], unsigned bits) {
+// 1 when an element of this share that lies outside the degree blocks (bits
+// from off_block_bits_rows) is non-zero (-0 counts as zero).
+template <int NR>
+__device__ __forceinline__ int off_block_nonzero_rows(const float (&v)[NR], unsigned bits) {
     unsigned acc = 0;
 #pragma unroll
-    for (int n = 0; n < NV; ++n) {
-        const float f[4] = {v[n].x, v[n].y, v[n].z, v[n].w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc |= ((bits >> (4 * n + c)) & 1u) ? __float_as_uint(f[c]) : 0u;
-    }
+    for (int k = 0; k < NR; ++k) acc |= ((bits >> k) & 1u) ? __float_as_uint(v[k]) : 0u;
     return (acc & 0x7fffffffu) != 0;
 }
 
@@ -441,8 +482,6 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
     constexpr int KP = K;                                        // rank components per pass
     constexpr int CHUNK = 1024;                                  // bytes per fragment chunk
     constexpr int NPR = (kNE * NC4 + kThreads - 1) / kThreads;   // producer passes
-    constexpr int NPL = (kNE * DIN * DIN / 4 + kThreads - 1) / kThreads;
-    constexpr int NQL = (kNE * DOUT * DOUT / 4 + kThreads - 1) / kThreads;
     static_assert(COUT % 64 == 0 && CIN % 32 == 0 && NC4 <= 64, "unsupported channel counts");
     static_assert((kNE * NC4) % kThreads == 0 || kNE * NC4 < kThreads, "producer split");
 
@@ -461,14 +500,14 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
     const int le = lane & 15, lg = lane >> 4;
-    const unsigned pbits = off_block_bits<LIN, NPL>(), qbits = off_block_bits<LOUT, NQL>();
+    const unsigned pbits = off_block_bits_rows<LIN>(), qbits = off_block_bits_rows<LOUT>();
     const int fkw = tid % KW, fe0 = tid / KW, fl = T::wl_of(fkw % WD);   // radial fill: fixed (k, w)
 
     if (tid < K) sInvK[tid] = Cinv[tid];   // read after the first tile barrier
 
     // global loads of one tile (zeros past the last edge)
     float xr[NPR][4 * DIN];
-    float4 pr[NPL], qr[NQL];
+    float pr[rows_per_thread<DIN * DIN>()], qr[rows_per_thread<DOUT * DOUT>()];
     float rd;
     auto load_tile = [&](int64_t t) {
         const int64_t f0 = t * kNE;
@@ -492,8 +531,8 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
                 for (int v = 0; v < 4 * DIN; ++v) xr[p][v] = 0.0f;
             }
         }
-        load_tile4<DIN * DIN, NPL>(P, f0, E, pr);
-        load_tile4<DOUT * DOUT, NQL>(Q, f0, E, qr);
+        load_rows<DIN * DIN, false>(P, f0, E, nullptr, pr);
+        load_rows<DOUT * DOUT, false>(Q, f0, E, nullptr, qr);
         rd = (tid < kNE && f0 + tid < E) ? dist[f0 + tid] : 1.0f;
     };
 
@@ -543,8 +582,8 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
         const int64_t e0 = tile * kNE;
         __syncthreads();   // the previous tile's readers of every LDS buffer are done
         // (1) P, Q and edge state to LDS; block-structure test of the tile
-        store_tile4<DIN * DIN, NPL, PS>(pr, sP);
-        store_tile4<DOUT * DOUT, NQL, QS>(qr, sQ);
+        store_rows<DIN * DIN, PS>(pr, sP);
+        store_rows<DOUT * DOUT, QS>(qr, sQ);
         if (tid < kNE) {
             EdgeState es;
             es.valid = e0 + tid < E;
@@ -556,7 +595,7 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
             edge_powers(es.s, NSP, sSp + tid * NSP);
         }
         const bool dense =
-            __syncthreads_or(off_block_nonzero(pr, pbits) | off_block_nonzero(qr, qbits)) != 0;
+            __syncthreads_or(off_block_nonzero_rows(pr, pbits) | off_block_nonzero_rows(qr, qbits)) != 0;
 
         // (2) radial functions of the tile (1/scale_k folded in) and fs fragments
         if (fe0 < FG) {
@@ -706,13 +745,15 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
 // summed over the wave's four lane groups with lane swaps (four values per
 // register), unscaled, and summed over the four waves in LDS.  Rotations use the degree blocks when the tile's P
 // and Q have no entry off them; dx is staged in LDS and stored coalesced.
-template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER>
+template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER, bool SCATTER>
 __global__ void __launch_bounds__(kThreads, 2)
 k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
             XRows X, const float* __restrict__ P,
             const float* __restrict__ Q, const float* __restrict__ dist,
             const h8* __restrict__ Cfrag, const float* __restrict__ Cinv,
-            const float* __restrict__ F, float* __restrict__ gx, float* __restrict__ dFe) {
+            const float* __restrict__ F, float* __restrict__ gx, float* __restrict__ dFe,
+            NodeScatter NS) {
+    static_assert(GATHER || !SCATTER, "the per-node sums need the message-passing form");
     using T = Canon<LIN, LOUT>;
     using TG = TermGroups<LIN, LOUT, true>;
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
@@ -727,8 +768,6 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     constexpr int RPW = CIN / 64, NKS = COUT / 32, NC4 = COUT / 4;
     constexpr int CHUNK = 1024;
     constexpr int NPR = (kNE * NC4 + kThreads - 1) / kThreads;
-    constexpr int NPL = (kNE * DIN * DIN / 4 + kThreads - 1) / kThreads;
-    constexpr int NQL = (kNE * DOUT * DOUT / 4 + kThreads - 1) / kThreads;
     constexpr int BREG = 2 * DOUT * NKS * CHUNK > 4 * kNE * stage_stride(CIN * DIN)
                              ? 2 * DOUT * NKS * CHUNK : 4 * kNE * stage_stride(CIN * DIN);
     static_assert(CIN % 64 == 0 && COUT % 32 == 0 && NC4 <= 64, "unsupported channel counts");
@@ -744,11 +783,16 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     float* sEinv = sSp + kNE * NSP;                               // 1 / scale_e
     float* sInvK = sEinv + kNE;
     EdgeState* sE = reinterpret_cast<EdgeState*>(sInvK + K);
+    int* sNode = reinterpret_cast<int*>(sE + kNE);                // source node per position (SCATTER)
+    // tile position -> edge: the identity, or the CSR-by-source permutation
+    auto edge = [&](int64_t j) -> int64_t {
+        if constexpr (SCATTER) return NS.perm[j]; else return j;
+    };
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
     const int le = lane & 15, lg = lane >> 4;
-    const unsigned pbits = off_block_bits<LIN, NPL>(), qbits = off_block_bits<LOUT, NQL>();
+    const unsigned pbits = off_block_bits_rows<LIN>(), qbits = off_block_bits_rows<LOUT>();
     const int fkw = tid % KW, fe0 = tid / KW, fl = T::wl_of(fkw % WD);   // radial fill: fixed (k, w)
     if (tid < K) sInvK[tid] = Cinv[tid];
 
@@ -756,8 +800,10 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     // lane layout, P, Q, distances (zeros past the last edge)
     float gr[NPR][4 * DOUT];
     float xl[RPW][4 * DIN];
-    float4 pr[NPL], qr[NQL];
+    // P and Q of the prefetched tile: each thread's share of one edge row
+    float prs[rows_per_thread<DIN * DIN>()], qrs[rows_per_thread<DOUT * DOUT>()];
     float rd;
+    int nd = -1;
     auto load_tile = [&](int64_t t) {
         const int64_t f0 = t * kNE;
 #pragma unroll
@@ -765,7 +811,7 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             const int q = tid + kThreads * p;
             const int e = q / NC4, c4 = q % NC4;
             if (q < kNE * NC4 && f0 + e < E) {
-                const float4* src = reinterpret_cast<const float4*>(gy + ((f0 + e) * COUT + 4 * c4) * DOUT);
+                const float4* src = reinterpret_cast<const float4*>(gy + (edge(f0 + e) * COUT + 4 * c4) * DOUT);
 #pragma unroll
                 for (int v = 0; v < DOUT; ++v) {
                     const float4 f = src[v];
@@ -781,7 +827,7 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
         }
 #pragma unroll
         for (int j = 0; j < RPW; ++j) {
-            const int64_t row = f0 + le < E ? x_row<GATHER>(X, f0 + le) : -1;
+            const int64_t row = f0 + le < E ? x_row<GATHER>(X, edge(f0 + le)) : -1;
             if (row >= 0) {
                 const float4* src = reinterpret_cast<const float4*>(
                     X.x + (row * CIN + 16 * (wave + 4 * j) + 4 * lg) * DIN);
@@ -798,9 +844,11 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
                 for (int v = 0; v < 4 * DIN; ++v) xl[j][v] = 0.0f;
             }
         }
-        load_tile4<DIN * DIN, NPL>(P, f0, E, pr);
-        load_tile4<DOUT * DOUT, NQL>(Q, f0, E, qr);
-        rd = (tid < kNE && f0 + tid < E) ? dist[f0 + tid] : 1.0f;
+        load_rows<DIN * DIN, SCATTER>(P, f0, E, NS.perm, prs);
+        load_rows<DOUT * DOUT, SCATTER>(Q, f0, E, NS.perm, qrs);
+        if constexpr (SCATTER)
+            nd = (tid < kNE && f0 + tid < E) ? static_cast<int>(x_row<GATHER>(X, edge(f0 + tid))) : -1;
+        rd = (tid < kNE && f0 + tid < E) ? dist[edge(f0 + tid)] : 1.0f;
     };
 
     // gd fragments (producer threads) and fs in the lane layout
@@ -851,8 +899,8 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
         const int64_t e0 = tile * kNE;
         __syncthreads();   // the previous tile's readers of every LDS buffer are done
-        store_tile4<DIN * DIN, NPL, PS>(pr, sP);
-        store_tile4<DOUT * DOUT, NQL, QS>(qr, sQ);
+        store_rows<DIN * DIN, PS>(prs, sP);
+        store_rows<DOUT * DOUT, QS>(qrs, sQ);
         if (tid < kNE) {
             EdgeState es;
             es.valid = e0 + tid < E;
@@ -862,9 +910,10 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             es.s = rd / (rd + B.sh_scale);
             sE[tid] = es;
             edge_powers(es.s, NSP, sSp + tid * NSP);
+            if constexpr (SCATTER) sNode[tid] = nd;
         }
         const bool dense =
-            __syncthreads_or(off_block_nonzero(pr, pbits) | off_block_nonzero(qr, qbits)) != 0;
+            __syncthreads_or(off_block_nonzero_rows(prs, pbits) | off_block_nonzero_rows(qrs, qbits)) != 0;
 
         // radial functions (1/scale_k folded in), gd fragments, fs in lane layout
         if (fe0 < FG) {
@@ -1034,11 +1083,14 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
                 float a = sDF[q];
 #pragma unroll
                 for (int v = 1; v < 4; ++v) a += sDF[v * kNE * KW + q];
-                dFe[e0 * KW + q] = a * sSp[e * NSP + fl];
+                dFe[edge(e0 + e) * KW + fkw] = a * sSp[e * NSP + fl];
             }
         }
         __syncthreads();
-        flush_stage<CIN, DIN>(reinterpret_cast<const float*>(sB), gx + e0 * CIN * DIN, nval);
+        if constexpr (SCATTER)
+            scatter_stage<CIN, DIN>(reinterpret_cast<const float*>(sB), sNode, NS, tile, nval);
+        else
+            flush_stage<CIN, DIN>(reinterpret_cast<const float*>(sB), gx + e0 * CIN * DIN, nval);
     }
 }
 
@@ -1071,8 +1123,6 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     constexpr int NKG = 2 * DIN;                                 // 8-edge groups of the reduction
     constexpr int NKS = (NKG + 3) / 4;                           // 32-steps
     constexpr int ARR = NKG * 256;                               // bytes per (split, block) array
-    constexpr int NPL = (kNE * DIN * DIN / 4 + kThreads - 1) / kThreads;
-    constexpr int NQL = (kNE * DOUT * DOUT / 4 + kThreads - 1) / kThreads;
     static_assert(RB == kThreads / 64 && 4 * CIN <= kThreads && 4 * COUT == kThreads,
                   "unsupported channel counts");
     static_assert(4 * (kNE * PS + kNE * QS) <= 2 * RB * ARR, "P and Q must fit the U buffer");
@@ -1090,7 +1140,7 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int le = lane & 15, lg = lane >> 4;
-    const unsigned pbits = off_block_bits<LIN, NPL>(), qbits = off_block_bits<LOUT, NQL>();
+    const unsigned pbits = off_block_bits_rows<LIN>(), qbits = off_block_bits_rows<LOUT>();
     const int pc = tid >> 2, pq = tid & 3;                        // producer: channel, edge quad
 
     v4f acc_tot[K][CB];
@@ -1120,14 +1170,14 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 #pragma unroll
             for (int d = 0; d < DOUT; ++d) gr[q][d] = gs[d];
         }
-        float4 pr[NPL], qr[NQL];
-        load_tile4<DIN * DIN, NPL>(P, e0, E, pr);
-        load_tile4<DOUT * DOUT, NQL>(Q, e0, E, qr);
+        float pr[rows_per_thread<DIN * DIN>()], qr[rows_per_thread<DOUT * DOUT>()];
+        load_rows<DIN * DIN, false>(P, e0, E, nullptr, pr);
+        load_rows<DOUT * DOUT, false>(Q, e0, E, nullptr, qr);
         const float rd = (tid < kNE && e0 + tid < E) ? dist[e0 + tid] : 1.0f;
 
         __syncthreads();   // the previous tile's readers of every LDS buffer are done
-        store_tile4<DIN * DIN, NPL, PS>(pr, sP);
-        store_tile4<DOUT * DOUT, NQL, QS>(qr, sQ);
+        store_rows<DIN * DIN, PS>(pr, sP);
+        store_rows<DOUT * DOUT, QS>(qr, sQ);
         if (tid < kNE) {
             EdgeState es;
             es.valid = e0 + tid < E && x_row<GATHER>(X, e0 + tid) >= 0;
@@ -1138,7 +1188,7 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             sE[tid] = es;
         }
         const bool dense =
-            __syncthreads_or(off_block_nonzero(pr, pbits) | off_block_nonzero(qr, qbits)) != 0;
+            __syncthreads_or(off_block_nonzero_rows(pr, pbits) | off_block_nonzero_rows(qr, qbits)) != 0;
 
         for (int q = tid; q < kNE * KW; q += kThreads) {
             const int e = q / KW, rest = q % KW;
@@ -1323,7 +1373,7 @@ constexpr size_t ews_bwd_x_lds() {
     constexpr size_t FR = 2 * T::DOUT * (COUT / 32) * 1024, ST = 4 * kNE * stage_stride(CIN * T::DIN);
     return (FR > ST ? FR : ST) +
            4 * (kNE * PS + kNE * QS + kNE * KWS + 4 * kNE * KW + kNE * (LIN + LOUT + 1) + kNE + K) +
-           kNE * sizeof(EdgeState);
+           kNE * sizeof(EdgeState) + kNE * sizeof(int);
 }
 
 template <int CIN, int COUT, int LIN, int LOUT, int K>
@@ -1395,23 +1445,27 @@ int launch_ews_fwd(const feq_binning& B, int64_t E, XRows x, const float* P, con
 }
 
 // Workspace of the split backward: dF_e (E, K Wdim), the per-workgroup dC
-// partials, the tail's histogram partials and sums, the C^T fragments.
+// partials, the tail's histogram partials and sums, the C^T fragments; with
+// the per-node sums, two partial rows per tile.
 template <int CIN, int COUT, int LIN, int LOUT, int K>
-size_t ews_bwd_ws(const feq_binning& B, int64_t E) {
+size_t ews_bwd_ws(const feq_binning& B, int64_t E, bool nodes) {
     using T = Canon<LIN, LOUT>;
     const int64_t ntiles = ceil_div(E, kNE), g = static_cast<int64_t>(ews_cus()) * 2;
     const int G = static_cast<int>(ntiles < g ? ntiles : g);
     const int64_t kw = static_cast<int64_t>(K) * T::WD, ncc = static_cast<int64_t>(K) * COUT * CIN;
+    const size_t part = nodes ? align_up(4 * static_cast<size_t>(ntiles) * 2 * CIN * T::DIN, 256) : 0;
     return align_up(4 * E * kw, 256) + align_up(4 * static_cast<size_t>(G) * ncc, 256) +
            align_up(4 * ew_tail_floats(B, static_cast<int>(kw), E, G, ncc), 256) +
-           ews_cfrag_bytes<CIN, COUT, K>() + 1024;
+           ews_cfrag_bytes<CIN, COUT, K>() + part + 1024;
 }
 
+// ns: NULL for the per-edge input gradient gx; else the per-node sums into
+// ns->out (gx unused; ns->part is carved from the workspace here).
 template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER>
 int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const float* gy,
                    XRows x, const float* P, const float* Q, const float* dist,
                    const float* C, const float* F, float* gx, float* gC, float* gF, float* gdist,
-                   void* ws, size_t ws_bytes, hipStream_t s) {
+                   const NodeScatter* ns, void* ws, size_t ws_bytes, hipStream_t s) {
     using T = Canon<LIN, LOUT>;
     constexpr size_t xlds = ews_bwd_x_lds<CIN, COUT, LIN, LOUT, K>();
     constexpr size_t clds = ews_bwd_c_lds<CIN, COUT, LIN, LOUT, K>();
@@ -1428,13 +1482,33 @@ int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const f
     float* tail = cv.take<float>(ew_tail_floats(B, kw, E, G, ncc));
     h8* frag = cv.take<h8>(static_cast<size_t>(K) * COUT * CIN / 4);
     float* inv = cv.take<float>(K);
+    NodeScatter NS{};
+    if (ns) {
+        NS = *ns;
+        NS.part = cv.take<float>(static_cast<size_t>(ntiles) * 2 * CIN * T::DIN);
+    }
     if (!ws || cv.used > ws_bytes) return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
     auto prep = k_ews_prep<K, CIN, COUT, true>;
     FEQ_LAUNCH("k_ews_prep", prep, dim3(K * CIN / 16), dim3(kThreads), 0, s, C, frag, inv);
-    auto kx = k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, GATHER>;
-    if (int rc = ews_set_lds(reinterpret_cast<const void*>(kx), xlds)) return rc;
-    FEQ_LAUNCH("k_ews_bwd_x", kx, dim3(G), dim3(kThreads), xlds, s, B, E, ntiles, gy, x, P, Q,
-               dist, frag, inv, F, gx, dFe);
+    if constexpr (GATHER) {
+        if (ns) {
+            auto kx = k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true>;
+            if (int rc = ews_set_lds(reinterpret_cast<const void*>(kx), xlds)) return rc;
+            FEQ_LAUNCH("k_ews_bwd_x", kx, dim3(G), dim3(kThreads), xlds, s, B, E, ntiles, gy, x, P, Q,
+                       dist, frag, inv, F, nullptr, dFe, NS);
+            if (x.nsrc > 0)
+                FEQ_LAUNCH("k_ews_node_fix", k_ews_node_fix, dim3(static_cast<unsigned>(x.nsrc)),
+                           dim3(64), 0, s, NS, static_cast<int64_t>(CIN * T::DIN / 4));
+        }
+    } else {
+        if (ns) return fail(FEQ_ERR_INVALID, "per-node sums need the message-passing form");
+    }
+    if (!ns) {
+        auto kx = k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, GATHER, false>;
+        if (int rc = ews_set_lds(reinterpret_cast<const void*>(kx), xlds)) return rc;
+        FEQ_LAUNCH("k_ews_bwd_x", kx, dim3(G), dim3(kThreads), xlds, s, B, E, ntiles, gy, x, P, Q,
+                   dist, frag, inv, F, gx, dFe, NS);
+    }
     auto kc = k_ews_bwd_c<CIN, COUT, LIN, LOUT, K, GATHER>;
     if (int rc = ews_set_lds(reinterpret_cast<const void*>(kc), clds)) return rc;
     FEQ_LAUNCH("k_ews_bwd_c", kc, dim3(G), dim3(kThreads), clds, s, B, E, ntiles, gy, x, P, Q,
@@ -1480,12 +1554,13 @@ size_t ew_split_workspace(const feq_layout& L, int rank) {
 // The split kernels read and write x, P, Q and y with 16-byte accesses.
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-size_t ew_split_bwd_workspace(const feq_layout& L, const feq_binning& B, int rank, int64_t E) {
+size_t ew_split_bwd_workspace(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
+                              bool nodes) {
     if (rank != 4) return 0;
 #define FEQ_WS(ci, co, li, lo)                                                                 \
     if constexpr ((ci) % 64 == 0) {                                                            \
         if (L.cin == ci && L.cout == co && canonical(L, li, lo))                               \
-            return ews_bwd_ws<ci, co, li, lo, 4>(B, E);                                        \
+            return ews_bwd_ws<ci, co, li, lo, 4>(B, E, nodes);                                 \
     }
     FEQ_EWS_SHAPES(FEQ_WS)
 #undef FEQ_WS
@@ -1495,18 +1570,19 @@ size_t ew_split_bwd_workspace(const feq_layout& L, const feq_binning& B, int ran
 int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* gy,
                  const float* x, const int64_t* src, int64_t nsrc, const float* P, const float* Q,
                  const float* dist, const float* C, const float* F, float* gx, float* gC, float* gF,
-                 float* gdist, void* ws, size_t ws_bytes, hipStream_t s) {
-    if (rank != 4 || !gx || !aligned16(gy) || !aligned16(x) || !aligned16(P) || !aligned16(Q) ||
-        !aligned16(gx))
+                 float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, hipStream_t s) {
+    float* gout = ns ? ns->out : gx;
+    if (rank != 4 || !gout || !aligned16(gy) || !aligned16(x) || !aligned16(P) || !aligned16(Q) ||
+        !aligned16(gout) || (ns && !src))
         return -1;
     const XRows X{x, src, nsrc};
 #define FEQ_BWD(ci, co, li, lo)                                                                   \
     if constexpr ((ci) % 64 == 0) {                                                               \
         if (L.cin == ci && L.cout == co && canonical(L, li, lo))                                  \
             return src ? launch_ews_bwd<ci, co, li, lo, 4, true>(L, B, E, gy, X, P, Q, dist, C, F, \
-                                                                 gx, gC, gF, gdist, ws, ws_bytes, s) \
+                                                                 gx, gC, gF, gdist, ns, ws, ws_bytes, s) \
                        : launch_ews_bwd<ci, co, li, lo, 4, false>(L, B, E, gy, X, P, Q, dist, C, F, \
-                                                                  gx, gC, gF, gdist, ws, ws_bytes, s); \
+                                                                  gx, gC, gF, gdist, ns, ws, ws_bytes, s); \
     }
     FEQ_EWS_SHAPES(FEQ_BWD)
 #undef FEQ_BWD

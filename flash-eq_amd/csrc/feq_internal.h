@@ -82,15 +82,34 @@ int ew_tail(const feq_layout& L, const feq_binning& B, int K, int64_t E, const f
             const float* F, const float* dFe, const float* dCp, int groups, int64_t ncc, float* gC,
             float* gF, float* gdist, float* tail, hipStream_t s);
 
+// The input gradient of the message-passing form summed per source node inside
+// the input-gradient kernel.  Tiles walk the edges in source order (perm,
+// offsets: the CSR by source over the nsrc nodes); a tile sums its rows per
+// node in tile order.  A node whose edges lie in one tile gets its row written
+// by that tile; a node whose edges cross a tile boundary leaves one partial row
+// per tile in part[(tile, slot)] (slot 0: the tile's first node, slot 1: its
+// last), summed in tile order by a fix-up kernel, which also zeroes the rows of
+// nodes without edges.  The same bits on every run, no atomics.
+struct NodeScatter {
+    const int32_t* perm;
+    const int32_t* offsets;
+    float* out;    // (nsrc, Cin, Din)
+    float* part;   // (ntiles, 2, Cin, Din), carved from the backward's workspace
+};
+
 // Split-fp16 fast paths (edgewise_split.hip); -1 when the shape has none.
 size_t ew_split_workspace(const feq_layout& L, int rank);
-size_t ew_split_bwd_workspace(const feq_layout& L, const feq_binning& B, int rank, int64_t E);
+// nodes: with the per-node sums (NodeScatter partial rows).
+size_t ew_split_bwd_workspace(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
+                              bool nodes);
 // src (may be NULL): message-passing form, edge e reads row src[e] of the node
-// table x (nsrc rows; indices outside [0, nsrc) read zeros).
+// table x (nsrc rows; indices outside [0, nsrc) read zeros).  ns (may be NULL,
+// needs src): the input gradient summed per source node into ns->out instead
+// of per edge into gx.
 int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* gy,
                  const float* x, const int64_t* src, int64_t nsrc, const float* P, const float* Q,
                  const float* dist, const float* C, const float* F, float* gx, float* gC, float* gF,
-                 float* gdist, void* ws, size_t ws_bytes, hipStream_t s);
+                 float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, hipStream_t s);
 int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
                  const int64_t* src, int64_t nsrc, const float* P, const float* Q, const float* dist,
                  const float* C, const float* F, float* y, void* ws, size_t ws_bytes, hipStream_t s);

@@ -74,6 +74,9 @@ _SIGS = {
                                      ctypes.c_int),
     "feq_edgewise_bwd_src": ([_P, _P, _I32, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P,
                               _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
+    "feq_edgewise_bwd_src_nodes_workspace": ([_P, _P, _I32, _I64], _SZ),
+    "feq_edgewise_bwd_src_nodes": ([_P, _P, _I32, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P,
+                                    _P, _P, _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
     "feq_edgewise_hl_supported": ([_P, _P, _I32], ctypes.c_int),
     "feq_edgewise_hl_workspace": ([_P, _P, _I32, _I64, _I32], _SZ),
     # node-side norms and gating: (lvals, nreps, mult, N, ...)

@@ -107,9 +107,10 @@ class EdgewiseLinearFn(torch.autograd.Function):
 
 class EdgewiseLinearSrcFn(torch.autograd.Function):
     """The message-passing form: y = layer(x[src]) with the gather inside the
-    kernels (``feq_edgewise_fwd_src``); the backward sums the per-edge input
-    gradient over every source node's edges (``perm``, ``offsets``: the CSR by
-    source), so x[src] is never materialised in either direction."""
+    kernels (``feq_edgewise_fwd_src``); the backward sums the input gradient
+    over every source node's edges inside the input-gradient kernel
+    (``feq_edgewise_bwd_src_nodes``, walking ``perm``, ``offsets``: the CSR by
+    source), so neither x[src] nor its gradient is ever materialised."""
 
     @staticmethod
     def forward(ctx, x, src, perm, offsets, P, Q, dist, C, F, layout: N.FeqLayout,
@@ -120,6 +121,9 @@ class EdgewiseLinearSrcFn(torch.autograd.Function):
         rs, Cs, Fs = _f32(dist, "distances"), _f32(C, "channel_patterns"), _f32(F, "radial")
         if xs.dim() != 3 or xs.shape[1:] != (layout.cin, layout.din):
             raise ValueError(f"node_features must be (N, {layout.cin}, {layout.din}), got {tuple(xs.shape)}")
+        if perm.shape != (E,) or offsets.shape != (xs.shape[0] + 1,):
+            raise ValueError(f"the CSR by source must cover {E} edges and {xs.shape[0]} nodes; got "
+                             f"perm {tuple(perm.shape)}, offsets {tuple(offsets.shape)}")
         _check_edgewise_shapes(layout, binning, rank, torch.empty(E, layout.cin, layout.din, device="meta"),
                                Ps, Qs, rs, Cs, Fs)
         si = src.to(torch.int64).contiguous()
@@ -146,29 +150,21 @@ class EdgewiseLinearSrcFn(torch.autograd.Function):
         E = si.shape[0]
         need = ctx.needs_input_grad
         g = gy.detach().to(torch.float32).contiguous()
-        gxe = torch.empty(E, layout.cin, layout.din, dtype=torch.float32, device=dev)
+        gx = torch.empty_like(xs)
         gr = torch.empty_like(rs) if need[6] else None
         gC = torch.empty_like(Cs)
         gF = torch.empty_like(Fs)
         lib = N.lib()
-        ws = N.workspace(lib.feq_edgewise_workspace(N.ctypes.byref(layout), N.ctypes.byref(binning),
-                                                    rank, E), dev)
+        ws = N.workspace(lib.feq_edgewise_bwd_src_nodes_workspace(
+            N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E), dev)
         with torch.cuda.device(dev):
-            rc = lib.feq_edgewise_bwd_src(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
-                                          N.ptr(g) if E else None, N.ptr(xs), xs.shape[0], N.ptr(si),
-                                          N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs), N.ptr(Fs),
-                                          N.ptr(gxe), N.ptr(gC), N.ptr(gF), N.ptr(gr), N.ptr(ws),
-                                          ws.numel(), N.stream_ptr(dev))
-        N.check(rc, "feq_edgewise_bwd_src")
-        gx = None
-        if need[0]:
-            gx = torch.empty_like(xs)
-            row = layout.cin * layout.din
-            with torch.cuda.device(dev):
-                rc = lib.feq_segment_sum(N.ptr(gxe) if E else None, row, N.ptr(perm) if E else None,
-                                         N.ptr(offsets), xs.shape[0], N.ptr(gx), N.stream_ptr(dev))
-            N.check(rc, "feq_segment_sum")
-            gx = gx.to(xdt)
+            rc = lib.feq_edgewise_bwd_src_nodes(
+                N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E, N.ptr(g) if E else None,
+                N.ptr(xs), xs.shape[0], N.ptr(si), N.ptr(perm) if E else None, N.ptr(offsets),
+                N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs), N.ptr(Fs), N.ptr(gx), N.ptr(gC),
+                N.ptr(gF), N.ptr(gr), N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+        N.check(rc, "feq_edgewise_bwd_src_nodes")
+        gx = gx.to(xdt) if need[0] else None
         return (gx, None, None, None, None, None, None if gr is None else gr.to(rdt),
                 gC.to(cdt) if need[7] else None, gF.to(fdt) if need[8] else None, None, None, None)
 

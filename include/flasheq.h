@@ -197,6 +197,25 @@ int feq_edgewise_bwd_src(const feq_layout* L, const feq_binning* b, int32_t rank
                          const float* P, const float* Q, const float* dist, const float* C,
                          const float* F, float* grad_x_edges, float* grad_C, float* grad_F,
                          float* grad_dist, void* workspace, size_t ws_bytes, feq_stream_t stream);
+/* The same backward with the input gradient summed per source node inside the
+ * kernel: grad_x_nodes (num_src, Cin, Din) = the scatter-sum over src of the
+ * per-edge gradient (reference: the backward of the x[src] gather, index_select,
+ * summed with atomics; attention.py:307-310).  perm_src / offsets_src (int32,
+ * E and num_src + 1 entries) are the CSR by source (feq_csr_by_dst with src as
+ * the key); the kernel walks the edges in that order and sums each node's rows
+ * in CSR order (nodes whose edges cross a 16-edge tile boundary through two
+ * partial rows per tile, summed in tile order).  Every node row is written,
+ * zeros for nodes without edges; deterministic.  Workspace:
+ * feq_edgewise_bwd_src_nodes_workspace bytes. */
+size_t feq_edgewise_bwd_src_nodes_workspace(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                            int64_t num_edges);
+int feq_edgewise_bwd_src_nodes(const feq_layout* L, const feq_binning* b, int32_t rank,
+                               int64_t num_edges, const float* grad_y, const float* x,
+                               int64_t num_src, const int64_t* src, const int32_t* perm_src,
+                               const int32_t* offsets_src, const float* P, const float* Q,
+                               const float* dist, const float* C, const float* F,
+                               float* grad_x_nodes, float* grad_C, float* grad_F, float* grad_dist,
+                               void* workspace, size_t ws_bytes, feq_stream_t stream);
 
 /* ---- Wigner-D basis ------------------------------------------------------------
  * plan: host-built per-representation constants (see feq_wigner_plan_size);
