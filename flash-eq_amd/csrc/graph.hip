@@ -209,13 +209,13 @@ __device__ inline float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0
 
 // Sum of y^2 of float32 (BF16 = false) or bfloat16 (BF16 = true) values, each
 // squared and summed in float32: 16-byte loads (4 floats or 8 bf16) when y is
-// aligned, two of them in flight per thread.
+// aligned.
 template <bool BF16>
 __global__ void __launch_bounds__(256)
 k_sum_squares(const void* __restrict__ yv, int64_t n, float* __restrict__ part) {
     __shared__ float s[4];
     constexpr int PER = BF16 ? 8 : 4;     // values per 16-byte load
-    float acc = 0.0f, acc2 = 0.0f;
+    float acc = 0.0f;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     auto sq = [](uint4 v) {
@@ -248,17 +248,10 @@ k_sum_squares(const void* __restrict__ yv, int64_t n, float* __restrict__ part) 
     if ((reinterpret_cast<uintptr_t>(yv) & 15u) == 0) {
         const uint4* y4 = static_cast<const uint4*>(yv);
         const int64_t n4 = n / PER;
-        int64_t i = t0;
-        for (; i + stride < n4; i += 2 * stride) {
-            const uint4 a = y4[i], b = y4[i + stride];
-            acc += sq(a);
-            acc2 += sq(b);
-        }
-        if (i < n4) acc += sq(y4[i]);
+        for (int64_t i = t0; i < n4; i += stride) acc += sq(y4[i]);
         tail0 = PER * n4;
     }
     for (int64_t i = tail0 + t0; i < n; i += stride) acc += scalar(i);
-    acc += acc2;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
     if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = acc;

@@ -1083,4 +1083,5 @@ class SumSquaresFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g):
         (ys,) = ctx.saved_tensors
-        return ys * (2.0 * g)
+        # the scalar in y's dtype: a same-dtype product needs no per-element casts
+        return ys * (2.0 * g).to(ys.dtype)
