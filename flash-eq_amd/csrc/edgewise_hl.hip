@@ -19,13 +19,12 @@
 //   k_hl_dfe      dF_e[k, w] = sum over the terms (o, i, w) of sign <gd_o, C_k fs_i>,
 //                 G_k recomputed on MFMA, the sums over the 128 rows taken with
 //                 lane swaps (lane rows) and a per-wave LDS buffer (waves);
-//   k_hl_u        U_k[e, i, co] = sum over the terms (o, i, w) of sign F_e[k, w] gd[e, o, co];
-//   dC_k = sum over (e, i) of U_k fs^T: a plain GEMM with a reduction over
-//                 E * dim rows, run by rocBLAS as split-K batches whose partials
-//                 are summed in a fixed order.
+//   k_hl_dc       dC_k = sum over (e, i) of U_k fs^T with U_k = M_ek^T gd formed per
+//                 16-edge tile in registers (bf16 dot products) and fed straight
+//                 to the matrix cores; per-workgroup partials summed in a fixed
+//                 order.
 // The binned radial-function and distance gradients reuse the tail of the
 // other fused families (edgewise_tail.hip).
-#include <rocblas/rocblas.h>
 
 #include "ew_canon.h"
 #include "feq_internal.h"
@@ -36,6 +35,8 @@ namespace {
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kT = 256;   // threads per workgroup
 constexpr int kNE = 16;   // edges per MFMA tile (the B columns)
@@ -567,61 +568,223 @@ k_hl_dfe(int64_t E, int64_t ntiles, const __bf16* __restrict__ fsT,
     }
 }
 
-// ---- U for the channel-pattern gradient ---------------------------------------------------
-// U[e, i, k, co] = sum over the terms (o, i, w) of sign F_e[k, w] gd[e, o, co]
-// (bf16), one workgroup per edge; a thread holds the edge's gd column of one
-// channel co in registers and serves 256 / C of the ranks.
-template <int L, int K>
-__global__ void __launch_bounds__(kT)
-k_hl_u(feq_binning B, int C, const __bf16* __restrict__ gdT, const float* __restrict__ dist,
-       const float* __restrict__ F, __bf16* __restrict__ U) {
+// ---- channel-pattern gradient, fused -------------------------------------------------------
+// dC_k[co][ci] = sum over (e, i) of U_k[co][e, i] fs[ci][e, i], U_k = M_ek^T gd:
+//   m = 0:   U(i) = sum_o F_e[k, w0 + o n + i] gd(o)
+//   m >= 1:  U_re(i) = sum_o a gd_re(o) - b gd_im(o),  U_im(i) = sum_o b gd_re(o) + a gd_im(o)
+//            with a = F_e[k, w], b = F_e[k, w + 1], w = w_off(m) + 2 (o n + i)
+// (the transposed mixing of block_diagonal.cu:483-503).  Per 16-edge tile and
+// m-group, gd and fs of the group's slots are staged in LDS edge-minor, gd as
+// (re, im) bf16 pairs (consecutive slots for m = 0); U is formed in registers
+// with v_dot2_f32_bf16 against bf16 coefficient pairs (the pair that multiplies
+// (gd_re, gd_im), or two consecutive o for m = 0), rounded to bf16 and fed to
+// the matrix cores as the A operand (rows co, reduction (slot, edge): a 32-step
+// covers two slots x 16 edges, lane group g serving slot 2 s + g / 2, edges
+// 8 (g % 2) .. + 7), fs as the B operand.  A workgroup has C / 16 waves; wave w
+// owns the output rows 16 w .. 16 w + 15 for every rank, so each gd value read
+// from LDS serves all four ranks.  The dC accumulators live in registers for
+// the whole launch; one partial dC per workgroup.
+template <int C>
+constexpr int dc_threads() { return 4 * C; }
+
+// 16-byte chunk c of LDS row r, swizzled so that 16 consecutive rows read by
+// one 16-lane pass hit distinct banks.
+__device__ __forceinline__ int dc_chunk2(int r, int c) { return c ^ ((r >> 3) & 1); }   // 2 chunks / row
+__device__ __forceinline__ int dc_chunk4(int r, int c) { return c ^ ((r >> 2) & 3); }   // 4 chunks / row
+
+template <int L, int C, int K>
+__global__ void __launch_bounds__(dc_threads<C>(), 1)
+k_hl_dc(feq_binning B, int64_t E, int64_t ntiles, const __bf16* __restrict__ gdT,
+        const __bf16* __restrict__ fsT, const float* __restrict__ dist, const float* __restrict__ F,
+        float* __restrict__ dCp) {
     using H = HL<L>;
-    using TG = TermGroups<L, L, false>;
+    using Cn = Canon<L, L>;
     constexpr int D = H::D, WD = H::WD, KW = K * WD;
-    __shared__ float sFe[KW];
-    const int64_t e = blockIdx.x;
-    const int tid = threadIdx.x;
-    const EdgeBin eb = edge_bin(dist[e], B);
-    for (int q = tid; q < KW; q += kT)
-        sFe[q] = lerp_bins(F[static_cast<int64_t>(eb.lo) * KW + q],
-                           F[static_cast<int64_t>(eb.lo + 1) * KW + q], eb.t);
-    __syncthreads();
-    const __bf16* ge = gdT + e * D * C;
-    __bf16* ue = U + e * D * K * C;
-    // thread (co, h) serves ranks h, h + KS, ... with the gd column of co in registers
-    const int KS = kT / C;
-    const int co = tid % C, h = tid / C;
-    float g[D];
+    constexpr int NT = dc_threads<C>();            // one wave per 16 rows of co
+    constexpr int NCB = C / 16;                    // 16-column blocks of ci
+    constexpr int GMAX = H::GMAX, NPMAX = (GMAX + 1) / 2;
+    constexpr int NQ0 = (L + 2) / 2;               // o-pairs of m-group 0
+    constexpr int CO_MAX = [] {
+        int v = K * (L + 1) * NQ0;                 // m = 0: [k][i][o pair]
+        for (int m = 1; m <= L; ++m) {
+            const int n = L - m + 1;
+            if (K * 2 * n * n > v) v = K * 2 * n * n;   // m >= 1: [k][part][i][o]
+        }
+        return v;
+    }();
+    static_assert(K == 4 && C % 64 == 0 && NT <= 1024, "four ranks; 64 or 128 channels");
+    __shared__ __align__(16) __bf16 sFS[GMAX * C * kNE];             // [slot][ci][edge]
+    __shared__ __align__(16) uint32_t sGD[NPMAX * C * kNE];          // [pair][co][edge] (re | im << 16)
+    __shared__ __align__(16) uint32_t sCo[CO_MAX * kNE];             // coefficient pairs [..][edge]
+    __shared__ __align__(16) __bf16 sFb[KW * kNE];                   // F_e of the tile [k WD + w][edge]
+    __shared__ int slo[kNE];
+    __shared__ float st[kNE];
+
+    const int tid = threadIdx.x, lane = tid & 63, le = lane & 15, lg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lg & 1, half_slot = lg >> 1;
+    const int corow = 16 * wave + le;               // this lane's A-operand row
+
+    v4f acc[K][NCB];
 #pragma unroll
-    for (int o = 0; o < D; ++o) g[o] = static_cast<float>(ge[o * C + co]);
-    for (int k = h; k < K; k += KS) {
-        const float* fk = sFe + k * WD;
-        static_for<D>([&](auto II) __attribute__((always_inline)) {
-            constexpr int i = decltype(II)::value;
-            float u = 0.0f;
-            static_for<TG::count(i)>([&](auto TT) __attribute__((always_inline)) {
-                constexpr Term tm = TG::sorted[TG::start[i] + decltype(TT)::value];
-                const float f = fk[tm.w];
-                u += (tm.neg ? -f : f) * g[tm.o];
-            });
-            ue[(i * K + k) * C + co] = static_cast<__bf16>(u);
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) acc[k][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const int64_t e0 = tile * kNE;
+        __syncthreads();   // the previous tile's readers of slo / st are done
+        if (tid < kNE) {
+            const int64_t e = e0 + tid;
+            const bool valid = e < E;
+            const EdgeBin eb = edge_bin(valid ? dist[e] : 0.0f, B);
+            slo[tid] = valid ? eb.lo : -1;
+            st[tid] = eb.t;
+        }
+        __syncthreads();   // slo / st written
+        // the tile's interpolated radial functions, bf16 (the precision of the
+        // coefficient pairs): each edge's two bin rows read as float4s
+        static_assert(KW % 4 == 0, "radial rows of whole float4s");
+        for (int q = tid; q < kNE * (KW / 4); q += NT) {
+            const int e = q / (KW / 4), c4 = q % (KW / 4);
+            const int lo = slo[e];
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (lo >= 0) {
+                const float4 a = reinterpret_cast<const float4*>(F + static_cast<int64_t>(lo) * KW)[c4];
+                const float4 b = reinterpret_cast<const float4*>(F + static_cast<int64_t>(lo + 1) * KW)[c4];
+                const float t = st[e];
+                v = make_float4(lerp_bins(a.x, b.x, t), lerp_bins(a.y, b.y, t), lerp_bins(a.z, b.z, t),
+                                lerp_bins(a.w, b.w, t));
+            }
+            sFb[(4 * c4) * kNE + e] = static_cast<__bf16>(v.x);
+            sFb[(4 * c4 + 1) * kNE + e] = static_cast<__bf16>(v.y);
+            sFb[(4 * c4 + 2) * kNE + e] = static_cast<__bf16>(v.z);
+            sFb[(4 * c4 + 3) * kNE + e] = static_cast<__bf16>(v.w);
+        }
+        static_for<H::NG>([&](auto MM) __attribute__((always_inline)) {
+            constexpr int m = decltype(MM)::value, n = L - m + 1;
+            constexpr int s0 = H::goff(m), ns = H::gsize(m), wo = Cn::w_off(m);
+            constexpr int NP = m ? n : NQ0;                  // gd pairs of the group
+            constexpr int NKS = (ns + 1) / 2;                // 32-steps of the group
+            __syncthreads();   // sFb written; the previous group's readers are done
+            // fs of the group's slots: sFS[(s C + ci) 16 + e], 16-byte chunks swizzled
+#pragma unroll 2
+            for (int q = tid; q < ns * kNE * (C / 8); q += NT) {
+                const int e = q % kNE, c8 = (q / kNE) % (C / 8), sl = q / (kNE * (C / 8));
+                const bool ok = e0 + e < E;
+                bf8 v = bf8{};
+                if (ok) v = *reinterpret_cast<const bf8*>(fsT + ((e0 + e) * D + s0 + sl) * C + 8 * c8);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int row = sl * C + 8 * c8 + j;
+                    sFS[row * kNE + 8 * dc_chunk2(row, e >> 3) + (e & 7)] = v[j];
+                }
+            }
+            // gd pairs: sGD[(p C + co) 16 + e] = gd(slot 2p) | gd(slot 2p + 1) << 16
+#pragma unroll 2
+            for (int q = tid; q < NP * kNE * (C / 8); q += NT) {
+                const int e = q % kNE, c8 = (q / kNE) % (C / 8), pr = q / (kNE * (C / 8));
+                const bool ok = e0 + e < E;
+                const int sa = 2 * pr, sb = 2 * pr + 1;
+                bf8 a = bf8{}, b = bf8{};
+                if (ok) {
+                    a = *reinterpret_cast<const bf8*>(gdT + ((e0 + e) * D + s0 + sa) * C + 8 * c8);
+                    if (sb < ns) b = *reinterpret_cast<const bf8*>(gdT + ((e0 + e) * D + s0 + sb) * C + 8 * c8);
+                }
+                const u16x8 au = __builtin_bit_cast(u16x8, a), bu = __builtin_bit_cast(u16x8, b);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int row = pr * C + 8 * c8 + j;
+                    const uint32_t bits = static_cast<uint32_t>(au[j]) | (static_cast<uint32_t>(bu[j]) << 16);
+                    sGD[row * kNE + 4 * dc_chunk4(row, e >> 2) + (e & 3)] = bits;
+                }
+            }
+            // coefficient pairs of the interpolated radial functions
+            constexpr int NCO = m ? K * 2 * n * n : K * n * NQ0;
+            for (int q = tid; q < NCO * kNE; q += NT) {
+                const int e = q % kNE, c = q / kNE;
+                auto fe = [&](int k, int w) -> uint32_t {
+                    return __builtin_bit_cast(uint16_t, sFb[(k * WD + w) * kNE + e]);
+                };
+                uint32_t v;
+                if constexpr (m == 0) {
+                    const int pq = c % NQ0, i = (c / NQ0) % n, k = c / (NQ0 * n);
+                    const int oa = 2 * pq, ob = 2 * pq + 1;
+                    v = fe(k, wo + oa * n + i) | ((ob < n ? fe(k, wo + ob * n + i) : 0u) << 16);
+                } else {
+                    const int o = c % n, i = (c / n) % n, part = (c / (n * n)) % 2, k = c / (2 * n * n);
+                    const int w = wo + 2 * (o * n + i);
+                    const uint32_t a = fe(k, w), b = fe(k, w + 1);
+                    // part 0: (a, -b), part 1: (b, a); the sign of a bf16 is its top bit
+                    v = part == 0 ? (a | ((b ^ 0x8000u) << 16)) : (b | (a << 16));
+                }
+                sCo[c * kNE + e] = v;
+            }
+            __syncthreads();
+#pragma unroll 1
+            for (int ks = 0; ks < NKS; ++ks) {
+                const int sl = 2 * ks + half_slot;
+                const bool live = sl < ns;
+                // U of this lane's slot and 8 edges for every rank
+                const int i = m ? sl >> 1 : sl, part = sl & 1;
+                float u[K][8];
+#pragma unroll
+                for (int k = 0; k < K; ++k)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) u[k][j] = 0.0f;
+                if (live) {
+#pragma unroll 1
+                    for (int p = 0; p < NP; ++p) {
+                        const int row = p * C + corow;
+                        const uint4 g0 = *reinterpret_cast<const uint4*>(sGD + row * kNE + 4 * dc_chunk4(row, 2 * h));
+                        const uint4 g1 = *reinterpret_cast<const uint4*>(sGD + row * kNE + 4 * dc_chunk4(row, 2 * h + 1));
+                        const uint32_t g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+                        for (int k = 0; k < K; ++k) {
+                            const int c = m ? ((k * 2 + part) * n + i) * n + p : (k * n + i) * NQ0 + p;
+                            const uint4 c0 = *reinterpret_cast<const uint4*>(sCo + c * kNE + 8 * h);
+                            const uint4 c1 = *reinterpret_cast<const uint4*>(sCo + c * kNE + 8 * h + 4);
+                            const uint32_t cf[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+                            for (int j = 0; j < 8; ++j)
+                                u[k][j] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, cf[j]),
+                                                                          __builtin_bit_cast(bf2, g[j]), u[k][j],
+                                                                          false);
+                        }
+                    }
+                }
+                bf8 a[K];
+#pragma unroll
+                for (int k = 0; k < K; ++k)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) a[k][j] = static_cast<__bf16>(u[k][j]);
+                // fs fragments one column block at a time, each feeding the four ranks
+#pragma unroll
+                for (int cb = 0; cb < NCB; ++cb) {
+                    const int row = sl * C + 16 * cb + le;
+                    const bf8 b = live ? *reinterpret_cast<const bf8*>(sFS + row * kNE + 8 * dc_chunk2(row, h))
+                                       : bf8{};
+#pragma unroll
+                    for (int k = 0; k < K; ++k) acc[k][cb] = mfma_bf(a[k], b, acc[k][cb]);
+                }
+            }
         });
     }
+    // partial dC of this workgroup: lane holds rows 4 lg + r of each 16-row block
+    float* part = dCp + static_cast<int64_t>(blockIdx.x) * K * C * C;
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int co = 16 * wave + 4 * lg + r;
+                part[(k * C + co) * C + 16 * cb + le] = acc[k][cb][r];
+            }
 }
 
 // ---- host side ----------------------------------------------------------------------------
 constexpr int kRank = 4;
-constexpr int kSplitK = 64;              // dC GEMM batches
-constexpr size_t kBlasWs = 32u << 20;    // rocBLAS workspace carved from the caller's
-
-rocblas_handle blas_handle() {
-    static rocblas_handle h[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    if (!h[dev] && rocblas_create_handle(&h[dev]) != rocblas_status_success) h[dev] = nullptr;
-    return h[dev];
-}
-
 int grid_tiles(int64_t ntiles) {
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -636,11 +799,12 @@ struct HLWs {
     float* stage;    // ym (E, D, Cout) or dfs^T (E, D, Cin)
     __bf16* gdT;     // (E, D, Cout)               backward
     float* dFe;      // (E, K WD)                  backward
-    __bf16* U;       // (E, D, K, Cout)            backward
-    float* dCp;      // (kSplitK + 1, K Cout, Cin) backward
+    float* dCp;      // (groups, K Cout, Cin)      backward: per-workgroup dC partials
     float* tail;     // ew_tail workspace          backward
-    void* blas;      // rocBLAS workspace          backward
 };
+
+// Workgroups of the fused channel-pattern gradient: one per CU.
+int dc_groups(int64_t E) { return grid_tiles(ceil_div(E, kNE)); }
 
 template <int L>
 size_t hl_layout(const feq_binning& B, int C, int64_t E, bool backward, HLWs* w, void* base) {
@@ -658,13 +822,12 @@ size_t hl_layout(const feq_binning& B, int C, int64_t E, bool backward, HLWs* w,
     t.fsT = static_cast<__bf16*>(take(2 * static_cast<size_t>(E) * D * C));
     t.stage = static_cast<float*>(take(4 * static_cast<size_t>(E) * D * C));
     if (backward) {
+        const int groups = dc_groups(E);
         t.gdT = static_cast<__bf16*>(take(2 * static_cast<size_t>(E) * D * C));
         t.dFe = static_cast<float*>(take(4 * static_cast<size_t>(E) * KW));
-        t.U = static_cast<__bf16*>(take(2 * static_cast<size_t>(E) * D * kRank * C));
-        t.dCp = static_cast<float*>(take(4 * static_cast<size_t>(kSplitK + 1) * kRank * C * C));
-        t.tail = static_cast<float*>(take(4 * ew_tail_floats(B, KW, E, kSplitK + 1,
+        t.dCp = static_cast<float*>(take(4 * static_cast<size_t>(groups) * kRank * C * C));
+        t.tail = static_cast<float*>(take(4 * ew_tail_floats(B, KW, E, groups,
                                                              static_cast<int64_t>(kRank) * C * C)));
-        t.blas = take(kBlasWs);
     }
     if (w) *w = t;
     return off + 256;
@@ -710,44 +873,6 @@ int hl_fwd(const feq_binning& B, int64_t E, const __bf16* x, const __bf16* P, co
     return hl_rot_out<L, CH>(E, w.stage, Q, dist, B.sh_scale, y, s);
 }
 
-// dC = sum over the E D rows of U^T fs (column-major view: dC^T (C x K C) =
-// fs^T-matrix (C x R) * U-matrix^T), as kSplitK equal batches plus a remainder,
-// then the partials summed in batch order.
-template <int CH>
-int hl_dc(int64_t rows, const __bf16* U, const __bf16* fsT, float* dCp, float* gC, float* tmp,
-          void* blas_ws, hipStream_t s) {
-    rocblas_handle h = blas_handle();
-    if (!h) return fail(FEQ_ERR_HIP, "rocBLAS handle creation failed");
-    if (rocblas_set_stream(h, s) != rocblas_status_success) return fail(FEQ_ERR_HIP, "rocblas_set_stream failed");
-    if (rocblas_set_workspace(h, blas_ws, kBlasWs) != rocblas_status_success)
-        return fail(FEQ_ERR_HIP, "rocblas_set_workspace failed");
-    const int m = CH, n = kRank * CH;
-    const float one = 1.0f, zero = 0.0f;
-    const int64_t ks = rows / kSplitK, rem = rows - ks * kSplitK;
-    const int64_t nout = static_cast<int64_t>(m) * n;
-    int parts = 0;
-    if (ks > 0) {
-        const rocblas_status st = rocblas_gemm_strided_batched_ex(
-            h, rocblas_operation_none, rocblas_operation_transpose, m, n, static_cast<rocblas_int>(ks), &one,
-            fsT, rocblas_datatype_bf16_r, m, ks * m, U, rocblas_datatype_bf16_r, n, ks * n, &zero,
-            dCp, rocblas_datatype_f32_r, m, nout, dCp, rocblas_datatype_f32_r, m, nout, kSplitK,
-            rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-        if (st != rocblas_status_success) return fail(FEQ_ERR_HIP, "rocblas_gemm_strided_batched_ex failed (%d)", static_cast<int>(st));
-        parts = kSplitK;
-    }
-    if (rem > 0) {
-        const int64_t r0 = ks * kSplitK;
-        const rocblas_status st = rocblas_gemm_ex(
-            h, rocblas_operation_none, rocblas_operation_transpose, m, n, static_cast<rocblas_int>(rem), &one,
-            fsT + r0 * m, rocblas_datatype_bf16_r, m, U + r0 * n, rocblas_datatype_bf16_r, n, &zero,
-            dCp + parts * nout, rocblas_datatype_f32_r, m, dCp + parts * nout, rocblas_datatype_f32_r, m,
-            rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-        if (st != rocblas_status_success) return fail(FEQ_ERR_HIP, "rocblas_gemm_ex failed (%d)", static_cast<int>(st));
-        ++parts;
-    }
-    return reduce_partials(dCp, parts, nout, gC, tmp, s);
-}
-
 template <int L, int CH>
 int hl_bwd(const feq_layout& Lay, const feq_binning& B, int64_t E, const __bf16* gy, const __bf16* x,
            const __bf16* P, const __bf16* Q, const float* dist, const float* C, const float* F,
@@ -777,13 +902,15 @@ int hl_bwd(const feq_layout& Lay, const feq_binning& B, int64_t E, const __bf16*
                    w.cfrag, w.stage);
         if (int rc = hl_rot_out<L, CH>(E, w.stage, P, dist, B.sh_scale, gx, s)) return rc;
     }
-    // dC = sum U^T fs
-    auto ku = k_hl_u<L, kRank>;
-    FEQ_LAUNCH("k_hl_u", ku, dim3(E), dim3(kT), 0, s, B, CH, w.gdT, dist, F, w.U);
-    float* tmp = w.tail + align_up(static_cast<size_t>(256) * (B.num_bins + 1) * kRank * H::WD, 64);
-    if (int rc = hl_dc<CH>(E * H::D, w.U, fs, w.dCp, gC, tmp, w.blas, s)) return rc;
-    // binned radial-function gradient and distance gradient (no dC partials left)
-    return ew_tail(Lay, B, kRank, E, dist, F, w.dFe, nullptr, 0, 0, nullptr, gF, gdist, w.tail, s);
+    // dC = sum over (e, i) of (M_ek^T gd) fs^T, per-workgroup partials; the
+    // shared tail sums them in a fixed order with the binned radial-function
+    // gradient and the distance gradient
+    const int groups = dc_groups(E);
+    auto kc = k_hl_dc<L, CH, kRank>;
+    FEQ_LAUNCH("k_hl_dc", kc, dim3(groups), dim3(dc_threads<CH>()), 0, s, B, E, ntiles, w.gdT, fs, dist, F,
+               w.dCp);
+    return ew_tail(Lay, B, kRank, E, dist, F, w.dFe, w.dCp, groups, static_cast<int64_t>(kRank) * CH * CH,
+                   gC, gF, gdist, w.tail, s);
 }
 
 bool canonical_pair(const feq_layout& L, int lmax) {

@@ -265,7 +265,8 @@ int feq_sum_squares_bf16(const void* y, int64_t n, float* out, void* workspace, 
  * flash_eq/layers/linear.py:100-160) to bf16 accuracy: the GEMMs against the
  * channel patterns run on bf16 matrix cores with float32 accumulation.  The
  * backward forms no P/Q gradients.  The workspace holds rotated features and
- * staging (about 24 * E * Din * Cin bytes for the backward). */
+ * staging (about 8 * E * Din * Cin bytes for the backward) and per-workgroup
+ * partials of the channel-pattern gradient. */
 int feq_edgewise_hl_supported(const feq_layout* layout, const feq_binning* binning, int32_t rank);
 size_t feq_edgewise_hl_workspace(const feq_layout* layout, const feq_binning* binning, int32_t rank,
                                  int64_t num_edges, int32_t backward);
