@@ -9,13 +9,15 @@
 // functions F_e (2x2 [[a, b], [-b, a]] blocks on (+m, -m) pairs, block
 // diagonal over m).  At dim 49 an edge's slots no longer fit the registers of
 // the lanes that own it, so the layer runs in stages:
-//   k_hl_rot_in   fs^T[e, j, c] = s^l(j) sum_d x[e, c, d] P[e, d, j]  (bf16, slot-major);
-//                 the same kernel forms gd^T = s^l (gy Q) in the backward;
+//   k_hl_rot_in   fs^T[e, j, c] = s^l(j) sum_d x[e, c, d] P[e, d, j]  (bf16, slot-major),
+//                 one (C x D) x (D x D) bf16 MFMA product per edge; the same
+//                 kernel forms gd^T = s^l (gy Q) in the backward;
 //   k_hl_mix      per 16-edge tile and m-group, G_k = C_k fs on MFMA (bf16 in,
 //                 fp32 out) and the contraction with F_e in registers, one
 //                 source slot at a time: ym[e, o, co] (fp32, slot-major); with
 //                 C_k^T and the transposed terms it forms dfs^T from gd^T;
-//   k_hl_rot_out  y[e, c, d] = sum_j Q[e, d, j] s^l(j) ym[e, j, c] (and dx from dfs);
+//   k_hl_rot_out  y[e, c, d] = sum_j Q[e, d, j] s^l(j) ym[e, j, c] (and dx from dfs),
+//                 per edge on MFMA with ym split into bf16 hi and lo parts;
 //   k_hl_dfe      dF_e[k, w] = sum over the terms (o, i, w) of sign <gd_o, C_k fs_i>,
 //                 G_k recomputed on MFMA, the sums over the 128 rows taken with
 //                 lane swaps (lane rows) and a per-wave LDS buffer (waves);
@@ -37,6 +39,7 @@ typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kT = 256;   // threads per workgroup
 constexpr int kNE = 16;   // edges per MFMA tile (the B columns)
@@ -73,6 +76,11 @@ struct HL {
     }
 };
 
+// s^l for 0 <= l <= 7 from s, s^2 and s^4, without a loop
+__device__ __forceinline__ float pow_sel(float s1, float s2, float s4, int l) {
+    return ((l & 1) ? s1 : 1.0f) * ((l & 2) ? s2 : 1.0f) * ((l & 4) ? s4 : 1.0f);
+}
+
 __device__ __forceinline__ float ipowf_small(float s, int l) {
     float p = 1.0f;
     for (int i = 0; i < l; ++i) p *= s;
@@ -80,176 +88,283 @@ __device__ __forceinline__ float ipowf_small(float s, int l) {
 }
 
 // ---- rotations ------------------------------------------------------------------
-// A workgroup rotates EPB = 256 / C edges; thread (edge el, channel c) holds
-// its channel's D values in registers and walks the degree blocks at compile
-// time, reading the basis entries as LDS broadcasts (every lane of a wave
-// serves the same edge).  Rows move between HBM and LDS with coalesced
-// 16-byte accesses.  Basis rows d are in the standard (l, m) order, columns j
-// in the m-first order (the WignerDBasis layout).  Only the degree blocks of
-// each basis are staged (455 of 2401 entries at L = 6), so several
-// workgroups share a CU; when an edge's basis has a non-zero entry off the
-// blocks, the workgroup sums over all entries, read from global memory.
-
-template <int L>
-struct Blocks {
-    static constexpr int boff(int l) {        // offset of degree l's block in the compact store
-        int o = 0;
-        for (int q = 0; q < l; ++q) o += (2 * q + 1) * (2 * q + 1);
-        return o;
-    }
-    static constexpr int NB = boff(L + 1);
-    // position t of m-first slot j among the slots of its degree
-    static constexpr std::array<int, (L + 1) * (L + 1)> make_tpos() {
-        std::array<int, (L + 1) * (L + 1)> v{};
-        for (int k = 0; k < (L + 1) * (L + 1); ++k) {
-            const int j = DegreeBlocks<L>::slots[k];
-            const int l = SlotL<L>::l[j];
-            v[j] = k - l * l;
-        }
-        return v;
-    }
-    static constexpr std::array<int, (L + 1) * (L + 1)> tpos = make_tpos();
-};
-
-// Stages the degree blocks of the workgroup's EPB bases in LDS, sB[el][boff(l)
-// + r (2l + 1) + t] = R[e, l^2 + r, slots(l)[t]] s_e^l, and the powers s_e^l in
-// pw; returns whether any basis has a non-zero entry off the blocks.
-template <int L, typename T, int EPB>
-__device__ __forceinline__ bool stage_bases(int64_t E, int64_t e0, const T* __restrict__ R,
-                                            const float* __restrict__ dist, float sigma, float* sB,
-                                            float (*pw)[L + 1]) {
-    using H = HL<L>;
-    using BL = Blocks<L>;
-    constexpr int D = H::D;
-    __shared__ int s_lj[D], s_ld[D], s_tp[D], s_bo[L + 1];
-    const int tid = threadIdx.x;
-    if (tid < D) {
-        s_lj[tid] = SlotL<L>::l[tid];
-        s_ld[tid] = H::deg(tid);
-        s_tp[tid] = BL::tpos[tid];
-    }
-    if (tid <= L) s_bo[tid] = BL::boff(tid);
-    if (tid < EPB) {
-        const int64_t e = e0 + tid;
-        const float r = e < E ? dist[e] : 0.0f;
-        const float sv = r / (r + sigma);
-        float p = 1.0f;
-        for (int l = 0; l <= L; ++l) {
-            pw[tid][l] = e < E ? p : 0.0f;
-            p *= sv;
-        }
-    }
-    __syncthreads();
-    int off = 0;
-    const int64_t nvalid = E - e0 < EPB ? E - e0 : EPB;
-    const T* Rb = R + e0 * D * D;
-    for (int q = tid; q < EPB * D * D; q += kT) {
-        const int el = q / (D * D), dj = q - el * (D * D), d = dj / D, j = dj - d * D;
-        const float v = el < nvalid ? static_cast<float>(Rb[q]) : 0.0f;
-        const int lj = s_lj[j], ld = s_ld[d];
-        if (ld != lj) {
-            off |= v != 0.0f;
-        } else {
-            sB[el * BL::NB + s_bo[lj] + (d - lj * lj) * (2 * lj + 1) + s_tp[j]] = v * pw[el][lj];
-        }
-    }
-    return __syncthreads_or(off) != 0;
-}
+// Basis rows d are in the standard (l, m) order, columns j in the m-first order
+// (the WignerDBasis layout); the kernels take any basis, block-diagonal or not.
 
 // out[e, j, c] = s_e^{l(j)} sum_d in[e, c, d] R[e, d, j]   (fs^T = s^l (x P), gd^T = s^l (gy Q))
-template <int L, typename T, int C>
-__global__ void __launch_bounds__(kT)
-k_hl_rot_in(int64_t E, const T* __restrict__ in, const T* __restrict__ R,
+//
+// On the bf16 matrix cores: a wave takes one edge at a time and forms the
+// (C x D) x (D x D) product as (C / 16) x ceil(D / 16) tiles of
+// v_mfma_f32_16x16x32_bf16, the reduction over d padded to whole 32-steps with
+// zeros.  Inputs are bf16 already, so the products are exact and only the
+// fp32 accumulation order differs from a scalar loop; a dense basis costs the
+// same as a block-diagonal one (64 MFMAs per edge at D = 49, C = 128).
+//   A (rows c, reduction d): the edge's (C, D) row copied to LDS with 16-byte
+//     moves; a lane's eight consecutive d of channel c start at element
+//     c D + d0, which is 2-byte aligned only, so each fragment is five dword
+//     reads shifted by v_alignbyte.
+//   B (reduction d, columns j): eight d of basis column j, strided by D in
+//     memory, read from global memory as 16-bit loads (the basis is read once).
+//   D (rows c, columns j): lane holds four consecutive channels of one slot;
+//     staged as [j][c] rows (stride C + 8 against bank conflicts) over the A
+//     copy, then written with 16-byte stores in the slot-major output order.
+template <int L, int C>
+struct RotIn {
+    static constexpr int D = (L + 1) * (L + 1), ROW = C * D;
+    static constexpr int NCB = C / 16, NJB = (D + 15) / 16, KS = (D + 31) / 32;
+    static constexpr int SST = C + 8;                                   // stage row stride
+    static constexpr int BYTES_A = 2 * ROW + 16;                        // + the last fragment's over-read
+    static constexpr int BYTES_S = 2 * D * SST;
+    static constexpr int REG = ((BYTES_A > BYTES_S ? BYTES_A : BYTES_S) + 15) / 16 * 16;
+    static constexpr int EPW = 4;                                       // edges per wave
+};
+
+template <int L, int C>
+__global__ void __launch_bounds__(kT, 2)
+k_hl_rot_in(int64_t E, const __bf16* __restrict__ in, const __bf16* __restrict__ R,
             const float* __restrict__ dist, float sigma, __bf16* __restrict__ out) {
-    using H = HL<L>;
-    using BL = Blocks<L>;
-    constexpr int D = H::D, EPB = kT / C, ROW = C * D;
-    static_assert(kT % C == 0 && (ROW * sizeof(T)) % 16 == 0, "rows of whole 16-byte units");
-    constexpr int VE = 16 / sizeof(T);                 // elements per 16-byte unit
-    __shared__ uint4 sx4[EPB * ROW / VE];              // the rows, [el][c][d]
-    __shared__ float sB[EPB * BL::NB];
-    __shared__ float pw[EPB][L + 1];
-    const T* sx = reinterpret_cast<const T*>(sx4);
-    const int tid = threadIdx.x, el = tid / C, c = tid % C;
-    const int64_t e0 = static_cast<int64_t>(blockIdx.x) * EPB;
-    const int ne = static_cast<int>(E - e0 < EPB ? E - e0 : EPB);
-    for (int q = tid; q < ne * ROW / VE; q += kT) sx4[q] = reinterpret_cast<const uint4*>(in + e0 * ROW)[q];
-    const bool dense = stage_bases<L, T, EPB>(E, e0, R, dist, sigma, sB, pw);
-    if (el >= ne) return;
-    float xr[D];
+    using RI = RotIn<L, C>;
+    constexpr int D = RI::D, ROW = RI::ROW, NCB = RI::NCB, NJB = RI::NJB, KS = RI::KS;
+    constexpr int SST = RI::SST, REG = RI::REG;
+    static_assert(C % 16 == 0 && (2 * ROW) % 16 == 0 && (2 * SST) % 16 == 0, "tile shapes");
+    __shared__ uint4 smem[4 * REG / 16];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int le = lane & 15, lg = lane >> 4;
+    char* reg = reinterpret_cast<char*>(smem) + wave * REG;
+    const uint32_t* rw = reinterpret_cast<const uint32_t*>(reg);
+    __bf16* stage = reinterpret_cast<__bf16*>(reg);
+    int lj[NJB];
 #pragma unroll
-    for (int d = 0; d < D; ++d) xr[d] = static_cast<float>(sx[el * ROW + c * D + d]);
-    __bf16* oe = out + (e0 + el) * ROW + c;
-    if (!dense) {
-        const float* Bl = sB + el * BL::NB;
-        static_for<D>([&](auto JJ) __attribute__((always_inline)) {
-            constexpr int j = decltype(JJ)::value, l = SlotL<L>::l[j], n = 2 * l + 1;
-            constexpr int t = BL::tpos[j], bo = BL::boff(l);
-            float acc = 0.0f;
+    for (int jb = 0; jb < NJB; ++jb) {
+        const int j = 16 * jb + le;
+        lj[jb] = j < D ? SlotL<L>::l[j] : 0;
+    }
+    const int64_t w0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * RI::EPW;
+#pragma unroll 1
+    for (int i = 0; i < RI::EPW; ++i) {
+        const int64_t e = w0 + i;
+        if (e >= E) break;
+        // the edge's input row to LDS, every load issued before the first
+        // write (the previous edge's stage reads are done: a wave's LDS
+        // operations complete in issue order)
+        const uint4* src = reinterpret_cast<const uint4*>(in + e * ROW);
+        constexpr int NQ = (ROW / 8 + 63) / 64;
+        uint4 xv[NQ];
 #pragma unroll
-            for (int r = 0; r < n; ++r) acc += xr[l * l + r] * Bl[bo + r * n + t];
-            oe[j * C] = static_cast<__bf16>(acc);
-        });
-    } else {
-        const T* Re = R + (e0 + el) * D * D;
-        for (int j = 0; j < D; ++j) {
-            const float sc = pw[el][SlotL<L>::l[j]];
-            float acc = 0.0f;
+        for (int n = 0; n < NQ; ++n) xv[n] = src[lane + 64 * n < ROW / 8 ? lane + 64 * n : ROW / 8 - 1];
 #pragma unroll
-            for (int d = 0; d < D; ++d) acc += xr[d] * static_cast<float>(Re[d * D + j]);
-            oe[j * C] = static_cast<__bf16>(acc * sc);
+        for (int n = 0; n < NQ; ++n)
+            if (lane + 64 * n < ROW / 8) reinterpret_cast<uint4*>(reg)[lane + 64 * n] = xv[n];
+        // B fragments: basis column j, rows d0 .. d0 + 7
+        const unsigned short* Rs = reinterpret_cast<const unsigned short*>(R) + e * D * D;
+        bf8 b[NJB][KS];
+#pragma unroll
+        for (int jb = 0; jb < NJB; ++jb)
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const int j = 16 * jb + le, d0 = 32 * s + 8 * lg;
+                u16x8 v;
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                    v[t] = (j < D && d0 + t < D) ? Rs[(d0 + t) * D + j] : static_cast<unsigned short>(0);
+                b[jb][s] = __builtin_bit_cast(bf8, v);
+            }
+        const float r = dist[e];
+        const float sv = r / (r + sigma);
+        asm volatile("" ::: "memory");
+        const float s2 = sv * sv, s4 = s2 * s2;
+        float pw[NJB];
+#pragma unroll
+        for (int jb = 0; jb < NJB; ++jb) pw[jb] = pow_sel(sv, s2, s4, lj[jb]);
+        // A fragments: channel c, elements d0 .. d0 + 7 (zero past D)
+        auto frag_a = [&](int cb, int s) -> bf8 {
+            const int d0 = 32 * s + 8 * lg;
+            uint32_t o[4] = {0u, 0u, 0u, 0u};
+            if (d0 < D) {
+                const int f0 = (16 * cb + le) * D + d0;
+                const uint32_t* w = rw + (f0 >> 1);
+                const uint32_t sh = static_cast<uint32_t>(f0 & 1) * 2u;
+                uint32_t wv[5];
+#pragma unroll
+                for (int k = 0; k < 5; ++k) wv[k] = w[k];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) o[k] = __builtin_amdgcn_alignbyte(wv[k + 1], wv[k], sh);
+                if (32 * s + 32 > D) {   // the step that crosses D: zero elements d >= D
+                    const int nv = D - d0;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        o[k] &= (2 * k < nv ? 0x0000ffffu : 0u) | (2 * k + 1 < nv ? 0xffff0000u : 0u);
+                }
+            }
+            return __builtin_bit_cast(bf8, (u32x4{o[0], o[1], o[2], o[3]}));
+        };
+        bf8 a[NCB][KS];
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+            for (int s = 0; s < KS; ++s) a[cb][s] = frag_a(cb, s);
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+            for (int jb = 0; jb < NJB; ++jb) {
+                v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int s = 0; s < KS; ++s) acc = mfma_bf(a[cb][s], b[jb][s], acc);
+                const int j = 16 * jb + le;
+                if (j < D) {
+                    bf4 v;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) v[q] = static_cast<__bf16>(acc[q] * pw[jb]);
+                    *reinterpret_cast<bf4*>(stage + j * SST + 16 * cb + 4 * lg) = v;
+                }
+            }
+        asm volatile("" ::: "memory");
+        uint4* dst = reinterpret_cast<uint4*>(out + e * ROW);
+#pragma unroll
+        for (int n = 0; n < NQ; ++n) {
+            const int q = lane + 64 * n;
+            if (q < ROW / 8) {
+                const int j = q / (C / 8), c8 = q - j * (C / 8);
+                dst[q] = *reinterpret_cast<const uint4*>(stage + j * SST + 8 * c8);
+            }
         }
+        asm volatile("" ::: "memory");
     }
 }
 
 // out[e, c, d] = sum_j R[e, d, j] s_e^{l(j)} in[e, j, c]   (y = (s^l ym) Q^T, dx = (s^l dfs) P^T)
-template <int L, typename T, int C>
-__global__ void __launch_bounds__(kT)
-k_hl_rot_out(int64_t E, const float* __restrict__ in, const T* __restrict__ R,
-             const float* __restrict__ dist, float sigma, T* __restrict__ out) {
-    using H = HL<L>;
-    using BL = Blocks<L>;
-    constexpr int D = H::D, EPB = kT / C, ROW = C * D;
-    static_assert(kT % C == 0 && (ROW * sizeof(T)) % 16 == 0, "rows of whole 16-byte units");
-    constexpr int VE = 16 / sizeof(T);
-    __shared__ T so[EPB * ROW];                        // the output rows, [el][c][d]
-    __shared__ float sB[EPB * BL::NB];
-    __shared__ float pw[EPB][L + 1];
-    const int tid = threadIdx.x, el = tid / C, c = tid % C;
-    const int64_t e0 = static_cast<int64_t>(blockIdx.x) * EPB;
-    const int ne = static_cast<int>(E - e0 < EPB ? E - e0 : EPB);
-    float v[D];
-    const int64_t ec = e0 + (el < ne ? el : 0);
+//
+// On the bf16 matrix cores, one edge per wave at a time: D[c][d] =
+// sum_j v[j][c] R[d][j] with v = s^l in (float32) split into bf16 hi and lo
+// parts (two products per step, 16 significant bits: far below the bf16
+// rounding of the output) and the basis rows exact in bf16.
+//   A (rows c, reduction j): eight j of channel c, strided by C floats in
+//     memory, read as float32 and split;
+//   B (reduction j, columns d): eight consecutive j of basis row d (2-byte
+//     aligned), dword reads shifted by v_alignbyte;
+//   D: lane holds slot d of four channels, staged in LDS as the output's
+//     [c][d] rows and written with 16-byte stores.
+template <int L, int C>
+__global__ void __launch_bounds__(kT, 2)
+k_hl_rot_out(int64_t E, const float* __restrict__ in, const __bf16* __restrict__ R,
+             const float* __restrict__ dist, float sigma, __bf16* __restrict__ out) {
+    using RI = RotIn<L, C>;
+    constexpr int D = RI::D, ROW = RI::ROW, NCB = RI::NCB, NDB = RI::NJB, KS = RI::KS;
+    constexpr int REG = (2 * ROW + 15) / 16 * 16, NQ = (ROW / 8 + 63) / 64;
+    static_assert(C % 16 == 0 && (2 * ROW) % 16 == 0, "tile shapes");
+    __shared__ uint4 smem[4 * REG / 16];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int le = lane & 15, lg = lane >> 4;
+    char* reg = reinterpret_cast<char*>(smem) + wave * REG;
+    __bf16* stage = reinterpret_cast<__bf16*>(reg);
+    int lj[KS][8];
 #pragma unroll
-    for (int j = 0; j < D; ++j) v[j] = in[(ec * D + j) * C + c];     // coalesced over c
-    const bool dense = stage_bases<L, T, EPB>(E, e0, R, dist, sigma, sB, pw);
-    T* ol = so + el * ROW + c * D;
-    if (!dense) {
-        const float* Bl = sB + el * BL::NB;
-        static_for<D>([&](auto DD) __attribute__((always_inline)) {
-            constexpr int d = decltype(DD)::value, l = H::deg(d), n = 2 * l + 1, r = d - l * l;
-            constexpr int bo = BL::boff(l);
-            float acc = 0.0f;
-            static_for<n>([&](auto TT) __attribute__((always_inline)) {
-                constexpr int t = decltype(TT)::value;
-                constexpr int j = DegreeBlocks<L>::slots[l * l + t];
-                acc += Bl[bo + r * n + t] * v[j];
-            });
-            ol[d] = static_cast<T>(acc);
-        });
-    } else {
-        const T* Re = R + ec * D * D;
-        for (int d = 0; d < D; ++d) {
-            float acc = 0.0f;
+    for (int s = 0; s < KS; ++s)
 #pragma unroll
-            for (int j = 0; j < D; ++j)
-                acc += static_cast<float>(Re[d * D + j]) * pw[el][SlotL<L>::l[j]] * v[j];
-            ol[d] = static_cast<T>(acc);
+        for (int t = 0; t < 8; ++t) {
+            const int j = 32 * s + 8 * lg + t;
+            lj[s][t] = j < D ? SlotL<L>::l[j] : 0;
         }
+    const uint32_t* Rw = reinterpret_cast<const uint32_t*>(R);
+    const int64_t w0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * RI::EPW;
+#pragma unroll 1
+    for (int i = 0; i < RI::EPW; ++i) {
+        const int64_t e = w0 + i;
+        if (e >= E) break;
+        // B fragments: basis row d, elements j0 .. j0 + 7 (zero past D); only
+        // the dwords that hold needed elements are read
+        bf8 b[NDB][KS];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const int d = 16 * db + le, j0 = 32 * s + 8 * lg;
+                // dword k is read when it holds an element j0 .. min(j0 + 8, D) - 1
+                // of a real row, at a clamped index otherwise (no branch)
+                const bool row = d < D && j0 < D;
+                const int64_t f0 = (e * D + (row ? d : 0)) * D + (row ? j0 : 0);
+                const int odd = static_cast<int>(f0 & 1);
+                const int nv = !row ? 0 : (D - j0 < 8 ? D - j0 : 8);
+                uint32_t wv[5];
+#pragma unroll
+                for (int k = 0; k < 5; ++k) {
+                    const bool need = 2 * k <= odd + nv - 1;
+                    const uint32_t u = Rw[need ? (f0 >> 1) + k : (f0 >> 1)];
+                    wv[k] = need ? u : 0u;
+                }
+                uint32_t o[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    o[k] = __builtin_amdgcn_alignbyte(wv[k + 1], wv[k], static_cast<uint32_t>(2 * odd));
+                    o[k] &= (2 * k < nv ? 0x0000ffffu : 0u) | (2 * k + 1 < nv ? 0xffff0000u : 0u);
+                }
+                b[db][s] = __builtin_bit_cast(bf8, (u32x4{o[0], o[1], o[2], o[3]}));
+            }
+        const float r = dist[e];
+        const float sv = r / (r + sigma);
+        const float s2 = sv * sv, s4 = s2 * s2;
+        float pw[KS][8];
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int t = 0; t < 8; ++t) pw[s][t] = pow_sel(sv, s2, s4, lj[s][t]);
+        // A operand values: channel c of slots j (clamped into the row; the
+        // slots past D are masked to zero bits below, so no branch holds a
+        // load back), double-buffered one channel block ahead
+        const float* ie = in + e * D * C;
+        float raw[2][KS][8];
+        auto load_a = [&](int cb, float (&dst)[KS][8]) {
+#pragma unroll
+            for (int s = 0; s < KS; ++s)
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const int j = 32 * s + 8 * lg + t;
+                    dst[s][t] = ie[(j < D ? j : D - 1) * C + 16 * cb + le];
+                }
+        };
+        load_a(0, raw[0]);
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) {
+            if (cb + 1 < NCB) load_a(cb + 1, raw[(cb + 1) & 1]);
+            bf8 ah[KS], al[KS];
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const int j = 32 * s + 8 * lg + t;
+                    float u = raw[cb & 1][s][t];
+                    if (32 * s + 32 > D) u = __uint_as_float(__float_as_uint(u) & (j < D ? ~0u : 0u));
+                    const float v = u * pw[s][t];
+                    const __bf16 h = static_cast<__bf16>(v);
+                    ah[s][t] = h;
+                    al[s][t] = static_cast<__bf16>(v - static_cast<float>(h));
+                }
+            }
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int s = 0; s < KS; ++s) {
+                    acc = mfma_bf(ah[s], b[db][s], acc);
+                    acc = mfma_bf(al[s], b[db][s], acc);
+                }
+                const int d = 16 * db + le;
+                if (d < D) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) stage[(16 * cb + 4 * lg + q) * D + d] = static_cast<__bf16>(acc[q]);
+                }
+            }
+        }
+        asm volatile("" ::: "memory");
+        uint4* dst = reinterpret_cast<uint4*>(out + e * ROW);
+#pragma unroll
+        for (int n = 0; n < NQ; ++n) {
+            const int q = lane + 64 * n;
+            if (q < ROW / 8) dst[q] = reinterpret_cast<const uint4*>(reg)[q];
+        }
+        asm volatile("" ::: "memory");
     }
-    __syncthreads();
-    for (int q = tid; q < ne * ROW / VE; q += kT)
-        reinterpret_cast<uint4*>(out + e0 * ROW)[q] = reinterpret_cast<const uint4*>(so)[q];
 }
 
 // ---- constant GEMM operand --------------------------------------------------------
@@ -836,16 +951,18 @@ size_t hl_layout(const feq_binning& B, int C, int64_t E, bool backward, HLWs* w,
 template <int L, int C>
 int hl_rot_in(int64_t E, const __bf16* in, const __bf16* R, const float* dist, float sigma,
               __bf16* out, hipStream_t s) {
-    auto kern = k_hl_rot_in<L, __bf16, C>;
-    FEQ_LAUNCH("k_hl_rot_in", kern, dim3(ceil_div(E, kT / C)), dim3(kT), 0, s, E, in, R, dist, sigma, out);
+    auto kern = k_hl_rot_in<L, C>;
+    FEQ_LAUNCH("k_hl_rot_in", kern, dim3(ceil_div(E, 4 * RotIn<L, C>::EPW)), dim3(kT), 0, s, E, in, R,
+               dist, sigma, out);
     return FEQ_OK;
 }
 
 template <int L, int C>
 int hl_rot_out(int64_t E, const float* in, const __bf16* R, const float* dist, float sigma,
                __bf16* out, hipStream_t s) {
-    auto kern = k_hl_rot_out<L, __bf16, C>;
-    FEQ_LAUNCH("k_hl_rot_out", kern, dim3(ceil_div(E, kT / C)), dim3(kT), 0, s, E, in, R, dist, sigma, out);
+    auto kern = k_hl_rot_out<L, C>;
+    FEQ_LAUNCH("k_hl_rot_out", kern, dim3(ceil_div(E, 4 * RotIn<L, C>::EPW)), dim3(kT), 0, s, E, in, R,
+               dist, sigma, out);
     return FEQ_OK;
 }
 
@@ -974,8 +1091,8 @@ extern "C" int feq_edgewise_hl_fwd(const feq_layout* L, const feq_binning* b, in
     if (E == 0) return FEQ_OK;
     if (E > 0x7fffffffLL) return fail(FEQ_ERR_UNSUPPORTED, "more than 2^31-1 edges");
     if (!x || !P || !Q || !dist || !C || !F || !y || !ws) return fail(FEQ_ERR_INVALID, "NULL pointer");
-    if (!al16(x) || !al16(ws) || !al16(fs_out))
-        return fail(FEQ_ERR_INVALID, "x, fs_out and the workspace must be 16-byte aligned");
+    if (!al16(x) || !al16(y) || !al16(ws) || !al16(fs_out))
+        return fail(FEQ_ERR_INVALID, "x, y, fs_out and the workspace must be 16-byte aligned");
     hipStream_t s = stream_of(stream);
     const auto* xb = static_cast<const __bf16*>(x);
     const auto* Pb = static_cast<const __bf16*>(P);
@@ -1006,8 +1123,8 @@ extern "C" int feq_edgewise_hl_bwd(const feq_layout* L, const feq_binning* b, in
         return fill_zero(gC, static_cast<int64_t>(rank) * L->cout * L->cin, s);
     }
     if (!gy || !x || !P || !Q || !dist || !C || !F || !ws) return fail(FEQ_ERR_INVALID, "NULL pointer");
-    if (!al16(gy) || !al16(x) || !al16(ws) || !al16(fs_in))
-        return fail(FEQ_ERR_INVALID, "gy, x, fs_in and the workspace must be 16-byte aligned");
+    if (!al16(gy) || !al16(x) || !al16(gx) || !al16(ws) || !al16(fs_in))
+        return fail(FEQ_ERR_INVALID, "gy, x, gx, fs_in and the workspace must be 16-byte aligned");
     const auto* gyb = static_cast<const __bf16*>(gy);
     const auto* xb = static_cast<const __bf16*>(x);
     const auto* Pb = static_cast<const __bf16*>(P);
