@@ -460,7 +460,7 @@ extern "C" int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32
     // fixed-order binning and partial sums of the shared tail (no atomics)
     const int kw = rank * L->wdim;
     if (!ew_tail_supported(*b, kw))
-        return fail(FEQ_ERR_UNSUPPORTED, "radial-function histogram does not fit LDS");
+        return fail(FEQ_ERR_UNSUPPORTED, "empty radial-function rows");
     const size_t lds = bwd_lds(*L, rank);
     if (int rc = ensure_lds(reinterpret_cast<const void*>(&k_ew_bwd), lds)) return rc;
     const int G = groups_for(E);

@@ -1,8 +1,8 @@
-// Tail of the fused backward passes, shared by the split-fp16 and fp32-MFMA
-// families: the binned radial-function gradient from the per-edge gradient
-// dF_e (lo/hi split with the interpolation weights, as the reference's table
-// gradient, block_diagonal.cu:990-1036), the distance gradient, and the
-// deterministic sums of per-workgroup partials.
+// Tail of the fused backward passes, shared by the edgewise families: the
+// binned radial-function gradient from the per-edge gradient dF_e (lo/hi split
+// with the interpolation weights, as the reference's table gradient,
+// block_diagonal.cu:990-1036), the distance gradient, and the deterministic
+// sums of per-workgroup partials.
 #include "feq_internal.h"
 
 #include <algorithm>
@@ -34,7 +34,7 @@ __device__ void weight_lsum(const feq_layout& L, int* fl) {
 }
 
 // Binned radial-function gradient: dF[lo] += (1 - t) dF_e and dF[lo + 1] += t dF_e.
-// Every wave owns a private LDS histogram and a contiguous run of edges, and
+// Two forms.  Narrow rows (a few private histograms fit LDS): every wave owns a private LDS histogram and a contiguous run of edges, and
 // adds into it in edge order (plain read-add-write; LDS float atomics are
 // several times slower), so every cell's summation order is fixed and the
 // result is deterministic.  Lane c serves the columns c, c + 64, ... of an edge.  Edges
@@ -43,8 +43,6 @@ __device__ void weight_lsum(const feq_layout& L, int* fl) {
 // partial histogram per workgroup (its waves' histograms summed in wave order).
 constexpr int kHistBatch = 16;
 
-// A launch bins the column window [cw0, cw0 + cwn) of the kw-wide rows (the
-// whole row when it fits LDS) into the same columns of its partial.
 __global__ void __launch_bounds__(kThreads)
 k_ewm_hist(feq_binning B, int kw_row, int cw0, int kw, int64_t E, int64_t per_wave,
            const float* __restrict__ dist, const float* __restrict__ dFe,
@@ -129,6 +127,112 @@ k_ewm_hist(feq_binning B, int kw_row, int cw0, int kw, int64_t E, int64_t per_wa
     }
 }
 
+// Wide rows (no room for several histograms in LDS): the edges are grouped by lower bin (a stable CSR by bin from the library's
+// radix sort) and the sorted positions cut into tiles of kBinTile.  Per bin n
+// the kernels form S0[n] = sum (1 - t) dF_e and S1[n] = sum t dF_e over the
+// bin's edges in sorted order; dF[b] = S0[b] + S1[b - 1].  A workgroup (tile,
+// column block) walks its positions in order and closes every run of equal
+// bins: a bin inside the tile is written whole, a bin that crosses a tile
+// boundary leaves a partial row per tile (slot 0 for the tile's first run,
+// slot 1 for its last), summed in tile order by the output kernel.  No
+// atomics and no LDS histogram: every cell's summation order is fixed, so the
+// result is deterministic, and the work spreads over tiles x column blocks
+// whatever the row width.
+constexpr int kBinTile = 256;     // sorted positions per tile
+constexpr int kBinBatch = 8;      // loads in flight per thread
+
+__global__ void k_ewm_keys(feq_binning B, int64_t E, const float* __restrict__ dist,
+                           int64_t* __restrict__ lo) {
+    const int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (e < E) lo[e] = bin_index(dist[e], B);
+}
+
+__device__ __forceinline__ bool bin_crosses_tiles(int b, int e) { return b / kBinTile != (e - 1) / kBinTile; }
+
+// grid (tiles, column blocks of blockDim.x); S holds S0 rows [0, nb) then S1 rows.
+__global__ void __launch_bounds__(kThreads)
+k_ewm_binsum(feq_binning B, int kw, int64_t E, const float* __restrict__ dist,
+             const float* __restrict__ dFe, const int32_t* __restrict__ perm,
+             const int32_t* __restrict__ offsets, float* __restrict__ S, float* __restrict__ part) {
+    __shared__ int spe[kBinTile], slo[kBinTile];
+    __shared__ float st[kBinTile];
+    const int nb = B.num_bins;
+    const int64_t tile = blockIdx.x;
+    const int64_t p0 = tile * kBinTile;
+    const int np = static_cast<int>(E - p0 < kBinTile ? E - p0 : kBinTile);
+    for (int j = threadIdx.x; j < np; j += blockDim.x) {
+        const int e = perm[p0 + j];
+        const EdgeBin eb = edge_bin(dist[e], B);
+        spe[j] = e;
+        slo[j] = eb.lo;
+        st[j] = eb.t;
+    }
+    __syncthreads();
+    const int c = blockIdx.y * blockDim.x + threadIdx.x;
+    if (c >= kw) return;
+    float a0 = 0.0f, a1 = 0.0f;
+    int js = 0;   // first position of the current run
+    for (int j0 = 0; j0 < np; j0 += kBinBatch) {
+        float v[kBinBatch];
+#pragma unroll
+        for (int q = 0; q < kBinBatch; ++q) {
+            const int j = j0 + q < np ? j0 + q : np - 1;
+            v[q] = dFe[static_cast<int64_t>(spe[j]) * kw + c];
+        }
+#pragma unroll
+        for (int q = 0; q < kBinBatch; ++q) {
+            const int j = j0 + q;
+            if (j >= np) break;
+            const float t = st[j];
+            a0 += (1.0f - t) * v[q];
+            a1 += t * v[q];
+            const int n = slo[j];
+            if (j + 1 < np && slo[j + 1] == n) continue;
+            if (bin_crosses_tiles(offsets[n], offsets[n + 1])) {
+                const int64_t row = (2 * tile + (js == 0 ? 0 : 1)) * 2;
+                part[row * kw + c] = a0;
+                part[(row + 1) * kw + c] = a1;
+            } else {
+                S[static_cast<int64_t>(n) * kw + c] = a0;
+                S[static_cast<int64_t>(nb + n) * kw + c] = a1;
+            }
+            a0 = a1 = 0.0f;
+            js = j + 1;
+        }
+    }
+}
+
+// S0 (comp 0) or S1 (comp 1) of bin n at column c: zero for an empty bin, the
+// tile partials in tile order for a bin that crosses tiles, else the row
+// k_ewm_binsum wrote.
+__device__ __forceinline__ float bin_sum(const float* __restrict__ S, const float* __restrict__ part,
+                                         const int32_t* __restrict__ offsets, int nb, int kw, int n,
+                                         int comp, int c) {
+    const int b = offsets[n], e = offsets[n + 1];
+    if (b >= e) return 0.0f;
+    if (!bin_crosses_tiles(b, e)) return S[static_cast<int64_t>(comp * nb + n) * kw + c];
+    const int t0 = b / kBinTile, t1 = (e - 1) / kBinTile;
+    float acc = 0.0f;
+    for (int t = t0; t <= t1; ++t) {
+        const int slot = (t == t0 && b % kBinTile != 0) ? 1 : 0;
+        acc += part[((2 * static_cast<int64_t>(t) + slot) * 2 + comp) * kw + c];
+    }
+    return acc;
+}
+
+// dF[b] = S0[b] + S1[b - 1], b = 0 .. nb; grid (nb + 1, column blocks).
+__global__ void __launch_bounds__(kThreads)
+k_ewm_binout(feq_binning B, int kw, const float* __restrict__ S, const float* __restrict__ part,
+             const int32_t* __restrict__ offsets, float* __restrict__ gF) {
+    const int nb = B.num_bins, b = blockIdx.x;
+    const int c = blockIdx.y * blockDim.x + threadIdx.x;
+    if (c >= kw) return;
+    float v = 0.0f;
+    if (b < nb) v = bin_sum(S, part, offsets, nb, kw, b, 0, c);
+    if (b > 0) v += bin_sum(S, part, offsets, nb, kw, b - 1, 1, c);
+    gF[static_cast<int64_t>(b) * kw + c] = v;
+}
+
 // Distance gradient from dF_e, one thread per edge (sums in slot order):
 // dr = dt/dr sum (F[hi] - F[lo]) dF_e + [l > 0 pairs] sigma/(r(r+sigma)) sum (l_i+l_o) F_e dF_e.
 __global__ void __launch_bounds__(kThreads)
@@ -201,57 +305,101 @@ namespace {
 constexpr int kHistGroups = 256;           // histogram workgroups (fixed: the order is set by E alone)
 constexpr size_t kHistLds = 160 * 1024;
 
-// Waves (private histograms) per histogram workgroup; 0: one does not fit LDS.
+// Waves (private histograms) per histogram workgroup.
 int hist_waves(const feq_binning& B, int kw) {
     const size_t hbytes = 4 * static_cast<size_t>(B.num_bins + 1) * kw;
     const size_t w = kHistLds / hbytes;
     return static_cast<int>(w < 4 ? w : 4);
 }
 
-// Column window of the histogram: the whole row when one histogram fits LDS,
-// else the widest multiple of 128 columns that does (0: not even 128 fit).
-int hist_window(const feq_binning& B, int kw) {
-    if (hist_waves(B, kw) >= 1) return kw;
-    const int w = static_cast<int>(kHistLds / (4 * static_cast<size_t>(B.num_bins + 1))) / 128 * 128;
+// The LDS histograms serve rows for which at least two fit a workgroup's LDS;
+// wider rows take the sorted-bin form.
+bool use_hist(const feq_binning& B, int kw) { return hist_waves(B, kw) >= 2; }
+
+// Workspace of the binned gradient, carved from `tail` in this order.
+struct BinWs {
+    int64_t* keys;
+    int32_t* perm;
+    int32_t* offsets;
+    void* csr;
+    float* S;
+    float* part;
+    float* tmp;
+    size_t bytes;
+};
+
+BinWs bin_ws(const feq_binning& B, int kw, int64_t E, int groups, int64_t ncc, void* base) {
+    Carver cv(base);
+    BinWs w{};
+    const int64_t hsz = (B.num_bins + 1) * static_cast<int64_t>(kw);
+    size_t tmp = reduce_tmp_floats(groups, ncc) + 1;
+    if (use_hist(B, kw)) {
+        // per-workgroup histogram partials
+        w.part = cv.take<float>(static_cast<size_t>(kHistGroups) * hsz);
+        tmp = std::max(tmp, reduce_tmp_floats(kHistGroups, hsz));
+    } else {
+        const int64_t ntiles = ceil_div(E, kBinTile);
+        w.keys = cv.take<int64_t>(E);
+        w.perm = cv.take<int32_t>(E);
+        w.offsets = cv.take<int32_t>(B.num_bins + 1);
+        w.csr = cv.take<char>(feq_csr_workspace(E, B.num_bins));
+        w.S = cv.take<float>(2 * static_cast<size_t>(B.num_bins) * kw);
+        w.part = cv.take<float>(4 * static_cast<size_t>(ntiles) * kw);
+    }
+    w.tmp = cv.take<float>(tmp);
+    w.bytes = cv.used + 256;
     return w;
 }
 
 }  // namespace
 
-bool ew_tail_supported(const feq_binning& B, int kw) { return hist_window(B, kw) >= 1; }
+bool ew_tail_supported(const feq_binning& B, int kw) { return B.num_bins >= 1 && kw >= 1; }
 
 size_t ew_tail_floats(const feq_binning& B, int kw, int64_t E, int groups, int64_t ncc) {
-    (void)E;
-    const int64_t hsz = (B.num_bins + 1) * static_cast<int64_t>(kw);
-    const size_t tmp = std::max(reduce_tmp_floats(groups, ncc), reduce_tmp_floats(kHistGroups, hsz));
-    return align_up(static_cast<size_t>(kHistGroups) * hsz, 64) + align_up(tmp, 64) + 64;
+    return (bin_ws(B, kw, E, groups, ncc, nullptr).bytes + 3) / 4;
 }
 
 int ew_tail(const feq_layout& L, const feq_binning& B, int K, int64_t E, const float* dist,
             const float* F, const float* dFe, const float* dCp, int groups, int64_t ncc, float* gC,
             float* gF, float* gdist, float* tail, hipStream_t s) {
     const int kw = K * L.wdim;
-    const int win = hist_window(B, kw);
-    if (win < 1) return fail(FEQ_ERR_UNSUPPORTED, "radial-function histogram does not fit LDS");
-    const int64_t hsz = (B.num_bins + 1) * static_cast<int64_t>(kw);
-    float* hp = tail;
-    float* tmp = tail + align_up(static_cast<size_t>(kHistGroups) * hsz, 64);
-    FEQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_ewm_hist),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kHistLds)));
-    for (int c0 = 0; c0 < kw; c0 += win) {
-        const int cn = kw - c0 < win ? kw - c0 : win;
-        const int waves = hist_waves(B, cn);
-        const size_t hlds = 4 * static_cast<size_t>(waves) * (B.num_bins + 1) * cn;
+    const int nb = B.num_bins;
+    if (!ew_tail_supported(B, kw)) return fail(FEQ_ERR_UNSUPPORTED, "empty radial-function rows");
+    if (E == 0) {
+        if (groups > 0)
+            if (int rc = reduce_partials(dCp, groups, ncc, gC, tail, s)) return rc;
+        return fill_zero(gF, static_cast<int64_t>(nb + 1) * kw, s);
+    }
+    const BinWs w = bin_ws(B, kw, E, groups, ncc, tail);
+    if (use_hist(B, kw)) {
+        FEQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_ewm_hist),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kHistLds)));
+        const int waves = hist_waves(B, kw);
+        const size_t hlds = 4 * static_cast<size_t>(waves) * (nb + 1) * kw;
         const int64_t per_wave = ceil_div(E, static_cast<int64_t>(kHistGroups) * waves);
-        FEQ_LAUNCH("k_ewm_hist", k_ewm_hist, dim3(kHistGroups), dim3(64 * waves), hlds, s, B, kw,
-                   c0, cn, E, per_wave, dist, dFe, hp);
+        FEQ_LAUNCH("k_ewm_hist", k_ewm_hist, dim3(kHistGroups), dim3(64 * waves), hlds, s, B, kw, 0, kw,
+                   E, per_wave, dist, dFe, w.part);
+        if (int rc = reduce_partials(w.part, kHistGroups, (nb + 1) * static_cast<int64_t>(kw), gF, w.tmp, s))
+            return rc;
+    } else {
+        FEQ_LAUNCH("k_ewm_keys", k_ewm_keys, dim3(ceil_div(E, kThreads)), dim3(kThreads), 0, s, B, E,
+                   dist, w.keys);
+        if (int rc = feq_csr_by_dst(w.keys, E, nb, w.perm, w.offsets, w.csr, feq_csr_workspace(E, nb),
+                                    reinterpret_cast<feq_stream_t>(s)))
+            return rc;
+        const int bt = kw < kThreads ? static_cast<int>(ceil_div(kw, 64)) * 64 : kThreads;
+        const unsigned cbs = static_cast<unsigned>(ceil_div(kw, bt));
+        FEQ_LAUNCH("k_ewm_binsum", k_ewm_binsum, dim3(static_cast<unsigned>(ceil_div(E, kBinTile)), cbs),
+                   dim3(bt), 0, s, B, kw, E, dist, dFe, w.perm, w.offsets, w.S, w.part);
+        FEQ_LAUNCH("k_ewm_binout", k_ewm_binout, dim3(static_cast<unsigned>(nb + 1), cbs), dim3(bt), 0, s,
+                   B, kw, w.S, w.part, w.offsets, gF);
     }
     if (gdist)
         FEQ_LAUNCH("k_ewm_dr", k_ewm_dr, dim3(ceil_div(E, kThreads)), dim3(kThreads),
                    sizeof(int) * L.wdim, s, L, B, K, E, dist, F, dFe, gdist);
     if (groups > 0)
-        if (int rc = reduce_partials(dCp, groups, ncc, gC, tmp, s)) return rc;
-    return reduce_partials(hp, kHistGroups, hsz, gF, tmp, s);
+        if (int rc = reduce_partials(dCp, groups, ncc, gC, w.tmp, s)) return rc;
+    return FEQ_OK;
 }
 
 }  // namespace feq
