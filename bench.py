@@ -264,7 +264,8 @@ def build_workload(name: str):
             vec = xyz[graph.src] - xyz[graph.dst]
             dist = vec.norm(dim=-1)
             (P,) = basis(vec)
-            out = block(P.to(dtype), P.to(dtype), feats, dist.to(dtype), graph)
+            Pd = P.to(dtype)
+            out = block(Pd, Pd, feats, dist.to(dtype), graph)
             loss = SumSquaresFn.apply(out)
             loss.backward()
             return loss

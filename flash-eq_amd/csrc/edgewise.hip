@@ -418,7 +418,7 @@ extern "C" int feq_edgewise_fwd(const feq_layout* L, const feq_binning* b, int32
     const int path = ew_path();
     if (path == kPathSplit) {
         const int rc = ew_split_fwd(*L, *b, rank, E, x, nullptr, 0, P, Q, dist, C, F, y, ws,
-                                    ws_bytes, stream_of(stream));
+                                    ws_bytes, false, stream_of(stream));
         if (rc != -1) return rc;
     }
     const size_t lds = fwd_lds(*L, rank);
@@ -453,7 +453,7 @@ extern "C" int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32
     const int path = ew_path();
     if (path == kPathSplit && !gP && !gQ) {
         const int rc = ew_split_bwd(*L, *b, rank, E, gy, x, nullptr, 0, P, Q, dist, C, F, gx, gC, gF,
-                                    gdist, nullptr, ws, ws_bytes, s);
+                                    gdist, nullptr, ws, ws_bytes, false, s);
         if (rc != -1) return rc;
     }
     // generic kernel: per-workgroup dC partials and the per-edge dF_e, then the
@@ -533,7 +533,17 @@ extern "C" int feq_edgewise_fwd_src(const feq_layout* L, const feq_binning* b, i
                                     const float* P, const float* Q, const float* dist,
                                     const float* C, const float* F, float* y, void* ws,
                                     size_t ws_bytes, feq_stream_t stream) {
+    return feq_edgewise_fwd_src_ex(L, b, rank, E, x, num_src, src, P, Q, dist, C, F, y, 0, ws,
+                                   ws_bytes, stream);
+}
+
+extern "C" int feq_edgewise_fwd_src_ex(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                       int64_t E, const float* x, int64_t num_src, const int64_t* src,
+                                       const float* P, const float* Q, const float* dist,
+                                       const float* C, const float* F, float* y, int32_t flags,
+                                       void* ws, size_t ws_bytes, feq_stream_t stream) {
     if (int rc = check_layout(L)) return rc;
+    if (flags & ~FEQ_EW_HALF_ACCURACY) return fail(FEQ_ERR_INVALID, "unknown flags 0x%x", flags);
     if (int rc = check_binning(b)) return rc;
     if (rank < 1) return fail(FEQ_ERR_INVALID, "rank must be positive");
     if (E < 0 || num_src < 0) return fail(FEQ_ERR_INVALID, "negative edge or node count");
@@ -543,7 +553,7 @@ extern "C" int feq_edgewise_fwd_src(const feq_layout* L, const feq_binning* b, i
     if (!feq_edgewise_src_supported(L, b, rank))
         return fail(FEQ_ERR_UNSUPPORTED, "no message-passing kernels for this layout");
     const int rc = ew_split_fwd(*L, *b, rank, E, x, src, num_src, P, Q, dist, C, F, y, ws, ws_bytes,
-                                stream_of(stream));
+                                (flags & FEQ_EW_HALF_ACCURACY) != 0, stream_of(stream));
     return rc == -1 ? fail(FEQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned") : rc;
 }
 
@@ -570,7 +580,7 @@ extern "C" int feq_edgewise_bwd_src(const feq_layout* L, const feq_binning* b, i
     if (!ws || ws_bytes < feq_edgewise_workspace(L, b, rank, E))
         return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
     const int rc = ew_split_bwd(*L, *b, rank, E, gy, x, src, num_src, P, Q, dist, C, F, gx_edges, gC,
-                                gF, gdist, nullptr, ws, ws_bytes, s);
+                                gF, gdist, nullptr, ws, ws_bytes, false, s);
     return rc == -1 ? fail(FEQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned") : rc;
 }
 
@@ -587,7 +597,21 @@ extern "C" int feq_edgewise_bwd_src_nodes(const feq_layout* L, const feq_binning
                                           const float* dist, const float* C, const float* F,
                                           float* gx_nodes, float* gC, float* gF, float* gdist,
                                           void* ws, size_t ws_bytes, feq_stream_t stream) {
+    return feq_edgewise_bwd_src_nodes_ex(L, b, rank, E, gy, x, num_src, src, perm_src, offsets_src, P,
+                                         Q, dist, C, F, gx_nodes, gC, gF, gdist, 0, ws, ws_bytes,
+                                         stream);
+}
+
+extern "C" int feq_edgewise_bwd_src_nodes_ex(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                             int64_t E, const float* gy, const float* x,
+                                             int64_t num_src, const int64_t* src,
+                                             const int32_t* perm_src, const int32_t* offsets_src,
+                                             const float* P, const float* Q, const float* dist,
+                                             const float* C, const float* F, float* gx_nodes,
+                                             float* gC, float* gF, float* gdist, int32_t flags,
+                                             void* ws, size_t ws_bytes, feq_stream_t stream) {
     if (int rc = check_layout(L)) return rc;
+    if (flags & ~FEQ_EW_HALF_ACCURACY) return fail(FEQ_ERR_INVALID, "unknown flags 0x%x", flags);
     if (int rc = check_binning(b)) return rc;
     if (rank < 1) return fail(FEQ_ERR_INVALID, "rank must be positive");
     if (E < 0 || num_src < 0) return fail(FEQ_ERR_INVALID, "negative edge or node count");
@@ -609,6 +633,6 @@ extern "C" int feq_edgewise_bwd_src_nodes(const feq_layout* L, const feq_binning
         return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
     const NodeScatter ns{perm_src, offsets_src, gx_nodes, nullptr};
     const int rc = ew_split_bwd(*L, *b, rank, E, gy, x, src, num_src, P, Q, dist, C, F, nullptr, gC,
-                                gF, gdist, &ns, ws, ws_bytes, s);
+                                gF, gdist, &ns, ws, ws_bytes, (flags & FEQ_EW_HALF_ACCURACY) != 0, s);
     return rc == -1 ? fail(FEQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned") : rc;
 }

@@ -466,7 +466,7 @@ __device__ __forceinline__ void edge_powers(float s, int n, float* out) {
 // are issued, then the Q rotation, staged in LDS and stored with coalesced
 // 16-byte stores.  Row strides of the per-edge LDS blocks are odd, so the 16
 // edges of a wave's lanes hit distinct banks.
-template <int CIN, int COUT, int LIN, int LOUT, int K, int OCC, bool GATHER>
+template <int CIN, int COUT, int LIN, int LOUT, int K, int OCC, bool GATHER, bool LP>
 __global__ void __launch_bounds__(kThreads, OCC)
 k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
           const float* __restrict__ P, const float* __restrict__ Q,
@@ -566,12 +566,16 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         _Float16 h, l;
-                        split_f16s(fs[r][i], sc, h, l);
+                        if constexpr (LP) {
+                            h = static_cast<_Float16>(fs[r][i] * sc);
+                        } else {
+                            split_f16s(fs[r][i], sc, h, l);
+                            lv[r] = l;
+                        }
                         hv[r] = h;
-                        lv[r] = l;
                     }
                     *reinterpret_cast<h4*>(base + (i * NKS) * CHUNK) = hv;
-                    *reinterpret_cast<h4*>(base + ((DIN + i) * NKS) * CHUNK) = lv;
+                    if constexpr (!LP) *reinterpret_cast<h4*>(base + ((DIN + i) * NKS) * CHUNK) = lv;
                 }
             }
         }
@@ -638,7 +642,7 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
                         const h8* src =
                             cfr + 2 * ((((k0 + kk) * (COUT / 16) + wave + 4 * j) * NKS + ks) * 64 + lane);
                         ahi[j][kk][ks] = src[0];
-                        alo[j][kk][ks] = src[1];
+                        if constexpr (!LP) alo[j][kk][ks] = src[1];
                     }
             // Software pipeline over the slots: iteration i issues the MFMAs of
             // slot i + 1 (B fragments loaded one iteration earlier) and the
@@ -651,7 +655,8 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks) {
                     bh[buf][ks] = *reinterpret_cast<const h8*>(sB + (slot * NKS + ks) * CHUNK + myslot);
-                    bl[buf][ks] = *reinterpret_cast<const h8*>(sB + ((DIN + slot) * NKS + ks) * CHUNK + myslot);
+                    if constexpr (!LP)
+                        bl[buf][ks] = *reinterpret_cast<const h8*>(sB + ((DIN + slot) * NKS + ks) * CHUNK + myslot);
                 }
             };
             auto mfma_slot = [&](int buf, int ab) {
@@ -665,8 +670,10 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
                     for (int j = 0; j < RPW; ++j)
 #pragma unroll
                         for (int kk = 0; kk < KP; ++kk) {
-                            acc[ab][j][kk] = mfma_h(alo[j][kk][ks], bh[buf][ks], acc[ab][j][kk]);
-                            acc[ab][j][kk] = mfma_h(ahi[j][kk][ks], bl[buf][ks], acc[ab][j][kk]);
+                            if constexpr (!LP) {
+                                acc[ab][j][kk] = mfma_h(alo[j][kk][ks], bh[buf][ks], acc[ab][j][kk]);
+                                acc[ab][j][kk] = mfma_h(ahi[j][kk][ks], bl[buf][ks], acc[ab][j][kk]);
+                            }
                             acc[ab][j][kk] = mfma_h(ahi[j][kk][ks], bh[buf][ks], acc[ab][j][kk]);
                         }
             };
@@ -745,7 +752,7 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
 // summed over the wave's four lane groups with lane swaps (four values per
 // register), unscaled, and summed over the four waves in LDS.  Rotations use the degree blocks when the tile's P
 // and Q have no entry off them; dx is staged in LDS and stored coalesced.
-template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER, bool SCATTER>
+template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER, bool SCATTER, bool LP>
 __global__ void __launch_bounds__(kThreads, 2)
 k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
             XRows X, const float* __restrict__ P,
@@ -882,12 +889,16 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         _Float16 h, l;
-                        split_f16s(gd[r][o], sc, h, l);
+                        if constexpr (LP) {
+                            h = static_cast<_Float16>(gd[r][o] * sc);
+                        } else {
+                            split_f16s(gd[r][o], sc, h, l);
+                            lv[r] = l;
+                        }
                         hv[r] = h;
-                        lv[r] = l;
                     }
                     *reinterpret_cast<h4*>(base + (o * NKS) * CHUNK) = hv;
-                    *reinterpret_cast<h4*>(base + ((DOUT + o) * NKS) * CHUNK) = lv;
+                    if constexpr (!LP) *reinterpret_cast<h4*>(base + ((DOUT + o) * NKS) * CHUNK) = lv;
                 }
             }
         }
@@ -956,7 +967,7 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
                         const h8* src =
                             cfr + 2 * ((((k0 + kk) * (CIN / 16) + wave + 4 * j) * NKS + ks) * 64 + lane);
                         ahi[j][kk][ks] = src[0];
-                        alo[j][kk][ks] = src[1];
+                        if constexpr (!LP) alo[j][kk][ks] = src[1];
                     }
             float pf[KP][WD];
 #pragma unroll
@@ -971,7 +982,8 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks) {
                     bh[buf][ks] = *reinterpret_cast<const h8*>(sB + (slot * NKS + ks) * CHUNK + myslot);
-                    bl[buf][ks] = *reinterpret_cast<const h8*>(sB + ((DOUT + slot) * NKS + ks) * CHUNK + myslot);
+                    if constexpr (!LP)
+                        bl[buf][ks] = *reinterpret_cast<const h8*>(sB + ((DOUT + slot) * NKS + ks) * CHUNK + myslot);
                 }
             };
             auto mfma_slot = [&](int buf, int ab) {
@@ -985,8 +997,10 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
                     for (int j = 0; j < RPW; ++j)
 #pragma unroll
                         for (int kk = 0; kk < KP; ++kk) {
-                            acc2[ab][j][kk] = mfma_h(alo[j][kk][ks], bh[buf][ks], acc2[ab][j][kk]);
-                            acc2[ab][j][kk] = mfma_h(ahi[j][kk][ks], bl[buf][ks], acc2[ab][j][kk]);
+                            if constexpr (!LP) {
+                                acc2[ab][j][kk] = mfma_h(alo[j][kk][ks], bh[buf][ks], acc2[ab][j][kk]);
+                                acc2[ab][j][kk] = mfma_h(ahi[j][kk][ks], bl[buf][ks], acc2[ab][j][kk]);
+                            }
                             acc2[ab][j][kk] = mfma_h(ahi[j][kk][ks], bh[buf][ks], acc2[ab][j][kk]);
                         }
             };
@@ -1109,7 +1123,7 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 // buffer with the tile's P and Q.  Wave w owns output rows 16 w .. 16 w + 15,
 // whose U_k rows its own lanes produce, so only the fs fragments are shared
 // between waves.  One partial dC per workgroup.
-template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER>
+template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER, bool LP>
 __global__ void __launch_bounds__(kThreads, 2)
 k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
             XRows X, const float* __restrict__ P,
@@ -1236,13 +1250,17 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         _Float16 h, l;
-                        split_f16s(fs[q][i], sc, h, l);
+                        if constexpr (LP) {
+                            h = static_cast<_Float16>(fs[q][i] * sc);
+                        } else {
+                            split_f16s(fs[q][i], sc, h, l);
+                            lv[q] = l;
+                        }
                         hv[q] = h;
-                        lv[q] = l;
                     }
                     const int off = ((2 * i + (pq >> 1)) * 16 + pc % 16) * 16 + 8 * (pq & 1);
                     *reinterpret_cast<h4*>(arr + off) = hv;
-                    *reinterpret_cast<h4*>(arr + CB * ARR + off) = lv;
+                    if constexpr (!LP) *reinterpret_cast<h4*>(arr + CB * ARR + off) = lv;
                 }
             }
         }
@@ -1298,13 +1316,17 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         _Float16 h, l;
-                        split_f16s(u[q][i], sc, h, l);
+                        if constexpr (LP) {
+                            h = static_cast<_Float16>(u[q][i] * sc);
+                        } else {
+                            split_f16s(u[q][i], sc, h, l);
+                            lv[q] = l;
+                        }
                         hv[q] = h;
-                        lv[q] = l;
                     }
                     const int off = ((2 * i + (pq >> 1)) * 16 + pc % 16) * 16 + 8 * (pq & 1);
                     *reinterpret_cast<h4*>(uarr + off) = hv;
-                    *reinterpret_cast<h4*>(uarr + RB * ARR + off) = lv;
+                    if constexpr (!LP) *reinterpret_cast<h4*>(uarr + RB * ARR + off) = lv;
                 }
             }
 
@@ -1320,18 +1342,20 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
                 // the CB blocks interleaved (CB independent accumulation chains)
                 const char* ua = uarr + (16 * ks * 4 + nbase) * 16;
                 const h8 ah = live ? *reinterpret_cast<const h8*>(ua) : z;
-                const h8 al = live ? *reinterpret_cast<const h8*>(ua + RB * ARR) : z;
-                h8 bh[CB], bl[CB];
+                h8 al = z, bh[CB], bl[CB];
+                if constexpr (!LP) al = live ? *reinterpret_cast<const h8*>(ua + RB * ARR) : z;
 #pragma unroll
                 for (int b = 0; b < CB; ++b) {
                     const char* arr = sF + b * ARR + (16 * ks * 4 + nbase) * 16;
                     bh[b] = live ? *reinterpret_cast<const h8*>(arr) : z;
-                    bl[b] = live ? *reinterpret_cast<const h8*>(arr + CB * ARR) : z;
+                    if constexpr (!LP) bl[b] = live ? *reinterpret_cast<const h8*>(arr + CB * ARR) : z;
                 }
+                if constexpr (!LP) {
 #pragma unroll
-                for (int b = 0; b < CB; ++b) acc[b] = mfma_h(al, bh[b], acc[b]);
+                    for (int b = 0; b < CB; ++b) acc[b] = mfma_h(al, bh[b], acc[b]);
 #pragma unroll
-                for (int b = 0; b < CB; ++b) acc[b] = mfma_h(ah, bl[b], acc[b]);
+                    for (int b = 0; b < CB; ++b) acc[b] = mfma_h(ah, bl[b], acc[b]);
+                }
 #pragma unroll
                 for (int b = 0; b < CB; ++b) acc[b] = mfma_h(ah, bh[b], acc[b]);
             }
@@ -1420,10 +1444,11 @@ constexpr size_t ews_cfrag_bytes() {
     return align_up(static_cast<size_t>(K) * COUT * CIN * 2 * sizeof(_Float16), 256) + 256;
 }
 
+// lp: one fp16 product per operand pair (message-passing form only).
 template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER>
 int launch_ews_fwd(const feq_binning& B, int64_t E, XRows x, const float* P, const float* Q,
                    const float* dist, const float* C, const float* F, float* y, void* ws,
-                   size_t ws_bytes, hipStream_t s) {
+                   size_t ws_bytes, bool lp, hipStream_t s) {
     constexpr size_t lds = ews_fwd_lds<CIN, COUT, LIN, LOUT, K>();
     constexpr int occ = ews_fwd_occ<CIN, COUT, LIN, LOUT, K>();
     static_assert(lds <= 80 * 1024, "two forward workgroups must fit one CU's LDS");
@@ -1434,7 +1459,9 @@ int launch_ews_fwd(const feq_binning& B, int64_t E, XRows x, const float* P, con
     float* inv = cv.take<float>(K);
     auto prep = k_ews_prep<K, COUT, CIN, false>;
     FEQ_LAUNCH("k_ews_prep", prep, dim3(K * COUT / 16), dim3(kThreads), 0, s, C, frag, inv);
-    auto kern = k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, GATHER>;
+    auto kern = k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, GATHER, false>;
+    if constexpr (GATHER)
+        if (lp) kern = k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, true, true>;
     if (int rc = ews_set_lds(reinterpret_cast<const void*>(kern), lds)) return rc;
     const int64_t ntiles = ceil_div(E, kNE);
     const int64_t g = static_cast<int64_t>(ews_cus()) * occ;
@@ -1465,7 +1492,7 @@ template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER>
 int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const float* gy,
                    XRows x, const float* P, const float* Q, const float* dist,
                    const float* C, const float* F, float* gx, float* gC, float* gF, float* gdist,
-                   const NodeScatter* ns, void* ws, size_t ws_bytes, hipStream_t s) {
+                   const NodeScatter* ns, void* ws, size_t ws_bytes, bool lp, hipStream_t s) {
     using T = Canon<LIN, LOUT>;
     constexpr size_t xlds = ews_bwd_x_lds<CIN, COUT, LIN, LOUT, K>();
     constexpr size_t clds = ews_bwd_c_lds<CIN, COUT, LIN, LOUT, K>();
@@ -1492,7 +1519,8 @@ int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const f
     FEQ_LAUNCH("k_ews_prep", prep, dim3(K * CIN / 16), dim3(kThreads), 0, s, C, frag, inv);
     if constexpr (GATHER) {
         if (ns) {
-            auto kx = k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true>;
+            auto kx = lp ? k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, true>
+                         : k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, false>;
             if (int rc = ews_set_lds(reinterpret_cast<const void*>(kx), xlds)) return rc;
             FEQ_LAUNCH("k_ews_bwd_x", kx, dim3(G), dim3(kThreads), xlds, s, B, E, ntiles, gy, x, P, Q,
                        dist, frag, inv, F, nullptr, dFe, NS);
@@ -1504,12 +1532,14 @@ int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const f
         if (ns) return fail(FEQ_ERR_INVALID, "per-node sums need the message-passing form");
     }
     if (!ns) {
-        auto kx = k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, GATHER, false>;
+        auto kx = k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, GATHER, false, false>;
         if (int rc = ews_set_lds(reinterpret_cast<const void*>(kx), xlds)) return rc;
         FEQ_LAUNCH("k_ews_bwd_x", kx, dim3(G), dim3(kThreads), xlds, s, B, E, ntiles, gy, x, P, Q,
                    dist, frag, inv, F, gx, dFe, NS);
     }
-    auto kc = k_ews_bwd_c<CIN, COUT, LIN, LOUT, K, GATHER>;
+    auto kc = k_ews_bwd_c<CIN, COUT, LIN, LOUT, K, GATHER, false>;
+    if constexpr (GATHER)
+        if (lp) kc = k_ews_bwd_c<CIN, COUT, LIN, LOUT, K, true, true>;
     if (int rc = ews_set_lds(reinterpret_cast<const void*>(kc), clds)) return rc;
     FEQ_LAUNCH("k_ews_bwd_c", kc, dim3(G), dim3(kThreads), clds, s, B, E, ntiles, gy, x, P, Q,
                dist, F, dCp);
@@ -1570,7 +1600,7 @@ size_t ew_split_bwd_workspace(const feq_layout& L, const feq_binning& B, int ran
 int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* gy,
                  const float* x, const int64_t* src, int64_t nsrc, const float* P, const float* Q,
                  const float* dist, const float* C, const float* F, float* gx, float* gC, float* gF,
-                 float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, hipStream_t s) {
+                 float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, bool lp, hipStream_t s) {
     float* gout = ns ? ns->out : gx;
     if (rank != 4 || !gout || !aligned16(gy) || !aligned16(x) || !aligned16(P) || !aligned16(Q) ||
         !aligned16(gout) || (ns && !src))
@@ -1580,9 +1610,9 @@ int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
     if constexpr ((ci) % 64 == 0) {                                                               \
         if (L.cin == ci && L.cout == co && canonical(L, li, lo))                                  \
             return src ? launch_ews_bwd<ci, co, li, lo, 4, true>(L, B, E, gy, X, P, Q, dist, C, F, \
-                                                                 gx, gC, gF, gdist, ns, ws, ws_bytes, s) \
+                                                                 gx, gC, gF, gdist, ns, ws, ws_bytes, lp, s) \
                        : launch_ews_bwd<ci, co, li, lo, 4, false>(L, B, E, gy, X, P, Q, dist, C, F, \
-                                                                  gx, gC, gF, gdist, ns, ws, ws_bytes, s); \
+                                                                  gx, gC, gF, gdist, ns, ws, ws_bytes, lp, s); \
     }
     FEQ_EWS_SHAPES(FEQ_BWD)
 #undef FEQ_BWD
@@ -1591,15 +1621,16 @@ int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
 
 int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
                  const int64_t* src, int64_t nsrc, const float* P, const float* Q, const float* dist,
-                 const float* C, const float* F, float* y, void* ws, size_t ws_bytes, hipStream_t s) {
+                 const float* C, const float* F, float* y, void* ws, size_t ws_bytes, bool lp,
+                 hipStream_t s) {
     if (rank != 4 || !aligned16(x) || !aligned16(P) || !aligned16(Q) || !aligned16(y)) return -1;
     const XRows X{x, src, nsrc};
 #define FEQ_FWD(ci, co, li, lo)                                                                  \
     if (L.cin == ci && L.cout == co && canonical(L, li, lo))                                     \
         return src ? launch_ews_fwd<ci, co, li, lo, 4, true>(B, E, X, P, Q, dist, C, F, y, ws,    \
-                                                             ws_bytes, s)                         \
+                                                             ws_bytes, lp, s)                     \
                    : launch_ews_fwd<ci, co, li, lo, 4, false>(B, E, X, P, Q, dist, C, F, y, ws,   \
-                                                              ws_bytes, s);
+                                                              ws_bytes, lp, s);
     FEQ_EWS_SHAPES(FEQ_FWD)
 #undef FEQ_FWD
     return -1;

@@ -105,14 +105,16 @@ size_t ew_split_bwd_workspace(const feq_layout& L, const feq_binning& B, int ran
 // src (may be NULL): message-passing form, edge e reads row src[e] of the node
 // table x (nsrc rows; indices outside [0, nsrc) read zeros).  ns (may be NULL,
 // needs src): the input gradient summed per source node into ns->out instead
-// of per edge into gx.
+// of per edge into gx.  lp (message-passing form only, else ignored): one fp16
+// product per operand pair instead of the three of the hi/lo split.
 int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* gy,
                  const float* x, const int64_t* src, int64_t nsrc, const float* P, const float* Q,
                  const float* dist, const float* C, const float* F, float* gx, float* gC, float* gF,
-                 float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, hipStream_t s);
+                 float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, bool lp, hipStream_t s);
 int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
                  const int64_t* src, int64_t nsrc, const float* P, const float* Q, const float* dist,
-                 const float* C, const float* F, float* y, void* ws, size_t ws_bytes, hipStream_t s);
+                 const float* C, const float* F, float* y, void* ws, size_t ws_bytes, bool lp,
+                 hipStream_t s);
 bool ew_split_supported(const feq_layout& L, const feq_binning& B, int rank, bool backward);
 
 // Kernel family of the fused edgewise layer.  The default tries the split-fp16

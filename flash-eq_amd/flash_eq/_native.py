@@ -17,6 +17,7 @@ from ._build import LIB_PATH
 
 FEQ_MAX_BLOCKS = 17
 FEQ_MAX_SLOTS = 128
+FEQ_EW_HALF_ACCURACY = 1          # flags of feq_edgewise_*_ex
 
 
 class CUDANotAvailableError(RuntimeError):
@@ -74,6 +75,10 @@ _SIGS = {
                                      ctypes.c_int),
     "feq_edgewise_bwd_src": ([_P, _P, _I32, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P,
                               _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
+    "feq_edgewise_fwd_src_ex": ([_P, _P, _I32, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _I32, _P,
+                                 _SZ, _P], ctypes.c_int),
+    "feq_edgewise_bwd_src_nodes_ex": ([_P, _P, _I32, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P,
+                                       _P, _P, _P, _P, _P, _P, _I32, _P, _SZ, _P], ctypes.c_int),
     "feq_edgewise_bwd_src_nodes_workspace": ([_P, _P, _I32, _I64], _SZ),
     "feq_edgewise_bwd_src_nodes": ([_P, _P, _I32, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P,
                                     _P, _P, _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),

@@ -42,7 +42,16 @@ def run_float32(module: nn.Module, dtype: torch.dtype, args: tuple, kwargs: dict
     parameters, buffers and tensor arguments; the output cast to ``dtype``."""
     state = {k: _up(p) for k, p in module.named_parameters()}
     state.update({k: _up(b) for k, b in module.named_buffers()})
+    seen = {}
+
+    def up(v):   # one float32 copy per distinct argument (P passed as P and Q: one cast)
+        if not isinstance(v, torch.Tensor):
+            return v
+        if id(v) not in seen:
+            seen[id(v)] = _up(v)
+        return seen[id(v)]
+
     with epsilon_dtype(dtype):          # the norms keep get_epsilon(dtype) (utils.py:19-27)
-        out = torch.func.functional_call(module, state, tuple(_up(a) for a in args),
-                                         {k: _up(v) for k, v in kwargs.items()})
+        out = torch.func.functional_call(module, state, tuple(up(a) for a in args),
+                                         {k: up(v) for k, v in kwargs.items()})
     return out.to(dtype)

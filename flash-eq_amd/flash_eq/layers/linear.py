@@ -25,6 +25,7 @@ from ..ops import (edgewise_linear, edgewise_linear_src, edgewise_src_supported,
                    rows_weight_grad, BiasRowsFn, EqLinearFn)
 from ..representations import ProductRepr, Repr
 from .radial import SeparableRadialNet
+from ..utils import half_precision_active
 
 
 class RowsLinearFn(torch.autograd.Function):
@@ -141,7 +142,8 @@ class EquivariantEdgewiseLinear(nn.Module):
                     raise ValueError(f"graph has {graph.num_edges} edges, distances {distances.shape[0]}")
                 perm, offsets = graph.csr_src()
                 y = edgewise_linear_src(x, graph.src, perm, offsets, Pp, Qp, distances, C, F,
-                                        emb.layout, binning, rw.rank)
+                                        emb.layout, binning, rw.rank,
+                                        half_precision_active(edge_features))
             else:
                 y = edgewise_linear(x, Pp, Qp, distances, C, F, emb.layout, binning, rw.rank)
             return emb.output(y)
@@ -152,7 +154,7 @@ class EquivariantEdgewiseLinear(nn.Module):
                 perm, offsets = graph.csr_src()
                 return edgewise_linear_src(edge_features, graph.src, perm, offsets, P, Q, distances,
                                            rw.channel_patterns, rw.radial_functions(), layout,
-                                           binning, rw.rank)
+                                           binning, rw.rank, half_precision_active(edge_features))
             edge_features = graph.gather_src(edge_features)
         return edgewise_linear(edge_features, P, Q, distances, rw.channel_patterns,
                                rw.radial_functions(), layout, binning, rw.rank)

@@ -110,11 +110,13 @@ class EdgewiseLinearSrcFn(torch.autograd.Function):
     kernels (``feq_edgewise_fwd_src``); the backward sums the input gradient
     over every source node's edges inside the input-gradient kernel
     (``feq_edgewise_bwd_src_nodes``, walking ``perm``, ``offsets``: the CSR by
-    source), so neither x[src] nor its gradient is ever materialised."""
+    source), so neither x[src] nor its gradient is ever materialised.
+    ``half_accuracy``: one fp16 product per operand pair (FEQ_EW_HALF_ACCURACY),
+    for callers held to the half-precision bar."""
 
     @staticmethod
     def forward(ctx, x, src, perm, offsets, P, Q, dist, C, F, layout: N.FeqLayout,
-                binning: N.FeqBinning, rank: int):
+                binning: N.FeqBinning, rank: int, half_accuracy: bool = False):
         dev = _same_device(x, src, perm, offsets, P, Q, dist, C, F)
         E = src.shape[0]
         xs, Ps, Qs = _f32(x, "node_features"), _f32(P, "P"), _f32(Q, "Q")
@@ -127,25 +129,26 @@ class EdgewiseLinearSrcFn(torch.autograd.Function):
         _check_edgewise_shapes(layout, binning, rank, torch.empty(E, layout.cin, layout.din, device="meta"),
                                Ps, Qs, rs, Cs, Fs)
         si = src.to(torch.int64).contiguous()
+        flags = N.FEQ_EW_HALF_ACCURACY if half_accuracy else 0
         y = torch.empty(E, layout.cout, layout.dout, dtype=torch.float32, device=dev)
         if E:
             lib = N.lib()
             ws = N.workspace(lib.feq_edgewise_fwd_workspace(N.ctypes.byref(layout),
                                                             N.ctypes.byref(binning), rank, E), dev)
             with torch.cuda.device(dev):
-                rc = lib.feq_edgewise_fwd_src(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
-                                              N.ptr(xs), xs.shape[0], N.ptr(si), N.ptr(Ps), N.ptr(Qs),
-                                              N.ptr(rs), N.ptr(Cs), N.ptr(Fs), N.ptr(y), N.ptr(ws),
-                                              ws.numel(), N.stream_ptr(dev))
-            N.check(rc, "feq_edgewise_fwd_src")
+                rc = lib.feq_edgewise_fwd_src_ex(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
+                                                 N.ptr(xs), xs.shape[0], N.ptr(si), N.ptr(Ps), N.ptr(Qs),
+                                                 N.ptr(rs), N.ptr(Cs), N.ptr(Fs), N.ptr(y), flags,
+                                                 N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+            N.check(rc, "feq_edgewise_fwd_src_ex")
         ctx.save_for_backward(xs, si, perm, offsets, Ps, Qs, rs, Cs, Fs)
-        ctx.meta = (layout, binning, rank, x.dtype, dist.dtype, C.dtype, F.dtype)
+        ctx.meta = (layout, binning, rank, x.dtype, dist.dtype, C.dtype, F.dtype, flags)
         return y.to(x.dtype)
 
     @staticmethod
     def backward(ctx, gy):
         xs, si, perm, offsets, Ps, Qs, rs, Cs, Fs = ctx.saved_tensors
-        layout, binning, rank, xdt, rdt, cdt, fdt = ctx.meta
+        layout, binning, rank, xdt, rdt, cdt, fdt, flags = ctx.meta
         dev = xs.device
         E = si.shape[0]
         need = ctx.needs_input_grad
@@ -158,15 +161,16 @@ class EdgewiseLinearSrcFn(torch.autograd.Function):
         ws = N.workspace(lib.feq_edgewise_bwd_src_nodes_workspace(
             N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E), dev)
         with torch.cuda.device(dev):
-            rc = lib.feq_edgewise_bwd_src_nodes(
+            rc = lib.feq_edgewise_bwd_src_nodes_ex(
                 N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E, N.ptr(g) if E else None,
                 N.ptr(xs), xs.shape[0], N.ptr(si), N.ptr(perm) if E else None, N.ptr(offsets),
                 N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs), N.ptr(Fs), N.ptr(gx), N.ptr(gC),
-                N.ptr(gF), N.ptr(gr), N.ptr(ws), ws.numel(), N.stream_ptr(dev))
-        N.check(rc, "feq_edgewise_bwd_src_nodes")
+                N.ptr(gF), N.ptr(gr), flags, N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+        N.check(rc, "feq_edgewise_bwd_src_nodes_ex")
         gx = gx.to(xdt) if need[0] else None
         return (gx, None, None, None, None, None, None if gr is None else gr.to(rdt),
-                gC.to(cdt) if need[7] else None, gF.to(fdt) if need[8] else None, None, None, None)
+                gC.to(cdt) if need[7] else None, gF.to(fdt) if need[8] else None, None, None, None,
+                None)
 
 
 def edgewise_src_supported(layout: N.FeqLayout, binning: N.FeqBinning, rank: int) -> bool:
@@ -174,11 +178,13 @@ def edgewise_src_supported(layout: N.FeqLayout, binning: N.FeqBinning, rank: int
     return bool(N.lib().feq_edgewise_src_supported(N.ctypes.byref(layout), N.ctypes.byref(binning), rank))
 
 
-def edgewise_linear_src(x, src, perm, offsets, P, Q, dist, C, F, layout, binning, rank) -> torch.Tensor:
+def edgewise_linear_src(x, src, perm, offsets, P, Q, dist, C, F, layout, binning, rank,
+                        half_accuracy: bool = False) -> torch.Tensor:
     if torch.is_grad_enabled() and (P.requires_grad or Q.requires_grad):
         raise ValueError("the message-passing form does not form gradients for P and Q; "
                          "gather the rows and call edgewise_linear")
-    return EdgewiseLinearSrcFn.apply(x, src, perm, offsets, P, Q, dist, C, F, layout, binning, rank)
+    return EdgewiseLinearSrcFn.apply(x, src, perm, offsets, P, Q, dist, C, F, layout, binning, rank,
+                                     half_accuracy)
 
 
 # ---------------------------------------------------------------------------

@@ -42,6 +42,15 @@ def get_epsilon(dtype: torch.dtype) -> float:
     return 1e-5 if dtype in _LOW_PRECISION else 1e-8
 
 
+def half_precision_active(*tensors) -> bool:
+    """True inside ``epsilon_dtype(d)`` for a 16-bit d (a half-precision module
+    computed in float32), or when one of ``tensors`` is 16-bit: the caller's
+    accuracy bar is then the half-precision one."""
+    if getattr(_EPS, "dtype", None) in _LOW_PRECISION:
+        return True
+    return any(isinstance(t, torch.Tensor) and t.dtype in _LOW_PRECISION for t in tensors)
+
+
 @contextlib.contextmanager
 def epsilon_dtype(dtype: torch.dtype):
     prev = getattr(_EPS, "dtype", None)

@@ -217,6 +217,32 @@ int feq_edgewise_bwd_src_nodes(const feq_layout* L, const feq_binning* b, int32_
                                float* grad_x_nodes, float* grad_C, float* grad_F, float* grad_dist,
                                void* workspace, size_t ws_bytes, feq_stream_t stream);
 
+/* Forms of feq_edgewise_fwd_src / feq_edgewise_bwd_src_nodes with a flags
+ * word (flags = 0: identical to them).  The reference dispatches its kernel on
+ * the tensor dtype (block_diagonal.cu:1332, AT_DISPATCH_FLOATING_TYPES_AND_HALF)
+ * and computes at that precision; here the data stay float32 and the caller
+ * states the accuracy it needs.  FEQ_EW_HALF_ACCURACY: the channel mixes use
+ * one fp16 matrix-core product per operand pair instead of the three of the
+ * hi/lo split: each operand is rounded to fp16 after its power-of-two scaling,
+ * so a product carries a relative error up to about 2^-10 and a sum an error
+ * up to about 2^-10 of the sum of its absolute terms, far inside the bfloat16
+ * bar of 2e-2, for a third of the matrix-core work and half the split work.  For modules that
+ * compute in bfloat16 or float16. */
+#define FEQ_EW_HALF_ACCURACY 1
+int feq_edgewise_fwd_src_ex(const feq_layout* L, const feq_binning* b, int32_t rank,
+                            int64_t num_edges, const float* x, int64_t num_src, const int64_t* src,
+                            const float* P, const float* Q, const float* dist, const float* C,
+                            const float* F, float* y, int32_t flags, void* workspace,
+                            size_t ws_bytes, feq_stream_t stream);
+int feq_edgewise_bwd_src_nodes_ex(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                  int64_t num_edges, const float* grad_y, const float* x,
+                                  int64_t num_src, const int64_t* src, const int32_t* perm_src,
+                                  const int32_t* offsets_src, const float* P, const float* Q,
+                                  const float* dist, const float* C, const float* F,
+                                  float* grad_x_nodes, float* grad_C, float* grad_F,
+                                  float* grad_dist, int32_t flags, void* workspace, size_t ws_bytes,
+                                  feq_stream_t stream);
+
 /* ---- Wigner-D basis ------------------------------------------------------------
  * plan: host-built per-representation constants (see feq_wigner_plan_size);
  * out (E, dim, dim): column j = column perm[j] of D(g), g e_z = dir/|dir|. */

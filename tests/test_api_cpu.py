@@ -93,3 +93,16 @@ def test_block_diagonal_empty_returns_zeros_on_cpu():
     out = block_diagonal_cuda(torch.zeros(0, 2, 4), torch.zeros(11, 3, 2, 10), torch.zeros(0), pr,
                               0.0, 1.0, 10)
     assert out.shape == (0, 3, 9)
+
+
+def test_half_precision_active_inside_half_modules():
+    """The edgewise layer asks for the single-product kernels when its input is
+    16-bit or when it runs inside a half-precision module computed in float32."""
+    from flash_eq.utils import epsilon_dtype, half_precision_active
+    assert not half_precision_active()
+    assert not half_precision_active(torch.zeros(1))
+    assert half_precision_active(torch.zeros(1, dtype=torch.bfloat16))
+    with epsilon_dtype(torch.bfloat16):
+        assert half_precision_active(torch.zeros(1))
+    with epsilon_dtype(torch.float32):
+        assert not half_precision_active(torch.zeros(1))
