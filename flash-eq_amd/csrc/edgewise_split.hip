@@ -1524,9 +1524,7 @@ int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const f
             if (int rc = ews_set_lds(reinterpret_cast<const void*>(kx), xlds)) return rc;
             FEQ_LAUNCH("k_ews_bwd_x", kx, dim3(G), dim3(kThreads), xlds, s, B, E, ntiles, gy, x, P, Q,
                        dist, frag, inv, F, nullptr, dFe, NS);
-            if (x.nsrc > 0)
-                FEQ_LAUNCH("k_ews_node_fix", k_ews_node_fix, dim3(static_cast<unsigned>(x.nsrc)),
-                           dim3(64), 0, s, NS, static_cast<int64_t>(CIN * T::DIN / 4));
+            if (int rc = node_fix(NS, x.nsrc, static_cast<int64_t>(CIN * T::DIN / 4), s)) return rc;
         }
     } else {
         if (ns) return fail(FEQ_ERR_INVALID, "per-node sums need the message-passing form");
@@ -1567,6 +1565,13 @@ bool canonical(const feq_layout& L, int lin, int lout) {
 
 }  // namespace
 
+int node_fix(const NodeScatter& ns, int64_t nsrc, int64_t row4, hipStream_t s) {
+    if (nsrc > 0)
+        FEQ_LAUNCH("k_ews_node_fix", k_ews_node_fix, dim3(static_cast<unsigned>(nsrc)), dim3(64), 0, s,
+                   ns, row4);
+    return FEQ_OK;
+}
+
 // Shapes with a split-fp16 fast path: (Cin, Cout, Lin, Lout), rank 4.
 #define FEQ_EWS_SHAPES(X) \
     X(64, 64, 2, 2)       \
@@ -1587,6 +1592,7 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 size_t ew_split_bwd_workspace(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
                               bool nodes) {
     if (rank != 4) return 0;
+    if (ew0_supported(L, rank)) return ew0_bwd_workspace(L, B, rank, E, nodes);
 #define FEQ_WS(ci, co, li, lo)                                                                 \
     if constexpr ((ci) % 64 == 0) {                                                            \
         if (L.cin == ci && L.cout == co && canonical(L, li, lo))                               \
@@ -1605,6 +1611,9 @@ int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
     if (rank != 4 || !gout || !aligned16(gy) || !aligned16(x) || !aligned16(P) || !aligned16(Q) ||
         !aligned16(gout) || (ns && !src))
         return -1;
+    if (ew0_supported(L, rank))
+        return ew0_bwd(L, B, rank, E, gy, x, src, nsrc, P, Q, dist, C, F, gx, gC, gF, gdist, ns, ws,
+                       ws_bytes, s);
     const XRows X{x, src, nsrc};
 #define FEQ_BWD(ci, co, li, lo)                                                                   \
     if constexpr ((ci) % 64 == 0) {                                                               \
@@ -1623,7 +1632,9 @@ int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
                  const int64_t* src, int64_t nsrc, const float* P, const float* Q, const float* dist,
                  const float* C, const float* F, float* y, void* ws, size_t ws_bytes, bool lp,
                  hipStream_t s) {
-    if (rank != 4 || !aligned16(x) || !aligned16(P) || !aligned16(Q) || !aligned16(y)) return -1;
+    if (rank != 4) return -1;
+    if (ew0_supported(L, rank)) return ew0_fwd(L, B, rank, E, x, src, nsrc, P, Q, dist, C, F, y, s);
+    if (!aligned16(x) || !aligned16(P) || !aligned16(Q) || !aligned16(y)) return -1;
     const XRows X{x, src, nsrc};
 #define FEQ_FWD(ci, co, li, lo)                                                                  \
     if (L.cin == ci && L.cout == co && canonical(L, li, lo))                                     \
@@ -1639,6 +1650,7 @@ int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
 // Shapes the split kernels (and so the message-passing entry points) serve.
 bool ew_split_supported(const feq_layout& L, const feq_binning& B, int rank, bool backward) {
     if (rank != 4) return false;
+    if (ew0_supported(L, rank)) return true;
     bool ok = false;
 #define FEQ_SUP(ci, co, li, lo)                                                          \
     if (L.cin == ci && L.cout == co && canonical(L, li, lo))                             \

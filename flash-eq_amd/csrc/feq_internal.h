@@ -116,6 +116,22 @@ int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
                  const float* C, const float* F, float* y, void* ws, size_t ws_bytes, bool lp,
                  hipStream_t s);
 bool ew_split_supported(const feq_layout& L, const feq_binning& B, int rank, bool backward);
+// Rows of the nodes that the per-node sums of a tile walk did not write (nodes
+// crossing 16-edge tile boundaries: their partial rows summed in tile order;
+// nodes without edges: zeros).  row4 = Cin Din / 4.
+int node_fix(const NodeScatter& ns, int64_t nsrc, int64_t row4, hipStream_t s);
+
+// Scalar-output family (edgewise_scalar.hip): lvals_out = [0], Cin = 64, rank 4,
+// reached through the split family's entry points above.
+bool ew0_supported(const feq_layout& L, int rank);
+size_t ew0_bwd_workspace(const feq_layout& L, const feq_binning& B, int rank, int64_t E, bool nodes);
+int ew0_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
+            const int64_t* src, int64_t nsrc, const float* P, const float* Q, const float* dist,
+            const float* C, const float* F, float* y, hipStream_t s);
+int ew0_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* gy,
+            const float* x, const int64_t* src, int64_t nsrc, const float* P, const float* Q,
+            const float* dist, const float* C, const float* F, float* gx, float* gC, float* gF,
+            float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, hipStream_t s);
 
 // Kernel family of the fused edgewise layer.  The default tries the split-fp16
 // kernels, then the shape-generic ones; FEQ_EW_PATH=generic (or
