@@ -35,6 +35,8 @@ constexpr int kCin = 64;      // a lane per input channel
 constexpr int kWaves = 4;     // waves per workgroup
 constexpr int kTile = 16;     // edges per backward tile (the NodeScatter tile)
 
+__device__ __forceinline__ int64_t ceil_div_d(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
 int sc_cus() {
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) == hipSuccess) {
@@ -46,153 +48,222 @@ int sc_cus() {
 }
 
 // Sums over the 64 lanes of N per-lane values (N a power of two <= 64): each
-// exchange halves the values a lane keeps, then the single value is summed
-// over the remaining lane groups.  Lane l returns value (l >> (6 - log2 N)).
+// exchange halves the values a lane keeps (lanes with the exchanged lane bit
+// set keep the upper half), then the single value is summed over the
+// remaining lane bits.  Lane l returns value l / (64 / N).  The exchanges over
+// lane bits 5 and 4 are v_permlane32_swap / v_permlane16_swap (one swap and
+// one add per pair, no select); the later ones add both halves and select the
+// result (a select between two loaded array elements would be turned into an
+// indexed access of the whole array).
 template <int N>
-__device__ __forceinline__ float wave_sums(float (&v)[N]) {
+__device__ __forceinline__ float wave_sums(const float (&v)[N]) {
     static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "power of two");
     const int lane = threadIdx.x & 63;
-    int n = N, half_lanes = 32;
     float w[N];
 #pragma unroll
     for (int i = 0; i < N; ++i) w[i] = v[i];
-#pragma unroll
-    for (int step = 0; (1 << step) < N; ++step) {
-        // lanes with bit `half_lanes` set keep the upper half of the values
-        const bool upper = (lane & half_lanes) != 0;
-        n >>= 1;
+    if constexpr (N >= 2) {
 #pragma unroll
         for (int i = 0; i < N / 2; ++i) {
-            if (i < n) {
-                const float send = upper ? w[i] : w[i + n];
-                const float keep = upper ? w[i + n] : w[i];
-                w[i] = keep + __shfl_xor(send, half_lanes, 64);
-            }
+            const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(w[i]), __float_as_uint(w[i + N / 2]),
+                                                            false, false);
+            w[i] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
         }
-        half_lanes >>= 1;
+    }
+    if constexpr (N >= 4) {
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) {
+            const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(w[i]), __float_as_uint(w[i + N / 4]),
+                                                            false, false);
+            w[i] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+        }
+    }
+    int bit = 8;
+#pragma unroll
+    for (int m = N / 8; m >= 1; m >>= 1) {
+        const bool upper = (lane & bit) != 0;
+#pragma unroll
+        for (int i = 0; i < m; ++i) {
+            const float a = w[i] + __shfl_xor(w[i], bit, 64);
+            const float b = w[i + m] + __shfl_xor(w[i + m], bit, 64);
+            w[i] = upper ? b : a;
+        }
+        bit >>= 1;
     }
     float s = w[0];
-    for (int off = half_lanes; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+    for (int off = N >= 4 ? bit : (N == 2 ? 16 : 32); off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
     return s;
 }
 
-struct SRows {
-    const float* x;
-    const int64_t* src;   // NULL: edge e reads row e
-    int64_t nsrc;
-};
-
-__device__ __forceinline__ int64_t s_row(const SRows& X, int64_t e) {
-    if (!X.src) return e;
-    const int64_t r = X.src[e];
-    return r >= 0 && r < X.nsrc ? r : -1;
+// The radial-function table F (num_bins + 1, K, Lin + 1) in LDS: a few KB,
+// read by every edge.
+__device__ __forceinline__ void stage_table(float* sF, const float* __restrict__ F, int n) {
+    for (int q = threadIdx.x; q < n; q += blockDim.x) sF[q] = F[q];
+    __syncthreads();
 }
 
-// Per-edge state shared by both directions: fs0 of this lane's channel, the
-// scaled radial functions F_e[k, l] s^l, Q[0, 0].
-template <int LIN, int K>
-struct Edge0 {
+// Per-edge constants of a group of NB edges; every load of the group is
+// issued before the first use (indices clamped in range, then masked), so one
+// memory latency covers the group.  The edge index is wave-uniform: the row
+// index, distance, basis columns and Q[0, 0] are scalar loads.  The bin, the
+// interpolation weight and s = r / (r + sigma) of edge i are computed by lane i
+// and broadcast, not by every lane.
+template <int LIN, int NB>
+struct Group0 {
     static constexpr int DIN = (LIN + 1) * (LIN + 1), NL = LIN + 1;
-    float xr[DIN];
-    float fs0[NL];
-    float fe[K][NL];
-    float pw[NL];
-    float q00;
-    float pcol[DIN][NL];
+    static_assert(NB <= 64, "a lane per edge of the group");
+    float xr[NB][DIN];
+    float pc[NB][DIN][NL];
+    float r[NB], q[NB], t[NB], sh[NB];
+    int lo[NB];
+    int64_t row[NB];
 
-    __device__ __forceinline__ void load(const feq_binning& B, const SRows& X, int64_t e,
-                                         const float* __restrict__ P, const float* __restrict__ Q,
-                                         const float* __restrict__ dist, const float* __restrict__ F,
-                                         int lane) {
-        const int64_t row = s_row(X, e);
-        const float* xs = X.x + ((row >= 0 ? row : 0) * kCin + lane) * DIN;
+    __device__ __forceinline__ void load(int64_t e0, int64_t E, const float* __restrict__ x,
+                                         const int64_t* __restrict__ src, int64_t nsrc,
+                                         const int32_t* __restrict__ perm, const float* __restrict__ P,
+                                         const float* __restrict__ Q, const float* __restrict__ dist,
+                                         int64_t (&e)[NB], int lane, const feq_binning& B) {
 #pragma unroll
-        for (int d = 0; d < DIN; ++d) xr[d] = row >= 0 ? xs[d] : 0.0f;
-        const float* pe = P + e * DIN * DIN;
-#pragma unroll
-        for (int d = 0; d < DIN; ++d)
-#pragma unroll
-            for (int l = 0; l < NL; ++l) pcol[d][l] = pe[d * DIN + l];
-        q00 = Q[e];
-        const float r = dist[e];
-        const EdgeBin eb = edge_bin(r, B);
-        const float s = r / (r + B.sh_scale);
-        float p = 1.0f;
-#pragma unroll
-        for (int l = 0; l < NL; ++l) {
-            pw[l] = p;
-            p *= s;
+        for (int i = 0; i < NB; ++i) {
+            const int64_t p = e0 + i < E ? e0 + i : E - 1;
+            e[i] = perm ? perm[p] : p;
         }
-        const float* flo = F + static_cast<int64_t>(eb.lo) * K * NL;
 #pragma unroll
-        for (int k = 0; k < K; ++k)
+        for (int i = 0; i < NB; ++i) {
+            int64_t rw = e[i];
+            if (src) {
+                rw = src[e[i]];
+                rw = rw >= 0 && rw < nsrc ? rw : -1;
+            }
+            row[i] = e0 + i < E ? rw : -1;
+            r[i] = dist[e[i]];
+            q[i] = Q[e[i]];
+        }
 #pragma unroll
-            for (int l = 0; l < NL; ++l)
-                fe[k][l] = lerp_bins(flo[k * NL + l], flo[K * NL + k * NL + l], eb.t) * pw[l];
+        for (int i = 0; i < NB; ++i) {
+            const float* xs = x + ((row[i] >= 0 ? row[i] : 0) * kCin + lane) * DIN;
+            const uint32_t mk = row[i] >= 0 ? ~0u : 0u;
+#pragma unroll
+            for (int d = 0; d < DIN; ++d) xr[i][d] = __uint_as_float(__float_as_uint(xs[d]) & mk);
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const float* pe = P + e[i] * DIN * DIN;
+#pragma unroll
+            for (int d = 0; d < DIN; ++d)
+#pragma unroll
+                for (int l = 0; l < NL; ++l) pc[i][d][l] = pe[d * DIN + l];
+        }
+        float rl = r[0];
+#pragma unroll
+        for (int i = 1; i < NB; ++i) rl = lane == i ? r[i] : rl;
+        const EdgeBin eb = edge_bin(rl, B);
+        const float sl = rl / (rl + B.sh_scale);
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            lo[i] = __builtin_amdgcn_readlane(eb.lo, i);
+            t[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(eb.t), i));
+            sh[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sl), i));
+        }
+    }
+
+    // fs0[l] = sum_d x[d] P[d, l]; fe[k][l] = F_e[k, l] s^l from the LDS table
+    template <int K>
+    __device__ __forceinline__ void edge(int i, const float* sF, float (&fs0)[NL], float (&fe)[K][NL],
+                                         float (&pw)[NL]) const {
 #pragma unroll
         for (int l = 0; l < NL; ++l) {
             float a = 0.0f;
 #pragma unroll
-            for (int d = 0; d < DIN; ++d) a += xr[d] * pcol[d][l];
+            for (int d = 0; d < DIN; ++d) a += xr[i][d] * pc[i][d][l];
             fs0[l] = a;
         }
+        float p = 1.0f;
+#pragma unroll
+        for (int l = 0; l < NL; ++l) {
+            pw[l] = p;
+            p *= sh[i];
+        }
+        const float* flo = sF + lo[i] * K * NL;
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+#pragma unroll
+            for (int l = 0; l < NL; ++l) fe[k][l] = lerp_bins(flo[k * NL + l], flo[K * NL + k * NL + l], t[i]) * pw[l];
     }
 };
 
-// Forward: waves walk the edges (grid-stride), one edge at a time.
+constexpr int kGroup = 4;   // edges loaded together (forward)
+constexpr int kGroupB = 2;  // edges loaded together (backward: more state per edge)
+
+// Forward: waves walk groups of kGroup consecutive edges (grid-stride).
 template <int LIN, int COUT, int K>
 __global__ void __launch_bounds__(64 * kWaves)
-k_ew0_fwd(feq_binning B, int64_t E, SRows X, const float* __restrict__ P, const float* __restrict__ Q,
+k_ew0_fwd(feq_binning B, int64_t E, const float* __restrict__ x, const int64_t* __restrict__ src,
+          int64_t nsrc, const float* __restrict__ P, const float* __restrict__ Q,
           const float* __restrict__ dist, const float* __restrict__ C, const float* __restrict__ F,
           float* __restrict__ y) {
-    using ED = Edge0<LIN, K>;
+    using G = Group0<LIN, kGroup>;
+    constexpr int NL = G::NL;
+    extern __shared__ float sF[];
+    stage_table(sF, F, (B.num_bins + 1) * K * NL);
     const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float cw[K][COUT];   // C_k[co, lane]
 #pragma unroll
     for (int k = 0; k < K; ++k)
 #pragma unroll
         for (int co = 0; co < COUT; ++co) cw[k][co] = C[(k * COUT + co) * kCin + lane];
-    const int64_t w0 = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    const int64_t ng = ceil_div_d(E, kGroup);
+    const int64_t w0 = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
     const int64_t nw = static_cast<int64_t>(gridDim.x) * kWaves;
-    for (int64_t e = w0; e < E; e += nw) {
-        ED ed;
-        ed.load(B, X, e, P, Q, dist, F, lane);
-        float z[K];
+    for (int64_t gi = w0; gi < ng; gi += nw) {
+        const int64_t e0 = gi * kGroup;
+        G g;
+        int64_t e[kGroup];
+        g.load(e0, E, x, src, nsrc, nullptr, P, Q, dist, e, lane, B);
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
-            float a = 0.0f;
+        for (int i = 0; i < kGroup; ++i) {
+            if (e0 + i >= E) break;
+            float fs0[NL], fe[K][NL], pw[NL];
+            g.template edge<K>(i, sF, fs0, fe, pw);
+            float v[COUT];
 #pragma unroll
-            for (int l = 0; l < ED::NL; ++l) a += ed.fe[k][l] * ed.fs0[l];
-            z[k] = a;
+            for (int co = 0; co < COUT; ++co) v[co] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+                float z = 0.0f;
+#pragma unroll
+                for (int l = 0; l < NL; ++l) z += fe[k][l] * fs0[l];
+#pragma unroll
+                for (int co = 0; co < COUT; ++co) v[co] += cw[k][co] * z;
+            }
+            const float sum = wave_sums<COUT>(v);
+            constexpr int GROUP = 64 / COUT;   // lanes that hold one output
+            if (lane % GROUP == 0) y[(e0 + i) * COUT + lane / GROUP] = sum * g.q[i];
         }
-        float v[COUT];
-#pragma unroll
-        for (int co = 0; co < COUT; ++co) {
-            float a = 0.0f;
-#pragma unroll
-            for (int k = 0; k < K; ++k) a += cw[k][co] * z[k];
-            v[co] = a;
-        }
-        const float sum = wave_sums<COUT>(v);
-        constexpr int GROUP = 64 / COUT;   // lanes that hold one output
-        if (lane % GROUP == 0) y[e * COUT + lane / GROUP] = sum * ed.q00;
     }
 }
 
-// Backward: a wave per 16-edge tile (grid-stride over tiles).  perm: NULL for
-// the identity order; ns: NULL for per-edge dx rows into gx.
+// Backward: a wave per 16-edge tile (grid-stride over tiles), its positions in
+// groups of kGroupB.  perm: NULL for the identity order; without NS.perm the
+// per-edge dx rows go to gx.
 template <int LIN, int COUT, int K>
 __global__ void __launch_bounds__(64 * kWaves)
-k_ew0_bwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy, SRows X,
+k_ew0_bwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
+          const float* __restrict__ x, const int64_t* __restrict__ src, int64_t nsrc,
           const float* __restrict__ P, const float* __restrict__ Q, const float* __restrict__ dist,
           const float* __restrict__ C, const float* __restrict__ F, float* __restrict__ gx,
           float* __restrict__ dFe, float* __restrict__ dCp, NodeScatter NS) {
-    using ED = Edge0<LIN, K>;
-    constexpr int DIN = ED::DIN, NL = ED::NL, KW = K * NL;
+    using G = Group0<LIN, kGroupB>;
+    constexpr int DIN = G::DIN, NL = G::NL, KW = K * NL;
     constexpr int NV = KW <= 1 ? 1 : (KW <= 2 ? 2 : (KW <= 4 ? 4 : (KW <= 8 ? 8 : (KW <= 16 ? 16 : 32))));
     static_assert(KW <= 32, "radial row of at most 32 values");
-    __shared__ float sdc[kWaves][K * COUT * kCin / 64][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    static_assert(kTile % kGroupB == 0, "whole groups per tile");
+    extern __shared__ float sF[];
+    __shared__ float sdc[kWaves][K * COUT][64];
+    stage_table(sF, F, (B.num_bins + 1) * K * NL);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const bool nodes = NS.perm != nullptr;
     float cw[K][COUT], acc[K][COUT];
 #pragma unroll
@@ -211,76 +282,93 @@ k_ew0_bwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy
 #pragma unroll
         for (int d = 0; d < DIN; ++d) run[d] = 0.0f;
         int js = 0;
-        for (int j = 0; j < np; ++j) {
-            const int64_t e = nodes ? NS.perm[p0 + j] : p0 + j;
-            ED ed;
-            ed.load(B, X, e, P, Q, dist, F, lane);
-            float gq[COUT];
+        int64_t nnext = -2;   // source of the position after the current group
+        for (int j0 = 0; j0 < np; j0 += kGroupB) {
+            G g;
+            int64_t e[kGroupB];
+            g.load(p0 + j0, p0 + np, x, src, nsrc, nodes ? NS.perm : nullptr, P, Q, dist, e, lane, B);
+            float gq[kGroupB][COUT];
 #pragma unroll
-            for (int co = 0; co < COUT; ++co) gq[co] = gy[e * COUT + co] * ed.q00;
-            float z[K], gz[K];
+            for (int i = 0; i < kGroupB; ++i)
 #pragma unroll
-            for (int k = 0; k < K; ++k) {
-                float a = 0.0f, g = 0.0f;
-#pragma unroll
-                for (int l = 0; l < NL; ++l) a += ed.fe[k][l] * ed.fs0[l];
-#pragma unroll
-                for (int co = 0; co < COUT; ++co) g += cw[k][co] * gq[co];
-                z[k] = a;
-                gz[k] = g;
+                for (int co = 0; co < COUT; ++co) gq[i][co] = gy[e[i] * COUT + co] * g.q[i];
+            if (nodes) {
+                const int jn = j0 + kGroupB;
+                nnext = -2;
+                if (jn < np) {
+                    const int64_t en = NS.perm[p0 + jn];
+                    const int64_t rn = src[en];
+                    nnext = rn >= 0 && rn < nsrc ? rn : -1;
+                }
             }
 #pragma unroll
-            for (int k = 0; k < K; ++k)
+            for (int i = 0; i < kGroupB; ++i) {
+                const int j = j0 + i;
+                if (j >= np) break;
+                float fs0[NL], fe[K][NL], pw[NL];
+                g.template edge<K>(i, sF, fs0, fe, pw);
+                float gz[K];
 #pragma unroll
-                for (int co = 0; co < COUT; ++co) acc[k][co] += gq[co] * z[k];
-            // dx of this edge and channel
-            float gfs[NL];
+                for (int k = 0; k < K; ++k) {
+                    float z = 0.0f, gk = 0.0f;
 #pragma unroll
-            for (int l = 0; l < NL; ++l) {
-                float a = 0.0f;
+                    for (int l = 0; l < NL; ++l) z += fe[k][l] * fs0[l];
 #pragma unroll
-                for (int k = 0; k < K; ++k) a += ed.fe[k][l] * gz[k];
-                gfs[l] = a;
+                    for (int co = 0; co < COUT; ++co) {
+                        gk += cw[k][co] * gq[i][co];
+                        acc[k][co] += gq[i][co] * z;
+                    }
+                    gz[k] = gk;
+                }
+                float gfs[NL];
+#pragma unroll
+                for (int l = 0; l < NL; ++l) {
+                    float a = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < K; ++k) a += fe[k][l] * gz[k];
+                    gfs[l] = a;
+                }
+                float dx[DIN];
+#pragma unroll
+                for (int d = 0; d < DIN; ++d) {
+                    float a = 0.0f;
+#pragma unroll
+                    for (int l = 0; l < NL; ++l) a += g.pc[i][d][l] * gfs[l];
+                    dx[d] = a;
+                }
+                // dF_e[k, l] = s^l sum_c gz[c, k] fs0[c, l]
+                float dv[NV];
+#pragma unroll
+                for (int q = 0; q < NV; ++q) dv[q] = q < KW ? gz[q / NL] * fs0[q % NL] * pw[q % NL] : 0.0f;
+                const float ds = wave_sums<NV>(dv);
+                constexpr int GROUP = 64 / NV;
+                if (lane % GROUP == 0 && lane / GROUP < KW) dFe[e[i] * KW + lane / GROUP] = ds;
+                if (!nodes) {
+                    float* gr = gx + (e[i] * kCin + lane) * DIN;
+#pragma unroll
+                    for (int d = 0; d < DIN; ++d) gr[d] = dx[d];
+                    continue;
+                }
+                // per-node sums in tile order (edges without a valid source are dropped)
+#pragma unroll
+                for (int d = 0; d < DIN; ++d) run[d] += dx[d];
+                const int64_t n = g.row[i];
+                const int64_t nn = i + 1 < kGroupB ? (j + 1 < np ? g.row[i + 1] : -2) : nnext;
+                if (nn == n) continue;
+                if (n >= 0) {
+                    float* dst;
+                    const int b = NS.offsets[n], en = NS.offsets[n + 1];
+                    if (b / kTile != (en - 1) / kTile)
+                        dst = NS.part + ((2 * tile + (js == 0 ? 0 : 1)) * kCin + lane) * DIN;
+                    else
+                        dst = NS.out + (n * kCin + lane) * DIN;
+#pragma unroll
+                    for (int d = 0; d < DIN; ++d) dst[d] = run[d];
+                }
+#pragma unroll
+                for (int d = 0; d < DIN; ++d) run[d] = 0.0f;
+                js = j + 1;
             }
-            float dx[DIN];
-#pragma unroll
-            for (int d = 0; d < DIN; ++d) {
-                float a = 0.0f;
-#pragma unroll
-                for (int l = 0; l < NL; ++l) a += ed.pcol[d][l] * gfs[l];
-                dx[d] = a;
-            }
-            // dF_e[k, l] = s^l sum_c gz[c, k] fs0[c, l]
-            float dv[NV];
-#pragma unroll
-            for (int q = 0; q < NV; ++q) dv[q] = q < KW ? gz[q / NL] * ed.fs0[q % NL] * ed.pw[q % NL] : 0.0f;
-            const float ds = wave_sums<NV>(dv);
-            constexpr int GROUP = 64 / NV;
-            if (lane % GROUP == 0 && lane / GROUP < KW) dFe[e * KW + lane / GROUP] = ds;
-            if (!nodes) {
-                float* g = gx + (e * kCin + lane) * DIN;
-#pragma unroll
-                for (int d = 0; d < DIN; ++d) g[d] = dx[d];
-                continue;
-            }
-            // per-node sums in tile order (rows of edges with no valid source are dropped)
-#pragma unroll
-            for (int d = 0; d < DIN; ++d) run[d] += dx[d];
-            const int64_t n = s_row(X, e);
-            if (j + 1 < np && s_row(X, NS.perm[p0 + j + 1]) == n) continue;
-            if (n >= 0) {
-                float* dst;
-                const int b = NS.offsets[n], en = NS.offsets[n + 1];
-                if (b / kTile != (en - 1) / kTile)
-                    dst = NS.part + ((2 * tile + (js == 0 ? 0 : 1)) * kCin + lane) * DIN;
-                else
-                    dst = NS.out + (n * kCin + lane) * DIN;
-#pragma unroll
-                for (int d = 0; d < DIN; ++d) dst[d] = run[d];
-            }
-#pragma unroll
-            for (int d = 0; d < DIN; ++d) run[d] = 0.0f;
-            js = j + 1;
         }
     }
     // dC partial of the workgroup: the waves' lane accumulators summed in wave order
@@ -319,6 +407,14 @@ bool canonical0(const feq_layout& L, int lin) {
     return ref.lslot_out[0] == L.lslot_out[0];
 }
 
+// The radial table's LDS (dynamic); beyond 64 KB the kernel's limit is raised.
+int table_lds(const void* kern, size_t lds) {
+    if (lds > 96 * 1024) return fail(FEQ_ERR_UNSUPPORTED, "radial table of %zu B does not fit LDS", lds);
+    if (lds > 64 * 1024)
+        FEQ_HIP(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    return FEQ_OK;
+}
+
 int groups0(int64_t ntiles) {
     const int64_t g = static_cast<int64_t>(sc_cus()) * 4;
     const int64_t w = ceil_div(ntiles, kWaves);
@@ -352,14 +448,15 @@ size_t ew0_bwd_workspace(const feq_layout& L, const feq_binning& B, int rank, in
 int ew0_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
             const int64_t* src, int64_t nsrc, const float* P, const float* Q, const float* dist,
             const float* C, const float* F, float* y, hipStream_t s) {
-    const SRows X{x, src, nsrc};
-    const int64_t g = static_cast<int64_t>(sc_cus()) * 8, need = ceil_div(E, kWaves);
+    const int64_t g = static_cast<int64_t>(sc_cus()) * 8, need = ceil_div(ceil_div(E, kGroup), kWaves);
     const unsigned grid = static_cast<unsigned>(need < g ? need : g);
+    const size_t lds = 4 * static_cast<size_t>(B.num_bins + 1) * rank * L.wdim;
 #define FEQ_FWD(li, co)                                                                      \
     if (L.cout == co && canonical0(L, li)) {                                                 \
         auto kern = k_ew0_fwd<li, co, kRank0>;                                               \
-        FEQ_LAUNCH("k_ew0_fwd", kern, dim3(grid), dim3(64 * kWaves), 0, s, B, E, X, P, Q, dist, C, \
-                   F, y);                                                                    \
+        if (int rc = table_lds(reinterpret_cast<const void*>(kern), lds)) return rc;         \
+        FEQ_LAUNCH("k_ew0_fwd", kern, dim3(grid), dim3(64 * kWaves), lds, s, B, E, x, src, nsrc, P, \
+                   Q, dist, C, F, y);                                                        \
         return FEQ_OK;                                                                       \
     }
     if (rank == kRank0 && L.cin == kCin) {
@@ -388,12 +485,13 @@ int ew0_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, cons
         NS = *ns;
         NS.part = cv.take<float>(static_cast<size_t>(ntiles) * 2 * L.cin * L.din);
     }
-    const SRows X{x, src, nsrc};
+    const size_t lds = 4 * static_cast<size_t>(B.num_bins + 1) * rank * L.wdim;
 #define FEQ_BWD(li, co)                                                                          \
     if (L.cout == co && canonical0(L, li)) {                                                     \
         auto kern = k_ew0_bwd<li, co, kRank0>;                                                   \
-        FEQ_LAUNCH("k_ew0_bwd", kern, dim3(G), dim3(64 * kWaves), 0, s, B, E, ntiles, gy, X, P, Q, \
-                   dist, C, F, gx, dFe, dCp, NS);                                                \
+        if (int rc = table_lds(reinterpret_cast<const void*>(kern), lds)) return rc;             \
+        FEQ_LAUNCH("k_ew0_bwd", kern, dim3(G), dim3(64 * kWaves), lds, s, B, E, ntiles, gy, x, src, \
+                   nsrc, P, Q, dist, C, F, gx, dFe, dCp, NS);                                   \
         if (ns)                                                                                  \
             if (int rc = node_fix(NS, nsrc, static_cast<int64_t>(L.cin) * L.din / 4, s)) return rc; \
         return ew_tail(L, B, rank, E, dist, F, dFe, dCp, G, ncc, gC, gF, gdist, tail, s);        \
