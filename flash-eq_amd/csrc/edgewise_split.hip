@@ -1575,6 +1575,7 @@ int node_fix(const NodeScatter& ns, int64_t nsrc, int64_t row4, hipStream_t s) {
 // Shapes with a split-fp16 fast path: (Cin, Cout, Lin, Lout), rank 4.
 #define FEQ_EWS_SHAPES(X) \
     X(64, 64, 2, 2)       \
+    X(64, 64, 1, 2)       \
     X(32, 64, 1, 2)
 
 size_t ew_split_workspace(const feq_layout& L, int rank) {

@@ -135,7 +135,7 @@ class EquivariantEdgewiseLinear(nn.Module):
             # a small layout without split-fp16 backward kernels: run it
             # zero-embedded in the [0,1,2]x64 kernels (ops._Embedding)
             x = emb.features(edge_features)
-            Pp, Qp = emb.basis(P, emb.pcols), emb.basis(Q, emb.qcols)
+            Pp, Qp = emb.basis_in(P), emb.basis_out(Q)
             C, F = emb.channels(rw.channel_patterns), emb.radial(rw.radial_functions())
             if graph is not None:
                 if graph.num_edges != distances.shape[0]:

@@ -226,20 +226,22 @@ def _weight_positions(lin: int, lout: int) -> dict:
 
 
 class _Embedding:
-    """Runs a layer of canonical lvals 0..lin -> 0..lout (lin, lout <= 2) and at
-    most 64 channels with the kernels of [0,1,2]x64 -> [0,1,2]x64: features,
-    channel patterns and bases are zero-padded, the radial functions placed at
-    their weights' positions in the larger layout (zeros elsewhere), and the
-    output cut back.  Padded inputs are zero, so they add exact zeros; the
-    power-of-two block scales of the split kernels come from block maxima and
-    do not change.  All steps are torch ops, so autograd carries the gradients."""
+    """Runs a layer of canonical lvals 0..lin -> 0..lout and at most 64 channels
+    with the kernels of a larger canonical layout, lvals 0..tin -> 0..tout with
+    64 channels (tin >= lin, tout >= lout): features, channel patterns and bases
+    are zero-padded, the radial functions placed at their weights' positions in
+    the larger layout (zeros elsewhere), and the output cut back.  Padded inputs
+    are zero, so they add exact zeros; the power-of-two block scales of the
+    split kernels come from block maxima and do not change.  All steps are
+    torch ops, so autograd carries the gradients."""
 
-    def __init__(self, lin: int, lout: int, cin: int, cout: int, device):
-        L = _EMB_L
+    def __init__(self, lin: int, lout: int, cin: int, cout: int, device, tin: int = _EMB_L,
+                 tout: int = _EMB_L):
         self.lin, self.lout, self.cin, self.cout = lin, lout, cin, cout
-        self.din, self.dout, self.D = (lin + 1) ** 2, (lout + 1) ** 2, (L + 1) ** 2
+        self.din, self.dout = (lin + 1) ** 2, (lout + 1) ** 2
+        self.Din, self.Dout = (tin + 1) ** 2, (tout + 1) ** 2
 
-        def cols(lmax):
+        def cols(lmax, L):
             """Slots of the larger m-first order that the small order's slots take
             (None when the small order is the larger one)."""
             if lmax == L:
@@ -250,27 +252,33 @@ class _Embedding:
                 at[js] = big[key]
             return torch.tensor(at, device=device)
 
-        self.pcols, self.qcols = cols(lin), cols(lout)
-        ws, wb = _weight_positions(lin, lout), _weight_positions(L, L)
+        self.pcols, self.qcols = cols(lin, tin), cols(lout, tout)
+        ws, wb = _weight_positions(lin, lout), _weight_positions(tin, tout)
         self.wdim = len(ws)
         wsrc = [self.wdim] * len(wb)          # index wdim: an appended zero column
         for key, w in ws.items():
             wsrc[wb[key]] = w
         self.wsrc = torch.tensor(wsrc, device=device)
-        self.layout = N.make_layout(list(range(L + 1)), list(range(L + 1)), _EMB_C, _EMB_C)
+        self.layout = N.make_layout(list(range(tin + 1)), list(range(tout + 1)), _EMB_C, _EMB_C)
 
     def features(self, x):
-        return torch.nn.functional.pad(x, (0, self.D - x.shape[-1], 0, _EMB_C - x.shape[-2]))
+        return torch.nn.functional.pad(x, (0, self.Din - x.shape[-1], 0, _EMB_C - x.shape[-2]))
 
-    def basis(self, R, cols):
+    @staticmethod
+    def _place(R, cols, D):
         """R (E, d, d) placed in a zero (E, D, D): rows d in the standard order
         keep their index, column j goes to cols[j]."""
         if cols is None:
             return R
-        d = R.shape[-1]
-        Rp = R.new_zeros(R.shape[0], self.D, self.D)
-        Rp[:, :d, cols] = R
+        Rp = R.new_zeros(R.shape[0], D, D)
+        Rp[:, :R.shape[-1], cols] = R
         return Rp
+
+    def basis_in(self, P):
+        return self._place(P, self.pcols, self.Din)
+
+    def basis_out(self, Q):
+        return self._place(Q, self.qcols, self.Dout)
 
     def channels(self, C):
         return torch.nn.functional.pad(C, (0, _EMB_C - self.cin, 0, _EMB_C - self.cout))
@@ -285,19 +293,27 @@ class _Embedding:
 _EMB_CACHE: dict = {}
 
 
+# Canonical (lin, lout) layouts with 64 channels in and out whose split kernels
+# (forward and backward) exist, smallest first: the embedding targets.
+_EMB_TARGETS = ((1, 2), (2, 2))
+
+
 def embedding_for(lvals_in, lvals_out, cin: int, cout: int, rank: int, device) -> Optional[_Embedding]:
-    """The embedding of a layout into the config-2 kernels, or None when the
-    layout is not a canonical prefix of [0, 1, 2] with at most 64 channels."""
+    """The embedding of a layout into the smallest target layout with split
+    kernels that holds it, or None when the layout is not a canonical prefix of
+    [0, 1, 2] with at most 64 channels."""
     lin, lout = tuple(lvals_in), tuple(lvals_out)
     if rank != 4 or cin > _EMB_C or cout > _EMB_C:
         return None
     if lin != tuple(range(len(lin))) or lout != tuple(range(len(lout))):
         return None
-    if len(lin) - 1 > _EMB_L or len(lout) - 1 > _EMB_L:
+    li, lo = len(lin) - 1, len(lout) - 1
+    target = next(((ti, to) for ti, to in _EMB_TARGETS if li <= ti and lo <= to), None)
+    if target is None:
         return None
     key = (lin, lout, cin, cout, str(device))
     if key not in _EMB_CACHE:
-        _EMB_CACHE[key] = _Embedding(len(lin) - 1, len(lout) - 1, cin, cout, device)
+        _EMB_CACHE[key] = _Embedding(li, lo, cin, cout, device, *target)
     return _EMB_CACHE[key]
 
 
