@@ -953,7 +953,13 @@ def rows_weight_grad(gy: torch.Tensor, x: torch.Tensor, dtype: torch.dtype,
     s = chunks if rows >= 64 * chunks else 1
     per = rows // s
     head = s * per
-    gyc = transpose_last2(gy[:head].contiguous(), per, gy.shape[1]).view(s, gy.shape[1], per)
+    if gy.dtype in (torch.float32, torch.float64):
+        # the chunks of gy as transposed views: the library reads the transposed
+        # operand in place
+        gyc = gy[:head].contiguous().view(s, per, gy.shape[1]).transpose(1, 2)
+    else:
+        # 16-bit batched products take no transposed views here (copied instead)
+        gyc = transpose_last2(gy[:head].contiguous(), per, gy.shape[1]).view(s, gy.shape[1], per)
     xc = x[:head].reshape(s, per, x.shape[1])
     acc = torch.promote_types(dtype, torch.float32)
     gw = column_sums(torch.bmm(gyc, xc).to(acc).reshape(s, -1)).view(gy.shape[1], x.shape[1])
