@@ -123,3 +123,38 @@ def test_scalar_output_deterministic_and_dispatched(dev):
     for k in ("k_ew0_fwd", "k_ew0_bwd", "k_ews_node_fix"):
         assert k in names, (k, names)
     assert "k_ews_fwd" not in names and "k_ews_bwd_x" not in names, names
+
+
+def test_scalar_output_out_of_range_rows_and_empty(dev):
+    """Source indices outside [0, N) read zero rows (their edges output Q00 * 0 and
+    scatter nothing); no edges gives empty outputs, zero radial gradients and
+    zero node gradients.  Checked against the gather form with zero rows."""
+    E, N = 400, 50
+    layer, graph, P, Q, x, r, gy = _mp_setup(dev, E, N, seed=31)
+    src = graph.src.clone()
+    src[::7] = N + 5
+    src[3::11] = -2
+    g2 = fe.Graph(src, graph.dst, N)
+    xg = x.clone().requires_grad_(True)
+    y = layer(P, Q, xg, r, graph=g2)
+    y.backward(gy)
+    valid = (src >= 0) & (src < N)
+    xz = torch.cat([x, torch.zeros(1, 64, 9, device=dev)])
+    xr = xz[torch.where(valid, src, torch.full_like(src, N))].clone().requires_grad_(True)
+    yref = layer(P, Q, xr, r)
+    assert torch.equal(y, yref)
+    yref.backward(gy)
+    gref = torch.zeros_like(x).index_add_(0, src[valid], xr.grad[valid])
+    assert rel_err(xg.grad, gref) < 1e-6
+    # no edges
+    e0 = torch.zeros(0, dtype=torch.long, device=dev)
+    g0 = fe.Graph(e0, e0, N)
+    x0 = x.clone().requires_grad_(True)
+    for p in layer.parameters():
+        p.grad = None
+    y0 = layer(P[:0], Q[:0], x0, r[:0], graph=g0)
+    assert y0.shape == (0, 8, 1)
+    y0.sum().backward()
+    assert torch.count_nonzero(x0.grad) == 0
+    for p in layer.radial_weights.parameters():
+        assert p.grad is None or torch.count_nonzero(p.grad) == 0
