@@ -6,7 +6,7 @@
 // (the reference scatters with atomics: pooling.py:21-30, attention.py:124-141).
 #include "feq_internal.h"
 
-#include <hipcub/hipcub.hpp>
+#include <rocprim/device/device_radix_sort.hpp>
 
 namespace feq {
 namespace {
@@ -114,12 +114,23 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 using namespace feq;
 
+// The stable key sort is rocPRIM's radix sort held to its block-sort + merge
+// form at every size.  Above 2^20 items rocPRIM would otherwise switch to its
+// onesweep form, which clears its look-back states with hipMemsetAsync and
+// resets a block-id counter from the host on every call; recorded into a HIP
+// graph, those nodes are not redone correctly on replays, the stale states and
+// block ids give scatter positions out of range and the replay faults.  The
+// merge form launches kernels only, so a captured CSR build replays like the
+// eager one.  Both forms are stable.
+using CsrSortConfig = rocprim::radix_sort_config<rocprim::default_config, rocprim::default_config,
+                                                 rocprim::default_config, size_t(1) << 31>;
+
 static size_t radix_temp_bytes(int64_t E) {
     size_t bytes = 0;
-    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, static_cast<const int32_t*>(nullptr),
-                                       static_cast<int32_t*>(nullptr),
-                                       static_cast<const int32_t*>(nullptr),
-                                       static_cast<int32_t*>(nullptr), static_cast<int>(E), 0, 32);
+    (void)rocprim::radix_sort_pairs<CsrSortConfig>(nullptr, bytes, static_cast<const int32_t*>(nullptr),
+                                                   static_cast<int32_t*>(nullptr),
+                                                   static_cast<const int32_t*>(nullptr),
+                                                   static_cast<int32_t*>(nullptr), static_cast<int>(E), 0, 32);
     return bytes;
 }
 
@@ -154,8 +165,8 @@ extern "C" int feq_csr_by_dst(const int64_t* dst, int64_t E, int64_t N, int32_t*
                        vals_in);
     int end_bit = 1;
     while ((int64_t(1) << end_bit) <= N) ++end_bit;  // keys lie in [0, N]
-    FEQ_HIP(hipcub::DeviceRadixSort::SortPairs(temp, tb, keys_in, keys_out, vals_in, perm,
-                                               static_cast<int>(E), 0, end_bit, s));
+    FEQ_HIP(rocprim::radix_sort_pairs<CsrSortConfig>(temp, tb, keys_in, keys_out, vals_in, perm,
+                                                     static_cast<int>(E), 0, end_bit, s));
     FEQ_LAUNCH("k_csr_offsets", k_csr_offsets, dim3(ceil_div(N + 1, 256)), dim3(256), 0, s, keys_out, E, N,
                        offsets);
     return FEQ_OK;

@@ -131,3 +131,62 @@ def test_captured_block_step_replays_match_eager(dev):
             vec = xyz[graph.src] - xyz[graph.dst]
             (P2,) = basis(vec)
             SumSquaresFn.apply(block(P2, P2, other, vec.norm(dim=-1), graph)).item()
+
+
+@pytest.mark.parametrize("num_keys", [100, 50000])
+def test_captured_csr_build_above_2pow20_edges(dev, num_keys):
+    """The stable grouping by key (feq_csr_by_dst) recorded in a HIP graph at
+    E = 1.3M > 2^20, the size above which the radix sort's default would switch
+    to a form that records memset nodes: every replay, with eager work between
+    replays, gives the stable argsort and the segment offsets (keys out of
+    range sorted past the last one).  num_keys = 100 is the bin count of the
+    radial-function gradient's sorted form; 50000 a node count."""
+    from flash_eq import _native as N
+    g = torch.Generator().manual_seed(31 + num_keys)
+    E = 1_300_000
+    keys = torch.randint(0, num_keys, (E,), generator=g)
+    keys[torch.randint(0, E, (1000,), generator=g)] = -1
+    keys[torch.randint(0, E, (1000,), generator=g)] = num_keys
+    in_range = (keys >= 0) & (keys < num_keys)
+    ref_perm = torch.argsort(torch.where(in_range, keys, num_keys), stable=True)
+    counts = torch.bincount(keys[in_range], minlength=num_keys)
+    ref_off = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)])
+    kd = keys.to(dev)
+    lib = N.lib()
+    ws = N.workspace(lib.feq_csr_workspace(E, num_keys), dev)
+    perm = torch.full((E,), -7, dtype=torch.int32, device=dev)
+    offsets = torch.full((num_keys + 1,), -7, dtype=torch.int32, device=dev)
+
+    def build():
+        rc = lib.feq_csr_by_dst(N.ptr(kd), E, num_keys, N.ptr(perm), N.ptr(offsets), N.ptr(ws),
+                                ws.numel(), N.stream_ptr(dev))
+        N.check(rc, "feq_csr_by_dst")
+
+    build()
+    torch.cuda.synchronize()
+    assert torch.equal(perm.cpu().long(), ref_perm)
+    assert torch.equal(offsets.cpu().long(), ref_off)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        build()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    cg = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(cg):
+        build()
+    for it in range(4):
+        perm.fill_(-7)
+        offsets.fill_(-7)
+        cg.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(perm.cpu().long(), ref_perm), it
+        assert torch.equal(offsets.cpu().long(), ref_off), it
+        # eager work between replays: the same build on other keys
+        kd2 = torch.randint(0, num_keys, (E,), device=dev)
+        p2 = torch.empty(E, dtype=torch.int32, device=dev)
+        o2 = torch.empty(num_keys + 1, dtype=torch.int32, device=dev)
+        N.check(lib.feq_csr_by_dst(N.ptr(kd2), E, num_keys, N.ptr(p2), N.ptr(o2), N.ptr(ws),
+                                   ws.numel(), N.stream_ptr(dev)), "feq_csr_by_dst")
+        torch.cuda.synchronize()
+        assert int(o2[-1]) == E, it
