@@ -382,7 +382,9 @@ k_pool_fwd(const float* __restrict__ Vt, const float* __restrict__ attn, int64_t
 
 // gV[e, h] = attn[e,h] gout[n, h]; gattn[e,h] = <V[e, h], gout[n, h]> for the
 // edges into n (gout[n] loaded once per segment); out-of-range edges get zeros.
-template <int V, int NT>
+// VPOS: V holds the rows in CSR position order (row b + i, as the pooled
+// edgewise forward keeps them) and only gattn is formed (gV is not written).
+template <int V, int NT, bool VPOS>
 __global__ void __launch_bounds__(64 * kWaves)
 k_pool_bwd(const float* __restrict__ Vt, const float* __restrict__ attn,
            const float* __restrict__ gout, int64_t E, int H, int Dh, int lgG,
@@ -395,6 +397,7 @@ k_pool_bwd(const float* __restrict__ Vt, const float* __restrict__ attn,
     const int64_t row = static_cast<int64_t>(H) * Dh;
     if (n == N) {
         for (int t = lane; t < cnt * H; t += 64) gattn[static_cast<int64_t>(perm[b + t / H]) * H + t % H] = 0.0f;
+        if (VPOS) return;
         for (int i = 0; i < cnt; ++i) {
             const int64_t e = perm[b + i];
             for (int64_t c = lane; c < row; c += 64) gV[e * row + c] = 0.0f;
@@ -415,9 +418,11 @@ k_pool_bwd(const float* __restrict__ Vt, const float* __restrict__ attn,
 #pragma unroll
             for (int u = 0; u < kUE; ++u) {
                 const bool live = hv && i0 + u < cnt;
-                eu[u] = perm[b + (i0 + u < cnt ? i0 + u : i0)];
-                a[u] = live ? attn[eu[u] * H + h] : 0.0f;
-                ld_head<V, NT>(Vt + eu[u] * row + h * Dh, j, G, NC, live, v[u]);
+                const int pos = b + (i0 + u < cnt ? i0 + u : i0);
+                eu[u] = perm[pos];
+                a[u] = live && !VPOS ? attn[eu[u] * H + h] : 0.0f;   // VPOS: attn unused (NULL)
+                ld_head<V, NT>(Vt + (VPOS ? static_cast<int64_t>(pos) : eu[u]) * row + h * Dh, j, G, NC,
+                               live, v[u]);
             }
             float dot[kUE];
 #pragma unroll
@@ -426,7 +431,7 @@ k_pool_bwd(const float* __restrict__ Vt, const float* __restrict__ attn,
             for (int u = 0; u < kUE; ++u) {
                 const bool live = hv && i0 + u < cnt;
                 if (live && ((i0 + u) & (G - 1)) == j) gattn[eu[u] * H + h] = dot[u];
-                st_head_scaled<V, NT>(gV + eu[u] * row + h * Dh, j, G, NC, live, a[u], go);
+                if (!VPOS) st_head_scaled<V, NT>(gV + eu[u] * row + h * Dh, j, G, NC, live, a[u], go);
             }
         }
     }
@@ -622,10 +627,33 @@ extern "C" int feq_attn_pool_bwd(const float* V, const float* attn, const float*
     hipStream_t s = stream_of(stream);
     return with_cfg(c, [&](auto VV, auto TT) -> int {
         constexpr int Vw = decltype(VV)::value, NT = decltype(TT)::value;
-        auto kern = k_pool_bwd<Vw, NT>;
+        auto kern = k_pool_bwd<Vw, NT, false>;
         FEQ_LAUNCH("k_pool_bwd", kern, seg_grid(num_nodes + 1), dim3(64 * kWaves), 0, s, V, attn,
                    grad_out, num_edges, heads, Dh, c.lgG, perm, offsets, num_nodes, grad_V,
                    grad_attn);
+        return FEQ_OK;
+    });
+}
+
+extern "C" int feq_attn_pool_grad_attn(const float* V_pos, const float* grad_out,
+                                       const int32_t* perm, const int32_t* offsets, int64_t num_edges,
+                                       int64_t num_nodes, int32_t mult, int32_t dim, int32_t heads,
+                                       float* grad_attn, feq_stream_t stream) {
+    if (heads < 1 || mult % heads) return fail(FEQ_ERR_INVALID, "num_heads must divide mult");
+    if (dim < 1) return fail(FEQ_ERR_INVALID, "invalid sizes");
+    if (int rc = check_graph(num_edges, num_nodes)) return rc;
+    if (num_edges == 0) return FEQ_OK;
+    if (!V_pos || !grad_out || !perm || !offsets || !grad_attn) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    const int Dh = mult / heads * dim;
+    HeadCfg c;
+    if (int rc = head_cfg(heads, Dh, {}, {V_pos, grad_out}, c)) return rc;
+    hipStream_t s = stream_of(stream);
+    return with_cfg(c, [&](auto VV, auto TT) -> int {
+        constexpr int Vw = decltype(VV)::value, NT = decltype(TT)::value;
+        auto kern = k_pool_bwd<Vw, NT, true>;
+        FEQ_LAUNCH("k_pool_grad_attn", kern, seg_grid(num_nodes + 1), dim3(64 * kWaves), 0, s, V_pos,
+                   static_cast<const float*>(nullptr), grad_out, num_edges, heads, Dh, c.lgG, perm,
+                   offsets, num_nodes, static_cast<float*>(nullptr), grad_attn);
         return FEQ_OK;
     });
 }

@@ -636,3 +636,106 @@ extern "C" int feq_edgewise_bwd_src_nodes_ex(const feq_layout* L, const feq_binn
                                 gF, gdist, &ns, ws, ws_bytes, (flags & FEQ_EW_HALF_ACCURACY) != 0, s);
     return rc == -1 ? fail(FEQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned") : rc;
 }
+
+// ---- message-passing form fused with the attention's head weighting and sum pooling ----
+namespace {
+int check_pool_args(const feq_layout* L, int32_t heads, int32_t chan_per_head) {
+    if (heads < 1 || heads > kPoolMaxHeads)
+        return fail(FEQ_ERR_UNSUPPORTED, "pooled form: heads must be in [1, %d], got %d", kPoolMaxHeads, heads);
+    if (chan_per_head < 4 || chan_per_head % 4 || static_cast<int64_t>(chan_per_head) * heads > L->cout)
+        return fail(FEQ_ERR_UNSUPPORTED,
+                    "pooled form: channels per head must be a positive multiple of 4 with "
+                    "heads * channels per head <= Cout, got %d x %d for Cout %d",
+                    heads, chan_per_head, L->cout);
+    return FEQ_OK;
+}
+}  // namespace
+
+extern "C" int feq_edgewise_pool_supported(const feq_layout* L, const feq_binning* b, int32_t rank) {
+    if (!L || !b || check_layout(L) || check_binning(b)) return 0;
+    if (ew_path() != kPathSplit) return 0;
+    return ew_pool_supported(*L, *b, rank);
+}
+
+extern "C" size_t feq_edgewise_fwd_src_pool_workspace(const feq_layout* L, const feq_binning*,
+                                                      int32_t rank, int64_t E) {
+    if (!L || rank < 1 || E < 0) return 0;
+    return ew_pool_fwd_workspace(*L, rank, E) + 256;
+}
+
+extern "C" int feq_edgewise_fwd_src_pool(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                         int64_t E, const float* x, int64_t num_src,
+                                         const int64_t* src, const float* P, const float* Q,
+                                         const float* dist, const float* C, const float* F,
+                                         const float* attn, int32_t heads, int32_t chan_per_head,
+                                         const int64_t* dst, const int32_t* perm_dst,
+                                         const int32_t* offsets_dst, int64_t num_dst, float* out,
+                                         float* y_pos, int32_t flags, void* ws, size_t ws_bytes,
+                                         feq_stream_t stream) {
+    if (int rc = check_layout(L)) return rc;
+    if (flags & ~FEQ_EW_HALF_ACCURACY) return fail(FEQ_ERR_INVALID, "unknown flags 0x%x", flags);
+    if (int rc = check_binning(b)) return rc;
+    if (rank < 1) return fail(FEQ_ERR_INVALID, "rank must be positive");
+    if (E < 0 || num_src < 0 || num_dst < 0) return fail(FEQ_ERR_INVALID, "negative edge or node count");
+    if (E > 0x7fffffffLL || num_dst > 0x7fffffffLL)
+        return fail(FEQ_ERR_UNSUPPORTED, "more than 2^31-1 edges or nodes");
+    if (int rc = check_pool_args(L, heads, chan_per_head)) return rc;
+    if (!feq_edgewise_pool_supported(L, b, rank))
+        return fail(FEQ_ERR_UNSUPPORTED, "no pooled message-passing kernels for this layout");
+    hipStream_t s = stream_of(stream);
+    if (num_dst > 0 && !out) return fail(FEQ_ERR_INVALID, "NULL out");
+    if (E == 0) return fill_zero(out, num_dst * L->cout * L->dout, s);
+    if (num_dst == 0) return FEQ_OK;   // no edge has a destination: nothing to sum
+    if (!x || !src || !P || !Q || !dist || !C || !F || !attn || !dst || !perm_dst || !offsets_dst)
+        return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (!ws || ws_bytes < feq_edgewise_fwd_src_pool_workspace(L, b, rank, E))
+        return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
+    const DstPool dp{perm_dst, offsets_dst, dst, attn, num_dst, heads, chan_per_head, out, nullptr};
+    const int rc = ew_split_fwd(*L, *b, rank, E, x, src, num_src, P, Q, dist, C, F, y_pos, ws, ws_bytes,
+                                (flags & FEQ_EW_HALF_ACCURACY) != 0, s, &dp);
+    return rc == -1 ? fail(FEQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned") : rc;
+}
+
+extern "C" int feq_edgewise_bwd_src_pool(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                         int64_t E, const float* grad_out, const float* attn,
+                                         int32_t heads, int32_t chan_per_head, const int64_t* dst,
+                                         int64_t num_dst, const float* x, int64_t num_src,
+                                         const int64_t* src, const int32_t* perm_src,
+                                         const int32_t* offsets_src, const float* P, const float* Q,
+                                         const float* dist, const float* C, const float* F,
+                                         float* gx_nodes, float* gC, float* gF, float* gdist,
+                                         int32_t flags, void* ws, size_t ws_bytes,
+                                         feq_stream_t stream) {
+    if (int rc = check_layout(L)) return rc;
+    if (flags & ~FEQ_EW_HALF_ACCURACY) return fail(FEQ_ERR_INVALID, "unknown flags 0x%x", flags);
+    if (int rc = check_binning(b)) return rc;
+    if (rank < 1) return fail(FEQ_ERR_INVALID, "rank must be positive");
+    if (E < 0 || num_src < 0 || num_dst < 0) return fail(FEQ_ERR_INVALID, "negative edge or node count");
+    if (E > 0x7fffffffLL || num_src > 0x7fffffffLL || num_dst > 0x7fffffffLL)
+        return fail(FEQ_ERR_UNSUPPORTED, "more than 2^31-1 edges or nodes");
+    if (int rc = check_pool_args(L, heads, chan_per_head)) return rc;
+    if (!gC || !gF || (num_src > 0 && !gx_nodes))
+        return fail(FEQ_ERR_INVALID, "grad_x_nodes, grad_C and grad_F are required");
+    if (!feq_edgewise_pool_supported(L, b, rank))
+        return fail(FEQ_ERR_UNSUPPORTED, "no pooled message-passing kernels for this layout");
+    hipStream_t s = stream_of(stream);
+    if (E == 0 || num_dst == 0) {
+        // no edge reaches the pooled output: every gradient is zero
+        if (int rc = fill_zero(gF, static_cast<int64_t>(b->num_bins + 1) * rank * L->wdim, s)) return rc;
+        if (int rc = fill_zero(gx_nodes, num_src * L->cin * L->din, s)) return rc;
+        if (gdist)
+            if (int rc = fill_zero(gdist, E, s)) return rc;
+        return fill_zero(gC, static_cast<int64_t>(rank) * L->cout * L->cin, s);
+    }
+    if (!grad_out || !attn || !dst || !x || !src || !perm_src || !offsets_src || !P || !Q || !dist ||
+        !C || !F)
+        return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (!ws || ws_bytes < feq_edgewise_bwd_src_nodes_workspace(L, b, rank, E))
+        return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
+    const NodeScatter ns{perm_src, offsets_src, gx_nodes, nullptr};
+    const DstPool dp{nullptr, nullptr, dst, attn, num_dst, heads, chan_per_head, nullptr, nullptr};
+    const int rc = ew_split_bwd(*L, *b, rank, E, grad_out, x, src, num_src, P, Q, dist, C, F, nullptr,
+                                gC, gF, gdist, &ns, ws, ws_bytes, (flags & FEQ_EW_HALF_ACCURACY) != 0, s,
+                                &dp);
+    return rc == -1 ? fail(FEQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned") : rc;
+}

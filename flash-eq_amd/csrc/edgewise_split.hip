@@ -277,6 +277,56 @@ __device__ __forceinline__ void scatter_stage(const float* stage, const int* nod
     }
 }
 
+// scatter_stage for the pooled forward: row j of the staged tile weighted by
+// w[j][head] (w: kPoolMaxHeads floats per position) before the per-node sums
+// by destination.  A float4 of a row lies within one head (hc * D % 4 == 0,
+// checked by the host).
+template <int CH, int D>
+__device__ __forceinline__ void scatter_stage_w(const float* stage, const int* node, const float* w,
+                                                const DstPool& DP, int64_t tile, int nval) {
+    constexpr int ROW4 = CH * D / 4, SS4 = stage_stride(CH * D) / 4;
+    static_assert((CH * D) % 4 == 0, "rows of whole float4s");
+    const float4* s4 = reinterpret_cast<const float4*>(stage);
+    float4* out4 = reinterpret_cast<float4*>(DP.out);
+    float4* part4 = reinterpret_cast<float4*>(DP.part);
+    for (int q = threadIdx.x; q < ROW4; q += kThreads) {
+        const int hq = (4 * q) / (DP.hc * D);
+        const int h = hq < DP.heads ? hq : DP.heads - 1;
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        int js = 0;   // first position of the current node's run
+        for (int j = 0; j < nval; ++j) {
+            const float4 v = s4[j * SS4 + q];
+            const float a = w[j * kPoolMaxHeads + h];
+            acc.x += a * v.x;
+            acc.y += a * v.y;
+            acc.z += a * v.z;
+            acc.w += a * v.w;
+            const int n = node[j];
+            if (j + 1 < nval && node[j + 1] == n) continue;
+            if (n >= 0) {
+                if (node_crosses_tiles(DP.offsets[n], DP.offsets[n + 1]))
+                    part4[(2 * tile + (js == 0 ? 0 : 1)) * ROW4 + q] = acc;
+                else
+                    out4[static_cast<int64_t>(n) * ROW4 + q] = acc;
+            }
+            acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            js = j + 1;
+        }
+    }
+}
+
+// Destination node of an edge of the pooled form, -1 outside [0, ndst).
+__device__ __forceinline__ int64_t pool_node(const DstPool& DP, int64_t e) {
+    const int64_t n = DP.dst[e];
+    return n >= 0 && n < DP.ndst ? n : -1;
+}
+
+// Head of output channel c in the pooled form.
+__device__ __forceinline__ int pool_head(const DstPool& DP, int c) {
+    const int h = c / DP.hc;
+    return h < DP.heads ? h : DP.heads - 1;
+}
+
 // Rows of the nodes that scatter_stage did not write: the sums of the partial
 // rows of a node that crosses tile boundaries (in tile order), zeros for a node
 // without edges.  One 64-lane workgroup per node.
@@ -466,12 +516,19 @@ __device__ __forceinline__ void edge_powers(float s, int n, float* out) {
 // are issued, then the Q rotation, staged in LDS and stored with coalesced
 // 16-byte stores.  Row strides of the per-edge LDS blocks are odd, so the 16
 // edges of a wave's lanes hit distinct banks.
-template <int CIN, int COUT, int LIN, int LOUT, int K, int OCC, bool GATHER, bool LP>
+//
+// POOL (message-passing form only): tile positions walk the CSR by destination
+// (DP.perm), and the staged tile is summed per destination node with the
+// attention weights (scatter_stage_w) instead of stored per edge; y, when not
+// NULL, receives the unweighted rows in that position order.
+template <int CIN, int COUT, int LIN, int LOUT, int K, int OCC, bool GATHER, bool LP, bool POOL>
 __global__ void __launch_bounds__(kThreads, OCC)
 k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
           const float* __restrict__ P, const float* __restrict__ Q,
           const float* __restrict__ dist, const h8* __restrict__ Cfrag,
-          const float* __restrict__ Cinv, const float* __restrict__ F, float* __restrict__ y) {
+          const float* __restrict__ Cinv, const float* __restrict__ F, float* __restrict__ y,
+          DstPool DP) {
+    static_assert(GATHER || !POOL, "the pooled form is a message-passing form");
     using T = Canon<LIN, LOUT>;
     using TG = TermGroups<LIN, LOUT, false>;
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
@@ -496,6 +553,12 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
     float* sSp = sSout + kNE;                                    // s_e^l, l < NSP
     float* sInvK = sSp + kNE * NSP;
     EdgeState* sE = reinterpret_cast<EdgeState*>(sInvK + K);
+    int* sNode = reinterpret_cast<int*>(sE + kNE);               // destination per position (POOL)
+    float* sW = reinterpret_cast<float*>(sNode + kNE);           // [kNE][kPoolMaxHeads] weights (POOL)
+    // tile position -> edge: the identity, or the CSR-by-destination permutation
+    auto edge = [&](int64_t j) -> int64_t {
+        if constexpr (POOL) return DP.perm[j]; else return j;
+    };
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
@@ -509,13 +572,16 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
     float xr[NPR][4 * DIN];
     float pr[rows_per_thread<DIN * DIN>()], qr[rows_per_thread<DOUT * DOUT>()];
     float rd;
+    int nd = -1;       // POOL: destination of position tid (tid < kNE)
+    float wt = 0.0f;   // POOL: weight (position tid / kPoolMaxHeads, head tid % kPoolMaxHeads)
+    static_assert(kNE * kPoolMaxHeads <= kThreads, "one weight per thread");
     auto load_tile = [&](int64_t t) {
         const int64_t f0 = t * kNE;
 #pragma unroll
         for (int p = 0; p < NPR; ++p) {
             const int q = tid + kThreads * p;
             const int e = q / NC4, c4 = q % NC4;
-            const int64_t row = q < kNE * NC4 && f0 + e < E ? x_row<GATHER>(X, f0 + e) : -1;
+            const int64_t row = q < kNE * NC4 && f0 + e < E ? x_row<GATHER>(X, edge(f0 + e)) : -1;
             if (row >= 0) {
                 const float4* src = reinterpret_cast<const float4*>(X.x + (row * CIN + 4 * c4) * DIN);
 #pragma unroll
@@ -531,9 +597,15 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
                 for (int v = 0; v < 4 * DIN; ++v) xr[p][v] = 0.0f;
             }
         }
-        load_rows<DIN * DIN, false>(P, f0, E, nullptr, pr);
-        load_rows<DOUT * DOUT, false>(Q, f0, E, nullptr, qr);
-        rd = (tid < kNE && f0 + tid < E) ? dist[f0 + tid] : 1.0f;
+        load_rows<DIN * DIN, POOL>(P, f0, E, DP.perm, pr);
+        load_rows<DOUT * DOUT, POOL>(Q, f0, E, DP.perm, qr);
+        rd = (tid < kNE && f0 + tid < E) ? dist[edge(f0 + tid)] : 1.0f;
+        if constexpr (POOL) {
+            nd = (tid < kNE && f0 + tid < E) ? static_cast<int>(pool_node(DP, edge(f0 + tid))) : -1;
+            const int wj = tid / kPoolMaxHeads, wh = tid % kPoolMaxHeads;
+            wt = (wj < kNE && f0 + wj < E && wh < DP.heads)
+                     ? DP.attn[edge(f0 + wj) * DP.heads + wh] : 0.0f;
+        }
     };
 
     // fs rows of this thread: rotation, per-edge scale, split, fragment writes
@@ -597,7 +669,9 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
             es.s = rd / (rd + B.sh_scale);
             sE[tid] = es;
             edge_powers(es.s, NSP, sSp + tid * NSP);
+            if constexpr (POOL) sNode[tid] = nd;
         }
+        if constexpr (POOL) sW[tid] = wt;
         const bool dense =
             __syncthreads_or(off_block_nonzero_rows(pr, pbits) | off_block_nonzero_rows(qr, qbits)) != 0;
 
@@ -733,8 +807,10 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
             stage_rows<COUT, DOUT>(reinterpret_cast<float*>(sB), le, 16 * (wave + 4 * j) + 4 * lg, out);
         }
         __syncthreads();
-        flush_stage<COUT, DOUT>(reinterpret_cast<const float*>(sB), y + e0 * COUT * DOUT,
-                                static_cast<int>(E - e0 < kNE ? E - e0 : kNE));
+        const int nval = static_cast<int>(E - e0 < kNE ? E - e0 : kNE);
+        if (!POOL || y) flush_stage<COUT, DOUT>(reinterpret_cast<const float*>(sB), y + e0 * COUT * DOUT, nval);
+        if constexpr (POOL)
+            scatter_stage_w<COUT, DOUT>(reinterpret_cast<const float*>(sB), sNode, sW, DP, tile, nval);
     }
 }
 
@@ -752,15 +828,19 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
 // summed over the wave's four lane groups with lane swaps (four values per
 // register), unscaled, and summed over the four waves in LDS.  Rotations use the degree blocks when the tile's P
 // and Q have no entry off them; dx is staged in LDS and stored coalesced.
-template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER, bool SCATTER, bool LP>
+//
+// GP (pooled form): gy is the pooled output's gradient (ndst rows) and edge e
+// reads attn[e, head(c)] gy[dst[e], c, :] (DstPool).
+template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER, bool SCATTER, bool LP, bool GP>
 __global__ void __launch_bounds__(kThreads, 2)
 k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
             XRows X, const float* __restrict__ P,
             const float* __restrict__ Q, const float* __restrict__ dist,
             const h8* __restrict__ Cfrag, const float* __restrict__ Cinv,
             const float* __restrict__ F, float* __restrict__ gx, float* __restrict__ dFe,
-            NodeScatter NS) {
+            NodeScatter NS, DstPool DP) {
     static_assert(GATHER || !SCATTER, "the per-node sums need the message-passing form");
+    static_assert(GATHER || !GP, "the pooled form is a message-passing form");
     using T = Canon<LIN, LOUT>;
     using TG = TermGroups<LIN, LOUT, true>;
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
@@ -806,6 +886,7 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     // global loads of one tile: gy rows of the producer threads, x rows of the
     // lane layout, P, Q, distances (zeros past the last edge)
     float gr[NPR][4 * DOUT];
+    float gw[NPR];   // GP: attention weight of the producer's channels (0 without a destination)
     float xl[RPW][4 * DIN];
     // P and Q of the prefetched tile: each thread's share of one edge row
     float prs[rows_per_thread<DIN * DIN>()], qrs[rows_per_thread<DOUT * DOUT>()];
@@ -817,8 +898,19 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
         for (int p = 0; p < NPR; ++p) {
             const int q = tid + kThreads * p;
             const int e = q / NC4, c4 = q % NC4;
+            int64_t grow = -1;   // row of gy this producer reads
+            gw[p] = 1.0f;
             if (q < kNE * NC4 && f0 + e < E) {
-                const float4* src = reinterpret_cast<const float4*>(gy + (edge(f0 + e) * COUT + 4 * c4) * DOUT);
+                const int64_t ee = edge(f0 + e);
+                if constexpr (GP) {
+                    grow = pool_node(DP, ee);
+                    gw[p] = grow >= 0 ? DP.attn[ee * DP.heads + pool_head(DP, 4 * c4)] : 0.0f;
+                } else {
+                    grow = ee;
+                }
+            }
+            if (grow >= 0) {
+                const float4* src = reinterpret_cast<const float4*>(gy + (grow * COUT + 4 * c4) * DOUT);
 #pragma unroll
                 for (int v = 0; v < DOUT; ++v) {
                     const float4 f = src[v];
@@ -870,6 +962,12 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             const int ee = act ? e : 0;
             float gd[4][DOUT];
             rotate_cols<LOUT, SP, 4>(gr[p], sQ + ee * QS, gd);
+            if constexpr (GP) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int o = 0; o < DOUT; ++o) gd[r][o] *= gw[p];
+            }
             float m = 0.0f;
 #pragma unroll
             for (int r = 0; r < 4; ++r)
@@ -1123,12 +1221,15 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 // buffer with the tile's P and Q.  Wave w owns output rows 16 w .. 16 w + 15,
 // whose U_k rows its own lanes produce, so only the fs fragments are shared
 // between waves.  One partial dC per workgroup.
-template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER, bool LP>
+//
+// GP (pooled form): edge e reads attn[e, head(c)] gy[dst[e], c, :] (DstPool).
+template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER, bool LP, bool GP>
 __global__ void __launch_bounds__(kThreads, 2)
 k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
             XRows X, const float* __restrict__ P,
             const float* __restrict__ Q, const float* __restrict__ dist,
-            const float* __restrict__ F, float* __restrict__ dC_part) {
+            const float* __restrict__ F, float* __restrict__ dC_part, DstPool DP) {
+    static_assert(GATHER || !GP, "the pooled form is a message-passing form");
     using T = Canon<LIN, LOUT>;
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
     constexpr int PS = DIN * DIN | 1, QS = DOUT * DOUT | 1;
@@ -1169,7 +1270,7 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
         // Unconditional: edges past the last (and channels past Cin / Cout) read
         // the last one's rows; their radial functions are zero, so their U_k rows
         // are zero and they add nothing to dC.
-        float xr[4][DIN], gr[4][DOUT];
+        float xr[4][DIN], gr[4][DOUT], gw[4];
         const int pci = pc < CIN ? pc : CIN - 1, pco = pc < COUT ? pc : COUT - 1;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -1178,7 +1279,15 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             // the edge is then marked invalid, so it adds nothing either
             const int64_t row = x_row<GATHER>(X, e);
             const float* xs = X.x + ((row >= 0 ? row : 0) * CIN + pci) * DIN;
-            const float* gs = gy + (e * COUT + pco) * DOUT;
+            int64_t grow = e;
+            gw[q] = 1.0f;
+            if constexpr (GP) {
+                // pooled form: a destination outside [0, ndst) reads row 0 with weight 0
+                grow = pool_node(DP, e);
+                gw[q] = grow >= 0 ? DP.attn[e * DP.heads + pool_head(DP, pco)] : 0.0f;
+                grow = grow >= 0 ? grow : 0;
+            }
+            const float* gs = gy + (grow * COUT + pco) * DOUT;
 #pragma unroll
             for (int d = 0; d < DIN; ++d) xr[q][d] = xs[d];
 #pragma unroll
@@ -1230,7 +1339,7 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 #pragma unroll
                 for (int i = 0; i < DIN; ++i) fs[q][i] = t1[0][i] * pi[i];
 #pragma unroll
-                for (int o = 0; o < DOUT; ++o) gd[q][o] = t2[0][o] * po[o];
+                for (int o = 0; o < DOUT; ++o) gd[q][o] = t2[0][o] * po[o] * gw[q];
             }
             float m = 0.0f;
 #pragma unroll
@@ -1407,7 +1516,7 @@ constexpr size_t ews_fwd_lds() {
     constexpr size_t FR = 2 * T::DIN * (CIN / 32) * 1024, ST = 4 * kNE * stage_stride(COUT * T::DOUT);
     return (FR > ST ? FR : ST) +
            4 * (kNE * PS + kNE * QS + kNE * KWS + kNE + kNE * (LIN + LOUT + 1) + K) +
-           kNE * sizeof(EdgeState);
+           kNE * sizeof(EdgeState) + kNE * sizeof(int) + 4 * kNE * kPoolMaxHeads;
 }
 
 // Workgroups per CU of the forward.  Two, measured on MI355X at 160k edges
@@ -1444,30 +1553,56 @@ constexpr size_t ews_cfrag_bytes() {
     return align_up(static_cast<size_t>(K) * COUT * CIN * 2 * sizeof(_Float16), 256) + 256;
 }
 
+// Workspace of the pooled forward: the C fragments, then two partial rows per tile.
+template <int CIN, int COUT, int LIN, int LOUT, int K>
+size_t ews_pool_fwd_ws(int64_t E) {
+    using T = Canon<LIN, LOUT>;
+    return ews_cfrag_bytes<CIN, COUT, K>() +
+           align_up(4 * static_cast<size_t>(ceil_div(E, kNE)) * 2 * COUT * T::DOUT, 256) + 256;
+}
+
 // lp: one fp16 product per operand pair (message-passing form only).
+// dp: the pooled form (message-passing form only).
 template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER>
 int launch_ews_fwd(const feq_binning& B, int64_t E, XRows x, const float* P, const float* Q,
                    const float* dist, const float* C, const float* F, float* y, void* ws,
-                   size_t ws_bytes, bool lp, hipStream_t s) {
+                   size_t ws_bytes, bool lp, const DstPool* dp, hipStream_t s) {
+    using T = Canon<LIN, LOUT>;
     constexpr size_t lds = ews_fwd_lds<CIN, COUT, LIN, LOUT, K>();
     constexpr int occ = ews_fwd_occ<CIN, COUT, LIN, LOUT, K>();
     static_assert(lds <= 80 * 1024, "two forward workgroups must fit one CU's LDS");
-    if (!ws || ws_bytes < ews_cfrag_bytes<CIN, COUT, K>())
-        return fail(FEQ_ERR_WORKSPACE, "edgewise forward workspace too small");
+    const size_t need = dp ? ews_pool_fwd_ws<CIN, COUT, LIN, LOUT, K>(E) : ews_cfrag_bytes<CIN, COUT, K>();
+    if (!ws || ws_bytes < need) return fail(FEQ_ERR_WORKSPACE, "edgewise forward workspace too small");
+    const int64_t ntiles = ceil_div(E, kNE);
     Carver cv(ws);
     h8* frag = cv.take<h8>(static_cast<size_t>(K) * COUT * CIN / 4);
     float* inv = cv.take<float>(K);
+    DstPool DP{};
+    if (dp) {
+        DP = *dp;
+        DP.part = cv.take<float>(static_cast<size_t>(ntiles) * 2 * COUT * T::DOUT);
+    }
     auto prep = k_ews_prep<K, COUT, CIN, false>;
     FEQ_LAUNCH("k_ews_prep", prep, dim3(K * COUT / 16), dim3(kThreads), 0, s, C, frag, inv);
-    auto kern = k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, GATHER, false>;
-    if constexpr (GATHER)
-        if (lp) kern = k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, true, true>;
+    auto kern = k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, GATHER, false, false>;
+    if constexpr (GATHER) {
+        if (dp)
+            kern = lp ? k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, true, true, true>
+                      : k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, true, false, true>;
+        else if (lp)
+            kern = k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, true, true, false>;
+    } else {
+        if (dp) return fail(FEQ_ERR_INVALID, "the pooled form needs the message-passing form");
+    }
     if (int rc = ews_set_lds(reinterpret_cast<const void*>(kern), lds)) return rc;
-    const int64_t ntiles = ceil_div(E, kNE);
     const int64_t g = static_cast<int64_t>(ews_cus()) * occ;
     const int grid = static_cast<int>(ntiles < g ? ntiles : g);
     FEQ_LAUNCH("k_ews_fwd", kern, dim3(grid), dim3(kThreads), lds, s, B, E, ntiles, x, P, Q, dist,
-               frag, inv, F, y);
+               frag, inv, F, y, DP);
+    if (dp) {
+        const NodeScatter NS{DP.perm, DP.offsets, DP.out, DP.part};
+        if (int rc = node_fix(NS, DP.ndst, static_cast<int64_t>(COUT * T::DOUT / 4), s)) return rc;
+    }
     return FEQ_OK;
 }
 
@@ -1492,7 +1627,8 @@ template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER>
 int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const float* gy,
                    XRows x, const float* P, const float* Q, const float* dist,
                    const float* C, const float* F, float* gx, float* gC, float* gF, float* gdist,
-                   const NodeScatter* ns, void* ws, size_t ws_bytes, bool lp, hipStream_t s) {
+                   const NodeScatter* ns, void* ws, size_t ws_bytes, bool lp, const DstPool* dp,
+                   hipStream_t s) {
     using T = Canon<LIN, LOUT>;
     constexpr size_t xlds = ews_bwd_x_lds<CIN, COUT, LIN, LOUT, K>();
     constexpr size_t clds = ews_bwd_c_lds<CIN, COUT, LIN, LOUT, K>();
@@ -1515,32 +1651,40 @@ int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const f
         NS.part = cv.take<float>(static_cast<size_t>(ntiles) * 2 * CIN * T::DIN);
     }
     if (!ws || cv.used > ws_bytes) return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
+    if (dp && !ns) return fail(FEQ_ERR_INVALID, "the pooled form needs the per-node input gradient");
+    const DstPool DP = dp ? *dp : DstPool{};
     auto prep = k_ews_prep<K, CIN, COUT, true>;
     FEQ_LAUNCH("k_ews_prep", prep, dim3(K * CIN / 16), dim3(kThreads), 0, s, C, frag, inv);
+    auto kc = k_ews_bwd_c<CIN, COUT, LIN, LOUT, K, GATHER, false, false>;
     if constexpr (GATHER) {
         if (ns) {
-            auto kx = lp ? k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, true>
-                         : k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, false>;
+            auto kx = lp ? k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, true, false>
+                         : k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, false, false>;
+            if (dp)
+                kx = lp ? k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, true, true>
+                        : k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, false, true>;
             if (int rc = ews_set_lds(reinterpret_cast<const void*>(kx), xlds)) return rc;
             FEQ_LAUNCH("k_ews_bwd_x", kx, dim3(G), dim3(kThreads), xlds, s, B, E, ntiles, gy, x, P, Q,
-                       dist, frag, inv, F, nullptr, dFe, NS);
+                       dist, frag, inv, F, nullptr, dFe, NS, DP);
             if (int rc = node_fix(NS, x.nsrc, static_cast<int64_t>(CIN * T::DIN / 4), s)) return rc;
         }
+        if (dp)
+            kc = lp ? k_ews_bwd_c<CIN, COUT, LIN, LOUT, K, true, true, true>
+                    : k_ews_bwd_c<CIN, COUT, LIN, LOUT, K, true, false, true>;
+        else if (lp)
+            kc = k_ews_bwd_c<CIN, COUT, LIN, LOUT, K, true, true, false>;
     } else {
         if (ns) return fail(FEQ_ERR_INVALID, "per-node sums need the message-passing form");
     }
     if (!ns) {
-        auto kx = k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, GATHER, false, false>;
+        auto kx = k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, GATHER, false, false, false>;
         if (int rc = ews_set_lds(reinterpret_cast<const void*>(kx), xlds)) return rc;
         FEQ_LAUNCH("k_ews_bwd_x", kx, dim3(G), dim3(kThreads), xlds, s, B, E, ntiles, gy, x, P, Q,
-                   dist, frag, inv, F, gx, dFe, NS);
+                   dist, frag, inv, F, gx, dFe, NS, DP);
     }
-    auto kc = k_ews_bwd_c<CIN, COUT, LIN, LOUT, K, GATHER, false>;
-    if constexpr (GATHER)
-        if (lp) kc = k_ews_bwd_c<CIN, COUT, LIN, LOUT, K, true, true>;
     if (int rc = ews_set_lds(reinterpret_cast<const void*>(kc), clds)) return rc;
     FEQ_LAUNCH("k_ews_bwd_c", kc, dim3(G), dim3(kThreads), clds, s, B, E, ntiles, gy, x, P, Q,
-               dist, F, dCp);
+               dist, F, dCp, DP);
     return ew_tail(L, B, K, E, dist, F, dFe, dCp, G, ncc, gC, gF, gdist, tail, s);
 }
 
@@ -1607,22 +1751,26 @@ size_t ew_split_bwd_workspace(const feq_layout& L, const feq_binning& B, int ran
 int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* gy,
                  const float* x, const int64_t* src, int64_t nsrc, const float* P, const float* Q,
                  const float* dist, const float* C, const float* F, float* gx, float* gC, float* gF,
-                 float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, bool lp, hipStream_t s) {
+                 float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, bool lp, hipStream_t s,
+                 const DstPool* dp) {
     float* gout = ns ? ns->out : gx;
     if (rank != 4 || !gout || !aligned16(gy) || !aligned16(x) || !aligned16(P) || !aligned16(Q) ||
         !aligned16(gout) || (ns && !src))
         return -1;
-    if (ew0_supported(L, rank))
+    if (ew0_supported(L, rank)) {
+        if (dp) return fail(FEQ_ERR_UNSUPPORTED, "no pooled form for scalar-output layouts");
         return ew0_bwd(L, B, rank, E, gy, x, src, nsrc, P, Q, dist, C, F, gx, gC, gF, gdist, ns, ws,
                        ws_bytes, s);
+    }
+    if (dp && !src) return fail(FEQ_ERR_INVALID, "the pooled form needs the message-passing form");
     const XRows X{x, src, nsrc};
 #define FEQ_BWD(ci, co, li, lo)                                                                   \
     if constexpr ((ci) % 64 == 0) {                                                               \
         if (L.cin == ci && L.cout == co && canonical(L, li, lo))                                  \
             return src ? launch_ews_bwd<ci, co, li, lo, 4, true>(L, B, E, gy, X, P, Q, dist, C, F, \
-                                                                 gx, gC, gF, gdist, ns, ws, ws_bytes, lp, s) \
+                                                                 gx, gC, gF, gdist, ns, ws, ws_bytes, lp, dp, s) \
                        : launch_ews_bwd<ci, co, li, lo, 4, false>(L, B, E, gy, X, P, Q, dist, C, F, \
-                                                                  gx, gC, gF, gdist, ns, ws, ws_bytes, lp, s); \
+                                                                  gx, gC, gF, gdist, ns, ws, ws_bytes, lp, dp, s); \
     }
     FEQ_EWS_SHAPES(FEQ_BWD)
 #undef FEQ_BWD
@@ -1632,17 +1780,22 @@ int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
 int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
                  const int64_t* src, int64_t nsrc, const float* P, const float* Q, const float* dist,
                  const float* C, const float* F, float* y, void* ws, size_t ws_bytes, bool lp,
-                 hipStream_t s) {
+                 hipStream_t s, const DstPool* dp) {
     if (rank != 4) return -1;
-    if (ew0_supported(L, rank)) return ew0_fwd(L, B, rank, E, x, src, nsrc, P, Q, dist, C, F, y, s);
-    if (!aligned16(x) || !aligned16(P) || !aligned16(Q) || !aligned16(y)) return -1;
+    if (ew0_supported(L, rank)) {
+        if (dp) return fail(FEQ_ERR_UNSUPPORTED, "no pooled form for scalar-output layouts");
+        return ew0_fwd(L, B, rank, E, x, src, nsrc, P, Q, dist, C, F, y, s);
+    }
+    if (!aligned16(x) || !aligned16(P) || !aligned16(Q) || !aligned16(y) || (dp && !aligned16(dp->out)))
+        return -1;
+    if (dp && !src) return fail(FEQ_ERR_INVALID, "the pooled form needs the message-passing form");
     const XRows X{x, src, nsrc};
 #define FEQ_FWD(ci, co, li, lo)                                                                  \
     if (L.cin == ci && L.cout == co && canonical(L, li, lo))                                     \
         return src ? launch_ews_fwd<ci, co, li, lo, 4, true>(B, E, X, P, Q, dist, C, F, y, ws,    \
-                                                             ws_bytes, lp, s)                     \
+                                                             ws_bytes, lp, dp, s)                 \
                    : launch_ews_fwd<ci, co, li, lo, 4, false>(B, E, X, P, Q, dist, C, F, y, ws,   \
-                                                              ws_bytes, lp, s);
+                                                              ws_bytes, lp, dp, s);
     FEQ_EWS_SHAPES(FEQ_FWD)
 #undef FEQ_FWD
     return -1;
@@ -1659,6 +1812,19 @@ bool ew_split_supported(const feq_layout& L, const feq_binning& B, int rank, boo
     FEQ_EWS_SHAPES(FEQ_SUP)
 #undef FEQ_SUP
     return ok;
+}
+
+bool ew_pool_supported(const feq_layout& L, const feq_binning& B, int rank) {
+    return rank == 4 && !ew0_supported(L, rank) && ew_split_supported(L, B, rank, true);
+}
+
+size_t ew_pool_fwd_workspace(const feq_layout& L, int rank, int64_t E) {
+    if (rank != 4) return 0;
+#define FEQ_WS(ci, co, li, lo) \
+    if (L.cin == ci && L.cout == co && canonical(L, li, lo)) return ews_pool_fwd_ws<ci, co, li, lo, 4>(E);
+    FEQ_EWS_SHAPES(FEQ_WS)
+#undef FEQ_WS
+    return 0;
 }
 
 }  // namespace feq

@@ -97,6 +97,29 @@ struct NodeScatter {
     float* part;   // (ntiles, 2, Cin, Din), carved from the backward's workspace
 };
 
+// The V projection of attention fused with the attention's head weighting and
+// sum pooling (attention.py:307-314 with pooling.py:21-30).  The forward walks
+// the edges in destination order (perm, offsets: the CSR by destination over
+// ndst nodes) and sums attn[e, head(c)] y_e[c, :] per destination node, a
+// node crossing a tile boundary leaving partial rows as in NodeScatter; y_e is
+// never written unless the caller keeps it (in destination order) for the
+// backward.  The backward reads gy_e[c, :] = attn[e, head(c)] gout[dst[e], c, :]
+// where the unfused form reads the per-edge gradient, so that is never formed
+// either.  head(c) = min(c / hc, heads - 1); edges whose destination lies
+// outside [0, ndst) add nothing and get a zero gradient.
+constexpr int kPoolMaxHeads = 16;
+struct DstPool {
+    const int32_t* perm;
+    const int32_t* offsets;
+    const int64_t* dst;
+    const float* attn;   // (E, heads)
+    int64_t ndst;
+    int heads;
+    int hc;              // channels per head
+    float* out;          // forward: (ndst, Cout, Dout)
+    float* part;         // forward: (ntiles, 2, Cout, Dout), carved from the workspace
+};
+
 // Split-fp16 fast paths (edgewise_split.hip); -1 when the shape has none.
 size_t ew_split_workspace(const feq_layout& L, int rank);
 // nodes: with the per-node sums (NodeScatter partial rows).
@@ -110,12 +133,19 @@ size_t ew_split_bwd_workspace(const feq_layout& L, const feq_binning& B, int ran
 int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* gy,
                  const float* x, const int64_t* src, int64_t nsrc, const float* P, const float* Q,
                  const float* dist, const float* C, const float* F, float* gx, float* gC, float* gF,
-                 float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, bool lp, hipStream_t s);
+                 float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, bool lp, hipStream_t s,
+                 const DstPool* dp = nullptr);
+// dp (may be NULL, needs src): the pooled form; y then receives the per-edge
+// rows in destination order, or is NULL.
 int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
                  const int64_t* src, int64_t nsrc, const float* P, const float* Q, const float* dist,
                  const float* C, const float* F, float* y, void* ws, size_t ws_bytes, bool lp,
-                 hipStream_t s);
+                 hipStream_t s, const DstPool* dp = nullptr);
 bool ew_split_supported(const feq_layout& L, const feq_binning& B, int rank, bool backward);
+// Layouts with the pooled form (the split shapes with Cin = 64, not the
+// scalar-output family) and its forward workspace.
+bool ew_pool_supported(const feq_layout& L, const feq_binning& B, int rank);
+size_t ew_pool_fwd_workspace(const feq_layout& L, int rank, int64_t E);
 // Rows of the nodes that the per-node sums of a tile walk did not write (nodes
 // crossing 16-edge tile boundaries: their partial rows summed in tile order;
 // nodes without edges: zeros).  row4 = Cin Din / 4.

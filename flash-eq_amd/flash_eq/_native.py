@@ -18,6 +18,7 @@ from ._build import LIB_PATH
 FEQ_MAX_BLOCKS = 17
 FEQ_MAX_SLOTS = 128
 FEQ_EW_HALF_ACCURACY = 1          # flags of feq_edgewise_*_ex
+POOL_MAX_HEADS = 16               # heads of feq_edgewise_*_src_pool
 
 
 class CUDANotAvailableError(RuntimeError):
@@ -80,6 +81,13 @@ _SIGS = {
     "feq_edgewise_bwd_src_nodes_ex": ([_P, _P, _I32, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P,
                                        _P, _P, _P, _P, _P, _P, _I32, _P, _SZ, _P], ctypes.c_int),
     "feq_edgewise_bwd_src_nodes_workspace": ([_P, _P, _I32, _I64], _SZ),
+    "feq_edgewise_pool_supported": ([_P, _P, _I32], ctypes.c_int),
+    "feq_edgewise_fwd_src_pool_workspace": ([_P, _P, _I32, _I64], _SZ),
+    "feq_edgewise_fwd_src_pool": ([_P, _P, _I32, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _I32, _I32,
+                                   _P, _P, _P, _I64, _P, _P, _I32, _P, _SZ, _P], ctypes.c_int),
+    "feq_edgewise_bwd_src_pool": ([_P, _P, _I32, _I64, _P, _P, _I32, _I32, _P, _I64, _P, _I64, _P, _P,
+                                   _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _SZ, _P],
+                                  ctypes.c_int),
     "feq_edgewise_bwd_src_nodes": ([_P, _P, _I32, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P,
                                     _P, _P, _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
     "feq_edgewise_hl_supported": ([_P, _P, _I32], ctypes.c_int),
@@ -123,6 +131,7 @@ _SIGS = {
     "feq_attn_pool_fwd": ([_P, _P, _I64, _I32, _I32, _I32, _P, _P, _I64, _P, _P], ctypes.c_int),
     "feq_attn_pool_bwd": ([_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P],
                           ctypes.c_int),
+    "feq_attn_pool_grad_attn": ([_P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P], ctypes.c_int),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGS)

@@ -122,6 +122,18 @@ class EquivariantAttention(nn.Module):
             return run_float32(self, half, (P, Q_basis, node_features, distances, graph),
                                dict(edge_features=edge_features))
         qk = self.linear_qk(self.norm_qk(node_features))            # (N, 2 mult, dim)
+        if edge_features is None and self.pool.reduce == "sum":
+            # V projection, head weighting and sum pooling in one pass over the
+            # edges where the fused kernels cover the layer (neither attn * V
+            # nor its gradient is formed)
+            attn = self.attention.node_attention_weights(qk, graph, distances)
+            out = self.linear_v.attention_pool(P, Q_basis, node_features.contiguous(), distances, graph,
+                                               attn, self.num_heads)
+            if out is not None:
+                return out
+            V = self.linear_v(P, Q_basis, node_features.contiguous(), distances, graph=graph)
+            perm, offsets = graph.csr()
+            return AttnPoolFn.apply(V, attn, graph.dst, perm, offsets, graph.num_nodes, self.num_heads)
         if edge_features is not None:
             gathered = graph.gather_src(node_features) + edge_features
             V = self.linear_v(P, Q_basis, gathered, distances)       # (E, mult_out, dim_out)

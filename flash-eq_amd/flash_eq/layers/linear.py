@@ -21,8 +21,9 @@ import torch
 import torch.nn as nn
 
 from .. import _native as N
-from ..ops import (edgewise_linear, edgewise_linear_src, edgewise_src_supported, embedding_for,
-                   rows_weight_grad, BiasRowsFn, EqLinearFn)
+from ..ops import (edgewise_attention_pool, edgewise_linear, edgewise_linear_src,
+                   edgewise_pool_supported, edgewise_src_supported, embedding_for, rows_weight_grad,
+                   BiasRowsFn, EqLinearFn)
 from ..representations import ProductRepr, Repr
 from .radial import SeparableRadialNet
 from ..utils import half_precision_active
@@ -158,6 +159,41 @@ class EquivariantEdgewiseLinear(nn.Module):
             edge_features = graph.gather_src(edge_features)
         return edgewise_linear(edge_features, P, Q, distances, rw.channel_patterns,
                                rw.radial_functions(), layout, binning, rw.rank)
+
+    def attention_pool(self, P: torch.Tensor, Q: torch.Tensor, node_features: torch.Tensor,
+                       distances: torch.Tensor, graph, attn: torch.Tensor, num_heads: int):
+        """sum over the edges e into n of attn[e, head(c)] * layer(x[src])[e, c, :]:
+        the layer in message-passing form fused with an attention's head
+        weighting and sum pooling by destination (``attention.py:307-314``,
+        ``pooling.py:21-30``), channel c in head c // (Cout / num_heads).  Returns
+        (num_nodes, Cout, Dout), or None where the fused kernels do not cover the
+        call (the caller then forms V and pools it)."""
+        if not node_features.is_cuda or graph is None or graph.num_edges != distances.shape[0]:
+            return None
+        if torch.is_grad_enabled() and (P.requires_grad or Q.requires_grad):
+            return None
+        cout = self.channels_out
+        if (num_heads < 1 or num_heads > N.POOL_MAX_HEADS or cout % num_heads
+                or (cout // num_heads) % 4 or attn.shape != (graph.num_edges, num_heads)
+                or graph.num_nodes < 1):
+            return None
+        rw = self.radial_weights
+        layout, binning = self.layout(), self.binning()
+        x, Pp, Qp, C, F, emb = node_features, P, Q, rw.channel_patterns, rw.radial_functions(), None
+        if not edgewise_pool_supported(layout, binning, rw.rank):
+            emb = self._embedding(node_features, distances.shape[0], layout, binning)
+            if emb is None or emb.layout.cout != cout or not edgewise_pool_supported(emb.layout, binning,
+                                                                                    rw.rank):
+                return None
+            x, Pp, Qp = emb.features(node_features), emb.basis_in(P), emb.basis_out(Q)
+            C, F, layout = emb.channels(C), emb.radial(F), emb.layout
+        perm_s, offsets_s = graph.csr_src()
+        perm_d, offsets_d = graph.csr()
+        out = edgewise_attention_pool(x.contiguous(), attn, graph.src, graph.dst, perm_s, offsets_s,
+                                      perm_d, offsets_d, graph.num_nodes, Pp, Qp, distances, C, F,
+                                      layout, binning, rw.rank, num_heads, cout // num_heads,
+                                      half_precision_active(node_features))
+        return out if emb is None else emb.output(out)
 
     def extra_repr(self) -> str:
         rw = self.radial_weights

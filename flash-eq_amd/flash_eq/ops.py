@@ -187,6 +187,111 @@ def edgewise_linear_src(x, src, perm, offsets, P, Q, dist, C, F, layout, binning
                                      half_accuracy)
 
 
+def edgewise_pool_supported(layout: N.FeqLayout, binning: N.FeqBinning, rank: int) -> bool:
+    """Whether ``feq_edgewise_fwd_src_pool``/``_bwd_src_pool`` have kernels for this layout."""
+    return bool(N.lib().feq_edgewise_pool_supported(N.ctypes.byref(layout), N.ctypes.byref(binning), rank))
+
+
+class EdgewiseAttnPoolFn(torch.autograd.Function):
+    """The V projection of ``EquivariantAttention`` (the layer over x[src])
+    fused with the attention's head weighting and sum pooling by destination
+    (``attention.py:307-314``, ``pooling.py:21-30``):
+    out[n, c, :] = sum over the edges e into n of attn[e, c // chan_per_head] * V[e, c, :]
+    (``feq_edgewise_fwd_src_pool``).  Neither attn * V nor its gradient is ever
+    formed; V itself is kept, in destination order, only when the attention
+    weights need a gradient (``feq_attn_pool_grad_attn``).  The backward reads
+    attn * grad_out[dst] inside the layer's backward kernels
+    (``feq_edgewise_bwd_src_pool``), the input gradient summed per source node."""
+
+    @staticmethod
+    def forward(ctx, x, attn, src, dst, perm_s, offsets_s, perm_d, offsets_d, num_dst: int, P, Q, dist,
+                C, F, layout: N.FeqLayout, binning: N.FeqBinning, rank: int, heads: int,
+                chan_per_head: int, half_accuracy: bool = False):
+        dev = _same_device(x, attn, src, dst, perm_s, offsets_s, perm_d, offsets_d, P, Q, dist, C, F)
+        E = src.shape[0]
+        xs, As, Ps, Qs = _f32(x, "node_features"), _f32(attn, "attention"), _f32(P, "P"), _f32(Q, "Q")
+        rs, Cs, Fs = _f32(dist, "distances"), _f32(C, "channel_patterns"), _f32(F, "radial")
+        if xs.dim() != 3 or xs.shape[1:] != (layout.cin, layout.din):
+            raise ValueError(f"node_features must be (N, {layout.cin}, {layout.din}), got {tuple(xs.shape)}")
+        if As.shape != (E, heads):
+            raise ValueError(f"attention must be ({E}, {heads}), got {tuple(As.shape)}")
+        if dst.shape != (E,) or perm_d.shape != (E,) or offsets_d.shape != (num_dst + 1,):
+            raise ValueError(f"the CSR by destination must cover {E} edges and {num_dst} nodes")
+        if perm_s.shape != (E,) or offsets_s.shape != (xs.shape[0] + 1,):
+            raise ValueError(f"the CSR by source must cover {E} edges and {xs.shape[0]} nodes")
+        _check_edgewise_shapes(layout, binning, rank, torch.empty(E, layout.cin, layout.din, device="meta"),
+                               Ps, Qs, rs, Cs, Fs)
+        si = src.to(torch.int64).contiguous()
+        di = dst.to(torch.int64).contiguous()
+        flags = N.FEQ_EW_HALF_ACCURACY if half_accuracy else 0
+        out = torch.empty(num_dst, layout.cout, layout.dout, dtype=torch.float32, device=dev)
+        keep = ctx.needs_input_grad[1] and E > 0
+        y_pos = torch.empty(E, layout.cout, layout.dout, dtype=torch.float32, device=dev) if keep else None
+        lib = N.lib()
+        ws = N.workspace(lib.feq_edgewise_fwd_src_pool_workspace(N.ctypes.byref(layout),
+                                                                 N.ctypes.byref(binning), rank, E), dev)
+        with torch.cuda.device(dev):
+            rc = lib.feq_edgewise_fwd_src_pool(
+                N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E, N.ptr(xs), xs.shape[0],
+                N.ptr(si), N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs), N.ptr(Fs), N.ptr(As), heads,
+                chan_per_head, N.ptr(di), N.ptr(perm_d) if E else None, N.ptr(offsets_d), num_dst,
+                N.ptr(out) if num_dst else None, N.ptr(y_pos), flags, N.ptr(ws), ws.numel(),
+                N.stream_ptr(dev))
+        N.check(rc, "feq_edgewise_fwd_src_pool")
+        ctx.save_for_backward(xs, As, si, di, perm_s, offsets_s, perm_d, offsets_d, Ps, Qs, rs, Cs, Fs,
+                              y_pos)
+        ctx.meta = (layout, binning, rank, heads, chan_per_head, num_dst, flags,
+                    x.dtype, attn.dtype, dist.dtype, C.dtype, F.dtype)
+        return out.to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, gout):
+        xs, As, si, di, perm_s, offsets_s, perm_d, offsets_d, Ps, Qs, rs, Cs, Fs, y_pos = ctx.saved_tensors
+        layout, binning, rank, heads, cph, num_dst, flags, xdt, adt, rdt, cdt, fdt = ctx.meta
+        dev = xs.device
+        E = si.shape[0]
+        need = ctx.needs_input_grad
+        g = gout.detach().to(torch.float32).contiguous()
+        lib = N.lib()
+        gA = None
+        if need[1]:
+            gA = torch.empty_like(As)
+            if E:
+                with torch.cuda.device(dev):
+                    rc = lib.feq_attn_pool_grad_attn(N.ptr(y_pos), N.ptr(g), N.ptr(perm_d), N.ptr(offsets_d),
+                                                     E, num_dst, layout.cout, layout.dout, heads, N.ptr(gA),
+                                                     N.stream_ptr(dev))
+                N.check(rc, "feq_attn_pool_grad_attn")
+        gx = torch.empty_like(xs)
+        gr = torch.empty_like(rs) if need[11] else None
+        gC = torch.empty_like(Cs)
+        gF = torch.empty_like(Fs)
+        ws = N.workspace(lib.feq_edgewise_bwd_src_nodes_workspace(
+            N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E), dev)
+        with torch.cuda.device(dev):
+            rc = lib.feq_edgewise_bwd_src_pool(
+                N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E, N.ptr(g) if num_dst else None,
+                N.ptr(As), heads, cph, N.ptr(di), num_dst, N.ptr(xs), xs.shape[0], N.ptr(si),
+                N.ptr(perm_s) if E else None, N.ptr(offsets_s), N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs),
+                N.ptr(Fs), N.ptr(gx), N.ptr(gC), N.ptr(gF), N.ptr(gr), flags, N.ptr(ws), ws.numel(),
+                N.stream_ptr(dev))
+        N.check(rc, "feq_edgewise_bwd_src_pool")
+        return (gx.to(xdt) if need[0] else None, None if gA is None else gA.to(adt),
+                None, None, None, None, None, None, None, None, None,
+                None if gr is None else gr.to(rdt), gC.to(cdt) if need[12] else None,
+                gF.to(fdt) if need[13] else None, None, None, None, None, None, None)
+
+
+def edgewise_attention_pool(x, attn, src, dst, perm_s, offsets_s, perm_d, offsets_d, num_dst, P, Q,
+                            dist, C, F, layout, binning, rank, heads: int, chan_per_head: int,
+                            half_accuracy: bool = False) -> torch.Tensor:
+    if torch.is_grad_enabled() and (P.requires_grad or Q.requires_grad):
+        raise ValueError("the pooled message-passing form does not form gradients for P and Q")
+    return EdgewiseAttnPoolFn.apply(x, attn, src, dst, perm_s, offsets_s, perm_d, offsets_d, num_dst, P,
+                                    Q, dist, C, F, layout, binning, rank, heads, chan_per_head,
+                                    half_accuracy)
+
+
 # ---------------------------------------------------------------------------
 # embedding of small canonical layouts into the config-2 shape
 # ---------------------------------------------------------------------------

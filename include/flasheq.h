@@ -243,6 +243,49 @@ int feq_edgewise_bwd_src_nodes_ex(const feq_layout* L, const feq_binning* b, int
                                   float* grad_dist, int32_t flags, void* workspace, size_t ws_bytes,
                                   feq_stream_t stream);
 
+/* The V projection of EquivariantAttention fused with the attention's head
+ * weighting and sum pooling.  The reference makes three passes over (E, Cout,
+ * Dout) tensors: the layer over x[src] (attention.py:307-310), attn * V
+ * (attention.py:311-313) and the scatter-sum to dst (pooling.py:21-30).  Here
+ * out (num_dst, Cout, Dout)[n, c, :] = sum over the edges e into n of
+ * attn[e, h(c)] y_e[c, :], y_e the layer's output for edge e (as
+ * feq_edgewise_fwd_src_ex, flags alike), attn (E, heads) float32,
+ * h(c) = min(c / chan_per_head, heads - 1); heads <= 16, chan_per_head a
+ * multiple of 4.  The kernel walks the edges in the order of the CSR by
+ * destination (perm_dst, offsets_dst over num_dst nodes: feq_csr_by_dst with
+ * dst as the key) and sums each node's rows in that order (nodes crossing a
+ * 16-edge tile boundary through partial rows summed in tile order), so the
+ * result is deterministic; every node row is written; edges whose dst lies
+ * outside [0, num_dst) add nothing.  The rows y_e are not formed unless y_pos
+ * is given: y_pos (E, Cout, Dout) then receives them in CSR position order
+ * (row p holds edge perm_dst[p]), the form feq_attn_pool_grad_attn reads.
+ * Layouts: feq_edgewise_pool_supported.  Workspace:
+ * feq_edgewise_fwd_src_pool_workspace bytes. */
+int feq_edgewise_pool_supported(const feq_layout* L, const feq_binning* b, int32_t rank);
+size_t feq_edgewise_fwd_src_pool_workspace(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                           int64_t num_edges);
+int feq_edgewise_fwd_src_pool(const feq_layout* L, const feq_binning* b, int32_t rank,
+                              int64_t num_edges, const float* x, int64_t num_src, const int64_t* src,
+                              const float* P, const float* Q, const float* dist, const float* C,
+                              const float* F, const float* attn, int32_t heads,
+                              int32_t chan_per_head, const int64_t* dst, const int32_t* perm_dst,
+                              const int32_t* offsets_dst, int64_t num_dst, float* out, float* y_pos,
+                              int32_t flags, void* workspace, size_t ws_bytes, feq_stream_t stream);
+/* Its backward: feq_edgewise_bwd_src_nodes_ex with the per-edge gradient
+ * grad_y[e, c, :] = attn[e, h(c)] grad_out[dst[e], c, :] read inside the
+ * kernels (never formed); grad_out (num_dst, Cout, Dout).  Edges whose dst lies
+ * outside [0, num_dst) get zero gradients.  The attention weights' gradient is
+ * feq_attn_pool_grad_attn's.  Workspace: feq_edgewise_bwd_src_nodes_workspace
+ * bytes. */
+int feq_edgewise_bwd_src_pool(const feq_layout* L, const feq_binning* b, int32_t rank,
+                              int64_t num_edges, const float* grad_out, const float* attn,
+                              int32_t heads, int32_t chan_per_head, const int64_t* dst,
+                              int64_t num_dst, const float* x, int64_t num_src, const int64_t* src,
+                              const int32_t* perm_src, const int32_t* offsets_src, const float* P,
+                              const float* Q, const float* dist, const float* C, const float* F,
+                              float* grad_x_nodes, float* grad_C, float* grad_F, float* grad_dist,
+                              int32_t flags, void* workspace, size_t ws_bytes, feq_stream_t stream);
+
 /* ---- Wigner-D basis ------------------------------------------------------------
  * plan: host-built per-representation constants (see feq_wigner_plan_size);
  * out (E, dim, dim): column j = column perm[j] of D(g), g e_z = dir/|dir|. */
@@ -358,6 +401,15 @@ int feq_attn_pool_bwd(const float* V, const float* attn, const float* grad_out,
                       const int32_t* perm, const int32_t* offsets, int64_t num_edges,
                       int64_t num_nodes, int32_t mult, int32_t dim, int32_t heads,
                       float* grad_V, float* grad_attn, feq_stream_t stream);
+/* grad_attn[e, h] = sum_{c in h, d} V_pos[p, c, d] grad_out[n, c, d] for the edge
+ * e = perm[p] at position p of node n's CSR segment (perm, offsets: the CSR by
+ * destination); V_pos holds the per-edge rows in position order, as
+ * feq_edgewise_fwd_src_pool keeps them (the attention-weight half of
+ * feq_attn_pool_bwd; grad_V is not formed).  Edges outside the nodes get 0. */
+int feq_attn_pool_grad_attn(const float* V_pos, const float* grad_out, const int32_t* perm,
+                            const int32_t* offsets, int64_t num_edges, int64_t num_nodes,
+                            int32_t mult, int32_t dim, int32_t heads, float* grad_attn,
+                            feq_stream_t stream);
 
 /* ---- node-side neighbours of the path (transformer block norms, gating) ----
  * Node tables x, y, gy, gx are (N, mult, dim) float32, contiguous; the layout is

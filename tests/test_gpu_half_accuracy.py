@@ -113,15 +113,16 @@ def test_flags_zero_is_the_full_path_and_unknown_flags_fail(dev):
 
 def test_bfloat16_block_selects_half_accuracy(dev, monkeypatch):
     """Inside a bfloat16 transformer block (computed in float32) the edgewise
-    layer asks for the single-product kernels."""
+    layer asks for the single-product kernels (its V projection takes the form
+    fused with the attention pooling; half_accuracy is the last argument of
+    both message-passing functions)."""
     seen = []
-    real = ops.EdgewiseLinearSrcFn.apply
+    for fn in (ops.EdgewiseLinearSrcFn, ops.EdgewiseAttnPoolFn):
+        def spy(*a, _real=fn.apply):
+            seen.append(a[-1])
+            return _real(*a)
 
-    def spy(*a):
-        seen.append(a[-1])
-        return real(*a)
-
-    monkeypatch.setattr(ops.EdgewiseLinearSrcFn, "apply", spy)
+        monkeypatch.setattr(fn, "apply", spy)
     torch.manual_seed(0)
     rep = fe.Repr([0, 1, 2], 64)
     block = fe.EquivariantTransformerBlock(rep, rep, num_heads=8).to(dev)
