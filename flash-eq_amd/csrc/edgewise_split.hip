@@ -195,6 +195,19 @@ __device__ __forceinline__ void load_rows(const float* __restrict__ src, int64_t
     }
 }
 
+// load_rows for a row index already known (row r, ok = the position is in range).
+template <int N>
+__device__ __forceinline__ void load_row_at(const float* __restrict__ src, int64_t r, bool ok,
+                                            float (&v)[rows_per_thread<N>()]) {
+    const int c = threadIdx.x & 15;
+    const float* row = src + (ok ? r : 0) * N;
+#pragma unroll
+    for (int k = 0; k < rows_per_thread<N>(); ++k) {
+        const int idx = c + 16 * k;
+        v[k] = (ok && idx < N) ? row[idx] : 0.0f;
+    }
+}
+
 // Stores rows read by load_rows into LDS with a row stride of S floats.
 template <int N, int S>
 __device__ __forceinline__ void store_rows(const float (&v)[rows_per_thread<N>()], float* dst) {
@@ -245,7 +258,12 @@ __device__ __forceinline__ void flush_stage(const float* stage, float* __restric
 
 // The staged tile's rows (nval edges, source nodes node[j], -1 for none) summed
 // per node in tile order: a node within the tile gets its row, a node that
-// crosses a tile boundary a partial row (NodeScatter).
+// crosses a tile boundary a partial row (NodeScatter).  node[kNE] and
+// node[kNE + 1] are the nodes of the positions just before and just after the
+// tile (-1 for none): a run crosses a boundary when it starts the tile and
+// continues the previous position's node, or ends the tile and the next
+// position continues it (the CSR offsets give the same answer, at the price of
+// dependent global loads in the epilogue).
 template <int CH, int D>
 __device__ __forceinline__ void scatter_stage(const float* stage, const int* node, const NodeScatter& NS,
                                               int64_t tile, int nval) {
@@ -266,7 +284,7 @@ __device__ __forceinline__ void scatter_stage(const float* stage, const int* nod
             const int n = node[j];
             if (j + 1 < nval && node[j + 1] == n) continue;
             if (n >= 0) {
-                if (node_crosses_tiles(NS.offsets[n], NS.offsets[n + 1]))
+                if ((js == 0 && n == node[kNE]) || (j + 1 == kNE && n == node[kNE + 1]))
                     part4[(2 * tile + (js == 0 ? 0 : 1)) * ROW4 + q] = acc;
                 else
                     out4[static_cast<int64_t>(n) * ROW4 + q] = acc;
@@ -304,7 +322,7 @@ __device__ __forceinline__ void scatter_stage_w(const float* stage, const int* n
             const int n = node[j];
             if (j + 1 < nval && node[j + 1] == n) continue;
             if (n >= 0) {
-                if (node_crosses_tiles(DP.offsets[n], DP.offsets[n + 1]))
+                if ((js == 0 && n == node[kNE]) || (j + 1 == kNE && n == node[kNE + 1]))
                     part4[(2 * tile + (js == 0 ? 0 : 1)) * ROW4 + q] = acc;
                 else
                     out4[static_cast<int64_t>(n) * ROW4 + q] = acc;
@@ -553,12 +571,8 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
     float* sSp = sSout + kNE;                                    // s_e^l, l < NSP
     float* sInvK = sSp + kNE * NSP;
     EdgeState* sE = reinterpret_cast<EdgeState*>(sInvK + K);
-    int* sNode = reinterpret_cast<int*>(sE + kNE);               // destination per position (POOL)
-    float* sW = reinterpret_cast<float*>(sNode + kNE);           // [kNE][kPoolMaxHeads] weights (POOL)
-    // tile position -> edge: the identity, or the CSR-by-destination permutation
-    auto edge = [&](int64_t j) -> int64_t {
-        if constexpr (POOL) return DP.perm[j]; else return j;
-    };
+    int* sNode = reinterpret_cast<int*>(sE + kNE);               // destination per position, + 2 neighbours (POOL)
+    float* sW = reinterpret_cast<float*>(sNode + kNE + 4);       // [kNE][kPoolMaxHeads] weights (POOL)
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
@@ -572,18 +586,41 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
     float xr[NPR][4 * DIN];
     float pr[rows_per_thread<DIN * DIN>()], qr[rows_per_thread<DOUT * DOUT>()];
     float rd;
-    int nd = -1;       // POOL: destination of position tid (tid < kNE)
+    int nd = -1;       // POOL: destination of position tid (tid < kNE; kNE, kNE + 1: the neighbours)
     float wt = 0.0f;   // POOL: weight (position tid / kPoolMaxHeads, head tid % kPoolMaxHeads)
     static_assert(kNE * kPoolMaxHeads <= kThreads, "one weight per thread");
     auto load_tile = [&](int64_t t) {
         const int64_t f0 = t * kNE;
+        // Every index first (the source rows, the CSR permutation for the P, Q
+        // and attention rows, the positions' destinations and distances): the
+        // in-order memory counter then waits once for all of them before the
+        // rows they point to are requested.  Without POOL the P and Q rows are
+        // the tile's own and only the source rows are indexed.
+        int64_t xrow[NPR];
 #pragma unroll
         for (int p = 0; p < NPR; ++p) {
             const int q = tid + kThreads * p;
-            const int e = q / NC4, c4 = q % NC4;
-            const int64_t row = q < kNE * NC4 && f0 + e < E ? x_row<GATHER>(X, edge(f0 + e)) : -1;
-            if (row >= 0) {
-                const float4* src = reinterpret_cast<const float4*>(X.x + (row * CIN + 4 * c4) * DIN);
+            const int e = q / NC4;
+            xrow[p] = q < kNE * NC4 && f0 + e < E ? x_row<GATHER>(X, f0 + e) : -1;
+        }
+        const int rj = tid >> 4;                     // the P / Q / attention row of this thread
+        const bool rok = f0 + rj < E;
+        int64_t re = f0 + rj;
+        if constexpr (POOL) {
+            re = rok ? DP.perm[f0 + rj] : 0;
+            // positions f0 .. f0 + kNE - 1, then f0 - 1 and f0 + kNE (the neighbours)
+            const int64_t pn = tid < kNE ? f0 + tid : tid == kNE ? f0 - 1 : f0 + kNE;
+            nd = (tid < kNE + 2 && pn >= 0 && pn < E) ? DP.node_pos[pn] : -1;
+            rd = (tid < kNE && f0 + tid < E) ? DP.dist_pos[f0 + tid] : 1.0f;
+        } else {
+            rd = (tid < kNE && f0 + tid < E) ? dist[f0 + tid] : 1.0f;
+        }
+#pragma unroll
+        for (int p = 0; p < NPR; ++p) {
+            const int q = tid + kThreads * p;
+            const int c4 = q % NC4;
+            if (xrow[p] >= 0) {
+                const float4* src = reinterpret_cast<const float4*>(X.x + (xrow[p] * CIN + 4 * c4) * DIN);
 #pragma unroll
                 for (int v = 0; v < DIN; ++v) {
                     const float4 f = src[v];
@@ -597,14 +634,12 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
                 for (int v = 0; v < 4 * DIN; ++v) xr[p][v] = 0.0f;
             }
         }
-        load_rows<DIN * DIN, POOL>(P, f0, E, DP.perm, pr);
-        load_rows<DOUT * DOUT, POOL>(Q, f0, E, DP.perm, qr);
-        rd = (tid < kNE && f0 + tid < E) ? dist[edge(f0 + tid)] : 1.0f;
+        load_row_at<DIN * DIN>(P, re, rok, pr);
+        load_row_at<DOUT * DOUT>(Q, re, rok, qr);
         if constexpr (POOL) {
-            nd = (tid < kNE && f0 + tid < E) ? static_cast<int>(pool_node(DP, edge(f0 + tid))) : -1;
-            const int wj = tid / kPoolMaxHeads, wh = tid % kPoolMaxHeads;
-            wt = (wj < kNE && f0 + wj < E && wh < DP.heads)
-                     ? DP.attn[edge(f0 + wj) * DP.heads + wh] : 0.0f;
+            const int wh = tid % kPoolMaxHeads;       // weight (position rj, head wh)
+            static_assert(kPoolMaxHeads == 16, "the weight row of a thread is its P / Q row");
+            wt = (rok && wh < DP.heads) ? DP.attn[re * DP.heads + wh] : 0.0f;
         }
     };
 
@@ -669,9 +704,11 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
             es.s = rd / (rd + B.sh_scale);
             sE[tid] = es;
             edge_powers(es.s, NSP, sSp + tid * NSP);
-            if constexpr (POOL) sNode[tid] = nd;
         }
-        if constexpr (POOL) sW[tid] = wt;
+        if constexpr (POOL) {
+            if (tid < kNE + 2) sNode[tid] = nd;
+            sW[tid] = wt;
+        }
         const bool dense =
             __syncthreads_or(off_block_nonzero_rows(pr, pbits) | off_block_nonzero_rows(qr, qbits)) != 0;
 
@@ -840,7 +877,7 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             const float* __restrict__ F, float* __restrict__ gx, float* __restrict__ dFe,
             NodeScatter NS, DstPool DP) {
     static_assert(GATHER || !SCATTER, "the per-node sums need the message-passing form");
-    static_assert(GATHER || !GP, "the pooled form is a message-passing form");
+    static_assert(SCATTER || !GP, "the pooled form sums the input gradient per source node");
     using T = Canon<LIN, LOUT>;
     using TG = TermGroups<LIN, LOUT, true>;
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
@@ -870,11 +907,8 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     float* sEinv = sSp + kNE * NSP;                               // 1 / scale_e
     float* sInvK = sEinv + kNE;
     EdgeState* sE = reinterpret_cast<EdgeState*>(sInvK + K);
-    int* sNode = reinterpret_cast<int*>(sE + kNE);                // source node per position (SCATTER)
-    // tile position -> edge: the identity, or the CSR-by-source permutation
-    auto edge = [&](int64_t j) -> int64_t {
-        if constexpr (SCATTER) return NS.perm[j]; else return j;
-    };
+    int* sNode = reinterpret_cast<int*>(sE + kNE);                // source node per position, + 2 neighbours (SCATTER)
+    int* sEid = sNode + kNE + 4;                                  // edge per position (SCATTER)
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
@@ -891,26 +925,57 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     // P and Q of the prefetched tile: each thread's share of one edge row
     float prs[rows_per_thread<DIN * DIN>()], qrs[rows_per_thread<DOUT * DOUT>()];
     float rd;
-    int nd = -1;
+    int nd = -1, eid = 0;   // SCATTER: source node of position tid (and neighbours), edge of position tid
     auto load_tile = [&](int64_t t) {
         const int64_t f0 = t * kNE;
+        // Every index first (position-ordered arrays with SCATTER, see the
+        // forward), then the rows they point to.
+        int64_t grow[NPR];   // row of gy each producer reads (-1: none)
+        int64_t gedge[NPR];  // GP: the producer's edge (its attention weights)
 #pragma unroll
         for (int p = 0; p < NPR; ++p) {
             const int q = tid + kThreads * p;
-            const int e = q / NC4, c4 = q % NC4;
-            int64_t grow = -1;   // row of gy this producer reads
-            gw[p] = 1.0f;
-            if (q < kNE * NC4 && f0 + e < E) {
-                const int64_t ee = edge(f0 + e);
-                if constexpr (GP) {
-                    grow = pool_node(DP, ee);
-                    gw[p] = grow >= 0 ? DP.attn[ee * DP.heads + pool_head(DP, 4 * c4)] : 0.0f;
-                } else {
-                    grow = ee;
-                }
+            const int e = q / NC4;
+            const bool valid = q < kNE * NC4 && f0 + e < E;
+            gedge[p] = 0;
+            if constexpr (GP) {
+                grow[p] = valid ? NS.dnode_pos[f0 + e] : -1;
+                gedge[p] = valid ? NS.perm[f0 + e] : 0;
+            } else if constexpr (SCATTER) {
+                grow[p] = valid ? NS.perm[f0 + e] : -1;
+            } else {
+                grow[p] = valid ? f0 + e : -1;
             }
-            if (grow >= 0) {
-                const float4* src = reinterpret_cast<const float4*>(gy + (grow * COUT + 4 * c4) * DOUT);
+        }
+        int64_t xrow[RPW];
+#pragma unroll
+        for (int j = 0; j < RPW; ++j) {
+            if constexpr (SCATTER)
+                xrow[j] = f0 + le < E ? NS.src_pos[f0 + le] : -1;
+            else
+                xrow[j] = f0 + le < E ? x_row<GATHER>(X, f0 + le) : -1;
+        }
+        const int rj = tid >> 4;                     // the P / Q row of this thread
+        const bool rok = f0 + rj < E;
+        int64_t re = f0 + rj;
+        if constexpr (SCATTER) {
+            re = rok ? NS.perm[f0 + rj] : 0;
+            // positions f0 .. f0 + kNE - 1, then f0 - 1 and f0 + kNE (the neighbours)
+            const int64_t pn = tid < kNE ? f0 + tid : tid == kNE ? f0 - 1 : f0 + kNE;
+            nd = (tid < kNE + 2 && pn >= 0 && pn < E) ? NS.src_pos[pn] : -1;
+            eid = (tid < kNE && f0 + tid < E) ? NS.perm[f0 + tid] : 0;
+            rd = (tid < kNE && f0 + tid < E) ? NS.dist_pos[f0 + tid] : 1.0f;
+        } else {
+            rd = (tid < kNE && f0 + tid < E) ? dist[f0 + tid] : 1.0f;
+        }
+#pragma unroll
+        for (int p = 0; p < NPR; ++p) {
+            const int q = tid + kThreads * p;
+            const int c4 = q % NC4;
+            gw[p] = 1.0f;
+            if constexpr (GP) gw[p] = grow[p] >= 0 ? DP.attn[gedge[p] * DP.heads + pool_head(DP, 4 * c4)] : 0.0f;
+            if (grow[p] >= 0) {
+                const float4* src = reinterpret_cast<const float4*>(gy + (grow[p] * COUT + 4 * c4) * DOUT);
 #pragma unroll
                 for (int v = 0; v < DOUT; ++v) {
                     const float4 f = src[v];
@@ -926,10 +991,9 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
         }
 #pragma unroll
         for (int j = 0; j < RPW; ++j) {
-            const int64_t row = f0 + le < E ? x_row<GATHER>(X, edge(f0 + le)) : -1;
-            if (row >= 0) {
+            if (xrow[j] >= 0) {
                 const float4* src = reinterpret_cast<const float4*>(
-                    X.x + (row * CIN + 16 * (wave + 4 * j) + 4 * lg) * DIN);
+                    X.x + (xrow[j] * CIN + 16 * (wave + 4 * j) + 4 * lg) * DIN);
 #pragma unroll
                 for (int v = 0; v < DIN; ++v) {
                     const float4 f = src[v];
@@ -943,11 +1007,8 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
                 for (int v = 0; v < 4 * DIN; ++v) xl[j][v] = 0.0f;
             }
         }
-        load_rows<DIN * DIN, SCATTER>(P, f0, E, NS.perm, prs);
-        load_rows<DOUT * DOUT, SCATTER>(Q, f0, E, NS.perm, qrs);
-        if constexpr (SCATTER)
-            nd = (tid < kNE && f0 + tid < E) ? static_cast<int>(x_row<GATHER>(X, edge(f0 + tid))) : -1;
-        rd = (tid < kNE && f0 + tid < E) ? dist[edge(f0 + tid)] : 1.0f;
+        load_row_at<DIN * DIN>(P, re, rok, prs);
+        load_row_at<DOUT * DOUT>(Q, re, rok, qrs);
     };
 
     // gd fragments (producer threads) and fs in the lane layout
@@ -1019,7 +1080,10 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             es.s = rd / (rd + B.sh_scale);
             sE[tid] = es;
             edge_powers(es.s, NSP, sSp + tid * NSP);
-            if constexpr (SCATTER) sNode[tid] = nd;
+        }
+        if constexpr (SCATTER) {
+            if (tid < kNE + 2) sNode[tid] = nd;
+            if (tid < kNE) sEid[tid] = eid;
         }
         const bool dense =
             __syncthreads_or(off_block_nonzero_rows(prs, pbits) | off_block_nonzero_rows(qrs, qbits)) != 0;
@@ -1195,7 +1259,8 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
                 float a = sDF[q];
 #pragma unroll
                 for (int v = 1; v < 4; ++v) a += sDF[v * kNE * KW + q];
-                dFe[edge(e0 + e) * KW + fkw] = a * sSp[e * NSP + fl];
+                const int64_t ed = SCATTER ? static_cast<int64_t>(sEid[e]) : e0 + e;
+                dFe[ed * KW + fkw] = a * sSp[e * NSP + fl];
             }
         }
         __syncthreads();
@@ -1269,25 +1334,27 @@ k_ews_bwd_c(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
         // global loads: four edges' rows of one input channel / one output channel.
         // Unconditional: edges past the last (and channels past Cin / Cout) read
         // the last one's rows; their radial functions are zero, so their U_k rows
-        // are zero and they add nothing to dC.
+        // are zero and they add nothing to dC.  The row indices (sources; with
+        // GP, destinations) are all requested before the rows they point to.
         float xr[4][DIN], gr[4][DOUT], gw[4];
         const int pci = pc < CIN ? pc : CIN - 1, pco = pc < COUT ? pc : COUT - 1;
+        int64_t xi[4], gi[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int64_t e = e0 + 4 * pq + q < E ? e0 + 4 * pq + q : E - 1;
+            xi[q] = x_row<GATHER>(X, e);
+            if constexpr (GP) gi[q] = pool_node(DP, e); else gi[q] = e;
+        }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int64_t e = e0 + 4 * pq + q < E ? e0 + 4 * pq + q : E - 1;
             // an index outside the node table (message-passing form) reads row 0;
             // the edge is then marked invalid, so it adds nothing either
-            const int64_t row = x_row<GATHER>(X, e);
-            const float* xs = X.x + ((row >= 0 ? row : 0) * CIN + pci) * DIN;
-            int64_t grow = e;
+            const float* xs = X.x + ((xi[q] >= 0 ? xi[q] : 0) * CIN + pci) * DIN;
             gw[q] = 1.0f;
-            if constexpr (GP) {
-                // pooled form: a destination outside [0, ndst) reads row 0 with weight 0
-                grow = pool_node(DP, e);
-                gw[q] = grow >= 0 ? DP.attn[e * DP.heads + pool_head(DP, pco)] : 0.0f;
-                grow = grow >= 0 ? grow : 0;
-            }
-            const float* gs = gy + (grow * COUT + pco) * DOUT;
+            // pooled form: a destination outside [0, ndst) reads row 0 with weight 0
+            if constexpr (GP) gw[q] = gi[q] >= 0 ? DP.attn[e * DP.heads + pool_head(DP, pco)] : 0.0f;
+            const float* gs = gy + ((gi[q] >= 0 ? gi[q] : 0) * COUT + pco) * DOUT;
 #pragma unroll
             for (int d = 0; d < DIN; ++d) xr[q][d] = xs[d];
 #pragma unroll
@@ -1506,7 +1573,7 @@ constexpr size_t ews_bwd_x_lds() {
     constexpr size_t FR = 2 * T::DOUT * (COUT / 32) * 1024, ST = 4 * kNE * stage_stride(CIN * T::DIN);
     return (FR > ST ? FR : ST) +
            4 * (kNE * PS + kNE * QS + kNE * KWS + 4 * kNE * KW + kNE * (LIN + LOUT + 1) + kNE + K) +
-           kNE * sizeof(EdgeState) + kNE * sizeof(int);
+           kNE * sizeof(EdgeState) + (2 * kNE + 4) * sizeof(int);
 }
 
 template <int CIN, int COUT, int LIN, int LOUT, int K>
@@ -1516,7 +1583,7 @@ constexpr size_t ews_fwd_lds() {
     constexpr size_t FR = 2 * T::DIN * (CIN / 32) * 1024, ST = 4 * kNE * stage_stride(COUT * T::DOUT);
     return (FR > ST ? FR : ST) +
            4 * (kNE * PS + kNE * QS + kNE * KWS + kNE + kNE * (LIN + LOUT + 1) + K) +
-           kNE * sizeof(EdgeState) + kNE * sizeof(int) + 4 * kNE * kPoolMaxHeads;
+           kNE * sizeof(EdgeState) + (kNE + 4) * sizeof(int) + 4 * kNE * kPoolMaxHeads;
 }
 
 // Workgroups per CU of the forward.  Two, measured on MI355X at 160k edges
@@ -1553,12 +1620,29 @@ constexpr size_t ews_cfrag_bytes() {
     return align_up(static_cast<size_t>(K) * COUT * CIN * 2 * sizeof(_Float16), 256) + 256;
 }
 
-// Workspace of the pooled forward: the C fragments, then two partial rows per tile.
+// Workspace of the pooled forward: the C fragments, two partial rows per tile,
+// the sources and destinations in CSR position order.
 template <int CIN, int COUT, int LIN, int LOUT, int K>
 size_t ews_pool_fwd_ws(int64_t E) {
     using T = Canon<LIN, LOUT>;
     return ews_cfrag_bytes<CIN, COUT, K>() +
-           align_up(4 * static_cast<size_t>(ceil_div(E, kNE)) * 2 * COUT * T::DOUT, 256) + 256;
+           align_up(4 * static_cast<size_t>(ceil_div(E, kNE)) * 2 * COUT * T::DOUT, 256) +
+           align_up(8 * static_cast<size_t>(E), 256) + 2 * align_up(4 * static_cast<size_t>(E), 256) + 512;
+}
+
+// Source, destination and distance of every CSR position p (edge perm[p]) of
+// the pooled forward, so that its tile loads index them directly.
+__global__ void k_pool_order(int64_t E, const int32_t* __restrict__ perm, const int64_t* __restrict__ src,
+                             const int64_t* __restrict__ dst, const float* __restrict__ dist, int64_t ndst,
+                             int64_t* __restrict__ src_pos, int32_t* __restrict__ node_pos,
+                             float* __restrict__ dist_pos) {
+    const int64_t p = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (p >= E) return;
+    const int64_t e = perm[p];
+    src_pos[p] = src[e];
+    dist_pos[p] = dist[e];
+    const int64_t n = dst[e];
+    node_pos[p] = n >= 0 && n < ndst ? static_cast<int32_t>(n) : -1;
 }
 
 // lp: one fp16 product per operand pair (message-passing form only).
@@ -1578,9 +1662,20 @@ int launch_ews_fwd(const feq_binning& B, int64_t E, XRows x, const float* P, con
     h8* frag = cv.take<h8>(static_cast<size_t>(K) * COUT * CIN / 4);
     float* inv = cv.take<float>(K);
     DstPool DP{};
+    XRows X = x;
     if (dp) {
         DP = *dp;
         DP.part = cv.take<float>(static_cast<size_t>(ntiles) * 2 * COUT * T::DOUT);
+        int64_t* src_pos = cv.take<int64_t>(E);
+        int32_t* node_pos = cv.take<int32_t>(E);
+        float* dist_pos = cv.take<float>(E);
+        FEQ_LAUNCH("k_pool_order", k_pool_order, dim3(static_cast<unsigned>(ceil_div(E, kThreads))),
+                   dim3(kThreads), 0, s, E, DP.perm, x.src, DP.dst, dist, DP.ndst, src_pos, node_pos,
+                   dist_pos);
+        DP.src_pos = src_pos;
+        DP.node_pos = node_pos;
+        DP.dist_pos = dist_pos;
+        X.src = src_pos;
     }
     auto prep = k_ews_prep<K, COUT, CIN, false>;
     FEQ_LAUNCH("k_ews_prep", prep, dim3(K * COUT / 16), dim3(kThreads), 0, s, C, frag, inv);
@@ -1597,7 +1692,7 @@ int launch_ews_fwd(const feq_binning& B, int64_t E, XRows x, const float* P, con
     if (int rc = ews_set_lds(reinterpret_cast<const void*>(kern), lds)) return rc;
     const int64_t g = static_cast<int64_t>(ews_cus()) * occ;
     const int grid = static_cast<int>(ntiles < g ? ntiles : g);
-    FEQ_LAUNCH("k_ews_fwd", kern, dim3(grid), dim3(kThreads), lds, s, B, E, ntiles, x, P, Q, dist,
+    FEQ_LAUNCH("k_ews_fwd", kern, dim3(grid), dim3(kThreads), lds, s, B, E, ntiles, X, P, Q, dist,
                frag, inv, F, y, DP);
     if (dp) {
         const NodeScatter NS{DP.perm, DP.offsets, DP.out, DP.part};
@@ -1615,10 +1710,30 @@ size_t ews_bwd_ws(const feq_binning& B, int64_t E, bool nodes) {
     const int64_t ntiles = ceil_div(E, kNE), g = static_cast<int64_t>(ews_cus()) * 2;
     const int G = static_cast<int>(ntiles < g ? ntiles : g);
     const int64_t kw = static_cast<int64_t>(K) * T::WD, ncc = static_cast<int64_t>(K) * COUT * CIN;
-    const size_t part = nodes ? align_up(4 * static_cast<size_t>(ntiles) * 2 * CIN * T::DIN, 256) : 0;
+    const size_t part = nodes ? align_up(4 * static_cast<size_t>(ntiles) * 2 * CIN * T::DIN, 256) +
+                                    3 * align_up(4 * static_cast<size_t>(E), 256)
+                              : 0;
     return align_up(4 * E * kw, 256) + align_up(4 * static_cast<size_t>(G) * ncc, 256) +
            align_up(4 * ew_tail_floats(B, static_cast<int>(kw), E, G, ncc), 256) +
            ews_cfrag_bytes<CIN, COUT, K>() + part + 1024;
+}
+
+// Source row, distance and (pooled form) destination of every CSR-by-source
+// position p (edge perm[p]) of the input-gradient kernel's tile walk.
+__global__ void k_scatter_order(int64_t E, const int32_t* __restrict__ perm, const int64_t* __restrict__ src,
+                                int64_t nsrc, const float* __restrict__ dist, const int64_t* __restrict__ dst,
+                                int64_t ndst, int32_t* __restrict__ src_pos, float* __restrict__ dist_pos,
+                                int32_t* __restrict__ dnode_pos) {
+    const int64_t p = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (p >= E) return;
+    const int64_t e = perm[p];
+    const int64_t r = src[e];
+    src_pos[p] = r >= 0 && r < nsrc ? static_cast<int32_t>(r) : -1;
+    dist_pos[p] = dist[e];
+    if (dst) {
+        const int64_t n = dst[e];
+        dnode_pos[p] = n >= 0 && n < ndst ? static_cast<int32_t>(n) : -1;
+    }
 }
 
 // ns: NULL for the per-edge input gradient gx; else the per-node sums into
@@ -1649,10 +1764,20 @@ int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const f
     if (ns) {
         NS = *ns;
         NS.part = cv.take<float>(static_cast<size_t>(ntiles) * 2 * CIN * T::DIN);
+        NS.src_pos = cv.take<int32_t>(E);
+        NS.dist_pos = cv.take<float>(E);
+        NS.dnode_pos = cv.take<int32_t>(E);
     }
     if (!ws || cv.used > ws_bytes) return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
     if (dp && !ns) return fail(FEQ_ERR_INVALID, "the pooled form needs the per-node input gradient");
     const DstPool DP = dp ? *dp : DstPool{};
+    if (ns) {
+        if (!x.src) return fail(FEQ_ERR_INVALID, "per-node sums need the message-passing form");
+        FEQ_LAUNCH("k_scatter_order", k_scatter_order, dim3(static_cast<unsigned>(ceil_div(E, kThreads))),
+                   dim3(kThreads), 0, s, E, NS.perm, x.src, x.nsrc, dist, dp ? DP.dst : nullptr, DP.ndst,
+                   const_cast<int32_t*>(NS.src_pos), const_cast<float*>(NS.dist_pos),
+                   const_cast<int32_t*>(NS.dnode_pos));
+    }
     auto prep = k_ews_prep<K, CIN, COUT, true>;
     FEQ_LAUNCH("k_ews_prep", prep, dim3(K * CIN / 16), dim3(kThreads), 0, s, C, frag, inv);
     auto kc = k_ews_bwd_c<CIN, COUT, LIN, LOUT, K, GATHER, false, false>;

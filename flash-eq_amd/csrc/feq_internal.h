@@ -95,6 +95,12 @@ struct NodeScatter {
     const int32_t* offsets;
     float* out;    // (nsrc, Cin, Din)
     float* part;   // (ntiles, 2, Cin, Din), carved from the backward's workspace
+    // by CSR position p (edge perm[p]), formed per call in the workspace so that
+    // the kernel's tile loads index them directly: the source row (-1 outside
+    // [0, nsrc)), the distance and, for the pooled form, the destination
+    const int32_t* src_pos;
+    const float* dist_pos;
+    const int32_t* dnode_pos;
 };
 
 // The V projection of attention fused with the attention's head weighting and
@@ -118,6 +124,9 @@ struct DstPool {
     int hc;              // channels per head
     float* out;          // forward: (ndst, Cout, Dout)
     float* part;         // forward: (ntiles, 2, Cout, Dout), carved from the workspace
+    const int64_t* src_pos;   // forward: src[perm[p]] by CSR position, formed per call
+    const int32_t* node_pos;  // forward: destination by CSR position (-1 outside [0, ndst))
+    const float* dist_pos;    // forward: distance by CSR position
 };
 
 // Split-fp16 fast paths (edgewise_split.hip); -1 when the shape has none.
