@@ -121,6 +121,29 @@ __device__ inline bool wave_segment(const int32_t* __restrict__ offsets, int64_t
     return true;
 }
 
+// The segment's edge indices and gathered row indices, one lane per position of
+// a 64-position chunk: loaded once per chunk, so the row loads of the chunk's
+// edges go out without waiting on index loads edge by edge.  chunk_at reads
+// position i's values (i wave-uniform) from the lane that loaded them.
+// Row r of the gathered table: ridx[e] (node form, -1 outside [0, nr)) or e.
+struct SegChunk {
+    int e, r;
+    template <bool GATHER>
+    __device__ __forceinline__ void load(const int32_t* __restrict__ perm, int b, int cnt, int i0,
+                                         const int64_t* __restrict__ ridx, int64_t nr) {
+        const int p = i0 + static_cast<int>(threadIdx.x & 63);
+        e = p < cnt ? perm[b + p] : 0;
+        if constexpr (GATHER) {
+            const int64_t rr = p < cnt ? ridx[e] : -1;
+            r = rr >= 0 && rr < nr ? static_cast<int>(rr) : -1;
+        } else {
+            r = p < cnt ? e : -1;
+        }
+    }
+    __device__ __forceinline__ int edge(int i) const { return __builtin_amdgcn_readlane(e, i & 63); }
+    __device__ __forceinline__ int row(int i) const { return __builtin_amdgcn_readlane(r, i & 63); }
+};
+
 // ---- logits + softmax --------------------------------------------------------
 // logit[e,h] = scale <Q[row q(e), h], K[row k(e), h]> - dist[e] / decay (decay > 0),
 // attn = exp(logit - max) / (sum exp(logit - max) + 1e-8) over the segment
@@ -155,15 +178,18 @@ k_att_fwd(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ K,
         float q[NT][V];
         if constexpr (NODE) ld_head<V, NT>(Q + n * ldq + h * Dh, j, G, NC, hv && cnt > 0, q);
         float m = -INFINITY, s = 0.0f;
+        SegChunk sc{};
         for (int i0 = 0; i0 < cnt; i0 += kUE) {
+            if ((i0 & 63) == 0) sc.load<NODE>(perm, b, cnt, i0, kidx, nk);
             int64_t eu[kUE];
             float k[kUE][NT][V];
 #pragma unroll
             for (int u = 0; u < kUE; ++u) {
                 const bool live = i0 + u < cnt;
-                eu[u] = perm[b + (live ? i0 + u : i0)];
-                const int64_t kr = NODE ? kidx[eu[u]] : eu[u];
-                const bool ok = hv && live && kr >= 0 && kr < nk;
+                const int iu = live ? i0 + u : i0;
+                eu[u] = sc.edge(iu);
+                const int64_t kr = sc.row(iu);
+                const bool ok = hv && live && kr >= 0;
                 ld_head<V, NT>(K + (ok ? kr : 0) * ldk + h * Dh, j, G, NC, ok, k[u]);
             }
             float dot[kUE];
@@ -253,20 +279,23 @@ k_att_bwd_dst(const float* __restrict__ Q, int64_t ldq, const float* __restrict_
         for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int u = 0; u < V; ++u) acc[t][u] = 0.0f;
+        SegChunk sc{};
         for (int i0 = 0; i0 < cnt; i0 += kUE) {
+            if ((i0 & 63) == 0) sc.load<NODE>(perm, b, cnt, i0, kidx, nk);
             int64_t eu[kUE];
             float gl[kUE];
             float k[kUE][NT][V];
 #pragma unroll
             for (int u = 0; u < kUE; ++u) {
                 const bool live = i0 + u < cnt;
-                eu[u] = perm[b + (live ? i0 + u : i0)];
+                const int iu = live ? i0 + u : i0;
+                eu[u] = sc.edge(iu);
                 const int64_t e = eu[u];
+                const int64_t kr = sc.row(iu);
+                const bool ok = hv && live && kr >= 0;
+                ld_head<V, NT>(K + (ok ? kr : 0) * ldk + h * Dh, j, G, NC, ok, k[u]);
                 gl[u] = (hv && live) ? attn[e * H + h] * (gattn[e * H + h] - S) : 0.0f;
                 if (hv && live && ((i0 + u) & (G - 1)) == j) glogit[e * H + h] = gl[u];
-                const int64_t kr = NODE ? kidx[e] : e;
-                const bool ok = hv && live && kr >= 0 && kr < nk;
-                ld_head<V, NT>(K + (ok ? kr : 0) * ldk + h * Dh, j, G, NC, ok, k[u]);
             }
 #pragma unroll
             for (int u = 0; u < kUE; ++u) {
@@ -314,17 +343,20 @@ k_att_bwd_src(const float* __restrict__ Q, int64_t ldq, const int64_t* __restric
         for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int u = 0; u < V; ++u) acc[t][u] = 0.0f;
+        SegChunk sc{};
         for (int i0 = 0; i0 < cnt; i0 += kUE) {
+            if ((i0 & 63) == 0) sc.load<true>(perm, b, cnt, i0, qidx, nq);
             float gl[kUE];
             float q[kUE][NT][V];
 #pragma unroll
             for (int u = 0; u < kUE; ++u) {
                 const bool live = i0 + u < cnt;
-                const int64_t e = perm[b + (live ? i0 + u : i0)];
-                const int64_t qr = qidx[e];
-                const bool ok = hv && live && qr >= 0 && qr < nq;
-                gl[u] = ok ? glogit[e * H + h] * scale : 0.0f;
+                const int iu = live ? i0 + u : i0;
+                const int64_t e = sc.edge(iu);
+                const int64_t qr = sc.row(iu);
+                const bool ok = hv && live && qr >= 0;
                 ld_head<V, NT>(Q + (ok ? qr : 0) * ldq + h * Dh, j, G, NC, ok, q[u]);
+                gl[u] = ok ? glogit[e * H + h] * scale : 0.0f;
             }
 #pragma unroll
             for (int u = 0; u < kUE; ++u)
