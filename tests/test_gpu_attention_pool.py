@@ -100,10 +100,15 @@ def test_pooled_out_of_range_destinations(dev):
     assert torch.count_nonzero(got[2].cpu()[bad]) == 0
 
 
-def test_pooled_embedded_layout(dev):
-    """[0,1]x32 -> [0,1,2]x64 (the first layer of config 4) runs zero-embedded
-    in the [0,1] -> [0,1,2] x64 kernels from 4096 edges."""
-    layer, graph, P, Q, x, r, attn, gout = _setup(dev, [0, 1], [0, 1, 2], 32, 64, 700, 6000, 8, 9)
+@pytest.mark.parametrize("lin,lout,cin", [([0, 1], [0, 1, 2], 32), ([0, 1, 2], [0, 1], 64),
+                                          ([0, 1], [0, 1], 64)])
+def test_pooled_embedded_layout(dev, lin, lout, cin):
+    """Small layouts run zero-embedded in the [0,1] / [0,1,2] -> [0,1,2] x64
+    kernels from 4096 edges ([0,1]x32 -> [0,1,2]x64 is the first layer of
+    config 4); an output with fewer slots than the kernels' is sliced after the
+    pooling, and its gradient enters zero-padded."""
+    print(f"pooled embedded {lin} -> {lout} cin={cin}", flush=True)
+    layer, graph, P, Q, x, r, attn, gout = _setup(dev, lin, lout, cin, 64, 700, 6000, 8, 9)
     ref = _run(layer, graph, P, Q, x, r, attn, gout, 8, False)
     got = _run(layer, graph, P, Q, x, r, attn, gout, 8, True)
     for n, a, b in zip(["out", "grad_x", "grad_r", "grad_attn"], got[:4], ref[:4]):
