@@ -5,6 +5,8 @@
 // speed, deterministic, and free of memsets (safe to record into HIP graphs).
 #include "feq_internal.h"
 
+#include <type_traits>
+
 namespace feq {
 namespace {
 
@@ -52,6 +54,70 @@ k_transpose(const T* __restrict__ in, int64_t M, int64_t N, int TM, int TN, int 
     }
 }
 
+// The narrow transposes of float tables (in (batch, M, N) with N <= 32 or
+// M <= 32: node-major <-> component-major moves) with 16-byte accesses on both
+// sides.  NARROW_N: a tile is TM whole input rows, one contiguous run of TM N
+// floats, and N output rows of TM floats; LDS holds it as the output rows
+// (stride S = TM + 4, 16-byte aligned rows).  Otherwise (M <= 32) a tile is TN
+// columns of the M input rows and one contiguous output run of TN M floats,
+// held densely in LDS in output order.  The host takes this form when every
+// row start is 16-byte aligned (M % 4 == 0, resp. N % 4 == 0, aligned bases).
+template <bool NARROW_N>
+__global__ void __launch_bounds__(256)
+k_transpose4(const float* __restrict__ in, int64_t M, int64_t N, int TM, int TN, int S, uint64_t mag,
+             int64_t tiles_n, float* __restrict__ out) {
+    extern __shared__ float4 lds4[];
+    float* s = reinterpret_cast<float*>(lds4);
+    const int64_t tile = blockIdx.x;
+    const int64_t tm = tile / tiles_n, tn = tile - tm * tiles_n;
+    const int64_t m0 = tm * TM, n0 = tn * TN;
+    const int h = static_cast<int>(M - m0 < TM ? M - m0 : TM);
+    const int w = static_cast<int>(N - n0 < TN ? N - n0 : TN);
+    const int64_t boff = static_cast<int64_t>(blockIdx.y) * M * N;
+    const float* src = in + boff;
+    float* dst = out + boff;
+    const int tid = threadIdx.x;
+    if constexpr (NARROW_N) {
+        // read: the run of h rows x N, element i -> (r = i / N, c = i % N) -> s[c S + r]
+        const float4* r4 = reinterpret_cast<const float4*>(src + m0 * N);
+        const int run4 = h * static_cast<int>(N) / 4;
+        for (int q = tid; q < run4; q += 256) {
+            const float4 v = r4[q];
+            const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t i = 4 * q + j;
+                const int r = static_cast<int>(div16(i, mag));
+                const int c = static_cast<int>(i) - r * static_cast<int>(N);
+                s[c * S + r] = e[j];
+            }
+        }
+        __syncthreads();
+        // write: N output rows of h floats at dst + c M + m0
+        const int h4 = h / 4;
+        for (int q = tid; q < static_cast<int>(N) * h4; q += 256) {
+            const int c = q / h4, r = 4 * (q - c * h4);
+            *reinterpret_cast<float4*>(dst + c * M + m0 + r) = *reinterpret_cast<const float4*>(s + c * S + r);
+        }
+    } else {
+        // read: M input rows of w floats at src + r N + n0 -> s[c M + r] (output order)
+        const int w4 = w / 4;
+        for (int q = tid; q < static_cast<int>(M) * w4; q += 256) {
+            const int r = q / w4, c = 4 * (q - r * w4);
+            const float4 v = *reinterpret_cast<const float4*>(src + r * N + n0 + c);
+            s[c * M + r] = v.x;
+            s[(c + 1) * M + r] = v.y;
+            s[(c + 2) * M + r] = v.z;
+            s[(c + 3) * M + r] = v.w;
+        }
+        __syncthreads();
+        // write: one contiguous run of w M floats at dst + n0 M
+        float4* d4 = reinterpret_cast<float4*>(dst + n0 * M);
+        const float4* s4 = reinterpret_cast<const float4*>(s);
+        for (int q = tid; q < w * static_cast<int>(M) / 4; q += 256) d4[q] = s4[q];
+    }
+}
+
 struct TransposePlan {
     int TM, TN, S;
     int64_t tiles_m, tiles_n;
@@ -75,9 +141,33 @@ TransposePlan transpose_plan(int64_t M, int64_t N) {
     return p;
 }
 
+bool al16p(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 template <typename T>
 int transpose(const T* in, int64_t batch, int64_t M, int64_t N, T* out, hipStream_t s) {
     const TransposePlan p = transpose_plan(M, N);
+    if constexpr (std::is_same<T, float>::value) {
+        const bool narrow_n = N <= 32 && M > 32 && M % 4 == 0;
+        const bool narrow_m = M <= 32 && N > 32 && N % 4 == 0;
+        if ((narrow_n || narrow_m) && al16p(in) && al16p(out)) {
+            const int64_t tiles = p.tiles_m * p.tiles_n;
+            if (tiles > 0x7fffffff || batch > 65535)
+                return fail(FEQ_ERR_UNSUPPORTED, "transpose: %lld tiles x %lld matrices exceeds the grid",
+                            static_cast<long long>(tiles), static_cast<long long>(batch));
+            const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(batch));
+            if (narrow_n) {
+                const int S = p.TM + 4;
+                const size_t lds = sizeof(float) * static_cast<size_t>(S) * p.TN;
+                FEQ_LAUNCH("k_transpose", k_transpose4<true>, grid, dim3(256), lds, s, in, M, N, p.TM, p.TN,
+                           S, div16_magic(static_cast<uint32_t>(N)), p.tiles_n, out);
+            } else {
+                const size_t lds = sizeof(float) * static_cast<size_t>(p.TM) * p.TN;
+                FEQ_LAUNCH("k_transpose", k_transpose4<false>, grid, dim3(256), lds, s, in, M, N, p.TM,
+                           p.TN, 0, uint64_t{0}, p.tiles_n, out);
+            }
+            return FEQ_OK;
+        }
+    }
     const int64_t tiles = p.tiles_m * p.tiles_n;
     if (tiles > 0x7fffffff || batch > 65535)
         return fail(FEQ_ERR_UNSUPPORTED, "transpose: %lld tiles x %lld matrices exceeds the grid",

@@ -13,8 +13,10 @@ from flash_eq import ops
 
 pytestmark = pytest.mark.gpu
 
+# (rows % 4 == 0 with cols <= 32, or the mirror, take the 16-byte form; partial last tiles)
 SHAPES = [(1, 1), (7, 3), (1000, 9), (100003, 25), (9, 100003), (49, 4097), (129, 65), (64, 64),
-          (3, 5000), (4096, 1), (1, 4096), (333, 777)]
+          (3, 5000), (4096, 1), (1, 4096), (333, 777), (100004, 9), (9, 100004), (1000, 32),
+          (32, 1000), (36, 5), (5, 36)]
 
 
 @pytest.mark.parametrize("rows,cols", SHAPES)
@@ -26,7 +28,8 @@ def test_transpose_is_exact(dev, rows, cols, dtype):
     assert torch.equal(y.view(cols, rows), x.t().contiguous())
 
 
-@pytest.mark.parametrize("batch,rows,cols", [(64, 1563, 16), (5, 33, 70), (3, 9, 2000)])
+@pytest.mark.parametrize("batch,rows,cols", [(64, 1563, 16), (5, 33, 70), (3, 9, 2000), (7, 1000, 9),
+                                             (7, 9, 1004)])
 def test_batched_transpose(dev, batch, rows, cols):
     x = torch.randn(batch, rows, cols, device=dev)
     y = ops.transpose_last2(x, rows, cols).view(batch, cols, rows)
