@@ -92,6 +92,36 @@ __device__ __forceinline__ void row_copy(float* __restrict__ d, const float* __r
     for (int64_t i = lane; i < n; i += 64) d[i] = s[i];
 }
 
+// Each lane's share (elements lane, lane + 64, ...) of one node's x and gy
+// rows, held in registers: the backward kernels load the next node's rows
+// while the current node is computed, then move them into LDS.
+constexpr int kRowPer = kStageRow / 64;
+struct RowPrefetch {
+    float x[kRowPer], g[kRowPer];
+    __device__ __forceinline__ void load(const float* __restrict__ xs, const float* __restrict__ gs,
+                                         int64_t n, int64_t N, int64_t row, int lane) {
+        if (n >= N) return;
+#pragma unroll
+        for (int i = 0; i < kRowPer; ++i) {
+            const int64_t idx = lane + 64 * i;
+            if (idx < row) {
+                x[i] = xs[n * row + idx];
+                g[i] = gs[n * row + idx];
+            }
+        }
+    }
+    __device__ __forceinline__ void store(float* sx, float* sg, int64_t row, int lane) const {
+#pragma unroll
+        for (int i = 0; i < kRowPer; ++i) {
+            const int64_t idx = lane + 64 * i;
+            if (idx < row) {
+                sx[idx] = x[i];
+                sg[idx] = g[i];
+            }
+        }
+    }
+};
+
 __device__ __forceinline__ float sigmoidf(float v) { return 1.0f / (1.0f + expf(-v)); }
 
 // ---- separable layer norm ---------------------------------------------------
@@ -204,11 +234,13 @@ k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __r
     __shared__ float lds[STAGE ? 2 * kWaves * kStageRow : 1];
     float* sx = lds + (threadIdx.x >> 6) * 2 * kStageRow;
     float* sg = sx + kStageRow;
+    RowPrefetch pf;
+    if (STAGE) pf.load(x, gy, wave, N, row, lane);
     for (int64_t n = wave; n < N; n += nw) {
         if (STAGE) {
             wave_sync();  // the previous node's stores have read sg
-            row_copy(sx, x + n * row, row, lane);
-            row_copy(sg, gy + n * row, row, lane);
+            pf.store(sx, sg, row, lane);
+            pf.load(x, gy, n + nw, N, row, lane);   // in flight during this node
             wave_sync();
         }
         const float* xn = STAGE ? sx : x + n * row;
@@ -394,11 +426,13 @@ k_eqnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __re
     __shared__ float lds[STAGE ? 2 * kWaves * kStageRow : 1];
     float* sx = lds + (threadIdx.x >> 6) * 2 * kStageRow;
     float* sg = sx + kStageRow;
+    RowPrefetch pf;
+    if (STAGE) pf.load(x, gy, wave, N, row, lane);
     for (int64_t n = wave; n < N; n += nw) {
         if (STAGE) {
-            wave_sync();
-            row_copy(sx, x + n * row, row, lane);
-            row_copy(sg, gy + n * row, row, lane);
+            wave_sync();  // the previous node's stores have read sg
+            pf.store(sx, sg, row, lane);
+            pf.load(x, gy, n + nw, N, row, lane);   // in flight during this node
             wave_sync();
         }
         const float* xn = STAGE ? sx : x + n * row;
