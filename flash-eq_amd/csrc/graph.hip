@@ -208,7 +208,7 @@ extern "C" int feq_gather_rows(const float* src, int64_t nsrc, int64_t row, cons
 }
 
 // ---- sum of squares (the benchmarks' training loss sum(y^2)) -----------------
-// A fixed grid of kSsqGroups workgroups each sums a strided share of y^2 into
+// A fixed grid of kSsqGroups workgroups each sums a contiguous share of y^2 into
 // one partial; the partials are summed in a fixed order.  Deterministic, and
 // no memset: safe to record into a HIP graph.
 namespace feq {
@@ -217,6 +217,7 @@ constexpr int kSsqGroups = 1024;
 
 __device__ inline float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ inline float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ inline int64_t ceil_div_i(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Sum of y^2 of float32 (BF16 = false) or bfloat16 (BF16 = true) values, each
 // squared and summed in float32: 16-byte loads (4 floats or 8 bf16) when y is
@@ -257,9 +258,26 @@ k_sum_squares(const void* __restrict__ yv, int64_t n, float* __restrict__ part) 
     };
     int64_t tail0 = 0;
     if ((reinterpret_cast<uintptr_t>(yv) & 15u) == 0) {
+        // each workgroup walks a contiguous chunk of whole 1024-load steps: four
+        // coalesced loads in flight per thread, four partial sums combined in a
+        // fixed order
         const uint4* y4 = static_cast<const uint4*>(yv);
         const int64_t n4 = n / PER;
-        for (int64_t i = t0; i < n4; i += stride) acc += sq(y4[i]);
+        const int64_t steps = ceil_div_i(n4, 1024);
+        const int64_t per_wg = ceil_div_i(steps, gridDim.x);
+        const int64_t b0 = static_cast<int64_t>(blockIdx.x) * per_wg * 1024;
+        const int64_t b1 = b0 + per_wg * 1024 < n4 ? b0 + per_wg * 1024 : n4;
+        float a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+        int64_t i = b0 + threadIdx.x;
+        for (; i + 768 < b1; i += 1024) {
+            const uint4 v0 = y4[i], v1 = y4[i + 256], v2 = y4[i + 512], v3 = y4[i + 768];
+            acc += sq(v0);
+            a1 += sq(v1);
+            a2 += sq(v2);
+            a3 += sq(v3);
+        }
+        for (; i < b1; i += 256) acc += sq(y4[i]);
+        acc = (acc + a1) + (a2 + a3);
         tail0 = PER * n4;
     }
     for (int64_t i = tail0 + t0; i < n; i += stride) acc += scalar(i);

@@ -41,6 +41,24 @@ def test_sum_squares_bf16(dev):
     assert abs(SumSquaresFn.apply(y).item() - (y.double() ** 2).sum().item()) < 1e-3
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sum_squares_gradient(dev, dtype):
+    """The loss and its gradient y * (2 g).to(y.dtype) for a non-unit upstream
+    gradient, lengths with a scalar tail, unaligned (offset) inputs and an
+    empty input; the loss within 1e-6 of the float64 sum."""
+    g = torch.Generator().manual_seed(8)
+    for n, off in ((0, 0), (5, 0), (1029, 0), (3 * 1024 * 256 * 8 + 11, 0), (4001, 3)):
+        base = torch.randn(n + off, generator=g).to(dev, dtype)
+        y = base[off:].clone().requires_grad_(True) if off == 0 else base[off:].detach().requires_grad_(True)
+        s = SumSquaresFn.apply(y)
+        ref_s = (y.detach().double() ** 2).sum().item()
+        assert abs(s.item() - ref_s) <= 1e-6 * max(ref_s, 1.0), (n, off)
+        up = torch.tensor(0.37, device=dev)
+        s.backward(up)
+        ref = y.detach() * (2.0 * up).to(dtype)
+        assert y.grad.dtype == dtype and torch.equal(y.grad, ref), (n, off)
+
+
 def test_captured_step_replays_match_eager(dev):
     torch.manual_seed(2)
     rep = fe.Repr([0, 1, 2], 64)
