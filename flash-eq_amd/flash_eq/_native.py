@@ -119,6 +119,11 @@ _SIGS = {
     "feq_sum_squares_workspace": ([], _SZ),
     "feq_sum_squares": ([_P, _I64, _P, _P, _SZ, _P], ctypes.c_int),
     "feq_sum_squares_bf16": ([_P, _I64, _P, _P, _SZ, _P], ctypes.c_int),
+    "feq_radial_supported": ([_I32, _I32, _I32, _I32], ctypes.c_int),
+    "feq_radial_workspace": ([_I32, _I32], _SZ),
+    "feq_radial_fwd": ([_P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P], ctypes.c_int),
+    "feq_radial_bwd": ([_P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+                       ctypes.c_int),
     "feq_transpose": ([_P, _I64, _I64, _I64, _I32, _P, _P], ctypes.c_int),
     "feq_column_sums_workspace": ([_I64, _I64, _I32], _SZ),
     "feq_column_sums": ([_P, _I64, _I64, _I32, _P, _P, _SZ, _P], ctypes.c_int),

@@ -104,10 +104,42 @@ class SeparableRadialNet(nn.Module):
         ang = x.unsqueeze(-1) * self.frequencies
         return torch.cat([torch.sin(ang) * env.unsqueeze(-1), torch.cos(ang) * env.unsqueeze(-1)], -1)
 
+    def _edge_basis(self) -> torch.Tensor:
+        """The sinusoidal basis at the bin edges, formed from buffers only and
+        kept until a buffer changes (device, storage or in-place version)."""
+        be, fq = self.bin_edges, self.frequencies
+        key = (be.device, be.dtype, be.data_ptr(), be._version, fq.data_ptr(), fq._version)
+        cached = self.__dict__.get("_basis_cache")
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        basis = self._sinusoidal_basis(be)
+        self.__dict__["_basis_cache"] = (key, basis)
+        return basis
+
+    def _fused_mlp_ok(self, basis: torch.Tensor) -> bool:
+        t = self.trunk
+        if not (basis.is_cuda and len(t) == 4 and isinstance(t[0], nn.Linear) and isinstance(t[1], nn.SiLU)
+                and isinstance(t[2], nn.Linear) and isinstance(t[3], nn.SiLU)):
+            return False
+        params = (t[0].weight, t[0].bias, t[2].weight, t[2].bias, self.head.weight, self.head.bias)
+        if any(p is None or p.dtype != torch.float32 or not p.is_cuda for p in params) or basis.dtype != torch.float32:
+            return False
+        from ..ops import radial_mlp_supported
+        return radial_mlp_supported(basis.shape[0], basis.shape[1], t[0].out_features, self.head.out_features)
+
     def radial_functions(self) -> torch.Tensor:
-        """F[b, k, w]: the radial factor at every bin edge, shape (num_bins+1, rank, weight_dim)."""
-        h = self.trunk(self._sinusoidal_basis(self.bin_edges))
-        return self.head(h).view(-1, self.rank, self.weight_dim)
+        """F[b, k, w]: the radial factor at every bin edge, shape (num_bins+1, rank, weight_dim).
+        On the GPU in float32 the network runs as the fused kernels of
+        ``RadialMLPFn`` (one workgroup forward, one backward)."""
+        basis = self._edge_basis()
+        if self._fused_mlp_ok(basis):
+            from ..ops import RadialMLPFn
+            t = self.trunk
+            F = RadialMLPFn.apply(basis, t[0].weight, t[0].bias, t[2].weight, t[2].bias, self.head.weight,
+                                  self.head.bias)
+        else:
+            F = self.head(self.trunk(basis))
+        return F.view(-1, self.rank, self.weight_dim)
 
     def forward(self) -> torch.Tensor:
         """Full table (num_bins+1, out_mult, in_mult, weight_dim) (``radial.py:259-275``)."""

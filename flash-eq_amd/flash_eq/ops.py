@@ -1192,6 +1192,52 @@ class EqLinearFn(torch.autograd.Function):
                 None, None, None, None, None, None)
 
 
+class RadialMLPFn(torch.autograd.Function):
+    """The radial network of ``SeparableRadialNet`` at the bin edges
+    (``radial.py:200-275``): F = head(silu(W2 silu(W1 basis + b1) + b2)) + b3 as
+    ``feq_radial_fwd`` (a workgroup per row) and the parameter gradients as
+    ``feq_radial_bwd`` (per-row gradients, then one thread per weight summing
+    the rows in order: deterministic).  basis needs no gradient (it is formed
+    from buffers)."""
+
+    @staticmethod
+    def forward(ctx, basis, W1, b1, W2, b2, W3, b3):
+        B, I = basis.shape
+        H, O = W1.shape[0], W3.shape[0]
+        dev = basis.device
+        F = torch.empty(B, O, dtype=torch.float32, device=dev)
+        acts = torch.empty(B, 4 * H, dtype=torch.float32, device=dev)
+        ts = [t.detach().contiguous() for t in (basis, W1, b1, W2, b2, W3, b3)]
+        with torch.cuda.device(dev):
+            rc = N.lib().feq_radial_fwd(N.ptr(ts[0]), B, I, H, O, *[N.ptr(t) for t in ts[1:]], N.ptr(F),
+                                        N.ptr(acts), N.stream_ptr(dev))
+        N.check(rc, "feq_radial_fwd")
+        ctx.save_for_backward(ts[0], ts[3], ts[5], acts)
+        ctx.meta = (I, H, O, W1.shape, b1.shape)
+        return F
+
+    @staticmethod
+    def backward(ctx, gF):
+        basis, W2, W3, acts = ctx.saved_tensors
+        I, H, O, w1s, b1s = ctx.meta
+        B = basis.shape[0]
+        dev = basis.device
+        g = gF.detach().to(torch.float32).contiguous()
+        grads = [torch.empty(w1s, device=dev), torch.empty(b1s, device=dev), torch.empty_like(W2),
+                 torch.empty(H, device=dev), torch.empty_like(W3), torch.empty(O, device=dev)]
+        lib = N.lib()
+        ws = N.workspace(lib.feq_radial_workspace(B, H), dev)
+        with torch.cuda.device(dev):
+            rc = lib.feq_radial_bwd(N.ptr(basis), B, I, H, O, N.ptr(W2), N.ptr(W3), N.ptr(acts), N.ptr(g),
+                                    *[N.ptr(t) for t in grads], N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+        N.check(rc, "feq_radial_bwd")
+        return (None, *grads)
+
+
+def radial_mlp_supported(rows: int, in_dim: int, hidden: int, out_dim: int) -> bool:
+    return bool(N.lib().feq_radial_supported(rows, in_dim, hidden, out_dim))
+
+
 class SumSquaresFn(torch.autograd.Function):
     """sum(y ** 2) of a float32 or bfloat16 GPU tensor (feq_sum_squares /
     feq_sum_squares_bf16: float32 sums, deterministic, graph capturable), a

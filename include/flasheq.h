@@ -327,6 +327,29 @@ int feq_sum_squares(const float* y, int64_t n, float* out, void* workspace, size
 int feq_sum_squares_bf16(const void* y, int64_t n, float* out, void* workspace, size_t ws_bytes,
                          feq_stream_t stream);
 
+/* The radial network of SeparableRadialNet at the bin edges (radial.py:200-275:
+ * trunk = Linear(in_dim, hidden), SiLU, Linear(hidden, hidden), SiLU; head =
+ * Linear(hidden, out_dim)): F (rows, out_dim) = head(trunk(basis)) for the
+ * (rows, in_dim) sinusoidal basis, float32, weights row-major as nn.Linear
+ * holds them (W1 (hidden, in_dim), W2 (hidden, hidden), W3 (out_dim, hidden)).
+ * The reference runs these few hundred thousand flops as a dozen library
+ * launches per step; here the forward is one launch (a workgroup per row) and
+ * the backward two.  acts (rows, 4 hidden floats) receives the trunk's
+ * activations for feq_radial_bwd, which writes (does not accumulate) the six
+ * parameter gradients from grad_F, deterministically; its workspace is
+ * feq_radial_workspace(rows, hidden) bytes.  Shapes: feq_radial_supported. */
+#define FEQ_RADIAL_MAX_WIDTH 1024
+#define FEQ_RADIAL_MAX_OUT 4096
+int feq_radial_supported(int32_t rows, int32_t in_dim, int32_t hidden, int32_t out_dim);
+size_t feq_radial_workspace(int32_t rows, int32_t hidden);
+int feq_radial_fwd(const float* basis, int32_t rows, int32_t in_dim, int32_t hidden, int32_t out_dim,
+                   const float* W1, const float* b1, const float* W2, const float* b2, const float* W3,
+                   const float* b3, float* F, float* acts, feq_stream_t stream);
+int feq_radial_bwd(const float* basis, int32_t rows, int32_t in_dim, int32_t hidden, int32_t out_dim,
+                   const float* W2, const float* W3, const float* acts, const float* grad_F,
+                   float* grad_W1, float* grad_b1, float* grad_W2, float* grad_b2, float* grad_W3,
+                   float* grad_b3, void* workspace, size_t ws_bytes, feq_stream_t stream);
+
 /* High-degree form for bfloat16 features (canonical lvals 0..6 in and out,
  * Cin = Cout in {64, 128}, rank 4): x (E, Cin, Din), P, Q, y and the gradients
  * of x and y are bf16 (uint16 storage), dist, C, F and their gradients float32.
