@@ -273,6 +273,25 @@ __global__ void k_sum_partials(const float* __restrict__ part, int groups, int p
     out[blockIdx.y * n + q] = acc;
 }
 
+// Few sums of many partials (n <= kSmallN): a workgroup per output, its
+// threads summing interleaved partials, combined by a fixed tree in LDS.
+__global__ void __launch_bounds__(256)
+k_sum_partials_small(const float* __restrict__ part, int groups, int64_t n, float* __restrict__ out) {
+    __shared__ float s[256];
+    const int64_t q = blockIdx.x;
+    float acc = 0.0f;
+    for (int g = threadIdx.x; g < groups; g += 256) acc += part[static_cast<int64_t>(g) * n + q];
+    s[threadIdx.x] = acc;
+    __syncthreads();
+    for (int h = 128; h > 0; h >>= 1) {
+        if (threadIdx.x < h) s[threadIdx.x] += s[threadIdx.x + h];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[q] = s[0];
+}
+
+constexpr int64_t kSmallN = 256;
+
 constexpr int kSliceGroups = 32;   // partials summed per thread in one pass
 
 size_t reduce_tmp_floats(int groups, int64_t n) {
@@ -283,10 +302,16 @@ size_t reduce_tmp_floats(int groups, int64_t n) {
 }  // namespace
 
 // Deterministic sum of `groups` partial arrays of n floats: slices of at most
-// kSliceGroups partials into tmp, then the slices into out.
+// kSliceGroups partials into tmp, then the slices into out (up to kSmallN
+// outputs: one launch, a workgroup per output).
 int reduce_partials(const float* part, int groups, int64_t n, float* out, float* tmp,
                     hipStream_t s) {
     const unsigned nb = static_cast<unsigned>(ceil_div(n, 256));
+    if (n <= kSmallN && groups > kSliceGroups) {
+        FEQ_LAUNCH("k_sum_partials", k_sum_partials_small, dim3(static_cast<unsigned>(n)), dim3(256), 0, s,
+                   part, groups, n, out);
+        return FEQ_OK;
+    }
     if (groups <= kSliceGroups) {
         FEQ_LAUNCH("k_sum_partials", k_sum_partials, dim3(nb, 1), dim3(256), 0, s, part, groups,
                    groups, n, out);

@@ -100,24 +100,31 @@ k_radial_bwd_rows(const float* __restrict__ W2, const float* __restrict__ W3, co
     }
 }
 
-// Weight gradients, one thread per weight (rows summed in order):
+// Weight gradients (rows summed in a fixed order):
 //   gW3[o][i] = sum_b gF[b][o] h2[b][i], gb3[o] = sum_b gF[b][o]
 //   gW2[j][i] = sum_b gz2[b][j] h1[b][i], gb2[j] = sum_b gz2[b][j]
 //   gW1[j][i] = sum_b gz1[b][j] basis[b][i], gb1[j] = sum_b gz1[b][j]
+// A workgroup takes 64 weights; its four waves sum interleaved quarters of the
+// rows (b = 4 r + wave), combined in wave order through LDS.
+constexpr int kRadWeights = 64;
+
 __global__ void __launch_bounds__(kRadThreads)
 k_radial_bwd_weights(const float* __restrict__ basis, const float* __restrict__ gF,
                      const float* __restrict__ acts, const float* __restrict__ grows, int B, int I, int H,
                      int O, float* __restrict__ gW1, float* __restrict__ gb1, float* __restrict__ gW2,
                      float* __restrict__ gb2, float* __restrict__ gW3, float* __restrict__ gb3) {
-    const int64_t q = static_cast<int64_t>(blockIdx.x) * kRadThreads + threadIdx.x;
+    __shared__ float part[4][kRadWeights];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t q = static_cast<int64_t>(blockIdx.x) * kRadWeights + lane;
     const int64_t n3 = static_cast<int64_t>(O) * (H + 1), n2 = static_cast<int64_t>(H) * (H + 1);
     const int64_t n1 = static_cast<int64_t>(H) * (I + 1);
-    // (left operand row stride, column; right operand row stride, column; or -1: bias)
-    const float* L;
-    const float* R;
-    int64_t ls, rs;
-    int lc, rc;
-    float* out;
+    // the weight's left operand (row stride, column) and right operand (row
+    // stride, column; -1 for a bias: a plain sum of the left operand)
+    const float* L = gF;
+    const float* R = basis;
+    int64_t ls = 0, rs = 0;
+    int lc = 0, rc = -1;
+    float* out = nullptr;
     if (q < n3) {
         const int o = static_cast<int>(q / (H + 1)), i = static_cast<int>(q % (H + 1));
         L = gF; ls = O; lc = o;
@@ -135,25 +142,18 @@ k_radial_bwd_weights(const float* __restrict__ basis, const float* __restrict__ 
         L = grows + H; ls = 2 * H; lc = j;
         R = basis; rs = I; rc = i < I ? i : -1;
         out = i < I ? gW1 + static_cast<int64_t>(j) * I + i : gb1 + j;
-    } else {
-        return;
     }
-    float a0 = 0.0f, a1 = 0.0f;
-    int b = 0;
-    if (rc >= 0) {
-        for (; b + 1 < B; b += 2) {
-            a0 += L[b * ls + lc] * R[b * rs + rc];
-            a1 += L[(b + 1) * ls + lc] * R[(b + 1) * rs + rc];
+    float a = 0.0f;
+    if (out) {
+        if (rc >= 0) {
+            for (int b = wave; b < B; b += 4) a += L[b * ls + lc] * R[b * rs + rc];
+        } else {
+            for (int b = wave; b < B; b += 4) a += L[b * ls + lc];
         }
-        if (b < B) a0 += L[b * ls + lc] * R[b * rs + rc];
-    } else {
-        for (; b + 1 < B; b += 2) {
-            a0 += L[b * ls + lc];
-            a1 += L[(b + 1) * ls + lc];
-        }
-        if (b < B) a0 += L[b * ls + lc];
     }
-    *out = a0 + a1;
+    part[wave][lane] = a;
+    __syncthreads();
+    if (wave == 0 && out) *out = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
 }
 
 int radial_check(int B, int I, int H, int O) {
@@ -206,7 +206,7 @@ extern "C" int feq_radial_bwd(const float* basis, int32_t rows, int32_t in_dim, 
                W2, W3, grad_F, acts, hidden, out_dim, grows);
     const int64_t nw = static_cast<int64_t>(out_dim) * (hidden + 1) + static_cast<int64_t>(hidden) * (hidden + 1) +
                        static_cast<int64_t>(hidden) * (in_dim + 1);
-    FEQ_LAUNCH("k_radial_bwd", k_radial_bwd_weights, dim3(static_cast<unsigned>(ceil_div(nw, kRadThreads))),
+    FEQ_LAUNCH("k_radial_bwd", k_radial_bwd_weights, dim3(static_cast<unsigned>(ceil_div(nw, kRadWeights))),
                dim3(kRadThreads), 0, s, basis, grad_F, acts, grows, rows, in_dim, hidden, out_dim, gW1, gb1, gW2,
                gb2, gW3, gb3);
     return FEQ_OK;
