@@ -257,7 +257,9 @@ ColsumPass colsum_pass(int64_t rows, int64_t cols, int vec) {
     int64_t chunks = ceil_div(kColsumGroups, p.ctiles);
     const int64_t most = ceil_div(rows, rpp * 8);     // at least eight rows per thread
     if (chunks > most) chunks = most;
-    if (chunks < 1) chunks = 1;
+    // few rows (the chunked weight gradients' partial products): one pass, so
+    // one launch, however few workgroups it has
+    if (chunks < 1 || rows <= 256) chunks = 1;
     p.rows_per_chunk = ceil_div(rows, chunks);
     p.chunks = p.rows_per_chunk > 0 ? ceil_div(rows, p.rows_per_chunk) : 1;
     return p;
