@@ -43,6 +43,11 @@ __device__ void weight_lsum(const feq_layout& L, int* fl) {
 // partial histogram per workgroup (its waves' histograms summed in wave order).
 constexpr int kHistBatch = 16;
 
+// PAIR (even rows, 8-byte aligned): lane c owns the adjacent columns c0 + 2c and
+// c0 + 2c + 1 of each 128-column block, one 8-byte load and one 8-byte LDS read
+// and write per cell pair.  Otherwise lane c owns the columns c0 + c and c0 + 64 + c.
+// Both forms add every cell's edges in edge order with the same operations.
+template <bool PAIR>
 __global__ void __launch_bounds__(kThreads)
 k_ewm_hist(feq_binning B, int kw_row, int cw0, int kw, int64_t E, int64_t per_wave,
            const float* __restrict__ dist, const float* __restrict__ dFe,
@@ -58,35 +63,98 @@ k_ewm_hist(feq_binning B, int kw_row, int cw0, int kw, int64_t E, int64_t per_wa
     const int64_t e_begin = (static_cast<int64_t>(blockIdx.x) * waves + wave) * per_wave;
     const int64_t e_end = e_begin + per_wave < E ? e_begin + per_wave : E;
     for (int c0 = 0; c0 < kw; c0 += 128) {
-        const int ca = c0 + lane, cb = c0 + 64 + lane;
-        const int la = ca < kw ? ca : kw - 1, lb = cb < kw ? cb : kw - 1;   // in-bounds loads
+        // columns of the lane's two slots (in-bounds loads: clamped, not added)
+        const int ca = PAIR ? c0 + 2 * lane : c0 + lane, cb = PAIR ? ca + 1 : c0 + 64 + lane;
         const bool ina = ca < kw, inb = cb < kw;
-        // Batch of kHistBatch edges from e: lane j < kHistBatch bins edge e + j;
-        // the loads are unconditional (rows past the run repeat its last edge and
-        // are not added).  The next batch's loads are issued before this one is
-        // added in.
+        const int la = ina ? ca : (PAIR ? kw - 2 : kw - 1), lb = inb ? cb : kw - 1;
+        // Batch of kHistBatch edges from e: lane j < kHistBatch bins edge e + j.
+        // The loads are unconditional (rows past the run repeat its last edge and
+        // are not added; a batch wholly past it reads the last edge), and the
+        // bins are computed only where the batch is added, so nothing waits on a
+        // batch's loads before the batch ahead of it is added in: the compiler's
+        // in-order load counter then keeps the next batch in flight.
         struct Batch {
             float va[kHistBatch], vb[kHistBatch];
-            EdgeBin eb;
+            float r;
         };
         auto load = [&](int64_t e, Batch& b) {
-            const int nb = static_cast<int>(e_end - e < kHistBatch ? e_end - e : kHistBatch);
+            const int64_t ec = e < e_end ? e : e_end - 1;
+            const int nb = static_cast<int>(e_end - ec < kHistBatch ? e_end - ec : kHistBatch);
             const int jl = (lane % kHistBatch) < nb ? lane % kHistBatch : nb - 1;
-            b.eb = edge_bin(dist[e + jl], B);
+            b.r = dist[ec + jl];
 #pragma unroll
             for (int j = 0; j < kHistBatch; ++j) {
-                const float* row = dFe + (e + (j < nb ? j : nb - 1)) * kw_row + cw0;
-                b.va[j] = row[la];
-                b.vb[j] = row[lb];
+                const float* row = dFe + (ec + (j < nb ? j : nb - 1)) * kw_row + cw0;
+                if constexpr (PAIR) {
+                    const float2 v = *reinterpret_cast<const float2*>(row + la);
+                    b.va[j] = v.x;
+                    b.vb[j] = v.y;
+                } else {
+                    b.va[j] = row[la];
+                    b.vb[j] = row[lb];
+                }
             }
         };
         auto add = [&](int64_t e, const Batch& b) {
             const int nb = static_cast<int>(e_end - e < kHistBatch ? e_end - e : kHistBatch);
+            const EdgeBin eb = edge_bin(b.r, B);
+            if constexpr (PAIR) {
+                // Edges in groups of four.  When a group's lower bins are pairwise
+                // at least two apart its cells are distinct, and all its reads are
+                // issued before any write (one LDS round trip instead of four);
+                // otherwise its edges go one at a time.  Every cell receives its
+                // edges in edge order either way.
+#pragma unroll
+                for (int g = 0; g < kHistBatch; g += 4) {
+                    int lo[4];
+                    float t[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        lo[q] = __builtin_amdgcn_readlane(eb.lo, g + q);
+                        t[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(eb.t), g + q));
+                    }
+                    bool apart = g + 3 < nb;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int r = q + 1; r < 4; ++r)
+                            apart = apart && (lo[q] - lo[r] >= 2 || lo[r] - lo[q] >= 2);
+                    if (!ina) continue;
+                    if (apart) {
+                        float2 c[4][2];
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            c[q][0] = *reinterpret_cast<const float2*>(h + lo[q] * kw + ca);
+                            c[q][1] = *reinterpret_cast<const float2*>(h + lo[q] * kw + kw + ca);
+                        }
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const float u = 1.0f - t[q], va = b.va[g + q], vb = b.vb[g + q];
+                            *reinterpret_cast<float2*>(h + lo[q] * kw + ca) =
+                                make_float2(c[q][0].x + u * va, c[q][0].y + u * vb);
+                            *reinterpret_cast<float2*>(h + lo[q] * kw + kw + ca) =
+                                make_float2(c[q][1].x + t[q] * va, c[q][1].y + t[q] * vb);
+                        }
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            if (g + q >= nb) break;
+                            float2* p0 = reinterpret_cast<float2*>(h + lo[q] * kw + ca);
+                            float2* p1 = reinterpret_cast<float2*>(h + lo[q] * kw + kw + ca);
+                            const float2 a = *p0, c = *p1;
+                            const float u = 1.0f - t[q], va = b.va[g + q], vb = b.vb[g + q];
+                            *p0 = make_float2(a.x + u * va, a.y + u * vb);
+                            *p1 = make_float2(c.x + t[q] * va, c.y + t[q] * vb);
+                        }
+                    }
+                }
+                return;
+            }
 #pragma unroll
             for (int j = 0; j < kHistBatch; ++j) {
                 if (j < nb) {
-                    const int lo = __builtin_amdgcn_readlane(b.eb.lo, j);
-                    const float t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b.eb.t), j));
+                    const int lo = __builtin_amdgcn_readlane(eb.lo, j);
+                    const float t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(eb.t), j));
                     float* hl = h + lo * kw;
                     // read-add-write: the wave's LDS operations execute in issue
                     // order, so the next edge's reads see these writes (a lane's
@@ -106,16 +174,18 @@ k_ewm_hist(feq_binning B, int kw_row, int cw0, int kw, int64_t E, int64_t per_wa
         };
         Batch b0, b1;
         int64_t e = e_begin;
-        if (e < e_end) load(e, b0);
-        while (e < e_end) {
-            const int64_t e1 = e + kHistBatch;
-            if (e1 < e_end) load(e1, b1);
-            add(e, b0);
-            if (e1 >= e_end) break;
-            const int64_t e2 = e1 + kHistBatch;
-            if (e2 < e_end) load(e2, b0);
-            add(e1, b1);
-            e = e2;
+        if (e < e_end) {
+            load(e, b0);
+            for (;;) {
+                load(e + kHistBatch, b1);
+                add(e, b0);
+                e += kHistBatch;
+                if (e >= e_end) break;
+                load(e + kHistBatch, b0);
+                add(e, b1);
+                e += kHistBatch;
+                if (e >= e_end) break;
+            }
         }
     }
     __syncthreads();
@@ -397,13 +467,20 @@ int ew_tail(const feq_layout& L, const feq_binning& B, int K, int64_t E, const f
     }
     const BinWs w = bin_ws(B, kw, E, groups, ncc, tail);
     if (use_hist(B, kw)) {
-        FEQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_ewm_hist),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kHistLds)));
         const int waves = hist_waves(B, kw);
         const size_t hlds = 4 * static_cast<size_t>(waves) * (nb + 1) * kw;
         const int64_t per_wave = ceil_div(E, static_cast<int64_t>(kHistGroups) * waves);
-        FEQ_LAUNCH("k_ewm_hist", k_ewm_hist, dim3(kHistGroups), dim3(64 * waves), hlds, s, B, kw, 0, kw,
-                   E, per_wave, dist, dFe, w.part);
+        if (kw % 2 == 0 && reinterpret_cast<uintptr_t>(dFe) % 8 == 0) {
+            FEQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_ewm_hist<true>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kHistLds)));
+            FEQ_LAUNCH("k_ewm_hist", k_ewm_hist<true>, dim3(kHistGroups), dim3(64 * waves), hlds, s, B, kw, 0,
+                       kw, E, per_wave, dist, dFe, w.part);
+        } else {
+            FEQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_ewm_hist<false>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kHistLds)));
+            FEQ_LAUNCH("k_ewm_hist", k_ewm_hist<false>, dim3(kHistGroups), dim3(64 * waves), hlds, s, B, kw, 0,
+                       kw, E, per_wave, dist, dFe, w.part);
+        }
         if (int rc = reduce_partials(w.part, kHistGroups, (nb + 1) * static_cast<int64_t>(kw), gF, w.tmp, s))
             return rc;
     } else {
