@@ -258,9 +258,9 @@ k_sum_squares(const void* __restrict__ yv, int64_t n, float* __restrict__ part) 
     };
     int64_t tail0 = 0;
     if ((reinterpret_cast<uintptr_t>(yv) & 15u) == 0) {
-        // each workgroup walks a contiguous chunk of whole 1024-load steps: four
-        // coalesced loads in flight per thread, four partial sums combined in a
-        // fixed order
+        // each workgroup walks a contiguous chunk of whole 1024-load steps: eight
+        // (then four) coalesced loads in flight per thread, streamed past the
+        // caches, four partial sums combined in a fixed order
         const uint4* y4 = static_cast<const uint4*>(yv);
         const int64_t n4 = n / PER;
         const int64_t steps = ceil_div_i(n4, 1024);
@@ -269,6 +269,20 @@ k_sum_squares(const void* __restrict__ yv, int64_t n, float* __restrict__ part) 
         const int64_t b1 = b0 + per_wg * 1024 < n4 ? b0 + per_wg * 1024 : n4;
         float a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
         int64_t i = b0 + threadIdx.x;
+        for (; i + 1792 < b1; i += 2048) {
+            typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+            const u32x4* yn = reinterpret_cast<const u32x4*>(y4 + i);
+            uint4 v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const u32x4 w = __builtin_nontemporal_load(yn + 256 * k);
+                v[k] = make_uint4(w.x, w.y, w.z, w.w);
+            }
+            acc += sq(v[0]) + sq(v[4]);
+            a1 += sq(v[1]) + sq(v[5]);
+            a2 += sq(v[2]) + sq(v[6]);
+            a3 += sq(v[3]) + sq(v[7]);
+        }
         for (; i + 768 < b1; i += 1024) {
             const uint4 v0 = y4[i], v1 = y4[i + 256], v2 = y4[i + 512], v3 = y4[i + 768];
             acc += sq(v0);

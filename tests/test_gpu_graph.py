@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 
 def test_sum_squares_matches_torch(dev):
     g = torch.Generator().manual_seed(5)
-    for n in (0, 1, 7, 1000, 3 * 1024 * 256 + 5):
+    for n in (0, 1, 7, 1000, 3 * 1024 * 256 + 5, 9 * 1024 * 1024 * 4 + 3 * 1024 + 7):   # the last: 8-load steps
         y = torch.randn(n, generator=g).to(dev).requires_grad_(True)
         s = SumSquaresFn.apply(y)
         ref = (y.detach().double() ** 2).sum()
@@ -29,7 +29,7 @@ def test_sum_squares_matches_torch(dev):
 def test_sum_squares_bf16(dev):
     """bfloat16 input: float32 squares and sums (8 values per 16-byte load), gradient 2y in bf16."""
     g = torch.Generator().manual_seed(6)
-    for n in (0, 1, 9, 4001, 2 * 1024 * 256 * 8 + 13):
+    for n in (0, 1, 9, 4001, 2 * 1024 * 256 * 8 + 13, 9 * 1024 * 1024 * 8 + 13):
         y = torch.randn(n, generator=g).to(dev, torch.bfloat16).requires_grad_(True)
         s = SumSquaresFn.apply(y)
         assert s.dtype == torch.float32
