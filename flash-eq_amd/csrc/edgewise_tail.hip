@@ -52,7 +52,7 @@ __global__ void __launch_bounds__(kThreads)
 k_ewm_hist(feq_binning B, int kw_row, int cw0, int kw, int64_t E, int64_t per_wave,
            const float* __restrict__ dist, const float* __restrict__ dFe,
            float* __restrict__ hist_part) {
-    extern __shared__ float sh[];
+    extern __shared__ __align__(16) float sh[];   // 8-byte cell pairs in the PAIR form
     const int waves = blockDim.x / 64;
     const int hsz = (B.num_bins + 1) * kw;
     for (int q = threadIdx.x; q < waves * hsz; q += blockDim.x) sh[q] = 0.0f;
