@@ -27,10 +27,11 @@ def _inputs(lin, lout, E, cin, seed, rmax=12.0, rmin=0.0):
     return x, d, r, gy_seed
 
 
-def _run_parity(dev, lin, lout, cin, cout, E, seed=0, log=False, grad_pq=False, rmin=0.0, rvals=None):
+def _run_parity(dev, lin, lout, cin, cout, E, seed=0, log=False, grad_pq=False, rmin=0.0, rvals=None,
+                rank=4):
     torch.manual_seed(seed)
     kw = dict(log_bins=True, min_dist=0.5) if log else {}
-    layer = fe.EquivariantEdgewiseLinear(fe.Repr(lin, cin), fe.Repr(lout, cout), num_bins=50, **kw)
+    layer = fe.EquivariantEdgewiseLinear(fe.Repr(lin, cin), fe.Repr(lout, cout), num_bins=50, rank=rank, **kw)
     x, d, r, g = _inputs(lin, lout, E, cin, seed, rmin=rmin)
     if rvals is not None:      # distances drawn from a few values: neighbouring edges share bins
         r = torch.tensor(rvals)[torch.randint(len(rvals), (E,), generator=g)]
@@ -264,13 +265,14 @@ def test_zero_distance_self_loop(dev):
     assert torch.isnan(rg.grad[0]) and torch.isfinite(rg.grad[1:]).all()
 
 
-@pytest.mark.parametrize("rvals", [None, [2.0, 2.1, 2.3, 7.3]])
-def test_binned_gradient_many_edges_per_wave(dev, rvals):
+@pytest.mark.parametrize("rvals,rank", [(None, 4), ([2.0, 2.1, 2.3, 7.3], 4), (None, 3)])
+def test_binned_gradient_many_edges_per_wave(dev, rvals, rank):
     """E large enough that each wave of the binned radial-function gradient adds
-    several whole batches of edges and a partial one (the rows are c2's:
-    K * wdim = 76 columns); with clustered distances neighbouring edges mostly
+    several whole batches of edges and a partial one.  Rank 4 gives c2's rows
+    (K * wdim = 76 columns, lanes on column pairs); rank 3 an odd row of 57
+    (a lane per column).  With clustered distances neighbouring edges mostly
     fall in the same or adjacent bins."""
-    _run_parity(dev, [0, 1, 2], [0, 1, 2], cin=8, cout=8, E=40000, seed=11, rvals=rvals)
+    _run_parity(dev, [0, 1, 2], [0, 1, 2], cin=8, cout=8, E=40000, seed=11, rvals=rvals, rank=rank)
 
 
 def test_out_of_range_distances_extrapolate(dev):
