@@ -28,6 +28,7 @@ __device__ __forceinline__ void row_dense(const float* __restrict__ W, const flo
         const float* w = W + static_cast<int64_t>(j) * I;
         float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
         int i = 0;
+#pragma unroll 4
         for (; i + 3 < I; i += 4) {
             a0 += w[i] * src[i];
             a1 += w[i + 1] * src[i + 1];
@@ -79,6 +80,7 @@ k_radial_bwd_rows(const float* __restrict__ W2, const float* __restrict__ W3, co
     for (int i = threadIdx.x; i < H; i += kRadThreads) {
         float s0 = 0.0f, s1 = 0.0f;
         int o = 0;
+#pragma unroll 8
         for (; o + 1 < O; o += 2) {
             s0 += gf[o] * W3[static_cast<int64_t>(o) * H + i];
             s1 += gf[o + 1] * W3[static_cast<int64_t>(o + 1) * H + i];
@@ -90,6 +92,7 @@ k_radial_bwd_rows(const float* __restrict__ W2, const float* __restrict__ W3, co
     for (int i = threadIdx.x; i < H; i += kRadThreads) {
         float s0 = 0.0f, s1 = 0.0f;
         int j = 0;
+#pragma unroll 8
         for (; j + 1 < H; j += 2) {
             s0 += g2[j] * W2[j * H + i];
             s1 += g2[j + 1] * W2[(j + 1) * H + i];
@@ -145,9 +148,12 @@ k_radial_bwd_weights(const float* __restrict__ basis, const float* __restrict__ 
     }
     float a = 0.0f;
     if (out) {
+        // unrolled: eight rows' loads in flight ahead of the (ordered) sum
         if (rc >= 0) {
+#pragma unroll 8
             for (int b = wave; b < B; b += 4) a += L[b * ls + lc] * R[b * rs + rc];
         } else {
+#pragma unroll 8
             for (int b = wave; b < B; b += 4) a += L[b * ls + lc];
         }
     }
