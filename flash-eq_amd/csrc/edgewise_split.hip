@@ -116,8 +116,21 @@ k_ews_prep(const float* __restrict__ C, h8* __restrict__ frag, float* __restrict
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int k = blockIdx.x / NRB, rb = blockIdx.x % NRB;
     const float* Ck = C + static_cast<int64_t>(k) * NCH;
+    // the thread's eight fragment values are requested before the rank's
+    // maximum (they do not depend on its scale): one memory latency, not two
+    const int l = tid & 63, ks = tid >> 6;
+    const int row = 16 * rb + (l & 15), c0 = 32 * ks + 8 * (l >> 4);
+    float av[8];
+    if (tid < NKS * 64) {
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+            // A = C_k (row co, reduction ci) or C_k^T (row ci, reduction co); C is (K, Cout, Cin)
+            av[jj] = TRANS ? Ck[(c0 + jj) * NROW + row] : Ck[row * NRED + c0 + jj];
+    }
+    static_assert(NCH % kThreads == 0, "whole rows of the rank per thread");
     float v = 0.0f;
-    for (int q = tid; q < NCH; q += kThreads) v = fmaxf(v, fabsf(Ck[q]));
+#pragma unroll
+    for (int r = 0; r < NCH / kThreads; ++r) v = fmaxf(v, fabsf(Ck[tid + r * kThreads]));
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
     if (lane == 0) red[wave] = v;
@@ -129,15 +142,11 @@ k_ews_prep(const float* __restrict__ C, h8* __restrict__ frag, float* __restrict
     const float sc = exp2i(e);
     if (rb == 0 && tid == 0) inv[k] = exp2i(-e);
     if (tid < NKS * 64) {
-        const int l = tid & 63, ks = tid >> 6;
-        const int row = 16 * rb + (l & 15), c0 = 32 * ks + 8 * (l >> 4);
         h8 hi, lo;
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
-            // A = C_k (row co, reduction ci) or C_k^T (row ci, reduction co); C is (K, Cout, Cin)
-            const float a = TRANS ? Ck[(c0 + jj) * NROW + row] : Ck[row * NRED + c0 + jj];
             _Float16 h, lw;
-            split_f16s(a, sc, h, lw);
+            split_f16s(av[jj], sc, h, lw);
             hi[jj] = h;
             lo[jj] = lw;
         }
