@@ -64,13 +64,18 @@ def algorithmic_per_edge(lin, lout, cin, cout, same_pq=True, nodes_per_edge=None
 
     The mix of one (co, ci) pair costs M real MACs, M = n0_in n0_out +
     2 sum_{m>=1} 2 n_in(m) n_out(m); a rotation of one channel costs
-    S = sum (2l+1)^2 MACs (P and Q are block diagonal over irreps).  Bytes are
-    the tensors each kernel must move once: x, P (= Q), r, y for the forward;
-    gy, x, P, r, gx for the input-gradient kernel; gy, x, P, r for the
-    channel-pattern-gradient kernel.  In the message-passing form
-    (nodes_per_edge = N / E) the input-gradient kernel writes node rows, N / E
-    of them per edge, instead of a row per edge.  The distance-gradient mix is
-    excluded (the benchmark does not differentiate the distances).
+    S = sum (2l+1)^2 MACs (P and Q are block diagonal over irreps).
+
+    Bytes follow one convention everywhere (SURVEY 8(d)'s yardstick, the one
+    the north-star 60% target is stated in): every tensor of the reference
+    layer's interface once per edge, as the reference's EquivariantEdgewiseLinear
+    reads and writes them (linear.py:144-160) -- x, P (= Q), r, y for the
+    forward; gy, x, P, r, gx for the input-gradient kernel; gy, x, P, r for
+    the channel-pattern-gradient kernel.  The message-passing form moves fewer
+    bytes than that (it writes gx as node rows, N / E of them per edge); with
+    nodes_per_edge set, the "_node_rows" entries count gx that way.  The
+    distance-gradient mix is excluded (the benchmark does not differentiate the
+    distances).
     """
     mmax = max(max(lin), max(lout))
     M = 0
@@ -86,12 +91,15 @@ def algorithmic_per_edge(lin, lout, cin, cout, same_pq=True, nodes_per_edge=None
     rot = 2 * cin * s_in + 2 * cout * s_out
     X, Y = 4 * cin * din, 4 * cout * dout
     PQ = 4 * din * din + (0 if same_pq else 4 * dout * dout)
-    return {
+    out = {
         "k_ews_fwd": (mix + rot, X + PQ + 4 + Y),
-        "k_ews_bwd_x": (mix + rot, Y + X + PQ + 4 + X * (1.0 if nodes_per_edge is None else nodes_per_edge)),
+        "k_ews_bwd_x": (mix + rot, Y + X + PQ + 4 + X),
         "k_ews_bwd_c": (mix, Y + X + PQ + 4),
         "_mix_macs_per_pair": M,
     }
+    if nodes_per_edge is not None:
+        out["_node_rows"] = {"k_ews_bwd_x": Y + X + PQ + 4 + X * nodes_per_edge}
+    return out
 
 
 def executed_mfma_flop_per_edge(lin, lout, cin, cout, rank=4):
@@ -105,6 +113,30 @@ def executed_mfma_flop_per_edge(lin, lout, cin, cout, rank=4):
     kpad = -(-16 * din // 32) * 32 / 16                     # padded slots per edge
     g_c = 3 * 2 * rank * cout * cin * kpad                  # dC_k += U_k fs^T
     return {"k_ews_fwd": g_fwd, "k_ews_bwd_x": g_x, "k_ews_bwd_c": g_c}
+
+
+def highl_mfma_flop_per_edge(C: int = 128, L: int = 6, rank: int = 4) -> dict:
+    """bf16 matrix-core flops the high-degree kernels (csrc/edgewise_hl.hip)
+    execute per edge, counted from their tile loops (one 16x16x32 MFMA =
+    16 384 flop, one 16x16x16 = 8 192): the rotations take (C x D) x (D x D)
+    per edge with D padded to 16-column blocks and 32-steps (rot_out twice, for
+    the hi and lo parts); the mixes and the per-edge radial-function gradient
+    one G_k = C_k fs per slot, rank and 16-row block, 32-steps over the channels,
+    per 16-edge tile; the channel-pattern gradient one product per 32-step of
+    two slots x 16 edges, column block and rank."""
+    D = (L + 1) ** 2
+    f32 = 16 * 16 * 32 * 2
+    rot = (C // 16) * -(-D // 16) * -(-D // 32) * f32
+    mix = D * rank * (C // 32) * (C // 16) * f32 / 16
+    steps = sum(-(-((2 if m else 1) * (L - m + 1)) // 2) for m in range(L + 1))
+    dc = steps * (C // 16) * rank * (C // 16) * f32 / 16
+    return {"k_hl_rot_in": rot, "k_hl_rot_out": 2 * rot, "k_hl_mix": mix, "k_hl_mix_t": mix,
+            "k_hl_dfe": mix, "k_hl_dc": dc}
+
+
+# SURVEY 8(d): config 5's algorithmic work, 54.7 MFLOP per edge fwd + bwd, bounds
+# the step at 3.479 ms on the bf16 matrix cores
+C5_BOUND_MS = 3.479
 
 
 def read_traffic(path: str = TRAFFIC_FILE) -> dict:
@@ -286,30 +318,33 @@ def build_workload(name: str):
             return equivariance_error(o1, o2)
 
         def cpu():
-            # the oracle's block (float32) on the edges into the first 500 nodes
+            # the oracle's block (float32) on its own graph: 500 nodes at config
+            # 3's density (box scaled by (500/20000)^(1/3)), radius 10, k <= 32,
+            # fed the values the GPU run sees (bf16-rounded for the bf16 variant)
             from oracle import model as OM
             from oracle import wigner as OW
-            sel = dst < 500
-            s, d = src[sel], dst[sel]
-            vec = coords[s] - coords[d]
-            P = OW.basis([0, 1, 2], vec).float()
-            r = vec.norm(dim=-1)
-            params = {k: (v.float().requires_grad_(True) if v.is_floating_point()
+            n = 500
+            c, s, d = radius_graph(n, 60.0 * (n / 20000) ** (1.0 / 3.0), 10.0, 32, seed=1103)
+            vec = c[s] - c[d]
+            P = OW.basis([0, 1, 2], vec).to(dtype).float()
+            r = vec.norm(dim=-1).to(dtype).float()
+            params = {k: (v.to(dtype).float().requires_grad_(True) if v.is_floating_point()
                           and not k.endswith(("bin_edges", "frequencies")) else v.float()
                           if v.is_floating_point() else v) for k, v in block_cpu.items()}
             cfg = OM.block_cfg([0, 1, 2], [0, 1, 2], 64, 64, heads=8, num_bins=100, max_dist=10.0)
-            x = feats_cpu.clone().requires_grad_(True)
+            x = feats_cpu[:n].to(dtype).float().clone().requires_grad_(True)
 
             def run():
-                out = OM.block(params, cfg, P, P, x, r, s, d, N)
+                out = OM.block(params, cfg, P, P, x, r, s, d, n)
                 (out ** 2).sum().backward()
             med, times = _median_time(run, 2)
-            return {"value": round(int(sel.sum()) / med, 1),
-                    "sample": f"edges into nodes 0..499 ({int(sel.sum())} of {E}), all {N} node "
-                              f"rows: fwd + (out**2).sum() + bwd of the float32 oracle block "
-                              f"(oracle/model.py), median of 2 after 1 warmup ({sum(times):.1f} s)"}
+            return {"value": round(s.numel() / med, 1),
+                    "sample": f"its own graph of {n} nodes at config 3's density (radius 10, k <= 32, "
+                              f"{s.numel()} edges): fwd + (out**2).sum() + bwd of the float32 oracle "
+                              f"block (oracle/model.py) on the {str(dtype).replace('torch.', '')} "
+                              f"values, median of 2 after 1 warmup ({sum(times):.1f} s)"}
 
-        wl.update(step=step, E=E, N=N, equiv=equiv, cpu=None if dtype != torch.float32 else cpu,
+        wl.update(step=step, E=E, N=N, equiv=equiv, cpu=cpu,
                   leaves=[feats] + list(block.parameters()),
                   work=algorithmic_per_edge([0, 1, 2], [0, 1, 2], 64, 64, nodes_per_edge=N / E),
                   config=(f"c3: EquivariantTransformerBlock 8 heads [0,1,2]x64, radius-10 graph "
@@ -371,7 +406,19 @@ def build_workload(name: str):
                               f"oracle transformer (oracle/model.py), median of 1 after 1 warmup "
                               f"({sum(times):.1f} s)"}
 
-        wl.update(step=step, E=E, N=N, equiv=None, cpu=cpu, leaves=[feats] + list(model.parameters()),
+        def equiv():
+            # the output is Repr([0], 8): invariant under a rotation of the
+            # coordinates with the input features Wigner-rotated
+            axis, angle = _rotation(dev, 79)
+            D = fe.WignerD(fe.Repr([0, 1])).to(dev).rot(axis, angle)
+            R = fe.WignerD(fe.Repr([1])).to(dev).rot(axis, angle, cartesian=True)
+            with torch.no_grad():
+                x = feats.detach()
+                o1 = model(xyz, x, graph)
+                o2 = model(xyz @ R.T, torch.einsum("ij,ncj->nci", D, x), graph)
+            return equivariance_error(o1, o2)
+
+        wl.update(step=step, E=E, N=N, equiv=equiv, cpu=cpu, leaves=[feats] + list(model.parameters()),
                   work=algorithmic_per_edge([0, 1, 2], [0, 1, 2], 64, 64, nodes_per_edge=N / E),
                   config=(f"c4: EquivariantTransformer 6 layers, in [0,1]x32, hidden [0,1,2]x64, "
                           f"out [0]x8 (x1 is not divisible into 8 heads), 8 heads, random-walk "
@@ -424,7 +471,19 @@ def build_workload(name: str):
                     "sample": f"all {E} edges: gather + float32 oracle layer + sum pooling, fwd + "
                               f"bwd, median of 5 after 1 warmup ({sum(times):.2f} s)"}
 
-        wl.update(step=step, E=E, N=N, equiv=None, cpu=cpu, leaves=[feats] + list(layer.parameters()),
+        def equiv():
+            axis, angle = _rotation(dev, 78)
+            Din = fe.WignerD(rin).to(dev).rot(axis, angle)
+            Dout = fe.WignerD(rout).to(dev).rot(axis, angle)
+            R = fe.WignerD(fe.Repr([1])).to(dev).rot(axis, angle, cartesian=True)
+            with torch.no_grad():
+                x = feats.detach()
+                o1 = torch.einsum("ij,ncj->nci", Dout, pool(layer(P, Q, x, dist, graph=graph), graph))
+                P2, Q2 = fe.WignerDBasis([rin, rout]).to(dev)(vec @ R.T)
+                o2 = pool(layer(P2, Q2, torch.einsum("ij,ncj->nci", Din, x), dist, graph=graph), graph)
+            return equivariance_error(o1, o2)
+
+        wl.update(step=step, E=E, N=N, equiv=equiv, cpu=cpu, leaves=[feats] + list(layer.parameters()),
                   work=algorithmic_per_edge([0, 1], [0, 1, 2], 32, 64),
                   config=("c1: EquivariantEdgewiseLinear [0,1]x32 -> [0,1,2]x64, N=100, E=500 "
                           "random edges (self-loops resampled), gather + layer + scatter-sum, fp32"),
@@ -453,26 +512,52 @@ def build_workload(name: str):
             return loss
 
         def cpu():
+            # the oracle forms the (101, 128, 128, 231) radial table once per step
+            # whatever the edge count: two sample sizes give the table's time a and
+            # the per-edge time b (t = a + b n), and the full step a + b E
             from oracle import layer as OL
-            n = 400
-            Pc = P[:n].float().cpu()
-            r = dist[:n].to(torch.bfloat16).float().cpu()
             params, cfg = OL.module_cfg(layer_cpu)
             params = {k: t.detach().float().requires_grad_(True) for k, t in params.items()}
             cfg["bin_edges"] = cfg["bin_edges"].float()
-            xs = x_cpu[:n].float().requires_grad_(True)
+            meds, spent = {}, 0.0
+            for n in (128, 640):
+                Pc = P[:n].float().cpu()
+                r = dist[:n].to(torch.bfloat16).float().cpu()
+                xs = x_cpu[:n].float().requires_grad_(True)
 
-            def run():
-                y = OL.edgewise_linear(xs, Pc, Pc, r, params, cfg)
-                (y ** 2).sum().backward()
-            med, times = _median_time(run, 1)
-            return {"value": round(n / med, 1),
-                    "sample": f"the first {n} of the {E} edges: fwd + (y**2).sum() + bwd of the "
-                              f"float32 oracle layer on the bf16 values (its (101, 128, 128, 231) "
-                              f"radial table dominates), 1 run after 1 warmup ({sum(times):.1f} s)"}
+                def run():
+                    y = OL.edgewise_linear(xs, Pc, Pc, r, params, cfg)
+                    (y ** 2).sum().backward()
+                meds[n], times = _median_time(run, 1)
+                spent += sum(times)
+            b = (meds[640] - meds[128]) / (640 - 128)
+            a = max(meds[128] - b * 128, 0.0)
+            step_s = a + b * E
+            return {"value": round(E / step_s, 1),
+                    "sample": f"fwd + (y**2).sum() + bwd of the float32 oracle layer on the bf16 "
+                              f"values at 128 and 640 edges (1 run after 1 warmup each, "
+                              f"{spent:.1f} s): {a:.2f} s per step for the (101, 128, 128, 231) "
+                              f"radial table and its gradient, {b * 1e3:.2f} ms per edge; edges/s "
+                              f"of the full step E / (a + b E), E = {E}",
+                    "table_s": round(a, 3), "per_edge_ms": round(b * 1e3, 3)}
 
-        wl.update(step=step, E=E, N=N, equiv=None, cpu=cpu, leaves=[x] + list(layer.parameters()),
+        def equiv():
+            axis, angle = _rotation(dev, 80)
+            D = fe.WignerD(rep).to(dev).rot(axis, angle)
+            R = fe.WignerD(fe.Repr([1])).to(dev).rot(axis, angle, cartesian=True)
+            with torch.no_grad():
+                xf = x.detach()
+                db = dist.to(torch.bfloat16)
+                o1 = torch.einsum("ij,ecj->eci", D, layer(P, P, xf, db).float())
+                (P2,) = fe.WignerDBasis([rep]).to(dev)(vec @ R.T)
+                P2 = P2.to(torch.bfloat16)
+                x2 = torch.einsum("ij,ecj->eci", D, xf.float()).to(torch.bfloat16)
+                o2 = layer(P2, P2, x2, db).float()
+            return equivariance_error(o1, o2)
+
+        wl.update(step=step, E=E, N=N, equiv=equiv, cpu=cpu, leaves=[x] + list(layer.parameters()),
                   work=algorithmic_per_edge(lv, lv, 128, 128),
+                  mfma=highl_mfma_flop_per_edge(128, 6),
                   config=("c5: EquivariantEdgewiseLinear [0..6]x128 -> [0..6]x128, kNN k=32 on 5k "
                           f"nodes in 30^3, E={E}, bf16 edge features, fwd+bwd"),
                   dtype="bf16")
@@ -530,12 +615,17 @@ def run_workload(name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
     NAT.profile_enable(False)
     kern = NAT.profile_summary()
     per_kernel, dom = {}, None
-    for kname, (calls, tot) in sorted(kern.items(), key=lambda kv: -kv[1][1]):
+    mfma = wl.get("mfma", {})
+    for kname, (calls, tot) in sorted(kern.items(), key=lambda kv: -kv[1][1])[:5]:
         avg = tot / calls
         entry = {"launches": calls, "avg_ms": round(avg, 4), "ms_per_step": round(tot / steps, 4)}
         if kname in wl["work"]:
             fl, by = wl["work"][kname]
             entry["hbm_frac_algorithmic"] = round(by * E / (avg * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
+        if kname in mfma:
+            tf = mfma[kname] * E / (avg * 1e-3) / 1e12
+            entry["bf16_mfma_tflops_executed"] = round(tf, 1)
+            entry["bf16_mfma_frac"] = round(tf / PEAK_F16_TFLOPS, 4)
         per_kernel[kname] = entry
         dom = dom or kname
     out = {"workload": name, "config": wl["config"], "edges": E, "nodes": wl["N"],
@@ -548,6 +638,22 @@ def run_workload(name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
            "warmup": warmup, "dominant_kernel": dom,
            "dominant_kernel_hbm_frac": per_kernel.get(dom, {}).get("hbm_frac_algorithmic"),
            "per_kernel": per_kernel}
+    if mfma:
+        # the matrix-core kernels against the bf16 MFMA peak (executed flops) and
+        # the whole step against SURVEY 8(d)'s algorithmic bound
+        frac = {}
+        for kname, fl in mfma.items():
+            if kname in kern:
+                calls, tot = kern[kname]
+                frac[kname] = round(fl * E / (tot / calls * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 4)
+        top = max(frac, key=lambda k: kern[k][1]) if frac else None
+        out["roofline"] = {"bound": "mfma", "kernel": top,
+                           "achieved": None if top is None else
+                           round(mfma[top] * E / (kern[top][1] / kern[top][0] * 1e-3) / 1e12, 1),
+                           "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                           "frac": None if top is None else frac[top],
+                           "frac_per_kernel": frac,
+                           "step_vs_algorithmic_bound": round(C5_BOUND_MS / ms, 4)}
     if wl.get("equiv") is not None:
         out["equivariance_err"] = wl["equiv"]()
     if with_cpu and wl.get("cpu") is not None:
@@ -703,7 +809,16 @@ def main() -> int:
     roofline.update({"traffic": (round(traffic[dom]) if dom in traffic else None),
                      "kernel": dom, "kernel_avg_ms": round(avg_ms, 4),
                      "algorithmic_flop_per_edge": fl, "algorithmic_bytes_per_edge": by,
-                     "edges_per_launch": E, "per_kernel": per_kernel})
+                     "byte_convention": "the reference layer's tensors once per edge (x, gx, y, gy, "
+                                        "P, r), SURVEY 8(d)",
+                     "edges_per_launch": E,
+                     "per_kernel": dict(sorted(per_kernel.items(),
+                                               key=lambda kv: -kv[1]["ms_per_step"])[:8])})
+    if dom in work["_node_rows"]:
+        # the same launch against the bytes the message-passing form must move
+        # (gx as node rows)
+        roofline["frac_gx_node_rows"] = round(work["_node_rows"][dom] * E / (avg_ms * 1e-3) / 1e9
+                                              / PEAK_HBM_GBS, 4)
 
     cpu = None
     if not args.no_cpu:

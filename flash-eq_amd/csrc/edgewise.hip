@@ -491,16 +491,30 @@ namespace {
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[FEQ_MAX_DEVICES] = {};
 
-// Device address of `scratch` on the current device, looked up once per device
-// (the array's host-side name is not a device address).
-int scratch_ptr(void** out) {
+// Device address of `scratch` on the device of stream s (the current device
+// for the null stream), looked up once per device with that device current
+// (the array's host-side name is not a device address; each device holds its
+// own copy at its own address).
+int scratch_ptr(hipStream_t s, void** out) {
     int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= FEQ_MAX_DEVICES)
-        return fail(FEQ_ERR_HIP, "no current HIP device (or device id beyond %d)", FEQ_MAX_DEVICES);
+    if (s) {
+        hipDevice_t d = -1;
+        const hipError_t err = hipStreamGetDevice(s, &d);
+        if (err != hipSuccess) return fail(FEQ_ERR_HIP, "hipStreamGetDevice: %s", hipGetErrorString(err));
+        dev = static_cast<int>(d);
+    } else if (hipGetDevice(&dev) != hipSuccess) {
+        return fail(FEQ_ERR_HIP, "no current HIP device");
+    }
+    if (dev < 0 || dev >= FEQ_MAX_DEVICES)
+        return fail(FEQ_ERR_HIP, "device id %d beyond %d", dev, FEQ_MAX_DEVICES);
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_ptr[dev]) {
+        int cur = -1;
+        if (hipGetDevice(&cur) != hipSuccess) return fail(FEQ_ERR_HIP, "no current HIP device");
+        if (cur != dev && hipSetDevice(dev) != hipSuccess) return fail(FEQ_ERR_HIP, "hipSetDevice(%d)", dev);
         void* p = nullptr;
         const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) (void)hipSetDevice(cur);
         if (err != hipSuccess || !p)
             return fail(FEQ_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(err));
         g_scratch_ptr[dev] = p;
@@ -523,7 +537,7 @@ extern "C" int feq_edgewise_fwd_src_noalloc(const feq_layout* L, const feq_binni
         return fail(FEQ_ERR_UNSUPPORTED, "layout needs %zu bytes of scratch, the static array holds %d",
                     need, FEQ_NOALLOC_SCRATCH_BYTES);
     void* ws = nullptr;
-    if (int rc = scratch_ptr(&ws)) return rc;
+    if (int rc = scratch_ptr(stream_of(stream), &ws)) return rc;
     return feq_edgewise_fwd_src(L, b, rank, E, x, num_src, src, P, Q, dist, C, F, y, ws,
                                 FEQ_NOALLOC_SCRATCH_BYTES, stream);
 }

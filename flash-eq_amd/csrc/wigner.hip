@@ -339,7 +339,10 @@ k_wigner_bwd(WignerArgs A, int epb, const double* __restrict__ plan, const int32
         const double na = nav + eps;
         a0v = a0r / na;
         a1v = a1r / na;
-        thv = acos(fmin(fmax(dzv, -1.0), 1.0));
+        // the reference's clamp to [-1 + eps, 1 - eps] (wigner.py:235), which
+        // binds in float64 (within ~1.4e-4 rad of the poles; in float32 its
+        // bounds round to +-1, as the forward's float32 frame has them)
+        thv = acos(fmin(fmax(dzv, -1.0 + eps), 1.0 - eps));
         const double rho = sqrt(a0v * a0v + a1v * a1v);
         EdgeFrame f;
         f.ident = rho == 0.0;
@@ -407,9 +410,12 @@ k_wigner_bwd(WignerArgs A, int epb, const double* __restrict__ plan, const int32
         gr1 -= dotp * ar1;
     }
     double gd0 = gr1, gd1 = -gr0, gd2 = 0.0;
-    // theta = acos(clamp(d_z, -1, 1)): -1/sqrt(1 - d_z^2), passed through the clamp
+    // theta = acos(clamp(d_z, -1 + eps, 1 - eps)): -1/sqrt(1 - d_z^2) where the
+    // clamp passes d_z, 0 where it binds (torch's clamp gradient), so the
+    // directions along +-e_z get finite gradients, the float64 values of the
+    // reference's formula (its float32 autograd has 0 * -inf = NaN there)
     const double dz = dzv;
-    if (gth != 0.0) gd2 = -gth / sqrt(1.0 - dz * dz);
+    if (gth != 0.0 && dz >= -1.0 + eps && dz <= 1.0 - eps) gd2 = -gth / sqrt(1.0 - dz * dz);
     // d = v / (|v| + eps)
     const int64_t e = e0 + threadIdx.x;
     const double vx = dirs[3 * e], vy = dirs[3 * e + 1], vz = dirs[3 * e + 2];

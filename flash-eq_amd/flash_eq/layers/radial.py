@@ -10,11 +10,16 @@ and initialised in the reference's order so seeded construction matches.
 from __future__ import annotations
 
 import math
+import weakref
 
 import torch
 import torch.nn as nn
 
 from ..utils import get_epsilon, init_linear_weights
+
+
+# SeparableRadialNet -> (bin-edge buffer refs and versions, basis): see _edge_basis
+_BASIS_CACHE: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
 
 
 class RadialBasisFunctions(nn.Module):
@@ -106,14 +111,25 @@ class SeparableRadialNet(nn.Module):
 
     def _edge_basis(self) -> torch.Tensor:
         """The sinusoidal basis at the bin edges, formed from buffers only and
-        kept until a buffer changes (device, storage or in-place version)."""
+        kept until a buffer changes.
+
+        The cache (outside the module's state, so pickling and deepcopy are
+        unaffected) holds weak references to the very buffer objects it was
+        formed from and their in-place versions: a replaced buffer (``.to()``,
+        the float32 copies of a half-precision module run in float32) misses.
+        A basis formed under ``torch.inference_mode()`` is an inference tensor,
+        which autograd cannot save for a later backward: it is never kept."""
         be, fq = self.bin_edges, self.frequencies
-        key = (be.device, be.dtype, be.data_ptr(), be._version, fq.data_ptr(), fq._version)
-        cached = self.__dict__.get("_basis_cache")
-        if cached is not None and cached[0] == key:
-            return cached[1]
+        cached = _BASIS_CACHE.get(self)
+        if cached is not None:
+            rbe, vbe, rfq, vfq, basis = cached
+            if rbe() is be and rfq() is fq and vbe == be._version and vfq == fq._version:
+                return basis
         basis = self._sinusoidal_basis(be)
-        self.__dict__["_basis_cache"] = (key, basis)
+        if basis.is_inference():
+            _BASIS_CACHE.pop(self, None)
+        else:
+            _BASIS_CACHE[self] = (weakref.ref(be), be._version, weakref.ref(fq), fq._version, basis)
         return basis
 
     def _fused_mlp_ok(self, basis: torch.Tensor) -> bool:

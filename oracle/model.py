@@ -77,7 +77,18 @@ def edgewise(params: Dict[str, torch.Tensor], cfg: dict, x, P, Q, r) -> torch.Te
     """EquivariantEdgewiseLinear.forward (linear.py:131-160) with the table of
     ``SeparableRadialNet.forward`` (radial.py:259-275): bmm(x, P) -> block
     mix -> bmm(., Q^T).  ``params``: the radial net's parameters."""
-    F = radial_functions(params, params["bin_edges"], cfg["min"], cfg["max"], cfg["rank"], cfg["wdim"])
+    if cfg.get("radial_fp32"):
+        # the radial network in float32, as the reference's float32 forward runs
+        # it (see oracle/layer.py: edgewise_linear)
+        p32 = {k: v.float() for k, v in params.items()}
+        F = radial_functions(p32, p32["bin_edges"], cfg["min"], cfg["max"], cfg["rank"],
+                             cfg["wdim"]).to(params["channel_patterns"].dtype)
+    else:
+        F = radial_functions(params, params["bin_edges"], cfg["min"], cfg["max"], cfg["rank"], cfg["wdim"])
+    if cfg.get("F_pinned") is not None:
+        # the radial functions' values fixed to given ones (another
+        # implementation's float32 evaluation), their derivative this network's
+        F = cfg["F_pinned"].to(F.dtype) + (F - F.detach())
     T = torch.einsum("koi,bkw->boiw", params["channel_patterns"], F)
     if cfg["log"]:
         b = BD.Binning.log(cfg["num_bins"], cfg["min"], cfg["max"], cfg["sigma"])
@@ -132,15 +143,26 @@ def block(params, cfg: dict, P, Q, x, r, src, dst, num_nodes: int,
     return x + (m * g if g is not None else m)
 
 
-def transformer(params, cfg: dict, coords, x, src, dst, num_nodes: int) -> torch.Tensor:
-    """EquivariantTransformer.forward (transformer.py:389-431)."""
-    vec = coords[src] - coords[dst]
-    r = vec.norm(dim=-1)
-    # (the bases are formed in float64; a float32 evaluation of the composition
-    # rounds them, as the reference's float32 matrix_exp would)
-    m_in = W.basis(cfg["lin"], vec).to(vec.dtype)
-    m_hid = W.basis(cfg["lhid"], vec).to(vec.dtype)
-    m_out = W.basis(cfg["lout"], vec).to(vec.dtype)
+def transformer(params, cfg: dict, coords, x, src, dst, num_nodes: int,
+                edge_inputs: dict = None) -> torch.Tensor:
+    """EquivariantTransformer.forward (transformer.py:389-431).
+
+    ``edge_inputs`` (optional, no coordinate gradient): the distances ``r`` and
+    the bases ``m_in``, ``m_hid``, ``m_out`` given instead of formed from the
+    coordinates (another implementation's float32 values, so that a comparison
+    covers what the blocks compute from them)."""
+    if edge_inputs is not None:
+        dt = x.dtype
+        r = edge_inputs["r"].to(dt)
+        m_in, m_hid, m_out = (edge_inputs[k].to(dt) for k in ("m_in", "m_hid", "m_out"))
+    else:
+        vec = coords[src] - coords[dst]
+        r = vec.norm(dim=-1)
+        # (the bases are formed in float64; a float32 evaluation of the composition
+        # rounds them, as the reference's float32 matrix_exp would)
+        m_in = W.basis(cfg["lin"], vec).to(vec.dtype)
+        m_hid = W.basis(cfg["lhid"], vec).to(vec.dtype)
+        m_out = W.basis(cfg["lout"], vec).to(vec.dtype)
     L = cfg["num_layers"]
     for i in range(L):
         P = m_in if i == 0 else m_hid
@@ -155,10 +177,14 @@ def transformer(params, cfg: dict, coords, x, src, dst, num_nodes: int) -> torch
 # ---- configs from module hyper-parameters --------------------------------------------------
 
 def edgewise_cfg(lin, lout, cin, cout, num_bins=100, min_dist=0.0, max_dist=10.0, log=False,
-                 sigma=0.1, rank=4) -> dict:
+                 sigma=0.1, rank=4, radial_fp32=False) -> dict:
+    """``radial_fp32``: evaluate the radial network in float32 whatever the
+    composition's dtype (linear bins extrapolate beyond max_dist and multiply
+    its rounding by |t|; the reference's float32 forward has exactly that)."""
     from .layout import weight_dim
     return dict(lin=list(lin), lout=list(lout), cin=cin, cout=cout, num_bins=num_bins, min=min_dist,
-                max=max_dist, log=log, sigma=sigma, rank=rank, wdim=weight_dim(lin, lout))
+                max=max_dist, log=log, sigma=sigma, rank=rank, wdim=weight_dim(lin, lout),
+                radial_fp32=radial_fp32)
 
 
 def attention_cfg(lin, lout, mult_in, mult_out, heads, decay=None, eps=1e-8, **ew) -> dict:

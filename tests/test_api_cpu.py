@@ -106,3 +106,30 @@ def test_half_precision_active_inside_half_modules():
         assert half_precision_active(torch.zeros(1))
     with epsilon_dtype(torch.float32):
         assert not half_precision_active(torch.zeros(1))
+
+
+def test_radial_basis_cache_inference_then_training():
+    """A first call under torch.inference_mode() must not leave an inference
+    tensor behind: the training call after it differentiates through the
+    basis (the reference recomputes it every call and has no such failure)."""
+    import pickle
+    net = fe.layers.radial.SeparableRadialNet(num_bins=8, out_mult=4, in_mult=4, weight_dim=3)
+    with torch.inference_mode():
+        F0 = net.radial_functions()
+    F1 = net.radial_functions()
+    F1.sum().backward()
+    assert torch.equal(F0, F1.detach())
+    assert net.trunk[0].weight.grad is not None
+    basis = net._edge_basis()
+    assert net._edge_basis() is basis                    # kept once formed outside inference mode
+    with torch.inference_mode():
+        assert net._edge_basis() is basis                # a normal tensor serves inference calls too
+    pickle.loads(pickle.dumps(net))                      # the cache is not part of the module's state
+    # a float32 copy of the buffers (as a half-precision module run in float32
+    # passes) is a different tensor: it misses instead of matching a stale key
+    copies = {k: v.clone() for k, v in net.named_buffers()}
+    copies["bin_edges"].mul_(0.5)
+    b2 = torch.func.functional_call(net, {**dict(net.named_parameters()), **copies}, ())
+    ref = torch.func.functional_call(net, {**dict(net.named_parameters()), **copies}, ())
+    assert torch.equal(b2, ref)
+    assert not torch.equal(b2, net())

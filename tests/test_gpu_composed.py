@@ -25,8 +25,9 @@ cannot.  bf16 runs use 2e-2 in place of 1e-5, on bf16-rounded inputs.
   (config 3's block) on a kNN graph, fp32 and bf16.
 * ``test_model_config4_*``: the 6-layer EquivariantTransformer in [0,1]x32,
   hidden [0,1,2]x64, out [0]x8, 8 heads (config 4's model) on a random-walk
-  chain, including the coordinate gradient through WignerDBasis, and its first
-  and last blocks alone.
+  chain: as bench.py times it (max_dist 10, no coordinate gradient, the launch
+  log checked), with the coordinate gradient through WignerDBasis, and its
+  first and last blocks alone.
 """
 import os
 
@@ -35,6 +36,7 @@ import pytest
 import torch
 
 import flash_eq as fe
+from flash_eq import _native as NAT
 from helpers import rel_err
 from oracle import model as OM
 from oracle import wigner as OW
@@ -356,11 +358,77 @@ def test_model_config4_shape(dev):
                    {"x": x.detach().double().cpu(), "coords": coords.double()}, w, torch.float32, TOL)
 
 
+def test_model_config4_timed_path(dev):
+    """Config 4's model as bench.py times it: max_dist 10 and coordinates
+    without gradient, so every V projection runs the kernels of the timed step
+    -- the first ([0,1]x32 -> [0,1,2]x64) in the [0,1]x64 -> [0,1,2]x64 split
+    kernels with zero-padded channels, the hidden ones in the split kernels
+    fused with the head weighting and sum pooling, the last ([0,1,2]x64 ->
+    [0]x8) in the scalar-output kernels -- as the launch log confirms.
+
+    17% of these edges lie beyond max_dist, where the linear bins extrapolate
+    (t up to ~200) and multiply any rounding difference in the distances or in
+    the radial functions F at the bin edges by |t|.  Measured on this model:
+    float32 evaluations of the reference's algorithm whose F is PyTorch's
+    float64 network instead of its float32 one differ from each other by ~30% in
+    parameter gradients, and by 1-5% when the coordinates move by 2^-23
+    relative.  So the oracle compositions (the float64 truth and the float32
+    runs of the bound) take the inputs of the blocks from the product -- its
+    float32 distances and bases (WignerDBasis is pinned on its own by the
+    Wigner tests) and F's values (the radial network by
+    test_gpu_radial_mlp.py), F's derivative from their own network -- and the
+    check covers everything the six blocks compute from them at the
+    conditioning-aware bound of this file."""
+    coords, src, dst = _config4_graph()
+    Nn = coords.shape[0]
+    g = torch.Generator().manual_seed(46)
+    torch.manual_seed(4)
+    model = fe.EquivariantTransformer(R([0, 1], 32), R([0, 1, 2], 64), R([0], 8), num_layers=6,
+                                      num_heads=8, max_dist=10.0, layer_scale_init=0.3).to(dev)
+    x = torch.randn(Nn, 32, 4, generator=g).to(dev).requires_grad_(True)
+    xyz = coords.to(dev)
+    graph = fe.Graph(src.to(dev), dst.to(dev), Nn)
+    w = torch.randn(Nn, 8, 1, generator=g)
+    NAT.profile_summary()
+    NAT.profile_enable(True)
+    out = model(xyz, x, graph)
+    got = _product(model, out, w, {"x": x})
+    torch.cuda.synchronize()
+    NAT.profile_enable(False)
+    launched = NAT.profile_summary()
+    print("launches:", {k: v[0] for k, v in sorted(launched.items())})
+    assert "k_ew_fwd" not in launched and "k_ew_bwd" not in launched, launched   # no generic kernels
+    assert launched["k_ews_fwd"][0] == 5 and launched["k_pool_order"][0] == 5
+    assert launched["k_ews_bwd_x"][0] == 5 and launched["k_ews_bwd_c"][0] == 5
+    assert launched["k_scatter_order"][0] == 5 and launched["k_pool_grad_attn"][0] == 5
+    assert launched["k_ew0_fwd"][0] == 1 and launched["k_ew0_bwd"][0] == 1
+    cfg = OM.transformer_cfg([0, 1], [0, 1, 2], [0], 32, 64, 8, num_layers=6, heads=8,
+                             num_bins=100, max_dist=10.0)
+    with torch.no_grad():
+        for i, blk in enumerate(model.layers):
+            cfg["layers"][i]["attn"]["v"]["F_pinned"] = (
+                blk.attn.linear_v.radial_weights.radial_functions().double().cpu())
+        vec = xyz[graph.src] - xyz[graph.dst]                 # as EquivariantTransformer.forward
+        bases = model.basis(vec)
+        edge_inputs = {"r": vec.norm(dim=-1).double().cpu()}
+        edge_inputs.update({k: b.double().cpu() for k, b in zip(("m_in", "m_hid", "m_out"), bases)})
+
+    def fn(p, i):
+        return OM.transformer(p, cfg, None, i["x"], src, dst, Nn, edge_inputs=edge_inputs)
+
+    state = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    inputs_cpu = {"x": x.detach().double().cpu()}
+    truth = _pack(*_oracle(fn, state, inputs_cpu, ("x",), w.double(), torch.float64))
+    f32 = _float32_runs(fn, state, inputs_cpu, ("x",), w.double())
+    _assert_within("config-4 model, timed path", got, truth, f32, TOL)
+
+
 @pytest.mark.parametrize("which", ["first", "last"])
 def test_model_config4_end_blocks_with_coordinate_gradient(dev, which):
     """Config 4's first block ([0,1]x32 -> [0,1,2]x64, P != Q, no attention
     residual) and last block ([0,1,2]x64 -> [0]x8), with the bases built from
-    coordinates that require grad (P and Q carry gradients), max_dist 10."""
+    coordinates that require grad (P and Q carry gradients), max_dist 30 (see
+    C4_MAX_DIST)."""
     coords, src, dst = _config4_graph()
     Nn = coords.shape[0]
     g = torch.Generator().manual_seed(45)

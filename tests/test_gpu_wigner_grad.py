@@ -74,6 +74,33 @@ def test_degenerate_frames_follow_the_reference(dev):
     assert rel < 1e-4, (got, ref)
 
 
+def test_plus_z_directions_take_the_float64_frame(dev):
+    """Directions exactly along +e_z (and -e_z): the gradient kernel evaluates
+    the reference's frame formula (rot_to_ez, wigner.py:198-240) in float64,
+    where its clamp of d_z to [-1 + eps, 1 - eps] binds (d_z = |v| / (|v| +
+    eps) lies within eps of +-1): the angle is arccos(1 - eps) whatever |v|,
+    and no gradient passes the clamp, so every entry is finite.  The
+    reference's own float32 autograd rounds the clamp's bounds to +-1 and
+    returns NaN there (0 * -inf).  This pins the chosen, finite value: the
+    float64 evaluation of the formula."""
+    v = torch.tensor([[0.0, 0.0, 1.0], [0.0, 0.0, 2.5], [0.0, 0.0, 0.25], [0.0, 0.0, -1.0]])
+    lv = [0, 1, 2]
+    vd = v.to(dev).requires_grad_(True)
+    (M,) = fe.WignerDBasis([fe.Repr(lv, 1)]).to(dev)(vd)
+    W = torch.randn(M.shape, generator=torch.Generator().manual_seed(11))
+    (M * W.to(dev)).sum().backward()
+    got = vd.grad.double().cpu()
+    vo = v.double().requires_grad_(True)
+    (OW.basis(lv, vo) * W.double()).sum().backward()
+    assert torch.isfinite(got).all()
+    assert torch.all(got[:, 2] == 0.0)            # d_z itself carries no gradient on the axis
+    rel = ((got - vo.grad).abs() / vo.grad.abs().clamp(min=1.0)).max().item()
+    assert rel < 1e-4, (got, vo.grad)
+    v32 = v.clone().requires_grad_(True)          # the float32 evaluation: NaN, as in the reference
+    (OW.basis(lv, v32) * W).sum().backward()
+    assert torch.isnan(v32.grad).any()
+
+
 def test_zero_edges(dev):
     vd = torch.zeros(0, 3, device=dev, requires_grad=True)
     (M,) = fe.WignerDBasis([fe.Repr([0, 1, 2], 1)]).to(dev)(vd)

@@ -65,3 +65,23 @@ def test_size_queries_need_no_gpu():
     assert lib.feq_csr_workspace(1000, 100) > 0
     lv = (ctypes.c_int32 * 3)(0, 1, 2)
     assert lib.feq_wigner_plan_doubles(lv, 3) == (1 + 2) + (9 + 6) + (25 + 10)
+
+
+def test_noalloc_scratch_covers_every_message_passing_layout():
+    """The allocation-free forward keeps the forward workspace in a static
+    array of FEQ_NOALLOC_SCRATCH_BYTES: every layout with message-passing
+    kernels must fit it, and the workspace query must be the fp16 hi/lo
+    fragments of the rank's channel patterns plus the rank scales (the size
+    the entry point checks against the array before it touches it)."""
+    lib = N.load_library()
+    text = open(HEADER).read()
+    cap = int(eval(re.search(r"#define FEQ_NOALLOC_SCRATCH_BYTES \(([^)]*)\)", text).group(1)))
+    assert cap == 256 * 1024
+    b = N.make_binning(0.0, 10.0, 100, False, 0.1)
+    for lin, lout, cin, cout in [([0, 1, 2], [0, 1, 2], 64, 64), ([0, 1], [0, 1, 2], 64, 64),
+                                 ([0, 1], [0, 1, 2], 32, 64)]:
+        L = N.make_layout(lin, lout, cin, cout)
+        need = lib.feq_edgewise_fwd_workspace(ctypes.byref(L), ctypes.byref(b), 4, 160000)
+        frag = 4 * cout * cin * 2 * 2                  # rank x Cout x Cin, hi + lo halves
+        assert need == -(-frag // 256) * 256 + 256 + 256, (lin, lout, cin, cout, need)
+        assert need <= cap
