@@ -118,20 +118,23 @@ def executed_mfma_flop_per_edge(lin, lout, cin, cout, rank=4):
 def highl_mfma_flop_per_edge(C: int = 128, L: int = 6, rank: int = 4) -> dict:
     """bf16 matrix-core flops the high-degree kernels (csrc/edgewise_hl.hip)
     execute per edge, counted from their tile loops (one 16x16x32 MFMA =
-    16 384 flop, one 16x16x16 = 8 192): the rotations take (C x D) x (D x D)
-    per edge with D padded to 16-column blocks and 32-steps (rot_out twice, for
-    the hi and lo parts); the mixes and the per-edge radial-function gradient
-    one G_k = C_k fs per slot, rank and 16-row block, 32-steps over the channels,
-    per 16-edge tile; the channel-pattern gradient one product per 32-step of
-    two slots x 16 edges, column block and rank."""
+    16 384 flop): the input rotation takes (C x D) x (D x D) per edge with D
+    padded to 16-column blocks and 32-steps; the mixes (k_hl_mixr) per 16
+    channels, with the D slots in NB = 4 blocks of 16 rows, stage 1 NB x rank x
+    C/32 products, stage 2 NB x rank/2 and the output rotation ceil(D/16) x NB;
+    the per-edge radial-function gradient (k_hl_dfer) per rank and 64
+    channels NB x 4 x C/32 stage-1 and NB x 4 stage-2 products; the
+    channel-pattern gradient one product per 32-step of two slots x 16 edges,
+    column block and rank."""
     D = (L + 1) ** 2
     f32 = 16 * 16 * 32 * 2
+    nb, ndb = 4, -(-D // 16)
     rot = (C // 16) * -(-D // 16) * -(-D // 32) * f32
-    mix = D * rank * (C // 32) * (C // 16) * f32 / 16
+    mixr = (C // 16) * (nb * rank * (C // 32) + nb * rank // 2 + ndb * nb) * f32
+    dfe = rank * (C // 64) * (nb * 4 * (C // 32) + nb * 4) * f32
     steps = sum(-(-((2 if m else 1) * (L - m + 1)) // 2) for m in range(L + 1))
     dc = steps * (C // 16) * rank * (C // 16) * f32 / 16
-    return {"k_hl_rot_in": rot, "k_hl_rot_out": 2 * rot, "k_hl_mix": mix, "k_hl_mix_t": mix,
-            "k_hl_dfe": mix, "k_hl_dc": dc}
+    return {"k_hl_rot_in": rot, "k_hl_mix": mixr, "k_hl_mix_t": mixr, "k_hl_dfe": dfe, "k_hl_dc": dc}
 
 
 # SURVEY 8(d): config 5's algorithmic work, 54.7 MFLOP per edge fwd + bwd, bounds

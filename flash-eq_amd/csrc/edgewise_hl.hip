@@ -12,12 +12,12 @@
 //   k_hl_rot_in   fs^T[e, j, c] = s^l(j) sum_d x[e, c, d] P[e, d, j]  (bf16, slot-major),
 //                 one (C x D) x (D x D) bf16 MFMA product per edge; the same
 //                 kernel forms gd^T = s^l (gy Q) in the backward;
-//   k_hl_mix      per 16-edge tile and m-group, G_k = C_k fs on MFMA (bf16 in,
-//                 fp32 out) and the contraction with F_e in registers, one
-//                 source slot at a time: ym[e, o, co] (fp32, slot-major); with
-//                 C_k^T and the transposed terms it forms dfs^T from gd^T;
-//   k_hl_rot_out  y[e, c, d] = sum_j Q[e, d, j] s^l(j) ym[e, j, c] (and dx from dfs),
-//                 per edge on MFMA with ym split into bf16 hi and lo parts;
+//   k_hl_mix      per edge, G_k^T = fs^T C_k^T, the contraction with F_e and
+//                 the rotation back y = (s^l ym) Q^T as three chained bf16
+//                 MFMA products (each product's accumulators are the next
+//                 one's B operand, split into hi and lo bf16 halves where the
+//                 precision needs it; below at k_hl_mixr); with C_k^T, M_ek^T
+//                 and P it forms dx from gd^T (k_hl_mix_t);
 //   k_hl_dfe      dF_e[k, w] = sum over the terms (o, i, w) of sign <gd_o, C_k fs_i>,
 //                 G_k recomputed on MFMA, the sums over the 128 rows taken with
 //                 lane swaps (lane rows) and a per-wave LDS buffer (waves);
@@ -245,128 +245,6 @@ k_hl_rot_in(int64_t E, const __bf16* __restrict__ in, const __bf16* __restrict__
 //     aligned), dword reads shifted by v_alignbyte;
 //   D: lane holds slot d of four channels, staged in LDS as the output's
 //     [c][d] rows and written with 16-byte stores.
-template <int L, int C>
-__global__ void __launch_bounds__(kT, 2)
-k_hl_rot_out(int64_t E, const float* __restrict__ in, const __bf16* __restrict__ R,
-             const float* __restrict__ dist, float sigma, __bf16* __restrict__ out) {
-    using RI = RotIn<L, C>;
-    constexpr int D = RI::D, ROW = RI::ROW, NCB = RI::NCB, NDB = RI::NJB, KS = RI::KS;
-    constexpr int REG = (2 * ROW + 15) / 16 * 16, NQ = (ROW / 8 + 63) / 64;
-    static_assert(C % 16 == 0 && (2 * ROW) % 16 == 0, "tile shapes");
-    __shared__ uint4 smem[4 * REG / 16];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int le = lane & 15, lg = lane >> 4;
-    char* reg = reinterpret_cast<char*>(smem) + wave * REG;
-    __bf16* stage = reinterpret_cast<__bf16*>(reg);
-    int lj[KS][8];
-#pragma unroll
-    for (int s = 0; s < KS; ++s)
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const int j = 32 * s + 8 * lg + t;
-            lj[s][t] = j < D ? SlotL<L>::l[j] : 0;
-        }
-    const uint32_t* Rw = reinterpret_cast<const uint32_t*>(R);
-    const int64_t w0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * RI::EPW;
-#pragma unroll 1
-    for (int i = 0; i < RI::EPW; ++i) {
-        const int64_t e = w0 + i;
-        if (e >= E) break;
-        // B fragments: basis row d, elements j0 .. j0 + 7 (zero past D); only
-        // the dwords that hold needed elements are read
-        bf8 b[NDB][KS];
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-            for (int s = 0; s < KS; ++s) {
-                const int d = 16 * db + le, j0 = 32 * s + 8 * lg;
-                // dword k is read when it holds an element j0 .. min(j0 + 8, D) - 1
-                // of a real row, at a clamped index otherwise (no branch)
-                const bool row = d < D && j0 < D;
-                const int64_t f0 = (e * D + (row ? d : 0)) * D + (row ? j0 : 0);
-                const int odd = static_cast<int>(f0 & 1);
-                const int nv = !row ? 0 : (D - j0 < 8 ? D - j0 : 8);
-                uint32_t wv[5];
-#pragma unroll
-                for (int k = 0; k < 5; ++k) {
-                    const bool need = 2 * k <= odd + nv - 1;
-                    const uint32_t u = Rw[need ? (f0 >> 1) + k : (f0 >> 1)];
-                    wv[k] = need ? u : 0u;
-                }
-                uint32_t o[4];
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    o[k] = __builtin_amdgcn_alignbyte(wv[k + 1], wv[k], static_cast<uint32_t>(2 * odd));
-                    o[k] &= (2 * k < nv ? 0x0000ffffu : 0u) | (2 * k + 1 < nv ? 0xffff0000u : 0u);
-                }
-                b[db][s] = __builtin_bit_cast(bf8, (u32x4{o[0], o[1], o[2], o[3]}));
-            }
-        const float r = dist[e];
-        const float sv = r / (r + sigma);
-        const float s2 = sv * sv, s4 = s2 * s2;
-        float pw[KS][8];
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-#pragma unroll
-            for (int t = 0; t < 8; ++t) pw[s][t] = pow_sel(sv, s2, s4, lj[s][t]);
-        // A operand values: channel c of slots j (clamped into the row; the
-        // slots past D are masked to zero bits below, so no branch holds a
-        // load back), double-buffered one channel block ahead
-        const float* ie = in + e * D * C;
-        float raw[2][KS][8];
-        auto load_a = [&](int cb, float (&dst)[KS][8]) {
-#pragma unroll
-            for (int s = 0; s < KS; ++s)
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const int j = 32 * s + 8 * lg + t;
-                    dst[s][t] = ie[(j < D ? j : D - 1) * C + 16 * cb + le];
-                }
-        };
-        load_a(0, raw[0]);
-#pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) {
-            if (cb + 1 < NCB) load_a(cb + 1, raw[(cb + 1) & 1]);
-            bf8 ah[KS], al[KS];
-#pragma unroll
-            for (int s = 0; s < KS; ++s) {
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const int j = 32 * s + 8 * lg + t;
-                    float u = raw[cb & 1][s][t];
-                    if (32 * s + 32 > D) u = __uint_as_float(__float_as_uint(u) & (j < D ? ~0u : 0u));
-                    const float v = u * pw[s][t];
-                    const __bf16 h = static_cast<__bf16>(v);
-                    ah[s][t] = h;
-                    al[s][t] = static_cast<__bf16>(v - static_cast<float>(h));
-                }
-            }
-#pragma unroll
-            for (int db = 0; db < NDB; ++db) {
-                v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int s = 0; s < KS; ++s) {
-                    acc = mfma_bf(ah[s], b[db][s], acc);
-                    acc = mfma_bf(al[s], b[db][s], acc);
-                }
-                const int d = 16 * db + le;
-                if (d < D) {
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) stage[(16 * cb + 4 * lg + q) * D + d] = static_cast<__bf16>(acc[q]);
-                }
-            }
-        }
-        asm volatile("" ::: "memory");
-        uint4* dst = reinterpret_cast<uint4*>(out + e * ROW);
-#pragma unroll
-        for (int n = 0; n < NQ; ++n) {
-            const int q = lane + 64 * n;
-            if (q < ROW / 8) dst[q] = reinterpret_cast<const uint4*>(reg)[q];
-        }
-        asm volatile("" ::: "memory");
-    }
-}
-
 // ---- constant GEMM operand --------------------------------------------------------
 // bf16 A-operand fragments of C_k (TRANS = false: rows co, reduction ci) or C_k^T
 // (rows ci, reduction co); C is (K, Cout, Cin).  Fragment (k, rb, ks) of lane l
@@ -416,125 +294,381 @@ __device__ __forceinline__ void fill_tile_F(const feq_binning& B, int64_t E, int
     __syncthreads();
 }
 
-// ---- the mix on the matrix cores -----------------------------------------------------
-// Forward (TRANS = false): src = fs^T (E, D, NRED = Cin) bf16, A = C_k,
-//   dst[e, o, co] = sum_k (M_ek G_k[co, (e, .)])[o],  G_k = C_k fs;
-// input gradient (TRANS = true): src = gd^T (E, D, NRED = Cout), A = C_k^T,
-//   dst[e, i, ci] = sum_k (M_ek^T H_k[ci, (e, .)])[i], H_k = C_k^T gd.
-// M_ek is applied block by block: in m-block m (n = L - m + 1 degrees) with
-// weights a = F_e[k, w], b = F_e[k, w + 1], w = w_off(m) + 2 (o n + i),
-//   forward:  y_re(o) += a G_re(i) + b G_im(i),   y_im(o) += a G_im(i) - b G_re(i)
-//   gradient: g_re(i) += a H_re(o) - b H_im(o),   g_im(i) += b H_re(o) + a H_im(o)
-// (block_diagonal.cu:483-503), and y(o) += F_e[k, o n + i] G(i) in m-block 0.
-// A workgroup of NROW / 16 waves owns a 16-edge tile at a time (lane l serves
-// edge l % 16, the B column); wave w owns the output rows 16 w .. 16 w + 15 and
-// holds the A fragments of every rank for them.  The m-groups are unrolled;
-// the source units of a group (single slots for m = 0, (+m, -m) pairs above)
-// run as a loop, whose bounds keep each unit's products, weights and
-// accumulator updates together (fully unrolled, the compiler interleaves the
-// units and spills).  The group's accumulators live in registers until its
-// end, then go out as 16-byte stores; each unit's B fragments are loaded
-// while the previous unit is contracted.
-template <int L, int NROW, int NRED, int K, bool TRANS>
-__global__ void __launch_bounds__(NROW * 4, 1)
-k_hl_mix(feq_binning B, int64_t E, int64_t ntiles, const __bf16* __restrict__ src,
-         const float* __restrict__ dist, const float* __restrict__ F,
-         const bf8* __restrict__ frag, float* __restrict__ dst) {
-    using H = HL<L>;
-    constexpr int D = H::D, WD = H::WD, KW = K * WD;
-    constexpr int NKS = NRED / 32, NRB = NROW / 16, NT = NROW * 4;
-    static_assert(NROW % 16 == 0 && NRED % 32 == 0 && NT <= 1024, "channel counts");
-    __shared__ float sF[KW * kNE];
-    __shared__ int slo[kNE];
-    __shared__ float st[kNE];
+// ---- the mix and the output rotation as chained matrix-core products ---------------
+// The per-edge contraction with the radial functions (~13k VALU cycles per edge
+// at C = 128 when done in registers) runs on the matrix cores, fed straight
+// from the accumulators of the product before it:
+//   stage 1  G^T[j, c] = sum_ci fs^T[j, ci] C_k^T[ci, c]   (16 slot rows x 16 channels
+//            per v_mfma_f32_16x16x32_bf16; A: the edge's staged slot rows, B: the
+//            C_k fragments of k_hl_prep held for the launch)
+//   stage 2  ym^T[o, c] = sum_k sum_i M_ek[o, i] G_k^T[i, c]
+//   stage 3  out[c, d] = sum_j R[d, j] s^l(j) ym[j, c]
+// The accumulator layout of a 16 x 16 product (lane l holds rows 4 (l / 16) + r
+// of column l % 16) is exactly the B-operand layout of the next product's
+// reduction over those rows, so stages 2 and 3 take their B operands from the
+// previous accumulators: stage 2 G rounded to bf16, two ranks per 32-step;
+// stage 3 s^l ym split into bf16 hi and lo halves that share one 32-step (its
+// A operand repeats its four values).  (G split into hi and lo as well measured
+// 3.57 against 3.13 ms per forward at config 5 and moved the output's error
+// against float64 from 5.2e-3 to 4.4e-3 of its largest entry, with a 2e-2
+// bar.)  The slots are grouped into 16-row blocks that each hold whole m-groups
+// (HLB), so M_ek -- block diagonal over m -- has only diagonal block tiles.  The
+// A operands of stages 2 and 3 (the interpolated radial functions with the
+// m-block signs, and the basis gathered at the block's slots) are built once
+// per edge in LDS and read by every wave.  A workgroup of C / 16 waves takes
+// one edge at a time (wave w owns the channels 16 w .. 16 w + 15).
+// TRANS = false: fs^T -> y with C_k and Q (forward); TRANS = true: gd^T -> dx
+// with C_k^T, M_ek^T and P (input gradient).
+template <int L>
+struct HLB {
+    static constexpr int D = (L + 1) * (L + 1), NG = L + 1, MAXB = 8;
+    struct Plan {
+        int nb;
+        int slot[MAXB][16];           // m-first slot of row r of block b, -1 for padding
+        int deg[MAXB][16];            // its degree (0 for padding)
+        short coef[MAXB][16][16];     // 2 w + neg of M_e[o row, i row] (-1: zero)
+    };
+    static constexpr Plan make() {
+        Plan p{};
+        for (int b = 0; b < MAXB; ++b)
+            for (int r = 0; r < 16; ++r) {
+                p.slot[b][r] = -1;
+                p.deg[b][r] = 0;
+                for (int c = 0; c < 16; ++c) p.coef[b][r][c] = -1;
+            }
+        int order[NG] = {}, size[NG] = {};
+        for (int m = 0; m < NG; ++m) {
+            order[m] = m;
+            size[m] = (m ? 2 : 1) * (L - m + 1);
+        }
+        for (int a = 0; a < NG; ++a)                 // by size, largest first (stable)
+            for (int c = a + 1; c < NG; ++c)
+                if (size[order[c]] > size[order[a]]) {
+                    const int t = order[a];
+                    order[a] = order[c];
+                    order[c] = t;
+                }
+        int fill[MAXB] = {}, blk[D] = {}, row[D] = {};
+        p.nb = 0;
+        for (int q = 0; q < NG; ++q) {               // first fit
+            const int m = order[q];
+            int b = 0;
+            while (b < p.nb && fill[b] + size[m] > 16) ++b;
+            if (b == p.nb) ++p.nb;
+            for (int u = 0; u < size[m]; ++u) {
+                const int s = Canon<L, L>::in_off(m) + u;
+                p.slot[b][fill[b]] = s;
+                p.deg[b][fill[b]] = SlotL<L>::l[s];
+                blk[s] = b;
+                row[s] = fill[b]++;
+            }
+        }
+        for (int t = 0; t < Canon<L, L>::NT; ++t) {
+            const Term tm = Canon<L, L>::terms[t];
+            p.coef[blk[tm.o]][row[tm.o]][row[tm.i]] = static_cast<short>(2 * tm.w + tm.neg);
+        }
+        return p;
+    }
+    static constexpr Plan P = make();
+    static constexpr int NB = P.nb;
+};
+
+__device__ __forceinline__ void split_bf(float v, __bf16& h, __bf16& l) {
+    h = static_cast<__bf16>(v);
+    l = static_cast<__bf16>(v - static_cast<float>(h));
+}
+
+template <int L, int C, int K, bool TRANS>
+__global__ void __launch_bounds__(4 * C, 1)
+k_hl_mixr(feq_binning B, int64_t E, const __bf16* __restrict__ src, const float* __restrict__ dist,
+          const float* __restrict__ F, const bf8* __restrict__ frag, const __bf16* __restrict__ R,
+          __bf16* __restrict__ out) {
+    using HB = HLB<L>;
+    constexpr int D = HB::D, NB = HB::NB, WD = HL<L>::WD, KW = K * WD;
+    constexpr int NT = 4 * C, NW = C / 16, NKS = C / 32, NDB = (D + 15) / 16;
+    constexpr int RS = 2 * C + 16;                              // LDS row stride in bytes (odd 16-byte units)
+    constexpr int NQ = (D * C / 8 + NT - 1) / NT;               // 16-byte row chunks per thread
+    constexpr int NF = (KW + NT - 1) / NT;                      // radial functions per thread
+    constexpr int NRF = NDB * NB * 64, NCF = NB * K * 64;        // fragments per edge
+    constexpr int NRI = (NRF + NT - 1) / NT;                    // basis fragments per thread
+    constexpr int NCI = (NCF + NT - 1) / NT;                    // coefficient fragments per thread
+    static_assert(C % 32 == 0 && NB <= HB::MAXB && D <= 16 * NDB, "shapes");
+    __shared__ __align__(16) char sRows[2][(D + 1) * RS];   // + a zero row for padding
+    __shared__ float sPow[2][8];                             // s^l, l <= 7
+    __shared__ __align__(16) float sFe[2][KW];
+    __shared__ __align__(16) u32x4 sCo[2][NCF];   // A fragments, four values repeated
+    __shared__ __align__(16) u32x4 sR[2][NRF];
+    __shared__ __align__(16) __bf16 sOut[NW][16 * D];
+
     const int tid = threadIdx.x, lane = tid & 63, le = lane & 15, lg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    bf8 A[K][NKS];
+
+    // the rank fragments of this wave's 16 channels, for the launch
+    bf8 Bk[K][NKS];
 #pragma unroll
     for (int k = 0; k < K; ++k)
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) A[k][ks] = frag[((k * NRB + wave) * NKS + ks) * 64 + lane];
+        for (int ks = 0; ks < NKS; ++ks) Bk[k][ks] = frag[((k * NW + wave) * NKS + ks) * 64 + lane];
+    // per-lane rows of every block: the stage-1 A row (slot of row le) and the
+    // degrees of the accumulator rows 4 lg + r
+    // (padding rows read the zero row D; every per-lane choice below is an
+    // address or a mask, never a condition, so that the compiler keeps no
+    // launch-long lane masks in scalar registers)
+    int arow[NB], adeg[NB][4];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int sl = HB::P.slot[b][le];
+        arow[b] = (sl >= 0 ? sl : D) * RS;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) adeg[b][r] = HB::P.deg[b][4 * lg + r];
+    }
+    // Table lookups of this thread's fragment items, once per launch, as 16-bit
+    // fields two per register: the basis element offsets d D + j (0 where the
+    // entry is zero, cleared by rmask), and for the coefficients the element k
+    // WD + w of the radial functions (bits 0-13), its sign (bit 14) and
+    // whether it is non-zero (bit 15)
+    static_assert(D * D < 0x10000 && KW < 0x4000, "16-bit table fields");
+    unsigned roff[NRI][2], rmask[NRI][2], ccode[NCI][2];
+#pragma unroll
+    for (int n = 0; n < NRI; ++n) {
+        const int q = tid + NT * n;
+        const int fl = q & 63, b = (q >> 6) % NB, db = (q >> 6) / NB;
+        const int d = 16 * db + (fl & 15);
+        unsigned v[4], m[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int j = q < NRF ? HB::P.slot[b][4 * (fl >> 4) + t] : -1;
+            const bool ok = d < D && j >= 0;
+            v[t] = ok ? static_cast<unsigned>(d * D + j) : 0u;
+            m[t] = ok ? 0xffffu : 0u;
+        }
+        roff[n][0] = v[0] | (v[1] << 16);
+        roff[n][1] = v[2] | (v[3] << 16);
+        rmask[n][0] = m[0] | (m[1] << 16);
+        rmask[n][1] = m[2] | (m[3] << 16);
+    }
+#pragma unroll
+    for (int n = 0; n < NCI; ++n) {
+        const int q = tid + NT * n;
+        const int fl = q & 63, k = (q >> 6) % K, b = (q >> 6) / K;
+        unsigned v[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int c = q >= NCF ? -1
+                          : TRANS ? HB::P.coef[b][4 * (fl >> 4) + t][fl & 15]
+                                  : HB::P.coef[b][fl & 15][4 * (fl >> 4) + t];
+            v[t] = c < 0 ? 0u : static_cast<unsigned>(k * WD + (c >> 1)) | ((c & 1u) << 14) | 0x8000u;
+        }
+        ccode[n][0] = v[0] | (v[1] << 16);
+        ccode[n][1] = v[2] | (v[3] << 16);
+    }
+    auto field = [](const unsigned (&w)[2], int t) -> unsigned { return (w[t >> 1] >> (16 * (t & 1))) & 0xffffu; };
 
-    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        const int64_t e0 = tile * kNE;
-        __syncthreads();   // the previous tile's readers of sF are done
-        fill_tile_F<KW, NT>(B, E, e0, dist, F, sF, slo, st);
-        const bool ok = e0 + le < E;
-        const int64_t ec = ok ? e0 + le : E - 1;
-        const __bf16* srow = src + ec * D * NRED + 8 * lg;
-        float* drow = dst + ec * D * NROW + 16 * wave + 4 * lg;
-        const float* fl = sF + le;
-        bf8 b[2][NKS];                           // the unit's slots x k-steps
-        auto load = [&](int s0, int w) __attribute__((always_inline)) {
+    // Edge i of this workgroup is e_i = blockIdx.x + i gridDim.x.  Iteration i
+    // computes e_i from LDS buffers i % 2 and, around that, prepares the
+    // edges after it: it writes the slot rows and basis fragments of e_{i+1}
+    // and the interpolated radial functions of e_{i+2} (loaded into
+    // registers during iteration i - 1), builds the coefficient fragments of
+    // e_{i+1} from the radial functions written during iteration i - 1, and
+    // issues the loads of e_{i+2}'s rows and basis and of e_{i+3}'s radial
+    // functions (whose bin needs e_{i+3}'s distance, loaded one iteration
+    // earlier still).  One barrier per edge; the waves of a SIMD overlap one
+    // edge's products with another's preparation.  Every load is unconditional
+    // (indices clamped; what is loaded for edges past the last is not used).
+    const int64_t stride = gridDim.x;
+    auto edge = [&](int64_t i) -> int64_t {
+        const int64_t e = blockIdx.x + i * stride;
+        return e < E ? e : E - 1;
+    };
+    u32x4 pq[NQ];
+    unsigned short pr[NRI][4];
+    float pflo[NF], pfhi[NF], pt = 0.0f;
+    auto load_rows = [&](int64_t e) {
+        const u32x4* s4 = reinterpret_cast<const u32x4*>(src + e * D * C);
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                if (j < w)
+        for (int n = 0; n < NQ; ++n) {
+            const int q = tid + NT * n;
+            pq[n] = s4[q < D * C / 8 ? q : 0];
+        }
+        const unsigned short* Rb = reinterpret_cast<const unsigned short*>(R + e * D * D);
 #pragma unroll
-                    for (int ks = 0; ks < NKS; ++ks)
-                        b[j][ks] = *reinterpret_cast<const bf8*>(srow + (s0 + j) * NRED + 32 * ks);
-        };
-        load(0, 1);
-        float acc[H::GMAX][4];
-        static_for<H::NG>([&](auto MM) __attribute__((always_inline)) {
-            constexpr int m = decltype(MM)::value, n = L - m + 1, wdt = m ? 2 : 1;
-            constexpr int s0 = H::goff(m), ns = H::gsize(m), wo = Canon<L, L>::w_off(m);
+        for (int n = 0; n < NRI; ++n)
 #pragma unroll
-            for (int d = 0; d < ns; ++d)
+            for (int t = 0; t < 4; ++t) pr[n][t] = Rb[field(roff[n], t)];
+    };
+    auto load_radial = [&](float rd) {   // the two bin rows of an edge at distance rd
+        const EdgeBin eb = edge_bin(rd, B);
+        pt = eb.t;
+        const float* flo = F + static_cast<int64_t>(eb.lo) * KW;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc[d][r] = 0.0f;
-#pragma unroll 1
-            for (int p = 0; p < n; ++p) {
-                v4f G[2][K];
+        for (int n = 0; n < NF; ++n) {
+            const int q = tid + NT * n < KW ? tid + NT * n : 0;
+            pflo[n] = flo[q];
+            pfhi[n] = flo[q + KW];
+        }
+    };
+    auto write_rows = [&](int buf) {
 #pragma unroll
-                for (int j = 0; j < wdt; ++j)
+        for (int n = 0; n < NQ; ++n) {
+            const int q = tid + NT * n;
+            if ((D * C / 8) % NT == 0 || q < D * C / 8)
+                *reinterpret_cast<u32x4*>(sRows[buf] + (q / (C / 8)) * RS + (q % (C / 8)) * 16) = pq[n];
+        }
 #pragma unroll
-                    for (int k = 0; k < K; ++k) {
-                        v4f g = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int n = 0; n < NRI; ++n) {
+            const int q = tid + NT * n;
+            const unsigned lo = (pr[n][0] | (static_cast<unsigned>(pr[n][1]) << 16)) & rmask[n][0];
+            const unsigned hi = (pr[n][2] | (static_cast<unsigned>(pr[n][3]) << 16)) & rmask[n][1];
+            if (NRF % NT == 0 || q < NRF) sR[buf][q] = u32x4{lo, hi, lo, hi};
+        }
+    };
+    auto write_radial = [&](int buf) {
 #pragma unroll
-                        for (int ks = 0; ks < NKS; ++ks) g = mfma_bf(A[k][ks], b[j][ks], g);
-                        G[j][k] = g;
-                    }
-                // the unit's B fragments are consumed: the next unit's (or the
-                // next group's first) loads fly during this unit's contraction
-                if (p + 1 < n) {
-                    load(s0 + wdt * (p + 1), wdt);
-                } else if constexpr (m + 1 < H::NG) {
-                    load(H::goff(m + 1), 2);
+        for (int n = 0; n < NF; ++n) {
+            const int q = tid + NT * n;
+            if (KW % NT == 0 || q < KW) sFe[buf][q] = lerp_bins(pflo[n], pfhi[n], pt);
+        }
+    };
+    // stage-2 A fragments: M_ek (rows o = le, columns i = 4 lg + t) or M_ek^T
+    auto build_coef = [&](int buf) {
+#pragma unroll
+        for (int n = 0; n < NCI; ++n) {
+            const int q = tid + NT * n;
+            if (NCF % NT == 0 || q < NCF) {
+                unsigned v[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const unsigned code = field(ccode[n], t);
+                    unsigned u = __float_as_uint(sFe[buf][code & 0x3fffu]);
+                    u = (u ^ ((code & 0x4000u) << 17)) & (0u - (code >> 15));
+                    v[t] = __builtin_bit_cast(unsigned short, static_cast<__bf16>(__uint_as_float(u)));
                 }
-#pragma unroll
-                for (int q = 0; q < n; ++q) {
-#pragma unroll
-                    for (int k = 0; k < K; ++k) {
-                        if constexpr (m == 0) {
-                            const int w = TRANS ? wo + p * n + q : wo + q * n + p;
-                            const float f = fl[(k * WD + w) * kNE];
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) acc[q][r] += f * G[0][k][r];
-                        } else {
-                            const int w = TRANS ? wo + 2 * (p * n + q) : wo + 2 * (q * n + p);
-                            const float fa = fl[(k * WD + w) * kNE], fb = fl[(k * WD + w + 1) * kNE];
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) {
-                                const float gre = G[0][k][r], gim = G[1][k][r];
-                                if constexpr (!TRANS) {
-                                    acc[2 * q][r] += fa * gre + fb * gim;
-                                    acc[2 * q + 1][r] += fa * gim - fb * gre;
-                                } else {
-                                    acc[2 * q][r] += fa * gre - fb * gim;
-                                    acc[2 * q + 1][r] += fb * gre + fa * gim;
-                                }
-                            }
-                        }
-                    }
-                }
+                const unsigned lo = v[0] | (v[1] << 16), hi = v[2] | (v[3] << 16);
+                sCo[buf][q] = u32x4{lo, hi, lo, hi};
             }
-            if (ok) {
+        }
+    };
+    auto s_of = [&](float rd) { return rd / (rd + B.sh_scale); };
+
+    // prologue: e_0's rows, basis, radial functions and coefficients, e_1's
+    // radial functions in LDS; e_1's rows and basis and e_2's bin rows in
+    // registers; the distances of e_2 and e_3 known
+    float d0 = dist[edge(0)], d1 = dist[edge(1)];
+    float s_cur = s_of(d0), s_n1 = s_of(d1);
+    load_rows(edge(0));
+    load_radial(d0);
+    for (int q = tid; q < 2 * (RS / 16); q += NT)   // the zero rows
+        *reinterpret_cast<u32x4*>(sRows[q / (RS / 16)] + D * RS + (q % (RS / 16)) * 16) = u32x4{0u, 0u, 0u, 0u};
+    if (tid < 8) sPow[0][tid] = ipowf_small(s_cur, tid);
+    write_rows(0);
+    write_radial(0);
+    load_radial(d1);
+    write_radial(1);
+    __syncthreads();
+    build_coef(0);
+    float d2 = dist[edge(2)];
+    float s_n2 = s_of(d2);
+    float dq = dist[edge(3)];
+    load_rows(edge(1));
+    load_radial(d2);
+
+    // two iterations per trip, so that the buffer of each is a compile-time
+    // constant (LDS addresses then fold into instruction offsets)
+    auto iteration = [&](int64_t i, auto CB) __attribute__((always_inline)) {
+        const int64_t e = blockIdx.x + i * stride;
+        constexpr int cb = decltype(CB)::value, nb = cb ^ 1;
+        __syncthreads();
+        write_rows(nb);               // e_{i+1}
+        write_radial(cb);             // e_{i+2}
+        build_coef(nb);               // e_{i+1}, from its radial functions written last iteration
+        if (tid < 8) sPow[nb][tid] = ipowf_small(s_n1, tid);
+        s_cur = s_n1;
+        s_n1 = s_n2;
+        s_n2 = s_of(dq);
+        load_rows(edge(i + 2));
+        load_radial(dq);              // e_{i+3}
+        dq = dist[edge(i + 4)];
+
+        // stages 1 and 2 over the blocks, software-pipelined: the next block's
+        // stage-1 products are issued before this block's splits and stage-2
+        // products, which wait on the previous accumulators
+        const char* rows = sRows[cb];
+        const u32x4* coef = sCo[cb];
+        const u32x4* rfr = sR[cb];
+        bf8 ym[NB];   // s^l ym rows 4 lg + r of each block: hi in [0, 4), lo in [4, 8)
+        v4f gacc[2][K];
+        auto stage1 = [&](int b, v4f (&g)[K]) __attribute__((always_inline)) {
+            bf8 a[NKS];
 #pragma unroll
-                for (int d = 0; d < ns; ++d)
-                    *reinterpret_cast<float4*>(drow + (s0 + d) * NROW) =
-                        make_float4(acc[d][0], acc[d][1], acc[d][2], acc[d][3]);
+            for (int ks = 0; ks < NKS; ++ks)
+                a[ks] = *reinterpret_cast<const bf8*>(rows + arow[b] + (32 * ks + 8 * lg) * 2);
+#pragma unroll
+            for (int k = 0; k < K; ++k) g[k] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+                for (int k = 0; k < K; ++k) g[k] = mfma_bf(a[ks], Bk[k][ks], g[k]);
+        };
+        const float* pw = sPow[cb];
+        stage1(0, gacc[0]);
+        static_for<NB>([&](auto BB) __attribute__((always_inline)) {
+            constexpr int b = decltype(BB)::value, cur = b & 1;
+            if constexpr (b + 1 < NB) stage1(b + 1, gacc[cur ^ 1]);
+            v4f y = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            // G rounded to bf16, two ranks per 32-step
+#pragma unroll
+            for (int k = 0; k < K; k += 2) {
+                bf8 gb;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    gb[r] = static_cast<__bf16>(gacc[cur][k][r]);
+                    gb[4 + r] = static_cast<__bf16>(gacc[cur][k + 1][r]);
+                }
+                const u32x4 c0 = coef[(b * K + k) * 64 + lane], c1 = coef[(b * K + k + 1) * 64 + lane];
+                y = mfma_bf(__builtin_bit_cast(bf8, (u32x4{c0.x, c0.y, c1.x, c1.y})), gb, y);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                __bf16 h, l;
+                split_bf(y[r] * pw[adeg[b][r]], h, l);
+                ym[b][r] = h;
+                ym[b][4 + r] = l;
             }
         });
+        // stage 3: out^T[d, c] for the 16-row blocks of d (independent
+        // accumulators, one per d block), staged per wave and stored
+        v4f o[NDB];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) o[db] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+                o[db] = mfma_bf(__builtin_bit_cast(bf8, rfr[(db * NB + b) * 64 + lane]), ym[b], o[db]);
+        __bf16* so = sOut[wave];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int d = 16 * db + 4 * lg + r;
+                if (d < D) so[le * D + d] = static_cast<__bf16>(o[db][r]);
+            }
+        // the wave's 16 channel rows are contiguous in out: 16-byte stores
+        asm volatile("" ::: "memory");
+        constexpr int NCH = 16 * D * 2 / 16;
+        uint4* dst = reinterpret_cast<uint4*>(out + (e * C + 16 * wave) * D);
+        const uint4* s4o = reinterpret_cast<const uint4*>(so);
+#pragma unroll
+        for (int n = 0; n < (NCH + 63) / 64; ++n) {
+            const int q = lane + 64 * n;
+            if (q < NCH) dst[q] = s4o[q];
+        }
+        asm volatile("" ::: "memory");
+    };
+    for (int64_t i = 0; blockIdx.x + i * stride < E; i += 2) {
+        iteration(i, std::integral_constant<int, 0>{});
+        if (blockIdx.x + (i + 1) * stride >= E) break;
+        iteration(i + 1, std::integral_constant<int, 1>{});
     }
 }
 
@@ -681,6 +815,207 @@ k_hl_dfe(int64_t E, int64_t ntiles, const __bf16* __restrict__ fsT,
             __syncthreads();   // the buffers are read before the next group writes them
         });
     }
+}
+
+// ---- per-edge radial-function gradient as chained matrix-core products ----------
+// dF_e[k, w] = sum over the terms (o, i, w) of sign Z_k[o, i], with
+//   Z_k[o, i] = sum_co gd^T[o, co] G_k[co, i],   G_k = C_k fs,
+// where (o, i) ranges over the diagonal blocks of HLB (every term couples two
+// slots of one m-group).  Stage 1 forms G_k for 16 channels x 16 slots per
+// v_mfma_f32_16x16x32_bf16 (A: the C_k fragments held for the launch, B: the
+// edge's staged fs^T slot rows); its accumulators (lane l: channels 4 (l / 16)
+// + r of slot l % 16) are the B operand of stage 2's reduction over those
+// channels, split into bf16 hi and lo halves that share one 32-step, with the
+// edge's gd^T rows as the A operand.  Wave w owns rank k = w / H and the
+// channels 64 h .. 64 h + 63, h = w % H (H = C / 64 waves per rank): the H
+// partial Z_k of an edge go to LDS and are summed, and mapped to
+// the radial functions' terms, in the next iteration, after its barrier.  The
+// edge loop is pipelined as in k_hl_mixr: one barrier per edge, the next
+// edge's rows loaded into registers while the current one is computed.
+template <int L>
+struct HLTerms {   // the (at most two) Z entries of every radial function w
+    static constexpr int WD = Canon<L, L>::WD;
+    struct Tab {
+        int n[WD];
+        int b[WD][2], ro[WD][2], ri[WD][2], neg[WD][2];
+    };
+    static constexpr Tab make() {
+        Tab t{};
+        using HB = HLB<L>;
+        int blk[HB::D] = {}, row[HB::D] = {};
+        for (int b = 0; b < HB::NB; ++b)
+            for (int r = 0; r < 16; ++r)
+                if (HB::P.slot[b][r] >= 0) {
+                    blk[HB::P.slot[b][r]] = b;
+                    row[HB::P.slot[b][r]] = r;
+                }
+        for (int q = 0; q < Canon<L, L>::NT; ++q) {
+            const Term tm = Canon<L, L>::terms[q];
+            const int j = t.n[tm.w]++;
+            t.b[tm.w][j] = blk[tm.o];
+            t.ro[tm.w][j] = row[tm.o];
+            t.ri[tm.w][j] = row[tm.i];
+            t.neg[tm.w][j] = tm.neg;
+        }
+        return t;
+    }
+    static constexpr Tab T = make();
+};
+
+template <int L, int C, int K>
+__global__ void __launch_bounds__(4 * C, 1)
+k_hl_dfer(int64_t E, const __bf16* __restrict__ fsT, const __bf16* __restrict__ gdT,
+          const bf8* __restrict__ frag, float* __restrict__ dFe) {
+    using HB = HLB<L>;
+    using HT = HLTerms<L>;
+    constexpr int D = HB::D, NB = HB::NB, WD = HL<L>::WD, KW = K * WD;
+    constexpr int NT = 4 * C, NRB = C / 16, NKS = C / 32, H = C / 64;
+    constexpr int RS = 2 * C + 16;                              // LDS row stride in bytes
+    constexpr int NQ = (D * C / 8 + NT - 1) / NT;               // 16-byte row chunks per thread and operand
+    constexpr int NI = (KW + NT - 1) / NT;                      // radial functions per thread
+    constexpr int ZT = NB * 64;                                 // u32x4 of one wave's Z tiles
+    static_assert(C % 64 == 0 && NT / 64 == K * H, "one wave per rank and 64 channels");
+    static_assert(D * D < 0x10000, "16-bit table fields");
+    __shared__ __align__(16) char sFs[2][(D + 1) * RS];          // + a zero row for padding
+    __shared__ __align__(16) char sGd[2][(D + 1) * RS];
+    __shared__ __align__(16) u32x4 sZ[2][K * H * ZT];
+
+    const int tid = threadIdx.x, lane = tid & 63, le = lane & 15, lg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wk = wave / H, wh = wave % H;
+
+    // C_k rows of this wave's four 16-channel blocks, for the launch
+    bf8 Ak[4][NKS];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) Ak[c][ks] = frag[((wk * NRB + 4 * wh + c) * NKS + ks) * 64 + lane];
+    int arow[NB];   // byte offset of the slot row of lane row le in each block (zero row for padding)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int sl = HB::P.slot[b][le];
+        arow[b] = (sl >= 0 ? sl : D) * RS;
+    }
+    // the Z entries of this thread's radial functions (k, w): LDS element
+    // offsets (u32 units) within one buffer and their weights (the sign; 0
+    // for the unused second entry of an m = 0 function)
+    unsigned zoff[NI][2];
+    float zw[NI][2];
+#pragma unroll
+    for (int n = 0; n < NI; ++n) {
+        const int q = (tid + NT * n) % KW, k = q / WD, w = q % WD;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int jj = j < HT::T.n[w] ? j : 0;
+            const int b = HT::T.b[w][jj], ro = HT::T.ro[w][jj], ri = HT::T.ri[w][jj];
+            // Z[ro][ri] sits in lane 16 (ro / 4) + ri, component ro % 4, of tile (k, h, b)
+            zoff[n][j] = static_cast<unsigned>(((k * H) * NB + b) * 64 * 4 + (16 * (ro / 4) + ri) * 4 + ro % 4);
+            zw[n][j] = j < HT::T.n[w] ? (HT::T.neg[w][jj] ? -1.0f : 1.0f) : 0.0f;
+        }
+    }
+
+    const int64_t stride = gridDim.x;
+    auto edge = [&](int64_t i) -> int64_t {
+        const int64_t e = blockIdx.x + i * stride;
+        return e < E ? e : E - 1;
+    };
+    u32x4 pf[NQ], pg[NQ];
+    auto load_rows = [&](int64_t e) {
+        const u32x4* f4 = reinterpret_cast<const u32x4*>(fsT + e * D * C);
+        const u32x4* g4 = reinterpret_cast<const u32x4*>(gdT + e * D * C);
+#pragma unroll
+        for (int n = 0; n < NQ; ++n) {
+            const int q = tid + NT * n < D * C / 8 ? tid + NT * n : 0;
+            pf[n] = f4[q];
+            pg[n] = g4[q];
+        }
+    };
+    auto write_rows = [&](int buf) {
+#pragma unroll
+        for (int n = 0; n < NQ; ++n) {
+            const int q = tid + NT * n;
+            if ((D * C / 8) % NT == 0 || q < D * C / 8) {
+                const int off = (q / (C / 8)) * RS + (q % (C / 8)) * 16;
+                *reinterpret_cast<u32x4*>(sFs[buf] + off) = pf[n];
+                *reinterpret_cast<u32x4*>(sGd[buf] + off) = pg[n];
+            }
+        }
+    };
+    // dF_e of an edge from its Z partials (summed over the channel halves)
+    auto emit = [&](int buf, int64_t e) {
+        const unsigned* z = reinterpret_cast<const unsigned*>(sZ[buf]);
+#pragma unroll
+        for (int n = 0; n < NI; ++n) {
+            const int q = tid + NT * n;
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int h = 0; h < H; ++h) acc = fmaf(zw[n][j], __uint_as_float(z[zoff[n][j] + h * ZT * 4]), acc);
+            if (KW % NT == 0 || q < KW) dFe[e * KW + q] = acc;
+        }
+    };
+
+    for (int q = tid; q < 2 * (RS / 16); q += NT) {   // the zero rows
+        *reinterpret_cast<u32x4*>(sFs[q / (RS / 16)] + D * RS + (q % (RS / 16)) * 16) = u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(sGd[q / (RS / 16)] + D * RS + (q % (RS / 16)) * 16) = u32x4{0u, 0u, 0u, 0u};
+    }
+    load_rows(edge(0));
+    write_rows(0);
+    load_rows(edge(1));
+
+    auto iteration = [&](int64_t i, auto CB) __attribute__((always_inline)) {
+        constexpr int cb = decltype(CB)::value, nb = cb ^ 1;
+        __syncthreads();
+        write_rows(nb);                                  // e_{i+1}
+        if (i > 0) emit(nb, blockIdx.x + (i - 1) * stride);   // e_{i-1}
+        load_rows(edge(i + 2));
+        const char* fr = sFs[cb];
+        const char* gr = sGd[cb];
+        u32x4* zo = sZ[cb] + (wk * H + wh) * ZT;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            bf8 bfs[NKS];
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks)
+                bfs[ks] = *reinterpret_cast<const bf8*>(fr + arow[b] + (32 * ks + 8 * lg) * 2);
+            v4f g[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) g[c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) g[c] = mfma_bf(Ak[c][ks], bfs[ks], g[c]);
+            v4f z = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                // gd^T[o = slot(b, le)][channels 16 (4 h + c) + 4 lg .. + 3], twice (hi, lo)
+                const uint2 a2 = *reinterpret_cast<const uint2*>(gr + arow[b] + (16 * (4 * wh + c) + 4 * lg) * 2);
+                bf8 gb;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    __bf16 hh, ll;
+                    split_bf(g[c][r], hh, ll);
+                    gb[r] = hh;
+                    gb[4 + r] = ll;
+                }
+                z = mfma_bf(__builtin_bit_cast(bf8, (u32x4{a2.x, a2.y, a2.x, a2.y})), gb, z);
+            }
+            zo[b * 64 + lane] = __builtin_bit_cast(u32x4, z);
+        }
+    };
+    int64_t i = 0;
+    for (; blockIdx.x + i * stride < E; i += 2) {
+        iteration(i, std::integral_constant<int, 0>{});
+        if (blockIdx.x + (i + 1) * stride >= E) {
+            i += 1;
+            break;
+        }
+        iteration(i + 1, std::integral_constant<int, 1>{});
+    }
+    // the last edge's Z (written into buffer (i - 1) % 2)
+    __syncthreads();
+    if (i > 0) emit(static_cast<int>((i - 1) & 1), blockIdx.x + (i - 1) * stride);
 }
 
 // ---- channel-pattern gradient, fused -------------------------------------------------------
@@ -911,7 +1246,6 @@ int grid_tiles(int64_t ntiles) {
 struct HLWs {
     bf8* cfrag;      // A fragments (C_k or C_k^T)
     __bf16* fsT;     // (E, D, Cin)
-    float* stage;    // ym (E, D, Cout) or dfs^T (E, D, Cin)
     __bf16* gdT;     // (E, D, Cout)               backward
     float* dFe;      // (E, K WD)                  backward
     float* dCp;      // (groups, K Cout, Cin)      backward: per-workgroup dC partials
@@ -935,7 +1269,6 @@ size_t hl_layout(const feq_binning& B, int C, int64_t E, bool backward, HLWs* w,
     HLWs t{};
     t.cfrag = static_cast<bf8*>(take(nfrag * sizeof(bf8)));
     t.fsT = static_cast<__bf16*>(take(2 * static_cast<size_t>(E) * D * C));
-    t.stage = static_cast<float*>(take(4 * static_cast<size_t>(E) * D * C));
     if (backward) {
         const int groups = dc_groups(E);
         t.gdT = static_cast<__bf16*>(take(2 * static_cast<size_t>(E) * D * C));
@@ -957,15 +1290,6 @@ int hl_rot_in(int64_t E, const __bf16* in, const __bf16* R, const float* dist, f
     return FEQ_OK;
 }
 
-template <int L, int C>
-int hl_rot_out(int64_t E, const float* in, const __bf16* R, const float* dist, float sigma,
-               __bf16* out, hipStream_t s) {
-    auto kern = k_hl_rot_out<L, C>;
-    FEQ_LAUNCH("k_hl_rot_out", kern, dim3(ceil_div(E, 4 * RotIn<L, C>::EPW)), dim3(kT), 0, s, E, in, R,
-               dist, sigma, out);
-    return FEQ_OK;
-}
-
 template <bool TRANS>
 int hl_prep(const float* C, int K, int cout, int cin, bf8* frag, hipStream_t s) {
     const int64_t n = static_cast<int64_t>(K) * cout * cin / 8;
@@ -983,11 +1307,9 @@ int hl_fwd(const feq_binning& B, int64_t E, const __bf16* x, const __bf16* P, co
     __bf16* fs = fs_out ? fs_out : w.fsT;
     if (int rc = hl_prep<false>(C, kRank, CH, CH, w.cfrag, s)) return rc;
     if (int rc = hl_rot_in<L, CH>(E, x, P, dist, B.sh_scale, fs, s)) return rc;
-    const int64_t ntiles = ceil_div(E, kNE);
-    auto mix = k_hl_mix<L, CH, CH, kRank, false>;
-    FEQ_LAUNCH("k_hl_mix", mix, dim3(grid_tiles(ntiles)), dim3(4 * CH), 0, s, B, E, ntiles, fs,
-               dist, F, w.cfrag, w.stage);
-    return hl_rot_out<L, CH>(E, w.stage, Q, dist, B.sh_scale, y, s);
+    auto mix = k_hl_mixr<L, CH, kRank, false>;
+    FEQ_LAUNCH("k_hl_mix", mix, dim3(grid_tiles(E)), dim3(4 * CH), 0, s, B, E, fs, dist, F, w.cfrag, Q, y);
+    return FEQ_OK;
 }
 
 template <int L, int CH>
@@ -1009,15 +1331,14 @@ int hl_bwd(const feq_layout& Lay, const feq_binning& B, int64_t E, const __bf16*
     }
     // dF_e from <gd, C_k fs>
     if (int rc = hl_prep<false>(C, kRank, CH, CH, w.cfrag, s)) return rc;
-    auto kd = k_hl_dfe<L, CH, CH, kRank>;
-    FEQ_LAUNCH("k_hl_dfe", kd, dim3(G), dim3(kT), 0, s, E, ntiles, fs, w.gdT, w.cfrag, w.dFe);
+    auto kd = k_hl_dfer<L, CH, kRank>;
+    FEQ_LAUNCH("k_hl_dfe", kd, dim3(grid_tiles(E)), dim3(4 * CH), 0, s, E, fs, w.gdT, w.cfrag, w.dFe);
     // dfs = sum_k M_ek^T C_k^T gd, dx = (s^l_in dfs) P^T
     if (gx) {
         if (int rc = hl_prep<true>(C, kRank, CH, CH, w.cfrag, s)) return rc;
-        auto km = k_hl_mix<L, CH, CH, kRank, true>;
-        FEQ_LAUNCH("k_hl_mix_t", km, dim3(G), dim3(4 * CH), 0, s, B, E, ntiles, w.gdT, dist, F,
-                   w.cfrag, w.stage);
-        if (int rc = hl_rot_out<L, CH>(E, w.stage, P, dist, B.sh_scale, gx, s)) return rc;
+        auto km = k_hl_mixr<L, CH, kRank, true>;
+        FEQ_LAUNCH("k_hl_mix_t", km, dim3(grid_tiles(E)), dim3(4 * CH), 0, s, B, E, w.gdT, dist, F, w.cfrag,
+                   P, gx);
     }
     // dC = sum over (e, i) of (M_ek^T gd) fs^T, per-workgroup partials; the
     // shared tail sums them in a fixed order with the binned radial-function
