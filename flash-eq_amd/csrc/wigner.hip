@@ -31,12 +31,19 @@ struct WignerArgs {
     int32_t plan_off[FEQ_MAX_IRREPS];  // offset of every irrep's plan block (doubles)
 };
 
-__device__ __forceinline__ float sanitize(double v) {
-    // nan_to_num(x, 0.0): NaN -> 0, +-inf -> +-FLT_MAX
-    if (v != v) return 0.0f;
-    if (v > static_cast<double>(FLT_MAX)) return FLT_MAX;
-    if (v < -static_cast<double>(FLT_MAX)) return -FLT_MAX;
-    return static_cast<float>(v);
+// nan_to_num(x, 0.0) in the output type: NaN -> 0, +-inf -> +-max
+template <class T>
+__device__ __forceinline__ T sanitize(double v) {
+    if (v != v) return T(0);
+    if constexpr (std::is_same_v<T, float>) {
+        if (v > static_cast<double>(FLT_MAX)) return FLT_MAX;
+        if (v < -static_cast<double>(FLT_MAX)) return -FLT_MAX;
+        return static_cast<float>(v);
+    } else {
+        if (v > DBL_MAX) return DBL_MAX;
+        if (v < -DBL_MAX) return -DBL_MAX;
+        return v;
+    }
 }
 
 // Column c of D for an irrep of degree L (n = 2L + 1) and edge angles (phi,
@@ -102,9 +109,9 @@ __device__ __forceinline__ void wigner_column(const double* __restrict__ V, int 
     }
 }
 
-template <int L>
+template <int L, class T>
 __device__ __forceinline__ void column_into(const double* V, int c, double phi, double ang,
-                                            bool ident, float* dst, int stride) {
+                                            bool ident, T* dst, int stride) {
     constexpr int n = 2 * L + 1;
     double y[n];
     if (L == 0) {
@@ -116,7 +123,7 @@ __device__ __forceinline__ void column_into(const double* V, int c, double phi, 
         wigner_column<L>(V, c, phi, ang, y);
     }
 #pragma unroll
-    for (int r = 0; r < n; ++r) dst[r * stride] = sanitize(y[r]);
+    for (int r = 0; r < n; ++r) dst[r * stride] = sanitize<T>(y[r]);
 }
 
 struct EdgeFrame {
@@ -129,30 +136,34 @@ struct EdgeFrame {
 // is then written with coalesced stores.
 // LMAX: the largest degree the launch handles (the register footprint of the
 // per-column vectors grows with it, so small representations get a small kernel).
-template <int LMAX>
+// T = float: the frame in float32, as the reference's float32 rot_to_ez (whose
+// clamp bounds +-(1 - eps) round to +-1); T = double: the frame in float64 with
+// the clamp as written (a float64 module runs rot_to_ez in float64).
+template <int LMAX, class T>
 __global__ void __launch_bounds__(256)
 k_wigner(WignerArgs A, int epb, const double* __restrict__ plan, const int32_t* __restrict__ perm,
-         int64_t E, const float* __restrict__ dirs, float* __restrict__ out) {
-    extern __shared__ float sM[];                      // epb x dim x dim
+         int64_t E, const T* __restrict__ dirs, T* __restrict__ out) {
+    extern __shared__ __align__(16) char sMraw[];
+    T* sM = reinterpret_cast<T*>(sMraw);              // epb x dim x dim
     __shared__ EdgeFrame sFr[256];
     __shared__ int sInv[FEQ_MAX_SLOTS];
     const int dim = A.dim, dd = dim * dim;
     const int64_t e0 = static_cast<int64_t>(blockIdx.x) * epb;
     const int ne = static_cast<int>(E - e0 < epb ? E - e0 : epb);
-    for (int q = threadIdx.x; q < epb * dd; q += blockDim.x) sM[q] = 0.0f;
+    for (int q = threadIdx.x; q < epb * dd; q += blockDim.x) sM[q] = T(0);
     for (int j = threadIdx.x; j < dim; j += blockDim.x) sInv[perm[j]] = j;
     if (threadIdx.x < ne) {
         // edge frame in float32 like rot_to_ez: d = v/(|v|+eps), axis = (-d_y, d_x, 0)/(|.|+eps),
         // theta = acos(clamp(d_z, -1, 1)); a = rho (cos phi, sin phi)
         const int64_t e = e0 + threadIdx.x;
-        const float eps = 1e-8f;
-        const float vx = dirs[3 * e], vy = dirs[3 * e + 1], vz = dirs[3 * e + 2];
-        const float nv = sqrtf(vx * vx + vy * vy + vz * vz) + eps;
-        const float dx = vx / nv, dy = vy / nv, dz = vz / nv;
-        const float a0r = -dy, a1r = dx;
-        const float na = sqrtf(a0r * a0r + a1r * a1r) + eps;
-        const float a0 = a0r / na, a1 = a1r / na;
-        const float theta = acosf(fminf(fmaxf(dz, -1.0f), 1.0f));
+        const T eps = T(1e-8);
+        const T vx = dirs[3 * e], vy = dirs[3 * e + 1], vz = dirs[3 * e + 2];
+        const T nv = sqrt(vx * vx + vy * vy + vz * vz) + eps;
+        const T dx = vx / nv, dy = vy / nv, dz = vz / nv;
+        const T a0r = -dy, a1r = dx;
+        const T na = sqrt(a0r * a0r + a1r * a1r) + eps;
+        const T a0 = a0r / na, a1 = a1r / na;
+        const T theta = acos(fmin(fmax(dz, T(-1) + eps), T(1) - eps));
         const double rho = sqrt(static_cast<double>(a0) * a0 + static_cast<double>(a1) * a1);
         EdgeFrame f;
         f.ident = rho == 0.0;
@@ -169,7 +180,7 @@ k_wigner(WignerArgs A, int epb, const double* __restrict__ plan, const int32_t* 
         const int l = A.lvals[k], base = A.off[k], c = c0 - base;
         const double* V = plan + A.plan_off[k];
         const EdgeFrame f = sFr[el];
-        float* dst = sM + el * dd + base * dim + sInv[c0];   // rows base.., column j
+        T* dst = sM + el * dd + base * dim + sInv[c0];   // rows base.., column j
         switch (l) {
 #define FEQ_WCASE(LL) \
     case LL:                                                                             \
@@ -183,7 +194,7 @@ k_wigner(WignerArgs A, int epb, const double* __restrict__ plan, const int32_t* 
         }
     }
     __syncthreads();
-    float* o = out + e0 * dd;
+    T* o = out + e0 * dd;
     for (int q = threadIdx.x; q < ne * dd; q += blockDim.x) o[q] = sM[q];
 }
 
@@ -266,9 +277,9 @@ __device__ __forceinline__ void multiples(double ang, double (&c)[L + 1], double
 // Contributions of column c of one irrep block.  gcol / gpar: columns c and
 // n-1-c of dL/dD restricted to the block's rows.  t0/t1: (dL/dang, dL/dphi), or
 // at rho = 0 (ident) (dL/da0, dL/da1) without the factor theta.
-template <int L>
+template <int L, class T>
 __device__ __forceinline__ void column_grad(const double* V, int c, double phi, double ang,
-                                            bool ident, const float* gcol, const float* gpar,
+                                            bool ident, const T* gcol, const T* gpar,
                                             int stride, double& t0, double& t1) {
     constexpr int n = 2 * L + 1;
     t0 = 0.0;
@@ -305,19 +316,20 @@ __device__ __forceinline__ void column_grad(const double* V, int c, double phi, 
     }
 }
 
-template <int LMAX>
+template <int LMAX, class T>
 __global__ void __launch_bounds__(256)
 k_wigner_bwd(WignerArgs A, int epb, const double* __restrict__ plan, const int32_t* __restrict__ perm,
-             int64_t E, const float* __restrict__ dirs, const float* __restrict__ gM,
-             float* __restrict__ gdirs) {
-    extern __shared__ float sG[];                      // epb x dim x dim (dL/dM tile)
+             int64_t E, const T* __restrict__ dirs, const T* __restrict__ gM,
+             T* __restrict__ gdirs) {
+    extern __shared__ __align__(16) char sGraw[];
+    T* sG = reinterpret_cast<T*>(sGraw);              // epb x dim x dim (dL/dM tile)
     __shared__ EdgeFrame sFr[256];
     __shared__ int sInv[FEQ_MAX_SLOTS];
     __shared__ double sT0[256], sT1[256];
     const int dim = A.dim, dd = dim * dim;
     const int64_t e0 = static_cast<int64_t>(blockIdx.x) * epb;
     const int ne = static_cast<int>(E - e0 < epb ? E - e0 : epb);
-    const float* gsrc = gM + e0 * dd;
+    const T* gsrc = gM + e0 * dd;
     for (int q = threadIdx.x; q < ne * dd; q += blockDim.x) sG[q] = gsrc[q];
     for (int j = threadIdx.x; j < dim; j += blockDim.x) sInv[perm[j]] = j;
     // The frame in double from the float32 directions: near the poles (|d_z| -> 1)
@@ -361,8 +373,8 @@ k_wigner_bwd(WignerArgs A, int epb, const double* __restrict__ plan, const int32
         const double* V = plan + A.plan_off[k];
         const EdgeFrame f = sFr[el];
         // column c of dL/dD is column sInv[c] of dL/dM; rows base.. of the block
-        const float* gcol = sG + el * dd + base * dim + sInv[c0];
-        const float* gpar = sG + el * dd + base * dim + sInv[base + n - 1 - c];
+        const T* gcol = sG + el * dd + base * dim + sInv[c0];
+        const T* gpar = sG + el * dd + base * dim + sInv[base + n - 1 - c];
         switch (l) {
 #define FEQ_WCASE(LL)                                                                    \
     case LL:                                                                             \
@@ -427,9 +439,9 @@ k_wigner_bwd(WignerArgs A, int epb, const double* __restrict__ plan, const int32
         gv1 -= dotv * vy;
         gv2 -= dotv * vz;
     }
-    gdirs[3 * e] = static_cast<float>(gv0);
-    gdirs[3 * e + 1] = static_cast<float>(gv1);
-    gdirs[3 * e + 2] = static_cast<float>(gv2);
+    gdirs[3 * e] = static_cast<T>(gv0);
+    gdirs[3 * e + 1] = static_cast<T>(gv1);
+    gdirs[3 * e + 2] = static_cast<T>(gv2);
 }
 
 // Calls f with std::integral_constant<int, LMAX> for the smallest compiled LMAX
@@ -459,13 +471,11 @@ extern "C" size_t feq_wigner_plan_doubles(const int32_t* lvals, int32_t n) {
     return s;
 }
 
-extern "C" int feq_wigner_basis(const int32_t* lvals, int32_t n, const double* plan,
-                                const int32_t* perm, int64_t E, const float* dirs, float* out,
-                                feq_stream_t stream) {
+namespace {
+int wigner_args(const int32_t* lvals, int32_t n, WignerArgs& A) {
     if (!lvals || n < 1) return fail(FEQ_ERR_INVALID, "lvals must be non-empty");
     if (n > FEQ_MAX_IRREPS) return fail(FEQ_ERR_UNSUPPORTED, "more than %d irreps", FEQ_MAX_IRREPS);
-    if (E < 0) return fail(FEQ_ERR_INVALID, "negative edge count");
-    WignerArgs A{};
+    A = WignerArgs{};
     A.nirr = n;
     int dim = 0;
     size_t po = 0;
@@ -480,51 +490,81 @@ extern "C" int feq_wigner_basis(const int32_t* lvals, int32_t n, const double* p
         po += static_cast<size_t>(d) * d + 2 * d;
     }
     A.dim = dim;
+    return FEQ_OK;
+}
+
+// Edges per workgroup: one thread per (edge, column), the edges' matrices
+// (dim x dim values of T) staged in at most 64 KB of LDS.
+template <class T>
+int wigner_epb(int dim, int* epb, size_t* lds) {
+    int e = 256 / dim;
+    const int cap = static_cast<int>((64 * 1024) / (sizeof(T) * static_cast<size_t>(dim) * dim));
+    e = e < cap ? e : cap;
+    if (e < 1) return fail(FEQ_ERR_UNSUPPORTED, "representation dimension %d too large", dim);
+    *epb = e;
+    *lds = sizeof(T) * static_cast<size_t>(e) * dim * dim;
+    return FEQ_OK;
+}
+
+template <class T>
+int wigner_fwd(const int32_t* lvals, int32_t n, const double* plan, const int32_t* perm, int64_t E,
+               const T* dirs, T* out, feq_stream_t stream) {
+    WignerArgs A;
+    if (int rc = wigner_args(lvals, n, A)) return rc;
+    if (E < 0) return fail(FEQ_ERR_INVALID, "negative edge count");
     if (E == 0) return FEQ_OK;
     if (!plan || !perm || !dirs || !out) return fail(FEQ_ERR_INVALID, "NULL pointer");
-    // one thread per (edge, column); the edges' matrices are staged in LDS
-    const int epb = 256 / dim;
-    const size_t lds = sizeof(float) * static_cast<size_t>(epb) * dim * dim;
-    if (lds > 64 * 1024) return fail(FEQ_ERR_UNSUPPORTED, "representation dimension %d too large", dim);
+    int epb;
+    size_t lds;
+    if (int rc = wigner_epb<T>(A.dim, &epb, &lds)) return rc;
     return with_lmax(A, [&](auto LL) -> int {
-        auto kern = k_wigner<decltype(LL)::value>;
+        auto kern = k_wigner<decltype(LL)::value, T>;
         FEQ_LAUNCH("k_wigner", kern, dim3(ceil_div(E, epb)), dim3(256), lds, stream_of(stream), A,
                    epb, plan, perm, E, dirs, out);
         return FEQ_OK;
     });
 }
 
+template <class T>
+int wigner_bwd(const int32_t* lvals, int32_t n, const double* plan, const int32_t* perm, int64_t E,
+               const T* dirs, const T* grad_out, T* grad_dirs, feq_stream_t stream) {
+    WignerArgs A;
+    if (int rc = wigner_args(lvals, n, A)) return rc;
+    if (E < 0) return fail(FEQ_ERR_INVALID, "negative edge count");
+    if (E == 0) return FEQ_OK;
+    if (!plan || !perm || !dirs || !grad_out || !grad_dirs) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    int epb;
+    size_t lds;
+    if (int rc = wigner_epb<T>(A.dim, &epb, &lds)) return rc;
+    return with_lmax(A, [&](auto LL) -> int {
+        auto kern = k_wigner_bwd<decltype(LL)::value, T>;
+        FEQ_LAUNCH("k_wigner_bwd", kern, dim3(ceil_div(E, epb)), dim3(256), lds, stream_of(stream), A,
+                   epb, plan, perm, E, dirs, grad_out, grad_dirs);
+        return FEQ_OK;
+    });
+}
+}  // namespace
+
+extern "C" int feq_wigner_basis(const int32_t* lvals, int32_t n, const double* plan,
+                                const int32_t* perm, int64_t E, const float* dirs, float* out,
+                                feq_stream_t stream) {
+    return wigner_fwd<float>(lvals, n, plan, perm, E, dirs, out, stream);
+}
+
+extern "C" int feq_wigner_basis_f64(const int32_t* lvals, int32_t n, const double* plan,
+                                    const int32_t* perm, int64_t E, const double* dirs, double* out,
+                                    feq_stream_t stream) {
+    return wigner_fwd<double>(lvals, n, plan, perm, E, dirs, out, stream);
+}
+
 extern "C" int feq_wigner_basis_bwd(const int32_t* lvals, int32_t n, const double* plan,
                                     const int32_t* perm, int64_t E, const float* dirs,
                                     const float* grad_out, float* grad_dirs, feq_stream_t stream) {
-    if (!lvals || n < 1) return fail(FEQ_ERR_INVALID, "lvals must be non-empty");
-    if (n > FEQ_MAX_IRREPS) return fail(FEQ_ERR_UNSUPPORTED, "more than %d irreps", FEQ_MAX_IRREPS);
-    if (E < 0) return fail(FEQ_ERR_INVALID, "negative edge count");
-    WignerArgs A{};
-    A.nirr = n;
-    int dim = 0;
-    size_t po = 0;
-    for (int i = 0; i < n; ++i) {
-        if (lvals[i] < 0 || lvals[i] >= FEQ_MAX_BLOCKS)
-            return fail(FEQ_ERR_UNSUPPORTED, "degree %d outside [0, %d]", lvals[i], FEQ_MAX_BLOCKS - 1);
-        A.lvals[i] = lvals[i];
-        A.off[i] = dim;
-        A.plan_off[i] = static_cast<int32_t>(po);
-        const int d = 2 * lvals[i] + 1;
-        dim += d;
-        po += static_cast<size_t>(d) * d + 2 * d;
-    }
-    A.dim = dim;
-    if (E == 0) return FEQ_OK;
-    if (!plan || !perm || !dirs || !grad_out || !grad_dirs) return fail(FEQ_ERR_INVALID, "NULL pointer");
-    const int epb = 256 / dim;
-    if (epb < 1) return fail(FEQ_ERR_UNSUPPORTED, "representation dimension %d too large", dim);
-    const size_t lds = sizeof(float) * static_cast<size_t>(epb) * dim * dim;
-    if (lds > 64 * 1024) return fail(FEQ_ERR_UNSUPPORTED, "representation dimension %d too large", dim);
-    return with_lmax(A, [&](auto LL) -> int {
-        auto kern = k_wigner_bwd<decltype(LL)::value>;
-        FEQ_LAUNCH("k_wigner_bwd", kern, dim3(ceil_div(E, epb)), dim3(256), lds,
-                   stream_of(stream), A, epb, plan, perm, E, dirs, grad_out, grad_dirs);
-        return FEQ_OK;
-    });
+    return wigner_bwd<float>(lvals, n, plan, perm, E, dirs, grad_out, grad_dirs, stream);
+}
+
+extern "C" int feq_wigner_basis_bwd_f64(const int32_t* lvals, int32_t n, const double* plan,
+                                        const int32_t* perm, int64_t E, const double* dirs,
+                                        const double* grad_out, double* grad_dirs, feq_stream_t stream) {
+    return wigner_bwd<double>(lvals, n, plan, perm, E, dirs, grad_out, grad_dirs, stream);
 }

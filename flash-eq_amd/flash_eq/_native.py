@@ -112,6 +112,8 @@ _SIGS = {
     "feq_wigner_plan_doubles": ([_P, _I32], _SZ),
     "feq_wigner_basis": ([_P, _I32, _P, _P, _I64, _P, _P, _P], ctypes.c_int),
     "feq_wigner_basis_bwd": ([_P, _I32, _P, _P, _I64, _P, _P, _P, _P], ctypes.c_int),
+    "feq_wigner_basis_f64": ([_P, _I32, _P, _P, _I64, _P, _P, _P], ctypes.c_int),
+    "feq_wigner_basis_bwd_f64": ([_P, _I32, _P, _P, _I64, _P, _P, _P, _P], ctypes.c_int),
     "feq_csr_workspace": ([_I64, _I64], _SZ),
     "feq_csr_by_dst": ([_P, _I64, _I64, _P, _P, _P, _SZ, _P], ctypes.c_int),
     "feq_segment_sum": ([_P, _I64, _P, _P, _I64, _P, _P], ctypes.c_int),

@@ -121,6 +121,8 @@ class EquivariantEdgewiseLinear(nn.Module):
         over the graph's CSR by source; otherwise the rows are gathered first."""
         N.require_cuda_tensor(edge_features, "edge_features")
         rw = self.radial_weights
+        if edge_features.dtype == torch.float64:
+            return self._forward_f64(P, Q, edge_features, distances, graph)
         layout, binning = self.layout(), self.binning()
         if torch.is_grad_enabled() and (P.requires_grad or Q.requires_grad):
             # gradients for the bases: the kernels that form gP and gQ take
@@ -159,6 +161,25 @@ class EquivariantEdgewiseLinear(nn.Module):
             edge_features = graph.gather_src(edge_features)
         return edgewise_linear(edge_features, P, Q, distances, rw.channel_patterns,
                                rw.radial_functions(), layout, binning, rw.rank)
+
+    def _forward_f64(self, P, Q, edge_features, distances, graph):
+        """float64: the reference's own composition (linear.py:131-160) -- x P by
+        library bmm, the block-diagonal op on the full radial table
+        (``block_diagonal_cuda``, whose float64 kernels are block_diagonal.cu:1332's
+        dispatch), then by Q^T -- every operand in float64 and every gradient
+        (features, bases, radial network, distances) by autograd through it."""
+        from ..cuda.block_diagonal import block_diagonal_cuda
+        if graph is not None:
+            if graph.num_edges != distances.shape[0]:
+                raise ValueError(f"graph has {graph.num_edges} edges, distances {distances.shape[0]}")
+            edge_features = edge_features.index_select(0, graph.src)
+        rw = self.radial_weights
+        p1, p2 = rw.binning_params()
+        f = torch.bmm(edge_features, P.to(torch.float64))
+        out = block_diagonal_cuda(f, rw().to(torch.float64), distances.to(torch.float64), self.product_repr,
+                                  bin_param1=p1, bin_param2=p2, num_bins=rw.num_bins, log_bins=rw.log,
+                                  sh_scale=self.solid_harmonic_scale)
+        return torch.bmm(out, Q.to(torch.float64).mT.contiguous())
 
     def attention_pool(self, P: torch.Tensor, Q: torch.Tensor, node_features: torch.Tensor,
                        distances: torch.Tensor, graph, attn: torch.Tensor, num_heads: int):

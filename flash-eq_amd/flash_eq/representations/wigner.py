@@ -171,16 +171,21 @@ class _WignerBasisFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, directions, lvals_i32, plan, perm_i32):
         dev = directions.device
-        dirs = directions.detach().to(torch.float32).contiguous()
+        # float64 directions run the float64 kernels (a float64 module); every
+        # other dtype the float32 ones (the reference computes half-precision
+        # bases in float32, wigner.py:132-142)
+        wdt = torch.float64 if directions.dtype == torch.float64 else torch.float32
+        dirs = directions.detach().to(wdt).contiguous()
         E = dirs.shape[0]
         dim = int(perm_i32.numel())
-        out = torch.empty(E, dim, dim, dtype=torch.float32, device=dev)
+        out = torch.empty(E, dim, dim, dtype=wdt, device=dev)
         lv = (N.ctypes.c_int32 * len(lvals_i32))(*lvals_i32)
+        fn = "feq_wigner_basis_f64" if wdt == torch.float64 else "feq_wigner_basis"
         with torch.cuda.device(dev):
-            rc = N.lib().feq_wigner_basis(lv, len(lvals_i32), N.ptr(plan), N.ptr(perm_i32), E,
-                                          N.ptr(dirs) if E else None, N.ptr(out) if E else None,
-                                          N.stream_ptr(dev))
-        N.check(rc, "feq_wigner_basis")
+            rc = getattr(N.lib(), fn)(lv, len(lvals_i32), N.ptr(plan), N.ptr(perm_i32), E,
+                                      N.ptr(dirs) if E else None, N.ptr(out) if E else None,
+                                      N.stream_ptr(dev))
+        N.check(rc, fn)
         ctx.save_for_backward(dirs, plan, perm_i32)
         ctx.meta = (tuple(lvals_i32), directions.dtype)
         return out
@@ -191,21 +196,23 @@ class _WignerBasisFn(torch.autograd.Function):
         lvals, ddt = ctx.meta
         dev = dirs.device
         E = dirs.shape[0]
-        g = grad.detach().to(torch.float32).contiguous()
+        g = grad.detach().to(dirs.dtype).contiguous()
         gd = torch.empty_like(dirs)
         lv = (N.ctypes.c_int32 * len(lvals))(*lvals)
+        fn = "feq_wigner_basis_bwd_f64" if dirs.dtype == torch.float64 else "feq_wigner_basis_bwd"
         with torch.cuda.device(dev):
-            rc = N.lib().feq_wigner_basis_bwd(lv, len(lvals), N.ptr(plan), N.ptr(perm_i32), E,
-                                              N.ptr(dirs) if E else None, N.ptr(g) if E else None,
-                                              N.ptr(gd) if E else None, N.stream_ptr(dev))
-        N.check(rc, "feq_wigner_basis_bwd")
+            rc = getattr(N.lib(), fn)(lv, len(lvals), N.ptr(plan), N.ptr(perm_i32), E,
+                                      N.ptr(dirs) if E else None, N.ptr(g) if E else None,
+                                      N.ptr(gd) if E else None, N.stream_ptr(dev))
+        N.check(rc, fn)
         return gd.to(ddt), None, None, None
 
 
 class WignerDBasis(nn.Module):
     """Per-edge basis matrices for a list of representations (``wigner.py:275-370``).
 
-    Returns one (E, dim, dim) float32 matrix per representation; column j is
+    Returns one (E, dim, dim) matrix per representation (float64 for float64
+    directions, else float32 cast to a half-precision input's dtype); column j is
     column ``perm[j]`` of the Wigner-D matrix of the rotation taking e_z to the
     edge direction.  Representations with equal lvals share one result tensor.
     """
@@ -252,7 +259,7 @@ class WignerDBasis(nn.Module):
         for i in range(self._num_unique):
             plan, perm = consts[i]
             m = _WignerBasisFn.apply(directions, self._lvals[i], plan, perm)
-            if directions.dtype in (torch.float16, torch.bfloat16, torch.float64):
+            if directions.dtype in (torch.float16, torch.bfloat16):
                 m = m.to(directions.dtype)
             outs.append(m)
         return tuple(outs[k] for k in self._input_to_unique)

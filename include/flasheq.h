@@ -302,6 +302,16 @@ int feq_wigner_basis(const int32_t* lvals, int32_t n, const double* plan_dev,
 int feq_wigner_basis_bwd(const int32_t* lvals, int32_t n, const double* plan_dev,
                          const int32_t* perm_dev, int64_t num_edges, const float* dirs,
                          const float* grad_out, float* grad_dirs, feq_stream_t stream);
+/* float64 forms of the two above, for a WignerDBasis of float64 directions
+ * (a module moved with .double(): its rot_to_ez and matrix_exp run in float64,
+ * wigner.py:132-142, 198-240): the edge frame in float64 with the clamp of d_z
+ * to [-1 + eps, 1 - eps] as written (in float32 its bounds round to +-1). */
+int feq_wigner_basis_f64(const int32_t* lvals, int32_t n, const double* plan_dev,
+                         const int32_t* perm_dev, int64_t num_edges, const double* dirs,
+                         double* out, feq_stream_t stream);
+int feq_wigner_basis_bwd_f64(const int32_t* lvals, int32_t n, const double* plan_dev,
+                             const int32_t* perm_dev, int64_t num_edges, const double* dirs,
+                             const double* grad_out, double* grad_dirs, feq_stream_t stream);
 
 /* ---- graph ops -----------------------------------------------------------------
  * CSR by destination: perm (E) lists edge ids grouped by dst in increasing

@@ -63,6 +63,9 @@ def module_cfg(layer) -> dict:
     rw = layer.radial_weights
     params = {k: v.detach().double().cpu().clone().requires_grad_(True)
               for k, v in rw.named_parameters()}
+    # the module's frequency buffer: k pi rounded to float32 (radial.py:206-209),
+    # which a float64 module keeps (.double() converts the rounded values)
+    params["frequencies"] = rw.frequencies.detach().double().cpu()
     cfg = dict(lin=[int(l) for l in layer.in_repr.lvals], lout=[int(l) for l in layer.out_repr.lvals],
                num_bins=rw.num_bins, min=rw.min_val, max=rw.max_val, log=rw.log,
                sigma=layer.solid_harmonic_scale, rank=rw.rank, wdim=rw.weight_dim,
@@ -164,5 +167,5 @@ def attention_layer(layer, P, Qb, x, r, src, dst, num_nodes):
     out = G.pool_sum(G.apply_heads(V, attn), dst, num_nodes)
     params = {"norm_qk.lnorm.weight": ln_w, "norm_qk.lnorm.bias": ln_b,
               "linear_qk.weight": wqk, "attention.log_scale": ls}
-    params.update({"linear_v.radial_weights." + k: v for k, v in vparams.items()})
+    params.update({"linear_v.radial_weights." + k: v for k, v in vparams.items() if v.requires_grad})
     return out, params
