@@ -667,6 +667,72 @@ def run_workload(name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
     return out
 
 
+# the reference's published EquivariantEdgewiseLinear
+# numbers (H100, benchmarks/compare_all.py:146-182, README.md:281-305):
+# (lmax, edges, ms per fwd + MSE + bwd + Adam step) at C = 32, num_bins = 64
+PUBLISHED_FP32 = [(1, 32000, 5.3), (2, 32000, 11.5), (4, 5000, 7.1), (6, 5000, 14.7), (4, 20000, 21.5),
+                  (6, 20000, 50.6), (4, 50000, 50.1), (6, 50000, 123.5), (4, 128000, 125.6),
+                  (6, 128000, 309.7)]
+PUBLISHED_AMP = [(1, 32000, 5.4), (2, 32000, 10.5), (4, 5000, 6.6), (6, 5000, 13.6), (4, 20000, 19.7),
+                 (6, 20000, 46.2), (4, 50000, 45.3), (6, 50000, 110.9), (4, 128000, 112.9),
+                 (6, 128000, 279.8)]
+
+
+def run_published(amp: bool, n_warmup: int = 3, n_iter: int = 10) -> list:
+    """The reference's own benchmark step (compare_all.py:146-182) at its
+    published configurations: EquivariantEdgewiseLinear(Repr(0..L, 32)) with
+    num_bins = 64, features (E, 32, dim) requiring grad, P = Q from WignerDBasis
+    of random unit directions (outside the step), distances U[0, 10), one step =
+    zero_grad + forward + MSE against a random target + backward + Adam (lr
+    1e-4); fp16 autocast with a GradScaler for the AMP rows; mean over 10 steps
+    after 3 warmups, timed with events as the reference does (compare_all.py:
+    60-81)."""
+    import flash_eq as fe
+    dev = torch.device("cuda", 0)
+    rows = []
+    for lmax, E, ref_ms in (PUBLISHED_AMP if amp else PUBLISHED_FP32):
+        torch.manual_seed(lmax * 1000 + E // 1000)
+        rep = fe.Repr(list(range(lmax + 1)), 32)
+        dim = rep.dim()
+        layer = fe.EquivariantEdgewiseLinear(rep, rep, num_bins=64, min_dist=0.0, max_dist=10.0).to(dev)
+        basis = fe.WignerDBasis([rep, rep]).to(dev)
+        opt = torch.optim.Adam(layer.parameters(), lr=1e-4)
+        scaler = torch.amp.GradScaler("cuda", enabled=amp)
+        feats = torch.randn(E, 32, dim, device=dev, requires_grad=True)
+        dirs = torch.randn(E, 3, device=dev)
+        dirs = dirs / dirs.norm(dim=-1, keepdim=True)
+        dist = torch.rand(E, device=dev) * 10.0
+        target = torch.randn(E, 32, dim, device=dev)
+        P, Q = basis(dirs)
+
+        def step():
+            opt.zero_grad()
+            with torch.amp.autocast("cuda", enabled=amp):
+                out = layer(P, Q, feats, dist)
+                loss = ((out - target) ** 2).mean()
+            scaler.scale(loss).backward()
+            scaler.step(opt)
+            scaler.update()
+        try:
+            for _ in range(n_warmup):
+                step()
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for _ in range(n_iter):
+                step()
+            t1.record()
+            torch.cuda.synchronize()
+            ms = t0.elapsed_time(t1) / n_iter
+            rows.append({"lmax": lmax, "edges": E, "ms_per_step": round(ms, 3),
+                         "reference_h100_ms": ref_ms, "speedup_vs_reference": round(ref_ms / ms, 2)})
+        except Exception as exc:      # one failing row must not lose the others
+            rows.append({"lmax": lmax, "edges": E, "error": f"{type(exc).__name__}: {exc}"[:200]})
+        del layer, basis, opt, feats, target, P, Q
+        torch.cuda.empty_cache()
+    return rows
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -681,7 +747,8 @@ def main() -> int:
     ap.add_argument("--grad-dist", action="store_true", help="also differentiate w.r.t. distances")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run 1 GiB device copies first (for rocprofv3 --pmc byte calibration)")
-    ap.add_argument("--workload", default="c2", choices=["c2", "c1", "c3", "c3bf16", "c4", "c5"],
+    ap.add_argument("--workload", default="c2",
+                    choices=["c2", "c1", "c3", "c3bf16", "c4", "c5", "published", "published_amp"],
                     help="c2 (default) is the metric's configuration; the others print a "
                          "secondary line with their full-size throughput and kernel times")
     ap.add_argument("--no-secondary", action="store_true",
@@ -693,6 +760,9 @@ def main() -> int:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
               "multi-GPU path; run it with --gpus 1.", file=sys.stderr)
         return 2
+    if args.workload.startswith("published"):
+        print(json.dumps({"workload": args.workload, "rows": run_published(args.workload == "published_amp")}))
+        return 0
     if args.workload != "c2":
         print(json.dumps(run_workload(args.workload, args.steps, args.warmup, not args.no_cpu)))
         return 0
