@@ -473,6 +473,13 @@ extern "C" int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32
     return ew_tail(*L, *b, rank, E, dist, F, dFe, part, G, ncc, gC, gF, nullptr, tail, s);
 }
 
+extern "C" int feq_edgewise_fused_supported(const feq_layout* L, const feq_binning* b, int32_t rank) {
+    if (!L || !b || rank < 1 || check_layout(L) || check_binning(b)) return 0;
+    if (ew_path() == kPathSplit && ew_split_supported(*L, *b, rank, false)) return 1;
+    return fwd_lds(*L, rank) <= 160 * 1024 && bwd_lds(*L, rank) <= 160 * 1024 &&
+           ew_tail_supported(*b, rank * L->wdim);
+}
+
 // ---- message-passing form: x is a node table, edge e reads row src[e] -----------
 extern "C" int feq_edgewise_src_supported(const feq_layout* L, const feq_binning* b, int32_t rank) {
     if (!L || !b || check_layout(L) || check_binning(b)) return 0;

@@ -70,6 +70,7 @@ _SIGS = {
     "feq_edgewise_bwd": ([_P, _P, _I32, _I64, _P, _P, _P, _P, _P, _P, _P,
                           _P, _P, _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
     "feq_edgewise_src_supported": ([_P, _P, _I32], ctypes.c_int),
+    "feq_edgewise_fused_supported": ([_P, _P, _I32], ctypes.c_int),
     "feq_edgewise_fwd_src": ([_P, _P, _I32, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
                              ctypes.c_int),
     "feq_edgewise_fwd_src_noalloc": ([_P, _P, _I32, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P],

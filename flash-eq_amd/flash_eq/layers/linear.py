@@ -21,7 +21,7 @@ import torch
 import torch.nn as nn
 
 from .. import _native as N
-from ..ops import (edgewise_attention_pool, edgewise_linear, edgewise_linear_src,
+from ..ops import (_use_hl, edgewise_attention_pool, edgewise_linear, edgewise_linear_src,
                    edgewise_pool_supported, edgewise_src_supported, embedding_for, rows_weight_grad,
                    BiasRowsFn, EqLinearFn)
 from ..representations import ProductRepr, Repr
@@ -122,8 +122,15 @@ class EquivariantEdgewiseLinear(nn.Module):
         N.require_cuda_tensor(edge_features, "edge_features")
         rw = self.radial_weights
         if edge_features.dtype == torch.float64:
-            return self._forward_f64(P, Q, edge_features, distances, graph)
+            return self._forward_composed(P, Q, edge_features, distances, graph, torch.float64)
         layout, binning = self.layout(), self.binning()
+        if not (_use_hl(edge_features, P, Q, layout, binning, rw.rank)
+                or N.lib().feq_edgewise_fused_supported(N.ctypes.byref(layout), N.ctypes.byref(binning),
+                                                        rw.rank)):
+            # wider than the fused kernels' LDS (e.g. lvals 0..6 at 64+ channels
+            # in float32): the reference's own composition, in float32
+            out = self._forward_composed(P, Q, edge_features, distances, graph, torch.float32)
+            return out.to(edge_features.dtype)
         if torch.is_grad_enabled() and (P.requires_grad or Q.requires_grad):
             # gradients for the bases: the kernels that form gP and gQ take
             # edge rows, so the gather (if any) happens first
@@ -162,12 +169,14 @@ class EquivariantEdgewiseLinear(nn.Module):
         return edgewise_linear(edge_features, P, Q, distances, rw.channel_patterns,
                                rw.radial_functions(), layout, binning, rw.rank)
 
-    def _forward_f64(self, P, Q, edge_features, distances, graph):
-        """float64: the reference's own composition (linear.py:131-160) -- x P by
+    def _forward_composed(self, P, Q, edge_features, distances, graph, dtype):
+        """The reference's own composition (linear.py:131-160) in ``dtype``: x P by
         library bmm, the block-diagonal op on the full radial table
-        (``block_diagonal_cuda``, whose float64 kernels are block_diagonal.cu:1332's
-        dispatch), then by Q^T -- every operand in float64 and every gradient
-        (features, bases, radial network, distances) by autograd through it."""
+        (``block_diagonal_cuda``: blockdiag.hip's kernels, float32 and float64 as
+        block_diagonal.cu:1332 dispatches), then by Q^T, every gradient
+        (features, bases, radial network, distances) by autograd through it.
+        float64 layers take it, and float32 layouts too wide for the fused
+        kernels (their table, (num_bins+1) Cout Cin Wdim floats, is formed)."""
         from ..cuda.block_diagonal import block_diagonal_cuda
         if graph is not None:
             if graph.num_edges != distances.shape[0]:
@@ -175,11 +184,11 @@ class EquivariantEdgewiseLinear(nn.Module):
             edge_features = edge_features.index_select(0, graph.src)
         rw = self.radial_weights
         p1, p2 = rw.binning_params()
-        f = torch.bmm(edge_features, P.to(torch.float64))
-        out = block_diagonal_cuda(f, rw().to(torch.float64), distances.to(torch.float64), self.product_repr,
+        f = torch.bmm(edge_features.to(dtype), P.to(dtype))
+        out = block_diagonal_cuda(f, rw().to(dtype), distances.to(dtype), self.product_repr,
                                   bin_param1=p1, bin_param2=p2, num_bins=rw.num_bins, log_bins=rw.log,
                                   sh_scale=self.solid_harmonic_scale)
-        return torch.bmm(out, Q.to(torch.float64).mT.contiguous())
+        return torch.bmm(out, Q.to(dtype).mT.contiguous())
 
     def attention_pool(self, P: torch.Tensor, Q: torch.Tensor, node_features: torch.Tensor,
                        distances: torch.Tensor, graph, attn: torch.Tensor, num_heads: int):

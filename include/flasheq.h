@@ -161,6 +161,15 @@ int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32_t rank, in
                      float* grad_x, float* grad_C, float* grad_F, float* grad_dist,
                      float* grad_P, float* grad_Q,
                      void* workspace, size_t ws_bytes, feq_stream_t stream);
+/* 1 when feq_edgewise_fwd and feq_edgewise_bwd have kernels for this layout
+ * and rank (the shape-generic pair keeps an edge's rows and the workgroup's
+ * channel-pattern gradient in at most 160 KB of LDS: Cin Din, Din^2, Dout^2,
+ * Cout Dout and K Cout Cin floats), else 0; they then return
+ * FEQ_ERR_UNSUPPORTED.  The reference accepts any layout with lmax <= 16
+ * (block_diagonal.cu:1298); a caller routes the others through the
+ * composition x P -> feq_blockdiag_* on the formed radial table -> Q^T
+ * (flash_eq/layers/linear.py:131-160). */
+int feq_edgewise_fused_supported(const feq_layout* L, const feq_binning* b, int32_t rank);
 
 /* ---- message-passing form of the fused layer ---------------------------------
  * The same layer with its input gathered inside the kernels: x is a node table
