@@ -658,6 +658,74 @@ extern "C" int feq_edgewise_bwd_src_nodes_ex(const feq_layout* L, const feq_binn
     return rc == -1 ? fail(FEQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned") : rc;
 }
 
+// ---- gradients for the bases on the split kernels --------------------------------------
+extern "C" int feq_edgewise_pq_supported(const feq_layout* L, const feq_binning* b, int32_t rank) {
+    if (!L || !b || check_layout(L) || check_binning(b)) return 0;
+    if (ew_path() != kPathSplit) return 0;
+    return ew_split_pq_supported(*L, *b, rank);
+}
+
+extern "C" int feq_edgewise_fwd_ym(const feq_layout* L, const feq_binning* b, int32_t rank, int64_t E,
+                                   const float* x, int64_t num_src, const int64_t* src, const float* P,
+                                   const float* Q, const float* dist, const float* C, const float* F,
+                                   float* y, float* ym, int32_t flags, void* ws, size_t ws_bytes,
+                                   feq_stream_t stream) {
+    if (int rc = check_layout(L)) return rc;
+    if (flags & ~FEQ_EW_HALF_ACCURACY) return fail(FEQ_ERR_INVALID, "unknown flags 0x%x", flags);
+    if (int rc = check_binning(b)) return rc;
+    if (rank < 1) return fail(FEQ_ERR_INVALID, "rank must be positive");
+    if (E < 0 || num_src < 0) return fail(FEQ_ERR_INVALID, "negative edge or node count");
+    if (E == 0) return FEQ_OK;
+    if (E > 0x7fffffffLL) return fail(FEQ_ERR_UNSUPPORTED, "more than 2^31-1 edges");
+    if (!x || !P || !Q || !dist || !C || !F || !y || !ym) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (!feq_edgewise_pq_supported(L, b, rank))
+        return fail(FEQ_ERR_UNSUPPORTED, "no kernels forming the bases' gradients for this layout");
+    const BasisGrads bg{ym, nullptr, nullptr, nullptr};
+    const int rc = ew_split_fwd(*L, *b, rank, E, x, src, src ? num_src : 0, P, Q, dist, C, F, y, ws,
+                                ws_bytes, src && (flags & FEQ_EW_HALF_ACCURACY) != 0, stream_of(stream),
+                                nullptr, &bg);
+    return rc == -1 ? fail(FEQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned") : rc;
+}
+
+extern "C" int feq_edgewise_bwd_pq(const feq_layout* L, const feq_binning* b, int32_t rank, int64_t E,
+                                   const float* gy, const float* x, int64_t num_src, const int64_t* src,
+                                   const int32_t* perm_src, const int32_t* offsets_src, const float* P,
+                                   const float* Q, const float* dist, const float* C, const float* F,
+                                   const float* ym, float* gx, float* gC, float* gF, float* gdist,
+                                   float* gP, float* gQ, int32_t flags, void* ws, size_t ws_bytes,
+                                   feq_stream_t stream) {
+    if (int rc = check_layout(L)) return rc;
+    if (flags & ~FEQ_EW_HALF_ACCURACY) return fail(FEQ_ERR_INVALID, "unknown flags 0x%x", flags);
+    if (int rc = check_binning(b)) return rc;
+    if (rank < 1) return fail(FEQ_ERR_INVALID, "rank must be positive");
+    if (E < 0 || num_src < 0) return fail(FEQ_ERR_INVALID, "negative edge or node count");
+    if (E > 0x7fffffffLL || num_src > 0x7fffffffLL)
+        return fail(FEQ_ERR_UNSUPPORTED, "more than 2^31-1 edges or nodes");
+    const bool nodes = src != nullptr;
+    if (!gC || !gF || !gx) return fail(FEQ_ERR_INVALID, "grad_x, grad_C and grad_F are required");
+    hipStream_t s = stream_of(stream);
+    if (E == 0) {
+        if (int rc = fill_zero(gF, static_cast<int64_t>(b->num_bins + 1) * rank * L->wdim, s)) return rc;
+        if (nodes)
+            if (int rc = fill_zero(gx, num_src * L->cin * L->din, s)) return rc;
+        return fill_zero(gC, static_cast<int64_t>(rank) * L->cout * L->cin, s);
+    }
+    if (!gy || !x || !P || !Q || !dist || !C || !F || (nodes && (!perm_src || !offsets_src)))
+        return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (gQ && !ym) return fail(FEQ_ERR_INVALID, "grad_Q needs ym, the rows before the rotation");
+    if (!feq_edgewise_pq_supported(L, b, rank))
+        return fail(FEQ_ERR_UNSUPPORTED, "no kernels forming the bases' gradients for this layout");
+    const size_t need = nodes ? feq_edgewise_bwd_src_nodes_workspace(L, b, rank, E)
+                              : feq_edgewise_workspace(L, b, rank, E);
+    if (!ws || ws_bytes < need) return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
+    const BasisGrads bg{nullptr, ym, gP, gQ};
+    const NodeScatter ns{perm_src, offsets_src, gx, nullptr};
+    const int rc = ew_split_bwd(*L, *b, rank, E, gy, x, src, nodes ? num_src : 0, P, Q, dist, C, F,
+                                nodes ? nullptr : gx, gC, gF, gdist, nodes ? &ns : nullptr, ws, ws_bytes,
+                                nodes && (flags & FEQ_EW_HALF_ACCURACY) != 0, s, nullptr, &bg);
+    return rc == -1 ? fail(FEQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned") : rc;
+}
+
 // ---- message-passing form fused with the attention's head weighting and sum pooling ----
 namespace {
 int check_pool_args(const feq_layout* L, int32_t heads, int32_t chan_per_head) {

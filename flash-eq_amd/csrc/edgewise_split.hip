@@ -441,6 +441,20 @@ __device__ __forceinline__ int off_block_nonzero_rows(const float (&v)[NR], unsi
 // v_permlane16_swap (odd rows of the first operand <-> even rows of the second)
 // and one v_permlane32_swap (upper half of the first <-> lower half of the
 // second) instead of eight cross-lane shuffles.
+// Sum over the 16 lanes of a row (every lane receives it): lane swaps within
+// quads, then the half-row and row mirrors (DPP).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+    v += dpp_f<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+    v += dpp_f<0x141>(v);   // row_half_mirror: quads 0 <-> 1, 2 <-> 3
+    v += dpp_f<0x140>(v);   // row_mirror: half-rows 0 <-> 1
+    return v;
+}
+
 __device__ __forceinline__ float quad_lane_sums(const float (&v)[4]) {
     const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[0]), __float_as_uint(v[1]), false, false);
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[2]), __float_as_uint(v[3]), false, false);
@@ -548,14 +562,16 @@ __device__ __forceinline__ void edge_powers(float s, int n, float* out) {
 // (DP.perm), and the staged tile is summed per destination node with the
 // attention weights (scatter_stage_w) instead of stored per edge; y, when not
 // NULL, receives the unweighted rows in that position order.
-template <int CIN, int COUT, int LIN, int LOUT, int K, int OCC, bool GATHER, bool LP, bool POOL>
+template <int CIN, int COUT, int LIN, int LOUT, int K, int OCC, bool GATHER, bool LP, bool POOL,
+          bool YM = false>
 __global__ void __launch_bounds__(kThreads, OCC)
 k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
           const float* __restrict__ P, const float* __restrict__ Q,
           const float* __restrict__ dist, const h8* __restrict__ Cfrag,
           const float* __restrict__ Cinv, const float* __restrict__ F, float* __restrict__ y,
-          DstPool DP) {
+          DstPool DP, float* __restrict__ ym) {
     static_assert(GATHER || !POOL, "the pooled form is a message-passing form");
+    static_assert(!(YM && POOL), "the rows before the rotation are kept in edge order");
     using T = Canon<LIN, LOUT>;
     using TG = TermGroups<LIN, LOUT, false>;
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
@@ -857,6 +873,22 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
         if (!POOL || y) flush_stage<COUT, DOUT>(reinterpret_cast<const float*>(sB), y + e0 * COUT * DOUT, nval);
         if constexpr (POOL)
             scatter_stage_w<COUT, DOUT>(reinterpret_cast<const float*>(sB), sNode, sW, DP, tile, nval);
+        if constexpr (YM) {
+            // the rows before the rotation (the block-diagonal output m, y = m
+            // Q^T), kept for the gradient of Q: staged and stored like y
+            __syncthreads();   // the y stage is read
+#pragma unroll
+            for (int j = 0; j < RPW; ++j) {
+                float out[4 * DOUT];
+#pragma unroll
+                for (int o = 0; o < DOUT; ++o)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) out[r * DOUT + o] = yv[j][o][r];
+                stage_rows<COUT, DOUT>(reinterpret_cast<float*>(sB), le, 16 * (wave + 4 * j) + 4 * lg, out);
+            }
+            __syncthreads();
+            flush_stage<COUT, DOUT>(reinterpret_cast<const float*>(sB), ym + e0 * COUT * DOUT, nval);
+        }
     }
 }
 
@@ -877,16 +909,19 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
 //
 // GP (pooled form): gy is the pooled output's gradient (ndst rows) and edge e
 // reads attn[e, head(c)] gy[dst[e], c, :] (DstPool).
-template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER, bool SCATTER, bool LP, bool GP>
+template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER, bool SCATTER, bool LP, bool GP,
+          bool GPQ = false>
 __global__ void __launch_bounds__(kThreads, 2)
 k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
             XRows X, const float* __restrict__ P,
             const float* __restrict__ Q, const float* __restrict__ dist,
             const h8* __restrict__ Cfrag, const float* __restrict__ Cinv,
             const float* __restrict__ F, float* __restrict__ gx, float* __restrict__ dFe,
-            NodeScatter NS, DstPool DP) {
+            NodeScatter NS, DstPool DP, const float* __restrict__ ym, float* __restrict__ gPo,
+            float* __restrict__ gQo) {
     static_assert(GATHER || !SCATTER, "the per-node sums need the message-passing form");
     static_assert(SCATTER || !GP, "the pooled form sums the input gradient per source node");
+    static_assert(!(GPQ && GP), "the bases' gradients are formed for per-edge gradients of y");
     using T = Canon<LIN, LOUT>;
     using TG = TermGroups<LIN, LOUT, true>;
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
@@ -930,6 +965,7 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
     // lane layout, P, Q, distances (zeros past the last edge)
     float gr[NPR][4 * DOUT];
     float gw[NPR];   // GP: attention weight of the producer's channels (0 without a destination)
+    int64_t gqe[NPR];   // GPQ: the producer's edge (-1: none)
     float xl[RPW][4 * DIN];
     // P and Q of the prefetched tile: each thread's share of one edge row
     float prs[rows_per_thread<DIN * DIN>()], qrs[rows_per_thread<DOUT * DOUT>()];
@@ -997,6 +1033,7 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 #pragma unroll
                 for (int v = 0; v < 4 * DOUT; ++v) gr[p][v] = 0.0f;
             }
+            if constexpr (GPQ) gqe[p] = grow[p];   // without GP the gy row of a producer is its edge's row
         }
 #pragma unroll
         for (int j = 0; j < RPW; ++j) {
@@ -1110,6 +1147,47 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             produce(std::false_type{});
         else
             produce(std::true_type{});
+        if constexpr (GPQ) {
+            // gQ[e][d][o] = sum over the edge's channels c of gy[c][d] m[c][o]:
+            // each producer's four channels, then the sum over the 16 producers
+            // of the edge (one 16-lane row), stored by the row's first lane
+            static_assert(NC4 == 16 && NPR == 1, "one edge per 16-lane row of producers");
+            if (gQo) {
+                const int c4 = tid % NC4;
+#pragma unroll
+                for (int p = 0; p < NPR; ++p) {
+                    // the producer's rows of m (y = m Q^T), loaded here rather
+                    // than with the tile's prefetch, whose registers stay live
+                    // through the previous tile's epilogue
+                    float yk[4 * DOUT];
+                    if (gqe[p] >= 0) {
+                        const float4* src = reinterpret_cast<const float4*>(ym + (gqe[p] * COUT + 4 * c4) * DOUT);
+#pragma unroll
+                        for (int v = 0; v < DOUT; ++v) {
+                            const float4 f = src[v];
+                            yk[4 * v] = f.x;
+                            yk[4 * v + 1] = f.y;
+                            yk[4 * v + 2] = f.z;
+                            yk[4 * v + 3] = f.w;
+                        }
+                    } else {
+#pragma unroll
+                        for (int v = 0; v < 4 * DOUT; ++v) yk[v] = 0.0f;
+                    }
+                    float* dst = gQo + (gqe[p] >= 0 ? gqe[p] : 0) * DOUT * DOUT;
+#pragma unroll
+                    for (int d = 0; d < DOUT; ++d)
+#pragma unroll
+                        for (int o = 0; o < DOUT; ++o) {
+                            float a = 0.0f;
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) a += gr[p][r * DOUT + d] * yk[r * DOUT + o];
+                            a = row16_sum(a);
+                            if (c4 == 0 && gqe[p] >= 0) dst[d * DOUT + o] = a;
+                        }
+                }
+            }
+        }
         __syncthreads();
 
         // GEMM per output slot o, rank components in passes of KP; contractions
@@ -1234,6 +1312,58 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 
         // next tile's global loads, then dx = dfs P^T / scale_e (s^l_in is in
         // the radial functions) staged in LDS, and the dF_e sums over the waves
+        constexpr int kGPQuads = (DIN * DIN + 3) / 4;
+        float gpl[GPQ ? kGPQuads : 1];   // GPQ: gP partials, lane group g holds value 4 q + g
+        if constexpr (GPQ) {
+            // gP[e][d][i] = sum over the channels c of x[c][d] (dL/df)[c][i]
+            // with dL/df = dfs / scale_e: this lane's rows (x reloaded; before
+            // the next tile's prefetch, so that its registers are free), then
+            // the sum over the wave's four lane groups; the four waves are
+            // summed after the tile's stores
+            if (gPo) {
+                const float sc = sEinv[le];
+                int64_t xr0;
+                if constexpr (SCATTER)
+                    xr0 = e0 + le < E ? NS.src_pos[e0 + le] : -1;
+                else
+                    xr0 = e0 + le < E ? x_row<GATHER>(X, e0 + le) : -1;
+                float xg[RPW][4 * DIN];
+#pragma unroll
+                for (int j = 0; j < RPW; ++j) {
+                    if (xr0 >= 0) {
+                        const float4* src = reinterpret_cast<const float4*>(
+                            X.x + (xr0 * CIN + 16 * (wave + 4 * j) + 4 * lg) * DIN);
+#pragma unroll
+                        for (int v = 0; v < DIN; ++v) {
+                            const float4 f = src[v];
+                            xg[j][4 * v] = f.x;
+                            xg[j][4 * v + 1] = f.y;
+                            xg[j][4 * v + 2] = f.z;
+                            xg[j][4 * v + 3] = f.w;
+                        }
+                    } else {
+#pragma unroll
+                        for (int v = 0; v < 4 * DIN; ++v) xg[j][v] = 0.0f;
+                    }
+                }
+                static_for<kGPQuads>([&](auto QQ) {
+                    constexpr int q = decltype(QQ)::value;
+                    float v[4];
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int n = 4 * q + g, d = n / DIN, i = n % DIN;
+                        float a = 0.0f;
+                        if (n < DIN * DIN)
+#pragma unroll
+                            for (int j = 0; j < RPW; ++j)
+#pragma unroll
+                                for (int r = 0; r < 4; ++r) a += xg[j][r * DIN + d] * dfs[j][r][i];
+                        v[g] = a;
+                    }
+                    gpl[q] = quad_lane_sums(v) * sc;
+                });
+            }
+        }
         load_tile(tile + gridDim.x);
         __syncthreads();   // fragments consumed, dF_e partials complete
         {
@@ -1277,6 +1407,25 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             scatter_stage<CIN, DIN>(reinterpret_cast<const float*>(sB), sNode, NS, tile, nval);
         else
             flush_stage<CIN, DIN>(reinterpret_cast<const float*>(sB), gx + e0 * CIN * DIN, nval);
+        if constexpr (GPQ) {
+            if (gPo) {
+                // the four waves' partials through the (now read) stage buffer
+                constexpr int GS = 4 * kGPQuads;
+                float* sG = reinterpret_cast<float*>(sB);   // [wave][edge][GS]
+                static_assert(4 * kNE * GS * sizeof(float) <= BREG, "gP partials fit the stage");
+                __syncthreads();
+#pragma unroll
+                for (int q = 0; q < kGPQuads; ++q) sG[(wave * kNE + le) * GS + 4 * q + lg] = gpl[q];
+                __syncthreads();
+                for (int idx = tid; idx < nval * DIN * DIN; idx += kThreads) {
+                    const int e = idx / (DIN * DIN), n = idx % (DIN * DIN);
+                    const float a = sG[e * GS + n] + sG[(kNE + e) * GS + n] + sG[(2 * kNE + e) * GS + n] +
+                                    sG[(3 * kNE + e) * GS + n];
+                    const int64_t ed = SCATTER ? static_cast<int64_t>(sEid[e]) : e0 + e;
+                    gPo[ed * DIN * DIN + n] = a;
+                }
+            }
+        }
     }
 }
 
@@ -1659,7 +1808,7 @@ __global__ void k_pool_order(int64_t E, const int32_t* __restrict__ perm, const 
 template <int CIN, int COUT, int LIN, int LOUT, int K, bool GATHER>
 int launch_ews_fwd(const feq_binning& B, int64_t E, XRows x, const float* P, const float* Q,
                    const float* dist, const float* C, const float* F, float* y, void* ws,
-                   size_t ws_bytes, bool lp, const DstPool* dp, hipStream_t s) {
+                   size_t ws_bytes, bool lp, const DstPool* dp, hipStream_t s, float* ym) {
     using T = Canon<LIN, LOUT>;
     constexpr size_t lds = ews_fwd_lds<CIN, COUT, LIN, LOUT, K>();
     constexpr int occ = ews_fwd_occ<CIN, COUT, LIN, LOUT, K>();
@@ -1698,11 +1847,17 @@ int launch_ews_fwd(const feq_binning& B, int64_t E, XRows x, const float* P, con
     } else {
         if (dp) return fail(FEQ_ERR_INVALID, "the pooled form needs the message-passing form");
     }
+    if (ym) {
+        if (dp) return fail(FEQ_ERR_UNSUPPORTED, "the pooled form keeps no rows before the rotation");
+        // (one fp16 product per pair only in the message-passing form)
+        kern = lp ? k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, GATHER, GATHER, false, true>
+                  : k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, GATHER, false, false, true>;
+    }
     if (int rc = ews_set_lds(reinterpret_cast<const void*>(kern), lds)) return rc;
     const int64_t g = static_cast<int64_t>(ews_cus()) * occ;
     const int grid = static_cast<int>(ntiles < g ? ntiles : g);
     FEQ_LAUNCH("k_ews_fwd", kern, dim3(grid), dim3(kThreads), lds, s, B, E, ntiles, X, P, Q, dist,
-               frag, inv, F, y, DP);
+               frag, inv, F, y, DP, ym);
     if (dp) {
         const NodeScatter NS{DP.perm, DP.offsets, DP.out, DP.part};
         if (int rc = node_fix(NS, DP.ndst, static_cast<int64_t>(COUT * T::DOUT / 4), s)) return rc;
@@ -1752,7 +1907,7 @@ int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const f
                    XRows x, const float* P, const float* Q, const float* dist,
                    const float* C, const float* F, float* gx, float* gC, float* gF, float* gdist,
                    const NodeScatter* ns, void* ws, size_t ws_bytes, bool lp, const DstPool* dp,
-                   hipStream_t s) {
+                   hipStream_t s, const BasisGrads* bg) {
     using T = Canon<LIN, LOUT>;
     constexpr size_t xlds = ews_bwd_x_lds<CIN, COUT, LIN, LOUT, K>();
     constexpr size_t clds = ews_bwd_c_lds<CIN, COUT, LIN, LOUT, K>();
@@ -1779,6 +1934,12 @@ int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const f
     }
     if (!ws || cv.used > ws_bytes) return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
     if (dp && !ns) return fail(FEQ_ERR_INVALID, "the pooled form needs the per-node input gradient");
+    const bool gpq = bg && (bg->gP || bg->gQ);
+    if (gpq && dp) return fail(FEQ_ERR_UNSUPPORTED, "no gradients for the bases in the pooled form");
+    if (bg && bg->gQ && !bg->ym) return fail(FEQ_ERR_INVALID, "grad_Q needs the rows before the rotation");
+    const float* bym = bg ? bg->ym : nullptr;
+    float* bgP = bg ? bg->gP : nullptr;
+    float* bgQ = bg ? bg->gQ : nullptr;
     const DstPool DP = dp ? *dp : DstPool{};
     if (ns) {
         if (!x.src) return fail(FEQ_ERR_INVALID, "per-node sums need the message-passing form");
@@ -1797,9 +1958,12 @@ int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const f
             if (dp)
                 kx = lp ? k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, true, true>
                         : k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, false, true>;
+            else if (gpq)
+                kx = lp ? k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, true, false, true>
+                        : k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, false, false, true>;
             if (int rc = ews_set_lds(reinterpret_cast<const void*>(kx), xlds)) return rc;
             FEQ_LAUNCH("k_ews_bwd_x", kx, dim3(G), dim3(kThreads), xlds, s, B, E, ntiles, gy, x, P, Q,
-                       dist, frag, inv, F, nullptr, dFe, NS, DP);
+                       dist, frag, inv, F, nullptr, dFe, NS, DP, bym, bgP, bgQ);
             if (int rc = node_fix(NS, x.nsrc, static_cast<int64_t>(CIN * T::DIN / 4), s)) return rc;
         }
         if (dp)
@@ -1811,10 +1975,11 @@ int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const f
         if (ns) return fail(FEQ_ERR_INVALID, "per-node sums need the message-passing form");
     }
     if (!ns) {
-        auto kx = k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, GATHER, false, false, false>;
+        auto kx = gpq ? k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, GATHER, false, false, false, true>
+                      : k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, GATHER, false, false, false>;
         if (int rc = ews_set_lds(reinterpret_cast<const void*>(kx), xlds)) return rc;
         FEQ_LAUNCH("k_ews_bwd_x", kx, dim3(G), dim3(kThreads), xlds, s, B, E, ntiles, gy, x, P, Q,
-                   dist, frag, inv, F, gx, dFe, NS, DP);
+                   dist, frag, inv, F, gx, dFe, NS, DP, bym, bgP, bgQ);
     }
     if (int rc = ews_set_lds(reinterpret_cast<const void*>(kc), clds)) return rc;
     FEQ_LAUNCH("k_ews_bwd_c", kc, dim3(G), dim3(kThreads), clds, s, B, E, ntiles, gy, x, P, Q,
@@ -1886,13 +2051,14 @@ int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
                  const float* x, const int64_t* src, int64_t nsrc, const float* P, const float* Q,
                  const float* dist, const float* C, const float* F, float* gx, float* gC, float* gF,
                  float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, bool lp, hipStream_t s,
-                 const DstPool* dp) {
+                 const DstPool* dp, const BasisGrads* bg) {
     float* gout = ns ? ns->out : gx;
     if (rank != 4 || !gout || !aligned16(gy) || !aligned16(x) || !aligned16(P) || !aligned16(Q) ||
         !aligned16(gout) || (ns && !src))
         return -1;
     if (ew0_supported(L, rank)) {
         if (dp) return fail(FEQ_ERR_UNSUPPORTED, "no pooled form for scalar-output layouts");
+        if (bg && (bg->gP || bg->gQ)) return -1;
         return ew0_bwd(L, B, rank, E, gy, x, src, nsrc, P, Q, dist, C, F, gx, gC, gF, gdist, ns, ws,
                        ws_bytes, s);
     }
@@ -1902,9 +2068,9 @@ int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
     if constexpr ((ci) % 64 == 0) {                                                               \
         if (L.cin == ci && L.cout == co && canonical(L, li, lo))                                  \
             return src ? launch_ews_bwd<ci, co, li, lo, 4, true>(L, B, E, gy, X, P, Q, dist, C, F, \
-                                                                 gx, gC, gF, gdist, ns, ws, ws_bytes, lp, dp, s) \
+                                                                 gx, gC, gF, gdist, ns, ws, ws_bytes, lp, dp, s, bg) \
                        : launch_ews_bwd<ci, co, li, lo, 4, false>(L, B, E, gy, X, P, Q, dist, C, F, \
-                                                                  gx, gC, gF, gdist, ns, ws, ws_bytes, lp, dp, s); \
+                                                                  gx, gC, gF, gdist, ns, ws, ws_bytes, lp, dp, s, bg); \
     }
     FEQ_EWS_SHAPES(FEQ_BWD)
 #undef FEQ_BWD
@@ -1914,22 +2080,25 @@ int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
 int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
                  const int64_t* src, int64_t nsrc, const float* P, const float* Q, const float* dist,
                  const float* C, const float* F, float* y, void* ws, size_t ws_bytes, bool lp,
-                 hipStream_t s, const DstPool* dp) {
+                 hipStream_t s, const DstPool* dp, const BasisGrads* bg) {
     if (rank != 4) return -1;
+    float* ym = bg ? bg->ym_out : nullptr;
     if (ew0_supported(L, rank)) {
         if (dp) return fail(FEQ_ERR_UNSUPPORTED, "no pooled form for scalar-output layouts");
+        if (ym) return -1;
         return ew0_fwd(L, B, rank, E, x, src, nsrc, P, Q, dist, C, F, y, s);
     }
-    if (!aligned16(x) || !aligned16(P) || !aligned16(Q) || !aligned16(y) || (dp && !aligned16(dp->out)))
+    if (!aligned16(x) || !aligned16(P) || !aligned16(Q) || !aligned16(y) || (dp && !aligned16(dp->out)) ||
+        (ym && !aligned16(ym)))
         return -1;
     if (dp && !src) return fail(FEQ_ERR_INVALID, "the pooled form needs the message-passing form");
     const XRows X{x, src, nsrc};
 #define FEQ_FWD(ci, co, li, lo)                                                                  \
     if (L.cin == ci && L.cout == co && canonical(L, li, lo))                                     \
         return src ? launch_ews_fwd<ci, co, li, lo, 4, true>(B, E, X, P, Q, dist, C, F, y, ws,    \
-                                                             ws_bytes, lp, dp, s)                 \
+                                                             ws_bytes, lp, dp, s, ym)             \
                    : launch_ews_fwd<ci, co, li, lo, 4, false>(B, E, X, P, Q, dist, C, F, y, ws,   \
-                                                              ws_bytes, lp, dp, s);
+                                                              ws_bytes, lp, dp, s, ym);
     FEQ_EWS_SHAPES(FEQ_FWD)
 #undef FEQ_FWD
     return -1;
@@ -1946,6 +2115,10 @@ bool ew_split_supported(const feq_layout& L, const feq_binning& B, int rank, boo
     FEQ_EWS_SHAPES(FEQ_SUP)
 #undef FEQ_SUP
     return ok;
+}
+
+bool ew_split_pq_supported(const feq_layout& L, const feq_binning& B, int rank) {
+    return rank == 4 && !ew0_supported(L, rank) && ew_split_supported(L, B, rank, true);
 }
 
 bool ew_pool_supported(const feq_layout& L, const feq_binning& B, int rank) {

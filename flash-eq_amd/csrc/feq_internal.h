@@ -129,6 +129,18 @@ struct DstPool {
     const float* dist_pos;    // forward: distance by CSR position
 };
 
+// Gradients for the bases on the split kernels, with y = m Q^T and f = x P (m:
+// the block-diagonal output before the rotation): the forward writes m to
+// ym_out (E, Cout, Dout) in edge order when it is not NULL; the backward reads
+// it back from ym and writes gQ (E, Dout, Dout) = gy^T m and gP (E, Din, Din) =
+// x^T dL/df per edge when they are not NULL.
+struct BasisGrads {
+    float* ym_out;
+    const float* ym;
+    float* gP;
+    float* gQ;
+};
+
 // Split-fp16 fast paths (edgewise_split.hip); -1 when the shape has none.
 size_t ew_split_workspace(const feq_layout& L, int rank);
 // nodes: with the per-node sums (NodeScatter partial rows).
@@ -143,14 +155,17 @@ int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
                  const float* x, const int64_t* src, int64_t nsrc, const float* P, const float* Q,
                  const float* dist, const float* C, const float* F, float* gx, float* gC, float* gF,
                  float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, bool lp, hipStream_t s,
-                 const DstPool* dp = nullptr);
+                 const DstPool* dp = nullptr, const BasisGrads* bg = nullptr);
 // dp (may be NULL, needs src): the pooled form; y then receives the per-edge
 // rows in destination order, or is NULL.
 int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
                  const int64_t* src, int64_t nsrc, const float* P, const float* Q, const float* dist,
                  const float* C, const float* F, float* y, void* ws, size_t ws_bytes, bool lp,
-                 hipStream_t s, const DstPool* dp = nullptr);
+                 hipStream_t s, const DstPool* dp = nullptr, const BasisGrads* bg = nullptr);
 bool ew_split_supported(const feq_layout& L, const feq_binning& B, int rank, bool backward);
+// Layouts whose split kernels form the bases' gradients (BasisGrads): the
+// split shapes with a backward, not the scalar-output family.
+bool ew_split_pq_supported(const feq_layout& L, const feq_binning& B, int rank);
 // Layouts with the pooled form (the split shapes with Cin = 64, not the
 // scalar-output family) and its forward workspace.
 bool ew_pool_supported(const feq_layout& L, const feq_binning& B, int rank);

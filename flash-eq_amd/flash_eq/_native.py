@@ -71,6 +71,14 @@ _SIGS = {
                           _P, _P, _P, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
     "feq_edgewise_src_supported": ([_P, _P, _I32], ctypes.c_int),
     "feq_edgewise_fused_supported": ([_P, _P, _I32], ctypes.c_int),
+    "feq_edgewise_pq_supported": ([_P, _P, _I32], ctypes.c_int),
+    # L, b, rank, E, x, num_src, src, P, Q, dist, C, F, y, ym, flags, ws, ws_bytes, stream
+    "feq_edgewise_fwd_ym": ([_P, _P, _I32, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _SZ,
+                             _P], ctypes.c_int),
+    # L, b, rank, E, gy, x, num_src, src, perm_src, offsets_src, P, Q, dist, C, F, ym,
+    # gx, gC, gF, gdist, gP, gQ, flags, ws, ws_bytes, stream
+    "feq_edgewise_bwd_pq": ([_P, _P, _I32, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                             _P, _P, _P, _P, _P, _P, _I32, _P, _SZ, _P], ctypes.c_int),
     "feq_edgewise_fwd_src": ([_P, _P, _I32, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
                              ctypes.c_int),
     "feq_edgewise_fwd_src_noalloc": ([_P, _P, _I32, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P],

@@ -22,8 +22,8 @@ import torch.nn as nn
 
 from .. import _native as N
 from ..ops import (_use_hl, edgewise_attention_pool, edgewise_linear, edgewise_linear_src,
-                   edgewise_pool_supported, edgewise_src_supported, embedding_for, rows_weight_grad,
-                   BiasRowsFn, EqLinearFn)
+                   edgewise_pool_supported, edgewise_pq_supported, edgewise_src_supported,
+                   embedding_for, rows_weight_grad, BiasRowsFn, EqLinearFn)
 from ..representations import ProductRepr, Repr
 from .radial import SeparableRadialNet
 from ..utils import half_precision_active
@@ -131,16 +131,18 @@ class EquivariantEdgewiseLinear(nn.Module):
             # in float32): the reference's own composition, in float32
             out = self._forward_composed(P, Q, edge_features, distances, graph, torch.float32)
             return out.to(edge_features.dtype)
-        if torch.is_grad_enabled() and (P.requires_grad or Q.requires_grad):
-            # gradients for the bases: the kernels that form gP and gQ take
-            # edge rows, so the gather (if any) happens first
+        emb = self._embedding(edge_features, distances.shape[0], layout, binning)
+        if (torch.is_grad_enabled() and (P.requires_grad or Q.requires_grad)
+                and not edgewise_pq_supported(emb.layout if emb is not None else layout, binning, rw.rank)):
+            # gradients for the bases without split kernels that form them: the
+            # shape-generic kernels do, on edge rows, so the gather (if any)
+            # happens first
             if graph is not None:
                 if graph.num_edges != distances.shape[0]:
                     raise ValueError(f"graph has {graph.num_edges} edges, distances {distances.shape[0]}")
                 edge_features = graph.gather_src(edge_features)
             return edgewise_linear(edge_features, P, Q, distances, rw.channel_patterns,
                                    rw.radial_functions(), layout, binning, rw.rank)
-        emb = self._embedding(edge_features, distances.shape[0], layout, binning)
         if emb is not None:
             # a small layout without split-fp16 backward kernels: run it
             # zero-embedded in the [0,1,2]x64 kernels (ops._Embedding)

@@ -61,29 +61,40 @@ class EdgewiseLinearFn(torch.autograd.Function):
         rs, Cs, Fs = _f32(dist, "distances"), _f32(C, "channel_patterns"), _f32(F, "radial")
         _check_edgewise_shapes(layout, binning, rank, xs, Ps, Qs, rs, Cs, Fs)
         y = torch.empty(E, layout.cout, layout.dout, dtype=torch.float32, device=dev)
+        # gradients for the bases on the split kernels: keep the rows before
+        # the Q rotation (feq_edgewise_fwd_ym / _bwd_pq)
+        keep = E > 0 and (ctx.needs_input_grad[1] or ctx.needs_input_grad[2]) and \
+            edgewise_pq_supported(layout, binning, rank)
+        ym = torch.empty_like(y) if keep else None
         if E:
             lib = N.lib()
             ws = N.workspace(lib.feq_edgewise_fwd_workspace(N.ctypes.byref(layout),
                                                             N.ctypes.byref(binning), rank, E), dev)
             with torch.cuda.device(dev):
-                rc = lib.feq_edgewise_fwd(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
-                                          N.ptr(xs), N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs),
-                                          N.ptr(Fs), N.ptr(y), N.ptr(ws), ws.numel(),
-                                          N.stream_ptr(dev))
-            N.check(rc, "feq_edgewise_fwd")
-        ctx.save_for_backward(xs, Ps, Qs, rs, Cs, Fs)
+                if keep:
+                    rc = lib.feq_edgewise_fwd_ym(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
+                                                 N.ptr(xs), 0, None, N.ptr(Ps), N.ptr(Qs), N.ptr(rs),
+                                                 N.ptr(Cs), N.ptr(Fs), N.ptr(y), N.ptr(ym), 0, N.ptr(ws),
+                                                 ws.numel(), N.stream_ptr(dev))
+                else:
+                    rc = lib.feq_edgewise_fwd(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
+                                              N.ptr(xs), N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs),
+                                              N.ptr(Fs), N.ptr(y), N.ptr(ws), ws.numel(),
+                                              N.stream_ptr(dev))
+            N.check(rc, "feq_edgewise_fwd_ym" if keep else "feq_edgewise_fwd")
+        ctx.save_for_backward(xs, Ps, Qs, rs, Cs, Fs, ym)
         ctx.meta = (layout, binning, rank, x.dtype, P.dtype, Q.dtype, dist.dtype, C.dtype, F.dtype)
         return y.to(x.dtype)
 
     @staticmethod
     def backward(ctx, gy):
-        xs, Ps, Qs, rs, Cs, Fs = ctx.saved_tensors
+        xs, Ps, Qs, rs, Cs, Fs, ym = ctx.saved_tensors
         layout, binning, rank, xdt, pdt, qdt, rdt, cdt, fdt = ctx.meta
         dev = xs.device
         E = xs.shape[0]
         need = ctx.needs_input_grad
         g = gy.detach().to(torch.float32).contiguous()
-        gx = torch.empty_like(xs) if need[0] else None
+        gx = torch.empty_like(xs) if (need[0] or ym is not None) else None
         gP = torch.empty_like(Ps) if need[1] else None
         gQ = torch.empty_like(Qs) if need[2] else None
         gr = torch.empty_like(rs) if need[3] else None
@@ -93,12 +104,21 @@ class EdgewiseLinearFn(torch.autograd.Function):
         ws = N.workspace(lib.feq_edgewise_workspace(N.ctypes.byref(layout), N.ctypes.byref(binning),
                                                     rank, E), dev)
         with torch.cuda.device(dev):
-            rc = lib.feq_edgewise_bwd(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
-                                      N.ptr(g), N.ptr(xs), N.ptr(Ps), N.ptr(Qs), N.ptr(rs),
-                                      N.ptr(Cs), N.ptr(Fs), N.ptr(gx), N.ptr(gC), N.ptr(gF),
-                                      N.ptr(gr), N.ptr(gP), N.ptr(gQ), N.ptr(ws), ws.numel(),
-                                      N.stream_ptr(dev))
-        N.check(rc, "feq_edgewise_bwd")
+            if ym is not None:
+                rc = lib.feq_edgewise_bwd_pq(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
+                                             N.ptr(g), N.ptr(xs), 0, None, None, None, N.ptr(Ps), N.ptr(Qs),
+                                             N.ptr(rs), N.ptr(Cs), N.ptr(Fs), N.ptr(ym), N.ptr(gx),
+                                             N.ptr(gC), N.ptr(gF), N.ptr(gr), N.ptr(gP), N.ptr(gQ), 0,
+                                             N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+            else:
+                rc = lib.feq_edgewise_bwd(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
+                                          N.ptr(g), N.ptr(xs), N.ptr(Ps), N.ptr(Qs), N.ptr(rs),
+                                          N.ptr(Cs), N.ptr(Fs), N.ptr(gx), N.ptr(gC), N.ptr(gF),
+                                          N.ptr(gr), N.ptr(gP), N.ptr(gQ), N.ptr(ws), ws.numel(),
+                                          N.stream_ptr(dev))
+        N.check(rc, "feq_edgewise_bwd_pq" if ym is not None else "feq_edgewise_bwd")
+        if not need[0]:
+            gx = None
         cast = lambda t, dt: None if t is None else t.to(dt)
         return (cast(gx, xdt), cast(gP, pdt), cast(gQ, qdt), cast(gr, rdt),
                 gC.to(cdt) if need[4] else None, gF.to(fdt) if need[5] else None,
@@ -131,29 +151,42 @@ class EdgewiseLinearSrcFn(torch.autograd.Function):
         si = src.to(torch.int64).contiguous()
         flags = N.FEQ_EW_HALF_ACCURACY if half_accuracy else 0
         y = torch.empty(E, layout.cout, layout.dout, dtype=torch.float32, device=dev)
+        keep = E > 0 and (ctx.needs_input_grad[4] or ctx.needs_input_grad[5])
+        if keep and not edgewise_pq_supported(layout, binning, rank):
+            raise ValueError("no message-passing kernels forming gradients for P and Q for this layout; "
+                             "gather the rows and call edgewise_linear")
+        ym = torch.empty_like(y) if keep else None
         if E:
             lib = N.lib()
             ws = N.workspace(lib.feq_edgewise_fwd_workspace(N.ctypes.byref(layout),
                                                             N.ctypes.byref(binning), rank, E), dev)
             with torch.cuda.device(dev):
-                rc = lib.feq_edgewise_fwd_src_ex(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
+                if keep:
+                    rc = lib.feq_edgewise_fwd_ym(N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E,
                                                  N.ptr(xs), xs.shape[0], N.ptr(si), N.ptr(Ps), N.ptr(Qs),
-                                                 N.ptr(rs), N.ptr(Cs), N.ptr(Fs), N.ptr(y), flags,
+                                                 N.ptr(rs), N.ptr(Cs), N.ptr(Fs), N.ptr(y), N.ptr(ym), flags,
                                                  N.ptr(ws), ws.numel(), N.stream_ptr(dev))
-            N.check(rc, "feq_edgewise_fwd_src_ex")
-        ctx.save_for_backward(xs, si, perm, offsets, Ps, Qs, rs, Cs, Fs)
-        ctx.meta = (layout, binning, rank, x.dtype, dist.dtype, C.dtype, F.dtype, flags)
+                else:
+                    rc = lib.feq_edgewise_fwd_src_ex(N.ctypes.byref(layout), N.ctypes.byref(binning), rank,
+                                                     E, N.ptr(xs), xs.shape[0], N.ptr(si), N.ptr(Ps),
+                                                     N.ptr(Qs), N.ptr(rs), N.ptr(Cs), N.ptr(Fs), N.ptr(y),
+                                                     flags, N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+            N.check(rc, "feq_edgewise_fwd_ym" if keep else "feq_edgewise_fwd_src_ex")
+        ctx.save_for_backward(xs, si, perm, offsets, Ps, Qs, rs, Cs, Fs, ym)
+        ctx.meta = (layout, binning, rank, x.dtype, P.dtype, Q.dtype, dist.dtype, C.dtype, F.dtype, flags)
         return y.to(x.dtype)
 
     @staticmethod
     def backward(ctx, gy):
-        xs, si, perm, offsets, Ps, Qs, rs, Cs, Fs = ctx.saved_tensors
-        layout, binning, rank, xdt, rdt, cdt, fdt, flags = ctx.meta
+        xs, si, perm, offsets, Ps, Qs, rs, Cs, Fs, ym = ctx.saved_tensors
+        layout, binning, rank, xdt, pdt, qdt, rdt, cdt, fdt, flags = ctx.meta
         dev = xs.device
         E = si.shape[0]
         need = ctx.needs_input_grad
         g = gy.detach().to(torch.float32).contiguous()
         gx = torch.empty_like(xs)
+        gP = torch.empty_like(Ps) if need[4] else None
+        gQ = torch.empty_like(Qs) if need[5] else None
         gr = torch.empty_like(rs) if need[6] else None
         gC = torch.empty_like(Cs)
         gF = torch.empty_like(Fs)
@@ -161,14 +194,26 @@ class EdgewiseLinearSrcFn(torch.autograd.Function):
         ws = N.workspace(lib.feq_edgewise_bwd_src_nodes_workspace(
             N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E), dev)
         with torch.cuda.device(dev):
-            rc = lib.feq_edgewise_bwd_src_nodes_ex(
-                N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E, N.ptr(g) if E else None,
-                N.ptr(xs), xs.shape[0], N.ptr(si), N.ptr(perm) if E else None, N.ptr(offsets),
-                N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs), N.ptr(Fs), N.ptr(gx), N.ptr(gC),
-                N.ptr(gF), N.ptr(gr), flags, N.ptr(ws), ws.numel(), N.stream_ptr(dev))
-        N.check(rc, "feq_edgewise_bwd_src_nodes_ex")
+            if ym is not None:
+                rc = lib.feq_edgewise_bwd_pq(
+                    N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E, N.ptr(g), N.ptr(xs),
+                    xs.shape[0], N.ptr(si), N.ptr(perm), N.ptr(offsets), N.ptr(Ps), N.ptr(Qs), N.ptr(rs),
+                    N.ptr(Cs), N.ptr(Fs), N.ptr(ym), N.ptr(gx), N.ptr(gC), N.ptr(gF), N.ptr(gr),
+                    N.ptr(gP), N.ptr(gQ), flags, N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+            else:
+                rc = lib.feq_edgewise_bwd_src_nodes_ex(
+                    N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E, N.ptr(g) if E else None,
+                    N.ptr(xs), xs.shape[0], N.ptr(si), N.ptr(perm) if E else None, N.ptr(offsets),
+                    N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs), N.ptr(Fs), N.ptr(gx), N.ptr(gC),
+                    N.ptr(gF), N.ptr(gr), flags, N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+        N.check(rc, "feq_edgewise_bwd_pq" if ym is not None else "feq_edgewise_bwd_src_nodes_ex")
+        if gP is None and need[4]:
+            gP = torch.zeros_like(Ps)
+        if gQ is None and need[5]:
+            gQ = torch.zeros_like(Qs)
         gx = gx.to(xdt) if need[0] else None
-        return (gx, None, None, None, None, None, None if gr is None else gr.to(rdt),
+        cast = lambda t, dt: None if t is None else t.to(dt)
+        return (gx, None, None, None, cast(gP, pdt), cast(gQ, qdt), None if gr is None else gr.to(rdt),
                 gC.to(cdt) if need[7] else None, gF.to(fdt) if need[8] else None, None, None, None,
                 None)
 
@@ -178,11 +223,14 @@ def edgewise_src_supported(layout: N.FeqLayout, binning: N.FeqBinning, rank: int
     return bool(N.lib().feq_edgewise_src_supported(N.ctypes.byref(layout), N.ctypes.byref(binning), rank))
 
 
+def edgewise_pq_supported(layout: N.FeqLayout, binning: N.FeqBinning, rank: int) -> bool:
+    """Whether the split kernels form the bases' gradients for this layout
+    (``feq_edgewise_fwd_ym``/``_bwd_pq``)."""
+    return bool(N.lib().feq_edgewise_pq_supported(N.ctypes.byref(layout), N.ctypes.byref(binning), rank))
+
+
 def edgewise_linear_src(x, src, perm, offsets, P, Q, dist, C, F, layout, binning, rank,
                         half_accuracy: bool = False) -> torch.Tensor:
-    if torch.is_grad_enabled() and (P.requires_grad or Q.requires_grad):
-        raise ValueError("the message-passing form does not form gradients for P and Q; "
-                         "gather the rows and call edgewise_linear")
     return EdgewiseLinearSrcFn.apply(x, src, perm, offsets, P, Q, dist, C, F, layout, binning, rank,
                                      half_accuracy)
 

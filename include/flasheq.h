@@ -171,6 +171,39 @@ int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32_t rank, in
  * (flash_eq/layers/linear.py:131-160). */
 int feq_edgewise_fused_supported(const feq_layout* L, const feq_binning* b, int32_t rank);
 
+/* ---- gradients for the bases on the fused kernels ------------------------------
+ * The reference gets grad_P and grad_Q from torch.bmm autograd around its
+ * block-diagonal op (flash_eq/layers/linear.py:135, :160): with f = x P and
+ * y = m Q^T (m the block-diagonal output before the rotation),
+ *   grad_P[e] = x_e^T (dL/df)_e   (Din x Din),   grad_Q[e] = grad_y_e^T m_e   (Dout x Dout).
+ * feq_edgewise_fwd_ym is the forward (src NULL: x holds edge rows, as
+ * feq_edgewise_fwd; else x is a node table read at src, as
+ * feq_edgewise_fwd_src_ex, flags alike) that also writes m to ym (E, Cout,
+ * Dout).  feq_edgewise_bwd_pq is the backward that also writes grad_P
+ * (E, Din, Din) and grad_Q (E, Dout, Dout) (each may be NULL; ym is required
+ * with grad_Q), both formed inside the input-gradient kernel's tiles: grad_Q
+ * from the grad_y and m rows its producers load, grad_P from the tile's dL/df
+ * and x rows.  src NULL: grad_x (E, Cin, Din) per edge, workspace
+ * feq_edgewise_workspace bytes; src set: grad_x (num_src, Cin, Din) summed per
+ * source node over the CSR by source perm_src / offsets_src, as
+ * feq_edgewise_bwd_src_nodes_ex, workspace
+ * feq_edgewise_bwd_src_nodes_workspace bytes.  Layouts:
+ * feq_edgewise_pq_supported (1); the others return FEQ_ERR_UNSUPPORTED, and
+ * the shape-generic feq_edgewise_bwd forms grad_P and grad_Q itself. */
+int feq_edgewise_pq_supported(const feq_layout* L, const feq_binning* b, int32_t rank);
+int feq_edgewise_fwd_ym(const feq_layout* L, const feq_binning* b, int32_t rank, int64_t num_edges,
+                        const float* x, int64_t num_src, const int64_t* src, const float* P,
+                        const float* Q, const float* dist, const float* C, const float* F, float* y,
+                        float* ym, int32_t flags, void* workspace, size_t ws_bytes,
+                        feq_stream_t stream);
+int feq_edgewise_bwd_pq(const feq_layout* L, const feq_binning* b, int32_t rank, int64_t num_edges,
+                        const float* grad_y, const float* x, int64_t num_src, const int64_t* src,
+                        const int32_t* perm_src, const int32_t* offsets_src, const float* P,
+                        const float* Q, const float* dist, const float* C, const float* F,
+                        const float* ym, float* grad_x, float* grad_C, float* grad_F,
+                        float* grad_dist, float* grad_P, float* grad_Q, int32_t flags,
+                        void* workspace, size_t ws_bytes, feq_stream_t stream);
+
 /* ---- message-passing form of the fused layer ---------------------------------
  * The same layer with its input gathered inside the kernels: x is a node table
  * (num_src, Cin, Din) and edge e reads row src[e] (int64; an index outside
