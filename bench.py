@@ -354,7 +354,9 @@ def build_workload(name: str):
                           f"capped at k=32 on 20k nodes in 60^3, E={E}, fwd+bwd incl. "
                           f"WignerDBasis, {str(dtype).replace('torch.', '')}"),
                   dtype="bf16" if dtype == torch.bfloat16 else "f32")
-    elif name == "c4":
+    elif name in ("c4", "c4pq"):
+        # c4pq: the same step with the coordinates requiring grad (force
+        # training): every edgewise layer then also forms grad_P and grad_Q
         g = torch.Generator().manual_seed(1004)
         N = 50000
         u = torch.randn(N, 3, generator=g, dtype=torch.float64)
@@ -376,7 +378,7 @@ def build_workload(name: str):
         model_cpu = {k: v.clone() for k, v in model.state_dict().items()}
         model = model.to(dev)
         graph = fe.Graph(src.to(dev), dst.to(dev), N)
-        xyz = coords.to(dev)
+        xyz = coords.to(dev).requires_grad_(name == "c4pq")
 
         def step():
             out = model(xyz, feats, graph)
@@ -421,11 +423,14 @@ def build_workload(name: str):
                 o2 = model(xyz @ R.T, torch.einsum("ij,ncj->nci", D, x), graph)
             return equivariance_error(o1, o2)
 
-        wl.update(step=step, E=E, N=N, equiv=equiv, cpu=cpu, leaves=[feats] + list(model.parameters()),
+        wl.update(step=step, E=E, N=N, equiv=equiv, cpu=cpu if name == "c4" else None,
+                  leaves=[feats] + list(model.parameters()) + ([xyz] if name == "c4pq" else []),
                   work=algorithmic_per_edge([0, 1, 2], [0, 1, 2], 64, 64, nodes_per_edge=N / E),
-                  config=(f"c4: EquivariantTransformer 6 layers, in [0,1]x32, hidden [0,1,2]x64, "
+                  config=(f"{name}: EquivariantTransformer 6 layers, in [0,1]x32, hidden [0,1,2]x64, "
                           f"out [0]x8 (x1 is not divisible into 8 heads), 8 heads, random-walk "
-                          f"chain of 50k nodes, kNN k=24, E={E}, fwd+bwd incl. WignerDBasis, fp32"),
+                          f"chain of 50k nodes, kNN k=24, E={E}, fwd+bwd incl. WignerDBasis, fp32"
+                          + (", coordinates with grad (gradients through every basis)"
+                             if name == "c4pq" else "")),
                   dtype="f32")
     elif name == "c1":
         g = torch.Generator().manual_seed(1001)
@@ -748,7 +753,7 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run 1 GiB device copies first (for rocprofv3 --pmc byte calibration)")
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c1", "c3", "c3bf16", "c4", "c5", "published", "published_amp"],
+                    choices=["c2", "c1", "c3", "c3bf16", "c4", "c4pq", "c5", "published", "published_amp"],
                     help="c2 (default) is the metric's configuration; the others print a "
                          "secondary line with their full-size throughput and kernel times")
     ap.add_argument("--no-secondary", action="store_true",

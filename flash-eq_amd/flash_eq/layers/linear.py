@@ -90,19 +90,25 @@ class EquivariantEdgewiseLinear(nn.Module):
     # below this many edges the shape-generic kernels beat the padded fast ones
     EMBED_MIN_EDGES = 4096
 
-    def _embedding(self, x, num_edges, layout, binning):
+    def _embedding(self, x, num_edges, layout, binning, pq: bool = False):
         """The zero-embedding into the [0,1,2]x64 kernels when this layout has no
-        split-fp16 backward of its own, else None (only canonical prefixes of
-        [0, 1, 2] with at most 64 channels embed).  ``FEQ_EW_PATH`` other than the default keeps the
-        layout's own kernels."""
+        split-fp16 backward of its own (with ``pq``: none that forms the bases'
+        gradients), else None (only canonical prefixes of [0, 1, 2] with at
+        most 64 channels embed).  ``FEQ_EW_PATH`` other than the default keeps
+        the layout's own kernels."""
         if os.environ.get("FEQ_EW_PATH") or os.environ.get("FEQ_FORCE_GENERIC") == "1":
             return None
         if num_edges < self.EMBED_MIN_EDGES:
             return None
-        if edgewise_src_supported(layout, binning, self.radial_weights.rank):
+        rank = self.radial_weights.rank
+        own = (edgewise_pq_supported(layout, binning, rank) if pq
+               else edgewise_src_supported(layout, binning, rank))
+        if own:
             return None
-        return embedding_for(self._lin, self._lout, self.channels_in, self.channels_out,
-                             self.radial_weights.rank, x.device)
+        emb = embedding_for(self._lin, self._lout, self.channels_in, self.channels_out, rank, x.device)
+        if emb is not None and pq and not edgewise_pq_supported(emb.layout, binning, rank):
+            return None
+        return emb
 
     def binning(self) -> N.FeqBinning:
         rw = self.radial_weights
@@ -131,9 +137,9 @@ class EquivariantEdgewiseLinear(nn.Module):
             # in float32): the reference's own composition, in float32
             out = self._forward_composed(P, Q, edge_features, distances, graph, torch.float32)
             return out.to(edge_features.dtype)
-        emb = self._embedding(edge_features, distances.shape[0], layout, binning)
-        if (torch.is_grad_enabled() and (P.requires_grad or Q.requires_grad)
-                and not edgewise_pq_supported(emb.layout if emb is not None else layout, binning, rw.rank)):
+        pq = torch.is_grad_enabled() and (P.requires_grad or Q.requires_grad)
+        emb = self._embedding(edge_features, distances.shape[0], layout, binning, pq)
+        if pq and not edgewise_pq_supported(emb.layout if emb is not None else layout, binning, rw.rank):
             # gradients for the bases without split kernels that form them: the
             # shape-generic kernels do, on edge rows, so the gather (if any)
             # happens first

@@ -150,7 +150,14 @@ class EquivariantTransformer(nn.Module):
         half = half_dtype(node_features)
         if half is not None:
             return run_float32(self, half, (coordinates, node_features, graph), {})
-        vec = coordinates[graph.src] - coordinates[graph.dst]      # src - dst, as transformer.py:406
+        # src - dst, as transformer.py:406.  In float32 through the graph's CSR
+        # gathers: their backward (the coordinate gradient) is a fixed-order
+        # segmented sum, where torch's indexing backward sorts the indices
+        # (a radix sort that must not be captured in a HIP graph above 2^20 keys)
+        if coordinates.dtype == torch.float32 and coordinates.is_cuda:
+            vec = graph.gather_src(coordinates) - graph.gather_dst(coordinates)
+        else:
+            vec = coordinates[graph.src] - coordinates[graph.dst]
         distances = vec.norm(dim=-1)
         m_in, m_hidden, m_out = self.basis(vec)
         x = node_features

@@ -8,7 +8,7 @@ from the tile's accumulators, so a layer whose bases require grad (coordinate
 gradients through WignerDBasis) stays on the split kernels.  Checked against
 the float64 oracle at 1e-5 relative for every gradient, in the edge-rows form,
 the message-passing form (gather and per-node input-gradient sums inside the
-kernels), the zero-embedded small layouts, with only one of P and Q requiring
+kernels), the zero-embedded small and scalar-output layouts, with only one of P and Q requiring
 grad, and for ragged tiles; the launch log shows the split kernels and no
 shape-generic ones.
 """
@@ -106,6 +106,13 @@ def test_embedded_layout(dev):
     in the [0,1,2]x64 kernels; the embedded bases' gradients flow back through
     the embedding."""
     _check(dev, [0, 1], [0, 1, 2], 32, 64, 4500, seed=13, graph_nodes=900)
+
+
+def test_scalar_output_layout_embeds(dev):
+    """[0,1,2]x64 -> [0]x8 (the last layer of config 4's model): its
+    scalar-output kernels form no basis gradients, so with P or Q requiring
+    grad it runs zero-embedded in the [0,1,2]x64 split kernels."""
+    _check(dev, [0, 1, 2], [0], 64, 8, 4200, seed=17, graph_nodes=700)
 
 
 def test_pq_entry_points_reject_unsupported(dev):

@@ -151,6 +151,50 @@ def test_captured_block_step_replays_match_eager(dev):
             SumSquaresFn.apply(block(P2, P2, other, vec.norm(dim=-1), graph)).item()
 
 
+def test_captured_model_step_with_coordinate_gradients(dev):
+    """A transformer step whose coordinates require grad (force training)
+    recorded in one HIP graph: the edge vectors come from the graph's CSR
+    gathers (their backward a fixed-order segmented sum, no index sort), the
+    bases' gradients from the split kernels (grad_P, grad_Q) and the Wigner
+    backward.  Every replay gives the eager step's loss and gradients for the
+    coordinates, the features and the parameters."""
+    torch.manual_seed(5)
+    model = fe.EquivariantTransformer(fe.Repr([0, 1], 32), fe.Repr([0, 1, 2], 64), fe.Repr([0], 8),
+                                      num_layers=2, num_heads=8, max_dist=10.0).to(dev)
+    g = torch.Generator().manual_seed(17)
+    Nn, E = 512, 8192
+    src = torch.randint(0, Nn, (E,), generator=g)
+    dst = torch.randint(0, Nn, (E,), generator=g)
+    dst = torch.where(dst == src, (dst + 1) % Nn, dst)   # no self-loops: |0|'s gradient is NaN
+    src, dst = src.to(dev), dst.to(dev)
+    xyz = (torch.rand(Nn, 3, generator=g) * 12).to(dev).requires_grad_(True)
+    feats = torch.randn(Nn, 32, 4, generator=g).to(dev).requires_grad_(True)
+    graph = fe.Graph(src, dst, Nn)
+    graph.csr()
+    graph.csr_src()
+    leaves = [xyz, feats] + list(model.parameters())
+
+    def step():
+        loss = SumSquaresFn.apply(model(xyz, feats, graph))
+        loss.backward()
+        return loss
+
+    for t in leaves:
+        t.grad = None
+    ref_loss = step().detach().clone()
+    ref = [t.grad.clone() for t in leaves]
+    names = ["coordinates", "features"] + [n for n, _ in model.named_parameters()]
+    cg, loss = capture_step(step, leaves)
+    for it in range(3):
+        cg.replay()
+        torch.cuda.synchronize()
+        assert rel_err(loss, ref_loss) < 1e-6, it
+        for n, t, r in zip(names, leaves, ref):
+            assert rel_err(t.grad, r) < 1e-5, (it, n)
+        with torch.no_grad():      # eager work between replays
+            SumSquaresFn.apply(model(xyz + 0.5, feats, graph)).item()
+
+
 @pytest.mark.parametrize("num_keys", [100, 50000])
 def test_captured_csr_build_above_2pow20_edges(dev, num_keys):
     """The stable grouping by key (feq_csr_by_dst) recorded in a HIP graph at
