@@ -66,8 +66,8 @@ def algorithmic_per_edge(lin, lout, cin, cout, same_pq=True, nodes_per_edge=None
     2 sum_{m>=1} 2 n_in(m) n_out(m); a rotation of one channel costs
     S = sum (2l+1)^2 MACs (P and Q are block diagonal over irreps).
 
-    Bytes follow one convention everywhere (SURVEY 8(d)'s yardstick, the one
-    the north-star 60% target is stated in): every tensor of the reference
+    Bytes follow one convention everywhere (the yardstick the 60%-of-HBM
+    target for this layer is stated in): every tensor of the reference
     layer's interface once per edge, as the reference's EquivariantEdgewiseLinear
     reads and writes them (linear.py:144-160) -- x, P (= Q), r, y for the
     forward; gy, x, P, r, gx for the input-gradient kernel; gy, x, P, r for
@@ -124,21 +124,21 @@ def highl_mfma_flop_per_edge(C: int = 128, L: int = 6, rank: int = 4) -> dict:
     C/32 products, stage 2 NB x rank/2 and the output rotation ceil(D/16) x NB;
     the per-edge radial-function gradient (k_hl_dfer) per rank and 64
     channels NB x 4 x C/32 stage-1 and NB x 4 stage-2 products; the
-    channel-pattern gradient one product per 32-step of two slots x 16 edges,
-    column block and rank."""
+    channel-pattern gradient (k_hl_dcc) per 16 output channels, rank and pair
+    of blocks one stage-1 product per block and C/16 stage-2 products."""
     D = (L + 1) ** 2
     f32 = 16 * 16 * 32 * 2
     nb, ndb = 4, -(-D // 16)
     rot = (C // 16) * -(-D // 16) * -(-D // 32) * f32
     mixr = (C // 16) * (nb * rank * (C // 32) + nb * rank // 2 + ndb * nb) * f32
     dfe = rank * (C // 64) * (nb * 4 * (C // 32) + nb * 4) * f32
-    steps = sum(-(-((2 if m else 1) * (L - m + 1)) // 2) for m in range(L + 1))
-    dc = steps * (C // 16) * rank * (C // 16) * f32 / 16
+    dc = (C // 16) * (nb // 2) * rank * (2 + C // 16) * f32
     return {"k_hl_rot_in": rot, "k_hl_mix": mixr, "k_hl_mix_t": mixr, "k_hl_dfe": dfe, "k_hl_dc": dc}
 
 
-# SURVEY 8(d): config 5's algorithmic work, 54.7 MFLOP per edge fwd + bwd, bounds
-# the step at 3.479 ms on the bf16 matrix cores
+# config 5's algorithmic work, 54.7 MFLOP per edge fwd + bwd (the products of
+# the layer at [0..6]x128 without padding), bounds the step at 3.479 ms on the
+# bf16 matrix cores
 C5_BOUND_MS = 3.479
 
 
@@ -648,7 +648,7 @@ def run_workload(name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
            "per_kernel": per_kernel}
     if mfma:
         # the matrix-core kernels against the bf16 MFMA peak (executed flops) and
-        # the whole step against SURVEY 8(d)'s algorithmic bound
+        # the whole step against its algorithmic bound (C5_BOUND_MS)
         frac = {}
         for kname, fl in mfma.items():
             if kname in kern:
@@ -672,8 +672,8 @@ def run_workload(name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
     return out
 
 
-# the reference's published EquivariantEdgewiseLinear
-# numbers (H100, benchmarks/compare_all.py:146-182, README.md:281-305):
+# The reference's published EquivariantEdgewiseLinear numbers (H100,
+# benchmarks/compare_all.py:146-182, README.md:281-305):
 # (lmax, edges, ms per fwd + MSE + bwd + Adam step) at C = 32, num_bins = 64
 PUBLISHED_FP32 = [(1, 32000, 5.3), (2, 32000, 11.5), (4, 5000, 7.1), (6, 5000, 14.7), (4, 20000, 21.5),
                   (6, 20000, 50.6), (4, 50000, 50.1), (6, 50000, 123.5), (4, 128000, 125.6),
@@ -888,7 +888,7 @@ def main() -> int:
                      "kernel": dom, "kernel_avg_ms": round(avg_ms, 4),
                      "algorithmic_flop_per_edge": fl, "algorithmic_bytes_per_edge": by,
                      "byte_convention": "the reference layer's tensors once per edge (x, gx, y, gy, "
-                                        "P, r), SURVEY 8(d)",
+                                        "P, r)",
                      "edges_per_launch": E,
                      "per_kernel": dict(sorted(per_kernel.items(),
                                                key=lambda kv: -kv[1]["ms_per_step"])[:8])})
@@ -921,7 +921,7 @@ def main() -> int:
 
     value = E / (ms_per_step * 1e-3)
     # each tensor once per pass: forward (x, P, r, y), backward (gy, x, P, r, gx) and the
-    # radial table read and its gradient written once per step (SURVEY's 12 573 B per edge;
+    # radial table read and its gradient written once per step (12 573 B per edge;
     # gx counted per edge, as the reference's layer writes it, for a fixed yardstick)
     table_bytes = 4 * (layer.radial_weights.num_bins + 1) * MULT * MULT * layer.weight_dim
     work_ref = algorithmic_per_edge([0, 1, 2], [0, 1, 2], MULT, MULT)

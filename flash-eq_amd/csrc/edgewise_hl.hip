@@ -19,12 +19,12 @@
 //                 precision needs it; below at k_hl_mixr); with C_k^T, M_ek^T
 //                 and P it forms dx from gd^T (k_hl_mix_t);
 //   k_hl_dfe      dF_e[k, w] = sum over the terms (o, i, w) of sign <gd_o, C_k fs_i>,
-//                 G_k recomputed on MFMA, the sums over the 128 rows taken with
-//                 lane swaps (lane rows) and a per-wave LDS buffer (waves);
-//   k_hl_dc       dC_k = sum over (e, i) of U_k fs^T with U_k = M_ek^T gd formed per
-//                 16-edge tile in registers (bf16 dot products) and fed straight
-//                 to the matrix cores; per-workgroup partials summed in a fixed
-//                 order.
+//                 G_k = C_k fs and Z_k = gd^T G_k as two chained bf16 MFMA
+//                 products per edge (below at k_hl_dfer);
+//   k_hl_dc       dC_k = sum over (e, i) of U_k fs^T with U_k = gd M_ek, both as
+//                 chained bf16 MFMA products per edge whose B operands are read
+//                 transposed from LDS (below at k_hl_dcc); per-workgroup
+//                 partials summed in a fixed order.
 // The binned radial-function and distance gradients reuse the tail of the
 // other fused families (edgewise_tail.hip).
 
@@ -683,140 +683,6 @@ __device__ __forceinline__ float quad_row_sums(float v0, float v1, float v2, flo
     return __uint_as_float(z[0]) + __uint_as_float(z[1]);
 }
 
-// ---- per-edge radial-function gradient ---------------------------------------------------
-// dF_e[e, k, w] = sum over the terms (o, i, w) of sign <gd[e, o, :], G_k[:, (e, i)]>,
-// G_k = C_k fs recomputed on the matrix cores (m-groups unrolled, the units of
-// a group in a loop, as in k_hl_mix).
-// In m-block m a source unit i and a destination o give, per rank,
-//   da = <gd_re(o), G_re(i)> + <gd_im(o), G_im(i)>,   db = <gd_re(o), G_im(i)> - <gd_im(o), G_re(i)>
-// for w = w_off(m) + 2 (o n + i) and w + 1 (block_diagonal.cu:514-517), and
-// <gd(o), G(i)> for w_off(0) + o n + i in m-block 0.  A lane forms the dot
-// products over its 4 RBW rows; the four ranks' values of one weight are
-// summed over the wave's lane rows with lane swaps (lane row g receives rank
-// g) and stored into the wave's LDS buffer of the m-group's weights; at the
-// group's end the four waves' buffers are summed in wave order and stored.
-template <int L, int COUT, int CIN, int K>
-__global__ void __launch_bounds__(kT, 1)
-k_hl_dfe(int64_t E, int64_t ntiles, const __bf16* __restrict__ fsT,
-         const __bf16* __restrict__ gdT, const bf8* __restrict__ frag, float* __restrict__ dFe) {
-    using H = HL<L>;
-    constexpr int D = H::D, WD = H::WD, KW = K * WD;
-    constexpr int RBW = COUT / 64, NKS = CIN / 32, NRB = COUT / 16;
-    constexpr int WGM = H::WGMAX;
-    static_assert(K == 4, "one lane-row sum per weight: the four ranks");
-    __shared__ float sD[4][K * WGM * kNE];     // per wave: [k WGM + w - w_off(m)][edge]
-    const int tid = threadIdx.x, lane = tid & 63, le = lane & 15, lg = lane >> 4;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    bf8 A[K][RBW][NKS];
-#pragma unroll
-    for (int k = 0; k < K; ++k)
-#pragma unroll
-        for (int rb = 0; rb < RBW; ++rb)
-#pragma unroll
-            for (int ks = 0; ks < NKS; ++ks)
-                A[k][rb][ks] = frag[((k * NRB + wave * RBW + rb) * NKS + ks) * 64 + lane];
-    float* sw = sD[wave];
-
-    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        const int64_t e0 = tile * kNE;
-        const bool ok = e0 + le < E;
-        const int64_t ec = ok ? e0 + le : E - 1;
-        const __bf16* srow = fsT + ec * D * CIN + 8 * lg;
-        const __bf16* grow = gdT + ec * D * COUT + 16 * wave * RBW + 4 * lg;
-        bf8 b[2][NKS];
-        auto load = [&](int s0, int w) __attribute__((always_inline)) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                if (j < w)
-#pragma unroll
-                    for (int ks = 0; ks < NKS; ++ks)
-                        b[j][ks] = *reinterpret_cast<const bf8*>(srow + (s0 + j) * CIN + 32 * ks);
-        };
-        load(0, 1);
-        float gd[H::GMAX][RBW][4];
-        static_for<H::NG>([&](auto MM) __attribute__((always_inline)) {
-            constexpr int m = decltype(MM)::value, n = L - m + 1, wdt = m ? 2 : 1;
-            constexpr int s0 = H::goff(m), ns = H::gsize(m);
-            constexpr int wo = Canon<L, L>::w_off(m);
-            // gd rows of this lane for the group's slots (zero for edges past the
-            // last: their dot products then vanish)
-#pragma unroll
-            for (int d = 0; d < ns; ++d)
-#pragma unroll
-                for (int rb = 0; rb < RBW; ++rb) {
-                    const bf4 v = *reinterpret_cast<const bf4*>(grow + (s0 + d) * COUT + 16 * rb);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) gd[d][rb][r] = ok ? static_cast<float>(v[r]) : 0.0f;
-                }
-#pragma unroll 1
-            for (int p = 0; p < n; ++p) {
-                v4f G[2][K][RBW];
-#pragma unroll
-                for (int j = 0; j < wdt; ++j)
-#pragma unroll
-                    for (int k = 0; k < K; ++k)
-#pragma unroll
-                        for (int rb = 0; rb < RBW; ++rb) {
-                            v4f g = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                            for (int ks = 0; ks < NKS; ++ks) g = mfma_bf(A[k][rb][ks], b[j][ks], g);
-                            G[j][k][rb] = g;
-                        }
-                if (p + 1 < n) {
-                    load(s0 + wdt * (p + 1), wdt);
-                } else if constexpr (m + 1 < H::NG) {
-                    load(H::goff(m + 1), 2);
-                }
-#pragma unroll
-                for (int q = 0; q < n; ++q) {     // destination degree index o
-                    if constexpr (m == 0) {
-                        float v[K];
-#pragma unroll
-                        for (int k = 0; k < K; ++k) {
-                            float a = 0.0f;
-#pragma unroll
-                            for (int rb = 0; rb < RBW; ++rb)
-#pragma unroll
-                                for (int r = 0; r < 4; ++r) a += gd[q][rb][r] * G[0][k][rb][r];
-                            v[k] = a;
-                        }
-                        const int wl = q * n + p;
-                        sw[(lg * WGM + wl) * kNE + le] = quad_row_sums(v[0], v[1], v[2], v[3]);
-                    } else {
-                        float va[K], vb[K];
-#pragma unroll
-                        for (int k = 0; k < K; ++k) {
-                            float da = 0.0f, db = 0.0f;
-#pragma unroll
-                            for (int rb = 0; rb < RBW; ++rb)
-#pragma unroll
-                                for (int r = 0; r < 4; ++r) {
-                                    const float gre = gd[2 * q][rb][r], gim = gd[2 * q + 1][rb][r];
-                                    da += gre * G[0][k][rb][r] + gim * G[1][k][rb][r];
-                                    db += gre * G[1][k][rb][r] - gim * G[0][k][rb][r];
-                                }
-                            va[k] = da;
-                            vb[k] = db;
-                        }
-                        const int wl = 2 * (q * n + p);
-                        sw[(lg * WGM + wl) * kNE + le] = quad_row_sums(va[0], va[1], va[2], va[3]);
-                        sw[(lg * WGM + wl + 1) * kNE + le] = quad_row_sums(vb[0], vb[1], vb[2], vb[3]);
-                    }
-                }
-            }
-            __syncthreads();   // every wave's buffer of the group is complete
-            constexpr int nw = H::wsize(m);
-            for (int q = tid; q < K * nw * kNE; q += kT) {
-                const int ed = q % kNE, kwl = q / kNE, k = kwl / nw, w = kwl % nw;
-                const int cell = (k * WGM + w) * kNE + ed;
-                const float v = sD[0][cell] + sD[1][cell] + sD[2][cell] + sD[3][cell];
-                if (e0 + ed < E) dFe[(e0 + ed) * KW + k * WD + wo + w] = v;
-            }
-            __syncthreads();   // the buffers are read before the next group writes them
-        });
-    }
-}
-
 // ---- per-edge radial-function gradient as chained matrix-core products ----------
 // dF_e[k, w] = sum over the terms (o, i, w) of sign Z_k[o, i], with
 //   Z_k[o, i] = sum_co gd^T[o, co] G_k[co, i],   G_k = C_k fs,
@@ -1018,62 +884,103 @@ k_hl_dfer(int64_t E, const __bf16* __restrict__ fsT, const __bf16* __restrict__ 
     if (i > 0) emit(static_cast<int>((i - 1) & 1), blockIdx.x + (i - 1) * stride);
 }
 
-// ---- channel-pattern gradient, fused -------------------------------------------------------
-// dC_k[co][ci] = sum over (e, i) of U_k[co][e, i] fs[ci][e, i], U_k = M_ek^T gd:
-//   m = 0:   U(i) = sum_o F_e[k, w0 + o n + i] gd(o)
-//   m >= 1:  U_re(i) = sum_o a gd_re(o) - b gd_im(o),  U_im(i) = sum_o b gd_re(o) + a gd_im(o)
-//            with a = F_e[k, w], b = F_e[k, w + 1], w = w_off(m) + 2 (o n + i)
-// (the transposed mixing of block_diagonal.cu:483-503).  Per 16-edge tile and
-// m-group, gd and fs of the group's slots are staged in LDS edge-minor, gd as
-// (re, im) bf16 pairs (consecutive slots for m = 0); U is formed in registers
-// with v_dot2_f32_bf16 against bf16 coefficient pairs (the pair that multiplies
-// (gd_re, gd_im), or two consecutive o for m = 0), rounded to bf16 and fed to
-// the matrix cores as the A operand (rows co, reduction (slot, edge): a 32-step
-// covers two slots x 16 edges, lane group g serving slot 2 s + g / 2, edges
-// 8 (g % 2) .. + 7), fs as the B operand.  A workgroup has C / 16 waves; wave w
-// owns the output rows 16 w .. 16 w + 15 for every rank, so each gd value read
-// from LDS serves all four ranks.  The dC accumulators live in registers for
-// the whole launch; one partial dC per workgroup.
+// ---- channel-pattern gradient as chained matrix-core products --------------------
+// dC_k[co][ci] = sum over the edges e and slots i of U_k[co][i] fs[ci][i], with
+// U_k = gd M_ek (U_k^T[i][co] = sum_o M_ek[o][i] gd^T[o][co], the transposed
+// mixing of block_diagonal.cu:483-503), per edge in two chained bf16 products:
+//   stage 1  U_k^T for the 16 slot rows of one HLB block (B: the edge's gd^T
+//            rows of the block, k = the block's 16 o rows, the other 16 zero;
+//            A: the per-edge M_ek^T fragment of the block, built in LDS);
+//   stage 2  dC_k += U_k fs^T over the slots of two blocks per 32-step: the two
+//            stage-1 accumulators (lane l: rows 4 (l / 16) + r of column co =
+//            l % 16) rounded to bf16 are the A operand (rows co, reduction
+//            (block, row)), the edge's fs^T rows of the same (block, row) pairs
+//            the B operand.
+// Both B operands read slot rows transposed straight from LDS with
+// ds_read_b64_tr_b16: within a 16-lane group, lane s points at row s / 4 and
+// 4-column chunk s % 4 of its read and receives 4 rows of one column (lane t:
+// element j of row j, column t), so the rows may sit anywhere (the HLB block
+// order is a per-lane address; padding rows point at a zero row).  A workgroup
+// of C / 16 waves takes one edge at a time; wave w owns the output rows
+// 16 w .. 16 w + 15 of every rank, its dC accumulators live for the launch,
+// and each workgroup writes one partial dC.  The edge loop is pipelined as in
+// k_hl_mixr: one barrier per edge, the rows of the next edge and the radial
+// functions of the one after it loaded into registers during the current one.
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+
+__device__ __forceinline__ bf8 tr_pair(const char* lo, const char* hi) {
+    const v4s a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(lo));
+    const v4s b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(hi));
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    const v8s v = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    return __builtin_bit_cast(bf8, v);
+}
+
 template <int C>
 constexpr int dc_threads() { return 4 * C; }
 
-// 16-byte chunk c of LDS row r, swizzled so that 16 consecutive rows read by
-// one 16-lane pass hit distinct banks.
-__device__ __forceinline__ int dc_chunk2(int r, int c) { return c ^ ((r >> 3) & 1); }   // 2 chunks / row
-__device__ __forceinline__ int dc_chunk4(int r, int c) { return c ^ ((r >> 2) & 3); }   // 4 chunks / row
-
 template <int L, int C, int K>
 __global__ void __launch_bounds__(dc_threads<C>(), 1)
-k_hl_dc(feq_binning B, int64_t E, int64_t ntiles, const __bf16* __restrict__ gdT,
-        const __bf16* __restrict__ fsT, const float* __restrict__ dist, const float* __restrict__ F,
-        float* __restrict__ dCp) {
-    using H = HL<L>;
-    using Cn = Canon<L, L>;
-    constexpr int D = H::D, WD = H::WD, KW = K * WD;
-    constexpr int NT = dc_threads<C>();            // one wave per 16 rows of co
-    constexpr int NCB = C / 16;                    // 16-column blocks of ci
-    constexpr int GMAX = H::GMAX, NPMAX = (GMAX + 1) / 2;
-    constexpr int NQ0 = (L + 2) / 2;               // o-pairs of m-group 0
-    constexpr int CO_MAX = [] {
-        int v = K * (L + 1) * NQ0;                 // m = 0: [k][i][o pair]
-        for (int m = 1; m <= L; ++m) {
-            const int n = L - m + 1;
-            if (K * 2 * n * n > v) v = K * 2 * n * n;   // m >= 1: [k][part][i][o]
-        }
-        return v;
-    }();
+k_hl_dcc(feq_binning B, int64_t E, const __bf16* __restrict__ gdT, const __bf16* __restrict__ fsT,
+         const float* __restrict__ dist, const float* __restrict__ F, float* __restrict__ dCp) {
+    using HB = HLB<L>;
+    constexpr int D = HB::D, NB = HB::NB, WD = HL<L>::WD, KW = K * WD;
+    constexpr int NT = dc_threads<C>(), NCB = C / 16, NPAIR = (NB + 1) / 2;
+    constexpr int RS = 2 * C + 32;                  // row stride (bytes): consecutive rows 8 banks apart
+    constexpr int NQ = (D * C / 8 + NT - 1) / NT;   // 16-byte row chunks per thread and tensor
+    constexpr int NF = (KW + NT - 1) / NT;          // radial functions per thread
+    constexpr int NCF = NB * K * 32;                // coefficient fragments (lane groups 0 and 1) per edge
+    constexpr int NCI = (NCF + NT - 1) / NT;
     static_assert(K == 4 && C % 64 == 0 && NT <= 1024, "four ranks; 64 or 128 channels");
-    __shared__ __align__(16) __bf16 sFS[GMAX * C * kNE];             // [slot][ci][edge]
-    __shared__ __align__(16) uint32_t sGD[NPMAX * C * kNE];          // [pair][co][edge] (re | im << 16)
-    __shared__ __align__(16) uint32_t sCo[CO_MAX * kNE];             // coefficient pairs [..][edge]
-    __shared__ __align__(16) __bf16 sFb[KW * kNE];                   // F_e of the tile [k WD + w][edge]
-    __shared__ int slo[kNE];
-    __shared__ float st[kNE];
+    static_assert(KW < 0x4000 && RS % 8 == 0, "16-bit coefficient codes; 8-byte transposed reads");
+    __shared__ __align__(16) char sFs[2][(D + 1) * RS];   // + a zero row for padding
+    __shared__ __align__(16) char sGd[2][(D + 1) * RS];
+    __shared__ __align__(16) float sFe[2][KW];
+    __shared__ __align__(16) u32x4 sCo[2][NCF];
 
     const int tid = threadIdx.x, lane = tid & 63, le = lane & 15, lg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = lg & 1, half_slot = lg >> 1;
-    const int corow = 16 * wave + le;               // this lane's A-operand row
+    const int rsel = le >> 2, csel = le & 3;        // the row and 4-column chunk this lane points at
+    const unsigned amask = lg < 2 ? 0xffffffffu : 0u;   // stage-1 A: reduction rows 16 .. 31 are zero
+
+    // per-lane byte offsets of the transposed reads: stage-1 B (gd rows of
+    // block b, rows 8 lg + 4 h + rsel; lane groups 2 and 3 read the zero row)
+    // and stage-2 B (fs rows of pair p, block 2 p + h, rows 4 lg + rsel)
+    int gdo[NB][2], fso[NPAIR][2];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int sl = lg < 2 ? HB::P.slot[b][8 * lg + 4 * h + rsel] : -1;
+            gdo[b][h] = (sl >= 0 ? sl : D) * RS + 32 * wave + 8 * csel;
+        }
+#pragma unroll
+    for (int p = 0; p < NPAIR; ++p)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int b = 2 * p + h;
+            const int sl = b < NB ? HB::P.slot[b][4 * lg + rsel] : -1;
+            fso[p][h] = (sl >= 0 ? sl : D) * RS + 8 * csel;
+        }
+    // this thread's coefficient fragment items: lane fl (groups 0, 1) of
+    // fragment (b, k) holds M_ek^T[row fl % 16][row 8 (fl / 16) + t] of block
+    // b, t < 8: the element k WD + w of the radial functions (bits 0-13), its
+    // sign (bit 14), whether it is non-zero (bit 15); two per register
+    unsigned ccode[NCI][4];
+#pragma unroll
+    for (int n = 0; n < NCI; ++n) {
+        const int q = tid + NT * n;
+        const int fl = q & 31, k = (q >> 5) % K, b = (q >> 5) / K;
+        unsigned v[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int c = q < NCF ? HB::P.coef[b][8 * (fl >> 4) + t][fl & 15] : -1;
+            v[t] = c < 0 ? 0u : static_cast<unsigned>(k * WD + (c >> 1)) | ((c & 1u) << 14) | 0x8000u;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) ccode[n][t] = v[2 * t] | (v[2 * t + 1] << 16);
+    }
 
     v4f acc[K][NCB];
 #pragma unroll
@@ -1081,155 +988,163 @@ k_hl_dc(feq_binning B, int64_t E, int64_t ntiles, const __bf16* __restrict__ gdT
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb) acc[k][cb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        const int64_t e0 = tile * kNE;
-        __syncthreads();   // the previous tile's readers of slo / st are done
-        if (tid < kNE) {
-            const int64_t e = e0 + tid;
-            const bool valid = e < E;
-            const EdgeBin eb = edge_bin(valid ? dist[e] : 0.0f, B);
-            slo[tid] = valid ? eb.lo : -1;
-            st[tid] = eb.t;
+    // Edge i of this workgroup is e_i = blockIdx.x + i gridDim.x.  Iteration i
+    // computes e_i from LDS buffers i % 2; around that it writes the rows of
+    // e_{i+1} and the interpolated radial functions of e_{i+2} (loaded during
+    // iteration i - 1), builds e_{i+1}'s coefficient fragments from its radial
+    // functions (written during iteration i - 1), and loads e_{i+2}'s rows and
+    // e_{i+3}'s bin rows.  Loads are unconditional (indices clamped).
+    const int64_t stride = gridDim.x;
+    auto edge = [&](int64_t i) -> int64_t {
+        const int64_t e = blockIdx.x + i * stride;
+        return e < E ? e : E - 1;
+    };
+    u32x4 pf[NQ], pg[NQ];
+    float pflo[NF], pfhi[NF], pt = 0.0f;
+    auto load_rows = [&](int64_t e) {
+        const u32x4* f4 = reinterpret_cast<const u32x4*>(fsT + e * D * C);
+        const u32x4* g4 = reinterpret_cast<const u32x4*>(gdT + e * D * C);
+#pragma unroll
+        for (int n = 0; n < NQ; ++n) {
+            const int q = tid + NT * n;
+            const int qq = q < D * C / 8 ? q : 0;
+            pf[n] = f4[qq];
+            pg[n] = g4[qq];
         }
-        __syncthreads();   // slo / st written
-        // the tile's interpolated radial functions, bf16 (the precision of the
-        // coefficient pairs): each edge's two bin rows read as float4s
-        static_assert(KW % 4 == 0, "radial rows of whole float4s");
-        for (int q = tid; q < kNE * (KW / 4); q += NT) {
-            const int e = q / (KW / 4), c4 = q % (KW / 4);
-            const int lo = slo[e];
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (lo >= 0) {
-                const float4 a = reinterpret_cast<const float4*>(F + static_cast<int64_t>(lo) * KW)[c4];
-                const float4 b = reinterpret_cast<const float4*>(F + static_cast<int64_t>(lo + 1) * KW)[c4];
-                const float t = st[e];
-                v = make_float4(lerp_bins(a.x, b.x, t), lerp_bins(a.y, b.y, t), lerp_bins(a.z, b.z, t),
-                                lerp_bins(a.w, b.w, t));
-            }
-            sFb[(4 * c4) * kNE + e] = static_cast<__bf16>(v.x);
-            sFb[(4 * c4 + 1) * kNE + e] = static_cast<__bf16>(v.y);
-            sFb[(4 * c4 + 2) * kNE + e] = static_cast<__bf16>(v.z);
-            sFb[(4 * c4 + 3) * kNE + e] = static_cast<__bf16>(v.w);
+    };
+    auto load_radial = [&](float rd) {
+        const EdgeBin eb = edge_bin(rd, B);
+        pt = eb.t;
+        const float* flo = F + static_cast<int64_t>(eb.lo) * KW;
+#pragma unroll
+        for (int n = 0; n < NF; ++n) {
+            const int q = tid + NT * n < KW ? tid + NT * n : 0;
+            pflo[n] = flo[q];
+            pfhi[n] = flo[q + KW];
         }
-        static_for<H::NG>([&](auto MM) __attribute__((always_inline)) {
-            constexpr int m = decltype(MM)::value, n = L - m + 1;
-            constexpr int s0 = H::goff(m), ns = H::gsize(m), wo = Cn::w_off(m);
-            constexpr int NP = m ? n : NQ0;                  // gd pairs of the group
-            constexpr int NKS = (ns + 1) / 2;                // 32-steps of the group
-            __syncthreads();   // sFb written; the previous group's readers are done
-            // fs of the group's slots: sFS[(s C + ci) 16 + e], 16-byte chunks swizzled
-#pragma unroll 2
-            for (int q = tid; q < ns * kNE * (C / 8); q += NT) {
-                const int e = q % kNE, c8 = (q / kNE) % (C / 8), sl = q / (kNE * (C / 8));
-                const bool ok = e0 + e < E;
-                bf8 v = bf8{};
-                if (ok) v = *reinterpret_cast<const bf8*>(fsT + ((e0 + e) * D + s0 + sl) * C + 8 * c8);
+    };
+    auto write_rows = [&](int buf) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int row = sl * C + 8 * c8 + j;
-                    sFS[row * kNE + 8 * dc_chunk2(row, e >> 3) + (e & 7)] = v[j];
-                }
+        for (int n = 0; n < NQ; ++n) {
+            const int q = tid + NT * n;
+            if ((D * C / 8) % NT == 0 || q < D * C / 8) {
+                const int off = (q / (C / 8)) * RS + (q % (C / 8)) * 16;
+                *reinterpret_cast<u32x4*>(sFs[buf] + off) = pf[n];
+                *reinterpret_cast<u32x4*>(sGd[buf] + off) = pg[n];
             }
-            // gd pairs: sGD[(p C + co) 16 + e] = gd(slot 2p) | gd(slot 2p + 1) << 16
-#pragma unroll 2
-            for (int q = tid; q < NP * kNE * (C / 8); q += NT) {
-                const int e = q % kNE, c8 = (q / kNE) % (C / 8), pr = q / (kNE * (C / 8));
-                const bool ok = e0 + e < E;
-                const int sa = 2 * pr, sb = 2 * pr + 1;
-                bf8 a = bf8{}, b = bf8{};
-                if (ok) {
-                    a = *reinterpret_cast<const bf8*>(gdT + ((e0 + e) * D + s0 + sa) * C + 8 * c8);
-                    if (sb < ns) b = *reinterpret_cast<const bf8*>(gdT + ((e0 + e) * D + s0 + sb) * C + 8 * c8);
-                }
-                const u16x8 au = __builtin_bit_cast(u16x8, a), bu = __builtin_bit_cast(u16x8, b);
+        }
+    };
+    auto write_radial = [&](int buf) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int row = pr * C + 8 * c8 + j;
-                    const uint32_t bits = static_cast<uint32_t>(au[j]) | (static_cast<uint32_t>(bu[j]) << 16);
-                    sGD[row * kNE + 4 * dc_chunk4(row, e >> 2) + (e & 3)] = bits;
+        for (int n = 0; n < NF; ++n) {
+            const int q = tid + NT * n;
+            if (KW % NT == 0 || q < KW) sFe[buf][q] = lerp_bins(pflo[n], pfhi[n], pt);
+        }
+    };
+    auto build_coef = [&](int buf) {
+#pragma unroll
+        for (int n = 0; n < NCI; ++n) {
+            const int q = tid + NT * n;
+            if (NCF % NT == 0 || q < NCF) {
+                unsigned w[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    unsigned h2[2];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const unsigned code = (ccode[n][t] >> (16 * u)) & 0xffffu;
+                        unsigned x = __float_as_uint(sFe[buf][code & 0x3fffu]);
+                        x = (x ^ ((code & 0x4000u) << 17)) & (0u - (code >> 15));
+                        h2[u] = __builtin_bit_cast(unsigned short, static_cast<__bf16>(__uint_as_float(x)));
+                    }
+                    w[t] = h2[0] | (h2[1] << 16);
                 }
+                sCo[buf][q] = u32x4{w[0], w[1], w[2], w[3]};
             }
-            // coefficient pairs of the interpolated radial functions
-            constexpr int NCO = m ? K * 2 * n * n : K * n * NQ0;
-            for (int q = tid; q < NCO * kNE; q += NT) {
-                const int e = q % kNE, c = q / kNE;
-                auto fe = [&](int k, int w) -> uint32_t {
-                    return __builtin_bit_cast(uint16_t, sFb[(k * WD + w) * kNE + e]);
-                };
-                uint32_t v;
-                if constexpr (m == 0) {
-                    const int pq = c % NQ0, i = (c / NQ0) % n, k = c / (NQ0 * n);
-                    const int oa = 2 * pq, ob = 2 * pq + 1;
-                    v = fe(k, wo + oa * n + i) | ((ob < n ? fe(k, wo + ob * n + i) : 0u) << 16);
-                } else {
-                    const int o = c % n, i = (c / n) % n, part = (c / (n * n)) % 2, k = c / (2 * n * n);
-                    const int w = wo + 2 * (o * n + i);
-                    const uint32_t a = fe(k, w), b = fe(k, w + 1);
-                    // part 0: (a, -b), part 1: (b, a); the sign of a bf16 is its top bit
-                    v = part == 0 ? (a | ((b ^ 0x8000u) << 16)) : (b | (a << 16));
-                }
-                sCo[c * kNE + e] = v;
-            }
-            __syncthreads();
-#pragma unroll 1
-            for (int ks = 0; ks < NKS; ++ks) {
-                const int sl = 2 * ks + half_slot;
-                const bool live = sl < ns;
-                // U of this lane's slot and 8 edges for every rank
-                const int i = m ? sl >> 1 : sl, part = sl & 1;
-                float u[K][8];
+        }
+    };
+
+    // prologue: e_0's rows, radial functions and coefficients, e_1's radial
+    // functions in LDS; e_1's rows and e_2's bin rows in registers
+    float d0 = dist[edge(0)], d1 = dist[edge(1)];
+    load_rows(edge(0));
+    load_radial(d0);
+    for (int q = tid; q < 2 * (RS / 16); q += NT) {   // the zero rows
+        const int buf = q / (RS / 16), c = q % (RS / 16);
+        *reinterpret_cast<u32x4*>(sFs[buf] + D * RS + c * 16) = u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(sGd[buf] + D * RS + c * 16) = u32x4{0u, 0u, 0u, 0u};
+    }
+    write_rows(0);
+    write_radial(0);
+    load_radial(d1);
+    write_radial(1);
+    __syncthreads();
+    build_coef(0);
+    float dq = dist[edge(3)];
+    load_rows(edge(1));
+    load_radial(dist[edge(2)]);
+
+    auto iteration = [&](int64_t i, auto CB) __attribute__((always_inline)) {
+        constexpr int cb = decltype(CB)::value, nb = cb ^ 1;
+        __syncthreads();
+        write_rows(nb);               // e_{i+1}
+        write_radial(cb);             // e_{i+2}
+        build_coef(nb);               // e_{i+1}, from its radial functions written last iteration
+        load_rows(edge(i + 2));
+        load_radial(dq);              // e_{i+3}
+        dq = dist[edge(i + 4)];
+
+        const char* fs = sFs[cb];
+        const char* gd = sGd[cb];
+        const u32x4* co = sCo[cb];
+        const int cl = lane & 31;
 #pragma unroll
-                for (int k = 0; k < K; ++k)
+        for (int p = 0; p < NPAIR; ++p) {
+            // stage 1 for the pair's blocks, rounded into the stage-2 A operands
+            bf8 a2[K];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) u[k][j] = 0.0f;
-                if (live) {
-#pragma unroll 1
-                    for (int p = 0; p < NP; ++p) {
-                        const int row = p * C + corow;
-                        const uint4 g0 = *reinterpret_cast<const uint4*>(sGD + row * kNE + 4 * dc_chunk4(row, 2 * h));
-                        const uint4 g1 = *reinterpret_cast<const uint4*>(sGD + row * kNE + 4 * dc_chunk4(row, 2 * h + 1));
-                        const uint32_t g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+            for (int k = 0; k < K; ++k) {
+                v4f u[2] = {v4f{0.0f, 0.0f, 0.0f, 0.0f}, v4f{0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
-                        for (int k = 0; k < K; ++k) {
-                            const int c = m ? ((k * 2 + part) * n + i) * n + p : (k * n + i) * NQ0 + p;
-                            const uint4 c0 = *reinterpret_cast<const uint4*>(sCo + c * kNE + 8 * h);
-                            const uint4 c1 = *reinterpret_cast<const uint4*>(sCo + c * kNE + 8 * h + 4);
-                            const uint32_t cf[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-#pragma unroll
-                            for (int j = 0; j < 8; ++j)
-                                u[k][j] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, cf[j]),
-                                                                          __builtin_bit_cast(bf2, g[j]), u[k][j],
-                                                                          false);
-                        }
+                for (int h = 0; h < 2; ++h) {
+                    const int b = 2 * p + h;
+                    if (b < NB) {
+                        u32x4 c = co[(b * K + k) * 32 + cl];
+                        c &= amask;
+                        const bf8 bg = tr_pair(gd + gdo[b][0], gd + gdo[b][1]);
+                        u[h] = mfma_bf(__builtin_bit_cast(bf8, c), bg, u[h]);
                     }
                 }
-                bf8 a[K];
 #pragma unroll
-                for (int k = 0; k < K; ++k)
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) a[k][j] = static_cast<__bf16>(u[k][j]);
-                // fs fragments one column block at a time, each feeding the four ranks
-#pragma unroll
-                for (int cb = 0; cb < NCB; ++cb) {
-                    const int row = sl * C + 16 * cb + le;
-                    const bf8 b = live ? *reinterpret_cast<const bf8*>(sFS + row * kNE + 8 * dc_chunk2(row, h))
-                                       : bf8{};
-#pragma unroll
-                    for (int k = 0; k < K; ++k) acc[k][cb] = mfma_bf(a[k], b, acc[k][cb]);
+                for (int r = 0; r < 4; ++r) {
+                    a2[k][r] = static_cast<__bf16>(u[0][r]);
+                    a2[k][4 + r] = static_cast<__bf16>(u[1][r]);
                 }
             }
-        });
+            // stage 2: one fs fragment per column block serves the four ranks
+#pragma unroll
+            for (int c = 0; c < NCB; ++c) {
+                const bf8 bf = tr_pair(fs + fso[p][0] + 32 * c, fs + fso[p][1] + 32 * c);
+#pragma unroll
+                for (int k = 0; k < K; ++k) acc[k][c] = mfma_bf(a2[k], bf, acc[k][c]);
+            }
+        }
+    };
+    for (int64_t i = 0; blockIdx.x + i * stride < E; i += 2) {
+        iteration(i, std::integral_constant<int, 0>{});
+        if (blockIdx.x + (i + 1) * stride >= E) break;
+        iteration(i + 1, std::integral_constant<int, 1>{});
     }
     // partial dC of this workgroup: lane holds rows 4 lg + r of each 16-row block
     float* part = dCp + static_cast<int64_t>(blockIdx.x) * K * C * C;
 #pragma unroll
     for (int k = 0; k < K; ++k)
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb)
+        for (int c = 0; c < NCB; ++c)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int co = 16 * wave + 4 * lg + r;
-                part[(k * C + co) * C + 16 * cb + le] = acc[k][cb][r];
+                const int orow = 16 * wave + 4 * lg + r;
+                part[(k * C + orow) * C + 16 * c + le] = acc[k][c][r];
             }
 }
 
@@ -1252,8 +1167,8 @@ struct HLWs {
     float* tail;     // ew_tail workspace          backward
 };
 
-// Workgroups of the fused channel-pattern gradient: one per CU.
-int dc_groups(int64_t E) { return grid_tiles(ceil_div(E, kNE)); }
+// Workgroups of the channel-pattern gradient: one per CU (one edge at a time).
+int dc_groups(int64_t E) { return grid_tiles(E); }
 
 template <int L>
 size_t hl_layout(const feq_binning& B, int C, int64_t E, bool backward, HLWs* w, void* base) {
@@ -1317,11 +1232,8 @@ int hl_bwd(const feq_layout& Lay, const feq_binning& B, int64_t E, const __bf16*
            const __bf16* P, const __bf16* Q, const float* dist, const float* C, const float* F,
            __bf16* gx, float* gC, float* gF, float* gdist, const __bf16* fs_in, void* ws,
            size_t ws_bytes, hipStream_t s) {
-    using H = HL<L>;
     HLWs w;
     if (ws_bytes < hl_layout<L>(B, CH, E, true, &w, ws)) return fail(FEQ_ERR_WORKSPACE, "high-degree workspace too small");
-    const int64_t ntiles = ceil_div(E, kNE);
-    const int G = grid_tiles(ntiles);
     // gd = s^l_out (gy Q), fs = s^l_in (x P)
     if (int rc = hl_rot_in<L, CH>(E, gy, Q, dist, B.sh_scale, w.gdT, s)) return rc;
     const __bf16* fs = fs_in;
@@ -1344,9 +1256,8 @@ int hl_bwd(const feq_layout& Lay, const feq_binning& B, int64_t E, const __bf16*
     // shared tail sums them in a fixed order with the binned radial-function
     // gradient and the distance gradient
     const int groups = dc_groups(E);
-    auto kc = k_hl_dc<L, CH, kRank>;
-    FEQ_LAUNCH("k_hl_dc", kc, dim3(groups), dim3(dc_threads<CH>()), 0, s, B, E, ntiles, w.gdT, fs, dist, F,
-               w.dCp);
+    auto kc = k_hl_dcc<L, CH, kRank>;
+    FEQ_LAUNCH("k_hl_dc", kc, dim3(groups), dim3(dc_threads<CH>()), 0, s, B, E, w.gdT, fs, dist, F, w.dCp);
     return ew_tail(Lay, B, kRank, E, dist, F, w.dFe, w.dCp, groups, static_cast<int64_t>(kRank) * CH * CH,
                    gC, gF, gdist, w.tail, s);
 }
