@@ -337,7 +337,10 @@ C4_MAX_DIST = 30.0
 
 def test_model_config4_shape(dev):
     """Config 4's model (6 layers, [0,1]x32 -> [0,1,2]x64 -> [0]x8, 8 heads) on a
-    random-walk chain of 200 nodes with k = 24 neighbours, coordinates with grad."""
+    random-walk chain of 200 nodes with k = 24 neighbours, coordinates with grad.
+    Every edgewise layer forms the bases' gradients on the split kernels (the
+    first and the scalar-output last layer zero-embedded in [0,1,2]x64), as the
+    launch log confirms: no shape-generic kernel runs."""
     coords, src, dst = _config4_graph()
     Nn = coords.shape[0]
     g = torch.Generator().manual_seed(44)
@@ -346,6 +349,18 @@ def test_model_config4_shape(dev):
                                       num_heads=8, max_dist=C4_MAX_DIST, layer_scale_init=0.3).to(dev)
     x = torch.randn(Nn, 32, 4, generator=g).to(dev).requires_grad_(True)
     xyz = coords.to(dev).requires_grad_(True)
+    NAT.profile_summary()
+    NAT.profile_enable(True)
+    out = model(xyz, x, fe.Graph(src.to(dev), dst.to(dev), Nn))
+    out.square().sum().backward()
+    torch.cuda.synchronize()
+    NAT.profile_enable(False)
+    launched = NAT.profile_summary()
+    assert "k_ew_fwd" not in launched and "k_ew_bwd" not in launched, launched
+    assert launched["k_ews_bwd_x"][0] == 6 and launched["k_ews_fwd"][0] == 6, launched
+    x.grad, xyz.grad = None, None
+    for p in model.parameters():
+        p.grad = None
     out = model(xyz, x, fe.Graph(src.to(dev), dst.to(dev), Nn))
     w = torch.randn(out.shape, generator=g)
     cfg = OM.transformer_cfg([0, 1], [0, 1, 2], [0], 32, 64, 8, num_layers=6, heads=8,
