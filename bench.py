@@ -683,7 +683,7 @@ PUBLISHED_AMP = [(1, 32000, 5.4), (2, 32000, 10.5), (4, 5000, 6.6), (6, 5000, 13
                  (6, 128000, 279.8)]
 
 
-def run_published(amp: bool, n_warmup: int = 3, n_iter: int = 10) -> list:
+def run_published(amp: bool, n_warmup: int = 3, n_iter: int = 10, only=None) -> list:
     """The reference's own benchmark step (compare_all.py:146-182) at its
     published configurations: EquivariantEdgewiseLinear(Repr(0..L, 32)) with
     num_bins = 64, features (E, 32, dim) requiring grad, P = Q from WignerDBasis
@@ -696,6 +696,8 @@ def run_published(amp: bool, n_warmup: int = 3, n_iter: int = 10) -> list:
     dev = torch.device("cuda", 0)
     rows = []
     for lmax, E, ref_ms in (PUBLISHED_AMP if amp else PUBLISHED_FP32):
+        if only and (lmax, E) not in only:
+            continue
         torch.manual_seed(lmax * 1000 + E // 1000)
         rep = fe.Repr(list(range(lmax + 1)), 32)
         dim = rep.dim()
@@ -752,6 +754,8 @@ def main() -> int:
     ap.add_argument("--grad-dist", action="store_true", help="also differentiate w.r.t. distances")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run 1 GiB device copies first (for rocprofv3 --pmc byte calibration)")
+    ap.add_argument("--rows", default="",
+                    help="published workloads: only these L:E rows, comma-separated (e.g. 6:20000)")
     ap.add_argument("--workload", default="c2",
                     choices=["c2", "c1", "c3", "c3bf16", "c4", "c4pq", "c5", "published", "published_amp"],
                     help="c2 (default) is the metric's configuration; the others print a "
@@ -766,7 +770,9 @@ def main() -> int:
               "multi-GPU path; run it with --gpus 1.", file=sys.stderr)
         return 2
     if args.workload.startswith("published"):
-        print(json.dumps({"workload": args.workload, "rows": run_published(args.workload == "published_amp")}))
+        only = {tuple(int(v) for v in r.split(":")) for r in args.rows.split(",")} if args.rows else None
+        print(json.dumps({"workload": args.workload,
+                          "rows": run_published(args.workload == "published_amp", only=only)}))
         return 0
     if args.workload != "c2":
         print(json.dumps(run_workload(args.workload, args.steps, args.warmup, not args.no_cpu)))

@@ -25,7 +25,12 @@
 namespace feq {
 namespace {
 
-constexpr int kThreads = 256;
+// Threads per workgroup of the shape-generic kernels: 256, 512 or 1024, the
+// smallest that gives a CU at least 16 waves at the layout's LDS (pick_threads;
+// measured at lvals 0..6 x 32 channels: the backward at 89 KB of LDS, one
+// workgroup per CU, 28.2 / 17.2 / 11.5 ms per published step with 256 / 512 /
+// 1024 threads; lvals 0..4 (48 KB, three workgroups) 7.6 / 5.1 / 6.3 ms).
+constexpr int kMaxThreads = 1024;
 constexpr int kBwdGroups = 1024;  // workgroups of the backward pass
 
 struct Blk {
@@ -127,6 +132,7 @@ __device__ __forceinline__ int weight_info(const feq_layout& L, int w, Blk& b, i
     return L.lslot_in[b.in_off + 2 * i] + L.lslot_out[b.out_off + 2 * o];
 }
 
+template <int NT>
 __device__ __forceinline__ float block_sum(float v, float* red) {
     for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -134,7 +140,7 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     if (lane == 0) red[wid] = v;
     __syncthreads();
     float s = 0.0f;
-    for (int w = 0; w < kThreads / 64; ++w) s += red[w];
+    for (int w = 0; w < NT / 64; ++w) s += red[w];
     __syncthreads();
     return s;
 }
@@ -145,6 +151,7 @@ struct EwDims {
 };
 
 // ---------------------------------------------------------------------------
+template <int kThreads>
 __global__ void __launch_bounds__(kThreads)
 k_ew_fwd(feq_layout L, feq_binning B, EwDims D, const float* __restrict__ x,
          const float* __restrict__ P, const float* __restrict__ Q, const float* __restrict__ dist,
@@ -208,6 +215,7 @@ k_ew_fwd(feq_layout L, feq_binning B, EwDims D, const float* __restrict__ x,
 // workgroup in LDS and written as a partial, and the per-edge radial-function
 // gradient dF_e is written per edge; the shared tail bins dF_e and sums the
 // partials in a fixed order (deterministic, no atomics).
+template <int kThreads>
 __global__ void __launch_bounds__(kThreads)
 k_ew_bwd(feq_layout L, feq_binning B, EwDims D, int64_t E, const float* __restrict__ gy,
          const float* __restrict__ x, const float* __restrict__ P, const float* __restrict__ Q,
@@ -320,8 +328,8 @@ k_ew_bwd(feq_layout L, feq_binning B, EwDims D, int64_t E, const float* __restri
             __syncthreads();
         }
         if (gdist) {
-            const float st = block_sum(acc_t, red);
-            const float ss = block_sum(acc_s, red);
+            const float st = block_sum<kThreads>(acc_t, red);
+            const float ss = block_sum<kThreads>(acc_s, red);
             if (tid == 0) {
                 float v = st * eb.dtdr;
                 if (L.has_lpos) v += ss * (sigma / (r * (r + sigma)));
@@ -380,6 +388,17 @@ int ensure_lds(const void* fn, size_t bytes) {
 
 int groups_for(int64_t E) { return static_cast<int>(E < kBwdGroups ? (E > 0 ? E : 1) : kBwdGroups); }
 
+// Threads per workgroup for a kernel needing `lds` bytes: the smallest of 256,
+// 512 and 1024 with which the workgroups that fit a CU's 160 KB of LDS give it
+// at least 16 waves (more threads per edge when LDS keeps occupancy low).
+int pick_threads(size_t lds) {
+    const int groups = static_cast<int>((160 * 1024) / (lds > 0 ? lds : 1));
+    for (int nt = 256; nt < kMaxThreads; nt *= 2)
+        if (groups * (nt / 64) >= 16) return nt;
+    return kMaxThreads;
+}
+
+
 }  // namespace
 }  // namespace feq
 
@@ -422,10 +441,12 @@ extern "C" int feq_edgewise_fwd(const feq_layout* L, const feq_binning* b, int32
         if (rc != -1) return rc;
     }
     const size_t lds = fwd_lds(*L, rank);
-    if (int rc = ensure_lds(reinterpret_cast<const void*>(&k_ew_fwd), lds)) return rc;
+    const int nt = pick_threads(lds);
+    auto kern = nt == 256 ? k_ew_fwd<256> : nt == 512 ? k_ew_fwd<512> : k_ew_fwd<1024>;
+    if (int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds)) return rc;
     EwDims D{rank, b->num_bins};
-    FEQ_LAUNCH("k_ew_fwd", k_ew_fwd, dim3(E), dim3(kThreads), lds, stream_of(stream), *L, *b, D, x, P,
-                       Q, dist, C, F, y);
+    FEQ_LAUNCH("k_ew_fwd", kern, dim3(E), dim3(nt), lds, stream_of(stream), *L, *b, D, x, P, Q, dist, C,
+               F, y);
     return FEQ_OK;
 }
 
@@ -462,13 +483,15 @@ extern "C" int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32
     if (!ew_tail_supported(*b, kw))
         return fail(FEQ_ERR_UNSUPPORTED, "empty radial-function rows");
     const size_t lds = bwd_lds(*L, rank);
-    if (int rc = ensure_lds(reinterpret_cast<const void*>(&k_ew_bwd), lds)) return rc;
+    const int nt = pick_threads(lds);
+    auto kern = nt == 256 ? k_ew_bwd<256> : nt == 512 ? k_ew_bwd<512> : k_ew_bwd<1024>;
+    if (int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds)) return rc;
     const int G = groups_for(E);
     float* part = static_cast<float*>(ws);
     float* dFe = part + align_up(static_cast<size_t>(G) * ncc, 64);
     float* tail = dFe + align_up(static_cast<size_t>(E) * kw, 64);
     EwDims D{rank, b->num_bins};
-    FEQ_LAUNCH("k_ew_bwd", k_ew_bwd, dim3(G), dim3(kThreads), lds, s, *L, *b, D, E, gy, x, P, Q, dist,
+    FEQ_LAUNCH("k_ew_bwd", kern, dim3(G), dim3(nt), lds, s, *L, *b, D, E, gy, x, P, Q, dist,
                        C, F, gx, dFe, gdist, gP, gQ, part);
     return ew_tail(*L, *b, rank, E, dist, F, dFe, part, G, ncc, gC, gF, nullptr, tail, s);
 }
