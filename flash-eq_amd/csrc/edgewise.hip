@@ -775,15 +775,13 @@ extern "C" size_t feq_edgewise_fwd_src_pool_workspace(const feq_layout* L, const
     return ew_pool_fwd_workspace(*L, rank, E) + 256;
 }
 
-extern "C" int feq_edgewise_fwd_src_pool(const feq_layout* L, const feq_binning* b, int32_t rank,
-                                         int64_t E, const float* x, int64_t num_src,
-                                         const int64_t* src, const float* P, const float* Q,
-                                         const float* dist, const float* C, const float* F,
-                                         const float* attn, int32_t heads, int32_t chan_per_head,
-                                         const int64_t* dst, const int32_t* perm_dst,
-                                         const int32_t* offsets_dst, int64_t num_dst, float* out,
-                                         float* y_pos, int32_t flags, void* ws, size_t ws_bytes,
-                                         feq_stream_t stream) {
+namespace {
+int fwd_src_pool(const feq_layout* L, const feq_binning* b, int32_t rank, int64_t E, const float* x,
+                 int64_t num_src, const int64_t* src, const float* P, const float* Q, const float* dist,
+                 const float* C, const float* F, const float* attn, int32_t heads, int32_t chan_per_head,
+                 const int64_t* dst, const int32_t* perm_dst, const int32_t* offsets_dst, int64_t num_dst,
+                 float* out, float* y_pos, float* ym, int32_t flags, void* ws, size_t ws_bytes,
+                 feq_stream_t stream) {
     if (int rc = check_layout(L)) return rc;
     if (flags & ~FEQ_EW_HALF_ACCURACY) return fail(FEQ_ERR_INVALID, "unknown flags 0x%x", flags);
     if (int rc = check_binning(b)) return rc;
@@ -797,27 +795,58 @@ extern "C" int feq_edgewise_fwd_src_pool(const feq_layout* L, const feq_binning*
     hipStream_t s = stream_of(stream);
     if (num_dst > 0 && !out) return fail(FEQ_ERR_INVALID, "NULL out");
     if (E == 0) return fill_zero(out, num_dst * L->cout * L->dout, s);
-    if (num_dst == 0) return FEQ_OK;   // no edge has a destination: nothing to sum
+    // no edge has a destination: nothing to sum (and the backward's grad_Q is zero
+    // without reading ym)
+    if (num_dst == 0) return FEQ_OK;
+    if (ym && !feq_edgewise_pq_supported(L, b, rank))
+        return fail(FEQ_ERR_UNSUPPORTED, "no kernels forming the bases' gradients for this layout");
     if (!x || !src || !P || !Q || !dist || !C || !F || !attn || !dst || !perm_dst || !offsets_dst)
         return fail(FEQ_ERR_INVALID, "NULL pointer");
     if (!ws || ws_bytes < feq_edgewise_fwd_src_pool_workspace(L, b, rank, E))
         return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
     const DstPool dp{perm_dst, offsets_dst, dst, attn, num_dst, heads, chan_per_head, out, nullptr};
+    const BasisGrads bg{ym, nullptr, nullptr, nullptr};
     const int rc = ew_split_fwd(*L, *b, rank, E, x, src, num_src, P, Q, dist, C, F, y_pos, ws, ws_bytes,
-                                (flags & FEQ_EW_HALF_ACCURACY) != 0, s, &dp);
+                                (flags & FEQ_EW_HALF_ACCURACY) != 0, s, &dp, ym ? &bg : nullptr);
     return rc == -1 ? fail(FEQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned") : rc;
 }
+}  // namespace
 
-extern "C" int feq_edgewise_bwd_src_pool(const feq_layout* L, const feq_binning* b, int32_t rank,
-                                         int64_t E, const float* grad_out, const float* attn,
-                                         int32_t heads, int32_t chan_per_head, const int64_t* dst,
-                                         int64_t num_dst, const float* x, int64_t num_src,
-                                         const int64_t* src, const int32_t* perm_src,
-                                         const int32_t* offsets_src, const float* P, const float* Q,
+extern "C" int feq_edgewise_fwd_src_pool(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                         int64_t E, const float* x, int64_t num_src,
+                                         const int64_t* src, const float* P, const float* Q,
                                          const float* dist, const float* C, const float* F,
-                                         float* gx_nodes, float* gC, float* gF, float* gdist,
-                                         int32_t flags, void* ws, size_t ws_bytes,
+                                         const float* attn, int32_t heads, int32_t chan_per_head,
+                                         const int64_t* dst, const int32_t* perm_dst,
+                                         const int32_t* offsets_dst, int64_t num_dst, float* out,
+                                         float* y_pos, int32_t flags, void* ws, size_t ws_bytes,
                                          feq_stream_t stream) {
+    return fwd_src_pool(L, b, rank, E, x, num_src, src, P, Q, dist, C, F, attn, heads, chan_per_head, dst,
+                        perm_dst, offsets_dst, num_dst, out, y_pos, nullptr, flags, ws, ws_bytes, stream);
+}
+
+extern "C" int feq_edgewise_fwd_src_pool_ym(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                            int64_t E, const float* x, int64_t num_src,
+                                            const int64_t* src, const float* P, const float* Q,
+                                            const float* dist, const float* C, const float* F,
+                                            const float* attn, int32_t heads, int32_t chan_per_head,
+                                            const int64_t* dst, const int32_t* perm_dst,
+                                            const int32_t* offsets_dst, int64_t num_dst, float* out,
+                                            float* y_pos, float* ym, int32_t flags, void* ws,
+                                            size_t ws_bytes, feq_stream_t stream) {
+    if (!ym) return fail(FEQ_ERR_INVALID, "NULL ym");
+    return fwd_src_pool(L, b, rank, E, x, num_src, src, P, Q, dist, C, F, attn, heads, chan_per_head, dst,
+                        perm_dst, offsets_dst, num_dst, out, y_pos, ym, flags, ws, ws_bytes, stream);
+}
+
+namespace {
+int bwd_src_pool(const feq_layout* L, const feq_binning* b, int32_t rank, int64_t E, const float* grad_out,
+                 const float* attn, int32_t heads, int32_t chan_per_head, const int64_t* dst,
+                 int64_t num_dst, const float* x, int64_t num_src, const int64_t* src,
+                 const int32_t* perm_src, const int32_t* offsets_src, const float* P, const float* Q,
+                 const float* dist, const float* C, const float* F, const float* ym, float* gx_nodes,
+                 float* gC, float* gF, float* gdist, float* gP, float* gQ, int32_t flags, void* ws,
+                 size_t ws_bytes, feq_stream_t stream) {
     if (int rc = check_layout(L)) return rc;
     if (flags & ~FEQ_EW_HALF_ACCURACY) return fail(FEQ_ERR_INVALID, "unknown flags 0x%x", flags);
     if (int rc = check_binning(b)) return rc;
@@ -831,12 +860,20 @@ extern "C" int feq_edgewise_bwd_src_pool(const feq_layout* L, const feq_binning*
     if (!feq_edgewise_pool_supported(L, b, rank))
         return fail(FEQ_ERR_UNSUPPORTED, "no pooled message-passing kernels for this layout");
     hipStream_t s = stream_of(stream);
+    if ((gP || gQ) && !feq_edgewise_pq_supported(L, b, rank))
+        return fail(FEQ_ERR_UNSUPPORTED, "no kernels forming the bases' gradients for this layout");
+    if (gQ && E > 0 && num_dst > 0 && !ym)
+        return fail(FEQ_ERR_INVALID, "grad_Q needs ym, the rows before the rotation");
     if (E == 0 || num_dst == 0) {
         // no edge reaches the pooled output: every gradient is zero
         if (int rc = fill_zero(gF, static_cast<int64_t>(b->num_bins + 1) * rank * L->wdim, s)) return rc;
         if (int rc = fill_zero(gx_nodes, num_src * L->cin * L->din, s)) return rc;
         if (gdist)
             if (int rc = fill_zero(gdist, E, s)) return rc;
+        if (gP)
+            if (int rc = fill_zero(gP, E * L->din * L->din, s)) return rc;
+        if (gQ)
+            if (int rc = fill_zero(gQ, E * L->dout * L->dout, s)) return rc;
         return fill_zero(gC, static_cast<int64_t>(rank) * L->cout * L->cin, s);
     }
     if (!grad_out || !attn || !dst || !x || !src || !perm_src || !offsets_src || !P || !Q || !dist ||
@@ -846,8 +883,40 @@ extern "C" int feq_edgewise_bwd_src_pool(const feq_layout* L, const feq_binning*
         return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
     const NodeScatter ns{perm_src, offsets_src, gx_nodes, nullptr};
     const DstPool dp{nullptr, nullptr, dst, attn, num_dst, heads, chan_per_head, nullptr, nullptr};
+    const BasisGrads bg{nullptr, ym, gP, gQ};
     const int rc = ew_split_bwd(*L, *b, rank, E, grad_out, x, src, num_src, P, Q, dist, C, F, nullptr,
                                 gC, gF, gdist, &ns, ws, ws_bytes, (flags & FEQ_EW_HALF_ACCURACY) != 0, s,
-                                &dp);
+                                &dp, (gP || gQ) ? &bg : nullptr);
     return rc == -1 ? fail(FEQ_ERR_UNSUPPORTED, "tensors must be 16-byte aligned") : rc;
+}
+}  // namespace
+
+extern "C" int feq_edgewise_bwd_src_pool(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                         int64_t E, const float* grad_out, const float* attn,
+                                         int32_t heads, int32_t chan_per_head, const int64_t* dst,
+                                         int64_t num_dst, const float* x, int64_t num_src,
+                                         const int64_t* src, const int32_t* perm_src,
+                                         const int32_t* offsets_src, const float* P, const float* Q,
+                                         const float* dist, const float* C, const float* F,
+                                         float* gx_nodes, float* gC, float* gF, float* gdist,
+                                         int32_t flags, void* ws, size_t ws_bytes,
+                                         feq_stream_t stream) {
+    return bwd_src_pool(L, b, rank, E, grad_out, attn, heads, chan_per_head, dst, num_dst, x, num_src, src,
+                        perm_src, offsets_src, P, Q, dist, C, F, nullptr, gx_nodes, gC, gF, gdist, nullptr,
+                        nullptr, flags, ws, ws_bytes, stream);
+}
+
+extern "C" int feq_edgewise_bwd_src_pool_pq(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                            int64_t E, const float* grad_out, const float* attn,
+                                            int32_t heads, int32_t chan_per_head, const int64_t* dst,
+                                            int64_t num_dst, const float* x, int64_t num_src,
+                                            const int64_t* src, const int32_t* perm_src,
+                                            const int32_t* offsets_src, const float* P, const float* Q,
+                                            const float* dist, const float* C, const float* F,
+                                            const float* ym, float* gx_nodes, float* gC, float* gF,
+                                            float* gdist, float* gP, float* gQ, int32_t flags, void* ws,
+                                            size_t ws_bytes, feq_stream_t stream) {
+    return bwd_src_pool(L, b, rank, E, grad_out, attn, heads, chan_per_head, dst, num_dst, x, num_src, src,
+                        perm_src, offsets_src, P, Q, dist, C, F, ym, gx_nodes, gC, gF, gdist, gP, gQ, flags,
+                        ws, ws_bytes, stream);
 }

@@ -265,6 +265,20 @@ __device__ __forceinline__ void flush_stage(const float* stage, float* __restric
     }
 }
 
+// flush_stage with the rows scattered: staged row j goes to global row rows[j].
+template <int CH, int D>
+__device__ __forceinline__ void flush_stage_rows(const float* stage, float* __restrict__ g,
+                                                 const int32_t* __restrict__ rows, int nval) {
+    constexpr int ROW4 = CH * D / 4, SS4 = stage_stride(CH * D) / 4;
+    static_assert((CH * D) % 4 == 0, "rows of whole float4s");
+    const float4* s4 = reinterpret_cast<const float4*>(stage);
+    float4* g4 = reinterpret_cast<float4*>(g);
+    for (int q = threadIdx.x; q < nval * ROW4; q += kThreads) {
+        const int j = q / ROW4, c = q % ROW4;
+        g4[static_cast<int64_t>(rows[j]) * ROW4 + c] = s4[j * SS4 + c];
+    }
+}
+
 // The staged tile's rows (nval edges, source nodes node[j], -1 for none) summed
 // per node in tile order: a node within the tile gets its row, a node that
 // crosses a tile boundary a partial row (NodeScatter).  node[kNE] and
@@ -571,7 +585,6 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
           const float* __restrict__ Cinv, const float* __restrict__ F, float* __restrict__ y,
           DstPool DP, float* __restrict__ ym) {
     static_assert(GATHER || !POOL, "the pooled form is a message-passing form");
-    static_assert(!(YM && POOL), "the rows before the rotation are kept in edge order");
     using T = Canon<LIN, LOUT>;
     using TG = TermGroups<LIN, LOUT, false>;
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
@@ -887,7 +900,10 @@ k_ews_fwd(feq_binning B, int64_t E, int64_t ntiles, XRows X,
                 stage_rows<COUT, DOUT>(reinterpret_cast<float*>(sB), le, 16 * (wave + 4 * j) + 4 * lg, out);
             }
             __syncthreads();
-            flush_stage<COUT, DOUT>(reinterpret_cast<const float*>(sB), ym + e0 * COUT * DOUT, nval);
+            if constexpr (POOL)   // rows in edge order: tile row e is edge DP.perm[e0 + e]
+                flush_stage_rows<COUT, DOUT>(reinterpret_cast<const float*>(sB), ym, DP.perm + e0, nval);
+            else
+                flush_stage<COUT, DOUT>(reinterpret_cast<const float*>(sB), ym + e0 * COUT * DOUT, nval);
         }
     }
 }
@@ -921,7 +937,6 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             float* __restrict__ gQo) {
     static_assert(GATHER || !SCATTER, "the per-node sums need the message-passing form");
     static_assert(SCATTER || !GP, "the pooled form sums the input gradient per source node");
-    static_assert(!(GPQ && GP), "the bases' gradients are formed for per-edge gradients of y");
     using T = Canon<LIN, LOUT>;
     using TG = TermGroups<LIN, LOUT, true>;
     constexpr int DIN = T::DIN, DOUT = T::DOUT, WD = T::WD, KW = K * WD;
@@ -991,6 +1006,8 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
             } else {
                 grow[p] = valid ? f0 + e : -1;
             }
+            // GPQ: the producer's edge (with GP the gy row is its destination's)
+            if constexpr (GPQ) gqe[p] = GP ? (valid ? gedge[p] : -1) : grow[p];
         }
         int64_t xrow[RPW];
 #pragma unroll
@@ -1033,7 +1050,6 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
 #pragma unroll
                 for (int v = 0; v < 4 * DOUT; ++v) gr[p][v] = 0.0f;
             }
-            if constexpr (GPQ) gqe[p] = grow[p];   // without GP the gy row of a producer is its edge's row
         }
 #pragma unroll
         for (int j = 0; j < RPW; ++j) {
@@ -1182,6 +1198,7 @@ k_ews_bwd_x(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ 
                             float a = 0.0f;
 #pragma unroll
                             for (int r = 0; r < 4; ++r) a += gr[p][r * DOUT + d] * yk[r * DOUT + o];
+                            if constexpr (GP) a *= gw[p];   // gy_e = attn[e, head] gout[dst[e]]
                             a = row16_sum(a);
                             if (c4 == 0 && gqe[p] >= 0) dst[d * DOUT + o] = a;
                         }
@@ -1848,10 +1865,13 @@ int launch_ews_fwd(const feq_binning& B, int64_t E, XRows x, const float* P, con
         if (dp) return fail(FEQ_ERR_INVALID, "the pooled form needs the message-passing form");
     }
     if (ym) {
-        if (dp) return fail(FEQ_ERR_UNSUPPORTED, "the pooled form keeps no rows before the rotation");
         // (one fp16 product per pair only in the message-passing form)
-        kern = lp ? k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, GATHER, GATHER, false, true>
-                  : k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, GATHER, false, false, true>;
+        if (dp)
+            kern = lp ? k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, GATHER, GATHER, GATHER, true>
+                      : k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, GATHER, false, GATHER, true>;
+        else
+            kern = lp ? k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, GATHER, GATHER, false, true>
+                      : k_ews_fwd<CIN, COUT, LIN, LOUT, K, occ, GATHER, false, false, true>;
     }
     if (int rc = ews_set_lds(reinterpret_cast<const void*>(kern), lds)) return rc;
     const int64_t g = static_cast<int64_t>(ews_cus()) * occ;
@@ -1935,7 +1955,6 @@ int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const f
     if (!ws || cv.used > ws_bytes) return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
     if (dp && !ns) return fail(FEQ_ERR_INVALID, "the pooled form needs the per-node input gradient");
     const bool gpq = bg && (bg->gP || bg->gQ);
-    if (gpq && dp) return fail(FEQ_ERR_UNSUPPORTED, "no gradients for the bases in the pooled form");
     if (bg && bg->gQ && !bg->ym) return fail(FEQ_ERR_INVALID, "grad_Q needs the rows before the rotation");
     const float* bym = bg ? bg->ym : nullptr;
     float* bgP = bg ? bg->gP : nullptr;
@@ -1955,7 +1974,10 @@ int launch_ews_bwd(const feq_layout& L, const feq_binning& B, int64_t E, const f
         if (ns) {
             auto kx = lp ? k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, true, false>
                          : k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, false, false>;
-            if (dp)
+            if (dp && gpq)
+                kx = lp ? k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, true, true, true>
+                        : k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, false, true, true>;
+            else if (dp)
                 kx = lp ? k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, true, true>
                         : k_ews_bwd_x<CIN, COUT, LIN, LOUT, K, true, true, false, true>;
             else if (gpq)

@@ -91,6 +91,13 @@ _SIGS = {
                                        _P, _P, _P, _P, _P, _P, _I32, _P, _SZ, _P], ctypes.c_int),
     "feq_edgewise_bwd_src_nodes_workspace": ([_P, _P, _I32, _I64], _SZ),
     "feq_edgewise_pool_supported": ([_P, _P, _I32], ctypes.c_int),
+    # as feq_edgewise_fwd_src_pool with ym after y_pos
+    "feq_edgewise_fwd_src_pool_ym": ([_P, _P, _I32, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _I32, _I32,
+                                      _P, _P, _P, _I64, _P, _P, _P, _I32, _P, _SZ, _P], ctypes.c_int),
+    # as feq_edgewise_bwd_src_pool with ym after F and grad_P, grad_Q after grad_dist
+    "feq_edgewise_bwd_src_pool_pq": ([_P, _P, _I32, _I64, _P, _P, _I32, _I32, _P, _I64, _P, _I64, _P, _P,
+                                      _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _SZ, _P],
+                                     ctypes.c_int),
     "feq_edgewise_fwd_src_pool_workspace": ([_P, _P, _I32, _I64], _SZ),
     "feq_edgewise_fwd_src_pool": ([_P, _P, _I32, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _I32, _I32,
                                    _P, _P, _P, _I64, _P, _P, _I32, _P, _SZ, _P], ctypes.c_int),

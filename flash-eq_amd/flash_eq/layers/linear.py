@@ -208,8 +208,7 @@ class EquivariantEdgewiseLinear(nn.Module):
         call (the caller then forms V and pools it)."""
         if not node_features.is_cuda or graph is None or graph.num_edges != distances.shape[0]:
             return None
-        if torch.is_grad_enabled() and (P.requires_grad or Q.requires_grad):
-            return None
+        pq = torch.is_grad_enabled() and (P.requires_grad or Q.requires_grad)
         cout = self.channels_out
         if (num_heads < 1 or num_heads > N.POOL_MAX_HEADS or cout % num_heads
                 or (cout // num_heads) % 4 or attn.shape != (graph.num_edges, num_heads)
@@ -225,6 +224,8 @@ class EquivariantEdgewiseLinear(nn.Module):
                 return None
             x, Pp, Qp = emb.features(node_features), emb.basis_in(P), emb.basis_out(Q)
             C, F, layout = emb.channels(C), emb.radial(F), emb.layout
+        if pq and not edgewise_pq_supported(layout, binning, rw.rank):
+            return None   # the caller forms V (whose layer forms the bases' gradients) and pools it
         perm_s, offsets_s = graph.csr_src()
         perm_d, offsets_d = graph.csr()
         out = edgewise_attention_pool(x.contiguous(), attn, graph.src, graph.dst, perm_s, offsets_s,

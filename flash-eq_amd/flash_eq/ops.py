@@ -275,27 +275,35 @@ class EdgewiseAttnPoolFn(torch.autograd.Function):
         out = torch.empty(num_dst, layout.cout, layout.dout, dtype=torch.float32, device=dev)
         keep = ctx.needs_input_grad[1] and E > 0
         y_pos = torch.empty(E, layout.cout, layout.dout, dtype=torch.float32, device=dev) if keep else None
+        # gradients for the bases: the rows before the Q rotation, in edge order
+        pq = E > 0 and (ctx.needs_input_grad[9] or ctx.needs_input_grad[10])
+        if pq and not edgewise_pq_supported(layout, binning, rank):
+            raise ValueError("no pooled kernels forming gradients for P and Q for this layout")
+        ym = torch.empty(E, layout.cout, layout.dout, dtype=torch.float32, device=dev) if pq else None
         lib = N.lib()
         ws = N.workspace(lib.feq_edgewise_fwd_src_pool_workspace(N.ctypes.byref(layout),
                                                                  N.ctypes.byref(binning), rank, E), dev)
         with torch.cuda.device(dev):
-            rc = lib.feq_edgewise_fwd_src_pool(
-                N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E, N.ptr(xs), xs.shape[0],
-                N.ptr(si), N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs), N.ptr(Fs), N.ptr(As), heads,
-                chan_per_head, N.ptr(di), N.ptr(perm_d) if E else None, N.ptr(offsets_d), num_dst,
-                N.ptr(out) if num_dst else None, N.ptr(y_pos), flags, N.ptr(ws), ws.numel(),
-                N.stream_ptr(dev))
-        N.check(rc, "feq_edgewise_fwd_src_pool")
+            args = (N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E, N.ptr(xs), xs.shape[0],
+                    N.ptr(si), N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs), N.ptr(Fs), N.ptr(As), heads,
+                    chan_per_head, N.ptr(di), N.ptr(perm_d) if E else None, N.ptr(offsets_d), num_dst,
+                    N.ptr(out) if num_dst else None, N.ptr(y_pos))
+            tail = (flags, N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+            if pq:
+                rc = lib.feq_edgewise_fwd_src_pool_ym(*args, N.ptr(ym), *tail)
+            else:
+                rc = lib.feq_edgewise_fwd_src_pool(*args, *tail)
+        N.check(rc, "feq_edgewise_fwd_src_pool_ym" if pq else "feq_edgewise_fwd_src_pool")
         ctx.save_for_backward(xs, As, si, di, perm_s, offsets_s, perm_d, offsets_d, Ps, Qs, rs, Cs, Fs,
-                              y_pos)
+                              y_pos, ym)
         ctx.meta = (layout, binning, rank, heads, chan_per_head, num_dst, flags,
-                    x.dtype, attn.dtype, dist.dtype, C.dtype, F.dtype)
+                    x.dtype, attn.dtype, dist.dtype, C.dtype, F.dtype, P.dtype, Q.dtype)
         return out.to(x.dtype)
 
     @staticmethod
     def backward(ctx, gout):
-        xs, As, si, di, perm_s, offsets_s, perm_d, offsets_d, Ps, Qs, rs, Cs, Fs, y_pos = ctx.saved_tensors
-        layout, binning, rank, heads, cph, num_dst, flags, xdt, adt, rdt, cdt, fdt = ctx.meta
+        xs, As, si, di, perm_s, offsets_s, perm_d, offsets_d, Ps, Qs, rs, Cs, Fs, y_pos, ym = ctx.saved_tensors
+        layout, binning, rank, heads, cph, num_dst, flags, xdt, adt, rdt, cdt, fdt, pdt, qdt = ctx.meta
         dev = xs.device
         E = si.shape[0]
         need = ctx.needs_input_grad
@@ -311,21 +319,28 @@ class EdgewiseAttnPoolFn(torch.autograd.Function):
                                                      N.stream_ptr(dev))
                 N.check(rc, "feq_attn_pool_grad_attn")
         gx = torch.empty_like(xs)
+        gP = torch.empty_like(Ps) if need[9] else None
+        gQ = torch.empty_like(Qs) if need[10] else None
         gr = torch.empty_like(rs) if need[11] else None
         gC = torch.empty_like(Cs)
         gF = torch.empty_like(Fs)
         ws = N.workspace(lib.feq_edgewise_bwd_src_nodes_workspace(
             N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E), dev)
         with torch.cuda.device(dev):
-            rc = lib.feq_edgewise_bwd_src_pool(
-                N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E, N.ptr(g) if num_dst else None,
-                N.ptr(As), heads, cph, N.ptr(di), num_dst, N.ptr(xs), xs.shape[0], N.ptr(si),
-                N.ptr(perm_s) if E else None, N.ptr(offsets_s), N.ptr(Ps), N.ptr(Qs), N.ptr(rs), N.ptr(Cs),
-                N.ptr(Fs), N.ptr(gx), N.ptr(gC), N.ptr(gF), N.ptr(gr), flags, N.ptr(ws), ws.numel(),
-                N.stream_ptr(dev))
-        N.check(rc, "feq_edgewise_bwd_src_pool")
+            head = (N.ctypes.byref(layout), N.ctypes.byref(binning), rank, E, N.ptr(g) if num_dst else None,
+                    N.ptr(As), heads, cph, N.ptr(di), num_dst, N.ptr(xs), xs.shape[0], N.ptr(si),
+                    N.ptr(perm_s) if E else None, N.ptr(offsets_s), N.ptr(Ps), N.ptr(Qs), N.ptr(rs),
+                    N.ptr(Cs), N.ptr(Fs))
+            tail = (flags, N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+            if ym is not None:
+                rc = lib.feq_edgewise_bwd_src_pool_pq(*head, N.ptr(ym), N.ptr(gx), N.ptr(gC), N.ptr(gF),
+                                                      N.ptr(gr), N.ptr(gP), N.ptr(gQ), *tail)
+            else:
+                rc = lib.feq_edgewise_bwd_src_pool(*head, N.ptr(gx), N.ptr(gC), N.ptr(gF), N.ptr(gr), *tail)
+        N.check(rc, "feq_edgewise_bwd_src_pool_pq" if ym is not None else "feq_edgewise_bwd_src_pool")
+        cast = lambda t, dt: None if t is None else t.to(dt)
         return (gx.to(xdt) if need[0] else None, None if gA is None else gA.to(adt),
-                None, None, None, None, None, None, None, None, None,
+                None, None, None, None, None, None, None, cast(gP, pdt), cast(gQ, qdt),
                 None if gr is None else gr.to(rdt), gC.to(cdt) if need[12] else None,
                 gF.to(fdt) if need[13] else None, None, None, None, None, None, None)
 
@@ -333,8 +348,6 @@ class EdgewiseAttnPoolFn(torch.autograd.Function):
 def edgewise_attention_pool(x, attn, src, dst, perm_s, offsets_s, perm_d, offsets_d, num_dst, P, Q,
                             dist, C, F, layout, binning, rank, heads: int, chan_per_head: int,
                             half_accuracy: bool = False) -> torch.Tensor:
-    if torch.is_grad_enabled() and (P.requires_grad or Q.requires_grad):
-        raise ValueError("the pooled message-passing form does not form gradients for P and Q")
     return EdgewiseAttnPoolFn.apply(x, attn, src, dst, perm_s, offsets_s, perm_d, offsets_d, num_dst, P,
                                     Q, dist, C, F, layout, binning, rank, heads, chan_per_head,
                                     half_accuracy)

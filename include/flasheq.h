@@ -328,6 +328,31 @@ int feq_edgewise_bwd_src_pool(const feq_layout* L, const feq_binning* b, int32_t
                               float* grad_x_nodes, float* grad_C, float* grad_F, float* grad_dist,
                               int32_t flags, void* workspace, size_t ws_bytes, feq_stream_t stream);
 
+/* The pooled form with the gradients for the bases (as feq_edgewise_fwd_ym /
+ * feq_edgewise_bwd_pq for the message-passing form): the forward also writes
+ * m (E, Cout, Dout), the rows before the Q rotation, in edge order; the
+ * backward writes grad_P (E, Din, Din) and grad_Q (E, Dout, Dout) (each may be
+ * NULL; ym is required with grad_Q) with grad_y[e] = attn[e, h(c)]
+ * grad_out[dst[e]] (zero for edges without a destination).  Layouts:
+ * feq_edgewise_pq_supported. */
+int feq_edgewise_fwd_src_pool_ym(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                 int64_t num_edges, const float* x, int64_t num_src, const int64_t* src,
+                                 const float* P, const float* Q, const float* dist, const float* C,
+                                 const float* F, const float* attn, int32_t heads,
+                                 int32_t chan_per_head, const int64_t* dst, const int32_t* perm_dst,
+                                 const int32_t* offsets_dst, int64_t num_dst, float* out, float* y_pos,
+                                 float* ym, int32_t flags, void* workspace, size_t ws_bytes,
+                                 feq_stream_t stream);
+int feq_edgewise_bwd_src_pool_pq(const feq_layout* L, const feq_binning* b, int32_t rank,
+                                 int64_t num_edges, const float* grad_out, const float* attn,
+                                 int32_t heads, int32_t chan_per_head, const int64_t* dst,
+                                 int64_t num_dst, const float* x, int64_t num_src, const int64_t* src,
+                                 const int32_t* perm_src, const int32_t* offsets_src, const float* P,
+                                 const float* Q, const float* dist, const float* C, const float* F,
+                                 const float* ym, float* grad_x_nodes, float* grad_C, float* grad_F,
+                                 float* grad_dist, float* grad_P, float* grad_Q, int32_t flags,
+                                 void* workspace, size_t ws_bytes, feq_stream_t stream);
+
 /* ---- Wigner-D basis ------------------------------------------------------------
  * plan: host-built per-representation constants (see feq_wigner_plan_size);
  * out (E, dim, dim): column j = column perm[j] of D(g), g e_z = dir/|dir|. */

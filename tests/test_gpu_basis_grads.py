@@ -8,7 +8,8 @@ from the tile's accumulators, so a layer whose bases require grad (coordinate
 gradients through WignerDBasis) stays on the split kernels.  Checked against
 the float64 oracle at 1e-5 relative for every gradient, in the edge-rows form,
 the message-passing form (gather and per-node input-gradient sums inside the
-kernels), the zero-embedded small and scalar-output layouts, with only one of P and Q requiring
+kernels), the pooled form of the attention's V projection, the zero-embedded
+small and scalar-output layouts, with only one of P and Q requiring
 grad, and for ragged tiles; the launch log shows the split kernels and no
 shape-generic ones.
 """
@@ -113,6 +114,60 @@ def test_scalar_output_layout_embeds(dev):
     scalar-output kernels form no basis gradients, so with P or Q requiring
     grad it runs zero-embedded in the [0,1,2]x64 split kernels."""
     _check(dev, [0, 1, 2], [0], 64, 8, 4200, seed=17, graph_nodes=700)
+
+
+@pytest.mark.parametrize("lin,cin", [([0, 1, 2], 64), ([0, 1], 32)])
+def test_pooled_form(dev, lin, cin):
+    """The V projection fused with the head weighting and the sum by
+    destination (feq_edgewise_fwd_src_pool_ym / _bwd_src_pool_pq), bases with
+    gradients: out[n] = sum over e into n of attn[e, head(c)] layer(x[src])[e]
+    against the float64 oracle, with the gradients of x, P, Q, attn, r and the
+    radial network; edges without a destination (dst outside the node range)
+    add nothing and get zero basis gradients.  [0,1]x32 runs zero-embedded."""
+    torch.manual_seed(21)
+    heads, Nn, E = 8, 500, 4700
+    lout = [0, 1, 2]
+    layer = fe.EquivariantEdgewiseLinear(fe.Repr(lin, cin), fe.Repr(lout, 64), num_bins=40).to(dev)
+    g = torch.Generator().manual_seed(22)
+    din = sum(2 * l + 1 for l in lin)
+    xn = torch.randn(Nn, cin, din, generator=g)
+    src = torch.randint(0, Nn, (E,), generator=g)
+    dst = torch.randint(0, Nn, (E,), generator=g)
+    d = torch.randn(E, 3, generator=g)
+    r = torch.rand(E, generator=g) * 9.5 + 0.05
+    attn = torch.rand(E, heads, generator=g)
+    P, Q = OW.basis(lin, d).float(), OW.basis(lout, d).float()
+    graph = fe.Graph(src.to(dev), dst.to(dev), Nn)
+    xg, rg, ag = (t.to(dev).requires_grad_(True) for t in (xn, r, attn))
+    Pg, Qg = P.to(dev).requires_grad_(True), Q.to(dev).requires_grad_(True)
+    NAT.profile_summary()
+    NAT.profile_enable(True)
+    out = layer.attention_pool(Pg, Qg, xg, rg, graph, ag, heads)
+    assert out is not None
+    w = torch.randn(out.shape, generator=g)
+    (out * w.to(dev)).sum().backward()
+    torch.cuda.synchronize()
+    NAT.profile_enable(False)
+    launched = NAT.profile_summary()
+    assert "k_pool_order" in launched and "k_ews_bwd_x" in launched, launched
+    assert "k_pool_fwd" not in launched and "k_ew_bwd" not in launched, launched
+
+    params, cfg = OL.module_cfg(layer)
+    xd, rd, ad = xn.double().requires_grad_(True), r.double().requires_grad_(True), \
+        attn.double().requires_grad_(True)
+    Pd, Qd = P.double().requires_grad_(True), Q.double().requires_grad_(True)
+    v = OL.edgewise_linear(xd[src], Pd, Qd, rd, params, cfg)              # (E, 64, 9)
+    head_of = torch.arange(64) // (64 // heads)
+    ref = torch.zeros(Nn, 64, 9, dtype=torch.float64).index_add_(0, dst, v * ad[:, head_of, None])
+    (ref * w.double()).sum().backward()
+    errs = {"out": rel_err(out, ref), "gx": rel_err(xg.grad, xd.grad), "gP": rel_err(Pg.grad, Pd.grad),
+            "gQ": rel_err(Qg.grad, Qd.grad), "gattn": rel_err(ag.grad, ad.grad), "gr": rel_err(rg.grad, rd.grad)}
+    for name, p in layer.radial_weights.named_parameters():
+        errs[name] = rel_err(p.grad, params[name].grad)
+    print({k: f"{v:.1e}" for k, v in errs.items()})
+    bars = {"gr": 1e-4}
+    for k, v in errs.items():
+        assert v < bars.get(k, TOL), (k, errs)
 
 
 def test_pq_entry_points_reject_unsupported(dev):
