@@ -172,6 +172,11 @@ k_att_fwd(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ K,
     }
     const int G = 1 << lgG, NG = 64 >> lgG, g = lane >> lgG, j = lane & (G - 1);
     const int NC = Dh / V;
+    // edges in flight: kUE, fewer when a lane's share of a head row is long
+    // (16 chunks of 4 floats: the rows of kUE edges, and in the edge form the
+    // Q rows too, would not fit the registers)
+    constexpr int UE = NT * V >= 64 ? (NODE ? 2 : 1) : NT * V >= 32 ? 2 : kUE;
+    static_assert(64 % UE == 0, "chunks of 64 positions hold whole groups of UE edges");
     for (int h0 = 0; h0 < H; h0 += NG) {
         const int h = h0 + g;
         const bool hv = h < H;
@@ -179,12 +184,12 @@ k_att_fwd(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ K,
         if constexpr (NODE) ld_head<V, NT>(Q + n * ldq + h * Dh, j, G, NC, hv && cnt > 0, q);
         float m = -INFINITY, s = 0.0f;
         SegChunk sc{};
-        for (int i0 = 0; i0 < cnt; i0 += kUE) {
+        for (int i0 = 0; i0 < cnt; i0 += UE) {
             if ((i0 & 63) == 0) sc.load<NODE>(perm, b, cnt, i0, kidx, nk);
-            int64_t eu[kUE];
-            float k[kUE][NT][V];
+            int64_t eu[UE];
+            float k[UE][NT][V];
 #pragma unroll
-            for (int u = 0; u < kUE; ++u) {
+            for (int u = 0; u < UE; ++u) {
                 const bool live = i0 + u < cnt;
                 const int iu = live ? i0 + u : i0;
                 eu[u] = sc.edge(iu);
@@ -192,22 +197,22 @@ k_att_fwd(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ K,
                 const bool ok = hv && live && kr >= 0;
                 ld_head<V, NT>(K + (ok ? kr : 0) * ldk + h * Dh, j, G, NC, ok, k[u]);
             }
-            float dot[kUE];
+            float dot[UE];
             if constexpr (NODE) {
 #pragma unroll
-                for (int u = 0; u < kUE; ++u) dot[u] = dot_head<V, NT>(q, k[u]);
+                for (int u = 0; u < UE; ++u) dot[u] = dot_head<V, NT>(q, k[u]);
             } else {
 #pragma unroll
-                for (int u = 0; u < kUE; ++u) {
+                for (int u = 0; u < UE; ++u) {
                     float qe[NT][V];
                     ld_head<V, NT>(Q + eu[u] * ldq + h * Dh, j, G, NC, hv && i0 + u < cnt, qe);
                     dot[u] = dot_head<V, NT>(qe, k[u]);
                 }
             }
 #pragma unroll
-            for (int u = 0; u < kUE; ++u) dot[u] = group_sum(dot[u], G);
+            for (int u = 0; u < UE; ++u) dot[u] = group_sum(dot[u], G);
 #pragma unroll
-            for (int u = 0; u < kUE; ++u) {
+            for (int u = 0; u < UE; ++u) {
                 if (i0 + u >= cnt) break;
                 const int64_t e = eu[u];
                 const float qkv = dot[u] * scale;
