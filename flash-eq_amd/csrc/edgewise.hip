@@ -151,7 +151,10 @@ struct EwDims {
 };
 
 // ---------------------------------------------------------------------------
-template <int kThreads>
+// SC: the channel patterns C (K, Cout, Cin) staged in LDS (read in the
+// innermost GEMM loops; from global memory each read exposed the L2 latency),
+// where they fit beside the edge's rows.
+template <int kThreads, bool SC>
 __global__ void __launch_bounds__(kThreads)
 k_ew_fwd(feq_layout L, feq_binning B, EwDims D, const float* __restrict__ x,
          const float* __restrict__ P, const float* __restrict__ Q, const float* __restrict__ dist,
@@ -165,8 +168,11 @@ k_ew_fwd(feq_layout L, feq_binning B, EwDims D, const float* __restrict__ x,
     float* sF = sf + cin * din;     // K*wd
     float* sZ = sF + K * wd;        // cin*dout
     float* sy = sZ + cin * dout;    // cout*dout
+    float* sC = sy + cout * dout;   // K*cout*cin (SC)
     const int64_t e = blockIdx.x;
     const int tid = threadIdx.x;
+    if constexpr (SC)
+        for (int q = tid; q < K * cout * cin; q += kThreads) sC[q] = C[q];
     for (int q = tid; q < cin * din; q += kThreads) sx[q] = x[e * cin * din + q];
     for (int q = tid; q < din * din; q += kThreads) sP[q] = P[e * din * din + q];
     for (int q = tid; q < dout * dout; q += kThreads) sQ[q] = Q[e * dout * dout + q];
@@ -191,7 +197,7 @@ k_ew_fwd(feq_layout L, feq_binning B, EwDims D, const float* __restrict__ x,
         for (int q = tid; q < cin * dout; q += kThreads)
             sZ[q] = z_entry(L, sF + k * wd, sf, q / dout, q % dout);
         __syncthreads();
-        const float* Ck = C + static_cast<int64_t>(k) * cout * cin;
+        const float* Ck = (SC ? sC : C) + static_cast<int64_t>(k) * cout * cin;
         for (int q = tid; q < cout * dout; q += kThreads) {
             const int co = q / dout, slot = q % dout;
             float acc = 0.0f;
@@ -215,7 +221,7 @@ k_ew_fwd(feq_layout L, feq_binning B, EwDims D, const float* __restrict__ x,
 // workgroup in LDS and written as a partial, and the per-edge radial-function
 // gradient dF_e is written per edge; the shared tail bins dF_e and sums the
 // partials in a fixed order (deterministic, no atomics).
-template <int kThreads>
+template <int kThreads, bool SC>
 __global__ void __launch_bounds__(kThreads)
 k_ew_bwd(feq_layout L, feq_binning B, EwDims D, int64_t E, const float* __restrict__ gy,
          const float* __restrict__ x, const float* __restrict__ P, const float* __restrict__ Q,
@@ -238,7 +244,10 @@ k_ew_bwd(feq_layout L, feq_binning B, EwDims D, int64_t E, const float* __restri
     float* sH = sZ + cin * dout;    // cin*dout
     float* sy = sH + cin * dout;    // cout*dout (only with gQ)
     float* sdC = sy + cout * dout;  // K*cout*cin
+    float* sC = sdC + K * cout * cin;   // K*cout*cin (SC)
     const int tid = threadIdx.x;
+    if constexpr (SC)
+        for (int q = tid; q < K * cout * cin; q += kThreads) sC[q] = C[q];   // read after the first barrier
     const int64_t per = (E + gridDim.x - 1) / gridDim.x;
     const int64_t e0 = blockIdx.x * per;
     const int64_t e1 = e0 + per < E ? e0 + per : E;
@@ -276,7 +285,7 @@ k_ew_bwd(feq_layout L, feq_binning B, EwDims D, int64_t E, const float* __restri
         __syncthreads();
         float acc_t = 0.0f, acc_s = 0.0f;
         for (int k = 0; k < K; ++k) {
-            const float* Ck = C + static_cast<int64_t>(k) * cout * cin;
+            const float* Ck = (SC ? sC : C) + static_cast<int64_t>(k) * cout * cin;
             for (int q = tid; q < cin * dout; q += kThreads) {
                 const int ci = q / dout, slot = q % dout;
                 float acc = 0.0f;
@@ -378,6 +387,13 @@ size_t bwd_lds(const feq_layout& L, int K) {
                             2 * L.cin * L.dout + static_cast<size_t>(K) * L.cout * L.cin);
 }
 
+// Bytes of the staged channel patterns (the SC kernels), 0 where they would not
+// fit beside the kernel's other LDS.
+size_t c_lds(const feq_layout& L, int K, size_t base) {
+    const size_t c = sizeof(float) * static_cast<size_t>(K) * L.cout * L.cin;
+    return base + c <= 160 * 1024 ? c : 0;
+}
+
 int ensure_lds(const void* fn, size_t bytes) {
     if (bytes > 160 * 1024) return fail(FEQ_ERR_UNSUPPORTED, "needs %zu bytes of LDS", bytes);
     if (bytes > 64 * 1024)
@@ -440,9 +456,10 @@ extern "C" int feq_edgewise_fwd(const feq_layout* L, const feq_binning* b, int32
                                     ws_bytes, false, stream_of(stream));
         if (rc != -1) return rc;
     }
-    const size_t lds = fwd_lds(*L, rank);
+    const size_t clds = c_lds(*L, rank, fwd_lds(*L, rank)), lds = fwd_lds(*L, rank) + clds;
     const int nt = pick_threads(lds);
-    auto kern = nt == 256 ? k_ew_fwd<256> : nt == 512 ? k_ew_fwd<512> : k_ew_fwd<1024>;
+    auto kern = clds ? (nt == 256 ? k_ew_fwd<256, true> : nt == 512 ? k_ew_fwd<512, true> : k_ew_fwd<1024, true>)
+                     : (nt == 256 ? k_ew_fwd<256, false> : nt == 512 ? k_ew_fwd<512, false> : k_ew_fwd<1024, false>);
     if (int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds)) return rc;
     EwDims D{rank, b->num_bins};
     FEQ_LAUNCH("k_ew_fwd", kern, dim3(E), dim3(nt), lds, stream_of(stream), *L, *b, D, x, P, Q, dist, C,
@@ -482,9 +499,10 @@ extern "C" int feq_edgewise_bwd(const feq_layout* L, const feq_binning* b, int32
     const int kw = rank * L->wdim;
     if (!ew_tail_supported(*b, kw))
         return fail(FEQ_ERR_UNSUPPORTED, "empty radial-function rows");
-    const size_t lds = bwd_lds(*L, rank);
+    const size_t clds = c_lds(*L, rank, bwd_lds(*L, rank)), lds = bwd_lds(*L, rank) + clds;
     const int nt = pick_threads(lds);
-    auto kern = nt == 256 ? k_ew_bwd<256> : nt == 512 ? k_ew_bwd<512> : k_ew_bwd<1024>;
+    auto kern = clds ? (nt == 256 ? k_ew_bwd<256, true> : nt == 512 ? k_ew_bwd<512, true> : k_ew_bwd<1024, true>)
+                     : (nt == 256 ? k_ew_bwd<256, false> : nt == 512 ? k_ew_bwd<512, false> : k_ew_bwd<1024, false>);
     if (int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds)) return rc;
     const int G = groups_for(E);
     float* part = static_cast<float*>(ws);
