@@ -85,3 +85,45 @@ def test_noalloc_scratch_covers_every_message_passing_layout():
         frag = 4 * cout * cin * 2 * 2                  # rank x Cout x Cin, hi + lo halves
         assert need == -(-frag // 256) * 256 + 256 + 256, (lin, lout, cin, cout, need)
         assert need <= cap
+
+
+def test_support_queries_and_basis_gradient_argument_errors():
+    """Host-side behaviour of the fused layer's support queries and of the
+    basis-gradient entry points' argument checks (no GPU work: the checks run
+    before any launch; the pointers are never dereferenced)."""
+    lib = N.load_library()
+    b = N.make_binning(0.0, 10.0, 100, False, 0.1)
+
+    def lay(lin, lout, cin, cout):
+        return N.make_layout(lin, lout, cin, cout)
+
+    # the split family forms the bases' gradients; the scalar-output and
+    # shape-generic layouts do not
+    assert lib.feq_edgewise_pq_supported(ctypes.byref(lay([0, 1, 2], [0, 1, 2], 64, 64)), ctypes.byref(b), 4) == 1
+    assert lib.feq_edgewise_pq_supported(ctypes.byref(lay([0, 1, 2], [0], 64, 8)), ctypes.byref(b), 4) == 0
+    assert lib.feq_edgewise_pq_supported(ctypes.byref(lay([0, 1], [0, 1], 8, 8)), ctypes.byref(b), 4) == 0
+    assert lib.feq_edgewise_pq_supported(ctypes.byref(lay([0, 1, 2], [0, 1, 2], 64, 64)), ctypes.byref(b), 3) == 0
+    # LDS: lvals 0..6 fit the fused pair at 32 channels, not at 64
+    L6 = list(range(7))
+    assert lib.feq_edgewise_fused_supported(ctypes.byref(lay(L6, L6, 32, 32)), ctypes.byref(b), 4) == 1
+    assert lib.feq_edgewise_fused_supported(ctypes.byref(lay(L6, L6, 64, 64)), ctypes.byref(b), 4) == 0
+    assert lib.feq_edgewise_fused_supported(ctypes.byref(lay([0, 1, 2], [0, 1, 2], 64, 64)), ctypes.byref(b), 4) == 1
+
+    L = lay([0, 1, 2], [0, 1, 2], 64, 64)
+    fake = ctypes.c_void_p(256)          # never dereferenced: the checks fail first
+    E = 10
+    rc = lib.feq_edgewise_bwd_pq(ctypes.byref(L), ctypes.byref(b), 4, E, fake, fake, 0, None, None, None,
+                                 fake, fake, fake, fake, fake, None, fake, fake, fake, None, None, fake, 0,
+                                 fake, 1 << 30, None)
+    assert rc != 0 and "grad_Q needs ym" in lib.feq_last_error().decode()
+    rc = lib.feq_edgewise_fwd_ym(ctypes.byref(L), ctypes.byref(b), 4, E, fake, 0, None, fake, fake, fake,
+                                 fake, fake, fake, None, 0, fake, 1 << 20, None)
+    assert rc != 0 and "NULL pointer" in lib.feq_last_error().decode()
+    rc = lib.feq_edgewise_fwd_ym(ctypes.byref(L), ctypes.byref(b), 4, E, fake, 0, None, fake, fake, fake,
+                                 fake, fake, fake, fake, 2, fake, 1 << 20, None)
+    assert rc != 0 and "unknown flags" in lib.feq_last_error().decode()
+    S = lay([0, 1, 2], [0], 64, 8)
+    rc = lib.feq_edgewise_bwd_pq(ctypes.byref(S), ctypes.byref(b), 4, E, fake, fake, 0, None, None, None,
+                                 fake, fake, fake, fake, fake, fake, fake, fake, fake, None, fake, fake, 0,
+                                 fake, 1 << 30, None)
+    assert rc != 0 and "bases' gradients" in lib.feq_last_error().decode()
