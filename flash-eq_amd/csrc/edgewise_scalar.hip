@@ -196,12 +196,13 @@ constexpr int kGroup = 4;   // edges loaded together (forward)
 constexpr int kGroupB = 2;  // edges loaded together (backward: more state per edge)
 
 // Forward: waves walk groups of kGroup consecutive edges (grid-stride).
-template <int LIN, int COUT, int K>
+// YM: also writes m = y / Q[0, 0] (the rows before the rotation) to ym.
+template <int LIN, int COUT, int K, bool YM = false>
 __global__ void __launch_bounds__(64 * kWaves)
 k_ew0_fwd(feq_binning B, int64_t E, const float* __restrict__ x, const int64_t* __restrict__ src,
           int64_t nsrc, const float* __restrict__ P, const float* __restrict__ Q,
           const float* __restrict__ dist, const float* __restrict__ C, const float* __restrict__ F,
-          float* __restrict__ y) {
+          float* __restrict__ y, float* __restrict__ ym) {
     using G = Group0<LIN, kGroup>;
     constexpr int NL = G::NL;
     extern __shared__ float sF[];
@@ -239,7 +240,10 @@ k_ew0_fwd(feq_binning B, int64_t E, const float* __restrict__ x, const int64_t* 
             }
             const float sum = wave_sums<COUT>(v);
             constexpr int GROUP = 64 / COUT;   // lanes that hold one output
-            if (lane % GROUP == 0) y[(e0 + i) * COUT + lane / GROUP] = sum * g.q[i];
+            if (lane % GROUP == 0) {
+                y[(e0 + i) * COUT + lane / GROUP] = sum * g.q[i];
+                if constexpr (YM) ym[(e0 + i) * COUT + lane / GROUP] = sum;
+            }
         }
     }
 }
@@ -247,17 +251,25 @@ k_ew0_fwd(feq_binning B, int64_t E, const float* __restrict__ x, const int64_t* 
 // Backward: a wave per 16-edge tile (grid-stride over tiles), its positions in
 // groups of kGroupB.  perm: NULL for the identity order; without NS.perm the
 // per-edge dx rows go to gx.
-template <int LIN, int COUT, int K>
+// GPQ: also the gradients for the bases (either pointer may be NULL):
+//   gP[e][d, l] = sum_c x[c, d] dL/dfs0[c, l] for the m = 0 columns l <= Lin
+//                 (zero in the other columns: y does not read them),
+//   gQ[e]       = sum_co gy[co] ym[co]  (ym: the forward's rows before Q).
+// The gP sums ride in the same wave reduction as the dF_e row.
+template <int LIN, int COUT, int K, bool GPQ = false>
 __global__ void __launch_bounds__(64 * kWaves)
 k_ew0_bwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy,
           const float* __restrict__ x, const int64_t* __restrict__ src, int64_t nsrc,
           const float* __restrict__ P, const float* __restrict__ Q, const float* __restrict__ dist,
           const float* __restrict__ C, const float* __restrict__ F, float* __restrict__ gx,
-          float* __restrict__ dFe, float* __restrict__ dCp, NodeScatter NS) {
+          float* __restrict__ dFe, float* __restrict__ dCp, NodeScatter NS,
+          const float* __restrict__ ym, float* __restrict__ gPo, float* __restrict__ gQo) {
     using G = Group0<LIN, kGroupB>;
     constexpr int DIN = G::DIN, NL = G::NL, KW = K * NL;
-    constexpr int NV = KW <= 1 ? 1 : (KW <= 2 ? 2 : (KW <= 4 ? 4 : (KW <= 8 ? 8 : (KW <= 16 ? 16 : 32))));
-    static_assert(KW <= 32, "radial row of at most 32 values");
+    constexpr int NS0 = GPQ ? KW + DIN * NL : KW;   // wave sums per edge
+    constexpr int NV = NS0 <= 1 ? 1 : (NS0 <= 2 ? 2 : (NS0 <= 4 ? 4 : (NS0 <= 8 ? 8 : (NS0 <= 16 ? 16 : (NS0 <= 32 ? 32 : 64)))));
+    static_assert(NS0 <= 64, "at most 64 sums per edge");
+    static_assert(!GPQ || DIN * DIN <= 128, "two gP entries per lane");
     static_assert(kTile % kGroupB == 0, "whole groups per tile");
     extern __shared__ float sF[];
     __shared__ float sdc[kWaves][K * COUT][64];
@@ -336,13 +348,40 @@ k_ew0_bwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy
                     for (int l = 0; l < NL; ++l) a += g.pc[i][d][l] * gfs[l];
                     dx[d] = a;
                 }
-                // dF_e[k, l] = s^l sum_c gz[c, k] fs0[c, l]
+                // dF_e[k, l] = s^l sum_c gz[c, k] fs0[c, l]  (then gP's sums)
                 float dv[NV];
 #pragma unroll
-                for (int q = 0; q < NV; ++q) dv[q] = q < KW ? gz[q / NL] * fs0[q % NL] * pw[q % NL] : 0.0f;
+                for (int q = 0; q < NV; ++q) {
+                    float v = 0.0f;
+                    if (q < KW)
+                        v = gz[q / NL] * fs0[q % NL] * pw[q % NL];
+                    else if (q < NS0)
+                        v = g.xr[i][(q - KW) / NL] * gfs[(q - KW) % NL];
+                    dv[q] = v;
+                }
                 const float ds = wave_sums<NV>(dv);
                 constexpr int GROUP = 64 / NV;
                 if (lane % GROUP == 0 && lane / GROUP < KW) dFe[e[i] * KW + lane / GROUP] = ds;
+                if constexpr (GPQ) {
+                    // lane q GROUP holds sum q; entry n = d DIN + l of gP reads sum
+                    // KW + d NL + l when l < NL
+                    if (gPo) {
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const int n = lane + 64 * h;
+                            const int d = n / DIN, l = n % DIN;
+                            const bool m0 = l < NL && n < DIN * DIN;
+                            const float v = __shfl(ds, m0 ? (KW + d * NL + l) * GROUP : 0, 64);
+                            if (n < DIN * DIN) gPo[e[i] * DIN * DIN + n] = m0 ? v : 0.0f;
+                        }
+                    }
+                    if (gQo) {
+                        float a = 0.0f;
+#pragma unroll
+                        for (int co = 0; co < COUT; ++co) a += gy[e[i] * COUT + co] * ym[e[i] * COUT + co];
+                        if (lane == 0) gQo[e[i]] = a;
+                    }
+                }
                 if (!nodes) {
                     float* gr = gx + (e[i] * kCin + lane) * DIN;
 #pragma unroll
@@ -447,16 +486,16 @@ size_t ew0_bwd_workspace(const feq_layout& L, const feq_binning& B, int rank, in
 
 int ew0_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
             const int64_t* src, int64_t nsrc, const float* P, const float* Q, const float* dist,
-            const float* C, const float* F, float* y, hipStream_t s) {
+            const float* C, const float* F, float* y, float* ym, hipStream_t s) {
     const int64_t g = static_cast<int64_t>(sc_cus()) * 8, need = ceil_div(ceil_div(E, kGroup), kWaves);
     const unsigned grid = static_cast<unsigned>(need < g ? need : g);
     const size_t lds = 4 * static_cast<size_t>(B.num_bins + 1) * rank * L.wdim;
 #define FEQ_FWD(li, co)                                                                      \
     if (L.cout == co && canonical0(L, li)) {                                                 \
-        auto kern = k_ew0_fwd<li, co, kRank0>;                                               \
+        auto kern = ym ? k_ew0_fwd<li, co, kRank0, true> : k_ew0_fwd<li, co, kRank0>;        \
         if (int rc = table_lds(reinterpret_cast<const void*>(kern), lds)) return rc;         \
         FEQ_LAUNCH("k_ew0_fwd", kern, dim3(grid), dim3(64 * kWaves), lds, s, B, E, x, src, nsrc, P, \
-                   Q, dist, C, F, y);                                                        \
+                   Q, dist, C, F, y, ym);                                                    \
         return FEQ_OK;                                                                       \
     }
     if (rank == kRank0 && L.cin == kCin) {
@@ -469,7 +508,9 @@ int ew0_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, cons
 int ew0_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* gy,
             const float* x, const int64_t* src, int64_t nsrc, const float* P, const float* Q,
             const float* dist, const float* C, const float* F, float* gx, float* gC, float* gF,
-            float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, hipStream_t s) {
+            float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, hipStream_t s,
+            const float* ym, float* gP, float* gQ) {
+    if (gQ && !ym) return fail(FEQ_ERR_INVALID, "grad_Q needs the rows before the rotation");
     if (ws_bytes < ew0_bwd_workspace(L, B, rank, E, ns != nullptr))
         return fail(FEQ_ERR_WORKSPACE, "edgewise workspace too small");
     const int64_t ntiles = ceil_div(E, kTile);
@@ -488,10 +529,10 @@ int ew0_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, cons
     const size_t lds = 4 * static_cast<size_t>(B.num_bins + 1) * rank * L.wdim;
 #define FEQ_BWD(li, co)                                                                          \
     if (L.cout == co && canonical0(L, li)) {                                                     \
-        auto kern = k_ew0_bwd<li, co, kRank0>;                                                   \
+        auto kern = (gP || gQ) ? k_ew0_bwd<li, co, kRank0, true> : k_ew0_bwd<li, co, kRank0>;   \
         if (int rc = table_lds(reinterpret_cast<const void*>(kern), lds)) return rc;             \
         FEQ_LAUNCH("k_ew0_bwd", kern, dim3(G), dim3(64 * kWaves), lds, s, B, E, ntiles, gy, x, src, \
-                   nsrc, P, Q, dist, C, F, gx, dFe, dCp, NS);                                   \
+                   nsrc, P, Q, dist, C, F, gx, dFe, dCp, NS, ym, gP, gQ);                       \
         if (ns)                                                                                  \
             if (int rc = node_fix(NS, nsrc, static_cast<int64_t>(L.cin) * L.din / 4, s)) return rc; \
         return ew_tail(L, B, rank, E, dist, F, dFe, dCp, G, ncc, gC, gF, gdist, tail, s);        \

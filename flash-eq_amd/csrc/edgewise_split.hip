@@ -2080,9 +2080,8 @@ int ew_split_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
         return -1;
     if (ew0_supported(L, rank)) {
         if (dp) return fail(FEQ_ERR_UNSUPPORTED, "no pooled form for scalar-output layouts");
-        if (bg && (bg->gP || bg->gQ)) return -1;
         return ew0_bwd(L, B, rank, E, gy, x, src, nsrc, P, Q, dist, C, F, gx, gC, gF, gdist, ns, ws,
-                       ws_bytes, s);
+                       ws_bytes, s, bg ? bg->ym : nullptr, bg ? bg->gP : nullptr, bg ? bg->gQ : nullptr);
     }
     if (dp && !src) return fail(FEQ_ERR_INVALID, "the pooled form needs the message-passing form");
     const XRows X{x, src, nsrc};
@@ -2107,8 +2106,7 @@ int ew_split_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E,
     float* ym = bg ? bg->ym_out : nullptr;
     if (ew0_supported(L, rank)) {
         if (dp) return fail(FEQ_ERR_UNSUPPORTED, "no pooled form for scalar-output layouts");
-        if (ym) return -1;
-        return ew0_fwd(L, B, rank, E, x, src, nsrc, P, Q, dist, C, F, y, s);
+        return ew0_fwd(L, B, rank, E, x, src, nsrc, P, Q, dist, C, F, y, ym, s);
     }
     if (!aligned16(x) || !aligned16(P) || !aligned16(Q) || !aligned16(y) || (dp && !aligned16(dp->out)) ||
         (ym && !aligned16(ym)))
@@ -2140,7 +2138,7 @@ bool ew_split_supported(const feq_layout& L, const feq_binning& B, int rank, boo
 }
 
 bool ew_split_pq_supported(const feq_layout& L, const feq_binning& B, int rank) {
-    return rank == 4 && !ew0_supported(L, rank) && ew_split_supported(L, B, rank, true);
+    return rank == 4 && ew_split_supported(L, B, rank, true);
 }
 
 bool ew_pool_supported(const feq_layout& L, const feq_binning& B, int rank) {

@@ -181,11 +181,12 @@ bool ew0_supported(const feq_layout& L, int rank);
 size_t ew0_bwd_workspace(const feq_layout& L, const feq_binning& B, int rank, int64_t E, bool nodes);
 int ew0_fwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* x,
             const int64_t* src, int64_t nsrc, const float* P, const float* Q, const float* dist,
-            const float* C, const float* F, float* y, hipStream_t s);
+            const float* C, const float* F, float* y, float* ym, hipStream_t s);
 int ew0_bwd(const feq_layout& L, const feq_binning& B, int rank, int64_t E, const float* gy,
             const float* x, const int64_t* src, int64_t nsrc, const float* P, const float* Q,
             const float* dist, const float* C, const float* F, float* gx, float* gC, float* gF,
-            float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, hipStream_t s);
+            float* gdist, const NodeScatter* ns, void* ws, size_t ws_bytes, hipStream_t s,
+            const float* ym = nullptr, float* gP = nullptr, float* gQ = nullptr);
 
 // Kernel family of the fused edgewise layer.  The default tries the split-fp16
 // kernels, then the shape-generic ones; FEQ_EW_PATH=generic (or

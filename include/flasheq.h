@@ -183,7 +183,8 @@ int feq_edgewise_fused_supported(const feq_layout* L, const feq_binning* b, int3
  * (E, Din, Din) and grad_Q (E, Dout, Dout) (each may be NULL; ym is required
  * with grad_Q), both formed inside the input-gradient kernel's tiles: grad_Q
  * from the grad_y and m rows its producers load, grad_P from the tile's dL/df
- * and x rows.  src NULL: grad_x (E, Cin, Din) per edge, workspace
+ * and x rows (scalar-output layouts, lvals_out = [0]: in the wave-per-edge
+ * backward, grad_P zero outside the m = 0 columns that y reads).  src NULL: grad_x (E, Cin, Din) per edge, workspace
  * feq_edgewise_workspace bytes; src set: grad_x (num_src, Cin, Din) summed per
  * source node over the CSR by source perm_src / offsets_src, as
  * feq_edgewise_bwd_src_nodes_ex, workspace

@@ -9,9 +9,9 @@ gradients through WignerDBasis) stays on the split kernels.  Checked against
 the float64 oracle at 1e-5 relative for every gradient, in the edge-rows form,
 the message-passing form (gather and per-node input-gradient sums inside the
 kernels), the pooled form of the attention's V projection, the zero-embedded
-small and scalar-output layouts, with only one of P and Q requiring
-grad, and for ragged tiles; the launch log shows the split kernels and no
-shape-generic ones.
+small layouts, the scalar-output layouts on their own wave-per-edge kernels,
+with only one of P and Q requiring grad, and for ragged tiles; the launch log
+shows the fast kernels and no shape-generic ones.
 """
 import pytest
 import torch
@@ -26,7 +26,8 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-5
 
 
-def _check(dev, lin, lout, cin, cout, E, seed, graph_nodes=None, grad_p=True, grad_q=True, rmax=9.5):
+def _check(dev, lin, lout, cin, cout, E, seed, graph_nodes=None, grad_p=True, grad_q=True, rmax=9.5,
+           kernels=("k_ews_fwd", "k_ews_bwd_x")):
     torch.manual_seed(seed)
     layer = fe.EquivariantEdgewiseLinear(fe.Repr(lin, cin), fe.Repr(lout, cout), num_bins=50).to(dev)
     g = torch.Generator().manual_seed(seed + 1)
@@ -58,7 +59,7 @@ def _check(dev, lin, lout, cin, cout, E, seed, graph_nodes=None, grad_p=True, gr
     torch.cuda.synchronize()
     NAT.profile_enable(False)
     launched = NAT.profile_summary()
-    assert "k_ews_bwd_x" in launched and "k_ews_fwd" in launched, launched
+    assert all(k in launched for k in kernels), launched
     assert "k_ew_bwd" not in launched and "k_ew_fwd" not in launched, launched
 
     params, cfg = OL.module_cfg(layer)
@@ -109,11 +110,21 @@ def test_embedded_layout(dev):
     _check(dev, [0, 1], [0, 1, 2], 32, 64, 4500, seed=13, graph_nodes=900)
 
 
-def test_scalar_output_layout_embeds(dev):
-    """[0,1,2]x64 -> [0]x8 (the last layer of config 4's model): its
-    scalar-output kernels form no basis gradients, so with P or Q requiring
-    grad it runs zero-embedded in the [0,1,2]x64 split kernels."""
-    _check(dev, [0, 1, 2], [0], 64, 8, 4200, seed=17, graph_nodes=700)
+@pytest.mark.parametrize("graph_nodes,grad_p,grad_q", [(700, True, True), (None, True, True),
+                                                       (700, True, False), (None, False, True)])
+def test_scalar_output_layout(dev, graph_nodes, grad_p, grad_q):
+    """[0,1,2]x64 -> [0]x8 (the last layer of config 4's model) on its own
+    scalar-output kernels: the forward keeps m = y / Q, the wave-per-edge
+    backward forms grad_Q = gy . m and grad_P in the m = 0 columns (zero in
+    the others, which y does not read)."""
+    _check(dev, [0, 1, 2], [0], 64, 8, 4200, seed=17, graph_nodes=graph_nodes, grad_p=grad_p,
+           grad_q=grad_q, kernels=("k_ew0_fwd", "k_ew0_bwd"))
+
+
+def test_scalar_output_one_channel(dev):
+    """[0,1,2]x64 -> [0]x1, ragged tiles."""
+    _check(dev, [0, 1, 2], [0], 64, 1, 1001, seed=19, graph_nodes=300,
+           kernels=("k_ew0_fwd", "k_ew0_bwd"))
 
 
 @pytest.mark.parametrize("lin,cin", [([0, 1, 2], 64), ([0, 1], 32)])

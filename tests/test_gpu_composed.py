@@ -338,9 +338,10 @@ C4_MAX_DIST = 30.0
 def test_model_config4_shape(dev):
     """Config 4's model (6 layers, [0,1]x32 -> [0,1,2]x64 -> [0]x8, 8 heads) on a
     random-walk chain of 200 nodes with k = 24 neighbours, coordinates with grad.
-    Every edgewise layer forms the bases' gradients on the split kernels (the
-    first and the scalar-output last layer zero-embedded in [0,1,2]x64), as the
-    launch log confirms: no shape-generic kernel runs."""
+    Every edgewise layer forms the bases' gradients on the fast kernels (the
+    first zero-embedded in the [0,1,2]x64 split kernels, the scalar-output last
+    one on its own wave-per-edge kernels), as the launch log confirms: no
+    shape-generic kernel runs."""
     coords, src, dst = _config4_graph()
     Nn = coords.shape[0]
     g = torch.Generator().manual_seed(44)
@@ -357,7 +358,8 @@ def test_model_config4_shape(dev):
     NAT.profile_enable(False)
     launched = NAT.profile_summary()
     assert "k_ew_fwd" not in launched and "k_ew_bwd" not in launched, launched
-    assert launched["k_ews_bwd_x"][0] == 6 and launched["k_ews_fwd"][0] == 6, launched
+    assert launched["k_ews_bwd_x"][0] == 5 and launched["k_ews_fwd"][0] == 5, launched
+    assert launched["k_ew0_bwd"][0] == 1 and launched["k_ew0_fwd"][0] == 1, launched
     x.grad, xyz.grad = None, None
     for p in model.parameters():
         p.grad = None

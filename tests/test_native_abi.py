@@ -97,10 +97,10 @@ def test_support_queries_and_basis_gradient_argument_errors():
     def lay(lin, lout, cin, cout):
         return N.make_layout(lin, lout, cin, cout)
 
-    # the split family forms the bases' gradients; the scalar-output and
+    # the split and scalar-output families form the bases' gradients; the
     # shape-generic layouts do not
     assert lib.feq_edgewise_pq_supported(ctypes.byref(lay([0, 1, 2], [0, 1, 2], 64, 64)), ctypes.byref(b), 4) == 1
-    assert lib.feq_edgewise_pq_supported(ctypes.byref(lay([0, 1, 2], [0], 64, 8)), ctypes.byref(b), 4) == 0
+    assert lib.feq_edgewise_pq_supported(ctypes.byref(lay([0, 1, 2], [0], 64, 8)), ctypes.byref(b), 4) == 1
     assert lib.feq_edgewise_pq_supported(ctypes.byref(lay([0, 1], [0, 1], 8, 8)), ctypes.byref(b), 4) == 0
     assert lib.feq_edgewise_pq_supported(ctypes.byref(lay([0, 1, 2], [0, 1, 2], 64, 64)), ctypes.byref(b), 3) == 0
     # LDS: lvals 0..6 fit the fused pair at 32 channels, not at 64
@@ -122,7 +122,7 @@ def test_support_queries_and_basis_gradient_argument_errors():
     rc = lib.feq_edgewise_fwd_ym(ctypes.byref(L), ctypes.byref(b), 4, E, fake, 0, None, fake, fake, fake,
                                  fake, fake, fake, fake, 2, fake, 1 << 20, None)
     assert rc != 0 and "unknown flags" in lib.feq_last_error().decode()
-    S = lay([0, 1, 2], [0], 64, 8)
+    S = lay([0, 1], [0, 1], 8, 8)        # shape-generic: no kernels forming grad_P / grad_Q
     rc = lib.feq_edgewise_bwd_pq(ctypes.byref(S), ctypes.byref(b), 4, E, fake, fake, 0, None, None, None,
                                  fake, fake, fake, fake, fake, fake, fake, fake, fake, None, fake, fake, 0,
                                  fake, 1 << 30, None)
