@@ -142,6 +142,12 @@ _SIGS = {
     "feq_radial_fwd": ([_P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P], ctypes.c_int),
     "feq_radial_bwd": ([_P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
                        ctypes.c_int),
+    "feq_eqlinear_supported": ([_I32, _I32], ctypes.c_int),
+    "feq_eqlinear_workspace": ([_I32, _I32, _I32], _SZ),
+    "feq_eqlinear_fwd": ([_P, _I32, _I64, _I32, _I32, _P, _P, _P, _I32, _P, _P, _P, _SZ, _P], ctypes.c_int),
+    "feq_eqlinear_bwd_x": ([_P, _I32, _I64, _I32, _I32, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
+    "feq_eqlinear_bwd_w_workspace": ([_P, _I32, _I64, _I32, _I32], _SZ),
+    "feq_eqlinear_bwd_w": ([_P, _I32, _I64, _I32, _I32, _P, _P, _I32, _P, _P, _P, _P, _SZ, _P], ctypes.c_int),
     "feq_transpose": ([_P, _I64, _I64, _I64, _I32, _P, _P], ctypes.c_int),
     "feq_column_sums_workspace": ([_I64, _I64, _I32], _SZ),
     "feq_column_sums": ([_P, _I64, _I64, _I32, _P, _P, _SZ, _P], ctypes.c_int),

@@ -9,6 +9,7 @@ generic block-diagonal op's own float64 kernels and is rejected elsewhere
 """
 from __future__ import annotations
 
+import os
 from functools import lru_cache
 from typing import Optional, Sequence, Tuple
 
@@ -1195,11 +1196,26 @@ class GatingFn(torch.autograd.Function):
         return gx, gw, gb, None, None, None, None
 
 
+def _slice_lvals(slices) -> Tuple[int, ...]:
+    return tuple((b - a - 1) // 2 for a, b in slices)
+
+
+def eqlinear_kernels_ok(fd: torch.Tensor, weight: torch.Tensor, slices, cin: int, cout: int) -> bool:
+    """One ``feq_eqlinear_*`` launch per map: float32 GPU tables, channel
+    counts the kernels have (32, 64 or 128 each), at most 16 irreps and
+    64 components.  ``FEQ_EQLINEAR=lib`` keeps the per-irrep library GEMMs."""
+    return (fd.is_cuda and fd.dtype == torch.float32 and weight.dtype == torch.float32
+            and os.environ.get("FEQ_EQLINEAR") != "lib" and len(slices) <= 16
+            and slices[-1][1] <= 64 and bool(N.lib().feq_eqlinear_supported(cin, cout)))
+
+
 class EqLinearFn(torch.autograd.Function):
-    """EquivariantLinear (linear.py:242-268) in component-major form: one GEMM
-    per irrep, (rows * (2l+1), cin) x (cin, cout), written straight into its
-    slice of a (dim, rows, cout) table (no concatenation); the bias of the j-th
-    scalar irrep is the GEMM's bias column.  Input and output are node-major
+    """EquivariantLinear (linear.py:242-268) in component-major form: one
+    feq_eqlinear_* launch per direction over every irrep (split-fp16 matrix-core
+    products, float32 accuracy), or, where those kernels lack the channel
+    counts, one library GEMM per irrep, (rows * (2l+1), cin) x (cin, cout),
+    written straight into its slice of a (dim, rows, cout) table; the bias of
+    the j-th scalar irrep is the GEMM's bias column.  Input and output are node-major
     (rows, c, dim) or, with in_cm / out_cm, component-major (dim, rows, c), so
     consecutive linear maps and the gating can skip the transposes."""
 
@@ -1214,14 +1230,28 @@ class EqLinearFn(torch.autograd.Function):
         D, rows = fd.shape[0], fd.shape[1]
         w = weight.detach().view(-1, cout, cin)
         out = torch.empty(D, rows, cout, dtype=fd.dtype, device=fd.device)
-        for k, (a, b) in enumerate(slices):
-            xk = fd[a:b].view(-1, cin)
-            ok = out[a:b].view(-1, cout)
-            j = bias_cols[k]
-            if bias is not None and j >= 0:
-                torch.addmm(bias.detach()[:, j], xk, w[k].t(), out=ok)
-            else:
-                torch.mm(xk, w[k].t(), out=ok)
+        if eqlinear_kernels_ok(fd, weight, slices, cin, cout):
+            lib = N.lib()
+            nreps = len(slices)
+            wc = weight.detach().contiguous()
+            bc = bias.detach().contiguous() if bias is not None else None
+            ws = N.workspace(lib.feq_eqlinear_workspace(nreps, cin, cout), fd.device)
+            with torch.cuda.device(fd.device):
+                rc = lib.feq_eqlinear_fwd(_lvals_i32(_slice_lvals(slices)), nreps, rows, cin, cout,
+                                          N.ptr(fd), N.ptr(wc), N.ptr(bc) if bc is not None else None,
+                                          bc.shape[1] if bc is not None else 0,
+                                          _lvals_i32(bias_cols) if bc is not None else None, N.ptr(out),
+                                          N.ptr(ws), ws.numel(), N.stream_ptr(fd.device))
+            N.check(rc, "feq_eqlinear_fwd")
+        else:
+            for k, (a, b) in enumerate(slices):
+                xk = fd[a:b].view(-1, cin)
+                ok = out[a:b].view(-1, cout)
+                j = bias_cols[k]
+                if bias is not None and j >= 0:
+                    torch.addmm(bias.detach()[:, j], xk, w[k].t(), out=ok)
+                else:
+                    torch.mm(xk, w[k].t(), out=ok)
         ctx.save_for_backward(fd, weight, bias)
         ctx.meta = (slices, bias_cols, cin, cout, in_cm, out_cm, tuple(f.shape))
         return out if out_cm else transpose_last2(out, D, rows * cout).view(rows, cout, D)
@@ -1238,13 +1268,39 @@ class EqLinearFn(torch.autograd.Function):
         gfd = torch.empty_like(fd) if ctx.needs_input_grad[0] else None
         gw = torch.empty_like(w) if ctx.needs_input_grad[1] else None
         gb = torch.zeros_like(bias) if bias is not None and ctx.needs_input_grad[2] else None
+        fused_x = gfd is not None and eqlinear_kernels_ok(gyd, weight, slices, cin, cout)
+        if fused_x:
+            lib = N.lib()
+            nreps = len(slices)
+            wc = weight.detach().contiguous()
+            ws = N.workspace(lib.feq_eqlinear_workspace(nreps, cin, cout), gyd.device)
+            with torch.cuda.device(gyd.device):
+                rc = lib.feq_eqlinear_bwd_x(_lvals_i32(_slice_lvals(slices)), nreps, gyd.shape[1], cin,
+                                            cout, N.ptr(gyd), N.ptr(wc), N.ptr(gfd), N.ptr(ws), ws.numel(),
+                                            N.stream_ptr(gyd.device))
+            N.check(rc, "feq_eqlinear_bwd_x")
+        fused_w = (gw is not None or gb is not None) and eqlinear_kernels_ok(gyd, weight, slices, cin, cout)
+        if fused_w:
+            lib = N.lib()
+            nreps = len(slices)
+            lv = _lvals_i32(_slice_lvals(slices))
+            rows = gyd.shape[1]
+            gwk = gw if gw is not None else torch.empty_like(w)
+            ws = N.workspace(lib.feq_eqlinear_bwd_w_workspace(lv, nreps, rows, cin, cout), gyd.device)
+            with torch.cuda.device(gyd.device):
+                rc = lib.feq_eqlinear_bwd_w(lv, nreps, rows, cin, cout, N.ptr(gyd), N.ptr(fd),
+                                            gb.shape[1] if gb is not None else 0,
+                                            _lvals_i32(bias_cols) if gb is not None else None, N.ptr(gwk),
+                                            N.ptr(gb) if gb is not None else None, N.ptr(ws), ws.numel(),
+                                            N.stream_ptr(gyd.device))
+            N.check(rc, "feq_eqlinear_bwd_w")
         for k, (a, b) in enumerate(slices):
             gk = gyd[a:b].view(-1, cout)
-            if gfd is not None:
+            if gfd is not None and not fused_x:
                 torch.mm(gk, w[k], out=gfd[a:b].view(-1, cin))
-            if gw is not None:
+            if gw is not None and not fused_w:
                 gw[k] = rows_weight_grad(gk, fd[a:b].view(-1, cin), weight.dtype)
-            if gb is not None and bias_cols[k] >= 0:
+            if gb is not None and bias_cols[k] >= 0 and not fused_w:
                 gb[:, bias_cols[k]] = column_sums(gk)
         gx = None
         if gfd is not None:

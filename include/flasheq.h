@@ -41,6 +41,9 @@
  *   feq_eqnorm_fwd/bwd       EquivariantLayerNorm.forward (norm.py:148-174, RepNorm :51-73)
  *   feq_gate_*               EquivariantGating.forward (flash_eq/layers/gating.py:54-76)
  *                            around its nn.Linear, which stays a library GEMM
+ *   feq_eqlinear_fwd/bwd_x/bwd_w
+ *                            EquivariantLinear.forward and its autograd gradients
+ *                            (flash_eq/layers/linear.py:242-268)
  *   feq_transpose, feq_column_sums, feq_dot_f64
  *                            PyTorch work inside the reference's modules: layout
  *                            changes around EquivariantLinear (linear.py:242-268),
@@ -583,6 +586,41 @@ int feq_gate_bwd_x(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t nu
  * (attention.py:64-70) and LayerScale's gamma (transformer.py:35-39), are dot
  * products.  Here each is one deterministic pass, free of memsets (safe in HIP
  * graphs). */
+
+/* EquivariantLinear (linear.py:242-268) on component-major tables: for each
+ * component d of the representation (irrep k(d) of lvals[0..nreps)),
+ *   y[d] = x[d] W_k^T (+ bias[:, bias_cols[k]] when irrep k is scalar and
+ *   bias_cols[k] >= 0),
+ * x (dim, rows, cin), y (dim, rows, cout), weight (nreps cout, cin) as the
+ * module's parameter, bias (cout, nbias) or NULL.  feq_eqlinear_bwd_x is the
+ * input gradient grad_x[d] = grad_y[d] W_k.  One launch for every component
+ * (plus one that splits the weight): the products on the fp16 matrix cores
+ * with split operands (hi + lo of power-of-two-scaled values, three products),
+ * float32 accumulation: a float32 GEMM's accuracy.  Channel counts:
+ * feq_eqlinear_supported(cin, cout) (32, 64 or 128 each); x and workspace 16-byte aligned; workspace
+ * feq_eqlinear_workspace(nreps, cin, cout) bytes. */
+int feq_eqlinear_supported(int32_t cin, int32_t cout);
+size_t feq_eqlinear_workspace(int32_t nreps, int32_t cin, int32_t cout);
+int feq_eqlinear_fwd(const int32_t* lvals, int32_t nreps, int64_t rows, int32_t cin, int32_t cout,
+                     const float* x, const float* weight, const float* bias, int32_t nbias,
+                     const int32_t* bias_cols, float* y, void* workspace, size_t ws_bytes,
+                     feq_stream_t stream);
+int feq_eqlinear_bwd_x(const int32_t* lvals, int32_t nreps, int64_t rows, int32_t cin, int32_t cout,
+                       const float* grad_y, const float* weight, float* grad_x, void* workspace,
+                       size_t ws_bytes, feq_stream_t stream);
+/* The parameter gradients: grad_w[k] = sum over the rows of irrep k's components
+ * of grad_y^T x ((nreps cout, cin), as weight), and, with grad_b (cout, nbias),
+ * grad_b[:, bias_cols[k]] = sum of grad_y over those rows for each scalar irrep
+ * k with bias_cols[k] >= 0.  Per-workgroup partials over 64-row chunks (split
+ * fp16 products, per-column scales), summed in a fixed order: the same bits on
+ * every run.  grad_y and x as above (component-major, 16-byte aligned);
+ * workspace feq_eqlinear_bwd_w_workspace bytes (it depends on rows). */
+size_t feq_eqlinear_bwd_w_workspace(const int32_t* lvals, int32_t nreps, int64_t rows, int32_t cin,
+                                    int32_t cout);
+int feq_eqlinear_bwd_w(const int32_t* lvals, int32_t nreps, int64_t rows, int32_t cin, int32_t cout,
+                       const float* grad_y, const float* x, int32_t nbias, const int32_t* bias_cols,
+                       float* grad_w, float* grad_b, void* workspace, size_t ws_bytes,
+                       feq_stream_t stream);
 
 /* out[b][j][i] = in[b][i][j] for in (batch, rows, cols) of elem_bytes-wide
  * elements (2, 4 or 8); out must not overlap in. */

@@ -127,3 +127,36 @@ def test_support_queries_and_basis_gradient_argument_errors():
                                  fake, fake, fake, fake, fake, fake, fake, fake, fake, None, fake, fake, 0,
                                  fake, 1 << 30, None)
     assert rc != 0 and "bases' gradients" in lib.feq_last_error().decode()
+
+
+def test_eqlinear_queries_and_argument_errors():
+    """The equivariant-linear entry points' size queries and argument checks
+    (host side: every check runs before a launch, so no pointer here is
+    dereferenced)."""
+    lib = N.load_library()
+    assert lib.feq_eqlinear_supported(64, 128) == 1
+    assert lib.feq_eqlinear_supported(32, 64) == 1
+    assert lib.feq_eqlinear_supported(128, 64) == 1
+    assert lib.feq_eqlinear_supported(8, 16) == 0
+    assert lib.feq_eqlinear_supported(64, 96) == 0
+    assert lib.feq_eqlinear_workspace(3, 64, 128) >= 3 * 2 * 8 * 64 * 32
+    assert lib.feq_eqlinear_workspace(0, 64, 128) == 0
+    lv = (ctypes.c_int32 * 3)(0, 1, 2)
+    rc = lib.feq_eqlinear_fwd(lv, 3, 10, 64, 128, None, None, None, 0, None, None, None, 0, None)
+    assert rc != 0 and "NULL pointer" in lib.feq_last_error().decode()
+    rc = lib.feq_eqlinear_fwd(lv, 3, 10, 64, 96, None, None, None, 0, None, None, None, 0, None)
+    assert rc != 0 and "no kernel" in lib.feq_last_error().decode()
+    bad = (ctypes.c_int32 * 3)(0, -1, 2)
+    rc = lib.feq_eqlinear_bwd_x(bad, 3, 10, 64, 128, None, None, None, None, 0, None)
+    assert rc != 0 and "invalid lvals" in lib.feq_last_error().decode()
+    # no rows: nothing to do
+    assert lib.feq_eqlinear_bwd_x(lv, 3, 0, 64, 128, None, None, None, None, 0, None) == 0
+    # the weight gradient's workspace grows with the rows (per-workgroup partials)
+    w0 = lib.feq_eqlinear_bwd_w_workspace(lv, 3, 0, 64, 128)
+    w1 = lib.feq_eqlinear_bwd_w_workspace(lv, 3, 100000, 64, 128)
+    assert 0 < w0 < w1
+    rc = lib.feq_eqlinear_bwd_w(lv, 3, 10, 64, 128, None, None, 0, None, None, None, None, 0, None)
+    assert rc != 0 and "NULL grad_w" in lib.feq_last_error().decode()
+    rc = lib.feq_eqlinear_bwd_w(lv, 3, 10, 64, 128, None, None, 1, None, None, ctypes.c_void_p(256), None, 0,
+                                None)
+    assert rc != 0 and "bias columns" in lib.feq_last_error().decode()
