@@ -120,12 +120,16 @@ constexpr int eql_wpb() {
     return NS * NC * 8 + NS * 24 <= 200 ? 1 : NS * (NC / 2) * 8 + NS * 24 <= 200 ? 2 : 4;
 }
 
+// Blocks in flight per wave.
+template <int K, int NOUT>
+constexpr int eql_depth() { return 2; }
+
 // out[d] = in[d] B_k(d) (+ bias) for in (D, rows, K), out (D, rows, NOUT).
 // Workgroups of four waves; WPB waves share a 16-row block (each with NCB of
 // its column blocks), so a workgroup works on 4 / WPB blocks at a time.  Each
 // wave takes a contiguous run of blocks (so its irrep, and with it the B
-// fragments in its registers, rarely changes) and keeps the rows of the next
-// two blocks in flight.  The finished block goes through LDS, so that it
+// fragments in its registers, rarely changes) and keeps the rows of its next
+// PD blocks in flight.  The finished block goes through LDS, so that it
 // leaves as 16-byte row segments (a few wide stores rather than one 4-byte
 // store per accumulator: vector-memory waits count stores too); each wave
 // stages and stores only its own columns, so no barrier spans waves.
@@ -138,6 +142,7 @@ k_eql_mm(const float* __restrict__ in, int64_t rows, int D, EqlMap map, const h8
     constexpr int NCB = NOUT / 16 / WPB;                 // column blocks per wave
     constexpr int NS = K / 32;                           // 32-steps
     constexpr int SLOTS = 4 / WPB;                       // row blocks per workgroup at a time
+    constexpr int PD = eql_depth<K, NOUT>();             // blocks in flight per wave
     constexpr int OS = NOUT + 4;                         // LDS row stride of the output stage (floats)
     static_assert(K % 32 == 0 && NOUT % 16 == 0 && NCB * WPB * 16 == NOUT, "unsupported sizes");
     __shared__ __align__(16) float sOut[SLOTS][16 * OS];
@@ -251,16 +256,18 @@ k_eql_mm(const float* __restrict__ in, int64_t rows, int D, EqlMap map, const h8
         __builtin_amdgcn_wave_barrier();
     };
 
-    // two blocks in flight: buffers a0 / a1 alternate with static indices
-    float a0[NS][8], a1[NS][8];
-    if (bbeg < bend) load(bbeg, a0);
-    if (bbeg + 1 < bend) load(bbeg + 1, a1);
-    for (uint32_t blk = bbeg; blk < bend; blk += 2) {
-        block(blk, a0);
-        if (blk + 2 < bend) load(blk + 2, a0);
-        if (blk + 1 < bend) {
-            block(blk + 1, a1);
-            if (blk + 3 < bend) load(blk + 3, a1);
+    // PD blocks in flight: the buffers rotate with static indices (unrolled)
+    float a[PD][NS][8];
+#pragma unroll
+    for (int p = 0; p < PD; ++p)
+        if (bbeg + p < bend) load(bbeg + p, a[p]);
+    for (uint32_t blk = bbeg; blk < bend; blk += PD) {
+#pragma unroll
+        for (int p = 0; p < PD; ++p) {
+            if (blk + p < bend) {
+                block(blk + p, a[p]);
+                if (blk + p + PD < bend) load(blk + p + PD, a[p]);
+            }
         }
     }
 }
