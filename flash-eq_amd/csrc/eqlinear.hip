@@ -22,7 +22,7 @@
 // reads row l % 16 of the block, columns 8 (l / 16) .. + 7 of each 32-step
 // (two 16-byte loads), which is the A layout of v_mfma_f32_16x16x32_f16; each
 // row gets its own scale from its largest magnitude (four lanes hold a row),
-// undone on the accumulators with the B scale of the irrep.  The next two
+// undone on the accumulators with the column's B scale.  The next two
 // blocks' rows are in flight during a block's products.
 #include "feq_internal.h"
 
@@ -69,42 +69,47 @@ __device__ __forceinline__ void eql_split(float a, float sc, _Float16& hi, _Floa
 
 // B fragments of every irrep: for irrep k, 32-step s and column block c, lane
 // l holds column 16 c + l % 16, rows 32 s + 8 (l / 16) + j (j = 0..7) of B_k
-// as fp16 hi and lo (two h8 per lane, hi first).  One workgroup per irrep:
-// the largest magnitude of B_k first (its scale), then the fragments.
+// as fp16 hi and lo (two h8 per lane, hi first), each column scaled by its own
+// power of two (binv[k NOUT + n] = 1 / scale).  One wave per (irrep, column
+// block): its four lane groups hold a column's rows, so the column maximum is
+// two lane exchanges.
 // trans = 0: B_k[kk][n] = W[(k NOUT + n) K + kk] (W_k^T of W (nreps NOUT, K));
 // trans = 1: B_k[kk][n] = W[(k K + kk) NOUT + n] (W_k of W (nreps K, NOUT)).
-__global__ void __launch_bounds__(256)
-k_eql_prep(const float* __restrict__ W, int K, int NOUT, int trans, h8* __restrict__ frag,
-           float* __restrict__ binv) {
-    __shared__ float red[256];
-    const int k = blockIdx.x;
+template <int K, int NOUT>
+__global__ void __launch_bounds__(64)
+k_eql_prep(const float* __restrict__ W, int trans, h8* __restrict__ frag, float* __restrict__ binv) {
+    constexpr int NS = K / 32, NC = NOUT / 16;
+    const int k = blockIdx.x / NC, c = blockIdx.x % NC;
+    const int lane = threadIdx.x, lr = lane & 15, lg = lane >> 4;
+    const int n = 16 * c + lr;
     const float* Wk = W + static_cast<int64_t>(k) * K * NOUT;
+    float b[NS][8];
     float m = 0.0f;
-    for (int i = threadIdx.x; i < K * NOUT; i += 256) m = fmaxf(m, fabsf(Wk[i]));
-    red[threadIdx.x] = m;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if (static_cast<int>(threadIdx.x) < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
-        __syncthreads();
-    }
-    const int e = eql_scale_exp(red[0]);
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int kk = 32 * s + 8 * lg + j;
+            b[s][j] = trans ? Wk[kk * NOUT + n] : Wk[n * K + kk];
+            m = fmaxf(m, fabsf(b[s][j]));
+        }
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    const int e = eql_scale_exp(m);
     const float sc = eql_exp2i(e);
-    if (threadIdx.x == 0) binv[k] = eql_exp2i(-e);
-    const int NS = K / 32, NC = NOUT / 16;
+    if (lg == 0) binv[k * NOUT + n] = eql_exp2i(-e);
     h8* fk = frag + static_cast<int64_t>(k) * NS * NC * 64 * 2;
-    for (int q = threadIdx.x; q < NS * NC * 64; q += 256) {
-        const int lane = q & 63, c = (q >> 6) % NC, s = (q >> 6) / NC;
-        const int n = 16 * c + (lane & 15);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
         h8 hi, lo;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const int kk = 32 * s + 8 * (lane >> 4) + j;
-            const float b = trans ? Wk[kk * NOUT + n] : Wk[n * K + kk];
             _Float16 h, l;
-            eql_split(b, sc, h, l);
+            eql_split(b[s][j], sc, h, l);
             hi[j] = h;
             lo[j] = l;
         }
+        const int q = (s * NC + c) * 64 + lane;
         fk[2 * q] = hi;
         fk[2 * q + 1] = lo;
     }
@@ -159,8 +164,8 @@ k_eql_mm(const float* __restrict__ in, int64_t rows, int D, EqlMap map, const h8
     const uint32_t bend = bbeg + per + (sid < extra ? 1 : 0);
 
     h8 bh[NS][NCB], bl[NS][NCB];
+    float cinv[NCB];   // 1 / scale of this lane's column in each of the wave's column blocks
     int kcur = -1;
-    float bsc = 0.0f;
 
     auto load = [&](uint32_t blk, float (&a)[NS][8]) {
         const uint32_t d = blk / nb;
@@ -196,7 +201,8 @@ k_eql_mm(const float* __restrict__ in, int64_t rows, int D, EqlMap map, const h8
                     bh[s][c] = fk[2 * q];
                     bl[s][c] = fk[2 * q + 1];
                 }
-            bsc = binv[k];
+#pragma unroll
+            for (int c = 0; c < NCB; ++c) cinv[c] = binv[k * NOUT + 16 * (cg * NCB + c) + lr];
             kcur = k;
         }
         // this row's scale: its largest magnitude over the four lanes holding it
@@ -209,7 +215,7 @@ k_eql_mm(const float* __restrict__ in, int64_t rows, int D, EqlMap map, const h8
         m = fmaxf(m, __shfl_xor(m, 32, 64));
         const int e = eql_scale_exp(m);
         const float sc = eql_exp2i(e);
-        const float rinv = eql_exp2i(-e) * bsc;
+        const float rinv = eql_exp2i(-e);
         h8 ah[NS], al[NS];
 #pragma unroll
         for (int s = 0; s < NS; ++s)
@@ -238,7 +244,7 @@ k_eql_mm(const float* __restrict__ in, int64_t rows, int D, EqlMap map, const h8
             const int n = 16 * (cg * NCB + c) + lr;
             const float bv = bc >= 0 ? bias[static_cast<int64_t>(n) * nbias + bc] : 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) so[(4 * lg + i) * OS + n] = acc[i] * ri[i] + bv;
+            for (int i = 0; i < 4; ++i) so[(4 * lg + i) * OS + n] = acc[i] * (ri[i] * cinv[c]) + bv;
         }
         // the wave's own columns of the 16 rows leave as 16-byte segments (each
         // wave reads back only what it staged: no barrier between waves)
@@ -603,7 +609,7 @@ int eql_run(const int32_t* lvals, int32_t nreps, int64_t rows, int K, int NOUT, 
         for (int k = 0; k < nreps; ++k)
             if (bias_cols[k] >= nbias) return fail(FEQ_ERR_INVALID, "bias column out of range");
     const size_t fb = eql_frag_bytes(nreps, K, NOUT);
-    const size_t need = fb + 256 + sizeof(float) * kEqlMaxReps;
+    const size_t need = fb + 256 + sizeof(float) * kEqlMaxReps * NOUT;
     return with_sizes(K, NOUT, [&](auto KK, auto NN) -> int {
         constexpr int Kc = decltype(KK)::value, Nc = decltype(NN)::value;
         if (rows == 0) return FEQ_OK;
@@ -613,7 +619,8 @@ int eql_run(const int32_t* lvals, int32_t nreps, int64_t rows, int K, int NOUT, 
         if (ws_bytes < need) return fail(FEQ_ERR_WORKSPACE, "equivariant linear workspace too small");
         h8* frag = static_cast<h8*>(ws);
         float* binv = reinterpret_cast<float*>(static_cast<char*>(ws) + ((fb + 255) / 256) * 256);
-        FEQ_LAUNCH("k_eql_prep", k_eql_prep, dim3(nreps), dim3(256), 0, s, W, Kc, Nc, trans, frag, binv);
+        FEQ_LAUNCH("k_eql_prep", (k_eql_prep<Kc, Nc>), dim3(nreps * (Nc / 16)), dim3(64), 0, s, W, trans, frag,
+                   binv);
         constexpr int SLOTS = 4 / eql_wpb<Kc, Nc>();
         const int64_t blocks = (rows + 15) / 16 * D;
         if (blocks > 0x7fffffffLL) return fail(FEQ_ERR_UNSUPPORTED, "equivariant linear: too many rows");
@@ -716,7 +723,8 @@ extern "C" int feq_eqlinear_bwd_w(const int32_t* lvals, int32_t nreps, int64_t r
 extern "C" size_t feq_eqlinear_workspace(int32_t nreps, int32_t cin, int32_t cout) {
     if (nreps < 1 || cin < 32 || cout < 32) return 0;
     const size_t f = eql_frag_bytes(nreps, cin, cout), b = eql_frag_bytes(nreps, cout, cin);
-    return (f > b ? f : b) + 256 + sizeof(float) * kEqlMaxReps;
+    const size_t n = static_cast<size_t>(cin > cout ? cin : cout);
+    return (f > b ? f : b) + 256 + sizeof(float) * kEqlMaxReps * n;
 }
 
 extern "C" int feq_eqlinear_supported(int32_t cin, int32_t cout) {
