@@ -347,12 +347,15 @@ __device__ inline double wave_sum_d(double v) {
 
 __global__ void __launch_bounds__(256)
 k_dot_f64(const float* __restrict__ a, const float* __restrict__ b, int64_t n,
-          double* __restrict__ part) {
+          double* __restrict__ part, const float* __restrict__ scale, float* __restrict__ sa) {
+    // sa (may be NULL): sa[i] = scale[0] a[i], written in the same pass
     __shared__ double s[4];
     double acc = 0.0;
+    const float sc = sa ? scale[0] : 0.0f;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15u) == 0) {
+    if (((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+          reinterpret_cast<uintptr_t>(sa)) & 15u) == 0) {
         const float4* a4 = reinterpret_cast<const float4*>(a);
         const float4* b4 = reinterpret_cast<const float4*>(b);
         const int64_t n4 = n / 4;
@@ -360,15 +363,54 @@ k_dot_f64(const float* __restrict__ a, const float* __restrict__ b, int64_t n,
             const float4 x = a4[i], y = b4[i];
             acc += (static_cast<double>(x.x) * y.x + static_cast<double>(x.y) * y.y) +
                    (static_cast<double>(x.z) * y.z + static_cast<double>(x.w) * y.w);
+            if (sa) reinterpret_cast<float4*>(sa)[i] = make_float4(sc * x.x, sc * x.y, sc * x.z, sc * x.w);
         }
-        for (int64_t i = 4 * n4 + t0; i < n; i += stride) acc += static_cast<double>(a[i]) * b[i];
+        for (int64_t i = 4 * n4 + t0; i < n; i += stride) {
+            acc += static_cast<double>(a[i]) * b[i];
+            if (sa) sa[i] = sc * a[i];
+        }
     } else {
-        for (int64_t i = t0; i < n; i += stride) acc += static_cast<double>(a[i]) * b[i];
+        for (int64_t i = t0; i < n; i += stride) {
+            acc += static_cast<double>(a[i]) * b[i];
+            if (sa) sa[i] = sc * a[i];
+        }
     }
     acc = wave_sum_d(acc);
     if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = acc;
     __syncthreads();
     if (threadIdx.x == 0) part[blockIdx.x] = (s[0] + s[1]) + (s[2] + s[3]);
+}
+
+// out = x + scale[0] y (a residual connection with a scalar layer scale);
+// x NULL: out = scale[0] y.
+template <bool X>
+__global__ void __launch_bounds__(256)
+k_scale_add(const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ scale,
+            int64_t n, float* __restrict__ out) {
+    const float sc = scale[0];
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
+          reinterpret_cast<uintptr_t>(out)) & 15u) == 0) {
+        const int64_t n4 = n / 4;
+        for (int64_t i = t0; i < n4; i += stride) {
+            const float4 b = reinterpret_cast<const float4*>(y)[i];
+            float4 r = make_float4(sc * b.x, sc * b.y, sc * b.z, sc * b.w);
+            if constexpr (X) {
+                const float4 a = reinterpret_cast<const float4*>(x)[i];
+                r = make_float4(a.x + r.x, a.y + r.y, a.z + r.z, a.w + r.w);
+            }
+            reinterpret_cast<float4*>(out)[i] = r;
+        }
+        for (int64_t i = 4 * n4 + t0; i < n; i += stride) out[i] = (X ? x[i] : 0.0f) + sc * y[i];
+    } else {
+        for (int64_t i = t0; i < n; i += stride) out[i] = (X ? x[i] : 0.0f) + sc * y[i];
+    }
+}
+
+unsigned stream_grid(int64_t n) {
+    const int64_t g = (n / 4 + 255) / 256;
+    return static_cast<unsigned>(g < 4096 ? (g < 1 ? 1 : g) : 4096);
 }
 
 // out[0] = (float) sum of part[0..groups) by one workgroup in a fixed order.
@@ -436,7 +478,38 @@ extern "C" int feq_dot_f64(const float* a, const float* b, int64_t n, float* out
         return fail(FEQ_ERR_WORKSPACE, "dot workspace too small");
     hipStream_t s = stream_of(stream);
     double* part = static_cast<double*>(ws);
-    FEQ_LAUNCH("k_dot_f64", k_dot_f64, dim3(kDotGroups), dim3(256), 0, s, a, b, n, part);
+    FEQ_LAUNCH("k_dot_f64", k_dot_f64, dim3(kDotGroups), dim3(256), 0, s, a, b, n, part,
+               static_cast<const float*>(nullptr), static_cast<float*>(nullptr));
     FEQ_LAUNCH("k_dot_finish", k_dot_finish, dim3(1), dim3(256), 0, s, part, kDotGroups, out);
+    return FEQ_OK;
+}
+
+extern "C" int feq_scale_add(const float* x, const float* y, const float* scale, int64_t n, float* out,
+                             feq_stream_t stream) {
+    if (n < 0) return fail(FEQ_ERR_INVALID, "negative length");
+    if (n == 0) return FEQ_OK;
+    if (!x || !y || !scale || !out) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    FEQ_LAUNCH("k_scale_add", k_scale_add<true>, dim3(stream_grid(n)), dim3(256), 0, stream_of(stream), x, y,
+               scale, n, out);
+    return FEQ_OK;
+}
+
+extern "C" int feq_scale_add_bwd(const float* grad_out, const float* y, const float* scale, int64_t n,
+                                 float* grad_y, float* grad_scale, void* ws, size_t ws_bytes,
+                                 feq_stream_t stream) {
+    if (n < 0) return fail(FEQ_ERR_INVALID, "negative length");
+    if (!grad_scale && !grad_y) return FEQ_OK;
+    if (!scale || (n > 0 && (!grad_out || !y))) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    hipStream_t s = stream_of(stream);
+    if (!grad_scale) {   // grad_y alone: the scaled copy
+        if (n == 0) return FEQ_OK;
+        FEQ_LAUNCH("k_scale_add", k_scale_add<false>, dim3(stream_grid(n)), dim3(256), 0, s,
+                   static_cast<const float*>(nullptr), grad_out, scale, n, grad_y);
+        return FEQ_OK;
+    }
+    if (!ws || ws_bytes < feq_dot_f64_workspace()) return fail(FEQ_ERR_WORKSPACE, "dot workspace too small");
+    double* part = static_cast<double*>(ws);
+    FEQ_LAUNCH("k_dot_f64", k_dot_f64, dim3(kDotGroups), dim3(256), 0, s, grad_out, y, n, part, scale, grad_y);
+    FEQ_LAUNCH("k_dot_finish", k_dot_finish, dim3(1), dim3(256), 0, s, part, kDotGroups, grad_scale);
     return FEQ_OK;
 }

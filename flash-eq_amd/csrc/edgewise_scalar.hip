@@ -167,6 +167,41 @@ struct Group0 {
         }
     }
 
+    // The group's positions j0 .. j0 + NB - 1 of a tile whose per-position
+    // values sit one per lane (lane j: position j; positions past np repeat the
+    // last): edge, row (-1: none), bin, weight, s, Q[0, 0] come by readlane, and
+    // only the rows x[row] and P[e] are loaded here.
+    __device__ __forceinline__ void load_known(int j0, int np, int el, int rl, int lol, float tl, float shl,
+                                               float ql, const float* __restrict__ x,
+                                               const float* __restrict__ P, int64_t (&e)[NB], int lane) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const int j = j0 + i < np ? j0 + i : np - 1;
+            e[i] = __builtin_amdgcn_readlane(el, j);
+            const int rw = __builtin_amdgcn_readlane(rl, j);
+            row[i] = j0 + i < np ? rw : -1;
+            lo[i] = __builtin_amdgcn_readlane(lol, j);
+            t[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tl), j));
+            sh[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(shl), j));
+            q[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ql), j));
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const float* xs = x + ((row[i] >= 0 ? row[i] : 0) * kCin + lane) * DIN;
+            const uint32_t mk = row[i] >= 0 ? ~0u : 0u;
+#pragma unroll
+            for (int d = 0; d < DIN; ++d) xr[i][d] = __uint_as_float(__float_as_uint(xs[d]) & mk);
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const float* pe = P + e[i] * DIN * DIN;
+#pragma unroll
+            for (int d = 0; d < DIN; ++d)
+#pragma unroll
+                for (int l = 0; l < NL; ++l) pc[i][d][l] = pe[d * DIN + l];
+        }
+    }
+
     // fs0[l] = sum_d x[d] P[d, l]; fe[k][l] = F_e[k, l] s^l from the LDS table
     template <int K>
     __device__ __forceinline__ void edge(int i, const float* sF, float (&fs0)[NL], float (&fe)[K][NL],
@@ -295,23 +330,37 @@ k_ew0_bwd(feq_binning B, int64_t E, int64_t ntiles, const float* __restrict__ gy
         for (int d = 0; d < DIN; ++d) run[d] = 0.0f;
         int js = 0;
         int64_t nnext = -2;   // source of the position after the current group
+        // the tile's per-position values, lane j for position j, in one round of
+        // dependent loads (CSR position -> edge -> source row, distance, Q, gy)
+        const int jl = lane < np ? lane : np - 1;
+        const int64_t el = nodes ? static_cast<int64_t>(NS.perm[p0 + jl]) : p0 + jl;
+        int64_t rl = el;
+        if (src) {
+            rl = src[el];
+            rl = rl >= 0 && rl < nsrc ? rl : -1;
+        }
+        const float dl = dist[el], ql = Q[el];
+        const EdgeBin ebl = edge_bin(dl, B);
+        const float shl = dl / (dl + B.sh_scale);
+        float gql[COUT];   // Q[0, 0] gy of position lane
+#pragma unroll
+        for (int co = 0; co < COUT; ++co) gql[co] = gy[el * COUT + co] * ql;
         for (int j0 = 0; j0 < np; j0 += kGroupB) {
             G g;
             int64_t e[kGroupB];
-            g.load(p0 + j0, p0 + np, x, src, nsrc, nodes ? NS.perm : nullptr, P, Q, dist, e, lane, B);
+            g.load_known(j0, np, static_cast<int>(el), static_cast<int>(rl), ebl.lo, ebl.t, shl, ql, x, P, e,
+                         lane);
             float gq[kGroupB][COUT];
 #pragma unroll
-            for (int i = 0; i < kGroupB; ++i)
+            for (int i = 0; i < kGroupB; ++i) {
+                const int j = j0 + i < np ? j0 + i : np - 1;
 #pragma unroll
-                for (int co = 0; co < COUT; ++co) gq[i][co] = gy[e[i] * COUT + co] * g.q[i];
+                for (int co = 0; co < COUT; ++co)
+                    gq[i][co] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gql[co]), j));
+            }
             if (nodes) {
                 const int jn = j0 + kGroupB;
-                nnext = -2;
-                if (jn < np) {
-                    const int64_t en = NS.perm[p0 + jn];
-                    const int64_t rn = src[en];
-                    nnext = rn >= 0 && rn < nsrc ? rn : -1;
-                }
+                nnext = jn < np ? __builtin_amdgcn_readlane(static_cast<int>(rl), jn) : -2;
             }
 #pragma unroll
             for (int i = 0; i < kGroupB; ++i) {

@@ -151,6 +151,8 @@ _SIGS = {
     "feq_transpose": ([_P, _I64, _I64, _I64, _I32, _P, _P], ctypes.c_int),
     "feq_column_sums_workspace": ([_I64, _I64, _I32], _SZ),
     "feq_column_sums": ([_P, _I64, _I64, _I32, _P, _P, _SZ, _P], ctypes.c_int),
+    "feq_scale_add": ([_P, _P, _P, _I64, _P, _P], ctypes.c_int),
+    "feq_scale_add_bwd": ([_P, _P, _P, _I64, _P, _P, _P, _SZ, _P], ctypes.c_int),
     "feq_dot_f64_workspace": ([], _SZ),
     "feq_dot_f64": ([_P, _P, _I64, _P, _P, _SZ, _P], ctypes.c_int),
     "feq_attn_softmax_fwd": ([_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I32, _I32, _P, _F,

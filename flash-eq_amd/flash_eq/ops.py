@@ -1110,6 +1110,45 @@ class ScaleFn(torch.autograd.Function):
         return gx, gg
 
 
+class ResidualScaleFn(torch.autograd.Function):
+    """x + gamma * y for a scalar parameter gamma: the transformer block's
+    residual connection with LayerScale (transformer.py:245, :252 and
+    LayerScale :23-38 of the reference) in one pass (feq_scale_add).  The
+    backward forms grad_y = gamma g and grad_gamma = sum g y (float64 products
+    and sum, fixed order) in one pass (feq_scale_add_bwd); grad_x is g itself."""
+
+    @staticmethod
+    def forward(ctx, x, y, gamma):
+        xs, ys = x.contiguous(), y.contiguous()
+        if xs.shape != ys.shape:
+            raise RuntimeError(f"residual: shapes {tuple(xs.shape)} and {tuple(ys.shape)}")
+        out = torch.empty_like(xs)
+        with torch.cuda.device(xs.device):
+            rc = N.lib().feq_scale_add(N.ptr(xs), N.ptr(ys), N.ptr(gamma), xs.numel(), N.ptr(out),
+                                       N.stream_ptr(xs.device))
+        N.check(rc, "feq_scale_add")
+        ctx.save_for_backward(ys, gamma)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        ys, gamma = ctx.saved_tensors
+        g = g.contiguous()
+        gy = torch.empty_like(g) if ctx.needs_input_grad[1] else None
+        gg = torch.empty((), dtype=torch.float32, device=g.device) if ctx.needs_input_grad[2] else None
+        if gy is not None or gg is not None:
+            lib = N.lib()
+            ws = N.workspace(lib.feq_dot_f64_workspace(), g.device)
+            with torch.cuda.device(g.device):
+                rc = lib.feq_scale_add_bwd(N.ptr(g), N.ptr(ys), N.ptr(gamma), g.numel(),
+                                           N.ptr(gy) if gy is not None else None,
+                                           N.ptr(gg) if gg is not None else None, N.ptr(ws), ws.numel(),
+                                           N.stream_ptr(g.device))
+            N.check(rc, "feq_scale_add_bwd")
+        return (g if ctx.needs_input_grad[0] else None, gy,
+                gg.reshape(gamma.shape) if gg is not None else None)
+
+
 def rows_weight_grad(gy: torch.Tensor, x: torch.Tensor, dtype: torch.dtype,
                      chunks: int = 64) -> torch.Tensor:
     """gy^T x over many rows, as a batched GEMM over row chunks whose partial

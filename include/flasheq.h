@@ -44,6 +44,8 @@
  *   feq_eqlinear_fwd/bwd_x/bwd_w
  *                            EquivariantLinear.forward and its autograd gradients
  *                            (flash_eq/layers/linear.py:242-268)
+ *   feq_scale_add(_bwd)     the block's residual connections with LayerScale
+ *                            (flash_eq/layers/transformer.py:23-38, 245, 252)
  *   feq_transpose, feq_column_sums, feq_dot_f64
  *                            PyTorch work inside the reference's modules: layout
  *                            changes around EquivariantLinear (linear.py:242-268),
@@ -632,6 +634,17 @@ int feq_transpose(const void* in, int64_t batch, int64_t rows, int64_t cols,
 size_t feq_column_sums_workspace(int64_t rows, int64_t cols, int32_t elem_bytes);
 int feq_column_sums(const void* in, int64_t rows, int64_t cols, int32_t elem_bytes, void* out,
                     void* workspace, size_t ws_bytes, feq_stream_t stream);
+/* The residual connection with LayerScale, x + gamma * y (transformer.py:245 and
+ * :252 of the reference, LayerScale :23-38), in one pass: out = x + scale[0] y
+ * (n floats, scale a device scalar).  Its backward for grad_out g in one pass:
+ * grad_y = scale[0] g (may be NULL) and grad_scale[0] = sum of g * y, products
+ * and sum in float64 in a fixed order (may be NULL; workspace
+ * feq_dot_f64_workspace() bytes when set).  The gradient for x is g itself. */
+int feq_scale_add(const float* x, const float* y, const float* scale, int64_t n, float* out,
+                  feq_stream_t stream);
+int feq_scale_add_bwd(const float* grad_out, const float* y, const float* scale, int64_t n,
+                      float* grad_y, float* grad_scale, void* workspace, size_t ws_bytes,
+                      feq_stream_t stream);
 /* out[0] = (float) sum of (double) a[i] * b[i], the products and their sum in
  * float64 in a fixed order (many products that largely cancel). */
 size_t feq_dot_f64_workspace(void);
