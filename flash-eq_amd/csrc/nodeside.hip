@@ -120,6 +120,34 @@ struct RowPrefetch {
             }
         }
     }
+    // The same with gy component-major (dim, N, mult): element i of a lane is
+    // component d = idx / mult, channel c = idx % mult (contiguous channel runs
+    // per component in memory), staged at the node-major position c dim + d.
+    __device__ __forceinline__ void load_cm(const float* __restrict__ xs, const float* __restrict__ gs,
+                                            int64_t n, int64_t N, int64_t row, int mult, int lane) {
+        if (n >= N) return;
+#pragma unroll
+        for (int i = 0; i < kRowPer; ++i) {
+            const int64_t idx = lane + 64 * i;
+            if (idx < row) {
+                const int d = static_cast<int>(idx) / mult, c = static_cast<int>(idx) - d * mult;
+                x[i] = xs[n * row + idx];
+                g[i] = gs[(d * N + n) * mult + c];
+            }
+        }
+    }
+    __device__ __forceinline__ void store_cm(float* sx, float* sg, int64_t row, int mult, int dim,
+                                             int lane) const {
+#pragma unroll
+        for (int i = 0; i < kRowPer; ++i) {
+            const int64_t idx = lane + 64 * i;
+            if (idx < row) {
+                const int d = static_cast<int>(idx) / mult, c = static_cast<int>(idx) - d * mult;
+                sx[idx] = x[i];
+                sg[c * dim + d] = g[i];
+            }
+        }
+    }
 };
 
 __device__ __forceinline__ float sigmoidf(float v) { return 1.0f / (1.0f + expf(-v)); }
@@ -130,11 +158,14 @@ __device__ __forceinline__ float sigmoidf(float v) { return 1.0f / (1.0f + expf(
 // mean over every channel and l > 0 component of the node.
 
 // STAGE: the node row moves through LDS (coalesced), computed in place.
-template <int CPL, bool STAGE>
+// CMO (with STAGE): y is component-major (dim, N, mult), the layout the
+// channel-mixing maps after the norm take, written as contiguous channel runs.
+template <int CPL, bool STAGE, bool CMO = false>
 __global__ void __launch_bounds__(64 * kWaves)
 k_sepnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __restrict__ ws,
               const float* __restrict__ bs, const float* __restrict__ wh, float eps,
               float* __restrict__ y) {
+    static_assert(STAGE || !CMO, "component-major output goes through the LDS stage");
     __shared__ float lds[STAGE ? kWaves * kStageRow : 1];
     const int lane = threadIdx.x & 63;
     const int64_t n = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
@@ -202,7 +233,12 @@ k_sepnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __re
     }
     if (STAGE) {
         wave_sync();
-        row_copy(y + n * row, sx, row, lane);
+        if constexpr (CMO) {
+            for (int d = 0; d < L.dim; ++d)
+                for (int c = lane; c < L.mult; c += 64) y[(d * N + n) * L.mult + c] = sx[c * L.dim + d];
+        } else {
+            row_copy(y + n * row, sx, row, lane);
+        }
     }
 }
 
@@ -212,12 +248,14 @@ k_sepnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __re
 //   gx = gy w_h[c] / rms - S v / (count rms^3).
 // Per-wave partials: pS, pB (mult, ns) of gy (v - mu) / den and gy; pH (mult) of
 // sum_d gy v / rms.
-template <int CPL, bool STAGE>
+// CMG (with STAGE): gy is component-major (dim, N, mult); x and gx node-major.
+template <int CPL, bool STAGE, bool CMG = false>
 __global__ void __launch_bounds__(64 * kWaves)
 k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __restrict__ x,
               const float* __restrict__ ws, const float* __restrict__ wh, float eps,
               float* __restrict__ gx, float* __restrict__ pS, float* __restrict__ pB,
               float* __restrict__ pH) {
+    static_assert(STAGE || !CMG, "component-major gradients go through the LDS stage");
     const int lane = threadIdx.x & 63;
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
     const int64_t nw = static_cast<int64_t>(gridDim.x) * kWaves;
@@ -235,12 +273,20 @@ k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __r
     float* sx = lds + (threadIdx.x >> 6) * 2 * kStageRow;
     float* sg = sx + kStageRow;
     RowPrefetch pf;
-    if (STAGE) pf.load(x, gy, wave, N, row, lane);
+    if (STAGE) {
+        if constexpr (CMG) pf.load_cm(x, gy, wave, N, row, L.mult, lane);
+        else pf.load(x, gy, wave, N, row, lane);
+    }
     for (int64_t n = wave; n < N; n += nw) {
         if (STAGE) {
             wave_sync();  // the previous node's stores have read sg
-            pf.store(sx, sg, row, lane);
-            pf.load(x, gy, n + nw, N, row, lane);   // in flight during this node
+            if constexpr (CMG) {
+                pf.store_cm(sx, sg, row, L.mult, L.dim, lane);
+                pf.load_cm(x, gy, n + nw, N, row, L.mult, lane);   // in flight during this node
+            } else {
+                pf.store(sx, sg, row, lane);
+                pf.load(x, gy, n + nw, N, row, lane);
+            }
             wave_sync();
         }
         const float* xn = STAGE ? sx : x + n * row;
@@ -344,15 +390,85 @@ k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __r
     }
 }
 
+// ---- residual connection with a component-major branch -------------------------
+// out (N, mult, dim) = x (N, mult, dim) + scale[0] y with y component-major
+// (dim, N, mult): the block's MLP output joins the residual stream without a
+// separate transpose.  A wave per node stages y's component runs in LDS, then
+// writes the node row.  Fixed grid (kResGroups workgroups, nodes grid-stride).
+constexpr int kResGroups = 1024;
+
+__global__ void __launch_bounds__(64 * kWaves)
+k_scale_add_cm(int64_t N, int mult, int dim, const float* __restrict__ x, const float* __restrict__ y,
+               const float* __restrict__ scale, float* __restrict__ out) {
+    __shared__ float lds[kWaves * kStageRow];
+    const int lane = threadIdx.x & 63;
+    float* sy = lds + (threadIdx.x >> 6) * kStageRow;
+    const float sc = scale[0];
+    const int64_t row = static_cast<int64_t>(mult) * dim;
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * kWaves;
+    for (int64_t n = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6); n < N; n += nw) {
+        for (int d = 0; d < dim; ++d)
+            for (int c = lane; c < mult; c += 64) sy[c * dim + d] = y[(d * N + n) * mult + c];
+        wave_sync();
+        for (int64_t i = lane; i < row; i += 64) out[n * row + i] = x[n * row + i] + sc * sy[i];
+        wave_sync();   // this node's reads of sy are done before the next node's writes
+    }
+}
+
+// Its backward for grad_out g (node-major): grad_y (component-major) =
+// scale[0] g (NULL: not formed) and per-workgroup float64 partials of sum g y.
+__global__ void __launch_bounds__(64 * kWaves)
+k_scale_add_cm_bwd(int64_t N, int mult, int dim, const float* __restrict__ g, const float* __restrict__ y,
+                   const float* __restrict__ scale, float* __restrict__ gy, double* __restrict__ part) {
+    __shared__ float lds[kWaves * kStageRow];
+    __shared__ double red[kWaves];
+    const int lane = threadIdx.x & 63;
+    float* sg = lds + (threadIdx.x >> 6) * kStageRow;
+    const float sc = scale[0];
+    const int64_t row = static_cast<int64_t>(mult) * dim;
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * kWaves;
+    double acc = 0.0;
+    for (int64_t n = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6); n < N; n += nw) {
+        row_copy(sg, g + n * row, row, lane);
+        wave_sync();
+        for (int d = 0; d < dim; ++d)
+            for (int c = lane; c < mult; c += 64) {
+                const float v = sg[c * dim + d];
+                const int64_t o = (d * N + n) * mult + c;
+                if (gy) gy[o] = sc * v;
+                acc += static_cast<double>(v) * y[o];
+            }
+        wave_sync();
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) part[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// out[0] = (float) sum of part[0 .. n) by one workgroup in a fixed order.
+__global__ void __launch_bounds__(64 * kWaves)
+k_sum_f64(const double* __restrict__ part, int n, float* __restrict__ out) {
+    __shared__ double red[kWaves];
+    double acc = 0.0;
+    for (int i = threadIdx.x; i < n; i += 64 * kWaves) acc += part[i];
+    acc = wave_sum(acc);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) out[0] = static_cast<float>((red[0] + red[1]) + (red[2] + red[3]));
+}
+
 // ---- equivariant layer norm ---------------------------------------------------
 // Per irrep k: norm n_c = sqrt(sum_d x^2 + eps); with weights, a LayerNorm over
 // the channels ln_c = (n_c - mu) rstd w_c + b_c (rstd = 1 / sqrt(var + ln_eps));
 // y = x ln_c / (n_c + eps), or x / (n_c + eps) without weights (one channel).
 
-template <int CPL, bool STAGE>
+// CMO (with STAGE): y component-major (dim, N, mult), as the separable norm's.
+template <int CPL, bool STAGE, bool CMO = false>
 __global__ void __launch_bounds__(64 * kWaves)
 k_eqnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __restrict__ w,
              const float* __restrict__ b, float eps, float ln_eps, float* __restrict__ y) {
+    static_assert(STAGE || !CMO, "component-major output goes through the LDS stage");
     __shared__ float lds[STAGE ? kWaves * kStageRow : 1];
     const int lane = threadIdx.x & 63;
     const int64_t n = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
@@ -402,7 +518,12 @@ k_eqnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __res
     }
     if (STAGE) {
         wave_sync();
-        row_copy(y + n * row, sx, row, lane);
+        if constexpr (CMO) {
+            for (int d = 0; d < L.dim; ++d)
+                for (int c = lane; c < L.mult; c += 64) y[(d * N + n) * L.mult + c] = sx[c * L.dim + d];
+        } else {
+            row_copy(y + n * row, sx, row, lane);
+        }
     }
 }
 
@@ -410,11 +531,13 @@ k_eqnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __res
 // dn = -dfac ln / (n + eps)^2 + rstd (dnh - mean(dnh) - nh mean(dnh nh)) with
 // dnh = dln w, nh = (n - mu) rstd; gx = gy fac + x dn / n.
 // Per-wave partials of sum dln nh (pW) and sum dln (pB), per channel.
-template <int CPL, bool STAGE>
+// CMG (with STAGE): gy component-major (dim, N, mult); x and gx node-major.
+template <int CPL, bool STAGE, bool CMG = false>
 __global__ void __launch_bounds__(64 * kWaves)
 k_eqnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __restrict__ x,
              const float* __restrict__ w, const float* __restrict__ b, float eps, float ln_eps,
              float* __restrict__ gx, float* __restrict__ pW, float* __restrict__ pB) {
+    static_assert(STAGE || !CMG, "component-major gradients go through the LDS stage");
     const int lane = threadIdx.x & 63;
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
     const int64_t nw = static_cast<int64_t>(gridDim.x) * kWaves;
@@ -427,12 +550,20 @@ k_eqnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __re
     float* sx = lds + (threadIdx.x >> 6) * 2 * kStageRow;
     float* sg = sx + kStageRow;
     RowPrefetch pf;
-    if (STAGE) pf.load(x, gy, wave, N, row, lane);
+    if (STAGE) {
+        if constexpr (CMG) pf.load_cm(x, gy, wave, N, row, L.mult, lane);
+        else pf.load(x, gy, wave, N, row, lane);
+    }
     for (int64_t n = wave; n < N; n += nw) {
         if (STAGE) {
             wave_sync();  // the previous node's stores have read sg
-            pf.store(sx, sg, row, lane);
-            pf.load(x, gy, n + nw, N, row, lane);   // in flight during this node
+            if constexpr (CMG) {
+                pf.store_cm(sx, sg, row, L.mult, L.dim, lane);
+                pf.load_cm(x, gy, n + nw, N, row, L.mult, lane);   // in flight during this node
+            } else {
+                pf.store(sx, sg, row, lane);
+                pf.load(x, gy, n + nw, N, row, lane);
+            }
             wave_sync();
         }
         const float* xn = STAGE ? sx : x + n * row;
@@ -722,22 +853,45 @@ using namespace feq;
         FEQ_NODE_DISPATCH_S(cpl_of(L_.mult), __VA_ARGS__)                                 \
     }
 
-extern "C" int feq_sepnorm_fwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
-                               const float* x, const float* w_s, const float* b_s,
-                               const float* w_h, float eps, float* y, feq_stream_t stream) {
+namespace {
+int sepnorm_fwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, const float* x,
+                const float* w_s, const float* b_s, const float* w_h, float eps, float* y, bool cm,
+                feq_stream_t stream) {
     NodeL L;
     if (int rc = make_nodel(lvals, nreps, mult, &L)) return rc;
     if (L.ns > kMaxS) return fail(FEQ_ERR_UNSUPPORTED, "at most %d scalar irreps", kMaxS);
     if (int rc = check_rows(N, x, y, x)) return rc;
     if ((L.ns && (!w_s || !b_s)) || (L.nhc && !w_h)) return fail(FEQ_ERR_INVALID, "NULL norm weight");
+    if (cm && int64_t(L.mult) * L.dim > kStageRow)
+        return fail(FEQ_ERR_UNSUPPORTED, "component-major norm output: at most %d floats per node", kStageRow);
     if (N == 0) return FEQ_OK;
     hipStream_t s = stream_of(stream);
     const dim3 grid(static_cast<unsigned>(ceil_div(N, kWaves)));
+    if (cm) {
+        FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
+            auto k = k_sepnorm_fwd<cpl, true, true>;
+            FEQ_LAUNCH("k_sepnorm_fwd", k, grid, dim3(64 * kWaves), 0, s, L, N, x, w_s, b_s, w_h, eps, y);
+        })
+        return FEQ_OK;
+    }
     FEQ_NODE_DISPATCH(L, {
         auto k = k_sepnorm_fwd<cpl, stage>;
         FEQ_LAUNCH("k_sepnorm_fwd", k, grid, dim3(64 * kWaves), 0, s, L, N, x, w_s, b_s, w_h, eps, y);
     })
     return FEQ_OK;
+}
+}  // namespace
+
+extern "C" int feq_sepnorm_fwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                               const float* x, const float* w_s, const float* b_s,
+                               const float* w_h, float eps, float* y, feq_stream_t stream) {
+    return sepnorm_fwd(lvals, nreps, mult, N, x, w_s, b_s, w_h, eps, y, false, stream);
+}
+
+extern "C" int feq_sepnorm_fwd_cm(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                                  const float* x, const float* w_s, const float* b_s,
+                                  const float* w_h, float eps, float* y, feq_stream_t stream) {
+    return sepnorm_fwd(lvals, nreps, mult, N, x, w_s, b_s, w_h, eps, y, true, stream);
 }
 
 extern "C" size_t feq_sepnorm_workspace(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N) {
@@ -747,12 +901,14 @@ extern "C" size_t feq_sepnorm_workspace(const int32_t* lvals, int32_t nreps, int
     return sizeof(float) * (2 * partial_floats(w, int64_t(mult) * L.ns) + partial_floats(w, mult)) + 256;
 }
 
-extern "C" int feq_sepnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
-                               const float* gy, const float* x, const float* w_s, const float* w_h,
-                               float eps, float* gx, float* gw_s, float* gb_s, float* gw_h,
-                               void* ws, size_t ws_bytes, feq_stream_t stream) {
+namespace {
+int sepnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, const float* gy,
+                const float* x, const float* w_s, const float* w_h, float eps, float* gx, float* gw_s,
+                float* gb_s, float* gw_h, void* ws, size_t ws_bytes, bool cm, feq_stream_t stream) {
     NodeL L;
     if (int rc = make_nodel(lvals, nreps, mult, &L)) return rc;
+    if (cm && int64_t(L.mult) * L.dim > kStageRow)
+        return fail(FEQ_ERR_UNSUPPORTED, "component-major norm gradient: at most %d floats per node", kStageRow);
     if (L.ns > kMaxS) return fail(FEQ_ERR_UNSUPPORTED, "at most %d scalar irreps", kMaxS);
     if (int rc = check_rows(N, gy, x, gx)) return rc;
     if ((L.ns && (!w_s || !gw_s || !gb_s)) || (L.nhc && (!w_h || !gw_h)))
@@ -774,11 +930,19 @@ extern "C" int feq_sepnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult
     float* pS = base;
     float* pB = pS + partial_floats(w, nsc);
     float* pH = pB + partial_floats(w, nsc);
-    FEQ_NODE_DISPATCH(L, {
-        auto k = k_sepnorm_bwd<cpl, stage>;
-        FEQ_LAUNCH("k_sepnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
-                   s, L, N, gy, x, w_s, w_h, eps, gx, pS, pB, L.nhc ? pH : nullptr);
-    })
+    if (cm) {
+        FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
+            auto k = k_sepnorm_bwd<cpl, true, true>;
+            FEQ_LAUNCH("k_sepnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
+                       s, L, N, gy, x, w_s, w_h, eps, gx, pS, pB, L.nhc ? pH : nullptr);
+        })
+    } else {
+        FEQ_NODE_DISPATCH(L, {
+            auto k = k_sepnorm_bwd<cpl, stage>;
+            FEQ_LAUNCH("k_sepnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
+                       s, L, N, gy, x, w_s, w_h, eps, gx, pS, pB, L.nhc ? pH : nullptr);
+        })
+    }
     if (L.ns) {
         if (int rc = reduce_partials(pS, int(w), nsc, gw_s, pS + w * nsc, s)) return rc;
         if (int rc = reduce_partials(pB, int(w), nsc, gb_s, pB + w * nsc, s)) return rc;
@@ -787,22 +951,62 @@ extern "C" int feq_sepnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult
         if (int rc = reduce_partials(pH, int(w), mult, gw_h, pH + w * mult, s)) return rc;
     return FEQ_OK;
 }
+}  // namespace
 
-extern "C" int feq_eqnorm_fwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
-                              const float* x, const float* w_ln, const float* b_ln, float eps,
-                              float ln_eps, float* y, feq_stream_t stream) {
+extern "C" int feq_sepnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                               const float* gy, const float* x, const float* w_s, const float* w_h,
+                               float eps, float* gx, float* gw_s, float* gb_s, float* gw_h,
+                               void* ws, size_t ws_bytes, feq_stream_t stream) {
+    return sepnorm_bwd(lvals, nreps, mult, N, gy, x, w_s, w_h, eps, gx, gw_s, gb_s, gw_h, ws, ws_bytes, false,
+                       stream);
+}
+
+extern "C" int feq_sepnorm_bwd_cm(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                                  const float* gy, const float* x, const float* w_s, const float* w_h,
+                                  float eps, float* gx, float* gw_s, float* gb_s, float* gw_h,
+                                  void* ws, size_t ws_bytes, feq_stream_t stream) {
+    return sepnorm_bwd(lvals, nreps, mult, N, gy, x, w_s, w_h, eps, gx, gw_s, gb_s, gw_h, ws, ws_bytes, true,
+                       stream);
+}
+
+namespace {
+int eqnorm_fwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, const float* x,
+               const float* w_ln, const float* b_ln, float eps, float ln_eps, float* y, bool cm,
+               feq_stream_t stream) {
     NodeL L;
     if (int rc = make_nodel(lvals, nreps, mult, &L)) return rc;
     if (int rc = check_rows(N, x, y, x)) return rc;
     if (!w_ln != !b_ln) return fail(FEQ_ERR_INVALID, "LayerNorm weight and bias go together");
+    if (cm && int64_t(L.mult) * L.dim > kStageRow)
+        return fail(FEQ_ERR_UNSUPPORTED, "component-major norm output: at most %d floats per node", kStageRow);
     if (N == 0) return FEQ_OK;
     hipStream_t s = stream_of(stream);
+    const dim3 grid(static_cast<unsigned>(ceil_div(N, kWaves)));
+    if (cm) {
+        FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
+            auto k = k_eqnorm_fwd<cpl, true, true>;
+            FEQ_LAUNCH("k_eqnorm_fwd", k, grid, dim3(64 * kWaves), 0, s, L, N, x, w_ln, b_ln, eps, ln_eps, y);
+        })
+        return FEQ_OK;
+    }
     FEQ_NODE_DISPATCH(L, {
         auto k = k_eqnorm_fwd<cpl, stage>;
-        FEQ_LAUNCH("k_eqnorm_fwd", k, dim3(static_cast<unsigned>(ceil_div(N, kWaves))),
-                   dim3(64 * kWaves), 0, s, L, N, x, w_ln, b_ln, eps, ln_eps, y);
+        FEQ_LAUNCH("k_eqnorm_fwd", k, grid, dim3(64 * kWaves), 0, s, L, N, x, w_ln, b_ln, eps, ln_eps, y);
     })
     return FEQ_OK;
+}
+}  // namespace
+
+extern "C" int feq_eqnorm_fwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                              const float* x, const float* w_ln, const float* b_ln, float eps,
+                              float ln_eps, float* y, feq_stream_t stream) {
+    return eqnorm_fwd(lvals, nreps, mult, N, x, w_ln, b_ln, eps, ln_eps, y, false, stream);
+}
+
+extern "C" int feq_eqnorm_fwd_cm(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                                 const float* x, const float* w_ln, const float* b_ln, float eps,
+                                 float ln_eps, float* y, feq_stream_t stream) {
+    return eqnorm_fwd(lvals, nreps, mult, N, x, w_ln, b_ln, eps, ln_eps, y, true, stream);
 }
 
 extern "C" size_t feq_eqnorm_workspace(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N) {
@@ -811,12 +1015,14 @@ extern "C" size_t feq_eqnorm_workspace(const int32_t* lvals, int32_t nreps, int3
     return sizeof(float) * 2 * partial_floats(bwd_waves(N), mult) + 256;
 }
 
-extern "C" int feq_eqnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
-                              const float* gy, const float* x, const float* w_ln, const float* b_ln,
-                              float eps, float ln_eps, float* gx, float* gw_ln, float* gb_ln,
-                              void* ws, size_t ws_bytes, feq_stream_t stream) {
+namespace {
+int eqnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, const float* gy,
+               const float* x, const float* w_ln, const float* b_ln, float eps, float ln_eps, float* gx,
+               float* gw_ln, float* gb_ln, void* ws, size_t ws_bytes, bool cm, feq_stream_t stream) {
     NodeL L;
     if (int rc = make_nodel(lvals, nreps, mult, &L)) return rc;
+    if (cm && int64_t(L.mult) * L.dim > kStageRow)
+        return fail(FEQ_ERR_UNSUPPORTED, "component-major norm gradient: at most %d floats per node", kStageRow);
     if (int rc = check_rows(N, gy, x, gx)) return rc;
     if (!w_ln != !b_ln) return fail(FEQ_ERR_INVALID, "LayerNorm weight and bias go together");
     if (w_ln && (!gw_ln || !gb_ln)) return fail(FEQ_ERR_INVALID, "NULL LayerNorm gradient");
@@ -831,14 +1037,39 @@ extern "C" int feq_eqnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult,
     const int64_t w = bwd_waves(N);
     float* pW = w_ln ? static_cast<float*>(ws) : nullptr;
     float* pB = w_ln ? pW + partial_floats(w, mult) : nullptr;
-    FEQ_NODE_DISPATCH(L, {
-        auto k = k_eqnorm_bwd<cpl, stage>;
-        FEQ_LAUNCH("k_eqnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
-                   s, L, N, gy, x, w_ln, b_ln, eps, ln_eps, gx, pW, pB);
-    })
+    if (cm) {
+        FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
+            auto k = k_eqnorm_bwd<cpl, true, true>;
+            FEQ_LAUNCH("k_eqnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
+                       s, L, N, gy, x, w_ln, b_ln, eps, ln_eps, gx, pW, pB);
+        })
+    } else {
+        FEQ_NODE_DISPATCH(L, {
+            auto k = k_eqnorm_bwd<cpl, stage>;
+            FEQ_LAUNCH("k_eqnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
+                       s, L, N, gy, x, w_ln, b_ln, eps, ln_eps, gx, pW, pB);
+        })
+    }
     if (!w_ln) return FEQ_OK;
     if (int rc = reduce_partials(pW, int(w), mult, gw_ln, pW + w * mult, s)) return rc;
     return reduce_partials(pB, int(w), mult, gb_ln, pB + w * mult, s);
+}
+}  // namespace
+
+extern "C" int feq_eqnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                              const float* gy, const float* x, const float* w_ln, const float* b_ln,
+                              float eps, float ln_eps, float* gx, float* gw_ln, float* gb_ln,
+                              void* ws, size_t ws_bytes, feq_stream_t stream) {
+    return eqnorm_bwd(lvals, nreps, mult, N, gy, x, w_ln, b_ln, eps, ln_eps, gx, gw_ln, gb_ln, ws, ws_bytes,
+                      false, stream);
+}
+
+extern "C" int feq_eqnorm_bwd_cm(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                                 const float* gy, const float* x, const float* w_ln, const float* b_ln,
+                                 float eps, float ln_eps, float* gx, float* gw_ln, float* gb_ln,
+                                 void* ws, size_t ws_bytes, feq_stream_t stream) {
+    return eqnorm_bwd(lvals, nreps, mult, N, gy, x, w_ln, b_ln, eps, ln_eps, gx, gw_ln, gb_ln, ws, ws_bytes,
+                      true, stream);
 }
 
 #define FEQ_GATE_PRELUDE(a, b, c)                                                         \
@@ -899,5 +1130,38 @@ extern "C" int feq_gate_bwd_x(const int32_t* lvals, int32_t nreps, int32_t mult,
     else
         FEQ_LAUNCH("k_gate_bwd_x", k_gate_bwd_x, grid, dim3(kRowThreads), 0, s, L, rows, gy, x, lin,
                    norms, grad_norms, gx);
+    return FEQ_OK;
+}
+
+extern "C" size_t feq_scale_add_cm_workspace(void) { return sizeof(double) * kResGroups; }
+
+extern "C" int feq_scale_add_cm(const float* x, const float* y, const float* scale, int64_t N, int32_t mult,
+                                int32_t dim, float* out, feq_stream_t stream) {
+    if (N < 0 || mult < 1 || dim < 1) return fail(FEQ_ERR_INVALID, "invalid sizes");
+    if (int64_t(mult) * dim > kStageRow)
+        return fail(FEQ_ERR_UNSUPPORTED, "component-major residual: at most %d floats per node", kStageRow);
+    if (N == 0) return FEQ_OK;
+    if (!x || !y || !scale || !out) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    const int64_t g = ceil_div(N, kWaves);
+    FEQ_LAUNCH("k_scale_add_cm", k_scale_add_cm, dim3(static_cast<unsigned>(g < kResGroups ? g : kResGroups)),
+               dim3(64 * kWaves), 0, stream_of(stream), N, int(mult), int(dim), x, y, scale, out);
+    return FEQ_OK;
+}
+
+extern "C" int feq_scale_add_cm_bwd(const float* grad_out, const float* y, const float* scale, int64_t N,
+                                    int32_t mult, int32_t dim, float* grad_y, float* grad_scale, void* ws,
+                                    size_t ws_bytes, feq_stream_t stream) {
+    if (N < 0 || mult < 1 || dim < 1) return fail(FEQ_ERR_INVALID, "invalid sizes");
+    if (int64_t(mult) * dim > kStageRow)
+        return fail(FEQ_ERR_UNSUPPORTED, "component-major residual: at most %d floats per node", kStageRow);
+    if (!grad_scale && !grad_y) return FEQ_OK;
+    if (!scale || (N > 0 && (!grad_out || !y))) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (!ws || ws_bytes < feq_scale_add_cm_workspace())
+        return fail(FEQ_ERR_WORKSPACE, "residual workspace too small");
+    hipStream_t s = stream_of(stream);
+    double* part = static_cast<double*>(ws);
+    FEQ_LAUNCH("k_scale_add_cm_bwd", k_scale_add_cm_bwd, dim3(kResGroups), dim3(64 * kWaves), 0, s, N, int(mult),
+               int(dim), grad_out, y, scale, grad_y, part);
+    if (grad_scale) FEQ_LAUNCH("k_sum_f64", k_sum_f64, dim3(1), dim3(64 * kWaves), 0, s, part, kResGroups, grad_scale);
     return FEQ_OK;
 }

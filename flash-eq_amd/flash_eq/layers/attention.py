@@ -121,7 +121,13 @@ class EquivariantAttention(nn.Module):
         if half is not None:
             return run_float32(self, half, (P, Q_basis, node_features, distances, graph),
                                dict(edge_features=edge_features))
-        qk = self.linear_qk(self.norm_qk(node_features))            # (N, 2 mult, dim)
+        if (node_features.dim() == 3 and self.norm_qk.cm_ok(node_features)
+                and self.linear_qk.fused_ok(node_features)):
+            # the norm writes the component-major layout the projection reads
+            qk = self.linear_qk.forward_layout(self.norm_qk.forward_cm(node_features), True, False).view(
+                node_features.shape[0], 2 * self.in_repr.mult, node_features.shape[-1])
+        else:
+            qk = self.linear_qk(self.norm_qk(node_features))        # (N, 2 mult, dim)
         if edge_features is None and self.pool.reduce == "sum":
             # V projection, head weighting and sum pooling in one pass over the
             # edges where the fused kernels cover the layer (neither attn * V

@@ -105,12 +105,30 @@ class EquivariantLayerNorm(nn.Module):
         self._slices = irrep_slices(repr)
         self._lv = tuple(int(l) for l in repr.lvals.tolist())
 
+    def _kernels_ok(self, f: torch.Tensor) -> bool:
+        w = self.lnorm.weight if self.lnorm is not None else None
+        b = self.lnorm.bias if self.lnorm is not None else None
+        return self._epsilon is None and ops.node_kernels_ok(f, self._lv, self.mult, w, b) and (
+            self.lnorm is None or (w is not None and b is not None))
+
+    def cm_ok(self, f: torch.Tensor) -> bool:
+        """Whether ``forward_cm`` takes these features (the kernels, and a node
+        row of at most 1152 floats)."""
+        return self._kernels_ok(f) and self.mult * sum(2 * l + 1 for l in self._lv) <= 1152
+
+    def forward_cm(self, f: torch.Tensor) -> torch.Tensor:
+        """The norm of node-major features returned component-major (dim, N,
+        mult), for a channel-mixing map that follows; ``cm_ok(f)``."""
+        w = self.lnorm.weight if self.lnorm is not None else None
+        b = self.lnorm.bias if self.lnorm is not None else None
+        ln_eps = self.lnorm.eps if self.lnorm is not None else 0.0
+        return ops.EqNormFn.apply(f, w, b, self._lv, self.mult, get_epsilon(f.dtype), ln_eps, True)
+
     def forward(self, f: torch.Tensor) -> torch.Tensor:
         eps = self._epsilon if self._epsilon is not None else get_epsilon(f.dtype)
         w = self.lnorm.weight if self.lnorm is not None else None
         b = self.lnorm.bias if self.lnorm is not None else None
-        if self._epsilon is None and ops.node_kernels_ok(f, self._lv, self.mult, w, b) and (
-                self.lnorm is None or (w is not None and b is not None)):
+        if self._kernels_ok(f):
             ln_eps = self.lnorm.eps if self.lnorm is not None else 0.0
             return ops.EqNormFn.apply(f, w, b, self._lv, self.mult, eps, ln_eps)
         norms = self.norm(f)                                  # (..., mult, nreps)
@@ -149,14 +167,32 @@ class SeparableEquivariantLayerNorm(nn.Module):
             else:
                 self._runs.append(("h", a, b))
 
-    def forward(self, f: torch.Tensor) -> torch.Tensor:
+    def _kernel_args(self, f: torch.Tensor):
         ws = self.scalar_norm.weight if self.nscalar > 0 else None
         bs = self.scalar_norm.bias if self.nscalar > 0 else None
         wh = self.higher_norm.weight if self.nhigher > 0 else None
-        if (self.nscalar <= ops.NODE_MAX_SCALARS
+        if not (self.nscalar <= ops.NODE_MAX_SCALARS
                 and ops.node_kernels_ok(f, self._lv, self.repr.mult, ws, bs, wh)):
-            mod = self.scalar_norm if self.nscalar > 0 else self.higher_norm
-            eps = mod._epsilon if mod._epsilon is not None else get_epsilon(f.dtype)
+            return None
+        mod = self.scalar_norm if self.nscalar > 0 else self.higher_norm
+        eps = mod._epsilon if mod._epsilon is not None else get_epsilon(f.dtype)
+        return ws, bs, wh, eps
+
+    def cm_ok(self, f: torch.Tensor) -> bool:
+        """Whether ``forward_cm`` takes these features (the kernels, and a node
+        row of at most 1152 floats)."""
+        return self._kernel_args(f) is not None and self.repr.mult * self.repr.dim() <= 1152
+
+    def forward_cm(self, f: torch.Tensor) -> torch.Tensor:
+        """The norm of node-major features returned component-major (dim, N,
+        mult), for a channel-mixing map that follows; ``cm_ok(f)``."""
+        ws, bs, wh, eps = self._kernel_args(f)
+        return ops.SepNormFn.apply(f, ws, bs, wh, self._lv, self.repr.mult, eps, True)
+
+    def forward(self, f: torch.Tensor) -> torch.Tensor:
+        args = self._kernel_args(f)
+        if args is not None:
+            ws, bs, wh, eps = args
             return ops.SepNormFn.apply(f, ws, bs, wh, self._lv, self.repr.mult, eps)
         ys = None
         if self.nscalar > 0:

@@ -12,7 +12,7 @@ import torch.nn as nn
 
 from ..graph import Graph
 from ..representations import Repr, WignerDBasis
-from ..ops import ResidualScaleFn, ScaleFn
+from ..ops import ResidualScaleCmFn, ResidualScaleFn, ScaleFn
 from .attention import EquivariantAttention
 from .gating import EquivariantGating
 from .linear import EquivariantLinear
@@ -109,16 +109,23 @@ class EquivariantTransformerBlock(nn.Module):
             x = _residual(node_features, attn_out, self.layer_scale_attn, self.drop_path)
         else:
             x = attn_out
-        h = self.norm2(x)
-        if (isinstance(self.mlp_act, EquivariantGating) and self.mlp_act.kernels_ok(h)
-                and self.mlp_up.fused_ok(h) and self.mlp_down.fused_ok(h)):
-            # the hidden features stay component-major (dim, N, 2 mult) between
-            # the two linear maps and the gating: no transposes in between
-            t = self.mlp_act.forward_cm(self.mlp_up.forward_layout(h, False, True))
+        if (isinstance(self.mlp_act, EquivariantGating) and self.mlp_act.kernels_ok(x)
+                and self.mlp_up.fused_ok(x) and self.mlp_down.fused_ok(x)):
+            # the MLP runs component-major (dim, N, c) from the norm's output to
+            # the residual: the norm writes that layout, the linear maps and the
+            # gating keep it, and the residual sum reads it (no transposes)
+            cm = (self.norm2.cm_ok(x) and x.dim() == 3 and isinstance(self.layer_scale_mlp, LayerScale)
+                  and isinstance(self.drop_path, nn.Identity)
+                  and self.layer_scale_mlp.gamma.dtype == torch.float32)
+            h = self.norm2.forward_cm(x) if cm else self.norm2(x)
+            t = self.mlp_act.forward_cm(self.mlp_up.forward_layout(h, cm, True))
+            if cm:
+                return ResidualScaleCmFn.apply(x, self.mlp_down.forward_layout(t, True, True),
+                                               self.layer_scale_mlp.gamma)
             mlp_out = self.mlp_down.forward_layout(t, True, False).view(
                 *h.shape[:-2], self.out_repr.mult, h.shape[-1])
         else:
-            mlp_out = self.mlp_down(self.mlp_act(self.mlp_up(h)))
+            mlp_out = self.mlp_down(self.mlp_act(self.mlp_up(self.norm2(x))))
         return _residual(x, mlp_out, self.layer_scale_mlp, self.drop_path)
 
     def extra_repr(self) -> str:

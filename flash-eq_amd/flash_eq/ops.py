@@ -933,29 +933,31 @@ def _c(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
 
 
 class SepNormFn(torch.autograd.Function):
-    """SeparableEquivariantLayerNorm (norm.py:177-246) on feq_sepnorm_fwd/bwd."""
+    """SeparableEquivariantLayerNorm (norm.py:177-246) on feq_sepnorm_fwd/bwd.
+    ``cm``: the output (and its gradient) component-major (dim, N, mult),
+    feq_sepnorm_fwd_cm / _bwd_cm (the input stays node-major)."""
 
     @staticmethod
-    def forward(ctx, x, w_s, b_s, w_h, lvals, mult, eps):
+    def forward(ctx, x, w_s, b_s, w_h, lvals, mult, eps, cm=False):
         dim = sum(2 * l + 1 for l in lvals)
         xs = x.contiguous()
         n = _node_rows(xs, mult, dim)
         w_s, b_s, w_h = _c(w_s), _c(b_s), _c(w_h)
-        y = torch.empty_like(xs)
+        y = torch.empty(dim, n, mult, dtype=xs.dtype, device=xs.device) if cm else torch.empty_like(xs)
         if n:
+            fn = N.lib().feq_sepnorm_fwd_cm if cm else N.lib().feq_sepnorm_fwd
             with torch.cuda.device(xs.device):
-                rc = N.lib().feq_sepnorm_fwd(_lvals_i32(lvals), len(lvals), mult, n, N.ptr(xs),
-                                             N.ptr(w_s), N.ptr(b_s), N.ptr(w_h), eps, N.ptr(y),
-                                             N.stream_ptr(xs.device))
+                rc = fn(_lvals_i32(lvals), len(lvals), mult, n, N.ptr(xs), N.ptr(w_s), N.ptr(b_s),
+                        N.ptr(w_h), eps, N.ptr(y), N.stream_ptr(xs.device))
             N.check(rc, "feq_sepnorm_fwd")
         ctx.save_for_backward(xs, w_s, b_s, w_h)
-        ctx.meta = (lvals, mult, eps, n)
+        ctx.meta = (lvals, mult, eps, n, cm)
         return y
 
     @staticmethod
     def backward(ctx, gy):
         xs, w_s, b_s, w_h = ctx.saved_tensors
-        lvals, mult, eps, n = ctx.meta
+        lvals, mult, eps, n, cm = ctx.meta
         gy = gy.contiguous()
         dev = xs.device
         gx = torch.empty_like(xs)
@@ -965,38 +967,41 @@ class SepNormFn(torch.autograd.Function):
         lib = N.lib()
         arr = _lvals_i32(lvals)
         ws = N.workspace(lib.feq_sepnorm_workspace(arr, len(lvals), mult, n), dev)
+        fn = lib.feq_sepnorm_bwd_cm if cm else lib.feq_sepnorm_bwd
         with torch.cuda.device(dev):
-            rc = lib.feq_sepnorm_bwd(arr, len(lvals), mult, n, N.ptr(gy), N.ptr(xs), N.ptr(w_s),
-                                     N.ptr(w_h), eps, N.ptr(gx), N.ptr(gws), N.ptr(gbs), N.ptr(gwh),
-                                     N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+            rc = fn(arr, len(lvals), mult, n, N.ptr(gy), N.ptr(xs), N.ptr(w_s), N.ptr(w_h), eps, N.ptr(gx),
+                    N.ptr(gws), N.ptr(gbs), N.ptr(gwh), N.ptr(ws), ws.numel(), N.stream_ptr(dev))
         N.check(rc, "feq_sepnorm_bwd")
-        return gx, gws, gbs, gwh, None, None, None
+        return gx, gws, gbs, gwh, None, None, None, None
 
 
 class EqNormFn(torch.autograd.Function):
-    """EquivariantLayerNorm (norm.py:148-174) on feq_eqnorm_fwd/bwd."""
+    """EquivariantLayerNorm (norm.py:148-174) on feq_eqnorm_fwd/bwd.  ``cm``:
+    the output (and its gradient) component-major (dim, N, mult),
+    feq_eqnorm_fwd_cm / _bwd_cm (the input stays node-major)."""
 
     @staticmethod
-    def forward(ctx, x, w_ln, b_ln, lvals, mult, eps, ln_eps):
+    def forward(ctx, x, w_ln, b_ln, lvals, mult, eps, ln_eps, cm=False):
         dim = sum(2 * l + 1 for l in lvals)
         xs = x.contiguous()
         n = _node_rows(xs, mult, dim)
         w_ln, b_ln = _c(w_ln), _c(b_ln)
-        y = torch.empty_like(xs)
+        y = torch.empty(dim, n, mult, dtype=xs.dtype, device=xs.device) if cm else torch.empty_like(xs)
         if n:
+            fn = N.lib().feq_eqnorm_fwd_cm if cm else N.lib().feq_eqnorm_fwd
             with torch.cuda.device(xs.device):
-                rc = N.lib().feq_eqnorm_fwd(_lvals_i32(lvals), len(lvals), mult, n, N.ptr(xs),
+                rc = fn(_lvals_i32(lvals), len(lvals), mult, n, N.ptr(xs),
                                             N.ptr(w_ln), N.ptr(b_ln), eps, ln_eps, N.ptr(y),
                                             N.stream_ptr(xs.device))
             N.check(rc, "feq_eqnorm_fwd")
         ctx.save_for_backward(xs, w_ln, b_ln)
-        ctx.meta = (lvals, mult, eps, ln_eps, n)
+        ctx.meta = (lvals, mult, eps, ln_eps, n, cm)
         return y
 
     @staticmethod
     def backward(ctx, gy):
         xs, w_ln, b_ln = ctx.saved_tensors
-        lvals, mult, eps, ln_eps, n = ctx.meta
+        lvals, mult, eps, ln_eps, n, cm = ctx.meta
         gy = gy.contiguous()
         dev = xs.device
         gx = torch.empty_like(xs)
@@ -1006,11 +1011,11 @@ class EqNormFn(torch.autograd.Function):
         arr = _lvals_i32(lvals)
         ws = N.workspace(lib.feq_eqnorm_workspace(arr, len(lvals), mult, n), dev)
         with torch.cuda.device(dev):
-            rc = lib.feq_eqnorm_bwd(arr, len(lvals), mult, n, N.ptr(gy), N.ptr(xs), N.ptr(w_ln),
+            rc = (lib.feq_eqnorm_bwd_cm if cm else lib.feq_eqnorm_bwd)(arr, len(lvals), mult, n, N.ptr(gy), N.ptr(xs), N.ptr(w_ln),
                                     N.ptr(b_ln), eps, ln_eps, N.ptr(gx), N.ptr(gw), N.ptr(gb),
                                     N.ptr(ws), ws.numel(), N.stream_ptr(dev))
         N.check(rc, "feq_eqnorm_bwd")
-        return gx, gw, gb, None, None, None, None
+        return gx, gw, gb, None, None, None, None, None
 
 
 def transpose_last2(t: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
@@ -1145,6 +1150,48 @@ class ResidualScaleFn(torch.autograd.Function):
                                            N.ptr(gg) if gg is not None else None, N.ptr(ws), ws.numel(),
                                            N.stream_ptr(g.device))
             N.check(rc, "feq_scale_add_bwd")
+        return (g if ctx.needs_input_grad[0] else None, gy,
+                gg.reshape(gamma.shape) if gg is not None else None)
+
+
+class ResidualScaleCmFn(torch.autograd.Function):
+    """x + gamma * y with x node-major (N, mult, dim) and y component-major
+    (dim, N, mult), returned node-major (feq_scale_add_cm): the block's MLP
+    output joins the residual stream without a separate transpose.  The
+    backward forms grad_y (component-major) and grad_gamma (float64 products
+    and sum, fixed order) in one pass (feq_scale_add_cm_bwd); grad_x is g."""
+
+    @staticmethod
+    def forward(ctx, x, y, gamma):
+        xs, ys = x.contiguous(), y.contiguous()
+        n, mult, dim = xs.shape[0], xs.shape[1], xs.shape[2]
+        if ys.shape != (dim, n, mult):
+            raise RuntimeError(f"residual: component-major branch {tuple(ys.shape)} for rows {tuple(xs.shape)}")
+        out = torch.empty_like(xs)
+        with torch.cuda.device(xs.device):
+            rc = N.lib().feq_scale_add_cm(N.ptr(xs), N.ptr(ys), N.ptr(gamma), n, mult, dim, N.ptr(out),
+                                          N.stream_ptr(xs.device))
+        N.check(rc, "feq_scale_add_cm")
+        ctx.save_for_backward(ys, gamma)
+        ctx.meta = (n, mult, dim)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        ys, gamma = ctx.saved_tensors
+        n, mult, dim = ctx.meta
+        g = g.contiguous()
+        gy = torch.empty_like(ys) if ctx.needs_input_grad[1] else None
+        gg = torch.empty((), dtype=torch.float32, device=g.device) if ctx.needs_input_grad[2] else None
+        if gy is not None or gg is not None:
+            lib = N.lib()
+            ws = N.workspace(lib.feq_scale_add_cm_workspace(), g.device)
+            with torch.cuda.device(g.device):
+                rc = lib.feq_scale_add_cm_bwd(N.ptr(g), N.ptr(ys), N.ptr(gamma), n, mult, dim,
+                                              N.ptr(gy) if gy is not None else None,
+                                              N.ptr(gg) if gg is not None else None, N.ptr(ws), ws.numel(),
+                                              N.stream_ptr(g.device))
+            N.check(rc, "feq_scale_add_cm_bwd")
         return (g if ctx.needs_input_grad[0] else None, gy,
                 gg.reshape(gamma.shape) if gg is not None else None)
 

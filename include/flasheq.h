@@ -536,11 +536,22 @@ int feq_sepnorm_fwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t n
                     float eps, float* y, feq_stream_t stream);
 size_t feq_sepnorm_workspace(const int32_t* lvals, int32_t nreps, int32_t mult,
                              int64_t num_nodes);
+/* The same with y (forward) or grad_y (backward) component-major (dim, N, mult),
+ * the layout of the channel-mixing maps that follow the norm in the block's
+ * MLP; x and grad_x stay node-major; mult * dim at most 1152. */
+int feq_sepnorm_fwd_cm(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
+                       const float* x, const float* w_s, const float* b_s, const float* w_h,
+                       float eps, float* y, feq_stream_t stream);
 int feq_sepnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
                     const float* grad_y, const float* x, const float* w_s, const float* w_h,
                     float eps, float* grad_x, float* grad_w_s, float* grad_b_s,
                     float* grad_w_h, void* workspace, size_t workspace_bytes,
                     feq_stream_t stream);
+int feq_sepnorm_bwd_cm(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
+                       const float* grad_y, const float* x, const float* w_s, const float* w_h,
+                       float eps, float* grad_x, float* grad_w_s, float* grad_b_s,
+                       float* grad_w_h, void* workspace, size_t workspace_bytes,
+                       feq_stream_t stream);
 
 /* EquivariantLayerNorm (norm.py:148-174): per irrep k, n = sqrt(sum x^2 + eps)
  * (RepNorm, norm.py:51-73); y = x * LayerNorm_c(n)[w_ln, b_ln, ln_eps] / (n + eps),
@@ -550,6 +561,16 @@ int feq_eqnorm_fwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t nu
                    float ln_eps, float* y, feq_stream_t stream);
 size_t feq_eqnorm_workspace(const int32_t* lvals, int32_t nreps, int32_t mult,
                             int64_t num_nodes);
+/* The same with y (forward) or grad_y (backward) component-major (dim, N, mult),
+ * as feq_sepnorm_fwd_cm / _bwd_cm (the attention's QK projection follows this
+ * norm); mult * dim at most 1152. */
+int feq_eqnorm_fwd_cm(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
+                      const float* x, const float* w_ln, const float* b_ln, float eps,
+                      float ln_eps, float* y, feq_stream_t stream);
+int feq_eqnorm_bwd_cm(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
+                      const float* grad_y, const float* x, const float* w_ln, const float* b_ln,
+                      float eps, float ln_eps, float* grad_x, float* grad_w_ln, float* grad_b_ln,
+                      void* workspace, size_t workspace_bytes, feq_stream_t stream);
 int feq_eqnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
                    const float* grad_y, const float* x, const float* w_ln, const float* b_ln,
                    float eps, float ln_eps, float* grad_x, float* grad_w_ln, float* grad_b_ln,
@@ -645,6 +666,17 @@ int feq_scale_add(const float* x, const float* y, const float* scale, int64_t n,
 int feq_scale_add_bwd(const float* grad_out, const float* y, const float* scale, int64_t n,
                       float* grad_y, float* grad_scale, void* workspace, size_t ws_bytes,
                       feq_stream_t stream);
+/* The same residual with y component-major (dim, N, mult), x and out node-major
+ * (N, mult, dim): the block's MLP output joins the residual stream without a
+ * separate transpose.  The backward writes grad_y component-major (may be NULL)
+ * and grad_scale (may be NULL); workspace feq_scale_add_cm_workspace() bytes.
+ * mult * dim at most 1152. */
+int feq_scale_add_cm(const float* x, const float* y, const float* scale, int64_t num_nodes, int32_t mult,
+                     int32_t dim, float* out, feq_stream_t stream);
+size_t feq_scale_add_cm_workspace(void);
+int feq_scale_add_cm_bwd(const float* grad_out, const float* y, const float* scale, int64_t num_nodes,
+                         int32_t mult, int32_t dim, float* grad_y, float* grad_scale, void* workspace,
+                         size_t ws_bytes, feq_stream_t stream);
 /* out[0] = (float) sum of (double) a[i] * b[i], the products and their sum in
  * float64 in a fixed order (many products that largely cancel). */
 size_t feq_dot_f64_workspace(void);

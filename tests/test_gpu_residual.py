@@ -6,8 +6,11 @@ The reference writes it as x + drop_path(layer_scale(y)) (transformer.py:245,
 grad_gamma = sum g y.  Checked against those float64 formulas: out, grad_x and
 grad_y at float32 rounding (1e-6 relative), grad_gamma at 1e-6 relative (its
 products and sum in float64), ragged lengths (vectorised body and scalar
-tail), gamma without gradient, and the block's launch log (the fused
-kernels, no elementwise multiply for the layer scale).
+tail), gamma without gradient, the MLP's component-major branch
+(feq_scale_add_cm, against the same formulas), the separable norm's
+component-major output (bit for bit the node-major kernels' values), and the
+block's launch log (the fused kernels; transposes only at the QK
+projection's output, for the attention's node-major rows).
 """
 import pytest
 import torch
@@ -71,5 +74,59 @@ def test_block_uses_the_fused_residuals(dev):
     torch.cuda.synchronize()
     NAT.profile_enable(False)
     launched = NAT.profile_summary()
-    assert launched.get("k_scale_add", (0,))[0] == 2, launched
+    # the attention residual in one pass; the MLP's component-major branch
+    # joins through the transposing sum, and the MLP runs without transposes
+    assert launched.get("k_scale_add", (0,))[0] == 1, launched
+    assert launched.get("k_scale_add_cm", (0,))[0] == 1, launched
+    assert launched.get("k_scale_add_cm_bwd", (0,))[0] == 1, launched
+    ntr = sum(v[0] for k, v in launched.items() if k.startswith("k_transpose"))
+    assert ntr == 2, launched      # the QK projection's output, forward and backward
     assert blk.layer_scale_attn.gamma.grad is not None and blk.layer_scale_mlp.gamma.grad is not None
+
+
+def test_component_major_branch_matches_float64(dev):
+    """x (N, mult, dim) + gamma y with y component-major (dim, N, mult)."""
+    N, mult, dim = 1001, 64, 9
+    g = torch.Generator().manual_seed(5)
+    x, go = torch.randn(N, mult, dim, generator=g), torch.randn(N, mult, dim, generator=g)
+    y = torch.randn(dim, N, mult, generator=g)
+    gamma = torch.tensor(-0.61)
+    xd, yd = x.to(dev).requires_grad_(True), y.to(dev).requires_grad_(True)
+    gd = gamma.to(dev).requires_grad_(True)
+    from flash_eq.ops import ResidualScaleCmFn
+    out = ResidualScaleCmFn.apply(xd, yd, gd)
+    out.backward(go.to(dev))
+    yt = y.double().permute(1, 2, 0)
+    assert rel_err(out, x.double() + gamma.double() * yt) < 1e-6
+    assert torch.equal(xd.grad.cpu(), go)
+    assert rel_err(yd.grad, (gamma.double() * go.double()).permute(2, 0, 1)) < 1e-6
+    gg = (go.double() * yt).sum()
+    assert abs(gd.grad.item() - gg.item()) <= 1e-6 * (go.double() * yt).abs().sum().item()
+
+
+@pytest.mark.parametrize("kind", ["separable", "equivariant"])
+def test_component_major_norm_output_is_the_transpose(dev, kind):
+    """The separable and the equivariant layer norm with their output (and
+    gradient) component-major: the node-major kernels' values, bit for bit."""
+    torch.manual_seed(1)
+    cls = fe.SeparableEquivariantLayerNorm if kind == "separable" else fe.EquivariantLayerNorm
+    norm = cls(fe.Repr([0, 1, 2], 64)).to(dev)
+    with torch.no_grad():
+        for p in norm.parameters():
+            p.normal_()
+    x = torch.randn(777, 64, 9, device=dev)
+    gy = torch.randn(777, 64, 9, device=dev)
+    x1 = x.clone().requires_grad_(True)
+    y1 = norm(x1)
+    y1.backward(gy)
+    g1 = [p.grad.clone() for p in norm.parameters()]
+    for p in norm.parameters():
+        p.grad = None
+    x2 = x.clone().requires_grad_(True)
+    assert norm.cm_ok(x2)
+    y2 = norm.forward_cm(x2)
+    y2.backward(gy.permute(2, 0, 1).contiguous())
+    assert torch.equal(y2, y1.detach().permute(2, 0, 1))
+    assert torch.equal(x2.grad, x1.grad)
+    for a, b in zip(g1, norm.parameters()):
+        assert torch.equal(a, b.grad)
