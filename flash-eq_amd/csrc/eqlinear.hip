@@ -283,7 +283,7 @@ k_eql_mm(const float* __restrict__ in, int64_t rows, int D, EqlMap map, const h8
 // rows of gy (scalar irreps with a bias); an irrep's rows are contiguous in the
 // component-major tables ((2l+1) rows per node).  A workgroup sums CPW chunks
 // of 64 (or 32) rows of one irrep into one partial; k_eql_wsum adds the partials of
-// each irrep in workgroup order (deterministic, no atomics).
+// each irrep in a fixed order (deterministic, no atomics).
 //
 // Per chunk the workgroup stages gy and x as fp16 hi / lo in LDS, row-major,
 // each column scaled by its own power of two over the chunk (a column's
@@ -514,38 +514,48 @@ k_eql_wgrad(const float* __restrict__ G, const float* __restrict__ X, EqlWg T, f
     if (tid < CO) pb[static_cast<int64_t>(blockIdx.x) * CO + tid] = bacc;
 }
 
-// Sum of the partials p[w0 .. w1) at stride st: eight interleaved chains (so
-// that eight loads are in flight), combined pairwise: a fixed order.
-__device__ __forceinline__ float eql_chain_sum(const float* __restrict__ p, int w0, int w1, int64_t st) {
-    float a[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) a[j] = 0.0f;
-    int w = w0;
-    for (; w + 8 <= w1; w += 8)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) a[j] += p[static_cast<int64_t>(w + j) * st];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-        if (w + j < w1) a[j] += p[static_cast<int64_t>(w + j) * st];
-    return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+// Sum of the partials p[w0 .. w1) at stride st by the eight lanes j = lane % 8
+// of an aligned lane octet: lane j adds partials w0 + j, w0 + j + 8, ... (two
+// chains, so that two loads are in flight), then the octet combines its eight
+// sums over lane bits 0, 1, 2: a fixed order.
+__device__ __forceinline__ float eql_octet_sum(const float* __restrict__ p, int w0, int w1, int64_t st,
+                                               int j) {
+    float a0 = 0.0f, a1 = 0.0f;
+    int w = w0 + j;
+    for (; w + 8 < w1; w += 16) {
+        a0 += p[static_cast<int64_t>(w) * st];
+        a1 += p[static_cast<int64_t>(w + 8) * st];
+    }
+    if (w < w1) a0 += p[static_cast<int64_t>(w) * st];
+    float v = a0 + a1;
+    v += __shfl_xor(v, 1, 64);
+    v += __shfl_xor(v, 2, 64);
+    v += __shfl_xor(v, 4, 64);
+    return v;
 }
 
 // gW[k] = sum of irrep k's partials (a fixed order); gb[co][bcol[k]] likewise
-// for the scalar irreps with a bias column.
+// for the scalar irreps with a bias column.  Eight lanes per output element.
 __global__ void __launch_bounds__(256)
 k_eql_wsum(const float* __restrict__ pw, const float* __restrict__ pb, EqlWg T, EqlMap bmap, int CO,
            int CI, int nbias, float* __restrict__ gw, float* __restrict__ gb) {
     const int64_t nw = static_cast<int64_t>(T.nreps) * CO * CI;
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 3;
+    const int j = threadIdx.x & 7;
+    // every lane of an octet takes the same branch (i is per octet)
     if (i < nw) {
         const int k = static_cast<int>(i / (static_cast<int64_t>(CO) * CI));
         const int64_t e = i - static_cast<int64_t>(k) * CO * CI;
-        gw[i] = eql_chain_sum(pw + e, T.wg0[k], T.wg0[k + 1], static_cast<int64_t>(CO) * CI);
+        const float v = eql_octet_sum(pw + e, T.wg0[k], T.wg0[k + 1], static_cast<int64_t>(CO) * CI, j);
+        if (j == 0) gw[i] = v;
     } else if (gb && i < nw + static_cast<int64_t>(T.nreps) * CO) {
-        const int64_t j = i - nw;
-        const int k = static_cast<int>(j / CO), co = static_cast<int>(j % CO);
+        const int64_t q = i - nw;
+        const int k = static_cast<int>(q / CO), co = static_cast<int>(q % CO);
         const int bc = bmap.bcol[k];
-        if (bc >= 0) gb[static_cast<int64_t>(co) * nbias + bc] = eql_chain_sum(pb + co, T.wg0[k], T.wg0[k + 1], CO);
+        if (bc >= 0) {
+            const float v = eql_octet_sum(pb + co, T.wg0[k], T.wg0[k + 1], CO, j);
+            if (j == 0) gb[static_cast<int64_t>(co) * nbias + bc] = v;
+        }
     }
 }
 
@@ -715,7 +725,7 @@ extern "C" int feq_eqlinear_bwd_w(const int32_t* lvals, int32_t nreps, int64_t r
         if (rc) return rc;
     }
     const int64_t n = static_cast<int64_t>(nreps) * cout * cin + static_cast<int64_t>(nreps) * cout;
-    FEQ_LAUNCH("k_eql_wsum", k_eql_wsum, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, pw,
+    FEQ_LAUNCH("k_eql_wsum", k_eql_wsum, dim3(static_cast<unsigned>((8 * n + 255) / 256)), dim3(256), 0, s, pw,
                pb, T, bmap, static_cast<int>(cout), static_cast<int>(cin), nbias, grad_w, grad_b);
     return FEQ_OK;
 }
