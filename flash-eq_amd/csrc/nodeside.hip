@@ -27,12 +27,15 @@ constexpr int kRowThreads = 256;
 
 struct NodeL {
     int mult, dim, nreps;
+    int vec;  // node rows move with 16-byte accesses (mult % 4 == 0, tables 16-byte aligned)
     int ns;   // scalar (l = 0) irreps
     int nhc;  // l > 0 components per channel
     int off[FEQ_MAX_IRREPS + 1];
     int deg[FEQ_MAX_IRREPS];
     int spos[kMaxS];  // component offset of each scalar irrep, in order
 };
+
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }  // NULL passes
 
 int make_nodel(const int32_t* lvals, int32_t nreps, int32_t mult, NodeL* L) {
     if (!lvals || nreps < 1 || nreps > FEQ_MAX_IRREPS)
@@ -42,6 +45,7 @@ int make_nodel(const int32_t* lvals, int32_t nreps, int32_t mult, NodeL* L) {
                     FEQ_NODE_MAX_MULT, mult);
     *L = NodeL{};
     L->mult = mult;
+    L->vec = mult % 4 == 0;   // and the caller ANDs in its tables' alignment
     L->nreps = nreps;
     int o = 0;
     for (int k = 0; k < nreps; ++k) {
@@ -86,65 +90,171 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Coalesced copy of one node row by a wave.
+// Coalesced copy of one node row by a wave: 16-byte accesses with vec (the row
+// a multiple of 4 floats, both ends 16-byte aligned), else 4-byte.
 __device__ __forceinline__ void row_copy(float* __restrict__ d, const float* __restrict__ s, int64_t n,
-                                         int lane) {
-    for (int64_t i = lane; i < n; i += 64) d[i] = s[i];
+                                         int lane, bool vec) {
+    if (vec) {
+        const int64_t n4 = n >> 2;
+        for (int64_t i = lane; i < n4; i += 64)
+            reinterpret_cast<float4*>(d)[i] = reinterpret_cast<const float4*>(s)[i];
+    } else {
+        for (int64_t i = lane; i < n; i += 64) d[i] = s[i];
+    }
 }
 
-// Each lane's share (elements lane, lane + 64, ...) of one node's x and gy
-// rows, held in registers: the backward kernels load the next node's rows
-// while the current node is computed, then move them into LDS.
+__device__ __forceinline__ void put4(float* v, const float4 a) {
+    v[0] = a.x;
+    v[1] = a.y;
+    v[2] = a.z;
+    v[3] = a.w;
+}
+__device__ __forceinline__ float4 get4(const float* v) { return make_float4(v[0], v[1], v[2], v[3]); }
+
+// A component-major row (dim, N, mult) of node n into a node-major LDS row
+// (c dim + d), and back: 16-byte runs of 4 channels with vec.
+__device__ __forceinline__ void cm_to_row(float* __restrict__ srow, const float* __restrict__ t, int64_t N,
+                                          int64_t n, int mult, int dim, int lane, bool vec) {
+    if (vec) {
+        const int m4 = mult >> 2;
+        for (int q = lane; q < dim * m4; q += 64) {
+            const int d = q / m4, c = 4 * (q - d * m4);
+            const float4 v = reinterpret_cast<const float4*>(t + (d * N + n) * mult)[c >> 2];
+            srow[c * dim + d] = v.x;
+            srow[(c + 1) * dim + d] = v.y;
+            srow[(c + 2) * dim + d] = v.z;
+            srow[(c + 3) * dim + d] = v.w;
+        }
+    } else {
+        for (int d = 0; d < dim; ++d)
+            for (int c = lane; c < mult; c += 64) srow[c * dim + d] = t[(d * N + n) * mult + c];
+    }
+}
+__device__ __forceinline__ void row_to_cm(float* __restrict__ t, const float* __restrict__ srow, int64_t N,
+                                          int64_t n, int mult, int dim, int lane, bool vec, float scale = 1.0f) {
+    if (vec) {
+        const int m4 = mult >> 2;
+        for (int q = lane; q < dim * m4; q += 64) {
+            const int d = q / m4, c = 4 * (q - d * m4);
+            reinterpret_cast<float4*>(t + (d * N + n) * mult)[c >> 2] =
+                make_float4(scale * srow[c * dim + d], scale * srow[(c + 1) * dim + d],
+                            scale * srow[(c + 2) * dim + d], scale * srow[(c + 3) * dim + d]);
+        }
+    } else {
+        for (int d = 0; d < dim; ++d)
+            for (int c = lane; c < mult; c += 64) t[(d * N + n) * mult + c] = scale * srow[c * dim + d];
+    }
+}
+
+// Each lane's share of one node's x and gy rows, held in registers: the
+// backward kernels load the next node's rows while the current node is
+// computed, then move them into LDS.  With vec, lane l holds the float4s l,
+// l + 64, ... of the row; else the floats l, l + 64, ....  With gy
+// component-major (the _cm forms), gy is read as the row's runs of channels
+// per component and staged at the node-major positions.
 constexpr int kRowPer = kStageRow / 64;
+constexpr int kRowPer4 = (kStageRow / 4 + 63) / 64;
 struct RowPrefetch {
-    float x[kRowPer], g[kRowPer];
+    float x[4 * kRowPer4], g[4 * kRowPer4];
     __device__ __forceinline__ void load(const float* __restrict__ xs, const float* __restrict__ gs,
-                                         int64_t n, int64_t N, int64_t row, int lane) {
+                                         int64_t n, int64_t N, int64_t row, int lane, bool vec) {
         if (n >= N) return;
+        if (vec) {
+            const float4* x4 = reinterpret_cast<const float4*>(xs + n * row);
+            const float4* g4 = reinterpret_cast<const float4*>(gs + n * row);
 #pragma unroll
-        for (int i = 0; i < kRowPer; ++i) {
-            const int64_t idx = lane + 64 * i;
-            if (idx < row) {
-                x[i] = xs[n * row + idx];
-                g[i] = gs[n * row + idx];
+            for (int i = 0; i < kRowPer4; ++i) {
+                const int64_t q = lane + 64 * i;
+                if (4 * q < row) {
+                    put4(x + 4 * i, x4[q]);
+                    put4(g + 4 * i, g4[q]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kRowPer; ++i) {
+                const int64_t idx = lane + 64 * i;
+                if (idx < row) {
+                    x[i] = xs[n * row + idx];
+                    g[i] = gs[n * row + idx];
+                }
             }
         }
     }
-    __device__ __forceinline__ void store(float* sx, float* sg, int64_t row, int lane) const {
+    __device__ __forceinline__ void store(float* sx, float* sg, int64_t row, int lane, bool vec) const {
+        if (vec) {
 #pragma unroll
-        for (int i = 0; i < kRowPer; ++i) {
-            const int64_t idx = lane + 64 * i;
-            if (idx < row) {
-                sx[idx] = x[i];
-                sg[idx] = g[i];
+            for (int i = 0; i < kRowPer4; ++i) {
+                const int64_t q = lane + 64 * i;
+                if (4 * q < row) {
+                    reinterpret_cast<float4*>(sx)[q] = get4(x + 4 * i);
+                    reinterpret_cast<float4*>(sg)[q] = get4(g + 4 * i);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kRowPer; ++i) {
+                const int64_t idx = lane + 64 * i;
+                if (idx < row) {
+                    sx[idx] = x[i];
+                    sg[idx] = g[i];
+                }
             }
         }
     }
-    // The same with gy component-major (dim, N, mult): element i of a lane is
-    // component d = idx / mult, channel c = idx % mult (contiguous channel runs
-    // per component in memory), staged at the node-major position c dim + d.
+    // gy component-major (dim, N, mult): element (d, c) of node n sits at
+    // (d N + n) mult + c; the lane's share is the same positions of the row in
+    // component-major order (d mult + c), so each component is a contiguous run.
     __device__ __forceinline__ void load_cm(const float* __restrict__ xs, const float* __restrict__ gs,
-                                            int64_t n, int64_t N, int64_t row, int mult, int lane) {
+                                            int64_t n, int64_t N, int64_t row, int mult, int lane, bool vec) {
         if (n >= N) return;
+        if (vec) {
+            const float4* x4 = reinterpret_cast<const float4*>(xs + n * row);
+            const int m4 = mult >> 2;
 #pragma unroll
-        for (int i = 0; i < kRowPer; ++i) {
-            const int64_t idx = lane + 64 * i;
-            if (idx < row) {
-                const int d = static_cast<int>(idx) / mult, c = static_cast<int>(idx) - d * mult;
-                x[i] = xs[n * row + idx];
-                g[i] = gs[(d * N + n) * mult + c];
+            for (int i = 0; i < kRowPer4; ++i) {
+                const int q = lane + 64 * i;
+                if (4 * q < row) {
+                    const int d = q / m4, c4 = q - d * m4;
+                    put4(x + 4 * i, x4[q]);
+                    put4(g + 4 * i, reinterpret_cast<const float4*>(gs + (d * N + n) * mult)[c4]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kRowPer; ++i) {
+                const int64_t idx = lane + 64 * i;
+                if (idx < row) {
+                    const int d = static_cast<int>(idx) / mult, c = static_cast<int>(idx) - d * mult;
+                    x[i] = xs[n * row + idx];
+                    g[i] = gs[(d * N + n) * mult + c];
+                }
             }
         }
     }
     __device__ __forceinline__ void store_cm(float* sx, float* sg, int64_t row, int mult, int dim,
-                                             int lane) const {
+                                             int lane, bool vec) const {
+        if (vec) {
+            const int m4 = mult >> 2;
 #pragma unroll
-        for (int i = 0; i < kRowPer; ++i) {
-            const int64_t idx = lane + 64 * i;
-            if (idx < row) {
-                const int d = static_cast<int>(idx) / mult, c = static_cast<int>(idx) - d * mult;
-                sx[idx] = x[i];
-                sg[c * dim + d] = g[i];
+            for (int i = 0; i < kRowPer4; ++i) {
+                const int q = lane + 64 * i;
+                if (4 * q < row) {
+                    const int d = q / m4, c = 4 * (q - d * m4);
+                    reinterpret_cast<float4*>(sx)[q] = get4(x + 4 * i);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) sg[(c + j) * dim + d] = g[4 * i + j];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kRowPer; ++i) {
+                const int64_t idx = lane + 64 * i;
+                if (idx < row) {
+                    const int d = static_cast<int>(idx) / mult, c = static_cast<int>(idx) - d * mult;
+                    sx[idx] = x[i];
+                    sg[c * dim + d] = g[i];
+                }
             }
         }
     }
@@ -160,20 +270,20 @@ __device__ __forceinline__ float sigmoidf(float v) { return 1.0f / (1.0f + expf(
 // STAGE: the node row moves through LDS (coalesced), computed in place.
 // CMO (with STAGE): y is component-major (dim, N, mult), the layout the
 // channel-mixing maps after the norm take, written as contiguous channel runs.
-template <int CPL, bool STAGE, bool CMO = false>
+template <int CPL, bool STAGE, bool CMO = false, bool VEC = false>
 __global__ void __launch_bounds__(64 * kWaves)
 k_sepnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __restrict__ ws,
               const float* __restrict__ bs, const float* __restrict__ wh, float eps,
               float* __restrict__ y) {
     static_assert(STAGE || !CMO, "component-major output goes through the LDS stage");
-    __shared__ float lds[STAGE ? kWaves * kStageRow : 1];
+    __shared__ __align__(16) float lds[STAGE ? kWaves * kStageRow : 1];
     const int lane = threadIdx.x & 63;
     const int64_t n = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
     if (n >= N) return;
     const int64_t row = static_cast<int64_t>(L.mult) * L.dim;
     float* sx = lds + (threadIdx.x >> 6) * kStageRow;
     if (STAGE) {
-        row_copy(sx, x + n * row, row, lane);
+        row_copy(sx, x + n * row, row, lane, VEC);
         wave_sync();
     }
     const float* xn = STAGE ? sx : x + n * row;
@@ -234,10 +344,9 @@ k_sepnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __re
     if (STAGE) {
         wave_sync();
         if constexpr (CMO) {
-            for (int d = 0; d < L.dim; ++d)
-                for (int c = lane; c < L.mult; c += 64) y[(d * N + n) * L.mult + c] = sx[c * L.dim + d];
+            row_to_cm(y, sx, N, n, L.mult, L.dim, lane, VEC);
         } else {
-            row_copy(y + n * row, sx, row, lane);
+            row_copy(y + n * row, sx, row, lane, VEC);
         }
     }
 }
@@ -249,7 +358,7 @@ k_sepnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __re
 // Per-wave partials: pS, pB (mult, ns) of gy (v - mu) / den and gy; pH (mult) of
 // sum_d gy v / rms.
 // CMG (with STAGE): gy is component-major (dim, N, mult); x and gx node-major.
-template <int CPL, bool STAGE, bool CMG = false>
+template <int CPL, bool STAGE, bool CMG = false, bool VEC = false>
 __global__ void __launch_bounds__(64 * kWaves)
 k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __restrict__ x,
               const float* __restrict__ ws, const float* __restrict__ wh, float eps,
@@ -269,23 +378,23 @@ k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __r
 #pragma unroll
         for (int j = 0; j < kMaxS; ++j) aS[i][j] = aB[i][j] = 0.0f;
     }
-    __shared__ float lds[STAGE ? 2 * kWaves * kStageRow : 1];
+    __shared__ __align__(16) float lds[STAGE ? 2 * kWaves * kStageRow : 1];
     float* sx = lds + (threadIdx.x >> 6) * 2 * kStageRow;
     float* sg = sx + kStageRow;
     RowPrefetch pf;
     if (STAGE) {
-        if constexpr (CMG) pf.load_cm(x, gy, wave, N, row, L.mult, lane);
-        else pf.load(x, gy, wave, N, row, lane);
+        if constexpr (CMG) pf.load_cm(x, gy, wave, N, row, L.mult, lane, VEC);
+        else pf.load(x, gy, wave, N, row, lane, VEC);
     }
     for (int64_t n = wave; n < N; n += nw) {
         if (STAGE) {
             wave_sync();  // the previous node's stores have read sg
             if constexpr (CMG) {
-                pf.store_cm(sx, sg, row, L.mult, L.dim, lane);
-                pf.load_cm(x, gy, n + nw, N, row, L.mult, lane);   // in flight during this node
+                pf.store_cm(sx, sg, row, L.mult, L.dim, lane, VEC);
+                pf.load_cm(x, gy, n + nw, N, row, L.mult, lane, VEC);   // in flight during this node
             } else {
-                pf.store(sx, sg, row, lane);
-                pf.load(x, gy, n + nw, N, row, lane);
+                pf.store(sx, sg, row, lane, VEC);
+                pf.load(x, gy, n + nw, N, row, lane, VEC);
             }
             wave_sync();
         }
@@ -373,7 +482,7 @@ k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __r
         }
         if (STAGE) {
             wave_sync();
-            row_copy(gx + n * row, sg, row, lane);
+            row_copy(gx + n * row, sg, row, lane, VEC);
         }
     }
 #pragma unroll
@@ -398,19 +507,27 @@ k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __r
 constexpr int kResGroups = 1024;
 
 __global__ void __launch_bounds__(64 * kWaves)
-k_scale_add_cm(int64_t N, int mult, int dim, const float* __restrict__ x, const float* __restrict__ y,
+k_scale_add_cm(int64_t N, int mult, int dim, int vec, const float* __restrict__ x, const float* __restrict__ y,
                const float* __restrict__ scale, float* __restrict__ out) {
-    __shared__ float lds[kWaves * kStageRow];
+    __shared__ __align__(16) float lds[kWaves * kStageRow];
     const int lane = threadIdx.x & 63;
     float* sy = lds + (threadIdx.x >> 6) * kStageRow;
     const float sc = scale[0];
     const int64_t row = static_cast<int64_t>(mult) * dim;
     const int64_t nw = static_cast<int64_t>(gridDim.x) * kWaves;
     for (int64_t n = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6); n < N; n += nw) {
-        for (int d = 0; d < dim; ++d)
-            for (int c = lane; c < mult; c += 64) sy[c * dim + d] = y[(d * N + n) * mult + c];
+        cm_to_row(sy, y, N, n, mult, dim, lane, vec);
         wave_sync();
-        for (int64_t i = lane; i < row; i += 64) out[n * row + i] = x[n * row + i] + sc * sy[i];
+        if (vec) {
+            const float4* x4 = reinterpret_cast<const float4*>(x + n * row);
+            float4* o4 = reinterpret_cast<float4*>(out + n * row);
+            for (int64_t i = lane; i < row / 4; i += 64) {
+                const float4 a = x4[i], b = reinterpret_cast<const float4*>(sy)[i];
+                o4[i] = make_float4(a.x + sc * b.x, a.y + sc * b.y, a.z + sc * b.z, a.w + sc * b.w);
+            }
+        } else {
+            for (int64_t i = lane; i < row; i += 64) out[n * row + i] = x[n * row + i] + sc * sy[i];
+        }
         wave_sync();   // this node's reads of sy are done before the next node's writes
     }
 }
@@ -418,9 +535,10 @@ k_scale_add_cm(int64_t N, int mult, int dim, const float* __restrict__ x, const 
 // Its backward for grad_out g (node-major): grad_y (component-major) =
 // scale[0] g (NULL: not formed) and per-workgroup float64 partials of sum g y.
 __global__ void __launch_bounds__(64 * kWaves)
-k_scale_add_cm_bwd(int64_t N, int mult, int dim, const float* __restrict__ g, const float* __restrict__ y,
-                   const float* __restrict__ scale, float* __restrict__ gy, double* __restrict__ part) {
-    __shared__ float lds[kWaves * kStageRow];
+k_scale_add_cm_bwd(int64_t N, int mult, int dim, int vec, const float* __restrict__ g,
+                   const float* __restrict__ y, const float* __restrict__ scale, float* __restrict__ gy,
+                   double* __restrict__ part) {
+    __shared__ __align__(16) float lds[kWaves * kStageRow];
     __shared__ double red[kWaves];
     const int lane = threadIdx.x & 63;
     float* sg = lds + (threadIdx.x >> 6) * kStageRow;
@@ -429,15 +547,29 @@ k_scale_add_cm_bwd(int64_t N, int mult, int dim, const float* __restrict__ g, co
     const int64_t nw = static_cast<int64_t>(gridDim.x) * kWaves;
     double acc = 0.0;
     for (int64_t n = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6); n < N; n += nw) {
-        row_copy(sg, g + n * row, row, lane);
+        row_copy(sg, g + n * row, row, lane, vec);
         wave_sync();
-        for (int d = 0; d < dim; ++d)
-            for (int c = lane; c < mult; c += 64) {
-                const float v = sg[c * dim + d];
-                const int64_t o = (d * N + n) * mult + c;
-                if (gy) gy[o] = sc * v;
-                acc += static_cast<double>(v) * y[o];
+        if (vec) {
+            const int m4 = mult >> 2;
+            for (int q = lane; q < dim * m4; q += 64) {
+                const int d = q / m4, c = 4 * (q - d * m4);
+                const float4 v = make_float4(sg[c * dim + d], sg[(c + 1) * dim + d], sg[(c + 2) * dim + d],
+                                             sg[(c + 3) * dim + d]);
+                const int64_t o4 = ((d * N + n) * mult + c) >> 2;
+                if (gy) reinterpret_cast<float4*>(gy)[o4] = make_float4(sc * v.x, sc * v.y, sc * v.z, sc * v.w);
+                const float4 w = reinterpret_cast<const float4*>(y)[o4];
+                acc += (static_cast<double>(v.x) * w.x + static_cast<double>(v.y) * w.y) +
+                       (static_cast<double>(v.z) * w.z + static_cast<double>(v.w) * w.w);
             }
+        } else {
+            for (int d = 0; d < dim; ++d)
+                for (int c = lane; c < mult; c += 64) {
+                    const float v = sg[c * dim + d];
+                    const int64_t o = (d * N + n) * mult + c;
+                    if (gy) gy[o] = sc * v;
+                    acc += static_cast<double>(v) * y[o];
+                }
+        }
         wave_sync();
     }
     acc = wave_sum(acc);
@@ -464,19 +596,19 @@ k_sum_f64(const double* __restrict__ part, int n, float* __restrict__ out) {
 // y = x ln_c / (n_c + eps), or x / (n_c + eps) without weights (one channel).
 
 // CMO (with STAGE): y component-major (dim, N, mult), as the separable norm's.
-template <int CPL, bool STAGE, bool CMO = false>
+template <int CPL, bool STAGE, bool CMO = false, bool VEC = false>
 __global__ void __launch_bounds__(64 * kWaves)
 k_eqnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __restrict__ w,
              const float* __restrict__ b, float eps, float ln_eps, float* __restrict__ y) {
     static_assert(STAGE || !CMO, "component-major output goes through the LDS stage");
-    __shared__ float lds[STAGE ? kWaves * kStageRow : 1];
+    __shared__ __align__(16) float lds[STAGE ? kWaves * kStageRow : 1];
     const int lane = threadIdx.x & 63;
     const int64_t n = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
     if (n >= N) return;
     const int64_t row = static_cast<int64_t>(L.mult) * L.dim;
     float* sx = lds + (threadIdx.x >> 6) * kStageRow;
     if (STAGE) {
-        row_copy(sx, x + n * row, row, lane);
+        row_copy(sx, x + n * row, row, lane, VEC);
         wave_sync();
     }
     const float* xn = STAGE ? sx : x + n * row;
@@ -519,10 +651,9 @@ k_eqnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __res
     if (STAGE) {
         wave_sync();
         if constexpr (CMO) {
-            for (int d = 0; d < L.dim; ++d)
-                for (int c = lane; c < L.mult; c += 64) y[(d * N + n) * L.mult + c] = sx[c * L.dim + d];
+            row_to_cm(y, sx, N, n, L.mult, L.dim, lane, VEC);
         } else {
-            row_copy(y + n * row, sx, row, lane);
+            row_copy(y + n * row, sx, row, lane, VEC);
         }
     }
 }
@@ -532,7 +663,7 @@ k_eqnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __res
 // dnh = dln w, nh = (n - mu) rstd; gx = gy fac + x dn / n.
 // Per-wave partials of sum dln nh (pW) and sum dln (pB), per channel.
 // CMG (with STAGE): gy component-major (dim, N, mult); x and gx node-major.
-template <int CPL, bool STAGE, bool CMG = false>
+template <int CPL, bool STAGE, bool CMG = false, bool VEC = false>
 __global__ void __launch_bounds__(64 * kWaves)
 k_eqnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __restrict__ x,
              const float* __restrict__ w, const float* __restrict__ b, float eps, float ln_eps,
@@ -546,23 +677,23 @@ k_eqnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __re
     float aW[CPL], aB[CPL];
 #pragma unroll
     for (int i = 0; i < CPL; ++i) aW[i] = aB[i] = 0.0f;
-    __shared__ float lds[STAGE ? 2 * kWaves * kStageRow : 1];
+    __shared__ __align__(16) float lds[STAGE ? 2 * kWaves * kStageRow : 1];
     float* sx = lds + (threadIdx.x >> 6) * 2 * kStageRow;
     float* sg = sx + kStageRow;
     RowPrefetch pf;
     if (STAGE) {
-        if constexpr (CMG) pf.load_cm(x, gy, wave, N, row, L.mult, lane);
-        else pf.load(x, gy, wave, N, row, lane);
+        if constexpr (CMG) pf.load_cm(x, gy, wave, N, row, L.mult, lane, VEC);
+        else pf.load(x, gy, wave, N, row, lane, VEC);
     }
     for (int64_t n = wave; n < N; n += nw) {
         if (STAGE) {
             wave_sync();  // the previous node's stores have read sg
             if constexpr (CMG) {
-                pf.store_cm(sx, sg, row, L.mult, L.dim, lane);
-                pf.load_cm(x, gy, n + nw, N, row, L.mult, lane);   // in flight during this node
+                pf.store_cm(sx, sg, row, L.mult, L.dim, lane, VEC);
+                pf.load_cm(x, gy, n + nw, N, row, L.mult, lane, VEC);   // in flight during this node
             } else {
-                pf.store(sx, sg, row, lane);
-                pf.load(x, gy, n + nw, N, row, lane);
+                pf.store(sx, sg, row, lane, VEC);
+                pf.load(x, gy, n + nw, N, row, lane, VEC);
             }
             wave_sync();
         }
@@ -643,7 +774,7 @@ k_eqnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __re
         }
         if (STAGE) {
             wave_sync();
-            row_copy(gx + n * row, sg, row, lane);
+            row_copy(gx + n * row, sg, row, lane, VEC);
         }
     }
     if (!pW) return;
@@ -843,6 +974,15 @@ using namespace feq;
         case 2: { constexpr int cpl = 2; __VA_ARGS__; } break; \
         default: { constexpr int cpl = 4; __VA_ARGS__; } break; \
     }
+// whether node rows move with 16-byte accesses
+#define FEQ_VEC_DISPATCH(COND_, ...)                           \
+    if (COND_) {                                               \
+        constexpr bool vec = true;                             \
+        __VA_ARGS__;                                           \
+    } else {                                                   \
+        constexpr bool vec = false;                            \
+        __VA_ARGS__;                                           \
+    }
 // channels per lane and whether a node row is staged in LDS
 #define FEQ_NODE_DISPATCH(L_, ...)                                                        \
     if (int64_t(L_.mult) * L_.dim <= kStageRow) {                                         \
@@ -862,22 +1002,23 @@ int sepnorm_fwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, co
     if (L.ns > kMaxS) return fail(FEQ_ERR_UNSUPPORTED, "at most %d scalar irreps", kMaxS);
     if (int rc = check_rows(N, x, y, x)) return rc;
     if ((L.ns && (!w_s || !b_s)) || (L.nhc && !w_h)) return fail(FEQ_ERR_INVALID, "NULL norm weight");
+    L.vec = L.vec && al16(x) && al16(y);
     if (cm && int64_t(L.mult) * L.dim > kStageRow)
         return fail(FEQ_ERR_UNSUPPORTED, "component-major norm output: at most %d floats per node", kStageRow);
     if (N == 0) return FEQ_OK;
     hipStream_t s = stream_of(stream);
     const dim3 grid(static_cast<unsigned>(ceil_div(N, kWaves)));
     if (cm) {
-        FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
-            auto k = k_sepnorm_fwd<cpl, true, true>;
+        FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
+            auto k = k_sepnorm_fwd<cpl, true, true, vec>;
             FEQ_LAUNCH("k_sepnorm_fwd", k, grid, dim3(64 * kWaves), 0, s, L, N, x, w_s, b_s, w_h, eps, y);
-        })
+        }))
         return FEQ_OK;
     }
-    FEQ_NODE_DISPATCH(L, {
-        auto k = k_sepnorm_fwd<cpl, stage>;
+    FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH(L, {
+        auto k = k_sepnorm_fwd<cpl, stage, false, stage && vec>;
         FEQ_LAUNCH("k_sepnorm_fwd", k, grid, dim3(64 * kWaves), 0, s, L, N, x, w_s, b_s, w_h, eps, y);
-    })
+    }))
     return FEQ_OK;
 }
 }  // namespace
@@ -913,6 +1054,7 @@ int sepnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, co
     if (int rc = check_rows(N, gy, x, gx)) return rc;
     if ((L.ns && (!w_s || !gw_s || !gb_s)) || (L.nhc && (!w_h || !gw_h)))
         return fail(FEQ_ERR_INVALID, "NULL norm weight or gradient");
+    L.vec = L.vec && al16(gy) && al16(x) && al16(gx);
     hipStream_t s = stream_of(stream);
     const int64_t nsc = int64_t(mult) * L.ns;
     if (N == 0) {
@@ -931,17 +1073,17 @@ int sepnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, co
     float* pB = pS + partial_floats(w, nsc);
     float* pH = pB + partial_floats(w, nsc);
     if (cm) {
-        FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
-            auto k = k_sepnorm_bwd<cpl, true, true>;
+        FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
+            auto k = k_sepnorm_bwd<cpl, true, true, vec>;
             FEQ_LAUNCH("k_sepnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
                        s, L, N, gy, x, w_s, w_h, eps, gx, pS, pB, L.nhc ? pH : nullptr);
-        })
+        }))
     } else {
-        FEQ_NODE_DISPATCH(L, {
-            auto k = k_sepnorm_bwd<cpl, stage>;
+        FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH(L, {
+            auto k = k_sepnorm_bwd<cpl, stage, false, stage && vec>;
             FEQ_LAUNCH("k_sepnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
                        s, L, N, gy, x, w_s, w_h, eps, gx, pS, pB, L.nhc ? pH : nullptr);
-        })
+        }))
     }
     if (L.ns) {
         if (int rc = reduce_partials(pS, int(w), nsc, gw_s, pS + w * nsc, s)) return rc;
@@ -977,22 +1119,23 @@ int eqnorm_fwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, con
     if (int rc = make_nodel(lvals, nreps, mult, &L)) return rc;
     if (int rc = check_rows(N, x, y, x)) return rc;
     if (!w_ln != !b_ln) return fail(FEQ_ERR_INVALID, "LayerNorm weight and bias go together");
+    L.vec = L.vec && al16(x) && al16(y);
     if (cm && int64_t(L.mult) * L.dim > kStageRow)
         return fail(FEQ_ERR_UNSUPPORTED, "component-major norm output: at most %d floats per node", kStageRow);
     if (N == 0) return FEQ_OK;
     hipStream_t s = stream_of(stream);
     const dim3 grid(static_cast<unsigned>(ceil_div(N, kWaves)));
     if (cm) {
-        FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
-            auto k = k_eqnorm_fwd<cpl, true, true>;
+        FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
+            auto k = k_eqnorm_fwd<cpl, true, true, vec>;
             FEQ_LAUNCH("k_eqnorm_fwd", k, grid, dim3(64 * kWaves), 0, s, L, N, x, w_ln, b_ln, eps, ln_eps, y);
-        })
+        }))
         return FEQ_OK;
     }
-    FEQ_NODE_DISPATCH(L, {
-        auto k = k_eqnorm_fwd<cpl, stage>;
+    FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH(L, {
+        auto k = k_eqnorm_fwd<cpl, stage, false, stage && vec>;
         FEQ_LAUNCH("k_eqnorm_fwd", k, grid, dim3(64 * kWaves), 0, s, L, N, x, w_ln, b_ln, eps, ln_eps, y);
-    })
+    }))
     return FEQ_OK;
 }
 }  // namespace
@@ -1025,6 +1168,7 @@ int eqnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, con
         return fail(FEQ_ERR_UNSUPPORTED, "component-major norm gradient: at most %d floats per node", kStageRow);
     if (int rc = check_rows(N, gy, x, gx)) return rc;
     if (!w_ln != !b_ln) return fail(FEQ_ERR_INVALID, "LayerNorm weight and bias go together");
+    L.vec = L.vec && al16(gy) && al16(x) && al16(gx);
     if (w_ln && (!gw_ln || !gb_ln)) return fail(FEQ_ERR_INVALID, "NULL LayerNorm gradient");
     hipStream_t s = stream_of(stream);
     if (N == 0) {
@@ -1038,17 +1182,17 @@ int eqnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, con
     float* pW = w_ln ? static_cast<float*>(ws) : nullptr;
     float* pB = w_ln ? pW + partial_floats(w, mult) : nullptr;
     if (cm) {
-        FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
-            auto k = k_eqnorm_bwd<cpl, true, true>;
+        FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
+            auto k = k_eqnorm_bwd<cpl, true, true, vec>;
             FEQ_LAUNCH("k_eqnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
                        s, L, N, gy, x, w_ln, b_ln, eps, ln_eps, gx, pW, pB);
-        })
+        }))
     } else {
-        FEQ_NODE_DISPATCH(L, {
-            auto k = k_eqnorm_bwd<cpl, stage>;
+        FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH(L, {
+            auto k = k_eqnorm_bwd<cpl, stage, false, stage && vec>;
             FEQ_LAUNCH("k_eqnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
                        s, L, N, gy, x, w_ln, b_ln, eps, ln_eps, gx, pW, pB);
-        })
+        }))
     }
     if (!w_ln) return FEQ_OK;
     if (int rc = reduce_partials(pW, int(w), mult, gw_ln, pW + w * mult, s)) return rc;
@@ -1143,8 +1287,9 @@ extern "C" int feq_scale_add_cm(const float* x, const float* y, const float* sca
     if (N == 0) return FEQ_OK;
     if (!x || !y || !scale || !out) return fail(FEQ_ERR_INVALID, "NULL pointer");
     const int64_t g = ceil_div(N, kWaves);
+    const int vec = mult % 4 == 0 && al16(x) && al16(y) && al16(out);
     FEQ_LAUNCH("k_scale_add_cm", k_scale_add_cm, dim3(static_cast<unsigned>(g < kResGroups ? g : kResGroups)),
-               dim3(64 * kWaves), 0, stream_of(stream), N, int(mult), int(dim), x, y, scale, out);
+               dim3(64 * kWaves), 0, stream_of(stream), N, int(mult), int(dim), vec, x, y, scale, out);
     return FEQ_OK;
 }
 
@@ -1160,8 +1305,9 @@ extern "C" int feq_scale_add_cm_bwd(const float* grad_out, const float* y, const
         return fail(FEQ_ERR_WORKSPACE, "residual workspace too small");
     hipStream_t s = stream_of(stream);
     double* part = static_cast<double*>(ws);
+    const int vec = mult % 4 == 0 && al16(grad_out) && al16(y) && al16(grad_y);
     FEQ_LAUNCH("k_scale_add_cm_bwd", k_scale_add_cm_bwd, dim3(kResGroups), dim3(64 * kWaves), 0, s, N, int(mult),
-               int(dim), grad_out, y, scale, grad_y, part);
+               int(dim), vec, grad_out, y, scale, grad_y, part);
     if (grad_scale) FEQ_LAUNCH("k_sum_f64", k_sum_f64, dim3(1), dim3(64 * kWaves), 0, s, part, kResGroups, grad_scale);
     return FEQ_OK;
 }
