@@ -362,6 +362,37 @@ k_sum_partials_small(const float* __restrict__ part, int groups, int64_t n, floa
 
 constexpr int64_t kSmallN = 256;
 
+// k_sum_partials_small over several jobs: workgroup b sums output b - start[j]
+// of the job j whose range [start[j], start[j + 1]) holds b.
+struct PartialJobs {
+    const float* part[kMaxPartialJobs];
+    float* out[kMaxPartialJobs];
+    int64_t n[kMaxPartialJobs];
+    int groups[kMaxPartialJobs];
+    int64_t start[kMaxPartialJobs + 1];
+    int count;
+};
+
+__global__ void __launch_bounds__(256)
+k_sum_partials_multi(PartialJobs J) {
+    __shared__ float s[256];
+    const int64_t b = blockIdx.x;
+    int j = 0;
+    while (j + 1 < J.count && b >= J.start[j + 1]) ++j;
+    const int64_t q = b - J.start[j], n = J.n[j];
+    const float* part = J.part[j];
+    const int groups = J.groups[j];
+    float acc = 0.0f;
+    for (int g = threadIdx.x; g < groups; g += 256) acc += part[static_cast<int64_t>(g) * n + q];
+    s[threadIdx.x] = acc;
+    __syncthreads();
+    for (int h = 128; h > 0; h >>= 1) {
+        if (threadIdx.x < h) s[threadIdx.x] += s[threadIdx.x + h];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) J.out[j][q] = s[0];
+}
+
 constexpr int kSliceGroups = 32;   // partials summed per thread in one pass
 
 size_t reduce_tmp_floats(int groups, int64_t n) {
@@ -392,6 +423,32 @@ int reduce_partials(const float* part, int groups, int64_t n, float* out, float*
                kSliceGroups, n, tmp);
     FEQ_LAUNCH("k_sum_partials", k_sum_partials, dim3(nb, 1), dim3(256), 0, s, tmp, slices, slices,
                n, out);
+    return FEQ_OK;
+}
+
+int reduce_partials_multi(const PartialJob* jobs, int njobs, hipStream_t s) {
+    if (njobs < 1) return FEQ_OK;
+    bool small = njobs <= kMaxPartialJobs;
+    for (int j = 0; j < njobs && small; ++j) small = jobs[j].n <= kSmallN && jobs[j].groups > kSliceGroups;
+    if (!small) {
+        for (int j = 0; j < njobs; ++j)
+            if (int rc = reduce_partials(jobs[j].part, jobs[j].groups, jobs[j].n, jobs[j].out, jobs[j].tmp, s))
+                return rc;
+        return FEQ_OK;
+    }
+    PartialJobs J{};
+    J.count = njobs;
+    J.start[0] = 0;
+    for (int j = 0; j < njobs; ++j) {
+        J.part[j] = jobs[j].part;
+        J.out[j] = jobs[j].out;
+        J.n[j] = jobs[j].n;
+        J.groups[j] = jobs[j].groups;
+        J.start[j + 1] = J.start[j] + jobs[j].n;
+    }
+    if (J.start[njobs] == 0) return FEQ_OK;
+    FEQ_LAUNCH("k_sum_partials", k_sum_partials_multi, dim3(static_cast<unsigned>(J.start[njobs])), dim3(256), 0,
+               s, J);
     return FEQ_OK;
 }
 

@@ -75,6 +75,19 @@ int fill_zero(float* p, int64_t n, hipStream_t s);
 int reduce_partials(const float* part, int groups, int64_t n, float* out, float* tmp,
                     hipStream_t s);
 
+// Several reduce_partials in one launch when each is a few sums of many
+// partials (n <= 256, groups > 32; otherwise one call each), with the same
+// summation order, so the results are bitwise those of separate calls.
+struct PartialJob {
+    const float* part;
+    int groups;
+    int64_t n;
+    float* out;
+    float* tmp;
+};
+constexpr int kMaxPartialJobs = 4;
+int reduce_partials_multi(const PartialJob* jobs, int njobs, hipStream_t s);
+
 // `tail` holds ew_tail_floats(...) floats of workspace.  groups = 0: no dC partials.
 bool ew_tail_supported(const feq_binning& B, int kw);
 size_t ew_tail_floats(const feq_binning& B, int kw, int64_t E, int groups, int64_t ncc);

@@ -894,55 +894,172 @@ k_gate_bwd_x(NodeL L, int64_t rows, const float* __restrict__ gy, const float* _
 
 // Component-major tables (dim, N, mult): element (p, d) of pair p = (node,
 // channel) sits at d * P + p, so consecutive threads read consecutive floats.
+// The per-pair values (norms, gate inputs and their gradients) are (P, nreps).
+// W = 4 (with NR = nreps): each thread takes four consecutive pairs with
+// 16-byte accesses (P a multiple of 4, the tables 16-byte aligned), its 4 NR
+// per-pair values as NR float4s, four independent sums per load.  W = 1: one
+// pair per thread, any nreps (NR = 0: read from L).
 
-__global__ void __launch_bounds__(kRowThreads)
-k_gate_norms_cm(NodeL L, int64_t P, const float* __restrict__ x, float eps, float* __restrict__ nrm) {
-    const int64_t p = static_cast<int64_t>(blockIdx.x) * kRowThreads + threadIdx.x;
-    if (p >= P) return;
-    for (int k = 0; k < L.nreps; ++k) {
-        float q = 0.0f;
-        for (int d = L.off[k]; d < L.off[k + 1]; ++d) q += x[d * P + p] * x[d * P + p];
-        nrm[p * L.nreps + k] = sqrtf(q + eps);
+template <int W>
+__device__ __forceinline__ void ld_w(const float* __restrict__ s, float (&v)[W]) {
+    if constexpr (W == 4) {
+        const float4 f = *reinterpret_cast<const float4*>(s);
+        v[0] = f.x;
+        v[1] = f.y;
+        v[2] = f.z;
+        v[3] = f.w;
+    } else {
+        v[0] = *s;
     }
 }
+template <int W>
+__device__ __forceinline__ void st_w(float* __restrict__ d, const float (&v)[W]) {
+    if constexpr (W == 4) *reinterpret_cast<float4*>(d) = make_float4(v[0], v[1], v[2], v[3]);
+    else *d = v[0];
+}
+// the W * nr per-pair values of the thread's pairs p .. p + W - 1 (contiguous)
+template <int W, int NRS>
+__device__ __forceinline__ void ld_pairs(const float* __restrict__ s, int64_t p, int nr, float (&v)[W * NRS]) {
+    if constexpr (W == 4) {
+#pragma unroll
+        for (int q = 0; q < NRS; ++q) {
+            float t[4];
+            ld_w<4>(s + p * NRS + 4 * q, t);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[4 * q + j] = t[j];
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < NRS; ++k) v[k] = k < nr ? s[p * nr + k] : 0.0f;
+    }
+}
+template <int W, int NRS>
+__device__ __forceinline__ void st_pairs(float* __restrict__ d, int64_t p, int nr, const float (&v)[W * NRS]) {
+    if constexpr (W == 4) {
+#pragma unroll
+        for (int q = 0; q < NRS; ++q) {
+            const float t[4] = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+            st_w<4>(d + p * NRS + 4 * q, t);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < NRS; ++k)
+            if (k < nr) d[p * nr + k] = v[k];
+    }
+}
+// per-pair value of pair w, irrep k
+template <int W, int NRS>
+__device__ __forceinline__ int pv(int w, int k) { return W == 4 ? w * NRS + k : k; }
 
+// NRS: the per-pair register rows (NR, or FEQ_MAX_IRREPS for W = 1)
+#define FEQ_GATE_CM_HEAD                                                                   \
+    constexpr int NRS = W == 4 ? NR : FEQ_MAX_IRREPS;                                       \
+    const int nr = W == 4 ? NR : L.nreps;                                                   \
+    const int64_t p = (static_cast<int64_t>(blockIdx.x) * kRowThreads + threadIdx.x) * W;  \
+    if (p >= P) return;
+
+template <int W, int NR>
+__global__ void __launch_bounds__(kRowThreads)
+k_gate_norms_cm(NodeL L, int64_t P, const float* __restrict__ x, float eps, float* __restrict__ nrm) {
+    FEQ_GATE_CM_HEAD
+    float out[W * NRS];
+#pragma unroll
+    for (int k = 0; k < NRS; ++k) {
+        if (k >= nr) break;
+        float q[W] = {};
+        for (int d = L.off[k]; d < L.off[k + 1]; ++d) {
+            float v[W];
+            ld_w<W>(x + d * P + p, v);
+#pragma unroll
+            for (int w = 0; w < W; ++w) q[w] += v[w] * v[w];
+        }
+#pragma unroll
+        for (int w = 0; w < W; ++w) out[pv<W, NRS>(w, k)] = sqrtf(q[w] + eps);
+    }
+    st_pairs<W, NRS>(nrm, p, nr, out);
+}
+
+template <int W, int NR>
 __global__ void __launch_bounds__(kRowThreads)
 k_gate_apply_cm(NodeL L, int64_t P, const float* __restrict__ x, const float* __restrict__ lin,
                 float* __restrict__ y) {
-    const int64_t p = static_cast<int64_t>(blockIdx.x) * kRowThreads + threadIdx.x;
-    if (p >= P) return;
-    for (int k = 0; k < L.nreps; ++k) {
-        const float g = sigmoidf(lin[p * L.nreps + k]);
-        for (int d = L.off[k]; d < L.off[k + 1]; ++d) y[d * P + p] = x[d * P + p] * g;
+    FEQ_GATE_CM_HEAD
+    float lv[W * NRS];
+    ld_pairs<W, NRS>(lin, p, nr, lv);
+#pragma unroll
+    for (int k = 0; k < NRS; ++k) {
+        if (k >= nr) break;
+        float g[W];
+#pragma unroll
+        for (int w = 0; w < W; ++w) g[w] = sigmoidf(lv[pv<W, NRS>(w, k)]);
+        for (int d = L.off[k]; d < L.off[k + 1]; ++d) {
+            float v[W];
+            ld_w<W>(x + d * P + p, v);
+#pragma unroll
+            for (int w = 0; w < W; ++w) v[w] *= g[w];
+            st_w<W>(y + d * P + p, v);
+        }
     }
 }
 
+template <int W, int NR>
 __global__ void __launch_bounds__(kRowThreads)
 k_gate_bwd_lin_cm(NodeL L, int64_t P, const float* __restrict__ gy, const float* __restrict__ x,
                   const float* __restrict__ lin, float* __restrict__ dlin) {
-    const int64_t p = static_cast<int64_t>(blockIdx.x) * kRowThreads + threadIdx.x;
-    if (p >= P) return;
-    for (int k = 0; k < L.nreps; ++k) {
-        float q = 0.0f;
-        for (int d = L.off[k]; d < L.off[k + 1]; ++d) q += gy[d * P + p] * x[d * P + p];
-        const float g = sigmoidf(lin[p * L.nreps + k]);
-        dlin[p * L.nreps + k] = q * (g * (1.0f - g));
+    FEQ_GATE_CM_HEAD
+    float lv[W * NRS];
+    ld_pairs<W, NRS>(lin, p, nr, lv);
+#pragma unroll
+    for (int k = 0; k < NRS; ++k) {
+        if (k >= nr) break;
+        float q[W] = {};
+        for (int d = L.off[k]; d < L.off[k + 1]; ++d) {
+            float a[W], v[W];
+            ld_w<W>(gy + d * P + p, a);
+            ld_w<W>(x + d * P + p, v);
+#pragma unroll
+            for (int w = 0; w < W; ++w) q[w] += a[w] * v[w];
+        }
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const float g = sigmoidf(lv[pv<W, NRS>(w, k)]);
+            lv[pv<W, NRS>(w, k)] = q[w] * (g * (1.0f - g));
+        }
     }
+    st_pairs<W, NRS>(dlin, p, nr, lv);
 }
 
+template <int W, int NR>
 __global__ void __launch_bounds__(kRowThreads)
 k_gate_bwd_x_cm(NodeL L, int64_t P, const float* __restrict__ gy, const float* __restrict__ x,
                 const float* __restrict__ lin, const float* __restrict__ nrm,
                 const float* __restrict__ dnrm, float* __restrict__ gx) {
-    const int64_t p = static_cast<int64_t>(blockIdx.x) * kRowThreads + threadIdx.x;
-    if (p >= P) return;
-    for (int k = 0; k < L.nreps; ++k) {
-        const int64_t i = p * L.nreps + k;
-        const float g = sigmoidf(lin[i]);
-        const float q = dnrm[i] / nrm[i];
-        for (int d = L.off[k]; d < L.off[k + 1]; ++d) gx[d * P + p] = gy[d * P + p] * g + x[d * P + p] * q;
+    FEQ_GATE_CM_HEAD
+    float lv[W * NRS], nv[W * NRS], dv[W * NRS];
+    ld_pairs<W, NRS>(lin, p, nr, lv);
+    ld_pairs<W, NRS>(nrm, p, nr, nv);
+    ld_pairs<W, NRS>(dnrm, p, nr, dv);
+#pragma unroll
+    for (int k = 0; k < NRS; ++k) {
+        if (k >= nr) break;
+        float g[W], q[W];
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const int i = pv<W, NRS>(w, k);
+            g[w] = sigmoidf(lv[i]);
+            q[w] = dv[i] / nv[i];
+        }
+        for (int d = L.off[k]; d < L.off[k + 1]; ++d) {
+            float a[W], v[W];
+            ld_w<W>(gy + d * P + p, a);
+            ld_w<W>(x + d * P + p, v);
+#pragma unroll
+            for (int w = 0; w < W; ++w) a[w] = a[w] * g[w] + v[w] * q[w];
+            st_w<W>(gx + d * P + p, a);
+        }
     }
 }
+#undef FEQ_GATE_CM_HEAD
 
 // ---- host ---------------------------------------------------------------------
 
@@ -1085,13 +1202,14 @@ int sepnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, co
                        s, L, N, gy, x, w_s, w_h, eps, gx, pS, pB, L.nhc ? pH : nullptr);
         }))
     }
+    PartialJob jobs[3];
+    int nj = 0;
     if (L.ns) {
-        if (int rc = reduce_partials(pS, int(w), nsc, gw_s, pS + w * nsc, s)) return rc;
-        if (int rc = reduce_partials(pB, int(w), nsc, gb_s, pB + w * nsc, s)) return rc;
+        jobs[nj++] = PartialJob{pS, int(w), nsc, gw_s, pS + w * nsc};
+        jobs[nj++] = PartialJob{pB, int(w), nsc, gb_s, pB + w * nsc};
     }
-    if (L.nhc)
-        if (int rc = reduce_partials(pH, int(w), mult, gw_h, pH + w * mult, s)) return rc;
-    return FEQ_OK;
+    if (L.nhc) jobs[nj++] = PartialJob{pH, int(w), mult, gw_h, pH + w * mult};
+    return reduce_partials_multi(jobs, nj, s);
 }
 }  // namespace
 
@@ -1195,8 +1313,9 @@ int eqnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, con
         }))
     }
     if (!w_ln) return FEQ_OK;
-    if (int rc = reduce_partials(pW, int(w), mult, gw_ln, pW + w * mult, s)) return rc;
-    return reduce_partials(pB, int(w), mult, gb_ln, pB + w * mult, s);
+    const PartialJob jobs[2] = {PartialJob{pW, int(w), mult, gw_ln, pW + w * mult},
+                                PartialJob{pB, int(w), mult, gb_ln, pB + w * mult}};
+    return reduce_partials_multi(jobs, 2, s);
 }
 }  // namespace
 
@@ -1216,23 +1335,27 @@ extern "C" int feq_eqnorm_bwd_cm(const int32_t* lvals, int32_t nreps, int32_t mu
                       true, stream);
 }
 
-#define FEQ_GATE_PRELUDE(a, b, c)                                                         \
+// v4: the component-major kernels' 16-byte form (four pairs per thread)
+#define FEQ_GATE_PRELUDE(a, b, c, d)                                                      \
     NodeL L;                                                                              \
     if (int rc = make_nodel(lvals, nreps, mult, &L)) return rc;                           \
     if (int rc = check_rows(N, a, b, c)) return rc;                                       \
     if (N == 0) return FEQ_OK;                                                            \
     const int64_t rows = N * mult;                                                        \
+    const bool v4 = cm && mult % 4 == 0 && nreps <= 4 && al16(a) && al16(b) && al16(c) && al16(d);  \
     const dim3 grid(static_cast<unsigned>(                                                \
-        ceil_div(rows, cm ? kRowThreads : std::min(kRowThreads, kTileFloats / L.dim))));  \
+        ceil_div(rows, cm ? kRowThreads * (v4 ? 4 : 1) : std::min(kRowThreads, kTileFloats / L.dim))));  \
     hipStream_t s = stream_of(stream);
 
 extern "C" int feq_gate_norms(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
                               int32_t cm, const float* x, float eps, float* norms,
                               feq_stream_t stream) {
-    FEQ_GATE_PRELUDE(x, norms, x)
-    if (cm)
-        FEQ_LAUNCH("k_gate_norms", k_gate_norms_cm, grid, dim3(kRowThreads), 0, s, L, rows, x, eps, norms);
-    else
+    FEQ_GATE_PRELUDE(x, norms, x, x)
+    if (cm) {
+        auto k = !v4 ? k_gate_norms_cm<1, 0> : nreps == 1 ? k_gate_norms_cm<4, 1> : nreps == 2 ? k_gate_norms_cm<4, 2>
+                 : nreps == 3 ? k_gate_norms_cm<4, 3> : k_gate_norms_cm<4, 4>;
+        FEQ_LAUNCH("k_gate_norms", k, grid, dim3(kRowThreads), 0, s, L, rows, x, eps, norms);
+    } else
         FEQ_LAUNCH("k_gate_norms", k_gate_norms, grid, dim3(kRowThreads), 0, s, L, rows, x, eps, norms);
     return FEQ_OK;
 }
@@ -1240,10 +1363,12 @@ extern "C" int feq_gate_norms(const int32_t* lvals, int32_t nreps, int32_t mult,
 extern "C" int feq_gate_apply(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
                               int32_t cm, const float* x, const float* lin, float* y,
                               feq_stream_t stream) {
-    FEQ_GATE_PRELUDE(x, lin, y)
-    if (cm)
-        FEQ_LAUNCH("k_gate_apply", k_gate_apply_cm, grid, dim3(kRowThreads), 0, s, L, rows, x, lin, y);
-    else
+    FEQ_GATE_PRELUDE(x, lin, y, y)
+    if (cm) {
+        auto k = !v4 ? k_gate_apply_cm<1, 0> : nreps == 1 ? k_gate_apply_cm<4, 1> : nreps == 2 ? k_gate_apply_cm<4, 2>
+                 : nreps == 3 ? k_gate_apply_cm<4, 3> : k_gate_apply_cm<4, 4>;
+        FEQ_LAUNCH("k_gate_apply", k, grid, dim3(kRowThreads), 0, s, L, rows, x, lin, y);
+    } else
         FEQ_LAUNCH("k_gate_apply", k_gate_apply, grid, dim3(kRowThreads), 0, s, L, rows, x, lin, y);
     return FEQ_OK;
 }
@@ -1251,12 +1376,13 @@ extern "C" int feq_gate_apply(const int32_t* lvals, int32_t nreps, int32_t mult,
 extern "C" int feq_gate_bwd_lin(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
                                 int32_t cm, const float* gy, const float* x, const float* lin,
                                 float* grad_lin, feq_stream_t stream) {
-    FEQ_GATE_PRELUDE(gy, x, lin)
+    FEQ_GATE_PRELUDE(gy, x, lin, grad_lin)
     if (!grad_lin) return fail(FEQ_ERR_INVALID, "NULL tensor pointer");
-    if (cm)
-        FEQ_LAUNCH("k_gate_bwd_lin", k_gate_bwd_lin_cm, grid, dim3(kRowThreads), 0, s, L, rows, gy, x,
-                   lin, grad_lin);
-    else
+    if (cm) {
+        auto k = !v4 ? k_gate_bwd_lin_cm<1, 0> : nreps == 1 ? k_gate_bwd_lin_cm<4, 1> : nreps == 2 ? k_gate_bwd_lin_cm<4, 2>
+                 : nreps == 3 ? k_gate_bwd_lin_cm<4, 3> : k_gate_bwd_lin_cm<4, 4>;
+        FEQ_LAUNCH("k_gate_bwd_lin", k, grid, dim3(kRowThreads), 0, s, L, rows, gy, x, lin, grad_lin);
+    } else
         FEQ_LAUNCH("k_gate_bwd_lin", k_gate_bwd_lin, grid, dim3(kRowThreads), 0, s, L, rows, gy, x,
                    lin, grad_lin);
     return FEQ_OK;
@@ -1266,12 +1392,14 @@ extern "C" int feq_gate_bwd_x(const int32_t* lvals, int32_t nreps, int32_t mult,
                               int32_t cm, const float* gy, const float* x, const float* lin,
                               const float* norms, const float* grad_norms, float* gx,
                               feq_stream_t stream) {
-    FEQ_GATE_PRELUDE(gy, x, lin)
+    FEQ_GATE_PRELUDE(gy, x, lin, gx)
     if (!norms || !grad_norms || !gx) return fail(FEQ_ERR_INVALID, "NULL tensor pointer");
-    if (cm)
-        FEQ_LAUNCH("k_gate_bwd_x", k_gate_bwd_x_cm, grid, dim3(kRowThreads), 0, s, L, rows, gy, x, lin,
-                   norms, grad_norms, gx);
-    else
+    if (cm) {
+        auto k = !v4 ? k_gate_bwd_x_cm<1, 0> : nreps == 1 ? k_gate_bwd_x_cm<4, 1> : nreps == 2 ? k_gate_bwd_x_cm<4, 2>
+                 : nreps == 3 ? k_gate_bwd_x_cm<4, 3> : k_gate_bwd_x_cm<4, 4>;
+        FEQ_LAUNCH("k_gate_bwd_x", k, grid, dim3(kRowThreads), 0, s, L, rows, gy, x, lin, norms, grad_norms,
+                   gx);
+    } else
         FEQ_LAUNCH("k_gate_bwd_x", k_gate_bwd_x, grid, dim3(kRowThreads), 0, s, L, rows, gy, x, lin,
                    norms, grad_norms, gx);
     return FEQ_OK;

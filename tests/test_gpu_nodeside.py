@@ -168,13 +168,15 @@ def test_equivariant_linear_matches_oracle(dev, lvals, cin, cout):
         assert rel_err(grads["bias"], bias.grad) < TOL
 
 
-def test_component_major_gating_equals_node_major(dev):
-    """The (dim, N, mult) gating kernels give the node-major kernels' results."""
+@pytest.mark.parametrize("lvals,mult,n", [([0, 1, 2], 128, 500), ([1, 2, 0, 1], 100, 333), ([0, 1, 2], 7, 301)])
+def test_component_major_gating_equals_node_major(dev, lvals, mult, n):
+    """The (dim, N, mult) gating kernels give the node-major kernels' results
+    (channel counts a multiple of 4 take the 16-byte form, 7 the 4-byte one)."""
     g = torch.Generator().manual_seed(17)
-    rp = fe.Repr([0, 1, 2], 128)
+    rp = fe.Repr(lvals, mult)
     m = fe.EquivariantGating(rp).to(dev)
-    x = torch.randn(500, 128, 9, generator=g).to(dev)
-    gy = torch.randn(500, 128, 9, generator=g).to(dev)
+    x = torch.randn(n, mult, rp.dim(), generator=g).to(dev)
+    gy = torch.randn(n, mult, rp.dim(), generator=g).to(dev)
     x1 = x.clone().requires_grad_(True)
     y1 = m(x1)
     y1.backward(gy)

@@ -84,9 +84,11 @@ def test_block_uses_the_fused_residuals(dev):
     assert blk.layer_scale_attn.gamma.grad is not None and blk.layer_scale_mlp.gamma.grad is not None
 
 
-def test_component_major_branch_matches_float64(dev):
-    """x (N, mult, dim) + gamma y with y component-major (dim, N, mult)."""
-    N, mult, dim = 1001, 64, 9
+@pytest.mark.parametrize("N,mult", [(1001, 64), (333, 6)])
+def test_component_major_branch_matches_float64(dev, N, mult):
+    """x (N, mult, dim) + gamma y with y component-major (dim, N, mult); 64
+    channels move in 16-byte pieces, 6 in 4-byte ones."""
+    dim = 9
     g = torch.Generator().manual_seed(5)
     x, go = torch.randn(N, mult, dim, generator=g), torch.randn(N, mult, dim, generator=g)
     y = torch.randn(dim, N, mult, generator=g)
@@ -104,18 +106,20 @@ def test_component_major_branch_matches_float64(dev):
     assert abs(gd.grad.item() - gg.item()) <= 1e-6 * (go.double() * yt).abs().sum().item()
 
 
+@pytest.mark.parametrize("mult", [64, 6])
 @pytest.mark.parametrize("kind", ["separable", "equivariant"])
-def test_component_major_norm_output_is_the_transpose(dev, kind):
+def test_component_major_norm_output_is_the_transpose(dev, kind, mult):
     """The separable and the equivariant layer norm with their output (and
-    gradient) component-major: the node-major kernels' values, bit for bit."""
+    gradient) component-major: the node-major kernels' values, bit for bit
+    (16-byte row accesses at 64 channels, 4-byte ones at 6)."""
     torch.manual_seed(1)
     cls = fe.SeparableEquivariantLayerNorm if kind == "separable" else fe.EquivariantLayerNorm
-    norm = cls(fe.Repr([0, 1, 2], 64)).to(dev)
+    norm = cls(fe.Repr([0, 1, 2], mult)).to(dev)
     with torch.no_grad():
         for p in norm.parameters():
             p.normal_()
-    x = torch.randn(777, 64, 9, device=dev)
-    gy = torch.randn(777, 64, 9, device=dev)
+    x = torch.randn(777, mult, 9, device=dev)
+    gy = torch.randn(777, mult, 9, device=dev)
     x1 = x.clone().requires_grad_(True)
     y1 = norm(x1)
     y1.backward(gy)
