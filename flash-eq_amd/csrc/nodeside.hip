@@ -260,6 +260,52 @@ struct RowPrefetch {
     }
 };
 
+// The rows of an addend to the input gradient (a second branch's gradient of
+// the same input, summed here instead of in a separate pass): loaded when a
+// node's computation starts, in flight during it, and added as the node's
+// gradient row is written.  Lane mapping as RowPrefetch.
+struct RowAddend {
+    float a[4 * kRowPer4];
+    template <bool VEC>
+    __device__ __forceinline__ void load(const float* __restrict__ ga, int64_t n, int64_t row, int lane) {
+        if constexpr (VEC) {
+            const float4* a4 = reinterpret_cast<const float4*>(ga + n * row);
+#pragma unroll
+            for (int i = 0; i < kRowPer4; ++i) {
+                const int64_t q = lane + 64 * i;
+                if (4 * q < row) put4(a + 4 * i, a4[q]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kRowPer; ++i) {
+                const int64_t idx = lane + 64 * i;
+                if (idx < row) a[i] = ga[n * row + idx];
+            }
+        }
+    }
+    template <bool VEC>
+    __device__ __forceinline__ void store_sum(float* __restrict__ gx, const float* sg, int64_t n, int64_t row,
+                                              int lane) const {
+        if constexpr (VEC) {
+            float4* g4 = reinterpret_cast<float4*>(gx + n * row);
+#pragma unroll
+            for (int i = 0; i < kRowPer4; ++i) {
+                const int64_t q = lane + 64 * i;
+                if (4 * q < row) {
+                    const float4 v = reinterpret_cast<const float4*>(sg)[q];
+                    g4[q] = make_float4(v.x + a[4 * i], v.y + a[4 * i + 1], v.z + a[4 * i + 2], v.w + a[4 * i + 3]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kRowPer; ++i) {
+                const int64_t idx = lane + 64 * i;
+                if (idx < row) gx[n * row + idx] = sg[idx] + a[i];
+            }
+        }
+    }
+};
+
 __device__ __forceinline__ float sigmoidf(float v) { return 1.0f / (1.0f + expf(-v)); }
 
 // ---- separable layer norm ---------------------------------------------------
@@ -358,13 +404,15 @@ k_sepnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __re
 // Per-wave partials: pS, pB (mult, ns) of gy (v - mu) / den and gy; pH (mult) of
 // sum_d gy v / rms.
 // CMG (with STAGE): gy is component-major (dim, N, mult); x and gx node-major.
-template <int CPL, bool STAGE, bool CMG = false, bool VEC = false>
+// ADD (with STAGE): gx = the norm's input gradient + ga (node-major).
+template <int CPL, bool STAGE, bool CMG = false, bool VEC = false, bool ADD = false>
 __global__ void __launch_bounds__(64 * kWaves)
 k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __restrict__ x,
               const float* __restrict__ ws, const float* __restrict__ wh, float eps,
               float* __restrict__ gx, float* __restrict__ pS, float* __restrict__ pB,
-              float* __restrict__ pH) {
+              float* __restrict__ pH, const float* __restrict__ ga) {
     static_assert(STAGE || !CMG, "component-major gradients go through the LDS stage");
+    static_assert(STAGE || !ADD, "the gradient addend goes through the LDS stage");
     const int lane = threadIdx.x & 63;
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
     const int64_t nw = static_cast<int64_t>(gridDim.x) * kWaves;
@@ -382,6 +430,7 @@ k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __r
     float* sx = lds + (threadIdx.x >> 6) * 2 * kStageRow;
     float* sg = sx + kStageRow;
     RowPrefetch pf;
+    RowAddend ad;
     if (STAGE) {
         if constexpr (CMG) pf.load_cm(x, gy, wave, N, row, L.mult, lane, VEC);
         else pf.load(x, gy, wave, N, row, lane, VEC);
@@ -396,6 +445,7 @@ k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __r
                 pf.store(sx, sg, row, lane, VEC);
                 pf.load(x, gy, n + nw, N, row, lane, VEC);
             }
+            if constexpr (ADD) ad.template load<VEC>(ga, n, row, lane);
             wave_sync();
         }
         const float* xn = STAGE ? sx : x + n * row;
@@ -482,7 +532,8 @@ k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __r
         }
         if (STAGE) {
             wave_sync();
-            row_copy(gx + n * row, sg, row, lane, VEC);
+            if constexpr (ADD) ad.template store_sum<VEC>(gx, sg, n, row, lane);
+            else row_copy(gx + n * row, sg, row, lane, VEC);
         }
     }
 #pragma unroll
@@ -663,11 +714,14 @@ k_eqnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __res
 // dnh = dln w, nh = (n - mu) rstd; gx = gy fac + x dn / n.
 // Per-wave partials of sum dln nh (pW) and sum dln (pB), per channel.
 // CMG (with STAGE): gy component-major (dim, N, mult); x and gx node-major.
-template <int CPL, bool STAGE, bool CMG = false, bool VEC = false>
+// ADD (with STAGE): gx = the norm's input gradient + ga (node-major).
+template <int CPL, bool STAGE, bool CMG = false, bool VEC = false, bool ADD = false>
 __global__ void __launch_bounds__(64 * kWaves)
 k_eqnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __restrict__ x,
              const float* __restrict__ w, const float* __restrict__ b, float eps, float ln_eps,
-             float* __restrict__ gx, float* __restrict__ pW, float* __restrict__ pB) {
+             float* __restrict__ gx, float* __restrict__ pW, float* __restrict__ pB,
+             const float* __restrict__ ga) {
+    static_assert(STAGE || !ADD, "the gradient addend goes through the LDS stage");
     static_assert(STAGE || !CMG, "component-major gradients go through the LDS stage");
     const int lane = threadIdx.x & 63;
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
@@ -681,6 +735,7 @@ k_eqnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __re
     float* sx = lds + (threadIdx.x >> 6) * 2 * kStageRow;
     float* sg = sx + kStageRow;
     RowPrefetch pf;
+    RowAddend ad;
     if (STAGE) {
         if constexpr (CMG) pf.load_cm(x, gy, wave, N, row, L.mult, lane, VEC);
         else pf.load(x, gy, wave, N, row, lane, VEC);
@@ -695,6 +750,7 @@ k_eqnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __re
                 pf.store(sx, sg, row, lane, VEC);
                 pf.load(x, gy, n + nw, N, row, lane, VEC);
             }
+            if constexpr (ADD) ad.template load<VEC>(ga, n, row, lane);
             wave_sync();
         }
         const float* xn = STAGE ? sx : x + n * row;
@@ -774,7 +830,8 @@ k_eqnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __re
         }
         if (STAGE) {
             wave_sync();
-            row_copy(gx + n * row, sg, row, lane, VEC);
+            if constexpr (ADD) ad.template store_sum<VEC>(gx, sg, n, row, lane);
+            else row_copy(gx + n * row, sg, row, lane, VEC);
         }
     }
     if (!pW) return;
@@ -1100,6 +1157,15 @@ using namespace feq;
         constexpr bool vec = false;                            \
         __VA_ARGS__;                                           \
     }
+// whether the input gradient takes an addend
+#define FEQ_ADD_DISPATCH(COND_, ...)                           \
+    if (COND_) {                                               \
+        constexpr bool add = true;                             \
+        __VA_ARGS__;                                           \
+    } else {                                                   \
+        constexpr bool add = false;                            \
+        __VA_ARGS__;                                           \
+    }
 // channels per lane and whether a node row is staged in LDS
 #define FEQ_NODE_DISPATCH(L_, ...)                                                        \
     if (int64_t(L_.mult) * L_.dim <= kStageRow) {                                         \
@@ -1161,17 +1227,20 @@ extern "C" size_t feq_sepnorm_workspace(const int32_t* lvals, int32_t nreps, int
 
 namespace {
 int sepnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, const float* gy,
-                const float* x, const float* w_s, const float* w_h, float eps, float* gx, float* gw_s,
-                float* gb_s, float* gw_h, void* ws, size_t ws_bytes, bool cm, feq_stream_t stream) {
+                const float* x, const float* w_s, const float* w_h, float eps, const float* ga, float* gx,
+                float* gw_s, float* gb_s, float* gw_h, void* ws, size_t ws_bytes, bool cm,
+                feq_stream_t stream) {
     NodeL L;
     if (int rc = make_nodel(lvals, nreps, mult, &L)) return rc;
     if (cm && int64_t(L.mult) * L.dim > kStageRow)
         return fail(FEQ_ERR_UNSUPPORTED, "component-major norm gradient: at most %d floats per node", kStageRow);
+    if (ga && int64_t(L.mult) * L.dim > kStageRow)
+        return fail(FEQ_ERR_UNSUPPORTED, "norm gradient with an addend: at most %d floats per node", kStageRow);
     if (L.ns > kMaxS) return fail(FEQ_ERR_UNSUPPORTED, "at most %d scalar irreps", kMaxS);
     if (int rc = check_rows(N, gy, x, gx)) return rc;
     if ((L.ns && (!w_s || !gw_s || !gb_s)) || (L.nhc && (!w_h || !gw_h)))
         return fail(FEQ_ERR_INVALID, "NULL norm weight or gradient");
-    L.vec = L.vec && al16(gy) && al16(x) && al16(gx);
+    L.vec = L.vec && al16(gy) && al16(x) && al16(gx) && al16(ga);
     hipStream_t s = stream_of(stream);
     const int64_t nsc = int64_t(mult) * L.ns;
     if (N == 0) {
@@ -1190,17 +1259,17 @@ int sepnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, co
     float* pB = pS + partial_floats(w, nsc);
     float* pH = pB + partial_floats(w, nsc);
     if (cm) {
-        FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
-            auto k = k_sepnorm_bwd<cpl, true, true, vec>;
+        FEQ_ADD_DISPATCH(ga != nullptr, FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
+            auto k = k_sepnorm_bwd<cpl, true, true, vec, add>;
             FEQ_LAUNCH("k_sepnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
-                       s, L, N, gy, x, w_s, w_h, eps, gx, pS, pB, L.nhc ? pH : nullptr);
-        }))
+                       s, L, N, gy, x, w_s, w_h, eps, gx, pS, pB, L.nhc ? pH : nullptr, ga);
+        })))
     } else {
-        FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH(L, {
-            auto k = k_sepnorm_bwd<cpl, stage, false, stage && vec>;
+        FEQ_ADD_DISPATCH(ga != nullptr, FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH(L, {
+            auto k = k_sepnorm_bwd<cpl, stage, false, stage && vec, stage && add>;
             FEQ_LAUNCH("k_sepnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
-                       s, L, N, gy, x, w_s, w_h, eps, gx, pS, pB, L.nhc ? pH : nullptr);
-        }))
+                       s, L, N, gy, x, w_s, w_h, eps, gx, pS, pB, L.nhc ? pH : nullptr, ga);
+        })))
     }
     PartialJob jobs[3];
     int nj = 0;
@@ -1217,16 +1286,25 @@ extern "C" int feq_sepnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult
                                const float* gy, const float* x, const float* w_s, const float* w_h,
                                float eps, float* gx, float* gw_s, float* gb_s, float* gw_h,
                                void* ws, size_t ws_bytes, feq_stream_t stream) {
-    return sepnorm_bwd(lvals, nreps, mult, N, gy, x, w_s, w_h, eps, gx, gw_s, gb_s, gw_h, ws, ws_bytes, false,
-                       stream);
+    return sepnorm_bwd(lvals, nreps, mult, N, gy, x, w_s, w_h, eps, nullptr, gx, gw_s, gb_s, gw_h, ws, ws_bytes,
+                       false, stream);
 }
 
 extern "C" int feq_sepnorm_bwd_cm(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
                                   const float* gy, const float* x, const float* w_s, const float* w_h,
                                   float eps, float* gx, float* gw_s, float* gb_s, float* gw_h,
                                   void* ws, size_t ws_bytes, feq_stream_t stream) {
-    return sepnorm_bwd(lvals, nreps, mult, N, gy, x, w_s, w_h, eps, gx, gw_s, gb_s, gw_h, ws, ws_bytes, true,
-                       stream);
+    return sepnorm_bwd(lvals, nreps, mult, N, gy, x, w_s, w_h, eps, nullptr, gx, gw_s, gb_s, gw_h, ws, ws_bytes,
+                       true, stream);
+}
+
+extern "C" int feq_sepnorm_bwd_add(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                                   const float* gy, const float* x, const float* w_s, const float* w_h,
+                                   float eps, const float* gx_add, float* gx, float* gw_s, float* gb_s,
+                                   float* gw_h, void* ws, size_t ws_bytes, int32_t cm, feq_stream_t stream) {
+    if (N > 0 && !gx_add) return fail(FEQ_ERR_INVALID, "NULL gradient addend");
+    return sepnorm_bwd(lvals, nreps, mult, N, gy, x, w_s, w_h, eps, gx_add, gx, gw_s, gb_s, gw_h, ws, ws_bytes,
+                       cm != 0, stream);
 }
 
 namespace {
@@ -1278,15 +1356,18 @@ extern "C" size_t feq_eqnorm_workspace(const int32_t* lvals, int32_t nreps, int3
 
 namespace {
 int eqnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, const float* gy,
-               const float* x, const float* w_ln, const float* b_ln, float eps, float ln_eps, float* gx,
-               float* gw_ln, float* gb_ln, void* ws, size_t ws_bytes, bool cm, feq_stream_t stream) {
+               const float* x, const float* w_ln, const float* b_ln, float eps, float ln_eps, const float* ga,
+               float* gx, float* gw_ln, float* gb_ln, void* ws, size_t ws_bytes, bool cm,
+               feq_stream_t stream) {
     NodeL L;
     if (int rc = make_nodel(lvals, nreps, mult, &L)) return rc;
     if (cm && int64_t(L.mult) * L.dim > kStageRow)
         return fail(FEQ_ERR_UNSUPPORTED, "component-major norm gradient: at most %d floats per node", kStageRow);
+    if (ga && int64_t(L.mult) * L.dim > kStageRow)
+        return fail(FEQ_ERR_UNSUPPORTED, "norm gradient with an addend: at most %d floats per node", kStageRow);
     if (int rc = check_rows(N, gy, x, gx)) return rc;
     if (!w_ln != !b_ln) return fail(FEQ_ERR_INVALID, "LayerNorm weight and bias go together");
-    L.vec = L.vec && al16(gy) && al16(x) && al16(gx);
+    L.vec = L.vec && al16(gy) && al16(x) && al16(gx) && al16(ga);
     if (w_ln && (!gw_ln || !gb_ln)) return fail(FEQ_ERR_INVALID, "NULL LayerNorm gradient");
     hipStream_t s = stream_of(stream);
     if (N == 0) {
@@ -1300,17 +1381,17 @@ int eqnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, con
     float* pW = w_ln ? static_cast<float*>(ws) : nullptr;
     float* pB = w_ln ? pW + partial_floats(w, mult) : nullptr;
     if (cm) {
-        FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
-            auto k = k_eqnorm_bwd<cpl, true, true, vec>;
+        FEQ_ADD_DISPATCH(ga != nullptr, FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
+            auto k = k_eqnorm_bwd<cpl, true, true, vec, add>;
             FEQ_LAUNCH("k_eqnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
-                       s, L, N, gy, x, w_ln, b_ln, eps, ln_eps, gx, pW, pB);
-        }))
+                       s, L, N, gy, x, w_ln, b_ln, eps, ln_eps, gx, pW, pB, ga);
+        })))
     } else {
-        FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH(L, {
-            auto k = k_eqnorm_bwd<cpl, stage, false, stage && vec>;
+        FEQ_ADD_DISPATCH(ga != nullptr, FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH(L, {
+            auto k = k_eqnorm_bwd<cpl, stage, false, stage && vec, stage && add>;
             FEQ_LAUNCH("k_eqnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
-                       s, L, N, gy, x, w_ln, b_ln, eps, ln_eps, gx, pW, pB);
-        }))
+                       s, L, N, gy, x, w_ln, b_ln, eps, ln_eps, gx, pW, pB, ga);
+        })))
     }
     if (!w_ln) return FEQ_OK;
     const PartialJob jobs[2] = {PartialJob{pW, int(w), mult, gw_ln, pW + w * mult},
@@ -1323,16 +1404,25 @@ extern "C" int feq_eqnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult,
                               const float* gy, const float* x, const float* w_ln, const float* b_ln,
                               float eps, float ln_eps, float* gx, float* gw_ln, float* gb_ln,
                               void* ws, size_t ws_bytes, feq_stream_t stream) {
-    return eqnorm_bwd(lvals, nreps, mult, N, gy, x, w_ln, b_ln, eps, ln_eps, gx, gw_ln, gb_ln, ws, ws_bytes,
-                      false, stream);
+    return eqnorm_bwd(lvals, nreps, mult, N, gy, x, w_ln, b_ln, eps, ln_eps, nullptr, gx, gw_ln, gb_ln, ws,
+                      ws_bytes, false, stream);
 }
 
 extern "C" int feq_eqnorm_bwd_cm(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
                                  const float* gy, const float* x, const float* w_ln, const float* b_ln,
                                  float eps, float ln_eps, float* gx, float* gw_ln, float* gb_ln,
                                  void* ws, size_t ws_bytes, feq_stream_t stream) {
-    return eqnorm_bwd(lvals, nreps, mult, N, gy, x, w_ln, b_ln, eps, ln_eps, gx, gw_ln, gb_ln, ws, ws_bytes,
-                      true, stream);
+    return eqnorm_bwd(lvals, nreps, mult, N, gy, x, w_ln, b_ln, eps, ln_eps, nullptr, gx, gw_ln, gb_ln, ws,
+                      ws_bytes, true, stream);
+}
+
+extern "C" int feq_eqnorm_bwd_add(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N,
+                                  const float* gy, const float* x, const float* w_ln, const float* b_ln,
+                                  float eps, float ln_eps, const float* gx_add, float* gx, float* gw_ln,
+                                  float* gb_ln, void* ws, size_t ws_bytes, int32_t cm, feq_stream_t stream) {
+    if (N > 0 && !gx_add) return fail(FEQ_ERR_INVALID, "NULL gradient addend");
+    return eqnorm_bwd(lvals, nreps, mult, N, gy, x, w_ln, b_ln, eps, ln_eps, gx_add, gx, gw_ln, gb_ln, ws,
+                      ws_bytes, cm != 0, stream);
 }
 
 // v4: the component-major kernels' 16-byte form (four pairs per thread)

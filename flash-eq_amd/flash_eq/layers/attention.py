@@ -123,8 +123,11 @@ class EquivariantAttention(nn.Module):
                                dict(edge_features=edge_features))
         if (node_features.dim() == 3 and self.norm_qk.cm_ok(node_features)
                 and self.linear_qk.fused_ok(node_features)):
-            # the norm writes the component-major layout the projection reads
-            qk = self.linear_qk.forward_layout(self.norm_qk.forward_cm(node_features), True, False).view(
+            # the norm writes the component-major layout the projection reads;
+            # the V projection's gradient of the features is added in the
+            # norm's backward kernel (node_features becomes the norm's alias)
+            q_in, node_features = self.norm_qk.forward_pair(node_features, cm=True)
+            qk = self.linear_qk.forward_layout(q_in, True, False).view(
                 node_features.shape[0], 2 * self.in_repr.mult, node_features.shape[-1])
         else:
             qk = self.linear_qk(self.norm_qk(node_features))        # (N, 2 mult, dim)

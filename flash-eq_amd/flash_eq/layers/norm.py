@@ -124,6 +124,15 @@ class EquivariantLayerNorm(nn.Module):
         ln_eps = self.lnorm.eps if self.lnorm is not None else 0.0
         return ops.EqNormFn.apply(f, w, b, self._lv, self.mult, get_epsilon(f.dtype), ln_eps, True)
 
+    def forward_pair(self, f: torch.Tensor, cm: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+        """(the norm of f, f again for a second branch): the second branch's
+        gradient is added in the norm's backward kernel, not by autograd in a
+        separate pass.  The norm is component-major with ``cm``; ``cm_ok(f)``."""
+        w = self.lnorm.weight if self.lnorm is not None else None
+        b = self.lnorm.bias if self.lnorm is not None else None
+        ln_eps = self.lnorm.eps if self.lnorm is not None else 0.0
+        return ops.EqNormFn.apply(f, w, b, self._lv, self.mult, get_epsilon(f.dtype), ln_eps, cm, True)
+
     def forward(self, f: torch.Tensor) -> torch.Tensor:
         eps = self._epsilon if self._epsilon is not None else get_epsilon(f.dtype)
         w = self.lnorm.weight if self.lnorm is not None else None
@@ -188,6 +197,14 @@ class SeparableEquivariantLayerNorm(nn.Module):
         mult), for a channel-mixing map that follows; ``cm_ok(f)``."""
         ws, bs, wh, eps = self._kernel_args(f)
         return ops.SepNormFn.apply(f, ws, bs, wh, self._lv, self.repr.mult, eps, True)
+
+    def forward_pair(self, f: torch.Tensor, cm: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+        """(the norm of f, f again for a second branch such as the residual
+        connection): the second branch's gradient is added in the norm's
+        backward kernel, not by autograd in a separate pass.  The norm is
+        component-major with ``cm``; ``cm_ok(f)``."""
+        ws, bs, wh, eps = self._kernel_args(f)
+        return ops.SepNormFn.apply(f, ws, bs, wh, self._lv, self.repr.mult, eps, cm, True)
 
     def forward(self, f: torch.Tensor) -> torch.Tensor:
         args = self._kernel_args(f)

@@ -103,10 +103,16 @@ class EquivariantTransformerBlock(nn.Module):
         if half is not None:
             return run_float32(self, half, (P, Q, node_features, distances, graph),
                                dict(edge_features=edge_features))
-        attn_out = self.attn(P, Q, self.norm1(node_features), distances, graph,
-                             edge_features=edge_features)
+        # With the residual connection, the norm also returns the features for
+        # it (forward_pair): the residual's gradient is then added inside the
+        # norm's backward kernel instead of by autograd in a separate pass.
+        if self._use_attn_residual and self.norm1.cm_ok(node_features):
+            h, nf = self.norm1.forward_pair(node_features)
+        else:
+            h, nf = self.norm1(node_features), node_features
+        attn_out = self.attn(P, Q, h, distances, graph, edge_features=edge_features)
         if self._use_attn_residual:
-            x = _residual(node_features, attn_out, self.layer_scale_attn, self.drop_path)
+            x = _residual(nf, attn_out, self.layer_scale_attn, self.drop_path)
         else:
             x = attn_out
         if (isinstance(self.mlp_act, EquivariantGating) and self.mlp_act.kernels_ok(x)
@@ -117,15 +123,15 @@ class EquivariantTransformerBlock(nn.Module):
             cm = (self.norm2.cm_ok(x) and x.dim() == 3 and isinstance(self.layer_scale_mlp, LayerScale)
                   and isinstance(self.drop_path, nn.Identity)
                   and self.layer_scale_mlp.gamma.dtype == torch.float32)
-            h = self.norm2.forward_cm(x) if cm else self.norm2(x)
+            h, xr = self.norm2.forward_pair(x, cm) if self.norm2.cm_ok(x) else (self.norm2(x), x)
             t = self.mlp_act.forward_cm(self.mlp_up.forward_layout(h, cm, True))
             if cm:
-                return ResidualScaleCmFn.apply(x, self.mlp_down.forward_layout(t, True, True),
+                return ResidualScaleCmFn.apply(xr, self.mlp_down.forward_layout(t, True, True),
                                                self.layer_scale_mlp.gamma)
-            mlp_out = self.mlp_down.forward_layout(t, True, False).view(
-                *h.shape[:-2], self.out_repr.mult, h.shape[-1])
-        else:
-            mlp_out = self.mlp_down(self.mlp_act(self.mlp_up(self.norm2(x))))
+            mlp_out = self.mlp_down.forward_layout(t, True, False).view(*x.shape[:-2], self.out_repr.mult,
+                                                                       x.shape[-1])
+            return _residual(xr, mlp_out, self.layer_scale_mlp, self.drop_path)
+        mlp_out = self.mlp_down(self.mlp_act(self.mlp_up(self.norm2(x))))
         return _residual(x, mlp_out, self.layer_scale_mlp, self.drop_path)
 
     def extra_repr(self) -> str:

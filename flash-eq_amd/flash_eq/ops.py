@@ -935,10 +935,13 @@ def _c(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
 class SepNormFn(torch.autograd.Function):
     """SeparableEquivariantLayerNorm (norm.py:177-246) on feq_sepnorm_fwd/bwd.
     ``cm``: the output (and its gradient) component-major (dim, N, mult),
-    feq_sepnorm_fwd_cm / _bwd_cm (the input stays node-major)."""
+    feq_sepnorm_fwd_cm / _bwd_cm (the input stays node-major).  ``alias``: also
+    returns the input (as a view) for a second branch; that branch's gradient
+    is added inside the backward kernel (feq_sepnorm_bwd_add) instead of by
+    autograd in a separate pass."""
 
     @staticmethod
-    def forward(ctx, x, w_s, b_s, w_h, lvals, mult, eps, cm=False):
+    def forward(ctx, x, w_s, b_s, w_h, lvals, mult, eps, cm=False, alias=False):
         dim = sum(2 * l + 1 for l in lvals)
         xs = x.contiguous()
         n = _node_rows(xs, mult, dim)
@@ -952,12 +955,17 @@ class SepNormFn(torch.autograd.Function):
             N.check(rc, "feq_sepnorm_fwd")
         ctx.save_for_backward(xs, w_s, b_s, w_h)
         ctx.meta = (lvals, mult, eps, n, cm)
+        if alias:
+            ctx.set_materialize_grads(False)
+            return y, xs.view_as(xs)
         return y
 
     @staticmethod
-    def backward(ctx, gy):
+    def backward(ctx, gy, ga=None):
         xs, w_s, b_s, w_h = ctx.saved_tensors
         lvals, mult, eps, n, cm = ctx.meta
+        if gy is None:
+            return ga, None, None, None, None, None, None, None, None
         gy = gy.contiguous()
         dev = xs.device
         gx = torch.empty_like(xs)
@@ -967,21 +975,28 @@ class SepNormFn(torch.autograd.Function):
         lib = N.lib()
         arr = _lvals_i32(lvals)
         ws = N.workspace(lib.feq_sepnorm_workspace(arr, len(lvals), mult, n), dev)
-        fn = lib.feq_sepnorm_bwd_cm if cm else lib.feq_sepnorm_bwd
         with torch.cuda.device(dev):
-            rc = fn(arr, len(lvals), mult, n, N.ptr(gy), N.ptr(xs), N.ptr(w_s), N.ptr(w_h), eps, N.ptr(gx),
-                    N.ptr(gws), N.ptr(gbs), N.ptr(gwh), N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+            if ga is not None:
+                ga = ga.contiguous()
+                rc = lib.feq_sepnorm_bwd_add(arr, len(lvals), mult, n, N.ptr(gy), N.ptr(xs), N.ptr(w_s),
+                                             N.ptr(w_h), eps, N.ptr(ga), N.ptr(gx), N.ptr(gws), N.ptr(gbs),
+                                             N.ptr(gwh), N.ptr(ws), ws.numel(), int(cm), N.stream_ptr(dev))
+            else:
+                fn = lib.feq_sepnorm_bwd_cm if cm else lib.feq_sepnorm_bwd
+                rc = fn(arr, len(lvals), mult, n, N.ptr(gy), N.ptr(xs), N.ptr(w_s), N.ptr(w_h), eps, N.ptr(gx),
+                        N.ptr(gws), N.ptr(gbs), N.ptr(gwh), N.ptr(ws), ws.numel(), N.stream_ptr(dev))
         N.check(rc, "feq_sepnorm_bwd")
-        return gx, gws, gbs, gwh, None, None, None, None
+        return gx, gws, gbs, gwh, None, None, None, None, None
 
 
 class EqNormFn(torch.autograd.Function):
     """EquivariantLayerNorm (norm.py:148-174) on feq_eqnorm_fwd/bwd.  ``cm``:
     the output (and its gradient) component-major (dim, N, mult),
-    feq_eqnorm_fwd_cm / _bwd_cm (the input stays node-major)."""
+    feq_eqnorm_fwd_cm / _bwd_cm (the input stays node-major).  ``alias``: as
+    SepNormFn's (feq_eqnorm_bwd_add)."""
 
     @staticmethod
-    def forward(ctx, x, w_ln, b_ln, lvals, mult, eps, ln_eps, cm=False):
+    def forward(ctx, x, w_ln, b_ln, lvals, mult, eps, ln_eps, cm=False, alias=False):
         dim = sum(2 * l + 1 for l in lvals)
         xs = x.contiguous()
         n = _node_rows(xs, mult, dim)
@@ -996,12 +1011,17 @@ class EqNormFn(torch.autograd.Function):
             N.check(rc, "feq_eqnorm_fwd")
         ctx.save_for_backward(xs, w_ln, b_ln)
         ctx.meta = (lvals, mult, eps, ln_eps, n, cm)
+        if alias:
+            ctx.set_materialize_grads(False)
+            return y, xs.view_as(xs)
         return y
 
     @staticmethod
-    def backward(ctx, gy):
+    def backward(ctx, gy, ga=None):
         xs, w_ln, b_ln = ctx.saved_tensors
         lvals, mult, eps, ln_eps, n, cm = ctx.meta
+        if gy is None:
+            return ga, None, None, None, None, None, None, None, None
         gy = gy.contiguous()
         dev = xs.device
         gx = torch.empty_like(xs)
@@ -1011,11 +1031,17 @@ class EqNormFn(torch.autograd.Function):
         arr = _lvals_i32(lvals)
         ws = N.workspace(lib.feq_eqnorm_workspace(arr, len(lvals), mult, n), dev)
         with torch.cuda.device(dev):
-            rc = (lib.feq_eqnorm_bwd_cm if cm else lib.feq_eqnorm_bwd)(arr, len(lvals), mult, n, N.ptr(gy), N.ptr(xs), N.ptr(w_ln),
-                                    N.ptr(b_ln), eps, ln_eps, N.ptr(gx), N.ptr(gw), N.ptr(gb),
-                                    N.ptr(ws), ws.numel(), N.stream_ptr(dev))
+            if ga is not None:
+                ga = ga.contiguous()
+                rc = lib.feq_eqnorm_bwd_add(arr, len(lvals), mult, n, N.ptr(gy), N.ptr(xs), N.ptr(w_ln),
+                                            N.ptr(b_ln), eps, ln_eps, N.ptr(ga), N.ptr(gx), N.ptr(gw), N.ptr(gb),
+                                            N.ptr(ws), ws.numel(), int(cm), N.stream_ptr(dev))
+            else:
+                fn = lib.feq_eqnorm_bwd_cm if cm else lib.feq_eqnorm_bwd
+                rc = fn(arr, len(lvals), mult, n, N.ptr(gy), N.ptr(xs), N.ptr(w_ln), N.ptr(b_ln), eps, ln_eps,
+                        N.ptr(gx), N.ptr(gw), N.ptr(gb), N.ptr(ws), ws.numel(), N.stream_ptr(dev))
         N.check(rc, "feq_eqnorm_bwd")
-        return gx, gw, gb, None, None, None, None, None
+        return gx, gw, gb, None, None, None, None, None, None
 
 
 def transpose_last2(t: torch.Tensor, rows: int, cols: int) -> torch.Tensor:

@@ -552,6 +552,17 @@ int feq_sepnorm_bwd_cm(const int32_t* lvals, int32_t nreps, int32_t mult, int64_
                        float eps, float* grad_x, float* grad_w_s, float* grad_b_s,
                        float* grad_w_h, void* workspace, size_t workspace_bytes,
                        feq_stream_t stream);
+/* feq_sepnorm_bwd (cm = 0) or _bwd_cm (cm != 0) with grad_x = the norm's input
+ * gradient + grad_x_add (node-major, like grad_x): the gradient of an input
+ * that also feeds a second branch (the block's residual connection), summed as
+ * grad_x is written instead of in a separate pass.  No counterpart in the
+ * reference, whose autograd adds the branches' gradients; mult * dim at most
+ * 1152. */
+int feq_sepnorm_bwd_add(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
+                        const float* grad_y, const float* x, const float* w_s, const float* w_h,
+                        float eps, const float* grad_x_add, float* grad_x, float* grad_w_s,
+                        float* grad_b_s, float* grad_w_h, void* workspace, size_t workspace_bytes,
+                        int32_t cm, feq_stream_t stream);
 
 /* EquivariantLayerNorm (norm.py:148-174): per irrep k, n = sqrt(sum x^2 + eps)
  * (RepNorm, norm.py:51-73); y = x * LayerNorm_c(n)[w_ln, b_ln, ln_eps] / (n + eps),
@@ -571,6 +582,14 @@ int feq_eqnorm_bwd_cm(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t
                       const float* grad_y, const float* x, const float* w_ln, const float* b_ln,
                       float eps, float ln_eps, float* grad_x, float* grad_w_ln, float* grad_b_ln,
                       void* workspace, size_t workspace_bytes, feq_stream_t stream);
+/* feq_eqnorm_bwd / _bwd_cm with grad_x = the norm's input gradient +
+ * grad_x_add (node-major), as feq_sepnorm_bwd_add (the attention's input feeds
+ * both this norm and the V projection).  No counterpart in the reference. */
+int feq_eqnorm_bwd_add(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
+                       const float* grad_y, const float* x, const float* w_ln, const float* b_ln,
+                       float eps, float ln_eps, const float* grad_x_add, float* grad_x,
+                       float* grad_w_ln, float* grad_b_ln, void* workspace, size_t workspace_bytes,
+                       int32_t cm, feq_stream_t stream);
 int feq_eqnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t num_nodes,
                    const float* grad_y, const float* x, const float* w_ln, const float* b_ln,
                    float eps, float ln_eps, float* grad_x, float* grad_w_ln, float* grad_b_ln,

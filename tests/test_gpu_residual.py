@@ -134,3 +134,49 @@ def test_component_major_norm_output_is_the_transpose(dev, kind, mult):
     assert torch.equal(x2.grad, x1.grad)
     for a, b in zip(g1, norm.parameters()):
         assert torch.equal(a, b.grad)
+
+
+@pytest.mark.parametrize("cm", [False, True])
+@pytest.mark.parametrize("mult", [64, 6])
+@pytest.mark.parametrize("kind", ["separable", "equivariant"])
+def test_norm_pair_adds_the_second_branch_gradient(dev, kind, mult, cm):
+    """forward_pair returns (norm(x), x); the second output's gradient is added
+    inside the norm's backward kernel (feq_*norm_bwd_add): x.grad is bitwise
+    the norm's input gradient plus that gradient, as autograd's separate sum
+    gives it; the parameter gradients are unchanged."""
+    torch.manual_seed(2)
+    cls = fe.SeparableEquivariantLayerNorm if kind == "separable" else fe.EquivariantLayerNorm
+    norm = cls(fe.Repr([0, 1, 2], mult)).to(dev)
+    with torch.no_grad():
+        for p in norm.parameters():
+            p.normal_()
+    x = torch.randn(501, mult, 9, device=dev)
+    gy = torch.randn(501, mult, 9, device=dev)
+    ga = torch.randn(501, mult, 9, device=dev)
+    gyl = gy.permute(2, 0, 1).contiguous() if cm else gy
+    x1 = x.clone().requires_grad_(True)
+    y1 = norm.forward_cm(x1) if cm else norm(x1)
+    (y1 * gyl).sum().backward()
+    g1 = [p.grad.clone() for p in norm.parameters()]
+    ref = x1.grad + ga
+    for p in norm.parameters():
+        p.grad = None
+    x2 = x.clone().requires_grad_(True)
+    assert norm.cm_ok(x2)
+    y2, a2 = norm.forward_pair(x2, cm)
+    assert torch.equal(a2, x2) and torch.equal(y2, y1)
+    NAT.profile_summary()
+    NAT.profile_enable(True)
+    ((y2 * gyl).sum() + (a2 * ga).sum()).backward()
+    torch.cuda.synchronize()
+    NAT.profile_enable(False)
+    launched = NAT.profile_summary()
+    assert launched.get("k_sepnorm_bwd" if kind == "separable" else "k_eqnorm_bwd", (0,))[0] == 1, launched
+    assert torch.equal(x2.grad, ref)
+    for a, b in zip(g1, norm.parameters()):
+        assert torch.equal(a, b.grad)
+    # only the second branch used: its gradient passes through
+    x3 = x.clone().requires_grad_(True)
+    _, a3 = norm.forward_pair(x3, cm)
+    (a3 * ga).sum().backward()
+    assert torch.equal(x3.grad, ga)
