@@ -93,6 +93,54 @@ __device__ inline void st_head_scaled(float* __restrict__ head, int j, int G, in
     }
 }
 
+// Layout of the Q / K node tables' heads: head h of row n starts at
+// n * ld + h * hs, and its chunk c (V floats) at (c / cpd) * cs + (c % cpd) * V
+// from there.  Node-major rows (n, channel, component): hs = Dh, cpd = Dh / V,
+// cs = 0 (the head's Dh floats are contiguous).  Component-major tables
+// (component, n, channel): hs = hc (channels per head), cpd = hc / V, cs = the
+// component stride (the head's hc channels of each component are contiguous).
+struct HeadLayout {
+    int64_t hs;
+    int cpd;
+    int64_t cs;
+};
+
+// The offsets of the lane's chunks j, j + G, ... within a head.
+template <int V, int NT>
+__device__ inline void head_offsets(const HeadLayout& hl, int j, int G, int64_t (&off)[NT]) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int c = j + G * t;
+        const int g = c / hl.cpd;
+        off[t] = g * hl.cs + static_cast<int64_t>(c - g * hl.cpd) * V;
+    }
+}
+
+template <int V, int NT>
+__device__ inline void ld_head_o(const float* __restrict__ head, const int64_t (&off)[NT], int j, int G, int NC,
+                                 bool ok, float (&v)[NT][V]) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int c = j + G * t;
+        if (ok && c < NC) {
+            ldv<V>(head + off[t], v[t]);
+        } else {
+#pragma unroll
+            for (int u = 0; u < V; ++u) v[t][u] = 0.0f;
+        }
+    }
+}
+
+template <int V, int NT>
+__device__ inline void st_head_o(float* __restrict__ head, const int64_t (&off)[NT], int j, int G, int NC, bool ok,
+                                 const float (&v)[NT][V]) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int c = j + G * t;
+        if (ok && c < NC) stv<V>(head + off[t], v[t]);
+    }
+}
+
 template <int V, int NT>
 __device__ inline float dot_head(const float (&a)[NT][V], const float (&b)[NT][V]) {
     float s = 0.0f;
@@ -156,7 +204,7 @@ k_att_fwd(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ K,
           const int64_t* __restrict__ kidx, int64_t nk, const float* __restrict__ dist, int64_t E,
           int H, int Dh, int lgG, const float* __restrict__ scale_p, float decay,
           const int32_t* __restrict__ perm, const int32_t* __restrict__ offsets, int64_t N,
-          float* __restrict__ attn, float* __restrict__ qk) {
+          float* __restrict__ attn, float* __restrict__ qk, HeadLayout hl) {
     const float scale = *scale_p;
     int64_t n;
     int b, cnt;
@@ -177,11 +225,13 @@ k_att_fwd(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ K,
     // Q rows too, would not fit the registers)
     constexpr int UE = NT * V >= 64 ? (NODE ? 2 : 1) : NT * V >= 32 ? 2 : kUE;
     static_assert(64 % UE == 0, "chunks of 64 positions hold whole groups of UE edges");
+    int64_t off[NT];
+    head_offsets<V, NT>(hl, j, G, off);
     for (int h0 = 0; h0 < H; h0 += NG) {
         const int h = h0 + g;
         const bool hv = h < H;
         float q[NT][V];
-        if constexpr (NODE) ld_head<V, NT>(Q + n * ldq + h * Dh, j, G, NC, hv && cnt > 0, q);
+        if constexpr (NODE) ld_head_o<V, NT>(Q + n * ldq + h * hl.hs, off, j, G, NC, hv && cnt > 0, q);
         float m = -INFINITY, s = 0.0f;
         SegChunk sc{};
         for (int i0 = 0; i0 < cnt; i0 += UE) {
@@ -195,7 +245,7 @@ k_att_fwd(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ K,
                 eu[u] = sc.edge(iu);
                 const int64_t kr = sc.row(iu);
                 const bool ok = hv && live && kr >= 0;
-                ld_head<V, NT>(K + (ok ? kr : 0) * ldk + h * Dh, j, G, NC, ok, k[u]);
+                ld_head_o<V, NT>(K + (ok ? kr : 0) * ldk + h * hl.hs, off, j, G, NC, ok, k[u]);
             }
             float dot[UE];
             if constexpr (NODE) {
@@ -205,7 +255,7 @@ k_att_fwd(const float* __restrict__ Q, int64_t ldq, const float* __restrict__ K,
 #pragma unroll
                 for (int u = 0; u < UE; ++u) {
                     float qe[NT][V];
-                    ld_head<V, NT>(Q + eu[u] * ldq + h * Dh, j, G, NC, hv && i0 + u < cnt, qe);
+                    ld_head_o<V, NT>(Q + eu[u] * ldq + h * hl.hs, off, j, G, NC, hv && i0 + u < cnt, qe);
                     dot[u] = dot_head<V, NT>(qe, k[u]);
                 }
             }
@@ -249,7 +299,7 @@ k_att_bwd_dst(const float* __restrict__ Q, int64_t ldq, const float* __restrict_
               const float* __restrict__ gattn, int64_t E, int H, int Dh, int lgG,
               const float* __restrict__ scale_p, const int32_t* __restrict__ perm,
               const int32_t* __restrict__ offsets, int64_t N, float* __restrict__ gQ, int64_t ldgq,
-              float* __restrict__ gK, int64_t ldgk, float* __restrict__ glogit) {
+              float* __restrict__ gK, int64_t ldgk, float* __restrict__ glogit, HeadLayout hl) {
     const float scale = *scale_p;
     int64_t n;
     int b, cnt;
@@ -269,6 +319,8 @@ k_att_bwd_dst(const float* __restrict__ Q, int64_t ldq, const float* __restrict_
     }
     const int G = 1 << lgG, NG = 64 >> lgG, g = lane >> lgG, j = lane & (G - 1);
     const int NC = Dh / V;
+    int64_t off[NT];
+    head_offsets<V, NT>(hl, j, G, off);
     for (int h0 = 0; h0 < H; h0 += NG) {
         const int h = h0 + g;
         const bool hv = h < H;
@@ -298,7 +350,7 @@ k_att_bwd_dst(const float* __restrict__ Q, int64_t ldq, const float* __restrict_
                 const int64_t e = eu[u];
                 const int64_t kr = sc.row(iu);
                 const bool ok = hv && live && kr >= 0;
-                ld_head<V, NT>(K + (ok ? kr : 0) * ldk + h * Dh, j, G, NC, ok, k[u]);
+                ld_head_o<V, NT>(K + (ok ? kr : 0) * ldk + h * hl.hs, off, j, G, NC, ok, k[u]);
                 gl[u] = (hv && live) ? attn[e * H + h] * (gattn[e * H + h] - S) : 0.0f;
                 if (hv && live && ((i0 + u) & (G - 1)) == j) glogit[e * H + h] = gl[u];
             }
@@ -320,7 +372,7 @@ k_att_bwd_dst(const float* __restrict__ Q, int64_t ldq, const float* __restrict_
                 }
             }
         }
-        if constexpr (NODE) st_head<V, NT>(gQ + n * ldgq + h * Dh, j, G, NC, hv, acc);
+        if constexpr (NODE) st_head_o<V, NT>(gQ + n * ldgq + h * hl.hs, off, j, G, NC, hv, acc);
     }
 }
 
@@ -332,7 +384,8 @@ __global__ void __launch_bounds__(64 * kWaves)
 k_att_bwd_src(const float* __restrict__ Q, int64_t ldq, const int64_t* __restrict__ qidx,
               int64_t nq, const float* __restrict__ glogit, int64_t E, int H, int Dh, int lgG,
               const float* __restrict__ scale_p, const int32_t* __restrict__ perm,
-              const int32_t* __restrict__ offsets, int64_t NK, float* __restrict__ gK, int64_t ldgk) {
+              const int32_t* __restrict__ offsets, int64_t NK, float* __restrict__ gK, int64_t ldgk,
+              HeadLayout hl) {
     const float scale = *scale_p;
     int64_t n;
     int b, cnt;
@@ -340,6 +393,8 @@ k_att_bwd_src(const float* __restrict__ Q, int64_t ldq, const int64_t* __restric
     const int lane = threadIdx.x & 63;
     const int G = 1 << lgG, NG = 64 >> lgG, g = lane >> lgG, j = lane & (G - 1);
     const int NC = Dh / V;
+    int64_t off[NT];
+    head_offsets<V, NT>(hl, j, G, off);
     for (int h0 = 0; h0 < H; h0 += NG) {
         const int h = h0 + g;
         const bool hv = h < H;
@@ -360,7 +415,7 @@ k_att_bwd_src(const float* __restrict__ Q, int64_t ldq, const int64_t* __restric
                 const int64_t e = sc.edge(iu);
                 const int64_t qr = sc.row(iu);
                 const bool ok = hv && live && qr >= 0;
-                ld_head<V, NT>(Q + (ok ? qr : 0) * ldq + h * Dh, j, G, NC, ok, q[u]);
+                ld_head_o<V, NT>(Q + (ok ? qr : 0) * ldq + h * hl.hs, off, j, G, NC, ok, q[u]);
                 gl[u] = ok ? glogit[e * H + h] * scale : 0.0f;
             }
 #pragma unroll
@@ -370,7 +425,7 @@ k_att_bwd_src(const float* __restrict__ Q, int64_t ldq, const int64_t* __restric
 #pragma unroll
                     for (int v = 0; v < V; ++v) acc[t][v] += gl[u] * q[u][t][v];
         }
-        st_head<V, NT>(gK + n * ldgk + h * Dh, j, G, NC, hv, acc);
+        st_head_o<V, NT>(gK + n * ldgk + h * hl.hs, off, j, G, NC, hv, acc);
     }
 }
 
@@ -540,12 +595,16 @@ int check_graph(int64_t E, int64_t N) {
 
 using namespace feq;
 
-extern "C" int feq_attn_softmax_fwd(const float* Q, int64_t ldq, const float* K, int64_t ldk,
-                                    const int64_t* q_idx, const int64_t* k_idx, int64_t num_k,
-                                    const float* dist, int64_t num_edges, int32_t heads,
-                                    int32_t head_dim, const float* scale, float decay,
-                                    const int32_t* perm, const int32_t* offsets, int64_t num_nodes,
-                                    float* attn, float* qk_out, feq_stream_t stream) {
+namespace {
+
+// The node-major (cs = 0: rows of heads * head_dim floats, ld / ldg their
+// strides) and component-major (cs > 0: element (n, channel c, component d)
+// at d cs + n ld + c, hc channels per head, head_dim = hc * dim) forms share
+// these.
+int softmax_fwd(const float* Q, int64_t ldq, const float* K, int64_t ldk, const int64_t* q_idx,
+                const int64_t* k_idx, int64_t num_k, const float* dist, int64_t num_edges, int32_t heads,
+                int32_t head_dim, int32_t hc, int64_t cs, const float* scale, float decay, const int32_t* perm,
+                const int32_t* offsets, int64_t num_nodes, float* attn, float* qk_out, hipStream_t s) {
     if (!scale) return fail(FEQ_ERR_INVALID, "NULL scale (a device float)");
     if (int rc = check_graph(num_edges, num_nodes)) return rc;
     const bool node = q_idx != nullptr;
@@ -553,27 +612,103 @@ extern "C" int feq_attn_softmax_fwd(const float* Q, int64_t ldq, const float* K,
     if (num_edges == 0) return FEQ_OK;
     if (!Q || !K || !perm || !offsets || !attn) return fail(FEQ_ERR_INVALID, "NULL pointer");
     if (decay > 0.0f && !dist) return fail(FEQ_ERR_INVALID, "distance decay needs distances");
-    const int64_t row = static_cast<int64_t>(heads) * head_dim;
-    if (ldq < row || ldk < row) return fail(FEQ_ERR_INVALID, "row stride shorter than heads * head_dim");
+    const int64_t row = static_cast<int64_t>(heads) * (cs ? hc : head_dim);
+    if (ldq < row || ldk < row) return fail(FEQ_ERR_INVALID, "row stride shorter than the heads' values");
     const int64_t nk = node ? num_k : num_edges;
     HeadCfg c;
-    if (int rc = head_cfg(heads, head_dim, {ldq, ldk}, {Q, K}, c)) return rc;
-    hipStream_t s = stream_of(stream);
+    if (int rc = cs ? head_cfg(heads, head_dim, {ldq, ldk, hc, cs}, {Q, K}, c)
+                    : head_cfg(heads, head_dim, {ldq, ldk}, {Q, K}, c))
+        return rc;
+    const HeadLayout hl = cs ? HeadLayout{hc, hc / c.V, cs} : HeadLayout{head_dim, head_dim / c.V, 0};
     return with_cfg(c, [&](auto VV, auto TT) -> int {
         constexpr int V = decltype(VV)::value, NT = decltype(TT)::value;
         if (node) {
             auto kern = k_att_fwd<V, NT, true>;
             FEQ_LAUNCH("k_att_fwd", kern, seg_grid(num_nodes + 1), dim3(64 * kWaves), 0, s, Q, ldq,
                        K, ldk, k_idx, nk, dist, num_edges, heads, head_dim, c.lgG, scale, decay,
-                       perm, offsets, num_nodes, attn, qk_out);
+                       perm, offsets, num_nodes, attn, qk_out, hl);
         } else {
             auto kern = k_att_fwd<V, NT, false>;
             FEQ_LAUNCH("k_att_fwd", kern, seg_grid(num_nodes + 1), dim3(64 * kWaves), 0, s, Q, ldq,
                        K, ldk, k_idx, nk, dist, num_edges, heads, head_dim, c.lgG, scale, decay,
-                       perm, offsets, num_nodes, attn, qk_out);
+                       perm, offsets, num_nodes, attn, qk_out, hl);
         }
         return FEQ_OK;
     });
+}
+
+int softmax_bwd(const float* Q, int64_t ldq, const float* K, int64_t ldk, const int64_t* q_idx,
+                const int64_t* k_idx, int64_t num_k, const float* attn, const float* grad_attn,
+                int64_t num_edges, int32_t heads, int32_t head_dim, int32_t hc, int64_t cs, const float* scale,
+                const int32_t* perm, const int32_t* offsets, int64_t num_nodes, const int32_t* perm_k,
+                const int32_t* offsets_k, float* grad_Q, int64_t ldgq, float* grad_K, int64_t ldgk,
+                float* grad_logits, hipStream_t s) {
+    if (!scale) return fail(FEQ_ERR_INVALID, "NULL scale (a device float)");
+    if (int rc = check_graph(num_edges, num_nodes)) return rc;
+    const bool node = q_idx != nullptr;
+    if (node != (k_idx != nullptr)) return fail(FEQ_ERR_INVALID, "q_idx and k_idx must both be given or both be NULL");
+    // node form: grad_Q gets one row per destination segment (num_nodes rows),
+    // grad_K one row per segment of the CSR by k_idx (num_k rows, offsets_k has
+    // num_k + 1 entries); rows without edges are written as zeros
+    if (node && (num_k < 1 || !offsets_k || (num_edges > 0 && !perm_k)))
+        return fail(FEQ_ERR_INVALID, "the node form needs the CSR of the edges by k_idx");
+    const int64_t row = static_cast<int64_t>(heads) * (cs ? hc : head_dim);
+    if (ldq < row || ldk < row || ldgq < row || ldgk < row)
+        return fail(FEQ_ERR_INVALID, "row stride shorter than the heads' values");
+    if (!grad_Q || !grad_K || !offsets) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    if (num_edges > 0 && (!Q || !K || !attn || !grad_attn || !perm || !grad_logits))
+        return fail(FEQ_ERR_INVALID, "NULL pointer");
+    HeadCfg c;
+    if (int rc = cs ? head_cfg(heads, head_dim, {ldq, ldk, ldgq, ldgk, hc, cs}, {Q, K, grad_Q, grad_K}, c)
+                    : head_cfg(heads, head_dim, {ldq, ldk, ldgq, ldgk}, {Q, K, grad_Q, grad_K}, c))
+        return rc;
+    const HeadLayout hl = cs ? HeadLayout{hc, hc / c.V, cs} : HeadLayout{head_dim, head_dim / c.V, 0};
+    if (!node && num_edges == 0) return FEQ_OK;
+    const int64_t nk = node ? num_k : num_edges;
+    return with_cfg(c, [&](auto VV, auto TT) -> int {
+        constexpr int V = decltype(VV)::value, NT = decltype(TT)::value;
+        if (node) {
+            auto kd = k_att_bwd_dst<V, NT, true>;
+            FEQ_LAUNCH("k_att_bwd_dst", kd, seg_grid(num_nodes + 1), dim3(64 * kWaves), 0, s, Q,
+                       ldq, K, ldk, k_idx, nk, attn, grad_attn, num_edges, heads, head_dim, c.lgG,
+                       scale, perm, offsets, num_nodes, grad_Q, ldgq, grad_K, ldgk, grad_logits, hl);
+            auto ks = k_att_bwd_src<V, NT>;
+            FEQ_LAUNCH("k_att_bwd_src", ks, seg_grid(num_k + 1), dim3(64 * kWaves), 0, s, Q, ldq,
+                       q_idx, num_nodes, grad_logits, num_edges, heads, head_dim, c.lgG, scale,
+                       perm_k, offsets_k, num_k, grad_K, ldgk, hl);
+        } else {
+            auto kd = k_att_bwd_dst<V, NT, false>;
+            FEQ_LAUNCH("k_att_bwd_dst", kd, seg_grid(num_nodes + 1), dim3(64 * kWaves), 0, s, Q,
+                       ldq, K, ldk, k_idx, nk, attn, grad_attn, num_edges, heads, head_dim, c.lgG,
+                       scale, perm, offsets, num_nodes, grad_Q, ldgq, grad_K, ldgk, grad_logits, hl);
+        }
+        return FEQ_OK;
+    });
+}
+
+}  // namespace
+
+extern "C" int feq_attn_softmax_fwd(const float* Q, int64_t ldq, const float* K, int64_t ldk,
+                                    const int64_t* q_idx, const int64_t* k_idx, int64_t num_k,
+                                    const float* dist, int64_t num_edges, int32_t heads,
+                                    int32_t head_dim, const float* scale, float decay,
+                                    const int32_t* perm, const int32_t* offsets, int64_t num_nodes,
+                                    float* attn, float* qk_out, feq_stream_t stream) {
+    return softmax_fwd(Q, ldq, K, ldk, q_idx, k_idx, num_k, dist, num_edges, heads, head_dim, 0, 0, scale, decay,
+                       perm, offsets, num_nodes, attn, qk_out, stream_of(stream));
+}
+
+extern "C" int feq_attn_softmax_fwd_cm(const float* Q, const float* K, int64_t ld, int64_t comp_stride,
+                                       int32_t dim, const int64_t* q_idx, const int64_t* k_idx, int64_t num_k,
+                                       const float* dist, int64_t num_edges, int32_t heads,
+                                       int32_t head_channels, const float* scale, float decay,
+                                       const int32_t* perm, const int32_t* offsets, int64_t num_nodes,
+                                       float* attn, float* qk_out, feq_stream_t stream) {
+    if (dim < 1 || head_channels < 1 || comp_stride < 1) return fail(FEQ_ERR_INVALID, "invalid sizes");
+    if (!q_idx || !k_idx) return fail(FEQ_ERR_INVALID, "the component-major tables are node tables");
+    return softmax_fwd(Q, ld, K, ld, q_idx, k_idx, num_k, dist, num_edges, heads, head_channels * dim,
+                       head_channels, comp_stride, scale, decay, perm, offsets, num_nodes, attn, qk_out,
+                       stream_of(stream));
 }
 
 extern "C" int feq_attn_softmax_bwd(const float* Q, int64_t ldq, const float* K, int64_t ldk,
@@ -584,46 +719,23 @@ extern "C" int feq_attn_softmax_bwd(const float* Q, int64_t ldq, const float* K,
                                     const int32_t* perm_k, const int32_t* offsets_k,
                                     float* grad_Q, int64_t ldgq, float* grad_K, int64_t ldgk,
                                     float* grad_logits, feq_stream_t stream) {
-    if (!scale) return fail(FEQ_ERR_INVALID, "NULL scale (a device float)");
-    if (int rc = check_graph(num_edges, num_nodes)) return rc;
-    const bool node = q_idx != nullptr;
-    if (node != (k_idx != nullptr)) return fail(FEQ_ERR_INVALID, "q_idx and k_idx must both be given or both be NULL");
-    // node form: grad_Q gets one row per destination segment (num_nodes rows),
-    // grad_K one row per segment of the CSR by k_idx (num_k rows, offsets_k has
-    // num_k + 1 entries); rows without edges are written as zeros
-    if (node && (num_k < 1 || !offsets_k || (num_edges > 0 && !perm_k)))
-        return fail(FEQ_ERR_INVALID, "the node form needs the CSR of the edges by k_idx");
-    const int64_t row = static_cast<int64_t>(heads) * head_dim;
-    if (ldq < row || ldk < row || ldgq < row || ldgk < row)
-        return fail(FEQ_ERR_INVALID, "row stride shorter than heads * head_dim");
-    if (!grad_Q || !grad_K || !offsets) return fail(FEQ_ERR_INVALID, "NULL pointer");
-    if (num_edges > 0 && (!Q || !K || !attn || !grad_attn || !perm || !grad_logits))
-        return fail(FEQ_ERR_INVALID, "NULL pointer");
-    HeadCfg c;
-    if (int rc = head_cfg(heads, head_dim, {ldq, ldk, ldgq, ldgk}, {Q, K, grad_Q, grad_K}, c))
-        return rc;
-    hipStream_t s = stream_of(stream);
-    if (!node && num_edges == 0) return FEQ_OK;
-    const int64_t nk = node ? num_k : num_edges;
-    return with_cfg(c, [&](auto VV, auto TT) -> int {
-        constexpr int V = decltype(VV)::value, NT = decltype(TT)::value;
-        if (node) {
-            auto kd = k_att_bwd_dst<V, NT, true>;
-            FEQ_LAUNCH("k_att_bwd_dst", kd, seg_grid(num_nodes + 1), dim3(64 * kWaves), 0, s, Q,
-                       ldq, K, ldk, k_idx, nk, attn, grad_attn, num_edges, heads, head_dim, c.lgG,
-                       scale, perm, offsets, num_nodes, grad_Q, ldgq, grad_K, ldgk, grad_logits);
-            auto ks = k_att_bwd_src<V, NT>;
-            FEQ_LAUNCH("k_att_bwd_src", ks, seg_grid(num_k + 1), dim3(64 * kWaves), 0, s, Q, ldq,
-                       q_idx, num_nodes, grad_logits, num_edges, heads, head_dim, c.lgG, scale,
-                       perm_k, offsets_k, num_k, grad_K, ldgk);
-        } else {
-            auto kd = k_att_bwd_dst<V, NT, false>;
-            FEQ_LAUNCH("k_att_bwd_dst", kd, seg_grid(num_nodes + 1), dim3(64 * kWaves), 0, s, Q,
-                       ldq, K, ldk, k_idx, nk, attn, grad_attn, num_edges, heads, head_dim, c.lgG,
-                       scale, perm, offsets, num_nodes, grad_Q, ldgq, grad_K, ldgk, grad_logits);
-        }
-        return FEQ_OK;
-    });
+    return softmax_bwd(Q, ldq, K, ldk, q_idx, k_idx, num_k, attn, grad_attn, num_edges, heads, head_dim, 0, 0,
+                       scale, perm, offsets, num_nodes, perm_k, offsets_k, grad_Q, ldgq, grad_K, ldgk, grad_logits,
+                       stream_of(stream));
+}
+
+extern "C" int feq_attn_softmax_bwd_cm(const float* Q, const float* K, int64_t ld, int64_t comp_stride,
+                                       int32_t dim, const int64_t* q_idx, const int64_t* k_idx, int64_t num_k,
+                                       const float* attn, const float* grad_attn, int64_t num_edges,
+                                       int32_t heads, int32_t head_channels, const float* scale,
+                                       const int32_t* perm, const int32_t* offsets, int64_t num_nodes,
+                                       const int32_t* perm_k, const int32_t* offsets_k, float* grad_Q,
+                                       float* grad_K, float* grad_logits, feq_stream_t stream) {
+    if (dim < 1 || head_channels < 1 || comp_stride < 1) return fail(FEQ_ERR_INVALID, "invalid sizes");
+    if (!q_idx || !k_idx) return fail(FEQ_ERR_INVALID, "the component-major tables are node tables");
+    return softmax_bwd(Q, ld, K, ld, q_idx, k_idx, num_k, attn, grad_attn, num_edges, heads, head_channels * dim,
+                       head_channels, comp_stride, scale, perm, offsets, num_nodes, perm_k, offsets_k, grad_Q, ld,
+                       grad_K, ld, grad_logits, stream_of(stream));
 }
 
 extern "C" int feq_attn_pool_fwd(const float* V, const float* attn, int64_t num_edges,

@@ -172,6 +172,10 @@ _SIGS = {
                               _P, _P, _I64, _P, _P, _P], ctypes.c_int),
     "feq_attn_softmax_bwd": ([_P, _I64, _P, _I64, _P, _P, _I64, _P, _P, _I64, _I32, _I32, _P,
                               _P, _P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _P], ctypes.c_int),
+    "feq_attn_softmax_fwd_cm": ([_P, _P, _I64, _I64, _I32, _P, _P, _I64, _P, _I64, _I32, _I32, _P, _F,
+                                 _P, _P, _I64, _P, _P, _P], ctypes.c_int),
+    "feq_attn_softmax_bwd_cm": ([_P, _P, _I64, _I64, _I32, _P, _P, _I64, _P, _P, _I64, _I32, _I32, _P,
+                                 _P, _P, _I64, _P, _P, _P, _P, _P, _P], ctypes.c_int),
     "feq_attn_pool_fwd": ([_P, _P, _I64, _I32, _I32, _I32, _P, _P, _I64, _P, _P], ctypes.c_int),
     "feq_attn_pool_bwd": ([_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _P, _P],
                           ctypes.c_int),

@@ -54,9 +54,10 @@ class EquivariantEdgeAttention(nn.Module):
         return self.dropout(attn)
 
     def node_attention_weights(self, qk: torch.Tensor, graph: Graph,
-                               distances: torch.Tensor | None = None) -> torch.Tensor:
+                               distances: torch.Tensor | None = None, cm: bool = False) -> torch.Tensor:
         """The same weights (E, H) with Q = qk[dst, :mult] and K = qk[src, mult:]
-        read from the (N, 2 mult, dim) node table inside the kernels."""
+        read from the (N, 2 mult, dim) node table inside the kernels (``cm``: the
+        component-major (dim, N, 2 mult) table)."""
         N.require_cuda_tensor(qk, "qk")
         perm, offsets = graph.csr()
         perm_s, offsets_s = graph.csr_src()
@@ -64,7 +65,7 @@ class EquivariantEdgeAttention(nn.Module):
             self.distance_decay_scale is not None and distances is not None) else 0.0
         attn = NodeSoftmaxFn.apply(qk, distances if decay > 0 else None, self.log_scale, decay,
                                    self.num_heads, graph.src, graph.dst, perm, offsets, perm_s,
-                                   offsets_s, graph.num_nodes)
+                                   offsets_s, graph.num_nodes, cm)
         return self.dropout(attn)
 
     def forward(self, Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, graph: Graph,
@@ -126,16 +127,17 @@ class EquivariantAttention(nn.Module):
             # the norm writes the component-major layout the projection reads;
             # the V projection's gradient of the features is added in the
             # norm's backward kernel (node_features becomes the norm's alias)
+            # the attention kernels read the projection's component-major
+            # (dim, N, 2 mult) table as it is written
             q_in, node_features = self.norm_qk.forward_pair(node_features, cm=True)
-            qk = self.linear_qk.forward_layout(q_in, True, False).view(
-                node_features.shape[0], 2 * self.in_repr.mult, node_features.shape[-1])
+            qk, qk_cm = self.linear_qk.forward_layout(q_in, True, True), True
         else:
-            qk = self.linear_qk(self.norm_qk(node_features))        # (N, 2 mult, dim)
+            qk, qk_cm = self.linear_qk(self.norm_qk(node_features)), False   # (N, 2 mult, dim)
         if edge_features is None and self.pool.reduce == "sum":
             # V projection, head weighting and sum pooling in one pass over the
             # edges where the fused kernels cover the layer (neither attn * V
             # nor its gradient is formed)
-            attn = self.attention.node_attention_weights(qk, graph, distances)
+            attn = self.attention.node_attention_weights(qk, graph, distances, qk_cm)
             out = self.linear_v.attention_pool(P, Q_basis, node_features.contiguous(), distances, graph,
                                                attn, self.num_heads)
             if out is not None:
@@ -149,7 +151,7 @@ class EquivariantAttention(nn.Module):
         else:
             # x[src] gathered inside the fused layer (message-passing form)
             V = self.linear_v(P, Q_basis, node_features.contiguous(), distances, graph=graph)
-        attn = self.attention.node_attention_weights(qk, graph, distances)
+        attn = self.attention.node_attention_weights(qk, graph, distances, qk_cm)
         if self.pool.reduce == "sum":
             perm, offsets = graph.csr()
             return AttnPoolFn.apply(V, attn, graph.dst, perm, offsets, graph.num_nodes,

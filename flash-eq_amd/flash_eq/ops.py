@@ -782,16 +782,21 @@ class NodeSoftmaxFn(torch.autograd.Function):
     heads of (mult / H) * dim values.  The gathers run inside the kernels (node
     form of ``feq_attn_softmax_fwd``), so the (E, H, Dh) Q and K are never
     formed; the backward sums the Q gradient per destination and the K
-    gradient per source (CSR by source), writing the (N, 2 mult, dim) gradient."""
+    gradient per source (CSR by source), writing the (N, 2 mult, dim) gradient.
+    ``cm``: qk (and its gradient) component-major (dim, N, 2 mult), the layout
+    the projection writes (feq_attn_softmax_fwd_cm / _bwd_cm)."""
 
     @staticmethod
     def forward(ctx, qk, dist, log_scale, decay: float, heads: int, src, dst, perm, offsets,
-                perm_s, offsets_s, num_nodes: int):
+                perm_s, offsets_s, num_nodes: int, cm: bool = False):
         dev = _same_device(qk, log_scale, src, dst, perm, offsets, perm_s, offsets_s)
         qs = _f32(qk, "qk")
         src = src.to(torch.int64).contiguous()
         dst = dst.to(torch.int64).contiguous()
-        Nn, two_mult, dim = qs.shape
+        if cm:
+            dim, Nn, two_mult = qs.shape
+        else:
+            Nn, two_mult, dim = qs.shape
         mult = two_mult // 2
         if two_mult != 2 * mult or mult % heads:
             raise ValueError(f"qk must be (N, 2*mult, dim) with heads | mult, got {tuple(qs.shape)}")
@@ -807,23 +812,34 @@ class NodeSoftmaxFn(torch.autograd.Function):
         qkv = torch.empty(E, heads, dtype=torch.float32, device=dev)
         if E:
             with torch.cuda.device(dev):
-                rc = N.lib().feq_attn_softmax_fwd(N.ptr(qs), ld, N.ptr(qs) + 4 * mult * dim, ld,
-                                                  N.ptr(dst), N.ptr(src), Nn, N.ptr(rs), E, heads,
-                                                  Dh, N.ptr(scale_t), float(decay),
-                                                  N.ptr(perm), N.ptr(offsets), num_nodes,
-                                                  N.ptr(attn), N.ptr(qkv), N.stream_ptr(dev))
+                if cm:
+                    rc = N.lib().feq_attn_softmax_fwd_cm(N.ptr(qs), N.ptr(qs) + 4 * mult, two_mult,
+                                                         Nn * two_mult, dim, N.ptr(dst), N.ptr(src), Nn,
+                                                         N.ptr(rs), E, heads, mult // heads, N.ptr(scale_t),
+                                                         float(decay), N.ptr(perm), N.ptr(offsets),
+                                                         num_nodes, N.ptr(attn), N.ptr(qkv),
+                                                         N.stream_ptr(dev))
+                else:
+                    rc = N.lib().feq_attn_softmax_fwd(N.ptr(qs), ld, N.ptr(qs) + 4 * mult * dim, ld,
+                                                      N.ptr(dst), N.ptr(src), Nn, N.ptr(rs), E, heads,
+                                                      Dh, N.ptr(scale_t), float(decay),
+                                                      N.ptr(perm), N.ptr(offsets), num_nodes,
+                                                      N.ptr(attn), N.ptr(qkv), N.stream_ptr(dev))
             N.check(rc, "feq_attn_softmax_fwd")
         ctx.save_for_backward(qs, attn, qkv, src, dst, perm, offsets, perm_s, offsets_s, scale_t)
         ctx.meta = (decay, num_nodes, heads, qk.dtype, None if dist is None else dist.dtype,
-                    log_scale.dtype)
+                    log_scale.dtype, cm)
         return attn.to(qk.dtype)
 
     @staticmethod
     def backward(ctx, gattn):
         qs, attn, qkv, src, dst, perm, offsets, perm_s, offsets_s, scale_t = ctx.saved_tensors
-        decay, num_nodes, heads, qdt, rdt, ldt = ctx.meta
+        decay, num_nodes, heads, qdt, rdt, ldt, cm = ctx.meta
         dev = qs.device
-        Nn, two_mult, dim = qs.shape
+        if cm:
+            dim, Nn, two_mult = qs.shape
+        else:
+            Nn, two_mult, dim = qs.shape
         mult = two_mult // 2
         E = src.shape[0]
         Dh, ld = mult // heads * dim, two_mult * dim
@@ -833,19 +849,27 @@ class NodeSoftmaxFn(torch.autograd.Function):
         if E == 0:
             g_dist, g_log = _softmax_scalar_grads(glog, qkv, need[1], need[2], decay, rdt, ldt)
             return (torch.zeros_like(qs).to(qdt), g_dist, g_log, None, None, None, None, None, None,
-                    None, None, None)
+                    None, None, None, None)
         gqk = torch.empty_like(qs)
         with torch.cuda.device(dev):
-            rc = N.lib().feq_attn_softmax_bwd(N.ptr(qs), ld, N.ptr(qs) + 4 * mult * dim, ld,
-                                              N.ptr(dst), N.ptr(src), Nn, N.ptr(attn), N.ptr(ga),
-                                              E, heads, Dh, N.ptr(scale_t), N.ptr(perm),
-                                              N.ptr(offsets), num_nodes, N.ptr(perm_s),
-                                              N.ptr(offsets_s), N.ptr(gqk), ld,
-                                              N.ptr(gqk) + 4 * mult * dim, ld, N.ptr(glog),
-                                              N.stream_ptr(dev))
+            if cm:
+                rc = N.lib().feq_attn_softmax_bwd_cm(N.ptr(qs), N.ptr(qs) + 4 * mult, two_mult, Nn * two_mult,
+                                                     dim, N.ptr(dst), N.ptr(src), Nn, N.ptr(attn), N.ptr(ga),
+                                                     E, heads, mult // heads, N.ptr(scale_t), N.ptr(perm),
+                                                     N.ptr(offsets), num_nodes, N.ptr(perm_s),
+                                                     N.ptr(offsets_s), N.ptr(gqk), N.ptr(gqk) + 4 * mult,
+                                                     N.ptr(glog), N.stream_ptr(dev))
+            else:
+                rc = N.lib().feq_attn_softmax_bwd(N.ptr(qs), ld, N.ptr(qs) + 4 * mult * dim, ld,
+                                                  N.ptr(dst), N.ptr(src), Nn, N.ptr(attn), N.ptr(ga),
+                                                  E, heads, Dh, N.ptr(scale_t), N.ptr(perm),
+                                                  N.ptr(offsets), num_nodes, N.ptr(perm_s),
+                                                  N.ptr(offsets_s), N.ptr(gqk), ld,
+                                                  N.ptr(gqk) + 4 * mult * dim, ld, N.ptr(glog),
+                                                  N.stream_ptr(dev))
         N.check(rc, "feq_attn_softmax_bwd")
         g_dist, g_log = _softmax_scalar_grads(glog, qkv, need[1], need[2], decay, rdt, ldt)
-        return (gqk.to(qdt), g_dist, g_log, None, None, None, None, None, None, None, None, None)
+        return (gqk.to(qdt), g_dist, g_log, None, None, None, None, None, None, None, None, None, None)
 
 
 class AttnPoolFn(torch.autograd.Function):

@@ -497,6 +497,27 @@ int feq_attn_softmax_bwd(const float* Q, int64_t ldq, const float* K, int64_t ld
                          const int32_t* offsets, int64_t num_nodes, const int32_t* perm_k,
                          const int32_t* offsets_k, float* grad_Q, int64_t ldgq, float* grad_K,
                          int64_t ldgk, float* grad_logits, feq_stream_t stream);
+/* The node form of feq_attn_softmax_fwd / _bwd on component-major node tables:
+ * element (node n, channel c, component d) of Q, K, grad_Q and grad_K at
+ * [d * comp_stride + n * ld + c] (the layout the fused QK projection writes:
+ * Q = channels [0, mult), K = the same table from channel mult on), head h
+ * the channels [h * head_channels, (h + 1) * head_channels) of every component
+ * (head_dim = head_channels * dim).  The weights, logits and gradients are the
+ * node-major form's up to the order of each head's dot-product sum.  No
+ * counterpart in the reference (its Q and K are edge tensors). */
+int feq_attn_softmax_fwd_cm(const float* Q, const float* K, int64_t ld, int64_t comp_stride,
+                            int32_t dim, const int64_t* q_idx, const int64_t* k_idx, int64_t num_k,
+                            const float* dist, int64_t num_edges, int32_t heads,
+                            int32_t head_channels, const float* scale, float decay,
+                            const int32_t* perm, const int32_t* offsets, int64_t num_nodes,
+                            float* attn, float* qk_out, feq_stream_t stream);
+int feq_attn_softmax_bwd_cm(const float* Q, const float* K, int64_t ld, int64_t comp_stride,
+                            int32_t dim, const int64_t* q_idx, const int64_t* k_idx, int64_t num_k,
+                            const float* attn, const float* grad_attn, int64_t num_edges,
+                            int32_t heads, int32_t head_channels, const float* scale,
+                            const int32_t* perm, const int32_t* offsets, int64_t num_nodes,
+                            const int32_t* perm_k, const int32_t* offsets_k, float* grad_Q,
+                            float* grad_K, float* grad_logits, feq_stream_t stream);
 /* out[n,c,:] = sum_{e in seg(n)} attn[e, c / (mult/H)] * V[e,c,:]; V (E, mult, dim). */
 int feq_attn_pool_fwd(const float* V, const float* attn, int64_t num_edges, int32_t mult,
                       int32_t dim, int32_t heads, const int32_t* perm, const int32_t* offsets,

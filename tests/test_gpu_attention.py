@@ -33,7 +33,10 @@ def _graph(Nn, E, g, empty_tail=3):
     (40, 900, 130, 1, 65),      # 65 heads of 2 floats: two head passes of 64
     (50, 700, 16, 9, 1),        # one head of 144 floats: 64-lane group
 ])
-def test_node_form_matches_oracle(dev, Nn, E, mult, dim, H):
+@pytest.mark.parametrize("cm", [False, True])
+def test_node_form_matches_oracle(dev, Nn, E, mult, dim, H, cm):
+    """cm: the table component-major (dim, N, 2 mult), as the fused QK
+    projection writes it (feq_attn_softmax_fwd_cm / _bwd_cm)."""
     g = torch.Generator().manual_seed(Nn + E + H)
     src, dst = _graph(Nn, E, g)
     qk = torch.randn(Nn, 2 * mult, dim, generator=g)
@@ -41,9 +44,10 @@ def test_node_form_matches_oracle(dev, Nn, E, mult, dim, H):
     graph = fe.Graph(src.to(dev), dst.to(dev), Nn)
     Dh = mult // H * dim
     att = fe.EquivariantEdgeAttention(num_heads=H, qk_dim=Dh, distance_decay_scale=2.5).to(dev)
-    qg = qk.to(dev).requires_grad_(True)
+    qin = qk.permute(2, 0, 1).contiguous() if cm else qk
+    qin = qin.to(dev).requires_grad_(True)
     rg = r.to(dev).requires_grad_(True)
-    a = att.node_attention_weights(qg, graph, rg)
+    a = att.node_attention_weights(qin, graph, rg, cm)
     qd, rd = qk.double().requires_grad_(True), r.double().requires_grad_(True)
     ls = att.log_scale.detach().double().cpu().requires_grad_(True)
     Qe = qd[dst, :mult].reshape(E, H, Dh)
@@ -54,15 +58,16 @@ def test_node_form_matches_oracle(dev, Nn, E, mult, dim, H):
     ga = torch.randn(E, H, generator=g)
     a.backward(ga.to(dev))
     aref.backward(ga.double())
-    assert rel_err(qg.grad, qd.grad) < TOL
+    qgrad = qin.grad.permute(1, 2, 0) if cm else qin.grad
+    assert rel_err(qgrad, qd.grad) < TOL
     assert rel_err(rg.grad, rd.grad) < TOL
     assert rel_err(att.log_scale.grad, ls.grad) < TOL
     # nodes without incoming edges: zero Q gradient; nodes without outgoing
     # edges: zero K gradient
     no_in = torch.bincount(dst, minlength=Nn) == 0
-    assert torch.all(qg.grad.cpu()[no_in, :mult] == 0)
+    assert torch.all(qgrad.cpu()[no_in, :mult] == 0)
     no_out = torch.bincount(src, minlength=Nn) == 0
-    assert torch.all(qg.grad.cpu()[no_out, mult:] == 0)
+    assert torch.all(qgrad.cpu()[no_out, mult:] == 0)
 
 
 def test_node_form_equals_edge_form(dev):

@@ -9,8 +9,8 @@ products and sum in float64), ragged lengths (vectorised body and scalar
 tail), gamma without gradient, the MLP's component-major branch
 (feq_scale_add_cm, against the same formulas), the separable norm's
 component-major output (bit for bit the node-major kernels' values), and the
-block's launch log (the fused kernels; transposes only at the QK
-projection's output, for the attention's node-major rows).
+block's launch log (the fused kernels, and no transposes: the attention
+reads the QK projection's component-major table).
 """
 import pytest
 import torch
@@ -80,7 +80,7 @@ def test_block_uses_the_fused_residuals(dev):
     assert launched.get("k_scale_add_cm", (0,))[0] == 1, launched
     assert launched.get("k_scale_add_cm_bwd", (0,))[0] == 1, launched
     ntr = sum(v[0] for k, v in launched.items() if k.startswith("k_transpose"))
-    assert ntr == 2, launched      # the QK projection's output, forward and backward
+    assert ntr == 0, launched      # the attention reads the projection's component-major table
     assert blk.layer_scale_attn.gamma.grad is not None and blk.layer_scale_mlp.gamma.grad is not None
 
 
