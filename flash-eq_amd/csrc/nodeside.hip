@@ -21,7 +21,7 @@ namespace {
 
 constexpr int kWaves = 4;                          // nodes per workgroup, one per wave
 constexpr int kMaxS = FEQ_NODE_MAX_SCALARS;
-constexpr int kBwdGroups = 1024;                   // workgroups of the backward norm kernels (4 per CU)
+constexpr int kBwdGroups = 1536;                   // workgroups of the backward norm kernels (6 per CU: whole rounds at 2 or 3 resident)
 constexpr int kStageRow = 1152;                    // node rows (mult * dim floats) staged in LDS
 constexpr int kRowThreads = 256;
 
@@ -260,6 +260,14 @@ struct RowPrefetch {
     }
 };
 
+// Workgroups per CU the norm backward kernels are compiled for: three (at
+// most 168 VGPRs) where one channel per lane and the staged rows fit without
+// spilling, so that more nodes' rows are in flight; otherwise no bound (the
+// compiler's choice).  `heavy`: the forms that do not fit 168 (the
+// component-major gradient read with 4-byte accesses, and the separable
+// norm's component-major form with an addend).
+constexpr int norm_bwd_blocks(int cpl, bool stage, bool heavy) { return cpl == 1 && stage && !heavy ? 3 : 1; }
+
 // The rows of an addend to the input gradient (a second branch's gradient of
 // the same input, summed here instead of in a separate pass): loaded when a
 // node's computation starts, in flight during it, and added as the node's
@@ -404,9 +412,11 @@ k_sepnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __re
 // Per-wave partials: pS, pB (mult, ns) of gy (v - mu) / den and gy; pH (mult) of
 // sum_d gy v / rms.
 // CMG (with STAGE): gy is component-major (dim, N, mult); x and gx node-major.
-// ADD (with STAGE): gx = the norm's input gradient + ga (node-major).
-template <int CPL, bool STAGE, bool CMG = false, bool VEC = false, bool ADD = false>
-__global__ void __launch_bounds__(64 * kWaves)
+// ADD (with STAGE): gx = the norm's input gradient + ga (node-major).  NSM:
+// the most scalar irreps the instance handles (1, the common case, keeps the
+// per-wave parameter partials to two registers per channel).
+template <int CPL, bool STAGE, bool CMG = false, bool VEC = false, bool ADD = false, int NSM = kMaxS>
+__global__ void __launch_bounds__(64 * kWaves, norm_bwd_blocks(CPL, STAGE, CMG && ((ADD && NSM > 1) || !VEC)))
 k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __restrict__ x,
               const float* __restrict__ ws, const float* __restrict__ wh, float eps,
               float* __restrict__ gx, float* __restrict__ pS, float* __restrict__ pB,
@@ -419,12 +429,12 @@ k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __r
     const int64_t row = static_cast<int64_t>(L.mult) * L.dim;
     const float fm = static_cast<float>(L.mult);
     const float cnt = fm * L.nhc;
-    float aS[CPL][kMaxS], aB[CPL][kMaxS], aH[CPL];
+    float aS[CPL][NSM], aB[CPL][NSM], aH[CPL];
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
         aH[i] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kMaxS; ++j) aS[i][j] = aB[i][j] = 0.0f;
+        for (int j = 0; j < NSM; ++j) aS[i][j] = aB[i][j] = 0.0f;
     }
     __shared__ __align__(16) float lds[STAGE ? 2 * kWaves * kStageRow : 1];
     float* sx = lds + (threadIdx.x >> 6) * 2 * kStageRow;
@@ -452,7 +462,7 @@ k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __r
         const float* gn = STAGE ? sg : gy + n * row;
         float* on = STAGE ? sg : gx + n * row;
 #pragma unroll
-        for (int j = 0; j < kMaxS; ++j) {
+        for (int j = 0; j < NSM; ++j) {
             if (j >= L.ns) break;
             const int d = L.spos[j];
             double v[CPL], gp[CPL];
@@ -542,7 +552,7 @@ k_sepnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __r
         if (c >= L.mult) continue;
         if (pH) pH[wave * L.mult + c] = aH[i];
 #pragma unroll
-        for (int j = 0; j < kMaxS; ++j) {
+        for (int j = 0; j < NSM; ++j) {
             if (j >= L.ns) break;
             pS[(wave * L.mult + c) * L.ns + j] = aS[i][j];
             pB[(wave * L.mult + c) * L.ns + j] = aB[i][j];
@@ -716,7 +726,7 @@ k_eqnorm_fwd(NodeL L, int64_t N, const float* __restrict__ x, const float* __res
 // CMG (with STAGE): gy component-major (dim, N, mult); x and gx node-major.
 // ADD (with STAGE): gx = the norm's input gradient + ga (node-major).
 template <int CPL, bool STAGE, bool CMG = false, bool VEC = false, bool ADD = false>
-__global__ void __launch_bounds__(64 * kWaves)
+__global__ void __launch_bounds__(64 * kWaves, norm_bwd_blocks(CPL, STAGE, CMG && !VEC))
 k_eqnorm_bwd(NodeL L, int64_t N, const float* __restrict__ gy, const float* __restrict__ x,
              const float* __restrict__ w, const float* __restrict__ b, float eps, float ln_eps,
              float* __restrict__ gx, float* __restrict__ pW, float* __restrict__ pB,
@@ -1260,13 +1270,14 @@ int sepnorm_bwd(const int32_t* lvals, int32_t nreps, int32_t mult, int64_t N, co
     float* pH = pB + partial_floats(w, nsc);
     if (cm) {
         FEQ_ADD_DISPATCH(ga != nullptr, FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH_S(cpl_of(L.mult), {
-            auto k = k_sepnorm_bwd<cpl, true, true, vec, add>;
+            auto k = L.ns <= 1 ? k_sepnorm_bwd<cpl, true, true, vec, add, 1> : k_sepnorm_bwd<cpl, true, true, vec, add>;
             FEQ_LAUNCH("k_sepnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
                        s, L, N, gy, x, w_s, w_h, eps, gx, pS, pB, L.nhc ? pH : nullptr, ga);
         })))
     } else {
         FEQ_ADD_DISPATCH(ga != nullptr, FEQ_VEC_DISPATCH(L.vec, FEQ_NODE_DISPATCH(L, {
-            auto k = k_sepnorm_bwd<cpl, stage, false, stage && vec, stage && add>;
+            auto k = L.ns <= 1 ? k_sepnorm_bwd<cpl, stage, false, stage && vec, stage && add, 1>
+                               : k_sepnorm_bwd<cpl, stage, false, stage && vec, stage && add>;
             FEQ_LAUNCH("k_sepnorm_bwd", k, dim3(static_cast<unsigned>(w / kWaves)), dim3(64 * kWaves), 0,
                        s, L, N, gy, x, w_s, w_h, eps, gx, pS, pB, L.nhc ? pH : nullptr, ga);
         })))
