@@ -454,19 +454,28 @@ int reduce_partials_multi(const PartialJob* jobs, int njobs, hipStream_t s) {
 
 namespace {
 
-constexpr int kHistGroups = 256;           // histogram workgroups (fixed: the order is set by E alone)
+constexpr int kHistCUs = 256;              // histogram workgroups per CU-round (fixed: the order is set by E alone)
 constexpr size_t kHistLds = 160 * 1024;
 
-// Waves (private histograms) per histogram workgroup.
-int hist_waves(const feq_binning& B, int kw) {
+// Launch shape of the histogram kernel: waves (private histograms) per
+// workgroup and workgroups.  Rows small enough for six histograms in a CU's
+// LDS take workgroups of two waves, three or four per CU (more waves resident,
+// each walking fewer edges: the walk is bound by LDS and load latency, not by
+// bandwidth); otherwise up to four waves in one workgroup per CU.  The shape
+// depends on the layout alone, so the summation order is fixed.
+struct HistShape {
+    int waves, groups;
+};
+HistShape hist_shape(const feq_binning& B, int kw) {
     const size_t hbytes = 4 * static_cast<size_t>(B.num_bins + 1) * kw;
-    const size_t w = kHistLds / hbytes;
-    return static_cast<int>(w < 4 ? w : 4);
+    const size_t per_cu = kHistLds / hbytes;
+    if (per_cu >= 6) return {2, kHistCUs * static_cast<int>(per_cu >= 8 ? 4 : 3)};
+    return {static_cast<int>(per_cu < 4 ? per_cu : 4), kHistCUs};
 }
 
 // The LDS histograms serve rows for which at least two fit a workgroup's LDS;
 // wider rows take the sorted-bin form.
-bool use_hist(const feq_binning& B, int kw) { return hist_waves(B, kw) >= 2; }
+bool use_hist(const feq_binning& B, int kw) { return hist_shape(B, kw).waves >= 2; }
 
 // Workspace of the binned gradient, carved from `tail` in this order.
 struct BinWs {
@@ -487,8 +496,9 @@ BinWs bin_ws(const feq_binning& B, int kw, int64_t E, int groups, int64_t ncc, v
     size_t tmp = reduce_tmp_floats(groups, ncc) + 1;
     if (use_hist(B, kw)) {
         // per-workgroup histogram partials
-        w.part = cv.take<float>(static_cast<size_t>(kHistGroups) * hsz);
-        tmp = std::max(tmp, reduce_tmp_floats(kHistGroups, hsz));
+        const int groups = hist_shape(B, kw).groups;
+        w.part = cv.take<float>(static_cast<size_t>(groups) * hsz);
+        tmp = std::max(tmp, reduce_tmp_floats(groups, hsz));
     } else {
         const int64_t ntiles = ceil_div(E, kBinTile);
         w.keys = cv.take<int64_t>(E);
@@ -524,21 +534,22 @@ int ew_tail(const feq_layout& L, const feq_binning& B, int K, int64_t E, const f
     }
     const BinWs w = bin_ws(B, kw, E, groups, ncc, tail);
     if (use_hist(B, kw)) {
-        const int waves = hist_waves(B, kw);
+        const HistShape hs = hist_shape(B, kw);
+        const int waves = hs.waves;
         const size_t hlds = 4 * static_cast<size_t>(waves) * (nb + 1) * kw;
-        const int64_t per_wave = ceil_div(E, static_cast<int64_t>(kHistGroups) * waves);
+        const int64_t per_wave = ceil_div(E, static_cast<int64_t>(hs.groups) * waves);
         if (kw % 2 == 0 && reinterpret_cast<uintptr_t>(dFe) % 8 == 0) {
             FEQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_ewm_hist<true>),
                                         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kHistLds)));
-            FEQ_LAUNCH("k_ewm_hist", k_ewm_hist<true>, dim3(kHistGroups), dim3(64 * waves), hlds, s, B, kw, 0,
+            FEQ_LAUNCH("k_ewm_hist", k_ewm_hist<true>, dim3(hs.groups), dim3(64 * waves), hlds, s, B, kw, 0,
                        kw, E, per_wave, dist, dFe, w.part);
         } else {
             FEQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_ewm_hist<false>),
                                         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kHistLds)));
-            FEQ_LAUNCH("k_ewm_hist", k_ewm_hist<false>, dim3(kHistGroups), dim3(64 * waves), hlds, s, B, kw, 0,
+            FEQ_LAUNCH("k_ewm_hist", k_ewm_hist<false>, dim3(hs.groups), dim3(64 * waves), hlds, s, B, kw, 0,
                        kw, E, per_wave, dist, dFe, w.part);
         }
-        if (int rc = reduce_partials(w.part, kHistGroups, (nb + 1) * static_cast<int64_t>(kw), gF, w.tmp, s))
+        if (int rc = reduce_partials(w.part, hs.groups, (nb + 1) * static_cast<int64_t>(kw), gF, w.tmp, s))
             return rc;
     } else {
         FEQ_LAUNCH("k_ewm_keys", k_ewm_keys, dim3(ceil_div(E, kThreads)), dim3(kThreads), 0, s, B, E,
