@@ -160,3 +160,19 @@ def test_eqlinear_queries_and_argument_errors():
     rc = lib.feq_eqlinear_bwd_w(lv, 3, 10, 64, 128, None, None, 1, None, None, ctypes.c_void_p(256), None, 0,
                                 None)
     assert rc != 0 and "bias columns" in lib.feq_last_error().decode()
+
+
+def test_component_major_attention_argument_checks():
+    """feq_attn_softmax_fwd_cm / _bwd_cm: invalid sizes and the edge form
+    (no node indices) are refused before any launch."""
+    lib = N.load_library()
+    one = ctypes.c_void_p(256)          # never dereferenced: the checks fail first
+    rc = lib.feq_attn_softmax_fwd_cm(one, one, 128, 0, 9, one, one, 10, None, 5, 8, 8, one, 0.0, one, one,
+                                     10, one, None, None)
+    assert rc != 0 and "invalid sizes" in lib.feq_last_error().decode()
+    rc = lib.feq_attn_softmax_fwd_cm(one, one, 128, 1280, 9, None, None, 10, None, 5, 8, 8, one, 0.0, one, one,
+                                     10, one, None, None)
+    assert rc != 0 and "node tables" in lib.feq_last_error().decode()
+    rc = lib.feq_attn_softmax_bwd_cm(one, one, 128, 1280, 0, one, one, 10, one, one, 5, 8, 8, one, one, one, 10,
+                                     one, one, one, one, one, None)
+    assert rc != 0 and "invalid sizes" in lib.feq_last_error().decode()
