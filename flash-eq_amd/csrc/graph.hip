@@ -48,6 +48,29 @@ k_segment_sum(const float* __restrict__ x, int64_t row, const int32_t* __restric
     }
 }
 
+// Short rows (coordinates: 3 floats), one node per thread, the same
+// summation order.
+constexpr int64_t kShortSegRow = 16;
+__global__ void __launch_bounds__(256)
+k_segment_sum_short(const float* __restrict__ x, int64_t row, const int32_t* __restrict__ perm,
+                    const int32_t* __restrict__ offsets, int64_t N, float* __restrict__ out) {
+    const int64_t n = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (n >= N) return;
+    const int b = offsets[n], e_end = offsets[n + 1];
+    float acc[kShortSegRow];
+#pragma unroll
+    for (int c = 0; c < kShortSegRow; ++c) acc[c] = 0.0f;
+    for (int i = b; i < e_end; ++i) {
+        const float* xr = x + static_cast<int64_t>(perm[i]) * row;
+#pragma unroll
+        for (int c = 0; c < kShortSegRow; ++c)
+            if (c < row) acc[c] += xr[c];
+    }
+#pragma unroll
+    for (int c = 0; c < kShortSegRow; ++c)
+        if (c < row) out[n * row + c] = acc[c];
+}
+
 // 16-byte variants for rows of whole float4s (row4 = row / 4): one thread per
 // float4 of the output (gather) or per float4 column of a node (segment sum).
 __global__ void k_segment_sum4(const float4* __restrict__ x, int64_t row4,
@@ -105,6 +128,18 @@ __global__ void k_gather_rows(const float* __restrict__ src, int64_t row,
     const bool ok = s >= 0 && s < nsrc;
     for (int64_t c = threadIdx.x; c < row; c += blockDim.x)
         out[r * row + c] = ok ? src[s * row + c] : 0.0f;
+}
+
+// Short rows (coordinates: 3 floats), one row per thread.
+constexpr int64_t kShortRow = 16;
+__global__ void __launch_bounds__(256)
+k_gather_rows_short(const float* __restrict__ src, int64_t row, const int64_t* __restrict__ idx, int64_t nrows,
+                    int64_t nsrc, float* __restrict__ out) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (r >= nrows) return;
+    const int64_t s = idx[r];
+    const bool ok = s >= 0 && s < nsrc;
+    for (int64_t c = 0; c < row; ++c) out[r * row + c] = ok ? src[s * row + c] : 0.0f;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -186,6 +221,11 @@ extern "C" int feq_segment_sum(const float* x, int64_t row, const int32_t* perm,
                    reinterpret_cast<float4*>(out));
         return FEQ_OK;
     }
+    if (row <= kShortSegRow) {
+        FEQ_LAUNCH("k_segment_sum", k_segment_sum_short, dim3(static_cast<unsigned>(ceil_div(N, 256))), dim3(256),
+                   0, stream_of(stream), x, row, perm, offsets, N, out);
+        return FEQ_OK;
+    }
     FEQ_LAUNCH("k_segment_sum", k_segment_sum, dim3(N), dim3(kThreads), 0, stream_of(stream), x, row, perm,
                        offsets, out);
     return FEQ_OK;
@@ -200,6 +240,11 @@ extern "C" int feq_gather_rows(const float* src, int64_t nsrc, int64_t row, cons
         FEQ_LAUNCH("k_gather_rows", k_gather_rows4, dim3(static_cast<unsigned>(ceil_div(nrows, 4))),
                    dim3(256), 0, stream_of(stream), reinterpret_cast<const float4*>(src), row / 4,
                    idx, nrows, nsrc, reinterpret_cast<float4*>(out));
+        return FEQ_OK;
+    }
+    if (row <= kShortRow) {
+        FEQ_LAUNCH("k_gather_rows", k_gather_rows_short, dim3(static_cast<unsigned>(ceil_div(nrows, 256))),
+                   dim3(256), 0, stream_of(stream), src, row, idx, nrows, nsrc, out);
         return FEQ_OK;
     }
     FEQ_LAUNCH("k_gather_rows", k_gather_rows, dim3(nrows), dim3(row < 256 ? 64 : 256), 0,

@@ -195,11 +195,13 @@ def test_edge_softmax_parity_and_sum_to_one(dev):
     assert rel_err(att.log_scale.grad, ls.grad) < TOL
 
 
-@pytest.mark.parametrize("row_shape", [(64, 9), (3, 5), (4,)])
+@pytest.mark.parametrize("row_shape", [(64, 9), (3, 5), (4,), (3,), (17,)])
 def test_gather_src_dst_and_grad(dev, row_shape):
     """Graph.gather_src / gather_dst equal x[src] / x[dst] exactly; their backward
     (segmented sums over the cached CSRs) matches a float64 index_add, including
-    nodes without edges.  (64, 9) and (4,) rows take the 16-byte kernels."""
+    nodes without edges.  (64, 9) and (4,) rows take the 16-byte kernels, rows
+    of at most 16 other floats (coordinates) a row per thread, (17,) the
+    workgroup-per-row kernels."""
     g = torch.Generator().manual_seed(21)
     N, E = 37, 400
     src = torch.randint(0, N - 3, (E,), generator=g)      # the last nodes have no edges
