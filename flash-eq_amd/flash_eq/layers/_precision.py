@@ -37,11 +37,34 @@ def _up(v):
     return v
 
 
+def _up_all(named) -> dict:
+    """float32 copies of named tensors: those of one half-precision dtype and
+    device are cast together (one concatenation and one cast, split back into
+    views: two launches instead of one per tensor, and one for their
+    gradients); the rest one by one."""
+    named = list(named)
+    out, groups = {}, {}
+    for k, v in named:
+        if (isinstance(v, torch.Tensor) and v.is_floating_point() and v.dtype in HALF
+                and v.numel() > 0):
+            groups.setdefault((v.dtype, v.device), []).append((k, v))
+        else:
+            out[k] = _up(v)
+    for items in groups.values():
+        if len(items) == 1:
+            out[items[0][0]] = _up(items[0][1])
+            continue
+        flat = torch.cat([v.reshape(-1) for _, v in items]).float()
+        for (k, v), piece in zip(items, torch.split(flat, [v.numel() for _, v in items])):
+            out[k] = piece.view(v.shape)
+    return out
+
+
 def run_float32(module: nn.Module, dtype: torch.dtype, args: tuple, kwargs: dict):
     """``module(*args, **kwargs)`` with float32 copies of its floating
     parameters, buffers and tensor arguments; the output cast to ``dtype``."""
-    state = {k: _up(p) for k, p in module.named_parameters()}
-    state.update({k: _up(b) for k, b in module.named_buffers()})
+    state = _up_all(module.named_parameters())
+    state.update(_up_all(module.named_buffers()))
     seen = {}
 
     def up(v):   # one float32 copy per distinct argument (P passed as P and Q: one cast)
