@@ -137,22 +137,26 @@ def test_component_major_norm_output_is_the_transpose(dev, kind, mult):
 
 
 @pytest.mark.parametrize("cm", [False, True])
-@pytest.mark.parametrize("mult", [64, 6])
+@pytest.mark.parametrize("lvals,mult", [([0, 1, 2], 64), ([0, 1, 2], 6), ([0, 0, 1, 2], 8), ([0, 1, 2], 128)])
 @pytest.mark.parametrize("kind", ["separable", "equivariant"])
-def test_norm_pair_adds_the_second_branch_gradient(dev, kind, mult, cm):
+def test_norm_pair_adds_the_second_branch_gradient(dev, kind, lvals, mult, cm):
     """forward_pair returns (norm(x), x); the second output's gradient is added
     inside the norm's backward kernel (feq_*norm_bwd_add): x.grad is bitwise
     the norm's input gradient plus that gradient, as autograd's separate sum
-    gives it; the parameter gradients are unchanged."""
+    gives it; the parameter gradients are unchanged.  Layouts: 16-byte rows
+    (64), 4-byte rows (6), two scalar irreps (the separable norm's general
+    instance), two channels per lane (128)."""
     torch.manual_seed(2)
     cls = fe.SeparableEquivariantLayerNorm if kind == "separable" else fe.EquivariantLayerNorm
-    norm = cls(fe.Repr([0, 1, 2], mult)).to(dev)
+    rp = fe.Repr(lvals, mult)
+    norm = cls(rp).to(dev)
     with torch.no_grad():
         for p in norm.parameters():
             p.normal_()
-    x = torch.randn(501, mult, 9, device=dev)
-    gy = torch.randn(501, mult, 9, device=dev)
-    ga = torch.randn(501, mult, 9, device=dev)
+    dim = rp.dim()
+    x = torch.randn(501, mult, dim, device=dev)
+    gy = torch.randn(501, mult, dim, device=dev)
+    ga = torch.randn(501, mult, dim, device=dev)
     gyl = gy.permute(2, 0, 1).contiguous() if cm else gy
     x1 = x.clone().requires_grad_(True)
     y1 = norm.forward_cm(x1) if cm else norm(x1)
