@@ -408,6 +408,41 @@ k_scale_add(const float* __restrict__ x, const float* __restrict__ y, const floa
     }
 }
 
+// out = tables[0] + tables[1] + ... (in that order) over n floats: the
+// gradients of a tensor that several consumers read, summed in one pass.
+constexpr int kMaxTables = 16;
+struct Tables {
+    const float* p[kMaxTables];
+};
+
+__global__ void __launch_bounds__(256)
+k_sum_tables(Tables T, int nt, int64_t n, int vec, float* __restrict__ out) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (vec) {
+        const int64_t n4 = n / 4;
+        for (int64_t i = t0; i < n4; i += stride) {
+            float4 a = reinterpret_cast<const float4*>(T.p[0])[i];
+            for (int j = 1; j < nt; ++j) {
+                const float4 b = reinterpret_cast<const float4*>(T.p[j])[i];
+                a = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+            }
+            reinterpret_cast<float4*>(out)[i] = a;
+        }
+        for (int64_t i = 4 * n4 + t0; i < n; i += stride) {
+            float a = T.p[0][i];
+            for (int j = 1; j < nt; ++j) a += T.p[j][i];
+            out[i] = a;
+        }
+    } else {
+        for (int64_t i = t0; i < n; i += stride) {
+            float a = T.p[0][i];
+            for (int j = 1; j < nt; ++j) a += T.p[j][i];
+            out[i] = a;
+        }
+    }
+}
+
 unsigned stream_grid(int64_t n) {
     const int64_t g = (n / 4 + 255) / 256;
     return static_cast<unsigned>(g < 4096 ? (g < 1 ? 1 : g) : 4096);
@@ -491,6 +526,24 @@ extern "C" int feq_scale_add(const float* x, const float* y, const float* scale,
     if (!x || !y || !scale || !out) return fail(FEQ_ERR_INVALID, "NULL pointer");
     FEQ_LAUNCH("k_scale_add", k_scale_add<true>, dim3(stream_grid(n)), dim3(256), 0, stream_of(stream), x, y,
                scale, n, out);
+    return FEQ_OK;
+}
+
+extern "C" int feq_sum_tables(const float* const* tables, int32_t num_tables, int64_t n, float* out,
+                              feq_stream_t stream) {
+    if (n < 0 || num_tables < 1 || num_tables > kMaxTables)
+        return fail(FEQ_ERR_INVALID, "sum of tables: 1 to %d tables of n >= 0 floats", kMaxTables);
+    if (n == 0) return FEQ_OK;
+    if (!tables || !out) return fail(FEQ_ERR_INVALID, "NULL pointer");
+    Tables T{};
+    bool vec = (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+    for (int j = 0; j < num_tables; ++j) {
+        if (!tables[j]) return fail(FEQ_ERR_INVALID, "NULL table");
+        T.p[j] = tables[j];
+        vec = vec && (reinterpret_cast<uintptr_t>(tables[j]) & 15u) == 0;
+    }
+    FEQ_LAUNCH("k_sum_tables", k_sum_tables, dim3(stream_grid(n)), dim3(256), 0, stream_of(stream), T,
+               int(num_tables), n, int(vec), out);
     return FEQ_OK;
 }
 

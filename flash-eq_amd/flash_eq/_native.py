@@ -113,6 +113,7 @@ _SIGS = {
     "feq_sepnorm_fwd_cm": ([_P, _I32, _I32, _I64, _P, _P, _P, _P, _F, _P, _P], ctypes.c_int),
     "feq_sepnorm_bwd_cm": ([_P, _I32, _I32, _I64, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _SZ, _P],
                            ctypes.c_int),
+    "feq_sum_tables": ([_P, _I32, _I64, _P, _P], ctypes.c_int),
     "feq_sepnorm_bwd_add": ([_P, _I32, _I32, _I64, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _SZ, _I32,
                              _P], ctypes.c_int),
     "feq_scale_add_cm": ([_P, _P, _P, _I64, _I32, _I32, _P, _P], ctypes.c_int),

@@ -12,7 +12,7 @@ import torch.nn as nn
 
 from ..graph import Graph
 from ..representations import Repr, WignerDBasis
-from ..ops import ResidualScaleCmFn, ResidualScaleFn, ScaleFn
+from ..ops import FanOutFn, ResidualScaleCmFn, ResidualScaleFn, ScaleFn
 from .attention import EquivariantAttention
 from .gating import EquivariantGating
 from .linear import EquivariantLinear
@@ -185,9 +185,17 @@ class EquivariantTransformer(nn.Module):
         distances = vec.norm(dim=-1)
         m_in, m_hidden, m_out = self.basis(vec)
         x = node_features
-        for i, layer in enumerate(self.layers):
-            P = m_in if i == 0 else m_hidden
-            Q = m_out if i == self.num_layers - 1 else m_hidden
+        uses = [(m_in if i == 0 else m_hidden, m_out if i == self.num_layers - 1 else m_hidden)
+                for i in range(self.num_layers)]
+        if m_hidden.requires_grad and m_hidden.is_cuda and m_hidden.dtype == torch.float32:
+            # the hidden bases feed every layer (as P and as Q): their gradients
+            # are summed in one pass (FanOutFn) rather than pairwise by autograd
+            k = sum((P is m_hidden) + (Q is m_hidden) for P, Q in uses)
+            if 1 < k <= 16:
+                views = iter(FanOutFn.apply(m_hidden, k))
+                uses = [(next(views) if P is m_hidden else P, next(views) if Q is m_hidden else Q)
+                        for P, Q in uses]
+        for layer, (P, Q) in zip(self.layers, uses):
             x = layer(P, Q, x, distances, graph)
         return self.final_norm(x)
 

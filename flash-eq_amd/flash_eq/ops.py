@@ -1271,6 +1271,38 @@ def rows_weight_grad(gy: torch.Tensor, x: torch.Tensor, dtype: torch.dtype,
     return gw.to(dtype)
 
 
+class FanOutFn(torch.autograd.Function):
+    """k views of one tensor for k consumers; the backward sums their
+    gradients in one pass (feq_sum_tables, in consumer order) where autograd
+    would add them pairwise (k - 1 passes over three tables each)."""
+
+    @staticmethod
+    def forward(ctx, x, k: int):
+        ctx.set_materialize_grads(False)
+        return tuple(x.view_as(x) for _ in range(k))
+
+    @staticmethod
+    def backward(ctx, *grads):
+        gs = [g for g in grads if g is not None]
+        if not gs:
+            return None, None
+        if len(gs) == 1:
+            return gs[0], None
+        if (all(g.is_cuda and g.dtype == torch.float32 and g.shape == gs[0].shape for g in gs)
+                and len(gs) <= 16):
+            gc = [g.contiguous() for g in gs]
+            out = torch.empty_like(gc[0])
+            ptrs = (N.ctypes.c_void_p * len(gc))(*[g.data_ptr() for g in gc])
+            with torch.cuda.device(out.device):
+                rc = N.lib().feq_sum_tables(ptrs, len(gc), out.numel(), N.ptr(out), N.stream_ptr(out.device))
+            N.check(rc, "feq_sum_tables")
+            return out, None
+        out = gs[0].clone()
+        for g in gs[1:]:
+            out += g
+        return out, None
+
+
 class GatingFn(torch.autograd.Function):
     """EquivariantGating (gating.py:54-76): irrep norms and the sigmoid gate
     in kernels (feq_gate_*), the Linear over the flattened norms as a GEMM."""

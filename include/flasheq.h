@@ -706,6 +706,12 @@ int feq_scale_add(const float* x, const float* y, const float* scale, int64_t n,
 int feq_scale_add_bwd(const float* grad_out, const float* y, const float* scale, int64_t n,
                       float* grad_y, float* grad_scale, void* workspace, size_t ws_bytes,
                       feq_stream_t stream);
+/* out = tables[0] + ... + tables[num_tables - 1] (1..16 float32 tables of n
+ * floats, summed in that order): the gradients of a tensor read by several
+ * consumers (the transformer's bases, used by every layer) in one pass instead
+ * of autograd's pairwise sums.  No counterpart in the reference. */
+int feq_sum_tables(const float* const* tables, int32_t num_tables, int64_t n, float* out,
+                   feq_stream_t stream);
 /* The same residual with y component-major (dim, N, mult), x and out node-major
  * (N, mult, dim): the block's MLP output joins the residual stream without a
  * separate transpose.  The backward writes grad_y component-major (may be NULL)

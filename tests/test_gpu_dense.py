@@ -103,3 +103,29 @@ def test_library_launches_the_helpers(dev):
         NAT.profile_enable(False)
     for k in ("k_transpose", "k_colsum", "k_dot_f64"):
         assert k in names, names
+
+
+@pytest.mark.parametrize("n", [1, 5, 1001, 65539])
+@pytest.mark.parametrize("k", [2, 3, 10, 16])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_sum_tables_is_the_ordered_sum(dev, n, k, offset):
+    """feq_sum_tables (through ops.FanOutFn's backward) gives the bits of
+    adding the tables left to right in float32 (16-byte and 4-byte forms)."""
+    g = torch.Generator(device=dev).manual_seed(n + k)
+    base = torch.randn(k, n + offset, device=dev, generator=g)
+    tabs = [base[j, offset:] for j in range(k)]        # offset 1: not 16-byte aligned
+    x = torch.zeros(n, device=dev, requires_grad=True)
+    views = ops.FanOutFn.apply(x, k)
+    sum((v * t).sum() for v, t in zip(views, tabs)).backward()
+    ref = tabs[0].clone()
+    for t in tabs[1:]:
+        ref += t
+    assert torch.equal(x.grad, ref)
+
+
+def test_fan_out_skips_unused_views(dev):
+    """Views without a gradient add nothing; one gradient passes through."""
+    x = torch.zeros(7, device=dev, requires_grad=True)
+    a, b, c = ops.FanOutFn.apply(x, 3)
+    (2.0 * b).sum().backward()
+    assert torch.equal(x.grad, torch.full((7,), 2.0, device=dev))

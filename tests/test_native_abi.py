@@ -176,3 +176,13 @@ def test_component_major_attention_argument_checks():
     rc = lib.feq_attn_softmax_bwd_cm(one, one, 128, 1280, 0, one, one, 10, one, one, 5, 8, 8, one, one, one, 10,
                                      one, one, one, one, one, None)
     assert rc != 0 and "invalid sizes" in lib.feq_last_error().decode()
+
+
+def test_sum_tables_argument_checks():
+    """feq_sum_tables refuses 0 or more than 16 tables and NULL tables before any launch."""
+    lib = N.load_library()
+    ptrs = (ctypes.c_void_p * 2)(256, None)
+    assert lib.feq_sum_tables(ptrs, 0, 10, ctypes.c_void_p(256), None) != 0
+    assert lib.feq_sum_tables(ptrs, 17, 10, ctypes.c_void_p(256), None) != 0
+    assert lib.feq_sum_tables(ptrs, 2, 10, ctypes.c_void_p(256), None) != 0
+    assert "NULL table" in lib.feq_last_error().decode()
