@@ -473,6 +473,15 @@ HistShape hist_shape(const feq_binning& B, int kw) {
     return {static_cast<int>(per_cu < 4 ? per_cu : 4), kHistCUs};
 }
 
+// Workgroups for E edges: the shape's, or fewer for few edges (at least 64
+// edges per wave), so that a small graph does not zero, write and sum hundreds
+// of empty histograms.  Set by E and the layout alone: a fixed order.
+int hist_groups(const feq_binning& B, int kw, int64_t E) {
+    const HistShape hs = hist_shape(B, kw);
+    const int64_t need = ceil_div(E > 0 ? E : 1, static_cast<int64_t>(hs.waves) * 64);
+    return static_cast<int>(need < hs.groups ? need : hs.groups);
+}
+
 // The LDS histograms serve rows for which at least two fit a workgroup's LDS;
 // wider rows take the sorted-bin form.
 bool use_hist(const feq_binning& B, int kw) { return hist_shape(B, kw).waves >= 2; }
@@ -496,7 +505,7 @@ BinWs bin_ws(const feq_binning& B, int kw, int64_t E, int groups, int64_t ncc, v
     size_t tmp = reduce_tmp_floats(groups, ncc) + 1;
     if (use_hist(B, kw)) {
         // per-workgroup histogram partials
-        const int groups = hist_shape(B, kw).groups;
+        const int groups = hist_groups(B, kw, E);
         w.part = cv.take<float>(static_cast<size_t>(groups) * hsz);
         tmp = std::max(tmp, reduce_tmp_floats(groups, hsz));
     } else {
@@ -535,21 +544,21 @@ int ew_tail(const feq_layout& L, const feq_binning& B, int K, int64_t E, const f
     const BinWs w = bin_ws(B, kw, E, groups, ncc, tail);
     if (use_hist(B, kw)) {
         const HistShape hs = hist_shape(B, kw);
-        const int waves = hs.waves;
+        const int waves = hs.waves, groups = hist_groups(B, kw, E);
         const size_t hlds = 4 * static_cast<size_t>(waves) * (nb + 1) * kw;
-        const int64_t per_wave = ceil_div(E, static_cast<int64_t>(hs.groups) * waves);
+        const int64_t per_wave = ceil_div(E, static_cast<int64_t>(groups) * waves);
         if (kw % 2 == 0 && reinterpret_cast<uintptr_t>(dFe) % 8 == 0) {
             FEQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_ewm_hist<true>),
                                         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kHistLds)));
-            FEQ_LAUNCH("k_ewm_hist", k_ewm_hist<true>, dim3(hs.groups), dim3(64 * waves), hlds, s, B, kw, 0,
+            FEQ_LAUNCH("k_ewm_hist", k_ewm_hist<true>, dim3(groups), dim3(64 * waves), hlds, s, B, kw, 0,
                        kw, E, per_wave, dist, dFe, w.part);
         } else {
             FEQ_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_ewm_hist<false>),
                                         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kHistLds)));
-            FEQ_LAUNCH("k_ewm_hist", k_ewm_hist<false>, dim3(hs.groups), dim3(64 * waves), hlds, s, B, kw, 0,
+            FEQ_LAUNCH("k_ewm_hist", k_ewm_hist<false>, dim3(groups), dim3(64 * waves), hlds, s, B, kw, 0,
                        kw, E, per_wave, dist, dFe, w.part);
         }
-        if (int rc = reduce_partials(w.part, hs.groups, (nb + 1) * static_cast<int64_t>(kw), gF, w.tmp, s))
+        if (int rc = reduce_partials(w.part, groups, (nb + 1) * static_cast<int64_t>(kw), gF, w.tmp, s))
             return rc;
     } else {
         FEQ_LAUNCH("k_ewm_keys", k_ewm_keys, dim3(ceil_div(E, kThreads)), dim3(kThreads), 0, s, B, E,
