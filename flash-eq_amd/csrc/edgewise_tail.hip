@@ -343,6 +343,37 @@ __global__ void k_sum_partials(const float* __restrict__ part, int groups, int p
     out[blockIdx.y * n + q] = acc;
 }
 
+// k_sum_partials over several jobs in one launch: job j owns the workgroups
+// [start[j], start[j + 1]), nb[j] per slice; each sums the same partials in
+// the same order as k_sum_partials.
+struct SliceJobs {
+    const float* part[2 * kMaxPartialJobs];
+    float* out[2 * kMaxPartialJobs];
+    int64_t n[2 * kMaxPartialJobs];
+    int groups[2 * kMaxPartialJobs], per_slice[2 * kMaxPartialJobs];
+    int64_t nb[2 * kMaxPartialJobs];
+    int64_t start[2 * kMaxPartialJobs + 1];
+    int count;
+};
+
+__global__ void __launch_bounds__(256)
+k_sum_slices_multi(SliceJobs J) {
+    const int64_t b = blockIdx.x;
+    int j = 0;
+    while (j + 1 < J.count && b >= J.start[j + 1]) ++j;
+    const int64_t local = b - J.start[j], nb = J.nb[j], n = J.n[j];
+    const int slice = static_cast<int>(local / nb);
+    const int64_t q = (local - slice * nb) * 256 + threadIdx.x;
+    if (q >= n) return;
+    const int g0 = slice * J.per_slice[j];
+    const int g1 = g0 + J.per_slice[j] < J.groups[j] ? g0 + J.per_slice[j] : J.groups[j];
+    const float* part = J.part[j];
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int g = g0; g < g1; ++g) acc += part[static_cast<int64_t>(g) * n + q];
+    J.out[j][slice * n + q] = acc;
+}
+
 // Few sums of many partials (n <= kSmallN): a workgroup per output, its
 // threads summing interleaved partials, combined by a fixed tree in LDS.
 __global__ void __launch_bounds__(256)
@@ -430,10 +461,45 @@ int reduce_partials_multi(const PartialJob* jobs, int njobs, hipStream_t s) {
     if (njobs < 1) return FEQ_OK;
     bool small = njobs <= kMaxPartialJobs;
     for (int j = 0; j < njobs && small; ++j) small = jobs[j].n <= kSmallN && jobs[j].groups > kSliceGroups;
-    if (!small) {
+    if (!small && njobs > kMaxPartialJobs) {
         for (int j = 0; j < njobs; ++j)
             if (int rc = reduce_partials(jobs[j].part, jobs[j].groups, jobs[j].n, jobs[j].out, jobs[j].tmp, s))
                 return rc;
+        return FEQ_OK;
+    }
+    if (!small) {
+        // the first slices of every job in one launch, the sums of the slices
+        // in a second (the same sums, in the same order, as reduce_partials;
+        // no partials: zeros); few-output jobs keep their own one-launch form
+        SliceJobs L1{}, L2{};
+        auto add = [](SliceJobs& J, const float* part, int groups, int per_slice, int64_t n, float* out) {
+            const int slices = groups > 0 ? (groups + per_slice - 1) / per_slice : 1;
+            const int k = J.count++;
+            J.part[k] = part;
+            J.out[k] = out;
+            J.n[k] = n;
+            J.groups[k] = groups;
+            J.per_slice[k] = per_slice;
+            J.nb[k] = ceil_div(n, 256);
+            J.start[k + 1] = J.start[k] + J.nb[k] * slices;
+        };
+        for (int j = 0; j < njobs; ++j) {
+            const PartialJob& p = jobs[j];
+            if (p.n <= 0) continue;
+            if (p.n <= kSmallN && p.groups > kSliceGroups) {
+                if (int rc = reduce_partials(p.part, p.groups, p.n, p.out, p.tmp, s)) return rc;
+            } else if (p.groups <= kSliceGroups) {
+                add(L1, p.part, p.groups > 0 ? p.groups : 0, p.groups > 0 ? p.groups : 1, p.n, p.out);
+            } else {
+                const int slices = (p.groups + kSliceGroups - 1) / kSliceGroups;
+                add(L1, p.part, p.groups, kSliceGroups, p.n, p.tmp);
+                add(L2, p.tmp, slices, slices, p.n, p.out);
+            }
+        }
+        for (const SliceJobs* J : {&L1, &L2})
+            if (J->count > 0)
+                FEQ_LAUNCH("k_sum_partials", k_sum_slices_multi, dim3(static_cast<unsigned>(J->start[J->count])),
+                           dim3(256), 0, s, *J);
         return FEQ_OK;
     }
     PartialJobs J{};
@@ -494,7 +560,8 @@ struct BinWs {
     void* csr;
     float* S;
     float* part;
-    float* tmp;
+    float* tmp;    // the channel patterns' partial sums
+    float* htmp;   // the histogram partials' sums (reduced in the same launches)
     size_t bytes;
 };
 
@@ -502,12 +569,13 @@ BinWs bin_ws(const feq_binning& B, int kw, int64_t E, int groups, int64_t ncc, v
     Carver cv(base);
     BinWs w{};
     const int64_t hsz = (B.num_bins + 1) * static_cast<int64_t>(kw);
-    size_t tmp = reduce_tmp_floats(groups, ncc) + 1;
+    const size_t tmp = reduce_tmp_floats(groups, ncc) + 1;
+    size_t htmp = 0;
     if (use_hist(B, kw)) {
         // per-workgroup histogram partials
         const int groups = hist_groups(B, kw, E);
         w.part = cv.take<float>(static_cast<size_t>(groups) * hsz);
-        tmp = std::max(tmp, reduce_tmp_floats(groups, hsz));
+        htmp = reduce_tmp_floats(groups, hsz);
     } else {
         const int64_t ntiles = ceil_div(E, kBinTile);
         w.keys = cv.take<int64_t>(E);
@@ -518,6 +586,7 @@ BinWs bin_ws(const feq_binning& B, int kw, int64_t E, int groups, int64_t ncc, v
         w.part = cv.take<float>(4 * static_cast<size_t>(ntiles) * kw);
     }
     w.tmp = cv.take<float>(tmp);
+    w.htmp = htmp ? cv.take<float>(htmp) : nullptr;
     w.bytes = cv.used + 256;
     return w;
 }
@@ -542,6 +611,8 @@ int ew_tail(const feq_layout& L, const feq_binning& B, int K, int64_t E, const f
         return fill_zero(gF, static_cast<int64_t>(nb + 1) * kw, s);
     }
     const BinWs w = bin_ws(B, kw, E, groups, ncc, tail);
+    PartialJob jobs[2];
+    int njobs = 0;
     if (use_hist(B, kw)) {
         const HistShape hs = hist_shape(B, kw);
         const int waves = hs.waves, groups = hist_groups(B, kw, E);
@@ -558,8 +629,7 @@ int ew_tail(const feq_layout& L, const feq_binning& B, int K, int64_t E, const f
             FEQ_LAUNCH("k_ewm_hist", k_ewm_hist<false>, dim3(groups), dim3(64 * waves), hlds, s, B, kw, 0,
                        kw, E, per_wave, dist, dFe, w.part);
         }
-        if (int rc = reduce_partials(w.part, groups, (nb + 1) * static_cast<int64_t>(kw), gF, w.tmp, s))
-            return rc;
+        jobs[njobs++] = PartialJob{w.part, groups, (nb + 1) * static_cast<int64_t>(kw), gF, w.htmp};
     } else {
         FEQ_LAUNCH("k_ewm_keys", k_ewm_keys, dim3(ceil_div(E, kThreads)), dim3(kThreads), 0, s, B, E,
                    dist, w.keys);
@@ -576,9 +646,9 @@ int ew_tail(const feq_layout& L, const feq_binning& B, int K, int64_t E, const f
     if (gdist)
         FEQ_LAUNCH("k_ewm_dr", k_ewm_dr, dim3(ceil_div(E, kThreads)), dim3(kThreads),
                    sizeof(int) * L.wdim, s, L, B, K, E, dist, F, dFe, gdist);
-    if (groups > 0)
-        if (int rc = reduce_partials(dCp, groups, ncc, gC, w.tmp, s)) return rc;
-    return FEQ_OK;
+    // the binned gradient's and the channel patterns' partial sums together
+    if (groups > 0) jobs[njobs++] = PartialJob{dCp, groups, ncc, gC, w.tmp};
+    return reduce_partials_multi(jobs, njobs, s);
 }
 
 }  // namespace feq
